@@ -1,0 +1,109 @@
+"""ctypes binding of ``libclifford_hip.so`` (the C ABI in ``include/clifford_hip.h``).
+
+The shared library is built in-tree by ``__graft_entry__.build()`` (hipcc,
+``--offload-arch=gfx950``). There is deliberately no fallback: if the library
+is missing, every op raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_NAME = "libclifford_hip.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+# status codes (include/clifford_hip.h)
+CLF_OK = 0
+CLF_ERR_ARG = 1
+CLF_ERR_UNSUPPORTED = 2
+CLF_ERR_HIP = 3
+CLF_ERR_WORKSPACE = 4
+
+OP_CODES = {"geom": 0, "wedge": 1, "inner": 2, "lc": 3, "rc": 4, "regressive": 5}
+GRADED_CODES = {"reverse": 0, "involution": 1, "conjugation": 2, "projection": 3,
+                "dual": 4, "dual_adj": 5}
+
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int
+_u32 = ctypes.c_uint32
+_i64 = ctypes.c_int64
+_sz = ctypes.c_size_t
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [("device", ctypes.c_int), ("compute_units", ctypes.c_int),
+                ("lds_bytes_per_block", ctypes.c_int), ("clock_khz", ctypes.c_int),
+                ("memory_clock_khz", ctypes.c_int), ("memory_bus_width_bits", ctypes.c_int),
+                ("arch_name", ctypes.c_char * 64)]
+
+
+# name -> (restype, argtypes); the exact export list of include/clifford_hip.h
+SIGNATURES = {
+    "clf_abi_version": (_i32, []),
+    "clf_last_error": (ctypes.c_char_p, []),
+    "clf_device_info_get": (_i32, [_i32, ctypes.POINTER(DeviceInfo)]),
+    "clf_product_max_n": (_i32, []),
+    "clf_product_fwd": (_i32, [_i32, _i32, _u32, _u32, _vp, _vp, _vp, _i64, _vp]),
+    "clf_product_bwd": (_i32, [_i32, _i32, _u32, _u32, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
+    "clf_graded": (_i32, [_i32, _i32, _u32, _u32, _i32, _vp, _vp, _i64, _vp]),
+    "clf_norm_sq_fwd": (_i32, [_i32, _u32, _u32, _vp, _vp, _i64, _vp]),
+    "clf_norm_sq_bwd": (_i32, [_i32, _u32, _u32, _vp, _vp, _vp, _i64, _vp]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load():
+    """Load (once) and return the native library; raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"cliffordcuda_amd: native library {LIB_PATH} is not built; run "
+                    "`python -c 'import __graft_entry__ as g; g.build()'` from the repo root")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            if lib.clf_abi_version() != 1:
+                raise RuntimeError("cliffordcuda_amd: ABI version mismatch")
+            _lib = lib
+    return _lib
+
+
+def last_error() -> str:
+    return load().clf_last_error().decode("utf-8", "replace")
+
+
+def check(rc: int, what: str):
+    """Map a CLF status to the reference's exception types (ValueError for
+    argument / unsupported errors, RuntimeError for HIP failures)."""
+    if rc == CLF_OK:
+        return
+    msg = last_error() or f"{what} failed with status {rc}"
+    if rc in (CLF_ERR_ARG, CLF_ERR_UNSUPPORTED):
+        raise ValueError(msg)
+    raise RuntimeError(f"{what}: {msg}")
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """The current HIP stream of ``t``'s device (torch's ``cuda`` namespace is HIP on ROCm)."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def device_info(device: int = 0) -> DeviceInfo:
+    info = DeviceInfo()
+    check(load().clf_device_info_get(device, ctypes.byref(info)), "clf_device_info_get")
+    return info

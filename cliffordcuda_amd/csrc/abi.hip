@@ -1,0 +1,84 @@
+// extern "C" entry points of libclifford_hip.so (declared in include/clifford_hip.h).
+#include <cstring>
+
+#include "clf_common.h"
+
+namespace clf {
+
+static thread_local std::string g_last_error;
+
+int set_error(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+int product_fwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const float* b, float* c,
+                int64_t batch, void* stream);
+int product_bwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const float* b, const float* gc,
+                float* ga, float* gb, int64_t batch, void* stream);
+int graded(int kind, int n, uint32_t neg, uint32_t nul, int grade, const float* x, float* y, int64_t batch,
+           void* stream);
+int norm_sq_fwd(int n, uint32_t neg, uint32_t nul, const float* x, float* out, int64_t batch, void* stream);
+int norm_sq_bwd(int n, uint32_t neg, uint32_t nul, const float* x, const float* gout, float* gx, int64_t batch,
+                void* stream);
+
+}  // namespace clf
+
+extern "C" {
+
+int clf_abi_version(void) { return CLF_ABI_VERSION; }
+
+const char* clf_last_error(void) { return clf::g_last_error.c_str(); }
+
+int clf_device_info_get(int device, clf_device_info* out) {
+    clf::clear_error();
+    if (!out) return clf::set_error(CLF_ERR_ARG, "out must not be NULL");
+    if (device < 0) return clf::set_error(CLF_ERR_ARG, "device must be >= 0");
+    hipDeviceProp_t p;
+    CLF_HIP_CHECK(hipGetDeviceProperties(&p, device));
+    std::memset(out, 0, sizeof(*out));
+    out->device = device;
+    out->compute_units = p.multiProcessorCount;
+    out->lds_bytes_per_block = (int)p.sharedMemPerBlock;
+    out->clock_khz = p.clockRate;
+    out->memory_clock_khz = p.memoryClockRate;
+    out->memory_bus_width_bits = p.memoryBusWidth;
+    std::strncpy(out->arch_name, p.gcnArchName, sizeof(out->arch_name) - 1);
+    return CLF_OK;
+}
+
+int clf_product_max_n(void) { return clf::kMaxN; }
+
+int clf_product_fwd(int op, int n, uint32_t neg_mask, uint32_t null_mask, const float* a, const float* b, float* c,
+                    int64_t batch, void* stream) {
+    clf::clear_error();
+    return clf::product_fwd(op, n, neg_mask, null_mask, a, b, c, batch, stream);
+}
+
+int clf_product_bwd(int op, int n, uint32_t neg_mask, uint32_t null_mask, const float* a, const float* b,
+                    const float* gc, float* ga, float* gb, int64_t batch, void* stream) {
+    clf::clear_error();
+    return clf::product_bwd(op, n, neg_mask, null_mask, a, b, gc, ga, gb, batch, stream);
+}
+
+int clf_graded(int kind, int n, uint32_t neg_mask, uint32_t null_mask, int grade, const float* x, float* y,
+               int64_t batch, void* stream) {
+    clf::clear_error();
+    return clf::graded(kind, n, neg_mask, null_mask, grade, x, y, batch, stream);
+}
+
+int clf_norm_sq_fwd(int n, uint32_t neg_mask, uint32_t null_mask, const float* x, float* out, int64_t batch,
+                    void* stream) {
+    clf::clear_error();
+    return clf::norm_sq_fwd(n, neg_mask, null_mask, x, out, batch, stream);
+}
+
+int clf_norm_sq_bwd(int n, uint32_t neg_mask, uint32_t null_mask, const float* x, const float* gout, float* gx,
+                    int64_t batch, void* stream) {
+    clf::clear_error();
+    return clf::norm_sq_bwd(n, neg_mask, null_mask, x, gout, gx, batch, stream);
+}
+
+}  // extern "C"

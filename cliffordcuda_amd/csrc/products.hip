@@ -1,0 +1,590 @@
+// Binary Clifford products on gfx950: forward and fused backward, all six ops,
+// any Cl(p,q,r), bit-pattern layout.
+//
+// Math. Every product is c[k] = sum_i sigma_op(i, i^k) a[i] b[i^k] (reference
+// kernels/ga/geom_prod.cu:17-18). The blocked kernels split a blade index into
+// a high part and a 4-bit low part, i = ih*16 + il. Because the reorder sign is
+// a bilinear form over GF(2) whose high-by-low cross term is all ones, the sign
+// factorises as
+//   sigma(i, j) = s_hi(ih, jh) * (-1)^{|ih| |jl|} * s_lo(il, jl)
+// s_lo is a compile-time 16x16 pattern (op predicate, low-bit metric), so the
+// 256 multiply-adds of one (ih, jh) block pair are straight-line FMAs with the
+// sign folded into the instruction's negate modifier. s_hi and the |ih||jl|
+// parity flip are applied once per block to the b operand (16 sign-bit XORs).
+//
+// Layout. One workgroup stages whole rows of a and b (and gc for backward) in
+// LDS with float4 loads; each lane owns one 16-blade output block of one row
+// and keeps its 16 accumulators in VGPRs. Lanes of a row read their b blocks
+// as a permutation of the row, the a block as a broadcast. Inside each 64-byte
+// block the four float4 slots are XOR-swizzled so the 16 lanes of a row hit
+// distinct LDS banks.
+#include <utility>
+
+#include "clf_common.h"
+
+namespace clf {
+
+// low-block variants: the op's predicate restricted to the low 4 bits
+enum LowVar : int { LV_GEOM = 0, LV_WEDGE = 1, LV_INNER = 2, LV_LC = 3, LV_RC = 4, LV_REGR = 5 };
+
+__host__ __device__ constexpr int low_sign(int var, bool lowneg, unsigned il, unsigned jl) {
+    const bool pred = var == LV_GEOM    ? true
+                      : var == LV_WEDGE ? ((il & jl) == 0u)
+                      : var == LV_INNER ? ((((il & ~jl) & 15u) == 0u) || (((jl & ~il) & 15u) == 0u))
+                      : var == LV_LC    ? (((il & ~jl) & 15u) == 0u)
+                      : var == LV_RC    ? (((jl & ~il) & 15u) == 0u)
+                                        : (((il | jl) & 15u) == 15u);
+    if (!pred) return 0;
+    int p = creorder(il, jl);
+    if (var == LV_REGR)
+        p += cbitsum(il) + cbitsum(jl);
+    else if (lowneg)
+        p += cpopc(il & jl);
+    return (p & 1) ? -1 : 1;
+}
+
+__device__ __forceinline__ float flip(float x, unsigned m) { return __uint_as_float(__float_as_uint(x) ^ m); }
+
+// XOR swizzle of the float4 slot inside a 64-byte block
+__device__ __forceinline__ unsigned swz(unsigned blk) { return ((blk >> 1) ^ (blk >> 3)) & 3u; }
+
+__device__ __forceinline__ void load_blk(const float4* __restrict__ base, unsigned blk, float (&v)[16]) {
+    const unsigned s = swz(blk);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 t = base[(blk << 2) + ((unsigned)q ^ s)];
+        v[4 * q + 0] = t.x;
+        v[4 * q + 1] = t.y;
+        v[4 * q + 2] = t.z;
+        v[4 * q + 3] = t.w;
+    }
+}
+
+// reversed element order: v[y] = block[15 - y]
+__device__ __forceinline__ void load_blk_rev(const float4* __restrict__ base, unsigned blk, float (&v)[16]) {
+    const unsigned s = swz(blk);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 t = base[(blk << 2) + ((unsigned)q ^ s)];
+        v[15 - (4 * q + 0)] = t.x;
+        v[15 - (4 * q + 1)] = t.y;
+        v[15 - (4 * q + 2)] = t.z;
+        v[15 - (4 * q + 3)] = t.w;
+    }
+}
+
+// The three low-block bodies below are expanded at compile time over all 256
+// (il, jl) pairs with a constexpr sign, so each term is one FMA (negate
+// modifier for -1, nothing for 0).
+
+// acc[t] += s_lo(il, il^t) a[il] b[il^t]
+template <int VAR, bool LOWNEG, int IL, int T>
+__device__ __forceinline__ void fwd_term(float (&acc)[16], const float (&a)[16], const float (&b)[16]) {
+    constexpr int s = low_sign(VAR, LOWNEG, (unsigned)IL, (unsigned)(IL ^ T));
+    if constexpr (s > 0) acc[T] = __builtin_fmaf(a[IL], b[IL ^ T], acc[T]);
+    else if constexpr (s < 0) acc[T] = __builtin_fmaf(-a[IL], b[IL ^ T], acc[T]);
+}
+
+// acc[il] += s_lo(il, jl) b[jl] g[il^jl]          (gradient w.r.t. the left operand)
+template <int VAR, bool LOWNEG, int JL, int IL>
+__device__ __forceinline__ void ga_term(float (&acc)[16], const float (&b)[16], const float (&g)[16]) {
+    constexpr int s = low_sign(VAR, LOWNEG, (unsigned)IL, (unsigned)JL);
+    if constexpr (s > 0) acc[IL] = __builtin_fmaf(b[JL], g[IL ^ JL], acc[IL]);
+    else if constexpr (s < 0) acc[IL] = __builtin_fmaf(-b[JL], g[IL ^ JL], acc[IL]);
+}
+
+// acc[jl] += s_lo(il, jl) a[il] g[il^jl]          (gradient w.r.t. the right operand)
+template <int VAR, bool LOWNEG, int IL, int JL>
+__device__ __forceinline__ void gb_term(float (&acc)[16], const float (&a)[16], const float (&g)[16]) {
+    constexpr int s = low_sign(VAR, LOWNEG, (unsigned)IL, (unsigned)JL);
+    if constexpr (s > 0) acc[JL] = __builtin_fmaf(a[IL], g[IL ^ JL], acc[JL]);
+    else if constexpr (s < 0) acc[JL] = __builtin_fmaf(-a[IL], g[IL ^ JL], acc[JL]);
+}
+
+template <int VAR, bool LOWNEG, int... Is>
+__device__ __forceinline__ void lowblock_fwd_seq(float (&acc)[16], const float (&a)[16], const float (&b)[16],
+                                                 std::integer_sequence<int, Is...>) {
+    (fwd_term<VAR, LOWNEG, Is / 16, Is % 16>(acc, a, b), ...);
+}
+template <int VAR, bool LOWNEG, int... Is>
+__device__ __forceinline__ void lowblock_ga_seq(float (&acc)[16], const float (&b)[16], const float (&g)[16],
+                                                std::integer_sequence<int, Is...>) {
+    (ga_term<VAR, LOWNEG, Is / 16, Is % 16>(acc, b, g), ...);
+}
+template <int VAR, bool LOWNEG, int... Is>
+__device__ __forceinline__ void lowblock_gb_seq(float (&acc)[16], const float (&a)[16], const float (&g)[16],
+                                                std::integer_sequence<int, Is...>) {
+    (gb_term<VAR, LOWNEG, Is / 16, Is % 16>(acc, a, g), ...);
+}
+
+template <int VAR, bool LOWNEG>
+__device__ __forceinline__ void lowblock_fwd(float (&acc)[16], const float (&a)[16], const float (&b)[16]) {
+    lowblock_fwd_seq<VAR, LOWNEG>(acc, a, b, std::make_integer_sequence<int, 256>{});
+}
+template <int VAR, bool LOWNEG>
+__device__ __forceinline__ void lowblock_ga(float (&acc)[16], const float (&b)[16], const float (&g)[16]) {
+    lowblock_ga_seq<VAR, LOWNEG>(acc, b, g, std::make_integer_sequence<int, 256>{});
+}
+template <int VAR, bool LOWNEG>
+__device__ __forceinline__ void lowblock_gb(float (&acc)[16], const float (&a)[16], const float (&g)[16]) {
+    lowblock_gb_seq<VAR, LOWNEG>(acc, a, g, std::make_integer_sequence<int, 256>{});
+}
+
+struct HiSign {
+    bool valid;
+    unsigned mask;  // 0 or 0x80000000
+};
+
+// s_hi(ih, jh): the high-part factor of sigma_op, including the op's block
+// predicate, the high-bit metric and (regressive) the global and per-operand
+// signs. Parameters: negh/nulh = metric masks shifted down by 4 bits,
+// fullh = all-ones over the high bits, nm1 = (n-1) & 1, mu = parity of |NEG|.
+template <int OP>
+__device__ __forceinline__ HiSign hi_sign(unsigned ih, unsigned jh, unsigned negh, unsigned nulh,
+                                          unsigned fullh, int nm1, int mu) {
+    int par = reorder_parity(ih, jh);
+    bool ok = true;
+    if (OP == OP_GEOM) {
+        ok = (ih & jh & nulh) == 0u;
+        par += __popc(ih & jh & negh);
+    } else if (OP == OP_WEDGE) {
+        ok = (ih & jh) == 0u;
+    } else if (OP == OP_INNER) {
+        ok = (((ih & ~jh) == 0u) || ((jh & ~ih) == 0u)) && ((ih & jh & nulh) == 0u);
+        par += __popc(ih & jh & negh);
+    } else if (OP == OP_LC) {
+        ok = ((ih & ~jh) == 0u) && ((ih & jh & nulh) == 0u);
+        par += __popc(ih & jh & negh);
+    } else if (OP == OP_RC) {
+        ok = ((jh & ~ih) == 0u) && ((ih & jh & nulh) == 0u);
+        par += __popc(ih & jh & negh);
+    } else {  // regressive
+        ok = (ih | jh) == fullh;
+        par += bitsum_parity(ih) + bitsum_parity(jh) + nm1 * __popc(jh) + mu;
+    }
+    return HiSign{ok, (unsigned)(par & 1) << 31};
+}
+
+// parity that multiplies |jl| in the cross term, for left-operand high block x
+template <int OP>
+__device__ __forceinline__ unsigned cross_pi(unsigned x, int nm1) {
+    return (unsigned)((__popc(x) + (OP == OP_REGR ? nm1 : 0)) & 1);
+}
+
+// b~[jl] = b[jl] * sign * (-1)^{|jl| pi}
+__device__ __forceinline__ void apply_flips(float (&v)[16], unsigned m_even, unsigned m_odd) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) v[e] = flip(v[e], (cpopc((unsigned)e) & 1) ? m_odd : m_even);
+}
+
+template <int OP, bool LOWNEG>
+__device__ __forceinline__ void fwd_block_dispatch(float (&acc)[16], const float (&av)[16], const float (&bv)[16],
+                                                   unsigned ih, unsigned jh) {
+    if (OP == OP_GEOM) {
+        lowblock_fwd<LV_GEOM, LOWNEG>(acc, av, bv);
+    } else if (OP == OP_WEDGE) {
+        lowblock_fwd<LV_WEDGE, false>(acc, av, bv);
+    } else if (OP == OP_LC) {
+        lowblock_fwd<LV_LC, LOWNEG>(acc, av, bv);
+    } else if (OP == OP_RC) {
+        lowblock_fwd<LV_RC, LOWNEG>(acc, av, bv);
+    } else if (OP == OP_REGR) {
+        lowblock_fwd<LV_REGR, false>(acc, av, bv);
+    } else {  // inner: the block relation picks the low predicate
+        const bool l = (ih & ~jh) == 0u, r = (jh & ~ih) == 0u;
+        if (l && r) lowblock_fwd<LV_INNER, LOWNEG>(acc, av, bv);
+        else if (l) lowblock_fwd<LV_LC, LOWNEG>(acc, av, bv);
+        else lowblock_fwd<LV_RC, LOWNEG>(acc, av, bv);
+    }
+}
+
+template <int OP, bool LOWNEG>
+__device__ __forceinline__ void ga_block_dispatch(float (&acc)[16], const float (&bv)[16], const float (&g)[16],
+                                                  unsigned ih, unsigned jh) {
+    if (OP == OP_GEOM) {
+        lowblock_ga<LV_GEOM, LOWNEG>(acc, bv, g);
+    } else if (OP == OP_WEDGE) {
+        lowblock_ga<LV_WEDGE, false>(acc, bv, g);
+    } else if (OP == OP_LC) {
+        lowblock_ga<LV_LC, LOWNEG>(acc, bv, g);
+    } else if (OP == OP_RC) {
+        lowblock_ga<LV_RC, LOWNEG>(acc, bv, g);
+    } else if (OP == OP_REGR) {
+        lowblock_ga<LV_REGR, false>(acc, bv, g);
+    } else {
+        const bool l = (ih & ~jh) == 0u, r = (jh & ~ih) == 0u;
+        if (l && r) lowblock_ga<LV_INNER, LOWNEG>(acc, bv, g);
+        else if (l) lowblock_ga<LV_LC, LOWNEG>(acc, bv, g);
+        else lowblock_ga<LV_RC, LOWNEG>(acc, bv, g);
+    }
+}
+
+template <int OP, bool LOWNEG>
+__device__ __forceinline__ void gb_block_dispatch(float (&acc)[16], const float (&av)[16], const float (&g)[16],
+                                                  unsigned ih, unsigned jh) {
+    if (OP == OP_GEOM) {
+        lowblock_gb<LV_GEOM, LOWNEG>(acc, av, g);
+    } else if (OP == OP_WEDGE) {
+        lowblock_gb<LV_WEDGE, false>(acc, av, g);
+    } else if (OP == OP_LC) {
+        lowblock_gb<LV_LC, LOWNEG>(acc, av, g);
+    } else if (OP == OP_RC) {
+        lowblock_gb<LV_RC, LOWNEG>(acc, av, g);
+    } else if (OP == OP_REGR) {
+        lowblock_gb<LV_REGR, false>(acc, av, g);
+    } else {
+        const bool l = (ih & ~jh) == 0u, r = (jh & ~ih) == 0u;
+        if (l && r) lowblock_gb<LV_INNER, LOWNEG>(acc, av, g);
+        else if (l) lowblock_gb<LV_LC, LOWNEG>(acc, av, g);
+        else lowblock_gb<LV_RC, LOWNEG>(acc, av, g);
+    }
+}
+
+struct BlkParams {
+    long long batch;
+    int n;          // algebra dimension, 4 <= n <= kMaxN
+    unsigned negh;  // metric masks >> 4
+    unsigned nulh;
+    int nm1;        // (n - 1) & 1
+    int mu;         // parity of popcount(neg) (regressive global sign)
+    int lpr_log;    // log2(lanes per row)
+    int rows_per_wg;
+    int kpl;        // output blocks per lane
+};
+
+// Stage `nops` row-major operands for the workgroup's rows into LDS (swizzled).
+__device__ __forceinline__ void stage_rows(float4* __restrict__ lds, const float4* const* __restrict__ src, int nops,
+                                           long long row0, int nrows, int n) {
+    const int d4_log = n - 2;
+    const int D4 = 1 << d4_log;
+    const int total = nrows << d4_log;
+    for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
+        const int r = idx >> d4_log;
+        const unsigned f = (unsigned)(idx & (D4 - 1));
+        const unsigned blk = f >> 2, q = f & 3u;
+        const int dst = r * nops * D4 + (int)((blk << 2) + (q ^ swz(blk)));
+        const long long g = (row0 << d4_log) + idx;
+        for (int o = 0; o < nops; ++o) lds[dst + o * D4] = src[o][g];
+    }
+}
+
+template <int OP, bool LOWNEG>
+__global__ __launch_bounds__(256) void prod_fwd_blk(const float* __restrict__ A, const float* __restrict__ B,
+                                                     float* __restrict__ C, BlkParams P) {
+    extern __shared__ float4 lds[];
+    const int n = P.n;
+    const int D4 = 1 << (n - 2);
+    const unsigned NB = 1u << (n - 4);
+    const long long row0 = (long long)blockIdx.x * P.rows_per_wg;
+    const int nrows = (int)((P.batch - row0) < P.rows_per_wg ? (P.batch - row0) : P.rows_per_wg);
+    {
+        const float4* src[2] = {reinterpret_cast<const float4*>(A), reinterpret_cast<const float4*>(B)};
+        stage_rows(lds, src, 2, row0, nrows, n);
+    }
+    __syncthreads();
+    const int r = threadIdx.x >> P.lpr_log;
+    if (r >= nrows) return;
+    const unsigned lane_blk = threadIdx.x & ((1u << P.lpr_log) - 1u);
+    const float4* la = lds + r * 2 * D4;
+    const float4* lb = la + D4;
+    float4* out = reinterpret_cast<float4*>(C) + ((row0 + r) << (n - 2));
+    const unsigned fullh = NB - 1u;
+
+    for (int kk = 0; kk < P.kpl; ++kk) {
+        const unsigned kh = lane_blk + ((unsigned)kk << P.lpr_log);
+        float acc[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+        for (unsigned ih = 0; ih < NB; ++ih) {
+            const unsigned jh = ih ^ kh;
+            const HiSign hs = hi_sign<OP>(ih, jh, P.negh, P.nulh, fullh, P.nm1, P.mu);
+            if (!hs.valid) continue;
+            float av[16], bv[16];
+            load_blk(la, ih, av);
+            load_blk(lb, jh, bv);
+            apply_flips(bv, hs.mask, hs.mask ^ (cross_pi<OP>(ih, P.nm1) << 31));
+            fwd_block_dispatch<OP, LOWNEG>(acc, av, bv, ih, jh);
+        }
+        if (OP == OP_REGR) {
+            const unsigned ob = fullh ^ kh;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                out[(ob << 2) + (3 - q)] = make_float4(acc[4 * q + 3], acc[4 * q + 2], acc[4 * q + 1], acc[4 * q]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                out[(kh << 2) + q] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+        }
+    }
+}
+
+template <int OP, bool LOWNEG>
+__global__ __launch_bounds__(256) void prod_bwd_blk(const float* __restrict__ A, const float* __restrict__ B,
+                                                     const float* __restrict__ GC, float* __restrict__ GA,
+                                                     float* __restrict__ GB, BlkParams P) {
+    extern __shared__ float4 lds[];
+    const int n = P.n;
+    const int D4 = 1 << (n - 2);
+    const unsigned NB = 1u << (n - 4);
+    const long long row0 = (long long)blockIdx.x * P.rows_per_wg;
+    const int nrows = (int)((P.batch - row0) < P.rows_per_wg ? (P.batch - row0) : P.rows_per_wg);
+    {
+        const float4* src[3] = {reinterpret_cast<const float4*>(A), reinterpret_cast<const float4*>(B),
+                                reinterpret_cast<const float4*>(GC)};
+        stage_rows(lds, src, 3, row0, nrows, n);
+    }
+    __syncthreads();
+    const int r = threadIdx.x >> P.lpr_log;
+    if (r >= nrows) return;
+    const unsigned lane_blk = threadIdx.x & ((1u << P.lpr_log) - 1u);
+    const float4* la = lds + r * 3 * D4;
+    const float4* lb = la + D4;
+    const float4* lg = la + 2 * D4;
+    const unsigned fullh = NB - 1u;
+    const bool want_a = GA != nullptr, want_b = GB != nullptr;
+
+    for (int kk = 0; kk < P.kpl; ++kk) {
+        const unsigned h = lane_blk + ((unsigned)kk << P.lpr_log);
+        const unsigned pi_h = cross_pi<OP>(h, P.nm1);
+        float ga[16], gb[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            ga[e] = 0.f;
+            gb[e] = 0.f;
+        }
+        for (unsigned m = 0; m < NB; ++m) {
+            const unsigned x = h ^ m;
+            const HiSign sa = hi_sign<OP>(h, m, P.negh, P.nulh, fullh, P.nm1, P.mu);  // (i, j) = (h, m)
+            const HiSign sb = hi_sign<OP>(m, h, P.negh, P.nulh, fullh, P.nm1, P.mu);  // (i, j) = (m, h)
+            const bool do_a = want_a && sa.valid, do_b = want_b && sb.valid;
+            if (!do_a && !do_b) continue;
+            float g[16];
+            if (OP == OP_REGR) load_blk_rev(lg, fullh ^ x, g);
+            else load_blk(lg, x, g);
+            if (do_a) {
+                float bv[16];
+                load_blk(lb, m, bv);
+                apply_flips(bv, sa.mask, sa.mask ^ (pi_h << 31));
+                ga_block_dispatch<OP, LOWNEG>(ga, bv, g, h, m);
+            }
+            if (do_b) {
+                const unsigned pm = cross_pi<OP>(m, P.nm1) << 31;
+                float av[16], gt[16];
+                load_blk(la, m, av);
+                apply_flips(av, sb.mask, sb.mask ^ pm);
+#pragma unroll
+                for (int e = 0; e < 16; ++e) gt[e] = (cpopc((unsigned)e) & 1) ? flip(g[e], pm) : g[e];
+                gb_block_dispatch<OP, LOWNEG>(gb, av, gt, m, h);
+            }
+        }
+        const long long base = (row0 + r) << (n - 2);
+        if (want_a) {
+            float4* o = reinterpret_cast<float4*>(GA) + base;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                o[(h << 2) + q] = make_float4(ga[4 * q], ga[4 * q + 1], ga[4 * q + 2], ga[4 * q + 3]);
+        }
+        if (want_b) {
+            float4* o = reinterpret_cast<float4*>(GB) + base;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                o[(h << 2) + q] = make_float4(gb[4 * q], gb[4 * q + 1], gb[4 * q + 2], gb[4 * q + 3]);
+        }
+    }
+}
+
+// ---- generic path: one thread per output coefficient, closed-form signs ----
+// Used for n < 4 and for metrics whose low four generators are not all +1 or
+// all -1 (or contain a null generator).
+__global__ __launch_bounds__(256) void prod_fwd_generic(int op, int n, unsigned neg, unsigned nul,
+                                                         const float* __restrict__ A, const float* __restrict__ B,
+                                                         float* __restrict__ C, long long batch) {
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const unsigned D = 1u << n;
+    if (idx >= (batch << n)) return;
+    const long long row = idx >> n;
+    const unsigned k = (unsigned)(idx & (D - 1));
+    const float* a = A + (row << n);
+    const float* b = B + (row << n);
+    float acc = 0.f;
+    for (unsigned i = 0; i < D; ++i) {
+        const int s = full_sign(op, n, i, i ^ k, neg, nul);
+        if (s) acc = __builtin_fmaf((float)s * a[i], b[i ^ k], acc);
+    }
+    const unsigned ok = (op == OP_REGR) ? (~k & (D - 1)) : k;
+    C[(row << n) + ok] = acc;
+}
+
+// ga[k] = sum_j sigma(k, j) b[j] gf[k^j]   (which == 0)
+// gb[k] = sum_i sigma(i, k) a[i] gf[i^k]   (which == 1)
+__global__ __launch_bounds__(256) void prod_bwd_generic(int op, int n, unsigned neg, unsigned nul, int which,
+                                                         const float* __restrict__ X, const float* __restrict__ GC,
+                                                         float* __restrict__ OUT, long long batch) {
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const unsigned D = 1u << n;
+    if (idx >= (batch << n)) return;
+    const long long row = idx >> n;
+    const unsigned k = (unsigned)(idx & (D - 1));
+    const float* x = X + (row << n);
+    const float* gc = GC + (row << n);
+    float acc = 0.f;
+    for (unsigned u = 0; u < D; ++u) {
+        const int s = which == 0 ? full_sign(op, n, k, u, neg, nul) : full_sign(op, n, u, k, neg, nul);
+        if (!s) continue;
+        const unsigned m = u ^ k;
+        const float gv = (op == OP_REGR) ? gc[~m & (D - 1)] : gc[m];
+        acc = __builtin_fmaf((float)s * x[u], gv, acc);
+    }
+    OUT[(row << n) + k] = acc;
+}
+
+// ---- host side --------------------------------------------------------------
+
+static int check_common(int op, int n, uint32_t neg, uint32_t nul, int64_t batch) {
+    if (op < CLF_OP_GEOM || op > CLF_OP_REGRESSIVE) return set_error(CLF_ERR_ARG, "unknown product op " + std::to_string(op));
+    if (n < 1 || n > kMaxN)
+        return set_error(CLF_ERR_ARG, "n must be in [1, " + std::to_string(kMaxN) + "], got " + std::to_string(n));
+    const uint32_t full = (1u << n) - 1u;
+    if ((neg & ~full) || (nul & ~full)) return set_error(CLF_ERR_ARG, "metric masks have bits above n");
+    if (neg & nul) return set_error(CLF_ERR_ARG, "neg_mask and null_mask overlap");
+    if (batch < 0) return set_error(CLF_ERR_ARG, "batch must be >= 0");
+    if (op == CLF_OP_REGRESSIVE && nul)
+        return set_error(CLF_ERR_UNSUPPORTED,
+                         "regressive_prod is undefined for degenerate metrics (any 0 in the metric makes the "
+                         "pseudoscalar non-invertible)");
+    return CLF_OK;
+}
+
+// Launch shape for the blocked kernels. Returns false if the generic path must be used.
+static bool blocked_plan(int op, int n, uint32_t neg, uint32_t nul, int nops, BlkParams& P, bool& lowneg,
+                         dim3& grid, dim3& block, size_t& lds_bytes) {
+    if (n < 4) return false;
+    const uint32_t neg4 = neg & 15u, nul4 = nul & 15u;
+    if (op == CLF_OP_WEDGE || op == CLF_OP_REGRESSIVE) {
+        lowneg = false;  // these signs do not depend on the low-bit metric
+    } else {
+        if (nul4) return false;
+        if (neg4 != 0u && neg4 != 15u) return false;
+        lowneg = neg4 == 15u;
+    }
+    const int nh = n - 4;
+    const int NB = 1 << nh;
+    const int lpr = NB < 64 ? NB : 64;
+    int lpr_log = 0;
+    while ((1 << lpr_log) < lpr) ++lpr_log;
+    const int rpw = 64 / lpr;
+    const size_t row_bytes = (size_t)nops * ((size_t)4 << n);
+    int nwaves = 4;
+    while (nwaves > 1 && (size_t)nwaves * rpw * row_bytes > 48 * 1024) nwaves >>= 1;
+    P.n = n;
+    P.negh = neg >> 4;
+    P.nulh = nul >> 4;
+    P.nm1 = (n - 1) & 1;
+    P.mu = popc_rt(neg) & 1;
+    P.lpr_log = lpr_log;
+    P.rows_per_wg = nwaves * rpw;
+    P.kpl = NB / lpr;
+    grid = dim3((unsigned)((P.batch + P.rows_per_wg - 1) / P.rows_per_wg));
+    block = dim3(64 * nwaves);
+    lds_bytes = (size_t)P.rows_per_wg * row_bytes;
+    return true;
+}
+
+template <int OP, bool LN>
+static void launch_fwd(dim3 g, dim3 b, size_t lds, hipStream_t s, const float* A, const float* B, float* C,
+                       const BlkParams& P) {
+    hipLaunchKernelGGL((prod_fwd_blk<OP, LN>), g, b, lds, s, A, B, C, P);
+}
+
+template <int OP, bool LN>
+static void launch_bwd(dim3 g, dim3 b, size_t lds, hipStream_t s, const float* A, const float* B, const float* GCp,
+                       float* GA, float* GB, const BlkParams& P) {
+    hipLaunchKernelGGL((prod_bwd_blk<OP, LN>), g, b, lds, s, A, B, GCp, GA, GB, P);
+}
+
+int product_fwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const float* b, float* c,
+                int64_t batch, void* stream) {
+    int rc = check_common(op, n, neg, nul, batch);
+    if (rc) return rc;
+    if (batch == 0) return CLF_OK;
+    if (!a || !b || !c) return set_error(CLF_ERR_ARG, "null pointer argument");
+    if (c == a || c == b) return set_error(CLF_ERR_ARG, "output must not alias an input");
+    if ((((uintptr_t)a) | ((uintptr_t)b) | ((uintptr_t)c)) & 15u)
+        return set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
+    hipStream_t s = (hipStream_t)stream;
+    BlkParams P{};
+    P.batch = batch;
+    bool ln = false;
+    dim3 g, bl;
+    size_t lds = 0;
+    if (blocked_plan(op, n, neg, nul, 2, P, ln, g, bl, lds)) {
+#define CLF_FWD_CASE(OPV)                                              \
+    case OPV:                                                          \
+        if (ln) launch_fwd<OPV, true>(g, bl, lds, s, a, b, c, P);      \
+        else launch_fwd<OPV, false>(g, bl, lds, s, a, b, c, P);        \
+        break;
+        switch (op) {
+            CLF_FWD_CASE(OP_GEOM)
+            CLF_FWD_CASE(OP_INNER)
+            CLF_FWD_CASE(OP_LC)
+            CLF_FWD_CASE(OP_RC)
+            case OP_WEDGE: launch_fwd<OP_WEDGE, false>(g, bl, lds, s, a, b, c, P); break;
+            case OP_REGR: launch_fwd<OP_REGR, false>(g, bl, lds, s, a, b, c, P); break;
+        }
+#undef CLF_FWD_CASE
+    } else {
+        const long long total = batch << n;
+        const unsigned blocks = (unsigned)((total + 255) / 256);
+        hipLaunchKernelGGL(prod_fwd_generic, dim3(blocks), dim3(256), 0, s, op, n, neg, nul, a, b, c,
+                           (long long)batch);
+    }
+    CLF_HIP_CHECK(hipGetLastError());
+    return CLF_OK;
+}
+
+int product_bwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const float* b, const float* gc,
+                float* ga, float* gb, int64_t batch, void* stream) {
+    int rc = check_common(op, n, neg, nul, batch);
+    if (rc) return rc;
+    if (batch == 0 || (!ga && !gb)) return CLF_OK;
+    if (!a || !b || !gc) return set_error(CLF_ERR_ARG, "null pointer argument");
+    if ((ga && (ga == a || ga == b || ga == gc)) || (gb && (gb == a || gb == b || gb == gc)) || (ga && ga == gb))
+        return set_error(CLF_ERR_ARG, "gradient outputs must not alias inputs or each other");
+    if ((((uintptr_t)a) | ((uintptr_t)b) | ((uintptr_t)gc) | ((uintptr_t)ga) | ((uintptr_t)gb)) & 15u)
+        return set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
+    hipStream_t s = (hipStream_t)stream;
+    BlkParams P{};
+    P.batch = batch;
+    bool ln = false;
+    dim3 g, bl;
+    size_t lds = 0;
+    if (blocked_plan(op, n, neg, nul, 3, P, ln, g, bl, lds)) {
+#define CLF_BWD_CASE(OPV)                                                      \
+    case OPV:                                                                  \
+        if (ln) launch_bwd<OPV, true>(g, bl, lds, s, a, b, gc, ga, gb, P);     \
+        else launch_bwd<OPV, false>(g, bl, lds, s, a, b, gc, ga, gb, P);       \
+        break;
+        switch (op) {
+            CLF_BWD_CASE(OP_GEOM)
+            CLF_BWD_CASE(OP_INNER)
+            CLF_BWD_CASE(OP_LC)
+            CLF_BWD_CASE(OP_RC)
+            case OP_WEDGE: launch_bwd<OP_WEDGE, false>(g, bl, lds, s, a, b, gc, ga, gb, P); break;
+            case OP_REGR: launch_bwd<OP_REGR, false>(g, bl, lds, s, a, b, gc, ga, gb, P); break;
+        }
+#undef CLF_BWD_CASE
+    } else {
+        const long long total = batch << n;
+        const unsigned blocks = (unsigned)((total + 255) / 256);
+        if (ga)
+            hipLaunchKernelGGL(prod_bwd_generic, dim3(blocks), dim3(256), 0, s, op, n, neg, nul, 0, b, gc, ga,
+                               (long long)batch);
+        if (gb)
+            hipLaunchKernelGGL(prod_bwd_generic, dim3(blocks), dim3(256), 0, s, op, n, neg, nul, 1, a, gc, gb,
+                               (long long)batch);
+    }
+    CLF_HIP_CHECK(hipGetLastError());
+    return CLF_OK;
+}
+
+}  // namespace clf

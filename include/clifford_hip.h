@@ -1,0 +1,125 @@
+/*
+ * clifford_hip.h — C ABI of the MI355X (gfx950) Clifford product & rotor library.
+ *
+ * This is the native boundary that replaces the reference's per-kernel pybind11
+ * modules (the PYBIND11_MODULE blocks of src/cliffordcuda/kernels/ga/ and kernels/rotor/, loaded by
+ * src/cliffordcuda/_config.py:29-38). Everything here takes plain device
+ * pointers and sizes; nothing allocates device memory except where a function
+ * says so, and nothing synchronises the host. Every call is asynchronous on the
+ * given HIP stream (pass the caller's current stream; NULL = legacy default).
+ *
+ * Conventions
+ *   - Multivectors are fp32, row-major (batch, 2^n), bit-pattern blade order:
+ *     blade index i has generator k iff bit k of i is set.
+ *   - The metric is passed as two bit masks over the n generators:
+ *     neg_mask bit k = 1 iff e_k^2 = -1, null_mask bit k = 1 iff e_k^2 = 0
+ *     (all other generators square to +1). The two masks must be disjoint.
+ *   - Row counts and offsets are 64-bit.
+ *   - Every argument is validated before any HIP call, so error paths run on a
+ *     host without a GPU. Return value: CLF_OK or a CLF_ERR_* code; the text of
+ *     the last error on the calling thread is clf_last_error().
+ */
+#ifndef CLIFFORD_HIP_H
+#define CLIFFORD_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CLF_ABI_VERSION 1
+
+/* status codes */
+#define CLF_OK               0
+#define CLF_ERR_ARG          1   /* invalid argument (null pointer, bad n, bad masks, ...) */
+#define CLF_ERR_UNSUPPORTED  2   /* valid but not supported (e.g. regressive on a degenerate metric) */
+#define CLF_ERR_HIP          3   /* a HIP runtime call failed */
+#define CLF_ERR_WORKSPACE    4   /* workspace missing or too small */
+
+/* binary products: c[k] = sum_i sigma_op(i, i^k) a[i] b[i^k] */
+#define CLF_OP_GEOM        0   /* geometric product                    (ref extensions/ga/geom_prod.py:253)      */
+#define CLF_OP_WEDGE       1   /* outer product, i&j == 0               (ref extensions/ga/wedge_prod/chunk.py:105) */
+#define CLF_OP_INNER       2   /* Hestenes inner incl. scalars          (ref extensions/ga/inner_prod/chunk.py:101) */
+#define CLF_OP_LC          3   /* left contraction, i subset j          (ref extensions/ga/left_contract.py:121)  */
+#define CLF_OP_RC          4   /* right contraction, j subset i         (ref extensions/ga/right_contract.py:110) */
+#define CLF_OP_REGRESSIVE  5   /* dual(dual a ^ dual b), non-degenerate (ref extensions/ga/regressive_prod.py:186) */
+
+/* graded (sign / mask / permutation) ops */
+#define CLF_GRADED_REVERSE      0  /* (-1)^{k(k-1)/2}                    (ref algebra.py:195-205) */
+#define CLF_GRADED_INVOLUTION   1  /* (-1)^k                             (ref algebra.py:278-286) */
+#define CLF_GRADED_CONJUGATION  2  /* (-1)^{k(k+1)/2}                    (ref algebra.py:288-296) */
+#define CLF_GRADED_PROJECTION   3  /* keep grade == `grade`              (ref algebra.py:298-306) */
+#define CLF_GRADED_DUAL         4  /* y[m] = x[~m] s[m], x I^{-1}        (ref algebra.py:208-265) */
+#define CLF_GRADED_DUAL_ADJ     5  /* adjoint of DUAL: y[k] = x[~k] s[~k] (backward of dual)      */
+
+typedef struct clf_device_info {
+    int    device;
+    int    compute_units;
+    int    lds_bytes_per_block;   /* max shared memory per workgroup */
+    int    clock_khz;
+    int    memory_clock_khz;
+    int    memory_bus_width_bits;
+    char   arch_name[64];
+} clf_device_info;
+
+/* ABI version (CLF_ABI_VERSION). */
+int clf_abi_version(void);
+
+/* Text of the last error on the calling thread ("" if none). Never NULL. */
+const char* clf_last_error(void);
+
+/* Device properties used for launch shaping and the roofline report.
+ * Replaces the reference's shared-memory probe
+ * (src/cliffordcuda/extensions/ga/geom_prod_tiled.py:88-117,
+ *  kernels/ga/geom_prod_tiled.cu:169-175). */
+int clf_device_info_get(int device, clf_device_info* out);
+
+/* Largest n the product kernels accept. */
+int clf_product_max_n(void);
+
+/* Forward of a binary product on `batch` rows.
+ * Replaces geom_prod_fwd (kernels/ga/geom_prod.cu:281-291), wedge_prod_fwd
+ * (kernels/ga/wedge_prod.cu:181-217), inner_prod_fwd (kernels/ga/inner_prod.cu:171-230),
+ * contract_fwd (kernels/ga/contract.cu:159-200) and the regressive forward
+ * (extensions/ga/regressive_prod.py:143-170, GP kernel + index_select).
+ * For CLF_OP_REGRESSIVE the output is written in final blade order (index ~k
+ * already applied). a, b, c: device pointers to batch * 2^n floats; c must not
+ * alias a or b. batch == 0 is a no-op. */
+int clf_product_fwd(int op, int n, uint32_t neg_mask, uint32_t null_mask,
+                    const float* a, const float* b, float* c,
+                    int64_t batch, void* stream);
+
+/* Fused backward of a binary product: one pass over gc produces
+ *   ga[k] = sum_j sigma_op(k, j) b[j] gf[k^j],  gb[k] = sum_i sigma_op(i, k) a[i] gf[i^k]
+ * (gf = gc, or gc[~.] for regressive). Replaces the reference's two forward-
+ * kernel launches per backward (extensions/ga/geom_prod.py:242-250 and the
+ * per-product backward wrappers). ga or gb may be NULL (that gradient is not
+ * needed). */
+int clf_product_bwd(int op, int n, uint32_t neg_mask, uint32_t null_mask,
+                    const float* a, const float* b, const float* gc,
+                    float* ga, float* gb, int64_t batch, void* stream);
+
+/* Single-pass graded op: y = kind(x). `grade` is used by PROJECTION only.
+ * DUAL / DUAL_ADJ need a non-degenerate metric. y must not alias x for the
+ * dual kinds (they permute). Replaces the eager torch passes of
+ * algebra.py:195-306. */
+int clf_graded(int kind, int n, uint32_t neg_mask, uint32_t null_mask, int grade,
+               const float* x, float* y, int64_t batch, void* stream);
+
+/* norm_sq: out[r] = sum_b x[r,b]^2 w[b], w[b] = prod_{k in b} metric[k]
+ * (ref algebra.py:309-334). */
+int clf_norm_sq_fwd(int n, uint32_t neg_mask, uint32_t null_mask,
+                    const float* x, float* out, int64_t batch, void* stream);
+
+/* Backward of norm_sq: gx[r,b] = 2 w[b] x[r,b] gout[r]. */
+int clf_norm_sq_bwd(int n, uint32_t neg_mask, uint32_t null_mask,
+                    const float* x, const float* gout, float* gx,
+                    int64_t batch, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CLIFFORD_HIP_H */

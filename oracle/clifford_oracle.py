@@ -1,0 +1,292 @@
+"""CPU oracle for the Clifford product & rotor hot path (TEST INFRASTRUCTURE).
+
+This module is the checker, never the product: only ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
+it. The shipped package (``cliffordcuda_amd``) never routes through it.
+
+It is a plain torch restatement (CPU, any float dtype; fp64 for parity) of the
+reference library's einsum/Cayley-table path:
+
+* ``sign_value_table``      follows ``src/cliffordcuda/extensions/ga/geom_prod.py:44-74``
+* ``product_masks``         follows ``_shared/_einsum_refs.py:58-83``
+* ``einsum_product``        follows ``_shared/_einsum_refs.py:26-55``
+                            (outer product x sign/mask table -> XOR scatter-add)
+* ``regressive``            follows ``_shared/_einsum_refs.py:86-124`` (dual o wedge o dual)
+* graded ops                follow ``src/cliffordcuda/algebra.py:195-334``
+* ``rotor_from_bivector`` / ``apply_bivector`` restate the composite of
+  ``src/cliffordcuda/algebra.py:343-373`` (eigh-exp -> Givens factor ->
+  Givens apply), which computes the Euclidean sandwich ``~R x R`` with
+  ``R = exp(sum_m b_m e_{i_m} e_{j_m})`` and the bivector in
+  ``torch.triu_indices(n, n, 1)`` order (``algebra.py:116-140``). The
+  reference ignores the metric on this path, so the oracle does too.
+
+Pinning (how each function is checked independently of its own formula) is
+listed per function below and exercised in ``tests/test_oracle.py``.
+Autograd through these functions is the backward oracle.
+"""
+from __future__ import annotations
+
+import math
+from functools import lru_cache
+
+import torch
+
+OPS = ("geom", "wedge", "inner", "lc", "rc", "regressive")
+
+
+def normalize_metric(n: int, metric) -> tuple:
+    """metric=None -> Cl(n,0); else a length-n tuple in {-1,0,1}.
+    Follows ``geom_prod.py:32-41``.
+    Pinned by: tests/test_oracle.py::test_normalize_metric."""
+    if metric is None:
+        return (1,) * n
+    metric = tuple(int(m) for m in metric)
+    if len(metric) != n:
+        raise ValueError(f"metric must have {n} entries, got {len(metric)}")
+    if any(m not in (-1, 0, 1) for m in metric):
+        raise ValueError(f"metric entries must be in {{-1, 0, 1}}, got {metric}")
+    return metric
+
+
+@lru_cache(maxsize=None)
+def _sign_value_table_cached(n: int, metric: tuple) -> torch.Tensor:
+    dim = 1 << n
+    i = torch.arange(dim, dtype=torch.int64).view(dim, 1).expand(dim, dim)
+    j = torch.arange(dim, dtype=torch.int64).view(1, dim).expand(dim, dim)
+    parity = torch.zeros(dim, dim, dtype=torch.int64)
+    # reorder parity: number of pairs (a, b), a > b, bit a of i and bit b of j
+    for a in range(n):
+        ia = (i >> a) & 1
+        for b in range(a):
+            parity += ia * ((j >> b) & 1)
+    sign = 1 - 2 * (parity & 1)
+    common = i & j
+    for k in range(n):
+        m = metric[k]
+        if m == 1:
+            continue
+        hit = ((common >> k) & 1).bool()
+        sign = torch.where(hit, sign * m, sign)
+    return sign.to(torch.int8)
+
+
+def sign_value_table(n: int, metric=None) -> torch.Tensor:
+    """sigma[i, j] in {-1, 0, +1}: e_i e_j = sigma[i, j] e_{i^j} in Cl(p,q,r),
+    bit-pattern blade order. Restates ``geom_prod.py:44-74``:
+    (-1)^{#(a>b: i_a=1, j_b=1)} * prod_{k in i&j} metric[k].
+    Pinned by: brute-force generator-list reordering (textbook canonical
+    ordering with contraction), real matrix representations (gamma matrices),
+    e_k^2 = metric[k], anticommutation and associativity."""
+    return _sign_value_table_cached(n, normalize_metric(n, metric))
+
+
+def product_masks(n: int, op: str) -> torch.Tensor:
+    """(D, D) bool mask of the (i, j) terms each product keeps.
+    Follows ``_einsum_refs.py:58-83``: geom all; wedge i&j==0; inner
+    (i sub j) or (j sub i); lc i sub j; rc j sub i.
+    Pinned by: grade-selection definitions on homogeneous inputs
+    (wedge = <AB>_{r+s}, lc = <AB>_{s-r}, rc = <AB>_{r-s}, inner = <AB>_{|r-s|})."""
+    dim = 1 << n
+    i = torch.arange(dim, dtype=torch.int64).view(dim, 1).expand(dim, dim)
+    j = torch.arange(dim, dtype=torch.int64).view(1, dim).expand(dim, dim)
+    if op == "geom":
+        return torch.ones(dim, dim, dtype=torch.bool)
+    if op == "wedge":
+        return (i & j) == 0
+    if op == "inner":
+        return ((i & ~j) == 0) | ((j & ~i) == 0)
+    if op == "lc":
+        return (i & j) == i
+    if op == "rc":
+        return (i & j) == j
+    raise ValueError(f"unknown op {op!r}")
+
+
+def _xor_scatter(a: torch.Tensor, b: torch.Tensor, signs: torch.Tensor) -> torch.Tensor:
+    """out[..., k] = sum_{i, j: i^j=k} signs[i, j] a[..., i] b[..., j].
+    The outer-product / scatter-add structure of ``_einsum_refs.py:26-55``,
+    chunked over the batch so large rows stay within memory."""
+    dim = a.shape[-1]
+    idx = torch.arange(dim)
+    xor_idx = (idx.view(-1, 1) ^ idx.view(1, -1)).reshape(-1)
+    s = signs.to(a.dtype)
+    rows = a.reshape(-1, dim)
+    cols = b.reshape(-1, dim)
+    chunk = max(1, (1 << 24) // (dim * dim))
+    outs = []
+    for r0 in range(0, rows.shape[0], chunk):
+        ra, rb = rows[r0:r0 + chunk], cols[r0:r0 + chunk]
+        outer = torch.einsum("bi,bj->bij", ra, rb) * s
+        flat = outer.reshape(outer.shape[0], -1)
+        out = torch.zeros(outer.shape[0], dim, dtype=a.dtype)
+        out = out.scatter_add(1, xor_idx.expand_as(flat), flat)
+        outs.append(out)
+    if not outs:
+        return torch.zeros_like(rows).reshape(a.shape)
+    return torch.cat(outs, 0).reshape(a.shape)
+
+
+def dual_perm_signs(n: int, metric) -> tuple:
+    """dual(x)[k] = x[~k] * s[k], s[k] = sigma[~k, full] / I^2.
+    Follows ``_einsum_refs.py:107-115``. Non-degenerate metrics only.
+    Pinned by: dual(x) == x * I^{-1} computed with the geometric product."""
+    metric = normalize_metric(n, metric)
+    if 0 in metric:
+        raise ValueError(f"dual undefined for degenerate metric {metric}")
+    sigma = sign_value_table(n, metric).to(torch.float64)
+    dim = 1 << n
+    full = dim - 1
+    isq = float(sigma[full, full])
+    comp = torch.arange(dim) ^ full
+    return comp, sigma[comp, full] / isq
+
+
+def dual(x: torch.Tensor, metric) -> torch.Tensor:
+    n = x.shape[-1].bit_length() - 1
+    comp, s = dual_perm_signs(n, metric)
+    return x.index_select(-1, comp) * s.to(x.dtype)
+
+
+def einsum_product(op: str, a: torch.Tensor, b: torch.Tensor, metric=None) -> torch.Tensor:
+    """The reference einsum product ``op`` (one of OPS) on (..., 2^n) inputs.
+    geom/wedge/inner/lc/rc follow ``_einsum_refs.py:26-83``; regressive
+    follows ``_einsum_refs.py:86-124`` as dual(dual(a) ^ dual(b))."""
+    n = a.shape[-1].bit_length() - 1
+    metric = normalize_metric(n, metric)
+    if op == "regressive":
+        if 0 in metric:
+            raise ValueError(f"regressive product undefined for degenerate metric {metric}")
+        return dual(einsum_product("wedge", dual(a, metric), dual(b, metric), metric), metric)
+    signs = sign_value_table(n, metric).to(torch.float64) * product_masks(n, op)
+    return _xor_scatter(a, b, signs)
+
+
+# ── graded ops (algebra.py:195-334) ─────────────────────────────────────────
+
+def grades(n: int) -> torch.Tensor:
+    idx = torch.arange(1 << n)
+    g = torch.zeros_like(idx)
+    for k in range(n):
+        g += (idx >> k) & 1
+    return g
+
+
+def reverse_signs(n: int) -> torch.Tensor:
+    """grade k -> (-1)^{k(k-1)/2} (``algebra.py:195-205``)."""
+    g = grades(n)
+    return torch.where(((g * (g - 1) // 2) % 2) == 1, -1.0, 1.0).to(torch.float64)
+
+
+def involution_signs(n: int) -> torch.Tensor:
+    """grade k -> (-1)^k (``algebra.py:278-286``)."""
+    return torch.where((grades(n) % 2) == 1, -1.0, 1.0).to(torch.float64)
+
+
+def conjugation_signs(n: int) -> torch.Tensor:
+    """grade k -> (-1)^{k(k+1)/2} (``algebra.py:288-296``)."""
+    g = grades(n)
+    return torch.where(((g * (g + 1) // 2) % 2) == 1, -1.0, 1.0).to(torch.float64)
+
+
+def reverse(x):
+    return x * reverse_signs(x.shape[-1].bit_length() - 1).to(x.dtype)
+
+
+def grade_involution(x):
+    return x * involution_signs(x.shape[-1].bit_length() - 1).to(x.dtype)
+
+
+def clifford_conjugation(x):
+    return x * conjugation_signs(x.shape[-1].bit_length() - 1).to(x.dtype)
+
+
+def grade_projection(x, grade: int):
+    """keep grade ``grade`` (``algebra.py:298-306``)."""
+    n = x.shape[-1].bit_length() - 1
+    return x * (grades(n) == grade).to(x.dtype)
+
+
+def norm_weights(n: int, metric) -> torch.Tensor:
+    """w[b] = prod_{i in b} metric[i] (``algebra.py:325-331``)."""
+    metric = normalize_metric(n, metric)
+    idx = torch.arange(1 << n)
+    w = torch.ones(1 << n, dtype=torch.float64)
+    for i in range(n):
+        w = w * torch.where(((idx >> i) & 1).bool(), float(metric[i]), 1.0)
+    return w
+
+
+def norm_sq(x, metric):
+    """<x ~x>_0 = sum_b x_b^2 w_b (``algebra.py:309-334``). Pinned by
+    norm_sq(x) == geom(x, reverse(x))[:, 0] (reference ``test_norm_sq.py:46-63``)."""
+    n = x.shape[-1].bit_length() - 1
+    return (x * x * norm_weights(n, metric).to(x.dtype)).sum(-1)
+
+
+# ── broadcast-weight layer (layers.py:30-50) ─────────────────────────────────
+
+def layer_forward(op: str, x: torch.Tensor, w: torch.Tensor, metric=None) -> torch.Tensor:
+    """``product(x, weight)`` with weight (1, 2^n) broadcast over the batch,
+    x on the left (``layers.py:43-47``)."""
+    return einsum_product(op, x, w.expand_as(x), metric)
+
+
+# ── rotor (algebra.py:337-373, Euclidean semantics) ─────────────────────────
+
+def bivector_blades(n: int):
+    """slot m <-> (i_m, j_m) = triu_indices(n, n, 1)[:, m] <-> blade 2^i + 2^j
+    (``algebra.py:124-126``, ``_rotor_apply_helpers.py:38-43``)."""
+    ij = torch.triu_indices(n, n, offset=1)
+    return [(int(i), int(j), (1 << int(i)) | (1 << int(j))) for i, j in ij.t()]
+
+
+def bivector_to_multivector(biv: torch.Tensor, n: int) -> torch.Tensor:
+    """(1, C(n,2)) lex-pair coefficients -> (1, 2^n) multivector sum b_m e_{i_m} e_{j_m}.
+    (e_i e_j with i < j is the bit-pattern blade 2^i+2^j with sign +1.)"""
+    out = torch.zeros(biv.shape[0], 1 << n, dtype=biv.dtype)
+    for m, (_, _, blade) in enumerate(bivector_blades(n)):
+        out = out.index_add(1, torch.tensor([blade]), biv[:, m:m + 1])
+    return out
+
+
+def rotor_from_bivector(biv: torch.Tensor, n: int, terms: int = 40) -> torch.Tensor:
+    """R = exp(B) in the Euclidean Cl(n,0) by scaling-and-squaring of the
+    Taylor series of the geometric-product exponential (fp64)."""
+    B = bivector_to_multivector(biv, n)
+    mag = float(B.abs().sum())
+    s = max(0, int(math.ceil(math.log2(mag + 1e-300))) + 2) if mag > 0.5 else 0
+    Bs = B / (2 ** s)
+    one = torch.zeros_like(B)
+    one[:, 0] = 1.0
+    R = one.clone()
+    term = one.clone()
+    for k in range(1, terms):
+        term = einsum_product("geom", term, Bs) / k
+        R = R + term
+    for _ in range(s):
+        R = einsum_product("geom", R, R)
+    return R
+
+
+def apply_bivector(biv: torch.Tensor, x: torch.Tensor, n: int | None = None) -> torch.Tensor:
+    """y = ~R x R with R = exp(sum b_m e_{i_m} e_{j_m}) (Euclidean). Restates
+    the composite ``compile_bivector`` + ``apply_rotor`` of ``algebra.py:343-373``.
+    Pinned by: grade-1 action equals expm(-B), B = 2(M - M^T), M[i_m, j_m] = b_m
+    (the matrix ``eigh_exp.cu:286-288`` builds), computed with an independent
+    matrix exponential; grade and norm preservation; ~R R = 1."""
+    if n is None:
+        n = x.shape[-1].bit_length() - 1
+    R = rotor_from_bivector(biv, n)
+    Rr = reverse(R)
+    Rb = R.expand_as(x)
+    return einsum_product("geom", einsum_product("geom", Rr.expand_as(x), x), Rb)
+
+
+def vector_rotation_matrix(biv: torch.Tensor, n: int) -> torch.Tensor:
+    """The n x n matrix the sandwich applies to grade-1 coefficients: y_vec = Q v."""
+    eye = torch.zeros(n, 1 << n, dtype=biv.dtype)
+    for a in range(n):
+        eye[a, 1 << a] = 1.0
+    y = apply_bivector(biv, eye, n)
+    cols = torch.stack([y[:, 1 << a] for a in range(n)], 0)  # (out a, in col)
+    return cols

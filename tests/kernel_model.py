@@ -1,0 +1,152 @@
+"""CPU model of the blocked product kernels in cliffordcuda_amd/csrc/products.hip.
+
+Restates, step by step, what the HIP kernels compute: the split of a blade
+index into (high block, 4-bit low part), the compile-time low sign pattern
+``low_sign``, the run-time high sign ``hi_sign``, the parity flip of the b
+operand, the INNER block-relation variants, the regressive output permutation
+and the fused backward. tests/test_kernel_model.py compares it with the oracle,
+so the sign factorisation the kernels rely on is checked on the CPU before any
+GPU run.
+"""
+import numpy as np
+
+GEOM, WEDGE, INNER, LC, RC, REGR = range(6)
+OPS = {"geom": GEOM, "wedge": WEDGE, "inner": INNER, "lc": LC, "rc": RC, "regressive": REGR}
+
+
+def popc(x):
+    return bin(x).count("1")
+
+
+def reorder(i, j):
+    return sum(popc(i >> (b + 1)) for b in range(32) if (j >> b) & 1)
+
+
+def bitsum(x):
+    return sum(a for a in range(32) if (x >> a) & 1)
+
+
+def low_sign(var, lowneg, il, jl):
+    pred = {GEOM: True, WEDGE: (il & jl) == 0,
+            INNER: ((il & ~jl) & 15) == 0 or ((jl & ~il) & 15) == 0,
+            LC: ((il & ~jl) & 15) == 0, RC: ((jl & ~il) & 15) == 0,
+            REGR: ((il | jl) & 15) == 15}[var]
+    if not pred:
+        return 0
+    p = reorder(il, jl)
+    if var == REGR:
+        p += bitsum(il) + bitsum(jl)
+    elif lowneg:
+        p += popc(il & jl)
+    return -1 if p & 1 else 1
+
+
+def hi_sign(op, ih, jh, negh, nulh, fullh, nm1, mu):
+    par = reorder(ih, jh)
+    if op == GEOM:
+        ok = (ih & jh & nulh) == 0
+        par += popc(ih & jh & negh)
+    elif op == WEDGE:
+        ok = (ih & jh) == 0
+    elif op in (INNER, LC, RC):
+        rel = {INNER: ((ih & ~jh) == 0) or ((jh & ~ih) == 0), LC: (ih & ~jh) == 0, RC: (jh & ~ih) == 0}[op]
+        ok = rel and (ih & jh & nulh) == 0
+        par += popc(ih & jh & negh)
+    else:
+        ok = (ih | jh) == fullh
+        par += (popc(ih & 0xAAAAAAAA) + popc(jh & 0xAAAAAAAA) + nm1 * popc(jh) + mu)
+    return ok, (-1.0 if par & 1 else 1.0)
+
+
+def cross_pi(op, x, nm1):
+    return (popc(x) + (nm1 if op == REGR else 0)) & 1
+
+
+def variant(op, ih, jh):
+    if op != INNER:
+        return op
+    l, r = (ih & ~jh) == 0, (jh & ~ih) == 0
+    return INNER if (l and r) else (LC if l else RC)
+
+
+def _tables(lowneg):
+    return {v: np.array([[low_sign(v, lowneg, il, jl) for jl in range(16)] for il in range(16)], dtype=np.float64)
+            for v in range(6)}
+
+
+PARITY16 = np.array([popc(e) & 1 for e in range(16)])
+
+
+def plan(op, metric):
+    n = len(metric)
+    neg = sum(1 << k for k, m in enumerate(metric) if m == -1)
+    nul = sum(1 << k for k, m in enumerate(metric) if m == 0)
+    if op in (WEDGE, REGR):
+        lowneg = False
+    else:
+        assert (nul & 15) == 0 and (neg & 15) in (0, 15), "generic path"
+        lowneg = (neg & 15) == 15
+    return dict(n=n, negh=neg >> 4, nulh=nul >> 4, nm1=(n - 1) & 1, mu=popc(neg) & 1,
+                fullh=(1 << (n - 4)) - 1, lowneg=lowneg)
+
+
+def forward(op_name, a, b, metric):
+    op = OPS[op_name]
+    P = plan(op, metric)
+    T = _tables(P["lowneg"])
+    NB = 1 << (P["n"] - 4)
+    A = a.reshape(a.shape[0], NB, 16)
+    B = b.reshape(b.shape[0], NB, 16)
+    out = np.zeros_like(A)
+    for kh in range(NB):
+        acc = np.zeros((a.shape[0], 16))
+        for ih in range(NB):
+            jh = ih ^ kh
+            ok, s = hi_sign(op, ih, jh, P["negh"], P["nulh"], P["fullh"], P["nm1"], P["mu"])
+            if not ok:
+                continue
+            pi = cross_pi(op, ih, P["nm1"])
+            bt = B[:, jh, :] * s * np.where(PARITY16 & pi, -1.0, 1.0)
+            tab = T[variant(op, ih, jh)]
+            for t in range(16):
+                il = np.arange(16)
+                acc[:, t] += (tab[il, il ^ t] * A[:, ih, il] * bt[:, il ^ t]).sum(-1)
+        if op == REGR:
+            out[:, P["fullh"] ^ kh, :] = acc[:, ::-1]
+        else:
+            out[:, kh, :] = acc
+    return out.reshape(a.shape)
+
+
+def backward(op_name, a, b, gc, metric):
+    op = OPS[op_name]
+    P = plan(op, metric)
+    T = _tables(P["lowneg"])
+    NB = 1 << (P["n"] - 4)
+    A = a.reshape(a.shape[0], NB, 16)
+    B = b.reshape(b.shape[0], NB, 16)
+    G = gc.reshape(gc.shape[0], NB, 16)
+    GA = np.zeros_like(A)
+    GB = np.zeros_like(A)
+    il = np.arange(16)
+    for h in range(NB):
+        pi_h = cross_pi(op, h, P["nm1"])
+        for m in range(NB):
+            x = h ^ m
+            g = G[:, P["fullh"] ^ x, ::-1] if op == REGR else G[:, x, :]
+            oka, sa = hi_sign(op, h, m, P["negh"], P["nulh"], P["fullh"], P["nm1"], P["mu"])
+            okb, sb = hi_sign(op, m, h, P["negh"], P["nulh"], P["fullh"], P["nm1"], P["mu"])
+            if oka:
+                bt = B[:, m, :] * sa * np.where(PARITY16 & pi_h, -1.0, 1.0)
+                tab = T[variant(op, h, m)]
+                for jl in range(16):
+                    GA[:, h, :] += tab[il, jl] * bt[:, jl:jl + 1] * g[:, il ^ jl]
+            if okb:
+                pm = cross_pi(op, m, P["nm1"])
+                fl = np.where(PARITY16 & pm, -1.0, 1.0)
+                at = A[:, m, :] * sb * fl
+                gt = g * fl
+                tab = T[variant(op, m, h)]
+                for jl in range(16):
+                    GB[:, h, jl] += (tab[il, jl] * at[:, il] * gt[:, il ^ jl]).sum(-1)
+    return GA.reshape(a.shape), GB.reshape(a.shape)

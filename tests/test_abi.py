@@ -1,0 +1,82 @@
+"""The C ABI library loads on a host without a GPU, exports every symbol
+include/clifford_hip.h declares, and rejects bad arguments before any HIP
+call (no compute is launched here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from cliffordcuda_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    names = set()
+    for fn in os.listdir(os.path.join(ROOT, "include")):
+        if fn.endswith(".h"):
+            text = open(os.path.join(ROOT, "include", fn)).read()
+            names |= set(re.findall(r"^\s*(?:const\s+)?[a-z_]+\*?\s+\*?(clf_[a-z0-9_]+)\s*\(", text, re.M))
+    return names
+
+
+def test_all_declared_symbols_exported():
+    lib = _lib.load()
+    decl = declared_symbols()
+    assert "clf_product_fwd" in decl and len(decl) >= 9
+    for name in decl:
+        assert hasattr(lib, name), name
+    assert decl == set(_lib.SIGNATURES), decl ^ set(_lib.SIGNATURES)
+
+
+def test_abi_version_and_limits():
+    lib = _lib.load()
+    assert lib.clf_abi_version() == 1
+    assert lib.clf_product_max_n() >= 10
+
+
+@pytest.mark.parametrize("args,code,msg", [
+    ((9, 5, 0, 0, None, None, None, 4, None), 1, "unknown product op"),
+    ((0, 0, 0, 0, None, None, None, 4, None), 1, "n must be in"),
+    ((0, 13, 0, 0, None, None, None, 4, None), 1, "n must be in"),
+    ((0, 5, 1 << 5, 0, None, None, None, 4, None), 1, "bits above n"),
+    ((0, 5, 3, 2, None, None, None, 4, None), 1, "overlap"),
+    ((0, 5, 0, 0, None, None, None, -1, None), 1, "batch"),
+    ((5, 5, 0, 1, None, None, None, 4, None), 2, "degenerate"),
+    ((0, 5, 0, 0, None, None, None, 4, None), 1, "null pointer"),
+    ((0, 5, 0, 0, 16, 16, 16, 4, None), 1, "alias"),
+    ((0, 5, 0, 0, 16, 32, 8, 4, None), 1, "aligned"),
+])
+def test_product_fwd_argument_errors(args, code, msg):
+    lib = _lib.load()
+    assert lib.clf_product_fwd(*args) == code
+    assert msg in _lib.last_error()
+
+
+def test_zero_batch_is_noop_and_clears_error():
+    lib = _lib.load()
+    lib.clf_product_fwd(9, 5, 0, 0, None, None, None, 4, None)
+    assert _lib.last_error()
+    assert lib.clf_product_fwd(0, 5, 0, 0, None, None, None, 0, None) == 0
+    assert _lib.last_error() == ""
+    assert lib.clf_product_bwd(0, 5, 0, 0, None, None, None, None, None, 7, None) == 0  # no grads requested
+
+
+def test_graded_and_norm_errors():
+    lib = _lib.load()
+    assert lib.clf_graded(9, 5, 0, 0, 0, None, None, 1, None) == 1
+    assert lib.clf_graded(3, 5, 0, 0, 6, None, None, 1, None) == 1
+    assert "grade must be in" in _lib.last_error()
+    assert lib.clf_graded(4, 5, 0, 1, 0, None, None, 1, None) == 2
+    assert lib.clf_graded(4, 5, 0, 0, 0, 16, 16, 1, None) == 1
+    assert lib.clf_norm_sq_fwd(5, 0, 0, None, None, 3, None) == 1
+    assert lib.clf_norm_sq_bwd(0, 0, 0, None, None, None, 3, None) == 1
+
+
+def test_status_mapping():
+    with pytest.raises(ValueError):
+        _lib.check(_lib.CLF_ERR_ARG, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.CLF_ERR_HIP, "x")
+    _lib.check(_lib.CLF_OK, "x")

@@ -1,0 +1,212 @@
+"""GPU parity of the six binary products (forward + fused backward) against the
+fp64 CPU oracle on identical seeded inputs. Bar: normwise relative error
+max|y - y_ref| / max|y_ref| <= 1e-5 for values and both gradients (the
+tolerance BASELINE.json's north star states)."""
+import pytest
+import torch
+
+import cliffordcuda_amd as cc
+from oracle import clifford_oracle as O
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def rel_err(got, ref):
+    got = got.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    den = float(ref.abs().max())
+    return float((got - ref).abs().max()) / (den if den > 0 else 1.0)
+
+
+def seeded(b, n, seed, count):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(b, 1 << n, generator=g) for _ in range(count)]
+
+
+def run_case(op, metric, batch, seed=0):
+    n = len(metric)
+    a, b, gc = seeded(batch, n, seed, 3)
+    ad = a.cuda().requires_grad_()
+    bd = b.cuda().requires_grad_()
+    c = cc.products.product(op, ad, bd, metric)
+    c.backward(gc.cuda())
+    a64 = a.double().requires_grad_()
+    b64 = b.double().requires_grad_()
+    c64 = O.einsum_product(op, a64, b64, metric)
+    c64.backward(gc.double())
+    print(f"[case] op={op} metric={metric} batch={batch}", flush=True)
+    return rel_err(c, c64), rel_err(ad.grad, a64.grad), rel_err(bd.grad, b64.grad)
+
+
+# blocked-path metrics (low 4 generators all +1 / all -1, no null there) and
+# generic-path metrics (n < 4, mixed or null low generators)
+METRICS = [
+    (1, 1, 1, 1, 1),
+    (-1, -1, -1, -1, -1),
+    (1, 1, 1, 1, -1),
+    (1, 1, 1, 1, 0),
+    (1, 1, 1, 1, 1, -1, 0),
+    (1, 1, 1, 1, 1, 1, 1, 1),
+    (1, 1, 1, -1, 0),          # generic: mixed low generators
+    (1, 1, 0),                 # generic: n < 4
+    (-1, 1, -1, 1, 1, 1),      # generic
+    (1,) * 9 + (0,),           # C5 signature
+]
+
+
+@pytest.mark.parametrize("metric", METRICS, ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
+@pytest.mark.parametrize("op", O.OPS)
+def test_product_parity(op, metric):
+    if op == "regressive" and 0 in metric:
+        pytest.skip("regressive undefined for degenerate metrics")
+    batch = 8 if len(metric) >= 10 else 37   # odd batch: partial workgroups
+    e = run_case(op, metric, batch)
+    assert max(e) <= TOL, e
+
+
+def test_c1_cl50_geom_forward():
+    """Cl(5,0) GP forward, batch 1024, seed 0."""
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(1024, 32, generator=g)
+    b = torch.randn(1024, 32, generator=g)
+    cl = cc.CliffordAlgebra([1] * 5, device="cuda")
+    c = cl.geom_prod(a.cuda(), b.cuda())
+    ref = O.einsum_product("geom", a.double(), b.double(), (1,) * 5)
+    assert rel_err(c, ref) <= TOL
+
+
+def test_c2_cl61_six_products_full_batch():
+    """Cl(6,1), batch 65536, all six products fwd + bwd,
+    upstream gradient all-ones. The oracle checks a 2048-row sample (first,
+    last and strided rows); the full batch is checked by bilinearity."""
+    metric = (1, 1, 1, 1, 1, 1, -1)
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(65536, 128, generator=g)
+    b = torch.randn(65536, 128, generator=g)
+    rows = torch.cat([torch.arange(0, 1024), torch.arange(65536 - 512, 65536), torch.arange(1024, 65536 - 512, 127)])
+    cl = cc.CliffordAlgebra(metric, device="cuda")
+    ad = a.cuda()
+    bd = b.cuda()
+    for op, meth in (("geom", cl.geom_prod), ("wedge", cl.wedge_prod), ("inner", cl.inner_prod),
+                     ("lc", cl.left_contraction), ("rc", cl.right_contraction), ("regressive", cl.regressive_prod)):
+        x = ad.clone().requires_grad_()
+        y = bd.clone().requires_grad_()
+        c = meth(x, y)
+        c.backward(torch.ones_like(c))
+        a64 = a[rows].double().requires_grad_()
+        b64 = b[rows].double().requires_grad_()
+        c64 = O.einsum_product(op, a64, b64, metric)
+        c64.backward(torch.ones_like(c64))
+        rs = rows.cuda()
+        assert rel_err(c[rs], c64) <= TOL, op
+        assert rel_err(x.grad[rs], a64.grad) <= TOL, op
+        assert rel_err(y.grad[rs], b64.grad) <= TOL, op
+        # bilinearity over the whole batch: op(a, b + 2a) = op(a, b) + 2 op(a, a)
+        with torch.no_grad():
+            lhs = meth(ad, bd + 2 * ad)
+            rhs = c + 2 * meth(ad, ad)
+            assert rel_err(lhs, rhs) <= 1e-5, op
+
+
+def test_c5_degenerate_n10():
+    """Cl(9,0,1), GP and lc fwd + bwd, then norm_sq and
+    grade_projection(2) of the product (oracle on 16 rows of the batch; the
+    full batch of 16384 is exercised for finiteness and row independence)."""
+    metric = (1,) * 9 + (0,)
+    g = torch.Generator().manual_seed(0)
+    B = 16384
+    a = torch.randn(B, 1024, generator=g)
+    b = torch.randn(B, 1024, generator=g)
+    cl = cc.CliffordAlgebra(metric, device="cuda")
+    x = a.cuda().requires_grad_()
+    y = b.cuda().requires_grad_()
+    gp = cl.geom_prod(x, y)
+    lc = cl.left_contraction(x, y)
+    ns = cl.norm_sq(gp)
+    pr = cl.grade_projection(gp, 2)
+    (gp.sum() + lc.sum() + ns.sum() + pr.sum()).backward()
+    rows = torch.tensor([0, 1, 2, 3, 100, 5000, 9999, B - 1])
+    a64 = a[rows].double().requires_grad_()
+    b64 = b[rows].double().requires_grad_()
+    gp64 = O.einsum_product("geom", a64, b64, metric)
+    lc64 = O.einsum_product("lc", a64, b64, metric)
+    ns64 = O.norm_sq(gp64, metric)
+    pr64 = O.grade_projection(gp64, 2)
+    (gp64.sum() + lc64.sum() + ns64.sum() + pr64.sum()).backward()
+    rs = rows.cuda()
+    assert rel_err(gp[rs], gp64) <= TOL
+    assert rel_err(lc[rs], lc64) <= TOL
+    assert rel_err(ns[rs], ns64) <= TOL
+    assert rel_err(pr[rs], pr64) <= TOL
+    assert rel_err(x.grad[rs], a64.grad) <= TOL
+    assert rel_err(y.grad[rs], b64.grad) <= TOL
+    assert torch.isfinite(x.grad).all() and torch.isfinite(y.grad).all()
+
+
+def test_headline_shape_row_independence():
+    """Headline shape Cl(8,0), batch 262144: rows computed at full batch equal
+    the same rows computed alone (size-independent property), and a sample of
+    rows matches the oracle."""
+    g = torch.Generator().manual_seed(0)
+    B = 262144
+    a = torch.randn(B, 256, generator=g).cuda()
+    b = torch.randn(B, 256, generator=g).cuda()
+    c = cc.geom_prod(a, b)
+    idx = torch.tensor([0, 17, 65535, 131072, B - 1], device="cuda")
+    c_small = cc.geom_prod(a[idx].contiguous(), b[idx].contiguous())
+    assert torch.equal(c[idx], c_small)
+    ref = O.einsum_product("geom", a[idx].double().cpu(), b[idx].double().cpu())
+    assert rel_err(c[idx], ref) <= TOL
+
+
+def test_edge_batches_and_layouts():
+    cl = cc.CliffordAlgebra([1] * 6, device="cuda")
+    empty = torch.empty(0, 64, device="cuda")
+    assert cl.geom_prod(empty, empty).shape == (0, 64)
+    one = torch.randn(1, 64, device="cuda")
+    ref = O.einsum_product("geom", one.double().cpu(), one.double().cpu())
+    assert rel_err(cl.geom_prod(one, one), ref) <= TOL
+    # free functions accept non-contiguous inputs and leading dims
+    x = torch.randn(64, 3, device="cuda").t()   # (3, 64) non-contiguous
+    y = torch.randn(3, 64, device="cuda")
+    got = cc.geom_prod(x, y)
+    assert rel_err(got, O.einsum_product("geom", x.double().cpu(), y.double().cpu())) <= TOL
+    z = torch.randn(2, 5, 64, device="cuda")
+    got = cc.wedge_prod(z, z)
+    assert got.shape == (2, 5, 64)
+
+
+def test_validation_errors():
+    cl = cc.CliffordAlgebra([1] * 5, device="cuda")
+    a = torch.randn(4, 32, device="cuda")
+    with pytest.raises(ValueError, match="must be 2D"):
+        cl.geom_prod(a.view(4, 2, 16), a.view(4, 2, 16))
+    with pytest.raises(ValueError, match="last dim"):
+        cl.geom_prod(a[:, :16].contiguous(), a[:, :16].contiguous())
+    with pytest.raises(ValueError, match="dtype"):
+        cl.geom_prod(a.double(), a.double())
+    with pytest.raises(ValueError, match="contiguous"):
+        cl.geom_prod(a.t().contiguous().t(), a)
+    with pytest.raises(ValueError, match="degenerate"):
+        cc.CliffordAlgebra([1, 1, 1, 1, 0], device="cuda").regressive_prod(a, a)
+    with pytest.raises(ValueError, match="grade must be in"):
+        cl.grade_projection(a, 6)
+
+
+@pytest.mark.parametrize("n", [5, 7])
+def test_gradcheck_signatures(n):
+    """The reference's gradcheck spread (tests/_gradcheck.py:9-19): six
+    signatures per n, fp64 finite differences through the fp32 kernels."""
+    sigs = [(1,) * n, (-1,) * n, (1,) * (n - 1) + (-1,), (1,) * (n // 2) + (-1,) * (n - n // 2),
+            (1,) * (n - 1) + (0,), (1,) * (n - 2) + (-1, 0)]
+    tol = max(1e-3, (1 << n) * 3e-5)
+    for metric in sigs:
+        for op in O.OPS:
+            if op == "regressive" and 0 in metric:
+                continue
+            torch.manual_seed(0)
+            a = torch.randn(2, 1 << n, dtype=torch.float64, device="cuda", requires_grad=True)
+            b = torch.randn(2, 1 << n, dtype=torch.float64, device="cuda", requires_grad=True)
+            fn = lambda x, y: cc.products.product(op, x.float(), y.float(), metric).double()  # noqa: E731
+            assert torch.autograd.gradcheck(fn, (a, b), eps=1e-3, atol=tol, rtol=tol, nondet_tol=tol), (op, metric)
