@@ -51,6 +51,12 @@ SIGNATURES = {
     "clf_graded": (_i32, [_i32, _i32, _u32, _u32, _i32, _vp, _vp, _i64, _vp]),
     "clf_norm_sq_fwd": (_i32, [_i32, _u32, _u32, _vp, _vp, _i64, _vp]),
     "clf_norm_sq_bwd": (_i32, [_i32, _u32, _u32, _vp, _vp, _vp, _i64, _vp]),
+    "clf_rotor_state_floats": (_i32, [_i32]),
+    "clf_rotor_compile_fwd": (_i32, [_i32, _vp, _vp, _vp]),
+    "clf_rotor_compile_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp]),
+    "clf_rotor_apply_fwd": (_i32, [_i32, _vp, _vp, _vp, _i64, _vp]),
+    "clf_rotor_apply_ws_bytes": (_sz, [_i32, _i64]),
+    "clf_rotor_apply_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
 }
 
 _lock = threading.Lock()

@@ -24,6 +24,14 @@ int norm_sq_fwd(int n, uint32_t neg, uint32_t nul, const float* x, float* out, i
 int norm_sq_bwd(int n, uint32_t neg, uint32_t nul, const float* x, const float* gout, float* gx, int64_t batch,
                 void* stream);
 
+int rotor_state_floats(int n);
+size_t rotor_apply_ws_bytes(int n, int64_t batch);
+int rotor_compile_fwd(int n, const float* biv, float* state, void* stream);
+int rotor_compile_bwd(int n, const float* biv, const float* g_state, float* g_biv, void* stream);
+int rotor_apply_fwd(int n, const float* state, const float* x, float* y, int64_t batch, void* stream);
+int rotor_apply_bwd(int n, const float* state, const float* x, const float* gy, float* gx, float* g_state,
+                    int64_t batch, void* ws, size_t ws_bytes, void* stream);
+
 }  // namespace clf
 
 extern "C" {
@@ -79,6 +87,31 @@ int clf_norm_sq_bwd(int n, uint32_t neg_mask, uint32_t null_mask, const float* x
                     int64_t batch, void* stream) {
     clf::clear_error();
     return clf::norm_sq_bwd(n, neg_mask, null_mask, x, gout, gx, batch, stream);
+}
+
+int clf_rotor_state_floats(int n) { return clf::rotor_state_floats(n); }
+
+int clf_rotor_compile_fwd(int n, const float* biv, float* state, void* stream) {
+    clf::clear_error();
+    return clf::rotor_compile_fwd(n, biv, state, stream);
+}
+
+int clf_rotor_compile_bwd(int n, const float* biv, const float* g_state, float* g_biv, void* stream) {
+    clf::clear_error();
+    return clf::rotor_compile_bwd(n, biv, g_state, g_biv, stream);
+}
+
+int clf_rotor_apply_fwd(int n, const float* state, const float* x, float* y, int64_t batch, void* stream) {
+    clf::clear_error();
+    return clf::rotor_apply_fwd(n, state, x, y, batch, stream);
+}
+
+size_t clf_rotor_apply_ws_bytes(int n, int64_t batch) { return clf::rotor_apply_ws_bytes(n, batch); }
+
+int clf_rotor_apply_bwd(int n, const float* state, const float* x, const float* gy, float* gx, float* g_state,
+                        int64_t batch, void* ws, size_t ws_bytes, void* stream) {
+    clf::clear_error();
+    return clf::rotor_apply_bwd(n, state, x, gy, gx, g_state, batch, ws, ws_bytes, stream);
 }
 
 }  // extern "C"

@@ -1,10 +1,102 @@
-"""Rotor compile (bivector -> rotor state) and sandwich application."""
+"""Rotor compile (bivector -> rotor state) and the sandwich ~R x R, differentiable
+to the bivector and to x, on the gfx950 kernels (``clf_rotor_*``).
+
+Semantics are the reference's composite ``compile_bivector`` + ``apply_rotor``
+(``src/cliffordcuda/algebra.py:343-373``): Euclidean rotor
+R = exp(sum_m b_m e_{i_m} e_{j_m}), bivector slots in ``triu_indices(n, n, 1)``
+order, y = ~R x R, whatever the algebra's metric (the reference ignores it on
+this path too). The rotor state is a 1-D float tensor (rotation matrix + its
+plane-rotation chain) that ``apply_rotor`` consumes; it is produced in one
+kernel launch with no host synchronisation.
+"""
 from __future__ import annotations
 
+import torch
 
-def compile_bivector(bivector, n):
-    raise NotImplementedError("rotor path not built yet")
+from . import _lib
 
 
-def apply_rotor(state, x, n):
-    raise NotImplementedError("rotor path not built yet")
+def _state_len(n: int) -> int:
+    k = _lib.load().clf_rotor_state_floats(n)
+    if k < 0:
+        raise ValueError(f"rotor kernels support 2 <= n <= 10; got n={n}")
+    return k
+
+
+class _CompileFunc(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, biv, n):
+        biv = biv.contiguous()
+        state = torch.empty(_state_len(n), dtype=torch.float32, device=biv.device)
+        lib = _lib.load()
+        with torch.cuda.device(biv.device):
+            rc = lib.clf_rotor_compile_fwd(n, biv.data_ptr(), state.data_ptr(), _lib.stream_of(biv))
+        _lib.check(rc, "clf_rotor_compile_fwd")
+        ctx.save_for_backward(biv)
+        ctx.n = n
+        return state
+
+    @staticmethod
+    def backward(ctx, g_state):
+        (biv,) = ctx.saved_tensors
+        g_state = g_state.contiguous()
+        g_biv = torch.empty_like(biv)
+        lib = _lib.load()
+        with torch.cuda.device(biv.device):
+            rc = lib.clf_rotor_compile_bwd(ctx.n, biv.data_ptr(), g_state.data_ptr(), g_biv.data_ptr(),
+                                           _lib.stream_of(biv))
+        _lib.check(rc, "clf_rotor_compile_bwd")
+        return g_biv, None
+
+
+class _ApplyFunc(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, state, x, n):
+        y = torch.empty_like(x)
+        lib = _lib.load()
+        with torch.cuda.device(x.device):
+            rc = lib.clf_rotor_apply_fwd(n, state.data_ptr(), x.data_ptr(), y.data_ptr(), x.shape[0],
+                                         _lib.stream_of(x))
+        _lib.check(rc, "clf_rotor_apply_fwd")
+        ctx.save_for_backward(state, x)
+        ctx.n = n
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        state, x = ctx.saved_tensors
+        n = ctx.n
+        need_state, need_x = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        if not (need_state or need_x):
+            return None, None, None
+        gy = gy.contiguous()
+        gx = torch.empty_like(x) if need_x else None
+        g_state = torch.empty_like(state) if need_state else None
+        lib = _lib.load()
+        ws = None
+        ws_bytes = 0
+        if need_state:
+            ws_bytes = lib.clf_rotor_apply_ws_bytes(n, x.shape[0])
+            ws = torch.empty(max(1, ws_bytes // 4), dtype=torch.float32, device=x.device)
+        with torch.cuda.device(x.device):
+            rc = lib.clf_rotor_apply_bwd(n, state.data_ptr(), x.data_ptr(), gy.data_ptr(), _lib.ptr(gx),
+                                         _lib.ptr(g_state), x.shape[0], _lib.ptr(ws), ws_bytes,
+                                         _lib.stream_of(x))
+        _lib.check(rc, "clf_rotor_apply_bwd")
+        return g_state, gx, None
+
+
+def compile_bivector(bivector: torch.Tensor, n: int) -> torch.Tensor:
+    """(1, C(n,2)) bivector -> rotor state (1-D). Differentiable."""
+    return _CompileFunc.apply(bivector.reshape(-1), n)
+
+
+def apply_rotor(state: torch.Tensor, x: torch.Tensor, n: int) -> torch.Tensor:
+    """y = ~R x R for x (batch, 2^n). Differentiable to the state and to x."""
+    if state.dim() != 1 or state.numel() != _state_len(n):
+        raise ValueError(
+            f"rotor state must be the 1-D tensor compile_bivector returns ({_state_len(n)} floats for "
+            f"n={n}); got shape {tuple(state.shape)}")
+    if state.device != x.device:
+        raise ValueError(f"rotor state on device {state.device}, x on {x.device}")
+    return _ApplyFunc.apply(state.contiguous(), x, n)

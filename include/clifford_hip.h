@@ -118,6 +118,44 @@ int clf_norm_sq_bwd(int n, uint32_t neg_mask, uint32_t null_mask,
                     const float* x, const float* gout, float* gx,
                     int64_t batch, void* stream);
 
+
+/* ---- rotor: bivector -> rotor state -> sandwich ~R x R --------------------
+ * Replaces the reference chain eigh_exp_fwd/bwd (kernels/rotor/eigh_exp.cu:270-361),
+ * givens_factor_fwd_v2/bwd_v2 (kernels/rotor/givens_factor.cu:176-231) and
+ * givens_mb_perm_packed_fwd/bwd (kernels/rotor/givens_apply_mb_perm_packed.cu:250-292),
+ * as wired by src/cliffordcuda/algebra.py:343-373. Euclidean semantics, like the
+ * reference: y = ~R x R, R = exp(sum_m b_m e_{i_m} e_{j_m}), bivector slots in
+ * triu_indices(n, n, 1) order. Supported n: 2..10.
+ *
+ * Rotor state layout (clf_rotor_state_floats(n) floats): the n x n rotation
+ * Q = expm(-2 (M - M^T)) acting on grade-1 coefficients (row-major), followed by
+ * the C(n,2) (c, s) pairs of its plane-rotation factorisation. */
+
+/* Number of floats of the rotor state for n, or -1 if n is unsupported. */
+int clf_rotor_state_floats(int n);
+
+/* state = compile(biv); biv: C(n,2) floats. One single-workgroup launch, no host sync. */
+int clf_rotor_compile_fwd(int n, const float* biv, float* state, void* stream);
+
+/* g_biv = d/d(biv) of <g_state, compile(biv)>, reading only the Q block of
+ * g_state (the chain block is a derived cache and carries no gradient). */
+int clf_rotor_compile_bwd(int n, const float* biv, const float* g_state, float* g_biv, void* stream);
+
+/* y = ~R x R for `batch` rows. y must not alias x. */
+int clf_rotor_apply_fwd(int n, const float* state, const float* x, float* y,
+                        int64_t batch, void* stream);
+
+/* Bytes of device workspace clf_rotor_apply_bwd needs when g_state != NULL. */
+size_t clf_rotor_apply_ws_bytes(int n, int64_t batch);
+
+/* Backward of the sandwich: gx = R gy ~R (the transpose of the action),
+ * g_state = dL/d(state) (Q block = dL/dQ, chain block = 0). gx or g_state may be
+ * NULL. x is read only when g_state != NULL. The reference returns no gradient
+ * to x (extensions/rotor/givens_apply/mb_perm_packed.py:34-42). */
+int clf_rotor_apply_bwd(int n, const float* state, const float* x, const float* gy,
+                        float* gx, float* g_state, int64_t batch,
+                        void* ws, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -253,7 +253,7 @@ def rotor_from_bivector(biv: torch.Tensor, n: int, terms: int = 40) -> torch.Ten
     """R = exp(B) in the Euclidean Cl(n,0) by scaling-and-squaring of the
     Taylor series of the geometric-product exponential (fp64)."""
     B = bivector_to_multivector(biv, n)
-    mag = float(B.abs().sum())
+    mag = float(B.detach().abs().sum())
     s = max(0, int(math.ceil(math.log2(mag + 1e-300))) + 2) if mag > 0.5 else 0
     Bs = B / (2 ** s)
     one = torch.zeros_like(B)

@@ -1,0 +1,30 @@
+"""The rotor kernels' math (tests/rotor_model.py) equals the oracle's
+Euclidean sandwich and its autograd gradients."""
+import numpy as np
+import scipy.linalg
+import torch
+
+from oracle import clifford_oracle as O
+from tests import rotor_model as M
+
+
+def test_rotor_model_matches_oracle():
+    n = 5
+    g = torch.Generator().manual_seed(1)
+    biv = 0.6 * torch.randn(1, 10, generator=g, dtype=torch.float64)
+    x = torch.randn(3, 32, generator=g, dtype=torch.float64)
+    gy = torch.randn(3, 32, generator=g, dtype=torch.float64)
+    bq = biv.clone().requires_grad_()
+    xq = x.clone().requires_grad_()
+    y = O.apply_bivector(bq, xq, n)
+    y.backward(gy)
+    Q = scipy.linalg.expm(M.generator(biv[0].numpy(), n))
+    cs, E = M.givens(Q)
+    np.testing.assert_allclose(E, np.eye(n), atol=1e-12)
+    ym = M.apply(cs, x.numpy())
+    np.testing.assert_allclose(ym, y.detach().numpy(), atol=1e-12)
+    gx = M.apply(cs, gy.numpy(), transpose=True)
+    np.testing.assert_allclose(gx, xq.grad.numpy(), atol=1e-12)
+    G = M.gamma(x.numpy(), gx, n)
+    gb = M.compile_bwd(biv[0].numpy(), n, Q @ G)
+    np.testing.assert_allclose(gb, bq.grad[0].numpy(), atol=1e-10)
