@@ -32,6 +32,12 @@ int rotor_apply_fwd(int n, const float* state, const float* x, float* y, int64_t
 int rotor_apply_bwd(int n, const float* state, const float* x, const float* gy, float* gx, float* g_state,
                     int64_t batch, void* ws, size_t ws_bytes, void* stream);
 
+size_t bcast_ws_bytes(int n, int64_t batch);
+int bcast_fwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w, float* y,
+              int64_t batch, void* ws, size_t ws_bytes, void* stream);
+int bcast_bwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w, const float* gy,
+              float* gx, float* gw, int64_t batch, void* ws, size_t ws_bytes, void* stream);
+
 }  // namespace clf
 
 extern "C" {
@@ -112,6 +118,21 @@ int clf_rotor_apply_bwd(int n, const float* state, const float* x, const float* 
                         int64_t batch, void* ws, size_t ws_bytes, void* stream) {
     clf::clear_error();
     return clf::rotor_apply_bwd(n, state, x, gy, gx, g_state, batch, ws, ws_bytes, stream);
+}
+
+size_t clf_product_bcast_ws_bytes(int n, int64_t batch) { return clf::bcast_ws_bytes(n, batch); }
+
+int clf_product_bcast_fwd(int op, int side, int n, uint32_t neg_mask, uint32_t null_mask, const float* x,
+                          const float* w, float* y, int64_t batch, void* ws, size_t ws_bytes, void* stream) {
+    clf::clear_error();
+    return clf::bcast_fwd(op, side, n, neg_mask, null_mask, x, w, y, batch, ws, ws_bytes, stream);
+}
+
+int clf_product_bcast_bwd(int op, int side, int n, uint32_t neg_mask, uint32_t null_mask, const float* x,
+                          const float* w, const float* gy, float* gx, float* gw, int64_t batch, void* ws,
+                          size_t ws_bytes, void* stream) {
+    clf::clear_error();
+    return clf::bcast_bwd(op, side, n, neg_mask, null_mask, x, w, gy, gx, gw, batch, ws, ws_bytes, stream);
 }
 
 }  // extern "C"

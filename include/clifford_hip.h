@@ -156,6 +156,27 @@ int clf_rotor_apply_bwd(int n, const float* state, const float* x, const float* 
                         float* gx, float* g_state, int64_t batch,
                         void* ws, size_t ws_bytes, void* stream);
 
+/* ---- broadcast-weight products (the product layers) ---------------------
+ * y = op(x, w) (side 0, x on the left, as the reference layers compute it,
+ * src/cliffordcuda/layers.py:43-47) or y = op(w, x) (side 1), with one weight
+ * multivector w (2^n floats) shared by all `batch` rows of x. Replaces the
+ * layer path expand -> per-row kernel -> autograd batch sum. Implemented as
+ * fp32 MFMA GEMMs against the signed 2^n x 2^n matrix of w. Supported n: 7..10.
+ * ws: device workspace of clf_product_bcast_ws_bytes(n, batch) bytes, 16-byte
+ * aligned, owned by the caller; calls that share a workspace must not overlap. */
+size_t clf_product_bcast_ws_bytes(int n, int64_t batch);
+
+int clf_product_bcast_fwd(int op, int side, int n, uint32_t neg_mask, uint32_t null_mask,
+                          const float* x, const float* w, float* y, int64_t batch,
+                          void* ws, size_t ws_bytes, void* stream);
+
+/* gx = dL/dx (batch x 2^n) and gw = dL/dw (2^n, summed over the batch); either
+ * may be NULL. */
+int clf_product_bcast_bwd(int op, int side, int n, uint32_t neg_mask, uint32_t null_mask,
+                          const float* x, const float* w, const float* gy,
+                          float* gx, float* gw, int64_t batch,
+                          void* ws, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
