@@ -1,14 +1,16 @@
-"""Headline benchmark: Cl(8,0) geometric product, forward + backward, fp32,
-batch 262144, one MI355X (BASELINE.json metric "multivector-pairs/s fwd+bwd,
-Cl(8,0) fp32, 1 MI355X; % FP32 VALU/MFMA peak").
+"""Benchmarks of the product & rotor hot path on one MI355X.
 
-One step = ``c = cl.geom_prod(a, b)`` + ``torch.autograd.grad(c, (a, b), gc)``
-with gc all-ones, inputs resident in HBM. Prints ONE JSON line.
+Default (the driver's contract): the headline workload of BASELINE.json's
+metric, "multivector-pairs/s fwd+bwd, Cl(8,0) fp32, 1 MI355X; % FP32 VALU/MFMA
+peak": Cl(8,0) geometric product, batch 262144, forward + backward, inputs
+resident in HBM. One step = ``c = cl.geom_prod(a, b)`` +
+``torch.autograd.grad(c, (a, b), gc)`` with gc all-ones. Prints ONE JSON line
+with a ``roofline`` object for the dominant kernel (timed with HIP events on
+the stream it runs on) and a ``cpu_baseline`` object (the oracle's einsum
+restatement timed on this host's cores on a bounded sample).
 
-The JSON carries a ``roofline`` object for the dominant kernel (the fused
-backward) timed with HIP events on the stream it runs on, and a
-``cpu_baseline`` object: the oracle's einsum restatement (torch fp32) timed on
-this host's cores on a bounded sample of the same workload.
+``--workload all`` (or c1..c5) additionally measures the other BASELINE
+configurations, one JSON line each, for the results table.
 """
 from __future__ import annotations
 
@@ -21,8 +23,9 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-PEAK_FP32_TFLOPS = 157.3   # MI355X FP32 (vector packed / matrix) peak
+PEAK_FP32_TFLOPS = 157.3   # MI355X FP32 peak (vector and matrix)
 PEAK_HBM_GBS = 8000.0
+METRIC = "multivector-pairs/s fwd+bwd, Cl(8,0) fp32, 1 MI355X; % FP32 VALU/MFMA peak"
 
 
 def parse():
@@ -30,10 +33,19 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--batch", type=int, default=262144)
+    p.add_argument("--workload", default="headline", choices=["headline", "c1", "c2", "c3", "c4", "c5", "all", "copycal"])
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
     return p.parse_args()
+
+
+def n_terms(op: str, metric) -> int:
+    """Nonzero sigma terms per row (counts of the reference's algorithmic flops)."""
+    n = len(metric)
+    r = sum(1 for m in metric if m == 0)
+    return {"geom": 4 ** (n - r) * 3 ** r, "wedge": 3 ** n, "lc": 3 ** (n - r) * 2 ** r,
+            "rc": 3 ** (n - r) * 2 ** r, "inner": 2 * 3 ** (n - r) * 2 ** r - 2 ** (n - r),
+            "regressive": 3 ** n}[op]
 
 
 def cpu_baseline(n: int, budget_s: float):
@@ -41,21 +53,19 @@ def cpu_baseline(n: int, budget_s: float):
     sample: fwd + bwd (autograd) of the Cl(n,0) geometric product."""
     import torch
     from oracle import clifford_oracle as O
-    threads = os.cpu_count() or 1
-    torch.set_num_threads(threads)
+    torch.set_num_threads(os.cpu_count() or 1)
     rows = 256
     g = torch.Generator().manual_seed(0)
     a = torch.randn(rows, 1 << n, generator=g).requires_grad_()
     b = torch.randn(rows, 1 << n, generator=g).requires_grad_()
     gc = torch.ones(rows, 1 << n)
-    done, t0 = 0, time.perf_counter()
+    t0 = time.perf_counter()
     times = []
     while True:
         t1 = time.perf_counter()
         c = O.einsum_product("geom", a, b)
         torch.autograd.grad(c, (a, b), gc)
         times.append(time.perf_counter() - t1)
-        done += rows
         if time.perf_counter() - t0 > budget_s or len(times) >= 50:
             break
     times.sort()
@@ -63,7 +73,37 @@ def cpu_baseline(n: int, budget_s: float):
     return {"value": rows / med, "unit": "multivector-pairs/s", "cores": torch.get_num_threads(),
             "kind": "port",
             "sample": f"{len(times)} chunks x {rows} rows of Cl({n},0) geom_prod fwd+bwd (oracle einsum "
-                      f"restatement, torch fp32 CPU, median chunk time)"}
+                      f"restatement, torch fp32 on the host CPU, median chunk time)"}
+
+
+class Timer:
+    def __init__(self, torch, stream, reps):
+        self.torch, self.stream, self.reps = torch, stream, reps
+
+    def kernel_ms(self, fn):
+        """Average duration of fn() over `reps` back-to-back calls, HIP events on the launch stream."""
+        torch = self.torch
+        fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(self.stream)
+        for _ in range(self.reps):
+            fn()
+        e1.record(self.stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / self.reps
+
+    def step_ms(self, fn, warmup, steps):
+        torch = self.torch
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / steps
 
 
 def load_traffic():
@@ -74,19 +114,10 @@ def load_traffic():
         return json.load(f)
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (sharding is designed, not built)"}))
-        sys.exit(2)
-    import torch
-    import cliffordcuda_amd as cc
-    from cliffordcuda_amd import _lib
-
-    n, B = 8, args.batch
+def headline(args, torch, cc, lib, T):
+    n, B = 8, 262144
     D = 1 << n
     dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
     g = torch.Generator().manual_seed(0)
     a = torch.randn(B, D, generator=g).to(dev).requires_grad_()
     b = torch.randn(B, D, generator=g).to(dev).requires_grad_()
@@ -97,46 +128,20 @@ def main():
         c = cl.geom_prod(a, b)
         return torch.autograd.grad(c, (a, b), gc)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / args.steps
-
-    # per-kernel average durations with HIP events on the launch stream
-    lib = _lib.load()
-    stream = torch.cuda.current_stream(dev)
-    sp = stream.cuda_stream
+    ms = T.step_ms(step, args.warmup, args.steps)
+    sp = T.stream.cuda_stream
     c = torch.empty_like(a)
     ga = torch.empty_like(a)
     gb = torch.empty_like(a)
-    reps = max(5, args.steps)
-
-    def time_kernel(fn):
-        fn()
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
-            fn()
-        e1.record(stream)
-        e1.synchronize()
-        return e0.elapsed_time(e1) / reps
-
-    fwd_ms = time_kernel(lambda: lib.clf_product_fwd(0, n, 0, 0, a.data_ptr(), b.data_ptr(), c.data_ptr(), B, sp))
-    bwd_ms = time_kernel(lambda: lib.clf_product_bwd(0, n, 0, 0, a.data_ptr(), b.data_ptr(), gc.data_ptr(),
+    fwd_ms = T.kernel_ms(lambda: lib.clf_product_fwd(0, n, 0, 0, a.data_ptr(), b.data_ptr(), c.data_ptr(), B, sp))
+    bwd_ms = T.kernel_ms(lambda: lib.clf_product_bwd(0, n, 0, 0, a.data_ptr(), b.data_ptr(), gc.data_ptr(),
                                                      ga.data_ptr(), gb.data_ptr(), B, sp))
-    n_terms = D * D                       # nonzero sigma terms per row (Cl(8,0))
-    bwd_flops = 4.0 * n_terms * B         # two gradient sums, FMA = 2 flops
-    fwd_flops = 2.0 * n_terms * B
+    nt = D * D
+    bwd_flops = 4.0 * nt * B
+    fwd_flops = 2.0 * nt * B
     achieved = bwd_flops / (bwd_ms * 1e-3) / 1e12
-    traffic = load_traffic().get("prod_bwd_blk<GEOM> Cl(8,0) B=262144")
-    out = {
-        "metric": "multivector-pairs/s fwd+bwd, Cl(8,0) fp32, 1 MI355X; % FP32 VALU/MFMA peak",
+    return {
+        "metric": METRIC,
         "value": B / (ms * 1e-3),
         "unit": "multivector-pairs/s",
         "n_gpus": 1,
@@ -147,19 +152,193 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic N(0,1) a, b (seed 0), gc = ones",
-        "config": {"workload": "headline: Cl(8,0) geom_prod fwd+bwd", "batch": B, "n": n, "dim": D,
-                   "parallelism": "none (1 GPU)"},
+        "data": "synthetic: a, b ~ N(0,1) seed 0, gc = ones",
+        "config": {"workload": "headline: Cl(8,0) geom_prod fwd+bwd (BASELINE.md headline row)", "batch": B,
+                   "n": n, "dim": D, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "valu", "kernel": "prod_bwd_blk<GEOM>", "achieved": achieved,
                      "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_TFLOPS,
-                     "traffic": traffic, "kernel_ms": bwd_ms,
-                     "algorithmic_flops_per_launch": bwd_flops},
+                     "traffic": load_traffic().get("prod_bwd_blk<GEOM> Cl(8,0) B=262144"),
+                     "kernel_ms": bwd_ms, "algorithmic_flops_per_launch": bwd_flops,
+                     "algorithmic_bytes_per_launch": 20.0 * D * B},
         "kernels": {"prod_fwd_blk<GEOM>": {"ms": fwd_ms, "tflops": fwd_flops / (fwd_ms * 1e-3) / 1e12},
-                    "prod_bwd_blk<GEOM>": {"ms": bwd_ms, "tflops": achieved},
-                    "step_tflops_algorithmic": (fwd_flops + bwd_flops) / (ms * 1e-3) / 1e12},
+                    "prod_bwd_blk<GEOM>": {"ms": bwd_ms, "tflops": achieved}},
+        "step_frac_of_fp32_peak": (fwd_flops + bwd_flops) / (ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS,
         "cpu_baseline": None if args.no_cpu else cpu_baseline(n, args.cpu_seconds),
     }
-    print(json.dumps(out))
+
+
+def products_config(args, torch, cc, lib, T, name, metric, B, ops, fwd_only=False):
+    n = len(metric)
+    D = 1 << n
+    dev = torch.device("cuda", 0)
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(B, D, generator=g).to(dev)
+    b = torch.randn(B, D, generator=g).to(dev)
+    gc = torch.ones(B, D, device=dev)
+    neg = sum(1 << k for k, m in enumerate(metric) if m == -1)
+    nul = sum(1 << k for k, m in enumerate(metric) if m == 0)
+    sp = T.stream.cuda_stream
+    c = torch.empty_like(a)
+    ga = torch.empty_like(a)
+    gb = torch.empty_like(a)
+    res = {}
+    for op in ops:
+        code = {"geom": 0, "wedge": 1, "inner": 2, "lc": 3, "rc": 4, "regressive": 5}[op]
+        fms = T.kernel_ms(lambda: lib.clf_product_fwd(code, n, neg, nul, a.data_ptr(), b.data_ptr(), c.data_ptr(),
+                                                      B, sp))
+        entry = {"fwd_ms": fms}
+        nt = n_terms(op, metric)
+        flops = 2.0 * nt * B
+        byts = 12.0 * D * B
+        if not fwd_only:
+            bms = T.kernel_ms(lambda: lib.clf_product_bwd(code, n, neg, nul, a.data_ptr(), b.data_ptr(),
+                                                          gc.data_ptr(), ga.data_ptr(), gb.data_ptr(), B, sp))
+            entry["bwd_ms"] = bms
+            flops += 4.0 * nt * B
+            byts += 20.0 * D * B
+        t = (entry["fwd_ms"] + entry.get("bwd_ms", 0.0)) * 1e-3
+        entry.update({"pairs_per_s": B / t, "tflops_algorithmic": flops / t / 1e12,
+                      "frac_fp32_peak": flops / t / 1e12 / PEAK_FP32_TFLOPS,
+                      "hbm_gbs_algorithmic": byts / t / 1e9, "frac_hbm": byts / t / 1e9 / PEAK_HBM_GBS})
+        res[op] = entry
+    return {"workload": name, "metric": metric, "batch": B, "results": res}
+
+
+def c3_layer(args, torch, cc, lib, T):
+    n, B = 8, 262144
+    D = 1 << n
+    dev = torch.device("cuda", 0)
+    cl = cc.CliffordAlgebra([1] * n, device=dev)
+    layer = cc.GeometricProductLayer(cl)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(B, D, generator=g).to(dev).requires_grad_()
+    with torch.no_grad():
+        layer.weight.copy_((0.25 * torch.randn(1, D, generator=g)).to(dev))
+    gy = torch.ones(B, D, device=dev)
+
+    def step():
+        y = layer(x)
+        return torch.autograd.grad(y, (x, layer.weight), gy)
+
+    ms = T.step_ms(step, args.warmup, args.steps)
+    flops = 6.0 * D * D * B
+    byts = 20.0 * D * B
+    sp = T.stream.cuda_stream
+    nb = lib.clf_product_bcast_ws_bytes(n, B)
+    ws = torch.empty(nb // 4, device=dev)
+    y = torch.empty_like(x)
+    gx = torch.empty_like(x)
+    gw = torch.empty(D, device=dev)
+    w = layer.weight.detach()
+    fms = T.kernel_ms(lambda: lib.clf_product_bcast_fwd(0, 0, n, 0, 0, x.data_ptr(), w.data_ptr(), y.data_ptr(), B,
+                                                        ws.data_ptr(), nb, sp))
+    bms = T.kernel_ms(lambda: lib.clf_product_bcast_bwd(0, 0, n, 0, 0, x.data_ptr(), w.data_ptr(), gy.data_ptr(),
+                                                        gx.data_ptr(), gw.data_ptr(), B, ws.data_ptr(), nb, sp))
+    return {"workload": "c3: GeometricProductLayer Cl(8,0) fwd+bwd (x and weight grads)", "batch": B,
+            "ms_per_step": ms, "rows_per_s": B / (ms * 1e-3),
+            "tflops_algorithmic": flops / (ms * 1e-3) / 1e12,
+            "frac_fp32_mfma_peak": flops / (ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS,
+            "bcast_fwd_ms": fms, "bcast_bwd_ms": bms,
+            "bcast_fwd_frac_mfma": 2.0 * D * D * B / (fms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS,
+            "bcast_bwd_frac_mfma": 4.0 * D * D * B / (bms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS,
+            "hbm_gbs_algorithmic": byts / (ms * 1e-3) / 1e9}
+
+
+def c4_rotor(args, torch, cc, lib, T):
+    n, B = 8, 131072
+    D = 1 << n
+    dev = torch.device("cuda", 0)
+    cl = cc.CliffordAlgebra([1] * 7 + [-1], device=dev)
+    layer = cc.RotorLayer(cl).train()
+    g = torch.Generator().manual_seed(0)
+    with torch.no_grad():
+        layer.bivector.copy_(((0.1 ** 0.5) * torch.randn(1, 28, generator=g)).to(dev))
+    x = torch.randn(B, D, generator=g).to(dev).requires_grad_()
+    gy = torch.ones(B, D, device=dev)
+
+    def step():
+        y = layer(x)
+        return torch.autograd.grad(y, (x, layer.bivector), gy)
+
+    ms = T.step_ms(step, args.warmup, args.steps)
+    sp = T.stream.cuda_stream
+    state = cl.compile_bivector(layer.bivector.detach())
+    y = torch.empty_like(x)
+    gx = torch.empty_like(x)
+    gs = torch.empty_like(state)
+    nb = lib.clf_rotor_apply_ws_bytes(n, B)
+    ws = torch.empty(max(4, nb) // 4, device=dev)
+    biv = layer.bivector.detach()
+    cms = T.kernel_ms(lambda: lib.clf_rotor_compile_fwd(n, biv.data_ptr(), state.data_ptr(), sp))
+    fms = T.kernel_ms(lambda: lib.clf_rotor_apply_fwd(n, state.data_ptr(), x.data_ptr(), y.data_ptr(), B, sp))
+    bms = T.kernel_ms(lambda: lib.clf_rotor_apply_bwd(n, state.data_ptr(), x.data_ptr(), gy.data_ptr(),
+                                                      gx.data_ptr(), gs.data_ptr(), B, ws.data_ptr(), nb, sp))
+    byts = 20.0 * D * B
+    return {"workload": "c4: RotorLayer train Cl(7,1) fwd+bwd (rotor recompiled each step)", "batch": B,
+            "ms_per_step": ms, "rows_per_s": B / (ms * 1e-3),
+            "hbm_gbs_algorithmic": byts / (ms * 1e-3) / 1e9, "frac_hbm": byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+            "compile_fwd_ms": cms, "apply_fwd_ms": fms, "apply_bwd_ms": bms,
+            "apply_fwd_frac_hbm": 8.0 * D * B / (fms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+            "apply_bwd_frac_hbm": 12.0 * D * B / (bms * 1e-3) / 1e9 / PEAK_HBM_GBS}
+
+
+def c5_degenerate(args, torch, cc, lib, T):
+    metric = (1,) * 9 + (0,)
+    B = 16384
+    out = products_config(args, torch, cc, lib, T, "c5: Cl(9,0,1) geom + lc fwd+bwd", metric, B, ["geom", "lc"])
+    dev = torch.device("cuda", 0)
+    n = 10
+    x = torch.randn(B, 1 << n, device=dev)
+    o = torch.empty(B, device=dev)
+    y = torch.empty_like(x)
+    sp = T.stream.cuda_stream
+    ns = T.kernel_ms(lambda: lib.clf_norm_sq_fwd(n, 0, 1 << 9, x.data_ptr(), o.data_ptr(), B, sp))
+    gp = T.kernel_ms(lambda: lib.clf_graded(3, n, 0, 1 << 9, 2, x.data_ptr(), y.data_ptr(), B, sp))
+    D = 1 << n
+    out["norm_sq_fwd"] = {"ms": ns, "frac_hbm": (4.0 * D + 4) * B / (ns * 1e-3) / 1e9 / PEAK_HBM_GBS}
+    out["grade_projection_fwd"] = {"ms": gp, "frac_hbm": 8.0 * D * B / (gp * 1e-3) / 1e9 / PEAK_HBM_GBS}
+    return out
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1. The multi-GPU design "
+                                   "(batch sharding + one small all-reduce) is described, not built."}))
+        sys.exit(2)
+    import torch
+    import cliffordcuda_amd as cc
+    from cliffordcuda_amd import _lib
+    torch.cuda.set_device(0)
+    lib = _lib.load()
+    T = Timer(torch, torch.cuda.current_stream(0), max(5, args.steps))
+    if args.workload == "headline":
+        print(json.dumps(headline(args, torch, cc, lib, T)))
+        return
+    if args.workload == "copycal":
+        # plain device copy of a known size: calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE
+        nbytes = 256 << 20
+        x = torch.ones(nbytes // 4, device="cuda")
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"workload": "copycal", "bytes_read_per_copy": nbytes, "bytes_written_per_copy": nbytes}))
+        return
+    runs = ["c1", "c2", "c3", "c4", "c5"] if args.workload == "all" else [args.workload]
+    for w in runs:
+        if w == "c1":
+            r = products_config(args, torch, cc, lib, T, "c1: Cl(5,0) geom fwd", (1,) * 5, 1024, ["geom"], True)
+        elif w == "c2":
+            r = products_config(args, torch, cc, lib, T, "c2: Cl(6,1) six products fwd+bwd", (1,) * 6 + (-1,), 65536,
+                                ["geom", "wedge", "inner", "lc", "rc", "regressive"])
+        elif w == "c3":
+            r = c3_layer(args, torch, cc, lib, T)
+        elif w == "c4":
+            r = c4_rotor(args, torch, cc, lib, T)
+        else:
+            r = c5_degenerate(args, torch, cc, lib, T)
+        print(json.dumps(r), flush=True)
 
 
 if __name__ == "__main__":

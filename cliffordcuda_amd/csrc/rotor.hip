@@ -93,11 +93,13 @@ __device__ __forceinline__ void rot_plane(float (&v)[1 << RB], const float* __re
             if (r0 & mp) continue;
             const int r1 = r0 | (int)mp;
             const float sg = between_par((unsigned)r1, P, RB) ? -s_l : s_l;
-            const float own = qset ? v[r0] : v[r1];
+            // value selects only (a select of addresses would force the row into memory)
+            const float x0 = v[r0], x1 = v[r1];
+            const float own = qset ? x0 : x1;
             const float recv = __shfl_xor(own, 1 << ql, 64);
             const float nv = __builtin_fmaf(c, own, (qset ? sg : -sg) * recv);
-            if (qset) v[r0] = nv;
-            else v[r1] = nv;
+            v[r0] = qset ? nv : x0;
+            v[r1] = qset ? x1 : nv;
         }
     } else {  // both in lanes
         constexpr int pl = P - RB, ql = Qb - RB;
@@ -227,8 +229,9 @@ __device__ __forceinline__ void gamma_plane(float* __restrict__ acc, const float
             const int r1 = r0 | (int)mp;
             const bool neg = between_par((unsigned)r1, P, RB) != lneg;
             // q-clear lane owns I = (L, r1): term x_I gx_J ; q-set lane owns J = (L, r0): term x_J gx_I
-            const float xo = qset ? x[r0] : x[r1];
-            const float go = qset ? g[r0] : g[r1];
+            const float x0 = x[r0], x1 = x[r1], g0 = g[r0], g1 = g[r1];
+            const float xo = qset ? x0 : x1;
+            const float go = qset ? g0 : g1;
             const float gp = __shfl_xor(go, 1 << ql, 64);
             acc[S] = __builtin_fmaf(neg ? -xo : xo, gp, acc[S]);
         }
