@@ -12,7 +12,7 @@
 // gw[m] = sum_{(i,kout) fed by w[m]} sigma * G[i, kout] with G = x^T gy, a
 // split-K MFMA GEMM over the batch followed by a deterministic reduction.
 //
-// GEMM kernel: 256 threads, 128 x 128 output tile, K staged through LDS in
+// GEMM kernels: 256 threads, 128 x 128 output tile, K staged through LDS in
 // chunks of 32, each wave a 64 x 64 sub-tile of 2 x 2 v_mfma_f32_32x32x2f32
 // blocks (operand lanes: A[m = l%32][k = l/32], B[k = l/32][n = l%32];
 // accumulator element e of lane l: row 8*(e/4) + 4*(l/32) + e%4, column l%32).
@@ -25,17 +25,17 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 constexpr int GBM = 128, GBN = 128, GBK = 32, GPAD = 4;
 constexpr int kBcastMinN = 7;  // D >= 128: whole 128-wide tiles
 
-// C[M x N] (+ split stride) = op(A) * B over the K range of this split.
-//   TA == false: A row-major [M x K], lda = K
-//   TA == true : A row-major [K x M], lda = M (op(A) = A^T)
-//   B row-major [K x N], ldb = N; C row-major, ldc = N
-template <bool TA>
-__global__ __launch_bounds__(256) void gemm_mfma_kernel(const float* __restrict__ A, const float* __restrict__ Bm,
-                                                         float* __restrict__ C, long long M, int N, long long K,
-                                                         long long k_per_split) {
+// Split-K C_z[M x N] = A^T B over rows [z * k_per_split, ...) of A and B,
+// A row-major [K x M], B row-major [K x N] (the weight-gradient product
+// x^T gy). Both tiles are stored k-major in LDS exactly as they sit in HBM;
+// rows past the split's end are loaded clamped and zeroed (no branches). The
+// next chunk is prefetched into registers while the current one is consumed.
+__global__ __launch_bounds__(256) void gemm_tn_kernel(const float* __restrict__ A, const float* __restrict__ Bm,
+                                                       float* __restrict__ C, int M, int N, long long K,
+                                                       long long k_per_split) {
     __shared__ float As[GBK][GBM + GPAD];
     __shared__ float Bs[GBK][GBN + GPAD];
-    const long long m_base = (long long)blockIdx.x * GBM;
+    const int m_base = blockIdx.x * GBM;
     const int n_base = blockIdx.y * GBN;
     const long long k_begin = (long long)blockIdx.z * k_per_split;
     const long long k_end = (k_begin + k_per_split < K) ? (k_begin + k_per_split) : K;
@@ -43,7 +43,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const float* __restrict_
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
-    const int lr = lane & 31, lk = lane >> 5;
+    const int lr = lane & 31, lg = lane >> 5;
+    const int krow = tid >> 5, col4 = (tid & 31) * 4;  // loader: 8 k-rows x 32 float4 per pass
 
     floatx16 acc[2][2];
 #pragma unroll
@@ -53,56 +54,132 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const float* __restrict_
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
+    float4 ra0, ra1, ra2, ra3, rb0, rb1, rb2, rb3;
+#define CLF_TN_FETCH1(P, K0)                                                               \
+    {                                                                                      \
+        const long long kr = (K0) + (P) * 8 + krow;                                        \
+        const bool ok = kr < k_end;                                                        \
+        const long long kc = ok ? kr : (k_end - 1);                                        \
+        ra##P = *reinterpret_cast<const float4*>(A + kc * M + m_base + col4);              \
+        rb##P = *reinterpret_cast<const float4*>(Bm + kc * N + n_base + col4);             \
+        if (!ok) {                                                                         \
+            ra##P = make_float4(0.f, 0.f, 0.f, 0.f);                                       \
+            rb##P = make_float4(0.f, 0.f, 0.f, 0.f);                                       \
+        }                                                                                  \
+    }
+#define CLF_TN_FETCH(K0) CLF_TN_FETCH1(0, K0) CLF_TN_FETCH1(1, K0) CLF_TN_FETCH1(2, K0) CLF_TN_FETCH1(3, K0)
+    CLF_TN_FETCH(k_begin)
     for (long long k0 = k_begin; k0 < k_end; k0 += GBK) {
         __syncthreads();  // the previous chunk's fragments have been read
-        // A tile -> As[k][m]
-        if (!TA) {
-            // 128 rows x 32 k: thread reads 4 consecutive k of one row, 4 passes
-#pragma unroll
-            for (int pass = 0; pass < 4; ++pass) {
-                const int mr = pass * 32 + (tid >> 3);
-                const int kc = (tid & 7) * 4;
-                const long long gm = m_base + mr;
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (gm < M) v = *reinterpret_cast<const float4*>(A + gm * K + k0 + kc);
-                As[kc + 0][mr] = v.x;
-                As[kc + 1][mr] = v.y;
-                As[kc + 2][mr] = v.z;
-                As[kc + 3][mr] = v.w;
-            }
-        } else {
-            // 32 k-rows x 128 m: thread reads 4 consecutive m of one k-row, 4 passes
-#pragma unroll
-            for (int pass = 0; pass < 4; ++pass) {
-                const int kr = pass * 8 + (tid >> 5);
-                const int mc = (tid & 31) * 4;
-                const long long gk = k0 + kr;
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (gk < k_end) v = *reinterpret_cast<const float4*>(A + gk * M + m_base + mc);
-                *reinterpret_cast<float4*>(&As[kr][mc]) = v;
-            }
-        }
-        // B tile -> Bs[k][n]
-#pragma unroll
-        for (int pass = 0; pass < 4; ++pass) {
-            const int kr = pass * 8 + (tid >> 5);
-            const int nc = (tid & 31) * 4;
-            const long long gk = k0 + kr;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (gk < k_end) v = *reinterpret_cast<const float4*>(Bm + gk * N + n_base + nc);
-            *reinterpret_cast<float4*>(&Bs[kr][nc]) = v;
-        }
+        *reinterpret_cast<float4*>(&As[krow][col4]) = ra0;
+        *reinterpret_cast<float4*>(&As[8 + krow][col4]) = ra1;
+        *reinterpret_cast<float4*>(&As[16 + krow][col4]) = ra2;
+        *reinterpret_cast<float4*>(&As[24 + krow][col4]) = ra3;
+        *reinterpret_cast<float4*>(&Bs[krow][col4]) = rb0;
+        *reinterpret_cast<float4*>(&Bs[8 + krow][col4]) = rb1;
+        *reinterpret_cast<float4*>(&Bs[16 + krow][col4]) = rb2;
+        *reinterpret_cast<float4*>(&Bs[24 + krow][col4]) = rb3;
         __syncthreads();
+        {
+            const long long kn = (k0 + GBK < k_end) ? (k0 + GBK) : k0;
+            CLF_TN_FETCH(kn)
+        }
 #pragma unroll
         for (int kk = 0; kk < GBK; kk += 2) {
-            const float a0 = As[kk + lk][wm * 64 + lr];
-            const float a1 = As[kk + lk][wm * 64 + 32 + lr];
-            const float b0 = Bs[kk + lk][wn * 64 + lr];
-            const float b1 = Bs[kk + lk][wn * 64 + 32 + lr];
+            const float a0 = As[kk + lg][wm * 64 + lr];
+            const float a1 = As[kk + lg][wm * 64 + 32 + lr];
+            const float b0 = Bs[kk + lg][wn * 64 + lr];
+            const float b1 = Bs[kk + lg][wn * 64 + 32 + lr];
             acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
             acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
             acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
             acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+        }
+    }
+#undef CLF_TN_FETCH
+#undef CLF_TN_FETCH1
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = m_base + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * lg + (e & 3);
+                const int col = n_base + wn * 64 + j * 32 + lr;
+                C[(long long)row * N + col] = acc[i][j][e];
+            }
+}
+
+// C[M x N] = A * B with A row-major [M x K] and B given transposed, Bt
+// row-major [N x K]: both operand tiles are k-contiguous in LDS, so a lane reads
+// four k values of its row with one 16-byte LDS read. The reduction index is
+// permuted inside each 8-wide k block (MFMA step s takes k = 8kb + s on lanes
+// 0-31 and k = 8kb + 4 + s on lanes 32-63; A and B use the same permutation).
+// The next K chunk is loaded into registers while the current one is consumed.
+constexpr int NBK = 32, NPAD = 4;
+__global__ __launch_bounds__(256) void gemm_nn_kernel(const float* __restrict__ A, const float* __restrict__ Bt,
+                                                       float* __restrict__ C, long long M, int N, int K) {
+    __shared__ float As[GBM][NBK + NPAD];
+    __shared__ float Bs[GBN][NBK + NPAD];
+    const long long m_base = (long long)blockIdx.x * GBM;
+    const int n_base = blockIdx.y * GBN;
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31, lg = lane >> 5;
+    const int lrow = tid >> 3, lk = (tid & 7) * 4;  // loader: 32 rows x 8 float4 per pass
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+    float4 ra0, ra1, ra2, ra3, rb0, rb1, rb2, rb3;
+#define CLF_NN_FETCH1(P, K0)                                                                                  \
+    {                                                                                                         \
+        /* rows past M read row M-1 (always valid); their results are never stored */                  \
+        const long long gm = (m_base + (P) * 32 + lrow) < M ? (m_base + (P) * 32 + lrow) : (M - 1);          \
+        ra##P = *reinterpret_cast<const float4*>(A + gm * K + (K0) + lk);                                    \
+        rb##P = *reinterpret_cast<const float4*>(Bt + (long long)(n_base + (P) * 32 + lrow) * K + (K0) + lk);   \
+    }
+#define CLF_NN_FETCH(K0) CLF_NN_FETCH1(0, K0) CLF_NN_FETCH1(1, K0) CLF_NN_FETCH1(2, K0) CLF_NN_FETCH1(3, K0)
+    CLF_NN_FETCH(0)
+    for (int k0 = 0; k0 < K; k0 += NBK) {
+        __syncthreads();  // the previous chunk's fragments have been read
+        *reinterpret_cast<float4*>(&As[lrow][lk]) = ra0;
+        *reinterpret_cast<float4*>(&As[32 + lrow][lk]) = ra1;
+        *reinterpret_cast<float4*>(&As[64 + lrow][lk]) = ra2;
+        *reinterpret_cast<float4*>(&As[96 + lrow][lk]) = ra3;
+        *reinterpret_cast<float4*>(&Bs[lrow][lk]) = rb0;
+        *reinterpret_cast<float4*>(&Bs[32 + lrow][lk]) = rb1;
+        *reinterpret_cast<float4*>(&Bs[64 + lrow][lk]) = rb2;
+        *reinterpret_cast<float4*>(&Bs[96 + lrow][lk]) = rb3;
+        __syncthreads();
+        {
+            // prefetch the next chunk (the last iteration re-reads its own chunk: no branch)
+            const int kn = (k0 + NBK < K) ? (k0 + NBK) : k0;
+            CLF_NN_FETCH(kn)
+        }
+#pragma unroll
+        for (int kb = 0; kb < NBK / 8; ++kb) {
+            const int kc = kb * 8 + 4 * lg;
+            const float4 a0 = *reinterpret_cast<const float4*>(&As[wm * 64 + lr][kc]);
+            const float4 a1 = *reinterpret_cast<const float4*>(&As[wm * 64 + 32 + lr][kc]);
+            const float4 b0 = *reinterpret_cast<const float4*>(&Bs[wn * 64 + lr][kc]);
+            const float4 b1 = *reinterpret_cast<const float4*>(&Bs[wn * 64 + 32 + lr][kc]);
+#define CLF_NN_STEP(F)                                                                       \
+    acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.F, b0.F, acc[0][0], 0, 0, 0);        \
+    acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.F, b1.F, acc[0][1], 0, 0, 0);        \
+    acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.F, b0.F, acc[1][0], 0, 0, 0);        \
+    acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.F, b1.F, acc[1][1], 0, 0, 0);
+            CLF_NN_STEP(x)
+            CLF_NN_STEP(y)
+            CLF_NN_STEP(z)
+            CLF_NN_STEP(w)
+#undef CLF_NN_STEP
         }
     }
 #pragma unroll
@@ -111,10 +188,12 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const float* __restrict_
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const long long row = m_base + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
+                const long long row = m_base + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * lg + (e & 3);
                 const int col = n_base + wn * 64 + j * 32 + lr;
                 if (row < M) C[row * N + col] = acc[i][j][e];
             }
+#undef CLF_NN_FETCH
+#undef CLF_NN_FETCH1
 }
 
 // M (and/or its transpose) from w
@@ -134,13 +213,19 @@ __global__ __launch_bounds__(256) void bcast_build_kernel(int op, int side, int 
     if (MwT) MwT[kout * D + r] = v;
 }
 
-// G = sum over splits of the partial products (D*D entries, one per thread)
-__global__ __launch_bounds__(256) void bcast_reduce_kernel(const float* __restrict__ parts, int nsplit, int DD,
-                                                            float* __restrict__ G) {
+// G = sum over splits of the partial products (four entries per thread)
+__global__ __launch_bounds__(256) void bcast_reduce_kernel(const float4* __restrict__ parts, int nsplit, int DD4,
+                                                            float4* __restrict__ G) {
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= DD) return;
-    float t = 0.f;
-    for (int s = 0; s < nsplit; ++s) t += parts[(long long)s * DD + idx];
+    if (idx >= DD4) return;
+    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s = 0; s < nsplit; ++s) {
+        const float4 v = parts[(long long)s * DD4 + idx];
+        t.x += v.x;
+        t.y += v.y;
+        t.z += v.z;
+        t.w += v.w;
+    }
     G[idx] = t;
 }
 
@@ -149,21 +234,25 @@ __global__ __launch_bounds__(256) void zero_kernel(float* __restrict__ p, long l
     if (i < count) p[i] = 0.f;
 }
 
-// gw[m] = sum_r sigma * G[r, kout(r ^ m)]
+// gw[m] = sum_r sigma * G[r, kout(r ^ m)]: one wave per output blade m, lanes
+// stride over r, then a butterfly sum
 __global__ __launch_bounds__(256) void bcast_gw_kernel(int op, int side, int n, unsigned neg, unsigned nul,
                                                         const float* __restrict__ G, float* __restrict__ gw) {
     const unsigned D = 1u << n;
-    const unsigned m = blockIdx.x * blockDim.x + threadIdx.x;
-    if (m >= D) return;
+    const unsigned m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const unsigned lane = threadIdx.x & 63;
     float t = 0.f;
-    for (unsigned r = 0; r < D; ++r) {
-        const int s = side == 0 ? full_sign(op, n, r, m, neg, nul) : full_sign(op, n, m, r, neg, nul);
-        if (!s) continue;
-        const unsigned k = r ^ m;
-        const unsigned kout = (op == OP_REGR) ? (~k & (D - 1)) : k;
-        t = __builtin_fmaf((float)s, G[r * D + kout], t);
+    if (m < D) {
+        for (unsigned r = lane; r < D; r += 64) {
+            const int s = side == 0 ? full_sign(op, n, r, m, neg, nul) : full_sign(op, n, m, r, neg, nul);
+            if (!s) continue;
+            const unsigned k = r ^ m;
+            const unsigned kout = (op == OP_REGR) ? (~k & (D - 1)) : k;
+            t = __builtin_fmaf((float)s, G[r * D + kout], t);
+        }
     }
-    gw[m] = t;
+    for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off, 64);
+    if (m < D && lane == 0) gw[m] = t;
 }
 
 // ---- host side --------------------------------------------------------------
@@ -198,11 +287,16 @@ static int check_bcast(int op, int side, int n, uint32_t neg, uint32_t nul, int6
     return CLF_OK;
 }
 
-static void launch_gemm(bool ta, const float* A, const float* B, float* C, long long M, int N, long long K,
-                        long long kps, int splits, hipStream_t s) {
-    const dim3 grid((unsigned)((M + GBM - 1) / GBM), (unsigned)(N / GBN), (unsigned)splits);
-    if (ta) hipLaunchKernelGGL((gemm_mfma_kernel<true>), grid, dim3(256), 0, s, A, B, C, M, N, K, kps);
-    else hipLaunchKernelGGL((gemm_mfma_kernel<false>), grid, dim3(256), 0, s, A, B, C, M, N, K, kps);
+static void launch_tn(const float* A, const float* B, float* C, int D, long long K, long long kps, int splits,
+                      hipStream_t s) {
+    const dim3 grid((unsigned)(D / GBM), (unsigned)(D / GBN), (unsigned)splits);
+    hipLaunchKernelGGL(gemm_tn_kernel, grid, dim3(256), 0, s, A, B, C, D, D, K, kps);
+}
+
+// C = A * Bt^T, A (rows x D), Bt (D x D) given transposed
+static void launch_nn(const float* A, const float* Bt, float* C, long long rows, int D, hipStream_t s) {
+    const dim3 grid((unsigned)((rows + GBM - 1) / GBM), (unsigned)(D / GBN));
+    hipLaunchKernelGGL(gemm_nn_kernel, grid, dim3(256), 0, s, A, Bt, C, rows, D, D);
 }
 
 int bcast_fwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w, float* y,
@@ -219,10 +313,10 @@ int bcast_fwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* 
         return set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
     hipStream_t s = (hipStream_t)stream;
     const int D = 1 << n;
-    float* Mw = (float*)ws;
+    float* MwT = (float*)ws;
     hipLaunchKernelGGL(bcast_build_kernel, dim3((unsigned)((D * D + 255) / 256)), dim3(256), 0, s, op, side, n, neg,
-                       nul, w, Mw, (float*)nullptr);
-    launch_gemm(false, x, Mw, y, batch, D, D, D, 1, s);
+                       nul, w, (float*)nullptr, MwT);
+    launch_nn(x, MwT, y, batch, D, s);
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }
@@ -245,22 +339,23 @@ int bcast_bwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* 
     const int splits = bcast_splits(batch);
     float* G = parts + (size_t)splits * DD;
     if (gx && batch > 0) {
+        float* Mw = (float*)ws;
         hipLaunchKernelGGL(bcast_build_kernel, dim3((unsigned)((DD + 255) / 256)), dim3(256), 0, s, op, side, n, neg,
-                           nul, w, (float*)nullptr, MwT);
-        launch_gemm(false, gy, MwT, gx, batch, D, D, D, 1, s);
+                           nul, w, Mw, (float*)nullptr);
+        launch_nn(gy, Mw, gx, batch, D, s);
     }
     if (gw) {
         if (batch > 0) {
             const long long kps = ((batch + splits - 1) / splits + GBK - 1) / GBK * GBK;
             const int used = (int)((batch + kps - 1) / kps);
-            launch_gemm(true, x, gy, parts, D, D, batch, kps, used, s);
-            hipLaunchKernelGGL(bcast_reduce_kernel, dim3((unsigned)((DD + 255) / 256)), dim3(256), 0, s, parts, used,
-                               (int)DD, G);
+            launch_tn(x, gy, parts, D, batch, kps, used, s);
+            hipLaunchKernelGGL(bcast_reduce_kernel, dim3((unsigned)((DD / 4 + 255) / 256)), dim3(256), 0, s,
+                               reinterpret_cast<const float4*>(parts), used, (int)(DD / 4), reinterpret_cast<float4*>(G));
         } else {
             hipLaunchKernelGGL(zero_kernel, dim3((unsigned)((DD + 255) / 256)), dim3(256), 0, s, G, (long long)DD);
         }
-        hipLaunchKernelGGL(bcast_gw_kernel, dim3((unsigned)((D + 255) / 256)), dim3(256), 0, s, op, side, n, neg, nul,
-                           G, gw);
+        hipLaunchKernelGGL(bcast_gw_kernel, dim3((unsigned)((D + 3) / 4)), dim3(256), 0, s, op, side, n, neg, nul, G,
+                           gw);
     }
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;

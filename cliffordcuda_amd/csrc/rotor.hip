@@ -14,8 +14,8 @@
 //
 // Gradients. With gx = Lambda(Q)^T gy (the chain run backwards with s -> -s),
 //   dL/dQ = Q Gamma,  Gamma_ab = sum_rows sum_{I: b in I, a not in I} sig x_I gx_{I^{a,b}}
-//                     Gamma_bb = sum_rows sum_{I: b in I} x_I gx_I
-// (the derivation extension of Q^{-1} dQ), and the bivector gradient follows
+// (the derivation extension of Q^{-1} dQ; only its antisymmetric part matters,
+// since Q stays orthogonal), and the bivector gradient follows
 // from the adjoint Frechet derivative of expm:
 //   dL/dA = [expm([[A^T, dL/dQ], [0, A^T]])]_{12},  A = -B,
 //   dL/db_m = 2 (dL/dB[i_m][j_m] - dL/dB[j_m][i_m]),  dL/dB = -dL/dA.
@@ -34,7 +34,6 @@ namespace clf {
 
 constexpr int kRotorMinN = 2;
 constexpr int kRotorMaxN = 10;
-constexpr int kRotorMaxM = 2 * kRotorMaxN;  // block matrix of the Frechet derivative
 
 __host__ __device__ constexpr int n_planes(int n) { return n * (n - 1) / 2; }
 __host__ __device__ constexpr int plane_p(int n, int k) {
@@ -53,7 +52,9 @@ __host__ __device__ constexpr int plane_q(int n, int k) {
     }
     return p + 1 + k;
 }
-__host__ __device__ constexpr int rotor_rb(int n) { return n < 4 ? n : (n - 4 <= 6 ? 4 : n - 6); }
+// register bits per lane: rows of n <= 8 use 4 lanes (partner exchanges are
+// quad-local DPP permutes), n = 9, 10 use 8 / 16 lanes of 64 blades each
+__host__ __device__ constexpr int rotor_rb(int n) { return n < 4 ? n : (n <= 8 ? n - 2 : 6); }
 // parity of the bits of r strictly between positions p and q (p < q)
 __host__ __device__ constexpr int between_par(unsigned r, int p, int q) {
     int c = 0;
@@ -63,6 +64,27 @@ __host__ __device__ constexpr int between_par(unsigned r, int p, int q) {
 __host__ __device__ constexpr int state_floats(int n) { return n * n + 2 * n_planes(n); }
 
 // ---- the plane-rotation chain on register-resident rows ---------------------
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// value of v in lane (lane ^ MASK) for MASK < 32: quad-local bits by DPP quad
+// permutes (full-rate VALU), bits 2..4 by one ds_swizzle in bit-mask mode
+template <unsigned MASK>
+__device__ __forceinline__ float lane_xor(float v) {
+    static_assert(MASK < 32, "lane exchange limited to 32 lanes");
+    float r = v;
+    if constexpr ((MASK & 3u) == 1u) r = dpp_mov<0xB1>(r);       // quad_perm [1,0,3,2]
+    else if constexpr ((MASK & 3u) == 2u) r = dpp_mov<0x4E>(r);  // quad_perm [2,3,0,1]
+    else if constexpr ((MASK & 3u) == 3u) r = dpp_mov<0x1B>(r);  // quad_perm [3,2,1,0]
+    if constexpr ((MASK & 0x1Cu) != 0u) {
+        constexpr int pattern = (int)(((MASK & 0x1Cu) << 10) | 0x1Fu);  // and 0x1F, or 0, xor MASK
+        r = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(r), pattern));
+    }
+    return r;
+}
 
 template <int N, int RB, int K, bool FWD>
 __device__ __forceinline__ void rot_plane(float (&v)[1 << RB], const float* __restrict__ cs, unsigned L) {
@@ -83,23 +105,28 @@ __device__ __forceinline__ void rot_plane(float (&v)[1 << RB], const float* __re
             }
         }
     } else if constexpr (P < RB) {  // p in registers, q in lanes
+        // Pair (I, J): the q-clear lane holds I in r1 = r0 | 2^p, the q-set
+        // partner holds J in r0. Both lanes exchange both registers and apply
+        //   x1' = a1 x1 + b1 (partner x0),  x0' = a0 x0 + b0 (partner x1)
+        // with lane constants (q clear: a1 = c, b1 = -s sig, a0 = 1, b0 = 0;
+        // q set: a1 = 1, b1 = 0, a0 = c, b0 = s sig): no selects per pair.
         constexpr unsigned mp = 1u << P;
         constexpr int ql = Qb - RB;
         const bool qset = (L >> ql) & 1u;
         const int lpar = __popc(L & ((1u << ql) - 1u)) & 1;
         const float s_l = lpar ? -s : s;
+        const float a1 = qset ? 1.f : c, b1 = qset ? 0.f : -s_l;
+        const float a0 = qset ? c : 1.f, b0 = qset ? s_l : 0.f;
 #pragma unroll
         for (int r0 = 0; r0 < V; ++r0) {
             if (r0 & mp) continue;
             const int r1 = r0 | (int)mp;
-            const float sg = between_par((unsigned)r1, P, RB) ? -s_l : s_l;
-            // value selects only (a select of addresses would force the row into memory)
+            const bool neg = between_par((unsigned)r1, P, RB);
             const float x0 = v[r0], x1 = v[r1];
-            const float own = qset ? x0 : x1;
-            const float recv = __shfl_xor(own, 1 << ql, 64);
-            const float nv = __builtin_fmaf(c, own, (qset ? sg : -sg) * recv);
-            v[r0] = qset ? nv : x0;
-            v[r1] = qset ? x1 : nv;
+            const float p0 = lane_xor<(1u << ql)>(x0);
+            const float p1 = lane_xor<(1u << ql)>(x1);
+            v[r1] = __builtin_fmaf(a1, x1, (neg ? -b1 : b1) * p0);
+            v[r0] = __builtin_fmaf(a0, x0, (neg ? -b0 : b0) * p1);
         }
     } else {  // both in lanes
         constexpr int pl = P - RB, ql = Qb - RB;
@@ -112,7 +139,7 @@ __device__ __forceinline__ void rot_plane(float (&v)[1 << RB], const float* __re
         const float se = part ? (qset ? sg : -sg) : 0.f;
 #pragma unroll
         for (int r = 0; r < V; ++r) {
-            const float recv = __shfl_xor(v[r], (1 << pl) | (1 << ql), 64);
+            const float recv = lane_xor<(1u << pl) | (1u << ql)>(v[r]);
             v[r] = __builtin_fmaf(ce, v[r], se * recv);
         }
     }
@@ -182,30 +209,21 @@ __global__ __launch_bounds__(256) void rotor_apply_kernel(const float* __restric
     store_row_part<RB>(v, Y + off);
 }
 
-// ---- backward: gx = Lambda(Q)^T gy and the per-workgroup partial Gamma ----
-
-// per-lane accumulator slots, per plane: 2 if both bits are register bits
-// (Gamma_qp and Gamma_pq), else 1 (the lane's own type); then RB register-bit
-// diagonals and one all-blades diagonal sum
-template <int N, int RB>
-struct AccLayout {
-    static constexpr int slot(int k) {
-        int s = 0;
-        for (int j = 0; j < k; ++j) s += (plane_q(N, j) < RB) ? 2 : 1;
-        return s;
-    }
-    static constexpr int planes_end = slot(n_planes(N));
-    static constexpr int diag = planes_end;           // RB register-bit diagonals
-    static constexpr int all = planes_end + RB;       // sum over all blades of the lane
-    static constexpr int total = planes_end + RB + 1;
-};
+// ---- backward: gx = Lambda(Q)^T gy and the per-workgroup partial skew(Gamma) --
+//
+// Only the antisymmetric part of Gamma reaches the bivector: Q stays in SO(n),
+// so Q^{-1} dQ is antisymmetric and <Gamma, Q^{-1} dQ> = <skew Gamma, Q^{-1} dQ>.
+// Per plane (p < q) the kernels accumulate
+//   K_pq = Gamma_pq - Gamma_qp = sum_rows sum_pairs sig (x_J gx_I - x_I gx_J)
+// (I holds p not q, J = I ^ {p,q}). One accumulator per plane and lane; the
+// lane-dependent sign of a term (which side of the pair the lane holds, and the
+// lane bits between p and q) is applied when the per-lane sums are combined.
 
 template <int N, int RB, int K>
-__device__ __forceinline__ void gamma_plane(float* __restrict__ acc, const float (&x)[1 << RB],
-                                            const float (&g)[1 << RB], unsigned L) {
+__device__ __forceinline__ void skew_plane(float* __restrict__ acc, const float (&x)[1 << RB],
+                                           const float (&g)[1 << RB], unsigned L) {
     constexpr int P = plane_p(N, K), Qb = plane_q(N, K);
     constexpr int V = 1 << RB;
-    constexpr int S = AccLayout<N, RB>::slot(K);
     if constexpr (Qb < RB) {
         constexpr unsigned mp = 1u << P, mq = 1u << Qb;
 #pragma unroll
@@ -213,67 +231,68 @@ __device__ __forceinline__ void gamma_plane(float* __restrict__ acc, const float
             if ((r & mp) && !(r & mq)) {
                 const int rj = r ^ (int)(mp | mq);
                 const bool neg = between_par((unsigned)r, P, Qb);
-                // Gamma_qp += sig x_I gx_J ; Gamma_pq += sig x_J gx_I
-                acc[S] = __builtin_fmaf(neg ? -x[r] : x[r], g[rj], acc[S]);
-                acc[S + 1] = __builtin_fmaf(neg ? -x[rj] : x[rj], g[r], acc[S + 1]);
+                // sig (x_J g_I - x_I g_J)
+                acc[K] = __builtin_fmaf(neg ? -x[rj] : x[rj], g[r], acc[K]);
+                acc[K] = __builtin_fmaf(neg ? x[r] : -x[r], g[rj], acc[K]);
             }
         }
     } else if constexpr (P < RB) {
         constexpr unsigned mp = 1u << P;
         constexpr int ql = Qb - RB;
         const bool qset = (L >> ql) & 1u;
-        const bool lneg = __popc(L & ((1u << ql) - 1u)) & 1;
 #pragma unroll
         for (int r0 = 0; r0 < V; ++r0) {
             if (r0 & mp) continue;
             const int r1 = r0 | (int)mp;
-            const bool neg = between_par((unsigned)r1, P, RB) != lneg;
-            // q-clear lane owns I = (L, r1): term x_I gx_J ; q-set lane owns J = (L, r0): term x_J gx_I
+            const bool neg = between_par((unsigned)r1, P, RB);
+            // q-clear lane owns I = (L, r1), q-set lane owns J = (L, r0); each
+            // multiplies its own x by the partner's g (sign applied later)
             const float x0 = x[r0], x1 = x[r1], g0 = g[r0], g1 = g[r1];
             const float xo = qset ? x0 : x1;
             const float go = qset ? g0 : g1;
-            const float gp = __shfl_xor(go, 1 << ql, 64);
-            acc[S] = __builtin_fmaf(neg ? -xo : xo, gp, acc[S]);
+            const float gp = lane_xor<(1u << ql)>(go);
+            acc[K] = __builtin_fmaf(neg ? -xo : xo, gp, acc[K]);
         }
     } else {
         constexpr int pl = P - RB, ql = Qb - RB;
-        const bool pset = (L >> pl) & 1u, qset = (L >> ql) & 1u;
-        const unsigned between = ((1u << ql) - 1u) & ~((2u << pl) - 1u);
-        const bool neg = __popc(L & between) & 1;
-        const float w = (pset != qset) ? (neg ? -1.f : 1.f) : 0.f;
 #pragma unroll
         for (int r = 0; r < V; ++r) {
-            const float gp = __shfl_xor(g[r], (1 << pl) | (1 << ql), 64);
-            acc[S] = __builtin_fmaf(w * x[r], gp, acc[S]);
+            const float gp = lane_xor<(1u << pl) | (1u << ql)>(g[r]);
+            acc[K] = __builtin_fmaf(x[r], gp, acc[K]);
         }
     }
 }
 
 template <int N, int RB, int... Ks>
-__device__ __forceinline__ void gamma_all_seq(float* __restrict__ acc, const float (&x)[1 << RB],
-                                              const float (&g)[1 << RB], unsigned L,
-                                              std::integer_sequence<int, Ks...>) {
-    (gamma_plane<N, RB, Ks>(acc, x, g, L), ...);
+__device__ __forceinline__ void skew_all_seq(float* __restrict__ acc, const float (&x)[1 << RB],
+                                             const float (&g)[1 << RB], unsigned L,
+                                             std::integer_sequence<int, Ks...>) {
+    (skew_plane<N, RB, Ks>(acc, x, g, L), ...);
 }
 
+// sign of lane position Lp's accumulator for plane k (0 if the lane holds no pair)
 template <int N, int RB>
-__device__ __forceinline__ void gamma_accumulate(float* __restrict__ acc, const float (&x)[1 << RB],
-                                                 const float (&g)[1 << RB], unsigned L) {
-    gamma_all_seq<N, RB>(acc, x, g, L, std::make_integer_sequence<int, n_planes(N)>{});
-    using AL = AccLayout<N, RB>;
-#pragma unroll
-    for (int r = 0; r < (1 << RB); ++r) {
-        const float t = x[r] * g[r];
-        acc[AL::all] += t;
-#pragma unroll
-        for (int b = 0; b < RB; ++b)
-            if ((r >> b) & 1) acc[AL::diag + b] += t;
+__device__ __forceinline__ float skew_lane_sign(int k, unsigned Lp) {
+    const int p = plane_p(N, k), q = plane_q(N, k);
+    if (q < RB) return 1.f;
+    if (p < RB) {
+        const int ql = q - RB;
+        const bool qset = (Lp >> ql) & 1u;
+        const bool lneg = __popc(Lp & ((1u << ql) - 1u)) & 1;
+        // q-set lane: +sig x_J g_I ; q-clear lane: -sig x_I g_J
+        return (qset != lneg) ? 1.f : -1.f;
     }
+    const int pl = p - RB, ql = q - RB;
+    const bool pset = (Lp >> pl) & 1u, qset = (Lp >> ql) & 1u;
+    if (pset == qset) return 0.f;
+    const unsigned between = ((1u << ql) - 1u) & ~((2u << pl) - 1u);
+    const bool lneg = __popc(Lp & between) & 1;
+    return (qset != lneg) ? 1.f : -1.f;
 }
 
 // Persistent: each workgroup walks rows with a grid stride, writes gx (if
-// requested) and, if gamma_ws != nullptr, its partial Gamma (N*N floats) to
-// gamma_ws[blockIdx.x * N * N].
+// requested) and, if gamma_ws != nullptr, its partial K (C(N,2) floats) to
+// gamma_ws[blockIdx.x * C(N,2)].
 template <int N>
 __global__ __launch_bounds__(256) void rotor_apply_bwd_kernel(const float* __restrict__ state,
                                                                const float* __restrict__ X,
@@ -283,14 +302,14 @@ __global__ __launch_bounds__(256) void rotor_apply_bwd_kernel(const float* __res
     constexpr int RB = rotor_rb(N);
     constexpr int LB = N - RB;
     constexpr int LPR = 1 << LB;
-    using AL = AccLayout<N, RB>;
+    constexpr int C = n_planes(N);
     const float* cs = state + N * N;
     const unsigned L = threadIdx.x & (LPR - 1);
     const int rows_per_block = blockDim.x >> LB;
     const bool want_gamma = gamma_ws != nullptr;
-    float acc[AL::total];
+    float acc[C];
 #pragma unroll
-    for (int i = 0; i < AL::total; ++i) acc[i] = 0.f;
+    for (int i = 0; i < C; ++i) acc[i] = 0.f;
     for (long long row0 = (long long)blockIdx.x * rows_per_block; row0 < batch;
          row0 += (long long)gridDim.x * rows_per_block) {
         const long long row = row0 + (threadIdx.x >> LB);
@@ -308,207 +327,302 @@ __global__ __launch_bounds__(256) void rotor_apply_bwd_kernel(const float* __res
             if (want_gamma) {
                 float x[1 << RB];
                 load_row_part<RB>(x, X + off);
-                gamma_accumulate<N, RB>(acc, x, g, Lr);
+                skew_all_seq<N, RB>(acc, x, g, Lr, std::make_integer_sequence<int, C>{});
             }
         }
     }
     if (!want_gamma) return;  // uniform: a kernel argument
     // 1) sum over the rows of each wave: lanes with equal L sit at stride LPR
 #pragma unroll
-    for (int i = 0; i < AL::total; ++i)
+    for (int i = 0; i < C; ++i)
         for (int off = LPR; off < 64; off <<= 1) acc[i] += __shfl_xor(acc[i], off, 64);
-    __shared__ float red[4][AL::total][LPR];  // blockDim.x == 256: four waves
-    __shared__ float gam[N * N];
+    __shared__ float red[4][C][LPR];  // blockDim.x == 256: four waves
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (lane < LPR) {
 #pragma unroll
-        for (int i = 0; i < AL::total; ++i) red[wave][i][lane] = acc[i];
+        for (int i = 0; i < C; ++i) red[wave][i][lane] = acc[i];
     }
     __syncthreads();
-    // 2) sum over waves and scatter the lane-position sums into Gamma
-    if (threadIdx.x == 0) {
-        for (int i = 0; i < N * N; ++i) gam[i] = 0.f;
-        auto S = [&](int i, int Lp) { return red[0][i][Lp] + red[1][i][Lp] + red[2][i][Lp] + red[3][i][Lp]; };
-        int slot = 0;
-        for (int k = 0; k < n_planes(N); ++k) {
-            const int p = plane_p(N, k), q = plane_q(N, k);
-            for (int Lp = 0; Lp < LPR; ++Lp) {
-                if (q < RB) {
-                    gam[q * N + p] += S(slot, Lp);      // Gamma_qp
-                    gam[p * N + q] += S(slot + 1, Lp);  // Gamma_pq
-                } else if (p < RB) {
-                    const bool qset = (Lp >> (q - RB)) & 1;
-                    gam[qset ? (p * N + q) : (q * N + p)] += S(slot, Lp);
-                } else {
-                    const bool pset = (Lp >> (p - RB)) & 1, qset = (Lp >> (q - RB)) & 1;
-                    if (pset != qset) gam[qset ? (p * N + q) : (q * N + p)] += S(slot, Lp);
-                }
-            }
-            slot += (q < RB) ? 2 : 1;
-        }
+    // 2) sum over waves and lane positions with each position's sign
+    for (int k = threadIdx.x; k < C; k += blockDim.x) {
+        float t = 0.f;
         for (int Lp = 0; Lp < LPR; ++Lp) {
-            for (int b = 0; b < RB; ++b) gam[b * N + b] += S(AL::diag + b, Lp);
-            for (int b = RB; b < N; ++b)
-                if ((Lp >> (b - RB)) & 1) gam[b * N + b] += S(AL::all, Lp);
+            const float sgn = skew_lane_sign<N, RB>(k, (unsigned)Lp);
+            t += sgn * (red[0][k][Lp] + red[1][k][Lp] + red[2][k][Lp] + red[3][k][Lp]);
         }
+        gamma_ws[(long long)blockIdx.x * C + k] = t;
     }
-    __syncthreads();
-    for (int i = threadIdx.x; i < N * N; i += blockDim.x) gamma_ws[(long long)blockIdx.x * N * N + i] = gam[i];
 }
 
-// ---- small dense fp64 helpers for one workgroup ------------------------------
+// ---- small dense fp64 matrix functions in one wave -----------------------
+// Lane j (< M) holds column j of an M x M matrix in registers (compile-time M,
+// so the row indices are register names); the other lanes run along idle.
 
-// C = A * B for m x m row-major matrices in LDS (C must not alias A or B)
-__device__ void mm(double* __restrict__ C, const double* __restrict__ A, const double* __restrict__ B, int m) {
-    for (int idx = threadIdx.x; idx < m * m; idx += blockDim.x) {
-        const int i = idx / m, j = idx % m;
-        double t = 0.0;
-        for (int k = 0; k < m; ++k) t += A[i * m + k] * B[k * m + j];
-        C[idx] = t;
-    }
-    __syncthreads();
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+    const long long bits = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)(bits & 0xffffffffll), lane);
+    const int hi = __builtin_amdgcn_readlane((int)(bits >> 32), lane);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
 
-// E = expm(Z), m x m, by scaling and squaring of a degree-18 Taylor series.
-// Z is left scaled; T1, T2 are scratch. All arrays m*m doubles in LDS.
-__device__ void expm(double* __restrict__ E, double* __restrict__ Z, double* __restrict__ T1,
-                     double* __restrict__ T2, int m) {
-    __shared__ double s_norm;
-    __shared__ int s_sq;
-    if (threadIdx.x == 0) {
-        double nrm = 0.0;
-        for (int i = 0; i < m; ++i) {
-            double r = 0.0;
-            for (int j = 0; j < m; ++j) r += fabs(Z[i * m + j]);
-            nrm = r > nrm ? r : nrm;
-        }
-        int sq = 0;
-        while (nrm > 0.5 && sq < 60) {
-            nrm *= 0.5;
-            ++sq;
-        }
-        s_norm = nrm;
-        s_sq = sq;
+__device__ __forceinline__ double wave_max_f64(double v) {
+    for (int off = 32; off > 0; off >>= 1) {
+        const double o = __shfl_xor(v, off, 64);
+        v = o > v ? o : v;
     }
-    __syncthreads();
-    const int sq = s_sq;
+    return v;
+}
+
+// col <- column j of expm(Z), Z row-major M x M in LDS, by scaling to 1-norm
+// <= 1/4 and squaring, with the degree-12 Taylor series (Horner form; truncation
+// below 1e-17 relative).
+template <int M>
+__device__ __forceinline__ void expm_cols(double (&col)[M], const double* __restrict__ Z, int j) {
+    // 1-norm, then the number of squarings that brings it to <= 1/2
+    double cs = 0.0;
+    if (j < M)
+        for (int i = 0; i < M; ++i) cs += fabs(Z[i * M + j]);
+    double nrm = wave_max_f64(cs);
+    int sq = 0;
+    while (nrm > 0.25 && sq < 60) {
+        nrm *= 0.5;
+        ++sq;
+    }
     const double scale = ldexp(1.0, -sq);
-    for (int i = threadIdx.x; i < m * m; i += blockDim.x) Z[i] *= scale;
-    // Horner: E = I + Z/1 (I + Z/2 (I + ... (I + Z/18)))
-    for (int i = threadIdx.x; i < m * m; i += blockDim.x) E[i] = (i / m == i % m) ? 1.0 : 0.0;
-    __syncthreads();
-    for (int k = 18; k >= 1; --k) {
-        mm(T1, Z, E, m);
-        for (int i = threadIdx.x; i < m * m; i += blockDim.x) E[i] = ((i / m == i % m) ? 1.0 : 0.0) + T1[i] / k;
-        __syncthreads();
+#pragma unroll
+    for (int i = 0; i < M; ++i) col[i] = (i == j) ? 1.0 : 0.0;
+    for (int k = 12; k >= 1; --k) {
+        const double f = scale / (double)k;
+        double t[M];
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            double acc = 0.0;
+#pragma unroll
+            for (int l = 0; l < M; ++l) acc += Z[i * M + l] * col[l];
+            t[i] = acc;
+        }
+#pragma unroll
+        for (int i = 0; i < M; ++i) col[i] = ((i == j) ? 1.0 : 0.0) + f * t[i];
     }
     for (int r = 0; r < sq; ++r) {
-        mm(T2, E, E, m);
-        for (int i = threadIdx.x; i < m * m; i += blockDim.x) E[i] = T2[i];
-        __syncthreads();
+        double t[M];
+#pragma unroll
+        for (int i = 0; i < M; ++i) t[i] = 0.0;
+#pragma unroll
+        for (int l = 0; l < M; ++l) {
+            const double cjl = col[l];
+#pragma unroll
+            for (int i = 0; i < M; ++i) t[i] += readlane_f64(col[i], l) * cjl;
+        }
+#pragma unroll
+        for (int i = 0; i < M; ++i) col[i] = t[i];
     }
 }
 
-// A = -B, B = 2 (M - M^T) from the lex-ordered bivector
-__device__ void build_generator(double* __restrict__ A, const float* __restrict__ biv, int n) {
-    for (int i = threadIdx.x; i < n * n; i += blockDim.x) A[i] = 0.0;
+// A = -B, B = 2 (M - M^T) from the lex-ordered bivector: A[i][j] = -2 b, A[j][i] = 2 b
+__device__ __forceinline__ double generator_entry(const float* __restrict__ biv, int n, int i, int j) {
+    if (i == j) return 0.0;
+    const int a = i < j ? i : j, c = i < j ? j : i;
+    const int m = a * n - a * (a + 1) / 2 + (c - a - 1);
+    const double b = (double)biv[m];
+    return i < j ? -2.0 * b : 2.0 * b;
+}
+
+template <int N>
+__global__ __launch_bounds__(64) void rotor_compile_fwd_kernel(const float* __restrict__ biv,
+                                                                float* __restrict__ state) {
+    __shared__ double Z[N * N];
+    const int j = threadIdx.x;
+    for (int idx = j; idx < N * N; idx += 64) Z[idx] = generator_entry(biv, N, idx / N, idx % N);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int m = 0;
-        for (int i = 0; i < n; ++i)
-            for (int j = i + 1; j < n; ++j, ++m) {
-                const double b = (double)biv[m];
-                A[i * n + j] = -2.0 * b;
-                A[j * n + i] = 2.0 * b;
+    double col[N];
+    expm_cols<N>(col, Z, j);
+    if (j < N)
+#pragma unroll
+        for (int i = 0; i < N; ++i) state[i * N + j] = (float)col[i];
+    // Givens elimination E <- G_k^T E (planes in lex order); E ends as I (det = +1)
+    float* cs = state + N * N;
+#pragma unroll
+    for (int p = 0; p < N - 1; ++p) {
+#pragma unroll
+        for (int q = p + 1; q < N; ++q) {
+            const int k = p * N - p * (p + 1) / 2 + (q - p - 1);
+            const double a = readlane_f64(col[p], p), bq = readlane_f64(col[q], p);
+            const double r = sqrt(a * a + bq * bq);
+            double c = 1.0, s = 0.0;
+            if (r > 1e-300) {
+                c = a / r;
+                s = bq / r;
             }
-    }
-    __syncthreads();
-}
-
-__global__ __launch_bounds__(256) void rotor_compile_fwd_kernel(int n, const float* __restrict__ biv,
-                                                                 float* __restrict__ state) {
-    __shared__ double A[kRotorMaxN * kRotorMaxN], E[kRotorMaxN * kRotorMaxN];
-    __shared__ double T1[kRotorMaxN * kRotorMaxN], T2[kRotorMaxN * kRotorMaxN];
-    build_generator(A, biv, n);
-    expm(E, A, T1, T2, n);
-    for (int i = threadIdx.x; i < n * n; i += blockDim.x) state[i] = (float)E[i];
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        // Givens elimination E <- G_k^T E column by column; E ends as I for det = +1
-        float* cs = state + n * n;
-        int k = 0;
-        for (int p = 0; p < n - 1; ++p)
-            for (int q = p + 1; q < n; ++q, ++k) {
-                const double a = E[p * n + p], b = E[q * n + p];
-                const double r = sqrt(a * a + b * b);
-                double c = 1.0, s = 0.0;
-                if (r > 1e-300) {
-                    c = a / r;
-                    s = b / r;
-                }
-                for (int j = 0; j < n; ++j) {
-                    const double ep = E[p * n + j], eq = E[q * n + j];
-                    E[p * n + j] = c * ep + s * eq;
-                    E[q * n + j] = -s * ep + c * eq;
-                }
+            const double ep = col[p], eq = col[q];
+            col[p] = c * ep + s * eq;
+            col[q] = -s * ep + c * eq;
+            if (j == 0) {
                 cs[2 * k] = (float)c;
                 cs[2 * k + 1] = (float)s;
             }
+        }
     }
 }
 
-// dL/dQ = Q Gamma, Gamma = sum of the per-workgroup partials; writes the Q
-// slot of g_state and zeroes its chain slot
-__global__ __launch_bounds__(256) void rotor_gamma_finalize_kernel(int n, const float* __restrict__ state,
-                                                                    const float* __restrict__ gamma_ws, int nparts,
-                                                                    float* __restrict__ g_state) {
-    __shared__ double G[kRotorMaxN * kRotorMaxN];
-    for (int i = threadIdx.x; i < n * n; i += blockDim.x) {
-        double t = 0.0;
-        for (int p = 0; p < nparts; ++p) t += (double)gamma_ws[(long long)p * n * n + i];
-        G[i] = t;
+// dL/dQ (tangent part) = Q skew(Gamma), skew(Gamma)[p][q] = K_pq / 2 = -skew(Gamma)[q][p],
+// K = sum of the per-workgroup partials. Writes the Q slot of g_state and zeroes
+// its chain slot. 1024 threads: entries padded to EP (a power of two >= C(n,2)),
+// thread t sums partials p = t/EP, t/EP + 1024/EP, ... of entry t % EP, then the
+// 1024/EP groups are added.
+__global__ __launch_bounds__(1024) void rotor_gamma_finalize_kernel(int n, const float* __restrict__ state,
+                                                                     const float* __restrict__ gamma_ws, int nparts,
+                                                                     float* __restrict__ g_state) {
+    __shared__ double part[1024];
+    __shared__ double S[kRotorMaxN * kRotorMaxN];
+    const int C = n_planes(n);
+    int ep = 1;
+    while (ep < C) ep <<= 1;
+    const int ngrp = 1024 / ep;
+    const int e = threadIdx.x & (ep - 1), grp = threadIdx.x / ep;
+    double t0 = 0.0, t1 = 0.0;
+    if (e < C) {
+        int p = grp;
+        for (; p + ngrp < nparts; p += 2 * ngrp) {
+            t0 += (double)gamma_ws[(long long)p * C + e];
+            t1 += (double)gamma_ws[(long long)(p + ngrp) * C + e];
+        }
+        if (p < nparts) t0 += (double)gamma_ws[(long long)p * C + e];
+    }
+    part[threadIdx.x] = t0 + t1;
+    for (int i = threadIdx.x; i < n * n; i += blockDim.x) S[i] = 0.0;
+    __syncthreads();
+    if (threadIdx.x < C) {
+        double u = 0.0;
+        for (int g = 0; g < ngrp; ++g) u += part[g * ep + threadIdx.x];
+        const int p = plane_p(n, threadIdx.x), q = plane_q(n, threadIdx.x);
+        S[p * n + q] = 0.5 * u;
+        S[q * n + p] = -0.5 * u;
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < n * n; idx += blockDim.x) {
-        const int i = idx / n, j = idx % n;
-        double t = 0.0;
-        for (int k = 0; k < n; ++k) t += (double)state[i * n + k] * G[k * n + j];
-        g_state[idx] = (float)t;
+    if (threadIdx.x < n * n) {
+        const int i = threadIdx.x / n, j = threadIdx.x % n;
+        double v = 0.0;
+        for (int k = 0; k < n; ++k) v += (double)state[i * n + k] * S[k * n + j];
+        g_state[threadIdx.x] = (float)v;
     }
     for (int i = n * n + threadIdx.x; i < state_floats(n); i += blockDim.x) g_state[i] = 0.f;
 }
 
-// g_biv from dL/dQ (Q slot of g_state) through Q = expm(-B(biv))
-__global__ __launch_bounds__(256) void rotor_compile_bwd_kernel(int n, const float* __restrict__ biv,
-                                                                 const float* __restrict__ g_state,
-                                                                 float* __restrict__ g_biv) {
-    constexpr int MM = kRotorMaxM * kRotorMaxM;
-    __shared__ double A[kRotorMaxN * kRotorMaxN];
-    __shared__ double Z[MM], E[MM], T1[MM], T2[MM];
-    build_generator(A, biv, n);
-    const int m = 2 * n;
-    for (int idx = threadIdx.x; idx < m * m; idx += blockDim.x) {
-        const int i = idx / m, j = idx % m;
-        double v = 0.0;
-        if (i < n && j < n) v = A[j * n + i];                              // A^T
-        else if (i >= n && j >= n) v = A[(j - n) * n + (i - n)];           // A^T
-        else if (i < n && j >= n) v = (double)g_state[i * n + (j - n)];    // dL/dQ
-        Z[idx] = v;
+// Frechet derivative of expm by the block identity
+//   expm([[X, G], [0, X]]) = [[e^X, L], [0, e^X]]:
+// Horner on the blocks (T_E <- I + X T_E / k, T_L <- (X T_L + G T_E) / k), then
+// squaring (E <- E E, L <- E L + L E). Lane j (< N) ends with column j of L.
+template <int N>
+__device__ __forceinline__ void expm_frechet_cols(double (&Lc)[N], const double* __restrict__ X,
+                                                  const double* __restrict__ G, int j) {
+    double cs = 0.0;
+    if (j < N)
+        for (int i = 0; i < N; ++i) cs += fabs(X[i * N + j]) + fabs(G[i * N + j]);
+    double xs = 0.0;
+    if (j < N)
+        for (int i = 0; i < N; ++i) xs += fabs(X[i * N + j]);
+    double nrm = wave_max_f64(cs > xs ? cs : xs);
+    int sq = 0;
+    while (nrm > 0.25 && sq < 60) {
+        nrm *= 0.5;
+        ++sq;
+    }
+    const double scale = ldexp(1.0, -sq);
+    double Ec[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        Ec[i] = (i == j) ? 1.0 : 0.0;
+        Lc[i] = 0.0;
+    }
+    for (int k = 12; k >= 1; --k) {
+        const double f = scale / (double)k;
+        double tE[N], tL[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            double ae = 0.0, al = 0.0;
+#pragma unroll
+            for (int l = 0; l < N; ++l) {
+                const double xil = X[i * N + l];
+                ae += xil * Ec[l];
+                al += xil * Lc[l] + G[i * N + l] * Ec[l];
+            }
+            tE[i] = ae;
+            tL[i] = al;
+        }
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            Ec[i] = ((i == j) ? 1.0 : 0.0) + f * tE[i];
+            Lc[i] = f * tL[i];
+        }
+    }
+    for (int r = 0; r < sq; ++r) {
+        double tE[N], tL[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            tE[i] = 0.0;
+            tL[i] = 0.0;
+        }
+#pragma unroll
+        for (int l = 0; l < N; ++l) {
+            const double ej = Ec[l], lj = Lc[l];
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                const double eil = readlane_f64(Ec[i], l), lil = readlane_f64(Lc[i], l);
+                tE[i] += eil * ej;
+                tL[i] += eil * lj + lil * ej;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            Ec[i] = tE[i];
+            Lc[i] = tL[i];
+        }
+    }
+}
+
+// g_biv from dL/dQ (Q slot of g_state) through Q = expm(A), A = -B(biv):
+// dL/dA = L(A^T, dL/dQ), the (1,2) block of expm([[A^T, dL/dQ], [0, A^T]]).
+template <int N>
+__global__ __launch_bounds__(64) void rotor_compile_bwd_kernel(const float* __restrict__ biv,
+                                                                const float* __restrict__ g_state,
+                                                                float* __restrict__ g_biv) {
+    __shared__ double X[N * N], G[N * N], F[N * N];
+    const int j = threadIdx.x;
+    for (int idx = j; idx < N * N; idx += 64) {
+        const int r = idx / N, c = idx % N;
+        X[idx] = generator_entry(biv, N, c, r);  // A^T
+        G[idx] = (double)g_state[idx];
     }
     __syncthreads();
-    expm(E, Z, T1, T2, m);
-    if (threadIdx.x == 0) {
-        int k = 0;
-        for (int i = 0; i < n; ++i)
-            for (int j = i + 1; j < n; ++j, ++k) {
-                const double dAij = E[i * m + (n + j)], dAji = E[j * m + (n + i)];
-                // dL/dB = -dL/dA; dL/db = 2 (dL/dB[i][j] - dL/dB[j][i])
-                g_biv[k] = (float)(-2.0 * (dAij - dAji));
-            }
+    double Lc[N];
+    expm_frechet_cols<N>(Lc, X, G, j);
+    if (j < N)
+#pragma unroll
+        for (int i = 0; i < N; ++i) F[i * N + j] = Lc[i];
+    __syncthreads();
+    for (int k = j; k < n_planes(N); k += 64) {
+        const int p = plane_p(N, k), q = plane_q(N, k);
+        // dL/dB = -dL/dA; dL/db = 2 (dL/dB[p][q] - dL/dB[q][p])
+        g_biv[k] = (float)(-2.0 * (F[p * N + q] - F[q * N + p]));
     }
 }
 
 // ---- host side --------------------------------------------------------------
+
+#define CLF_ROTOR_DISPATCH(n, CALL)       \
+    switch (n) {                          \
+        case 2: CALL(2); break;           \
+        case 3: CALL(3); break;           \
+        case 4: CALL(4); break;           \
+        case 5: CALL(5); break;           \
+        case 6: CALL(6); break;           \
+        case 7: CALL(7); break;           \
+        case 8: CALL(8); break;           \
+        case 9: CALL(9); break;           \
+        case 10: CALL(10); break;         \
+        default: break;                   \
+    }
 
 static int check_rotor_n(int n) {
     if (n < kRotorMinN || n > kRotorMaxN)
@@ -530,13 +644,16 @@ static int rotor_bwd_grid(int n, int64_t batch) {
 
 size_t rotor_apply_ws_bytes(int n, int64_t batch) {
     if (n < kRotorMinN || n > kRotorMaxN || batch < 0) return 0;
-    return (size_t)rotor_bwd_grid(n, batch) * n * n * sizeof(float);
+    return (size_t)rotor_bwd_grid(n, batch) * n_planes(n) * sizeof(float);
 }
 
 int rotor_compile_fwd(int n, const float* biv, float* state, void* stream) {
     if (int rc = check_rotor_n(n)) return rc;
     if (!biv || !state) return set_error(CLF_ERR_ARG, "null pointer argument");
-    hipLaunchKernelGGL(rotor_compile_fwd_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, n, biv, state);
+    hipStream_t s = (hipStream_t)stream;
+#define CLF_CALL(N) hipLaunchKernelGGL((rotor_compile_fwd_kernel<N>), dim3(1), dim3(64), 0, s, biv, state)
+    CLF_ROTOR_DISPATCH(n, CLF_CALL)
+#undef CLF_CALL
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }
@@ -544,7 +661,10 @@ int rotor_compile_fwd(int n, const float* biv, float* state, void* stream) {
 int rotor_compile_bwd(int n, const float* biv, const float* g_state, float* g_biv, void* stream) {
     if (int rc = check_rotor_n(n)) return rc;
     if (!biv || !g_state || !g_biv) return set_error(CLF_ERR_ARG, "null pointer argument");
-    hipLaunchKernelGGL(rotor_compile_bwd_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, n, biv, g_state, g_biv);
+    hipStream_t s = (hipStream_t)stream;
+#define CLF_CALL(N) hipLaunchKernelGGL((rotor_compile_bwd_kernel<N>), dim3(1), dim3(64), 0, s, biv, g_state, g_biv)
+    CLF_ROTOR_DISPATCH(n, CLF_CALL)
+#undef CLF_CALL
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }
@@ -565,19 +685,6 @@ static void launch_apply_bwd(const float* state, const float* x, const float* gy
                        ws, (long long)batch);
 }
 
-#define CLF_ROTOR_DISPATCH(n, CALL)       \
-    switch (n) {                          \
-        case 2: CALL(2); break;           \
-        case 3: CALL(3); break;           \
-        case 4: CALL(4); break;           \
-        case 5: CALL(5); break;           \
-        case 6: CALL(6); break;           \
-        case 7: CALL(7); break;           \
-        case 8: CALL(8); break;           \
-        case 9: CALL(9); break;           \
-        case 10: CALL(10); break;         \
-        default: break;                   \
-    }
 
 int rotor_apply_fwd(int n, const float* state, const float* x, float* y, int64_t batch, void* stream) {
     if (int rc = check_rotor_n(n)) return rc;
@@ -622,7 +729,7 @@ int rotor_apply_bwd(int n, const float* state, const float* x, const float* gy, 
     }
     if (g_state) {
         const int nparts = batch > 0 ? rotor_bwd_grid(n, batch) : 0;
-        hipLaunchKernelGGL(rotor_gamma_finalize_kernel, dim3(1), dim3(256), 0, s, n, state, gws, nparts, g_state);
+        hipLaunchKernelGGL(rotor_gamma_finalize_kernel, dim3(1), dim3(1024), 0, s, n, state, gws, nparts, g_state);
         CLF_HIP_CHECK(hipGetLastError());
     }
     return CLF_OK;

@@ -149,7 +149,9 @@ int clf_rotor_apply_fwd(int n, const float* state, const float* x, float* y,
 size_t clf_rotor_apply_ws_bytes(int n, int64_t batch);
 
 /* Backward of the sandwich: gx = R gy ~R (the transpose of the action),
- * g_state = dL/d(state) (Q block = dL/dQ, chain block = 0). gx or g_state may be
+ * g_state = dL/d(state): the Q block holds the component of dL/dQ tangent to
+ * SO(n) (Q skew(Gamma), which is all clf_rotor_compile_bwd needs), the chain
+ * block is 0. gx or g_state may be
  * NULL. x is read only when g_state != NULL. The reference returns no gradient
  * to x (extensions/rotor/givens_apply/mb_perm_packed.py:34-42). */
 int clf_rotor_apply_bwd(int n, const float* state, const float* x, const float* gy,

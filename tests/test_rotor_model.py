@@ -28,3 +28,6 @@ def test_rotor_model_matches_oracle():
     G = M.gamma(x.numpy(), gx, n)
     gb = M.compile_bwd(biv[0].numpy(), n, Q @ G)
     np.testing.assert_allclose(gb, bq.grad[0].numpy(), atol=1e-10)
+    # only the antisymmetric part of Gamma reaches the bivector (Q stays in SO(n))
+    gb_skew = M.compile_bwd(biv[0].numpy(), n, Q @ (0.5 * (G - G.T)))
+    np.testing.assert_allclose(gb_skew, bq.grad[0].numpy(), atol=1e-10)
