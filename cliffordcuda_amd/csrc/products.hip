@@ -18,6 +18,8 @@
 // as a permutation of the row, the a block as a broadcast. Inside each 64-byte
 // block the four float4 slots are XOR-swizzled so the 16 lanes of a row hit
 // distinct LDS banks.
+#include <cstdlib>
+#include <cstring>
 #include <utility>
 
 #include "clf_common.h"
@@ -502,6 +504,19 @@ static void launch_bwd(dim3 g, dim3 b, size_t lds, hipStream_t s, const float* A
     hipLaunchKernelGGL((prod_bwd_blk<OP, LN>), g, b, lds, s, A, B, GCp, GA, GB, P);
 }
 
+bool rep_applicable(int op, int n, uint32_t neg, uint32_t nul);
+int rep_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64_t batch, void* stream);
+int rep_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc, float* ga, float* gb, int64_t batch,
+            void* stream);
+
+// The geometric product of real-matrix-type signatures goes through the matrix
+// representation unless CLF_GEOM_PATH=direct asks for the per-term kernels.
+static bool use_rep(int op, int n, uint32_t neg, uint32_t nul) {
+    const char* e = std::getenv("CLF_GEOM_PATH");
+    if (e && std::strcmp(e, "direct") == 0) return false;
+    return rep_applicable(op, n, neg, nul);
+}
+
 int product_fwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const float* b, float* c,
                 int64_t batch, void* stream) {
     int rc = check_common(op, n, neg, nul, batch);
@@ -511,6 +526,7 @@ int product_fwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
     if (c == a || c == b) return set_error(CLF_ERR_ARG, "output must not alias an input");
     if ((((uintptr_t)a) | ((uintptr_t)b) | ((uintptr_t)c)) & 15u)
         return set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
+    if (use_rep(op, n, neg, nul)) return rep_fwd(n, neg, a, b, c, batch, stream);
     hipStream_t s = (hipStream_t)stream;
     BlkParams P{};
     P.batch = batch;
@@ -552,6 +568,7 @@ int product_bwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
         return set_error(CLF_ERR_ARG, "gradient outputs must not alias inputs or each other");
     if ((((uintptr_t)a) | ((uintptr_t)b) | ((uintptr_t)gc) | ((uintptr_t)ga) | ((uintptr_t)gb)) & 15u)
         return set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
+    if (use_rep(op, n, neg, nul)) return rep_bwd(n, neg, a, b, gc, ga, gb, batch, stream);
     hipStream_t s = (hipStream_t)stream;
     BlkParams P{};
     P.batch = batch;

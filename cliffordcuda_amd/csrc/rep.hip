@@ -1,0 +1,467 @@
+// Geometric product through the real matrix representation, for the
+// signatures where Cl(p,q) is the full real matrix algebra M_m(R), m = 2^(n/2)
+// (p - q = 0 or 2 mod 8, no null generator). The product of two rows is then
+// one m x m matrix product (m^3 multiply-adds) instead of the 4^n terms of the
+// XOR-indexed sum; forward and backward give the same values as the per-term
+// kernels up to fp32 rounding.
+//
+// Representation. Generators are real Pauli products gamma_g = P(x_g, z_g),
+//   P(x, z)[r][c] = [c == r ^ x] (-1)^{popc(z & c)},
+//   P(x1, z1) P(x2, z2) = (-1)^{popc(z1 & x2)} P(x1 ^ x2, z1 ^ z2),
+// chosen on the host so that they anticommute and square to the metric. Blade I
+// maps to phi(e_I) = s(I) P(x_I, z_I). A host table gives, for every label
+// (x, z), the blade and its sign. Conversion a -> phi(a): gather
+// t[x][z] = s(I) a_I, Walsh-Hadamard transform over z for each x,
+// W[x][c] = sum_z t[x][z] (-1)^{popc(z & c)}, and phi(a)[r][c] = W[r ^ c][c].
+// The inverse runs the same steps backwards with a factor 1/m.
+// Backward: ga = phi^{-1}(phi(gc) phi(b)^T), gb = phi^{-1}(phi(a)^T phi(gc))
+// (phi is orthogonal up to the factor m).
+//
+// Layout. One row is handled by m lanes of one wave (lane = x for the
+// conversions, lane = matrix row r for the products), so all exchanges are
+// wave-local through the row's LDS slots and need no workgroup barrier. Waves
+// walk row groups with a grid stride and prefetch the next group's rows into
+// registers while the current group is computed.
+#include <map>
+#include <mutex>
+
+#include "clf_common.h"
+
+namespace clf {
+
+constexpr int kRepMaxLogM = 4;  // m <= 16 (n <= 8): the table fits the kernel arguments
+
+struct RepTable {
+    // entry [x * m + z]: blade index | 0x80000000 if the sign s(I) is -1
+    unsigned e[1 << (2 * kRepMaxLogM)];
+};
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int M>
+__device__ __forceinline__ void wht_inplace(float (&v)[M]) {
+#pragma unroll
+    for (int h = 1; h < M; h <<= 1)
+#pragma unroll
+        for (int i = 0; i < M; ++i)
+            if (!(i & h)) {
+                const float a = v[i], b = v[i + h];
+                v[i] = a + b;
+                v[i + h] = a - b;
+            }
+}
+
+// gather t[z] = s * row[blade] from the staged row, WHT over z, and write the
+// standard-layout matrix phi[r][c] = W[r ^ c][c] (lane holds x) into mat
+template <int M>
+__device__ __forceinline__ void row_to_matrix(const float* __restrict__ row, float* __restrict__ mat,
+                                              const unsigned (&ent)[M], unsigned x) {
+    float w[M];
+#pragma unroll
+    for (int z = 0; z < M; ++z) {
+        const float v = row[ent[z] & 0xffffu];
+        w[z] = __uint_as_float(__float_as_uint(v) ^ (ent[z] & 0x80000000u));
+    }
+    wht_inplace<M>(w);
+#pragma unroll
+    for (int c = 0; c < M; ++c) mat[((x ^ (unsigned)c) * M) + c] = w[c];
+}
+
+// inverse: read W[x][c] = mat[x ^ c][c], inverse WHT, scatter s * t[z] / m into row
+template <int M>
+__device__ __forceinline__ void matrix_to_row(const float* __restrict__ mat, float* __restrict__ row,
+                                              const unsigned (&ent)[M], unsigned x) {
+    float w[M];
+#pragma unroll
+    for (int c = 0; c < M; ++c) w[c] = mat[((x ^ (unsigned)c) * M) + c];
+    wht_inplace<M>(w);
+    constexpr float inv = 1.0f / (float)M;
+#pragma unroll
+    for (int z = 0; z < M; ++z)
+        row[ent[z] & 0xffffu] = __uint_as_float(__float_as_uint(w[z] * inv) ^ (ent[z] & 0x80000000u));
+}
+
+template <int M>
+__device__ __forceinline__ void load_mrow(const float* __restrict__ mat, unsigned r, float (&v)[M]) {
+    const float4* p = reinterpret_cast<const float4*>(mat + r * M);
+#pragma unroll
+    for (int q = 0; q < M / 4; ++q) {
+        const float4 t = p[q];
+        v[4 * q] = t.x;
+        v[4 * q + 1] = t.y;
+        v[4 * q + 2] = t.z;
+        v[4 * q + 3] = t.w;
+    }
+}
+
+template <int M>
+__device__ __forceinline__ void store_mrow(float* __restrict__ mat, unsigned r, const float (&v)[M]) {
+    float4* p = reinterpret_cast<float4*>(mat + r * M);
+#pragma unroll
+    for (int q = 0; q < M / 4; ++q) p[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+}
+
+// out[c] = sum_k arow[k] * B[k][c]
+template <int M>
+__device__ __forceinline__ void row_times_mat(const float (&arow)[M], const float* __restrict__ B, float (&out)[M]) {
+#pragma unroll
+    for (int c = 0; c < M; ++c) out[c] = 0.f;
+#pragma unroll
+    for (int k = 0; k < M; ++k) {
+        float bk[M];
+        load_mrow<M>(B, (unsigned)k, bk);
+#pragma unroll
+        for (int c = 0; c < M; ++c) out[c] = __builtin_fmaf(arow[k], bk[c], out[c]);
+    }
+}
+
+// out[c] = sum_k arow[k] * B[c][k]   (row times B^T)
+template <int M>
+__device__ __forceinline__ void row_times_matT(const float (&arow)[M], const float* __restrict__ B, float (&out)[M]) {
+#pragma unroll
+    for (int c = 0; c < M; ++c) {
+        float bc[M];
+        load_mrow<M>(B, (unsigned)c, bc);
+        float t = 0.f;
+#pragma unroll
+        for (int k = 0; k < M; ++k) t = __builtin_fmaf(arow[k], bc[k], t);
+        out[c] = t;
+    }
+}
+
+// Per-wave row-group staging: rows row0 .. row0 + RPW - 1 (RPW = 64 / M), each
+// D = M*M floats; lane l moves float4 chunks l, l + 64, ... of the group.
+template <int M>
+struct RowGroup {
+    static constexpr int D = M * M;
+    static constexpr int RPW = 64 / M;
+    static constexpr int CH = RPW * D / 4 / 64;  // float4 chunks per lane
+};
+
+// Prefetch registers of one operand's row group: CH float4 per lane.
+template <int CH>
+struct Pre {
+    float4 v[CH];
+};
+
+template <int M>
+__device__ __forceinline__ Pre<RowGroup<M>::CH> fetch_group(const float* __restrict__ src, long long row0,
+                                                            long long batch, int lane) {
+    constexpr int D = RowGroup<M>::D, CH = RowGroup<M>::CH;
+    Pre<CH> p;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+        const int f = lane + 64 * j;          // float4 index inside the group
+        const int rl = (f * 4) / D;           // row inside the group
+        long long row = row0 + rl;
+        row = row < batch ? row : batch - 1;  // rows past the end re-read the last row; never stored
+        p.v[j] = reinterpret_cast<const float4*>(src + row * D)[(f * 4 - rl * D) / 4];
+    }
+    return p;
+}
+
+template <int CH>
+__device__ __forceinline__ void stage_group(float* __restrict__ dst, const Pre<CH>& p, int lane) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j) reinterpret_cast<float4*>(dst)[lane + 64 * j] = p.v[j];
+}
+
+template <int LOGM>
+__global__ __launch_bounds__(256) void rep_fwd_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                       float* __restrict__ C, long long batch, RepTable T) {
+    constexpr int M = 1 << LOGM;
+    constexpr int D = M * M;
+    constexpr int RPW = RowGroup<M>::RPW;
+    constexpr int CH = RowGroup<M>::CH;
+    __shared__ float lds[4][2][RPW * D];  // per wave: staged a (then phi(a), then c), staged b (then phi(b))
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const unsigned x = lane & (M - 1);
+    const int rl = lane >> LOGM;
+    float* sa = &lds[wave][0][0];
+    float* sb = &lds[wave][1][0];
+    unsigned ent[M];
+#pragma unroll
+    for (int z = 0; z < M; ++z) ent[z] = T.e[x * M + z];
+
+    const long long waves_total = (long long)gridDim.x * 4;
+    long long row0 = ((long long)blockIdx.x * 4 + wave) * RPW;
+    Pre<CH> pa = fetch_group<M>(A, row0, batch, lane);
+    Pre<CH> pb = fetch_group<M>(B, row0, batch, lane);
+    for (; row0 < batch; row0 += waves_total * RPW) {
+        // stage the prefetched rows, then prefetch the next group (past the end
+        // it re-reads clamped rows: no branch)
+        stage_group<CH>(sa, pa, lane);
+        stage_group<CH>(sb, pb, lane);
+        pa = fetch_group<M>(A, row0 + waves_total * RPW, batch, lane);
+        pb = fetch_group<M>(B, row0 + waves_total * RPW, batch, lane);
+        wave_lds_sync();
+        float* ra = sa + rl * D;
+        float* rb = sb + rl * D;
+        // conversions: gather + WHT in registers; matrices overwrite the staged rows
+        float wa[M], wb[M];
+#pragma unroll
+        for (int z = 0; z < M; ++z) {
+            wa[z] = __uint_as_float(__float_as_uint(ra[ent[z] & 0xffffu]) ^ (ent[z] & 0x80000000u));
+            wb[z] = __uint_as_float(__float_as_uint(rb[ent[z] & 0xffffu]) ^ (ent[z] & 0x80000000u));
+        }
+        wht_inplace<M>(wa);
+        wht_inplace<M>(wb);
+        wave_lds_sync();
+#pragma unroll
+        for (int c = 0; c < M; ++c) {
+            ra[((x ^ (unsigned)c) * M) + c] = wa[c];
+            rb[((x ^ (unsigned)c) * M) + c] = wb[c];
+        }
+        wave_lds_sync();
+        // product: lane r = x computes row r of phi(a) phi(b)
+        float arow[M], crow[M];
+        load_mrow<M>(ra, x, arow);
+        row_times_mat<M>(arow, rb, crow);
+        wave_lds_sync();
+        store_mrow<M>(ra, x, crow);
+        wave_lds_sync();
+        // inverse conversion into the b slot (blade order), then a coalesced store
+        matrix_to_row<M>(ra, rb, ent, x);
+        wave_lds_sync();
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int f = lane + 64 * j;
+            const int rr = (f * 4) / D;
+            if (row0 + rr < batch)
+                reinterpret_cast<float4*>(C + (row0 + rr) * D)[(f * 4 - rr * D) / 4] = reinterpret_cast<const float4*>(sb)[f];
+        }
+        wave_lds_sync();
+    }
+}
+
+template <int LOGM>
+__global__ __launch_bounds__(256) void rep_bwd_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                       const float* __restrict__ GC, float* __restrict__ GA,
+                                                       float* __restrict__ GB, long long batch, RepTable T) {
+    constexpr int M = 1 << LOGM;
+    constexpr int D = M * M;
+    constexpr int RPW = RowGroup<M>::RPW;
+    constexpr int CH = RowGroup<M>::CH;
+    __shared__ float lds[4][3][RPW * D];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const unsigned x = lane & (M - 1);
+    const int rl = lane >> LOGM;
+    float* sa = &lds[wave][0][0];
+    float* sb = &lds[wave][1][0];
+    float* sg = &lds[wave][2][0];
+    unsigned ent[M];
+#pragma unroll
+    for (int z = 0; z < M; ++z) ent[z] = T.e[x * M + z];
+    const bool want_a = GA != nullptr, want_b = GB != nullptr;
+
+    const long long waves_total = (long long)gridDim.x * 4;
+    long long row0 = ((long long)blockIdx.x * 4 + wave) * RPW;
+    Pre<CH> pa = fetch_group<M>(A, row0, batch, lane);
+    Pre<CH> pb = fetch_group<M>(B, row0, batch, lane);
+    Pre<CH> pg = fetch_group<M>(GC, row0, batch, lane);
+    for (; row0 < batch; row0 += waves_total * RPW) {
+        stage_group<CH>(sa, pa, lane);
+        stage_group<CH>(sb, pb, lane);
+        stage_group<CH>(sg, pg, lane);
+        pa = fetch_group<M>(A, row0 + waves_total * RPW, batch, lane);
+        pb = fetch_group<M>(B, row0 + waves_total * RPW, batch, lane);
+        pg = fetch_group<M>(GC, row0 + waves_total * RPW, batch, lane);
+        wave_lds_sync();
+        float* ra = sa + rl * D;
+        float* rb = sb + rl * D;
+        float* rg = sg + rl * D;
+        float wa[M], wb[M], wg[M];
+#pragma unroll
+        for (int z = 0; z < M; ++z) {
+            const unsigned bi = ent[z] & 0xffffu, sgn = ent[z] & 0x80000000u;
+            wa[z] = __uint_as_float(__float_as_uint(ra[bi]) ^ sgn);
+            wb[z] = __uint_as_float(__float_as_uint(rb[bi]) ^ sgn);
+            wg[z] = __uint_as_float(__float_as_uint(rg[bi]) ^ sgn);
+        }
+        wht_inplace<M>(wa);
+        wht_inplace<M>(wb);
+        wht_inplace<M>(wg);
+        wave_lds_sync();
+#pragma unroll
+        for (int c = 0; c < M; ++c) {
+            const unsigned o = ((x ^ (unsigned)c) * M) + c;
+            ra[o] = wa[c];
+            rb[o] = wb[c];
+            rg[o] = wg[c];
+        }
+        wave_lds_sync();
+        // lane r = x: dA[r][.] = G[r][.] B^T, dB[r][.] = (column r of A) G
+        float grow[M], dA[M], dB[M];
+        if (want_a) {
+            load_mrow<M>(rg, x, grow);
+            row_times_matT<M>(grow, rb, dA);
+        }
+        if (want_b) {
+            float acol[M];
+#pragma unroll
+            for (int k = 0; k < M; ++k) acol[k] = ra[k * M + x];
+            row_times_mat<M>(acol, rg, dB);
+        }
+        wave_lds_sync();
+        if (want_a) store_mrow<M>(ra, x, dA);
+        if (want_b) store_mrow<M>(rb, x, dB);
+        wave_lds_sync();
+        // inverse conversions: dA -> blade order in the g slot, dB -> the a slot... done in two passes
+        if (want_a) matrix_to_row<M>(ra, rg, ent, x);
+        wave_lds_sync();
+        if (want_a) {
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                const int f = lane + 64 * j;
+                const int rr = (f * 4) / D;
+                if (row0 + rr < batch)
+                    reinterpret_cast<float4*>(GA + (row0 + rr) * D)[(f * 4 - rr * D) / 4] =
+                        reinterpret_cast<const float4*>(sg)[f];
+            }
+        }
+        wave_lds_sync();
+        if (want_b) matrix_to_row<M>(rb, ra, ent, x);
+        wave_lds_sync();
+        if (want_b) {
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                const int f = lane + 64 * j;
+                const int rr = (f * 4) / D;
+                if (row0 + rr < batch)
+                    reinterpret_cast<float4*>(GB + (row0 + rr) * D)[(f * 4 - rr * D) / 4] =
+                        reinterpret_cast<const float4*>(sa)[f];
+            }
+        }
+        wave_lds_sync();
+    }
+}
+
+// ---- host side --------------------------------------------------------------
+
+static int host_popc(unsigned v) { return __builtin_popcount(v); }
+
+// Generators for the metric (bit g of neg set: e_g^2 = -1), or false if the
+// signature is not a real matrix algebra of size 2^(n/2).
+static bool rep_generators(int n, uint32_t neg, unsigned* gx, unsigned* gz) {
+    if (n % 2 || n < 2 || n > 2 * kRepMaxLogM) return false;
+    const int q = host_popc(neg), p = n - q;
+    const int d = ((p - q) % 8 + 8) % 8;
+    if (d != 0 && d != 2) return false;
+    const int k = n / 2;
+    const unsigned span = 1u << k;
+    // depth-first search in a fixed order (deterministic)
+    int g = 0;
+    unsigned cand[16] = {0};
+    while (g >= 0 && g < n) {
+        bool found = false;
+        for (unsigned c = cand[g] + 1; c < span * span; ++c) {
+            const unsigned cx = c / span, cz = c % span;
+            const int want = ((neg >> g) & 1u) ? 1 : 0;  // square -1 <=> popc(z & x) odd
+            if ((host_popc(cx & cz) & 1) != want) continue;
+            bool ok = true;
+            for (int h = 0; h < g && ok; ++h) ok = ((host_popc(cz & gx[h]) + host_popc(gz[h] & cx)) & 1) == 1;
+            if (!ok) continue;
+            cand[g] = c;
+            gx[g] = cx;
+            gz[g] = cz;
+            found = true;
+            break;
+        }
+        if (found) {
+            ++g;
+            if (g < n) cand[g] = 0;
+        } else {
+            cand[g] = 0;
+            --g;
+        }
+    }
+    return g == n;
+}
+
+static bool rep_table_build(int n, uint32_t neg, RepTable& T) {
+    unsigned gx[16], gz[16];
+    if (!rep_generators(n, neg, gx, gz)) return false;
+    const int m = 1 << (n / 2);
+    for (unsigned I = 0; I < (1u << n); ++I) {
+        unsigned x = 0, z = 0;
+        bool negsign = false;
+        for (int g = 0; g < n; ++g)
+            if ((I >> g) & 1u) {
+                if (host_popc(z & gx[g]) & 1) negsign = !negsign;
+                x ^= gx[g];
+                z ^= gz[g];
+            }
+        T.e[x * m + z] = I | (negsign ? 0x80000000u : 0u);
+    }
+    return true;
+}
+
+// Tables are built once per (n, neg) and kept (immutable after insertion).
+static bool rep_table(int n, uint32_t neg, RepTable& T) {
+    static std::mutex mu;
+    static std::map<unsigned, std::pair<bool, RepTable>> cache;
+    const unsigned key = ((unsigned)n << 24) | neg;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(key);
+    if (it == cache.end()) {
+        RepTable t{};
+        const bool ok = rep_table_build(n, neg, t);
+        it = cache.emplace(key, std::make_pair(ok, t)).first;
+    }
+    if (it->second.first) T = it->second.second;
+    return it->second.first;
+}
+
+// The matrix path serves the geometric product when the signature allows it;
+// returns false otherwise (the caller uses the per-term kernels).
+bool rep_applicable(int op, int n, uint32_t neg, uint32_t nul) {
+    if (op != CLF_OP_GEOM || nul != 0u || n < 4 || n > 2 * kRepMaxLogM) return false;
+    RepTable T;
+    return rep_table(n, neg, T);
+}
+
+static unsigned rep_grid(int n, int64_t batch) {
+    const int m = 1 << (n / 2);
+    const long long rows_per_block = 4LL * (64 / m);
+    long long g = (batch + rows_per_block - 1) / rows_per_block;
+    const long long cap = 256LL * 8;  // enough waves to fill the chip, then walk the batch
+    if (g > cap) g = cap;
+    return (unsigned)(g < 1 ? 1 : g);
+}
+
+int rep_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64_t batch, void* stream) {
+    RepTable T;
+    if (!rep_table(n, neg, T)) return set_error(CLF_ERR_UNSUPPORTED, "signature has no real matrix representation");
+    hipStream_t s = (hipStream_t)stream;
+    const dim3 grid(rep_grid(n, batch));
+    switch (n) {
+        case 4: hipLaunchKernelGGL((rep_fwd_kernel<2>), grid, dim3(256), 0, s, a, b, c, (long long)batch, T); break;
+        case 6: hipLaunchKernelGGL((rep_fwd_kernel<3>), grid, dim3(256), 0, s, a, b, c, (long long)batch, T); break;
+        case 8: hipLaunchKernelGGL((rep_fwd_kernel<4>), grid, dim3(256), 0, s, a, b, c, (long long)batch, T); break;
+        default: return set_error(CLF_ERR_UNSUPPORTED, "matrix path supports n = 4, 6, 8");
+    }
+    CLF_HIP_CHECK(hipGetLastError());
+    return CLF_OK;
+}
+
+int rep_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc, float* ga, float* gb, int64_t batch,
+            void* stream) {
+    RepTable T;
+    if (!rep_table(n, neg, T)) return set_error(CLF_ERR_UNSUPPORTED, "signature has no real matrix representation");
+    hipStream_t s = (hipStream_t)stream;
+    const dim3 grid(rep_grid(n, batch));
+    switch (n) {
+        case 4: hipLaunchKernelGGL((rep_bwd_kernel<2>), grid, dim3(256), 0, s, a, b, gc, ga, gb, (long long)batch, T); break;
+        case 6: hipLaunchKernelGGL((rep_bwd_kernel<3>), grid, dim3(256), 0, s, a, b, gc, ga, gb, (long long)batch, T); break;
+        case 8: hipLaunchKernelGGL((rep_bwd_kernel<4>), grid, dim3(256), 0, s, a, b, gc, ga, gb, (long long)batch, T); break;
+        default: return set_error(CLF_ERR_UNSUPPORTED, "matrix path supports n = 4, 6, 8");
+    }
+    CLF_HIP_CHECK(hipGetLastError());
+    return CLF_OK;
+}
+
+}  // namespace clf

@@ -210,3 +210,40 @@ def test_gradcheck_signatures(n):
             b = torch.randn(2, 1 << n, dtype=torch.float64, device="cuda", requires_grad=True)
             fn = lambda x, y: cc.products.product(op, x.float(), y.float(), metric).double()  # noqa: E731
             assert torch.autograd.gradcheck(fn, (a, b), eps=1e-3, atol=tol, rtol=tol, nondet_tol=tol), (op, metric)
+
+
+REAL_TYPE = [(1,) * 8, (1,) * 4 + (-1,) * 4, (1,) * 5 + (-1,) * 3, (-1,) * 8, (1, 1, 1, -1, -1, -1), (1, 1, 1, 1),
+             (-1, 1, 1, -1)]
+
+
+@pytest.mark.parametrize("metric", REAL_TYPE, ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
+def test_matrix_path_geom_parity(metric):
+    """Real-matrix-type signatures take the matrix-representation kernels for
+    the geometric product; check them against the oracle, forward and backward."""
+    e = run_case("geom", metric, 37)
+    assert max(e) <= TOL, e
+
+
+def test_matrix_path_equals_direct_path_full_batch(monkeypatch):
+    """Headline shape: the matrix-representation kernels and the per-term
+    kernels (an independent algorithm, forced with CLF_GEOM_PATH=direct) agree
+    at batch 262144, values and both gradients."""
+    g = torch.Generator().manual_seed(1)
+    B = 262144
+    a = torch.randn(B, 256, generator=g).cuda()
+    b = torch.randn(B, 256, generator=g).cuda()
+    gc = torch.randn(B, 256, generator=g).cuda()
+
+    def run():
+        x = a.clone().requires_grad_()
+        y = b.clone().requires_grad_()
+        c = cc.geom_prod(x, y)
+        c.backward(gc)
+        return c.detach(), x.grad, y.grad
+
+    c1, ga1, gb1 = run()
+    monkeypatch.setenv("CLF_GEOM_PATH", "direct")
+    c2, ga2, gb2 = run()
+    monkeypatch.delenv("CLF_GEOM_PATH")
+    for u, v in ((c1, c2), (ga1, ga2), (gb1, gb2)):
+        assert rel_err(u, v) <= TOL
