@@ -33,7 +33,11 @@ constexpr int kRepMaxLogM = 4;  // m <= 16 (n <= 8): the table fits the kernel a
 
 struct RepTable {
     // entry [x * m + z]: blade index | 0x80000000 if the sign s(I) is -1
+    //                    | 0x40000000 if s(I) (-1)^{popc(x & z)} is -1 (transposed conversion)
     unsigned e[1 << (2 * kRepMaxLogM)];
+    // m = 16: multiple of 4 xor-ed into the blade offsets of odd rows in LDS so
+    // that the gathers of two rows in one half-wave use distinct banks (0: none found)
+    unsigned odd_xor;
 };
 
 __device__ __forceinline__ void wave_lds_sync() {
@@ -340,6 +344,236 @@ __global__ __launch_bounds__(256) void rep_bwd_kernel(const float* __restrict__ 
     }
 }
 
+// ---- m = 16 (n = 8) on the matrix cores -------------------------------------
+// The 4-block v_mfma_f32_16x16x1f32 multiplies four independent 16x16 matrices,
+// block b taking its operands from lanes 16b .. 16b + 15 -- exactly the lanes
+// that convert row b. Operand k of lane (b, x):
+//   A[x][k] = phi(a)[x][k] = W_a[x ^ k][k]   (xor shuffle of register k)
+//   B[k][x] = phi(b)^T[x][k] = W'_b[x ^ k][k]
+// where W' is the conversion with the extra signs (-1)^{popc(x & z)}, because
+// P(x, z)^T = (-1)^{popc(x & z)} P(x, z). The shuffles are DPP moves
+// (quad_perm for xor 1..3, row_half_mirror = xor 7, row_mirror = xor 15).
+// The product C_b[4g + t][j] lands in lane 16g + j, register 4b + t; it goes
+// back through LDS as W_c[i ^ j][j] at row stride 20 floats, which keeps both
+// the scattered b32 writes and the b128 row reads free of bank conflicts.
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+template <unsigned CTRL>
+__device__ __forceinline__ float dpp16(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// value of v at lane (lane ^ K) of the same 16-lane row
+template <unsigned K>
+__device__ __forceinline__ float xor16(float v) {
+    constexpr unsigned k1 = (K & 8u) ? (K ^ 15u) : K;    // row_mirror: xor 15
+    constexpr unsigned k2 = (k1 & 4u) ? (k1 ^ 7u) : k1;  // row_half_mirror: xor 7
+    if constexpr ((K & 8u) != 0u) v = dpp16<0x140>(v);
+    if constexpr ((k1 & 4u) != 0u) v = dpp16<0x141>(v);
+    if constexpr (k2 == 1u) v = dpp16<0xB1>(v);       // quad_perm [1,0,3,2]
+    else if constexpr (k2 == 2u) v = dpp16<0x4E>(v);  // quad_perm [2,3,0,1]
+    else if constexpr (k2 == 3u) v = dpp16<0x1B>(v);  // quad_perm [3,2,1,0]
+    return v;
+}
+
+template <unsigned... K>
+__device__ __forceinline__ floatx16 mfma_chain(const float (&wa)[16], const float (&wb)[16],
+                                               std::integer_sequence<unsigned, K...>) {
+    floatx16 acc = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    ((acc = __builtin_amdgcn_mfma_f32_16x16x1f32(xor16<K>(wa[K]), xor16<K>(wb[K]), acc, 0, 0, 0)), ...);
+    return acc;
+}
+
+constexpr int kRelayoutStride = 20;
+constexpr int kRelayoutBlock = 16 * kRelayoutStride;  // floats per row of the group
+
+// lane (g, j) writes C_b[4g + t][j] (register 4b + t) to W_c[(4g + t) ^ j][j]
+__device__ __forceinline__ void relayout_store(float* __restrict__ dst, const floatx16& acc, int lane) {
+    const unsigned g = (unsigned)lane >> 4, j = (unsigned)lane & 15u;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            dst[b * kRelayoutBlock + (((4u * g + t) ^ j) * kRelayoutStride) + j] = acc[4 * b + t];
+}
+
+// lane (b, x) reads W_c[x][0..15] of row b
+__device__ __forceinline__ void relayout_load(const float* __restrict__ src, int b, unsigned x, float (&w)[16]) {
+    const float4* p = reinterpret_cast<const float4*>(src + b * kRelayoutBlock + x * kRelayoutStride);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 t = p[q];
+        w[4 * q] = t.x;
+        w[4 * q + 1] = t.y;
+        w[4 * q + 2] = t.z;
+        w[4 * q + 3] = t.w;
+    }
+}
+
+// Group of four rows: lane l moves float4 chunk l of row j (j = 0..3); rows
+// past the end re-read the last row and are never stored.
+struct Pre16 {
+    float4 v[4];
+};
+
+__device__ __forceinline__ Pre16 fetch16(const float* __restrict__ src, long long row0, long long batch, int lane) {
+    Pre16 p;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        long long row = row0 + j;
+        row = row < batch ? row : batch - 1;
+        p.v[j] = reinterpret_cast<const float4*>(src + row * 256)[lane];
+    }
+    return p;
+}
+
+// staged row j at [j * 256, (j + 1) * 256), odd rows with chunk index lane ^ oddc
+__device__ __forceinline__ void stage16(float* __restrict__ dst, const Pre16& p, int lane, unsigned oddc) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        reinterpret_cast<float4*>(dst + j * 256)[(j & 1) ? (lane ^ oddc) : lane] = p.v[j];
+}
+
+// Rows past the end were computed from clamped copies of the last row, so
+// their results are bit-identical to it: they are stored to the last row again
+// instead of branching around the stores.
+__device__ __forceinline__ void store16(float* __restrict__ dstg, const float* __restrict__ src, long long row0,
+                                        long long batch, int lane, unsigned oddc) {
+    float4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = reinterpret_cast<const float4*>(src + j * 256)[(j & 1) ? (lane ^ oddc) : lane];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        long long row = row0 + j;
+        row = row < batch ? row : batch - 1;
+        reinterpret_cast<float4*>(dstg + row * 256)[lane] = v[j];
+    }
+}
+
+// gather t[z] of the lane's row with the sign bit selected by SIGNSHIFT
+// (0: s(I), 1: the transposed conversion's sign), then WHT
+template <int SIGNSHIFT>
+__device__ __forceinline__ void gather16(const float* __restrict__ row, const unsigned (&ent)[16], float (&w)[16]) {
+#pragma unroll
+    for (int z = 0; z < 16; ++z)
+        w[z] = __uint_as_float(__float_as_uint(row[ent[z] & 0xffffu]) ^ ((ent[z] << SIGNSHIFT) & 0x80000000u));
+}
+
+// inverse WHT of W_c[x][.], scale 1/16, scatter s(I) t[z] into the row's blade slots
+__device__ __forceinline__ void unconvert16(float (&w)[16], float* __restrict__ row, const unsigned (&ent)[16]) {
+    wht_inplace<16>(w);
+#pragma unroll
+    for (int z = 0; z < 16; ++z)
+        row[ent[z] & 0xffffu] = __uint_as_float(__float_as_uint(w[z] * 0.0625f) ^ (ent[z] & 0x80000000u));
+}
+
+__global__ __launch_bounds__(256) void rep16_fwd_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                         float* __restrict__ C, long long batch, RepTable T) {
+    __shared__ float lds[4][2 * 4 * 256];  // per wave: staged a | staged b; later the relayout, then c
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const unsigned x = lane & 15u;
+    const int rb = lane >> 4;
+    float* sa = &lds[wave][0];
+    float* sb = sa + 4 * 256;
+    const unsigned oddx = (rb & 1) ? T.odd_xor : 0u, oddc = T.odd_xor >> 2;
+    unsigned ent[16];
+#pragma unroll
+    for (int z = 0; z < 16; ++z) ent[z] = T.e[x * 16 + z] ^ oddx;
+
+    const long long stride = (long long)gridDim.x * 4 * 4;
+    long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
+    Pre16 pa = fetch16(A, row0, batch, lane);
+    Pre16 pb = fetch16(B, row0, batch, lane);
+    for (; row0 < batch; row0 += stride) {
+        stage16(sa, pa, lane, oddc);
+        stage16(sb, pb, lane, oddc);
+        pa = fetch16(A, row0 + stride, batch, lane);
+        pb = fetch16(B, row0 + stride, batch, lane);
+        wave_lds_sync();
+        float wa[16], wb[16];
+        gather16<0>(sa + rb * 256, ent, wa);
+        gather16<1>(sb + rb * 256, ent, wb);
+        wave_lds_sync();
+        wht_inplace<16>(wa);
+        wht_inplace<16>(wb);
+        const floatx16 acc = mfma_chain(wa, wb, std::make_integer_sequence<unsigned, 16>{});
+        relayout_store(sa, acc, lane);
+        wave_lds_sync();
+        float wc[16];
+        relayout_load(sa, rb, x, wc);
+        wave_lds_sync();
+        unconvert16(wc, sa + rb * 256, ent);
+        wave_lds_sync();
+        store16(C, sa, row0, batch, lane, oddc);
+        wave_lds_sync();
+    }
+}
+
+__global__ __launch_bounds__(256) void rep16_bwd_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                         const float* __restrict__ GC, float* __restrict__ GA,
+                                                         float* __restrict__ GB, long long batch, RepTable T) {
+    __shared__ float lds[4][3 * 4 * 256];  // per wave: staged a | b | gc; later two relayouts, then ga | gb
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const unsigned x = lane & 15u;
+    const int rb = lane >> 4;
+    float* sa = &lds[wave][0];
+    float* sb = sa + 4 * 256;
+    float* sg = sb + 4 * 256;
+    float* rel_a = sa;                          // relayout of dA: 4 * 320 floats
+    float* rel_b = sa + 4 * kRelayoutBlock;     // relayout of dB: next 4 * 320 floats
+    const unsigned oddx = (rb & 1) ? T.odd_xor : 0u, oddc = T.odd_xor >> 2;
+    unsigned ent[16];
+#pragma unroll
+    for (int z = 0; z < 16; ++z) ent[z] = T.e[x * 16 + z] ^ oddx;
+    const bool want_a = GA != nullptr, want_b = GB != nullptr;
+
+    const long long stride = (long long)gridDim.x * 4 * 4;
+    long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
+    Pre16 pa = fetch16(A, row0, batch, lane);
+    Pre16 pb = fetch16(B, row0, batch, lane);
+    Pre16 pg = fetch16(GC, row0, batch, lane);
+    for (; row0 < batch; row0 += stride) {
+        stage16(sa, pa, lane, oddc);
+        stage16(sb, pb, lane, oddc);
+        stage16(sg, pg, lane, oddc);
+        pa = fetch16(A, row0 + stride, batch, lane);
+        pb = fetch16(B, row0 + stride, batch, lane);
+        pg = fetch16(GC, row0 + stride, batch, lane);
+        wave_lds_sync();
+        // dA = G B^T: operands W_g, W_b.  dB = A^T G: operands W'_a, W'_g.
+        float wg[16], wgt[16], wb[16], wat[16];
+        gather16<0>(sg + rb * 256, ent, wg);
+        gather16<1>(sg + rb * 256, ent, wgt);
+        if (want_a) gather16<0>(sb + rb * 256, ent, wb);
+        if (want_b) gather16<1>(sa + rb * 256, ent, wat);
+        wave_lds_sync();
+        if (want_a) {
+            wht_inplace<16>(wg);
+            wht_inplace<16>(wb);
+            const floatx16 acc = mfma_chain(wg, wb, std::make_integer_sequence<unsigned, 16>{});
+            relayout_store(rel_a, acc, lane);
+        }
+        if (want_b) {
+            wht_inplace<16>(wat);
+            wht_inplace<16>(wgt);
+            const floatx16 acc = mfma_chain(wat, wgt, std::make_integer_sequence<unsigned, 16>{});
+            relayout_store(rel_b, acc, lane);
+        }
+        wave_lds_sync();
+        float da[16], db[16];
+        if (want_a) relayout_load(rel_a, rb, x, da);
+        if (want_b) relayout_load(rel_b, rb, x, db);
+        wave_lds_sync();
+        if (want_a) unconvert16(da, sa + rb * 256, ent);
+        if (want_b) unconvert16(db, sb + rb * 256, ent);
+        wave_lds_sync();
+        if (want_a) store16(GA, sa, row0, batch, lane, oddc);
+        if (want_b) store16(GB, sb, row0, batch, lane, oddc);
+        wave_lds_sync();
+    }
+}
+
 // ---- host side --------------------------------------------------------------
 
 static int host_popc(unsigned v) { return __builtin_popcount(v); }
@@ -395,7 +629,29 @@ static bool rep_table_build(int n, uint32_t neg, RepTable& T) {
                 x ^= gx[g];
                 z ^= gz[g];
             }
-        T.e[x * m + z] = I | (negsign ? 0x80000000u : 0u);
+        const bool tsign = negsign != ((host_popc(x & z) & 1) != 0);
+        T.e[x * m + z] = I | (negsign ? 0x80000000u : 0u) | (tsign ? 0x40000000u : 0u);
+    }
+    T.odd_xor = 0;
+    if (m == 16) {
+        // smallest multiple of 4 for which, for every z, the 16 gathers of an
+        // even row (blade offsets I) and of the next odd row (256 + (I ^ h))
+        // fall on 32 distinct LDS banks
+        for (unsigned h = 4; h < 256 && T.odd_xor == 0; h += 4) {
+            bool ok = true;
+            for (unsigned z = 0; z < 16 && ok; ++z) {
+                unsigned used = 0;
+                for (unsigned xx = 0; xx < 16 && ok; ++xx) {
+                    const unsigned I = T.e[xx * 16 + z] & 0xffffu;
+                    const unsigned b0 = I % 32, b1 = (256 + (I ^ h)) % 32;
+                    if ((used >> b0) & 1u) ok = false;
+                    used |= 1u << b0;
+                    if ((used >> b1) & 1u) ok = false;
+                    used |= 1u << b1;
+                }
+            }
+            if (ok) T.odd_xor = h;
+        }
     }
     return true;
 }
@@ -441,7 +697,7 @@ int rep_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64
     switch (n) {
         case 4: hipLaunchKernelGGL((rep_fwd_kernel<2>), grid, dim3(256), 0, s, a, b, c, (long long)batch, T); break;
         case 6: hipLaunchKernelGGL((rep_fwd_kernel<3>), grid, dim3(256), 0, s, a, b, c, (long long)batch, T); break;
-        case 8: hipLaunchKernelGGL((rep_fwd_kernel<4>), grid, dim3(256), 0, s, a, b, c, (long long)batch, T); break;
+        case 8: hipLaunchKernelGGL(rep16_fwd_kernel, grid, dim3(256), 0, s, a, b, c, (long long)batch, T); break;
         default: return set_error(CLF_ERR_UNSUPPORTED, "matrix path supports n = 4, 6, 8");
     }
     CLF_HIP_CHECK(hipGetLastError());
@@ -457,7 +713,7 @@ int rep_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc
     switch (n) {
         case 4: hipLaunchKernelGGL((rep_bwd_kernel<2>), grid, dim3(256), 0, s, a, b, gc, ga, gb, (long long)batch, T); break;
         case 6: hipLaunchKernelGGL((rep_bwd_kernel<3>), grid, dim3(256), 0, s, a, b, gc, ga, gb, (long long)batch, T); break;
-        case 8: hipLaunchKernelGGL((rep_bwd_kernel<4>), grid, dim3(256), 0, s, a, b, gc, ga, gb, (long long)batch, T); break;
+        case 8: hipLaunchKernelGGL(rep16_bwd_kernel, grid, dim3(256), 0, s, a, b, gc, ga, gb, (long long)batch, T); break;
         default: return set_error(CLF_ERR_UNSUPPORTED, "matrix path supports n = 4, 6, 8");
     }
     CLF_HIP_CHECK(hipGetLastError());

@@ -114,3 +114,104 @@ def from_matrix(M, label, sign, m):
     for I, (x, z) in enumerate(label):
         out[..., I] = sign[I] * t[..., x, z]
     return out
+
+
+# ---- lane-level model of the m = 16 matrix-core kernels -------------------
+# One wave converts four rows (row b on lanes 16b .. 16b+15, lane x = l % 16
+# holds W[x][.]). MFMA operands come from xor shuffles inside each 16-lane
+# row: A[x][k] = W_a[x ^ k][k]; the second operand uses the transposed
+# conversion (signs (-1)^{popc(x & z)} folded into t), so that
+# B[k][x] = phi(b)^T[x][k] = W'_b[x ^ k][k]. The 4-block 16x16x1 MFMA leaves
+# C_b[4g + t][j] in lane 16g + j, register 4b + t; the relayout stores it at
+# W_c[i ^ j][j] with a row stride of 20 floats, where lane (b, x) reads row x.
+
+RELAYOUT_STRIDE = 20
+
+
+def transpose_signs(label):
+    """(-1)^{popc(x & z)} per blade: phi(a')  = phi(a)^T for a'_I = that sign * a_I."""
+    return [-1 if popc(x & z) & 1 else 1 for (x, z) in label]
+
+
+def lane_W(rows, label, sign):
+    """W[b][x][c] for a (4, 256) group: the per-lane gather + WHT."""
+    m = 16
+    t = np.zeros((rows.shape[0], m, m))
+    for I, (x, z) in enumerate(label):
+        t[:, x, z] = sign[I] * rows[:, I]
+    return wht(t)
+
+
+def xor_operand(W):
+    """Operand register k of lane (b, x): W[b][x ^ k][k]."""
+    m = W.shape[-1]
+    op = np.zeros_like(W)
+    for x in range(m):
+        for k in range(m):
+            op[:, x, k] = W[:, x ^ k, k]
+    return op
+
+
+def mfma_4block_16x16x1(opA, opB):
+    """acc[l][4b + t] after sum_k of the 4-block MFMA with lane (b, i) giving
+    A_b[i][k] = opA[b][i][k] and lane (b, j) giving B_b[k][j] = opB[b][j][k]."""
+    acc = np.zeros((64, 16))
+    for b in range(4):
+        Cb = opA[b] @ opB[b].T            # C_b[i][j] = sum_k A_b[i][k] B_b[k][j]
+        for l in range(64):
+            g, j = l // 16, l % 16
+            for t in range(4):
+                acc[l, 4 * b + t] = Cb[4 * g + t, j]
+    return acc
+
+
+def relayout(acc, S=RELAYOUT_STRIDE):
+    """LDS round trip of the product: returns W_c[b][x][c] read back by lane (b, x)."""
+    lds = np.full(4 * 16 * S, np.nan)
+    for l in range(64):
+        g, j = l // 16, l % 16
+        for b in range(4):
+            for t in range(4):
+                i = 4 * g + t
+                lds[b * 16 * S + (i ^ j) * S + j] = acc[l, 4 * b + t]
+    Wc = np.zeros((4, 16, 16))
+    for b in range(4):
+        for x in range(16):
+            Wc[b, x] = lds[b * 16 * S + x * S: b * 16 * S + x * S + 16]
+    return Wc
+
+
+def lane_unconvert(Wc, label, sign):
+    t = wht(Wc) / 16.0
+    out = np.zeros((Wc.shape[0], 256))
+    for I, (x, z) in enumerate(label):
+        out[:, I] = sign[I] * t[:, x, z]
+    return out
+
+
+def kernel16_fwd(a, b, label, sign):
+    st = transpose_signs(label)
+    Wa = lane_W(a, label, sign)
+    Wbt = lane_W(b, label, [s * u for s, u in zip(sign, st)])
+    return lane_unconvert(relayout(mfma_4block_16x16x1(xor_operand(Wa), xor_operand(Wbt))), label, sign)
+
+
+def kernel16_bwd(a, b, gc, label, sign):
+    st = [s * u for s, u in zip(sign, transpose_signs(label))]
+    Wb, Wg = lane_W(b, label, sign), lane_W(gc, label, sign)
+    Wat, Wgt = lane_W(a, label, st), lane_W(gc, label, st)
+    ga = lane_unconvert(relayout(mfma_4block_16x16x1(xor_operand(Wg), xor_operand(Wb))), label, sign)
+    gb = lane_unconvert(relayout(mfma_4block_16x16x1(xor_operand(Wat), xor_operand(Wgt))), label, sign)
+    return ga, gb
+
+
+def odd_row_xor(label, stride=256):
+    """Smallest multiple of 4 that, xor-ed into the blade offsets of the odd
+    rows, makes every gather of a 32-lane half-wave (two rows) hit 32 distinct
+    banks; 0 if none does."""
+    inv = {lab: I for I, lab in enumerate(label)}
+    for h in range(0, 256, 4):
+        if all(len({inv[(x, z)] % 32 for x in range(16)} | {(stride + (inv[(x, z)] ^ h)) % 32 for x in range(16)}) == 32
+               for z in range(16)):
+            return h
+    return 0

@@ -46,3 +46,34 @@ def test_rep_product(metric):
     gb = R.from_matrix(np.swapaxes(A, -1, -2) @ G, label, sign, m)
     np.testing.assert_allclose(ga, aq.grad.numpy(), atol=1e-10)
     np.testing.assert_allclose(gb, bq.grad.numpy(), atol=1e-10)
+
+
+@pytest.mark.parametrize("metric", [(1,) * 8, (1,) * 4 + (-1,) * 4, (1,) * 5 + (-1,) * 3, (-1,) * 8,
+                                    (1, -1, 1, 1, -1, -1, 1, -1)])
+def test_rep16_lane_model(metric):
+    """The lane dataflow of the m = 16 matrix-core kernels (xor-shuffled
+    operands, transposed conversion, 4-block MFMA layout, stride-20 relayout)
+    gives the oracle's product and gradients."""
+    gens = R.find_generators(list(metric))
+    label, sign = R.blade_tables(list(metric), gens)
+    # the transposed conversion is the matrix transpose
+    e = np.random.default_rng(0).standard_normal((2, 256))
+    st = R.transpose_signs(label)
+    np.testing.assert_allclose(R.to_matrix(e * np.array(st), label, sign, 16),
+                               np.swapaxes(R.to_matrix(e, label, sign, 16), -1, -2), atol=1e-12)
+    g = torch.Generator().manual_seed(3)
+    a, b, gc = (torch.randn(4, 256, generator=g, dtype=torch.float64) for _ in range(3))
+    aq, bq = a.clone().requires_grad_(), b.clone().requires_grad_()
+    c_ref = O.einsum_product("geom", aq, bq, list(metric))
+    c_ref.backward(gc)
+    c = R.kernel16_fwd(a.numpy(), b.numpy(), label, sign)
+    np.testing.assert_allclose(c, c_ref.detach().numpy(), atol=1e-10)
+    ga, gb = R.kernel16_bwd(a.numpy(), b.numpy(), gc.numpy(), label, sign)
+    np.testing.assert_allclose(ga, aq.grad.numpy(), atol=1e-10)
+    np.testing.assert_allclose(gb, bq.grad.numpy(), atol=1e-10)
+    # a bank-conflict-free odd-row offset exists for the Euclidean and split
+    # tables (others fall back to offset 0: correct, with two-way conflicts)
+    h = R.odd_row_xor(label)
+    assert h % 4 == 0
+    if metric in [(1,) * 8, (1,) * 4 + (-1,) * 4]:
+        assert h > 0
