@@ -1,6 +1,10 @@
 // extern "C" entry points of libclifford_hip.so (declared in include/clifford_hip.h).
 #include <cstring>
 
+#include <map>
+#include <mutex>
+#include <tuple>
+
 #include "clf_common.h"
 
 namespace clf {
@@ -13,6 +17,34 @@ int set_error(int code, const std::string& msg) {
 }
 
 void clear_error() { g_last_error.clear(); }
+
+unsigned resident_grid(const void* kernel, int block_threads, size_t dyn_lds, long long wanted) {
+    static std::mutex mu;
+    static std::map<std::tuple<int, const void*, size_t>, long long> cache;
+    if (wanted < 1) return 1;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    long long cap = 0;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        auto key = std::make_tuple(dev, kernel, dyn_lds);
+        auto it = cache.find(key);
+        if (it != cache.end()) {
+            cap = it->second;
+        } else {
+            int per_cu = 0, cus = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block_threads, dyn_lds) != hipSuccess ||
+                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+                (void)hipGetLastError();  // clear the query's error; fall back to a fixed cap
+                per_cu = 2;
+                cus = 256;
+            }
+            cap = (long long)(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+            cache.emplace(key, cap);
+        }
+    }
+    return (unsigned)(wanted < cap ? wanted : cap);
+}
 
 int product_fwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const float* b, float* c,
                 int64_t batch, void* stream);

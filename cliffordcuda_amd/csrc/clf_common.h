@@ -22,6 +22,11 @@ constexpr int kMaxNGraded = 20;    // graded ops are elementwise; bound rows * 2
 int set_error(int code, const std::string& msg);
 void clear_error();
 
+// Grid for a persistent (grid-stride) kernel: min(wanted, the number of
+// workgroups of `kernel` that are resident at once on the current device),
+// from the runtime occupancy query, cached per (device, kernel, dynamic LDS).
+unsigned resident_grid(const void* kernel, int block_threads, size_t dyn_lds, long long wanted);
+
 #define CLF_HIP_CHECK(expr)                                                       \
     do {                                                                          \
         hipError_t _e = (expr);                                                   \

@@ -680,24 +680,30 @@ bool rep_applicable(int op, int n, uint32_t neg, uint32_t nul) {
     return rep_table(n, neg, T);
 }
 
-static unsigned rep_grid(int n, int64_t batch) {
+// Workgroups: one per 4 * (64 / m) rows, at most 2048 (8 per CU); the waves
+// walk the batch with a grid stride. More workgroups than are resident at once
+// measured faster than a grid of exactly the resident count.
+static long long rep_blocks(int n, int64_t batch) {
     const int m = 1 << (n / 2);
     const long long rows_per_block = 4LL * (64 / m);
-    long long g = (batch + rows_per_block - 1) / rows_per_block;
-    const long long cap = 256LL * 8;  // enough waves to fill the chip, then walk the batch
-    if (g > cap) g = cap;
-    return (unsigned)(g < 1 ? 1 : g);
+    const long long g = (batch + rows_per_block - 1) / rows_per_block;
+    const long long cap = 256LL * 8;
+    return g < 1 ? 1 : (g > cap ? cap : g);
 }
 
 int rep_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64_t batch, void* stream) {
     RepTable T;
     if (!rep_table(n, neg, T)) return set_error(CLF_ERR_UNSUPPORTED, "signature has no real matrix representation");
     hipStream_t s = (hipStream_t)stream;
-    const dim3 grid(rep_grid(n, batch));
+    const long long want = rep_blocks(n, batch);
+#define CLF_REP_GRID(K) dim3((unsigned)want)
     switch (n) {
-        case 4: hipLaunchKernelGGL((rep_fwd_kernel<2>), grid, dim3(256), 0, s, a, b, c, (long long)batch, T); break;
-        case 6: hipLaunchKernelGGL((rep_fwd_kernel<3>), grid, dim3(256), 0, s, a, b, c, (long long)batch, T); break;
-        case 8: hipLaunchKernelGGL(rep16_fwd_kernel, grid, dim3(256), 0, s, a, b, c, (long long)batch, T); break;
+        case 4: hipLaunchKernelGGL((rep_fwd_kernel<2>), CLF_REP_GRID(rep_fwd_kernel<2>), dim3(256), 0, s, a, b, c,
+                                   (long long)batch, T); break;
+        case 6: hipLaunchKernelGGL((rep_fwd_kernel<3>), CLF_REP_GRID(rep_fwd_kernel<3>), dim3(256), 0, s, a, b, c,
+                                   (long long)batch, T); break;
+        case 8: hipLaunchKernelGGL(rep16_fwd_kernel, CLF_REP_GRID(rep16_fwd_kernel), dim3(256), 0, s, a, b, c,
+                                   (long long)batch, T); break;
         default: return set_error(CLF_ERR_UNSUPPORTED, "matrix path supports n = 4, 6, 8");
     }
     CLF_HIP_CHECK(hipGetLastError());
@@ -709,13 +715,17 @@ int rep_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc
     RepTable T;
     if (!rep_table(n, neg, T)) return set_error(CLF_ERR_UNSUPPORTED, "signature has no real matrix representation");
     hipStream_t s = (hipStream_t)stream;
-    const dim3 grid(rep_grid(n, batch));
+    const long long want = rep_blocks(n, batch);
     switch (n) {
-        case 4: hipLaunchKernelGGL((rep_bwd_kernel<2>), grid, dim3(256), 0, s, a, b, gc, ga, gb, (long long)batch, T); break;
-        case 6: hipLaunchKernelGGL((rep_bwd_kernel<3>), grid, dim3(256), 0, s, a, b, gc, ga, gb, (long long)batch, T); break;
-        case 8: hipLaunchKernelGGL(rep16_bwd_kernel, grid, dim3(256), 0, s, a, b, gc, ga, gb, (long long)batch, T); break;
+        case 4: hipLaunchKernelGGL((rep_bwd_kernel<2>), CLF_REP_GRID(rep_bwd_kernel<2>), dim3(256), 0, s, a, b, gc, ga,
+                                   gb, (long long)batch, T); break;
+        case 6: hipLaunchKernelGGL((rep_bwd_kernel<3>), CLF_REP_GRID(rep_bwd_kernel<3>), dim3(256), 0, s, a, b, gc, ga,
+                                   gb, (long long)batch, T); break;
+        case 8: hipLaunchKernelGGL(rep16_bwd_kernel, CLF_REP_GRID(rep16_bwd_kernel), dim3(256), 0, s, a, b, gc, ga, gb,
+                                   (long long)batch, T); break;
         default: return set_error(CLF_ERR_UNSUPPORTED, "matrix path supports n = 4, 6, 8");
     }
+#undef CLF_REP_GRID
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }

@@ -189,6 +189,11 @@ __device__ __forceinline__ void store_row_part(const float (&v)[1 << RB], float*
 }
 
 // y = Lambda(Q) x (FWD) or Lambda(Q)^T x (!FWD), one row per 2^(N-RB) lanes.
+// Persistent: the lanes of a row walk rows with a grid stride and load the
+// next row part while the current one is rotated. Rows past the end are never
+// stored; their prefetch re-reads the last row (a cache hit, no branch).
+// The loop condition is the same for all lanes of a row, so a row's lanes
+// stay active together and every shuffle partner is active.
 template <int N, bool FWD>
 __global__ __launch_bounds__(256) void rotor_apply_kernel(const float* __restrict__ state,
                                                            const float* __restrict__ X, float* __restrict__ Y,
@@ -196,17 +201,26 @@ __global__ __launch_bounds__(256) void rotor_apply_kernel(const float* __restric
     constexpr int RB = rotor_rb(N);
     constexpr int LB = N - RB;
     const float* cs = state + N * N;
-    const long long gtid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long row = gtid >> LB;
-    const unsigned L = (unsigned)(gtid & ((1 << LB) - 1));
-    // whole rows only: a row's lanes are in one wave, so every lane that
-    // shuffles with a partner has that partner active
-    if (row >= batch) return;
+    const unsigned L = threadIdx.x & ((1u << LB) - 1u);
+    const long long rows_per_block = 256 >> LB;
+    const long long stride = (long long)gridDim.x * rows_per_block;
+    long long row = (long long)blockIdx.x * rows_per_block + (threadIdx.x >> LB);
+    const long long lane_off = (long long)L << RB;
     float v[1 << RB];
-    const long long off = (row << N) + ((long long)L << RB);
-    load_row_part<RB>(v, X + off);
-    rot_chain<N, RB, FWD>(v, cs, L);
-    store_row_part<RB>(v, Y + off);
+    load_row_part<RB>(v, X + ((row < batch ? row : batch - 1) << N) + lane_off);
+    for (; row < batch; row += stride) {
+        const long long nrow = row + stride;
+        float nv[1 << RB];
+        load_row_part<RB>(nv, X + ((nrow < batch ? nrow : batch - 1) << N) + lane_off);
+        // an opaque copy of L per row keeps the per-plane lane factors inside
+        // the loop instead of being hoisted into VGPRs for all planes
+        unsigned Lr = L;
+        asm volatile("" : "+v"(Lr));
+        rot_chain<N, RB, FWD>(v, cs, Lr);
+        store_row_part<RB>(v, Y + (row << N) + lane_off);
+#pragma unroll
+        for (int r = 0; r < (1 << RB); ++r) v[r] = nv[r];
+    }
 }
 
 // ---- backward: gx = Lambda(Q)^T gy and the per-workgroup partial skew(Gamma) --
@@ -673,16 +687,28 @@ template <int N>
 static void launch_apply(bool fwd, const float* state, const float* x, float* y, int64_t batch, hipStream_t s) {
     constexpr int LB = N - rotor_rb(N);
     const long long threads = (long long)batch << LB;
-    const dim3 grid((unsigned)((threads + 255) / 256));
-    if (fwd) hipLaunchKernelGGL((rotor_apply_kernel<N, true>), grid, dim3(256), 0, s, state, x, y, (long long)batch);
-    else hipLaunchKernelGGL((rotor_apply_kernel<N, false>), grid, dim3(256), 0, s, state, x, y, (long long)batch);
+    const long long wanted = (threads + 255) / 256;
+    if (fwd) {
+        const dim3 grid(resident_grid((const void*)rotor_apply_kernel<N, true>, 256, 0, wanted));
+        hipLaunchKernelGGL((rotor_apply_kernel<N, true>), grid, dim3(256), 0, s, state, x, y, (long long)batch);
+    } else {
+        const dim3 grid(resident_grid((const void*)rotor_apply_kernel<N, false>, 256, 0, wanted));
+        hipLaunchKernelGGL((rotor_apply_kernel<N, false>), grid, dim3(256), 0, s, state, x, y, (long long)batch);
+    }
+}
+
+// Backward grid: at most rotor_bwd_grid (the workspace bound), at most the
+// resident workgroups. The gamma finalize reads this many partials.
+template <int N>
+static unsigned bwd_launch_grid(int64_t batch) {
+    return resident_grid((const void*)rotor_apply_bwd_kernel<N>, 256, 0, rotor_bwd_grid(N, batch));
 }
 
 template <int N>
 static void launch_apply_bwd(const float* state, const float* x, const float* gy, float* gx, float* ws,
                              int64_t batch, hipStream_t s) {
-    hipLaunchKernelGGL((rotor_apply_bwd_kernel<N>), dim3(rotor_bwd_grid(N, batch)), dim3(256), 0, s, state, x, gy, gx,
-                       ws, (long long)batch);
+    hipLaunchKernelGGL((rotor_apply_bwd_kernel<N>), dim3(bwd_launch_grid<N>(batch)), dim3(256), 0, s, state, x, gy,
+                       gx, ws, (long long)batch);
 }
 
 
@@ -728,7 +754,12 @@ int rotor_apply_bwd(int n, const float* state, const float* x, const float* gy, 
         CLF_HIP_CHECK(hipGetLastError());
     }
     if (g_state) {
-        const int nparts = batch > 0 ? rotor_bwd_grid(n, batch) : 0;
+        int nparts = 0;
+        if (batch > 0) {
+#define CLF_CALL(N) nparts = (int)bwd_launch_grid<N>(batch)
+            CLF_ROTOR_DISPATCH(n, CLF_CALL)
+#undef CLF_CALL
+        }
         hipLaunchKernelGGL(rotor_gamma_finalize_kernel, dim3(1), dim3(1024), 0, s, n, state, gws, nparts, g_state);
         CLF_HIP_CHECK(hipGetLastError());
     }

@@ -31,3 +31,28 @@ def test_rotor_model_matches_oracle():
     # only the antisymmetric part of Gamma reaches the bivector (Q stays in SO(n))
     gb_skew = M.compile_bwd(biv[0].numpy(), n, Q @ (0.5 * (G - G.T)))
     np.testing.assert_allclose(gb_skew, bq.grad[0].numpy(), atol=1e-10)
+
+
+def test_skew_sums_over_output_conjugate():
+    """The kernels accumulate the pair sums over the forward output and its
+    gradient: skew Gamma(x, gx) = Q^T skew Gamma(y, gy) Q, hence
+    dL/dQ = Q skew Gamma(x, gx) = skew Gamma(y, gy) Q."""
+    n = 6
+    rng = np.random.default_rng(5)
+    biv = 0.5 * rng.standard_normal(15)
+    Q = scipy.linalg.expm(M.generator(biv, n))
+    cs, _ = M.givens(Q)
+    x = rng.standard_normal((4, 64))
+    gy = rng.standard_normal((4, 64))
+    y = M.apply(cs, x)
+    gx = M.apply(cs, gy, transpose=True)
+    G, Gy = M.gamma(x, gx, n), M.gamma(y, gy, n)
+    K, Ky = 0.5 * (G - G.T), 0.5 * (Gy - Gy.T)
+    np.testing.assert_allclose(K, Q.T @ Ky @ Q, atol=1e-12)
+    np.testing.assert_allclose(Q @ K, Ky @ Q, atol=1e-12)
+    # and the result is the oracle's bivector gradient
+    g = torch.Generator().manual_seed(2)
+    bq = torch.tensor(biv, dtype=torch.float64).reshape(1, -1).requires_grad_()
+    xq = torch.tensor(x).requires_grad_()
+    O.apply_bivector(bq, xq, n).backward(torch.tensor(gy))
+    np.testing.assert_allclose(M.compile_bwd(biv, n, Ky @ Q), bq.grad[0].numpy(), atol=1e-10)
