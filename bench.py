@@ -230,9 +230,28 @@ def products_config(args, torch, cc, lib, T, name, metric, B, ops, fwd_only=Fals
             flops += 4.0 * nt * B
             byts += 20.0 * D * B
         t = (entry["fwd_ms"] + entry.get("bwd_ms", 0.0)) * 1e-3
+        # "tflops_algorithmic" counts the reference's nonzero sigma terms; for
+        # the geometric product of real / split signatures the library runs the
+        # matrix-representation kernels, so there it is an equivalent rate
         entry.update({"pairs_per_s": B / t, "tflops_algorithmic": flops / t / 1e12,
                       "frac_fp32_peak": flops / t / 1e12 / PEAK_FP32_TFLOPS,
                       "hbm_gbs_algorithmic": byts / t / 1e9, "frac_hbm": byts / t / 1e9 / PEAK_HBM_GBS})
+        if op == "geom":
+            # the per-term kernels at the same shape (the path of every other op)
+            os.environ["CLF_GEOM_PATH"] = "direct"
+            try:
+                dfms = T.kernel_ms(lambda: lib.clf_product_fwd(code, n, neg, nul, a.data_ptr(), b.data_ptr(),
+                                                               c.data_ptr(), B, sp))
+                dbms = 0.0
+                if not fwd_only:
+                    dbms = T.kernel_ms(lambda: lib.clf_product_bwd(code, n, neg, nul, a.data_ptr(), b.data_ptr(),
+                                                                   gc.data_ptr(), ga.data_ptr(), gb.data_ptr(), B,
+                                                                   sp))
+            finally:
+                del os.environ["CLF_GEOM_PATH"]
+            dt = (dfms + dbms) * 1e-3
+            entry["per_term_path"] = {"fwd_ms": dfms, "bwd_ms": dbms, "pairs_per_s": B / dt,
+                                      "valu_frac": flops / dt / 1e12 / PEAK_FP32_TFLOPS}
         res[op] = entry
     return {"workload": name, "metric": metric, "batch": B, "results": res}
 

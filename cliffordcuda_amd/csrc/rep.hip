@@ -25,11 +25,9 @@
 #include <map>
 #include <mutex>
 
-#include "clf_common.h"
+#include "rep_common.h"
 
 namespace clf {
-
-constexpr int kRepMaxLogM = 4;  // m <= 16 (n <= 8): the table fits the kernel arguments
 
 struct RepTable {
     // entry [x * m + z]: blade index | 0x80000000 if the sign s(I) is -1
@@ -39,25 +37,6 @@ struct RepTable {
     // that the gathers of two rows in one half-wave use distinct banks (0: none found)
     unsigned odd_xor;
 };
-
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-template <int M>
-__device__ __forceinline__ void wht_inplace(float (&v)[M]) {
-#pragma unroll
-    for (int h = 1; h < M; h <<= 1)
-#pragma unroll
-        for (int i = 0; i < M; ++i)
-            if (!(i & h)) {
-                const float a = v[i], b = v[i + h];
-                v[i] = a + b;
-                v[i + h] = a - b;
-            }
-}
 
 // gather t[z] = s * row[blade] from the staged row, WHT over z, and write the
 // standard-layout matrix phi[r][c] = W[r ^ c][c] (lane holds x) into mat
@@ -357,60 +336,6 @@ __global__ __launch_bounds__(256) void rep_bwd_kernel(const float* __restrict__ 
 // back through LDS as W_c[i ^ j][j] at row stride 20 floats, which keeps both
 // the scattered b32 writes and the b128 row reads free of bank conflicts.
 
-typedef float floatx16 __attribute__((ext_vector_type(16)));
-
-template <unsigned CTRL>
-__device__ __forceinline__ float dpp16(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
-}
-
-// value of v at lane (lane ^ K) of the same 16-lane row
-template <unsigned K>
-__device__ __forceinline__ float xor16(float v) {
-    constexpr unsigned k1 = (K & 8u) ? (K ^ 15u) : K;    // row_mirror: xor 15
-    constexpr unsigned k2 = (k1 & 4u) ? (k1 ^ 7u) : k1;  // row_half_mirror: xor 7
-    if constexpr ((K & 8u) != 0u) v = dpp16<0x140>(v);
-    if constexpr ((k1 & 4u) != 0u) v = dpp16<0x141>(v);
-    if constexpr (k2 == 1u) v = dpp16<0xB1>(v);       // quad_perm [1,0,3,2]
-    else if constexpr (k2 == 2u) v = dpp16<0x4E>(v);  // quad_perm [2,3,0,1]
-    else if constexpr (k2 == 3u) v = dpp16<0x1B>(v);  // quad_perm [3,2,1,0]
-    return v;
-}
-
-template <unsigned... K>
-__device__ __forceinline__ floatx16 mfma_chain(const float (&wa)[16], const float (&wb)[16],
-                                               std::integer_sequence<unsigned, K...>) {
-    floatx16 acc = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    ((acc = __builtin_amdgcn_mfma_f32_16x16x1f32(xor16<K>(wa[K]), xor16<K>(wb[K]), acc, 0, 0, 0)), ...);
-    return acc;
-}
-
-constexpr int kRelayoutStride = 20;
-constexpr int kRelayoutBlock = 16 * kRelayoutStride;  // floats per row of the group
-
-// lane (g, j) writes C_b[4g + t][j] (register 4b + t) to W_c[(4g + t) ^ j][j]
-__device__ __forceinline__ void relayout_store(float* __restrict__ dst, const floatx16& acc, int lane) {
-    const unsigned g = (unsigned)lane >> 4, j = (unsigned)lane & 15u;
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-            dst[b * kRelayoutBlock + (((4u * g + t) ^ j) * kRelayoutStride) + j] = acc[4 * b + t];
-}
-
-// lane (b, x) reads W_c[x][0..15] of row b
-__device__ __forceinline__ void relayout_load(const float* __restrict__ src, int b, unsigned x, float (&w)[16]) {
-    const float4* p = reinterpret_cast<const float4*>(src + b * kRelayoutBlock + x * kRelayoutStride);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const float4 t = p[q];
-        w[4 * q] = t.x;
-        w[4 * q + 1] = t.y;
-        w[4 * q + 2] = t.z;
-        w[4 * q + 3] = t.w;
-    }
-}
-
 // Group of four rows: lane l moves float4 chunk l of row j (j = 0..3); rows
 // past the end re-read the last row and are never stored.
 struct Pre16 {
@@ -497,7 +422,7 @@ __global__ __launch_bounds__(256) void rep16_fwd_kernel(const float* __restrict_
         wave_lds_sync();
         wht_inplace<16>(wa);
         wht_inplace<16>(wb);
-        const floatx16 acc = mfma_chain(wa, wb, std::make_integer_sequence<unsigned, 16>{});
+        const floatx16 acc = mfma_chain(wa, wb);
         relayout_store(sa, acc, lane);
         wave_lds_sync();
         float wc[16];
@@ -551,13 +476,13 @@ __global__ __launch_bounds__(256) void rep16_bwd_kernel(const float* __restrict_
         if (want_a) {
             wht_inplace<16>(wg);
             wht_inplace<16>(wb);
-            const floatx16 acc = mfma_chain(wg, wb, std::make_integer_sequence<unsigned, 16>{});
+            const floatx16 acc = mfma_chain(wg, wb);
             relayout_store(rel_a, acc, lane);
         }
         if (want_b) {
             wht_inplace<16>(wat);
             wht_inplace<16>(wgt);
-            const floatx16 acc = mfma_chain(wat, wgt, std::make_integer_sequence<unsigned, 16>{});
+            const floatx16 acc = mfma_chain(wat, wgt);
             relayout_store(rel_b, acc, lane);
         }
         wave_lds_sync();
@@ -575,46 +500,6 @@ __global__ __launch_bounds__(256) void rep16_bwd_kernel(const float* __restrict_
 }
 
 // ---- host side --------------------------------------------------------------
-
-static int host_popc(unsigned v) { return __builtin_popcount(v); }
-
-// Generators for the metric (bit g of neg set: e_g^2 = -1), or false if the
-// signature is not a real matrix algebra of size 2^(n/2).
-static bool rep_generators(int n, uint32_t neg, unsigned* gx, unsigned* gz) {
-    if (n % 2 || n < 2 || n > 2 * kRepMaxLogM) return false;
-    const int q = host_popc(neg), p = n - q;
-    const int d = ((p - q) % 8 + 8) % 8;
-    if (d != 0 && d != 2) return false;
-    const int k = n / 2;
-    const unsigned span = 1u << k;
-    // depth-first search in a fixed order (deterministic)
-    int g = 0;
-    unsigned cand[16] = {0};
-    while (g >= 0 && g < n) {
-        bool found = false;
-        for (unsigned c = cand[g] + 1; c < span * span; ++c) {
-            const unsigned cx = c / span, cz = c % span;
-            const int want = ((neg >> g) & 1u) ? 1 : 0;  // square -1 <=> popc(z & x) odd
-            if ((host_popc(cx & cz) & 1) != want) continue;
-            bool ok = true;
-            for (int h = 0; h < g && ok; ++h) ok = ((host_popc(cz & gx[h]) + host_popc(gz[h] & cx)) & 1) == 1;
-            if (!ok) continue;
-            cand[g] = c;
-            gx[g] = cx;
-            gz[g] = cz;
-            found = true;
-            break;
-        }
-        if (found) {
-            ++g;
-            if (g < n) cand[g] = 0;
-        } else {
-            cand[g] = 0;
-            --g;
-        }
-    }
-    return g == n;
-}
 
 static bool rep_table_build(int n, uint32_t neg, RepTable& T) {
     unsigned gx[16], gz[16];
@@ -672,9 +557,16 @@ static bool rep_table(int n, uint32_t neg, RepTable& T) {
     return it->second.first;
 }
 
-// The matrix path serves the geometric product when the signature allows it;
+bool split_applicable(int op, int n, uint32_t neg, uint32_t nul);
+int split_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64_t batch, void* stream);
+int split_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc, float* ga, float* gb,
+              int64_t batch, void* stream);
+
+// The matrix path serves the geometric product when the signature allows it
+// (real type, n = 4, 6, 8; split type n = 9, and n = 10 with e_9 null);
 // returns false otherwise (the caller uses the per-term kernels).
 bool rep_applicable(int op, int n, uint32_t neg, uint32_t nul) {
+    if (n == 9 || n == 10) return split_applicable(op, n, neg, nul);
     if (op != CLF_OP_GEOM || nul != 0u || n < 4 || n > 2 * kRepMaxLogM) return false;
     RepTable T;
     return rep_table(n, neg, T);
@@ -692,6 +584,7 @@ static long long rep_blocks(int n, int64_t batch) {
 }
 
 int rep_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64_t batch, void* stream) {
+    if (n == 9 || n == 10) return split_fwd(n, neg, a, b, c, batch, stream);
     RepTable T;
     if (!rep_table(n, neg, T)) return set_error(CLF_ERR_UNSUPPORTED, "signature has no real matrix representation");
     hipStream_t s = (hipStream_t)stream;
@@ -712,6 +605,7 @@ int rep_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64
 
 int rep_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc, float* ga, float* gb, int64_t batch,
             void* stream) {
+    if (n == 9 || n == 10) return split_bwd(n, neg, a, b, gc, ga, gb, batch, stream);
     RepTable T;
     if (!rep_table(n, neg, T)) return set_error(CLF_ERR_UNSUPPORTED, "signature has no real matrix representation");
     hipStream_t s = (hipStream_t)stream;

@@ -1,0 +1,145 @@
+// Shared pieces of the matrix-representation kernels (rep.hip, rep_split.hip):
+// wave-local LDS ordering, the in-register Walsh-Hadamard transform, the DPP
+// xor shuffles that build MFMA operands, the 4-block 16x16 MFMA chain with its
+// LDS relayout, and the host search for real Pauli generators.
+#pragma once
+
+#include <utility>
+
+#include "clf_common.h"
+
+namespace clf {
+
+constexpr int kRepMaxLogM = 4;  // m <= 16: the tables fit the kernel arguments
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int M>
+__device__ __forceinline__ void wht_inplace(float (&v)[M]) {
+#pragma unroll
+    for (int h = 1; h < M; h <<= 1)
+#pragma unroll
+        for (int i = 0; i < M; ++i)
+            if (!(i & h)) {
+                const float a = v[i], b = v[i + h];
+                v[i] = a + b;
+                v[i + h] = a - b;
+            }
+}
+
+// ---- 16 x 16 blocks on the matrix cores -------------------------------------
+// The 4-block v_mfma_f32_16x16x1f32 multiplies four independent 16x16 matrices,
+// block b taking its operands from lanes 16b .. 16b + 15. With lane x holding
+// W[x][.] of a conversion (phi[r][c] = W[r ^ c][c]), operand k of lane x is
+// W[x ^ k][k]: an xor shuffle inside the 16-lane row, done with DPP moves
+// (quad_perm for xor 1..3, row_half_mirror = xor 7, row_mirror = xor 15).
+// The product C_b[4g + t][j] lands in lane 16g + j, register 4b + t; it goes
+// back through LDS as W_c[i ^ j][j] at row stride 20 floats, which keeps both
+// the scattered b32 writes and the b128 row reads free of bank conflicts.
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+template <unsigned CTRL>
+__device__ __forceinline__ float dpp16(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// value of v at lane (lane ^ K) of the same 16-lane row
+template <unsigned K>
+__device__ __forceinline__ float xor16(float v) {
+    constexpr unsigned k1 = (K & 8u) ? (K ^ 15u) : K;    // row_mirror: xor 15
+    constexpr unsigned k2 = (k1 & 4u) ? (k1 ^ 7u) : k1;  // row_half_mirror: xor 7
+    if constexpr ((K & 8u) != 0u) v = dpp16<0x140>(v);
+    if constexpr ((k1 & 4u) != 0u) v = dpp16<0x141>(v);
+    if constexpr (k2 == 1u) v = dpp16<0xB1>(v);       // quad_perm [1,0,3,2]
+    else if constexpr (k2 == 2u) v = dpp16<0x4E>(v);  // quad_perm [2,3,0,1]
+    else if constexpr (k2 == 3u) v = dpp16<0x1B>(v);  // quad_perm [3,2,1,0]
+    return v;
+}
+
+template <unsigned... K>
+__device__ __forceinline__ floatx16 mfma_chain_acc(floatx16 acc, const float (&wa)[16], const float (&wb)[16],
+                                                   std::integer_sequence<unsigned, K...>) {
+    ((acc = __builtin_amdgcn_mfma_f32_16x16x1f32(xor16<K>(wa[K]), xor16<K>(wb[K]), acc, 0, 0, 0)), ...);
+    return acc;
+}
+
+// acc = sum_k A_b[.][k] B_b[k][.] for the four blocks, operands as above
+__device__ __forceinline__ floatx16 mfma_chain(const float (&wa)[16], const float (&wb)[16]) {
+    const floatx16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    return mfma_chain_acc(zero, wa, wb, std::make_integer_sequence<unsigned, 16>{});
+}
+
+constexpr int kRelayoutStride = 20;
+constexpr int kRelayoutBlock = 16 * kRelayoutStride;  // floats per row of the group
+
+// lane (g, j) writes C_b[4g + t][j] (register 4b + t) to W_c[(4g + t) ^ j][j]
+__device__ __forceinline__ void relayout_store(float* __restrict__ dst, const floatx16& acc, int lane) {
+    const unsigned g = (unsigned)lane >> 4, j = (unsigned)lane & 15u;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            dst[b * kRelayoutBlock + (((4u * g + t) ^ j) * kRelayoutStride) + j] = acc[4 * b + t];
+}
+
+// lane (b, x) reads W_c[x][0..15] of row b
+__device__ __forceinline__ void relayout_load(const float* __restrict__ src, int b, unsigned x, float (&w)[16]) {
+    const float4* p = reinterpret_cast<const float4*>(src + b * kRelayoutBlock + x * kRelayoutStride);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 t = p[q];
+        w[4 * q] = t.x;
+        w[4 * q + 1] = t.y;
+        w[4 * q + 2] = t.z;
+        w[4 * q + 3] = t.w;
+    }
+}
+
+// ---- host: generators -------------------------------------------------------
+
+inline int host_popc(unsigned v) { return __builtin_popcount(v); }
+
+// Generators for the metric (bit g of neg set: e_g^2 = -1), or false if the
+// signature is not a real matrix algebra of size 2^(n/2).
+inline bool rep_generators(int n, uint32_t neg, unsigned* gx, unsigned* gz) {
+    if (n % 2 || n < 2 || n > 2 * kRepMaxLogM) return false;
+    const int q = host_popc(neg), p = n - q;
+    const int d = ((p - q) % 8 + 8) % 8;
+    if (d != 0 && d != 2) return false;
+    const int k = n / 2;
+    const unsigned span = 1u << k;
+    // depth-first search in a fixed order (deterministic)
+    int g = 0;
+    unsigned cand[16] = {0};
+    while (g >= 0 && g < n) {
+        bool found = false;
+        for (unsigned c = cand[g] + 1; c < span * span; ++c) {
+            const unsigned cx = c / span, cz = c % span;
+            const int want = ((neg >> g) & 1u) ? 1 : 0;  // square -1 <=> popc(z & x) odd
+            if ((host_popc(cx & cz) & 1) != want) continue;
+            bool ok = true;
+            for (int h = 0; h < g && ok; ++h) ok = ((host_popc(cz & gx[h]) + host_popc(gz[h] & cx)) & 1) == 1;
+            if (!ok) continue;
+            cand[g] = c;
+            gx[g] = cx;
+            gz[g] = cz;
+            found = true;
+            break;
+        }
+        if (found) {
+            ++g;
+            if (g < n) cand[g] = 0;
+        } else {
+            cand[g] = 0;
+            --g;
+        }
+    }
+    return g == n;
+}
+
+}  // namespace clf

@@ -215,3 +215,104 @@ def odd_row_xor(label, stride=256):
                for z in range(16)):
             return h
     return 0
+
+
+# ---- split representation for n' = 9 (p - q = 1 mod 8) and one null top generator ----
+# Cl(p', q') with 9 generators and p' - q' = 1 (mod 8) is M_16(R) + M_16(R):
+# generators 0..7 (a real-type signature) use the m = 16 tables above and
+# phi_+-(e_8) = +-phi(E_8), E_8 = e_0 ... e_7 (phi(E_8)^2 = e_8^2 always holds
+# then). Every label (x, z) is hit by one blade I0 without e_8 and one blade I1
+# with it: t_+-[x][z] = s(I0) a_I0 +- s(I1) a_I1, and the inverse is
+# a_I0 = s(I0) (t_+ + t_-) / 2, a_I1 = s(I1) (t_+ - t_-) / 2 (times 1/16 after
+# the inverse WHT). T(a) = (phi_+(a), phi_-(a)) is orthogonal up to 32.
+
+
+def split_tables(metric9):
+    """label (x, z) and sign s(I) of each of the 512 blades of a 9-generator
+    signature with p - q = 1 (mod 8); None if it does not split that way."""
+    m9 = list(metric9)
+    if len(m9) != 9 or 0 in m9 or (m9.count(1) - m9.count(-1)) % 8 != 1:
+        return None
+    gens = find_generators(m9[:8])
+    lab8, sgn8 = blade_tables(m9[:8], gens)
+    xE, zE = lab8[255]
+    sE = sgn8[255]
+    label, sign = [], []
+    for I in range(512):
+        Il = I & 255
+        x, z = lab8[Il]
+        s = sgn8[Il]
+        if I >> 8:
+            if popc(z & xE) & 1:
+                s = -s
+            s *= sE
+            x, z = x ^ xE, z ^ zE
+        label.append((x, z))
+        sign.append(s)
+    return label, sign
+
+
+def split_to_matrices(a, label, sign, hat=False):
+    """(..., 512) -> (..., 2, 16, 16): phi_+(a), phi_-(a) (hat: of the grade involution)."""
+    tp = np.zeros(a.shape[:-1] + (16, 16))
+    tm = np.zeros_like(tp)
+    for I, (x, z) in enumerate(label):
+        v = sign[I] * a[..., I] * ((-1) ** popc(I) if hat else 1)
+        tp[..., x, z] += v
+        tm[..., x, z] += -v if I >> 8 else v
+    out = []
+    for t in (tp, tm):
+        W = wht(t)
+        M = np.zeros_like(W)
+        for r in range(16):
+            for c in range(16):
+                M[..., r, c] = W[..., r ^ c, c]
+        out.append(M)
+    return np.stack(out, axis=-3)
+
+
+def split_from_matrices(M, label, sign):
+    ts = []
+    for s in range(2):
+        W = np.zeros_like(M[..., s, :, :])
+        for x in range(16):
+            for c in range(16):
+                W[..., x, c] = M[..., s, x ^ c, c]
+        ts.append(wht(W) / 16.0)
+    tp, tm = ts
+    out = np.zeros(M.shape[:-3] + (512,))
+    for I, (x, z) in enumerate(label):
+        out[..., I] = sign[I] * ((tp[..., x, z] - tm[..., x, z]) if I >> 8 else (tp[..., x, z] + tm[..., x, z])) / 2.0
+    return out
+
+
+def pair_sum(pairs, label, sign):
+    """T^{-1}(sum_p opA(T(X_p)) opB(T(Y_p))); pairs of (X, Y, transA, transB, hatX, hatY)."""
+    acc = 0.0
+    for X, Y, ta, tb, hx, hy in pairs:
+        A = split_to_matrices(X, label, sign, hx)
+        B = split_to_matrices(Y, label, sign, hy)
+        if ta:
+            A = np.swapaxes(A, -1, -2)
+        if tb:
+            B = np.swapaxes(B, -1, -2)
+        acc = acc + A @ B
+    return split_from_matrices(acc, label, sign)
+
+
+def degenerate10_fwd(L, R, label, sign):
+    """Cl(p', q', 1), null generator 9: (L0 + L1 e9)(R0 + R1 e9) = L0 R0 + (L0 R1 + L1 R0^) e9."""
+    L0, L1, R0, R1 = L[..., :512], L[..., 512:], R[..., :512], R[..., 512:]
+    c0 = pair_sum([(L0, R0, False, False, False, False)], label, sign)
+    c1 = pair_sum([(L0, R1, False, False, False, False), (L1, R0, False, False, False, True)], label, sign)
+    return np.concatenate([c0, c1], axis=-1)
+
+
+def degenerate10_bwd(L, R, G, label, sign):
+    L0, L1, R0, R1 = L[..., :512], L[..., 512:], R[..., :512], R[..., 512:]
+    G0, G1 = G[..., :512], G[..., 512:]
+    gL0 = pair_sum([(G0, R0, False, True, False, False), (G1, R1, False, True, False, False)], label, sign)
+    gL1 = pair_sum([(G1, R0, False, True, False, True)], label, sign)
+    gR0 = pair_sum([(L0, G0, True, False, False, False), (L1, G1, True, False, True, True)], label, sign)
+    gR1 = pair_sum([(L0, G1, True, False, False, False)], label, sign)
+    return np.concatenate([gL0, gL1], axis=-1), np.concatenate([gR0, gR1], axis=-1)

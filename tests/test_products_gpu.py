@@ -247,3 +247,42 @@ def test_matrix_path_equals_direct_path_full_batch(monkeypatch):
     monkeypatch.delenv("CLF_GEOM_PATH")
     for u, v in ((c1, c2), (ga1, ga2), (gb1, gb2)):
         assert rel_err(u, v) <= TOL
+
+
+SPLIT_TYPE = [(1,) * 9, (1,) * 5 + (-1,) * 4, (1,) + (-1,) * 8, (1, -1) * 4 + (1,), (1,) * 9 + (0,),
+              (1,) * 5 + (-1,) * 4 + (0,)]
+
+
+@pytest.mark.parametrize("metric", SPLIT_TYPE, ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
+@pytest.mark.parametrize("batch", [1, 37])
+def test_split_path_geom_parity(metric, batch):
+    """n = 9 signatures with p - q = 1 (mod 8) and their extension by a null
+    e_9 take the split-representation kernels for the geometric product
+    (odd batches exercise the clamped last row of a two-row group)."""
+    e = run_case("geom", metric, batch)
+    assert max(e) <= TOL, e
+
+
+def test_split_path_equals_direct_path_c5_full_batch(monkeypatch):
+    """C5 shape (Cl(9,0,1), batch 16384): the split-representation kernels and
+    the per-term kernels agree on the whole batch, values and both gradients."""
+    metric = (1,) * 9 + (0,)
+    g = torch.Generator().manual_seed(2)
+    B = 16384
+    a = torch.randn(B, 1024, generator=g).cuda()
+    b = torch.randn(B, 1024, generator=g).cuda()
+    gc = torch.randn(B, 1024, generator=g).cuda()
+
+    def run():
+        x = a.clone().requires_grad_()
+        y = b.clone().requires_grad_()
+        c = cc.geom_prod(x, y, metric)
+        c.backward(gc)
+        return c.detach(), x.grad, y.grad
+
+    r1 = run()
+    monkeypatch.setenv("CLF_GEOM_PATH", "direct")
+    r2 = run()
+    monkeypatch.delenv("CLF_GEOM_PATH")
+    for u, v in zip(r1, r2):
+        assert rel_err(u, v) <= TOL
