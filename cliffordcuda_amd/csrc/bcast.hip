@@ -257,6 +257,13 @@ __global__ __launch_bounds__(256) void bcast_gw_kernel(int op, int side, int n, 
 
 // ---- host side --------------------------------------------------------------
 
+bool rep_bcast_applicable(int op, int n, uint32_t neg, uint32_t nul);
+size_t rep_bcast_ws_floats(int64_t batch);
+int rep_bcast_fwd(int side, int n, uint32_t neg, const float* x, const float* w, float* y, int64_t batch,
+                  void* stream);
+int rep_bcast_bwd(int side, int n, uint32_t neg, const float* x, const float* w, const float* gy, float* gx, float* gw,
+                  int64_t batch, float* ws, void* stream);
+
 static int bcast_splits(int64_t batch) {
     long long s = (batch + 2047) / 2048;
     if (s > 128) s = 128;
@@ -264,6 +271,9 @@ static int bcast_splits(int64_t batch) {
     return (int)s;
 }
 
+// The GEMM path's workspace; it also covers the matrix-representation path's
+// weight-gradient partials (256 floats per workgroup, at most 2048 workgroups
+// and at most 16 * batch floats, below (3 + splits) * 2^(2n) for n >= 7).
 size_t bcast_ws_bytes(int n, int64_t batch) {
     if (n < kBcastMinN || n > kMaxN || batch < 0) return 0;
     const size_t DD = (size_t)1 << (2 * n);
@@ -311,6 +321,7 @@ int bcast_fwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* 
     if (x == y) return set_error(CLF_ERR_ARG, "output must not alias the input");
     if ((((uintptr_t)x) | ((uintptr_t)y) | ((uintptr_t)ws)) & 15u)
         return set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
+    if (rep_bcast_applicable(op, n, neg, nul)) return rep_bcast_fwd(side, n, neg, x, w, y, batch, stream);
     hipStream_t s = (hipStream_t)stream;
     const int D = 1 << n;
     float* MwT = (float*)ws;
@@ -331,6 +342,11 @@ int bcast_bwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* 
                                                 " bytes required");
     if ((((uintptr_t)x) | ((uintptr_t)gy) | ((uintptr_t)gx) | ((uintptr_t)ws)) & 15u)
         return set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
+    if (rep_bcast_applicable(op, n, neg, nul)) {
+        if (rep_bcast_ws_floats(batch) * sizeof(float) > ws_bytes)
+            return set_error(CLF_ERR_WORKSPACE, "workspace too small for the weight-gradient partials");
+        return rep_bcast_bwd(side, n, neg, x, w, gy, gx, gw, batch, (float*)ws, stream);
+    }
     hipStream_t s = (hipStream_t)stream;
     const int D = 1 << n;
     const size_t DD = (size_t)D * D;

@@ -505,6 +505,7 @@ static void launch_bwd(dim3 g, dim3 b, size_t lds, hipStream_t s, const float* A
 }
 
 bool rep_applicable(int op, int n, uint32_t neg, uint32_t nul);
+bool rep_disabled_by_env();
 int rep_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64_t batch, void* stream);
 int rep_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc, float* ga, float* gb, int64_t batch,
             void* stream);
@@ -512,8 +513,7 @@ int rep_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc
 // The geometric product of real-matrix-type signatures goes through the matrix
 // representation unless CLF_GEOM_PATH=direct asks for the per-term kernels.
 static bool use_rep(int op, int n, uint32_t neg, uint32_t nul) {
-    const char* e = std::getenv("CLF_GEOM_PATH");
-    if (e && std::strcmp(e, "direct") == 0) return false;
+    if (rep_disabled_by_env()) return false;
     return rep_applicable(op, n, neg, nul);
 }
 

@@ -22,6 +22,8 @@
 // wave-local through the row's LDS slots and need no workgroup barrier. Waves
 // walk row groups with a grid stride and prefetch the next group's rows into
 // registers while the current group is computed.
+#include <cstdlib>
+#include <cstring>
 #include <map>
 #include <mutex>
 
@@ -396,6 +398,7 @@ __device__ __forceinline__ void unconvert16(float (&w)[16], float* __restrict__ 
 __global__ __launch_bounds__(256) void rep16_fwd_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                          float* __restrict__ C, long long batch, RepTable T) {
     __shared__ float lds[4][2 * 4 * 256];  // per wave: staged a | staged b; later the relayout, then c
+    static_assert(2 * 4 * 256 >= kRelayoutFloats, "relayout must fit the wave's LDS slots");
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const unsigned x = lane & 15u;
     const int rb = lane >> 4;
@@ -439,6 +442,7 @@ __global__ __launch_bounds__(256) void rep16_bwd_kernel(const float* __restrict_
                                                          const float* __restrict__ GC, float* __restrict__ GA,
                                                          float* __restrict__ GB, long long batch, RepTable T) {
     __shared__ float lds[4][3 * 4 * 256];  // per wave: staged a | b | gc; later two relayouts, then ga | gb
+    static_assert(3 * 4 * 256 >= 2 * kRelayoutFloats, "both relayouts must fit the wave's LDS slots");
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const unsigned x = lane & 15u;
     const int rb = lane >> 4;
@@ -497,6 +501,228 @@ __global__ __launch_bounds__(256) void rep16_bwd_kernel(const float* __restrict_
         if (want_b) store16(GB, sb, row0, batch, lane, oddc);
         wave_lds_sync();
     }
+}
+
+// ---- broadcast weight (the product layers), m = 16 --------------------------
+// y = x w (side 0) or y = w x (side 1) with one weight row w for the whole
+// batch: phi(y) = phi(x) phi(w) or phi(w) phi(x), 16^3 multiply-adds per row
+// instead of the (2^n)^2 of the dense weight matrix. The weight's MFMA operand
+// is the same for the four blocks of every wave, so each lane builds its 16
+// shuffled values once per kernel and keeps them in registers.
+// Backward (side 0): gx = phi^-1(phi(gy) phi(w)^T), gw = phi^-1(sum_rows phi(x)^T phi(gy));
+//          (side 1): gx = phi^-1(phi(w)^T phi(gy)), gw = phi^-1(sum_rows phi(gy) phi(x)^T).
+// The weight-gradient sum runs in the MFMA accumulators across a wave's rows;
+// workgroups write 16x16 partials that one small kernel sums and converts.
+
+// 16 x 16 x 16 product: operand k of A (B) is xor16<k>(a[k]) if SA (SB), else
+// a[k] as given (already shuffled)
+template <bool SA, bool SB, unsigned... K>
+__device__ __forceinline__ floatx16 mfma_chain_pre(floatx16 acc, const float (&a)[16], const float (&b)[16],
+                                                   std::integer_sequence<unsigned, K...>) {
+    ((acc = __builtin_amdgcn_mfma_f32_16x16x1f32(SA ? xor16<K>(a[K]) : a[K], SB ? xor16<K>(b[K]) : b[K], acc, 0, 0,
+                                                  0)),
+     ...);
+    return acc;
+}
+
+template <unsigned... K>
+__device__ __forceinline__ void shuffle_operand(const float (&w)[16], float (&op)[16],
+                                                std::integer_sequence<unsigned, K...>) {
+    ((op[K] = xor16<K>(w[K])), ...);
+}
+
+// the weight's conversion for lane x (sign bit 31 - SIGNSHIFT of the entries:
+// 0 = phi(w), 1 = the transposed conversion), shuffled into operand order
+template <int SIGNSHIFT>
+__device__ __forceinline__ void weight_operand(const float* __restrict__ w, const RepTable& T, unsigned x,
+                                               float (&op)[16]) {
+    float t[16];
+#pragma unroll
+    for (int z = 0; z < 16; ++z) {
+        const unsigned e = T.e[x * 16 + z];
+        t[z] = __uint_as_float(__float_as_uint(w[e & 0xffffu]) ^ ((e << SIGNSHIFT) & 0x80000000u));
+    }
+    wht_inplace<16>(t);
+    shuffle_operand(t, op, std::make_integer_sequence<unsigned, 16>{});
+}
+
+template <int SIDE>
+__global__ __launch_bounds__(256) void rep16_bcast_fwd_kernel(const float* __restrict__ X, const float* __restrict__ W,
+                                                               float* __restrict__ Y, long long batch, RepTable T) {
+    // per wave: staged x rows (1024 floats); later the relayout (1280), then y rows
+    __shared__ float lds[4][kRelayoutFloats];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const unsigned x = lane & 15u;
+    const int rb = lane >> 4;
+    float* sx = &lds[wave][0];
+    const unsigned oddx = (rb & 1) ? T.odd_xor : 0u, oddc = T.odd_xor >> 2;
+    unsigned ent[16];
+#pragma unroll
+    for (int z = 0; z < 16; ++z) ent[z] = T.e[x * 16 + z] ^ oddx;
+    // side 0: B = column x of phi(w) (transposed signs); side 1: A = row x of phi(w)
+    float wop[16];
+    weight_operand<SIDE == 0 ? 1 : 0>(W, T, x, wop);
+
+    const long long stride = (long long)gridDim.x * 4 * 4;
+    long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
+    Pre16 px = fetch16(X, row0, batch, lane);
+    for (; row0 < batch; row0 += stride) {
+        stage16(sx, px, lane, oddc);
+        px = fetch16(X, row0 + stride, batch, lane);
+        wave_lds_sync();
+        float wx[16];
+        // side 0: A = row x of phi(x); side 1: B = column x of phi(x) (transposed signs)
+        gather16<SIDE == 0 ? 0 : 1>(sx + rb * 256, ent, wx);
+        wave_lds_sync();
+        wht_inplace<16>(wx);
+        const floatx16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        floatx16 acc;
+        if constexpr (SIDE == 0)
+            acc = mfma_chain_pre<true, false>(zero, wx, wop, std::make_integer_sequence<unsigned, 16>{});
+        else
+            acc = mfma_chain_pre<false, true>(zero, wop, wx, std::make_integer_sequence<unsigned, 16>{});
+        relayout_store(sx, acc, lane);
+        wave_lds_sync();
+        float wc[16];
+        relayout_load(sx, rb, x, wc);
+        wave_lds_sync();
+        unconvert16(wc, sx + rb * 256, ent);
+        wave_lds_sync();
+        store16(Y, sx, row0, batch, lane, oddc);
+        wave_lds_sync();
+    }
+}
+
+// parts[blockIdx.x * 256 + r * 16 + c]: the workgroup's sum of the 16x16 weight-gradient products
+template <int SIDE>
+__global__ __launch_bounds__(256) void rep16_bcast_bwd_kernel(const float* __restrict__ X, const float* __restrict__ W,
+                                                               const float* __restrict__ GY, float* __restrict__ GX,
+                                                               float* __restrict__ parts, long long batch,
+                                                               RepTable T) {
+    __shared__ float lds[4][2 * 4 * 256];  // per wave: staged x | staged gy; later relayout, then gx rows
+    static_assert(2 * 4 * 256 >= kRelayoutFloats, "relayout must fit the wave's LDS slots");
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const unsigned x = lane & 15u;
+    const int rb = lane >> 4;
+    float* sx = &lds[wave][0];
+    float* sg = sx + 4 * 256;
+    const unsigned oddx = (rb & 1) ? T.odd_xor : 0u, oddc = T.odd_xor >> 2;
+    unsigned ent[16];
+#pragma unroll
+    for (int z = 0; z < 16; ++z) ent[z] = T.e[x * 16 + z] ^ oddx;
+    const bool want_x = GX != nullptr, want_w = parts != nullptr;
+    // gx operand of the weight: side 0: B = column x of phi(w)^T = row x of phi(w);
+    // side 1: A = row x of phi(w)^T (transposed signs)
+    float wop[16];
+    weight_operand<SIDE == 0 ? 0 : 1>(W, T, x, wop);
+    const floatx16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    floatx16 accw = zero;
+
+    const long long stride = (long long)gridDim.x * 4 * 4;
+    long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
+    Pre16 px = fetch16(X, row0, batch, lane);
+    Pre16 pg = fetch16(GY, row0, batch, lane);
+    for (; row0 < batch; row0 += stride) {
+        stage16(sx, px, lane, oddc);
+        stage16(sg, pg, lane, oddc);
+        px = fetch16(X, row0 + stride, batch, lane);
+        pg = fetch16(GY, row0 + stride, batch, lane);
+        wave_lds_sync();
+        // gy in both sign conventions; x as the weight-gradient operand
+        // (side 0: A = row of phi(x)^T, transposed signs; side 1: B = column of phi(x)^T = row of phi(x))
+        float wg[16], wgt[16], wx[16];
+        gather16<0>(sg + rb * 256, ent, wg);
+        gather16<1>(sg + rb * 256, ent, wgt);
+        if (want_w) gather16<SIDE == 0 ? 1 : 0>(sx + rb * 256, ent, wx);
+        wave_lds_sync();
+        wht_inplace<16>(wg);
+        wht_inplace<16>(wgt);
+        if (want_w) {
+            wht_inplace<16>(wx);
+            // rows past the end are clamped copies of the last row: zero their
+            // contribution to the sum (whole 16-lane blocks, so every lane's
+            // operand is zero for those blocks)
+            if (row0 + rb >= batch) {
+#pragma unroll
+                for (int k = 0; k < 16; ++k) wx[k] = 0.f;
+            }
+            if constexpr (SIDE == 0)
+                accw = mfma_chain_pre<true, true>(accw, wx, wgt, std::make_integer_sequence<unsigned, 16>{});
+            else
+                accw = mfma_chain_pre<true, true>(accw, wg, wx, std::make_integer_sequence<unsigned, 16>{});
+        }
+        if (want_x) {
+            floatx16 acc;
+            if constexpr (SIDE == 0)
+                acc = mfma_chain_pre<true, false>(zero, wg, wop, std::make_integer_sequence<unsigned, 16>{});
+            else
+                acc = mfma_chain_pre<false, true>(zero, wop, wgt, std::make_integer_sequence<unsigned, 16>{});
+            relayout_store(sx, acc, lane);
+            wave_lds_sync();
+            float wc[16];
+            relayout_load(sx, rb, x, wc);
+            wave_lds_sync();
+            unconvert16(wc, sx + rb * 256, ent);
+            wave_lds_sync();
+            store16(GX, sx, row0, batch, lane, oddc);
+        }
+        wave_lds_sync();
+    }
+    if (!want_w) return;  // uniform: a kernel argument
+    // sum the four blocks (rows) of the wave: lane (g, j) holds S[4g + t][j]
+    __syncthreads();  // every wave is done with its LDS slots
+    float* red = &lds[0][0];  // [4 waves][256]
+    const unsigned g = (unsigned)lane >> 4, j = (unsigned)lane & 15u;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+        red[wave * 256 + (4 * g + t) * 16 + j] = accw[t] + accw[4 + t] + accw[8 + t] + accw[12 + t];
+    __syncthreads();
+    const int e = threadIdx.x;
+    parts[(long long)blockIdx.x * 256 + e] = red[e] + red[256 + e] + red[512 + e] + red[768 + e];
+}
+
+// Deterministic sums of the 16x16 partials, in two stages so that every
+// thread has few dependent loads: out[k * 256 + e] = sum of partials
+// 32k .. 32k + 31 (element e); one workgroup per 32 partials.
+constexpr int kPartsPerSum = 32;
+
+__global__ __launch_bounds__(256) void rep16_parts_sum_kernel(const float* __restrict__ parts, int nparts,
+                                                               float* __restrict__ out) {
+    const int e = threadIdx.x;
+    const int p0 = blockIdx.x * kPartsPerSum;
+    const int p1 = p0 + kPartsPerSum < nparts ? p0 + kPartsPerSum : nparts;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int p = p0;
+    for (; p + 8 <= p1; p += 8)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc[u] += parts[(long long)(p + u) * 256 + e];
+    for (; p < p1; ++p) acc[0] += parts[(long long)p * 256 + e];
+    out[(long long)blockIdx.x * 256 + e] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+}
+
+// gw = phi^-1(sum of the first-stage sums); one workgroup of 256 threads
+__global__ __launch_bounds__(256) void rep16_bcast_gw_kernel(const float* __restrict__ sums, int nsums,
+                                                              float* __restrict__ gw, RepTable T) {
+    __shared__ float S[256];
+    const int e = threadIdx.x;
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    int p = 0;
+    for (; p + 4 <= nsums; p += 4)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[u] += (double)sums[(long long)(p + u) * 256 + e];
+    for (; p < nsums; ++p) acc[0] += (double)sums[(long long)p * 256 + e];
+    S[e] = (float)((acc[0] + acc[1]) + (acc[2] + acc[3]));
+    __syncthreads();
+    // thread (x, z): t[x][z] = (1/16) sum_c W[x][c] (-1)^{popc(z & c)}, W[x][c] = S[(x ^ c) * 16 + c]
+    const unsigned xx = (unsigned)e >> 4, z = (unsigned)e & 15u;
+    float t = 0.f;
+#pragma unroll
+    for (unsigned c = 0; c < 16; ++c) {
+        const float v = S[((xx ^ c) * 16) + c];
+        t += (__popc(z & c) & 1) ? -v : v;
+    }
+    const unsigned ent = T.e[xx * 16 + z];
+    gw[ent & 0xffffu] = __uint_as_float(__float_as_uint(t * 0.0625f) ^ (ent & 0x80000000u));
 }
 
 // ---- host side --------------------------------------------------------------
@@ -620,6 +846,79 @@ int rep_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc
         default: return set_error(CLF_ERR_UNSUPPORTED, "matrix path supports n = 4, 6, 8");
     }
 #undef CLF_REP_GRID
+    CLF_HIP_CHECK(hipGetLastError());
+    return CLF_OK;
+}
+
+}  // namespace clf
+
+namespace clf {
+
+// CLF_GEOM_PATH=direct in the environment (read at each call) turns the
+// matrix-representation paths off, for comparisons against the per-term and
+// GEMM kernels.
+bool rep_disabled_by_env() {
+    const char* e = std::getenv("CLF_GEOM_PATH");
+    return e && std::strcmp(e, "direct") == 0;
+}
+
+// Broadcast-weight geometric product on the m = 16 path (n = 8, real type).
+bool rep_bcast_applicable(int op, int n, uint32_t neg, uint32_t nul) {
+    if (op != CLF_OP_GEOM || n != 8 || nul != 0u || rep_disabled_by_env()) return false;
+    RepTable T;
+    return rep_table(n, neg, T);
+}
+
+static long long rep_bcast_grid(int64_t batch) {
+    long long g = (batch + 15) / 16;
+    const long long cap = 256LL * 8;
+    return g < 1 ? 1 : (g > cap ? cap : g);
+}
+
+// floats of workspace the backward's weight-gradient partials and their
+// first-stage sums need
+size_t rep_bcast_ws_floats(int64_t batch) {
+    const long long nb = rep_bcast_grid(batch);
+    return (size_t)(nb + (nb + kPartsPerSum - 1) / kPartsPerSum) * 256;
+}
+
+int rep_bcast_fwd(int side, int n, uint32_t neg, const float* x, const float* w, float* y, int64_t batch,
+                  void* stream) {
+    RepTable T;
+    if (n != 8 || !rep_table(n, neg, T)) return set_error(CLF_ERR_UNSUPPORTED, "no m = 16 matrix representation");
+    hipStream_t s = (hipStream_t)stream;
+    const dim3 grid((unsigned)rep_bcast_grid(batch));
+    if (side == 0) hipLaunchKernelGGL(rep16_bcast_fwd_kernel<0>, grid, dim3(256), 0, s, x, w, y, (long long)batch, T);
+    else hipLaunchKernelGGL(rep16_bcast_fwd_kernel<1>, grid, dim3(256), 0, s, x, w, y, (long long)batch, T);
+    CLF_HIP_CHECK(hipGetLastError());
+    return CLF_OK;
+}
+
+// ws: at least rep_bcast_ws_floats(batch) floats when gw != nullptr
+int rep_bcast_bwd(int side, int n, uint32_t neg, const float* x, const float* w, const float* gy, float* gx, float* gw,
+                  int64_t batch, float* ws, void* stream) {
+    RepTable T;
+    if (n != 8 || !rep_table(n, neg, T)) return set_error(CLF_ERR_UNSUPPORTED, "no m = 16 matrix representation");
+    hipStream_t s = (hipStream_t)stream;
+    const long long nb = rep_bcast_grid(batch);
+    float* parts = gw ? ws : nullptr;
+    if (batch > 0) {
+        if (side == 0)
+            hipLaunchKernelGGL(rep16_bcast_bwd_kernel<0>, dim3((unsigned)nb), dim3(256), 0, s, x, w, gy, gx, parts,
+                               (long long)batch, T);
+        else
+            hipLaunchKernelGGL(rep16_bcast_bwd_kernel<1>, dim3((unsigned)nb), dim3(256), 0, s, x, w, gy, gx, parts,
+                               (long long)batch, T);
+    }
+    if (gw) {
+        int nsums = 0;
+        float* sums = parts + nb * 256;
+        if (batch > 0) {
+            nsums = (int)((nb + kPartsPerSum - 1) / kPartsPerSum);
+            hipLaunchKernelGGL(rep16_parts_sum_kernel, dim3((unsigned)nsums), dim3(256), 0, s, parts, (int)nb, sums);
+        }
+        hipLaunchKernelGGL(rep16_bcast_gw_kernel, dim3(1), dim3(256), 0, s, sums, nsums, gw, T);
+    }
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }

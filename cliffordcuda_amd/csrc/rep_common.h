@@ -76,6 +76,7 @@ __device__ __forceinline__ floatx16 mfma_chain(const float (&wa)[16], const floa
 
 constexpr int kRelayoutStride = 20;
 constexpr int kRelayoutBlock = 16 * kRelayoutStride;  // floats per row of the group
+constexpr int kRelayoutFloats = 4 * kRelayoutBlock;   // LDS a wave's relayout writes (1280 floats)
 
 // lane (g, j) writes C_b[4g + t][j] (register 4b + t) to W_c[(4g + t) ^ j][j]
 __device__ __forceinline__ void relayout_store(float* __restrict__ dst, const floatx16& acc, int lane) {

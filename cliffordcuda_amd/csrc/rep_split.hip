@@ -118,6 +118,7 @@ __device__ __forceinline__ void gather_pair(const float* __restrict__ row, const
 template <int NP>
 __device__ __forceinline__ void split_pairs_body(const PairSum& P, const SplitTable& T) {
     __shared__ float lds[4][2048];  // per wave: staged X rows | staged Y rows; later the relayout, then out rows
+    static_assert(2048 >= kRelayoutFloats, "relayout must fit the wave's LDS slots");
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int b = lane >> 4, r = b >> 1;
     const unsigned s = (unsigned)b & 1u, x = lane & 15u;

@@ -74,11 +74,13 @@ def test_weight_on_left(op):
     assert rel_err(wd.grad, w64.grad) <= TOL
 
 
-def test_c3_full_batch_vs_per_row_kernels():
+def test_c3_full_batch_vs_per_row_kernels(monkeypatch):
     """GeometricProductLayer Cl(8,0), x (262144, 256) ~ N(0,1),
-    w ~ N(0, 1/16). The MFMA path must equal the per-row VALU kernels on the
-    expanded weight (an independent HIP algorithm) at the full batch, values
-    and both gradients; a row sample also matches the oracle."""
+    w ~ N(0, 1/16). Three independent HIP algorithms agree at the full batch,
+    values and both gradients: the matrix-representation layer kernels (the
+    path Cl(8,0) takes), the MFMA GEMM against the weight's 256 x 256 matrix,
+    and the per-term product kernels on the expanded weight (both forced with
+    CLF_GEOM_PATH=direct); a row sample also matches the oracle."""
     cl = cc.CliffordAlgebra([1] * 8, device="cuda")
     layer = cc.GeometricProductLayer(cl)
     g = torch.Generator().manual_seed(0)
@@ -87,19 +89,54 @@ def test_c3_full_batch_vs_per_row_kernels():
     w = 0.25 * torch.randn(1, 256, generator=g)
     with torch.no_grad():
         layer.weight.copy_(w.cuda())
-    xd = x.cuda().requires_grad_()
-    y = layer(xd)
-    y.sum().backward()
+
+    def run_layer():
+        layer.weight.grad = None
+        xd = x.cuda().requires_grad_()
+        y = layer(xd)
+        y.sum().backward()
+        return y.detach(), xd.grad, layer.weight.grad.clone()
+
+    y, gx, gw = run_layer()
+    monkeypatch.setenv("CLF_GEOM_PATH", "direct")
+    y1, gx1, gw1 = run_layer()
     x2 = x.cuda().requires_grad_()
     w2 = w.cuda().requires_grad_()
     y2 = cc.geom_prod(x2, w2.expand(B, 256).contiguous())
     y2.sum().backward()
-    assert rel_err(y, y2) <= TOL
-    assert rel_err(xd.grad, x2.grad) <= TOL
-    assert rel_err(layer.weight.grad, w2.grad) <= TOL
+    monkeypatch.delenv("CLF_GEOM_PATH")
+    for a, b, c in ((y, y1, y2), (gx, gx1, x2.grad), (gw, gw1, w2.grad)):
+        assert rel_err(a, b) <= TOL
+        assert rel_err(b, c) <= TOL
     rows = torch.tensor([0, 5, 123456, B - 1])
     y64 = O.layer_forward("geom", x[rows].double(), w.double())
     assert rel_err(y[rows.cuda()], y64) <= TOL
+
+
+@pytest.mark.parametrize("metric", [(1,) * 8, (1, -1) * 4], ids=["++++++++", "+-+-+-+-"])
+@pytest.mark.parametrize("side", [0, 1])
+@pytest.mark.parametrize("batch", [1, 77, 4099])
+def test_matrix_path_layer_sides(metric, side, batch):
+    """Real-type n = 8: the broadcast geometric product with the weight on
+    either side (matrix-representation layer kernels) against the oracle,
+    values and both gradients; odd batches exercise the clamped last rows
+    (which must not enter the weight gradient twice)."""
+    g = torch.Generator().manual_seed(7 + side)
+    x = torch.randn(batch, 256, generator=g)
+    w = torch.randn(1, 256, generator=g)
+    gy = torch.randn(batch, 256, generator=g)
+    xd = x.cuda().requires_grad_()
+    wd = w.cuda().requires_grad_()
+    y = bcast.bcast_product("geom", xd, wd, metric, side=side)
+    y.backward(gy.cuda())
+    x64 = x.double().requires_grad_()
+    w64 = w.double().requires_grad_()
+    wb = w64.expand_as(x64)
+    y64 = O.einsum_product("geom", x64, wb, metric) if side == 0 else O.einsum_product("geom", wb, x64, metric)
+    y64.backward(gy.double())
+    assert rel_err(y, y64) <= TOL
+    assert rel_err(xd.grad, x64.grad) <= TOL
+    assert rel_err(wd.grad, w64.grad) <= TOL
 
 
 def test_layer_small_batches():
