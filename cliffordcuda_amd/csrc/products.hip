@@ -254,19 +254,44 @@ struct BlkParams {
     int kpl;        // output blocks per lane
 };
 
-// Stage `nops` row-major operands for the workgroup's rows into LDS (swizzled).
-__device__ __forceinline__ void stage_rows(float4* __restrict__ lds, const float4* const* __restrict__ src, int nops,
+// Stage NOPS (2 or 3) row-major operands s0, s1[, s2] for the workgroup's rows
+// into LDS (swizzled). Each thread issues all its loads (up to four float4 per
+// operand per pass, addresses clamped to the last valid chunk) before any LDS
+// write, so a pass costs one memory latency instead of one per chunk.
+template <int NOPS>
+__device__ __forceinline__ void stage_rows(float4* __restrict__ lds, const float4* __restrict__ s0,
+                                           const float4* __restrict__ s1, const float4* __restrict__ s2,
                                            long long row0, int nrows, int n) {
     const int d4_log = n - 2;
     const int D4 = 1 << d4_log;
     const int total = nrows << d4_log;
-    for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
-        const int r = idx >> d4_log;
-        const unsigned f = (unsigned)(idx & (D4 - 1));
-        const unsigned blk = f >> 2, q = f & 3u;
-        const int dst = r * nops * D4 + (int)((blk << 2) + (q ^ swz(blk)));
-        const long long g = (row0 << d4_log) + idx;
-        for (int o = 0; o < nops; ++o) lds[dst + o * D4] = src[o][g];
+    const long long g0 = row0 << d4_log;
+    const int nt = (int)blockDim.x;
+    for (int base = (int)threadIdx.x; base < total; base += 4 * nt) {
+        const int i0 = base, i1 = base + nt, i2 = base + 2 * nt, i3 = base + 3 * nt;
+        const int c1 = i1 < total ? i1 : total - 1, c2 = i2 < total ? i2 : total - 1, c3 = i3 < total ? i3 : total - 1;
+        const float4 a0 = s0[g0 + i0], a1 = s0[g0 + c1], a2 = s0[g0 + c2], a3 = s0[g0 + c3];
+        const float4 b0 = s1[g0 + i0], b1 = s1[g0 + c1], b2 = s1[g0 + c2], b3 = s1[g0 + c3];
+        float4 e0, e1, e2, e3;
+        if constexpr (NOPS == 3) {
+            e0 = s2[g0 + i0];
+            e1 = s2[g0 + c1];
+            e2 = s2[g0 + c2];
+            e3 = s2[g0 + c3];
+        }
+        auto put = [&](int idx, const float4& x, const float4& y, const float4& z) {
+            const int r = idx >> d4_log;
+            const unsigned f = (unsigned)(idx & (D4 - 1));
+            const unsigned blk = f >> 2, q = f & 3u;
+            const int dst = r * NOPS * D4 + (int)((blk << 2) + (q ^ swz(blk)));
+            lds[dst] = x;
+            lds[dst + D4] = y;
+            if constexpr (NOPS == 3) lds[dst + 2 * D4] = z;
+        };
+        put(i0, a0, b0, e0);
+        if (i1 < total) put(i1, a1, b1, e1);
+        if (i2 < total) put(i2, a2, b2, e2);
+        if (i3 < total) put(i3, a3, b3, e3);
     }
 }
 
@@ -279,10 +304,7 @@ __global__ __launch_bounds__(256) void prod_fwd_blk(const float* __restrict__ A,
     const unsigned NB = 1u << (n - 4);
     const long long row0 = (long long)blockIdx.x * P.rows_per_wg;
     const int nrows = (int)((P.batch - row0) < P.rows_per_wg ? (P.batch - row0) : P.rows_per_wg);
-    {
-        const float4* src[2] = {reinterpret_cast<const float4*>(A), reinterpret_cast<const float4*>(B)};
-        stage_rows(lds, src, 2, row0, nrows, n);
-    }
+    stage_rows<2>(lds, reinterpret_cast<const float4*>(A), reinterpret_cast<const float4*>(B), nullptr, row0, nrows, n);
     __syncthreads();
     const int r = threadIdx.x >> P.lpr_log;
     if (r >= nrows) return;
@@ -330,11 +352,8 @@ __global__ __launch_bounds__(256) void prod_bwd_blk(const float* __restrict__ A,
     const unsigned NB = 1u << (n - 4);
     const long long row0 = (long long)blockIdx.x * P.rows_per_wg;
     const int nrows = (int)((P.batch - row0) < P.rows_per_wg ? (P.batch - row0) : P.rows_per_wg);
-    {
-        const float4* src[3] = {reinterpret_cast<const float4*>(A), reinterpret_cast<const float4*>(B),
-                                reinterpret_cast<const float4*>(GC)};
-        stage_rows(lds, src, 3, row0, nrows, n);
-    }
+    stage_rows<3>(lds, reinterpret_cast<const float4*>(A), reinterpret_cast<const float4*>(B),
+                  reinterpret_cast<const float4*>(GC), row0, nrows, n);
     __syncthreads();
     const int r = threadIdx.x >> P.lpr_log;
     if (r >= nrows) return;
