@@ -414,6 +414,158 @@ __global__ __launch_bounds__(256) void prod_bwd_blk(const float* __restrict__ A,
     }
 }
 
+// ---- tiled path (rows larger than LDS, n >= 12) -----------------------------
+// A workgroup of 256 lanes owns 256 output blocks kh = K0 + lane of one row and
+// walks the input blocks in aligned tiles of 256 (I0 = 256 t). Because both
+// ranges are aligned, the partner blocks jh = ih ^ kh of a tile form the aligned
+// tile starting at I0 ^ K0, so each step stages one 16 KB slab per operand in
+// LDS (same 64-byte swizzle as the whole-row kernels) and the lane reads its
+// partner at local index (ih & 255) ^ (kh & 255).
+constexpr int kTileBlocks = 256;                 // blocks per tile = lanes per workgroup
+constexpr int kTileF4 = kTileBlocks * 4;         // float4 per operand tile
+
+// stage tile blocks [blk0, blk0 + 256) of one row into dst (swizzled); all
+// loads of a pass are issued before its LDS writes
+__device__ __forceinline__ void stage_tile(float4* __restrict__ dst, const float4* __restrict__ row,
+                                           unsigned blk0) {
+    const float4* src = row + ((size_t)blk0 << 2);
+#pragma unroll
+    for (int pass = 0; pass < kTileF4 / 256 / 4; ++pass) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = src[(pass * 4 + u) * 256 + threadIdx.x];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const unsigned idx = (unsigned)((pass * 4 + u) * 256 + threadIdx.x);
+            const unsigned blk = idx >> 2, q = idx & 3u;
+            dst[(blk << 2) + (q ^ swz(blk))] = v[u];
+        }
+    }
+}
+
+// grid: (NB / 256) * batch workgroups; workgroup -> (row, output chunk)
+template <int OP, bool LOWNEG>
+__global__ __launch_bounds__(256) void prod_fwd_tiled(const float* __restrict__ A, const float* __restrict__ B,
+                                                       float* __restrict__ C, BlkParams P) {
+    __shared__ float4 la[kTileF4];
+    __shared__ float4 lb[kTileF4];
+    const int n = P.n;
+    const unsigned NB = 1u << (n - 4);
+    const unsigned chunks = NB / kTileBlocks;
+    const long long row = (long long)(blockIdx.x / chunks);
+    const unsigned K0 = (blockIdx.x % chunks) * kTileBlocks;
+    const unsigned kh = K0 + threadIdx.x;
+    const unsigned kl = kh & (kTileBlocks - 1);
+    const unsigned fullh = NB - 1u;
+    const float4* arow = reinterpret_cast<const float4*>(A) + (row << (n - 2));
+    const float4* brow = reinterpret_cast<const float4*>(B) + (row << (n - 2));
+    float acc[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+    for (unsigned I0 = 0; I0 < NB; I0 += kTileBlocks) {
+        __syncthreads();  // the previous tile is consumed
+        stage_tile(la, arow, I0);
+        stage_tile(lb, brow, I0 ^ K0);
+        __syncthreads();
+        for (unsigned il = 0; il < (unsigned)kTileBlocks; ++il) {
+            const unsigned ih = I0 + il, jh = ih ^ kh;
+            const HiSign hs = hi_sign<OP>(ih, jh, P.negh, P.nulh, fullh, P.nm1, P.mu);
+            if (!hs.valid) continue;
+            float av[16], bv[16];
+            load_blk(la, il, av);
+            load_blk(lb, il ^ kl, bv);
+            apply_flips(bv, hs.mask, hs.mask ^ (cross_pi<OP>(ih, P.nm1) << 31));
+            fwd_block_dispatch<OP, LOWNEG>(acc, av, bv, ih, jh);
+        }
+    }
+    float4* out = reinterpret_cast<float4*>(C) + (row << (n - 2));
+    if (OP == OP_REGR) {
+        const unsigned ob = fullh ^ kh;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            out[(ob << 2) + (3 - q)] = make_float4(acc[4 * q + 3], acc[4 * q + 2], acc[4 * q + 1], acc[4 * q]);
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            out[(kh << 2) + q] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+    }
+}
+
+// lane owns block h = H0 + lane of ga and gb; tiles over m stage a[m], b[m]
+// and gc[h ^ m] (regressive: gc[fullh ^ h ^ m]), an aligned tile as well
+template <int OP, bool LOWNEG>
+__global__ __launch_bounds__(256) void prod_bwd_tiled(const float* __restrict__ A, const float* __restrict__ B,
+                                                       const float* __restrict__ GC, float* __restrict__ GA,
+                                                       float* __restrict__ GB, BlkParams P) {
+    __shared__ float4 la[kTileF4];
+    __shared__ float4 lb[kTileF4];
+    __shared__ float4 lg[kTileF4];
+    const int n = P.n;
+    const unsigned NB = 1u << (n - 4);
+    const unsigned chunks = NB / kTileBlocks;
+    const long long row = (long long)(blockIdx.x / chunks);
+    const unsigned H0 = (blockIdx.x % chunks) * kTileBlocks;
+    const unsigned h = H0 + threadIdx.x;
+    const unsigned hl = h & (kTileBlocks - 1);
+    const unsigned fullh = NB - 1u;
+    const bool want_a = GA != nullptr, want_b = GB != nullptr;
+    const float4* arow = reinterpret_cast<const float4*>(A) + (row << (n - 2));
+    const float4* brow = reinterpret_cast<const float4*>(B) + (row << (n - 2));
+    const float4* grow = reinterpret_cast<const float4*>(GC) + (row << (n - 2));
+    const unsigned pi_h = cross_pi<OP>(h, P.nm1);
+    float ga[16], gb[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        ga[e] = 0.f;
+        gb[e] = 0.f;
+    }
+    for (unsigned M0 = 0; M0 < NB; M0 += kTileBlocks) {
+        const unsigned G0 = (OP == OP_REGR) ? ((fullh ^ H0 ^ M0) & ~(unsigned)(kTileBlocks - 1)) : (H0 ^ M0);
+        __syncthreads();
+        stage_tile(la, arow, M0);
+        stage_tile(lb, brow, M0);
+        stage_tile(lg, grow, G0);
+        __syncthreads();
+        for (unsigned ml = 0; ml < (unsigned)kTileBlocks; ++ml) {
+            const unsigned m = M0 + ml;
+            const HiSign sa = hi_sign<OP>(h, m, P.negh, P.nulh, fullh, P.nm1, P.mu);  // (i, j) = (h, m)
+            const HiSign sb = hi_sign<OP>(m, h, P.negh, P.nulh, fullh, P.nm1, P.mu);  // (i, j) = (m, h)
+            const bool do_a = want_a && sa.valid, do_b = want_b && sb.valid;
+            if (!do_a && !do_b) continue;
+            float g[16];
+            const unsigned gl = (OP == OP_REGR) ? ((kTileBlocks - 1) ^ hl ^ ml) : (hl ^ ml);
+            if (OP == OP_REGR) load_blk_rev(lg, gl, g);
+            else load_blk(lg, gl, g);
+            if (do_a) {
+                float bv[16];
+                load_blk(lb, ml, bv);
+                apply_flips(bv, sa.mask, sa.mask ^ (pi_h << 31));
+                ga_block_dispatch<OP, LOWNEG>(ga, bv, g, h, m);
+            }
+            if (do_b) {
+                const unsigned pm = cross_pi<OP>(m, P.nm1) << 31;
+                float av[16], gt[16];
+                load_blk(la, ml, av);
+                apply_flips(av, sb.mask, sb.mask ^ pm);
+#pragma unroll
+                for (int e = 0; e < 16; ++e) gt[e] = (cpopc((unsigned)e) & 1) ? flip(g[e], pm) : g[e];
+                gb_block_dispatch<OP, LOWNEG>(gb, av, gt, m, h);
+            }
+        }
+    }
+    const long long base = row << (n - 2);
+    if (want_a) {
+        float4* o = reinterpret_cast<float4*>(GA) + base;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) o[(h << 2) + q] = make_float4(ga[4 * q], ga[4 * q + 1], ga[4 * q + 2], ga[4 * q + 3]);
+    }
+    if (want_b) {
+        float4* o = reinterpret_cast<float4*>(GB) + base;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) o[(h << 2) + q] = make_float4(gb[4 * q], gb[4 * q + 1], gb[4 * q + 2], gb[4 * q + 3]);
+    }
+}
+
 // ---- generic path: one thread per output coefficient, closed-form signs ----
 // Used for n < 4 and for metrics whose low four generators are not all +1 or
 // all -1 (or contain a null generator).
@@ -476,18 +628,37 @@ static int check_common(int op, int n, uint32_t neg, uint32_t nul, int64_t batch
     return CLF_OK;
 }
 
-// Launch shape for the blocked kernels. Returns false if the generic path must be used.
-static bool blocked_plan(int op, int n, uint32_t neg, uint32_t nul, int nops, BlkParams& P, bool& lowneg,
-                         dim3& grid, dim3& block, size_t& lds_bytes) {
+// The block factorisation needs the low four generators to share one metric
+// value (+1 or -1, not null) for ops whose signs depend on it; wedge and
+// regressive signs do not. Sets the low-block sign variant.
+static bool blocked_metric(int op, int n, uint32_t neg, uint32_t nul, bool& lowneg) {
     if (n < 4) return false;
     const uint32_t neg4 = neg & 15u, nul4 = nul & 15u;
     if (op == CLF_OP_WEDGE || op == CLF_OP_REGRESSIVE) {
         lowneg = false;  // these signs do not depend on the low-bit metric
-    } else {
-        if (nul4) return false;
-        if (neg4 != 0u && neg4 != 15u) return false;
-        lowneg = neg4 == 15u;
+        return true;
     }
+    if (nul4) return false;
+    if (neg4 != 0u && neg4 != 15u) return false;
+    lowneg = neg4 == 15u;
+    return true;
+}
+
+static void block_sign_params(int n, uint32_t neg, uint32_t nul, BlkParams& P) {
+    P.n = n;
+    P.negh = neg >> 4;
+    P.nulh = nul >> 4;
+    P.nm1 = (n - 1) & 1;
+    P.mu = popc_rt(neg) & 1;
+}
+
+constexpr size_t kBlockedLdsMax = 48 * 1024;
+
+// Launch shape for the whole-row blocked kernels. Returns false if the rows do
+// not fit the LDS budget (tiled path) or the metric needs the generic path.
+static bool blocked_plan(int op, int n, uint32_t neg, uint32_t nul, int nops, BlkParams& P, bool& lowneg,
+                         dim3& grid, dim3& block, size_t& lds_bytes) {
+    if (!blocked_metric(op, n, neg, nul, lowneg)) return false;
     const int nh = n - 4;
     const int NB = 1 << nh;
     const int lpr = NB < 64 ? NB : 64;
@@ -496,12 +667,9 @@ static bool blocked_plan(int op, int n, uint32_t neg, uint32_t nul, int nops, Bl
     const int rpw = 64 / lpr;
     const size_t row_bytes = (size_t)nops * ((size_t)4 << n);
     int nwaves = 4;
-    while (nwaves > 1 && (size_t)nwaves * rpw * row_bytes > 48 * 1024) nwaves >>= 1;
-    P.n = n;
-    P.negh = neg >> 4;
-    P.nulh = nul >> 4;
-    P.nm1 = (n - 1) & 1;
-    P.mu = popc_rt(neg) & 1;
+    while (nwaves > 1 && (size_t)nwaves * rpw * row_bytes > kBlockedLdsMax) nwaves >>= 1;
+    if ((size_t)nwaves * rpw * row_bytes > kBlockedLdsMax) return false;
+    block_sign_params(n, neg, nul, P);
     P.lpr_log = lpr_log;
     P.rows_per_wg = nwaves * rpw;
     P.kpl = NB / lpr;
@@ -510,6 +678,25 @@ static bool blocked_plan(int op, int n, uint32_t neg, uint32_t nul, int nops, Bl
     lds_bytes = (size_t)P.rows_per_wg * row_bytes;
     return true;
 }
+
+// Tiled kernels: n >= 12 (at least one 256-block tile per row).
+static bool tiled_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, bool& lowneg, dim3& grid) {
+    if (n < 12 || !blocked_metric(op, n, neg, nul, lowneg)) return false;
+    block_sign_params(n, neg, nul, P);
+    const long long chunks = (1LL << (n - 4)) / kTileBlocks;
+    grid = dim3((unsigned)(chunks * P.batch));
+    return true;
+}
+
+// CLF_PRODUCT_PATH (read at each call) selects a path for comparisons where
+// several apply: "tiled" runs n = 12 on the tiled kernels instead of the
+// whole-row ones, "generic" runs the per-coefficient kernels for any n.
+static bool product_path_is(const char* what) {
+    const char* e = std::getenv("CLF_PRODUCT_PATH");
+    return e && std::strcmp(e, what) == 0;
+}
+static bool tiled_forced() { return product_path_is("tiled"); }
+static bool generic_forced() { return product_path_is("generic"); }
 
 template <int OP, bool LN>
 static void launch_fwd(dim3 g, dim3 b, size_t lds, hipStream_t s, const float* A, const float* B, float* C,
@@ -552,7 +739,8 @@ int product_fwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
     bool ln = false;
     dim3 g, bl;
     size_t lds = 0;
-    if (blocked_plan(op, n, neg, nul, 2, P, ln, g, bl, lds)) {
+    const bool force_tiled = n >= 12 && tiled_forced(), force_generic = generic_forced();
+    if (!force_generic && !force_tiled && blocked_plan(op, n, neg, nul, 2, P, ln, g, bl, lds)) {
 #define CLF_FWD_CASE(OPV)                                              \
     case OPV:                                                          \
         if (ln) launch_fwd<OPV, true>(g, bl, lds, s, a, b, c, P);      \
@@ -567,6 +755,17 @@ int product_fwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
             case OP_REGR: launch_fwd<OP_REGR, false>(g, bl, lds, s, a, b, c, P); break;
         }
 #undef CLF_FWD_CASE
+    } else if (!force_generic && tiled_plan(op, n, neg, nul, P, ln, g)) {
+#define CLF_FWD_TILED(OPV, LNV) hipLaunchKernelGGL((prod_fwd_tiled<OPV, LNV>), g, dim3(256), 0, s, a, b, c, P)
+        switch (op) {
+            case OP_GEOM: if (ln) CLF_FWD_TILED(OP_GEOM, true); else CLF_FWD_TILED(OP_GEOM, false); break;
+            case OP_INNER: if (ln) CLF_FWD_TILED(OP_INNER, true); else CLF_FWD_TILED(OP_INNER, false); break;
+            case OP_LC: if (ln) CLF_FWD_TILED(OP_LC, true); else CLF_FWD_TILED(OP_LC, false); break;
+            case OP_RC: if (ln) CLF_FWD_TILED(OP_RC, true); else CLF_FWD_TILED(OP_RC, false); break;
+            case OP_WEDGE: CLF_FWD_TILED(OP_WEDGE, false); break;
+            case OP_REGR: CLF_FWD_TILED(OP_REGR, false); break;
+        }
+#undef CLF_FWD_TILED
     } else {
         const long long total = batch << n;
         const unsigned blocks = (unsigned)((total + 255) / 256);
@@ -594,7 +793,8 @@ int product_bwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
     bool ln = false;
     dim3 g, bl;
     size_t lds = 0;
-    if (blocked_plan(op, n, neg, nul, 3, P, ln, g, bl, lds)) {
+    const bool force_tiled = n >= 12 && tiled_forced(), force_generic = generic_forced();
+    if (!force_generic && !force_tiled && blocked_plan(op, n, neg, nul, 3, P, ln, g, bl, lds)) {
 #define CLF_BWD_CASE(OPV)                                                      \
     case OPV:                                                                  \
         if (ln) launch_bwd<OPV, true>(g, bl, lds, s, a, b, gc, ga, gb, P);     \
@@ -609,6 +809,18 @@ int product_bwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
             case OP_REGR: launch_bwd<OP_REGR, false>(g, bl, lds, s, a, b, gc, ga, gb, P); break;
         }
 #undef CLF_BWD_CASE
+    } else if (!force_generic && tiled_plan(op, n, neg, nul, P, ln, g)) {
+#define CLF_BWD_TILED(OPV, LNV) \
+    hipLaunchKernelGGL((prod_bwd_tiled<OPV, LNV>), g, dim3(256), 0, s, a, b, gc, ga, gb, P)
+        switch (op) {
+            case OP_GEOM: if (ln) CLF_BWD_TILED(OP_GEOM, true); else CLF_BWD_TILED(OP_GEOM, false); break;
+            case OP_INNER: if (ln) CLF_BWD_TILED(OP_INNER, true); else CLF_BWD_TILED(OP_INNER, false); break;
+            case OP_LC: if (ln) CLF_BWD_TILED(OP_LC, true); else CLF_BWD_TILED(OP_LC, false); break;
+            case OP_RC: if (ln) CLF_BWD_TILED(OP_RC, true); else CLF_BWD_TILED(OP_RC, false); break;
+            case OP_WEDGE: CLF_BWD_TILED(OP_WEDGE, false); break;
+            case OP_REGR: CLF_BWD_TILED(OP_REGR, false); break;
+        }
+#undef CLF_BWD_TILED
     } else {
         const long long total = batch << n;
         const unsigned blocks = (unsigned)((total + 255) / 256);

@@ -76,7 +76,9 @@ const char* clf_last_error(void);
  *  kernels/ga/geom_prod_tiled.cu:169-175). */
 int clf_device_info_get(int device, clf_device_info* out);
 
-/* Largest n the product kernels accept. */
+/* Largest n the product kernels accept (16; rows past the LDS budget, n >= 13,
+ * run tiled kernels, as the reference's geom_prod_tiled_fused does,
+ * src/cliffordcuda/extensions/ga/geom_prod_tiled.py:370-398). */
 int clf_product_max_n(void);
 
 /* Forward of a binary product on `batch` rows.

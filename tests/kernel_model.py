@@ -150,3 +150,90 @@ def backward(op_name, a, b, gc, metric):
                 for jl in range(16):
                     GB[:, h, jl] += (tab[il, jl] * at[:, il] * gt[:, il ^ jl]).sum(-1)
     return GA.reshape(a.shape), GB.reshape(a.shape)
+
+
+# ---- tiled kernels (prod_fwd_tiled / prod_bwd_tiled) ------------------------
+# A workgroup owns the T output blocks K0 .. K0 + T - 1 and walks input tiles
+# I0 = 0, T, 2T, ...; the partner blocks of a tile are the aligned tile at
+# I0 ^ K0, read at local index (ih & (T-1)) ^ (kh & (T-1)). The kernels use
+# T = 256; the model takes T as a parameter so small n exercise several tiles.
+
+
+def forward_tiled(op_name, a, b, metric, T):
+    op = OPS[op_name]
+    P = plan(op, metric)
+    tabs = _tables(P["lowneg"])
+    NB = 1 << (P["n"] - 4)
+    assert NB % T == 0
+    A = a.reshape(a.shape[0], NB, 16)
+    B = b.reshape(b.shape[0], NB, 16)
+    out = np.zeros_like(A)
+    il16 = np.arange(16)
+    for K0 in range(0, NB, T):
+        acc = np.zeros((a.shape[0], T, 16))
+        for I0 in range(0, NB, T):
+            la = A[:, I0:I0 + T, :]
+            J0 = I0 ^ K0
+            lb = B[:, J0:J0 + T, :]
+            for lane in range(T):
+                kh = K0 + lane
+                for il in range(T):
+                    ih = I0 + il
+                    jh = ih ^ kh
+                    ok, s = hi_sign(op, ih, jh, P["negh"], P["nulh"], P["fullh"], P["nm1"], P["mu"])
+                    if not ok:
+                        continue
+                    pi = cross_pi(op, ih, P["nm1"])
+                    bt = lb[:, il ^ (kh & (T - 1)), :] * s * np.where(PARITY16 & pi, -1.0, 1.0)
+                    tab = tabs[variant(op, ih, jh)]
+                    for t in range(16):
+                        acc[:, lane, t] += (tab[il16, il16 ^ t] * la[:, il, il16] * bt[:, il16 ^ t]).sum(-1)
+        for lane in range(T):
+            kh = K0 + lane
+            if op == REGR:
+                out[:, P["fullh"] ^ kh, :] = acc[:, lane, ::-1]
+            else:
+                out[:, kh, :] = acc[:, lane, :]
+    return out.reshape(a.shape)
+
+
+def backward_tiled(op_name, a, b, gc, metric, T):
+    op = OPS[op_name]
+    P = plan(op, metric)
+    tabs = _tables(P["lowneg"])
+    NB = 1 << (P["n"] - 4)
+    fullh = P["fullh"]
+    A = a.reshape(a.shape[0], NB, 16)
+    B = b.reshape(b.shape[0], NB, 16)
+    G = gc.reshape(gc.shape[0], NB, 16)
+    GA = np.zeros_like(A)
+    GB = np.zeros_like(A)
+    il = np.arange(16)
+    for H0 in range(0, NB, T):
+        for M0 in range(0, NB, T):
+            G0 = ((fullh ^ H0 ^ M0) & ~(T - 1)) if op == REGR else (H0 ^ M0)
+            la, lb, lg = A[:, M0:M0 + T, :], B[:, M0:M0 + T, :], G[:, G0:G0 + T, :]
+            for hl in range(T):
+                h = H0 + hl
+                pi_h = cross_pi(op, h, P["nm1"])
+                for ml in range(T):
+                    m = M0 + ml
+                    oka, sa = hi_sign(op, h, m, P["negh"], P["nulh"], fullh, P["nm1"], P["mu"])
+                    okb, sb = hi_sign(op, m, h, P["negh"], P["nulh"], fullh, P["nm1"], P["mu"])
+                    if not (oka or okb):
+                        continue
+                    g = lg[:, (T - 1) ^ hl ^ ml, ::-1] if op == REGR else lg[:, hl ^ ml, :]
+                    if oka:
+                        bt = lb[:, ml, :] * sa * np.where(PARITY16 & pi_h, -1.0, 1.0)
+                        tab = tabs[variant(op, h, m)]
+                        for jl in range(16):
+                            GA[:, h, :] += tab[il, jl] * bt[:, jl:jl + 1] * g[:, il ^ jl]
+                    if okb:
+                        pm = cross_pi(op, m, P["nm1"])
+                        fl = np.where(PARITY16 & pm, -1.0, 1.0)
+                        at = la[:, ml, :] * sb * fl
+                        gt = g * fl
+                        tab = tabs[variant(op, m, h)]
+                        for jl in range(16):
+                            GB[:, h, jl] += (tab[il, jl] * at[:, il] * gt[:, il ^ jl]).sum(-1)
+    return GA.reshape(a.shape), GB.reshape(a.shape)

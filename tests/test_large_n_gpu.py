@@ -1,0 +1,99 @@
+"""Products past the whole-row LDS limit (n = 12 .. 16, the reference's tiled
+path, extensions/ga/geom_prod_tiled.py:1-31 and tests/correctness/
+test_geom_prod_tiled.py): the tiled kernels against the whole-row kernels at
+n = 12 (tiling forced with CLF_PRODUCT_PATH=tiled), against the
+per-coefficient generic kernels (an independent algorithm, forced with
+CLF_PRODUCT_PATH=generic) at n = 14 and 16, and against the oracle at n = 13.
+Bar: normwise relative error <= 1e-5 for values and both gradients."""
+import pytest
+import torch
+
+import cliffordcuda_amd as cc
+from oracle import clifford_oracle as O
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def rel_err(got, ref):
+    got = got.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    den = float(ref.abs().max())
+    return float((got - ref).abs().max()) / (den if den > 0 else 1.0)
+
+
+def run(op, metric, a, b, gc, monkeypatch, path=None):
+    if path:
+        monkeypatch.setenv("CLF_PRODUCT_PATH", path)
+    try:
+        x = a.clone().requires_grad_()
+        y = b.clone().requires_grad_()
+        c = cc.products.product(op, x, y, metric)
+        c.backward(gc)
+        torch.cuda.synchronize()
+    finally:
+        if path:
+            monkeypatch.delenv("CLF_PRODUCT_PATH")
+    return c.detach(), x.grad, y.grad
+
+
+def inputs(n, batch, seed):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(batch, 1 << n, generator=g).cuda() for _ in range(3)]
+
+
+def compare(r1, r2):
+    return [rel_err(u, v) for u, v in zip(r1, r2)]
+
+
+@pytest.mark.parametrize("metric", [(1,) * 12, (-1,) * 4 + (1, -1, 0, 1, 1, -1, 0, 1)], ids=["E12", "mixed12"])
+@pytest.mark.parametrize("op", O.OPS)
+def test_tiled_equals_whole_row_n12(op, metric, monkeypatch):
+    if op == "regressive" and 0 in metric:
+        pytest.skip("regressive is undefined for degenerate metrics")
+    a, b, gc = inputs(12, 3, 12)
+    print(f"[case] n=12 op={op} metric={metric}", flush=True)
+    e = compare(run(op, metric, a, b, gc, monkeypatch), run(op, metric, a, b, gc, monkeypatch, "tiled"))
+    assert max(e) <= TOL, e
+
+
+@pytest.mark.parametrize("op", O.OPS)
+def test_tiled_equals_generic_n14(op, monkeypatch):
+    metric = (1,) * 11 + (-1, -1, 1) if op == "regressive" else (1,) * 11 + (-1, -1, 0)
+    a, b, gc = inputs(14, 2, 14)
+    print(f"[case] n=14 op={op}", flush=True)
+    e = compare(run(op, metric, a, b, gc, monkeypatch), run(op, metric, a, b, gc, monkeypatch, "generic"))
+    assert max(e) <= TOL, e
+
+
+@pytest.mark.parametrize("op", ["geom", "lc"])
+def test_tiled_equals_generic_n16(op, monkeypatch):
+    """n = 16 (65536 components), Cl(13,2,1) as in the reference's largest
+    gradient case."""
+    metric = (1,) * 13 + (-1, -1, 0)
+    a, b, gc = inputs(16, 1, 16)
+    print(f"[case] n=16 op={op}", flush=True)
+    e = compare(run(op, metric, a, b, gc, monkeypatch), run(op, metric, a, b, gc, monkeypatch, "generic"))
+    assert max(e) <= TOL, e
+
+
+def test_tiled_geom_matches_oracle_n13():
+    """n = 13 (past the whole-row limit) against the fp64 oracle, one row."""
+    metric = (1,) * 10 + (-1, -1, 1)
+    g = torch.Generator().manual_seed(13)
+    a = torch.randn(1, 1 << 13, generator=g)
+    b = torch.randn(1, 1 << 13, generator=g)
+    c = cc.products.product("geom", a.cuda(), b.cuda(), metric)
+    ref = O.einsum_product("geom", a.double(), b.double(), metric)
+    assert rel_err(c, ref) <= TOL
+
+
+def test_public_api_past_limit():
+    """The algebra object and the free functions accept n = 16."""
+    metric = (1,) * 16
+    cl = cc.CliffordAlgebra(metric, device="cuda")
+    x = torch.randn(1, 1 << 16, device="cuda")
+    e0 = torch.zeros(1, 1 << 16, device="cuda")
+    e0[0, 1] = 1.0                        # the vector e_0
+    y = cl.geom_prod(e0, cl.geom_prod(e0, x))   # e_0 e_0 x = x (e_0^2 = +1)
+    assert rel_err(y, x) <= TOL
