@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import torch
 
-from . import _lib
+from . import _lib, _ops
 from . import products as _products
 from ._validate import check_mv
 
@@ -22,37 +22,44 @@ def _ws(lib, n, batch, device):
     return torch.empty(max(4, nbytes) // 4, dtype=torch.float32, device=device), nbytes
 
 
+def _bcast_fwd(x, w, op_code, side, n, neg, nul):
+    lib = _lib.load()
+    y = torch.empty_like(x)
+    ws, nbytes = _ws(lib, n, x.shape[0], x.device)
+    with torch.cuda.device(x.device):
+        rc = lib.clf_product_bcast_fwd(op_code, side, n, neg, nul, x.data_ptr(), w.data_ptr(), y.data_ptr(),
+                                       x.shape[0], ws.data_ptr(), nbytes, _lib.stream_of(x))
+    _lib.check(rc, "clf_product_bcast_fwd")
+    return y
+
+
+def _bcast_bwd(x, w, gy, op_code, side, n, neg, nul, need_x, need_w):
+    if not (need_x or need_w):
+        return None, None
+    lib = _lib.load()
+    gy = gy.contiguous()
+    gx = torch.empty_like(x) if need_x else None
+    gw = torch.empty_like(w) if need_w else None
+    ws, nbytes = _ws(lib, n, x.shape[0], x.device)
+    with torch.cuda.device(x.device):
+        rc = lib.clf_product_bcast_bwd(op_code, side, n, neg, nul, x.data_ptr(), w.data_ptr(), gy.data_ptr(),
+                                       _lib.ptr(gx), _lib.ptr(gw), x.shape[0], ws.data_ptr(), nbytes,
+                                       _lib.stream_of(x))
+    _lib.check(rc, "clf_product_bcast_bwd")
+    return gx, gw
+
+
 class _BcastFunc(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w, op_code, side, n, neg, nul):
-        lib = _lib.load()
-        y = torch.empty_like(x)
-        ws, nbytes = _ws(lib, n, x.shape[0], x.device)
-        with torch.cuda.device(x.device):
-            rc = lib.clf_product_bcast_fwd(op_code, side, n, neg, nul, x.data_ptr(), w.data_ptr(), y.data_ptr(),
-                                           x.shape[0], ws.data_ptr(), nbytes, _lib.stream_of(x))
-        _lib.check(rc, "clf_product_bcast_fwd")
         ctx.save_for_backward(x, w)
         ctx.meta = (op_code, side, n, neg, nul)
-        return y
+        return _bcast_fwd(x, w, op_code, side, n, neg, nul)
 
     @staticmethod
     def backward(ctx, gy):
         x, w = ctx.saved_tensors
-        op_code, side, n, neg, nul = ctx.meta
-        need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        if not (need_x or need_w):
-            return (None,) * 7
-        lib = _lib.load()
-        gy = gy.contiguous()
-        gx = torch.empty_like(x) if need_x else None
-        gw = torch.empty_like(w) if need_w else None
-        ws, nbytes = _ws(lib, n, x.shape[0], x.device)
-        with torch.cuda.device(x.device):
-            rc = lib.clf_product_bcast_bwd(op_code, side, n, neg, nul, x.data_ptr(), w.data_ptr(), gy.data_ptr(),
-                                           _lib.ptr(gx), _lib.ptr(gw), x.shape[0], ws.data_ptr(), nbytes,
-                                           _lib.stream_of(x))
-        _lib.check(rc, "clf_product_bcast_bwd")
+        gx, gw = _bcast_bwd(x, w, gy, *ctx.meta, ctx.needs_input_grad[0], ctx.needs_input_grad[1])
         return gx, gw, None, None, None, None, None
 
 
@@ -68,7 +75,10 @@ def bcast_product(op: str, x: torch.Tensor, w: torch.Tensor, metric: tuple, side
         wb = w.expand_as(x).contiguous()
         return _products.product(op, x, wb, metric) if side == 0 else _products.product(op, wb, x, metric)
     neg, nul = metric_masks(metric)
-    return _BcastFunc.apply(x.contiguous(), w.contiguous().reshape(1, -1), _lib.OP_CODES[op], side, n, neg, nul)
+    args = (x.contiguous(), w.contiguous().reshape(1, -1), _lib.OP_CODES[op], side, n, neg, nul)
+    if torch.compiler.is_compiling():
+        return _ops.bcast_product(*args)
+    return _BcastFunc.apply(*args)
 
 
 def product_bcast(op: str, x: torch.Tensor, w: torch.Tensor, cl) -> torch.Tensor:

@@ -9,7 +9,7 @@ from __future__ import annotations
 
 import torch
 
-from . import _lib
+from . import _lib, _ops
 from ._validate import dim_to_n
 
 
@@ -46,33 +46,44 @@ def graded(kind: str, x: torch.Tensor, neg: int = 0, nul: int = 0, grade: int = 
     n = dim_to_n(dim)
     shape = x.shape
     x2 = x.contiguous().reshape(-1, dim)
-    return _GradedFunc.apply(x2, _lib.GRADED_CODES[kind], n, neg, nul, grade).reshape(shape)
+    code = _lib.GRADED_CODES[kind]
+    if torch.compiler.is_compiling():
+        return _ops.graded(x2, code, n, neg, nul, grade).reshape(shape)
+    return _GradedFunc.apply(x2, code, n, neg, nul, grade).reshape(shape)
+
+
+def _norm_sq_fwd(x: torch.Tensor, n: int, neg: int, nul: int) -> torch.Tensor:
+    out = torch.empty(x.shape[0], dtype=x.dtype, device=x.device)
+    lib = _lib.load()
+    with torch.cuda.device(x.device):
+        rc = lib.clf_norm_sq_fwd(n, neg, nul, x.data_ptr(), out.data_ptr(), x.shape[0], _lib.stream_of(x))
+    _lib.check(rc, "clf_norm_sq_fwd")
+    return out
+
+
+def _norm_sq_bwd(x: torch.Tensor, gout: torch.Tensor, n: int, neg: int, nul: int) -> torch.Tensor:
+    gx = torch.empty_like(x)
+    gout = gout.contiguous()
+    lib = _lib.load()
+    with torch.cuda.device(x.device):
+        rc = lib.clf_norm_sq_bwd(n, neg, nul, x.data_ptr(), gout.data_ptr(), gx.data_ptr(), x.shape[0],
+                                 _lib.stream_of(x))
+    _lib.check(rc, "clf_norm_sq_bwd")
+    return gx
 
 
 class _NormSqFunc(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, n, neg, nul):
-        out = torch.empty(x.shape[0], dtype=x.dtype, device=x.device)
-        lib = _lib.load()
-        with torch.cuda.device(x.device):
-            rc = lib.clf_norm_sq_fwd(n, neg, nul, x.data_ptr(), out.data_ptr(), x.shape[0], _lib.stream_of(x))
-        _lib.check(rc, "clf_norm_sq_fwd")
         ctx.save_for_backward(x)
         ctx.meta = (n, neg, nul)
-        return out
+        return _norm_sq_fwd(x, n, neg, nul)
 
     @staticmethod
     def backward(ctx, gout):
         (x,) = ctx.saved_tensors
         n, neg, nul = ctx.meta
-        gx = torch.empty_like(x)
-        gout = gout.contiguous()
-        lib = _lib.load()
-        with torch.cuda.device(x.device):
-            rc = lib.clf_norm_sq_bwd(n, neg, nul, x.data_ptr(), gout.data_ptr(), gx.data_ptr(), x.shape[0],
-                                     _lib.stream_of(x))
-        _lib.check(rc, "clf_norm_sq_bwd")
-        return gx, None, None, None
+        return _norm_sq_bwd(x, gout, n, neg, nul), None, None, None
 
 
 def norm_sq(x: torch.Tensor, neg: int = 0, nul: int = 0) -> torch.Tensor:
@@ -81,7 +92,11 @@ def norm_sq(x: torch.Tensor, neg: int = 0, nul: int = 0) -> torch.Tensor:
     dim = x.shape[-1]
     n = dim_to_n(dim)
     lead = x.shape[:-1]
-    out = _NormSqFunc.apply(x.contiguous().reshape(-1, dim), n, neg, nul)
+    x2 = x.contiguous().reshape(-1, dim)
+    if torch.compiler.is_compiling():
+        out = _ops.norm_sq(x2, n, neg, nul)
+    else:
+        out = _NormSqFunc.apply(x2, n, neg, nul)
     return out.reshape(lead)
 
 

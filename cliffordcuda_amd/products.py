@@ -15,7 +15,7 @@ from __future__ import annotations
 
 import torch
 
-from . import _lib
+from . import _lib, _ops
 from ._validate import dim_to_n, metric_masks, normalize_metric
 
 
@@ -90,7 +90,10 @@ def product(op: str, a: torch.Tensor, b: torch.Tensor, metric=None) -> torch.Ten
     shape = a.shape
     a2 = a.contiguous().reshape(-1, dim)
     b2 = b.contiguous().reshape(-1, dim)
-    out = _ProductFunc.apply(a2, b2, _lib.OP_CODES[op], n, neg, nul)
+    if torch.compiler.is_compiling():
+        out = _ops.product(a2, b2, _lib.OP_CODES[op], n, neg, nul)
+    else:
+        out = _ProductFunc.apply(a2, b2, _lib.OP_CODES[op], n, neg, nul)
     return out.reshape(shape)
 
 

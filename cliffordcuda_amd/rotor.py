@@ -13,81 +13,98 @@ from __future__ import annotations
 
 import torch
 
-from . import _lib
+from . import _lib, _ops
 
 
 def _state_len(n: int) -> int:
-    k = _lib.load().clf_rotor_state_floats(n)
-    if k < 0:
+    """Floats of the rotor state: the n x n rotation and the (c, s) pairs of its
+    C(n, 2) plane rotations (``clf_rotor_state_floats``, computed here without
+    a library call so that traced graphs stay free of host calls)."""
+    if not 2 <= n <= 10:
         raise ValueError(f"rotor kernels support 2 <= n <= 10; got n={n}")
-    return k
+    return n * n + n * (n - 1)
+
+
+def _compile_fwd(biv: torch.Tensor, n: int) -> torch.Tensor:
+    biv = biv.contiguous()
+    state = torch.empty(_state_len(n), dtype=torch.float32, device=biv.device)
+    lib = _lib.load()
+    with torch.cuda.device(biv.device):
+        rc = lib.clf_rotor_compile_fwd(n, biv.data_ptr(), state.data_ptr(), _lib.stream_of(biv))
+    _lib.check(rc, "clf_rotor_compile_fwd")
+    return state
+
+
+def _compile_bwd(biv: torch.Tensor, g_state: torch.Tensor, n: int) -> torch.Tensor:
+    biv = biv.contiguous()
+    g_state = g_state.contiguous()
+    g_biv = torch.empty_like(biv)
+    lib = _lib.load()
+    with torch.cuda.device(biv.device):
+        rc = lib.clf_rotor_compile_bwd(n, biv.data_ptr(), g_state.data_ptr(), g_biv.data_ptr(), _lib.stream_of(biv))
+    _lib.check(rc, "clf_rotor_compile_bwd")
+    return g_biv
+
+
+def _apply_fwd(state: torch.Tensor, x: torch.Tensor, n: int) -> torch.Tensor:
+    y = torch.empty_like(x)
+    lib = _lib.load()
+    with torch.cuda.device(x.device):
+        rc = lib.clf_rotor_apply_fwd(n, state.data_ptr(), x.data_ptr(), y.data_ptr(), x.shape[0], _lib.stream_of(x))
+    _lib.check(rc, "clf_rotor_apply_fwd")
+    return y
+
+
+def _apply_bwd(state: torch.Tensor, x: torch.Tensor, gy: torch.Tensor, n: int, need_state: bool, need_x: bool):
+    if not (need_state or need_x):
+        return None, None
+    gy = gy.contiguous()
+    gx = torch.empty_like(x) if need_x else None
+    g_state = torch.empty_like(state) if need_state else None
+    lib = _lib.load()
+    ws = None
+    ws_bytes = 0
+    if need_state:
+        ws_bytes = lib.clf_rotor_apply_ws_bytes(n, x.shape[0])
+        ws = torch.empty(max(1, ws_bytes // 4), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        rc = lib.clf_rotor_apply_bwd(n, state.data_ptr(), x.data_ptr(), gy.data_ptr(), _lib.ptr(gx),
+                                     _lib.ptr(g_state), x.shape[0], _lib.ptr(ws), ws_bytes, _lib.stream_of(x))
+    _lib.check(rc, "clf_rotor_apply_bwd")
+    return g_state, gx
 
 
 class _CompileFunc(torch.autograd.Function):
     @staticmethod
     def forward(ctx, biv, n):
-        biv = biv.contiguous()
-        state = torch.empty(_state_len(n), dtype=torch.float32, device=biv.device)
-        lib = _lib.load()
-        with torch.cuda.device(biv.device):
-            rc = lib.clf_rotor_compile_fwd(n, biv.data_ptr(), state.data_ptr(), _lib.stream_of(biv))
-        _lib.check(rc, "clf_rotor_compile_fwd")
         ctx.save_for_backward(biv)
         ctx.n = n
-        return state
+        return _compile_fwd(biv, n)
 
     @staticmethod
     def backward(ctx, g_state):
         (biv,) = ctx.saved_tensors
-        g_state = g_state.contiguous()
-        g_biv = torch.empty_like(biv)
-        lib = _lib.load()
-        with torch.cuda.device(biv.device):
-            rc = lib.clf_rotor_compile_bwd(ctx.n, biv.data_ptr(), g_state.data_ptr(), g_biv.data_ptr(),
-                                           _lib.stream_of(biv))
-        _lib.check(rc, "clf_rotor_compile_bwd")
-        return g_biv, None
+        return _compile_bwd(biv, g_state, ctx.n), None
 
 
 class _ApplyFunc(torch.autograd.Function):
     @staticmethod
     def forward(ctx, state, x, n):
-        y = torch.empty_like(x)
-        lib = _lib.load()
-        with torch.cuda.device(x.device):
-            rc = lib.clf_rotor_apply_fwd(n, state.data_ptr(), x.data_ptr(), y.data_ptr(), x.shape[0],
-                                         _lib.stream_of(x))
-        _lib.check(rc, "clf_rotor_apply_fwd")
         ctx.save_for_backward(state, x)
         ctx.n = n
-        return y
+        return _apply_fwd(state, x, n)
 
     @staticmethod
     def backward(ctx, gy):
         state, x = ctx.saved_tensors
-        n = ctx.n
-        need_state, need_x = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        if not (need_state or need_x):
-            return None, None, None
-        gy = gy.contiguous()
-        gx = torch.empty_like(x) if need_x else None
-        g_state = torch.empty_like(state) if need_state else None
-        lib = _lib.load()
-        ws = None
-        ws_bytes = 0
-        if need_state:
-            ws_bytes = lib.clf_rotor_apply_ws_bytes(n, x.shape[0])
-            ws = torch.empty(max(1, ws_bytes // 4), dtype=torch.float32, device=x.device)
-        with torch.cuda.device(x.device):
-            rc = lib.clf_rotor_apply_bwd(n, state.data_ptr(), x.data_ptr(), gy.data_ptr(), _lib.ptr(gx),
-                                         _lib.ptr(g_state), x.shape[0], _lib.ptr(ws), ws_bytes,
-                                         _lib.stream_of(x))
-        _lib.check(rc, "clf_rotor_apply_bwd")
+        g_state, gx = _apply_bwd(state, x, gy, ctx.n, ctx.needs_input_grad[0], ctx.needs_input_grad[1])
         return g_state, gx, None
 
 
 def compile_bivector(bivector: torch.Tensor, n: int) -> torch.Tensor:
     """(1, C(n,2)) bivector -> rotor state (1-D). Differentiable."""
+    if torch.compiler.is_compiling():
+        return _ops.rotor_compile(bivector.reshape(-1).contiguous(), n)
     return _CompileFunc.apply(bivector.reshape(-1), n)
 
 
@@ -99,4 +116,6 @@ def apply_rotor(state: torch.Tensor, x: torch.Tensor, n: int) -> torch.Tensor:
             f"n={n}); got shape {tuple(state.shape)}")
     if state.device != x.device:
         raise ValueError(f"rotor state on device {state.device}, x on {x.device}")
+    if torch.compiler.is_compiling():
+        return _ops.rotor_apply(state.contiguous(), x.contiguous(), n)
     return _ApplyFunc.apply(state.contiguous(), x, n)
