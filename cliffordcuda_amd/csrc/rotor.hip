@@ -369,6 +369,10 @@ __global__ __launch_bounds__(256) void rotor_apply_bwd_kernel(const float* __res
 }
 
 // ---- small dense fp64 matrix functions in one wave -----------------------
+// Taylor degree after scaling to norm <= 1/4: the truncation (1/4)^9 / 9! ~ 1e-11
+// is far below the fp32 precision of the rotor state and the bivector gradient.
+constexpr int kTaylorDegree = 8;
+
 // Lane j (< M) holds column j of an M x M matrix in registers (compile-time M,
 // so the row indices are register names); the other lanes run along idle.
 
@@ -388,8 +392,8 @@ __device__ __forceinline__ double wave_max_f64(double v) {
 }
 
 // col <- column j of expm(Z), Z row-major M x M in LDS, by scaling to 1-norm
-// <= 1/4 and squaring, with the degree-12 Taylor series (Horner form; truncation
-// below 1e-17 relative).
+// <= 1/4 and squaring, with the degree-8 Taylor series (Horner form; truncation
+// (1/4)^9 / 9! = 1e-11 relative, far below the fp32 results).
 template <int M>
 __device__ __forceinline__ void expm_cols(double (&col)[M], const double* __restrict__ Z, int j) {
     // 1-norm, then the number of squarings that brings it to <= 1/2
@@ -405,7 +409,7 @@ __device__ __forceinline__ void expm_cols(double (&col)[M], const double* __rest
     const double scale = ldexp(1.0, -sq);
 #pragma unroll
     for (int i = 0; i < M; ++i) col[i] = (i == j) ? 1.0 : 0.0;
-    for (int k = 12; k >= 1; --k) {
+    for (int k = kTaylorDegree; k >= 1; --k) {
         const double f = scale / (double)k;
         double t[M];
 #pragma unroll
@@ -433,6 +437,44 @@ __device__ __forceinline__ void expm_cols(double (&col)[M], const double* __rest
     }
 }
 
+// c, s of the plane rotation that zeroes b against a: 1 / sqrt(a^2 + b^2) by the
+// hardware reciprocal square root refined with two Newton steps (full fp64
+// precision), instead of a square root and a division
+__device__ __forceinline__ void givens_cs(double a, double b, double& c, double& s) {
+    const double r2 = a * a + b * b;
+    c = 1.0;
+    s = 0.0;
+    if (r2 > 1e-300) {
+        double y = __builtin_amdgcn_rsq(r2);
+        y = y * (1.5 - 0.5 * r2 * y * y);
+        y = y * (1.5 - 0.5 * r2 * y * y);
+        c = a * y;
+        s = b * y;
+    }
+}
+
+// E <- G_k^T E for the planes in lex order (E ends as I), lane j < N holding
+// column j of E; lane 0 writes the (c, s) pairs
+template <int N>
+__device__ __forceinline__ void givens_cols(double (&col)[N], float* __restrict__ cs, int lane) {
+#pragma unroll
+    for (int p = 0; p < N - 1; ++p) {
+#pragma unroll
+        for (int q = p + 1; q < N; ++q) {
+            const int k = p * N - p * (p + 1) / 2 + (q - p - 1);
+            double c, s;
+            givens_cs(readlane_f64(col[p], p), readlane_f64(col[q], p), c, s);
+            const double ep = col[p], eq = col[q];
+            col[p] = c * ep + s * eq;
+            col[q] = -s * ep + c * eq;
+            if (lane == 0) {
+                cs[2 * k] = (float)c;
+                cs[2 * k + 1] = (float)s;
+            }
+        }
+    }
+}
+
 // A = -B, B = 2 (M - M^T) from the lex-ordered bivector: A[i][j] = -2 b, A[j][i] = 2 b
 __device__ __forceinline__ double generator_entry(const float* __restrict__ biv, int n, int i, int j) {
     if (i == j) return 0.0;
@@ -443,8 +485,8 @@ __device__ __forceinline__ double generator_entry(const float* __restrict__ biv,
 }
 
 template <int N>
-__global__ __launch_bounds__(64) void rotor_compile_fwd_kernel(const float* __restrict__ biv,
-                                                                float* __restrict__ state) {
+__global__ __launch_bounds__(64) void rotor_compile_fwd_cols_kernel(const float* __restrict__ biv,
+                                                                     float* __restrict__ state) {
     __shared__ double Z[N * N];
     const int j = threadIdx.x;
     for (int idx = j; idx < N * N; idx += 64) Z[idx] = generator_entry(biv, N, idx / N, idx % N);
@@ -455,28 +497,7 @@ __global__ __launch_bounds__(64) void rotor_compile_fwd_kernel(const float* __re
 #pragma unroll
         for (int i = 0; i < N; ++i) state[i * N + j] = (float)col[i];
     // Givens elimination E <- G_k^T E (planes in lex order); E ends as I (det = +1)
-    float* cs = state + N * N;
-#pragma unroll
-    for (int p = 0; p < N - 1; ++p) {
-#pragma unroll
-        for (int q = p + 1; q < N; ++q) {
-            const int k = p * N - p * (p + 1) / 2 + (q - p - 1);
-            const double a = readlane_f64(col[p], p), bq = readlane_f64(col[q], p);
-            const double r = sqrt(a * a + bq * bq);
-            double c = 1.0, s = 0.0;
-            if (r > 1e-300) {
-                c = a / r;
-                s = bq / r;
-            }
-            const double ep = col[p], eq = col[q];
-            col[p] = c * ep + s * eq;
-            col[q] = -s * ep + c * eq;
-            if (j == 0) {
-                cs[2 * k] = (float)c;
-                cs[2 * k + 1] = (float)s;
-            }
-        }
-    }
+    givens_cols<N>(col, state + N * N, j);
 }
 
 // dL/dQ (tangent part) = Q skew(Gamma), skew(Gamma)[p][q] = K_pq / 2 = -skew(Gamma)[q][p],
@@ -494,16 +515,16 @@ __global__ __launch_bounds__(1024) void rotor_gamma_finalize_kernel(int n, const
     while (ep < C) ep <<= 1;
     const int ngrp = 1024 / ep;
     const int e = threadIdx.x & (ep - 1), grp = threadIdx.x / ep;
-    double t0 = 0.0, t1 = 0.0;
+    // eight independent loads per iteration, so their latencies overlap
+    double t[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
     if (e < C) {
         int p = grp;
-        for (; p + ngrp < nparts; p += 2 * ngrp) {
-            t0 += (double)gamma_ws[(long long)p * C + e];
-            t1 += (double)gamma_ws[(long long)(p + ngrp) * C + e];
-        }
-        if (p < nparts) t0 += (double)gamma_ws[(long long)p * C + e];
+        for (; p + 7 * ngrp < nparts; p += 8 * ngrp)
+#pragma unroll
+            for (int u = 0; u < 8; ++u) t[u] += (double)gamma_ws[(long long)(p + u * ngrp) * C + e];
+        for (; p < nparts; p += ngrp) t[0] += (double)gamma_ws[(long long)p * C + e];
     }
-    part[threadIdx.x] = t0 + t1;
+    part[threadIdx.x] = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
     for (int i = threadIdx.x; i < n * n; i += blockDim.x) S[i] = 0.0;
     __syncthreads();
     if (threadIdx.x < C) {
@@ -530,6 +551,7 @@ __global__ __launch_bounds__(1024) void rotor_gamma_finalize_kernel(int n, const
 template <int N>
 __device__ __forceinline__ void expm_frechet_cols(double (&Lc)[N], const double* __restrict__ X,
                                                   const double* __restrict__ G, int j) {
+    // G is given pre-scaled to norm <= 1 by the caller (the result is linear in G)
     double cs = 0.0;
     if (j < N)
         for (int i = 0; i < N; ++i) cs += fabs(X[i * N + j]) + fabs(G[i * N + j]);
@@ -549,7 +571,7 @@ __device__ __forceinline__ void expm_frechet_cols(double (&Lc)[N], const double*
         Ec[i] = (i == j) ? 1.0 : 0.0;
         Lc[i] = 0.0;
     }
-    for (int k = 12; k >= 1; --k) {
+    for (int k = kTaylorDegree; k >= 1; --k) {
         const double f = scale / (double)k;
         double tE[N], tL[N];
 #pragma unroll
@@ -598,27 +620,169 @@ __device__ __forceinline__ void expm_frechet_cols(double (&Lc)[N], const double*
 // g_biv from dL/dQ (Q slot of g_state) through Q = expm(A), A = -B(biv):
 // dL/dA = L(A^T, dL/dQ), the (1,2) block of expm([[A^T, dL/dQ], [0, A^T]]).
 template <int N>
-__global__ __launch_bounds__(64) void rotor_compile_bwd_kernel(const float* __restrict__ biv,
-                                                                const float* __restrict__ g_state,
-                                                                float* __restrict__ g_biv) {
+__global__ __launch_bounds__(64) void rotor_compile_bwd_cols_kernel(const float* __restrict__ biv,
+                                                                     const float* __restrict__ g_state,
+                                                                     float* __restrict__ g_biv) {
     __shared__ double X[N * N], G[N * N], F[N * N];
     const int j = threadIdx.x;
+    double gmax = 0.0;
+    for (int idx = j; idx < N * N; idx += 64) gmax = fmax(gmax, fabs((double)g_state[idx]));
+    gmax = wave_max_f64(gmax) * N;  // bounds every column sum of |G|
+    int gexp = 0;
+    if (gmax > 1.0) frexp(gmax, &gexp);
     for (int idx = j; idx < N * N; idx += 64) {
         const int r = idx / N, c = idx % N;
         X[idx] = generator_entry(biv, N, c, r);  // A^T
-        G[idx] = (double)g_state[idx];
+        G[idx] = ldexp((double)g_state[idx], -gexp);
     }
     __syncthreads();
     double Lc[N];
     expm_frechet_cols<N>(Lc, X, G, j);
     if (j < N)
 #pragma unroll
-        for (int i = 0; i < N; ++i) F[i * N + j] = Lc[i];
+        for (int i = 0; i < N; ++i) F[i * N + j] = ldexp(Lc[i], gexp);
     __syncthreads();
     for (int k = j; k < n_planes(N); k += 64) {
         const int p = plane_p(N, k), q = plane_q(N, k);
         // dL/dB = -dL/dA; dL/db = 2 (dL/dB[p][q] - dL/dB[q][p])
         g_biv[k] = (float)(-2.0 * (F[p * N + q] - F[q * N + p]));
+    }
+}
+
+// ---- entry per lane (N <= 8) ------------------------------------------------
+// Lane e = i N + j holds entry (i, j) of each N x N matrix and row i of the
+// fixed operands in registers; a product needs column j of the other factor,
+// N doubles gathered with lane shuffles (ds_bpermute), so one step of the
+// Taylor recursion or of squaring is N FMAs per lane instead of N^2 in N lanes.
+// Lanes e >= N^2 compute on row/column 0 and never store.
+
+__device__ __forceinline__ double shfl_f64(double v, int src) {
+    const long long bits = __double_as_longlong(v);
+    const int lo = __shfl((int)(bits & 0xffffffffll), src, 64);
+    const int hi = __shfl((int)(bits >> 32), src, 64);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+// number of halvings that bring the infinity norm to <= 1/4 (rows in registers)
+template <int N>
+__device__ __forceinline__ int halvings(double rowsum) {
+    double nrm = wave_max_f64(rowsum);
+    int sq = 0;
+    while (nrm > 0.25 && sq < 60) {
+        nrm *= 0.5;
+        ++sq;
+    }
+    return sq;
+}
+
+// entry (i, j) of expm(Z), row i of Z given in z (degree-8 Taylor, Horner form,
+// after scaling; then squaring)
+template <int N>
+__device__ __forceinline__ double expm_entry(const double (&z)[N], int i, int j) {
+    double rs = 0.0;
+#pragma unroll
+    for (int l = 0; l < N; ++l) rs += fabs(z[l]);
+    const int sq = halvings<N>(rs);
+    const double scale = ldexp(1.0, -sq);
+    const double id = (i == j) ? 1.0 : 0.0;
+    double e = id;
+    for (int k = kTaylorDegree; k >= 1; --k) {
+        const double f = scale / (double)k;
+        double t = 0.0;
+#pragma unroll
+        for (int l = 0; l < N; ++l) t += z[l] * shfl_f64(e, l * N + j);
+        e = id + f * t;
+    }
+    for (int r = 0; r < sq; ++r) {
+        double t = 0.0;
+#pragma unroll
+        for (int l = 0; l < N; ++l) t += shfl_f64(e, i * N + l) * shfl_f64(e, l * N + j);
+        e = t;
+    }
+    return e;
+}
+
+template <int N>
+__global__ __launch_bounds__(64) void rotor_compile_fwd_ent_kernel(const float* __restrict__ biv,
+                                                                    float* __restrict__ state) {
+    static_assert(N * N <= 64, "one entry per lane");
+    const int lane = threadIdx.x;
+    const bool active = lane < N * N;
+    const int i = active ? lane / N : 0, j = active ? lane % N : 0;
+    double z[N];
+#pragma unroll
+    for (int l = 0; l < N; ++l) z[l] = generator_entry(biv, N, i, l);
+    const double e = expm_entry<N>(z, i, j);
+    if (active) state[i * N + j] = (float)e;
+    // Givens elimination on columns: lane j < N gathers column j, so the row
+    // updates of a plane are register operations
+    double col[N];
+#pragma unroll
+    for (int r = 0; r < N; ++r) col[r] = shfl_f64(e, r * N + (lane < N ? lane : 0));
+    givens_cols<N>(col, state + N * N, lane);
+}
+
+// Adjoint Frechet derivative by the block identity (see the column version):
+// lane (i, j) holds E[i][j] and L[i][j]; X = A^T and G rows in registers.
+template <int N>
+__global__ __launch_bounds__(64) void rotor_compile_bwd_ent_kernel(const float* __restrict__ biv,
+                                                                    const float* __restrict__ g_state,
+                                                                    float* __restrict__ g_biv) {
+    static_assert(N * N <= 64, "one entry per lane");
+    const int lane = threadIdx.x;
+    const bool active = lane < N * N;
+    const int i = active ? lane / N : 0, j = active ? lane % N : 0;
+    double x[N], g[N];
+    double xs = 0.0, gs = 0.0;
+#pragma unroll
+    for (int l = 0; l < N; ++l) {
+        x[l] = generator_entry(biv, N, l, i);  // (A^T)[i][l]
+        g[l] = (double)g_state[i * N + l];
+        xs += fabs(x[l]);
+        gs += fabs(g[l]);
+    }
+    // The derivative is linear in G: scale G to norm <= 1 by a power of two
+    // (exact) so that the number of squarings depends on X only, and scale the
+    // result back at the end. Summed over a batch, G is often 1e4 or larger.
+    int gexp = 0;
+    const double gmax = wave_max_f64(gs);
+    if (gmax > 1.0) frexp(gmax, &gexp);
+#pragma unroll
+    for (int l = 0; l < N; ++l) g[l] = ldexp(g[l], -gexp);
+    const int sq = halvings<N>(xs + ldexp(gs, -gexp));
+    const double scale = ldexp(1.0, -sq);
+    const double id = (i == j) ? 1.0 : 0.0;
+    double e = id, L = 0.0;
+    for (int k = kTaylorDegree; k >= 1; --k) {
+        const double f = scale / (double)k;
+        double te = 0.0, tl = 0.0;
+#pragma unroll
+        for (int l = 0; l < N; ++l) {
+            const double el = shfl_f64(e, l * N + j), ll = shfl_f64(L, l * N + j);
+            te += x[l] * el;
+            tl += x[l] * ll + g[l] * el;
+        }
+        e = id + f * te;
+        L = f * tl;
+    }
+    for (int r = 0; r < sq; ++r) {
+        double te = 0.0, tl = 0.0;
+#pragma unroll
+        for (int l = 0; l < N; ++l) {
+            const double eil = shfl_f64(e, i * N + l), lil = shfl_f64(L, i * N + l);
+            const double elj = shfl_f64(e, l * N + j), llj = shfl_f64(L, l * N + j);
+            te += eil * elj;
+            tl += eil * llj + lil * elj;
+        }
+        e = te;
+        L = tl;
+    }
+    // dL/dB = -dL/dA; dL/db = 2 (dL/dB[p][q] - dL/dB[q][p]), lane (p, q) with p < q
+    L = ldexp(L, gexp);
+    const double ft = shfl_f64(L, j * N + i);  // F[q][p]
+    if (active && i < j) {
+        const int k = i * N - i * (i + 1) / 2 + (j - i - 1);
+        g_biv[k] = (float)(-2.0 * (L - ft));
     }
 }
 
@@ -637,6 +801,20 @@ __global__ __launch_bounds__(64) void rotor_compile_bwd_kernel(const float* __re
         case 10: CALL(10); break;         \
         default: break;                   \
     }
+
+// one entry per lane up to n = 8 (64 entries), one column per lane above
+template <int N>
+static void launch_compile_fwd(const float* biv, float* state, hipStream_t s) {
+    if constexpr (N * N <= 64) hipLaunchKernelGGL((rotor_compile_fwd_ent_kernel<N>), dim3(1), dim3(64), 0, s, biv, state);
+    else hipLaunchKernelGGL((rotor_compile_fwd_cols_kernel<N>), dim3(1), dim3(64), 0, s, biv, state);
+}
+
+template <int N>
+static void launch_compile_bwd(const float* biv, const float* g_state, float* g_biv, hipStream_t s) {
+    if constexpr (N * N <= 64)
+        hipLaunchKernelGGL((rotor_compile_bwd_ent_kernel<N>), dim3(1), dim3(64), 0, s, biv, g_state, g_biv);
+    else hipLaunchKernelGGL((rotor_compile_bwd_cols_kernel<N>), dim3(1), dim3(64), 0, s, biv, g_state, g_biv);
+}
 
 static int check_rotor_n(int n) {
     if (n < kRotorMinN || n > kRotorMaxN)
@@ -665,7 +843,7 @@ int rotor_compile_fwd(int n, const float* biv, float* state, void* stream) {
     if (int rc = check_rotor_n(n)) return rc;
     if (!biv || !state) return set_error(CLF_ERR_ARG, "null pointer argument");
     hipStream_t s = (hipStream_t)stream;
-#define CLF_CALL(N) hipLaunchKernelGGL((rotor_compile_fwd_kernel<N>), dim3(1), dim3(64), 0, s, biv, state)
+#define CLF_CALL(N) launch_compile_fwd<N>(biv, state, s)
     CLF_ROTOR_DISPATCH(n, CLF_CALL)
 #undef CLF_CALL
     CLF_HIP_CHECK(hipGetLastError());
@@ -676,7 +854,7 @@ int rotor_compile_bwd(int n, const float* biv, const float* g_state, float* g_bi
     if (int rc = check_rotor_n(n)) return rc;
     if (!biv || !g_state || !g_biv) return set_error(CLF_ERR_ARG, "null pointer argument");
     hipStream_t s = (hipStream_t)stream;
-#define CLF_CALL(N) hipLaunchKernelGGL((rotor_compile_bwd_kernel<N>), dim3(1), dim3(64), 0, s, biv, g_state, g_biv)
+#define CLF_CALL(N) launch_compile_bwd<N>(biv, g_state, g_biv, s)
     CLF_ROTOR_DISPATCH(n, CLF_CALL)
 #undef CLF_CALL
     CLF_HIP_CHECK(hipGetLastError());
