@@ -344,8 +344,19 @@ def c4_rotor(args, torch, cc, lib, T):
     fms = T.kernel_ms(lambda: lib.clf_rotor_apply_fwd(n, state.data_ptr(), x.data_ptr(), y.data_ptr(), B, sp))
     bms = T.kernel_ms(lambda: lib.clf_rotor_apply_bwd(n, state.data_ptr(), x.data_ptr(), gy.data_ptr(),
                                                       gx.data_ptr(), gs.data_ptr(), B, ws.data_ptr(), nb, sp))
+    # the same entry points on the register plane-rotation chain (the n = 8
+    # default is the Cl(8,0) representation on the matrix cores)
+    os.environ["CLF_ROTOR_PATH"] = "chain"
+    try:
+        cfms = T.kernel_ms(lambda: lib.clf_rotor_apply_fwd(n, state.data_ptr(), x.data_ptr(), y.data_ptr(), B, sp))
+        cbms = T.kernel_ms(lambda: lib.clf_rotor_apply_bwd(n, state.data_ptr(), x.data_ptr(), gy.data_ptr(),
+                                                           gx.data_ptr(), gs.data_ptr(), B, ws.data_ptr(), nb, sp))
+    finally:
+        del os.environ["CLF_ROTOR_PATH"]
     byts = 20.0 * D * B
     return {"workload": "c4: RotorLayer train Cl(7,1) fwd+bwd (rotor recompiled each step)", "batch": B,
+            "path": "Cl(8,0) representation, MFMA (rotor16 kernels)",
+            "chain_path": {"apply_fwd_ms": cfms, "apply_bwd_ms": cbms},
             "ms_per_step": ms, "rows_per_s": B / (ms * 1e-3),
             "hbm_gbs_algorithmic": byts / (ms * 1e-3) / 1e9, "frac_hbm": byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
             "compile_fwd_ms": cms, "apply_fwd_ms": fms, "apply_bwd_ms": bms,

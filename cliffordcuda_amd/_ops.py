@@ -187,7 +187,8 @@ def rotor_compile(biv: Tensor, n: int) -> Tensor:
 
 @rotor_compile.register_fake
 def _(biv, n):
-    return biv.new_empty(n * n + n * (n - 1))
+    from .rotor import _state_len
+    return biv.new_empty(_state_len(n))
 
 
 @torch.library.custom_op(f"{_NS}::rotor_compile_bwd", mutates_args=())

@@ -31,14 +31,6 @@
 
 namespace clf {
 
-struct RepTable {
-    // entry [x * m + z]: blade index | 0x80000000 if the sign s(I) is -1
-    //                    | 0x40000000 if s(I) (-1)^{popc(x & z)} is -1 (transposed conversion)
-    unsigned e[1 << (2 * kRepMaxLogM)];
-    // m = 16: multiple of 4 xor-ed into the blade offsets of odd rows in LDS so
-    // that the gathers of two rows in one half-wave use distinct banks (0: none found)
-    unsigned odd_xor;
-};
 
 // gather t[z] = s * row[blade] from the staged row, WHT over z, and write the
 // standard-layout matrix phi[r][c] = W[r ^ c][c] (lane holds x) into mat
@@ -338,63 +330,6 @@ __global__ __launch_bounds__(256) void rep_bwd_kernel(const float* __restrict__ 
 // back through LDS as W_c[i ^ j][j] at row stride 20 floats, which keeps both
 // the scattered b32 writes and the b128 row reads free of bank conflicts.
 
-// Group of four rows: lane l moves float4 chunk l of row j (j = 0..3); rows
-// past the end re-read the last row and are never stored.
-struct Pre16 {
-    float4 v[4];
-};
-
-__device__ __forceinline__ Pre16 fetch16(const float* __restrict__ src, long long row0, long long batch, int lane) {
-    Pre16 p;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        long long row = row0 + j;
-        row = row < batch ? row : batch - 1;
-        p.v[j] = reinterpret_cast<const float4*>(src + row * 256)[lane];
-    }
-    return p;
-}
-
-// staged row j at [j * 256, (j + 1) * 256), odd rows with chunk index lane ^ oddc
-__device__ __forceinline__ void stage16(float* __restrict__ dst, const Pre16& p, int lane, unsigned oddc) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        reinterpret_cast<float4*>(dst + j * 256)[(j & 1) ? (lane ^ oddc) : lane] = p.v[j];
-}
-
-// Rows past the end were computed from clamped copies of the last row, so
-// their results are bit-identical to it: they are stored to the last row again
-// instead of branching around the stores.
-__device__ __forceinline__ void store16(float* __restrict__ dstg, const float* __restrict__ src, long long row0,
-                                        long long batch, int lane, unsigned oddc) {
-    float4 v[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = reinterpret_cast<const float4*>(src + j * 256)[(j & 1) ? (lane ^ oddc) : lane];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        long long row = row0 + j;
-        row = row < batch ? row : batch - 1;
-        reinterpret_cast<float4*>(dstg + row * 256)[lane] = v[j];
-    }
-}
-
-// gather t[z] of the lane's row with the sign bit selected by SIGNSHIFT
-// (0: s(I), 1: the transposed conversion's sign), then WHT
-template <int SIGNSHIFT>
-__device__ __forceinline__ void gather16(const float* __restrict__ row, const unsigned (&ent)[16], float (&w)[16]) {
-#pragma unroll
-    for (int z = 0; z < 16; ++z)
-        w[z] = __uint_as_float(__float_as_uint(row[ent[z] & 0xffffu]) ^ ((ent[z] << SIGNSHIFT) & 0x80000000u));
-}
-
-// inverse WHT of W_c[x][.], scale 1/16, scatter s(I) t[z] into the row's blade slots
-__device__ __forceinline__ void unconvert16(float (&w)[16], float* __restrict__ row, const unsigned (&ent)[16]) {
-    wht_inplace<16>(w);
-#pragma unroll
-    for (int z = 0; z < 16; ++z)
-        row[ent[z] & 0xffffu] = __uint_as_float(__float_as_uint(w[z] * 0.0625f) ^ (ent[z] & 0x80000000u));
-}
-
 __global__ __launch_bounds__(256) void rep16_fwd_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                          float* __restrict__ C, long long batch, RepTable T) {
     __shared__ float lds[4][2 * 4 * 256];  // per wave: staged a | staged b; later the relayout, then c
@@ -513,23 +448,6 @@ __global__ __launch_bounds__(256) void rep16_bwd_kernel(const float* __restrict_
 //          (side 1): gx = phi^-1(phi(w)^T phi(gy)), gw = phi^-1(sum_rows phi(gy) phi(x)^T).
 // The weight-gradient sum runs in the MFMA accumulators across a wave's rows;
 // workgroups write 16x16 partials that one small kernel sums and converts.
-
-// 16 x 16 x 16 product: operand k of A (B) is xor16<k>(a[k]) if SA (SB), else
-// a[k] as given (already shuffled)
-template <bool SA, bool SB, unsigned... K>
-__device__ __forceinline__ floatx16 mfma_chain_pre(floatx16 acc, const float (&a)[16], const float (&b)[16],
-                                                   std::integer_sequence<unsigned, K...>) {
-    ((acc = __builtin_amdgcn_mfma_f32_16x16x1f32(SA ? xor16<K>(a[K]) : a[K], SB ? xor16<K>(b[K]) : b[K], acc, 0, 0,
-                                                  0)),
-     ...);
-    return acc;
-}
-
-template <unsigned... K>
-__device__ __forceinline__ void shuffle_operand(const float (&w)[16], float (&op)[16],
-                                                std::integer_sequence<unsigned, K...>) {
-    ((op[K] = xor16<K>(w[K])), ...);
-}
 
 // the weight's conversion for lane x (sign bit 31 - SIGNSHIFT of the entries:
 // 0 = phi(w), 1 = the transposed conversion), shuffled into operand order
@@ -768,7 +686,7 @@ static bool rep_table_build(int n, uint32_t neg, RepTable& T) {
 }
 
 // Tables are built once per (n, neg) and kept (immutable after insertion).
-static bool rep_table(int n, uint32_t neg, RepTable& T) {
+bool rep_table(int n, uint32_t neg, RepTable& T) {
     static std::mutex mu;
     static std::map<unsigned, std::pair<bool, RepTable>> cache;
     const unsigned key = ((unsigned)n << 24) | neg;

@@ -1,7 +1,9 @@
-// Shared pieces of the matrix-representation kernels (rep.hip, rep_split.hip):
-// wave-local LDS ordering, the in-register Walsh-Hadamard transform, the DPP
-// xor shuffles that build MFMA operands, the 4-block 16x16 MFMA chain with its
-// LDS relayout, and the host search for real Pauli generators.
+// Shared pieces of the matrix-representation kernels (rep.hip, rep_split.hip,
+// rotor_rep.hip): wave-local LDS ordering, the in-register Walsh-Hadamard
+// transform, the DPP xor shuffles that build MFMA operands, the 4-block 16x16
+// MFMA chain with its LDS relayout and block transpose, the conversion tables
+// and row-group staging of m = 16, and the host search for real Pauli
+// generators.
 #pragma once
 
 #include <utility>
@@ -100,6 +102,143 @@ __device__ __forceinline__ void relayout_load(const float* __restrict__ src, int
         w[4 * q + 3] = t.w;
     }
 }
+
+// ---- conversion tables and the 16 x 16 row-group helpers ------------------
+
+struct RepTable {
+    // entry [x * m + z]: blade index | 0x80000000 if the sign s(I) is -1
+    //                    | 0x40000000 if s(I) (-1)^{popc(x & z)} is -1 (transposed conversion)
+    unsigned e[1 << (2 * kRepMaxLogM)];
+    // m = 16: multiple of 4 xor-ed into the blade offsets of odd rows in LDS so
+    // that the gathers of two rows in one half-wave use distinct banks (0: none found)
+    unsigned odd_xor;
+};
+
+// The table for (n, neg), built once and cached; false if the signature has
+// no real matrix representation of size 2^(n/2) <= 16.
+bool rep_table(int n, uint32_t neg, RepTable& T);
+
+// Group of four rows: lane l moves float4 chunk l of row j (j = 0..3); rows
+// past the end re-read the last row and are never stored.
+struct Pre16 {
+    float4 v[4];
+};
+
+__device__ __forceinline__ Pre16 fetch16(const float* __restrict__ src, long long row0, long long batch, int lane) {
+    Pre16 p;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        long long row = row0 + j;
+        row = row < batch ? row : batch - 1;
+        p.v[j] = reinterpret_cast<const float4*>(src + row * 256)[lane];
+    }
+    return p;
+}
+
+// staged row j at [j * 256, (j + 1) * 256), odd rows with chunk index lane ^ oddc
+__device__ __forceinline__ void stage16(float* __restrict__ dst, const Pre16& p, int lane, unsigned oddc) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        reinterpret_cast<float4*>(dst + j * 256)[(j & 1) ? (lane ^ oddc) : lane] = p.v[j];
+}
+
+// Rows past the end were computed from clamped copies of the last row, so
+// their results are bit-identical to it: they are stored to the last row again
+// instead of branching around the stores.
+__device__ __forceinline__ void store16(float* __restrict__ dstg, const float* __restrict__ src, long long row0,
+                                        long long batch, int lane, unsigned oddc) {
+    float4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = reinterpret_cast<const float4*>(src + j * 256)[(j & 1) ? (lane ^ oddc) : lane];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        long long row = row0 + j;
+        row = row < batch ? row : batch - 1;
+        reinterpret_cast<float4*>(dstg + row * 256)[lane] = v[j];
+    }
+}
+
+// gather t[z] of the lane's row with the sign bit selected by SIGNSHIFT
+// (0: s(I), 1: the transposed conversion's sign), then WHT
+template <int SIGNSHIFT>
+__device__ __forceinline__ void gather16(const float* __restrict__ row, const unsigned (&ent)[16], float (&w)[16]) {
+#pragma unroll
+    for (int z = 0; z < 16; ++z)
+        w[z] = __uint_as_float(__float_as_uint(row[ent[z] & 0xffffu]) ^ ((ent[z] << SIGNSHIFT) & 0x80000000u));
+}
+
+// inverse WHT of W_c[x][.], scale 1/16, scatter s(I) t[z] into the row's blade slots
+__device__ __forceinline__ void unconvert16(float (&w)[16], float* __restrict__ row, const unsigned (&ent)[16]) {
+    wht_inplace<16>(w);
+#pragma unroll
+    for (int z = 0; z < 16; ++z)
+        row[ent[z] & 0xffffu] = __uint_as_float(__float_as_uint(w[z] * 0.0625f) ^ (ent[z] & 0x80000000u));
+}
+
+// 16 x 16 x 16 product: operand k of A (B) is xor16<k>(a[k]) if SA (SB), else
+// a[k] as given (already shuffled)
+template <bool SA, bool SB, unsigned... K>
+__device__ __forceinline__ floatx16 mfma_chain_pre(floatx16 acc, const float (&a)[16], const float (&b)[16],
+                                                   std::integer_sequence<unsigned, K...>) {
+    ((acc = __builtin_amdgcn_mfma_f32_16x16x1f32(SA ? xor16<K>(a[K]) : a[K], SB ? xor16<K>(b[K]) : b[K], acc, 0, 0,
+                                                  0)),
+     ...);
+    return acc;
+}
+
+template <unsigned... K>
+__device__ __forceinline__ void shuffle_operand(const float (&w)[16], float (&op)[16],
+                                                std::integer_sequence<unsigned, K...>) {
+    ((op[K] = xor16<K>(w[K])), ...);
+}
+
+
+// Block transpose of a product for the next product. C_b[4g + t][j] sits in
+// lane 16g + j, register 4b + t; after the swaps, register k = 4g + t of lane
+// (b, j) holds C_b[k][j], the B operand of a following 4-block product (and,
+// read as C_b^T, its A operand). For each t the four registers 4b + t form a
+// 4 x 4 transpose between the register block b and the 16-lane row g: one
+// 32-lane swap (bit 1 of b and g), then one 16-lane swap (bit 0).
+__device__ __forceinline__ void permlane_swap32(float& a, float& b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ void permlane_swap16(float& a, float& b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ void transpose_blocks(const floatx16& acc, float (&op)[16]) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) op[k] = acc[k];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        permlane_swap32(op[t], op[8 + t]);
+        permlane_swap32(op[4 + t], op[12 + t]);
+        permlane_swap16(op[t], op[4 + t]);
+        permlane_swap16(op[8 + t], op[12 + t]);
+    }
+}
+
+// ---- rotors through the representation of Cl(8,0) ------------------------
+// The sandwich y = ~R x R of a Euclidean rotor acts on blade coefficients the
+// same way whatever the algebra's metric (it is the outermorphism of a
+// rotation), so for n = 8 it runs through the real 16 x 16 representation of
+// Cl(8,0): phi(y) = U^T phi(x) U with U = phi(R). Plane k = (p, q) (lex order)
+// has phi(e_p e_q) = sign P(x, z), a signed permutation taking row r to row
+// r ^ x with the factor f(r) = sign (-1)^{popc(z & (r ^ x))}; the table packs
+// x (bits 0-3) and the mask of rows with f(r) = -1 (bits 16-31).
+constexpr int kSpinN = 8;
+constexpr int kSpinPlanes = kSpinN * (kSpinN - 1) / 2;
+struct SpinTable {
+    unsigned plane[kSpinPlanes];
+};
+
+// The Cl(8,0) conversion table and the plane table, built once.
+bool spin_tables(RepTable& T, SpinTable& S);
 
 // ---- host: generators -------------------------------------------------------
 

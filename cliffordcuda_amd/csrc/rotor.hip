@@ -28,7 +28,7 @@
 // The plane list is unrolled at compile time per n.
 #include <utility>
 
-#include "clf_common.h"
+#include "rep_common.h"
 
 namespace clf {
 
@@ -61,7 +61,10 @@ __host__ __device__ constexpr int between_par(unsigned r, int p, int q) {
     for (int b = p + 1; b < q; ++b) c += (r >> b) & 1u;
     return c & 1;
 }
-__host__ __device__ constexpr int state_floats(int n) { return n * n + 2 * n_planes(n); }
+// state: Q (n x n), the (c, s) pairs of the chain, and for n = 8 also the
+// 16 x 16 matrix U = phi(R) of the Cl(8,0) representation (row-major)
+__host__ __device__ constexpr int spin_offset(int n) { return n * n + 2 * n_planes(n); }
+__host__ __device__ constexpr int state_floats(int n) { return spin_offset(n) + (n == kSpinN ? 256 : 0); }
 
 // ---- the plane-rotation chain on register-resident rows ---------------------
 
@@ -453,6 +456,13 @@ __device__ __forceinline__ void givens_cs(double a, double b, double& c, double&
     }
 }
 
+__device__ __forceinline__ double shfl_f64(double v, int src) {
+    const long long bits = __double_as_longlong(v);
+    const int lo = __shfl((int)(bits & 0xffffffffll), src, 64);
+    const int hi = __shfl((int)(bits >> 32), src, 64);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
 // E <- G_k^T E for the planes in lex order (E ends as I), lane j < N holding
 // column j of E; lane 0 writes the (c, s) pairs
 template <int N>
@@ -473,6 +483,78 @@ __device__ __forceinline__ void givens_cols(double (&col)[N], float* __restrict_
             }
         }
     }
+}
+
+// ---- the spin matrix U = phi(R) of Cl(8,0) (n = 8) -------------------------
+// R = exp(B) for the bivector B = sum_m b_m e_{i_m} e_{j_m}, so U = expm(phi(B)),
+// phi(B)[r][r ^ x_m] += f_m(r) b_m (the plane table). U is a 16 x 16 matrix
+// exponential, computed by a second wave of the compile kernel concurrently
+// with the rotation and its plane chain, on the fp64 matrix cores
+// (v_mfma_f64_16x16x4: A[i][k] from lane 16k + i, B[k][j] from lane 16k + j,
+// D[i][j] in register i / 4 of lane 16 (i % 4) + j). A 16 x 16 x 16 product
+// is four of them; chunk c takes k = 4c + g from lane group g, so the B
+// operand of chunk c is register c of the previous product's D layout and a
+// Horner step needs no data movement. Squaring also needs E as the A operand
+// (row i in lane i), through one LDS round trip. Scaling to infinity norm
+// <= 1/4, degree-8 Taylor, squaring.
+typedef double doublex4 __attribute__((ext_vector_type(4)));
+constexpr int kSpinLdsDoubles = 256;
+
+__device__ __forceinline__ doublex4 mfma16_f64(const double (&a)[4], const doublex4& b) {
+    doublex4 acc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a[c], b[c], acc, 0, 0, 0);
+    return acc;
+}
+
+__device__ __forceinline__ void spin_expm(const float* __restrict__ biv, const SpinTable& spin, float* __restrict__ U,
+                                          double* __restrict__ lds, int lane) {
+    const int g = lane >> 4, i = lane & 15;
+    // A operand of Z: za[c] = Z[i][4c + g]
+    double za[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int m = 0; m < kSpinPlanes; ++m) {
+        const unsigned pl = spin.plane[m];
+        const unsigned col = (unsigned)i ^ (pl & 15u);
+        const double b = (double)biv[m];
+        const double fb = ((pl >> (16 + i)) & 1u) ? -b : b;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) za[c] += (col == (unsigned)(4 * c + g)) ? fb : 0.0;
+    }
+    double rs = fabs(za[0]) + fabs(za[1]) + fabs(za[2]) + fabs(za[3]);
+    rs += __shfl_xor(rs, 16, 64);
+    rs += __shfl_xor(rs, 32, 64);
+    double nrm = wave_max_f64(rs);
+    int sq = 0;
+    while (nrm > 0.25 && sq < 60) {
+        nrm *= 0.5;
+        ++sq;
+    }
+    const double scale = ldexp(1.0, -sq);
+    // E in D layout: e[t] = E[4t + g][i]
+    doublex4 e;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) e[t] = (4 * t + g == i) ? 1.0 : 0.0;
+    // E <- I + (scale / k) Z E
+    for (int k = kTaylorDegree; k >= 1; --k) {
+        const doublex4 p = mfma16_f64(za, e);
+        const double f = scale / (double)k;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) e[t] = ((4 * t + g == i) ? 1.0 : 0.0) + f * p[t];
+    }
+    // E <- E E: the A operand E[i][4c + g] through LDS (row-major E)
+    for (int r = 0; r < sq; ++r) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) lds[(4 * t + g) * 16 + i] = e[t];
+        wave_lds_sync();
+        double ea[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) ea[c] = lds[i * 16 + 4 * c + g];
+        wave_lds_sync();
+        e = mfma16_f64(ea, e);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) U[(4 * t + g) * 16 + i] = (float)e[t];
 }
 
 // A = -B, B = 2 (M - M^T) from the lex-ordered bivector: A[i][j] = -2 b, A[j][i] = 2 b
@@ -656,13 +738,6 @@ __global__ __launch_bounds__(64) void rotor_compile_bwd_cols_kernel(const float*
 // Taylor recursion or of squaring is N FMAs per lane instead of N^2 in N lanes.
 // Lanes e >= N^2 compute on row/column 0 and never store.
 
-__device__ __forceinline__ double shfl_f64(double v, int src) {
-    const long long bits = __double_as_longlong(v);
-    const int lo = __shfl((int)(bits & 0xffffffffll), src, 64);
-    const int hi = __shfl((int)(bits >> 32), src, 64);
-    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
-}
-
 // number of halvings that bring the infinity norm to <= 1/4 (rows in registers)
 template <int N>
 __device__ __forceinline__ int halvings(double rowsum) {
@@ -702,10 +777,19 @@ __device__ __forceinline__ double expm_entry(const double (&z)[N], int i, int j)
     return e;
 }
 
+// Wave 0: Q = expm(A) one entry per lane, then the Givens chain. For n = 8 a
+// second wave builds the spin matrix U concurrently (spin_expm).
 template <int N>
-__global__ __launch_bounds__(64) void rotor_compile_fwd_ent_kernel(const float* __restrict__ biv,
-                                                                    float* __restrict__ state) {
+__global__ __launch_bounds__(128) void rotor_compile_fwd_ent_kernel(const float* __restrict__ biv,
+                                                                     float* __restrict__ state, SpinTable spin) {
     static_assert(N * N <= 64, "one entry per lane");
+    if constexpr (N == kSpinN) {
+        __shared__ double spin_lds[kSpinLdsDoubles];
+        if (threadIdx.x >= 64) {  // uniform per wave
+            spin_expm(biv, spin, state + spin_offset(N), spin_lds, (int)threadIdx.x - 64);
+            return;
+        }
+    }
     const int lane = threadIdx.x;
     const bool active = lane < N * N;
     const int i = active ? lane / N : 0, j = active ? lane % N : 0;
@@ -804,9 +888,19 @@ __global__ __launch_bounds__(64) void rotor_compile_bwd_ent_kernel(const float* 
 
 // one entry per lane up to n = 8 (64 entries), one column per lane above
 template <int N>
-static void launch_compile_fwd(const float* biv, float* state, hipStream_t s) {
-    if constexpr (N * N <= 64) hipLaunchKernelGGL((rotor_compile_fwd_ent_kernel<N>), dim3(1), dim3(64), 0, s, biv, state);
-    else hipLaunchKernelGGL((rotor_compile_fwd_cols_kernel<N>), dim3(1), dim3(64), 0, s, biv, state);
+static int launch_compile_fwd(const float* biv, float* state, hipStream_t s) {
+    if constexpr (N * N <= 64) {
+        SpinTable spin{};
+        if constexpr (N == kSpinN) {
+            RepTable T;
+            if (!spin_tables(T, spin)) return set_error(CLF_ERR_UNSUPPORTED, "Cl(8,0) representation tables unavailable");
+        }
+        hipLaunchKernelGGL((rotor_compile_fwd_ent_kernel<N>), dim3(1), dim3(N == kSpinN ? 128 : 64), 0, s, biv, state,
+                           spin);
+    } else {
+        hipLaunchKernelGGL((rotor_compile_fwd_cols_kernel<N>), dim3(1), dim3(64), 0, s, biv, state);
+    }
+    return CLF_OK;
 }
 
 template <int N>
@@ -843,9 +937,11 @@ int rotor_compile_fwd(int n, const float* biv, float* state, void* stream) {
     if (int rc = check_rotor_n(n)) return rc;
     if (!biv || !state) return set_error(CLF_ERR_ARG, "null pointer argument");
     hipStream_t s = (hipStream_t)stream;
-#define CLF_CALL(N) launch_compile_fwd<N>(biv, state, s)
+    int rc = CLF_OK;
+#define CLF_CALL(N) rc = launch_compile_fwd<N>(biv, state, s)
     CLF_ROTOR_DISPATCH(n, CLF_CALL)
 #undef CLF_CALL
+    if (rc) return rc;
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }
@@ -890,6 +986,12 @@ static void launch_apply_bwd(const float* state, const float* x, const float* gy
 }
 
 
+bool rotor16_enabled(int n);
+int rotor16_apply(bool fwd, const float* U, const float* x, float* y, int64_t batch, void* stream);
+int rotor16_bwd(const float* U, const float* x, const float* gy, float* gx, float* gamma_ws, int64_t batch,
+                unsigned grid, void* stream);
+unsigned rotor16_bwd_grid(long long wanted);
+
 int rotor_apply_fwd(int n, const float* state, const float* x, float* y, int64_t batch, void* stream) {
     if (int rc = check_rotor_n(n)) return rc;
     if (batch < 0) return set_error(CLF_ERR_ARG, "batch must be >= 0");
@@ -897,6 +999,7 @@ int rotor_apply_fwd(int n, const float* state, const float* x, float* y, int64_t
     if (!state || !x || !y) return set_error(CLF_ERR_ARG, "null pointer argument");
     if (x == y) return set_error(CLF_ERR_ARG, "output must not alias the input");
     if ((((uintptr_t)x) | ((uintptr_t)y)) & 15u) return set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
+    if (rotor16_enabled(n)) return rotor16_apply(true, state + spin_offset(n), x, y, batch, stream);
     hipStream_t s = (hipStream_t)stream;
 #define CLF_CALL(N) launch_apply<N>(true, state, x, y, batch, s)
     CLF_ROTOR_DISPATCH(n, CLF_CALL)
@@ -919,25 +1022,28 @@ int rotor_apply_bwd(int n, const float* state, const float* x, const float* gy, 
         return set_error(CLF_ERR_WORKSPACE, "workspace of at least " + std::to_string(need) + " bytes required");
     hipStream_t s = (hipStream_t)stream;
     float* gws = g_state ? (float*)ws : nullptr;
+    const bool mat = rotor16_enabled(n);
+    int nparts = 0;
     if (batch > 0) {
         if (!g_state) {
+            if (mat) return rotor16_apply(false, state + spin_offset(n), gy, gx, batch, stream);
 #define CLF_CALL(N) launch_apply<N>(false, state, gy, gx, batch, s)
             CLF_ROTOR_DISPATCH(n, CLF_CALL)
 #undef CLF_CALL
+        } else if (mat) {
+            nparts = (int)rotor16_bwd_grid(rotor_bwd_grid(n, batch));
+            if (int rc = rotor16_bwd(state + spin_offset(n), x, gy, gx, gws, batch, (unsigned)nparts, stream)) return rc;
         } else {
 #define CLF_CALL(N) launch_apply_bwd<N>(state, x, gy, gx, gws, batch, s)
+            CLF_ROTOR_DISPATCH(n, CLF_CALL)
+#undef CLF_CALL
+#define CLF_CALL(N) nparts = (int)bwd_launch_grid<N>(batch)
             CLF_ROTOR_DISPATCH(n, CLF_CALL)
 #undef CLF_CALL
         }
         CLF_HIP_CHECK(hipGetLastError());
     }
     if (g_state) {
-        int nparts = 0;
-        if (batch > 0) {
-#define CLF_CALL(N) nparts = (int)bwd_launch_grid<N>(batch)
-            CLF_ROTOR_DISPATCH(n, CLF_CALL)
-#undef CLF_CALL
-        }
         hipLaunchKernelGGL(rotor_gamma_finalize_kernel, dim3(1), dim3(1024), 0, s, n, state, gws, nparts, g_state);
         CLF_HIP_CHECK(hipGetLastError());
     }

@@ -17,12 +17,13 @@ from . import _lib, _ops
 
 
 def _state_len(n: int) -> int:
-    """Floats of the rotor state: the n x n rotation and the (c, s) pairs of its
-    C(n, 2) plane rotations (``clf_rotor_state_floats``, computed here without
+    """Floats of the rotor state: the n x n rotation, the (c, s) pairs of its
+    C(n, 2) plane rotations and, for n = 8, the 16 x 16 spin matrix of the
+    Cl(8,0) representation (``clf_rotor_state_floats``, computed here without
     a library call so that traced graphs stay free of host calls)."""
     if not 2 <= n <= 10:
         raise ValueError(f"rotor kernels support 2 <= n <= 10; got n={n}")
-    return n * n + n * (n - 1)
+    return n * n + n * (n - 1) + (256 if n == 8 else 0)
 
 
 def _compile_fwd(biv: torch.Tensor, n: int) -> torch.Tensor:

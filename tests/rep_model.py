@@ -316,3 +316,180 @@ def degenerate10_bwd(L, R, G, label, sign):
     gR0 = pair_sum([(L0, G0, True, False, False, False), (L1, G1, True, False, True, True)], label, sign)
     gR1 = pair_sum([(L0, G1, True, False, False, False)], label, sign)
     return np.concatenate([gL0, gL1], axis=-1), np.concatenate([gR0, gR1], axis=-1)
+
+
+# ---- rotor sandwich through the Cl(8,0) representation (csrc/rotor_rep.hip) ----
+
+def permlane_transpose(acc):
+    """transpose_blocks: for each t, v_permlane32_swap of registers (t, 8 + t)
+    and (4 + t, 12 + t) (upper 32 lanes of the first with lower 32 of the
+    second), then v_permlane16_swap of (t, 4 + t) and (8 + t, 12 + t) (odd
+    16-lane rows of the first with even rows of the second)."""
+    op = acc.copy()
+
+    def swap32(a, b):
+        tmp = op[32:, a].copy()
+        op[32:, a] = op[:32, b]
+        op[:32, b] = tmp
+
+    def swap16(a, b):
+        for r in (0, 2):
+            hi, lo = slice(16 * (r + 1), 16 * (r + 2)), slice(16 * r, 16 * (r + 1))
+            tmp = op[hi, a].copy()
+            op[hi, a] = op[lo, b]
+            op[lo, b] = tmp
+
+    for t in range(4):
+        swap32(t, 8 + t)
+        swap32(4 + t, 12 + t)
+        swap16(t, 4 + t)
+        swap16(8 + t, 12 + t)
+    return op.reshape(4, 16, 16)      # [b][j][k]: B operand of the next product
+
+
+def spin_planes(label, sign, n=8):
+    """Per lex plane (p, q): (x, z, sign) with phi(e_p e_q) = sign P(x, z)."""
+    out = []
+    for p in range(n):
+        for q in range(p + 1, n):
+            I = (1 << p) | (1 << q)
+            x, z = label[I]
+            out.append((x, z, sign[I]))
+    return out
+
+
+def spin_matrix(cs, planes):
+    """U = U_C ... U_1, U_k = cos(t/2) I + sin(t/2) phi(e_p e_q) for the chain's
+    (c, s) = (cos t, sin t), as the compile kernel builds it row by row."""
+    U = np.eye(16)
+    for (p, q, c, s), (x, z, sg) in zip(cs, planes):
+        if c >= 0:
+            ch = np.sqrt(0.5 * (1 + c))
+            sh = s / (2 * ch)
+        else:
+            sh = np.sqrt(0.5 * (1 - c)) * (-1 if s < 0 else 1)
+            ch = s / (2 * sh)
+        V = ch * U
+        for r in range(16):
+            rx = r ^ x
+            f = sg * (-1 if popc(z & rx) & 1 else 1)
+            V[r] += sh * f * U[rx]
+        U = V
+    return U
+
+
+def rotor16_fwd(x, U, label, sign, transpose=False):
+    """rotor16_apply_kernel: phi(y) = V^T phi(x) V, V = U (or U^T)."""
+    V = U.T if transpose else U
+    opV = np.broadcast_to(V.T, (4, 16, 16))     # lane x, register k: V[k][x]
+    p = mfma_4block_16x16x1(xor_operand(lane_W(x, label, sign)), opV)
+    acc = mfma_4block_16x16x1(opV, permlane_transpose(p))
+    return lane_unconvert(relayout(acc), label, sign)
+
+
+def rotor16_bwd(x, gy, U, label, sign, planes):
+    """rotor16_bwd_kernel for one group of four rows: gx and the per-plane K."""
+    st = [s * u for s, u in zip(sign, transpose_signs(label))]
+    opU = np.broadcast_to(U, (4, 16, 16))       # lane x, register k: U[x][k]
+    p = mfma_4block_16x16x1(xor_operand(lane_W(gy, label, sign)), opU)
+    g = mfma_4block_16x16x1(opU, permlane_transpose(p))
+    accm = mfma_4block_16x16x1(xor_operand(lane_W(x, label, st)), permlane_transpose(g))
+    wgx = relayout(g)
+    accm = accm + mfma_4block_16x16x1(xor_operand(lane_W(x, label, sign)), xor_operand(wgx))
+    gx = lane_unconvert(wgx, label, sign)
+    Mm = np.zeros((16, 16))
+    for l in range(64):
+        gq, j = l // 16, l % 16
+        for t in range(4):
+            Mm[4 * gq + t, j] = sum(accm[l, 4 * b + t] for b in range(4))
+    K = []
+    for (px, pz, sg) in planes:
+        tot = sum(Mm[r, r ^ px] * (-1 if popc(pz & (r ^ px)) & 1 else 1) for r in range(16))
+        K.append(-sg * tot / 32.0)
+    return gx, np.array(K)
+
+
+def spin_matrix_expm(biv, label, sign, n=8):
+    """U = expm(phi(B)), B = sum_m b_m e_{i_m} e_{j_m} in lex order: the spin
+    matrix as the compile kernel's second wave computes it (equal to the
+    chain's spin_matrix up to an overall sign, which the sandwich ignores)."""
+    import scipy.linalg
+    B = np.zeros(1 << n)
+    m = 0
+    for i in range(n):
+        for j in range(i + 1, n):
+            B[(1 << i) | (1 << j)] = biv[m]
+            m += 1
+    return scipy.linalg.expm(to_matrix(B, label, sign, 1 << (n // 2)))
+
+
+def spin_plane_masks(planes):
+    """The kernel's plane table: (x, mask) with bit r of mask set where
+    f(r) = sign (-1)^{popc(z & (r ^ x))} is -1."""
+    out = []
+    for x, z, sg in planes:
+        mask = 0
+        for r in range(16):
+            if sg * (-1 if popc(z & (r ^ x)) & 1 else 1) < 0:
+                mask |= 1 << r
+        out.append((x, mask))
+    return out
+
+
+def mfma_f64_16x16x4(a_lanes, b_lanes):
+    """v_mfma_f64_16x16x4: A[i][k] from lane 16k + i, B[k][j] from lane 16k + j;
+    returns D[i][j] as d[lane, reg] with lane 16 (i % 4) + j, reg i // 4 (as
+    measured on gfx950)."""
+    A = np.array([[a_lanes[16 * k + i] for k in range(4)] for i in range(16)])
+    Bm = np.array([[b_lanes[16 * k + j] for j in range(16)] for k in range(4)])
+    D = A @ Bm
+    d = np.zeros((64, 4))
+    for i in range(16):
+        for j in range(16):
+            d[16 * (i % 4) + j, i // 4] = D[i, j]
+    return d
+
+
+def spin_expm_lanes(biv, masks, degree=8):
+    """Lane model of the compile kernel's spin wave: Z's A operand, Horner steps
+    on the D layout, squaring with the A operand from a row-major copy."""
+    lanes = range(64)
+    za = np.zeros((64, 4))
+    for l in lanes:
+        g, i = l >> 4, l & 15
+        for m, (x, mask) in enumerate(masks):
+            col = i ^ x
+            fb = -biv[m] if (mask >> i) & 1 else biv[m]
+            for c in range(4):
+                if col == 4 * c + g:
+                    za[l, c] += fb
+    rs = np.abs(za).sum(1)
+    rowsum = np.array([rs[i] + rs[16 + i] + rs[32 + i] + rs[48 + i] for i in range(16)])
+    nrm, sq = rowsum.max(), 0
+    while nrm > 0.25 and sq < 60:
+        nrm *= 0.5
+        sq += 1
+    scale = 2.0 ** -sq
+    eye = np.array([[1.0 if 4 * t + (l >> 4) == (l & 15) else 0.0 for t in range(4)] for l in lanes])
+
+    def prod(a_op, e):
+        acc = np.zeros((64, 4))
+        for c in range(4):
+            acc += mfma_f64_16x16x4(a_op[:, c], e[:, c])
+        return acc
+
+    e = eye.copy()
+    for k in range(degree, 0, -1):
+        e = eye + (scale / k) * prod(za, e)
+    for _ in range(sq):
+        E = np.zeros((16, 16))
+        for l in lanes:
+            for t in range(4):
+                E[4 * t + (l >> 4), l & 15] = e[l, t]
+        ea = np.array([[E[l & 15, 4 * c + (l >> 4)] for c in range(4)] for l in lanes])
+        e = prod(ea, e)
+    U = np.zeros((16, 16))
+    for l in lanes:
+        for t in range(4):
+            U[4 * t + (l >> 4), l & 15] = e[l, t]
+    return U

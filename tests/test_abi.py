@@ -36,6 +36,16 @@ def test_abi_version_and_limits():
     assert lib.clf_product_max_n() >= 10
 
 
+def test_rotor_state_length_matches_python():
+    """The traced-graph state length (computed in Python) equals the library's."""
+    from cliffordcuda_amd.rotor import _state_len
+    lib = _lib.load()
+    for n in range(2, 11):
+        assert lib.clf_rotor_state_floats(n) == _state_len(n), n
+    assert lib.clf_rotor_state_floats(8) == 64 + 56 + 256
+    assert lib.clf_rotor_state_floats(11) == -1
+
+
 @pytest.mark.parametrize("args,code,msg", [
     ((9, 5, 0, 0, None, None, None, 4, None), 1, "unknown product op"),
     ((0, 0, 0, 0, None, None, None, 4, None), 1, "n must be in"),

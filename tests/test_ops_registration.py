@@ -30,5 +30,5 @@ def test_fake_shapes():
         gx, gw = ops.bcast_product_bwd(a, w, a, 0, 0, 8, 0, 0, True, True)
         assert gx.shape == (5, 256) and gw.shape == (1, 256)
         state = ops.rotor_compile(biv, 8)
-        assert state.shape == (8 * 8 + 8 * 7,)
+        assert state.shape == (8 * 8 + 8 * 7 + 256,)
         assert ops.rotor_apply(state, a, 8).shape == (5, 256)

@@ -56,3 +56,51 @@ def test_skew_sums_over_output_conjugate():
     xq = torch.tensor(x).requires_grad_()
     O.apply_bivector(bq, xq, n).backward(torch.tensor(gy))
     np.testing.assert_allclose(M.compile_bwd(biv, n, Ky @ Q), bq.grad[0].numpy(), atol=1e-10)
+
+
+def test_rotor16_lane_model_matches_oracle():
+    """n = 8 through the Cl(8,0) representation (csrc/rotor_rep.hip): the
+    spin matrix built from the chain's half angles, the block transpose by
+    permlane swaps between the two products, and the per-plane sums contracted
+    from the 16 x 16 accumulator give the oracle's sandwich, x gradient and
+    bivector gradient."""
+    from tests import rep_model as R
+    n = 8
+    gens = R.find_generators([1] * 8)
+    label, sign = R.blade_tables([1] * 8, gens)
+    planes = R.spin_planes(label, sign)
+    g = torch.Generator().manual_seed(5)
+    # angles past pi/2 exercise the c < 0 half-angle branch
+    biv = 0.9 * torch.randn(1, 28, generator=g, dtype=torch.float64)
+    x = torch.randn(4, 256, generator=g, dtype=torch.float64)
+    gy = torch.randn(4, 256, generator=g, dtype=torch.float64)
+    bq = biv.clone().requires_grad_()
+    xq = x.clone().requires_grad_()
+    y = O.apply_bivector(bq, xq, n)
+    y.backward(gy)
+    Q = scipy.linalg.expm(M.generator(biv[0].numpy(), n))
+    cs, _ = M.givens(Q)
+    assert min(c for _, _, c, _ in cs) < 0
+    U = R.spin_matrix(cs, planes)
+    np.testing.assert_allclose(U @ U.T, np.eye(16), atol=1e-12)
+    # the kernel builds U as expm(phi(B)): the same matrix up to sign
+    Ue = R.spin_matrix_expm(biv[0].numpy(), label, sign)
+    assert min(np.abs(Ue - U).max(), np.abs(Ue + U).max()) < 1e-10
+    # lane model of the kernel's fp64-MFMA exponential
+    Ul = R.spin_expm_lanes(biv[0].numpy(), R.spin_plane_masks(planes))
+    np.testing.assert_allclose(Ul, Ue, atol=1e-12)
+    U = Ul
+    np.testing.assert_allclose(R.rotor16_fwd(x.numpy(), U, label, sign), y.detach().numpy(), atol=1e-10)
+    np.testing.assert_allclose(R.rotor16_fwd(gy.numpy(), U, label, sign, transpose=True), xq.grad.numpy(),
+                               atol=1e-10)
+    gx, K = R.rotor16_bwd(x.numpy(), gy.numpy(), U, label, sign, planes)
+    np.testing.assert_allclose(gx, xq.grad.numpy(), atol=1e-10)
+    # K_pq = Gamma_pq - Gamma_qp, and dL/dQ = Q skew(Gamma) carries the bivector gradient
+    G = M.gamma(x.numpy(), gx, n)
+    iu = np.triu_indices(n, 1)
+    np.testing.assert_allclose(K, (G - G.T)[iu], atol=1e-9)
+    S = np.zeros((n, n))
+    S[iu] = 0.5 * K
+    S = S - S.T
+    gb = M.compile_bwd(biv[0].numpy(), n, Q @ S)
+    np.testing.assert_allclose(gb, bq.grad[0].numpy(), atol=1e-9)
