@@ -131,7 +131,9 @@ int clf_norm_sq_bwd(int n, uint32_t neg_mask, uint32_t null_mask,
  *
  * Rotor state layout (clf_rotor_state_floats(n) floats): the n x n rotation
  * Q = expm(-2 (M - M^T)) acting on grade-1 coefficients (row-major), followed by
- * the C(n,2) (c, s) pairs of its plane-rotation factorisation. */
+ * the C(n,2) (c, s) pairs of its plane-rotation factorisation and, for n = 8,
+ * the 16 x 16 matrix U = phi(R) of the rotor in the real representation of
+ * Cl(8,0) (row-major), which the n = 8 sandwich kernels use (phi(y) = U^T phi(x) U). */
 
 /* Number of floats of the rotor state for n, or -1 if n is unsupported. */
 int clf_rotor_state_floats(int n);
@@ -140,7 +142,7 @@ int clf_rotor_state_floats(int n);
 int clf_rotor_compile_fwd(int n, const float* biv, float* state, void* stream);
 
 /* g_biv = d/d(biv) of <g_state, compile(biv)>, reading only the Q block of
- * g_state (the chain block is a derived cache and carries no gradient). */
+ * g_state (the chain and spin blocks are derived caches and carry no gradient). */
 int clf_rotor_compile_bwd(int n, const float* biv, const float* g_state, float* g_biv, void* stream);
 
 /* y = ~R x R for `batch` rows. y must not alias x. */
@@ -153,7 +155,7 @@ size_t clf_rotor_apply_ws_bytes(int n, int64_t batch);
 /* Backward of the sandwich: gx = R gy ~R (the transpose of the action),
  * g_state = dL/d(state): the Q block holds the component of dL/dQ tangent to
  * SO(n) (Q skew(Gamma), which is all clf_rotor_compile_bwd needs), the chain
- * block is 0. gx or g_state may be
+ * and spin blocks are 0. gx or g_state may be
  * NULL. x is read only when g_state != NULL. The reference returns no gradient
  * to x (extensions/rotor/givens_apply/mb_perm_packed.py:34-42). */
 int clf_rotor_apply_bwd(int n, const float* state, const float* x, const float* gy,
