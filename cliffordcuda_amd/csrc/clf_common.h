@@ -27,6 +27,14 @@ void clear_error();
 // from the runtime occupancy query, cached per (device, kernel, dynamic LDS).
 unsigned resident_grid(const void* kernel, int block_threads, size_t dyn_lds, long long wanted);
 
+// Orders a wave's LDS accesses (writes by some lanes, reads by others) for the
+// compiler; the hardware executes one wave's LDS instructions in order.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 #define CLF_HIP_CHECK(expr)                                                       \
     do {                                                                          \
         hipError_t _e = (expr);                                                   \

@@ -414,6 +414,370 @@ __global__ __launch_bounds__(256) void prod_bwd_blk(const float* __restrict__ A,
     }
 }
 
+// ---- balanced persistent kernels (4 <= n <= 10) -----------------------------
+// For the masked products the work of an output block varies by up to 2^nh
+// (wedge: 2^|kh| partner blocks, lc: 2^(nh - |kh|), ...), so one lane per
+// output block leaves most lanes idle while the busiest one runs. Here the
+// valid (output, partner) block pairs of a row, ordered by output block, are
+// dealt out to the row's NB lanes in equal contiguous ranges of
+// T = ceil(total / NB) pairs. A lane closes a segment when its output's pairs
+// or its own range end: a segment that began in an earlier lane (a "head") is
+// written to LDS, one that began and ended here is stored, and a last segment
+// that continues in later lanes (a "tail") gets the later lanes' heads added
+// after the loop, in lane order (deterministic sums).
+// ROLE 0: output kh, partner ih (jh = ih ^ kh); ROLE 1: output ih (gradient
+// of the left operand), partner jh; ROLE 2: output jh, partner ih. Partners
+// of an output are one or two families {base | S : S subset of mask},
+// enumerated with S <- (S - mask) & mask.
+// Layout: a wave owns groups of 1024 floats per operand (R = 1024 / D rows,
+// NB lanes per row) in wave-private LDS and walks the groups with a grid
+// stride, loading the next group into registers while it computes.
+constexpr int kBalMinN = 4, kBalMaxN = 10;
+constexpr int kBalGroupF4 = 256;  // float4 per operand per group
+
+template <int OP, int ROLE>
+__device__ __forceinline__ void bal_families(unsigned o, unsigned full, unsigned& b0, unsigned& m0, unsigned& b1,
+                                             unsigned& m1, int& c1) {
+    const unsigned co = ~o & full;
+    b1 = 0u;
+    m1 = 0u;
+    c1 = 0;
+    if (OP == OP_GEOM) {
+        b0 = 0u;
+        m0 = full;
+    } else if (OP == OP_WEDGE) {
+        b0 = 0u;
+        m0 = ROLE == 0 ? o : co;
+    } else if (OP == OP_LC) {
+        b0 = ROLE == 1 ? o : 0u;
+        m0 = ROLE == 2 ? o : co;
+    } else if (OP == OP_RC) {
+        b0 = ROLE == 1 ? 0u : o;
+        m0 = ROLE == 1 ? o : co;
+    } else if (OP == OP_INNER) {
+        if (ROLE == 0) {  // ih disjoint from kh, or ih containing kh (the same set when kh = 0)
+            b0 = 0u;
+            m0 = co;
+            b1 = o;
+            m1 = co;
+            c1 = o ? (1 << __popc(co)) : 0;
+        } else {  // partners containing o, then those inside o except o itself
+            b0 = o;
+            m0 = co;
+            b1 = 0u;
+            m1 = o;
+            c1 = (1 << __popc(o)) - 1;
+        }
+    } else {  // regressive: ih | jh = full
+        b0 = co;
+        m0 = o;
+    }
+}
+
+template <int OP, int ROLE>
+__device__ __forceinline__ int bal_count(unsigned o, unsigned full) {
+    unsigned b0, m0, b1, m1;
+    int c1;
+    bal_families<OP, ROLE>(o, full, b0, m0, b1, m1, c1);
+    return (1 << __popc(m0)) + c1;
+}
+
+// the s-th subset of m in increasing order (bits of s deposited on the bits of m)
+__device__ __forceinline__ unsigned deposit_bits(unsigned s, unsigned m) {
+    unsigned r = 0u;
+    for (unsigned bit = 1u; m != 0u; bit <<= 1) {
+        const unsigned low = m & (0u - m);
+        if (s & bit) r |= low;
+        m ^= low;
+    }
+    return r;
+}
+
+struct BalSched {
+    int T;            // pairs per lane (the loop trip count, uniform)
+    int p0, p1;       // this lane's pair range [p0, p1)
+    unsigned o0;      // output of pair p0
+    int s0;           // index of p0 inside o0
+    bool cont0;       // o0 began in an earlier lane
+    bool tail;        // the last segment continues in later lanes
+    unsigned olast;   // output of the last segment
+    int last_lane;    // last lane holding pairs of olast
+};
+
+template <int OP, int ROLE>
+__device__ __forceinline__ BalSched bal_schedule(unsigned lr, unsigned NB) {
+    const unsigned full = NB - 1u;
+    int total = 0;
+    for (unsigned o = 0; o < NB; ++o) total += bal_count<OP, ROLE>(o, full);
+    BalSched sc;
+    sc.T = (total + (int)NB - 1) / (int)NB;
+    sc.p0 = (int)lr * sc.T;
+    sc.p1 = sc.p0 + sc.T < total ? sc.p0 + sc.T : total;
+    if (sc.p1 < sc.p0) sc.p1 = sc.p0;
+    sc.o0 = 0u;
+    sc.s0 = 0;
+    sc.olast = 0u;
+    int pre = 0, last_end = 0;
+    for (unsigned o = 0; o < NB; ++o) {
+        const int c = bal_count<OP, ROLE>(o, full);
+        if (sc.p0 >= pre && sc.p0 < pre + c) {
+            sc.o0 = o;
+            sc.s0 = sc.p0 - pre;
+        }
+        if (sc.p1 - 1 >= pre && sc.p1 - 1 < pre + c) {
+            sc.olast = o;
+            last_end = pre + c;
+        }
+        pre += c;
+    }
+    sc.cont0 = sc.s0 > 0;
+    sc.tail = sc.p1 > sc.p0 && sc.p1 < last_end && !(sc.olast == sc.o0 && sc.cont0);
+    sc.last_lane = sc.T > 0 ? (last_end - 1) / sc.T : 0;
+    return sc;
+}
+
+__device__ __forceinline__ void store_blk(float4* __restrict__ out, unsigned blk, const float (&acc)[16], bool rev) {
+    if (rev) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            out[(blk << 2) + (3 - q)] = make_float4(acc[4 * q + 3], acc[4 * q + 2], acc[4 * q + 1], acc[4 * q]);
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            out[(blk << 2) + q] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+    }
+}
+
+// One role over one row: la / lb / lg are the row's staged operands, heads the
+// row's head slots (4 float4 per lane), out the row's output (nullptr for a
+// row past the end of the batch: computed, not stored). The caller syncs the
+// wave's LDS before (staged data) and after (heads reused).
+template <int OP, int ROLE, bool LOWNEG>
+__device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __restrict__ la,
+                                         const float4* __restrict__ lb, const float4* __restrict__ lg,
+                                         float4* __restrict__ heads, unsigned lr, float4* __restrict__ out,
+                                         unsigned NB, const BlkParams& P) {
+    const unsigned full = NB - 1u;
+    constexpr bool kRev = OP == OP_REGR && ROLE == 0;
+    float acc[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+    unsigned o = sc.o0;
+    unsigned b0, m0, b1, m1;
+    int c1;
+    bal_families<OP, ROLE>(o, full, b0, m0, b1, m1, c1);
+    int c0 = 1 << __popc(m0);
+    int s = sc.s0;
+    bool fam1 = s >= c0;
+    unsigned S = fam1 ? deposit_bits((unsigned)(s - c0), m1) : deposit_bits((unsigned)s, m0);
+    bool first = true;
+    int p = sc.p0;
+    for (int t = 0; t < sc.T; ++t) {
+        if (p >= sc.p1) break;
+        const unsigned part = (fam1 ? b1 : b0) | S;
+        if (ROLE == 0) {
+            const unsigned ih = part, jh = part ^ o;
+            const HiSign hs = hi_sign<OP>(ih, jh, P.negh, P.nulh, full, P.nm1, P.mu);
+            if (hs.valid) {
+                float av[16], bv[16];
+                load_blk(la, ih, av);
+                load_blk(lb, jh, bv);
+                apply_flips(bv, hs.mask, hs.mask ^ (cross_pi<OP>(ih, P.nm1) << 31));
+                fwd_block_dispatch<OP, LOWNEG>(acc, av, bv, ih, jh);
+            }
+        } else {
+            const unsigned h = o, m = part, x = h ^ m;
+            const HiSign hs = ROLE == 1 ? hi_sign<OP>(h, m, P.negh, P.nulh, full, P.nm1, P.mu)
+                                        : hi_sign<OP>(m, h, P.negh, P.nulh, full, P.nm1, P.mu);
+            if (hs.valid) {
+                float g[16];
+                if (OP == OP_REGR) load_blk_rev(lg, full ^ x, g);
+                else load_blk(lg, x, g);
+                if (ROLE == 1) {
+                    float bv[16];
+                    load_blk(lb, m, bv);
+                    apply_flips(bv, hs.mask, hs.mask ^ (cross_pi<OP>(h, P.nm1) << 31));
+                    ga_block_dispatch<OP, LOWNEG>(acc, bv, g, h, m);
+                } else {
+                    const unsigned pm = cross_pi<OP>(m, P.nm1) << 31;
+                    float av[16], gt[16];
+                    load_blk(la, m, av);
+                    apply_flips(av, hs.mask, hs.mask ^ pm);
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) gt[e] = (cpopc((unsigned)e) & 1) ? flip(g[e], pm) : g[e];
+                    gb_block_dispatch<OP, LOWNEG>(acc, av, gt, m, h);
+                }
+            }
+        }
+        ++p;
+        ++s;
+        const unsigned mm = fam1 ? m1 : m0;
+        S = (S - mm) & mm;
+        if (!fam1 && s == c0 && c1 > 0) {
+            fam1 = true;
+            S = 0u;
+        }
+        const bool done = s == c0 + c1;
+        if (done || p == sc.p1) {
+            if (first && sc.cont0) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    heads[lr * 4 + q] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+            } else if (done && out) {
+                store_blk(out, kRev ? (full ^ o) : o, acc, kRev);
+            }
+            if (done) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+                first = false;
+                ++o;
+                if (o < NB) {
+                    bal_families<OP, ROLE>(o, full, b0, m0, b1, m1, c1);
+                    c0 = 1 << __popc(m0);
+                }
+                s = 0;
+                fam1 = false;
+                S = 0u;
+            }
+        }
+    }
+    wave_lds_sync();
+    if (sc.tail) {
+        for (int l = (int)lr + 1; l <= sc.last_lane; ++l) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 v = heads[l * 4 + q];
+                acc[4 * q] += v.x;
+                acc[4 * q + 1] += v.y;
+                acc[4 * q + 2] += v.z;
+                acc[4 * q + 3] += v.w;
+            }
+        }
+        if (out) store_blk(out, kRev ? (full ^ sc.olast) : sc.olast, acc, kRev);
+    }
+}
+
+// A group's operand: float4 chunk lane + 64 i (i < 4) of R consecutive rows,
+// rows past the end clamped to the last row.
+struct BalPre {
+    float4 v[4];
+};
+
+__device__ __forceinline__ BalPre bal_fetch(const float* __restrict__ src, long long grp, long long batch, int n,
+                                            int lane) {
+    BalPre p;
+    const int d4_log = n - 2;
+    const long long last = (batch << d4_log) - (1LL << d4_log);  // first chunk of the last row
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        long long c = grp * kBalGroupF4 + lane + 64 * i;
+        if (c >= (batch << d4_log)) c = last + (c & ((1LL << d4_log) - 1));
+        p.v[i] = reinterpret_cast<const float4*>(src)[c];
+    }
+    return p;
+}
+
+// staged like stage_rows: row r at r * D4, float4 slots swizzled inside a block
+__device__ __forceinline__ void bal_stage(float4* __restrict__ dst, const BalPre& p, int n, int lane) {
+    const int d4_log = n - 2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = lane + 64 * i;
+        const int r = c >> d4_log;
+        const unsigned f = (unsigned)c & ((1u << d4_log) - 1u);
+        const unsigned blk = f >> 2, q = f & 3u;
+        dst[(r << d4_log) + (int)((blk << 2) + (q ^ swz(blk)))] = p.v[i];
+    }
+}
+
+template <int OP, bool LOWNEG>
+__global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A, const float* __restrict__ B,
+                                                     float* __restrict__ C, BlkParams P) {
+    __shared__ float4 lds[4][3 * kBalGroupF4];  // per wave: a | b | heads
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n = P.n;
+    const int lpr_log = n - 4;
+    const unsigned NB = 1u << lpr_log;
+    const unsigned lr = (unsigned)lane & (NB - 1u);
+    const int r = lane >> lpr_log;
+    const int R = 64 >> lpr_log;
+    float4* sa = lds[wave];
+    float4* sb = sa + kBalGroupF4;
+    float4* heads = sb + kBalGroupF4 + (r << lpr_log) * 4;
+    const int roff = r << (n - 2);
+    const BalSched sc = bal_schedule<OP, 0>(lr, NB);
+    const long long ngrp = (P.batch + R - 1) / R;
+    const long long gstride = (long long)gridDim.x * 4;
+    long long grp = (long long)blockIdx.x * 4 + wave;
+    BalPre pa = bal_fetch(A, grp, P.batch, n, lane);
+    BalPre pb = bal_fetch(B, grp, P.batch, n, lane);
+    for (; grp < ngrp; grp += gstride) {
+        bal_stage(sa, pa, n, lane);
+        bal_stage(sb, pb, n, lane);
+        pa = bal_fetch(A, grp + gstride, P.batch, n, lane);
+        pb = bal_fetch(B, grp + gstride, P.batch, n, lane);
+        wave_lds_sync();
+        const long long row = grp * R + r;
+        float4* out = row < P.batch ? reinterpret_cast<float4*>(C) + (row << (n - 2)) : nullptr;
+        bal_role<OP, 0, LOWNEG>(sc, sa + roff, sb + roff, nullptr, heads, lr, out, NB, P);
+        wave_lds_sync();
+    }
+}
+
+// Backward: b and gc are staged first and the left-operand gradient runs with
+// its heads in the a slot; then a is staged and the right-operand gradient
+// runs with its heads in the b slot (12 KB of LDS per wave).
+template <int OP, bool LOWNEG>
+__global__ __launch_bounds__(256) void prod_bwd_bal(const float* __restrict__ A, const float* __restrict__ B,
+                                                     const float* __restrict__ GC, float* __restrict__ GA,
+                                                     float* __restrict__ GB, BlkParams P) {
+    __shared__ float4 lds[4][3 * kBalGroupF4];  // per wave: a (ga heads first) | b (gb heads later) | gc
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n = P.n;
+    const int lpr_log = n - 4;
+    const unsigned NB = 1u << lpr_log;
+    const unsigned lr = (unsigned)lane & (NB - 1u);
+    const int r = lane >> lpr_log;
+    const int R = 64 >> lpr_log;
+    float4* sa = lds[wave];
+    float4* sb = sa + kBalGroupF4;
+    float4* sg = sb + kBalGroupF4;
+    const int roff = r << (n - 2);
+    const int hoff = (r << lpr_log) * 4;
+    const bool want_a = GA != nullptr, want_b = GB != nullptr;
+    const BalSched sca = bal_schedule<OP, 1>(lr, NB);
+    const BalSched scb = bal_schedule<OP, 2>(lr, NB);
+    const long long ngrp = (P.batch + R - 1) / R;
+    const long long gstride = (long long)gridDim.x * 4;
+    long long grp = (long long)blockIdx.x * 4 + wave;
+    BalPre pa, pb;
+    if (want_b) pa = bal_fetch(A, grp, P.batch, n, lane);
+    if (want_a) pb = bal_fetch(B, grp, P.batch, n, lane);
+    BalPre pg = bal_fetch(GC, grp, P.batch, n, lane);
+    for (; grp < ngrp; grp += gstride) {
+        const long long row = grp * R + r;
+        const bool row_ok = row < P.batch;
+        bal_stage(sg, pg, n, lane);
+        pg = bal_fetch(GC, grp + gstride, P.batch, n, lane);
+        if (want_a) {  // uniform: a kernel argument
+            bal_stage(sb, pb, n, lane);
+            pb = bal_fetch(B, grp + gstride, P.batch, n, lane);
+            wave_lds_sync();
+            float4* out = row_ok ? reinterpret_cast<float4*>(GA) + (row << (n - 2)) : nullptr;
+            bal_role<OP, 1, LOWNEG>(sca, nullptr, sb + roff, sg + roff, sa + hoff, lr, out, NB, P);
+            wave_lds_sync();
+        }
+        if (want_b) {
+            bal_stage(sa, pa, n, lane);
+            pa = bal_fetch(A, grp + gstride, P.batch, n, lane);
+            wave_lds_sync();
+            float4* out = row_ok ? reinterpret_cast<float4*>(GB) + (row << (n - 2)) : nullptr;
+            bal_role<OP, 2, LOWNEG>(scb, sa + roff, nullptr, sg + roff, sb + hoff, lr, out, NB, P);
+        }
+        wave_lds_sync();
+    }
+}
+
 // ---- tiled path (rows larger than LDS, n >= 12) -----------------------------
 // A workgroup of 256 lanes owns 256 output blocks kh = K0 + lane of one row and
 // walks the input blocks in aligned tiles of 256 (I0 = 256 t). Because both
@@ -698,6 +1062,39 @@ static bool product_path_is(const char* what) {
 static bool tiled_forced() { return product_path_is("tiled"); }
 static bool generic_forced() { return product_path_is("generic"); }
 
+// Balanced kernels: wedge, lc, rc and regressive for 4 <= n <= 10
+// (CLF_PRODUCT_PATH=blocked keeps them on the one-lane-per-output kernels).
+// The geometric product (every output has the same work) and inner (whose
+// pairs need one of three low-block patterns, so lanes at different pairs
+// diverge) use them only when CLF_PRODUCT_PATH=balanced.
+static bool bal_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, bool& lowneg) {
+    if (n < kBalMinN || n > kBalMaxN) return false;
+    const bool opt_in = op == OP_GEOM || op == OP_INNER;
+    if (opt_in ? !product_path_is("balanced") : product_path_is("blocked")) return false;
+    if (!blocked_metric(op, n, neg, nul, lowneg)) return false;
+    block_sign_params(n, neg, nul, P);
+    return true;
+}
+
+static unsigned bal_grid(const void* kernel, const BlkParams& P) {
+    const long long R = 1LL << (10 - P.n);
+    const long long groups = (P.batch + R - 1) / R;
+    return resident_grid(kernel, 256, 0, (groups + 3) / 4);
+}
+
+template <int OP, bool LN>
+static void launch_fwd_bal(hipStream_t s, const float* A, const float* B, float* C, const BlkParams& P) {
+    const dim3 g(bal_grid((const void*)prod_fwd_bal<OP, LN>, P));
+    hipLaunchKernelGGL((prod_fwd_bal<OP, LN>), g, dim3(256), 0, s, A, B, C, P);
+}
+
+template <int OP, bool LN>
+static void launch_bwd_bal(hipStream_t s, const float* A, const float* B, const float* GCp, float* GA, float* GB,
+                           const BlkParams& P) {
+    const dim3 g(bal_grid((const void*)prod_bwd_bal<OP, LN>, P));
+    hipLaunchKernelGGL((prod_bwd_bal<OP, LN>), g, dim3(256), 0, s, A, B, GCp, GA, GB, P);
+}
+
 template <int OP, bool LN>
 static void launch_fwd(dim3 g, dim3 b, size_t lds, hipStream_t s, const float* A, const float* B, float* C,
                        const BlkParams& P) {
@@ -740,7 +1137,22 @@ int product_fwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
     dim3 g, bl;
     size_t lds = 0;
     const bool force_tiled = n >= 12 && tiled_forced(), force_generic = generic_forced();
-    if (!force_generic && !force_tiled && blocked_plan(op, n, neg, nul, 2, P, ln, g, bl, lds)) {
+    if (!force_generic && bal_plan(op, n, neg, nul, P, ln)) {
+#define CLF_FWD_BAL(OPV)                                               \
+    case OPV:                                                          \
+        if (ln) launch_fwd_bal<OPV, true>(s, a, b, c, P);              \
+        else launch_fwd_bal<OPV, false>(s, a, b, c, P);                \
+        break;
+        switch (op) {
+            CLF_FWD_BAL(OP_GEOM)
+            CLF_FWD_BAL(OP_INNER)
+            CLF_FWD_BAL(OP_LC)
+            CLF_FWD_BAL(OP_RC)
+            case OP_WEDGE: launch_fwd_bal<OP_WEDGE, false>(s, a, b, c, P); break;
+            case OP_REGR: launch_fwd_bal<OP_REGR, false>(s, a, b, c, P); break;
+        }
+#undef CLF_FWD_BAL
+    } else if (!force_generic && !force_tiled && blocked_plan(op, n, neg, nul, 2, P, ln, g, bl, lds)) {
 #define CLF_FWD_CASE(OPV)                                              \
     case OPV:                                                          \
         if (ln) launch_fwd<OPV, true>(g, bl, lds, s, a, b, c, P);      \
@@ -794,7 +1206,22 @@ int product_bwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
     dim3 g, bl;
     size_t lds = 0;
     const bool force_tiled = n >= 12 && tiled_forced(), force_generic = generic_forced();
-    if (!force_generic && !force_tiled && blocked_plan(op, n, neg, nul, 3, P, ln, g, bl, lds)) {
+    if (!force_generic && bal_plan(op, n, neg, nul, P, ln)) {
+#define CLF_BWD_BAL(OPV)                                                       \
+    case OPV:                                                                  \
+        if (ln) launch_bwd_bal<OPV, true>(s, a, b, gc, ga, gb, P);             \
+        else launch_bwd_bal<OPV, false>(s, a, b, gc, ga, gb, P);               \
+        break;
+        switch (op) {
+            CLF_BWD_BAL(OP_GEOM)
+            CLF_BWD_BAL(OP_INNER)
+            CLF_BWD_BAL(OP_LC)
+            CLF_BWD_BAL(OP_RC)
+            case OP_WEDGE: launch_bwd_bal<OP_WEDGE, false>(s, a, b, gc, ga, gb, P); break;
+            case OP_REGR: launch_bwd_bal<OP_REGR, false>(s, a, b, gc, ga, gb, P); break;
+        }
+#undef CLF_BWD_BAL
+    } else if (!force_generic && !force_tiled && blocked_plan(op, n, neg, nul, 3, P, ln, g, bl, lds)) {
 #define CLF_BWD_CASE(OPV)                                                      \
     case OPV:                                                                  \
         if (ln) launch_bwd<OPV, true>(g, bl, lds, s, a, b, gc, ga, gb, P);     \

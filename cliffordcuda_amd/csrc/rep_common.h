@@ -14,12 +14,6 @@ namespace clf {
 
 constexpr int kRepMaxLogM = 4;  // m <= 16: the tables fit the kernel arguments
 
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 template <int M>
 __device__ __forceinline__ void wht_inplace(float (&v)[M]) {
 #pragma unroll

@@ -237,3 +237,115 @@ def backward_tiled(op_name, a, b, gc, metric, T):
                         for jl in range(16):
                             GB[:, h, jl] += (tab[il, jl] * at[:, il] * gt[:, il ^ jl]).sum(-1)
     return GA.reshape(a.shape), GB.reshape(a.shape)
+
+
+# ---- balanced kernels (prod_fwd_bal / prod_bwd_bal) -------------------------
+# A row's valid (output block, partner block) pairs, ordered by output block
+# and, inside an output, by the kernel's subset enumeration, are dealt out to
+# the NB lanes of the row in equal contiguous ranges of T = ceil(total / NB).
+# ROLE 0: output kh, partner ih (jh = ih ^ kh); ROLE 1: output ih (ga),
+# partner jh; ROLE 2: output jh (gb), partner ih. A lane closes a segment when
+# its output's pairs end or its range ends: a segment that began in an earlier
+# lane is a "head" (written to LDS), a segment that began here and ends here
+# is stored, and a last segment that continues in later lanes is a "tail",
+# to which its lane adds the heads of the later lanes after the loop.
+
+
+def bal_families(op, role, o, full):
+    """[(base, mask, count)] of partner families for output block o."""
+    co = ~o & full
+    c = lambda m: 1 << popc(m)
+    if op == GEOM:
+        return [(0, full, c(full))]
+    if op == WEDGE:
+        m = o if role == 0 else co
+        return [(0, m, c(m))]
+    if op == LC:
+        return [[(0, co, c(co))], [(o, co, c(co))], [(0, o, c(o))]][role]
+    if op == RC:
+        return [[(o, co, c(co))], [(0, o, c(o))], [(o, co, c(co))]][role]
+    if op == INNER:
+        if role == 0:
+            return [(0, co, c(co))] + ([(o, co, c(co))] if o else [])
+        return [(o, co, c(co)), (0, o, c(o) - 1)]
+    return [(co, o, c(o))]          # regressive
+
+
+def subsets(m):
+    """Subsets of m in the kernel's order: S <- (S - m) & m from 0."""
+    out, S = [], 0
+    for _ in range(1 << popc(m)):
+        out.append(S)
+        S = (S - m) & m
+    return out
+
+
+def bal_partners(op, role, o, full):
+    return [b | S for (b, m, cnt) in bal_families(op, role, o, full) for S in subsets(m)[:cnt]]
+
+
+def bal_block_pair(role, o, part):
+    """(ih, jh) of a pair."""
+    return [(part, part ^ o), (o, part), (part, o)][role]
+
+
+def bal_schedule(op, role, NB):
+    full = NB - 1
+    counts = [len(bal_partners(op, role, o, full)) for o in range(NB)]
+    pre = np.concatenate([[0], np.cumsum(counts)])
+    total = int(pre[-1])
+    T = -(-total // NB)
+    lanes = []
+    for lr in range(NB):
+        p0, p1 = lr * T, min(lr * T + T, total)
+        if p1 <= p0:
+            lanes.append(None)
+            continue
+        o0 = int(np.searchsorted(pre, p0, side="right") - 1)
+        ol = int(np.searchsorted(pre, p1 - 1, side="right") - 1)
+        cont0 = p0 > pre[o0]
+        tail = p1 < pre[ol + 1] and not (ol == o0 and cont0)
+        lanes.append(dict(p0=p0, p1=p1, o0=o0, s0=int(p0 - pre[o0]), cont0=cont0, tail=tail, olast=ol,
+                          last_lane=int((pre[ol + 1] - 1) // T)))
+    return T, lanes, pre
+
+
+def bal_run(op, role, NB, pair_value):
+    """Emulate the lanes of one row: pair_value(o, part) -> contribution (16,)
+    array (zero for pairs the metric kills). Returns out[o] as the kernel
+    stores it (complete segments, then tails + heads)."""
+    full = NB - 1
+    T, lanes, pre = bal_schedule(op, role, NB)
+    out = {}
+    heads = {}
+    tails = {}
+    for lr, sc in enumerate(lanes):
+        if sc is None:
+            continue
+        o, s, first = sc["o0"], sc["s0"], True
+        partners = bal_partners(op, role, o, full)
+        acc = np.zeros(16)
+        for p in range(sc["p0"], sc["p1"]):
+            acc = acc + pair_value(o, partners[s])
+            s += 1
+            done = s == len(partners)
+            if done or p + 1 == sc["p1"]:
+                if first and sc["cont0"]:
+                    heads[lr] = acc
+                elif done:
+                    assert o not in out
+                    out[o] = acc
+                else:
+                    tails[lr] = (o, acc)
+                if done:
+                    acc = np.zeros(16)
+                    o, s, first = o + 1, 0, False
+                    if o < NB:
+                        partners = bal_partners(op, role, o, full)
+    for lr, (o, acc) in tails.items():
+        assert lanes[lr]["tail"] and lanes[lr]["olast"] == o
+        for l2 in range(lr + 1, lanes[lr]["last_lane"] + 1):
+            acc = acc + heads[l2]
+        assert o not in out
+        out[o] = acc
+    return out

@@ -286,3 +286,51 @@ def test_split_path_equals_direct_path_c5_full_batch(monkeypatch):
     monkeypatch.delenv("CLF_GEOM_PATH")
     for u, v in zip(r1, r2):
         assert rel_err(u, v) <= TOL
+
+
+BAL_METRICS = [
+    (1,) * 4,
+    (-1,) * 5,
+    (1,) * 6 + (-1,),           # C2
+    (1,) * 4 + (0, -1, 1, 0),
+    (-1,) * 4 + (1, -1, 1, 1, -1),
+    (1,) * 9 + (0,),            # C5
+]
+
+
+def _grads(op, a, b, gc, metric, need_a=True, need_b=True):
+    ad = a.clone().requires_grad_(need_a)
+    bd = b.clone().requires_grad_(need_b)
+    c = cc.products.product(op, ad, bd, metric)
+    c.backward(gc)
+    return c.detach(), (ad.grad if need_a else None), (bd.grad if need_b else None)
+
+
+@pytest.mark.parametrize("metric", BAL_METRICS, ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
+@pytest.mark.parametrize("op", O.OPS)
+def test_balanced_kernels_match_blocked_and_oracle(op, metric, monkeypatch):
+    """The balanced kernels (default for the masked products at 4 <= n <= 10,
+    forced for geom) give the one-lane-per-output kernels' results on batches
+    that end inside a row group, for both gradients and each one alone; small
+    batches also against the oracle."""
+    if op == "regressive" and 0 in metric:
+        pytest.skip("regressive undefined for degenerate metrics")
+    n = len(metric)
+    R = 1 << (10 - n)
+    for batch in (1, R + 3, 4 * 64 * R + 5):
+        a, b, gc = (t.cuda() for t in seeded(batch, n, batch + n, 3))
+        print(f"[case] balanced op={op} metric={metric} batch={batch}", flush=True)
+        monkeypatch.setenv("CLF_PRODUCT_PATH", "balanced")
+        c, ga, gb = _grads(op, a, b, gc, metric)
+        _, ga1, _ = _grads(op, a, b, gc, metric, need_b=False)
+        _, _, gb1 = _grads(op, a, b, gc, metric, need_a=False)
+        monkeypatch.setenv("CLF_PRODUCT_PATH", "blocked")
+        c0, ga0, gb0 = _grads(op, a, b, gc, metric)
+        monkeypatch.delenv("CLF_PRODUCT_PATH")
+        assert rel_err(c, c0) <= TOL and rel_err(ga, ga0) <= TOL and rel_err(gb, gb0) <= TOL
+        assert torch.equal(ga1, ga) and torch.equal(gb1, gb)
+        if batch <= 64:
+            a64, b64 = a.double().cpu().requires_grad_(), b.double().cpu().requires_grad_()
+            c64 = O.einsum_product(op, a64, b64, metric)
+            c64.backward(gc.double().cpu())
+            assert max(rel_err(c, c64), rel_err(ga, a64.grad), rel_err(gb, b64.grad)) <= TOL
