@@ -1,4 +1,5 @@
 // extern "C" entry points of libclifford_hip.so (declared in include/clifford_hip.h).
+#include <cstdlib>
 #include <cstring>
 
 #include <map>
@@ -17,6 +18,17 @@ int set_error(int code, const std::string& msg) {
 }
 
 void clear_error() { g_last_error.clear(); }
+
+// Nontemporal streaming pays when a kernel's rows clearly exceed the 256 MB
+// last-level cache (measured: 805 MB and more gain, 100-400 MB lose).
+constexpr double kStreamNtBytes = 512.0 * 1024 * 1024;
+
+bool stream_nt(double footprint_bytes) {
+    const char* e = std::getenv("CLF_STREAM_NT");
+    if (e && std::strcmp(e, "on") == 0) return true;
+    if (e && std::strcmp(e, "off") == 0) return false;
+    return footprint_bytes > kStreamNtBytes;
+}
 
 unsigned resident_grid(const void* kernel, int block_threads, size_t dyn_lds, long long wanted) {
     static std::mutex mu;

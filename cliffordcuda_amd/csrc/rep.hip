@@ -330,6 +330,7 @@ __global__ __launch_bounds__(256) void rep_bwd_kernel(const float* __restrict__ 
 // back through LDS as W_c[i ^ j][j] at row stride 20 floats, which keeps both
 // the scattered b32 writes and the b128 row reads free of bank conflicts.
 
+template <bool NT>
 __global__ __launch_bounds__(256) void rep16_fwd_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                          float* __restrict__ C, long long batch, RepTable T) {
     __shared__ float lds[4][2 * 4 * 256];  // per wave: staged a | staged b; later the relayout, then c
@@ -346,13 +347,13 @@ __global__ __launch_bounds__(256) void rep16_fwd_kernel(const float* __restrict_
 
     const long long stride = (long long)gridDim.x * 4 * 4;
     long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
-    Pre16 pa = fetch16(A, row0, batch, lane);
-    Pre16 pb = fetch16(B, row0, batch, lane);
+    Pre16 pa = fetch16<NT>(A, row0, batch, lane);
+    Pre16 pb = fetch16<NT>(B, row0, batch, lane);
     for (; row0 < batch; row0 += stride) {
         stage16(sa, pa, lane, oddc);
         stage16(sb, pb, lane, oddc);
-        pa = fetch16(A, row0 + stride, batch, lane);
-        pb = fetch16(B, row0 + stride, batch, lane);
+        pa = fetch16<NT>(A, row0 + stride, batch, lane);
+        pb = fetch16<NT>(B, row0 + stride, batch, lane);
         wave_lds_sync();
         float wa[16], wb[16];
         gather16<0>(sa + rb * 256, ent, wa);
@@ -368,11 +369,12 @@ __global__ __launch_bounds__(256) void rep16_fwd_kernel(const float* __restrict_
         wave_lds_sync();
         unconvert16(wc, sa + rb * 256, ent);
         wave_lds_sync();
-        store16(C, sa, row0, batch, lane, oddc);
+        store16<NT>(C, sa, row0, batch, lane, oddc);
         wave_lds_sync();
     }
 }
 
+template <bool NT>
 __global__ __launch_bounds__(256) void rep16_bwd_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                          const float* __restrict__ GC, float* __restrict__ GA,
                                                          float* __restrict__ GB, long long batch, RepTable T) {
@@ -394,16 +396,16 @@ __global__ __launch_bounds__(256) void rep16_bwd_kernel(const float* __restrict_
 
     const long long stride = (long long)gridDim.x * 4 * 4;
     long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
-    Pre16 pa = fetch16(A, row0, batch, lane);
-    Pre16 pb = fetch16(B, row0, batch, lane);
-    Pre16 pg = fetch16(GC, row0, batch, lane);
+    Pre16 pa = fetch16<NT>(A, row0, batch, lane);
+    Pre16 pb = fetch16<NT>(B, row0, batch, lane);
+    Pre16 pg = fetch16<NT>(GC, row0, batch, lane);
     for (; row0 < batch; row0 += stride) {
         stage16(sa, pa, lane, oddc);
         stage16(sb, pb, lane, oddc);
         stage16(sg, pg, lane, oddc);
-        pa = fetch16(A, row0 + stride, batch, lane);
-        pb = fetch16(B, row0 + stride, batch, lane);
-        pg = fetch16(GC, row0 + stride, batch, lane);
+        pa = fetch16<NT>(A, row0 + stride, batch, lane);
+        pb = fetch16<NT>(B, row0 + stride, batch, lane);
+        pg = fetch16<NT>(GC, row0 + stride, batch, lane);
         wave_lds_sync();
         // dA = G B^T: operands W_g, W_b.  dB = A^T G: operands W'_a, W'_g.
         float wg[16], wgt[16], wb[16], wat[16];
@@ -432,8 +434,8 @@ __global__ __launch_bounds__(256) void rep16_bwd_kernel(const float* __restrict_
         if (want_a) unconvert16(da, sa + rb * 256, ent);
         if (want_b) unconvert16(db, sb + rb * 256, ent);
         wave_lds_sync();
-        if (want_a) store16(GA, sa, row0, batch, lane, oddc);
-        if (want_b) store16(GB, sb, row0, batch, lane, oddc);
+        if (want_a) store16<NT>(GA, sa, row0, batch, lane, oddc);
+        if (want_b) store16<NT>(GB, sb, row0, batch, lane, oddc);
         wave_lds_sync();
     }
 }
@@ -464,7 +466,7 @@ __device__ __forceinline__ void weight_operand(const float* __restrict__ w, cons
     shuffle_operand(t, op, std::make_integer_sequence<unsigned, 16>{});
 }
 
-template <int SIDE>
+template <int SIDE, bool NT>
 __global__ __launch_bounds__(256) void rep16_bcast_fwd_kernel(const float* __restrict__ X, const float* __restrict__ W,
                                                                float* __restrict__ Y, long long batch, RepTable T) {
     // per wave: staged x rows (1024 floats); later the relayout (1280), then y rows
@@ -483,10 +485,10 @@ __global__ __launch_bounds__(256) void rep16_bcast_fwd_kernel(const float* __res
 
     const long long stride = (long long)gridDim.x * 4 * 4;
     long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
-    Pre16 px = fetch16(X, row0, batch, lane);
+    Pre16 px = fetch16<NT>(X, row0, batch, lane);
     for (; row0 < batch; row0 += stride) {
         stage16(sx, px, lane, oddc);
-        px = fetch16(X, row0 + stride, batch, lane);
+        px = fetch16<NT>(X, row0 + stride, batch, lane);
         wave_lds_sync();
         float wx[16];
         // side 0: A = row x of phi(x); side 1: B = column x of phi(x) (transposed signs)
@@ -506,13 +508,13 @@ __global__ __launch_bounds__(256) void rep16_bcast_fwd_kernel(const float* __res
         wave_lds_sync();
         unconvert16(wc, sx + rb * 256, ent);
         wave_lds_sync();
-        store16(Y, sx, row0, batch, lane, oddc);
+        store16<NT>(Y, sx, row0, batch, lane, oddc);
         wave_lds_sync();
     }
 }
 
 // parts[blockIdx.x * 256 + r * 16 + c]: the workgroup's sum of the 16x16 weight-gradient products
-template <int SIDE>
+template <int SIDE, bool NT>
 __global__ __launch_bounds__(256) void rep16_bcast_bwd_kernel(const float* __restrict__ X, const float* __restrict__ W,
                                                                const float* __restrict__ GY, float* __restrict__ GX,
                                                                float* __restrict__ parts, long long batch,
@@ -538,13 +540,13 @@ __global__ __launch_bounds__(256) void rep16_bcast_bwd_kernel(const float* __res
 
     const long long stride = (long long)gridDim.x * 4 * 4;
     long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
-    Pre16 px = fetch16(X, row0, batch, lane);
-    Pre16 pg = fetch16(GY, row0, batch, lane);
+    Pre16 px = fetch16<NT>(X, row0, batch, lane);
+    Pre16 pg = fetch16<NT>(GY, row0, batch, lane);
     for (; row0 < batch; row0 += stride) {
         stage16(sx, px, lane, oddc);
         stage16(sg, pg, lane, oddc);
-        px = fetch16(X, row0 + stride, batch, lane);
-        pg = fetch16(GY, row0 + stride, batch, lane);
+        px = fetch16<NT>(X, row0 + stride, batch, lane);
+        pg = fetch16<NT>(GY, row0 + stride, batch, lane);
         wave_lds_sync();
         // gy in both sign conventions; x as the weight-gradient operand
         // (side 0: A = row of phi(x)^T, transposed signs; side 1: B = column of phi(x)^T = row of phi(x))
@@ -582,7 +584,7 @@ __global__ __launch_bounds__(256) void rep16_bcast_bwd_kernel(const float* __res
             wave_lds_sync();
             unconvert16(wc, sx + rb * 256, ent);
             wave_lds_sync();
-            store16(GX, sx, row0, batch, lane, oddc);
+            store16<NT>(GX, sx, row0, batch, lane, oddc);
         }
         wave_lds_sync();
     }
@@ -739,8 +741,14 @@ int rep_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64
                                    (long long)batch, T); break;
         case 6: hipLaunchKernelGGL((rep_fwd_kernel<3>), CLF_REP_GRID(rep_fwd_kernel<3>), dim3(256), 0, s, a, b, c,
                                    (long long)batch, T); break;
-        case 8: hipLaunchKernelGGL(rep16_fwd_kernel, CLF_REP_GRID(rep16_fwd_kernel), dim3(256), 0, s, a, b, c,
-                                   (long long)batch, T); break;
+        case 8:
+            if (stream_nt(3.0 * 1024.0 * (double)batch))
+                hipLaunchKernelGGL(rep16_fwd_kernel<true>, dim3((unsigned)want), dim3(256), 0, s, a, b, c,
+                                   (long long)batch, T);
+            else
+                hipLaunchKernelGGL(rep16_fwd_kernel<false>, dim3((unsigned)want), dim3(256), 0, s, a, b, c,
+                                   (long long)batch, T);
+            break;
         default: return set_error(CLF_ERR_UNSUPPORTED, "matrix path supports n = 4, 6, 8");
     }
     CLF_HIP_CHECK(hipGetLastError());
@@ -759,8 +767,14 @@ int rep_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc
                                    gb, (long long)batch, T); break;
         case 6: hipLaunchKernelGGL((rep_bwd_kernel<3>), CLF_REP_GRID(rep_bwd_kernel<3>), dim3(256), 0, s, a, b, gc, ga,
                                    gb, (long long)batch, T); break;
-        case 8: hipLaunchKernelGGL(rep16_bwd_kernel, CLF_REP_GRID(rep16_bwd_kernel), dim3(256), 0, s, a, b, gc, ga, gb,
-                                   (long long)batch, T); break;
+        case 8:
+            if (stream_nt((3 + (ga != nullptr) + (gb != nullptr)) * 1024.0 * (double)batch))
+                hipLaunchKernelGGL(rep16_bwd_kernel<true>, dim3((unsigned)want), dim3(256), 0, s, a, b, gc, ga, gb,
+                                   (long long)batch, T);
+            else
+                hipLaunchKernelGGL(rep16_bwd_kernel<false>, dim3((unsigned)want), dim3(256), 0, s, a, b, gc, ga, gb,
+                                   (long long)batch, T);
+            break;
         default: return set_error(CLF_ERR_UNSUPPORTED, "matrix path supports n = 4, 6, 8");
     }
 #undef CLF_REP_GRID
@@ -806,8 +820,17 @@ int rep_bcast_fwd(int side, int n, uint32_t neg, const float* x, const float* w,
     if (n != 8 || !rep_table(n, neg, T)) return set_error(CLF_ERR_UNSUPPORTED, "no m = 16 matrix representation");
     hipStream_t s = (hipStream_t)stream;
     const dim3 grid((unsigned)rep_bcast_grid(batch));
-    if (side == 0) hipLaunchKernelGGL(rep16_bcast_fwd_kernel<0>, grid, dim3(256), 0, s, x, w, y, (long long)batch, T);
-    else hipLaunchKernelGGL(rep16_bcast_fwd_kernel<1>, grid, dim3(256), 0, s, x, w, y, (long long)batch, T);
+    const bool nt = stream_nt(2.0 * 1024.0 * (double)batch);
+#define CLF_BCAST_FWD(SIDE, NT) \
+    hipLaunchKernelGGL((rep16_bcast_fwd_kernel<SIDE, NT>), grid, dim3(256), 0, s, x, w, y, (long long)batch, T)
+    if (side == 0) {
+        if (nt) CLF_BCAST_FWD(0, true);
+        else CLF_BCAST_FWD(0, false);
+    } else {
+        if (nt) CLF_BCAST_FWD(1, true);
+        else CLF_BCAST_FWD(1, false);
+    }
+#undef CLF_BCAST_FWD
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }
@@ -821,12 +844,18 @@ int rep_bcast_bwd(int side, int n, uint32_t neg, const float* x, const float* w,
     const long long nb = rep_bcast_grid(batch);
     float* parts = gw ? ws : nullptr;
     if (batch > 0) {
-        if (side == 0)
-            hipLaunchKernelGGL(rep16_bcast_bwd_kernel<0>, dim3((unsigned)nb), dim3(256), 0, s, x, w, gy, gx, parts,
-                               (long long)batch, T);
-        else
-            hipLaunchKernelGGL(rep16_bcast_bwd_kernel<1>, dim3((unsigned)nb), dim3(256), 0, s, x, w, gy, gx, parts,
-                               (long long)batch, T);
+        const bool nt = stream_nt((1 + (gw != nullptr) + (gx != nullptr)) * 1024.0 * (double)batch);
+#define CLF_BCAST_BWD(SIDE, NT)                                                                                     \
+    hipLaunchKernelGGL((rep16_bcast_bwd_kernel<SIDE, NT>), dim3((unsigned)nb), dim3(256), 0, s, x, w, gy, gx, parts, \
+                       (long long)batch, T)
+        if (side == 0) {
+            if (nt) CLF_BCAST_BWD(0, true);
+            else CLF_BCAST_BWD(0, false);
+        } else {
+            if (nt) CLF_BCAST_BWD(1, true);
+            else CLF_BCAST_BWD(1, false);
+        }
+#undef CLF_BCAST_BWD
     }
     if (gw) {
         int nsums = 0;

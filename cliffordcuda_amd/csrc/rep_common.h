@@ -118,13 +118,16 @@ struct Pre16 {
     float4 v[4];
 };
 
+// NT: nontemporal accesses (stream_nt decides per launch)
+template <bool NT>
 __device__ __forceinline__ Pre16 fetch16(const float* __restrict__ src, long long row0, long long batch, int lane) {
     Pre16 p;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         long long row = row0 + j;
         row = row < batch ? row : batch - 1;
-        p.v[j] = reinterpret_cast<const float4*>(src + row * 256)[lane];
+        const float4* q = reinterpret_cast<const float4*>(src + row * 256) + lane;
+        p.v[j] = NT ? load_stream(q) : *q;
     }
     return p;
 }
@@ -139,6 +142,7 @@ __device__ __forceinline__ void stage16(float* __restrict__ dst, const Pre16& p,
 // Rows past the end were computed from clamped copies of the last row, so
 // their results are bit-identical to it: they are stored to the last row again
 // instead of branching around the stores.
+template <bool NT>
 __device__ __forceinline__ void store16(float* __restrict__ dstg, const float* __restrict__ src, long long row0,
                                         long long batch, int lane, unsigned oddc) {
     float4 v[4];
@@ -148,7 +152,9 @@ __device__ __forceinline__ void store16(float* __restrict__ dstg, const float* _
     for (int j = 0; j < 4; ++j) {
         long long row = row0 + j;
         row = row < batch ? row : batch - 1;
-        reinterpret_cast<float4*>(dstg + row * 256)[lane] = v[j];
+        float4* q = reinterpret_cast<float4*>(dstg + row * 256) + lane;
+        if (NT) store_stream(q, v[j]);
+        else *q = v[j];
     }
 }
 

@@ -45,7 +45,7 @@ __device__ __forceinline__ void load_spin_operand(const float* __restrict__ U, u
 // phi(y) = V^T phi(x) V with V = U (forward, TRANS = false) or V = U^T (the
 // transpose of the action). vop[k] = V[k][x] is both the B operand of
 // phi(x) V and the A operand of V^T (phi(x) V).
-template <bool TRANS>
+template <bool TRANS, bool NT>
 __global__ __launch_bounds__(256) void rotor16_apply_kernel(const float* __restrict__ U, const float* __restrict__ X,
                                                              float* __restrict__ Y, long long batch, RepTable T) {
     // per wave: staged x rows (1024 floats); later the relayout (1280), then y rows
@@ -64,10 +64,10 @@ __global__ __launch_bounds__(256) void rotor16_apply_kernel(const float* __restr
 
     const long long stride = (long long)gridDim.x * 4 * 4;
     long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
-    Pre16 px = fetch16(X, row0, batch, lane);
+    Pre16 px = fetch16<NT>(X, row0, batch, lane);
     for (; row0 < batch; row0 += stride) {
         stage16(sx, px, lane, oddc);
-        px = fetch16(X, row0 + stride, batch, lane);
+        px = fetch16<NT>(X, row0 + stride, batch, lane);
         wave_lds_sync();
         float wx[16];
         gather16<0>(sx + rb * 256, ent, wx);
@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256) void rotor16_apply_kernel(const float* __restr
         wave_lds_sync();
         unconvert16(wc, sx + rb * 256, ent);
         wave_lds_sync();
-        store16(Y, sx, row0, batch, lane, oddc);
+        store16<NT>(Y, sx, row0, batch, lane, oddc);
         wave_lds_sync();
     }
 }
@@ -97,6 +97,7 @@ __global__ __launch_bounds__(256) void rotor16_apply_kernel(const float* __restr
 // hoisting the later gathers, which would cost occupancy.
 constexpr int kRotorBwdWaveFloats = 4 * 256 + kRelayoutFloats;  // staged x | staged gy, then the relayout
 
+template <bool NT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void rotor16_bwd_kernel(const float* __restrict__ U, const float* __restrict__ X,
                                                            const float* __restrict__ GY, float* __restrict__ GX,
                                                            float* __restrict__ gamma_ws, long long batch, RepTable T,
@@ -121,13 +122,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void r
 
     const long long stride = (long long)gridDim.x * 4 * 4;
     long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
-    Pre16 px = fetch16(X, row0, batch, lane);
-    Pre16 pg = fetch16(GY, row0, batch, lane);
+    Pre16 px = fetch16<NT>(X, row0, batch, lane);
+    Pre16 pg = fetch16<NT>(GY, row0, batch, lane);
     for (; row0 < batch; row0 += stride) {
         stage16(sx, px, lane, oddc);
         stage16(sg, pg, lane, oddc);
-        px = fetch16(X, row0 + stride, batch, lane);
-        pg = fetch16(GY, row0 + stride, batch, lane);
+        px = fetch16<NT>(X, row0 + stride, batch, lane);
+        pg = fetch16<NT>(GY, row0 + stride, batch, lane);
         wave_lds_sync();
         // a block whose row is past the end (a clamped copy of the last row)
         // adds nothing to the sums: its phi(x) operands are zeroed
@@ -166,7 +167,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void r
         if (GX) {  // uniform: a kernel argument
             unconvert16(wgx, sx + rb * 256, ent);
             wave_lds_sync();
-            store16(GX, sx, row0, batch, lane, oddc);
+            store16<NT>(GX, sx, row0, batch, lane, oddc);
         }
         wave_lds_sync();
     }
@@ -255,8 +256,17 @@ int rotor16_apply(bool fwd, const float* U, const float* x, float* y, int64_t ba
     if (!spin_tables(T, S)) return set_error(CLF_ERR_UNSUPPORTED, "Cl(8,0) representation tables unavailable");
     hipStream_t s = (hipStream_t)stream;
     const dim3 grid(rotor16_grid(batch));
-    if (fwd) hipLaunchKernelGGL((rotor16_apply_kernel<false>), grid, dim3(256), 0, s, U, x, y, (long long)batch, T);
-    else hipLaunchKernelGGL((rotor16_apply_kernel<true>), grid, dim3(256), 0, s, U, x, y, (long long)batch, T);
+    const bool nt = stream_nt(2.0 * 1024.0 * (double)batch);
+#define CLF_ROTOR16(TR, NT) \
+    hipLaunchKernelGGL((rotor16_apply_kernel<TR, NT>), grid, dim3(256), 0, s, U, x, y, (long long)batch, T)
+    if (fwd) {
+        if (nt) CLF_ROTOR16(false, true);
+        else CLF_ROTOR16(false, false);
+    } else {
+        if (nt) CLF_ROTOR16(true, true);
+        else CLF_ROTOR16(true, false);
+    }
+#undef CLF_ROTOR16
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }
@@ -265,7 +275,7 @@ int rotor16_apply(bool fwd, const float* U, const float* x, float* y, int64_t ba
 // the resident ones (the kernel is persistent). The gamma finalize reads this
 // many partials.
 unsigned rotor16_bwd_grid(long long wanted) {
-    return resident_grid((const void*)rotor16_bwd_kernel, 256, 0, wanted);
+    return resident_grid((const void*)rotor16_bwd_kernel<false>, 256, 0, wanted);
 }
 
 // grid = the number of partials the gamma finalize reads (<= the workspace bound)
@@ -275,8 +285,12 @@ int rotor16_bwd(const float* U, const float* x, const float* gy, float* gx, floa
     SpinTable S;
     if (!spin_tables(T, S)) return set_error(CLF_ERR_UNSUPPORTED, "Cl(8,0) representation tables unavailable");
     hipStream_t s = (hipStream_t)stream;
-    hipLaunchKernelGGL(rotor16_bwd_kernel, dim3(grid), dim3(256), 0, s, U, x, gy, gx, gamma_ws, (long long)batch, T,
-                       S);
+    if (stream_nt((2 + (gx != nullptr)) * 1024.0 * (double)batch))
+        hipLaunchKernelGGL(rotor16_bwd_kernel<true>, dim3(grid), dim3(256), 0, s, U, x, gy, gx, gamma_ws,
+                           (long long)batch, T, S);
+    else
+        hipLaunchKernelGGL(rotor16_bwd_kernel<false>, dim3(grid), dim3(256), 0, s, U, x, gy, gx, gamma_ws,
+                           (long long)batch, T, S);
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }
