@@ -27,6 +27,8 @@
 // (row, sign) blocks at once with the operands built by xor shuffles; the pair
 // sum continues the same accumulator. The two halves of the output are combined
 // through one ds_swizzle (lane ^ 16) before the scatter to blade order.
+#include <cstdlib>
+#include <cstring>
 #include <map>
 #include <mutex>
 
@@ -229,6 +231,233 @@ __device__ __forceinline__ void split_pairs_body(const PairSum& P, const SplitTa
     }
 }
 
+// ---- fused kernels for n = 10 with the null e_9 ------------------------------
+// The pair sums of one direction read each operand half once (the separate
+// pair-sum launches read the shared halves once per sum):
+//   KIND 0 (forward): out0 = L0 R0,                   out1 = L0 R1 + L1 R0^
+//   KIND 1 (dL):      out0 = G0 R0^T + G1 R1^T,       out1 = G1 (R0^)^T
+//   KIND 2 (dR):      out0 = L0^T G0 + (L1^)^T G1^,   out1 = L0^T G1
+// with X = (L, G, L) and Y = (R, R, G) for KIND 0, 1, 2 and out0 / out1 the
+// halves of one output row. Stage 0 stages (X0, Y0), stage 1 (X1, Y1); the
+// operand forms both stages use stay in registers; two sign variants of one
+// half come from one gather.
+struct FusedSplit {
+    const float* X;  // rows of 1024 floats (halves at +0, +512)
+    const float* Y;
+    float* out;
+    long long batch;
+};
+
+// gather_pair with a fresh opaque copy of the table entries, so that the
+// blade offsets of several gathers in one group are not kept live together
+__device__ __forceinline__ void gather_pair_fresh(const float* __restrict__ row, const unsigned (&ent)[16], unsigned m,
+                                                  float (&w)[16]) {
+    unsigned e[16];
+#pragma unroll
+    for (int z = 0; z < 16; ++z) {
+        e[z] = ent[z];
+        asm volatile("" : "+v"(e[z]));
+    }
+    gather_pair(row, e, m, w);
+}
+
+// out half (rows 2g, 2g + 1 at dst, row stride 1024) = T^-1 of the product in acc
+__device__ __forceinline__ void split_store(const floatx16& acc, float* __restrict__ sx, float* __restrict__ dst,
+                                            long long g, long long batch, const unsigned (&en)[16], unsigned mout,
+                                            int lane) {
+    const int b = lane >> 4, r = b >> 1;
+    const unsigned s = (unsigned)b & 1u, x = lane & 15u;
+    const float pm = s ? -1.f : 1.f;
+    relayout_store(sx, acc, lane);
+    wave_lds_sync();
+    float w[16];
+    relayout_load(sx, b, x, w);
+    wave_lds_sync();
+    wht_inplace<16>(w);
+#pragma unroll
+    for (int z = 0; z < 16; ++z) {
+        const float other = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(w[z]), 0x401F));
+        const float v = __builtin_fmaf(pm, w[z], other) * (1.f / 32.f);
+        const unsigned blade = s ? ((en[z] >> 9) & 511u) : (en[z] & 511u);
+        sx[r * 512 + blade] = __uint_as_float(__float_as_uint(v) ^ (((mout >> z) & 1u) << 31));
+    }
+    wave_lds_sync();
+    const float4* src = reinterpret_cast<const float4*>(sx);
+    const float4 o0 = src[lane], o1 = src[lane + 64], o2 = src[lane + 128], o3 = src[lane + 192];
+    long long r0 = 2 * g, r1 = 2 * g + 1;
+    r0 = r0 < batch ? r0 : batch - 1;  // clamped rows repeat the last row's values
+    r1 = r1 < batch ? r1 : batch - 1;
+    float4* d0 = reinterpret_cast<float4*>(dst + r0 * 1024);
+    float4* d1 = reinterpret_cast<float4*>(dst + r1 * 1024);
+    d0[lane] = o0;
+    d0[lane + 64] = o1;
+    d1[lane] = o2;
+    d1[lane + 64] = o3;
+    wave_lds_sync();
+}
+
+// LDS per wave: four regions of two half rows (1024 floats each) so that the
+// stage-0 halves stay staged through stage 1 and are gathered again where a
+// sum needs them (instead of holding their operands in registers). Each
+// output's relayout and scatter use two adjacent regions whose halves are
+// consumed by then: region order per KIND is chosen for that.
+template <int KIND>
+struct FusedRegions {
+    // offsets (in units of 1024 floats) of X0, Y0, X1, Y1
+    static constexpr int x0 = 0;
+    static constexpr int y0 = KIND == 1 ? 3 : 1;
+    static constexpr int x1 = 2;
+    static constexpr int y1 = KIND == 1 ? 1 : 3;
+    // adjacent free regions for the outputs: out0, out1
+    static constexpr int out0 = KIND == 0 ? 2 : (KIND == 1 ? 0 : 1);
+    static constexpr int out1 = KIND == 0 ? 0 : (KIND == 1 ? 0 : 1);
+};
+
+template <int KIND>
+__global__ __launch_bounds__(256) void split_fused_kernel(FusedSplit P, SplitTable T) {
+    __shared__ float lds[4][4 * 1024];
+    using RG = FusedRegions<KIND>;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int b = lane >> 4, r = b >> 1;
+    const unsigned s = (unsigned)b & 1u, x = lane & 15u;
+    float* base = &lds[wave][0];
+    float* sx0 = base + RG::x0 * 1024;
+    float* sy0 = base + RG::y0 * 1024;
+    float* sx1 = base + RG::x1 * 1024;
+    float* sy1 = base + RG::y1 * 1024;
+    unsigned ent[16];
+#pragma unroll
+    for (int z = 0; z < 16; ++z) ent[z] = T.e[x * 16 + z];
+    // sign masks of the operand forms: A operand (W of X, W' if transposed),
+    // B operand (W' of Y unless transposed, then W); hats folded in
+    unsigned mx0, my0, my0b, mx1, my1, my1b;
+    if (KIND == 0) {
+        mx0 = gather_signs(ent, false, false, s);   // L0
+        my0 = gather_signs(ent, false, true, s);    // R0
+        my0b = gather_signs(ent, true, true, s);    // R0^
+        mx1 = gather_signs(ent, false, false, s);   // L1
+        my1 = gather_signs(ent, false, true, s);    // R1
+        my1b = 0u;
+    } else if (KIND == 1) {
+        mx0 = gather_signs(ent, false, false, s);   // G0
+        my0 = gather_signs(ent, false, false, s);   // R0^T
+        my0b = gather_signs(ent, true, false, s);   // (R0^)^T
+        mx1 = gather_signs(ent, false, false, s);   // G1
+        my1 = gather_signs(ent, false, false, s);   // R1^T
+        my1b = 0u;
+    } else {
+        mx0 = gather_signs(ent, false, true, s);    // L0^T
+        my0 = gather_signs(ent, false, true, s);    // G0
+        my0b = 0u;
+        mx1 = gather_signs(ent, true, true, s);     // (L1^)^T
+        my1 = gather_signs(ent, true, true, s);     // G1^
+        my1b = gather_signs(ent, false, true, s);   // G1
+    }
+    unsigned mo = 0;
+#pragma unroll
+    for (int z = 0; z < 16; ++z) mo |= ((ent[z] >> (18 + s)) & 1u) << z;
+
+    const long long batch = P.batch;
+    const long long ngroups = (batch + 1) / 2;
+    const long long gstride = (long long)gridDim.x * 4;
+    const float* X0 = P.X;
+    const float* Y0 = P.Y;
+    const float* X1 = P.X + 512;
+    const float* Y1 = P.Y + 512;
+    long long g = (long long)blockIdx.x * 4 + wave;
+    float4 ax0, ax1, ax2, ax3, ay0, ay1, ay2, ay3;
+    CLF_SPLIT_FETCH(ax0, ax1, ax2, ax3, X0, 1024, 2 * g);
+    CLF_SPLIT_FETCH(ay0, ay1, ay2, ay3, Y0, 1024, 2 * g);
+    for (; g < ngroups; g += gstride) {
+        unsigned m_x0 = mx0, m_y0 = my0, m_y0b = my0b, m_x1 = mx1, m_y1 = my1, m_y1b = my1b, mout = mo;
+        asm volatile("" : "+v"(m_x0), "+v"(m_y0), "+v"(m_y0b), "+v"(m_x1), "+v"(m_y1), "+v"(m_y1b), "+v"(mout));
+        unsigned en[16];
+#pragma unroll
+        for (int z = 0; z < 16; ++z) {
+            en[z] = ent[z];
+            asm volatile("" : "+v"(en[z]));
+        }
+        // stage 0: X0, Y0 (staged until the group ends)
+        CLF_SPLIT_STAGE(sx0, ax0, ax1, ax2, ax3);
+        CLF_SPLIT_STAGE(sy0, ay0, ay1, ay2, ay3);
+        CLF_SPLIT_FETCH(ax0, ax1, ax2, ax3, X1, 1024, 2 * g);
+        CLF_SPLIT_FETCH(ay0, ay1, ay2, ay3, Y1, 1024, 2 * g);
+        wave_lds_sync();
+        floatx16 acc0;
+        {
+            float wx[16], wy[16];
+            gather_pair_fresh(sx0 + r * 512, en, m_x0, wx);
+            gather_pair_fresh(sy0 + r * 512, en, m_y0, wy);
+            acc0 = mfma_chain(wx, wy);
+        }
+        if constexpr (KIND == 0) {  // C0 = L0 R0 is complete; X1 / Y1 regions are still free
+            split_store(acc0, base + RG::out0 * 1024, P.out, g, batch, en, mout, lane);
+        }
+        // stage 1: X1, Y1
+        CLF_SPLIT_STAGE(sx1, ax0, ax1, ax2, ax3);
+        CLF_SPLIT_STAGE(sy1, ay0, ay1, ay2, ay3);
+        CLF_SPLIT_FETCH(ax0, ax1, ax2, ax3, X0, 1024, 2 * (g + gstride));
+        CLF_SPLIT_FETCH(ay0, ay1, ay2, ay3, Y0, 1024, 2 * (g + gstride));
+        wave_lds_sync();
+        if constexpr (KIND == 0) {
+            // C1 = L0 R1 + L1 R0^
+            floatx16 acc1;
+            {
+                float wx[16], wy[16];
+                gather_pair_fresh(sx0 + r * 512, en, m_x0, wx);
+                gather_pair_fresh(sy1 + r * 512, en, m_y1, wy);
+                acc1 = mfma_chain(wx, wy);
+            }
+            {
+                float wx[16], wy[16];
+                gather_pair_fresh(sx1 + r * 512, en, m_x1, wx);
+                gather_pair_fresh(sy0 + r * 512, en, m_y0b, wy);
+                acc1 = mfma_chain_acc(acc1, wx, wy, std::make_integer_sequence<unsigned, 16>{});
+            }
+            wave_lds_sync();
+            split_store(acc1, base + RG::out1 * 1024, P.out + 512, g, batch, en, mout, lane);
+        } else if constexpr (KIND == 1) {
+            // out0 += G1 R1^T; out1 = G1 (R0^)^T
+            float wx[16];
+            gather_pair_fresh(sx1 + r * 512, en, m_x1, wx);
+            {
+                float wy[16];
+                gather_pair_fresh(sy1 + r * 512, en, m_y1, wy);
+                acc0 = mfma_chain_acc(acc0, wx, wy, std::make_integer_sequence<unsigned, 16>{});
+            }
+            wave_lds_sync();
+            split_store(acc0, base + RG::out0 * 1024, P.out, g, batch, en, mout, lane);
+            floatx16 acc1;
+            {
+                float wy[16];
+                gather_pair_fresh(sy0 + r * 512, en, m_y0b, wy);
+                acc1 = mfma_chain(wx, wy);
+            }
+            wave_lds_sync();
+            split_store(acc1, base + RG::out1 * 1024, P.out + 512, g, batch, en, mout, lane);
+        } else {
+            // out0 += (L1^)^T G1^; out1 = L0^T G1
+            {
+                float wx[16], wy[16];
+                gather_pair_fresh(sx1 + r * 512, en, m_x1, wx);
+                gather_pair_fresh(sy1 + r * 512, en, m_y1, wy);
+                acc0 = mfma_chain_acc(acc0, wx, wy, std::make_integer_sequence<unsigned, 16>{});
+            }
+            wave_lds_sync();
+            split_store(acc0, base + RG::out0 * 1024, P.out, g, batch, en, mout, lane);
+            floatx16 acc1;
+            {
+                float wx[16], wy[16];
+                gather_pair_fresh(sx0 + r * 512, en, m_x0, wx);
+                gather_pair_fresh(sy1 + r * 512, en, m_y1b, wy);
+                acc1 = mfma_chain(wx, wy);
+            }
+            wave_lds_sync();
+            split_store(acc1, base + RG::out1 * 1024, P.out + 512, g, batch, en, mout, lane);
+        }
+    }
+}
+
 #undef CLF_SPLIT_FETCH
 #undef CLF_SPLIT_STAGE
 
@@ -344,6 +573,23 @@ static int launch_pairs(const SplitTable& T, const PairSpec* ps, int npairs, lon
     return CLF_OK;
 }
 
+// n = 10: one launch per direction and gradient reads each operand half once
+// (CLF_SPLIT_PATH=pairs runs the separate pair-sum launches instead).
+static bool split_fused_enabled() {
+    const char* e = std::getenv("CLF_SPLIT_PATH");
+    return !(e && std::strcmp(e, "pairs") == 0);
+}
+
+template <int KIND>
+static void launch_fused(const SplitTable& T, const float* X, const float* Y, float* out, int64_t batch,
+                         hipStream_t s) {
+    FusedSplit P{X, Y, out, (long long)batch};
+    const long long groups = (batch + 1) / 2;
+    long long blocks = (groups + 3) / 4;
+    if (blocks > 256LL * 8) blocks = 256LL * 8;
+    hipLaunchKernelGGL(split_fused_kernel<KIND>, dim3((unsigned)(blocks < 1 ? 1 : blocks)), dim3(256), 0, s, P, T);
+}
+
 int split_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64_t batch, void* stream) {
     SplitTable T;
     if (!split_table(neg & 511u, T)) return set_error(CLF_ERR_UNSUPPORTED, "signature has no split representation");
@@ -351,6 +597,8 @@ int split_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int
     if (n == 9) {
         const PairSpec ab[1] = {{a, b, 0u}};
         launch_pairs(T, ab, 1, 512, c, 512, batch, s);
+    } else if (split_fused_enabled()) {
+        launch_fused<0>(T, a, b, c, batch, s);
     } else {
         const PairSpec c0[1] = {{a, b, 0u}};
         const PairSpec c1[2] = {{a, b + 512, 0u}, {a + 512, b, kHatY}};
@@ -375,6 +623,9 @@ int split_bwd(int n, uint32_t neg, const float* a, const float* b, const float* 
             const PairSpec p[1] = {{a, gc, kTransA}};
             launch_pairs(T, p, 1, 512, gb, 512, batch, s);
         }
+    } else if (split_fused_enabled()) {
+        if (ga) launch_fused<1>(T, gc, b, ga, batch, s);
+        if (gb) launch_fused<2>(T, a, gc, gb, batch, s);
     } else {
         const float *L0 = a, *L1 = a + 512, *R0 = b, *R1 = b + 512, *G0 = gc, *G1 = gc + 512;
         if (ga) {

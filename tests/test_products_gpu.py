@@ -334,3 +334,22 @@ def test_balanced_kernels_match_blocked_and_oracle(op, metric, monkeypatch):
             c64 = O.einsum_product(op, a64, b64, metric)
             c64.backward(gc.double().cpu())
             assert max(rel_err(c, c64), rel_err(ga, a64.grad), rel_err(gb, b64.grad)) <= TOL
+
+
+@pytest.mark.parametrize("metric", [m for m in SPLIT_TYPE if len(m) == 10],
+                         ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
+def test_split_fused_matches_pair_sums(metric, monkeypatch):
+    """n = 10 with a null e_9: the fused kernels (one launch per direction and
+    gradient) equal the separate pair-sum launches, on batches with a partial
+    two-row group, for both gradients and each one alone."""
+    for batch in (1, 3, 2 * 2048 * 4 + 3):
+        a, b, gc = (t.cuda() for t in seeded(batch, 10, batch, 3))
+        print(f"[case] split fused metric={metric} batch={batch}", flush=True)
+        c, ga, gb = _grads("geom", a, b, gc, metric)
+        _, ga1, _ = _grads("geom", a, b, gc, metric, need_b=False)
+        _, _, gb1 = _grads("geom", a, b, gc, metric, need_a=False)
+        monkeypatch.setenv("CLF_SPLIT_PATH", "pairs")
+        c0, ga0, gb0 = _grads("geom", a, b, gc, metric)
+        monkeypatch.delenv("CLF_SPLIT_PATH")
+        assert rel_err(c, c0) <= TOL and rel_err(ga, ga0) <= TOL and rel_err(gb, gb0) <= TOL
+        assert torch.equal(ga1, ga) and torch.equal(gb1, gb)
