@@ -426,60 +426,47 @@ __global__ __launch_bounds__(256) void prod_bwd_blk(const float* __restrict__ A,
 // that continues in later lanes (a "tail") gets the later lanes' heads added
 // after the loop, in lane order (deterministic sums).
 // ROLE 0: output kh, partner ih (jh = ih ^ kh); ROLE 1: output ih (gradient
-// of the left operand), partner jh; ROLE 2: output jh, partner ih. Partners
-// of an output are one or two families {base | S : S subset of mask},
-// enumerated with S <- (S - mask) & mask.
+// of the left operand), partner jh; ROLE 2: output jh, partner ih. The
+// partners of an output are a family {base | S}: the subsets S of mask in
+// increasing order (S <- (S - mask) & mask), from index `first`, `count` of
+// them. The inner product runs three rounds, one per low-block pattern
+// (CLS 0: ih strictly inside jh, lc pattern; CLS 1: jh strictly inside ih, rc
+// pattern; CLS 2: ih = jh, both), so the lanes of a round never diverge on the
+// pattern; its rounds add into an LDS copy of the output rows, stored at the end.
 // Layout: a wave owns groups of 1024 floats per operand (R = 1024 / D rows,
 // NB lanes per row) in wave-private LDS and walks the groups with a grid
 // stride, loading the next group into registers while it computes.
 constexpr int kBalMinN = 4, kBalMaxN = 10;
 constexpr int kBalGroupF4 = 256;  // float4 per operand per group
 
-template <int OP, int ROLE>
-__device__ __forceinline__ void bal_families(unsigned o, unsigned full, unsigned& b0, unsigned& m0, unsigned& b1,
-                                             unsigned& m1, int& c1) {
-    const unsigned co = ~o & full;
-    b1 = 0u;
-    m1 = 0u;
-    c1 = 0;
-    if (OP == OP_GEOM) {
-        b0 = 0u;
-        m0 = full;
-    } else if (OP == OP_WEDGE) {
-        b0 = 0u;
-        m0 = ROLE == 0 ? o : co;
-    } else if (OP == OP_LC) {
-        b0 = ROLE == 1 ? o : 0u;
-        m0 = ROLE == 2 ? o : co;
-    } else if (OP == OP_RC) {
-        b0 = ROLE == 1 ? 0u : o;
-        m0 = ROLE == 1 ? o : co;
-    } else if (OP == OP_INNER) {
-        if (ROLE == 0) {  // ih disjoint from kh, or ih containing kh (the same set when kh = 0)
-            b0 = 0u;
-            m0 = co;
-            b1 = o;
-            m1 = co;
-            c1 = o ? (1 << __popc(co)) : 0;
-        } else {  // partners containing o, then those inside o except o itself
-            b0 = o;
-            m0 = co;
-            b1 = 0u;
-            m1 = o;
-            c1 = (1 << __popc(o)) - 1;
-        }
-    } else {  // regressive: ih | jh = full
-        b0 = co;
-        m0 = o;
-    }
-}
+struct BalFam {
+    unsigned base, mask;
+    int first, count;
+};
 
-template <int OP, int ROLE>
-__device__ __forceinline__ int bal_count(unsigned o, unsigned full) {
-    unsigned b0, m0, b1, m1;
-    int c1;
-    bal_families<OP, ROLE>(o, full, b0, m0, b1, m1, c1);
-    return (1 << __popc(m0)) + c1;
+template <int OP, int ROLE, int CLS>
+__device__ __forceinline__ BalFam bal_family(unsigned o, unsigned full) {
+    const unsigned co = ~o & full;
+    const int nco = 1 << __popc(co), no = 1 << __popc(o);
+    if (OP == OP_GEOM) return BalFam{0u, full, 0, 1 << __popc(full)};
+    if (OP == OP_WEDGE) return ROLE == 0 ? BalFam{0u, o, 0, no} : BalFam{0u, co, 0, nco};
+    if (OP == OP_LC) return ROLE == 0 ? BalFam{0u, co, 0, nco} : (ROLE == 1 ? BalFam{o, co, 0, nco} : BalFam{0u, o, 0, no});
+    if (OP == OP_RC) return ROLE == 1 ? BalFam{0u, o, 0, no} : BalFam{o, co, 0, nco};
+    if (OP == OP_REGR) return BalFam{co, o, 0, no};
+    // inner, by class
+    if (CLS == 0) {  // ih strictly inside jh
+        if (ROLE == 0) return BalFam{0u, co, 0, o ? nco : 0};
+        if (ROLE == 1) return BalFam{o, co, 1, nco - 1};
+        return BalFam{0u, o, 0, no - 1};
+    }
+    if (CLS == 1) {  // jh strictly inside ih
+        if (ROLE == 0) return BalFam{o, co, 0, o ? nco : 0};
+        if (ROLE == 1) return BalFam{0u, o, 0, no - 1};
+        return BalFam{o, co, 1, nco - 1};
+    }
+    // ih = jh
+    if (ROLE == 0) return BalFam{0u, full, 0, o ? 0 : (1 << __popc(full))};
+    return BalFam{o, 0u, 0, 1};
 }
 
 // the s-th subset of m in increasing order (bits of s deposited on the bits of m)
@@ -504,11 +491,11 @@ struct BalSched {
     int last_lane;    // last lane holding pairs of olast
 };
 
-template <int OP, int ROLE>
+template <int OP, int ROLE, int CLS>
 __device__ __forceinline__ BalSched bal_schedule(unsigned lr, unsigned NB) {
     const unsigned full = NB - 1u;
     int total = 0;
-    for (unsigned o = 0; o < NB; ++o) total += bal_count<OP, ROLE>(o, full);
+    for (unsigned o = 0; o < NB; ++o) total += bal_family<OP, ROLE, CLS>(o, full).count;
     BalSched sc;
     sc.T = (total + (int)NB - 1) / (int)NB;
     sc.p0 = (int)lr * sc.T;
@@ -519,7 +506,7 @@ __device__ __forceinline__ BalSched bal_schedule(unsigned lr, unsigned NB) {
     sc.olast = 0u;
     int pre = 0, last_end = 0;
     for (unsigned o = 0; o < NB; ++o) {
-        const int c = bal_count<OP, ROLE>(o, full);
+        const int c = bal_family<OP, ROLE, CLS>(o, full).count;
         if (sc.p0 >= pre && sc.p0 < pre + c) {
             sc.o0 = o;
             sc.s0 = sc.p0 - pre;
@@ -548,33 +535,50 @@ __device__ __forceinline__ void store_blk(float4* __restrict__ out, unsigned blk
     }
 }
 
-// One role over one row: la / lb / lg are the row's staged operands, heads the
-// row's head slots (4 float4 per lane), out the row's output (nullptr for a
-// row past the end of the batch: computed, not stored). The caller syncs the
-// wave's LDS before (staged data) and after (heads reused).
-template <int OP, int ROLE, bool LOWNEG>
+__device__ __forceinline__ void add_blk(float4* __restrict__ out, unsigned blk, const float (&acc)[16]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float4 v = out[(blk << 2) + q];
+        v.x += acc[4 * q];
+        v.y += acc[4 * q + 1];
+        v.z += acc[4 * q + 2];
+        v.w += acc[4 * q + 3];
+        out[(blk << 2) + q] = v;
+    }
+}
+
+// low-block pattern of a pair: the op's, or for the inner product its class's
+template <int OP, int CLS>
+constexpr int bal_variant() {
+    return OP != OP_INNER ? OP : (CLS == 0 ? LV_LC : (CLS == 1 ? LV_RC : LV_INNER));
+}
+
+// One role (and class) over one row: la / lb / lg are the row's staged
+// operands, heads the row's head slots (4 float4 per lane). ADD: completed
+// outputs are added into out (the row's LDS copy); else stored to out (the
+// row in global memory, nullptr for a row past the end of the batch). The
+// caller syncs the wave's LDS before (staged data) and after (heads reused).
+template <int OP, int ROLE, int CLS, bool LOWNEG, bool ADD>
 __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __restrict__ la,
                                          const float4* __restrict__ lb, const float4* __restrict__ lg,
                                          float4* __restrict__ heads, unsigned lr, float4* __restrict__ out,
                                          unsigned NB, const BlkParams& P) {
     const unsigned full = NB - 1u;
     constexpr bool kRev = OP == OP_REGR && ROLE == 0;
+    constexpr int VAR = bal_variant<OP, CLS>();
+    constexpr bool kLowNeg = VAR == LV_WEDGE || VAR == LV_REGR ? false : LOWNEG;
     float acc[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.f;
     unsigned o = sc.o0;
-    unsigned b0, m0, b1, m1;
-    int c1;
-    bal_families<OP, ROLE>(o, full, b0, m0, b1, m1, c1);
-    int c0 = 1 << __popc(m0);
+    BalFam f = bal_family<OP, ROLE, CLS>(o, full);
     int s = sc.s0;
-    bool fam1 = s >= c0;
-    unsigned S = fam1 ? deposit_bits((unsigned)(s - c0), m1) : deposit_bits((unsigned)s, m0);
+    unsigned S = deposit_bits((unsigned)(f.first + s), f.mask);
     bool first = true;
     int p = sc.p0;
     for (int t = 0; t < sc.T; ++t) {
         if (p >= sc.p1) break;
-        const unsigned part = (fam1 ? b1 : b0) | S;
+        const unsigned part = f.base | S;
         if (ROLE == 0) {
             const unsigned ih = part, jh = part ^ o;
             const HiSign hs = hi_sign<OP>(ih, jh, P.negh, P.nulh, full, P.nm1, P.mu);
@@ -583,7 +587,8 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
                 load_blk(la, ih, av);
                 load_blk(lb, jh, bv);
                 apply_flips(bv, hs.mask, hs.mask ^ (cross_pi<OP>(ih, P.nm1) << 31));
-                fwd_block_dispatch<OP, LOWNEG>(acc, av, bv, ih, jh);
+                if (OP == OP_INNER) lowblock_fwd<VAR, kLowNeg>(acc, av, bv);
+                else fwd_block_dispatch<OP, LOWNEG>(acc, av, bv, ih, jh);
             }
         } else {
             const unsigned h = o, m = part, x = h ^ m;
@@ -597,7 +602,8 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
                     float bv[16];
                     load_blk(lb, m, bv);
                     apply_flips(bv, hs.mask, hs.mask ^ (cross_pi<OP>(h, P.nm1) << 31));
-                    ga_block_dispatch<OP, LOWNEG>(acc, bv, g, h, m);
+                    if (OP == OP_INNER) lowblock_ga<VAR, kLowNeg>(acc, bv, g);
+                    else ga_block_dispatch<OP, LOWNEG>(acc, bv, g, h, m);
                 } else {
                     const unsigned pm = cross_pi<OP>(m, P.nm1) << 31;
                     float av[16], gt[16];
@@ -605,39 +611,36 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
                     apply_flips(av, hs.mask, hs.mask ^ pm);
 #pragma unroll
                     for (int e = 0; e < 16; ++e) gt[e] = (cpopc((unsigned)e) & 1) ? flip(g[e], pm) : g[e];
-                    gb_block_dispatch<OP, LOWNEG>(acc, av, gt, m, h);
+                    if (OP == OP_INNER) lowblock_gb<VAR, kLowNeg>(acc, av, gt);
+                    else gb_block_dispatch<OP, LOWNEG>(acc, av, gt, m, h);
                 }
             }
         }
         ++p;
         ++s;
-        const unsigned mm = fam1 ? m1 : m0;
-        S = (S - mm) & mm;
-        if (!fam1 && s == c0 && c1 > 0) {
-            fam1 = true;
-            S = 0u;
-        }
-        const bool done = s == c0 + c1;
+        S = (S - f.mask) & f.mask;
+        const bool done = s == f.count;
         if (done || p == sc.p1) {
             if (first && sc.cont0) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
                     heads[lr * 4 + q] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
             } else if (done && out) {
-                store_blk(out, kRev ? (full ^ o) : o, acc, kRev);
+                if (ADD) add_blk(out, o, acc);
+                else store_blk(out, kRev ? (full ^ o) : o, acc, kRev);
             }
             if (done) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[e] = 0.f;
                 first = false;
-                ++o;
-                if (o < NB) {
-                    bal_families<OP, ROLE>(o, full, b0, m0, b1, m1, c1);
-                    c0 = 1 << __popc(m0);
-                }
+                // next output with pairs (outputs of a class may have none)
+                do {
+                    ++o;
+                    if (o >= NB) break;
+                    f = bal_family<OP, ROLE, CLS>(o, full);
+                } while (f.count == 0);
                 s = 0;
-                fam1 = false;
-                S = 0u;
+                S = deposit_bits((unsigned)f.first, f.mask);
             }
         }
     }
@@ -653,7 +656,10 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
                 acc[4 * q + 3] += v.w;
             }
         }
-        if (out) store_blk(out, kRev ? (full ^ sc.olast) : sc.olast, acc, kRev);
+        if (out) {
+            if (ADD) add_blk(out, sc.olast, acc);
+            else store_blk(out, kRev ? (full ^ sc.olast) : sc.olast, acc, kRev);
+        }
     }
 }
 
@@ -690,10 +696,54 @@ __device__ __forceinline__ void bal_stage(float4* __restrict__ dst, const BalPre
     }
 }
 
+// the group's LDS output copy (rows in natural order) -> global, rows past the end skipped
+__device__ __forceinline__ void bal_flush(const float4* __restrict__ src, float* __restrict__ dst, long long grp,
+                                          long long batch, int n, int lane) {
+    const int d4_log = n - 2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = lane + 64 * i;
+        const long long row = grp * (kBalGroupF4 >> d4_log) + (c >> d4_log);
+        if (row < batch) reinterpret_cast<float4*>(dst)[grp * kBalGroupF4 + c] = src[c];
+    }
+}
+
+__device__ __forceinline__ void bal_zero(float4* __restrict__ dst, int lane) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[lane + 64 * i] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+// the three class rounds of the inner product for one role
+template <int ROLE, bool LOWNEG>
+__device__ __forceinline__ void bal_inner_rounds(const BalSched (&sc)[3], const float4* la, const float4* lb,
+                                                 const float4* lg, float4* heads, unsigned lr, float4* out,
+                                                 unsigned NB, const BlkParams& P) {
+    bal_role<OP_INNER, ROLE, 0, LOWNEG, true>(sc[0], la, lb, lg, heads, lr, out, NB, P);
+    wave_lds_sync();
+    bal_role<OP_INNER, ROLE, 1, LOWNEG, true>(sc[1], la, lb, lg, heads, lr, out, NB, P);
+    wave_lds_sync();
+    bal_role<OP_INNER, ROLE, 2, LOWNEG, true>(sc[2], la, lb, lg, heads, lr, out, NB, P);
+}
+
+template <int OP, int ROLE>
+__device__ __forceinline__ void bal_schedules(BalSched (&sc)[3], unsigned lr, unsigned NB) {
+    sc[0] = bal_schedule<OP, ROLE, 0>(lr, NB);
+    if (OP == OP_INNER) {
+        sc[1] = bal_schedule<OP, ROLE, 1>(lr, NB);
+        sc[2] = bal_schedule<OP, ROLE, 2>(lr, NB);
+    }
+}
+
+// LDS per wave: a | b | heads, plus the output copy for the inner product
+template <int OP>
+constexpr int bal_regions() {
+    return OP == OP_INNER ? 4 : 3;
+}
+
 template <int OP, bool LOWNEG>
 __global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A, const float* __restrict__ B,
                                                      float* __restrict__ C, BlkParams P) {
-    __shared__ float4 lds[4][3 * kBalGroupF4];  // per wave: a | b | heads
+    __shared__ float4 lds[4][bal_regions<OP>() * kBalGroupF4];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int n = P.n;
     const int lpr_log = n - 4;
@@ -704,8 +754,10 @@ __global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A,
     float4* sa = lds[wave];
     float4* sb = sa + kBalGroupF4;
     float4* heads = sb + kBalGroupF4 + (r << lpr_log) * 4;
+    float4* sout = sb + 2 * kBalGroupF4;  // inner only
     const int roff = r << (n - 2);
-    const BalSched sc = bal_schedule<OP, 0>(lr, NB);
+    BalSched sc[3];
+    bal_schedules<OP, 0>(sc, lr, NB);
     const long long ngrp = (P.batch + R - 1) / R;
     const long long gstride = (long long)gridDim.x * 4;
     long long grp = (long long)blockIdx.x * 4 + wave;
@@ -716,22 +768,29 @@ __global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A,
         bal_stage(sb, pb, n, lane);
         pa = bal_fetch(A, grp + gstride, P.batch, n, lane);
         pb = bal_fetch(B, grp + gstride, P.batch, n, lane);
+        if constexpr (OP == OP_INNER) bal_zero(sout, lane);
         wave_lds_sync();
         const long long row = grp * R + r;
-        float4* out = row < P.batch ? reinterpret_cast<float4*>(C) + (row << (n - 2)) : nullptr;
-        bal_role<OP, 0, LOWNEG>(sc, sa + roff, sb + roff, nullptr, heads, lr, out, NB, P);
+        if constexpr (OP == OP_INNER) {
+            bal_inner_rounds<0, LOWNEG>(sc, sa + roff, sb + roff, nullptr, heads, lr, sout + roff, NB, P);
+            wave_lds_sync();
+            bal_flush(sout, C, grp, P.batch, n, lane);
+        } else {
+            float4* out = row < P.batch ? reinterpret_cast<float4*>(C) + (row << (n - 2)) : nullptr;
+            bal_role<OP, 0, 0, LOWNEG, false>(sc[0], sa + roff, sb + roff, nullptr, heads, lr, out, NB, P);
+        }
         wave_lds_sync();
     }
 }
 
 // Backward: b and gc are staged first and the left-operand gradient runs with
 // its heads in the a slot; then a is staged and the right-operand gradient
-// runs with its heads in the b slot (12 KB of LDS per wave).
+// runs with its heads in the b slot (12 KB of LDS per wave; 16 KB for inner).
 template <int OP, bool LOWNEG>
 __global__ __launch_bounds__(256) void prod_bwd_bal(const float* __restrict__ A, const float* __restrict__ B,
                                                      const float* __restrict__ GC, float* __restrict__ GA,
                                                      float* __restrict__ GB, BlkParams P) {
-    __shared__ float4 lds[4][3 * kBalGroupF4];  // per wave: a (ga heads first) | b (gb heads later) | gc
+    __shared__ float4 lds[4][bal_regions<OP>() * kBalGroupF4];  // a | b | gc [| output copy]
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int n = P.n;
     const int lpr_log = n - 4;
@@ -742,11 +801,13 @@ __global__ __launch_bounds__(256) void prod_bwd_bal(const float* __restrict__ A,
     float4* sa = lds[wave];
     float4* sb = sa + kBalGroupF4;
     float4* sg = sb + kBalGroupF4;
+    float4* sout = sg + kBalGroupF4;  // inner only
     const int roff = r << (n - 2);
     const int hoff = (r << lpr_log) * 4;
     const bool want_a = GA != nullptr, want_b = GB != nullptr;
-    const BalSched sca = bal_schedule<OP, 1>(lr, NB);
-    const BalSched scb = bal_schedule<OP, 2>(lr, NB);
+    BalSched sca[3], scb[3];
+    bal_schedules<OP, 1>(sca, lr, NB);
+    bal_schedules<OP, 2>(scb, lr, NB);
     const long long ngrp = (P.batch + R - 1) / R;
     const long long gstride = (long long)gridDim.x * 4;
     long long grp = (long long)blockIdx.x * 4 + wave;
@@ -762,17 +823,31 @@ __global__ __launch_bounds__(256) void prod_bwd_bal(const float* __restrict__ A,
         if (want_a) {  // uniform: a kernel argument
             bal_stage(sb, pb, n, lane);
             pb = bal_fetch(B, grp + gstride, P.batch, n, lane);
+            if constexpr (OP == OP_INNER) bal_zero(sout, lane);
             wave_lds_sync();
-            float4* out = row_ok ? reinterpret_cast<float4*>(GA) + (row << (n - 2)) : nullptr;
-            bal_role<OP, 1, LOWNEG>(sca, nullptr, sb + roff, sg + roff, sa + hoff, lr, out, NB, P);
+            if constexpr (OP == OP_INNER) {
+                bal_inner_rounds<1, LOWNEG>(sca, nullptr, sb + roff, sg + roff, sa + hoff, lr, sout + roff, NB, P);
+                wave_lds_sync();
+                bal_flush(sout, GA, grp, P.batch, n, lane);
+            } else {
+                float4* out = row_ok ? reinterpret_cast<float4*>(GA) + (row << (n - 2)) : nullptr;
+                bal_role<OP, 1, 0, LOWNEG, false>(sca[0], nullptr, sb + roff, sg + roff, sa + hoff, lr, out, NB, P);
+            }
             wave_lds_sync();
         }
         if (want_b) {
             bal_stage(sa, pa, n, lane);
             pa = bal_fetch(A, grp + gstride, P.batch, n, lane);
+            if constexpr (OP == OP_INNER) bal_zero(sout, lane);
             wave_lds_sync();
-            float4* out = row_ok ? reinterpret_cast<float4*>(GB) + (row << (n - 2)) : nullptr;
-            bal_role<OP, 2, LOWNEG>(scb, sa + roff, nullptr, sg + roff, sb + hoff, lr, out, NB, P);
+            if constexpr (OP == OP_INNER) {
+                bal_inner_rounds<2, LOWNEG>(scb, sa + roff, nullptr, sg + roff, sb + hoff, lr, sout + roff, NB, P);
+                wave_lds_sync();
+                bal_flush(sout, GB, grp, P.batch, n, lane);
+            } else {
+                float4* out = row_ok ? reinterpret_cast<float4*>(GB) + (row << (n - 2)) : nullptr;
+                bal_role<OP, 2, 0, LOWNEG, false>(scb[0], sa + roff, nullptr, sg + roff, sb + hoff, lr, out, NB, P);
+            }
         }
         wave_lds_sync();
     }
@@ -1062,14 +1137,15 @@ static bool product_path_is(const char* what) {
 static bool tiled_forced() { return product_path_is("tiled"); }
 static bool generic_forced() { return product_path_is("generic"); }
 
-// Balanced kernels: wedge, lc, rc and regressive for 4 <= n <= 10
-// (CLF_PRODUCT_PATH=blocked keeps them on the one-lane-per-output kernels).
-// The geometric product (every output has the same work) and inner (whose
-// pairs need one of three low-block patterns, so lanes at different pairs
-// diverge) use them only when CLF_PRODUCT_PATH=balanced.
+// Balanced kernels: wedge, lc, rc, regressive for 4 <= n <= 10, inner for
+// n >= 9 (CLF_PRODUCT_PATH=blocked keeps them on the one-lane-per-output
+// kernels). Inner's three class rounds cost more than its divergence saves
+// below n = 9 (measured), and the geometric product, whose outputs all have
+// the same work, gains nothing; both use them only when
+// CLF_PRODUCT_PATH=balanced.
 static bool bal_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, bool& lowneg) {
     if (n < kBalMinN || n > kBalMaxN) return false;
-    const bool opt_in = op == OP_GEOM || op == OP_INNER;
+    const bool opt_in = op == OP_GEOM || (op == OP_INNER && n < 9);
     if (opt_in ? !product_path_is("balanced") : product_path_is("blocked")) return false;
     if (!blocked_metric(op, n, neg, nul, lowneg)) return false;
     block_sign_params(n, neg, nul, P);

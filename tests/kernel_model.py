@@ -251,24 +251,31 @@ def backward_tiled(op_name, a, b, gc, metric, T):
 # to which its lane adds the heads of the later lanes after the loop.
 
 
-def bal_families(op, role, o, full):
-    """[(base, mask, count)] of partner families for output block o."""
+def bal_family(op, role, o, full, cls=0):
+    """(base, mask, first, count): partners base | S for the subsets S of mask
+    in the kernel's order, from index first. The inner product has three
+    classes (0: ih strictly inside jh, 1: jh strictly inside ih, 2: ih = jh)."""
     co = ~o & full
-    c = lambda m: 1 << popc(m)
+    nco, no = 1 << popc(co), 1 << popc(o)
     if op == GEOM:
-        return [(0, full, c(full))]
+        return (0, full, 0, 1 << popc(full))
     if op == WEDGE:
-        m = o if role == 0 else co
-        return [(0, m, c(m))]
+        return (0, o, 0, no) if role == 0 else (0, co, 0, nco)
     if op == LC:
-        return [[(0, co, c(co))], [(o, co, c(co))], [(0, o, c(o))]][role]
+        return [(0, co, 0, nco), (o, co, 0, nco), (0, o, 0, no)][role]
     if op == RC:
-        return [[(o, co, c(co))], [(0, o, c(o))], [(o, co, c(co))]][role]
-    if op == INNER:
-        if role == 0:
-            return [(0, co, c(co))] + ([(o, co, c(co))] if o else [])
-        return [(o, co, c(co)), (0, o, c(o) - 1)]
-    return [(co, o, c(o))]          # regressive
+        return (0, o, 0, no) if role == 1 else (o, co, 0, nco)
+    if op == REGR:
+        return (co, o, 0, no)
+    if cls == 0:
+        return [(0, co, 0, nco if o else 0), (o, co, 1, nco - 1), (0, o, 0, no - 1)][role]
+    if cls == 1:
+        return [(o, co, 0, nco if o else 0), (0, o, 0, no - 1), (o, co, 1, nco - 1)][role]
+    return (0, full, 0, 0 if o else 1 << popc(full)) if role == 0 else (o, 0, 0, 1)
+
+
+def bal_classes(op):
+    return 3 if op == INNER else 1
 
 
 def subsets(m):
@@ -280,8 +287,9 @@ def subsets(m):
     return out
 
 
-def bal_partners(op, role, o, full):
-    return [b | S for (b, m, cnt) in bal_families(op, role, o, full) for S in subsets(m)[:cnt]]
+def bal_partners(op, role, o, full, cls=0):
+    base, mask, first, count = bal_family(op, role, o, full, cls)
+    return [base | S for S in subsets(mask)[first:first + count]]
 
 
 def bal_block_pair(role, o, part):
@@ -289,9 +297,9 @@ def bal_block_pair(role, o, part):
     return [(part, part ^ o), (o, part), (part, o)][role]
 
 
-def bal_schedule(op, role, NB):
+def bal_schedule(op, role, NB, cls=0):
     full = NB - 1
-    counts = [len(bal_partners(op, role, o, full)) for o in range(NB)]
+    counts = [len(bal_partners(op, role, o, full, cls)) for o in range(NB)]
     pre = np.concatenate([[0], np.cumsum(counts)])
     total = int(pre[-1])
     T = -(-total // NB)
@@ -310,12 +318,12 @@ def bal_schedule(op, role, NB):
     return T, lanes, pre
 
 
-def bal_run(op, role, NB, pair_value):
-    """Emulate the lanes of one row: pair_value(o, part) -> contribution (16,)
-    array (zero for pairs the metric kills). Returns out[o] as the kernel
-    stores it (complete segments, then tails + heads)."""
+def bal_run(op, role, NB, pair_value, cls=0):
+    """Emulate the lanes of one row for one class: pair_value(o, part) ->
+    contribution (16,) array (zero for pairs the metric kills). Returns out[o]
+    as the kernel stores (or adds) it: complete segments, then tails + heads."""
     full = NB - 1
-    T, lanes, pre = bal_schedule(op, role, NB)
+    T, lanes, pre = bal_schedule(op, role, NB, cls)
     out = {}
     heads = {}
     tails = {}
@@ -323,7 +331,7 @@ def bal_run(op, role, NB, pair_value):
         if sc is None:
             continue
         o, s, first = sc["o0"], sc["s0"], True
-        partners = bal_partners(op, role, o, full)
+        partners = bal_partners(op, role, o, full, cls)
         acc = np.zeros(16)
         for p in range(sc["p0"], sc["p1"]):
             acc = acc + pair_value(o, partners[s])
@@ -339,9 +347,12 @@ def bal_run(op, role, NB, pair_value):
                     tails[lr] = (o, acc)
                 if done:
                     acc = np.zeros(16)
-                    o, s, first = o + 1, 0, False
+                    s, first = 0, False
+                    o += 1
+                    while o < NB and not bal_partners(op, role, o, full, cls):
+                        o += 1
                     if o < NB:
-                        partners = bal_partners(op, role, o, full)
+                        partners = bal_partners(op, role, o, full, cls)
     for lr, (o, acc) in tails.items():
         assert lanes[lr]["tail"] and lanes[lr]["olast"] == o
         for l2 in range(lr + 1, lanes[lr]["last_lane"] + 1):

@@ -62,29 +62,39 @@ def test_tiled_model_forward_backward(op, n, metric, T):
 
 @pytest.mark.parametrize("op", list(K.OPS.values()))
 def test_balanced_schedule_covers_every_valid_pair_once(op):
-    """The partner families enumerate exactly the structurally valid block
-    pairs of each output (every role, n = 4 .. 10), every output has at least
-    one pair, and the lanes' ranges with heads/tails rebuild each output once."""
+    """The partner families (over the classes of the inner product) enumerate
+    exactly the structurally valid block pairs of each output (every role,
+    n = 4 .. 10), each once; inner's classes hold the pairs of one low-block
+    pattern each; the lanes' ranges with heads/tails rebuild each output once."""
     rng = np.random.default_rng(op)
     for n in range(4, 11):
         NB = 1 << (n - 4)
         full = NB - 1
         for role in range(3):
-            seen = set()
-            for o in range(NB):
-                parts = K.bal_partners(op, role, o, full)
-                assert parts, (n, role, o)
-                assert len(set(parts)) == len(parts)
-                for part in parts:
-                    seen.add(K.bal_block_pair(role, o, part))
+            seen = []
+            for cls in range(K.bal_classes(op)):
+                for o in range(NB):
+                    for part in K.bal_partners(op, role, o, full, cls):
+                        ih, jh = K.bal_block_pair(role, o, part)
+                        seen.append((ih, jh))
+                        if op == K.INNER:
+                            assert K.variant(op, ih, jh) == [K.LC, K.RC, K.INNER][cls]
             valid = {(ih, jh) for ih in range(NB) for jh in range(NB)
                      if K.hi_sign(op, ih, jh, 0, 0, full, 0, 0)[0]}
-            assert seen == valid, (n, role)
-            vals = {(o, part): rng.standard_normal(16) for o in range(NB) for part in K.bal_partners(op, role, o, full)}
-            out = K.bal_run(op, role, NB, lambda o, part: vals[(o, part)])
-            assert sorted(out) == list(range(NB))
+            assert len(seen) == len(set(seen)) and set(seen) == valid, (n, role)
+            total = {o: np.zeros(16) for o in range(NB)}
+            ref = {o: np.zeros(16) for o in range(NB)}
+            for cls in range(K.bal_classes(op)):
+                vals = {(o, part): rng.standard_normal(16) for o in range(NB)
+                        for part in K.bal_partners(op, role, o, full, cls)}
+                out = K.bal_run(op, role, NB, lambda o, part: vals[(o, part)], cls)
+                for o in range(NB):
+                    parts = K.bal_partners(op, role, o, full, cls)
+                    assert (o in out) == bool(parts)
+                    if parts:
+                        total[o] = total[o] + out[o]
+                        ref[o] = ref[o] + sum(vals[(o, part)] for part in parts)
+                T, lanes, pre = K.bal_schedule(op, role, NB, cls)
+                assert T * NB >= pre[-1] > (T - 1) * NB or pre[-1] == 0
             for o in range(NB):
-                ref = sum(vals[(o, part)] for part in K.bal_partners(op, role, o, full))
-                np.testing.assert_allclose(out[o], ref, atol=1e-12)
-            T, lanes, pre = K.bal_schedule(op, role, NB)
-            assert T * NB >= pre[-1] > (T - 1) * NB
+                np.testing.assert_allclose(total[o], ref[o], atol=1e-12)
