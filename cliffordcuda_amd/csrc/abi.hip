@@ -20,8 +20,10 @@ int set_error(int code, const std::string& msg) {
 void clear_error() { g_last_error.clear(); }
 
 // Nontemporal streaming pays when a kernel's rows clearly exceed the 256 MB
-// last-level cache (measured: 805 MB and more gain, 100-400 MB lose).
-constexpr double kStreamNtBytes = 512.0 * 1024 * 1024;
+// last-level cache (measured on the m = 16 kernels: 400 MB and more gain 5-10 %,
+// about 270 MB is neutral; working sets of 100-400 MB that other kernels of a
+// step re-read lose their cache hits).
+constexpr double kStreamNtBytes = 320.0 * 1024 * 1024;
 
 bool stream_nt(double footprint_bytes) {
     const char* e = std::getenv("CLF_STREAM_NT");

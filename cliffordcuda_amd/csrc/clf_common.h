@@ -28,11 +28,11 @@ void clear_error();
 unsigned resident_grid(const void* kernel, int block_threads, size_t dyn_lds, long long wanted);
 
 // Streaming global accesses with the nontemporal hint. When a kernel's rows
-// (read once, written once) far exceed the 256 MB last-level cache, keeping
-// them out of the caches raises the sustained HBM rate (a 3-stream row copy of
+// (read once, written once) exceed the 256 MB last-level cache, keeping them
+// out of the caches raises the sustained HBM rate (a 3-stream row copy of
 // 768 MB: 5.5 TB/s plain, 6.3 TB/s nontemporal); when they fit, plain accesses
-// keep cache hits for the next kernel. stream_nt() decides per launch
-// (CLF_STREAM_NT=on / off forces it).
+// keep cache hits for the next kernel. stream_nt() decides per launch from the
+// launch's row bytes (CLF_STREAM_NT=on / off forces it).
 bool stream_nt(double footprint_bytes);
 typedef float clf_fvec4 __attribute__((ext_vector_type(4)));
 
