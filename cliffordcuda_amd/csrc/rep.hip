@@ -409,8 +409,7 @@ __global__ __launch_bounds__(256) void rep16_bwd_kernel(const float* __restrict_
         wave_lds_sync();
         // dA = G B^T: operands W_g, W_b.  dB = A^T G: operands W'_a, W'_g.
         float wg[16], wgt[16], wb[16], wat[16];
-        gather16<0>(sg + rb * 256, ent, wg);
-        gather16<1>(sg + rb * 256, ent, wgt);
+        gather16_pair(sg + rb * 256, ent, wg, wgt);
         if (want_a) gather16<0>(sb + rb * 256, ent, wb);
         if (want_b) gather16<1>(sa + rb * 256, ent, wat);
         wave_lds_sync();
@@ -551,8 +550,7 @@ __global__ __launch_bounds__(256) void rep16_bcast_bwd_kernel(const float* __res
         // gy in both sign conventions; x as the weight-gradient operand
         // (side 0: A = row of phi(x)^T, transposed signs; side 1: B = column of phi(x)^T = row of phi(x))
         float wg[16], wgt[16], wx[16];
-        gather16<0>(sg + rb * 256, ent, wg);
-        gather16<1>(sg + rb * 256, ent, wgt);
+        gather16_pair(sg + rb * 256, ent, wg, wgt);
         if (want_w) gather16<SIDE == 0 ? 1 : 0>(sx + rb * 256, ent, wx);
         wave_lds_sync();
         wht_inplace<16>(wg);
