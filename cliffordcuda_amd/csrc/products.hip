@@ -444,29 +444,49 @@ struct BalFam {
     int first, count;
 };
 
+// nul: the high-part null generators. Pairs whose blocks share one are zero
+// for the metric ops and are left out of the families; an output of a stored
+// (not added) op whose pairs all vanish keeps one such zero pair, so that it
+// is still written.
 template <int OP, int ROLE, int CLS>
-__device__ __forceinline__ BalFam bal_family(unsigned o, unsigned full) {
+__device__ __forceinline__ BalFam bal_family(unsigned o, unsigned full, unsigned nul) {
     const unsigned co = ~o & full;
     const int nco = 1 << __popc(co), no = 1 << __popc(o);
-    if (OP == OP_GEOM) return BalFam{0u, full, 0, 1 << __popc(full)};
+    const unsigned con = co & ~nul, onn = o & ~nul;  // partner bits that never meet a null
+    const int ncon = 1 << __popc(con), nonn = 1 << __popc(onn);
+    const bool onul = (o & nul) != 0u;
+    if (OP == OP_GEOM) {
+        const unsigned m = ROLE == 0 ? full & ~(nul & ~o) : full & ~(nul & o);
+        return BalFam{0u, m, 0, 1 << __popc(m)};
+    }
     if (OP == OP_WEDGE) return ROLE == 0 ? BalFam{0u, o, 0, no} : BalFam{0u, co, 0, nco};
-    if (OP == OP_LC) return ROLE == 0 ? BalFam{0u, co, 0, nco} : (ROLE == 1 ? BalFam{o, co, 0, nco} : BalFam{0u, o, 0, no});
-    if (OP == OP_RC) return ROLE == 1 ? BalFam{0u, o, 0, no} : BalFam{o, co, 0, nco};
+    if (OP == OP_LC) {
+        if (ROLE == 0) return BalFam{0u, con, 0, ncon};
+        if (ROLE == 1) return onul ? BalFam{o, 0u, 0, 1} : BalFam{o, co, 0, nco};
+        return BalFam{0u, onn, 0, nonn};
+    }
+    if (OP == OP_RC) {
+        if (ROLE == 0) return BalFam{o, con, 0, ncon};
+        if (ROLE == 1) return BalFam{0u, onn, 0, nonn};
+        return onul ? BalFam{o, 0u, 0, 1} : BalFam{o, co, 0, nco};
+    }
     if (OP == OP_REGR) return BalFam{co, o, 0, no};
-    // inner, by class
+    // inner, by class; strict: the subsets of onn strictly inside o
+    const int strict = nonn - (onul ? 0 : 1);
     if (CLS == 0) {  // ih strictly inside jh
-        if (ROLE == 0) return BalFam{0u, co, 0, o ? nco : 0};
-        if (ROLE == 1) return BalFam{o, co, 1, nco - 1};
-        return BalFam{0u, o, 0, no - 1};
+        if (ROLE == 0) return BalFam{0u, con, 0, o ? ncon : 0};
+        if (ROLE == 1) return BalFam{o, co, 1, onul ? 0 : nco - 1};
+        return BalFam{0u, onn, 0, strict};
     }
     if (CLS == 1) {  // jh strictly inside ih
-        if (ROLE == 0) return BalFam{o, co, 0, o ? nco : 0};
-        if (ROLE == 1) return BalFam{0u, o, 0, no - 1};
-        return BalFam{o, co, 1, nco - 1};
+        if (ROLE == 0) return BalFam{o, con, 0, o ? ncon : 0};
+        if (ROLE == 1) return BalFam{0u, onn, 0, strict};
+        return BalFam{o, co, 1, onul ? 0 : nco - 1};
     }
     // ih = jh
-    if (ROLE == 0) return BalFam{0u, full, 0, o ? 0 : (1 << __popc(full))};
-    return BalFam{o, 0u, 0, 1};
+    const unsigned fn = full & ~nul;
+    if (ROLE == 0) return BalFam{0u, fn, 0, o ? 0 : (1 << __popc(fn))};
+    return BalFam{o, 0u, 0, onul ? 0 : 1};
 }
 
 // the s-th subset of m in increasing order (bits of s deposited on the bits of m)
@@ -492,10 +512,10 @@ struct BalSched {
 };
 
 template <int OP, int ROLE, int CLS>
-__device__ __forceinline__ BalSched bal_schedule(unsigned lr, unsigned NB) {
+__device__ __forceinline__ BalSched bal_schedule(unsigned lr, unsigned NB, unsigned nul) {
     const unsigned full = NB - 1u;
     int total = 0;
-    for (unsigned o = 0; o < NB; ++o) total += bal_family<OP, ROLE, CLS>(o, full).count;
+    for (unsigned o = 0; o < NB; ++o) total += bal_family<OP, ROLE, CLS>(o, full, nul).count;
     BalSched sc;
     sc.T = (total + (int)NB - 1) / (int)NB;
     sc.p0 = (int)lr * sc.T;
@@ -506,7 +526,7 @@ __device__ __forceinline__ BalSched bal_schedule(unsigned lr, unsigned NB) {
     sc.olast = 0u;
     int pre = 0, last_end = 0;
     for (unsigned o = 0; o < NB; ++o) {
-        const int c = bal_family<OP, ROLE, CLS>(o, full).count;
+        const int c = bal_family<OP, ROLE, CLS>(o, full, nul).count;
         if (sc.p0 >= pre && sc.p0 < pre + c) {
             sc.o0 = o;
             sc.s0 = sc.p0 - pre;
@@ -571,7 +591,7 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.f;
     unsigned o = sc.o0;
-    BalFam f = bal_family<OP, ROLE, CLS>(o, full);
+    BalFam f = bal_family<OP, ROLE, CLS>(o, full, P.nulh);
     int s = sc.s0;
     unsigned S = deposit_bits((unsigned)(f.first + s), f.mask);
     bool first = true;
@@ -637,7 +657,7 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
                 do {
                     ++o;
                     if (o >= NB) break;
-                    f = bal_family<OP, ROLE, CLS>(o, full);
+                    f = bal_family<OP, ROLE, CLS>(o, full, P.nulh);
                 } while (f.count == 0);
                 s = 0;
                 S = deposit_bits((unsigned)f.first, f.mask);
@@ -726,11 +746,11 @@ __device__ __forceinline__ void bal_inner_rounds(const BalSched (&sc)[3], const 
 }
 
 template <int OP, int ROLE>
-__device__ __forceinline__ void bal_schedules(BalSched (&sc)[3], unsigned lr, unsigned NB) {
-    sc[0] = bal_schedule<OP, ROLE, 0>(lr, NB);
+__device__ __forceinline__ void bal_schedules(BalSched (&sc)[3], unsigned lr, unsigned NB, unsigned nul) {
+    sc[0] = bal_schedule<OP, ROLE, 0>(lr, NB, nul);
     if (OP == OP_INNER) {
-        sc[1] = bal_schedule<OP, ROLE, 1>(lr, NB);
-        sc[2] = bal_schedule<OP, ROLE, 2>(lr, NB);
+        sc[1] = bal_schedule<OP, ROLE, 1>(lr, NB, nul);
+        sc[2] = bal_schedule<OP, ROLE, 2>(lr, NB, nul);
     }
 }
 
@@ -757,7 +777,7 @@ __global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A,
     float4* sout = sb + 2 * kBalGroupF4;  // inner only
     const int roff = r << (n - 2);
     BalSched sc[3];
-    bal_schedules<OP, 0>(sc, lr, NB);
+    bal_schedules<OP, 0>(sc, lr, NB, P.nulh);
     const long long ngrp = (P.batch + R - 1) / R;
     const long long gstride = (long long)gridDim.x * 4;
     long long grp = (long long)blockIdx.x * 4 + wave;
@@ -806,8 +826,8 @@ __global__ __launch_bounds__(256) void prod_bwd_bal(const float* __restrict__ A,
     const int hoff = (r << lpr_log) * 4;
     const bool want_a = GA != nullptr, want_b = GB != nullptr;
     BalSched sca[3], scb[3];
-    bal_schedules<OP, 1>(sca, lr, NB);
-    bal_schedules<OP, 2>(scb, lr, NB);
+    bal_schedules<OP, 1>(sca, lr, NB, P.nulh);
+    bal_schedules<OP, 2>(scb, lr, NB, P.nulh);
     const long long ngrp = (P.batch + R - 1) / R;
     const long long gstride = (long long)gridDim.x * 4;
     long long grp = (long long)blockIdx.x * 4 + wave;

@@ -251,27 +251,38 @@ def backward_tiled(op_name, a, b, gc, metric, T):
 # to which its lane adds the heads of the later lanes after the loop.
 
 
-def bal_family(op, role, o, full, cls=0):
+def bal_family(op, role, o, full, cls=0, nul=0):
     """(base, mask, first, count): partners base | S for the subsets S of mask
     in the kernel's order, from index first. The inner product has three
-    classes (0: ih strictly inside jh, 1: jh strictly inside ih, 2: ih = jh)."""
+    classes (0: ih strictly inside jh, 1: jh strictly inside ih, 2: ih = jh).
+    nul: high-part null generators; pairs whose blocks share one are zero for
+    the metric ops and are left out. An output of a stored (not added) op
+    whose pairs are all zero keeps one zero pair so that it is still written."""
     co = ~o & full
     nco, no = 1 << popc(co), 1 << popc(o)
+    con, onn = co & ~nul, o & ~nul   # partner bits that never meet a null
     if op == GEOM:
-        return (0, full, 0, 1 << popc(full))
+        m = full & ~(nul & ~o) if role == 0 else full & ~(nul & o)
+        return (0, m, 0, 1 << popc(m))
     if op == WEDGE:
         return (0, o, 0, no) if role == 0 else (0, co, 0, nco)
     if op == LC:
-        return [(0, co, 0, nco), (o, co, 0, nco), (0, o, 0, no)][role]
+        return [(0, con, 0, 1 << popc(con)), (o, 0, 0, 1) if o & nul else (o, co, 0, nco),
+                (0, onn, 0, 1 << popc(onn))][role]
     if op == RC:
-        return (0, o, 0, no) if role == 1 else (o, co, 0, nco)
+        return [(o, con, 0, 1 << popc(con)), (0, onn, 0, 1 << popc(onn)),
+                (o, 0, 0, 1) if o & nul else (o, co, 0, nco)][role]
     if op == REGR:
         return (co, o, 0, no)
+    strict = (1 << popc(onn)) - (1 if onn == o else 0)  # subsets of onn strictly inside o
     if cls == 0:
-        return [(0, co, 0, nco if o else 0), (o, co, 1, nco - 1), (0, o, 0, no - 1)][role]
+        return [(0, con, 0, (1 << popc(con)) if o else 0), (o, co, 1, 0 if o & nul else nco - 1),
+                (0, onn, 0, strict)][role]
     if cls == 1:
-        return [(o, co, 0, nco if o else 0), (0, o, 0, no - 1), (o, co, 1, nco - 1)][role]
-    return (0, full, 0, 0 if o else 1 << popc(full)) if role == 0 else (o, 0, 0, 1)
+        return [(o, con, 0, (1 << popc(con)) if o else 0), (0, onn, 0, strict),
+                (o, co, 1, 0 if o & nul else nco - 1)][role]
+    fn = full & ~nul
+    return (0, fn, 0, 0 if o else 1 << popc(fn)) if role == 0 else (o, 0, 0, 0 if o & nul else 1)
 
 
 def bal_classes(op):
@@ -287,8 +298,8 @@ def subsets(m):
     return out
 
 
-def bal_partners(op, role, o, full, cls=0):
-    base, mask, first, count = bal_family(op, role, o, full, cls)
+def bal_partners(op, role, o, full, cls=0, nul=0):
+    base, mask, first, count = bal_family(op, role, o, full, cls, nul)
     return [base | S for S in subsets(mask)[first:first + count]]
 
 
@@ -297,9 +308,9 @@ def bal_block_pair(role, o, part):
     return [(part, part ^ o), (o, part), (part, o)][role]
 
 
-def bal_schedule(op, role, NB, cls=0):
+def bal_schedule(op, role, NB, cls=0, nul=0):
     full = NB - 1
-    counts = [len(bal_partners(op, role, o, full, cls)) for o in range(NB)]
+    counts = [len(bal_partners(op, role, o, full, cls, nul)) for o in range(NB)]
     pre = np.concatenate([[0], np.cumsum(counts)])
     total = int(pre[-1])
     T = -(-total // NB)
@@ -318,12 +329,12 @@ def bal_schedule(op, role, NB, cls=0):
     return T, lanes, pre
 
 
-def bal_run(op, role, NB, pair_value, cls=0):
+def bal_run(op, role, NB, pair_value, cls=0, nul=0):
     """Emulate the lanes of one row for one class: pair_value(o, part) ->
     contribution (16,) array (zero for pairs the metric kills). Returns out[o]
     as the kernel stores (or adds) it: complete segments, then tails + heads."""
     full = NB - 1
-    T, lanes, pre = bal_schedule(op, role, NB, cls)
+    T, lanes, pre = bal_schedule(op, role, NB, cls, nul)
     out = {}
     heads = {}
     tails = {}
@@ -331,7 +342,7 @@ def bal_run(op, role, NB, pair_value, cls=0):
         if sc is None:
             continue
         o, s, first = sc["o0"], sc["s0"], True
-        partners = bal_partners(op, role, o, full, cls)
+        partners = bal_partners(op, role, o, full, cls, nul)
         acc = np.zeros(16)
         for p in range(sc["p0"], sc["p1"]):
             acc = acc + pair_value(o, partners[s])
@@ -349,10 +360,10 @@ def bal_run(op, role, NB, pair_value, cls=0):
                     acc = np.zeros(16)
                     s, first = 0, False
                     o += 1
-                    while o < NB and not bal_partners(op, role, o, full, cls):
+                    while o < NB and not bal_partners(op, role, o, full, cls, nul):
                         o += 1
                     if o < NB:
-                        partners = bal_partners(op, role, o, full, cls)
+                        partners = bal_partners(op, role, o, full, cls, nul)
     for lr, (o, acc) in tails.items():
         assert lanes[lr]["tail"] and lanes[lr]["olast"] == o
         for l2 in range(lr + 1, lanes[lr]["last_lane"] + 1):

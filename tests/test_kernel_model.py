@@ -63,38 +63,54 @@ def test_tiled_model_forward_backward(op, n, metric, T):
 @pytest.mark.parametrize("op", list(K.OPS.values()))
 def test_balanced_schedule_covers_every_valid_pair_once(op):
     """The partner families (over the classes of the inner product) enumerate
-    exactly the structurally valid block pairs of each output (every role,
-    n = 4 .. 10), each once; inner's classes hold the pairs of one low-block
-    pattern each; the lanes' ranges with heads/tails rebuild each output once."""
+    exactly the valid block pairs of each output (every role, n = 4 .. 10,
+    without and with null generators in the high part: pairs meeting on a null
+    generator are left out), each once; an output of a stored op with no valid
+    pair gets exactly one (zero) pair so that it is written; inner's classes
+    hold the pairs of one low-block pattern each; the lanes' ranges with
+    heads/tails rebuild each output once."""
     rng = np.random.default_rng(op)
     for n in range(4, 11):
         NB = 1 << (n - 4)
         full = NB - 1
-        for role in range(3):
-            seen = []
-            for cls in range(K.bal_classes(op)):
+        nuls = sorted({0, full & (NB >> 1), full & 0b101, full & 0b110})
+        for nul in nuls:
+            for role in range(3):
+                seen = []
+                for cls in range(K.bal_classes(op)):
+                    for o in range(NB):
+                        for part in K.bal_partners(op, role, o, full, cls, nul):
+                            ih, jh = K.bal_block_pair(role, o, part)
+                            seen.append((ih, jh))
+                            if op == K.INNER:
+                                assert K.variant(op, ih, jh) == [K.LC, K.RC, K.INNER][cls]
+                valid = {(ih, jh) for ih in range(NB) for jh in range(NB)
+                         if K.hi_sign(op, ih, jh, 0, nul, full, 0, 0)[0]}
+                assert len(seen) == len(set(seen)), (n, nul, role)
+                extra = set(seen) - valid
+                assert valid <= set(seen), (n, nul, role)
+                out_of = [[ih ^ jh, ih, jh][role] for ih, jh in extra]
+                if op == K.INNER:
+                    assert not extra, (n, nul, role)
+                else:
+                    # one placeholder per output whose pairs all vanish, none elsewhere
+                    empty = {o for o in range(NB)
+                             if not any([ih ^ jh, ih, jh][role] == o for ih, jh in valid)}
+                    assert sorted(out_of) == sorted(empty), (n, nul, role)
+                    assert nul or not extra
+                total = {o: np.zeros(16) for o in range(NB)}
+                ref = {o: np.zeros(16) for o in range(NB)}
+                for cls in range(K.bal_classes(op)):
+                    vals = {(o, part): rng.standard_normal(16) for o in range(NB)
+                            for part in K.bal_partners(op, role, o, full, cls, nul)}
+                    out = K.bal_run(op, role, NB, lambda o, part: vals[(o, part)], cls, nul)
+                    for o in range(NB):
+                        parts = K.bal_partners(op, role, o, full, cls, nul)
+                        assert (o in out) == bool(parts)
+                        if parts:
+                            total[o] = total[o] + out[o]
+                            ref[o] = ref[o] + sum(vals[(o, part)] for part in parts)
+                    T, lanes, pre = K.bal_schedule(op, role, NB, cls, nul)
+                    assert T * NB >= pre[-1] > (T - 1) * NB or pre[-1] == 0
                 for o in range(NB):
-                    for part in K.bal_partners(op, role, o, full, cls):
-                        ih, jh = K.bal_block_pair(role, o, part)
-                        seen.append((ih, jh))
-                        if op == K.INNER:
-                            assert K.variant(op, ih, jh) == [K.LC, K.RC, K.INNER][cls]
-            valid = {(ih, jh) for ih in range(NB) for jh in range(NB)
-                     if K.hi_sign(op, ih, jh, 0, 0, full, 0, 0)[0]}
-            assert len(seen) == len(set(seen)) and set(seen) == valid, (n, role)
-            total = {o: np.zeros(16) for o in range(NB)}
-            ref = {o: np.zeros(16) for o in range(NB)}
-            for cls in range(K.bal_classes(op)):
-                vals = {(o, part): rng.standard_normal(16) for o in range(NB)
-                        for part in K.bal_partners(op, role, o, full, cls)}
-                out = K.bal_run(op, role, NB, lambda o, part: vals[(o, part)], cls)
-                for o in range(NB):
-                    parts = K.bal_partners(op, role, o, full, cls)
-                    assert (o in out) == bool(parts)
-                    if parts:
-                        total[o] = total[o] + out[o]
-                        ref[o] = ref[o] + sum(vals[(o, part)] for part in parts)
-                T, lanes, pre = K.bal_schedule(op, role, NB, cls)
-                assert T * NB >= pre[-1] > (T - 1) * NB or pre[-1] == 0
-            for o in range(NB):
-                np.testing.assert_allclose(total[o], ref[o], atol=1e-12)
+                    np.testing.assert_allclose(total[o], ref[o], atol=1e-12)
