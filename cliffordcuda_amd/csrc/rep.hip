@@ -702,15 +702,21 @@ bool rep_table(int n, uint32_t neg, RepTable& T) {
 }
 
 bool split_applicable(int op, int n, uint32_t neg, uint32_t nul);
+bool rep7_applicable(uint32_t neg);
+int rep7_fwd(uint32_t neg, const float* a, const float* b, float* c, int64_t batch, void* stream);
+int rep7_bwd(uint32_t neg, const float* a, const float* b, const float* gc, float* ga, float* gb, int64_t batch,
+             void* stream);
 int split_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64_t batch, void* stream);
 int split_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc, float* ga, float* gb,
               int64_t batch, void* stream);
 
 // The matrix path serves the geometric product when the signature allows it
-// (real type, n = 4, 6, 8; split type n = 9, and n = 10 with e_9 null);
-// returns false otherwise (the caller uses the per-term kernels).
+// (real type, n = 4, 6, 8; every non-degenerate n = 7 signature; split type
+// n = 9, and n = 10 with e_9 null); returns false otherwise (the caller uses
+// the per-term kernels).
 bool rep_applicable(int op, int n, uint32_t neg, uint32_t nul) {
     if (n == 9 || n == 10) return split_applicable(op, n, neg, nul);
+    if (n == 7) return op == CLF_OP_GEOM && nul == 0u && rep7_applicable(neg);
     if (op != CLF_OP_GEOM || nul != 0u || n < 4 || n > 2 * kRepMaxLogM) return false;
     RepTable T;
     return rep_table(n, neg, T);
@@ -729,6 +735,7 @@ static long long rep_blocks(int n, int64_t batch) {
 
 int rep_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64_t batch, void* stream) {
     if (n == 9 || n == 10) return split_fwd(n, neg, a, b, c, batch, stream);
+    if (n == 7) return rep7_fwd(neg, a, b, c, batch, stream);
     RepTable T;
     if (!rep_table(n, neg, T)) return set_error(CLF_ERR_UNSUPPORTED, "signature has no real matrix representation");
     hipStream_t s = (hipStream_t)stream;
@@ -756,6 +763,7 @@ int rep_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64
 int rep_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc, float* ga, float* gb, int64_t batch,
             void* stream) {
     if (n == 9 || n == 10) return split_bwd(n, neg, a, b, gc, ga, gb, batch, stream);
+    if (n == 7) return rep7_bwd(neg, a, b, gc, ga, gb, batch, stream);
     RepTable T;
     if (!rep_table(n, neg, T)) return set_error(CLF_ERR_UNSUPPORTED, "signature has no real matrix representation");
     hipStream_t s = (hipStream_t)stream;

@@ -493,3 +493,215 @@ def spin_expm_lanes(biv, masks, degree=8):
         for t in range(4):
             U[4 * t + (l >> 4), l & 15] = e[l, t]
     return U
+
+
+# ---- n = 7 on the 16 x 16 representation (csrc/rep7.hip) -------------------
+# Seven anticommuting real Pauli products on 4 qubits represent every
+# non-degenerate Cl(p, q), p + q = 7, in M_16(R). The labels of the 128 blades
+# span a subspace L of (x, z) space whose x part is all of F_2^4, so each lane x
+# holds the labels (x, z0(x) + v), v in V = {z : (0, z) in L}. When q is odd the
+# pseudoscalar squares to +1 and the generators are chosen with product label
+# (0, 0): phi(e_I) and phi(e_I E) then share a label, V has 4 elements and each
+# label carries one even and one odd blade ("pair" mode). phi alone is not
+# faithful then, but Phi(a) = (phi(a), phi(a^)) is (a^ the grade involution),
+# with Phi^* Phi = 32. When q is even, V has 8 elements and each label one
+# blade; phi is faithful and phi^* phi = 16 ("single" mode). A permutation of
+# the basis, P(x, z) -> P(A x, A^{-T} z), puts V on the low bits of z, so that
+# the lane's W[x][c] = sum_z t[x][z] (-1)^{popc(z & c)} is a small WHT over
+# the low bits of c times a sign that depends on the lane and the high bits of c.
+
+
+def _f2_basis(vecs):
+    """Row-reduced basis (list of ints) of the span of vecs over GF(2)."""
+    basis = []
+    for v in vecs:
+        for b in basis:
+            v = min(v, v ^ b)
+        if v:
+            basis.append(v)
+    return basis
+
+
+def find_generators7(metric):
+    """7 anticommuting real Pauli products on 4 qubits with squares metric[g],
+    whose x parts span F_2^4; for q odd their product label must be (0, 0).
+    Deterministic backtracking."""
+    if len(metric) != 7 or 0 in metric:
+        return None
+    pair = metric.count(-1) % 2 == 1
+    cands = [(x, z) for x in range(16) for z in range(16) if (x or z)]
+
+    def sq(c):
+        return -1 if popc(c[0] & c[1]) & 1 else 1
+
+    def anti(c, d):
+        return (popc(c[1] & d[0]) + popc(d[1] & c[0])) & 1 == 1
+
+    chosen = []
+
+    def rec(g):
+        if g == 7:
+            if len(_f2_basis([cx for cx, _ in chosen])) != 4:
+                return False          # every lane x must hold labels
+            x = z = 0
+            for cx, cz in chosen:
+                x ^= cx
+                z ^= cz
+            return not pair or (x == 0 and z == 0)
+        for c in cands:
+            if sq(c) != metric[g] or not all(anti(c, d) for d in chosen):
+                continue
+            chosen.append(c)
+            if rec(g + 1):
+                return True
+            chosen.pop()
+        return False
+
+    return list(chosen) if rec(0) else None
+
+
+def rep7_transform(gens):
+    """Generators after the basis permutation that puts V = {z : (0, z) in L}
+    on the low bits of z, and dim V."""
+    L = _f2_basis([x | (z << 4) for x, z in gens] + [])
+    # all of L, then its x = 0 part
+    span = {0}
+    for b in L:
+        span |= {s ^ b for s in span}
+    V = _f2_basis(sorted(v >> 4 for v in span if (v & 15) == 0))
+    d = len(V)
+    cols = list(V)
+    for e in (1, 2, 4, 8):
+        if len(_f2_basis(cols + [e])) > len(cols):
+            cols.append(e)
+    assert len(cols) == 4
+
+    def M(v):           # M e_i = cols[i]
+        r = 0
+        for i in range(4):
+            if (v >> i) & 1:
+                r ^= cols[i]
+        return r
+
+    Minv = {M(v): v for v in range(16)}
+    At = lambda x: sum(((popc(cols[i] & x) & 1) << i) for i in range(4))   # A = M^T
+    out = [(At(x), Minv[z]) for x, z in gens]
+    return out, d
+
+
+def rep7_tables(metric):
+    """(pair, ent, zhi): ent[x] = list of (blade, sign, transposed sign) in slot
+    order (pair: slot i -> even blade, odd blade of label (x, zhi << 2 | i);
+    single: slot i -> the blade of label (x, zhi << 3 | i)), zhi[x] the lane's
+    high z bits."""
+    gens = find_generators7(list(metric))
+    if gens is None:
+        return None
+    gens, d = rep7_transform(gens)
+    pair = d == 2
+    label, sign = blade_tables(list(metric), gens)
+    low = (1 << d) - 1
+    ent = [[None] * (8 if pair else 8) for _ in range(16)]
+    zhi = [None] * 16
+    for I, (x, z) in enumerate(label):
+        h = z >> d
+        assert zhi[x] in (None, h)
+        zhi[x] = h
+        ts = sign[I] * (-1 if popc(x & z) & 1 else 1)
+        k = 2 * (z & low) + (popc(I) & 1) if pair else (z & low)
+        assert ent[x][k] is None
+        ent[x][k] = (I, sign[I], ts)
+    return pair, ent, zhi, gens
+
+
+def _wht_small(v):
+    return wht(np.asarray(v))
+
+
+def rep7_lane_T(rows, ent, pair, transposed=False):
+    """Per lane: the small-WHT values T (and T^ in pair mode) of each row.
+    rows (B, 128) -> T (B, 16, 4|8), Th (B, 16, 4) or None."""
+    B = rows.shape[0]
+    si = 2 if transposed else 1
+    if pair:
+        u = np.zeros((B, 16, 4))
+        w = np.zeros((B, 16, 4))
+        for x in range(16):
+            for i in range(4):
+                E, O = ent[x][2 * i], ent[x][2 * i + 1]
+                u[:, x, i] = E[si] * rows[:, E[0]]
+                w[:, x, i] = O[si] * rows[:, O[0]]
+        return _wht_small(u + w), _wht_small(u - w)
+    t = np.zeros((B, 16, 8))
+    for x in range(16):
+        for i in range(8):
+            e = ent[x][i]
+            t[:, x, i] = e[si] * rows[:, e[0]]
+    return _wht_small(t), None
+
+
+def rep7_expand(T, zhi, pair):
+    """W[b][x][c] = (-1)^{popc(zhi(x) & (c >> d))} T[b][x][c & low]."""
+    d = 2 if pair else 3
+    W = np.zeros(T.shape[:2] + (16,))
+    for x in range(16):
+        for c in range(16):
+            s = -1 if popc(zhi[x] & (c >> d)) & 1 else 1
+            W[:, x, c] = s * T[:, x, c & ((1 << d) - 1)]
+    return W
+
+
+def rep7_lane_Q(Wc, zhi, pair):
+    """Q[b][x][i] = sum_c W_c[b][x][c] (-1)^{popc(z_i & c)}, z_i = zhi << d | i."""
+    d = 2 if pair else 3
+    Y = np.zeros(Wc.shape[:2] + (1 << d,))
+    for x in range(16):
+        for c in range(16):
+            s = -1 if popc(zhi[x] & (c >> d)) & 1 else 1
+            Y[:, x, c & ((1 << d) - 1)] += s * Wc[:, x, c]
+    return _wht_small(Y)
+
+
+def rep7_unconvert(Q, Qh, ent, pair):
+    out = np.zeros((Q.shape[0], 128))
+    for x in range(16):
+        if pair:
+            for i in range(4):
+                E, O = ent[x][2 * i], ent[x][2 * i + 1]
+                out[:, E[0]] = E[1] * (Q[:, x, i] + Qh[:, x, i]) / 32.0
+                out[:, O[0]] = O[1] * (Q[:, x, i] - Qh[:, x, i]) / 32.0
+        else:
+            for i in range(8):
+                e = ent[x][i]
+                out[:, e[0]] = e[1] * Q[:, x, i] / 16.0
+    return out
+
+
+def _rep7_product(Xs, tabs, fwd_pairs):
+    """Sum over (X, Y, X transposed conversion, Y transposed conversion) of the
+    blockwise MFMA products, unconverted. X, Y: (4, 128) row groups."""
+    pair, ent, zhi, _ = tabs
+    accs = [0.0, 0.0]
+    for X, Y, tx, ty in fwd_pairs:
+        TX, ThX = rep7_lane_T(X, ent, pair, tx)
+        TY, ThY = rep7_lane_T(Y, ent, pair, ty)
+        accs[0] = accs[0] + mfma_4block_16x16x1(xor_operand(rep7_expand(TX, zhi, pair)),
+                                                xor_operand(rep7_expand(TY, zhi, pair)))
+        if pair:
+            accs[1] = accs[1] + mfma_4block_16x16x1(xor_operand(rep7_expand(ThX, zhi, pair)),
+                                                    xor_operand(rep7_expand(ThY, zhi, pair)))
+    Q = rep7_lane_Q(relayout(accs[0]), zhi, pair)
+    Qh = rep7_lane_Q(relayout(accs[1]), zhi, pair) if pair else None
+    return rep7_unconvert(Q, Qh, ent, pair)
+
+
+def kernel7_fwd(a, b, tabs):
+    """The lanes of one wave on a (4, 128) group: c = a b."""
+    return _rep7_product(None, tabs, [(a, b, False, True)])
+
+
+def kernel7_bwd(a, b, gc, tabs):
+    """ga = Phi^-adjoint(G B^T), gb = Phi^-adjoint(A^T G), scaled like the forward."""
+    ga = _rep7_product(None, tabs, [(gc, b, False, False)])
+    gb = _rep7_product(None, tabs, [(a, gc, True, True)])
+    return ga, gb

@@ -353,3 +353,37 @@ def test_split_fused_matches_pair_sums(metric, monkeypatch):
         monkeypatch.delenv("CLF_SPLIT_PATH")
         assert rel_err(c, c0) <= TOL and rel_err(ga, ga0) <= TOL and rel_err(gb, gb0) <= TOL
         assert torch.equal(ga1, ga) and torch.equal(gb1, gb)
+
+
+ODD7 = [(1,) * (7 - q) + (-1,) * q for q in range(8)] + [(-1, 1, -1, 1, 1, -1, 1)]
+
+
+@pytest.mark.parametrize("metric", ODD7, ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
+@pytest.mark.parametrize("batch", [1, 6, 37])
+def test_n7_matrix_path_geom_parity(metric, batch):
+    """Every non-degenerate n = 7 signature takes the 16 x 16 representation
+    kernels for the geometric product (two matrices per row when q is odd, one
+    when q is even); batches that end inside a four-row group exercise the
+    clamped rows."""
+    e = run_case("geom", metric, batch)
+    assert max(e) <= TOL, e
+
+
+@pytest.mark.parametrize("metric", [(1,) * 6 + (-1,), (1,) * 7], ids=["C2", "+++++++"])
+def test_n7_matrix_path_equals_direct_path(metric, monkeypatch):
+    """C2 shape (batch 65536) and a ragged batch: the n = 7 representation
+    kernels give the per-term kernels' values and gradients (an independent
+    algorithm, CLF_GEOM_PATH=direct), also with one gradient requested; the
+    results are not bit-identical, so the matrix path did run."""
+    for B in (65536, 4099):
+        a, b, gc = (t.cuda() for t in seeded(B, 7, B, 3))
+        print(f"[case] n7 vs direct metric={metric} batch={B}", flush=True)
+        c, ga, gb = _grads("geom", a, b, gc, metric)
+        _, ga1, _ = _grads("geom", a, b, gc, metric, need_b=False)
+        _, _, gb1 = _grads("geom", a, b, gc, metric, need_a=False)
+        monkeypatch.setenv("CLF_GEOM_PATH", "direct")
+        c0, ga0, gb0 = _grads("geom", a, b, gc, metric)
+        monkeypatch.delenv("CLF_GEOM_PATH")
+        assert rel_err(c, c0) <= TOL and rel_err(ga, ga0) <= TOL and rel_err(gb, gb0) <= TOL
+        assert torch.equal(ga1, ga) and torch.equal(gb1, gb)
+        assert not torch.equal(c, c0)

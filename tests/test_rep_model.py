@@ -121,3 +121,57 @@ def test_split_rep_degenerate10(metric9):
     ga, gb = R.degenerate10_bwd(a.numpy(), b.numpy(), gc.numpy(), label, sign)
     np.testing.assert_allclose(ga, aq.grad.numpy(), atol=1e-9)
     np.testing.assert_allclose(gb, bq.grad.numpy(), atol=1e-9)
+
+
+ODD7 = [(1,) * (7 - q) + (-1,) * q for q in range(8)] + [(-1, 1, -1, 1, 1, -1, 1)]
+
+
+@pytest.mark.parametrize("metric", ODD7, ids=lambda m: "".join({1: "+", -1: "-"}[x] for x in m))
+def test_rep7_lane_model(metric):
+    """n = 7 on the 16 x 16 representation (csrc/rep7.hip): pair mode exactly
+    when q is odd; each lane holds 8 blades, all 128 once; the lane's small WHT
+    times its sign pattern is the x-diagonal of phi(a) = sum_I a_I s(I) P(x_I, z_I)
+    (and of phi(a^) in pair mode); the lane dataflow of the kernels (xor-shuffled
+    operands, 4-block MFMA, stride-20 relayout, Q sums, pair combination) gives
+    the oracle's product and both gradients."""
+    metric = list(metric)
+    pair, ent, zhi, gens = R.rep7_tables(metric)
+    assert pair == (metric.count(-1) % 2 == 1)
+    blades = sorted(e[0] for row in ent for e in row)
+    assert blades == list(range(128))
+    label, sign = R.blade_tables(metric, gens)
+    for x in range(16):
+        for k, (I, s, ts) in enumerate(ent[x]):
+            assert label[I][0] == x and sign[I] == s
+            if pair:
+                assert R.popc(I) % 2 == k % 2 and label[I][1] == (zhi[x] << 2 | k // 2)
+            else:
+                assert label[I][1] == (zhi[x] << 3 | k)
+    # generators: anticommuting, squares = metric
+    for g, (gx, gz) in enumerate(gens):
+        P = R.pauli(gx, gz, 16)
+        np.testing.assert_allclose(P @ P, metric[g] * np.eye(16))
+        for h in range(g):
+            Q = R.pauli(*gens[h], 16)
+            np.testing.assert_allclose(P @ Q, -Q @ P)
+    rng = np.random.default_rng(len(metric) + metric.count(-1))
+    a = rng.standard_normal((4, 128))
+    T, Th = R.rep7_lane_T(a, ent, pair)
+    W = R.rep7_expand(T, zhi, pair)
+    hat = np.array([(-1) ** R.popc(I) for I in range(128)])
+    for b_, (rowvals, Wrow) in enumerate([(a, W)] + ([(a * hat, R.rep7_expand(Th, zhi, pair))] if pair else [])):
+        for r in range(2):
+            M = sum(rowvals[r, I] * sign[I] * R.pauli(*label[I], 16) for I in range(128))
+            Wd = np.array([[M[x ^ c, c] for c in range(16)] for x in range(16)])
+            np.testing.assert_allclose(Wrow[r], Wd, atol=1e-12)
+    b = rng.standard_normal((4, 128))
+    gc = rng.standard_normal((4, 128))
+    tabs = (pair, ent, zhi, gens)
+    aq = torch.tensor(a, requires_grad=True)
+    bq = torch.tensor(b, requires_grad=True)
+    c_ref = O.einsum_product("geom", aq, bq, metric)
+    c_ref.backward(torch.tensor(gc))
+    np.testing.assert_allclose(R.kernel7_fwd(a, b, tabs), c_ref.detach().numpy(), atol=1e-10)
+    ga, gb = R.kernel7_bwd(a, b, gc, tabs)
+    np.testing.assert_allclose(ga, aq.grad.numpy(), atol=1e-10)
+    np.testing.assert_allclose(gb, bq.grad.numpy(), atol=1e-10)
