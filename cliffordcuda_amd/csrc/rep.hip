@@ -331,8 +331,8 @@ __global__ __launch_bounds__(256) void rep_bwd_kernel(const float* __restrict__ 
 // the scattered b32 writes and the b128 row reads free of bank conflicts.
 
 template <bool NT>
-__global__ __launch_bounds__(256) void rep16_fwd_kernel(const float* __restrict__ A, const float* __restrict__ B,
-                                                         float* __restrict__ C, long long batch, RepTable T) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void rep16_fwd_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, long long batch, RepTable T) {
     __shared__ float lds[4][2 * 4 * 256];  // per wave: staged a | staged b; later the relayout, then c
     static_assert(2 * 4 * 256 >= kRelayoutFloats, "relayout must fit the wave's LDS slots");
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -350,10 +350,13 @@ __global__ __launch_bounds__(256) void rep16_fwd_kernel(const float* __restrict_
     Pre16 pa = fetch16<NT>(A, row0, batch, lane);
     Pre16 pb = fetch16<NT>(B, row0, batch, lane);
     for (; row0 < batch; row0 += stride) {
+        // the table values are re-derived where they are used rather than kept
+        // in registers across the loop (register pressure sets the occupancy)
+#pragma unroll
+        for (int z = 0; z < 16; ++z) asm volatile("" : "+v"(ent[z]));
         stage16(sa, pa, lane, oddc);
         stage16(sb, pb, lane, oddc);
         pa = fetch16<NT>(A, row0 + stride, batch, lane);
-        pb = fetch16<NT>(B, row0 + stride, batch, lane);
         wave_lds_sync();
         float wa[16], wb[16];
         gather16<0>(sa + rb * 256, ent, wa);
@@ -362,6 +365,9 @@ __global__ __launch_bounds__(256) void rep16_fwd_kernel(const float* __restrict_
         wht_inplace<16>(wa);
         wht_inplace<16>(wb);
         const floatx16 acc = mfma_chain(wa, wb);
+        // b's next rows are requested once the operands are consumed (fewer
+        // registers live across the product)
+        pb = fetch16<NT>(B, row0 + stride, batch, lane);
         relayout_store(sa, acc, lane);
         wave_lds_sync();
         float wc[16];
@@ -375,19 +381,18 @@ __global__ __launch_bounds__(256) void rep16_fwd_kernel(const float* __restrict_
 }
 
 template <bool NT>
-__global__ __launch_bounds__(256) void rep16_bwd_kernel(const float* __restrict__ A, const float* __restrict__ B,
-                                                         const float* __restrict__ GC, float* __restrict__ GA,
-                                                         float* __restrict__ GB, long long batch, RepTable T) {
-    __shared__ float lds[4][3 * 4 * 256];  // per wave: staged a | b | gc; later two relayouts, then ga | gb
-    static_assert(3 * 4 * 256 >= 2 * kRelayoutFloats, "both relayouts must fit the wave's LDS slots");
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void rep16_bwd_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ GC, float* __restrict__ GA,
+    float* __restrict__ GB, long long batch, RepTable T) {
+    // per wave: gc | b, then a over b | scratch for each gradient's relayout and
+    // its rows in blade order; only two converted operands are live at a time
+    __shared__ float lds[4][2 * 4 * 256 + kRelayoutFloats];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const unsigned x = lane & 15u;
     const int rb = lane >> 4;
-    float* sa = &lds[wave][0];
-    float* sb = sa + 4 * 256;
-    float* sg = sb + 4 * 256;
-    float* rel_a = sa;                          // relayout of dA: 4 * 320 floats
-    float* rel_b = sa + 4 * kRelayoutBlock;     // relayout of dB: next 4 * 320 floats
+    float* s0 = &lds[wave][0];
+    float* s1 = s0 + 4 * 256;
+    float* sr = s1 + 4 * 256;
     const unsigned oddx = (rb & 1) ? T.odd_xor : 0u, oddc = T.odd_xor >> 2;
     unsigned ent[16];
 #pragma unroll
@@ -396,45 +401,57 @@ __global__ __launch_bounds__(256) void rep16_bwd_kernel(const float* __restrict_
 
     const long long stride = (long long)gridDim.x * 4 * 4;
     long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
-    Pre16 pa = fetch16<NT>(A, row0, batch, lane);
+    // gc and b of a group are loaded while the previous group's dB runs, a
+    // while the group's dA runs
     Pre16 pb = fetch16<NT>(B, row0, batch, lane);
     Pre16 pg = fetch16<NT>(GC, row0, batch, lane);
     for (; row0 < batch; row0 += stride) {
-        stage16(sa, pa, lane, oddc);
-        stage16(sb, pb, lane, oddc);
-        stage16(sg, pg, lane, oddc);
-        pa = fetch16<NT>(A, row0 + stride, batch, lane);
-        pb = fetch16<NT>(B, row0 + stride, batch, lane);
-        pg = fetch16<NT>(GC, row0 + stride, batch, lane);
-        wave_lds_sync();
+        // the table values are re-derived where they are used rather than kept
+        // in registers across the loop (register pressure sets the occupancy)
+#pragma unroll
+        for (int z = 0; z < 16; ++z) asm volatile("" : "+v"(ent[z]));
         // dA = G B^T: operands W_g, W_b.  dB = A^T G: operands W'_a, W'_g.
-        float wg[16], wgt[16], wb[16], wat[16];
-        gather16_pair(sg + rb * 256, ent, wg, wgt);
-        if (want_a) gather16<0>(sb + rb * 256, ent, wb);
-        if (want_b) gather16<1>(sa + rb * 256, ent, wat);
+        stage16(s0, pg, lane, oddc);
+        stage16(s1, pb, lane, oddc);
+        const Pre16 pa = fetch16<NT>(A, row0, batch, lane);
         wave_lds_sync();
         if (want_a) {
+            float wg[16], wb[16];
+            gather16<0>(s0 + rb * 256, ent, wg);
+            gather16<0>(s1 + rb * 256, ent, wb);
             wht_inplace<16>(wg);
             wht_inplace<16>(wb);
             const floatx16 acc = mfma_chain(wg, wb);
-            relayout_store(rel_a, acc, lane);
+            relayout_store(sr, acc, lane);
+            wave_lds_sync();
+            float da[16];
+            relayout_load(sr, rb, x, da);
+            wave_lds_sync();
+            unconvert16(da, sr + rb * 256, ent);
+            wave_lds_sync();
+            store16<NT>(GA, sr, row0, batch, lane, oddc);
         }
+        wave_lds_sync();
+        stage16(s1, pa, lane, oddc);
+        pg = fetch16<NT>(GC, row0 + stride, batch, lane);
+        pb = fetch16<NT>(B, row0 + stride, batch, lane);
+        wave_lds_sync();
         if (want_b) {
+            float wat[16], wgt[16];
+            gather16<1>(s1 + rb * 256, ent, wat);
+            gather16<1>(s0 + rb * 256, ent, wgt);
             wht_inplace<16>(wat);
             wht_inplace<16>(wgt);
             const floatx16 acc = mfma_chain(wat, wgt);
-            relayout_store(rel_b, acc, lane);
+            relayout_store(sr, acc, lane);
+            wave_lds_sync();
+            float db[16];
+            relayout_load(sr, rb, x, db);
+            wave_lds_sync();
+            unconvert16(db, sr + rb * 256, ent);
+            wave_lds_sync();
+            store16<NT>(GB, sr, row0, batch, lane, oddc);
         }
-        wave_lds_sync();
-        float da[16], db[16];
-        if (want_a) relayout_load(rel_a, rb, x, da);
-        if (want_b) relayout_load(rel_b, rb, x, db);
-        wave_lds_sync();
-        if (want_a) unconvert16(da, sa + rb * 256, ent);
-        if (want_b) unconvert16(db, sb + rb * 256, ent);
-        wave_lds_sync();
-        if (want_a) store16<NT>(GA, sa, row0, batch, lane, oddc);
-        if (want_b) store16<NT>(GB, sb, row0, batch, lane, oddc);
         wave_lds_sync();
     }
 }
@@ -514,10 +531,9 @@ __global__ __launch_bounds__(256) void rep16_bcast_fwd_kernel(const float* __res
 
 // parts[blockIdx.x * 256 + r * 16 + c]: the workgroup's sum of the 16x16 weight-gradient products
 template <int SIDE, bool NT>
-__global__ __launch_bounds__(256) void rep16_bcast_bwd_kernel(const float* __restrict__ X, const float* __restrict__ W,
-                                                               const float* __restrict__ GY, float* __restrict__ GX,
-                                                               float* __restrict__ parts, long long batch,
-                                                               RepTable T) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void rep16_bcast_bwd_kernel(
+    const float* __restrict__ X, const float* __restrict__ W, const float* __restrict__ GY, float* __restrict__ GX,
+    float* __restrict__ parts, long long batch, RepTable T) {
     __shared__ float lds[4][2 * 4 * 256];  // per wave: staged x | staged gy; later relayout, then gx rows
     static_assert(2 * 4 * 256 >= kRelayoutFloats, "relayout must fit the wave's LDS slots");
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -542,21 +558,24 @@ __global__ __launch_bounds__(256) void rep16_bcast_bwd_kernel(const float* __res
     Pre16 px = fetch16<NT>(X, row0, batch, lane);
     Pre16 pg = fetch16<NT>(GY, row0, batch, lane);
     for (; row0 < batch; row0 += stride) {
+        // the table values are re-derived where they are used rather than kept
+        // in registers across the loop (register pressure sets the occupancy)
+#pragma unroll
+        for (int z = 0; z < 16; ++z) asm volatile("" : "+v"(ent[z]));
         stage16(sx, px, lane, oddc);
         stage16(sg, pg, lane, oddc);
         px = fetch16<NT>(X, row0 + stride, batch, lane);
-        pg = fetch16<NT>(GY, row0 + stride, batch, lane);
         wave_lds_sync();
-        // gy in both sign conventions; x as the weight-gradient operand
-        // (side 0: A = row of phi(x)^T, transposed signs; side 1: B = column of phi(x)^T = row of phi(x))
-        float wg[16], wgt[16], wx[16];
-        gather16_pair(sg + rb * 256, ent, wg, wgt);
-        if (want_w) gather16<SIDE == 0 ? 1 : 0>(sx + rb * 256, ent, wx);
-        wave_lds_sync();
-        wht_inplace<16>(wg);
-        wht_inplace<16>(wgt);
+        // weight gradient first (x as its operand: side 0: A = row of phi(x)^T,
+        // transposed signs, with gy in transposed signs; side 1: B = column of
+        // phi(x)^T = row of phi(x), with gy in plain signs), then gx from gy in
+        // the other convention; one converted pair is live at a time
         if (want_w) {
+            float wx[16], wgw[16];
+            gather16<SIDE == 0 ? 1 : 0>(sx + rb * 256, ent, wx);
+            gather16<SIDE == 0 ? 1 : 0>(sg + rb * 256, ent, wgw);
             wht_inplace<16>(wx);
+            wht_inplace<16>(wgw);
             // rows past the end are clamped copies of the last row: zero their
             // contribution to the sum (whole 16-lane blocks, so every lane's
             // operand is zero for those blocks)
@@ -565,16 +584,21 @@ __global__ __launch_bounds__(256) void rep16_bcast_bwd_kernel(const float* __res
                 for (int k = 0; k < 16; ++k) wx[k] = 0.f;
             }
             if constexpr (SIDE == 0)
-                accw = mfma_chain_pre<true, true>(accw, wx, wgt, std::make_integer_sequence<unsigned, 16>{});
+                accw = mfma_chain_pre<true, true>(accw, wx, wgw, std::make_integer_sequence<unsigned, 16>{});
             else
-                accw = mfma_chain_pre<true, true>(accw, wg, wx, std::make_integer_sequence<unsigned, 16>{});
+                accw = mfma_chain_pre<true, true>(accw, wgw, wx, std::make_integer_sequence<unsigned, 16>{});
         }
+        pg = fetch16<NT>(GY, row0 + stride, batch, lane);
+        wave_lds_sync();
         if (want_x) {
+            float wgx[16];
+            gather16<SIDE == 0 ? 0 : 1>(sg + rb * 256, ent, wgx);
+            wht_inplace<16>(wgx);
             floatx16 acc;
             if constexpr (SIDE == 0)
-                acc = mfma_chain_pre<true, false>(zero, wg, wop, std::make_integer_sequence<unsigned, 16>{});
+                acc = mfma_chain_pre<true, false>(zero, wgx, wop, std::make_integer_sequence<unsigned, 16>{});
             else
-                acc = mfma_chain_pre<false, true>(zero, wop, wgt, std::make_integer_sequence<unsigned, 16>{});
+                acc = mfma_chain_pre<false, true>(zero, wop, wgx, std::make_integer_sequence<unsigned, 16>{});
             relayout_store(sx, acc, lane);
             wave_lds_sync();
             float wc[16];

@@ -167,18 +167,6 @@ __device__ __forceinline__ void gather16(const float* __restrict__ row, const un
         w[z] = __uint_as_float(__float_as_uint(row[ent[z] & 0xffffu]) ^ ((ent[z] << SIGNSHIFT) & 0x80000000u));
 }
 
-// both sign conventions of one row from one LDS read per blade: wa with s(I)
-// (gather16<0>), wb with the transposed conversion's sign (gather16<1>)
-__device__ __forceinline__ void gather16_pair(const float* __restrict__ row, const unsigned (&ent)[16], float (&wa)[16],
-                                              float (&wb)[16]) {
-#pragma unroll
-    for (int z = 0; z < 16; ++z) {
-        const unsigned v = __float_as_uint(row[ent[z] & 0xffffu]);
-        wa[z] = __uint_as_float(v ^ (ent[z] & 0x80000000u));
-        wb[z] = __uint_as_float(v ^ ((ent[z] << 1) & 0x80000000u));
-    }
-}
-
 // inverse WHT of W_c[x][.], scale 1/16, scatter s(I) t[z] into the row's blade slots
 __device__ __forceinline__ void unconvert16(float (&w)[16], float* __restrict__ row, const unsigned (&ent)[16]) {
     wht_inplace<16>(w);
