@@ -118,44 +118,12 @@ __device__ __forceinline__ void gather7_pair(const float* __restrict__ row, cons
     wht_inplace<4>(th);
 }
 
-// both sign conventions from one read per blade (the upstream gradient feeds
-// both backward products)
-__device__ __forceinline__ void gather7_pair2(const float* __restrict__ row, const unsigned (&ent)[8], float (&t)[4],
-                                              float (&th)[4], float (&tt)[4], float (&tth)[4]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float a = row[ent[2 * i] & 0x7fu], b = row[ent[2 * i + 1] & 0x7fu];
-        const float u = sgn7(a, ent[2 * i], 0), w = sgn7(b, ent[2 * i + 1], 0);
-        const float ut = sgn7(a, ent[2 * i], 1), wt = sgn7(b, ent[2 * i + 1], 1);
-        t[i] = u + w;
-        th[i] = u - w;
-        tt[i] = ut + wt;
-        tth[i] = ut - wt;
-    }
-    wht_inplace<4>(t);
-    wht_inplace<4>(th);
-    wht_inplace<4>(tt);
-    wht_inplace<4>(tth);
-}
-
 // Single mode: t = WHT8 of the lane's eight blades.
 template <int SIGNSHIFT>
 __device__ __forceinline__ void gather7_single(const float* __restrict__ row, const unsigned (&ent)[8], float (&t)[8]) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) t[i] = sgn7(row[ent[i] & 0x7fu], ent[i], SIGNSHIFT);
     wht_inplace<8>(t);
-}
-
-__device__ __forceinline__ void gather7_single2(const float* __restrict__ row, const unsigned (&ent)[8], float (&t)[8],
-                                                float (&tt)[8]) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float v = row[ent[i] & 0x7fu];
-        t[i] = sgn7(v, ent[i], 0);
-        tt[i] = sgn7(v, ent[i], 1);
-    }
-    wht_inplace<8>(t);
-    wht_inplace<8>(tt);
 }
 
 // W[x][c] = s_x(c >> D) T[c & (2^D - 1)]; sm[m] holds s_x(m) as a sign bit (sm[0] = 0)
@@ -275,21 +243,23 @@ __global__ __launch_bounds__(256) void rep7_fwd_kernel(const float* __restrict__
 }
 
 // Backward: ga from (gc, b) with gc in the s(I) convention and b in s(I);
-// gb from (a, gc) both in the transposed convention.
+// gb from (a, gc) both in the transposed convention. The gradients run one
+// after the other: gc and b are staged first (a is loaded meanwhile), then a
+// over b, and each gradient's relayout and rows in blade order use a scratch
+// slot, so few converted operands are live at once.
 template <bool PAIR, bool NT>
-__global__ __launch_bounds__(256) void rep7_bwd_kernel(const float* __restrict__ A, const float* __restrict__ B,
-                                                        const float* __restrict__ GC, float* __restrict__ GA,
-                                                        float* __restrict__ GB, long long batch, Rep7Table T) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void rep7_bwd_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ GC, float* __restrict__ GA,
+    float* __restrict__ GB, long long batch, Rep7Table T) {
     constexpr int D = PAIR ? 2 : 3;
     constexpr int L = 1 << D;
-    __shared__ float lds[4][3 * kRep7GroupFloats];  // per wave: staged a | b | gc; later the relayout, then ga | gb
-    static_assert(3 * kRep7GroupFloats >= kRelayoutFloats, "the relayout must fit the wave's LDS slots");
+    __shared__ float lds[4][2 * kRep7GroupFloats + kRelayoutFloats];  // per wave: gc | b, then a | scratch
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const unsigned x = lane & 15u;
     const int rb = lane >> 4;
-    float* sa = &lds[wave][0];
-    float* sb = sa + kRep7GroupFloats;
-    float* sg = sb + kRep7GroupFloats;
+    float* sg = &lds[wave][0];
+    float* sx = sg + kRep7GroupFloats;
+    float* sr = sx + kRep7GroupFloats;
     const unsigned oddc = T.odd_xor >> 2;
     unsigned ent[8], sm[16 >> D];
     lane_consts7<D>(T, x, rb, ent, sm);
@@ -297,49 +267,60 @@ __global__ __launch_bounds__(256) void rep7_bwd_kernel(const float* __restrict__
 
     const long long stride = (long long)gridDim.x * 16;
     long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
-    Pre7 pa = fetch7<NT>(A, row0, batch, lane);
     Pre7 pb = fetch7<NT>(B, row0, batch, lane);
     Pre7 pg = fetch7<NT>(GC, row0, batch, lane);
     for (; row0 < batch; row0 += stride) {
-        stage7(sa, pa, lane, oddc);
-        stage7(sb, pb, lane, oddc);
+        // the table values are re-derived where they are used rather than kept
+        // in registers across the loop (register pressure sets the occupancy)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) asm volatile("" : "+v"(ent[k]));
         stage7(sg, pg, lane, oddc);
-        pa = fetch7<NT>(A, row0 + stride, batch, lane);
-        pb = fetch7<NT>(B, row0 + stride, batch, lane);
-        pg = fetch7<NT>(GC, row0 + stride, batch, lane);
+        stage7(sx, pb, lane, oddc);
+        const Pre7 pa = fetch7<NT>(A, row0, batch, lane);
         wave_lds_sync();
-        float qa[L], qb[L];
-        if constexpr (PAIR) {
-            float tg[4], tgh[4], tgt[4], tgth[4], tb[4], tbh[4], tat[4], tath[4];
-            gather7_pair2(sg + rb * kRep7Dim, ent, tg, tgh, tgt, tgth);
-            if (want_a) gather7_pair<0>(sb + rb * kRep7Dim, ent, tb, tbh);
-            if (want_b) gather7_pair<1>(sa + rb * kRep7Dim, ent, tat, tath);
-            wave_lds_sync();
-            float qah[4], qbh[4];
-            if (want_a) {
-                product_q7<2>(sa, tg, tb, sm, lane, rb, x, qa);
-                product_q7<2>(sa, tgh, tbh, sm, lane, rb, x, qah);
+        if (want_a) {
+            float q[L];
+            if constexpr (PAIR) {
+                float tg[4], tgh[4], tb[4], tbh[4], qh[4];
+                gather7_pair<0>(sg + rb * kRep7Dim, ent, tg, tgh);
+                gather7_pair<0>(sx + rb * kRep7Dim, ent, tb, tbh);
+                product_q7<2>(sr, tg, tb, sm, lane, rb, x, q);
+                product_q7<2>(sr, tgh, tbh, sm, lane, rb, x, qh);
+                scatter7_pair(sr + rb * kRep7Dim, ent, q, qh);
+            } else {
+                float tg[8], tb[8];
+                gather7_single<0>(sg + rb * kRep7Dim, ent, tg);
+                gather7_single<0>(sx + rb * kRep7Dim, ent, tb);
+                product_q7<3>(sr, tg, tb, sm, lane, rb, x, q);
+                scatter7_single(sr + rb * kRep7Dim, ent, q);
             }
-            if (want_b) {
-                product_q7<2>(sa, tat, tgt, sm, lane, rb, x, qb);
-                product_q7<2>(sa, tath, tgth, sm, lane, rb, x, qbh);
-            }
-            if (want_a) scatter7_pair(sa + rb * kRep7Dim, ent, qa, qah);
-            if (want_b) scatter7_pair(sb + rb * kRep7Dim, ent, qb, qbh);
-        } else {
-            float tg[8], tgt[8], tb[8], tat[8];
-            gather7_single2(sg + rb * kRep7Dim, ent, tg, tgt);
-            if (want_a) gather7_single<0>(sb + rb * kRep7Dim, ent, tb);
-            if (want_b) gather7_single<1>(sa + rb * kRep7Dim, ent, tat);
             wave_lds_sync();
-            if (want_a) product_q7<3>(sa, tg, tb, sm, lane, rb, x, qa);
-            if (want_b) product_q7<3>(sa, tat, tgt, sm, lane, rb, x, qb);
-            if (want_a) scatter7_single(sa + rb * kRep7Dim, ent, qa);
-            if (want_b) scatter7_single(sb + rb * kRep7Dim, ent, qb);
+            store7<NT>(GA, sr, row0, batch, lane, oddc);
         }
         wave_lds_sync();
-        if (want_a) store7<NT>(GA, sa, row0, batch, lane, oddc);
-        if (want_b) store7<NT>(GB, sb, row0, batch, lane, oddc);
+        stage7(sx, pa, lane, oddc);
+        pg = fetch7<NT>(GC, row0 + stride, batch, lane);
+        pb = fetch7<NT>(B, row0 + stride, batch, lane);
+        wave_lds_sync();
+        if (want_b) {
+            float q[L];
+            if constexpr (PAIR) {
+                float tat[4], tath[4], tgt[4], tgth[4], qh[4];
+                gather7_pair<1>(sx + rb * kRep7Dim, ent, tat, tath);
+                gather7_pair<1>(sg + rb * kRep7Dim, ent, tgt, tgth);
+                product_q7<2>(sr, tat, tgt, sm, lane, rb, x, q);
+                product_q7<2>(sr, tath, tgth, sm, lane, rb, x, qh);
+                scatter7_pair(sr + rb * kRep7Dim, ent, q, qh);
+            } else {
+                float tat[8], tgt[8];
+                gather7_single<1>(sx + rb * kRep7Dim, ent, tat);
+                gather7_single<1>(sg + rb * kRep7Dim, ent, tgt);
+                product_q7<3>(sr, tat, tgt, sm, lane, rb, x, q);
+                scatter7_single(sr + rb * kRep7Dim, ent, q);
+            }
+            wave_lds_sync();
+            store7<NT>(GB, sr, row0, batch, lane, oddc);
+        }
         wave_lds_sync();
     }
 }

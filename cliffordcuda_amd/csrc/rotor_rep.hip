@@ -46,8 +46,8 @@ __device__ __forceinline__ void load_spin_operand(const float* __restrict__ U, u
 // transpose of the action). vop[k] = V[k][x] is both the B operand of
 // phi(x) V and the A operand of V^T (phi(x) V).
 template <bool TRANS, bool NT>
-__global__ __launch_bounds__(256) void rotor16_apply_kernel(const float* __restrict__ U, const float* __restrict__ X,
-                                                             float* __restrict__ Y, long long batch, RepTable T) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void rotor16_apply_kernel(
+    const float* __restrict__ U, const float* __restrict__ X, float* __restrict__ Y, long long batch, RepTable T) {
     // per wave: staged x rows (1024 floats); later the relayout (1280), then y rows
     __shared__ float lds[4][kRelayoutFloats];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -66,6 +66,10 @@ __global__ __launch_bounds__(256) void rotor16_apply_kernel(const float* __restr
     long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
     Pre16 px = fetch16<NT>(X, row0, batch, lane);
     for (; row0 < batch; row0 += stride) {
+        // the table values are re-derived where they are used rather than kept
+        // in registers across the loop (register pressure sets the occupancy)
+#pragma unroll
+        for (int z = 0; z < 16; ++z) asm volatile("" : "+v"(ent[z]));
         stage16(sx, px, lane, oddc);
         px = fetch16<NT>(X, row0 + stride, batch, lane);
         wave_lds_sync();
@@ -125,6 +129,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void r
     Pre16 px = fetch16<NT>(X, row0, batch, lane);
     Pre16 pg = fetch16<NT>(GY, row0, batch, lane);
     for (; row0 < batch; row0 += stride) {
+#pragma unroll
+        for (int z = 0; z < 16; ++z) asm volatile("" : "+v"(ent[z]));  // as in rotor16_apply_kernel
         stage16(sx, px, lane, oddc);
         stage16(sg, pg, lane, oddc);
         px = fetch16<NT>(X, row0 + stride, batch, lane);
