@@ -511,34 +511,48 @@ struct BalSched {
     int last_lane;    // last lane holding pairs of olast
 };
 
+// The schedule is the same for every row; the NB lanes of a row compute it
+// together: lane lr counts the pairs of output lr, a segmented scan gives the
+// output offsets, and binary searches over them (lane shuffles) find the
+// outputs holding the lane's first and last pair.
+__device__ __forceinline__ int bal_largest_le(int pre, int v, unsigned NB) {
+    // largest output o with pre[o] <= v (pre non-decreasing, pre[0] = 0)
+    int lo = 0;
+    for (int step = (int)NB >> 1; step > 0; step >>= 1) {
+        const int cand = __shfl(pre, lo + step, (int)NB);
+        if (cand <= v) lo += step;
+    }
+    return lo;
+}
+
 template <int OP, int ROLE, int CLS>
 __device__ __forceinline__ BalSched bal_schedule(unsigned lr, unsigned NB, unsigned nul) {
     const unsigned full = NB - 1u;
-    int total = 0;
-    for (unsigned o = 0; o < NB; ++o) total += bal_family<OP, ROLE, CLS>(o, full, nul).count;
+    const int c = bal_family<OP, ROLE, CLS>(lr, full, nul).count;
+    int inc = c;  // inclusive scan of the counts over the row's lanes
+    for (int d = 1; d < (int)NB; d <<= 1) {
+        const int v = __shfl_up(inc, (unsigned)d, (int)NB);
+        if ((int)lr >= d) inc += v;
+    }
+    const int pre = inc - c;
+    const int total = __shfl(inc, (int)NB - 1, (int)NB);
     BalSched sc;
     sc.T = (total + (int)NB - 1) / (int)NB;
     sc.p0 = (int)lr * sc.T;
     sc.p1 = sc.p0 + sc.T < total ? sc.p0 + sc.T : total;
     if (sc.p1 < sc.p0) sc.p1 = sc.p0;
-    sc.o0 = 0u;
-    sc.s0 = 0;
-    sc.olast = 0u;
-    int pre = 0, last_end = 0;
-    for (unsigned o = 0; o < NB; ++o) {
-        const int c = bal_family<OP, ROLE, CLS>(o, full, nul).count;
-        if (sc.p0 >= pre && sc.p0 < pre + c) {
-            sc.o0 = o;
-            sc.s0 = sc.p0 - pre;
-        }
-        if (sc.p1 - 1 >= pre && sc.p1 - 1 < pre + c) {
-            sc.olast = o;
-            last_end = pre + c;
-        }
-        pre += c;
-    }
+    // every lane takes part in the shuffles; lanes without pairs discard them
+    const int o0 = bal_largest_le(pre, sc.p0, NB);
+    const int ol = bal_largest_le(pre, sc.p1 - 1, NB);
+    const int pre_o0 = __shfl(pre, o0, (int)NB);
+    const int end_ol = __shfl(inc, ol, (int)NB);
+    const bool has = sc.p1 > sc.p0;
+    sc.o0 = has ? (unsigned)o0 : 0u;
+    sc.s0 = has ? sc.p0 - pre_o0 : 0;
+    sc.olast = has ? (unsigned)ol : 0u;
+    const int last_end = has ? end_ol : 0;
     sc.cont0 = sc.s0 > 0;
-    sc.tail = sc.p1 > sc.p0 && sc.p1 < last_end && !(sc.olast == sc.o0 && sc.cont0);
+    sc.tail = has && sc.p1 < last_end && !(sc.olast == sc.o0 && sc.cont0);
     sc.last_lane = sc.T > 0 ? (last_end - 1) / sc.T : 0;
     return sc;
 }
