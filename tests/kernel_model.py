@@ -329,6 +329,45 @@ def bal_schedule(op, role, NB, cls=0, nul=0):
     return T, lanes, pre
 
 
+def bal_schedule_lanes(op, role, NB, cls=0, nul=0):
+    """The kernel's computation of the same schedule (bal_schedule in
+    csrc/products.hip): lane lr counts output lr's pairs, a shuffle-up
+    inclusive scan over the NB lanes, then a binary search with shuffles for
+    the largest output whose exclusive offset is <= p0 (and p1 - 1)."""
+    full = NB - 1
+    c = [bal_family(op, role, lr, full, cls, nul)[3] for lr in range(NB)]
+    inc = list(c)
+    d = 1
+    while d < NB:
+        inc = [inc[lr] + (inc[lr - d] if lr >= d else 0) for lr in range(NB)]
+        d *= 2
+    pre = [inc[lr] - c[lr] for lr in range(NB)]
+    total = inc[NB - 1]
+    T = -(-total // NB)
+
+    def largest_le(v):
+        lo, step = 0, NB // 2
+        while step > 0:
+            if pre[lo + step] <= v:
+                lo += step
+            step //= 2
+        return lo
+
+    lanes = []
+    for lr in range(NB):
+        p0, p1 = lr * T, min(lr * T + T, total)
+        if p1 <= p0:
+            lanes.append(None)
+            continue
+        o0, ol = largest_le(p0), largest_le(p1 - 1)
+        s0 = p0 - pre[o0]
+        last_end = inc[ol]
+        tail = p1 < last_end and not (ol == o0 and s0 > 0)
+        lanes.append(dict(p0=p0, p1=p1, o0=o0, s0=s0, cont0=s0 > 0, tail=tail, olast=ol,
+                          last_lane=(last_end - 1) // T))
+    return T, lanes
+
+
 def bal_run(op, role, NB, pair_value, cls=0, nul=0):
     """Emulate the lanes of one row for one class: pair_value(o, part) ->
     contribution (16,) array (zero for pairs the metric kills). Returns out[o]

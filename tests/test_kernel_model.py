@@ -68,7 +68,8 @@ def test_balanced_schedule_covers_every_valid_pair_once(op):
     generator are left out), each once; an output of a stored op with no valid
     pair gets exactly one (zero) pair so that it is written; inner's classes
     hold the pairs of one low-block pattern each; the lanes' ranges with
-    heads/tails rebuild each output once."""
+    heads/tails rebuild each output once; the kernel's lane-parallel schedule
+    (scan + binary search) equals the reference schedule."""
     rng = np.random.default_rng(op)
     for n in range(4, 11):
         NB = 1 << (n - 4)
@@ -112,5 +113,12 @@ def test_balanced_schedule_covers_every_valid_pair_once(op):
                             ref[o] = ref[o] + sum(vals[(o, part)] for part in parts)
                     T, lanes, pre = K.bal_schedule(op, role, NB, cls, nul)
                     assert T * NB >= pre[-1] > (T - 1) * NB or pre[-1] == 0
+                    # the kernel's lane-parallel computation gives the same schedule
+                    T2, lanes2 = K.bal_schedule_lanes(op, role, NB, cls, nul)
+                    assert T2 == T and len(lanes2) == len(lanes)
+                    for l1, l2 in zip(lanes, lanes2):
+                        assert (l1 is None) == (l2 is None)
+                        if l1 is not None:
+                            assert {k: int(v) for k, v in l1.items()} == {k: int(v) for k, v in l2.items()}
                 for o in range(NB):
                     np.testing.assert_allclose(total[o], ref[o], atol=1e-12)
