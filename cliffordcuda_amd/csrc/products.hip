@@ -429,10 +429,14 @@ __global__ __launch_bounds__(256) void prod_bwd_blk(const float* __restrict__ A,
 // of the left operand), partner jh; ROLE 2: output jh, partner ih. The
 // partners of an output are a family {base | S}: the subsets S of mask in
 // increasing order (S <- (S - mask) & mask), from index `first`, `count` of
-// them. The inner product runs three rounds, one per low-block pattern
-// (CLS 0: ih strictly inside jh, lc pattern; CLS 1: jh strictly inside ih, rc
-// pattern; CLS 2: ih = jh, both), so the lanes of a round never diverge on the
-// pattern; its rounds add into an LDS copy of the output rows, stored at the end.
+// them. The inner product's backward runs three rounds, one per low-block
+// pattern (CLS 0: ih strictly inside jh, lc pattern; CLS 1: jh strictly inside
+// ih, rc pattern; CLS 2: ih = jh, both), so the lanes of a round never diverge
+// on the pattern; its rounds add into an LDS copy of the output rows, stored at
+// the end. Its forward runs one round (CLS 3): every pair (o, S) computes both
+// the lc half (S, S | o) and the rc half (S | o, S), which have the same
+// partner family, and for o = 0 the terms both halves share (il = jl) are
+// taken off the scalar slot once.
 // Layout: a wave owns groups of 1024 floats per operand (R = 1024 / D rows,
 // NB lanes per row) in wave-private LDS and walks the groups with a grid
 // stride, loading the next group into registers while it computes.
@@ -471,6 +475,9 @@ __device__ __forceinline__ BalFam bal_family(unsigned o, unsigned full, unsigned
         return onul ? BalFam{o, 0u, 0, 1} : BalFam{o, co, 0, nco};
     }
     if (OP == OP_REGR) return BalFam{co, o, 0, no};
+    // inner, fused forward round: output o, partners S (ih = S, jh = S | o for the
+    // lc half, ih = S | o, jh = S for the rc half)
+    if (CLS == 3) return BalFam{0u, con, 0, ncon};
     // inner, by class; strict: the subsets of onn strictly inside o
     const int strict = nonn - (onul ? 0 : 1);
     if (CLS == 0) {  // ih strictly inside jh
@@ -584,7 +591,18 @@ __device__ __forceinline__ void add_blk(float4* __restrict__ out, unsigned blk, 
 // low-block pattern of a pair: the op's, or for the inner product its class's
 template <int OP, int CLS>
 constexpr int bal_variant() {
-    return OP != OP_INNER ? OP : (CLS == 0 ? LV_LC : (CLS == 1 ? LV_RC : LV_INNER));
+    return OP != OP_INNER ? OP : (CLS == 0 || CLS == 3 ? LV_LC : (CLS == 1 ? LV_RC : LV_INNER));
+}
+
+// sum_l s_lo(l, l) a[l] b[l]: the terms the lc and rc low patterns share
+template <bool LOWNEG, int... L>
+__device__ __forceinline__ float lowblock_diag(const float (&a)[16], const float (&b)[16],
+                                               std::integer_sequence<int, L...>) {
+    float e = 0.f;
+    ((e = low_sign(LV_LC, LOWNEG, (unsigned)L, (unsigned)L) > 0 ? __builtin_fmaf(a[L], b[L], e)
+                                                                 : __builtin_fmaf(-a[L], b[L], e)),
+     ...);
+    return e;
 }
 
 // One role (and class) over one row: la / lb / lg are the row's staged
@@ -613,7 +631,32 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
     for (int t = 0; t < sc.T; ++t) {
         if (p >= sc.p1) break;
         const unsigned part = f.base | S;
-        if (ROLE == 0) {
+        if (OP == OP_INNER && CLS == 3) {
+            // lc half: (S, S | o), lc low pattern; rc half: (S | o, S), rc low
+            // pattern. For o = 0 both halves are (S, S) and count the terms with
+            // il = jl twice: those are taken off the scalar slot once.
+            const HiSign hl = hi_sign<OP>(part, part ^ o, P.negh, P.nulh, full, P.nm1, P.mu);
+            const HiSign hr = hi_sign<OP>(part ^ o, part, P.negh, P.nulh, full, P.nm1, P.mu);
+            {
+                float av[16], bv[16];
+                load_blk(la, part, av);
+                load_blk(lb, part ^ o, bv);
+                const unsigned m = hl.valid ? hl.mask : 0u;
+                apply_flips(bv, m, m ^ (cross_pi<OP>(part, P.nm1) << 31));
+                if (hl.valid) {
+                    lowblock_fwd<LV_LC, kLowNeg>(acc, av, bv);
+                    const float e = lowblock_diag<kLowNeg>(av, bv, std::make_integer_sequence<int, 16>{});
+                    acc[0] = __builtin_fmaf(o == 0u ? -1.f : 0.f, e, acc[0]);
+                }
+            }
+            if (hr.valid) {
+                float av[16], bv[16];
+                load_blk(la, part ^ o, av);
+                load_blk(lb, part, bv);
+                apply_flips(bv, hr.mask, hr.mask ^ (cross_pi<OP>(part ^ o, P.nm1) << 31));
+                lowblock_fwd<LV_RC, kLowNeg>(acc, av, bv);
+            }
+        } else if (ROLE == 0) {
             const unsigned ih = part, jh = part ^ o;
             const HiSign hs = hi_sign<OP>(ih, jh, P.negh, P.nulh, full, P.nm1, P.mu);
             if (hs.valid) {
@@ -777,7 +820,10 @@ constexpr int bal_regions() {
 template <int OP, bool LOWNEG>
 __global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A, const float* __restrict__ B,
                                                      float* __restrict__ C, BlkParams P) {
-    __shared__ float4 lds[4][bal_regions<OP>() * kBalGroupF4];
+    // LDS per wave: a | b | heads. The inner product runs its fused round
+    // (class 3: lc and rc halves of every pair), so every op stores directly.
+    constexpr int kCls = OP == OP_INNER ? 3 : 0;
+    __shared__ float4 lds[4][3 * kBalGroupF4];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int n = P.n;
     const int lpr_log = n - 4;
@@ -788,10 +834,8 @@ __global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A,
     float4* sa = lds[wave];
     float4* sb = sa + kBalGroupF4;
     float4* heads = sb + kBalGroupF4 + (r << lpr_log) * 4;
-    float4* sout = sb + 2 * kBalGroupF4;  // inner only
     const int roff = r << (n - 2);
-    BalSched sc[3];
-    bal_schedules<OP, 0>(sc, lr, NB, P.nulh);
+    const BalSched sc = bal_schedule<OP, 0, kCls>(lr, NB, P.nulh);
     const long long ngrp = (P.batch + R - 1) / R;
     const long long gstride = (long long)gridDim.x * 4;
     long long grp = (long long)blockIdx.x * 4 + wave;
@@ -802,17 +846,10 @@ __global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A,
         bal_stage(sb, pb, n, lane);
         pa = bal_fetch(A, grp + gstride, P.batch, n, lane);
         pb = bal_fetch(B, grp + gstride, P.batch, n, lane);
-        if constexpr (OP == OP_INNER) bal_zero(sout, lane);
         wave_lds_sync();
         const long long row = grp * R + r;
-        if constexpr (OP == OP_INNER) {
-            bal_inner_rounds<0, LOWNEG>(sc, sa + roff, sb + roff, nullptr, heads, lr, sout + roff, NB, P);
-            wave_lds_sync();
-            bal_flush(sout, C, grp, P.batch, n, lane);
-        } else {
-            float4* out = row < P.batch ? reinterpret_cast<float4*>(C) + (row << (n - 2)) : nullptr;
-            bal_role<OP, 0, 0, LOWNEG, false>(sc[0], sa + roff, sb + roff, nullptr, heads, lr, out, NB, P);
-        }
+        float4* out = row < P.batch ? reinterpret_cast<float4*>(C) + (row << (n - 2)) : nullptr;
+        bal_role<OP, 0, kCls, LOWNEG, false>(sc, sa + roff, sb + roff, nullptr, heads, lr, out, NB, P);
         wave_lds_sync();
     }
 }
@@ -1171,15 +1208,16 @@ static bool product_path_is(const char* what) {
 static bool tiled_forced() { return product_path_is("tiled"); }
 static bool generic_forced() { return product_path_is("generic"); }
 
-// Balanced kernels: wedge, lc, rc, regressive for 4 <= n <= 10, inner for
-// n >= 9 (CLF_PRODUCT_PATH=blocked keeps them on the one-lane-per-output
-// kernels). Inner's three class rounds cost more than its divergence saves
-// below n = 9 (measured), and the geometric product, whose outputs all have
-// the same work, gains nothing; both use them only when
+// Balanced kernels: wedge, lc, rc, regressive for 4 <= n <= 10; inner forward
+// for 4 <= n <= 10 (one fused round: every pair's lc and rc halves), inner
+// backward for n >= 9 (CLF_PRODUCT_PATH=blocked keeps them on the
+// one-lane-per-output kernels). The backward's three class rounds cost more
+// than its divergence saves below n = 9 (measured), and the geometric product,
+// whose outputs all have the same work, gains nothing; both use them only when
 // CLF_PRODUCT_PATH=balanced.
-static bool bal_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, bool& lowneg) {
+static bool bal_plan(int op, int n, uint32_t neg, uint32_t nul, bool fwd, BlkParams& P, bool& lowneg) {
     if (n < kBalMinN || n > kBalMaxN) return false;
-    const bool opt_in = op == OP_GEOM || (op == OP_INNER && n < 9);
+    const bool opt_in = op == OP_GEOM || (op == OP_INNER && !fwd && n < 9);
     if (opt_in ? !product_path_is("balanced") : product_path_is("blocked")) return false;
     if (!blocked_metric(op, n, neg, nul, lowneg)) return false;
     block_sign_params(n, neg, nul, P);
@@ -1247,7 +1285,7 @@ int product_fwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
     dim3 g, bl;
     size_t lds = 0;
     const bool force_tiled = n >= 12 && tiled_forced(), force_generic = generic_forced();
-    if (!force_generic && bal_plan(op, n, neg, nul, P, ln)) {
+    if (!force_generic && bal_plan(op, n, neg, nul, true, P, ln)) {
 #define CLF_FWD_BAL(OPV)                                               \
     case OPV:                                                          \
         if (ln) launch_fwd_bal<OPV, true>(s, a, b, c, P);              \
@@ -1316,7 +1354,7 @@ int product_bwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
     dim3 g, bl;
     size_t lds = 0;
     const bool force_tiled = n >= 12 && tiled_forced(), force_generic = generic_forced();
-    if (!force_generic && bal_plan(op, n, neg, nul, P, ln)) {
+    if (!force_generic && bal_plan(op, n, neg, nul, false, P, ln)) {
 #define CLF_BWD_BAL(OPV)                                                       \
     case OPV:                                                                  \
         if (ln) launch_bwd_bal<OPV, true>(s, a, b, gc, ga, gb, P);             \

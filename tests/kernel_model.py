@@ -254,7 +254,8 @@ def backward_tiled(op_name, a, b, gc, metric, T):
 def bal_family(op, role, o, full, cls=0, nul=0):
     """(base, mask, first, count): partners base | S for the subsets S of mask
     in the kernel's order, from index first. The inner product has three
-    classes (0: ih strictly inside jh, 1: jh strictly inside ih, 2: ih = jh).
+    classes (0: ih strictly inside jh, 1: jh strictly inside ih, 2: ih = jh);
+    class 3 is its fused forward round (both halves of every pair).
     nul: high-part null generators; pairs whose blocks share one are zero for
     the metric ops and are left out. An output of a stored (not added) op
     whose pairs are all zero keeps one zero pair so that it is still written."""
@@ -274,6 +275,9 @@ def bal_family(op, role, o, full, cls=0, nul=0):
                 (o, 0, 0, 1) if o & nul else (o, co, 0, nco)][role]
     if op == REGR:
         return (co, o, 0, no)
+    if cls == 3:  # fused forward round: lc half (S, S | o) and rc half (S | o, S) of each pair
+        assert role == 0
+        return (0, con, 0, 1 << popc(con))
     strict = (1 << popc(onn)) - (1 if onn == o else 0)  # subsets of onn strictly inside o
     if cls == 0:
         return [(0, con, 0, (1 << popc(con)) if o else 0), (o, co, 1, 0 if o & nul else nco - 1),
@@ -410,3 +414,32 @@ def bal_run(op, role, NB, pair_value, cls=0, nul=0):
         assert o not in out
         out[o] = acc
     return out
+
+
+def inner_fused_forward(a, b, metric):
+    """The inner product's fused forward round at the level of full blade
+    indices: for every output block o and partner S of the class-3 family, the
+    lc half (ih = S, jh = S | o, low pattern il inside jl) and the rc half
+    (ih = S | o, jh = S, low pattern jl inside il); for o = 0 both halves are
+    (S, S) and the shared terms il = jl are taken off the scalar once."""
+    import torch
+    from oracle import clifford_oracle as O
+    n = len(metric)
+    sig = O.sign_value_table(n, metric).double().numpy()
+    nul = sum(1 << k for k, m in enumerate(metric) if m == 0)
+    NB = 1 << (n - 4)
+    full = NB - 1
+    c = np.zeros(a.shape[:-1] + (1 << n,))
+    for o in range(NB):
+        for S in bal_partners(INNER, 0, o, full, 3, nul >> 4):
+            for il in range(16):
+                for jl in range(16):
+                    for ih, jh, ok in ((S, S | o, (il & ~jl) == 0), (S | o, S, (jl & ~il) == 0)):
+                        if not ok:
+                            continue
+                        i, j = (ih << 4) | il, (jh << 4) | jl
+                        c[..., i ^ j] += sig[i, j] * a[..., i] * b[..., j]
+                if o == 0:
+                    i = (S << 4) | il
+                    c[..., 0] -= sig[i, i] * a[..., i] * b[..., i]
+    return c

@@ -122,3 +122,18 @@ def test_balanced_schedule_covers_every_valid_pair_once(op):
                             assert {k: int(v) for k, v in l1.items()} == {k: int(v) for k, v in l2.items()}
                 for o in range(NB):
                     np.testing.assert_allclose(total[o], ref[o], atol=1e-12)
+
+
+@pytest.mark.parametrize("metric", [(1,) * 5, (-1,) * 6, (1,) * 4 + (0, -1, 1), (-1,) * 4 + (1, 0, -1, 1)],
+                         ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
+def test_inner_fused_forward_round(metric):
+    """The balanced forward of the inner product (one round: lc and rc halves of
+    every pair of the class-3 family, the doubly counted il = jl terms of
+    output block 0 removed once) equals the oracle's inner product, with and
+    without null generators in the high part."""
+    n = len(metric)
+    rng = np.random.default_rng(n)
+    a = rng.standard_normal((2, 1 << n))
+    b = rng.standard_normal((2, 1 << n))
+    ref = O.einsum_product("inner", torch.tensor(a), torch.tensor(b), list(metric)).numpy()
+    np.testing.assert_allclose(K.inner_fused_forward(a, b, list(metric)), ref, atol=1e-10)
