@@ -132,6 +132,75 @@ __device__ __forceinline__ void lowblock_gb(float (&acc)[16], const float (&a)[1
     lowblock_gb_seq<VAR, LOWNEG>(acc, a, g, std::make_integer_sequence<int, 256>{});
 }
 
+// The inner product's low pattern split by term class: il = jl (both lc and
+// rc), il strictly inside jl (lc only), jl strictly inside il (rc only). The
+// operand of an lc-only term comes from xl, of an rc-only term from xr, of a
+// shared term from x (xl / xr are x or zero, by the pair's high relation).
+template <bool LOWNEG, int IL, int JL>
+__device__ __forceinline__ const float (&split_operand(const float (&x)[16], const float (&xl)[16],
+                                                        const float (&xr)[16]))[16] {
+    if constexpr (IL == JL) return x;
+    else if constexpr ((IL & ~JL & 15) == 0) return xl;
+    else return xr;
+}
+
+template <bool LOWNEG, int JL, int IL>
+__device__ __forceinline__ void ga_split_term(float (&acc)[16], const float (&b)[16], const float (&bl)[16],
+                                              const float (&br)[16], const float (&g)[16]) {
+    constexpr int s = low_sign(LV_INNER, LOWNEG, (unsigned)IL, (unsigned)JL);
+    const float (&v)[16] = split_operand<LOWNEG, IL, JL>(b, bl, br);
+    if constexpr (s > 0) acc[IL] = __builtin_fmaf(v[JL], g[IL ^ JL], acc[IL]);
+    else if constexpr (s < 0) acc[IL] = __builtin_fmaf(-v[JL], g[IL ^ JL], acc[IL]);
+}
+
+template <bool LOWNEG, int IL, int JL>
+__device__ __forceinline__ void gb_split_term(float (&acc)[16], const float (&a)[16], const float (&al)[16],
+                                              const float (&ar)[16], const float (&g)[16]) {
+    constexpr int s = low_sign(LV_INNER, LOWNEG, (unsigned)IL, (unsigned)JL);
+    const float (&v)[16] = split_operand<LOWNEG, IL, JL>(a, al, ar);
+    if constexpr (s > 0) acc[JL] = __builtin_fmaf(v[IL], g[IL ^ JL], acc[JL]);
+    else if constexpr (s < 0) acc[JL] = __builtin_fmaf(-v[IL], g[IL ^ JL], acc[JL]);
+}
+
+template <bool LOWNEG, int... Is>
+__device__ __forceinline__ void lowblock_ga_split_seq(float (&acc)[16], const float (&b)[16], const float (&bl)[16],
+                                                      const float (&br)[16], const float (&g)[16],
+                                                      std::integer_sequence<int, Is...>) {
+    (ga_split_term<LOWNEG, Is / 16, Is % 16>(acc, b, bl, br, g), ...);
+}
+
+template <bool LOWNEG, int... Is>
+__device__ __forceinline__ void lowblock_gb_split_seq(float (&acc)[16], const float (&a)[16], const float (&al)[16],
+                                                      const float (&ar)[16], const float (&g)[16],
+                                                      std::integer_sequence<int, Is...>) {
+    (gb_split_term<LOWNEG, Is / 16, Is % 16>(acc, a, al, ar, g), ...);
+}
+
+// lc: the pair's blocks satisfy ih inside jh; rc: jh inside ih (both: ih = jh)
+template <bool LOWNEG>
+__device__ __forceinline__ void lowblock_ga_split(float (&acc)[16], const float (&b)[16], bool lc, bool rc,
+                                                  const float (&g)[16]) {
+    float bl[16], br[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        bl[e] = lc ? b[e] : 0.f;
+        br[e] = rc ? b[e] : 0.f;
+    }
+    lowblock_ga_split_seq<LOWNEG>(acc, b, bl, br, g, std::make_integer_sequence<int, 256>{});
+}
+
+template <bool LOWNEG>
+__device__ __forceinline__ void lowblock_gb_split(float (&acc)[16], const float (&a)[16], bool lc, bool rc,
+                                                  const float (&g)[16]) {
+    float al[16], ar[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        al[e] = lc ? a[e] : 0.f;
+        ar[e] = rc ? a[e] : 0.f;
+    }
+    lowblock_gb_split_seq<LOWNEG>(acc, a, al, ar, g, std::make_integer_sequence<int, 256>{});
+}
+
 struct HiSign {
     bool valid;
     unsigned mask;  // 0 or 0x80000000
@@ -429,14 +498,15 @@ __global__ __launch_bounds__(256) void prod_bwd_blk(const float* __restrict__ A,
 // of the left operand), partner jh; ROLE 2: output jh, partner ih. The
 // partners of an output are a family {base | S}: the subsets S of mask in
 // increasing order (S <- (S - mask) & mask), from index `first`, `count` of
-// them. The inner product's backward runs three rounds, one per low-block
-// pattern (CLS 0: ih strictly inside jh, lc pattern; CLS 1: jh strictly inside
-// ih, rc pattern; CLS 2: ih = jh, both), so the lanes of a round never diverge
-// on the pattern; its rounds add into an LDS copy of the output rows, stored at
-// the end. Its forward runs one round (CLS 3): every pair (o, S) computes both
-// the lc half (S, S | o) and the rc half (S | o, S), which have the same
-// partner family, and for o = 0 the terms both halves share (il = jl) are
-// taken off the scalar slot once.
+// them. The inner product's low pattern depends on the pair (lc when ih is
+// strictly inside jh, rc when jh is inside ih, both when ih = jh). Its forward
+// runs one round (CLS 3): every pair (o, S) computes both the lc half
+// (S, S | o) and the rc half (S | o, S), which share the partner family, and
+// for o = 0 the terms both halves share (il = jl) are taken off the scalar slot
+// once. Its backward (CLS 4) enumerates all partners of an output, the lc side
+// then the rc side (two sub-families), and splits the low pattern by term
+// class: shared terms always count, lc-only and rc-only terms take their
+// operand from a copy zeroed unless the pair's blocks are related that way.
 // Layout: a wave owns groups of 1024 floats per operand (R = 1024 / D rows,
 // NB lanes per row) in wave-private LDS and walks the groups with a grid
 // stride, loading the next group into registers while it computes.
@@ -446,7 +516,18 @@ constexpr int kBalGroupF4 = 256;  // float4 per operand per group
 struct BalFam {
     unsigned base, mask;
     int first, count;
+    // a second sub-family (the inner product's backward round: the lc-side and
+    // the rc-side partners of an output), enumerated after the first
+    unsigned base2, mask2;
+    int first2, count2;
 };
+
+__device__ __forceinline__ int fam_total(const BalFam& f) { return f.count + f.count2; }
+
+// number of subsets of onn (= o without its null generators) strictly inside o
+__device__ __forceinline__ int strict_sub(unsigned o, unsigned onn) {
+    return (1 << __popc(onn)) - (onn == o ? 1 : 0);
+}
 
 // nul: the high-part null generators. Pairs whose blocks share one are zero
 // for the metric ops and are left out of the families; an output of a stored
@@ -478,22 +559,15 @@ __device__ __forceinline__ BalFam bal_family(unsigned o, unsigned full, unsigned
     // inner, fused forward round: output o, partners S (ih = S, jh = S | o for the
     // lc half, ih = S | o, jh = S for the rc half)
     if (CLS == 3) return BalFam{0u, con, 0, ncon};
-    // inner, by class; strict: the subsets of onn strictly inside o
-    const int strict = nonn - (onul ? 0 : 1);
-    if (CLS == 0) {  // ih strictly inside jh
-        if (ROLE == 0) return BalFam{0u, con, 0, o ? ncon : 0};
-        if (ROLE == 1) return BalFam{o, co, 1, onul ? 0 : nco - 1};
-        return BalFam{0u, onn, 0, strict};
+    // inner, backward round: all partners of an output, the lc side (with the
+    // pair ih = jh) first, then the rc side
+    if (CLS == 4) {
+        if (ROLE == 1)  // output ih = o: jh = o | S (S inside co), then jh = S strictly inside o
+            return BalFam{o, co, 0, onul ? 0 : nco, 0u, onn, 0, strict_sub(o, onn)};
+        // ROLE 2, output jh = o: ih = S inside o, then ih = o | S (S nonempty, inside co)
+        return BalFam{0u, onn, 0, nonn, o, co, 1, onul ? 0 : nco - 1};
     }
-    if (CLS == 1) {  // jh strictly inside ih
-        if (ROLE == 0) return BalFam{o, con, 0, o ? ncon : 0};
-        if (ROLE == 1) return BalFam{0u, onn, 0, strict};
-        return BalFam{o, co, 1, onul ? 0 : nco - 1};
-    }
-    // ih = jh
-    const unsigned fn = full & ~nul;
-    if (ROLE == 0) return BalFam{0u, fn, 0, o ? 0 : (1 << __popc(fn))};
-    return BalFam{o, 0u, 0, onul ? 0 : 1};
+    return BalFam{0u, 0u, 0, 0};  // not reached: the inner product uses classes 3 and 4
 }
 
 // the s-th subset of m in increasing order (bits of s deposited on the bits of m)
@@ -535,7 +609,7 @@ __device__ __forceinline__ int bal_largest_le(int pre, int v, unsigned NB) {
 template <int OP, int ROLE, int CLS>
 __device__ __forceinline__ BalSched bal_schedule(unsigned lr, unsigned NB, unsigned nul) {
     const unsigned full = NB - 1u;
-    const int c = bal_family<OP, ROLE, CLS>(lr, full, nul).count;
+    const int c = fam_total(bal_family<OP, ROLE, CLS>(lr, full, nul));
     int inc = c;  // inclusive scan of the counts over the row's lanes
     for (int d = 1; d < (int)NB; d <<= 1) {
         const int v = __shfl_up(inc, (unsigned)d, (int)NB);
@@ -576,22 +650,11 @@ __device__ __forceinline__ void store_blk(float4* __restrict__ out, unsigned blk
     }
 }
 
-__device__ __forceinline__ void add_blk(float4* __restrict__ out, unsigned blk, const float (&acc)[16]) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        float4 v = out[(blk << 2) + q];
-        v.x += acc[4 * q];
-        v.y += acc[4 * q + 1];
-        v.z += acc[4 * q + 2];
-        v.w += acc[4 * q + 3];
-        out[(blk << 2) + q] = v;
-    }
-}
-
-// low-block pattern of a pair: the op's, or for the inner product its class's
+// low-block pattern of a pair: the op's; the inner product's rounds pick their
+// patterns per half (forward) or per term class (backward)
 template <int OP, int CLS>
 constexpr int bal_variant() {
-    return OP != OP_INNER ? OP : (CLS == 0 || CLS == 3 ? LV_LC : (CLS == 1 ? LV_RC : LV_INNER));
+    return OP != OP_INNER ? OP : (CLS == 3 ? LV_LC : LV_INNER);
 }
 
 // sum_l s_lo(l, l) a[l] b[l]: the terms the lc and rc low patterns share
@@ -606,11 +669,11 @@ __device__ __forceinline__ float lowblock_diag(const float (&a)[16], const float
 }
 
 // One role (and class) over one row: la / lb / lg are the row's staged
-// operands, heads the row's head slots (4 float4 per lane). ADD: completed
-// outputs are added into out (the row's LDS copy); else stored to out (the
-// row in global memory, nullptr for a row past the end of the batch). The
-// caller syncs the wave's LDS before (staged data) and after (heads reused).
-template <int OP, int ROLE, int CLS, bool LOWNEG, bool ADD>
+// operands, heads the row's head slots (4 float4 per lane). Completed outputs
+// are stored to out (the row in global memory, nullptr for a row past the end
+// of the batch). The caller syncs the wave's LDS before (staged data) and
+// after (heads reused).
+template <int OP, int ROLE, int CLS, bool LOWNEG>
 __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __restrict__ la,
                                          const float4* __restrict__ lb, const float4* __restrict__ lg,
                                          float4* __restrict__ heads, unsigned lr, float4* __restrict__ out,
@@ -625,12 +688,15 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
     unsigned o = sc.o0;
     BalFam f = bal_family<OP, ROLE, CLS>(o, full, P.nulh);
     int s = sc.s0;
-    unsigned S = deposit_bits((unsigned)(f.first + s), f.mask);
+    // S runs over the first sub-family, then (the inner backward round) the second
+    unsigned S = s < f.count ? deposit_bits((unsigned)(f.first + s), f.mask)
+                             : deposit_bits((unsigned)(f.first2 + s - f.count), f.mask2);
     bool first = true;
     int p = sc.p0;
     for (int t = 0; t < sc.T; ++t) {
         if (p >= sc.p1) break;
-        const unsigned part = f.base | S;
+        const bool in2 = CLS == 4 && s >= f.count;
+        const unsigned part = (in2 ? f.base2 : f.base) | S;
         if (OP == OP_INNER && CLS == 3) {
             // lc half: (S, S | o), lc low pattern; rc half: (S | o, S), rc low
             // pattern. For o = 0 both halves are (S, S) and count the terms with
@@ -679,7 +745,9 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
                     float bv[16];
                     load_blk(lb, m, bv);
                     apply_flips(bv, hs.mask, hs.mask ^ (cross_pi<OP>(h, P.nm1) << 31));
-                    if (OP == OP_INNER) lowblock_ga<VAR, kLowNeg>(acc, bv, g);
+                    if (OP == OP_INNER && CLS == 4)  // ih = h, jh = m
+                        lowblock_ga_split<kLowNeg>(acc, bv, (h & ~m) == 0u, (m & ~h) == 0u, g);
+                    else if (OP == OP_INNER) lowblock_ga<VAR, kLowNeg>(acc, bv, g);
                     else ga_block_dispatch<OP, LOWNEG>(acc, bv, g, h, m);
                 } else {
                     const unsigned pm = cross_pi<OP>(m, P.nm1) << 31;
@@ -688,23 +756,29 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
                     apply_flips(av, hs.mask, hs.mask ^ pm);
 #pragma unroll
                     for (int e = 0; e < 16; ++e) gt[e] = (cpopc((unsigned)e) & 1) ? flip(g[e], pm) : g[e];
-                    if (OP == OP_INNER) lowblock_gb<VAR, kLowNeg>(acc, av, gt);
+                    if (OP == OP_INNER && CLS == 4)  // ih = m, jh = h
+                        lowblock_gb_split<kLowNeg>(acc, av, (m & ~h) == 0u, (h & ~m) == 0u, gt);
+                    else if (OP == OP_INNER) lowblock_gb<VAR, kLowNeg>(acc, av, gt);
                     else gb_block_dispatch<OP, LOWNEG>(acc, av, gt, m, h);
                 }
             }
         }
         ++p;
         ++s;
-        S = (S - f.mask) & f.mask;
-        const bool done = s == f.count;
+        if (CLS == 4 && s == f.count) {
+            S = deposit_bits((unsigned)f.first2, f.mask2);
+        } else {
+            const unsigned msk = in2 ? f.mask2 : f.mask;
+            S = (S - msk) & msk;
+        }
+        const bool done = s == fam_total(f);
         if (done || p == sc.p1) {
             if (first && sc.cont0) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
                     heads[lr * 4 + q] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
             } else if (done && out) {
-                if (ADD) add_blk(out, o, acc);
-                else store_blk(out, kRev ? (full ^ o) : o, acc, kRev);
+                store_blk(out, kRev ? (full ^ o) : o, acc, kRev);
             }
             if (done) {
 #pragma unroll
@@ -715,9 +789,9 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
                     ++o;
                     if (o >= NB) break;
                     f = bal_family<OP, ROLE, CLS>(o, full, P.nulh);
-                } while (f.count == 0);
+                } while (fam_total(f) == 0);
                 s = 0;
-                S = deposit_bits((unsigned)f.first, f.mask);
+                S = f.count > 0 ? deposit_bits((unsigned)f.first, f.mask) : deposit_bits((unsigned)f.first2, f.mask2);
             }
         }
     }
@@ -733,10 +807,7 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
                 acc[4 * q + 3] += v.w;
             }
         }
-        if (out) {
-            if (ADD) add_blk(out, sc.olast, acc);
-            else store_blk(out, kRev ? (full ^ sc.olast) : sc.olast, acc, kRev);
-        }
+        if (out) store_blk(out, kRev ? (full ^ sc.olast) : sc.olast, acc, kRev);
     }
 }
 
@@ -773,50 +844,6 @@ __device__ __forceinline__ void bal_stage(float4* __restrict__ dst, const BalPre
     }
 }
 
-// the group's LDS output copy (rows in natural order) -> global, rows past the end skipped
-__device__ __forceinline__ void bal_flush(const float4* __restrict__ src, float* __restrict__ dst, long long grp,
-                                          long long batch, int n, int lane) {
-    const int d4_log = n - 2;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int c = lane + 64 * i;
-        const long long row = grp * (kBalGroupF4 >> d4_log) + (c >> d4_log);
-        if (row < batch) reinterpret_cast<float4*>(dst)[grp * kBalGroupF4 + c] = src[c];
-    }
-}
-
-__device__ __forceinline__ void bal_zero(float4* __restrict__ dst, int lane) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dst[lane + 64 * i] = make_float4(0.f, 0.f, 0.f, 0.f);
-}
-
-// the three class rounds of the inner product for one role
-template <int ROLE, bool LOWNEG>
-__device__ __forceinline__ void bal_inner_rounds(const BalSched (&sc)[3], const float4* la, const float4* lb,
-                                                 const float4* lg, float4* heads, unsigned lr, float4* out,
-                                                 unsigned NB, const BlkParams& P) {
-    bal_role<OP_INNER, ROLE, 0, LOWNEG, true>(sc[0], la, lb, lg, heads, lr, out, NB, P);
-    wave_lds_sync();
-    bal_role<OP_INNER, ROLE, 1, LOWNEG, true>(sc[1], la, lb, lg, heads, lr, out, NB, P);
-    wave_lds_sync();
-    bal_role<OP_INNER, ROLE, 2, LOWNEG, true>(sc[2], la, lb, lg, heads, lr, out, NB, P);
-}
-
-template <int OP, int ROLE>
-__device__ __forceinline__ void bal_schedules(BalSched (&sc)[3], unsigned lr, unsigned NB, unsigned nul) {
-    sc[0] = bal_schedule<OP, ROLE, 0>(lr, NB, nul);
-    if (OP == OP_INNER) {
-        sc[1] = bal_schedule<OP, ROLE, 1>(lr, NB, nul);
-        sc[2] = bal_schedule<OP, ROLE, 2>(lr, NB, nul);
-    }
-}
-
-// LDS per wave: a | b | heads, plus the output copy for the inner product
-template <int OP>
-constexpr int bal_regions() {
-    return OP == OP_INNER ? 4 : 3;
-}
-
 template <int OP, bool LOWNEG>
 __global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A, const float* __restrict__ B,
                                                      float* __restrict__ C, BlkParams P) {
@@ -849,7 +876,7 @@ __global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A,
         wave_lds_sync();
         const long long row = grp * R + r;
         float4* out = row < P.batch ? reinterpret_cast<float4*>(C) + (row << (n - 2)) : nullptr;
-        bal_role<OP, 0, kCls, LOWNEG, false>(sc, sa + roff, sb + roff, nullptr, heads, lr, out, NB, P);
+        bal_role<OP, 0, kCls, LOWNEG>(sc, sa + roff, sb + roff, nullptr, heads, lr, out, NB, P);
         wave_lds_sync();
     }
 }
@@ -858,10 +885,13 @@ __global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A,
 // its heads in the a slot; then a is staged and the right-operand gradient
 // runs with its heads in the b slot (12 KB of LDS per wave; 16 KB for inner).
 template <int OP, bool LOWNEG>
-__global__ __launch_bounds__(256) void prod_bwd_bal(const float* __restrict__ A, const float* __restrict__ B,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void prod_bwd_bal(const float* __restrict__ A, const float* __restrict__ B,
                                                      const float* __restrict__ GC, float* __restrict__ GA,
                                                      float* __restrict__ GB, BlkParams P) {
-    __shared__ float4 lds[4][bal_regions<OP>() * kBalGroupF4];  // a | b | gc [| output copy]
+    // The inner product runs its backward round (class 4: all partners of an
+    // output, lc side then rc side, with the low pattern split by term class).
+    constexpr int kCls = OP == OP_INNER ? 4 : 0;
+    __shared__ float4 lds[4][3 * kBalGroupF4];  // a | b | gc
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int n = P.n;
     const int lpr_log = n - 4;
@@ -872,13 +902,11 @@ __global__ __launch_bounds__(256) void prod_bwd_bal(const float* __restrict__ A,
     float4* sa = lds[wave];
     float4* sb = sa + kBalGroupF4;
     float4* sg = sb + kBalGroupF4;
-    float4* sout = sg + kBalGroupF4;  // inner only
     const int roff = r << (n - 2);
     const int hoff = (r << lpr_log) * 4;
     const bool want_a = GA != nullptr, want_b = GB != nullptr;
-    BalSched sca[3], scb[3];
-    bal_schedules<OP, 1>(sca, lr, NB, P.nulh);
-    bal_schedules<OP, 2>(scb, lr, NB, P.nulh);
+    const BalSched sca = bal_schedule<OP, 1, kCls>(lr, NB, P.nulh);
+    const BalSched scb = bal_schedule<OP, 2, kCls>(lr, NB, P.nulh);
     const long long ngrp = (P.batch + R - 1) / R;
     const long long gstride = (long long)gridDim.x * 4;
     long long grp = (long long)blockIdx.x * 4 + wave;
@@ -894,31 +922,17 @@ __global__ __launch_bounds__(256) void prod_bwd_bal(const float* __restrict__ A,
         if (want_a) {  // uniform: a kernel argument
             bal_stage(sb, pb, n, lane);
             pb = bal_fetch(B, grp + gstride, P.batch, n, lane);
-            if constexpr (OP == OP_INNER) bal_zero(sout, lane);
             wave_lds_sync();
-            if constexpr (OP == OP_INNER) {
-                bal_inner_rounds<1, LOWNEG>(sca, nullptr, sb + roff, sg + roff, sa + hoff, lr, sout + roff, NB, P);
-                wave_lds_sync();
-                bal_flush(sout, GA, grp, P.batch, n, lane);
-            } else {
-                float4* out = row_ok ? reinterpret_cast<float4*>(GA) + (row << (n - 2)) : nullptr;
-                bal_role<OP, 1, 0, LOWNEG, false>(sca[0], nullptr, sb + roff, sg + roff, sa + hoff, lr, out, NB, P);
-            }
+            float4* out = row_ok ? reinterpret_cast<float4*>(GA) + (row << (n - 2)) : nullptr;
+            bal_role<OP, 1, kCls, LOWNEG>(sca, nullptr, sb + roff, sg + roff, sa + hoff, lr, out, NB, P);
             wave_lds_sync();
         }
         if (want_b) {
             bal_stage(sa, pa, n, lane);
             pa = bal_fetch(A, grp + gstride, P.batch, n, lane);
-            if constexpr (OP == OP_INNER) bal_zero(sout, lane);
             wave_lds_sync();
-            if constexpr (OP == OP_INNER) {
-                bal_inner_rounds<2, LOWNEG>(scb, sa + roff, nullptr, sg + roff, sb + hoff, lr, sout + roff, NB, P);
-                wave_lds_sync();
-                bal_flush(sout, GB, grp, P.batch, n, lane);
-            } else {
-                float4* out = row_ok ? reinterpret_cast<float4*>(GB) + (row << (n - 2)) : nullptr;
-                bal_role<OP, 2, 0, LOWNEG, false>(scb[0], sa + roff, nullptr, sg + roff, sb + hoff, lr, out, NB, P);
-            }
+            float4* out = row_ok ? reinterpret_cast<float4*>(GB) + (row << (n - 2)) : nullptr;
+            bal_role<OP, 2, kCls, LOWNEG>(scb, sa + roff, nullptr, sg + roff, sb + hoff, lr, out, NB, P);
         }
         wave_lds_sync();
     }
@@ -1208,16 +1222,17 @@ static bool product_path_is(const char* what) {
 static bool tiled_forced() { return product_path_is("tiled"); }
 static bool generic_forced() { return product_path_is("generic"); }
 
-// Balanced kernels: wedge, lc, rc, regressive for 4 <= n <= 10; inner forward
-// for 4 <= n <= 10 (one fused round: every pair's lc and rc halves), inner
-// backward for n >= 9 (CLF_PRODUCT_PATH=blocked keeps them on the
-// one-lane-per-output kernels). The backward's three class rounds cost more
-// than its divergence saves below n = 9 (measured), and the geometric product,
-// whose outputs all have the same work, gains nothing; both use them only when
-// CLF_PRODUCT_PATH=balanced.
+// Balanced kernels: wedge, lc, rc, regressive and the inner product's forward
+// for 4 <= n <= 10, the inner product's backward for n >= 8
+// (CLF_PRODUCT_PATH=blocked keeps them on the one-lane-per-output kernels).
+// The inner backward's round computes both low patterns per pair and runs at
+// three waves per SIMD with a few spilled registers; at n = 7 the blocked
+// kernel is faster (measured), from n = 8 the balanced round. The geometric
+// product, whose outputs all have the same work, gains nothing; both use the
+// balanced kernels only when CLF_PRODUCT_PATH=balanced.
 static bool bal_plan(int op, int n, uint32_t neg, uint32_t nul, bool fwd, BlkParams& P, bool& lowneg) {
     if (n < kBalMinN || n > kBalMaxN) return false;
-    const bool opt_in = op == OP_GEOM || (op == OP_INNER && !fwd && n < 9);
+    const bool opt_in = op == OP_GEOM || (op == OP_INNER && !fwd && n < 8);
     if (opt_in ? !product_path_is("balanced") : product_path_is("blocked")) return false;
     if (!blocked_metric(op, n, neg, nul, lowneg)) return false;
     block_sign_params(n, neg, nul, P);

@@ -252,45 +252,44 @@ def backward_tiled(op_name, a, b, gc, metric, T):
 
 
 def bal_family(op, role, o, full, cls=0, nul=0):
-    """(base, mask, first, count): partners base | S for the subsets S of mask
-    in the kernel's order, from index first. The inner product has three
-    classes (0: ih strictly inside jh, 1: jh strictly inside ih, 2: ih = jh);
-    class 3 is its fused forward round (both halves of every pair).
+    """List of (base, mask, first, count) sub-families: partners base | S for the
+    subsets S of mask in the kernel's order, from index first, one sub-family
+    after the other. The inner product uses class 3 for its forward (one
+    family; each partner S stands for the lc half (S, S | o) and the rc half
+    (S | o, S)) and class 4 for its backward (the lc-side partners, the pair
+    ih = jh included, then the rc-side partners).
     nul: high-part null generators; pairs whose blocks share one are zero for
-    the metric ops and are left out. An output of a stored (not added) op
-    whose pairs are all zero keeps one zero pair so that it is still written."""
+    the metric ops and are left out. An output whose pairs are all zero keeps
+    one zero pair so that it is still written."""
     co = ~o & full
     nco, no = 1 << popc(co), 1 << popc(o)
     con, onn = co & ~nul, o & ~nul   # partner bits that never meet a null
     if op == GEOM:
         m = full & ~(nul & ~o) if role == 0 else full & ~(nul & o)
-        return (0, m, 0, 1 << popc(m))
+        return [(0, m, 0, 1 << popc(m))]
     if op == WEDGE:
-        return (0, o, 0, no) if role == 0 else (0, co, 0, nco)
+        return [(0, o, 0, no) if role == 0 else (0, co, 0, nco)]
     if op == LC:
-        return [(0, con, 0, 1 << popc(con)), (o, 0, 0, 1) if o & nul else (o, co, 0, nco),
-                (0, onn, 0, 1 << popc(onn))][role]
+        return [[(0, con, 0, 1 << popc(con)), (o, 0, 0, 1) if o & nul else (o, co, 0, nco),
+                 (0, onn, 0, 1 << popc(onn))][role]]
     if op == RC:
-        return [(o, con, 0, 1 << popc(con)), (0, onn, 0, 1 << popc(onn)),
-                (o, 0, 0, 1) if o & nul else (o, co, 0, nco)][role]
+        return [[(o, con, 0, 1 << popc(con)), (0, onn, 0, 1 << popc(onn)),
+                 (o, 0, 0, 1) if o & nul else (o, co, 0, nco)][role]]
     if op == REGR:
-        return (co, o, 0, no)
-    if cls == 3:  # fused forward round: lc half (S, S | o) and rc half (S | o, S) of each pair
-        assert role == 0
-        return (0, con, 0, 1 << popc(con))
+        return [(co, o, 0, no)]
     strict = (1 << popc(onn)) - (1 if onn == o else 0)  # subsets of onn strictly inside o
-    if cls == 0:
-        return [(0, con, 0, (1 << popc(con)) if o else 0), (o, co, 1, 0 if o & nul else nco - 1),
-                (0, onn, 0, strict)][role]
-    if cls == 1:
-        return [(o, con, 0, (1 << popc(con)) if o else 0), (0, onn, 0, strict),
-                (o, co, 1, 0 if o & nul else nco - 1)][role]
-    fn = full & ~nul
-    return (0, fn, 0, 0 if o else 1 << popc(fn)) if role == 0 else (o, 0, 0, 0 if o & nul else 1)
+    if role == 0:
+        assert cls == 3
+        return [(0, con, 0, 1 << popc(con))]
+    assert cls == 4
+    if role == 1:   # output ih = o: jh = o | S, then jh strictly inside o
+        return [(o, co, 0, 0 if o & nul else nco), (0, onn, 0, strict)]
+    return [(0, onn, 0, 1 << popc(onn)), (o, co, 1, 0 if o & nul else nco - 1)]
 
 
-def bal_classes(op):
-    return 3 if op == INNER else 1
+def bal_class(op, role):
+    """The class the kernels run for an op and role."""
+    return (3 if role == 0 else 4) if op == INNER else 0
 
 
 def subsets(m):
@@ -303,8 +302,8 @@ def subsets(m):
 
 
 def bal_partners(op, role, o, full, cls=0, nul=0):
-    base, mask, first, count = bal_family(op, role, o, full, cls, nul)
-    return [base | S for S in subsets(mask)[first:first + count]]
+    return [base | S for base, mask, first, count in bal_family(op, role, o, full, cls, nul)
+            for S in subsets(mask)[first:first + count]]
 
 
 def bal_block_pair(role, o, part):
@@ -339,7 +338,7 @@ def bal_schedule_lanes(op, role, NB, cls=0, nul=0):
     inclusive scan over the NB lanes, then a binary search with shuffles for
     the largest output whose exclusive offset is <= p0 (and p1 - 1)."""
     full = NB - 1
-    c = [bal_family(op, role, lr, full, cls, nul)[3] for lr in range(NB)]
+    c = [len(bal_partners(op, role, lr, full, cls, nul)) for lr in range(NB)]
     inc = list(c)
     d = 1
     while d < NB:
@@ -443,3 +442,35 @@ def inner_fused_forward(a, b, metric):
                     i = (S << 4) | il
                     c[..., 0] -= sig[i, i] * a[..., i] * b[..., i]
     return c
+
+
+def inner_union_backward(a, b, gc, metric):
+    """The inner product's backward round at the level of full blade indices:
+    for every output block o and partner m of the class-4 families, the terms
+    (il, jl) with il = jl always, il strictly inside jl when the left block is
+    inside the right one, jl strictly inside il when the right block is inside
+    the left one. Returns (ga, gb)."""
+    from oracle import clifford_oracle as O
+    n = len(metric)
+    sig = O.sign_value_table(n, metric).double().numpy()
+    nul = sum(1 << k for k, m in enumerate(metric) if m == 0) >> 4
+    NB = 1 << (n - 4)
+    full = NB - 1
+    ga = np.zeros(a.shape)
+    gb = np.zeros(b.shape)
+
+    def terms(ih, jh):
+        lc, rc = (ih & ~jh) == 0, (jh & ~ih) == 0
+        for il in range(16):
+            for jl in range(16):
+                if il == jl or (lc and (il & ~jl) == 0) or (rc and (jl & ~il) == 0):
+                    yield (ih << 4) | il, (jh << 4) | jl
+
+    for o in range(NB):
+        for m in bal_partners(INNER, 1, o, full, 4, nul):
+            for i, j in terms(o, m):
+                ga[..., i] += sig[i, j] * b[..., j] * gc[..., i ^ j]
+        for m in bal_partners(INNER, 2, o, full, 4, nul):
+            for i, j in terms(m, o):
+                gb[..., j] += sig[i, j] * a[..., i] * gc[..., i ^ j]
+    return ga, gb

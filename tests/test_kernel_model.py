@@ -62,14 +62,14 @@ def test_tiled_model_forward_backward(op, n, metric, T):
 
 @pytest.mark.parametrize("op", list(K.OPS.values()))
 def test_balanced_schedule_covers_every_valid_pair_once(op):
-    """The partner families (over the classes of the inner product) enumerate
-    exactly the valid block pairs of each output (every role, n = 4 .. 10,
-    without and with null generators in the high part: pairs meeting on a null
-    generator are left out), each once; an output of a stored op with no valid
-    pair gets exactly one (zero) pair so that it is written; inner's classes
-    hold the pairs of one low-block pattern each; the lanes' ranges with
-    heads/tails rebuild each output once; the kernel's lane-parallel schedule
-    (scan + binary search) equals the reference schedule."""
+    """The partner families enumerate exactly the valid block pairs of each
+    output (every role, n = 4 .. 10, without and with null generators in the
+    high part: pairs meeting on a null generator are left out), each once; an
+    output of an op with no valid pair gets exactly one (zero) pair so that it
+    is written; the inner product's forward partners stand for an lc and an rc
+    half each (the same pair twice only for output block 0); the lanes' ranges
+    with heads/tails rebuild each output once; the kernel's lane-parallel
+    schedule (scan + binary search) equals the reference schedule."""
     rng = np.random.default_rng(op)
     for n in range(4, 11):
         NB = 1 << (n - 4)
@@ -77,51 +77,41 @@ def test_balanced_schedule_covers_every_valid_pair_once(op):
         nuls = sorted({0, full & (NB >> 1), full & 0b101, full & 0b110})
         for nul in nuls:
             for role in range(3):
+                cls = K.bal_class(op, role)
                 seen = []
-                for cls in range(K.bal_classes(op)):
-                    for o in range(NB):
-                        for part in K.bal_partners(op, role, o, full, cls, nul):
-                            ih, jh = K.bal_block_pair(role, o, part)
-                            seen.append((ih, jh))
-                            if op == K.INNER:
-                                assert K.variant(op, ih, jh) == [K.LC, K.RC, K.INNER][cls]
+                for o in range(NB):
+                    for part in K.bal_partners(op, role, o, full, cls, nul):
+                        if cls == 3:
+                            seen += [(part, part | o), (part | o, part)] if o else [(part, part)]
+                        else:
+                            seen.append(K.bal_block_pair(role, o, part))
                 valid = {(ih, jh) for ih in range(NB) for jh in range(NB)
                          if K.hi_sign(op, ih, jh, 0, nul, full, 0, 0)[0]}
                 assert len(seen) == len(set(seen)), (n, nul, role)
                 extra = set(seen) - valid
                 assert valid <= set(seen), (n, nul, role)
                 out_of = [[ih ^ jh, ih, jh][role] for ih, jh in extra]
-                if op == K.INNER:
-                    assert not extra, (n, nul, role)
-                else:
-                    # one placeholder per output whose pairs all vanish, none elsewhere
-                    empty = {o for o in range(NB)
-                             if not any([ih ^ jh, ih, jh][role] == o for ih, jh in valid)}
-                    assert sorted(out_of) == sorted(empty), (n, nul, role)
-                    assert nul or not extra
-                total = {o: np.zeros(16) for o in range(NB)}
-                ref = {o: np.zeros(16) for o in range(NB)}
-                for cls in range(K.bal_classes(op)):
-                    vals = {(o, part): rng.standard_normal(16) for o in range(NB)
-                            for part in K.bal_partners(op, role, o, full, cls, nul)}
-                    out = K.bal_run(op, role, NB, lambda o, part: vals[(o, part)], cls, nul)
-                    for o in range(NB):
-                        parts = K.bal_partners(op, role, o, full, cls, nul)
-                        assert (o in out) == bool(parts)
-                        if parts:
-                            total[o] = total[o] + out[o]
-                            ref[o] = ref[o] + sum(vals[(o, part)] for part in parts)
-                    T, lanes, pre = K.bal_schedule(op, role, NB, cls, nul)
-                    assert T * NB >= pre[-1] > (T - 1) * NB or pre[-1] == 0
-                    # the kernel's lane-parallel computation gives the same schedule
-                    T2, lanes2 = K.bal_schedule_lanes(op, role, NB, cls, nul)
-                    assert T2 == T and len(lanes2) == len(lanes)
-                    for l1, l2 in zip(lanes, lanes2):
-                        assert (l1 is None) == (l2 is None)
-                        if l1 is not None:
-                            assert {k: int(v) for k, v in l1.items()} == {k: int(v) for k, v in l2.items()}
+                # one placeholder per output whose pairs all vanish, none elsewhere
+                empty = {o for o in range(NB) if not any([ih ^ jh, ih, jh][role] == o for ih, jh in valid)}
+                assert sorted(out_of) == sorted(empty), (n, nul, role)
+                assert nul or not extra
+                vals = {(o, part): rng.standard_normal(16) for o in range(NB)
+                        for part in K.bal_partners(op, role, o, full, cls, nul)}
+                out = K.bal_run(op, role, NB, lambda o, part: vals[(o, part)], cls, nul)
                 for o in range(NB):
-                    np.testing.assert_allclose(total[o], ref[o], atol=1e-12)
+                    parts = K.bal_partners(op, role, o, full, cls, nul)
+                    assert (o in out) == bool(parts)
+                    if parts:
+                        np.testing.assert_allclose(out[o], sum(vals[(o, part)] for part in parts), atol=1e-12)
+                T, lanes, pre = K.bal_schedule(op, role, NB, cls, nul)
+                assert T * NB >= pre[-1] > (T - 1) * NB or pre[-1] == 0
+                # the kernel's lane-parallel computation gives the same schedule
+                T2, lanes2 = K.bal_schedule_lanes(op, role, NB, cls, nul)
+                assert T2 == T and len(lanes2) == len(lanes)
+                for l1, l2 in zip(lanes, lanes2):
+                    assert (l1 is None) == (l2 is None)
+                    if l1 is not None:
+                        assert {k: int(v) for k, v in l1.items()} == {k: int(v) for k, v in l2.items()}
 
 
 @pytest.mark.parametrize("metric", [(1,) * 5, (-1,) * 6, (1,) * 4 + (0, -1, 1), (-1,) * 4 + (1, 0, -1, 1)],
@@ -137,3 +127,24 @@ def test_inner_fused_forward_round(metric):
     b = rng.standard_normal((2, 1 << n))
     ref = O.einsum_product("inner", torch.tensor(a), torch.tensor(b), list(metric)).numpy()
     np.testing.assert_allclose(K.inner_fused_forward(a, b, list(metric)), ref, atol=1e-10)
+
+
+@pytest.mark.parametrize("metric", [(1,) * 5, (-1,) * 6, (1,) * 4 + (0, -1, 1), (-1,) * 4 + (1, 0, -1, 1)],
+                         ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
+def test_inner_union_backward_round(metric):
+    """The balanced backward of the inner product (class-4 families: all
+    partners of an output; low terms split by class: shared ones always,
+    lc-only ones when the left block is inside the right, rc-only ones when the
+    right block is inside the left) gives the oracle's gradients, with and
+    without null generators in the high part."""
+    n = len(metric)
+    rng = np.random.default_rng(n + 1)
+    a = rng.standard_normal((2, 1 << n))
+    b = rng.standard_normal((2, 1 << n))
+    gc = rng.standard_normal((2, 1 << n))
+    at = torch.tensor(a, requires_grad=True)
+    bt = torch.tensor(b, requires_grad=True)
+    O.einsum_product("inner", at, bt, list(metric)).backward(torch.tensor(gc))
+    ga, gb = K.inner_union_backward(a, b, gc, list(metric))
+    np.testing.assert_allclose(ga, at.grad.numpy(), atol=1e-10)
+    np.testing.assert_allclose(gb, bt.grad.numpy(), atol=1e-10)
