@@ -350,8 +350,7 @@ int bcast_bwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* 
     hipStream_t s = (hipStream_t)stream;
     const int D = 1 << n;
     const size_t DD = (size_t)D * D;
-    float* MwT = (float*)ws + DD;
-    float* parts = (float*)ws + 2 * DD;
+    float* parts = (float*)ws + 2 * DD;  // [DD, 2 DD): the forward's transposed matrix, unused here
     const int splits = bcast_splits(batch);
     float* G = parts + (size_t)splits * DD;
     if (gx && batch > 0) {

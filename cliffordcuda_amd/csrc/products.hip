@@ -518,8 +518,8 @@ struct BalFam {
     int first, count;
     // a second sub-family (the inner product's backward round: the lc-side and
     // the rc-side partners of an output), enumerated after the first
-    unsigned base2, mask2;
-    int first2, count2;
+    unsigned base2 = 0u, mask2 = 0u;
+    int first2 = 0, count2 = 0;
 };
 
 __device__ __forceinline__ int fam_total(const BalFam& f) { return f.count + f.count2; }

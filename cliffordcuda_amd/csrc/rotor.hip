@@ -609,7 +609,7 @@ __global__ __launch_bounds__(1024) void rotor_gamma_finalize_kernel(int n, const
     part[threadIdx.x] = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
     for (int i = threadIdx.x; i < n * n; i += blockDim.x) S[i] = 0.0;
     __syncthreads();
-    if (threadIdx.x < C) {
+    if ((int)threadIdx.x < C) {
         double u = 0.0;
         for (int g = 0; g < ngrp; ++g) u += part[g * ep + threadIdx.x];
         const int p = plane_p(n, threadIdx.x), q = plane_q(n, threadIdx.x);
@@ -617,7 +617,7 @@ __global__ __launch_bounds__(1024) void rotor_gamma_finalize_kernel(int n, const
         S[q * n + p] = -0.5 * u;
     }
     __syncthreads();
-    if (threadIdx.x < n * n) {
+    if ((int)threadIdx.x < n * n) {
         const int i = threadIdx.x / n, j = threadIdx.x % n;
         double v = 0.0;
         for (int k = 0; k < n; ++k) v += (double)state[i * n + k] * S[k * n + j];
