@@ -76,6 +76,42 @@ def cpu_baseline(n: int, budget_s: float):
                       f"restatement, torch fp32 on the host CPU, median chunk time)"}
 
 
+def cpu_rate(work, rows: int, budget_s: float, label: str, dtype: str = "fp32"):
+    """Rows per second of work() (one chunk of `rows` rows through the oracle
+    restatement on the host CPU, all threads), median over a bounded sample."""
+    import torch
+    torch.set_num_threads(os.cpu_count() or 1)
+    times = []
+    t0 = time.perf_counter()
+    while True:
+        t1 = time.perf_counter()
+        work()
+        times.append(time.perf_counter() - t1)
+        if time.perf_counter() - t0 > budget_s or len(times) >= 20:
+            break
+    times.sort()
+    return {"value": rows / times[len(times) // 2], "unit": "rows/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{len(times)} chunks x {rows} rows: {label} (oracle restatement, torch {dtype} on the "
+                      f"host CPU, median chunk time)"}
+
+
+def cpu_product(op, metric, rows, fwd_only, budget_s):
+    import torch
+    from oracle import clifford_oracle as O
+    n = len(metric)
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(rows, 1 << n, generator=g).requires_grad_(not fwd_only)
+    b = torch.randn(rows, 1 << n, generator=g).requires_grad_(not fwd_only)
+
+    def work():
+        c = O.einsum_product(op, a, b, list(metric))
+        if not fwd_only:
+            torch.autograd.grad(c, (a, b), torch.ones_like(c))
+
+    return cpu_rate(work, rows, budget_s, f"{op} {'fwd' if fwd_only else 'fwd+bwd'} {metric}")
+
+
 class Timer:
     def __init__(self, torch, stream, reps):
         self.torch, self.stream, self.reps = torch, stream, reps
@@ -252,6 +288,9 @@ def products_config(args, torch, cc, lib, T, name, metric, B, ops, fwd_only=Fals
             dt = (dfms + dbms) * 1e-3
             entry["per_term_path"] = {"fwd_ms": dfms, "bwd_ms": dbms, "pairs_per_s": B / dt,
                                       "valu_frac": flops / dt / 1e12 / PEAK_FP32_TFLOPS}
+        if not args.no_cpu:
+            rows = max(1, min(256, (1 << 16) >> n))  # bounded: 256 rows at n = 8, 64 at n = 10
+            entry["cpu_baseline"] = cpu_product(op, metric, rows, fwd_only, args.cpu_seconds / 5)
         res[op] = entry
     return {"workload": name, "metric": metric, "batch": B, "results": res}
 
@@ -312,7 +351,38 @@ def c3_layer(args, torch, cc, lib, T):
                           "fwd_frac_mfma": 2.0 * D * D * B / (gfms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS,
                           "bwd_frac_mfma": 4.0 * D * D * B / (gbms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS,
                           "frac_mfma": 6.0 * D * D * B / ((gfms + gbms) * 1e-3) / 1e12 / PEAK_FP32_TFLOPS},
-            "hbm_gbs_algorithmic": byts / (ms * 1e-3) / 1e9}
+            "hbm_gbs_algorithmic": byts / (ms * 1e-3) / 1e9,
+            "cpu_baseline": None if args.no_cpu else cpu_layer(args.cpu_seconds / 3)}
+
+
+def cpu_layer(budget_s):
+    import torch
+    from oracle import clifford_oracle as O
+    rows = 256
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(rows, 256, generator=g).requires_grad_()
+    w = (0.25 * torch.randn(1, 256, generator=g)).requires_grad_()
+
+    def work():
+        y = O.layer_forward("geom", x, w, [1] * 8)
+        torch.autograd.grad(y, (x, w), torch.ones_like(y))
+
+    return cpu_rate(work, rows, budget_s, "GeometricProductLayer Cl(8,0) fwd+bwd (x and weight grads)")
+
+
+def cpu_rotor(budget_s):
+    import torch
+    from oracle import clifford_oracle as O
+    rows = 256
+    g = torch.Generator().manual_seed(0)
+    biv = ((0.1 ** 0.5) * torch.randn(1, 28, generator=g)).double().requires_grad_()
+    x = torch.randn(rows, 256, generator=g).double().requires_grad_()
+
+    def work():
+        y = O.apply_bivector(biv, x, 8)
+        torch.autograd.grad(y, (x, biv), torch.ones_like(y))
+
+    return cpu_rate(work, rows, budget_s, "RotorLayer n = 8 fwd+bwd, rotor recompiled per chunk", "fp64")
 
 
 def c4_rotor(args, torch, cc, lib, T):
@@ -361,7 +431,8 @@ def c4_rotor(args, torch, cc, lib, T):
             "hbm_gbs_algorithmic": byts / (ms * 1e-3) / 1e9, "frac_hbm": byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
             "compile_fwd_ms": cms, "apply_fwd_ms": fms, "apply_bwd_ms": bms,
             "apply_fwd_frac_hbm": 8.0 * D * B / (fms * 1e-3) / 1e9 / PEAK_HBM_GBS,
-            "apply_bwd_frac_hbm": 12.0 * D * B / (bms * 1e-3) / 1e9 / PEAK_HBM_GBS}
+            "apply_bwd_frac_hbm": 12.0 * D * B / (bms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+            "cpu_baseline": None if args.no_cpu else cpu_rotor(args.cpu_seconds / 3)}
 
 
 def c5_degenerate(args, torch, cc, lib, T):
