@@ -96,6 +96,12 @@ def cpu_rate(work, rows: int, budget_s: float, label: str, dtype: str = "fp32"):
                       f"host CPU, median chunk time)"}
 
 
+# CPU baselines of --workload c1..c5 / all run after every GPU measurement of
+# the invocation (host threads spinning after the oracle's parallel regions
+# would otherwise slow the launches of the GPU steps): (dict, key, thunk).
+CPU_JOBS = []
+
+
 def cpu_product(op, metric, rows, fwd_only, budget_s):
     import torch
     from oracle import clifford_oracle as O
@@ -290,7 +296,8 @@ def products_config(args, torch, cc, lib, T, name, metric, B, ops, fwd_only=Fals
                                       "valu_frac": flops / dt / 1e12 / PEAK_FP32_TFLOPS}
         if not args.no_cpu:
             rows = max(1, min(256, (1 << 16) >> n))  # bounded: 256 rows at n = 8, 64 at n = 10
-            entry["cpu_baseline"] = cpu_product(op, metric, rows, fwd_only, args.cpu_seconds / 5)
+            CPU_JOBS.append((entry, "cpu_baseline",
+                             lambda op=op, rows=rows: cpu_product(op, metric, rows, fwd_only, args.cpu_seconds / 5)))
         res[op] = entry
     return {"workload": name, "metric": metric, "batch": B, "results": res}
 
@@ -351,8 +358,7 @@ def c3_layer(args, torch, cc, lib, T):
                           "fwd_frac_mfma": 2.0 * D * D * B / (gfms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS,
                           "bwd_frac_mfma": 4.0 * D * D * B / (gbms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS,
                           "frac_mfma": 6.0 * D * D * B / ((gfms + gbms) * 1e-3) / 1e12 / PEAK_FP32_TFLOPS},
-            "hbm_gbs_algorithmic": byts / (ms * 1e-3) / 1e9,
-            "cpu_baseline": None if args.no_cpu else cpu_layer(args.cpu_seconds / 3)}
+            "hbm_gbs_algorithmic": byts / (ms * 1e-3) / 1e9, "cpu_baseline": None}
 
 
 def cpu_layer(budget_s):
@@ -431,8 +437,7 @@ def c4_rotor(args, torch, cc, lib, T):
             "hbm_gbs_algorithmic": byts / (ms * 1e-3) / 1e9, "frac_hbm": byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
             "compile_fwd_ms": cms, "apply_fwd_ms": fms, "apply_bwd_ms": bms,
             "apply_fwd_frac_hbm": 8.0 * D * B / (fms * 1e-3) / 1e9 / PEAK_HBM_GBS,
-            "apply_bwd_frac_hbm": 12.0 * D * B / (bms * 1e-3) / 1e9 / PEAK_HBM_GBS,
-            "cpu_baseline": None if args.no_cpu else cpu_rotor(args.cpu_seconds / 3)}
+            "apply_bwd_frac_hbm": 12.0 * D * B / (bms * 1e-3) / 1e9 / PEAK_HBM_GBS, "cpu_baseline": None}
 
 
 def c5_degenerate(args, torch, cc, lib, T):
@@ -486,6 +491,7 @@ def main():
                           "add_ms": ams, "add_gbs": 3.0 * nbytes / (ams * 1e-3) / 1e9}))
         return
     runs = ["c1", "c2", "c3", "c4", "c5"] if args.workload == "all" else [args.workload]
+    out = []
     for w in runs:
         if w == "c1":
             r = products_config(args, torch, cc, lib, T, "c1: Cl(5,0) geom fwd", (1,) * 5, 1024, ["geom"], True)
@@ -494,10 +500,18 @@ def main():
                                 ["geom", "wedge", "inner", "lc", "rc", "regressive"])
         elif w == "c3":
             r = c3_layer(args, torch, cc, lib, T)
+            if not args.no_cpu:
+                CPU_JOBS.append((r, "cpu_baseline", lambda: cpu_layer(args.cpu_seconds / 3)))
         elif w == "c4":
             r = c4_rotor(args, torch, cc, lib, T)
+            if not args.no_cpu:
+                CPU_JOBS.append((r, "cpu_baseline", lambda: cpu_rotor(args.cpu_seconds / 3)))
         else:
             r = c5_degenerate(args, torch, cc, lib, T)
+        out.append(r)
+    for d, key, job in CPU_JOBS:
+        d[key] = job()
+    for r in out:
         print(json.dumps(r), flush=True)
 
 
