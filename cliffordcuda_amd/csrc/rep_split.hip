@@ -564,10 +564,12 @@ static int launch_pairs(const SplitTable& T, const PairSpec* ps, int npairs, lon
     P.out = out;
     P.ldo = ld_out;
     P.batch = batch;
+    // at most the resident grid, then the waves walk the batch and each wave's
+    // next group is prefetched during its current one (16384 rows at n = 10:
+    // ~10 % faster than a grid of four times the resident workgroups)
     const long long groups = (batch + 1) / 2;
-    long long blocks = (groups + 3) / 4;
-    if (blocks > 256LL * 8) blocks = 256LL * 8;  // then the waves walk the batch
-    const dim3 grid((unsigned)(blocks < 1 ? 1 : blocks));
+    const void* k = npairs == 2 ? (const void*)split_pairs2_kernel : (const void*)split_pairs1_kernel;
+    const dim3 grid(resident_grid(k, 256, 0, (groups + 3) / 4));
     if (npairs == 2) hipLaunchKernelGGL(split_pairs2_kernel, grid, dim3(256), 0, s, P, T);
     else hipLaunchKernelGGL(split_pairs1_kernel, grid, dim3(256), 0, s, P, T);
     return CLF_OK;
@@ -585,9 +587,9 @@ static void launch_fused(const SplitTable& T, const float* X, const float* Y, fl
                          hipStream_t s) {
     FusedSplit P{X, Y, out, (long long)batch};
     const long long groups = (batch + 1) / 2;
-    long long blocks = (groups + 3) / 4;
-    if (blocks > 256LL * 8) blocks = 256LL * 8;
-    hipLaunchKernelGGL(split_fused_kernel<KIND>, dim3((unsigned)(blocks < 1 ? 1 : blocks)), dim3(256), 0, s, P, T);
+    // grid rule of the pair sums: at most the resident workgroups
+    const dim3 grid(resident_grid((const void*)split_fused_kernel<KIND>, 256, 0, (groups + 3) / 4));
+    hipLaunchKernelGGL(split_fused_kernel<KIND>, grid, dim3(256), 0, s, P, T);
 }
 
 int split_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64_t batch, void* stream) {
