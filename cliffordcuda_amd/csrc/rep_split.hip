@@ -313,9 +313,12 @@ struct FusedRegions {
     static constexpr int out1 = KIND == 0 ? 0 : (KIND == 1 ? 0 : 1);
 };
 
+// waves per workgroup of the fused kernels
+constexpr int kFusedWaves = 4;
+
 template <int KIND>
-__global__ __launch_bounds__(256) void split_fused_kernel(FusedSplit P, SplitTable T) {
-    __shared__ float lds[4][4 * 1024];
+__global__ __launch_bounds__(64 * kFusedWaves) void split_fused_kernel(FusedSplit P, SplitTable T) {
+    __shared__ float lds[kFusedWaves][4 * 1024];
     using RG = FusedRegions<KIND>;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int b = lane >> 4, r = b >> 1;
@@ -359,12 +362,12 @@ __global__ __launch_bounds__(256) void split_fused_kernel(FusedSplit P, SplitTab
 
     const long long batch = P.batch;
     const long long ngroups = (batch + 1) / 2;
-    const long long gstride = (long long)gridDim.x * 4;
+    const long long gstride = (long long)gridDim.x * kFusedWaves;
     const float* X0 = P.X;
     const float* Y0 = P.Y;
     const float* X1 = P.X + 512;
     const float* Y1 = P.Y + 512;
-    long long g = (long long)blockIdx.x * 4 + wave;
+    long long g = (long long)blockIdx.x * kFusedWaves + wave;
     float4 ax0, ax1, ax2, ax3, ay0, ay1, ay2, ay3;
     CLF_SPLIT_FETCH(ax0, ax1, ax2, ax3, X0, 1024, 2 * g);
     CLF_SPLIT_FETCH(ay0, ay1, ay2, ay3, Y0, 1024, 2 * g);
@@ -588,8 +591,9 @@ static void launch_fused(const SplitTable& T, const float* X, const float* Y, fl
     FusedSplit P{X, Y, out, (long long)batch};
     const long long groups = (batch + 1) / 2;
     // grid rule of the pair sums: at most the resident workgroups
-    const dim3 grid(resident_grid((const void*)split_fused_kernel<KIND>, 256, 0, (groups + 3) / 4));
-    hipLaunchKernelGGL(split_fused_kernel<KIND>, grid, dim3(256), 0, s, P, T);
+    const dim3 grid(resident_grid((const void*)split_fused_kernel<KIND>, 64 * kFusedWaves, 0,
+                                  (groups + kFusedWaves - 1) / kFusedWaves));
+    hipLaunchKernelGGL(split_fused_kernel<KIND>, grid, dim3(64 * kFusedWaves), 0, s, P, T);
 }
 
 int split_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64_t batch, void* stream) {
