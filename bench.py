@@ -213,7 +213,7 @@ def headline(args, torch, cc, lib, T):
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic: a, b ~ N(0,1) seed 0, gc = ones",
-        "config": {"workload": "headline: Cl(8,0) geom_prod fwd+bwd (BASELINE.md headline row)", "batch": B,
+        "config": {"workload": "headline: Cl(8,0) geom_prod fwd+bwd, batch 262144, upstream gradient all-ones", "batch": B,
                    "n": n, "dim": D, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "kernel": "rep16_bwd_kernel", "achieved": achieved,
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
