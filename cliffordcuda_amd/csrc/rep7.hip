@@ -398,7 +398,7 @@ static bool rep7_table_build(uint32_t neg, Rep7Table& T) {
     }
     unsigned cols[4];
     int d = 0;
-    for (int i = 0; i < ns; ++i) {
+    for (int i = 0; i < ns && d < 4; ++i) {  // dim V <= 3: the x parts alone have rank 4
         if ((span[i] & 15u) != 0u) continue;
         cols[d] = span[i] >> 4;
         if (f2_rank(cols, d + 1) == d + 1) ++d;
