@@ -65,3 +65,47 @@ def test_rows_past_2_31_floats(metric, op, path, monkeypatch):
         assert torch.equal(nsq, cl.norm_sq(xs))
     del a, b, gc
     torch.cuda.empty_cache()
+
+
+# (layer class, metric): the Cl(8,0) representation layer, the GEMM layer path,
+# the rotor on the Cl(8,0) representation and the register plane-rotation chain
+LAYER_CASES = [
+    ("GeometricProductLayer", (1,) * 8),
+    ("WedgeProductLayer", (1,) * 8),
+    ("RotorLayer", (1,) * 7 + (-1,)),
+    ("RotorLayer", (1,) * 9),
+]
+
+
+@pytest.mark.parametrize("cls,metric", LAYER_CASES, ids=lambda v: str(v))
+def test_layer_rows_past_2_31_floats(cls, metric):
+    """Layer outputs and input gradients of the large batch's rows equal those
+    of the same rows as a batch of their own (the parameter gradients sum over
+    the batch and are not compared)."""
+    n = len(metric)
+    D = 1 << n
+    B = (1 << (31 - n)) + 3
+    free, _ = torch.cuda.mem_get_info()
+    if free < 6 * B * D * 4 + (4 << 30):
+        pytest.skip("needs about 52 GiB of free device memory")
+    print(f"[case] large batch layer={cls} metric={metric} B={B}", flush=True)
+    cl = cc.CliffordAlgebra(metric, device="cuda")
+    layer = getattr(cc, cls)(cl).cuda()
+    g = torch.Generator(device="cuda").manual_seed(6)
+    with torch.no_grad():
+        for p in layer.parameters():
+            p.copy_(0.2 * torch.randn(p.shape, device="cuda", generator=g))
+    x = torch.randn(B, D, device="cuda", generator=g).requires_grad_()
+    gy = torch.randn(B, D, device="cuda", generator=g)
+    rows = _rows(B)
+    y = layer(x)
+    (gx,) = torch.autograd.grad(y, (x,), gy)
+    big = [t.detach()[rows].clone() for t in (y, gx)]
+    del y, gx
+    xs = x.detach()[rows].clone().requires_grad_()
+    ys = layer(xs)
+    (gxs,) = torch.autograd.grad(ys, (xs,), gy[rows].clone())
+    for name, u, v in zip(("y", "gx"), big, (ys, gxs)):
+        assert torch.equal(u, v.detach()), name
+    del x, gy
+    torch.cuda.empty_cache()
