@@ -64,3 +64,18 @@ def test_masks():
 def test_free_functions_reject_cpu_tensors():
     with pytest.raises(RuntimeError, match="GPU"):
         cc.geom_prod(torch.zeros(2, 32), torch.zeros(2, 32))
+
+
+def test_bench_refuses_several_gpus():
+    """bench.py measures one GPU; --gpus above 1 exits with a message before
+    touching any device."""
+    import json
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    res = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                         capture_output=True, text=True, timeout=120)
+    assert res.returncode == 2
+    msg = json.loads(res.stdout.strip().splitlines()[-1])
+    assert "one GPU" in msg["error"]
