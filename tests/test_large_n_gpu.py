@@ -57,6 +57,33 @@ def test_tiled_equals_whole_row_n12(op, metric, monkeypatch):
     assert max(e) <= TOL, e
 
 
+@pytest.mark.parametrize("metric", [(1,) * 10 + (-1,), (1, 1, 1, 1, 1, -1, 0, 1, 1, -1, 1),
+                                    (1, -1, 1, 0, 1, 1, -1, 1, 1, 1, -1)],
+                         ids=["blocked11", "blocked11null", "mixed11"])
+@pytest.mark.parametrize("op", O.OPS)
+def test_n11_matches_oracle(op, metric):
+    """n = 11 takes a launch plan of its own (whole-row blocked kernels with two
+    waves per workgroup); every op forward and backward against the fp64
+    oracle on an odd batch, for metrics on the blocked path (low generators
+    alike, with and without a null generator above them) and on the
+    per-coefficient path (mixed low generators)."""
+    if op == "regressive" and 0 in metric:
+        pytest.skip("regressive is undefined for degenerate metrics")
+    g = torch.Generator().manual_seed(11)
+    a, b, gc = (torch.randn(3, 1 << 11, generator=g) for _ in range(3))
+    print(f"[case] n=11 op={op} metric={metric}", flush=True)
+    ad = a.cuda().requires_grad_()
+    bd = b.cuda().requires_grad_()
+    c = cc.products.product(op, ad, bd, metric)
+    c.backward(gc.cuda())
+    a64 = a.double().requires_grad_()
+    b64 = b.double().requires_grad_()
+    c64 = O.einsum_product(op, a64, b64, metric)
+    c64.backward(gc.double())
+    e = [rel_err(c, c64), rel_err(ad.grad, a64.grad), rel_err(bd.grad, b64.grad)]
+    assert max(e) <= TOL, e
+
+
 @pytest.mark.parametrize("op", O.OPS)
 def test_tiled_equals_generic_n14(op, monkeypatch):
     metric = (1,) * 11 + (-1, -1, 1) if op == "regressive" else (1,) * 11 + (-1, -1, 0)

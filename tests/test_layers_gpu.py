@@ -113,6 +113,37 @@ def test_c3_full_batch_vs_per_row_kernels(monkeypatch):
     assert rel_err(y[rows.cuda()], y64) <= TOL
 
 
+def test_c3_full_batch_gradients_vs_oracle_batch_sum():
+    """BASELINE config C3 at its full batch against the fp64 oracle, both
+    gradients. With the upstream gradient all ones and the layer linear in x,
+    L = sum_b sum_k (x_b w)_k = sum_k (S w)_k with S = sum_b x_b (fp64), so
+    the full-batch weight gradient equals the oracle's gradient on the single
+    row S, and every row of the x gradient equals the oracle's x gradient of
+    one row (it does not depend on x). The forward is checked through the
+    same linearity: sum_b y_b = S w."""
+    cl = cc.CliffordAlgebra([1] * 8, device="cuda")
+    layer = cc.GeometricProductLayer(cl)
+    g = torch.Generator().manual_seed(0)
+    B = 262144
+    x = torch.randn(B, 256, generator=g)
+    w = 0.25 * torch.randn(1, 256, generator=g)
+    with torch.no_grad():
+        layer.weight.copy_(w.cuda())
+    xd = x.cuda().requires_grad_()
+    print(f"[case] C3 full batch B={B} batch-sum identity", flush=True)
+    y = layer(xd)
+    y.sum().backward()
+    S = x.double().sum(0, keepdim=True).requires_grad_()
+    w64 = w.double().requires_grad_()
+    yS = O.layer_forward("geom", S, w64)
+    yS.sum().backward()
+    assert rel_err(y.detach().double().sum(0, keepdim=True), yS) <= TOL
+    assert rel_err(layer.weight.grad, w64.grad) <= TOL
+    x1 = x[:1].double().requires_grad_()
+    O.layer_forward("geom", x1, w.double()).sum().backward()
+    assert rel_err(xd.grad, x1.grad.expand(B, 256)) <= TOL
+
+
 @pytest.mark.parametrize("metric", [(1,) * 8, (1, -1) * 4], ids=["++++++++", "+-+-+-+-"])
 @pytest.mark.parametrize("side", [0, 1])
 @pytest.mark.parametrize("batch", [1, 77, 4099])

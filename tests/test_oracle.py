@@ -131,6 +131,62 @@ def test_reverse_antiautomorphism():
     torch.testing.assert_close(lhs, rhs, rtol=1e-12, atol=1e-11)
 
 
+def _unit_vectors(n):
+    e = torch.zeros(n + 1, 1 << n, dtype=torch.float64)
+    e[0, 0] = 1.0                      # the scalar 1
+    for k in range(n):
+        e[k + 1, 1 << k] = 1.0         # e_k
+    return e
+
+
+@pytest.mark.parametrize("metric", [(1, 1, -1, 0, 1), (-1, -1, 1, 1, -1), (0, 1, -1, 1, 0)])
+def test_grade_involution_is_the_automorphism_negating_vectors(metric):
+    """The grade involution is the algebra automorphism with e_k -> -e_k. An
+    automorphism is fixed by its action on the generators, so
+    inv(1) = 1, inv(e_k) = -e_k and inv(ab) = inv(a) inv(b) (with the
+    independently pinned geometric product) determine it; a wrong grade parity
+    on any blade breaks the product rule for some pair."""
+    n = len(metric)
+    e = _unit_vectors(n)
+    inv_e = O.grade_involution(e)
+    torch.testing.assert_close(inv_e[0], e[0], rtol=0, atol=0)
+    torch.testing.assert_close(inv_e[1:], -e[1:], rtol=0, atol=0)
+    a, b = rand_mv(4, n, 31), rand_mv(4, n, 32)
+    lhs = O.grade_involution(O.einsum_product("geom", a, b, metric))
+    rhs = O.einsum_product("geom", O.grade_involution(a), O.grade_involution(b), metric)
+    torch.testing.assert_close(lhs, rhs, rtol=1e-12, atol=1e-11)
+    # every basis blade, built as an ordered product of generators
+    for blade in range(1 << n):
+        prod = e[0:1].clone()
+        for k in range(n):
+            if (blade >> k) & 1:
+                prod = O.einsum_product("geom", prod, e[k + 1:k + 2], (1,) * n)
+        expect = prod.clone()
+        for k in range(n):
+            if (blade >> k) & 1:
+                expect = -expect
+        torch.testing.assert_close(O.grade_involution(prod), expect, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("metric", [(1, 1, -1, 0, 1), (-1, 0, 1, 1, -1)])
+def test_clifford_conjugation_is_reverse_of_involution(metric):
+    """Clifford conjugation is the anti-automorphism with e_k -> -e_k:
+    conj(1) = 1, conj(e_k) = -e_k, conj(ab) = conj(b) conj(a), and it equals
+    the composition reverse(grade_involution(x)) (both pinned on their own)."""
+    n = len(metric)
+    e = _unit_vectors(n)
+    conj_e = O.clifford_conjugation(e)
+    torch.testing.assert_close(conj_e[0], e[0], rtol=0, atol=0)
+    torch.testing.assert_close(conj_e[1:], -e[1:], rtol=0, atol=0)
+    a, b = rand_mv(4, n, 33), rand_mv(4, n, 34)
+    lhs = O.clifford_conjugation(O.einsum_product("geom", a, b, metric))
+    rhs = O.einsum_product("geom", O.clifford_conjugation(b), O.clifford_conjugation(a), metric)
+    torch.testing.assert_close(lhs, rhs, rtol=1e-12, atol=1e-11)
+    x = rand_mv(3, n, 35)
+    torch.testing.assert_close(O.clifford_conjugation(x), O.reverse(O.grade_involution(x)), rtol=0, atol=0)
+    torch.testing.assert_close(O.clifford_conjugation(x), O.grade_involution(O.reverse(x)), rtol=0, atol=0)
+
+
 def test_wedge_of_vectors_is_antisymmetric_part():
     metric = (1, -1, 1, 0, 1)
     a, b = rand_mv(4, 5, 6, grade=1), rand_mv(4, 5, 7, grade=1)
