@@ -60,6 +60,8 @@ SIGNATURES = {
     "clf_product_bcast_ws_bytes": (_sz, [_i32, _i64]),
     "clf_product_bcast_fwd": (_i32, [_i32, _i32, _i32, _u32, _u32, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
     "clf_product_bcast_bwd": (_i32, [_i32, _i32, _i32, _u32, _u32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
+    "clf_product_bcast_bwd_noalloc_scratch_bytes": (_sz, []),
+    "clf_product_bcast_bwd_noalloc": (_i32, [_i32, _i32, _i32, _u32, _u32, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
 }
 
 _lock = threading.Lock()

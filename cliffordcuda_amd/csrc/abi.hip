@@ -83,6 +83,9 @@ int bcast_fwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* 
               int64_t batch, void* ws, size_t ws_bytes, void* stream);
 int bcast_bwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w, const float* gy,
               float* gx, float* gw, int64_t batch, void* ws, size_t ws_bytes, void* stream);
+size_t bcast_scratch_bytes();
+int bcast_bwd_noalloc(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w,
+                      const float* gy, float* gx, float* gw, int64_t batch, void* stream);
 
 }  // namespace clf
 
@@ -179,6 +182,15 @@ int clf_product_bcast_bwd(int op, int side, int n, uint32_t neg_mask, uint32_t n
                           size_t ws_bytes, void* stream) {
     clf::clear_error();
     return clf::bcast_bwd(op, side, n, neg_mask, null_mask, x, w, gy, gx, gw, batch, ws, ws_bytes, stream);
+}
+
+size_t clf_product_bcast_bwd_noalloc_scratch_bytes(void) { return clf::bcast_scratch_bytes(); }
+
+int clf_product_bcast_bwd_noalloc(int op, int side, int n, uint32_t neg_mask, uint32_t null_mask, const float* x,
+                                  const float* w, const float* gy, float* gx, float* gw, int64_t batch,
+                                  void* stream) {
+    clf::clear_error();
+    return clf::bcast_bwd_noalloc(op, side, n, neg_mask, null_mask, x, w, gy, gx, gw, batch, stream);
 }
 
 }  // extern "C"

@@ -16,6 +16,9 @@
 // chunks of 32, each wave a 64 x 64 sub-tile of 2 x 2 v_mfma_f32_32x32x2f32
 // blocks (operand lanes: A[m = l%32][k = l/32], B[k = l/32][n = l%32];
 // accumulator element e of lane l: row 8*(e/4) + 4*(l/32) + e%4, column l%32).
+#include <atomic>
+#include <mutex>
+
 #include "clf_common.h"
 
 namespace clf {
@@ -264,9 +267,9 @@ int rep_bcast_fwd(int side, int n, uint32_t neg, const float* x, const float* w,
 int rep_bcast_bwd(int side, int n, uint32_t neg, const float* x, const float* w, const float* gy, float* gx, float* gw,
                   int64_t batch, float* ws, void* stream);
 
-static int bcast_splits(int64_t batch) {
+static int bcast_splits(int64_t batch, int cap = 128) {
     long long s = (batch + 2047) / 2048;
-    if (s > 128) s = 128;
+    if (s > cap) s = cap;
     if (s < 1) s = 1;
     return (int)s;
 }
@@ -332,29 +335,33 @@ int bcast_fwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* 
     return CLF_OK;
 }
 
-int bcast_bwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w, const float* gy,
-              float* gx, float* gw, int64_t batch, void* ws, size_t ws_bytes, void* stream) {
+// Argument checks shared by both backward entry points (no HIP call).
+static int check_bcast_bwd_args(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w,
+                                const float* gy, float* gx, float* gw, int64_t batch) {
     if (int rc = check_bcast(op, side, n, neg, nul, batch)) return rc;
     if (!gx && !gw) return CLF_OK;
-    if (!w || !ws || (batch > 0 && (!gy || (gw && !x)))) return set_error(CLF_ERR_ARG, "null pointer argument");
-    if (ws_bytes < bcast_ws_bytes(n, batch))
-        return set_error(CLF_ERR_WORKSPACE, "workspace of at least " + std::to_string(bcast_ws_bytes(n, batch)) +
-                                                " bytes required");
-    if ((((uintptr_t)x) | ((uintptr_t)gy) | ((uintptr_t)gx) | ((uintptr_t)ws)) & 15u)
+    if (!w || (batch > 0 && (!gy || (gw && !x)))) return set_error(CLF_ERR_ARG, "null pointer argument");
+    if ((((uintptr_t)x) | ((uintptr_t)gy) | ((uintptr_t)gx)) & 15u)
         return set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
-    if (rep_bcast_applicable(op, n, neg, nul)) {
-        if (rep_bcast_ws_floats(batch) * sizeof(float) > ws_bytes)
-            return set_error(CLF_ERR_WORKSPACE, "workspace too small for the weight-gradient partials");
-        return rep_bcast_bwd(side, n, neg, x, w, gy, gx, gw, batch, (float*)ws, stream);
-    }
+    return CLF_OK;
+}
+
+// The backward's launches on an already checked workspace. GEMM path layout:
+// [0, DD) the weight matrix for gx, [DD, 2 DD) unused (the forward's transposed
+// matrix), then `splits` partial products of x^T gy and their sum G; the split
+// count is at most max_splits.
+static int bcast_bwd_launch(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w,
+                            const float* gy, float* gx, float* gw, int64_t batch, float* ws, int max_splits,
+                            void* stream) {
+    if (rep_bcast_applicable(op, n, neg, nul)) return rep_bcast_bwd(side, n, neg, x, w, gy, gx, gw, batch, ws, stream);
     hipStream_t s = (hipStream_t)stream;
     const int D = 1 << n;
     const size_t DD = (size_t)D * D;
-    float* parts = (float*)ws + 2 * DD;  // [DD, 2 DD): the forward's transposed matrix, unused here
-    const int splits = bcast_splits(batch);
+    float* parts = ws + 2 * DD;
+    const int splits = bcast_splits(batch, max_splits);
     float* G = parts + (size_t)splits * DD;
     if (gx && batch > 0) {
-        float* Mw = (float*)ws;
+        float* Mw = ws;
         hipLaunchKernelGGL(bcast_build_kernel, dim3((unsigned)((DD + 255) / 256)), dim3(256), 0, s, op, side, n, neg,
                            nul, w, Mw, (float*)nullptr);
         launch_nn(gy, Mw, gx, batch, D, s);
@@ -374,6 +381,89 @@ int bcast_bwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* 
     }
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
+}
+
+int bcast_bwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w, const float* gy,
+              float* gx, float* gw, int64_t batch, void* ws, size_t ws_bytes, void* stream) {
+    if (int rc = check_bcast_bwd_args(op, side, n, neg, nul, x, w, gy, gx, gw, batch)) return rc;
+    if (!gx && !gw) return CLF_OK;
+    if (!ws) return set_error(CLF_ERR_ARG, "null pointer argument");
+    if (((uintptr_t)ws) & 15u) return set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
+    if (ws_bytes < bcast_ws_bytes(n, batch))
+        return set_error(CLF_ERR_WORKSPACE, "workspace of at least " + std::to_string(bcast_ws_bytes(n, batch)) +
+                                                " bytes required");
+    if (rep_bcast_applicable(op, n, neg, nul) && rep_bcast_ws_floats(batch) * sizeof(float) > ws_bytes)
+        return set_error(CLF_ERR_WORKSPACE, "workspace too small for the weight-gradient partials");
+    return bcast_bwd_launch(op, side, n, neg, nul, x, w, gy, gx, gw, batch, (float*)ws, 128, stream);
+}
+
+// ---- allocation-free backward ------------------------------------------------
+// The same backward with its workspace in a fixed device array instead of a
+// caller buffer, for callers that cannot allocate (code under graph capture,
+// serving loops). The array lives for the whole process on every device the
+// entry point runs on. Its host-side name is only a stand-in for the symbol:
+// the device address comes from hipGetSymbolAddress, looked up once per device
+// with that device current, and only that address is ever passed to kernels.
+// Every call on a device shares the array; calls that overlap on one device
+// (different streams or threads) race on it. No kernel relies on its previous
+// contents: every workspace entry a launch reads was written earlier in the
+// same call.
+constexpr size_t kBcastScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) float scratch[kBcastScratchBytes / sizeof(float)];
+
+constexpr int kScratchMaxDevices = 64;
+static std::atomic<float*> g_scratch_ptr[kScratchMaxDevices];
+static std::mutex g_scratch_mu;
+
+static int scratch_address(float** out) {
+    int dev = 0;
+    CLF_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kScratchMaxDevices) return set_error(CLF_ERR_ARG, "device index beyond the scratch table");
+    float* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            void* addr = nullptr;
+            CLF_HIP_CHECK(hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)));
+            if (!addr) return set_error(CLF_ERR_HIP, "hipGetSymbolAddress returned a null scratch address");
+            p = (float*)addr;
+            g_scratch_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return CLF_OK;
+}
+
+size_t bcast_scratch_bytes() { return kBcastScratchBytes; }
+
+// Split count that keeps the GEMM path's workspace inside the scratch array.
+static int noalloc_max_splits(int n) {
+    const size_t DD = (size_t)1 << (2 * n);
+    const long long slots = (long long)(kBcastScratchBytes / (DD * sizeof(float)));
+    return (int)(slots - 3);
+}
+
+int bcast_bwd_noalloc(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w,
+                      const float* gy, float* gx, float* gw, int64_t batch, void* stream) {
+    if (int rc = check_bcast_bwd_args(op, side, n, neg, nul, x, w, gy, gx, gw, batch)) return rc;
+    if (!gx && !gw) return CLF_OK;
+    size_t need;
+    if (rep_bcast_applicable(op, n, neg, nul)) {
+        need = rep_bcast_ws_floats(batch) * sizeof(float);
+    } else {
+        const int cap = noalloc_max_splits(n);
+        if (cap < 1)
+            return set_error(CLF_ERR_WORKSPACE, "n = " + std::to_string(n) + " needs more than the " +
+                                                    std::to_string(kBcastScratchBytes) + "-byte scratch array");
+        need = (3 + (size_t)bcast_splits(batch, cap)) * ((size_t)1 << (2 * n)) * sizeof(float);
+    }
+    if (need > kBcastScratchBytes)
+        return set_error(CLF_ERR_WORKSPACE, "this call needs " + std::to_string(need) + " bytes of scratch; the " +
+                                                "allocation-free backward has " + std::to_string(kBcastScratchBytes));
+    float* ws = nullptr;
+    if (int rc = scratch_address(&ws)) return rc;
+    return bcast_bwd_launch(op, side, n, neg, nul, x, w, gy, gx, gw, batch, ws, noalloc_max_splits(n), stream);
 }
 
 }  // namespace clf

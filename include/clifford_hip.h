@@ -183,6 +183,24 @@ int clf_product_bcast_bwd(int op, int side, int n, uint32_t neg_mask, uint32_t n
                           float* gx, float* gw, int64_t batch,
                           void* ws, size_t ws_bytes, void* stream);
 
+/* Allocation-free variant of clf_product_bcast_bwd. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments and results as clf_product_bcast_bwd without ws / ws_bytes:
+ * the workspace is a fixed device array of the library
+ * (clf_product_bcast_bwd_noalloc_scratch_bytes() bytes, 32 MiB), held on each
+ * device it runs on until the process ends. The call allocates nothing (no
+ * hipMalloc, no library allocation); the GEMM path caps its split-K count so
+ * its partials fit the array, and a call that would need more returns
+ * CLF_ERR_WORKSPACE. All calls on one device share the array: calls that
+ * overlap on a device (several streams or threads at once) race and must be
+ * serialised by the caller. */
+size_t clf_product_bcast_bwd_noalloc_scratch_bytes(void);
+
+int clf_product_bcast_bwd_noalloc(int op, int side, int n, uint32_t neg_mask, uint32_t null_mask,
+                                  const float* x, const float* w, const float* gy,
+                                  float* gx, float* gw, int64_t batch, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
