@@ -19,6 +19,13 @@ reference library's einsum/Cayley-table path:
   ``R = exp(sum_m b_m e_{i_m} e_{j_m})`` and the bivector in
   ``torch.triu_indices(n, n, 1)`` order (``algebra.py:116-140``). The
   reference ignores the metric on this path, so the oracle does too.
+* ``rotation_matrix`` / ``givens_factor`` / ``compile_bivector_cs`` restate
+  ``compile_bivector`` (``algebra.py:343-352``: eigh-exp -> Givens factor,
+  ``givens_factor.cu:23-55``), the (C(n,2), 2) cs tensor it returns;
+  ``givens_chain_apply`` restates ``apply_rotor(cs, x)``
+  (``givens_apply_mb_perm_packed.cu:33-64``, tables ``_utils/core.py:19-50``)
+  and ``givens_chain_backward_ref`` its backward
+  (``givens_apply_mb_perm_packed.cu:111-160``).
 
 Pinning (how each function is checked independently of its own formula) is
 listed per function below and exercised in ``tests/test_oracle.py``.
@@ -290,3 +297,131 @@ def vector_rotation_matrix(biv: torch.Tensor, n: int) -> torch.Tensor:
     y = apply_bivector(biv, eye, n)
     cols = torch.stack([y[:, 1 << a] for a in range(n)], 0)  # (out a, in col)
     return cols
+
+
+# ── the reference's Givens cs chain (algebra.py:343-369) ────────────────────
+
+def plane_pairs(n: int):
+    """Rotation planes (p, q), p < q, in lex order (``givens_factor.cu:23-24``)."""
+    return [(p, q) for p in range(n - 1) for q in range(p + 1, n)]
+
+
+def rotation_matrix(biv: torch.Tensor, n: int) -> torch.Tensor:
+    """R = expm(B), B = 2 (M - M^T), M[i_m, j_m] = b_m: the matrix the reference
+    exponentiates and factors (``eigh_exp.cu:283-288``; its closed form
+    ``eigh_exp.cu:55-67`` is exp(B)). torch's fp64 matrix exponential, so the
+    result is differentiable. Pinned by: R^T equals the grade-1 action of the
+    sandwich (``vector_rotation_matrix``), itself pinned to scipy's expm(-B)."""
+    M = torch.zeros(n, n, dtype=biv.dtype)
+    ij = torch.triu_indices(n, n, offset=1)
+    M = M.index_put((ij[0], ij[1]), biv.reshape(-1))
+    return torch.linalg.matrix_exp(2.0 * (M - M.T))
+
+
+def givens_factor(R: torch.Tensor) -> torch.Tensor:
+    """cs (C(n,2), 2) of the reference's Givens factorisation
+    (``givens_factor.cu:23-55``): for the planes (p, q) in lex order,
+    a = A[p][p], b = A[q][p], r = sqrt(a^2 + b^2), c = a / r, s_raw = -b / r,
+    rows p, q of A rotated (A[p] <- c A[p] - s_raw A[q], A[q] <- s_raw A[p] + c A[q]),
+    and (c, -s_raw) stored at index C - 1 - k for the k-th plane (reversed).
+    A zero column pair (r = 0) gives the identity (c, s) = (1, 0) here; the
+    reference clamps r to 1e-12 and writes (0, 0) there.
+    Differentiable (torch ops). Pinned by: reconstruction R = prod_k G_k^T with
+    A_final = I (r >= 0 makes the factorisation unique), and the chain apply of
+    the factors equals the independently pinned sandwich."""
+    n = R.shape[-1]
+    A = R.clone()
+    pairs = plane_pairs(n)
+    C = len(pairs)
+    out = [None] * C
+    for k, (p, q) in enumerate(pairs):
+        a, b = A[p, p], A[q, p]
+        r = torch.sqrt(a * a + b * b)
+        if float(r) > 0.0:
+            c, s_raw = a / r, -b / r
+        else:
+            c, s_raw = torch.ones_like(a), torch.zeros_like(a)
+        rp, rq = A[p].clone(), A[q].clone()
+        A = A.clone()
+        A[p] = c * rp - s_raw * rq
+        A[q] = s_raw * rp + c * rq
+        out[C - 1 - k] = torch.stack([c, -s_raw])
+    return torch.stack(out, 0)
+
+
+def compile_bivector_cs(biv: torch.Tensor, n: int) -> torch.Tensor:
+    """The reference's ``compile_bivector`` (``algebra.py:343-352``):
+    Givens factors of R = expm(B), differentiable to the bivector."""
+    return givens_factor(rotation_matrix(biv, n))
+
+
+def plane_pair_table(n: int, p: int, q: int):
+    """Blade pairs of plane (p, q) and their signs (``_utils/core.py:19-50``):
+    i with bit p set and bit q clear, j = i ^ (2^p + 2^q), sign
+    (-1)^{(|i| - 1 - |i & (2^p - 1)|) + |i >> (q + 1)|}."""
+    ii, jj, sg = [], [], []
+    for i in range(1 << n):
+        if (i >> p) & 1 and not (i >> q) & 1:
+            removal = bin(i).count("1") - 1 - bin(i & ((1 << p) - 1)).count("1")
+            insert = bin(i >> (q + 1)).count("1")
+            ii.append(i)
+            jj.append(i ^ ((1 << p) | (1 << q)))
+            sg.append(-1.0 if (removal + insert) & 1 else 1.0)
+    return torch.tensor(ii), torch.tensor(jj), torch.tensor(sg, dtype=torch.float64)
+
+
+def givens_chain_apply(cs: torch.Tensor, x: torch.Tensor, n: int | None = None) -> torch.Tensor:
+    """The reference's ``apply_rotor(cs, x)`` forward
+    (``givens_apply_mb_perm_packed.cu:33-64``): planes applied lex-first
+    (cs index C-1 down to 0), each mapping the pair (x_i, x_j) to
+    (c x_i + s sig x_j, -s sig x_i + c x_j); blades holding both or neither of
+    p, q are unchanged. Any (c, s), unit or not. Differentiable to cs and x
+    (autograd gives the exact derivative of this forward).
+    Pinned by: with the factors of R it equals the sandwich ``apply_bivector``;
+    one plane of angle t rotates e_p towards e_q in closed form."""
+    if n is None:
+        n = x.shape[-1].bit_length() - 1
+    pairs = plane_pairs(n)
+    C = len(pairs)
+    y = x
+    for k, (p, q) in enumerate(pairs):
+        c, s = cs[C - 1 - k, 0], cs[C - 1 - k, 1]
+        ii, jj, sg = plane_pair_table(n, p, q)
+        sg = sg.to(x.dtype)
+        xi, xj = y[..., ii], y[..., jj]
+        y = y.clone()
+        y[..., ii] = c * xi + s * sg * xj
+        y[..., jj] = -s * sg * xi + c * xj
+    return y
+
+
+def givens_chain_backward_ref(cs: torch.Tensor, y: torch.Tensor, gy: torch.Tensor, n: int | None = None):
+    """The reference's Givens-apply backward (``givens_apply_mb_perm_packed.cu:111-160``
+    and ``mb_perm_packed.py:34-42``), restated: walk the planes from the last
+    applied to the first, rebuild each plane's input from its output with the
+    transposed pair map (the inverse only when c^2 + s^2 = 1), and accumulate
+      grad_c += g_i v_i + g_j v_j,   grad_s += sig (g_i v_j - g_j v_i)
+    with g the gradient of the plane's output and v its rebuilt input, summed
+    over the batch; the gradient itself goes through the transposed map.
+    Returns (grad_cs, grad_x); the reference returns no grad_x.
+    Pinned by: equals autograd through ``givens_chain_apply`` for unit pairs."""
+    if n is None:
+        n = y.shape[-1].bit_length() - 1
+    pairs = plane_pairs(n)
+    C = len(pairs)
+    v = y.clone()
+    g = gy.clone()
+    gcs = torch.zeros(C, 2, dtype=y.dtype)
+    for k in reversed(range(C)):
+        p, q = pairs[k]
+        c, s = float(cs[C - 1 - k, 0]), float(cs[C - 1 - k, 1])
+        ii, jj, sg = plane_pair_table(n, p, q)
+        sg = sg.to(y.dtype)
+        vi, vj, gi, gj = v[..., ii], v[..., jj], g[..., ii], g[..., jj]
+        vi_pre = c * vi - s * sg * vj
+        vj_pre = s * sg * vi + c * vj
+        gcs[C - 1 - k, 0] = (gi * vi_pre + gj * vj_pre).sum()
+        gcs[C - 1 - k, 1] = (sg * (gi * vj_pre - gj * vi_pre)).sum()
+        v[..., ii], v[..., jj] = vi_pre, vj_pre
+        g[..., ii], g[..., jj] = c * gi - s * sg * gj, s * sg * gi + c * gj
+    return gcs, g

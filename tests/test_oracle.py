@@ -338,3 +338,101 @@ def test_normalize_metric():
         O.normalize_metric(3, (1, 1))
     with pytest.raises(ValueError):
         O.normalize_metric(2, (1, 2))
+
+
+# ── the reference's Givens cs chain ─────────────────────────────────────────
+
+def _givens_matrix(n, p, q, c, s):
+    """Row rotation the factorisation applies for one plane:
+    A[p] <- c A[p] + s A[q], A[q] <- -s A[p] + c A[q] (s = -s_raw)."""
+    G = torch.eye(n, dtype=torch.float64)
+    G[p, p], G[p, q], G[q, p], G[q, q] = c, s, -s, c
+    return G
+
+
+@pytest.mark.parametrize("n,seed,scale", [(5, 1, 0.3), (7, 2, 1.0), (8, 3, 2.5)])
+def test_givens_factor_reconstructs_rotation(n, seed, scale):
+    """R = prod over planes (lex order) of G_k^T, i.e. G_C ... G_1 R = I, with
+    c^2 + s^2 = 1 per plane: the factorisation the cs pairs describe, checked by
+    rebuilding R from cs alone (the storage is reversed: plane k at C-1-k)."""
+    g = torch.Generator().manual_seed(seed)
+    biv = scale * torch.randn(1, n * (n - 1) // 2, generator=g, dtype=torch.float64)
+    R = O.rotation_matrix(biv, n)
+    torch.testing.assert_close(R @ R.T, torch.eye(n, dtype=torch.float64), rtol=0, atol=1e-12)
+    cs = O.givens_factor(R)
+    pairs = O.plane_pairs(n)
+    C = len(pairs)
+    assert cs.shape == (C, 2)
+    torch.testing.assert_close(cs.pow(2).sum(1), torch.ones(C, dtype=torch.float64), rtol=0, atol=1e-13)
+    A = R.clone()
+    for k, (p, q) in enumerate(pairs):
+        A = _givens_matrix(n, p, q, float(cs[C - 1 - k, 0]), float(cs[C - 1 - k, 1])) @ A
+        assert abs(float(A[q, p])) < 1e-12        # the plane's entry is eliminated
+        assert float(A[p, p]) >= -1e-12           # r >= 0 convention
+    torch.testing.assert_close(A, torch.eye(n, dtype=torch.float64), rtol=0, atol=1e-11)
+    # R^T is the grade-1 action of the sandwich (pinned to scipy's expm(-B) above)
+    torch.testing.assert_close(R.T, O.vector_rotation_matrix(biv, n), rtol=0, atol=1e-11)
+
+
+@pytest.mark.parametrize("n", [4, 5, 7])
+def test_givens_chain_of_factors_is_the_sandwich(n):
+    """apply_rotor(compile_bivector(b), x) of the reference equals ~R x R: the
+    chain of the factors against the independently pinned sandwich oracle."""
+    g = torch.Generator().manual_seed(20 + n)
+    biv = 0.5 * torch.randn(1, n * (n - 1) // 2, generator=g, dtype=torch.float64)
+    x = torch.randn(3, 1 << n, generator=g, dtype=torch.float64)
+    cs = O.compile_bivector_cs(biv, n)
+    torch.testing.assert_close(O.givens_chain_apply(cs, x, n), O.apply_bivector(biv, x, n), rtol=0, atol=1e-12)
+
+
+def test_givens_chain_single_plane_closed_form():
+    """One plane (p, q) with (c, s) and every other plane the identity: the
+    vector e_p goes to c e_p - s e_q, e_q to s e_p + c e_q, and the bivector
+    e_p e_r (r outside the plane) to c e_p e_r - s e_q e_r (a sign from moving
+    e_q past generators between p and q does not arise for r > q)."""
+    n = 5
+    pairs = O.plane_pairs(n)
+    C = len(pairs)
+    p, q, r = 1, 3, 4
+    k = pairs.index((p, q))
+    c, s = math.cos(0.7), math.sin(0.7)
+    cs = torch.zeros(C, 2, dtype=torch.float64)
+    cs[:, 0] = 1.0
+    cs[C - 1 - k] = torch.tensor([c, s], dtype=torch.float64)
+    x = torch.zeros(3, 1 << n, dtype=torch.float64)
+    x[0, 1 << p] = 1.0
+    x[1, 1 << q] = 1.0
+    x[2, (1 << p) | (1 << r)] = 1.0
+    y = O.givens_chain_apply(cs, x, n)
+    exp = torch.zeros_like(y)
+    exp[0, 1 << p], exp[0, 1 << q] = c, -s
+    exp[1, 1 << p], exp[1, 1 << q] = s, c
+    exp[2, (1 << p) | (1 << r)], exp[2, (1 << q) | (1 << r)] = c, -s
+    torch.testing.assert_close(y, exp, rtol=0, atol=1e-15)
+
+
+def test_givens_chain_backward_ref_is_autograd_for_unit_pairs():
+    """The reference's backward (inputs rebuilt with the transposed pair map)
+    equals the exact derivative of the chain when every (c, s) is a unit pair;
+    for non-unit pairs it does not (the transposed map is then not the inverse),
+    which is the reference's behaviour this restatement keeps."""
+    n = 5
+    C = n * (n - 1) // 2
+    g = torch.Generator().manual_seed(9)
+    ang = torch.randn(C, generator=g, dtype=torch.float64)
+    x = torch.randn(4, 1 << n, generator=g, dtype=torch.float64)
+    gy = torch.randn(4, 1 << n, generator=g, dtype=torch.float64)
+    for unit in (True, False):
+        cs = torch.stack([ang.cos(), ang.sin()], 1)
+        if not unit:
+            cs = cs * (1.0 + 0.3 * torch.rand(C, 1, generator=g, dtype=torch.float64))
+        cs_l = cs.clone().requires_grad_()
+        x_l = x.clone().requires_grad_()
+        y = O.givens_chain_apply(cs_l, x_l, n)
+        y.backward(gy)
+        gcs, gx = O.givens_chain_backward_ref(cs, y.detach(), gy, n)
+        torch.testing.assert_close(gx, x_l.grad, rtol=0, atol=1e-12)   # gx: exact for any pairs
+        if unit:
+            torch.testing.assert_close(gcs, cs_l.grad, rtol=0, atol=1e-11)
+        else:
+            assert float((gcs - cs_l.grad).abs().max()) > 1e-3
