@@ -409,14 +409,15 @@ def c4_rotor(args, torch, cc, lib, T):
 
     ms = T.step_ms(step, args.warmup, args.steps)
     sp = T.stream.cuda_stream
-    state = cl.compile_bivector(layer.bivector.detach())
+    from cliffordcuda_amd import rotor as rotor_mod
+    state = rotor_mod._compile_fwd(layer.bivector.detach().reshape(-1), n)
     y = torch.empty_like(x)
     gx = torch.empty_like(x)
     gs = torch.empty_like(state)
     nb = lib.clf_rotor_apply_ws_bytes(n, B)
     ws = torch.empty(max(4, nb) // 4, device=dev)
     biv = layer.bivector.detach()
-    cms = T.kernel_ms(lambda: lib.clf_rotor_compile_fwd(n, biv.data_ptr(), state.data_ptr(), sp))
+    cms = T.kernel_ms(lambda: lib.clf_rotor_compile_fwd(n, biv.data_ptr(), state.data_ptr(), None, sp))
     fms = T.kernel_ms(lambda: lib.clf_rotor_apply_fwd(n, state.data_ptr(), x.data_ptr(), y.data_ptr(), B, sp))
     bms = T.kernel_ms(lambda: lib.clf_rotor_apply_bwd(n, state.data_ptr(), x.data_ptr(), gy.data_ptr(),
                                                       gx.data_ptr(), gs.data_ptr(), B, ws.data_ptr(), nb, sp))

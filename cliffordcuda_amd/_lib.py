@@ -15,6 +15,8 @@ import torch
 LIB_NAME = "libclifford_hip.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
+ABI_VERSION = 2  # CLF_ABI_VERSION of include/clifford_hip.h
+
 # status codes (include/clifford_hip.h)
 CLF_OK = 0
 CLF_ERR_ARG = 1
@@ -52,11 +54,15 @@ SIGNATURES = {
     "clf_norm_sq_fwd": (_i32, [_i32, _u32, _u32, _vp, _vp, _i64, _vp]),
     "clf_norm_sq_bwd": (_i32, [_i32, _u32, _u32, _vp, _vp, _vp, _i64, _vp]),
     "clf_rotor_state_floats": (_i32, [_i32]),
-    "clf_rotor_compile_fwd": (_i32, [_i32, _vp, _vp, _vp]),
+    "clf_rotor_compile_fwd": (_i32, [_i32, _vp, _vp, _vp, _vp]),
     "clf_rotor_compile_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp]),
     "clf_rotor_apply_fwd": (_i32, [_i32, _vp, _vp, _vp, _i64, _vp]),
     "clf_rotor_apply_ws_bytes": (_sz, [_i32, _i64]),
     "clf_rotor_apply_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
+    "clf_rotor_cs_apply_fwd": (_i32, [_i32, _vp, _vp, _vp, _i64, _vp]),
+    "clf_rotor_cs_apply_ws_bytes": (_sz, [_i32, _i64]),
+    "clf_rotor_cs_apply_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
+    "clf_rotor_cs_compile_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp]),
     "clf_product_bcast_ws_bytes": (_sz, [_i32, _i64]),
     "clf_product_bcast_fwd": (_i32, [_i32, _i32, _i32, _u32, _u32, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
     "clf_product_bcast_bwd": (_i32, [_i32, _i32, _i32, _u32, _u32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
@@ -84,8 +90,10 @@ def load():
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args
-            if lib.clf_abi_version() != 1:
-                raise RuntimeError("cliffordcuda_amd: ABI version mismatch")
+            if lib.clf_abi_version() != ABI_VERSION:
+                raise RuntimeError(
+                    f"cliffordcuda_amd: {LIB_PATH} has ABI version {lib.clf_abi_version()}, this package needs "
+                    f"{ABI_VERSION}; rebuild it")
             _lib = lib
     return _lib
 

@@ -216,6 +216,10 @@ def _rotor_compile_backward(ctx, g_state):
 rotor_compile.register_autograd(_rotor_compile_backward, setup_context=_rotor_compile_setup)
 
 
+# The state operators serve apply_bivector: the state's gradient is the
+# component of dL/dQ that rotor_compile's backward reads (its cs and spin
+# blocks are caches of Q and get zero), not a derivative with respect to every
+# state entry, so the state is never handed to callers as a free tensor.
 @torch.library.custom_op(f"{_NS}::rotor_apply", mutates_args=())
 def rotor_apply(state: Tensor, x: Tensor, n: int) -> Tensor:
     from .rotor import _apply_fwd
@@ -255,3 +259,75 @@ def _rotor_apply_backward(ctx, gy):
 
 
 rotor_apply.register_autograd(_rotor_apply_backward, setup_context=_rotor_apply_setup)
+
+
+@torch.library.custom_op(f"{_NS}::rotor_compile_cs", mutates_args=())
+def rotor_compile_cs(biv: Tensor, n: int) -> Tensor:
+    from .rotor import _compile_fwd
+    return _compile_fwd(biv, n, want_cs=True)[1]
+
+
+@rotor_compile_cs.register_fake
+def _(biv, n):
+    from .rotor import n_planes
+    return biv.new_empty(n_planes(n), 2)
+
+
+@torch.library.custom_op(f"{_NS}::rotor_compile_cs_bwd", mutates_args=())
+def rotor_compile_cs_bwd(biv: Tensor, g_cs: Tensor, n: int) -> Tensor:
+    from .rotor import _cs_compile_bwd
+    return _cs_compile_bwd(biv, g_cs, n)
+
+
+@rotor_compile_cs_bwd.register_fake
+def _(biv, g_cs, n):
+    return torch.empty_like(biv)
+
+
+def _rotor_compile_cs_backward(ctx, g_cs):
+    (biv,) = ctx.saved_tensors
+    return rotor_compile_cs_bwd(biv, g_cs.contiguous(), ctx.n), None
+
+
+rotor_compile_cs.register_autograd(_rotor_compile_cs_backward, setup_context=_rotor_compile_setup)
+
+
+@torch.library.custom_op(f"{_NS}::rotor_cs_apply", mutates_args=())
+def rotor_cs_apply(cs: Tensor, x: Tensor, n: int) -> Tensor:
+    from .rotor import _cs_apply_fwd
+    return _cs_apply_fwd(cs, x, n)
+
+
+@rotor_cs_apply.register_fake
+def _(cs, x, n):
+    return torch.empty_like(x)
+
+
+@torch.library.custom_op(f"{_NS}::rotor_cs_apply_bwd", mutates_args=())
+def rotor_cs_apply_bwd(cs: Tensor, y: Tensor, gy: Tensor, n: int, need_cs: bool,
+                       need_x: bool) -> Tuple[Tensor, Tensor]:
+    from .rotor import _cs_apply_bwd
+    g_cs, gx = _cs_apply_bwd(cs, y, gy, n, need_cs, need_x)
+    return (g_cs if g_cs is not None else _placeholder(cs)), (gx if gx is not None else _placeholder(y))
+
+
+@rotor_cs_apply_bwd.register_fake
+def _(cs, y, gy, n, need_cs, need_x):
+    return ((torch.empty_like(cs) if need_cs else _placeholder(cs)),
+            (torch.empty_like(y) if need_x else _placeholder(y)))
+
+
+def _rotor_cs_apply_setup(ctx, inputs, output):
+    cs, x, n = inputs
+    ctx.save_for_backward(cs, output)
+    ctx.n = n
+
+
+def _rotor_cs_apply_backward(ctx, gy):
+    cs, y = ctx.saved_tensors
+    need_cs, need_x = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+    g_cs, gx = rotor_cs_apply_bwd(cs, y, gy.contiguous(), ctx.n, need_cs, need_x)
+    return _none_if_unneeded(g_cs, need_cs), _none_if_unneeded(gx, need_x), None
+
+
+rotor_cs_apply.register_autograd(_rotor_cs_apply_backward, setup_context=_rotor_cs_apply_setup)

@@ -5,7 +5,8 @@ messages, running on the gfx950 kernels of ``libclifford_hip.so``.
 Differences from the reference, all supersets:
   * products accept any n >= 1 (the reference requires n >= 5);
   * ``apply_rotor`` / ``apply_bivector`` also return a gradient to ``x``
-    (the reference's rotor backward returns ``None`` for x);
+    (the reference's rotor backward returns ``None`` for x), and rotors are
+    served for 7 <= n <= 12 (the reference's tables go to n = 12);
   * ``compile=`` on ``dual`` / ``norm_sq`` selects the same single-pass HIP
     kernel as the default (the reference uses torch.compile for it).
 """
@@ -106,20 +107,28 @@ class CliffordAlgebra:
                 f"at least 32 = warp size); got n={self.n}")
 
     def compile_bivector(self, bivector):
-        """Build the rotor state for ``bivector`` (1, C(n,2)) in lex-pair order.
-        Returns a tensor that ``apply_rotor`` consumes."""
+        """Givens cs chain (C(n,2), 2) of the rotor of ``bivector`` (1, C(n,2))
+        in lex-pair order; differentiable to the bivector. Returns a tensor
+        that ``apply_rotor`` consumes."""
         self._check_rotor_supported()
         _validate.check_bivector(bivector, self.n, self._num_basis_biv, self.device, self.dtype)
         return _rotor.compile_bivector(bivector, self.n)
 
     def apply_rotor(self, cs, x):
-        """y = ~R x R for a rotor state from ``compile_bivector``."""
+        """Apply a cs chain (from ``compile_bivector``, or any (C(n,2), 2)
+        tensor of (c, s) pairs) to a batch of multivectors; differentiable to
+        cs and to x."""
         self._check_rotor_supported()
         _validate.check_mv(x, "x", self.dim, self.device, self.dtype)
         return _rotor.apply_rotor(cs, x, self.n)
 
     def apply_bivector(self, bivector, x):
-        return self.apply_rotor(self.compile_bivector(bivector), x)
+        """``apply_rotor(compile_bivector(bivector), x)`` in one pass, without
+        materialising cs; differentiable to the bivector and to x."""
+        self._check_rotor_supported()
+        _validate.check_bivector(bivector, self.n, self._num_basis_biv, self.device, self.dtype)
+        _validate.check_mv(x, "x", self.dim, self.device, self.dtype)
+        return _rotor.apply_bivector(bivector, x, self.n)
 
     # ── misc ───────────────────────────────────────────────────────────
     def to(self, device):

@@ -72,11 +72,16 @@ int norm_sq_bwd(int n, uint32_t neg, uint32_t nul, const float* x, const float* 
 
 int rotor_state_floats(int n);
 size_t rotor_apply_ws_bytes(int n, int64_t batch);
-int rotor_compile_fwd(int n, const float* biv, float* state, void* stream);
+int rotor_compile_fwd(int n, const float* biv, float* state, float* cs, void* stream);
 int rotor_compile_bwd(int n, const float* biv, const float* g_state, float* g_biv, void* stream);
 int rotor_apply_fwd(int n, const float* state, const float* x, float* y, int64_t batch, void* stream);
 int rotor_apply_bwd(int n, const float* state, const float* x, const float* gy, float* gx, float* g_state,
                     int64_t batch, void* ws, size_t ws_bytes, void* stream);
+size_t rotor_cs_apply_ws_bytes(int n, int64_t batch);
+int rotor_cs_apply_fwd(int n, const float* cs, const float* x, float* y, int64_t batch, void* stream);
+int rotor_cs_apply_bwd(int n, const float* cs, const float* y, const float* gy, float* gx, float* g_cs,
+                       int64_t batch, void* ws, size_t ws_bytes, void* stream);
+int rotor_cs_compile_bwd(int n, const float* biv, const float* g_cs, float* g_biv, void* stream);
 
 size_t bcast_ws_bytes(int n, int64_t batch);
 int bcast_fwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w, float* y,
@@ -146,9 +151,9 @@ int clf_norm_sq_bwd(int n, uint32_t neg_mask, uint32_t null_mask, const float* x
 
 int clf_rotor_state_floats(int n) { return clf::rotor_state_floats(n); }
 
-int clf_rotor_compile_fwd(int n, const float* biv, float* state, void* stream) {
+int clf_rotor_compile_fwd(int n, const float* biv, float* state, float* cs, void* stream) {
     clf::clear_error();
-    return clf::rotor_compile_fwd(n, biv, state, stream);
+    return clf::rotor_compile_fwd(n, biv, state, cs, stream);
 }
 
 int clf_rotor_compile_bwd(int n, const float* biv, const float* g_state, float* g_biv, void* stream) {
@@ -167,6 +172,24 @@ int clf_rotor_apply_bwd(int n, const float* state, const float* x, const float* 
                         int64_t batch, void* ws, size_t ws_bytes, void* stream) {
     clf::clear_error();
     return clf::rotor_apply_bwd(n, state, x, gy, gx, g_state, batch, ws, ws_bytes, stream);
+}
+
+int clf_rotor_cs_apply_fwd(int n, const float* cs, const float* x, float* y, int64_t batch, void* stream) {
+    clf::clear_error();
+    return clf::rotor_cs_apply_fwd(n, cs, x, y, batch, stream);
+}
+
+size_t clf_rotor_cs_apply_ws_bytes(int n, int64_t batch) { return clf::rotor_cs_apply_ws_bytes(n, batch); }
+
+int clf_rotor_cs_apply_bwd(int n, const float* cs, const float* y, const float* gy, float* gx, float* g_cs,
+                           int64_t batch, void* ws, size_t ws_bytes, void* stream) {
+    clf::clear_error();
+    return clf::rotor_cs_apply_bwd(n, cs, y, gy, gx, g_cs, batch, ws, ws_bytes, stream);
+}
+
+int clf_rotor_cs_compile_bwd(int n, const float* biv, const float* g_cs, float* g_biv, void* stream) {
+    clf::clear_error();
+    return clf::rotor_cs_compile_bwd(n, biv, g_cs, g_biv, stream);
 }
 
 size_t clf_product_bcast_ws_bytes(int n, int64_t batch) { return clf::bcast_ws_bytes(n, batch); }

@@ -4,15 +4,23 @@
 //
 // What is computed (the composite of reference algebra.py:343-373, Euclidean):
 //   B = 2 (M - M^T), M[i_m, j_m] = b_m (lex pairs, kernels/rotor/eigh_exp.cu:283-288)
-//   Q = expm(-B)                 the grade-1 action of ~R x R, R = exp(sum b_m e_{i_m} e_{j_m})
-//   Q = G_1 G_2 ... G_C          Givens factorisation, planes (p, q) in lex order,
-//                                G_k e_p = c e_p + s e_q, G_k e_q = -s e_p + c e_q
-//   y = Lambda(Q) x              outermorphism: Lambda(G_1)(...(Lambda(G_C) x))
-// A plane rotation acts on the blade pairs (I with p not q, J = I ^ {p,q}):
-//   y_I = c x_I - s sig x_J,  y_J = c x_J + s sig x_I,  sig = (-1)^{|I & (p, q)|}
-// (bits of I strictly between p and q).
+//   R = expm(B)                  the matrix the reference factors (its closed form
+//                                kernels/rotor/eigh_exp.cu:55-67 is exp(B))
+//   Q = R^T = expm(-B)           the grade-1 action of ~R x R, R = exp(sum b_m e_{i_m} e_{j_m})
+//   cs                           the reference's Givens factors of R (givens_factor.cu:23-38):
+//                                planes (p, q) in lex order, c = a / r, s = b / r with
+//                                a = A[p][p], b = A[q][p]; rows A[p] <- c A[p] + s A[q],
+//                                A[q] <- -s A[p] + c A[q]; (c, s) of plane k stored at
+//                                index C - 1 - k (C = C(n,2))
+//   y = chain(cs) x              planes applied lex-first; plane (p, q) maps the blade
+//                                pairs (I with p not q, J = I ^ {p,q}) as
+//                                y_I = c x_I + s sig x_J,  y_J = c x_J - s sig x_I,
+//                                sig = (-1)^{|I & (p, q)|} (bits strictly between p
+//                                and q), the reference's givens_apply_mb_perm_packed.cu:33-64.
+// For the factors of a rotation the chain is the outermorphism Lambda(Q).
 //
-// Gradients. With gx = Lambda(Q)^T gy (the chain run backwards with s -> -s),
+// Gradients of the composite (bivector -> y). With gx = Lambda(Q)^T gy (the chain
+// transposed),
 //   dL/dQ = Q Gamma,  Gamma_ab = sum_rows sum_{I: b in I, a not in I} sig x_I gx_{I^{a,b}}
 // (the derivation extension of Q^{-1} dQ; only its antisymmetric part matters,
 // since Q stays orthogonal), and the bivector gradient follows
@@ -21,6 +29,15 @@
 //   dL/db_m = 2 (dL/dB[i_m][j_m] - dL/dB[j_m][i_m]),  dL/dB = -dL/dA.
 // The reference instead runs torch eigh + a closed form + Givens kernels with
 // host syncs and returns no gradient to x (extensions/rotor/*.py).
+//
+// Gradients of the chain on a caller's cs (apply_rotor(cs, x) with cs a free
+// tensor): the reference's backward (givens_apply_mb_perm_packed.cu:111-160):
+// walking the planes from the last applied, each plane's input is rebuilt from
+// its output with the transposed pair map and
+//   grad_c += g_I v_I + g_J v_J,  grad_s += sig (g_I v_J - g_J v_I)
+// summed over the batch (exact for unit pairs, the reference's rule for any);
+// and, through cs = Givens(expm(B)), the bivector gradient by reverse-mode
+// through the factorisation (fp64) followed by the Frechet step above.
 //
 // Apply layout: one row is spread over 2^(n-RB) lanes, each holding 2^RB
 // consecutive blades in registers. Planes inside the register bits are pure
@@ -33,7 +50,7 @@
 namespace clf {
 
 constexpr int kRotorMinN = 2;
-constexpr int kRotorMaxN = 10;
+constexpr int kRotorMaxN = 12;
 
 __host__ __device__ constexpr int n_planes(int n) { return n * (n - 1) / 2; }
 __host__ __device__ constexpr int plane_p(int n, int k) {
@@ -53,7 +70,7 @@ __host__ __device__ constexpr int plane_q(int n, int k) {
     return p + 1 + k;
 }
 // register bits per lane: rows of n <= 8 use 4 lanes (partner exchanges are
-// quad-local DPP permutes), n = 9, 10 use 8 / 16 lanes of 64 blades each
+// quad-local DPP permutes), n = 9 .. 12 use 8 .. 64 lanes of 64 blades each
 __host__ __device__ constexpr int rotor_rb(int n) { return n < 4 ? n : (n <= 8 ? n - 2 : 6); }
 // parity of the bits of r strictly between positions p and q (p < q)
 __host__ __device__ constexpr int between_par(unsigned r, int p, int q) {
@@ -61,8 +78,9 @@ __host__ __device__ constexpr int between_par(unsigned r, int p, int q) {
     for (int b = p + 1; b < q; ++b) c += (r >> b) & 1u;
     return c & 1;
 }
-// state: Q (n x n), the (c, s) pairs of the chain, and for n = 8 also the
-// 16 x 16 matrix U = phi(R) of the Cl(8,0) representation (row-major)
+// state: Q (n x n), the cs pairs of the chain (the reference's layout), and for
+// n = 8 also the 16 x 16 matrix U = phi(R) of the Cl(8,0) representation
+// (row-major)
 __host__ __device__ constexpr int spin_offset(int n) { return n * n + 2 * n_planes(n); }
 __host__ __device__ constexpr int state_floats(int n) { return spin_offset(n) + (n == kSpinN ? 256 : 0); }
 
@@ -73,11 +91,12 @@ __device__ __forceinline__ float dpp_mov(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 
-// value of v in lane (lane ^ MASK) for MASK < 32: quad-local bits by DPP quad
-// permutes (full-rate VALU), bits 2..4 by one ds_swizzle in bit-mask mode
+// value of v in lane (lane ^ MASK) for MASK < 64: quad-local bits by DPP quad
+// permutes (full-rate VALU), bits 2..4 by one ds_swizzle in bit-mask mode, bit 5
+// (the other half of the wave) by ds_bpermute
 template <unsigned MASK>
 __device__ __forceinline__ float lane_xor(float v) {
-    static_assert(MASK < 32, "lane exchange limited to 32 lanes");
+    static_assert(MASK < 64, "lane exchange limited to one wave");
     float r = v;
     if constexpr ((MASK & 3u) == 1u) r = dpp_mov<0xB1>(r);       // quad_perm [1,0,3,2]
     else if constexpr ((MASK & 3u) == 2u) r = dpp_mov<0x4E>(r);  // quad_perm [2,3,0,1]
@@ -86,15 +105,21 @@ __device__ __forceinline__ float lane_xor(float v) {
         constexpr int pattern = (int)(((MASK & 0x1Cu) << 10) | 0x1Fu);  // and 0x1F, or 0, xor MASK
         r = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(r), pattern));
     }
+    if constexpr ((MASK & 32u) != 0u) r = __shfl_xor(r, 32, 64);
     return r;
 }
 
+// One plane of the chain, in the form y_I = c x_I - s sig x_J,
+// y_J = c x_J + s sig x_I: the reference's pair map has the opposite sign of s,
+// so the forward uses s = -cs_s and the transposed map s = +cs_s. Plane K (lex)
+// reads the pair stored at index C - 1 - K.
 template <int N, int RB, int K, bool FWD>
 __device__ __forceinline__ void rot_plane(float (&v)[1 << RB], const float* __restrict__ cs, unsigned L) {
     constexpr int P = plane_p(N, K), Qb = plane_q(N, K);
     constexpr int V = 1 << RB;
-    const float c = cs[2 * K];
-    const float s = FWD ? cs[2 * K + 1] : -cs[2 * K + 1];
+    constexpr int SLOT = n_planes(N) - 1 - K;
+    const float c = cs[2 * SLOT];
+    const float s = FWD ? -cs[2 * SLOT + 1] : cs[2 * SLOT + 1];
     if constexpr (Qb < RB) {  // both generators in the register bits
         constexpr unsigned mp = 1u << P, mq = 1u << Qb;
 #pragma unroll
@@ -151,9 +176,9 @@ __device__ __forceinline__ void rot_plane(float (&v)[1 << RB], const float* __re
 template <int N, int RB, bool FWD, int... Ks>
 __device__ __forceinline__ void rot_chain_seq(float (&v)[1 << RB], const float* __restrict__ cs, unsigned L,
                                               std::integer_sequence<int, Ks...>) {
-    // forward: Lambda(G_1)(...(Lambda(G_C) x)) -> planes C-1 .. 0; transpose: 0 .. C-1
+    // forward: lex plane 0 first; transpose: the reverse order
     constexpr int C = n_planes(N);
-    (rot_plane<N, RB, FWD ? (C - 1 - Ks) : Ks, FWD>(v, cs, L), ...);
+    (rot_plane<N, RB, FWD ? Ks : (C - 1 - Ks), FWD>(v, cs, L), ...);
 }
 
 template <int N, int RB, bool FWD>
@@ -198,12 +223,11 @@ __device__ __forceinline__ void store_row_part(const float (&v)[1 << RB], float*
 // The loop condition is the same for all lanes of a row, so a row's lanes
 // stay active together and every shuffle partner is active.
 template <int N, bool FWD>
-__global__ __launch_bounds__(256) void rotor_apply_kernel(const float* __restrict__ state,
+__global__ __launch_bounds__(256) void rotor_apply_kernel(const float* __restrict__ cs,
                                                            const float* __restrict__ X, float* __restrict__ Y,
                                                            long long batch) {
     constexpr int RB = rotor_rb(N);
     constexpr int LB = N - RB;
-    const float* cs = state + N * N;
     const unsigned L = threadIdx.x & ((1u << LB) - 1u);
     const long long rows_per_block = 256 >> LB;
     const long long stride = (long long)gridDim.x * rows_per_block;
@@ -307,11 +331,16 @@ __device__ __forceinline__ float skew_lane_sign(int k, unsigned Lp) {
     return (qset != lneg) ? 1.f : -1.f;
 }
 
+__device__ __forceinline__ float wave_sum_f32(float v) {
+    for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
 // Persistent: each workgroup walks rows with a grid stride, writes gx (if
 // requested) and, if gamma_ws != nullptr, its partial K (C(N,2) floats) to
 // gamma_ws[blockIdx.x * C(N,2)].
 template <int N>
-__global__ __launch_bounds__(256) void rotor_apply_bwd_kernel(const float* __restrict__ state,
+__global__ __launch_bounds__(256) void rotor_apply_bwd_kernel(const float* __restrict__ cs,
                                                                const float* __restrict__ X,
                                                                const float* __restrict__ GY,
                                                                float* __restrict__ GX,
@@ -320,7 +349,6 @@ __global__ __launch_bounds__(256) void rotor_apply_bwd_kernel(const float* __res
     constexpr int LB = N - RB;
     constexpr int LPR = 1 << LB;
     constexpr int C = n_planes(N);
-    const float* cs = state + N * N;
     const unsigned L = threadIdx.x & (LPR - 1);
     const int rows_per_block = blockDim.x >> LB;
     const bool want_gamma = gamma_ws != nullptr;
@@ -349,25 +377,192 @@ __global__ __launch_bounds__(256) void rotor_apply_bwd_kernel(const float* __res
         }
     }
     if (!want_gamma) return;  // uniform: a kernel argument
-    // 1) sum over the rows of each wave: lanes with equal L sit at stride LPR
-#pragma unroll
-    for (int i = 0; i < C; ++i)
-        for (int off = LPR; off < 64; off <<= 1) acc[i] += __shfl_xor(acc[i], off, 64);
-    __shared__ float red[4][C][LPR];  // blockDim.x == 256: four waves
+    // each lane position's sign, then one sum over the whole wave (rows and
+    // lane positions), then over the four waves
+    __shared__ float red[4][C];  // blockDim.x == 256: four waves
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (lane < LPR) {
 #pragma unroll
-        for (int i = 0; i < C; ++i) red[wave][i][lane] = acc[i];
+    for (int i = 0; i < C; ++i) {
+        const float t = wave_sum_f32(skew_lane_sign<N, RB>(i, L) * acc[i]);
+        if (lane == 0) red[wave][i] = t;
     }
     __syncthreads();
-    // 2) sum over waves and lane positions with each position's sign
-    for (int k = threadIdx.x; k < C; k += blockDim.x) {
-        float t = 0.f;
-        for (int Lp = 0; Lp < LPR; ++Lp) {
-            const float sgn = skew_lane_sign<N, RB>(k, (unsigned)Lp);
-            t += sgn * (red[0][k][Lp] + red[1][k][Lp] + red[2][k][Lp] + red[3][k][Lp]);
+    for (int k = threadIdx.x; k < C; k += blockDim.x)
+        gamma_ws[(long long)blockIdx.x * C + k] = (red[0][k] + red[1][k]) + (red[2][k] + red[3][k]);
+}
+
+// ---- the chain with rows staged in LDS (any n up to 12, run-time planes) ----
+// Used for the reference's backward on a caller's cs (every n) and for all
+// chain work at n = 11, 12, whose rows (8 and 16 KB) do not fit a register
+// layout. A workgroup stages kLdsBlades floats per array (whole rows; one row
+// at n = 12) and walks the planes with a barrier between planes; each thread
+// owns kLdsBlades / 1024 blade pairs of every plane, found by inserting zero
+// bits at p and q into the pair number:
+//   base = deposit(t), I = base | 2^p (p set, q clear), J = base | 2^q.
+// Modes:
+//   LDS_FWD    y = chain(cs) x
+//   LDS_TR     gx = chain(cs)^T gy
+//   LDS_CS_BWD from (y, gy): gx and the cs gradient (the reference's rule:
+//              inputs rebuilt with the transposed pair map,
+//              grad_c += g_I v_I + g_J v_J, grad_s += sig (g_I v_J - g_J v_I))
+//   LDS_GAMMA  from (x, gy): gx = chain^T gy and the statistics
+//              K_pq = sum sig (x_J gx_I - x_I gx_J) of the composite backward
+// Per-plane sums go through a wave reduction into a per-wave LDS slot (no
+// atomics, fixed order), then one partial per workgroup.
+constexpr int kLdsBlades = 4096;
+enum LdsMode { LDS_FWD = 0, LDS_TR = 1, LDS_CS_BWD = 2, LDS_GAMMA = 3 };
+
+__device__ __forceinline__ unsigned deposit2(unsigned t, int p, int q) {
+    const unsigned lo = t & ((1u << p) - 1u);
+    const unsigned mid = (t >> p) & ((1u << (q - p - 1)) - 1u);
+    const unsigned hi = t >> (q - 1);
+    return lo | (mid << (p + 1)) | (hi << (q + 1));
+}
+
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256) void rotor_chain_lds_kernel(int n, const float* __restrict__ cs,
+                                                               const float* __restrict__ A,
+                                                               const float* __restrict__ B, float* __restrict__ OUT,
+                                                               float* __restrict__ parts, long long batch) {
+    constexpr bool TWO = (MODE == LDS_CS_BWD || MODE == LDS_GAMMA);
+    constexpr int kMaxW = 2 * 66;  // 2 C(12, 2)
+    __shared__ float va[kLdsBlades];
+    __shared__ float vb[TWO ? kLdsBlades : 1];
+    __shared__ float acc[TWO ? 4 : 1][TWO ? kMaxW : 1];
+    const int D = 1 << n;
+    const int C = n * (n - 1) / 2;
+    const int rpb = kLdsBlades >> n > 0 ? kLdsBlades >> n : 1;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int pairs = (rpb * D) >> 2;  // per plane in the staged rows
+    if (TWO)
+        for (int e = tid; e < 4 * kMaxW; e += blockDim.x) (&acc[0][0])[e] = 0.f;
+    for (long long row0 = (long long)blockIdx.x * rpb; row0 < batch; row0 += (long long)gridDim.x * rpb) {
+        const long long rows = (batch - row0) < rpb ? (batch - row0) : rpb;
+        const int nb = (int)(rows << n);
+        __syncthreads();  // the previous group's last plane and stores are done
+        for (int e = tid * 4; e < nb; e += blockDim.x * 4) {
+            *reinterpret_cast<float4*>(&va[e]) = *reinterpret_cast<const float4*>(A + (row0 << n) + e);
+            if (TWO) *reinterpret_cast<float4*>(&vb[e]) = *reinterpret_cast<const float4*>(B + (row0 << n) + e);
         }
-        gamma_ws[(long long)blockIdx.x * C + k] = t;
+        if (MODE == LDS_GAMMA) {
+            // gx = chain^T gy on vb (planes last to first), then K from (va = x, vb = gx)
+            for (int k = C - 1; k >= -C; --k) {
+                __syncthreads();
+                const bool stats = k < 0;
+                const int kk = stats ? -1 - k : k;
+                int p = 0, rem = kk;
+                while (rem >= n - 1 - p) {
+                    rem -= n - 1 - p;
+                    ++p;
+                }
+                const int q = p + 1 + rem;
+                const float c = cs[2 * (C - 1 - kk)], sv = cs[2 * (C - 1 - kk) + 1];
+                const unsigned between = ((1u << q) - 1u) & ~((2u << p) - 1u);
+                float part = 0.f;
+                for (int t = tid; t < pairs; t += blockDim.x) {
+                    const int r = t >> (n - 2), tt = t & ((D >> 2) - 1);
+                    const unsigned base = deposit2((unsigned)tt, p, q);
+                    const int I = (r << n) | (int)(base | (1u << p)), J = (r << n) | (int)(base | (1u << q));
+                    const float sig = (__popc(base & between) & 1) ? -1.f : 1.f;
+                    if (r >= rows) continue;
+                    const float gI = vb[I], gJ = vb[J];
+                    if (!stats) {
+                        // transposed pair map: (gI, gJ) <- (c gI - s sig gJ, c gJ + s sig gI)
+                        vb[I] = __builtin_fmaf(c, gI, -sv * sig * gJ);
+                        vb[J] = __builtin_fmaf(c, gJ, sv * sig * gI);
+                    } else {
+                        part = __builtin_fmaf(sig, __builtin_fmaf(va[J], gI, -va[I] * gJ), part);
+                    }
+                }
+                if (stats) {
+                    part = wave_sum_dpp(part);
+                    if (lane == 0) acc[wave][kk] += part;
+                }
+            }
+            __syncthreads();
+            for (int e = tid * 4; e < nb; e += blockDim.x * 4)
+                if (OUT) *reinterpret_cast<float4*>(OUT + (row0 << n) + e) = *reinterpret_cast<const float4*>(&vb[e]);
+            continue;
+        }
+        for (int step = 0; step < C; ++step) {
+            __syncthreads();
+            const int k = (MODE == LDS_FWD) ? step : C - 1 - step;
+            int p = 0, rem = k;
+            while (rem >= n - 1 - p) {
+                rem -= n - 1 - p;
+                ++p;
+            }
+            const int q = p + 1 + rem;
+            const float c = cs[2 * (C - 1 - k)], sv = cs[2 * (C - 1 - k) + 1];
+            const unsigned between = ((1u << q) - 1u) & ~((2u << p) - 1u);
+            float dc = 0.f, dsum = 0.f;
+            for (int t = tid; t < pairs; t += blockDim.x) {
+                const int r = t >> (n - 2), tt = t & ((D >> 2) - 1);
+                if (r >= rows) continue;
+                const unsigned base = deposit2((unsigned)tt, p, q);
+                const int I = (r << n) | (int)(base | (1u << p)), J = (r << n) | (int)(base | (1u << q));
+                const float ss = (__popc(base & between) & 1) ? -sv : sv;
+                const float xI = va[I], xJ = va[J];
+                if (MODE == LDS_FWD) {
+                    va[I] = __builtin_fmaf(c, xI, ss * xJ);
+                    va[J] = __builtin_fmaf(c, xJ, -ss * xI);
+                } else {
+                    // rebuilt input (LDS_CS_BWD) or transposed gradient (LDS_TR)
+                    const float pI = __builtin_fmaf(c, xI, -ss * xJ);
+                    const float pJ = __builtin_fmaf(c, xJ, ss * xI);
+                    va[I] = pI;
+                    va[J] = pJ;
+                    if (MODE == LDS_CS_BWD) {
+                        const float gI = vb[I], gJ = vb[J];
+                        const float sig = (__popc(base & between) & 1) ? -1.f : 1.f;
+                        dc = __builtin_fmaf(gI, pI, __builtin_fmaf(gJ, pJ, dc));
+                        dsum = __builtin_fmaf(sig, __builtin_fmaf(gI, pJ, -gJ * pI), dsum);
+                        vb[I] = __builtin_fmaf(c, gI, -ss * gJ);
+                        vb[J] = __builtin_fmaf(c, gJ, ss * gI);
+                    }
+                }
+            }
+            if (MODE == LDS_CS_BWD) {
+                dc = wave_sum_dpp(dc);
+                dsum = wave_sum_dpp(dsum);
+                if (lane == 0) {
+                    acc[wave][2 * (C - 1 - k)] += dc;
+                    acc[wave][2 * (C - 1 - k) + 1] += dsum;
+                }
+            }
+        }
+        __syncthreads();
+        const float* res = (MODE == LDS_CS_BWD) ? vb : va;
+        if (OUT)
+            for (int e = tid * 4; e < nb; e += blockDim.x * 4)
+                *reinterpret_cast<float4*>(OUT + (row0 << n) + e) = *reinterpret_cast<const float4*>(&res[e]);
+    }
+    if (!TWO || !parts) return;
+    __syncthreads();
+    const int W = (MODE == LDS_CS_BWD) ? 2 * C : C;
+    for (int e = tid; e < W; e += blockDim.x)
+        parts[(long long)blockIdx.x * W + e] = (acc[0][e] + acc[1][e]) + (acc[2][e] + acc[3][e]);
+}
+
+// out[e] = sum_p parts[p * width + e] in fp64, one workgroup, deterministic
+__global__ __launch_bounds__(256) void parts_sum_kernel(const float* __restrict__ parts, int nparts, int width,
+                                                        float* __restrict__ out) {
+    for (int e = threadIdx.x; e < width; e += blockDim.x) {
+        double t0 = 0.0, t1 = 0.0, t2 = 0.0, t3 = 0.0;
+        int p = 0;
+        for (; p + 3 < nparts; p += 4) {
+            t0 += (double)parts[(long long)p * width + e];
+            t1 += (double)parts[(long long)(p + 1) * width + e];
+            t2 += (double)parts[(long long)(p + 2) * width + e];
+            t3 += (double)parts[(long long)(p + 3) * width + e];
+        }
+        for (; p < nparts; ++p) t0 += (double)parts[(long long)p * width + e];
+        out[e] = (float)((t0 + t1) + (t2 + t3));
     }
 }
 
@@ -463,10 +658,13 @@ __device__ __forceinline__ double shfl_f64(double v, int src) {
     return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
 
-// E <- G_k^T E for the planes in lex order (E ends as I), lane j < N holding
-// column j of E; lane 0 writes the (c, s) pairs
+// The reference's Givens factorisation of R (lane j < N holding column j of
+// E = R): for the planes in lex order E <- G_k E (E ends as I), and lane 0
+// writes the (c, s) of plane k at index C - 1 - k of cs (and of cs2 if given).
 template <int N>
-__device__ __forceinline__ void givens_cols(double (&col)[N], float* __restrict__ cs, int lane) {
+__device__ __forceinline__ void givens_cols(double (&col)[N], float* __restrict__ cs, float* __restrict__ cs2,
+                                            int lane) {
+    constexpr int C = n_planes(N);
 #pragma unroll
     for (int p = 0; p < N - 1; ++p) {
 #pragma unroll
@@ -478,8 +676,12 @@ __device__ __forceinline__ void givens_cols(double (&col)[N], float* __restrict_
             col[p] = c * ep + s * eq;
             col[q] = -s * ep + c * eq;
             if (lane == 0) {
-                cs[2 * k] = (float)c;
-                cs[2 * k + 1] = (float)s;
+                cs[2 * (C - 1 - k)] = (float)c;
+                cs[2 * (C - 1 - k) + 1] = (float)s;
+                if (cs2) {
+                    cs2[2 * (C - 1 - k)] = (float)c;
+                    cs2[2 * (C - 1 - k) + 1] = (float)s;
+                }
             }
         }
     }
@@ -566,20 +768,22 @@ __device__ __forceinline__ double generator_entry(const float* __restrict__ biv,
     return i < j ? -2.0 * b : 2.0 * b;
 }
 
+// Lane j < N computes column j of R = expm(B) = Q^T, i.e. row j of Q.
 template <int N>
 __global__ __launch_bounds__(64) void rotor_compile_fwd_cols_kernel(const float* __restrict__ biv,
-                                                                     float* __restrict__ state) {
+                                                                     float* __restrict__ state,
+                                                                     float* __restrict__ cs_out) {
     __shared__ double Z[N * N];
     const int j = threadIdx.x;
-    for (int idx = j; idx < N * N; idx += 64) Z[idx] = generator_entry(biv, N, idx / N, idx % N);
+    for (int idx = j; idx < N * N; idx += 64) Z[idx] = generator_entry(biv, N, idx % N, idx / N);  // B = A^T
     __syncthreads();
     double col[N];
     expm_cols<N>(col, Z, j);
     if (j < N)
 #pragma unroll
-        for (int i = 0; i < N; ++i) state[i * N + j] = (float)col[i];
-    // Givens elimination E <- G_k^T E (planes in lex order); E ends as I (det = +1)
-    givens_cols<N>(col, state + N * N, j);
+        for (int i = 0; i < N; ++i) state[j * N + i] = (float)col[i];
+    // Givens elimination of R (planes in lex order); E ends as I (det = +1)
+    givens_cols<N>(col, state + N * N, cs_out, j);
 }
 
 // dL/dQ (tangent part) = Q skew(Gamma), skew(Gamma)[p][q] = K_pq / 2 = -skew(Gamma)[q][p],
@@ -699,36 +903,126 @@ __device__ __forceinline__ void expm_frechet_cols(double (&Lc)[N], const double*
     }
 }
 
-// g_biv from dL/dQ (Q slot of g_state) through Q = expm(A), A = -B(biv):
+// g_biv from dL/dQ (row-major in G, LDS) through Q = expm(A), A = -B(biv):
 // dL/dA = L(A^T, dL/dQ), the (1,2) block of expm([[A^T, dL/dQ], [0, A^T]]).
+// One wave; X and F are N x N LDS scratch. G is scaled in place.
+template <int N>
+__device__ __forceinline__ void frechet_to_biv(const float* __restrict__ biv, double* __restrict__ G,
+                                               double* __restrict__ X, double* __restrict__ F,
+                                               float* __restrict__ g_biv, int j) {
+    double gmax = 0.0;
+    for (int idx = j; idx < N * N; idx += 64) gmax = fmax(gmax, fabs(G[idx]));
+    gmax = wave_max_f64(gmax) * N;  // bounds every column sum of |G|
+    int gexp = 0;
+    if (gmax > 1.0) frexp(gmax, &gexp);
+    wave_lds_sync();
+    for (int idx = j; idx < N * N; idx += 64) {
+        const int r = idx / N, c = idx % N;
+        X[idx] = generator_entry(biv, N, c, r);  // A^T
+        G[idx] = ldexp(G[idx], -gexp);
+    }
+    wave_lds_sync();
+    double Lc[N];
+    expm_frechet_cols<N>(Lc, X, G, j);
+    if (j < N)
+#pragma unroll
+        for (int i = 0; i < N; ++i) F[i * N + j] = ldexp(Lc[i], gexp);
+    wave_lds_sync();
+    for (int k = j; k < n_planes(N); k += 64) {
+        const int p = plane_p(N, k), q = plane_q(N, k);
+        // dL/dB = -dL/dA; dL/db = 2 (dL/dB[p][q] - dL/dB[q][p])
+        g_biv[k] = (float)(-2.0 * (F[p * N + q] - F[q * N + p]));
+    }
+}
+
 template <int N>
 __global__ __launch_bounds__(64) void rotor_compile_bwd_cols_kernel(const float* __restrict__ biv,
                                                                      const float* __restrict__ g_state,
                                                                      float* __restrict__ g_biv) {
     __shared__ double X[N * N], G[N * N], F[N * N];
     const int j = threadIdx.x;
-    double gmax = 0.0;
-    for (int idx = j; idx < N * N; idx += 64) gmax = fmax(gmax, fabs((double)g_state[idx]));
-    gmax = wave_max_f64(gmax) * N;  // bounds every column sum of |G|
-    int gexp = 0;
-    if (gmax > 1.0) frexp(gmax, &gexp);
-    for (int idx = j; idx < N * N; idx += 64) {
-        const int r = idx / N, c = idx % N;
-        X[idx] = generator_entry(biv, N, c, r);  // A^T
-        G[idx] = ldexp((double)g_state[idx], -gexp);
-    }
-    __syncthreads();
-    double Lc[N];
-    expm_frechet_cols<N>(Lc, X, G, j);
-    if (j < N)
+    for (int idx = j; idx < N * N; idx += 64) G[idx] = (double)g_state[idx];
+    wave_lds_sync();
+    frechet_to_biv<N>(biv, G, X, F, g_biv, j);
+}
+
+// g_biv from the gradient of the reference-layout cs through
+// cs = Givens(R), R = expm(B) = Q^T. One wave: R's columns in lanes (fp64),
+// the factorisation replayed with each plane's input rows p and q recorded in
+// LDS, then reverse mode through it:
+//   rows P' = c P + s Qr, Q' = -s P + c Qr:  dc += <gP', P> + <gQ', Qr>,
+//   ds += <gP', Qr> - <gQ', P>,  gP = c gP' - s gQ',  gQ = s gP' + c gQ';
+//   (c, s) = (a, b) / r:  ga = (dc b^2 - ds a b) / r^3,  gb = (ds a^2 - dc a b) / r^3
+// with a = E[p][p], b = E[q][p]. dL/dQ = (dL/dR)^T, then the Frechet step.
+template <int N>
+__global__ __launch_bounds__(64) void rotor_cs_compile_bwd_kernel(const float* __restrict__ biv,
+                                                                   const float* __restrict__ g_cs,
+                                                                   float* __restrict__ g_biv) {
+    constexpr int C = n_planes(N);
+    __shared__ double Z[N * N], F[N * N];
+    __shared__ double rows[C][2][N];
+    const int j = threadIdx.x;
+    const bool act = j < N;
+    for (int idx = j; idx < N * N; idx += 64) Z[idx] = generator_entry(biv, N, idx % N, idx / N);  // B = A^T
+    wave_lds_sync();
+    double col[N];
+    expm_cols<N>(col, Z, j);
+    // forward replay (column j of E in lane j), recording the rows p, q entering each plane
 #pragma unroll
-        for (int i = 0; i < N; ++i) F[i * N + j] = ldexp(Lc[i], gexp);
-    __syncthreads();
-    for (int k = j; k < n_planes(N); k += 64) {
-        const int p = plane_p(N, k), q = plane_q(N, k);
-        // dL/dB = -dL/dA; dL/db = 2 (dL/dB[p][q] - dL/dB[q][p])
-        g_biv[k] = (float)(-2.0 * (F[p * N + q] - F[q * N + p]));
+    for (int p = 0; p < N - 1; ++p) {
+#pragma unroll
+        for (int q = p + 1; q < N; ++q) {
+            const int k = p * N - p * (p + 1) / 2 + (q - p - 1);
+            if (act) {
+                rows[k][0][j] = col[p];
+                rows[k][1][j] = col[q];
+            }
+            double c, s;
+            givens_cs(readlane_f64(col[p], p), readlane_f64(col[q], p), c, s);
+            const double ep = col[p], eq = col[q];
+            col[p] = c * ep + s * eq;
+            col[q] = -s * ep + c * eq;
+        }
     }
+    wave_lds_sync();
+    // reverse mode; gcol = column j of dL/dE (A_final is not an output: starts at 0)
+    double gcol[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) gcol[i] = 0.0;
+#pragma unroll
+    for (int p = N - 2; p >= 0; --p) {
+#pragma unroll
+        for (int q = N - 1; q > p; --q) {
+            const int k = p * N - p * (p + 1) / 2 + (q - p - 1);
+            const double P = act ? rows[k][0][j] : 0.0, Qr = act ? rows[k][1][j] : 0.0;
+            const double a = rows[k][0][p], b = rows[k][1][p];
+            double c, s;
+            givens_cs(a, b, c, s);
+            const double gp = gcol[p], gq = gcol[q];
+            double dc = gp * P + gq * Qr, ds = gp * Qr - gq * P;
+            for (int off = 1; off < 64; off <<= 1) {
+                dc += __shfl_xor(dc, off, 64);
+                ds += __shfl_xor(ds, off, 64);
+            }
+            dc += (double)g_cs[2 * (C - 1 - k)];
+            ds += (double)g_cs[2 * (C - 1 - k) + 1];
+            gcol[p] = c * gp - s * gq;
+            gcol[q] = s * gp + c * gq;
+            const double r2 = a * a + b * b;
+            if (r2 > 1e-300 && j == p) {
+                const double r = sqrt(r2);
+                const double ir3 = 1.0 / (r2 * r);
+                gcol[p] += (dc * b * b - ds * a * b) * ir3;
+                gcol[q] += (ds * a * a - dc * a * b) * ir3;
+            }
+        }
+    }
+    // dL/dQ[i][jj] = dL/dR[jj][i] = lane i's gcol[jj]
+    if (act)
+#pragma unroll
+        for (int jj = 0; jj < N; ++jj) F[j * N + jj] = gcol[jj];
+    wave_lds_sync();
+    frechet_to_biv<N>(biv, F, Z, (double*)&rows[0][0][0], g_biv, j);
 }
 
 // ---- entry per lane (N <= 8) ------------------------------------------------
@@ -781,7 +1075,8 @@ __device__ __forceinline__ double expm_entry(const double (&z)[N], int i, int j)
 // second wave builds the spin matrix U concurrently (spin_expm).
 template <int N>
 __global__ __launch_bounds__(128) void rotor_compile_fwd_ent_kernel(const float* __restrict__ biv,
-                                                                     float* __restrict__ state, SpinTable spin) {
+                                                                     float* __restrict__ state,
+                                                                     float* __restrict__ cs_out, SpinTable spin) {
     static_assert(N * N <= 64, "one entry per lane");
     if constexpr (N == kSpinN) {
         __shared__ double spin_lds[kSpinLdsDoubles];
@@ -798,12 +1093,12 @@ __global__ __launch_bounds__(128) void rotor_compile_fwd_ent_kernel(const float*
     for (int l = 0; l < N; ++l) z[l] = generator_entry(biv, N, i, l);
     const double e = expm_entry<N>(z, i, j);
     if (active) state[i * N + j] = (float)e;
-    // Givens elimination on columns: lane j < N gathers column j, so the row
-    // updates of a plane are register operations
+    // Givens elimination of R = Q^T on columns: lane j < N gathers column j of
+    // R (row j of Q), so the row updates of a plane are register operations
     double col[N];
 #pragma unroll
-    for (int r = 0; r < N; ++r) col[r] = shfl_f64(e, r * N + (lane < N ? lane : 0));
-    givens_cols<N>(col, state + N * N, lane);
+    for (int r = 0; r < N; ++r) col[r] = shfl_f64(e, (lane < N ? lane : 0) * N + r);
+    givens_cols<N>(col, state + N * N, cs_out, lane);
 }
 
 // Adjoint Frechet derivative by the block identity (see the column version):
@@ -872,6 +1167,7 @@ __global__ __launch_bounds__(64) void rotor_compile_bwd_ent_kernel(const float* 
 
 // ---- host side --------------------------------------------------------------
 
+// register-layout kernels: n = 2 .. 10
 #define CLF_ROTOR_DISPATCH(n, CALL)       \
     switch (n) {                          \
         case 2: CALL(2); break;           \
@@ -886,9 +1182,28 @@ __global__ __launch_bounds__(64) void rotor_compile_bwd_ent_kernel(const float* 
         default: break;                   \
     }
 
+// compile kernels: n = 2 .. 12
+#define CLF_COMPILE_DISPATCH(n, CALL)     \
+    switch (n) {                          \
+        case 2: CALL(2); break;           \
+        case 3: CALL(3); break;           \
+        case 4: CALL(4); break;           \
+        case 5: CALL(5); break;           \
+        case 6: CALL(6); break;           \
+        case 7: CALL(7); break;           \
+        case 8: CALL(8); break;           \
+        case 9: CALL(9); break;           \
+        case 10: CALL(10); break;         \
+        case 11: CALL(11); break;         \
+        case 12: CALL(12); break;         \
+        default: break;                   \
+    }
+
+constexpr int kRegChainMaxN = 10;  // larger rows run the LDS-staged chain
+
 // one entry per lane up to n = 8 (64 entries), one column per lane above
 template <int N>
-static int launch_compile_fwd(const float* biv, float* state, hipStream_t s) {
+static int launch_compile_fwd(const float* biv, float* state, float* cs, hipStream_t s) {
     if constexpr (N * N <= 64) {
         SpinTable spin{};
         if constexpr (N == kSpinN) {
@@ -896,9 +1211,9 @@ static int launch_compile_fwd(const float* biv, float* state, hipStream_t s) {
             if (!spin_tables(T, spin)) return set_error(CLF_ERR_UNSUPPORTED, "Cl(8,0) representation tables unavailable");
         }
         hipLaunchKernelGGL((rotor_compile_fwd_ent_kernel<N>), dim3(1), dim3(N == kSpinN ? 128 : 64), 0, s, biv, state,
-                           spin);
+                           cs, spin);
     } else {
-        hipLaunchKernelGGL((rotor_compile_fwd_cols_kernel<N>), dim3(1), dim3(64), 0, s, biv, state);
+        hipLaunchKernelGGL((rotor_compile_fwd_cols_kernel<N>), dim3(1), dim3(64), 0, s, biv, state, cs);
     }
     return CLF_OK;
 }
@@ -919,10 +1234,26 @@ static int check_rotor_n(int n) {
 
 int rotor_state_floats(int n) { return (n >= kRotorMinN && n <= kRotorMaxN) ? state_floats(n) : -1; }
 
+// Workgroups of a backward launch (and so partials in the workspace): the
+// register kernels take 256 >> (lanes per row) rows per workgroup, the
+// LDS-staged kernel kLdsBlades / 2^n rows.
 static int rotor_bwd_grid(int n, int64_t batch) {
-    const int lb = n - rotor_rb(n);
-    const long long rows_per_block = 256 >> lb;
+    long long rows_per_block;
+    if (n <= kRegChainMaxN) rows_per_block = 256 >> (n - rotor_rb(n));
+    else rows_per_block = kLdsBlades >> n > 0 ? kLdsBlades >> n : 1;
     long long g = (batch + rows_per_block - 1) / rows_per_block;
+    if (g > 1024) g = 1024;
+    if (g < 1) g = 1;
+    return (int)g;
+}
+
+static long long lds_groups(int n, int64_t batch) {
+    const long long rpb = kLdsBlades >> n > 0 ? kLdsBlades >> n : 1;
+    return (batch + rpb - 1) / rpb;
+}
+
+static int cs_bwd_grid(int n, int64_t batch) {
+    long long g = lds_groups(n, batch);
     if (g > 1024) g = 1024;
     if (g < 1) g = 1;
     return (int)g;
@@ -933,13 +1264,18 @@ size_t rotor_apply_ws_bytes(int n, int64_t batch) {
     return (size_t)rotor_bwd_grid(n, batch) * n_planes(n) * sizeof(float);
 }
 
-int rotor_compile_fwd(int n, const float* biv, float* state, void* stream) {
+size_t rotor_cs_apply_ws_bytes(int n, int64_t batch) {
+    if (n < kRotorMinN || n > kRotorMaxN || batch < 0) return 0;
+    return (size_t)cs_bwd_grid(n, batch) * 2 * n_planes(n) * sizeof(float);
+}
+
+int rotor_compile_fwd(int n, const float* biv, float* state, float* cs, void* stream) {
     if (int rc = check_rotor_n(n)) return rc;
     if (!biv || !state) return set_error(CLF_ERR_ARG, "null pointer argument");
     hipStream_t s = (hipStream_t)stream;
     int rc = CLF_OK;
-#define CLF_CALL(N) rc = launch_compile_fwd<N>(biv, state, s)
-    CLF_ROTOR_DISPATCH(n, CLF_CALL)
+#define CLF_CALL(N) rc = launch_compile_fwd<N>(biv, state, cs, s)
+    CLF_COMPILE_DISPATCH(n, CLF_CALL)
 #undef CLF_CALL
     if (rc) return rc;
     CLF_HIP_CHECK(hipGetLastError());
@@ -951,40 +1287,79 @@ int rotor_compile_bwd(int n, const float* biv, const float* g_state, float* g_bi
     if (!biv || !g_state || !g_biv) return set_error(CLF_ERR_ARG, "null pointer argument");
     hipStream_t s = (hipStream_t)stream;
 #define CLF_CALL(N) launch_compile_bwd<N>(biv, g_state, g_biv, s)
-    CLF_ROTOR_DISPATCH(n, CLF_CALL)
+    CLF_COMPILE_DISPATCH(n, CLF_CALL)
 #undef CLF_CALL
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }
 
+// LDS-staged chain launch: grid of at most `cap` workgroups and at most the
+// resident workgroups, never more than the row groups.
+template <int MODE>
+static unsigned lds_grid(int n, int64_t batch, long long cap) {
+    long long want = lds_groups(n, batch);
+    if (want > cap) want = cap;
+    return resident_grid((const void*)rotor_chain_lds_kernel<MODE>, 256, 0, want);
+}
+
+template <int MODE>
+static void launch_lds(int n, const float* cs, const float* a, const float* b, float* out, float* parts, int64_t batch,
+                       unsigned grid, hipStream_t s) {
+    hipLaunchKernelGGL((rotor_chain_lds_kernel<MODE>), dim3(grid), dim3(256), 0, s, n, cs, a, b, out, parts,
+                       (long long)batch);
+}
+
 template <int N>
-static void launch_apply(bool fwd, const float* state, const float* x, float* y, int64_t batch, hipStream_t s) {
+static void launch_apply_reg(bool fwd, const float* cs, const float* x, float* y, int64_t batch, hipStream_t s) {
     constexpr int LB = N - rotor_rb(N);
     const long long threads = (long long)batch << LB;
     const long long wanted = (threads + 255) / 256;
     if (fwd) {
         const dim3 grid(resident_grid((const void*)rotor_apply_kernel<N, true>, 256, 0, wanted));
-        hipLaunchKernelGGL((rotor_apply_kernel<N, true>), grid, dim3(256), 0, s, state, x, y, (long long)batch);
+        hipLaunchKernelGGL((rotor_apply_kernel<N, true>), grid, dim3(256), 0, s, cs, x, y, (long long)batch);
     } else {
         const dim3 grid(resident_grid((const void*)rotor_apply_kernel<N, false>, 256, 0, wanted));
-        hipLaunchKernelGGL((rotor_apply_kernel<N, false>), grid, dim3(256), 0, s, state, x, y, (long long)batch);
+        hipLaunchKernelGGL((rotor_apply_kernel<N, false>), grid, dim3(256), 0, s, cs, x, y, (long long)batch);
     }
 }
 
-// Backward grid: at most rotor_bwd_grid (the workspace bound), at most the
-// resident workgroups. The gamma finalize reads this many partials.
-template <int N>
-static unsigned bwd_launch_grid(int64_t batch) {
-    return resident_grid((const void*)rotor_apply_bwd_kernel<N>, 256, 0, rotor_bwd_grid(N, batch));
+// y = chain(cs) x (fwd) or chain(cs)^T x, any n in range, batch > 0
+static void launch_chain(int n, bool fwd, const float* cs, const float* x, float* y, int64_t batch, hipStream_t s) {
+    if (n <= kRegChainMaxN) {
+#define CLF_CALL(N) launch_apply_reg<N>(fwd, cs, x, y, batch, s)
+        CLF_ROTOR_DISPATCH(n, CLF_CALL)
+#undef CLF_CALL
+    } else if (fwd) {
+        launch_lds<LDS_FWD>(n, cs, x, nullptr, y, nullptr, batch, lds_grid<LDS_FWD>(n, batch, 1LL << 30), s);
+    } else {
+        launch_lds<LDS_TR>(n, cs, x, nullptr, y, nullptr, batch, lds_grid<LDS_TR>(n, batch, 1LL << 30), s);
+    }
 }
 
+// Composite backward with the K statistics: the register kernel (n <= 10) or
+// the LDS-staged kernel; returns the number of partials written.
 template <int N>
-static void launch_apply_bwd(const float* state, const float* x, const float* gy, float* gx, float* ws,
-                             int64_t batch, hipStream_t s) {
-    hipLaunchKernelGGL((rotor_apply_bwd_kernel<N>), dim3(bwd_launch_grid<N>(batch)), dim3(256), 0, s, state, x, gy,
-                       gx, ws, (long long)batch);
+static int launch_apply_bwd_reg(const float* cs, const float* x, const float* gy, float* gx, float* ws, int64_t batch,
+                                hipStream_t s) {
+    const unsigned grid = resident_grid((const void*)rotor_apply_bwd_kernel<N>, 256, 0, rotor_bwd_grid(N, batch));
+    hipLaunchKernelGGL((rotor_apply_bwd_kernel<N>), dim3(grid), dim3(256), 0, s, cs, x, gy, gx, ws, (long long)batch);
+    return (int)grid;
 }
 
+static int launch_gamma(int n, const float* cs, const float* x, const float* gy, float* gx, float* ws, int64_t batch,
+                        hipStream_t s) {
+    int nparts = 0;
+    if (n <= kRegChainMaxN) {
+#define CLF_CALL(N) nparts = launch_apply_bwd_reg<N>(cs, x, gy, gx, ws, batch, s)
+        CLF_ROTOR_DISPATCH(n, CLF_CALL)
+#undef CLF_CALL
+    } else {
+        const unsigned grid = lds_grid<LDS_GAMMA>(n, batch, rotor_bwd_grid(n, batch));
+        launch_lds<LDS_GAMMA>(n, cs, x, gy, gx, ws, batch, grid, s);
+        nparts = (int)grid;
+    }
+    return nparts;
+}
 
 bool rotor16_enabled(int n);
 int rotor16_apply(bool fwd, const float* U, const float* x, float* y, int64_t batch, void* stream);
@@ -1000,10 +1375,7 @@ int rotor_apply_fwd(int n, const float* state, const float* x, float* y, int64_t
     if (x == y) return set_error(CLF_ERR_ARG, "output must not alias the input");
     if ((((uintptr_t)x) | ((uintptr_t)y)) & 15u) return set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
     if (rotor16_enabled(n)) return rotor16_apply(true, state + spin_offset(n), x, y, batch, stream);
-    hipStream_t s = (hipStream_t)stream;
-#define CLF_CALL(N) launch_apply<N>(true, state, x, y, batch, s)
-    CLF_ROTOR_DISPATCH(n, CLF_CALL)
-#undef CLF_CALL
+    launch_chain(n, true, state + n * n, x, y, batch, (hipStream_t)stream);
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }
@@ -1013,7 +1385,7 @@ int rotor_apply_bwd(int n, const float* state, const float* x, const float* gy, 
     if (int rc = check_rotor_n(n)) return rc;
     if (batch < 0) return set_error(CLF_ERR_ARG, "batch must be >= 0");
     if (!gx && !g_state) return CLF_OK;
-    if (!state || !gy || (g_state && !x)) return set_error(CLF_ERR_ARG, "null pointer argument");
+    if (!state || (batch > 0 && (!gy || (g_state && !x)))) return set_error(CLF_ERR_ARG, "null pointer argument");
     if ((((uintptr_t)x) | ((uintptr_t)gy) | ((uintptr_t)gx)) & 15u)
         return set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
     if (gx && (gx == gy || gx == x)) return set_error(CLF_ERR_ARG, "gx must not alias x or gy");
@@ -1027,19 +1399,12 @@ int rotor_apply_bwd(int n, const float* state, const float* x, const float* gy, 
     if (batch > 0) {
         if (!g_state) {
             if (mat) return rotor16_apply(false, state + spin_offset(n), gy, gx, batch, stream);
-#define CLF_CALL(N) launch_apply<N>(false, state, gy, gx, batch, s)
-            CLF_ROTOR_DISPATCH(n, CLF_CALL)
-#undef CLF_CALL
+            launch_chain(n, false, state + n * n, gy, gx, batch, s);
         } else if (mat) {
             nparts = (int)rotor16_bwd_grid(rotor_bwd_grid(n, batch));
             if (int rc = rotor16_bwd(state + spin_offset(n), x, gy, gx, gws, batch, (unsigned)nparts, stream)) return rc;
         } else {
-#define CLF_CALL(N) launch_apply_bwd<N>(state, x, gy, gx, gws, batch, s)
-            CLF_ROTOR_DISPATCH(n, CLF_CALL)
-#undef CLF_CALL
-#define CLF_CALL(N) nparts = (int)bwd_launch_grid<N>(batch)
-            CLF_ROTOR_DISPATCH(n, CLF_CALL)
-#undef CLF_CALL
+            nparts = launch_gamma(n, state + n * n, x, gy, gx, gws, batch, s);
         }
         CLF_HIP_CHECK(hipGetLastError());
     }
@@ -1047,6 +1412,63 @@ int rotor_apply_bwd(int n, const float* state, const float* x, const float* gy, 
         hipLaunchKernelGGL(rotor_gamma_finalize_kernel, dim3(1), dim3(1024), 0, s, n, state, gws, nparts, g_state);
         CLF_HIP_CHECK(hipGetLastError());
     }
+    return CLF_OK;
+}
+
+// ---- the chain on a caller's cs (apply_rotor(cs, x)) ----------------------
+
+int rotor_cs_apply_fwd(int n, const float* cs, const float* x, float* y, int64_t batch, void* stream) {
+    if (int rc = check_rotor_n(n)) return rc;
+    if (batch < 0) return set_error(CLF_ERR_ARG, "batch must be >= 0");
+    if (batch == 0) return CLF_OK;
+    if (!cs || !x || !y) return set_error(CLF_ERR_ARG, "null pointer argument");
+    if (x == y) return set_error(CLF_ERR_ARG, "output must not alias the input");
+    if ((((uintptr_t)x) | ((uintptr_t)y)) & 15u) return set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
+    launch_chain(n, true, cs, x, y, batch, (hipStream_t)stream);
+    CLF_HIP_CHECK(hipGetLastError());
+    return CLF_OK;
+}
+
+int rotor_cs_apply_bwd(int n, const float* cs, const float* y, const float* gy, float* gx, float* g_cs,
+                       int64_t batch, void* ws, size_t ws_bytes, void* stream) {
+    if (int rc = check_rotor_n(n)) return rc;
+    if (batch < 0) return set_error(CLF_ERR_ARG, "batch must be >= 0");
+    if (!gx && !g_cs) return CLF_OK;
+    if (!cs || (batch > 0 && (!gy || (g_cs && !y)))) return set_error(CLF_ERR_ARG, "null pointer argument");
+    if ((((uintptr_t)y) | ((uintptr_t)gy) | ((uintptr_t)gx)) & 15u)
+        return set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
+    if (gx && (gx == gy || gx == y)) return set_error(CLF_ERR_ARG, "gx must not alias y or gy");
+    const size_t need = rotor_cs_apply_ws_bytes(n, batch);
+    if (g_cs && (!ws || ws_bytes < need))
+        return set_error(CLF_ERR_WORKSPACE, "workspace of at least " + std::to_string(need) + " bytes required");
+    hipStream_t s = (hipStream_t)stream;
+    float* parts = g_cs ? (float*)ws : nullptr;
+    int nparts = 0;
+    if (batch > 0) {
+        if (!g_cs) {
+            launch_chain(n, false, cs, gy, gx, batch, s);
+        } else {
+            const unsigned grid = lds_grid<LDS_CS_BWD>(n, batch, cs_bwd_grid(n, batch));
+            launch_lds<LDS_CS_BWD>(n, cs, y, gy, gx, parts, batch, grid, s);
+            nparts = (int)grid;
+        }
+        CLF_HIP_CHECK(hipGetLastError());
+    }
+    if (g_cs) {
+        hipLaunchKernelGGL(parts_sum_kernel, dim3(1), dim3(256), 0, s, parts, nparts, 2 * n_planes(n), g_cs);
+        CLF_HIP_CHECK(hipGetLastError());
+    }
+    return CLF_OK;
+}
+
+int rotor_cs_compile_bwd(int n, const float* biv, const float* g_cs, float* g_biv, void* stream) {
+    if (int rc = check_rotor_n(n)) return rc;
+    if (!biv || !g_cs || !g_biv) return set_error(CLF_ERR_ARG, "null pointer argument");
+    hipStream_t s = (hipStream_t)stream;
+#define CLF_CALL(N) hipLaunchKernelGGL((rotor_cs_compile_bwd_kernel<N>), dim3(1), dim3(64), 0, s, biv, g_cs, g_biv)
+    CLF_COMPILE_DISPATCH(n, CLF_CALL)
+#undef CLF_CALL
+    CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }
 

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define CLF_ABI_VERSION 1
+#define CLF_ABI_VERSION 2
 
 /* status codes */
 #define CLF_OK               0
@@ -121,46 +121,75 @@ int clf_norm_sq_bwd(int n, uint32_t neg_mask, uint32_t null_mask,
                     int64_t batch, void* stream);
 
 
-/* ---- rotor: bivector -> rotor state -> sandwich ~R x R --------------------
- * Replaces the reference chain eigh_exp_fwd/bwd (kernels/rotor/eigh_exp.cu:270-361),
- * givens_factor_fwd_v2/bwd_v2 (kernels/rotor/givens_factor.cu:176-231) and
- * givens_mb_perm_packed_fwd/bwd (kernels/rotor/givens_apply_mb_perm_packed.cu:250-292),
- * as wired by src/cliffordcuda/algebra.py:343-373. Euclidean semantics, like the
- * reference: y = ~R x R, R = exp(sum_m b_m e_{i_m} e_{j_m}), bivector slots in
- * triu_indices(n, n, 1) order. Supported n: 2..10.
+/* ---- rotor: bivector -> rotation -> Givens cs chain -> sandwich ~R x R ----
+ * Euclidean semantics, like the reference: y = ~R x R, R = exp(sum_m b_m e_{i_m} e_{j_m}),
+ * bivector slots in triu_indices(n, n, 1) order. Supported n: 2..12.
  *
- * Rotor state layout (clf_rotor_state_floats(n) floats): the n x n rotation
- * Q = expm(-2 (M - M^T)) acting on grade-1 coefficients (row-major), followed by
- * the C(n,2) (c, s) pairs of its plane-rotation factorisation and, for n = 8,
- * the 16 x 16 matrix U = phi(R) of the rotor in the real representation of
- * Cl(8,0) (row-major), which the n = 8 sandwich kernels use (phi(y) = U^T phi(x) U). */
+ * cs is the reference's (C(n,2), 2) tensor (src/cliffordcuda/algebra.py:343-369):
+ * the Givens factors of R = expm(2 (M - M^T)) (kernels/rotor/givens_factor.cu:23-38),
+ * planes (p, q) in lex order, plane k's (c, s) at row C(n,2) - 1 - k. The chain
+ * applies the planes lex-first, mapping each blade pair (I with p not q,
+ * J = I ^ {p,q}) as y_I = c x_I + s sig x_J, y_J = c x_J - s sig x_I
+ * (kernels/rotor/givens_apply_mb_perm_packed.cu:33-64).
+ *
+ * Rotor state (clf_rotor_state_floats(n) floats, the library's own cache of a
+ * compiled bivector): the n x n rotation Q = expm(-2 (M - M^T)) acting on grade-1
+ * coefficients (row-major), the cs pairs and, for n = 8, the 16 x 16 matrix
+ * U = phi(R) of the rotor in the real representation of Cl(8,0) (row-major),
+ * which the n = 8 state kernels use (phi(y) = U^T phi(x) U). */
 
 /* Number of floats of the rotor state for n, or -1 if n is unsupported. */
 int clf_rotor_state_floats(int n);
 
-/* state = compile(biv); biv: C(n,2) floats. One single-workgroup launch, no host sync. */
-int clf_rotor_compile_fwd(int n, const float* biv, float* state, void* stream);
+/* state = compile(biv) and, if cs != NULL, cs (2 C(n,2) floats) = the reference's
+ * compile_bivector output. biv: C(n,2) floats. One single-workgroup launch, no
+ * host sync. Replaces eigh_exp_fwd (kernels/rotor/eigh_exp.cu:270-322) and
+ * givens_factor_fwd_v2 (kernels/rotor/givens_factor.cu:176-199). */
+int clf_rotor_compile_fwd(int n, const float* biv, float* state, float* cs, void* stream);
 
 /* g_biv = d/d(biv) of <g_state, compile(biv)>, reading only the Q block of
- * g_state (the chain and spin blocks are derived caches and carry no gradient). */
+ * g_state (the cs and spin blocks are derived caches and carry no gradient).
+ * The backward of the state path (apply_bivector, RotorLayer). */
 int clf_rotor_compile_bwd(int n, const float* biv, const float* g_state, float* g_biv, void* stream);
 
-/* y = ~R x R for `batch` rows. y must not alias x. */
+/* y = ~R x R from a compiled state, for `batch` rows. y must not alias x. */
 int clf_rotor_apply_fwd(int n, const float* state, const float* x, float* y,
                         int64_t batch, void* stream);
 
 /* Bytes of device workspace clf_rotor_apply_bwd needs when g_state != NULL. */
 size_t clf_rotor_apply_ws_bytes(int n, int64_t batch);
 
-/* Backward of the sandwich: gx = R gy ~R (the transpose of the action),
- * g_state = dL/d(state): the Q block holds the component of dL/dQ tangent to
- * SO(n) (Q skew(Gamma), which is all clf_rotor_compile_bwd needs), the chain
- * and spin blocks are 0. gx or g_state may be
- * NULL. x is read only when g_state != NULL. The reference returns no gradient
- * to x (extensions/rotor/givens_apply/mb_perm_packed.py:34-42). */
+/* Backward of the state sandwich: gx = R gy ~R (the transpose of the action),
+ * g_state: the Q block holds the component of dL/dQ tangent to SO(n)
+ * (Q skew(Gamma), which is all clf_rotor_compile_bwd needs), the cs and spin
+ * blocks are 0. gx or g_state may be NULL. x is read only when g_state != NULL. */
 int clf_rotor_apply_bwd(int n, const float* state, const float* x, const float* gy,
                         float* gx, float* g_state, int64_t batch,
                         void* ws, size_t ws_bytes, void* stream);
+
+/* y = chain(cs) x for a caller's cs (any pairs, unit or not), `batch` rows.
+ * Replaces givens_mb_perm_packed_fwd (kernels/rotor/givens_apply_mb_perm_packed.cu:250-267). */
+int clf_rotor_cs_apply_fwd(int n, const float* cs, const float* x, float* y,
+                           int64_t batch, void* stream);
+
+/* Bytes of device workspace clf_rotor_cs_apply_bwd needs when g_cs != NULL. */
+size_t clf_rotor_cs_apply_ws_bytes(int n, int64_t batch);
+
+/* Backward of the cs chain from its output y: g_cs (2 C(n,2) floats, summed over
+ * the batch) by the reference's rule (each plane's input rebuilt with the
+ * transposed pair map: the exact gradient for unit pairs), and gx = the
+ * transposed chain of gy (the exact gradient for any pairs; the reference
+ * returns none). gx or g_cs may be NULL; y is read only when g_cs != NULL.
+ * Replaces givens_mb_perm_packed_bwd (kernels/rotor/givens_apply_mb_perm_packed.cu:270-285). */
+int clf_rotor_cs_apply_bwd(int n, const float* cs, const float* y, const float* gy,
+                           float* gx, float* g_cs, int64_t batch,
+                           void* ws, size_t ws_bytes, void* stream);
+
+/* g_biv = d/d(biv) of <g_cs, cs(biv)> through the Givens factorisation and
+ * expm (fp64, one single-workgroup launch). Replaces givens_factor_bwd_v2
+ * (kernels/rotor/givens_factor.cu:202-231) and eigh_exp_bwd
+ * (kernels/rotor/eigh_exp.cu:325-361). */
+int clf_rotor_cs_compile_bwd(int n, const float* biv, const float* g_cs, float* g_biv, void* stream);
 
 /* ---- broadcast-weight products (the product layers) ---------------------
  * y = op(x, w) (side 0, x on the left, as the reference layers compute it,

@@ -337,7 +337,7 @@ def givens_factor(R: torch.Tensor) -> torch.Tensor:
     for k, (p, q) in enumerate(pairs):
         a, b = A[p, p], A[q, p]
         r = torch.sqrt(a * a + b * b)
-        if float(r) > 0.0:
+        if float(r.detach()) > 0.0:
             c, s_raw = a / r, -b / r
         else:
             c, s_raw = torch.ones_like(a), torch.zeros_like(a)

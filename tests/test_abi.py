@@ -32,7 +32,7 @@ def test_all_declared_symbols_exported():
 
 def test_abi_version_and_limits():
     lib = _lib.load()
-    assert lib.clf_abi_version() == 1
+    assert lib.clf_abi_version() == 2
     assert lib.clf_product_max_n() >= 10
 
 
@@ -40,10 +40,12 @@ def test_rotor_state_length_matches_python():
     """The traced-graph state length (computed in Python) equals the library's."""
     from cliffordcuda_amd.rotor import _state_len
     lib = _lib.load()
-    for n in range(2, 11):
+    for n in range(2, 13):
         assert lib.clf_rotor_state_floats(n) == _state_len(n), n
     assert lib.clf_rotor_state_floats(8) == 64 + 56 + 256
-    assert lib.clf_rotor_state_floats(11) == -1
+    assert lib.clf_rotor_state_floats(13) == -1
+    assert lib.clf_rotor_cs_apply_ws_bytes(13, 4) == 0
+    assert lib.clf_rotor_cs_apply_ws_bytes(12, 4) > 0
 
 
 @pytest.mark.parametrize("args,code,msg", [
@@ -90,3 +92,21 @@ def test_status_mapping():
     with pytest.raises(RuntimeError):
         _lib.check(_lib.CLF_ERR_HIP, "x")
     _lib.check(_lib.CLF_OK, "x")
+
+
+def test_rotor_cs_argument_errors():
+    """The cs entry points check n, pointers, aliasing and the workspace before
+    any HIP call."""
+    lib = _lib.load()
+    assert lib.clf_rotor_cs_apply_fwd(13, 16, 16, 32, 4, None) == 1
+    assert "n in [2, 12]" in _lib.last_error()
+    assert lib.clf_rotor_cs_apply_fwd(8, None, 16, 32, 4, None) == 1
+    assert lib.clf_rotor_cs_apply_fwd(8, 16, 32, 32, 4, None) == 1
+    assert "alias" in _lib.last_error()
+    assert lib.clf_rotor_cs_apply_fwd(8, 16, 32, 48, 0, None) == 0           # empty batch
+    assert lib.clf_rotor_cs_apply_bwd(8, 16, 32, 48, None, None, 4, None, 0, None) == 0  # nothing requested
+    assert lib.clf_rotor_cs_apply_bwd(8, 16, 32, 48, 64, 80, 4, None, 0, None) == 4      # no workspace
+    assert "workspace" in _lib.last_error()
+    assert lib.clf_rotor_cs_apply_bwd(8, 16, 32, 48, 48, None, 4, None, 0, None) == 1    # gx aliases gy
+    assert lib.clf_rotor_cs_compile_bwd(8, 16, None, 32, None) == 1
+    assert lib.clf_rotor_compile_fwd(1, 16, 32, None, None) == 1

@@ -66,7 +66,31 @@ def test_compile_layers_fullgraph():
         assert rel_err(v, u) <= TOL
 
 
-@pytest.mark.parametrize("case", ["product", "graded", "norm_sq", "bcast_product", "rotor"])
+def test_compile_rotor_cs_fullgraph():
+    """The reference's explicit composition apply_rotor(compile_bivector(b), x)
+    traces as one graph (the cs operators) and gives the eager values and
+    gradients to the bivector and x."""
+    cl = cc.CliffordAlgebra([1] * 8, device="cuda")
+    g = torch.Generator().manual_seed(5)
+    b0 = (0.3 * torch.randn(1, 28, generator=g)).cuda()
+    x0 = torch.randn(33, 256, generator=g).cuda()
+    gy = torch.randn(33, 256, generator=g).cuda()   # (a rotation-invariant loss would have no bivector gradient)
+
+    def f(b, x):
+        return cl.apply_rotor(cl.compile_bivector(b), x)
+
+    res = []
+    for fn in (f, torch.compile(f, fullgraph=True)):
+        b = b0.clone().requires_grad_()
+        x = x0.clone().requires_grad_()
+        y = fn(b, x)
+        y.backward(gy)
+        res.append([y.detach(), b.grad, x.grad])
+    for u, v in zip(*res):
+        assert rel_err(v, u) <= TOL
+
+
+@pytest.mark.parametrize("case", ["product", "graded", "norm_sq", "bcast_product", "rotor", "rotor_cs"])
 def test_opcheck(case):
     ops = torch.ops.cliffordcuda_amd
     g = torch.Generator().manual_seed(2)
@@ -81,8 +105,13 @@ def test_opcheck(case):
         torch.library.opcheck(ops.norm_sq.default, (x, 8, 0, 0))
     elif case == "bcast_product":
         torch.library.opcheck(ops.bcast_product.default, (x, w, 2, 0, 8, 0, 0))
-    else:
+    elif case == "rotor":
         biv = (0.3 * torch.randn(28, generator=g)).cuda().requires_grad_()
         torch.library.opcheck(ops.rotor_compile.default, (biv, 8))
         state = ops.rotor_compile(biv.detach(), 8)
         torch.library.opcheck(ops.rotor_apply.default, (state.requires_grad_(), x, 8))
+    else:
+        biv = (0.3 * torch.randn(28, generator=g)).cuda().requires_grad_()
+        torch.library.opcheck(ops.rotor_compile_cs.default, (biv, 8))
+        cs = ops.rotor_compile_cs(biv.detach(), 8)
+        torch.library.opcheck(ops.rotor_cs_apply.default, (cs.requires_grad_(), x, 8))

@@ -26,11 +26,24 @@ def oracle_step(biv, x, gy, n):
     return y64, b64.grad, x64.grad
 
 
-@pytest.mark.parametrize("n,metric", [(7, (1,) * 7), (8, (1,) * 7 + (-1,)), (9, (1,) * 9), (10, (1,) * 9 + (0,))])
+def oracle_cs_step(biv, x, gy, n):
+    """The reference's compile_bivector + apply_rotor restated (Givens factors
+    of expm(B), plane chain), fp64, autograd to the bivector and x; pinned to
+    the sandwich oracle in tests/test_oracle.py. Cheap at n = 11, 12, where the
+    einsum sandwich's autograd graph would not fit."""
+    b64 = biv.double().requires_grad_()
+    x64 = x.double().requires_grad_()
+    y64 = O.givens_chain_apply(O.compile_bivector_cs(b64, n), x64, n)
+    y64.backward(gy.double())
+    return y64, b64.grad, x64.grad
+
+
+@pytest.mark.parametrize("n,metric", [(7, (1,) * 7), (8, (1,) * 7 + (-1,)), (9, (1,) * 9), (10, (1,) * 9 + (0,)),
+                                      (11, (1,) * 11), (12, (1,) * 10 + (-1, -1))])
 def test_apply_bivector_parity(n, metric):
     cl = cc.CliffordAlgebra(metric, device="cuda")
     g = torch.Generator().manual_seed(n)
-    B = 24 if n < 10 else 6
+    B = 24 if n < 10 else (6 if n == 10 else 5)
     biv = (0.1 ** 0.5) * torch.randn(1, n * (n - 1) // 2, generator=g)
     x = torch.randn(B, 1 << n, generator=g)
     gy = torch.randn(B, 1 << n, generator=g)
@@ -39,10 +52,121 @@ def test_apply_bivector_parity(n, metric):
     print(f"[case] rotor n={n} B={B}", flush=True)
     y = cl.apply_bivector(bd, xd)
     y.backward(gy.cuda())
-    y64, gb64, gx64 = oracle_step(biv, x, gy, n)
+    y64, gb64, gx64 = oracle_step(biv, x, gy, n) if n <= 10 else oracle_cs_step(biv, x, gy, n)
     assert rel_err(y, y64) <= TOL
     assert rel_err(xd.grad, gx64) <= TOL
     assert rel_err(bd.grad, gb64) <= TOL
+
+
+@pytest.mark.parametrize("n", [7, 8, 9, 10, 11, 12])
+def test_compile_bivector_returns_reference_cs(n):
+    """compile_bivector returns the reference's (C(n,2), 2) Givens factors of
+    expm(B) (planes in lex order, stored reversed, r >= 0), against the
+    oracle's restatement of givens_factor.cu at 1e-5; a small and a large
+    bivector (planes with c < 0)."""
+    cl = cc.CliffordAlgebra([1] * n, device="cuda")
+    C = n * (n - 1) // 2
+    for scale in (0.1 ** 0.5, 2.0):
+        biv = scale * torch.randn(1, C, generator=torch.Generator().manual_seed(40 + n))
+        print(f"[case] compile cs n={n} scale={scale}", flush=True)
+        cs = cl.compile_bivector(biv.cuda())
+        assert cs.shape == (C, 2) and cs.dtype == torch.float32
+        ref = O.compile_bivector_cs(biv.double(), n)
+        assert rel_err(cs, ref) <= TOL, scale
+
+
+def _unit_cs(C, seed):
+    g = torch.Generator().manual_seed(seed)
+    ang = 2.0 * torch.randn(C, generator=g)
+    return torch.stack([ang.cos(), ang.sin()], 1)
+
+
+@pytest.mark.parametrize("n", [7, 8, 10, 12])
+def test_apply_rotor_on_hand_built_cs(n):
+    """apply_rotor on a cs the caller built (unit pairs of random angles, a
+    leaf that requires grad): values against the oracle chain, and the
+    gradients to cs and to x against autograd through the oracle chain (for
+    unit pairs the reference's backward rule is that derivative)."""
+    cl = cc.CliffordAlgebra([1] * n, device="cuda")
+    C = n * (n - 1) // 2
+    cs = _unit_cs(C, n)
+    g = torch.Generator().manual_seed(100 + n)
+    B = 33 if n < 12 else 5
+    x = torch.randn(B, 1 << n, generator=g)
+    gy = torch.randn(B, 1 << n, generator=g)
+    csd = cs.cuda().requires_grad_()
+    xd = x.cuda().requires_grad_()
+    print(f"[case] apply_rotor hand-built cs n={n} B={B}", flush=True)
+    y = cl.apply_rotor(csd, xd)
+    y.backward(gy.cuda())
+    cs64 = cs.double().requires_grad_()
+    x64 = x.double().requires_grad_()
+    y64 = O.givens_chain_apply(cs64, x64, n)
+    y64.backward(gy.double())
+    assert rel_err(y, y64) <= TOL
+    assert rel_err(xd.grad, x64.grad) <= TOL
+    assert rel_err(csd.grad, cs64.grad) <= TOL
+
+
+@pytest.mark.parametrize("n", [7, 9])
+def test_apply_rotor_non_unit_cs_follows_reference_backward(n):
+    """For pairs off the unit circle the reference rebuilds each plane's input
+    with the transposed map; cs.grad follows that rule (the oracle's
+    restatement of the reference backward), the values and x.grad are exact."""
+    cl = cc.CliffordAlgebra([1] * n, device="cuda")
+    C = n * (n - 1) // 2
+    g = torch.Generator().manual_seed(7 * n)
+    cs = _unit_cs(C, n) * (0.8 + 0.4 * torch.rand(C, 1, generator=g))
+    x = torch.randn(17, 1 << n, generator=g)
+    gy = torch.randn(17, 1 << n, generator=g)
+    csd = cs.cuda().requires_grad_()
+    xd = x.cuda().requires_grad_()
+    y = cl.apply_rotor(csd, xd)
+    y.backward(gy.cuda())
+    x64 = x.double().requires_grad_()
+    y64 = O.givens_chain_apply(cs.double(), x64, n)
+    y64.backward(gy.double())
+    gcs_ref, _ = O.givens_chain_backward_ref(cs.double(), y64.detach(), gy.double(), n)
+    assert rel_err(y, y64) <= TOL
+    assert rel_err(xd.grad, x64.grad) <= TOL
+    assert rel_err(csd.grad, gcs_ref) <= TOL
+
+
+@pytest.mark.parametrize("n", [8, 9, 11])
+def test_compile_then_apply_gradients_on_every_path(n):
+    """The reference's explicit composition apply_rotor(compile_bivector(b), x):
+    the bivector gradient is the oracle's whichever way it flows: straight
+    through the compiled state (cs untouched), through cs and the Givens
+    factorisation's backward (cs.retain_grad(), which also exposes cs.grad),
+    and a detached copy of cs as a leaf of its own."""
+    cl = cc.CliffordAlgebra([1] * n, device="cuda")
+    C = n * (n - 1) // 2
+    g = torch.Generator().manual_seed(60 + n)
+    biv = 0.5 * torch.randn(1, C, generator=g)
+    x = torch.randn(9, 1 << n, generator=g)
+    gy = torch.randn(9, 1 << n, generator=g)
+    y64, gb64, gx64 = oracle_cs_step(biv, x, gy, n)
+    b64 = biv.double().requires_grad_()
+    cs64 = O.compile_bivector_cs(b64, n)
+    cs64.retain_grad()
+    O.givens_chain_apply(cs64, x.double(), n).backward(gy.double())
+    for mode in ("state", "retain", "detached"):
+        print(f"[case] compile->apply n={n} mode={mode}", flush=True)
+        bd = biv.cuda().requires_grad_()
+        xd = x.cuda().requires_grad_()
+        cs = cl.compile_bivector(bd)
+        if mode == "retain":
+            cs.retain_grad()
+        if mode == "detached":
+            cs = cs.detach().requires_grad_()
+        y = cl.apply_rotor(cs, xd)
+        y.backward(gy.cuda())
+        assert rel_err(y, y64) <= TOL, mode
+        assert rel_err(xd.grad, gx64) <= TOL, mode
+        if mode != "detached":
+            assert rel_err(bd.grad, gb64) <= TOL, mode
+        if mode != "state":
+            assert rel_err(cs.grad, cs64.grad) <= TOL, mode
 
 
 def test_rotor_layer_c4_shape():
@@ -124,8 +248,11 @@ def test_rotor_errors():
     cl8 = cc.CliffordAlgebra([1] * 8, device="cuda")
     with pytest.raises(ValueError, match="first dim must be 1"):
         cl8.compile_bivector(torch.zeros(2, 28, device="cuda"))
-    with pytest.raises(ValueError, match="rotor state"):
+    with pytest.raises(ValueError, match=r"cs must have shape \(28, 2\)"):
         cl8.apply_rotor(torch.zeros(5, device="cuda"), torch.zeros(2, 256, device="cuda"))
+    cl13 = cc.CliffordAlgebra([1] * 13, device="cuda")
+    with pytest.raises(ValueError, match="n <= 12"):
+        cl13.compile_bivector(torch.zeros(1, 78, device="cuda"))
 
 
 def _rotor_step(cl, biv, x, gy, need_biv=True, need_x=True):
@@ -174,7 +301,7 @@ def test_rotor8_state_spin_block():
     cl = cc.CliffordAlgebra([1] * 8, device="cuda")
     for scale in (0.05, 1.0, 3.0):
         biv = scale * torch.randn(1, 28, generator=torch.Generator().manual_seed(11))
-        state = cl.compile_bivector(biv.cuda())
+        state = cc.rotor._compile_fwd(biv.cuda().reshape(-1), 8)
         assert state.numel() == 8 * 8 + 56 + 256
         U = state[120:].double().view(16, 16).cpu()
         torch.testing.assert_close(U @ U.T, torch.eye(16, dtype=torch.float64), atol=2e-6, rtol=0)
