@@ -63,6 +63,9 @@ SIGNATURES = {
     "clf_rotor_cs_apply_ws_bytes": (_sz, [_i32, _i64]),
     "clf_rotor_cs_apply_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
     "clf_rotor_cs_compile_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp]),
+    "clf_inverse_rep_supported": (_i32, [_i32, _u32, _u32]),
+    "clf_inverse_rep": (_i32, [_i32, _u32, _u32, _vp, _vp, _vp, _i64, _vp]),
+    "clf_inverse_versor": (_i32, [_i32, _vp, _vp, _vp, _vp, ctypes.c_float, _i64, _vp]),
     "clf_product_bcast_ws_bytes": (_sz, [_i32, _i64]),
     "clf_product_bcast_fwd": (_i32, [_i32, _i32, _i32, _u32, _u32, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
     "clf_product_bcast_bwd": (_i32, [_i32, _i32, _i32, _u32, _u32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),

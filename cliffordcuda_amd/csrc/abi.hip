@@ -88,6 +88,11 @@ int bcast_fwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* 
               int64_t batch, void* ws, size_t ws_bytes, void* stream);
 int bcast_bwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w, const float* gy,
               float* gx, float* gw, int64_t batch, void* ws, size_t ws_bytes, void* stream);
+int inverse_rep_supported(int n, uint32_t neg, uint32_t nul);
+int inverse_rep(int n, uint32_t neg, uint32_t nul, const float* x, float* y, int* singular, int64_t batch,
+                void* stream);
+int inverse_versor(int n, const float* x, const float* xr, float* y, int* flags, float rtol, int64_t batch,
+                   void* stream);
 size_t bcast_scratch_bytes();
 int bcast_bwd_noalloc(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w,
                       const float* gy, float* gx, float* gw, int64_t batch, void* stream);
@@ -190,6 +195,22 @@ int clf_rotor_cs_apply_bwd(int n, const float* cs, const float* y, const float* 
 int clf_rotor_cs_compile_bwd(int n, const float* biv, const float* g_cs, float* g_biv, void* stream) {
     clf::clear_error();
     return clf::rotor_cs_compile_bwd(n, biv, g_cs, g_biv, stream);
+}
+
+int clf_inverse_rep_supported(int n, uint32_t neg_mask, uint32_t null_mask) {
+    return clf::inverse_rep_supported(n, neg_mask, null_mask);
+}
+
+int clf_inverse_rep(int n, uint32_t neg_mask, uint32_t null_mask, const float* x, float* y, int* singular,
+                    int64_t batch, void* stream) {
+    clf::clear_error();
+    return clf::inverse_rep(n, neg_mask, null_mask, x, y, singular, batch, stream);
+}
+
+int clf_inverse_versor(int n, const float* x, const float* xr, float* y, int* flags, float rtol, int64_t batch,
+                       void* stream) {
+    clf::clear_error();
+    return clf::inverse_versor(n, x, xr, y, flags, rtol, batch, stream);
 }
 
 size_t clf_product_bcast_ws_bytes(int n, int64_t batch) { return clf::bcast_ws_bytes(n, batch); }

@@ -191,6 +191,30 @@ int clf_rotor_cs_apply_bwd(int n, const float* cs, const float* y, const float* 
  * (kernels/rotor/eigh_exp.cu:325-361). */
 int clf_rotor_cs_compile_bwd(int n, const float* biv, const float* g_cs, float* g_biv, void* stream);
 
+/* ---- multivector inverse ---------------------------------------------------
+ * The native parts of the reference's inverse (src/cliffordcuda/extensions/ga/
+ * inverse.py:139-194, inverse_rep.py:126-255). */
+
+/* 1 if clf_inverse_rep serves this signature: the non-null generators (n' of
+ * them) have a complex matrix representation of side 2^floor(n'/2) <= 128
+ * (<= 64 when two copies are needed, odd n' with pseudoscalar^2 = +1). */
+int clf_inverse_rep_supported(int n, uint32_t neg_mask, uint32_t null_mask);
+
+/* y = inverse of the non-null part of each row of x (blades with a null
+ * generator are 0 in y), through the matrix representation, one workgroup per
+ * row; singular[r] = 1 if row r's matrix had a zero pivot (singular may be
+ * NULL). For a metric without null generators y is x^-1. Replaces
+ * rep_inverse / the first step of degenerate_rep_inverse (inverse_rep.py:182-255). */
+int clf_inverse_rep(int n, uint32_t neg_mask, uint32_t null_mask, const float* x, float* y,
+                    int* singular, int64_t batch, void* stream);
+
+/* Versor inverse from xr = x rev(x): y = rev(x) / xr_0 per row, and
+ * flags[r] bit 0 = xr is not a scalar (max |xr_k|, k > 0, above
+ * rtol * max |xr|), bit 1 = |xr_0| < 1e-20. Replaces _versor_inverse
+ * (inverse.py:70-78). */
+int clf_inverse_versor(int n, const float* x, const float* xr, float* y, int* flags,
+                       float rtol, int64_t batch, void* stream);
+
 /* ---- broadcast-weight products (the product layers) ---------------------
  * y = op(x, w) (side 0, x on the left, as the reference layers compute it,
  * src/cliffordcuda/layers.py:43-47) or y = op(w, x) (side 1), with one weight

@@ -425,3 +425,24 @@ def givens_chain_backward_ref(cs: torch.Tensor, y: torch.Tensor, gy: torch.Tenso
         v[..., ii], v[..., jj] = vi_pre, vj_pre
         g[..., ii], g[..., jj] = c * gi - s * sg * gj, s * sg * gi + c * gj
     return gcs, g
+
+
+# ── multivector inverse (extensions/ga/inverse.py) ──────────────────────────
+
+def inverse_dense(x: torch.Tensor, metric=None) -> torch.Tensor:
+    """x^-1 for rows x (B, 2^n) by the dense solve L(x) y = e_0 with
+    L[k, j] = sigma(j ^ k, j) x[j ^ k] (the left-multiplication matrix; the
+    ground truth of the reference's tests/correctness/test_inverse.py:35-47).
+    Differentiable (torch.linalg.solve). Pinned by: x y = y x = 1 with the
+    oracle's geometric product."""
+    n = x.shape[-1].bit_length() - 1
+    metric = normalize_metric(n, metric)
+    dim = 1 << n
+    sig = sign_value_table(n, metric).to(x.dtype)
+    k = torch.arange(dim).view(dim, 1)
+    j = torch.arange(dim).view(1, dim)
+    S = sig[j ^ k, j.expand(dim, dim)]
+    L = S * x[:, j ^ k]
+    e0 = torch.zeros(x.shape[0], dim, 1, dtype=x.dtype)
+    e0[:, 0, 0] = 1.0
+    return torch.linalg.solve(L, e0).squeeze(-1)

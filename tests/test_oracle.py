@@ -436,3 +436,15 @@ def test_givens_chain_backward_ref_is_autograd_for_unit_pairs():
             torch.testing.assert_close(gcs, cs_l.grad, rtol=0, atol=1e-11)
         else:
             assert float((gcs - cs_l.grad).abs().max()) > 1e-3
+
+
+@pytest.mark.parametrize("metric", [(1, 1, 1, 1, 1), (1, -1, 1, 0, -1), (0, 1, 1, -1)])
+def test_inverse_dense_is_two_sided_inverse(metric):
+    n = len(metric)
+    x = rand_mv(3, n, 50)
+    x[:, 0] += 3.0
+    y = O.inverse_dense(x, metric)
+    one = torch.zeros_like(x)
+    one[:, 0] = 1.0
+    torch.testing.assert_close(O.einsum_product("geom", x, y, metric), one, rtol=0, atol=1e-12)
+    torch.testing.assert_close(O.einsum_product("geom", y, x, metric), one, rtol=0, atol=1e-12)
