@@ -16,7 +16,7 @@
 
 namespace clf {
 
-constexpr int kMaxN = 16;          // largest n the product kernels accept (tiled above 12)
+constexpr int kMaxN = 20;          // largest n the product kernels accept (tiled above 12)
 constexpr int kMaxNGraded = 20;    // graded ops are elementwise; bound rows * 2^n only
 
 int set_error(int code, const std::string& msg);

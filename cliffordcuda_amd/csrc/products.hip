@@ -313,7 +313,7 @@ __device__ __forceinline__ void gb_block_dispatch(float (&acc)[16], const float 
 
 struct BlkParams {
     long long batch;
-    int n;          // algebra dimension, 4 <= n <= kMaxN
+    int n;          // algebra dimension, 4 <= n <= kMaxN (20)
     unsigned negh;  // metric masks >> 4
     unsigned nulh;
     int nm1;        // (n - 1) & 1
@@ -967,7 +967,8 @@ __device__ __forceinline__ void stage_tile(float4* __restrict__ dst, const float
     }
 }
 
-// grid: (NB / 256) * batch workgroups; workgroup -> (row, output chunk)
+// work items: (NB / 256) * batch (row, output chunk) pairs, walked with a
+// 64-bit grid stride (the grid is capped, so no batch or n overflows it)
 template <int OP, bool LOWNEG>
 __global__ __launch_bounds__(256) void prod_fwd_tiled(const float* __restrict__ A, const float* __restrict__ B,
                                                        float* __restrict__ C, BlkParams P) {
@@ -976,42 +977,45 @@ __global__ __launch_bounds__(256) void prod_fwd_tiled(const float* __restrict__ 
     const int n = P.n;
     const unsigned NB = 1u << (n - 4);
     const unsigned chunks = NB / kTileBlocks;
-    const long long row = (long long)(blockIdx.x / chunks);
-    const unsigned K0 = (blockIdx.x % chunks) * kTileBlocks;
-    const unsigned kh = K0 + threadIdx.x;
-    const unsigned kl = kh & (kTileBlocks - 1);
-    const unsigned fullh = NB - 1u;
-    const float4* arow = reinterpret_cast<const float4*>(A) + (row << (n - 2));
-    const float4* brow = reinterpret_cast<const float4*>(B) + (row << (n - 2));
-    float acc[16];
+    const long long items = (long long)chunks * P.batch;
+    for (long long w = blockIdx.x; w < items; w += gridDim.x) {
+        const long long row = w / chunks;
+        const unsigned K0 = (unsigned)(w % chunks) * kTileBlocks;
+        const unsigned kh = K0 + threadIdx.x;
+        const unsigned kl = kh & (kTileBlocks - 1);
+        const unsigned fullh = NB - 1u;
+        const float4* arow = reinterpret_cast<const float4*>(A) + (row << (n - 2));
+        const float4* brow = reinterpret_cast<const float4*>(B) + (row << (n - 2));
+        float acc[16];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
-    for (unsigned I0 = 0; I0 < NB; I0 += kTileBlocks) {
-        __syncthreads();  // the previous tile is consumed
-        stage_tile(la, arow, I0);
-        stage_tile(lb, brow, I0 ^ K0);
-        __syncthreads();
-        for (unsigned il = 0; il < (unsigned)kTileBlocks; ++il) {
-            const unsigned ih = I0 + il, jh = ih ^ kh;
-            const HiSign hs = hi_sign<OP>(ih, jh, P.negh, P.nulh, fullh, P.nm1, P.mu);
-            if (!hs.valid) continue;
-            float av[16], bv[16];
-            load_blk(la, il, av);
-            load_blk(lb, il ^ kl, bv);
-            apply_flips(bv, hs.mask, hs.mask ^ (cross_pi<OP>(ih, P.nm1) << 31));
-            fwd_block_dispatch<OP, LOWNEG>(acc, av, bv, ih, jh);
+        for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+        for (unsigned I0 = 0; I0 < NB; I0 += kTileBlocks) {
+            __syncthreads();  // the previous tile is consumed
+            stage_tile(la, arow, I0);
+            stage_tile(lb, brow, I0 ^ K0);
+            __syncthreads();
+            for (unsigned il = 0; il < (unsigned)kTileBlocks; ++il) {
+                const unsigned ih = I0 + il, jh = ih ^ kh;
+                const HiSign hs = hi_sign<OP>(ih, jh, P.negh, P.nulh, fullh, P.nm1, P.mu);
+                if (!hs.valid) continue;
+                float av[16], bv[16];
+                load_blk(la, il, av);
+                load_blk(lb, il ^ kl, bv);
+                apply_flips(bv, hs.mask, hs.mask ^ (cross_pi<OP>(ih, P.nm1) << 31));
+                fwd_block_dispatch<OP, LOWNEG>(acc, av, bv, ih, jh);
+            }
         }
-    }
-    float4* out = reinterpret_cast<float4*>(C) + (row << (n - 2));
-    if (OP == OP_REGR) {
-        const unsigned ob = fullh ^ kh;
+        float4* out = reinterpret_cast<float4*>(C) + (row << (n - 2));
+        if (OP == OP_REGR) {
+            const unsigned ob = fullh ^ kh;
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            out[(ob << 2) + (3 - q)] = make_float4(acc[4 * q + 3], acc[4 * q + 2], acc[4 * q + 1], acc[4 * q]);
-    } else {
+            for (int q = 0; q < 4; ++q)
+                out[(ob << 2) + (3 - q)] = make_float4(acc[4 * q + 3], acc[4 * q + 2], acc[4 * q + 1], acc[4 * q]);
+        } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            out[(kh << 2) + q] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+            for (int q = 0; q < 4; ++q)
+                out[(kh << 2) + q] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+        }
     }
 }
 
@@ -1027,66 +1031,69 @@ __global__ __launch_bounds__(256) void prod_bwd_tiled(const float* __restrict__ 
     const int n = P.n;
     const unsigned NB = 1u << (n - 4);
     const unsigned chunks = NB / kTileBlocks;
-    const long long row = (long long)(blockIdx.x / chunks);
-    const unsigned H0 = (blockIdx.x % chunks) * kTileBlocks;
-    const unsigned h = H0 + threadIdx.x;
-    const unsigned hl = h & (kTileBlocks - 1);
-    const unsigned fullh = NB - 1u;
-    const bool want_a = GA != nullptr, want_b = GB != nullptr;
-    const float4* arow = reinterpret_cast<const float4*>(A) + (row << (n - 2));
-    const float4* brow = reinterpret_cast<const float4*>(B) + (row << (n - 2));
-    const float4* grow = reinterpret_cast<const float4*>(GC) + (row << (n - 2));
-    const unsigned pi_h = cross_pi<OP>(h, P.nm1);
-    float ga[16], gb[16];
+    const long long items = (long long)chunks * P.batch;
+    for (long long w = blockIdx.x; w < items; w += gridDim.x) {
+        const long long row = w / chunks;
+        const unsigned H0 = (unsigned)(w % chunks) * kTileBlocks;
+        const unsigned h = H0 + threadIdx.x;
+        const unsigned hl = h & (kTileBlocks - 1);
+        const unsigned fullh = NB - 1u;
+        const bool want_a = GA != nullptr, want_b = GB != nullptr;
+        const float4* arow = reinterpret_cast<const float4*>(A) + (row << (n - 2));
+        const float4* brow = reinterpret_cast<const float4*>(B) + (row << (n - 2));
+        const float4* grow = reinterpret_cast<const float4*>(GC) + (row << (n - 2));
+        const unsigned pi_h = cross_pi<OP>(h, P.nm1);
+        float ga[16], gb[16];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        ga[e] = 0.f;
-        gb[e] = 0.f;
-    }
-    for (unsigned M0 = 0; M0 < NB; M0 += kTileBlocks) {
-        const unsigned G0 = (OP == OP_REGR) ? ((fullh ^ H0 ^ M0) & ~(unsigned)(kTileBlocks - 1)) : (H0 ^ M0);
-        __syncthreads();
-        stage_tile(la, arow, M0);
-        stage_tile(lb, brow, M0);
-        stage_tile(lg, grow, G0);
-        __syncthreads();
-        for (unsigned ml = 0; ml < (unsigned)kTileBlocks; ++ml) {
-            const unsigned m = M0 + ml;
-            const HiSign sa = hi_sign<OP>(h, m, P.negh, P.nulh, fullh, P.nm1, P.mu);  // (i, j) = (h, m)
-            const HiSign sb = hi_sign<OP>(m, h, P.negh, P.nulh, fullh, P.nm1, P.mu);  // (i, j) = (m, h)
-            const bool do_a = want_a && sa.valid, do_b = want_b && sb.valid;
-            if (!do_a && !do_b) continue;
-            float g[16];
-            const unsigned gl = (OP == OP_REGR) ? ((kTileBlocks - 1) ^ hl ^ ml) : (hl ^ ml);
-            if (OP == OP_REGR) load_blk_rev(lg, gl, g);
-            else load_blk(lg, gl, g);
-            if (do_a) {
-                float bv[16];
-                load_blk(lb, ml, bv);
-                apply_flips(bv, sa.mask, sa.mask ^ (pi_h << 31));
-                ga_block_dispatch<OP, LOWNEG>(ga, bv, g, h, m);
-            }
-            if (do_b) {
-                const unsigned pm = cross_pi<OP>(m, P.nm1) << 31;
-                float av[16], gt[16];
-                load_blk(la, ml, av);
-                apply_flips(av, sb.mask, sb.mask ^ pm);
+        for (int e = 0; e < 16; ++e) {
+            ga[e] = 0.f;
+            gb[e] = 0.f;
+        }
+        for (unsigned M0 = 0; M0 < NB; M0 += kTileBlocks) {
+            const unsigned G0 = (OP == OP_REGR) ? ((fullh ^ H0 ^ M0) & ~(unsigned)(kTileBlocks - 1)) : (H0 ^ M0);
+            __syncthreads();
+            stage_tile(la, arow, M0);
+            stage_tile(lb, brow, M0);
+            stage_tile(lg, grow, G0);
+            __syncthreads();
+            for (unsigned ml = 0; ml < (unsigned)kTileBlocks; ++ml) {
+                const unsigned m = M0 + ml;
+                const HiSign sa = hi_sign<OP>(h, m, P.negh, P.nulh, fullh, P.nm1, P.mu);  // (i, j) = (h, m)
+                const HiSign sb = hi_sign<OP>(m, h, P.negh, P.nulh, fullh, P.nm1, P.mu);  // (i, j) = (m, h)
+                const bool do_a = want_a && sa.valid, do_b = want_b && sb.valid;
+                if (!do_a && !do_b) continue;
+                float g[16];
+                const unsigned gl = (OP == OP_REGR) ? ((kTileBlocks - 1) ^ hl ^ ml) : (hl ^ ml);
+                if (OP == OP_REGR) load_blk_rev(lg, gl, g);
+                else load_blk(lg, gl, g);
+                if (do_a) {
+                    float bv[16];
+                    load_blk(lb, ml, bv);
+                    apply_flips(bv, sa.mask, sa.mask ^ (pi_h << 31));
+                    ga_block_dispatch<OP, LOWNEG>(ga, bv, g, h, m);
+                }
+                if (do_b) {
+                    const unsigned pm = cross_pi<OP>(m, P.nm1) << 31;
+                    float av[16], gt[16];
+                    load_blk(la, ml, av);
+                    apply_flips(av, sb.mask, sb.mask ^ pm);
 #pragma unroll
-                for (int e = 0; e < 16; ++e) gt[e] = (cpopc((unsigned)e) & 1) ? flip(g[e], pm) : g[e];
-                gb_block_dispatch<OP, LOWNEG>(gb, av, gt, m, h);
+                    for (int e = 0; e < 16; ++e) gt[e] = (cpopc((unsigned)e) & 1) ? flip(g[e], pm) : g[e];
+                    gb_block_dispatch<OP, LOWNEG>(gb, av, gt, m, h);
+                }
             }
         }
-    }
-    const long long base = row << (n - 2);
-    if (want_a) {
-        float4* o = reinterpret_cast<float4*>(GA) + base;
+        const long long base = row << (n - 2);
+        if (want_a) {
+            float4* o = reinterpret_cast<float4*>(GA) + base;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) o[(h << 2) + q] = make_float4(ga[4 * q], ga[4 * q + 1], ga[4 * q + 2], ga[4 * q + 3]);
-    }
-    if (want_b) {
-        float4* o = reinterpret_cast<float4*>(GB) + base;
+            for (int q = 0; q < 4; ++q) o[(h << 2) + q] = make_float4(ga[4 * q], ga[4 * q + 1], ga[4 * q + 2], ga[4 * q + 3]);
+        }
+        if (want_b) {
+            float4* o = reinterpret_cast<float4*>(GB) + base;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) o[(h << 2) + q] = make_float4(gb[4 * q], gb[4 * q + 1], gb[4 * q + 2], gb[4 * q + 3]);
+            for (int q = 0; q < 4; ++q) o[(h << 2) + q] = make_float4(gb[4 * q], gb[4 * q + 1], gb[4 * q + 2], gb[4 * q + 3]);
+        }
     }
 }
 
@@ -1096,20 +1103,22 @@ __global__ __launch_bounds__(256) void prod_bwd_tiled(const float* __restrict__ 
 __global__ __launch_bounds__(256) void prod_fwd_generic(int op, int n, unsigned neg, unsigned nul,
                                                          const float* __restrict__ A, const float* __restrict__ B,
                                                          float* __restrict__ C, long long batch) {
-    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     const unsigned D = 1u << n;
-    if (idx >= (batch << n)) return;
-    const long long row = idx >> n;
-    const unsigned k = (unsigned)(idx & (D - 1));
-    const float* a = A + (row << n);
-    const float* b = B + (row << n);
-    float acc = 0.f;
-    for (unsigned i = 0; i < D; ++i) {
-        const int s = full_sign(op, n, i, i ^ k, neg, nul);
-        if (s) acc = __builtin_fmaf((float)s * a[i], b[i ^ k], acc);
+    const long long total = batch << n;
+    for (long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (long long)gridDim.x * blockDim.x) {
+        const long long row = idx >> n;
+        const unsigned k = (unsigned)(idx & (D - 1));
+        const float* a = A + (row << n);
+        const float* b = B + (row << n);
+        float acc = 0.f;
+        for (unsigned i = 0; i < D; ++i) {
+            const int s = full_sign(op, n, i, i ^ k, neg, nul);
+            if (s) acc = __builtin_fmaf((float)s * a[i], b[i ^ k], acc);
+        }
+        const unsigned ok = (op == OP_REGR) ? (~k & (D - 1)) : k;
+        C[(row << n) + ok] = acc;
     }
-    const unsigned ok = (op == OP_REGR) ? (~k & (D - 1)) : k;
-    C[(row << n) + ok] = acc;
 }
 
 // ga[k] = sum_j sigma(k, j) b[j] gf[k^j]   (which == 0)
@@ -1117,22 +1126,24 @@ __global__ __launch_bounds__(256) void prod_fwd_generic(int op, int n, unsigned 
 __global__ __launch_bounds__(256) void prod_bwd_generic(int op, int n, unsigned neg, unsigned nul, int which,
                                                          const float* __restrict__ X, const float* __restrict__ GC,
                                                          float* __restrict__ OUT, long long batch) {
-    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     const unsigned D = 1u << n;
-    if (idx >= (batch << n)) return;
-    const long long row = idx >> n;
-    const unsigned k = (unsigned)(idx & (D - 1));
-    const float* x = X + (row << n);
-    const float* gc = GC + (row << n);
-    float acc = 0.f;
-    for (unsigned u = 0; u < D; ++u) {
-        const int s = which == 0 ? full_sign(op, n, k, u, neg, nul) : full_sign(op, n, u, k, neg, nul);
-        if (!s) continue;
-        const unsigned m = u ^ k;
-        const float gv = (op == OP_REGR) ? gc[~m & (D - 1)] : gc[m];
-        acc = __builtin_fmaf((float)s * x[u], gv, acc);
+    const long long total = batch << n;
+    for (long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (long long)gridDim.x * blockDim.x) {
+        const long long row = idx >> n;
+        const unsigned k = (unsigned)(idx & (D - 1));
+        const float* x = X + (row << n);
+        const float* gc = GC + (row << n);
+        float acc = 0.f;
+        for (unsigned u = 0; u < D; ++u) {
+            const int s = which == 0 ? full_sign(op, n, k, u, neg, nul) : full_sign(op, n, u, k, neg, nul);
+            if (!s) continue;
+            const unsigned m = u ^ k;
+            const float gv = (op == OP_REGR) ? gc[~m & (D - 1)] : gc[m];
+            acc = __builtin_fmaf((float)s * x[u], gv, acc);
+        }
+        OUT[(row << n) + k] = acc;
     }
-    OUT[(row << n) + k] = acc;
 }
 
 // ---- host side --------------------------------------------------------------
@@ -1203,12 +1214,16 @@ static bool blocked_plan(int op, int n, uint32_t neg, uint32_t nul, int nops, Bl
     return true;
 }
 
+// Grid cap of the grid-stride kernels (tiled, per-coefficient): well inside
+// the 2^32 work-items of one launch dimension.
+constexpr long long kMaxGrid = 1LL << 22;
+
 // Tiled kernels: n >= 12 (at least one 256-block tile per row).
 static bool tiled_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, bool& lowneg, dim3& grid) {
     if (n < 12 || !blocked_metric(op, n, neg, nul, lowneg)) return false;
     block_sign_params(n, neg, nul, P);
-    const long long chunks = (1LL << (n - 4)) / kTileBlocks;
-    grid = dim3((unsigned)(chunks * P.batch));
+    const long long items = (1LL << (n - 4)) / kTileBlocks * P.batch;
+    grid = dim3((unsigned)(items < kMaxGrid ? items : kMaxGrid));
     return true;
 }
 
@@ -1343,7 +1358,8 @@ int product_fwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
 #undef CLF_FWD_TILED
     } else {
         const long long total = batch << n;
-        const unsigned blocks = (unsigned)((total + 255) / 256);
+        const long long want = (total + 255) / 256;
+        const unsigned blocks = (unsigned)(want < kMaxGrid ? want : kMaxGrid);
         hipLaunchKernelGGL(prod_fwd_generic, dim3(blocks), dim3(256), 0, s, op, n, neg, nul, a, b, c,
                            (long long)batch);
     }
@@ -1413,7 +1429,8 @@ int product_bwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
 #undef CLF_BWD_TILED
     } else {
         const long long total = batch << n;
-        const unsigned blocks = (unsigned)((total + 255) / 256);
+        const long long want = (total + 255) / 256;
+        const unsigned blocks = (unsigned)(want < kMaxGrid ? want : kMaxGrid);
         if (ga)
             hipLaunchKernelGGL(prod_bwd_generic, dim3(blocks), dim3(256), 0, s, op, n, neg, nul, 0, b, gc, ga,
                                (long long)batch);

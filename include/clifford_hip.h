@@ -76,9 +76,11 @@ const char* clf_last_error(void);
  *  kernels/ga/geom_prod_tiled.cu:169-175). */
 int clf_device_info_get(int device, clf_device_info* out);
 
-/* Largest n the product kernels accept (16; rows past the LDS budget, n >= 13,
+/* Largest n the product kernels accept (20; rows past the LDS budget, n >= 13,
  * run tiled kernels, as the reference's geom_prod_tiled_fused does,
- * src/cliffordcuda/extensions/ga/geom_prod_tiled.py:370-398). */
+ * src/cliffordcuda/extensions/ga/geom_prod_tiled.py:370-398, which has no
+ * fixed ceiling; a row of n = 20 is 4 MiB and its geometric product 2^40
+ * multiply-adds). */
 int clf_product_max_n(void);
 
 /* Forward of a binary product on `batch` rows.

@@ -446,3 +446,48 @@ def inverse_dense(x: torch.Tensor, metric=None) -> torch.Tensor:
     e0 = torch.zeros(x.shape[0], dim, 1, dtype=x.dtype)
     e0[:, 0, 0] = 1.0
     return torch.linalg.solve(L, e0).squeeze(-1)
+
+
+def product_coefficients(op: str, a: torch.Tensor, b: torch.Tensor, metric, ks) -> torch.Tensor:
+    """Selected output coefficients c[:, k] (k in ks) of a product for large n,
+    where the (2^n)^2 sign table does not fit: sigma(i, i ^ k) evaluated for
+    one k at a time with the closed form of ``sign_value_table``
+    (``geom_prod.py:44-74``) times the op's mask (``_einsum_refs.py:58-83``).
+    Geometric, wedge, inner, lc and rc only. Pinned by: equals
+    ``einsum_product`` on every coefficient at small n."""
+    n = a.shape[-1].bit_length() - 1
+    metric = normalize_metric(n, metric)
+    dim = 1 << n
+    i = torch.arange(dim, dtype=torch.int64)
+    out = []
+    for k in ks:
+        j = i ^ k
+        parity = torch.zeros(dim, dtype=torch.int64)
+        for s in range(n):
+            parity += ((i >> s) & 1) * _bits_below(j, s)
+        sign = (1 - 2 * (parity & 1)).to(a.dtype)
+        common = i & j
+        for g, m in enumerate(metric):
+            if m != 1:
+                sign = torch.where(((common >> g) & 1).bool(), sign * m, sign)
+        if op == "wedge":
+            sign = sign * ((i & j) == 0)
+        elif op == "inner":
+            sign = sign * (((i & ~j) == 0) | ((j & ~i) == 0))
+        elif op == "lc":
+            sign = sign * ((i & j) == i)
+        elif op == "rc":
+            sign = sign * ((i & j) == j)
+        elif op != "geom":
+            raise ValueError(f"unsupported op {op!r}")
+        out.append((a * b[:, j] * sign).sum(-1))
+    return torch.stack(out, -1)
+
+
+def _bits_below(j: torch.Tensor, s: int) -> torch.Tensor:
+    """Number of set bits of j strictly below position s (the generators of j
+    that e_s of i has to pass: pairs (s, t) with s > t, i_s = 1, j_t = 1)."""
+    c = torch.zeros_like(j)
+    for t in range(s):
+        c += (j >> t) & 1
+    return c

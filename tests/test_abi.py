@@ -51,7 +51,7 @@ def test_rotor_state_length_matches_python():
 @pytest.mark.parametrize("args,code,msg", [
     ((9, 5, 0, 0, None, None, None, 4, None), 1, "unknown product op"),
     ((0, 0, 0, 0, None, None, None, 4, None), 1, "n must be in"),
-    ((0, 17, 0, 0, None, None, None, 4, None), 1, "n must be in"),
+    ((0, 21, 0, 0, None, None, None, 4, None), 1, "n must be in"),
     ((0, 5, 1 << 5, 0, None, None, None, 4, None), 1, "bits above n"),
     ((0, 5, 3, 2, None, None, None, 4, None), 1, "overlap"),
     ((0, 5, 0, 0, None, None, None, -1, None), 1, "batch"),

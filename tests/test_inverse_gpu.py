@@ -44,7 +44,7 @@ def _general(B, n, seed):
     return x
 
 
-@pytest.mark.parametrize("n", [5, 8, 11, 13, 15])
+@pytest.mark.parametrize("n", [5, 8, 11, 13, 15, 17])
 def test_versor_exact_all_n(n):
     """Versor inverse at every n, both sides (reference test_inverse.py:62-71)."""
     for metric in _metrics(n):

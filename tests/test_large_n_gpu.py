@@ -1,9 +1,10 @@
-"""Products past the whole-row LDS limit (n = 12 .. 16, the reference's tiled
+"""Products past the whole-row LDS limit (n = 12 .. 18, the reference's tiled
 path, extensions/ga/geom_prod_tiled.py:1-31 and tests/correctness/
 test_geom_prod_tiled.py): the tiled kernels against the whole-row kernels at
 n = 12 (tiling forced with CLF_PRODUCT_PATH=tiled), against the
 per-coefficient generic kernels (an independent algorithm, forced with
-CLF_PRODUCT_PATH=generic) at n = 14 and 16, and against the oracle at n = 13.
+CLF_PRODUCT_PATH=generic) at n = 14, 16 and 17, and against the oracle at
+n = 13 (every coefficient) and 17 (sampled coefficients).
 Bar: normwise relative error <= 1e-5 for values and both gradients."""
 import pytest
 import torch
@@ -115,12 +116,32 @@ def test_tiled_geom_matches_oracle_n13():
     assert rel_err(c, ref) <= TOL
 
 
+@pytest.mark.parametrize("op", ["geom", "lc", "wedge"])
+@pytest.mark.parametrize("metric", [(1,) * 15 + (-1, 0), (1, -1) * 8 + (1,)], ids=["blocked17", "mixed17"])
+def test_n17_matches_oracle_sample_and_generic(op, metric, monkeypatch):
+    """n = 17 (131072 components, the reference's test_inverse.py:64 size):
+    the default kernels (tiled for the blocked metric, per-coefficient for the
+    mixed one) against the oracle on sampled output coefficients, and the
+    tiled forward and backward against the per-coefficient kernels in full."""
+    a, b, gc = inputs(17, 2, 17)
+    print(f"[case] n=17 op={op} metric={metric}", flush=True)
+    res = run(op, metric, a, b, gc, monkeypatch)
+    ks = [0, 1, 5, 777, 65536, 131071]
+    ref = O.product_coefficients(op, a.double().cpu(), b.double().cpu(), metric, ks)
+    assert rel_err(res[0][:, ks], ref) <= TOL
+    if metric[:4] == (1, 1, 1, 1):
+        e = compare(res, run(op, metric, a, b, gc, monkeypatch, "generic"))
+        assert max(e) <= TOL, e
+    assert all(torch.isfinite(t).all() for t in res)
+
+
 def test_public_api_past_limit():
-    """The algebra object and the free functions accept n = 16."""
-    metric = (1,) * 16
+    """The algebra object and the free functions accept n = 18 (past 16, where
+    the earlier kernels stopped)."""
+    metric = (1,) * 18
     cl = cc.CliffordAlgebra(metric, device="cuda")
-    x = torch.randn(1, 1 << 16, device="cuda")
-    e0 = torch.zeros(1, 1 << 16, device="cuda")
+    x = torch.randn(1, 1 << 18, device="cuda")
+    e0 = torch.zeros(1, 1 << 18, device="cuda")
     e0[0, 1] = 1.0                        # the vector e_0
     y = cl.geom_prod(e0, cl.geom_prod(e0, x))   # e_0 e_0 x = x (e_0^2 = +1)
     assert rel_err(y, x) <= TOL

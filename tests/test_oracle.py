@@ -448,3 +448,12 @@ def test_inverse_dense_is_two_sided_inverse(metric):
     one[:, 0] = 1.0
     torch.testing.assert_close(O.einsum_product("geom", x, y, metric), one, rtol=0, atol=1e-12)
     torch.testing.assert_close(O.einsum_product("geom", y, x, metric), one, rtol=0, atol=1e-12)
+
+
+@pytest.mark.parametrize("op", ["geom", "wedge", "inner", "lc", "rc"])
+def test_product_coefficients_equal_einsum(op):
+    metric = (1, -1, 0, 1, -1)
+    a, b = rand_mv(2, 5, 60), rand_mv(2, 5, 61)
+    full = O.einsum_product(op, a, b, metric)
+    ks = list(range(32))
+    torch.testing.assert_close(O.product_coefficients(op, a, b, metric, ks), full, rtol=0, atol=1e-12)
