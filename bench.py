@@ -15,6 +15,7 @@ configurations, one JSON line each, for the results table.
 from __future__ import annotations
 
 import argparse
+import contextlib
 import json
 import os
 import sys
@@ -26,6 +27,20 @@ sys.path.insert(0, ROOT)
 PEAK_FP32_TFLOPS = 157.3   # MI355X FP32 peak (vector and matrix)
 PEAK_HBM_GBS = 8000.0
 METRIC = "multivector-pairs/s fwd+bwd, Cl(8,0) fp32, 1 MI355X; % FP32 VALU/MFMA peak"
+
+
+@contextlib.contextmanager
+def path_switch(name, value):
+    """Set a CLF_* path switch for the block (the library reads the switches
+    once per process, so each change is followed by a reload)."""
+    from cliffordcuda_amd import _lib
+    os.environ[name] = value
+    _lib.reload_options()
+    try:
+        yield
+    finally:
+        del os.environ[name]
+        _lib.reload_options()
 
 
 def parse():
@@ -46,6 +61,18 @@ def n_terms(op: str, metric) -> int:
     return {"geom": 4 ** (n - r) * 3 ** r, "wedge": 3 ** n, "lc": 3 ** (n - r) * 2 ** r,
             "rc": 3 ** (n - r) * 2 ** r, "inner": 2 * 3 ** (n - r) * 2 ** r - 2 ** (n - r),
             "regressive": 3 ** n}[op]
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (first 'model name' line of /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_baseline(n: int, budget_s: float):
@@ -71,7 +98,7 @@ def cpu_baseline(n: int, budget_s: float):
     times.sort()
     med = times[len(times) // 2]
     return {"value": rows / med, "unit": "multivector-pairs/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+            "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(), "kind": "port",
             "sample": f"{len(times)} chunks x {rows} rows of Cl({n},0) geom_prod fwd+bwd (oracle einsum "
                       f"restatement, torch fp32 on the host CPU, median chunk time)"}
 
@@ -91,7 +118,7 @@ def cpu_rate(work, rows: int, budget_s: float, label: str, dtype: str = "fp32"):
             break
     times.sort()
     return {"value": rows / times[len(times) // 2], "unit": "rows/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+            "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(), "kind": "port",
             "sample": f"{len(times)} chunks x {rows} rows: {label} (oracle restatement, torch {dtype} on the "
                       f"host CPU, median chunk time)"}
 
@@ -188,12 +215,9 @@ def headline(args, torch, cc, lib, T):
     bwd_ms = T.kernel_ms(bwd)
     # the per-term kernels (the path of every other signature and product),
     # forced for comparison at the same shape
-    os.environ["CLF_GEOM_PATH"] = "direct"
-    try:
+    with path_switch("CLF_GEOM_PATH", "direct"):
         dfwd_ms = T.kernel_ms(fwd)
         dbwd_ms = T.kernel_ms(bwd)
-    finally:
-        del os.environ["CLF_GEOM_PATH"]
     nt = D * D
     bwd_flops = 4.0 * nt * B       # reference term-sum count: 2 products of 4^n multiply-adds
     fwd_flops = 2.0 * nt * B
@@ -280,8 +304,7 @@ def products_config(args, torch, cc, lib, T, name, metric, B, ops, fwd_only=Fals
                       "hbm_gbs_algorithmic": byts / t / 1e9, "frac_hbm": byts / t / 1e9 / PEAK_HBM_GBS})
         if op == "geom":
             # the per-term kernels at the same shape (the path of every other op)
-            os.environ["CLF_GEOM_PATH"] = "direct"
-            try:
+            with path_switch("CLF_GEOM_PATH", "direct"):
                 dfms = T.kernel_ms(lambda: lib.clf_product_fwd(code, n, neg, nul, a.data_ptr(), b.data_ptr(),
                                                                c.data_ptr(), B, sp))
                 dbms = 0.0
@@ -289,8 +312,6 @@ def products_config(args, torch, cc, lib, T, name, metric, B, ops, fwd_only=Fals
                     dbms = T.kernel_ms(lambda: lib.clf_product_bwd(code, n, neg, nul, a.data_ptr(), b.data_ptr(),
                                                                    gc.data_ptr(), ga.data_ptr(), gb.data_ptr(), B,
                                                                    sp))
-            finally:
-                del os.environ["CLF_GEOM_PATH"]
             dt = (dfms + dbms) * 1e-3
             entry["per_term_path"] = {"fwd_ms": dfms, "bwd_ms": dbms, "pairs_per_s": B / dt,
                                       "valu_frac": flops / dt / 1e12 / PEAK_FP32_TFLOPS}
@@ -339,11 +360,8 @@ def c3_layer(args, torch, cc, lib, T):
     # (rep16_bcast_* kernels); the GEMM against the weight's 256 x 256 matrix
     # (the path of the other layer ops and signatures) forced for comparison
     fms, bms = T.kernel_ms(fwd), T.kernel_ms(bwd)
-    os.environ["CLF_GEOM_PATH"] = "direct"
-    try:
+    with path_switch("CLF_GEOM_PATH", "direct"):
         gfms, gbms = T.kernel_ms(fwd), T.kernel_ms(bwd)
-    finally:
-        del os.environ["CLF_GEOM_PATH"]
     fwd_bytes, bwd_bytes = 8.0 * D * B, 12.0 * D * B  # x, y; x, gy, gx
     return {"workload": "c3: GeometricProductLayer Cl(8,0) fwd+bwd (x and weight grads)", "batch": B,
             "ms_per_step": ms, "rows_per_s": B / (ms * 1e-3),
@@ -423,13 +441,10 @@ def c4_rotor(args, torch, cc, lib, T):
                                                       gx.data_ptr(), gs.data_ptr(), B, ws.data_ptr(), nb, sp))
     # the same entry points on the register plane-rotation chain (the n = 8
     # default is the Cl(8,0) representation on the matrix cores)
-    os.environ["CLF_ROTOR_PATH"] = "chain"
-    try:
+    with path_switch("CLF_ROTOR_PATH", "chain"):
         cfms = T.kernel_ms(lambda: lib.clf_rotor_apply_fwd(n, state.data_ptr(), x.data_ptr(), y.data_ptr(), B, sp))
         cbms = T.kernel_ms(lambda: lib.clf_rotor_apply_bwd(n, state.data_ptr(), x.data_ptr(), gy.data_ptr(),
                                                            gx.data_ptr(), gs.data_ptr(), B, ws.data_ptr(), nb, sp))
-    finally:
-        del os.environ["CLF_ROTOR_PATH"]
     byts = 20.0 * D * B
     return {"workload": "c4: RotorLayer train Cl(7,1) fwd+bwd (rotor recompiled each step)", "batch": B,
             "path": "Cl(8,0) representation, MFMA (rotor16 kernels)",

@@ -45,6 +45,7 @@ class DeviceInfo(ctypes.Structure):
 # name -> (restype, argtypes); the exact export list of include/clifford_hip.h
 SIGNATURES = {
     "clf_abi_version": (_i32, []),
+    "clf_options_reload": (None, []),
     "clf_last_error": (ctypes.c_char_p, []),
     "clf_device_info_get": (_i32, [_i32, ctypes.POINTER(DeviceInfo)]),
     "clf_product_max_n": (_i32, []),
@@ -118,6 +119,12 @@ def check(rc: int, what: str):
 
 def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
+
+
+def reload_options() -> None:
+    """Re-read the CLF_* path switches (the library reads them once per
+    process otherwise)."""
+    load().clf_options_reload()
 
 
 def stream_of(t: torch.Tensor) -> int:

@@ -2,9 +2,7 @@
 #include <cstdlib>
 #include <cstring>
 
-#include <map>
 #include <mutex>
-#include <tuple>
 
 #include "clf_common.h"
 
@@ -25,36 +23,111 @@ void clear_error() { g_last_error.clear(); }
 // step re-read lose their cache hits).
 constexpr double kStreamNtBytes = 320.0 * 1024 * 1024;
 
-bool stream_nt(double footprint_bytes) {
+// ---- options: the environment, read once --------------------------------
+
+static Options read_options() {
+    Options o{};
     const char* e = std::getenv("CLF_STREAM_NT");
-    if (e && std::strcmp(e, "on") == 0) return true;
-    if (e && std::strcmp(e, "off") == 0) return false;
+    o.stream_nt = (e && std::strcmp(e, "on") == 0) ? 1 : ((e && std::strcmp(e, "off") == 0) ? 0 : -1);
+    e = std::getenv("CLF_PRODUCT_PATH");
+    o.product_path = PATH_DEFAULT;
+    if (e) {
+        if (std::strcmp(e, "blocked") == 0) o.product_path = PATH_BLOCKED;
+        else if (std::strcmp(e, "balanced") == 0) o.product_path = PATH_BALANCED;
+        else if (std::strcmp(e, "tiled") == 0) o.product_path = PATH_TILED;
+        else if (std::strcmp(e, "generic") == 0) o.product_path = PATH_GENERIC;
+    }
+    e = std::getenv("CLF_GEOM_PATH");
+    o.geom_direct = e && std::strcmp(e, "direct") == 0;
+    e = std::getenv("CLF_SPLIT_PATH");
+    o.split_pairs = e && std::strcmp(e, "pairs") == 0;
+    e = std::getenv("CLF_ROTOR_PATH");
+    o.rotor_chain = e && std::strcmp(e, "chain") == 0;
+    return o;
+}
+
+// Published snapshots; a reload publishes a new one and keeps the old ones
+// alive (readers may still hold them), so a few bytes per reload stay.
+static std::atomic<const Options*> g_options{nullptr};
+static std::mutex g_options_mu;
+
+const Options& options() {
+    const Options* o = g_options.load(std::memory_order_acquire);
+    if (o) return *o;
+    std::lock_guard<std::mutex> lock(g_options_mu);
+    o = g_options.load(std::memory_order_relaxed);
+    if (!o) {
+        o = new Options(read_options());
+        g_options.store(o, std::memory_order_release);
+    }
+    return *o;
+}
+
+void options_reload() {
+    std::lock_guard<std::mutex> lock(g_options_mu);
+    g_options.store(new Options(read_options()), std::memory_order_release);
+}
+
+bool stream_nt(double footprint_bytes) {
+    const int f = options().stream_nt;
+    if (f >= 0) return f == 1;
     return footprint_bytes > kStreamNtBytes;
 }
 
+// ---- resident grid: occupancy per (device, kernel, dynamic LDS) ------------
+// Open-addressed table with lock-free reads: a slot's key is published (release)
+// after its value; a lookup that finds the key reads the value it guards.
+constexpr int kGridSlots = 4096;
+struct GridSlot {
+    std::atomic<uintptr_t> key;
+    long long cap;
+};
+static GridSlot g_grid[kGridSlots];
+static std::mutex g_grid_mu;
+
+static uintptr_t grid_key(int dev, const void* kernel, size_t dyn_lds) {
+    // distinct for distinct (dev, kernel, lds) in practice: kernels are code
+    // addresses, dev < 256 and the dynamic LDS is below 2^20 bytes
+    uintptr_t k = (uintptr_t)kernel;
+    k ^= ((uintptr_t)dyn_lds << 40) ^ ((uintptr_t)(dev & 0xff) << 32) ^ ((uintptr_t)(dev >> 8) << 60);
+    return k | 1u;  // never 0 (empty)
+}
+
 unsigned resident_grid(const void* kernel, int block_threads, size_t dyn_lds, long long wanted) {
-    static std::mutex mu;
-    static std::map<std::tuple<int, const void*, size_t>, long long> cache;
     if (wanted < 1) return 1;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    const uintptr_t key = grid_key(dev, kernel, dyn_lds);
+    const unsigned h0 = (unsigned)((key >> 4) ^ (key >> 17) ^ (key >> 33)) & (kGridSlots - 1);
     long long cap = 0;
-    {
-        std::lock_guard<std::mutex> lock(mu);
-        auto key = std::make_tuple(dev, kernel, dyn_lds);
-        auto it = cache.find(key);
-        if (it != cache.end()) {
-            cap = it->second;
-        } else {
-            int per_cu = 0, cus = 0;
-            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block_threads, dyn_lds) != hipSuccess ||
-                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
-                (void)hipGetLastError();  // clear the query's error; fall back to a fixed cap
-                per_cu = 2;
-                cus = 256;
+    for (unsigned probe = 0; probe < kGridSlots; ++probe) {
+        GridSlot& sl = g_grid[(h0 + probe) & (kGridSlots - 1)];
+        const uintptr_t k = sl.key.load(std::memory_order_acquire);
+        if (k == key) {
+            cap = sl.cap;
+            break;
+        }
+        if (k == 0) break;  // not cached yet
+    }
+    if (cap == 0) {
+        int per_cu = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block_threads, dyn_lds) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+            (void)hipGetLastError();  // clear the query's error; fall back to a fixed cap
+            per_cu = 2;
+            cus = 256;
+        }
+        cap = (long long)(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+        std::lock_guard<std::mutex> lock(g_grid_mu);
+        for (unsigned probe = 0; probe < kGridSlots; ++probe) {
+            GridSlot& sl = g_grid[(h0 + probe) & (kGridSlots - 1)];
+            const uintptr_t k = sl.key.load(std::memory_order_relaxed);
+            if (k == key) break;  // another thread inserted it meanwhile
+            if (k == 0) {
+                sl.cap = cap;
+                sl.key.store(key, std::memory_order_release);
+                break;
             }
-            cap = (long long)(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
-            cache.emplace(key, cap);
         }
     }
     return (unsigned)(wanted < cap ? wanted : cap);
@@ -102,6 +175,8 @@ int bcast_bwd_noalloc(int op, int side, int n, uint32_t neg, uint32_t nul, const
 extern "C" {
 
 int clf_abi_version(void) { return CLF_ABI_VERSION; }
+
+void clf_options_reload(void) { clf::options_reload(); }
 
 const char* clf_last_error(void) { return clf::g_last_error.c_str(); }
 

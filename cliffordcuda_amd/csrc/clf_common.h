@@ -10,6 +10,9 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <atomic>
+#include <mutex>
 #include <string>
 
 #include "../../include/clifford_hip.h"
@@ -34,6 +37,49 @@ unsigned resident_grid(const void* kernel, int block_threads, size_t dyn_lds, lo
 // keep cache hits for the next kernel. stream_nt() decides per launch from the
 // launch's row bytes (CLF_STREAM_NT=on / off forces it).
 bool stream_nt(double footprint_bytes);
+
+// Path switches for comparisons and measurements, read from the environment
+// once per process (at the first launch) and again only by
+// clf_options_reload(); a running model's kernels never change under it.
+//   CLF_STREAM_NT=on|off         nontemporal row streaming (default: by size)
+//   CLF_PRODUCT_PATH=blocked|balanced|tiled|generic   per-term kernel family
+//   CLF_GEOM_PATH=direct         geometric product on the per-term kernels
+//   CLF_SPLIT_PATH=pairs         n = 10 split path as separate pair sums
+//   CLF_ROTOR_PATH=chain         n = 8 rotor on the register plane chain
+enum ProductPath { PATH_DEFAULT = 0, PATH_BLOCKED, PATH_BALANCED, PATH_TILED, PATH_GENERIC };
+struct Options {
+    int stream_nt;  // -1 by size, 0 off, 1 on
+    int product_path;
+    bool geom_direct, split_pairs, rotor_chain;
+};
+const Options& options();
+void options_reload();
+
+// A cache of per-signature tables indexed by a small key (0 <= key < N):
+// built once under a lock, read without one afterwards (the ready flag is
+// published with release order after the entry is written).
+template <class T, int N>
+struct TableCache {
+    std::atomic<int> ready[N];
+    bool ok[N];
+    T tab[N];
+    std::mutex mu;
+    template <class Build>
+    bool get(int key, T& out, Build build) {
+        if (key < 0 || key >= N) return false;
+        if (ready[key].load(std::memory_order_acquire) != 1) {
+            std::lock_guard<std::mutex> lock(mu);
+            if (ready[key].load(std::memory_order_relaxed) != 1) {
+                T t{};
+                ok[key] = build(t);
+                tab[key] = t;
+                ready[key].store(1, std::memory_order_release);
+            }
+        }
+        if (ok[key]) out = tab[key];
+        return ok[key];
+    }
+};
 typedef float clf_fvec4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float4 load_stream(const float4* p) {

@@ -1227,15 +1227,11 @@ static bool tiled_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, 
     return true;
 }
 
-// CLF_PRODUCT_PATH (read at each call) selects a path for comparisons where
-// several apply: "tiled" runs n = 12 on the tiled kernels instead of the
-// whole-row ones, "generic" runs the per-coefficient kernels for any n.
-static bool product_path_is(const char* what) {
-    const char* e = std::getenv("CLF_PRODUCT_PATH");
-    return e && std::strcmp(e, what) == 0;
-}
-static bool tiled_forced() { return product_path_is("tiled"); }
-static bool generic_forced() { return product_path_is("generic"); }
+// CLF_PRODUCT_PATH (options()) selects a path for comparisons where several
+// apply: "tiled" runs n = 12 on the tiled kernels instead of the whole-row
+// ones, "generic" runs the per-coefficient kernels for any n.
+static bool tiled_forced() { return options().product_path == PATH_TILED; }
+static bool generic_forced() { return options().product_path == PATH_GENERIC; }
 
 // Balanced kernels: wedge, lc, rc, regressive and the inner product's forward
 // for 4 <= n <= 10, the inner product's backward for n >= 8
@@ -1248,7 +1244,7 @@ static bool generic_forced() { return product_path_is("generic"); }
 static bool bal_plan(int op, int n, uint32_t neg, uint32_t nul, bool fwd, BlkParams& P, bool& lowneg) {
     if (n < kBalMinN || n > kBalMaxN) return false;
     const bool opt_in = op == OP_GEOM || (op == OP_INNER && !fwd && n < 8);
-    if (opt_in ? !product_path_is("balanced") : product_path_is("blocked")) return false;
+    if (opt_in ? options().product_path != PATH_BALANCED : options().product_path == PATH_BLOCKED) return false;
     if (!blocked_metric(op, n, neg, nul, lowneg)) return false;
     block_sign_params(n, neg, nul, P);
     return true;

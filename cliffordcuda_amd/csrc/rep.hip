@@ -709,20 +709,13 @@ static bool rep_table_build(int n, uint32_t neg, RepTable& T) {
     return true;
 }
 
-// Tables are built once per (n, neg) and kept (immutable after insertion).
+// Tables are built once per (n, neg) and kept (immutable after insertion);
+// n is even and at most 2 kRepMaxLogM, so (n / 2, neg) indexes a small array.
 bool rep_table(int n, uint32_t neg, RepTable& T) {
-    static std::mutex mu;
-    static std::map<unsigned, std::pair<bool, RepTable>> cache;
-    const unsigned key = ((unsigned)n << 24) | neg;
-    std::lock_guard<std::mutex> lock(mu);
-    auto it = cache.find(key);
-    if (it == cache.end()) {
-        RepTable t{};
-        const bool ok = rep_table_build(n, neg, t);
-        it = cache.emplace(key, std::make_pair(ok, t)).first;
-    }
-    if (it->second.first) T = it->second.second;
-    return it->second.first;
+    constexpr int kNegs = 1 << (2 * kRepMaxLogM);  // neg has at most n <= 8 bits
+    static TableCache<RepTable, (kRepMaxLogM + 1) * kNegs> cache;
+    if (n < 0 || (n & 1) || n > 2 * kRepMaxLogM || neg >= (unsigned)kNegs) return rep_table_build(n, neg, T);
+    return cache.get((n / 2) * kNegs + (int)neg, T, [&](RepTable& t) { return rep_table_build(n, neg, t); });
 }
 
 bool split_applicable(int op, int n, uint32_t neg, uint32_t nul);
@@ -819,10 +812,7 @@ namespace clf {
 // CLF_GEOM_PATH=direct in the environment (read at each call) turns the
 // matrix-representation paths off, for comparisons against the per-term and
 // GEMM kernels.
-bool rep_disabled_by_env() {
-    const char* e = std::getenv("CLF_GEOM_PATH");
-    return e && std::strcmp(e, "direct") == 0;
-}
+bool rep_disabled_by_env() { return options().geom_direct; }
 
 // Broadcast-weight geometric product on the m = 16 path (n = 8, real type).
 bool rep_bcast_applicable(int op, int n, uint32_t neg, uint32_t nul) {

@@ -469,17 +469,8 @@ static bool rep7_table_build(uint32_t neg, Rep7Table& T) {
 
 // Tables are built once per signature and kept (immutable after insertion).
 static bool rep7_table(uint32_t neg, Rep7Table& T) {
-    static std::mutex mu;
-    static std::map<unsigned, std::pair<bool, Rep7Table>> cache;
-    std::lock_guard<std::mutex> lock(mu);
-    auto it = cache.find(neg);
-    if (it == cache.end()) {
-        Rep7Table t{};
-        const bool ok = rep7_table_build(neg, t);
-        it = cache.emplace(neg, std::make_pair(ok, t)).first;
-    }
-    if (it->second.first) T = it->second.second;
-    return it->second.first;
+    static TableCache<Rep7Table, 128> cache;
+    return cache.get((int)(neg & 0x7fu), T, [&](Rep7Table& t) { return rep7_table_build(neg & 0x7fu, t); });
 }
 
 bool rep7_applicable(uint32_t neg) {

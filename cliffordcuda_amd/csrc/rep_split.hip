@@ -525,17 +525,8 @@ static bool split_table_build(uint32_t neg9, SplitTable& T) {
 }
 
 static bool split_table(uint32_t neg9, SplitTable& T) {
-    static std::mutex mu;
-    static std::map<unsigned, std::pair<bool, SplitTable>> cache;
-    std::lock_guard<std::mutex> lock(mu);
-    auto it = cache.find(neg9);
-    if (it == cache.end()) {
-        SplitTable t{};
-        const bool ok = split_table_build(neg9, t);
-        it = cache.emplace(neg9, std::make_pair(ok, t)).first;
-    }
-    if (it->second.first) T = it->second.second;
-    return it->second.first;
+    static TableCache<SplitTable, 512> cache;
+    return cache.get((int)(neg9 & 0x1ffu), T, [&](SplitTable& t) { return split_table_build(neg9 & 0x1ffu, t); });
 }
 
 // n = 9 without null generators, or n = 10 whose only null generator is e_9
@@ -580,10 +571,7 @@ static int launch_pairs(const SplitTable& T, const PairSpec* ps, int npairs, lon
 
 // n = 10: one launch per direction and gradient reads each operand half once
 // (CLF_SPLIT_PATH=pairs runs the separate pair-sum launches instead).
-static bool split_fused_enabled() {
-    const char* e = std::getenv("CLF_SPLIT_PATH");
-    return !(e && std::strcmp(e, "pairs") == 0);
-}
+static bool split_fused_enabled() { return !options().split_pairs; }
 
 template <int KIND>
 static void launch_fused(const SplitTable& T, const float* X, const float* Y, float* out, int64_t batch,

@@ -243,8 +243,7 @@ bool spin_tables(RepTable& T, SpinTable& S) {
 // Environment override CLF_ROTOR_PATH=chain keeps n = 8 on the register chain.
 bool rotor16_enabled(int n) {
     if (n != kSpinN) return false;
-    const char* e = std::getenv("CLF_ROTOR_PATH");
-    if (e && std::strcmp(e, "chain") == 0) return false;
+    if (options().rotor_chain) return false;
     RepTable T;
     SpinTable S;
     return spin_tables(T, S);

@@ -70,6 +70,11 @@ int clf_abi_version(void);
 /* Text of the last error on the calling thread ("" if none). Never NULL. */
 const char* clf_last_error(void);
 
+/* Re-read the CLF_* path switches from the environment. The library reads
+ * them once, at its first launch; this lets a test or benchmark switch paths
+ * inside one process. No counterpart in the reference (it has no such switches). */
+void clf_options_reload(void);
+
 /* Device properties used for launch shaping and the roofline report.
  * Replaces the reference's shared-memory probe
  * (src/cliffordcuda/extensions/ga/geom_prod_tiled.py:88-117,

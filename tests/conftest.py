@@ -21,3 +21,32 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+class ClfEnv:
+    """Sets or clears CLF_* path switches for one test and makes the library
+    re-read them (it reads them once per process otherwise)."""
+
+    def __init__(self, mp):
+        self._mp = mp
+
+    def setenv(self, name, value):
+        from cliffordcuda_amd import _lib
+        self._mp.setenv(name, value)
+        _lib.reload_options()
+
+    def delenv(self, name, raising=True):
+        from cliffordcuda_amd import _lib
+        self._mp.delenv(name, raising=raising)
+        _lib.reload_options()
+
+
+@pytest.fixture
+def clf_env(monkeypatch):
+    env = ClfEnv(monkeypatch)
+    yield env
+    monkeypatch.undo()
+    from cliffordcuda_amd import _lib
+    if _lib._lib is not None:
+        _lib.reload_options()
+

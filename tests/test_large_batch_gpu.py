@@ -27,7 +27,7 @@ def _rows(B):
 
 
 @pytest.mark.parametrize("metric,op,path", CASES, ids=lambda v: str(v))
-def test_rows_past_2_31_floats(metric, op, path, monkeypatch):
+def test_rows_past_2_31_floats(metric, op, path, clf_env):
     n = len(metric)
     D = 1 << n
     B = (1 << (31 - n)) + 3
@@ -35,7 +35,7 @@ def test_rows_past_2_31_floats(metric, op, path, monkeypatch):
     if free < 7 * B * D * 4 + (4 << 30):
         pytest.skip("needs about 56 GiB of free device memory")
     if path is not None:
-        monkeypatch.setenv("CLF_GEOM_PATH", path)
+        clf_env.setenv("CLF_GEOM_PATH", path)
     print(f"[case] large batch metric={metric} op={op} path={path} B={B}", flush=True)
     cl = cc.CliffordAlgebra(metric, device="cuda")
     fn = getattr(cl, op)

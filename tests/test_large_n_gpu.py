@@ -23,9 +23,9 @@ def rel_err(got, ref):
     return float((got - ref).abs().max()) / (den if den > 0 else 1.0)
 
 
-def run(op, metric, a, b, gc, monkeypatch, path=None):
+def run(op, metric, a, b, gc, clf_env, path=None):
     if path:
-        monkeypatch.setenv("CLF_PRODUCT_PATH", path)
+        clf_env.setenv("CLF_PRODUCT_PATH", path)
     try:
         x = a.clone().requires_grad_()
         y = b.clone().requires_grad_()
@@ -34,7 +34,7 @@ def run(op, metric, a, b, gc, monkeypatch, path=None):
         torch.cuda.synchronize()
     finally:
         if path:
-            monkeypatch.delenv("CLF_PRODUCT_PATH")
+            clf_env.delenv("CLF_PRODUCT_PATH")
     return c.detach(), x.grad, y.grad
 
 
@@ -49,12 +49,12 @@ def compare(r1, r2):
 
 @pytest.mark.parametrize("metric", [(1,) * 12, (-1,) * 4 + (1, -1, 0, 1, 1, -1, 0, 1)], ids=["E12", "mixed12"])
 @pytest.mark.parametrize("op", O.OPS)
-def test_tiled_equals_whole_row_n12(op, metric, monkeypatch):
+def test_tiled_equals_whole_row_n12(op, metric, clf_env):
     if op == "regressive" and 0 in metric:
         pytest.skip("regressive is undefined for degenerate metrics")
     a, b, gc = inputs(12, 3, 12)
     print(f"[case] n=12 op={op} metric={metric}", flush=True)
-    e = compare(run(op, metric, a, b, gc, monkeypatch), run(op, metric, a, b, gc, monkeypatch, "tiled"))
+    e = compare(run(op, metric, a, b, gc, clf_env), run(op, metric, a, b, gc, clf_env, "tiled"))
     assert max(e) <= TOL, e
 
 
@@ -86,22 +86,22 @@ def test_n11_matches_oracle(op, metric):
 
 
 @pytest.mark.parametrize("op", O.OPS)
-def test_tiled_equals_generic_n14(op, monkeypatch):
+def test_tiled_equals_generic_n14(op, clf_env):
     metric = (1,) * 11 + (-1, -1, 1) if op == "regressive" else (1,) * 11 + (-1, -1, 0)
     a, b, gc = inputs(14, 2, 14)
     print(f"[case] n=14 op={op}", flush=True)
-    e = compare(run(op, metric, a, b, gc, monkeypatch), run(op, metric, a, b, gc, monkeypatch, "generic"))
+    e = compare(run(op, metric, a, b, gc, clf_env), run(op, metric, a, b, gc, clf_env, "generic"))
     assert max(e) <= TOL, e
 
 
 @pytest.mark.parametrize("op", ["geom", "lc"])
-def test_tiled_equals_generic_n16(op, monkeypatch):
+def test_tiled_equals_generic_n16(op, clf_env):
     """n = 16 (65536 components), Cl(13,2,1) as in the reference's largest
     gradient case."""
     metric = (1,) * 13 + (-1, -1, 0)
     a, b, gc = inputs(16, 1, 16)
     print(f"[case] n=16 op={op}", flush=True)
-    e = compare(run(op, metric, a, b, gc, monkeypatch), run(op, metric, a, b, gc, monkeypatch, "generic"))
+    e = compare(run(op, metric, a, b, gc, clf_env), run(op, metric, a, b, gc, clf_env, "generic"))
     assert max(e) <= TOL, e
 
 
@@ -118,19 +118,19 @@ def test_tiled_geom_matches_oracle_n13():
 
 @pytest.mark.parametrize("op", ["geom", "lc", "wedge"])
 @pytest.mark.parametrize("metric", [(1,) * 15 + (-1, 0), (1, -1) * 8 + (1,)], ids=["blocked17", "mixed17"])
-def test_n17_matches_oracle_sample_and_generic(op, metric, monkeypatch):
+def test_n17_matches_oracle_sample_and_generic(op, metric, clf_env):
     """n = 17 (131072 components, the reference's test_inverse.py:64 size):
     the default kernels (tiled for the blocked metric, per-coefficient for the
     mixed one) against the oracle on sampled output coefficients, and the
     tiled forward and backward against the per-coefficient kernels in full."""
     a, b, gc = inputs(17, 2, 17)
     print(f"[case] n=17 op={op} metric={metric}", flush=True)
-    res = run(op, metric, a, b, gc, monkeypatch)
+    res = run(op, metric, a, b, gc, clf_env)
     ks = [0, 1, 5, 777, 65536, 131071]
     ref = O.product_coefficients(op, a.double().cpu(), b.double().cpu(), metric, ks)
     assert rel_err(res[0][:, ks], ref) <= TOL
     if metric[:4] == (1, 1, 1, 1):
-        e = compare(res, run(op, metric, a, b, gc, monkeypatch, "generic"))
+        e = compare(res, run(op, metric, a, b, gc, clf_env, "generic"))
         assert max(e) <= TOL, e
     assert all(torch.isfinite(t).all() for t in res)
 

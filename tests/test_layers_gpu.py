@@ -74,7 +74,7 @@ def test_weight_on_left(op):
     assert rel_err(wd.grad, w64.grad) <= TOL
 
 
-def test_c3_full_batch_vs_per_row_kernels(monkeypatch):
+def test_c3_full_batch_vs_per_row_kernels(clf_env):
     """GeometricProductLayer Cl(8,0), x (262144, 256) ~ N(0,1),
     w ~ N(0, 1/16). Three independent HIP algorithms agree at the full batch,
     values and both gradients: the matrix-representation layer kernels (the
@@ -98,13 +98,13 @@ def test_c3_full_batch_vs_per_row_kernels(monkeypatch):
         return y.detach(), xd.grad, layer.weight.grad.clone()
 
     y, gx, gw = run_layer()
-    monkeypatch.setenv("CLF_GEOM_PATH", "direct")
+    clf_env.setenv("CLF_GEOM_PATH", "direct")
     y1, gx1, gw1 = run_layer()
     x2 = x.cuda().requires_grad_()
     w2 = w.cuda().requires_grad_()
     y2 = cc.geom_prod(x2, w2.expand(B, 256).contiguous())
     y2.sum().backward()
-    monkeypatch.delenv("CLF_GEOM_PATH")
+    clf_env.delenv("CLF_GEOM_PATH")
     for a, b, c in ((y, y1, y2), (gx, gx1, x2.grad), (gw, gw1, w2.grad)):
         assert rel_err(a, b) <= TOL
         assert rel_err(b, c) <= TOL

@@ -224,7 +224,7 @@ def test_matrix_path_geom_parity(metric):
     assert max(e) <= TOL, e
 
 
-def test_matrix_path_equals_direct_path_full_batch(monkeypatch):
+def test_matrix_path_equals_direct_path_full_batch(clf_env):
     """Headline shape: the matrix-representation kernels and the per-term
     kernels (an independent algorithm, forced with CLF_GEOM_PATH=direct) agree
     at batch 262144, values and both gradients."""
@@ -242,9 +242,9 @@ def test_matrix_path_equals_direct_path_full_batch(monkeypatch):
         return c.detach(), x.grad, y.grad
 
     c1, ga1, gb1 = run()
-    monkeypatch.setenv("CLF_GEOM_PATH", "direct")
+    clf_env.setenv("CLF_GEOM_PATH", "direct")
     c2, ga2, gb2 = run()
-    monkeypatch.delenv("CLF_GEOM_PATH")
+    clf_env.delenv("CLF_GEOM_PATH")
     for u, v in ((c1, c2), (ga1, ga2), (gb1, gb2)):
         assert rel_err(u, v) <= TOL
 
@@ -263,7 +263,7 @@ def test_split_path_geom_parity(metric, batch):
     assert max(e) <= TOL, e
 
 
-def test_split_path_equals_direct_path_c5_full_batch(monkeypatch):
+def test_split_path_equals_direct_path_c5_full_batch(clf_env):
     """C5 shape (Cl(9,0,1), batch 16384): the split-representation kernels and
     the per-term kernels agree on the whole batch, values and both gradients."""
     metric = (1,) * 9 + (0,)
@@ -281,9 +281,9 @@ def test_split_path_equals_direct_path_c5_full_batch(monkeypatch):
         return c.detach(), x.grad, y.grad
 
     r1 = run()
-    monkeypatch.setenv("CLF_GEOM_PATH", "direct")
+    clf_env.setenv("CLF_GEOM_PATH", "direct")
     r2 = run()
-    monkeypatch.delenv("CLF_GEOM_PATH")
+    clf_env.delenv("CLF_GEOM_PATH")
     for u, v in zip(r1, r2):
         assert rel_err(u, v) <= TOL
 
@@ -308,7 +308,7 @@ def _grads(op, a, b, gc, metric, need_a=True, need_b=True):
 
 @pytest.mark.parametrize("metric", BAL_METRICS, ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
 @pytest.mark.parametrize("op", O.OPS)
-def test_balanced_kernels_match_blocked_and_oracle(op, metric, monkeypatch):
+def test_balanced_kernels_match_blocked_and_oracle(op, metric, clf_env):
     """The balanced kernels (default for the masked products at 4 <= n <= 10,
     forced for geom) give the one-lane-per-output kernels' results on batches
     that end inside a row group, for both gradients and each one alone; small
@@ -320,13 +320,13 @@ def test_balanced_kernels_match_blocked_and_oracle(op, metric, monkeypatch):
     for batch in (1, R + 3, 4 * 64 * R + 5):
         a, b, gc = (t.cuda() for t in seeded(batch, n, batch + n, 3))
         print(f"[case] balanced op={op} metric={metric} batch={batch}", flush=True)
-        monkeypatch.setenv("CLF_PRODUCT_PATH", "balanced")
+        clf_env.setenv("CLF_PRODUCT_PATH", "balanced")
         c, ga, gb = _grads(op, a, b, gc, metric)
         _, ga1, _ = _grads(op, a, b, gc, metric, need_b=False)
         _, _, gb1 = _grads(op, a, b, gc, metric, need_a=False)
-        monkeypatch.setenv("CLF_PRODUCT_PATH", "blocked")
+        clf_env.setenv("CLF_PRODUCT_PATH", "blocked")
         c0, ga0, gb0 = _grads(op, a, b, gc, metric)
-        monkeypatch.delenv("CLF_PRODUCT_PATH")
+        clf_env.delenv("CLF_PRODUCT_PATH")
         assert rel_err(c, c0) <= TOL and rel_err(ga, ga0) <= TOL and rel_err(gb, gb0) <= TOL
         assert torch.equal(ga1, ga) and torch.equal(gb1, gb)
         if batch <= 64:
@@ -338,7 +338,7 @@ def test_balanced_kernels_match_blocked_and_oracle(op, metric, monkeypatch):
 
 @pytest.mark.parametrize("metric", [m for m in SPLIT_TYPE if len(m) == 10],
                          ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
-def test_split_fused_matches_pair_sums(metric, monkeypatch):
+def test_split_fused_matches_pair_sums(metric, clf_env):
     """n = 10 with a null e_9: the fused kernels (one launch per direction and
     gradient) equal the separate pair-sum launches, on batches with a partial
     two-row group, for both gradients and each one alone."""
@@ -348,9 +348,9 @@ def test_split_fused_matches_pair_sums(metric, monkeypatch):
         c, ga, gb = _grads("geom", a, b, gc, metric)
         _, ga1, _ = _grads("geom", a, b, gc, metric, need_b=False)
         _, _, gb1 = _grads("geom", a, b, gc, metric, need_a=False)
-        monkeypatch.setenv("CLF_SPLIT_PATH", "pairs")
+        clf_env.setenv("CLF_SPLIT_PATH", "pairs")
         c0, ga0, gb0 = _grads("geom", a, b, gc, metric)
-        monkeypatch.delenv("CLF_SPLIT_PATH")
+        clf_env.delenv("CLF_SPLIT_PATH")
         assert rel_err(c, c0) <= TOL and rel_err(ga, ga0) <= TOL and rel_err(gb, gb0) <= TOL
         assert torch.equal(ga1, ga) and torch.equal(gb1, gb)
 
@@ -370,7 +370,7 @@ def test_n7_matrix_path_geom_parity(metric, batch):
 
 
 @pytest.mark.parametrize("metric", [(1,) * 6 + (-1,), (1,) * 7], ids=["C2", "+++++++"])
-def test_n7_matrix_path_equals_direct_path(metric, monkeypatch):
+def test_n7_matrix_path_equals_direct_path(metric, clf_env):
     """C2 shape (batch 65536) and a ragged batch: the n = 7 representation
     kernels give the per-term kernels' values and gradients (an independent
     algorithm, CLF_GEOM_PATH=direct), also with one gradient requested; the
@@ -381,9 +381,9 @@ def test_n7_matrix_path_equals_direct_path(metric, monkeypatch):
         c, ga, gb = _grads("geom", a, b, gc, metric)
         _, ga1, _ = _grads("geom", a, b, gc, metric, need_b=False)
         _, _, gb1 = _grads("geom", a, b, gc, metric, need_a=False)
-        monkeypatch.setenv("CLF_GEOM_PATH", "direct")
+        clf_env.setenv("CLF_GEOM_PATH", "direct")
         c0, ga0, gb0 = _grads("geom", a, b, gc, metric)
-        monkeypatch.delenv("CLF_GEOM_PATH")
+        clf_env.delenv("CLF_GEOM_PATH")
         assert rel_err(c, c0) <= TOL and rel_err(ga, ga0) <= TOL and rel_err(gb, gb0) <= TOL
         assert torch.equal(ga1, ga) and torch.equal(gb1, gb)
         assert not torch.equal(c, c0)

@@ -264,7 +264,7 @@ def _rotor_step(cl, biv, x, gy, need_biv=True, need_x=True):
 
 
 @pytest.mark.parametrize("B", [1, 3, 16, 27, 1000, 40001])
-def test_rotor8_matrix_path_matches_chain_and_oracle(B, monkeypatch):
+def test_rotor8_matrix_path_matches_chain_and_oracle(B, clf_env):
     """n = 8 runs through the Cl(8,0) representation by default; the register
     chain (CLF_ROTOR_PATH=chain) and the oracle give the same values and
     gradients, for batches that leave partial row groups (rows past the end
@@ -279,9 +279,9 @@ def test_rotor8_matrix_path_matches_chain_and_oracle(B, monkeypatch):
     ym, gbm, gxm = _rotor_step(cl, biv, x, gy)
     _, gb_only, _ = _rotor_step(cl, biv, x, gy, need_x=False)
     _, _, gx_only = _rotor_step(cl, biv, x, gy, need_biv=False)
-    monkeypatch.setenv("CLF_ROTOR_PATH", "chain")
+    clf_env.setenv("CLF_ROTOR_PATH", "chain")
     yc, gbc, gxc = _rotor_step(cl, biv, x, gy)
-    monkeypatch.delenv("CLF_ROTOR_PATH")
+    clf_env.delenv("CLF_ROTOR_PATH")
     assert rel_err(ym, yc) <= TOL
     assert rel_err(gxm, gxc) <= TOL
     assert rel_err(gbm, gbc) <= TOL
