@@ -175,6 +175,22 @@ __device__ __forceinline__ void unconvert16(float (&w)[16], float* __restrict__ 
         row[ent[z] & 0xffffu] = __uint_as_float(__float_as_uint(w[z] * 0.0625f) ^ (ent[z] & 0x80000000u));
 }
 
+// the same for a W that already carries the factor 1/16
+__device__ __forceinline__ void unconvert16_prescaled(float (&w)[16], float* __restrict__ row,
+                                                      const unsigned (&ent)[16]) {
+    wht_inplace<16>(w);
+#pragma unroll
+    for (int z = 0; z < 16; ++z)
+        row[ent[z] & 0xffffu] = __uint_as_float(__float_as_uint(w[z]) ^ (ent[z] & 0x80000000u));
+}
+
+// LDS accesses at byte addresses computed by the kernel (xor-swizzled layouts
+// whose addresses are one xor away from a per-lane base)
+typedef __attribute__((address_space(3))) float lds_f32;
+__device__ __forceinline__ unsigned lds_byte_addr(float* p) { return (unsigned)(uintptr_t)(lds_f32*)p; }
+__device__ __forceinline__ float lds_load(unsigned a) { return *(lds_f32*)(uintptr_t)a; }
+__device__ __forceinline__ void lds_store(unsigned a, float v) { *(lds_f32*)(uintptr_t)a = v; }
+
 // 16 x 16 x 16 product: operand k of A (B) is xor16<k>(a[k]) if SA (SB), else
 // a[k] as given (already shuffled)
 template <bool SA, bool SB, unsigned... K>

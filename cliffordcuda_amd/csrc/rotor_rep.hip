@@ -45,25 +45,40 @@ __device__ __forceinline__ void load_spin_operand(const float* __restrict__ U, u
 // phi(y) = V^T phi(x) V with V = U (forward, TRANS = false) or V = U^T (the
 // transpose of the action). vop[k] = V[k][x] is both the B operand of
 // phi(x) V and the A operand of V^T (phi(x) V).
+//
+// Memory pipeline (both rotor16 kernels). A wave's global loads and stores
+// share one completion counter, and the compiler waits for all of them before
+// the staged rows are used, so a group's results are stored from their own LDS
+// slot halfway through the next group's work, not at the end of their own:
+// when the wave next waits, those stores have had half a group's time to
+// complete. The wave index is made wave-uniform (readfirstlane), so the row
+// bookkeeping runs on the scalar unit and the row clamps need no branches.
+constexpr int kApplyWaveFloats = kRelayoutFloats + 4 * 256;  // staged x, then the relayout | the previous group's y
+
 template <bool TRANS, bool NT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void rotor16_apply_kernel(
     const float* __restrict__ U, const float* __restrict__ X, float* __restrict__ Y, long long batch, RepTable T) {
-    // per wave: staged x rows (1024 floats); later the relayout (1280), then y rows
-    __shared__ float lds[4][kRelayoutFloats];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __shared__ float lds[4][kApplyWaveFloats];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const unsigned x = lane & 15u;
     const int rb = lane >> 4;
     float* sx = &lds[wave][0];
+    float* su = sx + kRelayoutFloats;
     const unsigned oddx = (rb & 1) ? T.odd_xor : 0u, oddc = T.odd_xor >> 2;
     unsigned ent[16];
 #pragma unroll
     for (int z = 0; z < 16; ++z) ent[z] = T.e[x * 16 + z] ^ oddx;
     float vop[16];
     load_spin_operand<TRANS>(U, x, vop);
+    // V / 4 on both sides: phi(y) comes out with the 1/16 of the inverse
+    // conversion already applied (exact: a power of two)
+#pragma unroll
+    for (int k = 0; k < 16; ++k) vop[k] *= 0.25f;
     const floatx16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 
     const long long stride = (long long)gridDim.x * 4 * 4;
-    long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
+    const long long rfirst = ((long long)blockIdx.x * 4 + wave) * 4;
+    long long row0 = rfirst;
     Pre16 px = fetch16<NT>(X, row0, batch, lane);
     for (; row0 < batch; row0 += stride) {
         // the table values are re-derived where they are used rather than kept
@@ -81,102 +96,114 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
         float pop[16];
         transpose_blocks(p, pop);
         const floatx16 acc = mfma_chain_pre<false, false>(zero, vop, pop, std::make_integer_sequence<unsigned, 16>{});
+        if (row0 != rfirst) store16<NT>(Y, su, row0 - stride, batch, lane, oddc);  // uniform
         relayout_store(sx, acc, lane);
         wave_lds_sync();
         float wc[16];
         relayout_load(sx, rb, x, wc);
-        wave_lds_sync();
-        unconvert16(wc, sx + rb * 256, ent);
-        wave_lds_sync();
-        store16<NT>(Y, sx, row0, batch, lane, oddc);
+        unconvert16_prescaled(wc, su + rb * 256, ent);
         wave_lds_sync();
     }
+    if (row0 != rfirst) store16<NT>(Y, su, row0 - stride, batch, lane, oddc);
 }
 
 // gx = Lambda(Q)^T gy (if GX) and the workgroup's partial K (C(8,2) floats at
-// gamma_ws[blockIdx.x * 28]). uop[k] = U[x][k] is the B operand of
-// phi(gy) U^T and the A operand of U (phi(gy) U^T). The steps are ordered so
-// that few operand sets are live at once (phi(gy), then the two products,
-// then phi(x)^T, then phi(x)); the scheduling barriers keep the compiler from
-// hoisting the later gathers, which would cost occupancy.
-constexpr int kRotorBwdWaveFloats = 4 * 256 + kRelayoutFloats;  // staged x | staged gy, then the relayout
+// gamma_ws[blockIdx.x * 28]). uop[k] = U[x][k] / 4 is the B operand of
+// phi(gy) U^T and the A operand of U (phi(gy) U^T), so phi(gx) comes out with
+// the 1/16 of the inverse conversion already applied (exact: a power of two).
+//
+// The kernel is issue-bound: on gfx950 the fp32 MFMA chains and the VALU work
+// of the conversions do not overlap, so the design removes VALU work.
+// phi(x) is converted once: its W rows are written to LDS transposed (block
+// rb, element (r, c) at float 256 rb + 16 (c ^ rb) + r), and both statistic
+// products read their A operands from there, one ds_read per operand with a
+// loop-invariant address: operand K of phi(x)^T (product phi(x)^T phi(gx)) is
+// W_x[l ^ K][l], because the transposed conversion of x is W_x with its
+// columns xor-ed by the lane's row (W_xt[c] = W_x[c ^ x]); operand K of
+// phi(x) (product phi(x) phi(gx)^T) is W_x[l ^ K][K]. Both patterns, and the
+// transposed writes, hit 64 distinct banks per instruction. This replaces the
+// second conversion of x (gather, signs, WHT) and 32 DPP shuffles.
+// staged x, then W_x^T | staged gy, then the relayout | the previous group's gx
+constexpr int kRotorBwdWaveFloats = 4 * 256 + kRelayoutFloats + 4 * 256;
 
-template <bool NT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void rotor16_bwd_kernel(const float* __restrict__ U, const float* __restrict__ X,
-                                                           const float* __restrict__ GY, float* __restrict__ GX,
-                                                           float* __restrict__ gamma_ws, long long batch, RepTable T,
-                                                           SpinTable S) {
-    // per wave: staged x rows [0, 1024), staged gy rows [1024, 2048); the
-    // relayout of phi(gx) reuses the gy slot [1024, 2304) once gy is gathered;
-    // the gx rows reuse the x slot once x is gathered
-    __shared__ float lds[4][kRotorBwdWaveFloats];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+template <bool NT, bool WGX>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void rotor16_bwd_kernel(
+    const float* __restrict__ U, const float* __restrict__ X, const float* __restrict__ GY, float* __restrict__ GX,
+    float* __restrict__ gamma_ws, long long batch, RepTable T, SpinTable S) {
+    // the W_x^T address forms below need the wave slots 1024-byte aligned
+    static_assert((kRotorBwdWaveFloats * 4) % 1024 == 0, "wave slots stay 1024-byte aligned");
+    __shared__ __attribute__((aligned(1024))) float lds[4][kRotorBwdWaveFloats];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const unsigned x = lane & 15u;
     const int rb = lane >> 4;
     float* sx = &lds[wave][0];
     float* sg = sx + 4 * 256;
+    float* su = sg + kRelayoutFloats;
     const unsigned oddx = (rb & 1) ? T.odd_xor : 0u, oddc = T.odd_xor >> 2;
     unsigned ent[16];
 #pragma unroll
     for (int z = 0; z < 16; ++z) ent[z] = T.e[x * 16 + z] ^ oddx;
     float uop[16];
-    load_spin_operand<true>(U, x, uop);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) uop[k] = 0.25f * U[x * 16 + k];
+    // byte addresses in the W_x^T layout: element (r, c) of block rb at
+    // xb + 1024 rb + 64 (c ^ rb) + 4 r; the xor forms need xb 1024-aligned
+    const unsigned xb = lds_byte_addr(sx);
+    const unsigned wbase = xb + 1024u * rb + 64u * rb + 4u * x;                // element (x ^ .., ..) writes
+    const unsigned tbase = xb + 1024u * rb + 64u * (x ^ (unsigned)rb) + 4u * x;  // element (x ^ K, x)
     const floatx16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     floatx16 accm = zero;
 
     const long long stride = (long long)gridDim.x * 4 * 4;
-    long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
+    const long long rfirst = ((long long)blockIdx.x * 4 + wave) * 4;
+    long long row0 = rfirst;
     Pre16 px = fetch16<NT>(X, row0, batch, lane);
     Pre16 pg = fetch16<NT>(GY, row0, batch, lane);
     for (; row0 < batch; row0 += stride) {
-#pragma unroll
-        for (int z = 0; z < 16; ++z) asm volatile("" : "+v"(ent[z]));  // as in rotor16_apply_kernel
         stage16(sx, px, lane, oddc);
         stage16(sg, pg, lane, oddc);
         px = fetch16<NT>(X, row0 + stride, batch, lane);
         pg = fetch16<NT>(GY, row0 + stride, batch, lane);
         wave_lds_sync();
-        // a block whose row is past the end (a clamped copy of the last row)
-        // adds nothing to the sums: its phi(x) operands are zeroed
-        const bool keep = row0 + rb < batch;
-        float wg[16];
+        float wg[16], wx[16];
         gather16<0>(sg + rb * 256, ent, wg);
+        gather16<0>(sx + rb * 256, ent, wx);
         wave_lds_sync();
         wht_inplace<16>(wg);
-        // phi(gx) = U (phi(gy) U^T)
+        // phi(gx) / 16 = (U / 4) (phi(gy) (U / 4)^T)
         const floatx16 p = mfma_chain_pre<true, false>(zero, wg, uop, std::make_integer_sequence<unsigned, 16>{});
+        wht_inplace<16>(wx);
+        if (row0 + 3 >= batch) {  // uniform; a block whose row is past the end (a clamped copy) adds nothing
+            const bool keep = row0 + rb < batch;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) wx[k] = keep ? wx[k] : 0.f;
+        }
+#pragma unroll
+        for (int c = 0; c < 16; ++c) lds_store(wbase ^ (64u * c), wx[c]);
+        wave_lds_sync();
+        float at[16], an[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) at[k] = lds_load(tbase ^ (4u * k));
+#pragma unroll
+        for (int k = 0; k < 16; ++k) an[k] = lds_load(wbase ^ (68u * k));
         float pop[16];
         transpose_blocks(p, pop);
         const floatx16 g = mfma_chain_pre<false, false>(zero, uop, pop, std::make_integer_sequence<unsigned, 16>{});
+        if (WGX && row0 != rfirst) store16<NT>(GX, su, row0 - stride, batch, lane, oddc);  // uniform
         relayout_store(sg, g, lane);
-        __builtin_amdgcn_sched_barrier(0);
         // phi(x)^T phi(gx): B operand phi(gx)[k][j] from the block transpose
         float gop[16];
         transpose_blocks(g, gop);
-        float wxt[16];
-        gather16<1>(sx + rb * 256, ent, wxt);
-        wht_inplace<16>(wxt);
-#pragma unroll
-        for (int k = 0; k < 16; ++k) wxt[k] = keep ? wxt[k] : 0.f;
-        accm = mfma_chain_pre<true, false>(accm, wxt, gop, std::make_integer_sequence<unsigned, 16>{});
-        __builtin_amdgcn_sched_barrier(0);
-        // phi(x) phi(gx)^T: B operand phi(gx)[j][k] = W_gx[j ^ k][k] after the relayout
-        float wx[16];
-        gather16<0>(sx + rb * 256, ent, wx);
+        accm = mfma_chain_pre<false, false>(accm, at, gop, std::make_integer_sequence<unsigned, 16>{});
         wave_lds_sync();
+        // phi(x) phi(gx)^T: B operand phi(gx)[j][k] = W_gx[j ^ k][k] after the relayout
         float wgx[16];
         relayout_load(sg, rb, x, wgx);
-        wht_inplace<16>(wx);
-#pragma unroll
-        for (int k = 0; k < 16; ++k) wx[k] = keep ? wx[k] : 0.f;
-        accm = mfma_chain_pre<true, true>(accm, wx, wgx, std::make_integer_sequence<unsigned, 16>{});
-        if (GX) {  // uniform: a kernel argument
-            unconvert16(wgx, sx + rb * 256, ent);
-            wave_lds_sync();
-            store16<NT>(GX, sx, row0, batch, lane, oddc);
-        }
+        accm = mfma_chain_pre<false, true>(accm, an, wgx, std::make_integer_sequence<unsigned, 16>{});
+        if (WGX) unconvert16_prescaled(wgx, su + rb * 256, ent);
         wave_lds_sync();
     }
+    if (WGX && row0 != rfirst) store16<NT>(GX, su, row0 - stride, batch, lane, oddc);
     // M = sum of the four blocks and four waves; lane (g, j) holds M[4g + t][j] in m[t]
     __syncthreads();
     float* red = &lds[0][0];
@@ -200,7 +227,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void r
             const float v = red[1024 + r * 16 + (r ^ px)];
             acc += ((mask >> r) & 1u) ? -v : v;
         }
-        gamma_ws[(long long)blockIdx.x * kSpinPlanes + tid] = acc * (-1.f / 32.f);
+        gamma_ws[(long long)blockIdx.x * kSpinPlanes + tid] = acc * (-16.f / 32.f);  // phi(gx) carries 1/16
     }
 }
 
@@ -280,7 +307,8 @@ int rotor16_apply(bool fwd, const float* U, const float* x, float* y, int64_t ba
 // the resident ones (the kernel is persistent). The gamma finalize reads this
 // many partials.
 unsigned rotor16_bwd_grid(long long wanted) {
-    return resident_grid((const void*)rotor16_bwd_kernel<false>, 256, 0, wanted);
+    // every instantiation has the same register and LDS footprint
+    return resident_grid((const void*)rotor16_bwd_kernel<false, true>, 256, 0, wanted);
 }
 
 // grid = the number of partials the gamma finalize reads (<= the workspace bound)
@@ -290,12 +318,18 @@ int rotor16_bwd(const float* U, const float* x, const float* gy, float* gx, floa
     SpinTable S;
     if (!spin_tables(T, S)) return set_error(CLF_ERR_UNSUPPORTED, "Cl(8,0) representation tables unavailable");
     hipStream_t s = (hipStream_t)stream;
-    if (stream_nt((2 + (gx != nullptr)) * 1024.0 * (double)batch))
-        hipLaunchKernelGGL(rotor16_bwd_kernel<true>, dim3(grid), dim3(256), 0, s, U, x, gy, gx, gamma_ws,
-                           (long long)batch, T, S);
-    else
-        hipLaunchKernelGGL(rotor16_bwd_kernel<false>, dim3(grid), dim3(256), 0, s, U, x, gy, gx, gamma_ws,
-                           (long long)batch, T, S);
+    const bool nt = stream_nt((2 + (gx != nullptr)) * 1024.0 * (double)batch);
+#define CLF_ROTOR16_BWD(NT, WGX)                                                                                 \
+    hipLaunchKernelGGL((rotor16_bwd_kernel<NT, WGX>), dim3(grid), dim3(256), 0, s, U, x, gy, gx, gamma_ws,       \
+                       (long long)batch, T, S)
+    if (gx) {
+        if (nt) CLF_ROTOR16_BWD(true, true);
+        else CLF_ROTOR16_BWD(false, true);
+    } else {
+        if (nt) CLF_ROTOR16_BWD(true, false);
+        else CLF_ROTOR16_BWD(false, false);
+    }
+#undef CLF_ROTOR16_BWD
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }
