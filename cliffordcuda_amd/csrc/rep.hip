@@ -330,12 +330,21 @@ __global__ __launch_bounds__(256) void rep_bwd_kernel(const float* __restrict__ 
 // back through LDS as W_c[i ^ j][j] at row stride 20 floats, which keeps both
 // the scattered b32 writes and the b128 row reads free of bank conflicts.
 
+// Memory pipeline. A wave's global loads and stores share one completion
+// counter and the compiler waits for all of them before staged rows are used,
+// so results are not stored at the end of their own group (the next group's
+// wait would take the whole store latency) but from their LDS slot right after
+// the next wait: they then have a full group's time to complete. The wave index
+// is wave-uniform (readfirstlane), so the row bookkeeping and the clamps run on
+// the scalar unit.
 template <bool NT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void rep16_fwd_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, long long batch, RepTable T) {
-    __shared__ float lds[4][2 * 4 * 256];  // per wave: staged a | staged b; later the relayout, then c
+    // per wave: staged a | staged b; later the relayout (over a and the start
+    // of b), then c in the b slot until the next group's stores
+    __shared__ float lds[4][2 * 4 * 256];
     static_assert(2 * 4 * 256 >= kRelayoutFloats, "relayout must fit the wave's LDS slots");
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const unsigned x = lane & 15u;
     const int rb = lane >> 4;
     float* sa = &lds[wave][0];
@@ -346,7 +355,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
     for (int z = 0; z < 16; ++z) ent[z] = T.e[x * 16 + z] ^ oddx;
 
     const long long stride = (long long)gridDim.x * 4 * 4;
-    long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
+    const long long rfirst = ((long long)blockIdx.x * 4 + wave) * 4;
+    long long row0 = rfirst;
     Pre16 pa = fetch16<NT>(A, row0, batch, lane);
     Pre16 pb = fetch16<NT>(B, row0, batch, lane);
     for (; row0 < batch; row0 += stride) {
@@ -355,6 +365,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
 #pragma unroll
         for (int z = 0; z < 16; ++z) asm volatile("" : "+v"(ent[z]));
         stage16(sa, pa, lane, oddc);
+        if (row0 != rfirst) {  // uniform: the previous group's c leaves its slot before b is staged there
+            wave_lds_sync();
+            store16<NT>(C, sb, row0 - stride, batch, lane, oddc);
+            wave_lds_sync();
+        }
         stage16(sb, pb, lane, oddc);
         pa = fetch16<NT>(A, row0 + stride, batch, lane);
         wave_lds_sync();
@@ -373,21 +388,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
         float wc[16];
         relayout_load(sa, rb, x, wc);
         wave_lds_sync();
-        unconvert16(wc, sa + rb * 256, ent);
-        wave_lds_sync();
-        store16<NT>(C, sa, row0, batch, lane, oddc);
+        unconvert16(wc, sb + rb * 256, ent);
         wave_lds_sync();
     }
+    if (row0 != rfirst) store16<NT>(C, sb, row0 - stride, batch, lane, oddc);
 }
 
-template <bool NT>
+// GA and GB are compile-time flags (a gradient that is not wanted has no
+// branch around its stores). dA of a group is stored right after the group's
+// second wait, dB right after the next group's first wait.
+template <bool NT, bool WA, bool WB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void rep16_bwd_kernel(
     const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ GC, float* __restrict__ GA,
     float* __restrict__ GB, long long batch, RepTable T) {
     // per wave: gc | b, then a over b | scratch for each gradient's relayout and
     // its rows in blade order; only two converted operands are live at a time
     __shared__ float lds[4][2 * 4 * 256 + kRelayoutFloats];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const unsigned x = lane & 15u;
     const int rb = lane >> 4;
     float* s0 = &lds[wave][0];
@@ -397,10 +414,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void r
     unsigned ent[16];
 #pragma unroll
     for (int z = 0; z < 16; ++z) ent[z] = T.e[x * 16 + z] ^ oddx;
-    const bool want_a = GA != nullptr, want_b = GB != nullptr;
 
     const long long stride = (long long)gridDim.x * 4 * 4;
-    long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
+    const long long rfirst = ((long long)blockIdx.x * 4 + wave) * 4;
+    long long row0 = rfirst;
     // gc and b of a group are loaded while the previous group's dB runs, a
     // while the group's dA runs
     Pre16 pb = fetch16<NT>(B, row0, batch, lane);
@@ -414,8 +431,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void r
         stage16(s0, pg, lane, oddc);
         stage16(s1, pb, lane, oddc);
         const Pre16 pa = fetch16<NT>(A, row0, batch, lane);
+        if (WB && row0 != rfirst) store16<NT>(GB, sr, row0 - stride, batch, lane, oddc);  // uniform
         wave_lds_sync();
-        if (want_a) {
+        if (WA) {
             float wg[16], wb[16];
             gather16<0>(s0 + rb * 256, ent, wg);
             gather16<0>(s1 + rb * 256, ent, wb);
@@ -428,15 +446,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void r
             relayout_load(sr, rb, x, da);
             wave_lds_sync();
             unconvert16(da, sr + rb * 256, ent);
-            wave_lds_sync();
-            store16<NT>(GA, sr, row0, batch, lane, oddc);
         }
         wave_lds_sync();
         stage16(s1, pa, lane, oddc);
         pg = fetch16<NT>(GC, row0 + stride, batch, lane);
         pb = fetch16<NT>(B, row0 + stride, batch, lane);
+        if (WA) store16<NT>(GA, sr, row0, batch, lane, oddc);
         wave_lds_sync();
-        if (want_b) {
+        if (WB) {
             float wat[16], wgt[16];
             gather16<1>(s1 + rb * 256, ent, wat);
             gather16<1>(s0 + rb * 256, ent, wgt);
@@ -449,11 +466,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void r
             relayout_load(sr, rb, x, db);
             wave_lds_sync();
             unconvert16(db, sr + rb * 256, ent);
-            wave_lds_sync();
-            store16<NT>(GB, sr, row0, batch, lane, oddc);
         }
         wave_lds_sync();
     }
+    if (WB && row0 != rfirst) store16<NT>(GB, sr, row0 - stride, batch, lane, oddc);
 }
 
 // ---- broadcast weight (the product layers), m = 16 --------------------------
@@ -791,12 +807,24 @@ int rep_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc
         case 6: hipLaunchKernelGGL((rep_bwd_kernel<3>), CLF_REP_GRID(rep_bwd_kernel<3>), dim3(256), 0, s, a, b, gc, ga,
                                    gb, (long long)batch, T); break;
         case 8:
-            if (stream_nt((3 + (ga != nullptr) + (gb != nullptr)) * 1024.0 * (double)batch))
-                hipLaunchKernelGGL(rep16_bwd_kernel<true>, dim3((unsigned)want), dim3(256), 0, s, a, b, gc, ga, gb,
-                                   (long long)batch, T);
-            else
-                hipLaunchKernelGGL(rep16_bwd_kernel<false>, dim3((unsigned)want), dim3(256), 0, s, a, b, gc, ga, gb,
-                                   (long long)batch, T);
+            if (!ga && !gb) break;
+            {
+                const bool nt = stream_nt((3 + (ga != nullptr) + (gb != nullptr)) * 1024.0 * (double)batch);
+#define CLF_REP16_BWD(NT, WA, WB)                                                                                 \
+    hipLaunchKernelGGL((rep16_bwd_kernel<NT, WA, WB>), dim3((unsigned)want), dim3(256), 0, s, a, b, gc, ga, gb,   \
+                       (long long)batch, T)
+                if (ga && gb) {
+                    if (nt) CLF_REP16_BWD(true, true, true);
+                    else CLF_REP16_BWD(false, true, true);
+                } else if (ga) {
+                    if (nt) CLF_REP16_BWD(true, true, false);
+                    else CLF_REP16_BWD(false, true, false);
+                } else {
+                    if (nt) CLF_REP16_BWD(true, false, true);
+                    else CLF_REP16_BWD(false, false, true);
+                }
+#undef CLF_REP16_BWD
+            }
             break;
         default: return set_error(CLF_ERR_UNSUPPORTED, "matrix path supports n = 4, 6, 8");
     }

@@ -193,13 +193,20 @@ __device__ __forceinline__ void product_q7(float* __restrict__ rel, const float 
     lane_q7<D>(wc, sm, q);
 }
 
+// Memory pipeline (both n = 7 kernels): a wave's loads and stores share one
+// completion counter and the compiler waits for all of them before staged rows
+// are used, so each group's results stay in an LDS slot and are stored right
+// after the next group's wait, with a full group's time to complete. The wave
+// index is wave-uniform, so the row bookkeeping runs on the scalar unit.
 template <bool PAIR, bool NT>
 __global__ __launch_bounds__(256) void rep7_fwd_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                         float* __restrict__ C, long long batch, Rep7Table T) {
     constexpr int D = PAIR ? 2 : 3;
-    __shared__ float lds[4][kRelayoutFloats];  // per wave: staged a | b, later the relayout, then c
+    // per wave: staged a | b, later the relayout (over both), then c in the b
+    // slot until the next group's stores
+    __shared__ float lds[4][kRelayoutFloats];
     static_assert(2 * kRep7GroupFloats <= kRelayoutFloats, "staging must fit the wave's LDS slots");
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const unsigned x = lane & 15u;
     const int rb = lane >> 4;
     float* sa = &lds[wave][0];
@@ -209,11 +216,17 @@ __global__ __launch_bounds__(256) void rep7_fwd_kernel(const float* __restrict__
     lane_consts7<D>(T, x, rb, ent, sm);
 
     const long long stride = (long long)gridDim.x * 16;
-    long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
+    const long long rfirst = ((long long)blockIdx.x * 4 + wave) * 4;
+    long long row0 = rfirst;
     Pre7 pa = fetch7<NT>(A, row0, batch, lane);
     Pre7 pb = fetch7<NT>(B, row0, batch, lane);
     for (; row0 < batch; row0 += stride) {
         stage7(sa, pa, lane, oddc);
+        if (row0 != rfirst) {  // uniform: the previous group's c leaves the b slot first
+            wave_lds_sync();
+            store7<NT>(C, sb, row0 - stride, batch, lane, oddc);
+            wave_lds_sync();
+        }
         stage7(sb, pb, lane, oddc);
         pa = fetch7<NT>(A, row0 + stride, batch, lane);
         pb = fetch7<NT>(B, row0 + stride, batch, lane);
@@ -226,7 +239,7 @@ __global__ __launch_bounds__(256) void rep7_fwd_kernel(const float* __restrict__
             float q[4], qh[4];
             product_q7<2>(sa, ta, tb, sm, lane, rb, x, q);
             product_q7<2>(sa, tah, tbh, sm, lane, rb, x, qh);
-            scatter7_pair(sa + rb * kRep7Dim, ent, q, qh);
+            scatter7_pair(sb + rb * kRep7Dim, ent, q, qh);
         } else {
             float ta[8], tb[8];
             gather7_single<0>(sa + rb * kRep7Dim, ent, ta);
@@ -234,12 +247,11 @@ __global__ __launch_bounds__(256) void rep7_fwd_kernel(const float* __restrict__
             wave_lds_sync();
             float q[8];
             product_q7<3>(sa, ta, tb, sm, lane, rb, x, q);
-            scatter7_single(sa + rb * kRep7Dim, ent, q);
+            scatter7_single(sb + rb * kRep7Dim, ent, q);
         }
         wave_lds_sync();
-        store7<NT>(C, sa, row0, batch, lane, oddc);
-        wave_lds_sync();
     }
+    if (row0 != rfirst) store7<NT>(C, sb, row0 - stride, batch, lane, oddc);
 }
 
 // Backward: ga from (gc, b) with gc in the s(I) convention and b in s(I);
@@ -247,14 +259,14 @@ __global__ __launch_bounds__(256) void rep7_fwd_kernel(const float* __restrict__
 // after the other: gc and b are staged first (a is loaded meanwhile), then a
 // over b, and each gradient's relayout and rows in blade order use a scratch
 // slot, so few converted operands are live at once.
-template <bool PAIR, bool NT>
+template <bool PAIR, bool NT, bool WA, bool WB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void rep7_bwd_kernel(
     const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ GC, float* __restrict__ GA,
     float* __restrict__ GB, long long batch, Rep7Table T) {
     constexpr int D = PAIR ? 2 : 3;
     constexpr int L = 1 << D;
     __shared__ float lds[4][2 * kRep7GroupFloats + kRelayoutFloats];  // per wave: gc | b, then a | scratch
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const unsigned x = lane & 15u;
     const int rb = lane >> 4;
     float* sg = &lds[wave][0];
@@ -263,10 +275,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
     const unsigned oddc = T.odd_xor >> 2;
     unsigned ent[8], sm[16 >> D];
     lane_consts7<D>(T, x, rb, ent, sm);
-    const bool want_a = GA != nullptr, want_b = GB != nullptr;
 
     const long long stride = (long long)gridDim.x * 16;
-    long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
+    const long long rfirst = ((long long)blockIdx.x * 4 + wave) * 4;
+    long long row0 = rfirst;
     Pre7 pb = fetch7<NT>(B, row0, batch, lane);
     Pre7 pg = fetch7<NT>(GC, row0, batch, lane);
     for (; row0 < batch; row0 += stride) {
@@ -277,8 +289,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
         stage7(sg, pg, lane, oddc);
         stage7(sx, pb, lane, oddc);
         const Pre7 pa = fetch7<NT>(A, row0, batch, lane);
+        // the previous group's gb leaves the scratch slot (stored after this wait)
+        if (WB && row0 != rfirst) store7<NT>(GB, sr, row0 - stride, batch, lane, oddc);  // uniform
         wave_lds_sync();
-        if (want_a) {
+        if (WA) {
             float q[L];
             if constexpr (PAIR) {
                 float tg[4], tgh[4], tb[4], tbh[4], qh[4];
@@ -294,15 +308,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
                 product_q7<3>(sr, tg, tb, sm, lane, rb, x, q);
                 scatter7_single(sr + rb * kRep7Dim, ent, q);
             }
-            wave_lds_sync();
-            store7<NT>(GA, sr, row0, batch, lane, oddc);
         }
         wave_lds_sync();
         stage7(sx, pa, lane, oddc);
         pg = fetch7<NT>(GC, row0 + stride, batch, lane);
         pb = fetch7<NT>(B, row0 + stride, batch, lane);
+        if (WA) store7<NT>(GA, sr, row0, batch, lane, oddc);  // after this group's second wait
         wave_lds_sync();
-        if (want_b) {
+        if (WB) {
             float q[L];
             if constexpr (PAIR) {
                 float tat[4], tath[4], tgt[4], tgth[4], qh[4];
@@ -318,11 +331,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
                 product_q7<3>(sr, tat, tgt, sm, lane, rb, x, q);
                 scatter7_single(sr + rb * kRep7Dim, ent, q);
             }
-            wave_lds_sync();
-            store7<NT>(GB, sr, row0, batch, lane, oddc);
         }
         wave_lds_sync();
     }
+    if (WB && row0 != rfirst) store7<NT>(GB, sr, row0 - stride, batch, lane, oddc);
 }
 
 // ---- host side --------------------------------------------------------------
@@ -512,21 +524,24 @@ int rep7_bwd(uint32_t neg, const float* a, const float* b, const float* gc, floa
     hipStream_t s = (hipStream_t)stream;
     const dim3 g(rep7_grid(batch));
     const bool nt = stream_nt((3 + (ga != nullptr) + (gb != nullptr)) * 512.0 * (double)batch);
+    if (!ga && !gb) return CLF_OK;
+#define CLF_REP7_BWD(P, NT, WA, WB) \
+    hipLaunchKernelGGL((rep7_bwd_kernel<P, NT, WA, WB>), g, dim3(256), 0, s, a, b, gc, ga, gb, (long long)batch, T)
+#define CLF_REP7_BWD_W(P, NT)                 \
+    do {                                      \
+        if (ga && gb) CLF_REP7_BWD(P, NT, true, true);   \
+        else if (ga) CLF_REP7_BWD(P, NT, true, false);   \
+        else CLF_REP7_BWD(P, NT, false, true);           \
+    } while (0)
     if (pair) {
-        if (nt)
-            hipLaunchKernelGGL((rep7_bwd_kernel<true, true>), g, dim3(256), 0, s, a, b, gc, ga, gb, (long long)batch,
-                               T);
-        else
-            hipLaunchKernelGGL((rep7_bwd_kernel<true, false>), g, dim3(256), 0, s, a, b, gc, ga, gb, (long long)batch,
-                               T);
+        if (nt) CLF_REP7_BWD_W(true, true);
+        else CLF_REP7_BWD_W(true, false);
     } else {
-        if (nt)
-            hipLaunchKernelGGL((rep7_bwd_kernel<false, true>), g, dim3(256), 0, s, a, b, gc, ga, gb, (long long)batch,
-                               T);
-        else
-            hipLaunchKernelGGL((rep7_bwd_kernel<false, false>), g, dim3(256), 0, s, a, b, gc, ga, gb,
-                               (long long)batch, T);
+        if (nt) CLF_REP7_BWD_W(false, true);
+        else CLF_REP7_BWD_W(false, false);
     }
+#undef CLF_REP7_BWD_W
+#undef CLF_REP7_BWD
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }
