@@ -50,8 +50,11 @@ __device__ __forceinline__ float flip(float x, unsigned m) { return __uint_as_fl
 // XOR swizzle of the float4 slot inside a 64-byte block
 __device__ __forceinline__ unsigned swz(unsigned blk) { return ((blk >> 1) ^ (blk >> 3)) & 3u; }
 
-__device__ __forceinline__ void load_blk(const float4* __restrict__ base, unsigned blk, float (&v)[16]) {
-    const unsigned s = swz(blk);
+// rs: the staged row's extra slot skew (balanced kernels: rows that share a
+// quarter-wave read the same blocks at the same step, so their slots differ)
+__device__ __forceinline__ void load_blk(const float4* __restrict__ base, unsigned blk, float (&v)[16],
+                                         unsigned rs = 0u) {
+    const unsigned s = swz(blk) ^ rs;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const float4 t = base[(blk << 2) + ((unsigned)q ^ s)];
@@ -63,8 +66,9 @@ __device__ __forceinline__ void load_blk(const float4* __restrict__ base, unsign
 }
 
 // reversed element order: v[y] = block[15 - y]
-__device__ __forceinline__ void load_blk_rev(const float4* __restrict__ base, unsigned blk, float (&v)[16]) {
-    const unsigned s = swz(blk);
+__device__ __forceinline__ void load_blk_rev(const float4* __restrict__ base, unsigned blk, float (&v)[16],
+                                             unsigned rs = 0u) {
+    const unsigned s = swz(blk) ^ rs;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const float4 t = base[(blk << 2) + ((unsigned)q ^ s)];
@@ -677,7 +681,7 @@ template <int OP, int ROLE, int CLS, bool LOWNEG>
 __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __restrict__ la,
                                          const float4* __restrict__ lb, const float4* __restrict__ lg,
                                          float4* __restrict__ heads, unsigned lr, float4* __restrict__ out,
-                                         unsigned NB, const BlkParams& P) {
+                                         unsigned NB, const BlkParams& P, unsigned rs) {
     const unsigned full = NB - 1u;
     constexpr bool kRev = OP == OP_REGR && ROLE == 0;
     constexpr int VAR = bal_variant<OP, CLS>();
@@ -705,8 +709,8 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
             const HiSign hr = hi_sign<OP>(part ^ o, part, P.negh, P.nulh, full, P.nm1, P.mu);
             {
                 float av[16], bv[16];
-                load_blk(la, part, av);
-                load_blk(lb, part ^ o, bv);
+                load_blk(la, part, av, rs);
+                load_blk(lb, part ^ o, bv, rs);
                 const unsigned m = hl.valid ? hl.mask : 0u;
                 apply_flips(bv, m, m ^ (cross_pi<OP>(part, P.nm1) << 31));
                 if (hl.valid) {
@@ -717,8 +721,8 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
             }
             if (hr.valid) {
                 float av[16], bv[16];
-                load_blk(la, part ^ o, av);
-                load_blk(lb, part, bv);
+                load_blk(la, part ^ o, av, rs);
+                load_blk(lb, part, bv, rs);
                 apply_flips(bv, hr.mask, hr.mask ^ (cross_pi<OP>(part ^ o, P.nm1) << 31));
                 lowblock_fwd<LV_RC, kLowNeg>(acc, av, bv);
             }
@@ -727,8 +731,8 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
             const HiSign hs = hi_sign<OP>(ih, jh, P.negh, P.nulh, full, P.nm1, P.mu);
             if (hs.valid) {
                 float av[16], bv[16];
-                load_blk(la, ih, av);
-                load_blk(lb, jh, bv);
+                load_blk(la, ih, av, rs);
+                load_blk(lb, jh, bv, rs);
                 apply_flips(bv, hs.mask, hs.mask ^ (cross_pi<OP>(ih, P.nm1) << 31));
                 if (OP == OP_INNER) lowblock_fwd<VAR, kLowNeg>(acc, av, bv);
                 else fwd_block_dispatch<OP, LOWNEG>(acc, av, bv, ih, jh);
@@ -739,11 +743,11 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
                                         : hi_sign<OP>(m, h, P.negh, P.nulh, full, P.nm1, P.mu);
             if (hs.valid) {
                 float g[16];
-                if (OP == OP_REGR) load_blk_rev(lg, full ^ x, g);
-                else load_blk(lg, x, g);
+                if (OP == OP_REGR) load_blk_rev(lg, full ^ x, g, rs);
+                else load_blk(lg, x, g, rs);
                 if (ROLE == 1) {
                     float bv[16];
-                    load_blk(lb, m, bv);
+                    load_blk(lb, m, bv, rs);
                     apply_flips(bv, hs.mask, hs.mask ^ (cross_pi<OP>(h, P.nm1) << 31));
                     if (OP == OP_INNER && CLS == 4)  // ih = h, jh = m
                         lowblock_ga_split<kLowNeg>(acc, bv, (h & ~m) == 0u, (m & ~h) == 0u, g);
@@ -752,7 +756,7 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
                 } else {
                     const unsigned pm = cross_pi<OP>(m, P.nm1) << 31;
                     float av[16], gt[16];
-                    load_blk(la, m, av);
+                    load_blk(la, m, av, rs);
                     apply_flips(av, hs.mask, hs.mask ^ pm);
 #pragma unroll
                     for (int e = 0; e < 16; ++e) gt[e] = (cpopc((unsigned)e) & 1) ? flip(g[e], pm) : g[e];
@@ -811,6 +815,136 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
     }
 }
 
+// ---- table-driven rounds (wedge, lc, rc, regressive) ----------------------
+// The schedule of a role is the same for every row, so its per-pair
+// bookkeeping (the family walk, the high-part sign, segment ends) is done once
+// per workgroup into a table in LDS: one 16-bit entry per (step, lane of the
+// row). The round over a row then reads an entry, loads two blocks, applies
+// two sign masks and runs the op's low pattern; it carries no family state.
+//   bits 0-5   partner block P (role 0: ih; role 1: jh; role 2: ih)
+//   bits 6-11  output block O (role 0: ih ^ jh; roles 1 and 2: the gradient's block)
+//   bit 12     high-part sign (1: negative)
+//   bit 13     compute (the pair's high blocks are related; else the pair adds nothing)
+//   bits 14-15 after this step: 0 continue, 1 write the head slot, 2 store the output
+// A lane with no pair at a step has the entry 0 (nothing to compute or store).
+constexpr unsigned kTabSign = 1u << 12, kTabCompute = 1u << 13;
+constexpr int kTabActShift = 14;
+constexpr int kBalTMax = 12;  // steps: at most ceil(3^nh / 2^nh) = 12 pairs per lane (nh <= 6)
+constexpr int kBalTabEntries = kBalTMax * 64;
+
+template <int OP, int ROLE>
+__device__ __forceinline__ void bal_build_tab(const BalSched& sc, unsigned lr, unsigned NB, const BlkParams& P,
+                                              unsigned short* __restrict__ tab) {
+    const unsigned full = NB - 1u;
+    unsigned o = sc.o0;
+    BalFam f = bal_family<OP, ROLE, 0>(o, full, P.nulh);
+    int s = sc.s0;
+    unsigned S = deposit_bits((unsigned)(f.first + s), f.mask);
+    bool first = true;
+    int p = sc.p0;
+    for (int t = 0; t < sc.T; ++t) {
+        unsigned e = 0u;
+        if (p < sc.p1) {
+            const unsigned part = f.base | S;
+            const HiSign hs = ROLE == 0   ? hi_sign<OP>(part, part ^ o, P.negh, P.nulh, full, P.nm1, P.mu)
+                              : ROLE == 1 ? hi_sign<OP>(o, part, P.negh, P.nulh, full, P.nm1, P.mu)
+                                          : hi_sign<OP>(part, o, P.negh, P.nulh, full, P.nm1, P.mu);
+            e = part | (o << 6) | (hs.valid ? kTabCompute : 0u) | (hs.mask ? kTabSign : 0u);
+            ++p;
+            ++s;
+            S = (S - f.mask) & f.mask;
+            const bool done = s == f.count;
+            if (done || p == sc.p1) {
+                if (first && sc.cont0) e |= 1u << kTabActShift;
+                else if (done) e |= 2u << kTabActShift;
+                if (done) {
+                    first = false;
+                    do {
+                        ++o;
+                        if (o >= NB) break;
+                        f = bal_family<OP, ROLE, 0>(o, full, P.nulh);
+                    } while (f.count == 0);
+                    s = 0;
+                    S = deposit_bits((unsigned)f.first, f.mask);
+                }
+            }
+        }
+        tab[t * NB + lr] = (unsigned short)e;
+    }
+}
+
+// One role over one row from its table (see bal_role for the arguments).
+template <int OP, int ROLE, bool LOWNEG>
+__device__ __forceinline__ void bal_role_tab(const BalSched& sc, const unsigned short* __restrict__ tab,
+                                             const float4* __restrict__ la, const float4* __restrict__ lb,
+                                             const float4* __restrict__ lg, float4* __restrict__ heads, unsigned lr,
+                                             float4* __restrict__ out, unsigned NB, const BlkParams& P, unsigned rs) {
+    const unsigned full = NB - 1u;
+    constexpr bool kRev = OP == OP_REGR && ROLE == 0;
+    float acc[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+    for (int t = 0; t < sc.T; ++t) {
+        const unsigned e = tab[t * NB + lr];
+        const unsigned pb = e & 63u, ob = (e >> 6) & 63u;
+        if (e & kTabCompute) {
+            const unsigned sm = (e & kTabSign) << 19;  // bit 12 -> the float sign bit
+            if (ROLE == 0) {  // ih = pb, jh = pb ^ ob
+                float av[16], bv[16];
+                load_blk(la, pb, av, rs);
+                load_blk(lb, pb ^ ob, bv, rs);
+                apply_flips(bv, sm, sm ^ (cross_pi<OP>(pb, P.nm1) << 31));
+                fwd_block_dispatch<OP, LOWNEG>(acc, av, bv, pb, pb ^ ob);
+            } else {
+                const unsigned x = ob ^ pb;
+                float g[16];
+                if (OP == OP_REGR) load_blk_rev(lg, full ^ x, g, rs);
+                else load_blk(lg, x, g, rs);
+                if (ROLE == 1) {  // h = ob, m = pb
+                    float bv[16];
+                    load_blk(lb, pb, bv, rs);
+                    apply_flips(bv, sm, sm ^ (cross_pi<OP>(ob, P.nm1) << 31));
+                    ga_block_dispatch<OP, LOWNEG>(acc, bv, g, ob, pb);
+                } else {  // h = ob (jh), m = pb (ih)
+                    const unsigned pm = cross_pi<OP>(pb, P.nm1) << 31;
+                    float av[16], gt[16];
+                    load_blk(la, pb, av, rs);
+                    apply_flips(av, sm, sm ^ pm);
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) gt[k] = (cpopc((unsigned)k) & 1) ? flip(g[k], pm) : g[k];
+                    gb_block_dispatch<OP, LOWNEG>(acc, av, gt, pb, ob);
+                }
+            }
+        }
+        const unsigned act = e >> kTabActShift;
+        if (act == 1u) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                heads[lr * 4 + q] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+        } else if (act == 2u && out) {
+            store_blk(out, kRev ? (full ^ ob) : ob, acc, kRev);
+        }
+        if (act != 0u) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) acc[k] = 0.f;
+        }
+    }
+    wave_lds_sync();
+    if (sc.tail) {
+        for (int l = (int)lr + 1; l <= sc.last_lane; ++l) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 v = heads[l * 4 + q];
+                acc[4 * q] += v.x;
+                acc[4 * q + 1] += v.y;
+                acc[4 * q + 2] += v.z;
+                acc[4 * q + 3] += v.w;
+            }
+        }
+        if (out) store_blk(out, kRev ? (full ^ sc.olast) : sc.olast, acc, kRev);
+    }
+}
+
 // A group's operand: float4 chunk lane + 64 i (i < 4) of R consecutive rows,
 // rows past the end clamped to the last row.
 struct BalPre {
@@ -831,7 +965,8 @@ __device__ __forceinline__ BalPre bal_fetch(const float* __restrict__ src, long 
     return p;
 }
 
-// staged like stage_rows: row r at r * D4, float4 slots swizzled inside a block
+// staged like stage_rows: row r at r * D4, float4 slots swizzled inside a block,
+// with the row's skew (r & 3) xor-ed into the slot
 __device__ __forceinline__ void bal_stage(float4* __restrict__ dst, const BalPre& p, int n, int lane) {
     const int d4_log = n - 2;
 #pragma unroll
@@ -840,7 +975,7 @@ __device__ __forceinline__ void bal_stage(float4* __restrict__ dst, const BalPre
         const int r = c >> d4_log;
         const unsigned f = (unsigned)c & ((1u << d4_log) - 1u);
         const unsigned blk = f >> 2, q = f & 3u;
-        dst[(r << d4_log) + (int)((blk << 2) + (q ^ swz(blk)))] = p.v[i];
+        dst[(r << d4_log) + (int)((blk << 2) + (q ^ swz(blk) ^ ((unsigned)r & 3u)))] = p.v[i];
     }
 }
 
@@ -862,7 +997,15 @@ __global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A,
     float4* sb = sa + kBalGroupF4;
     float4* heads = sb + kBalGroupF4 + (r << lpr_log) * 4;
     const int roff = r << (n - 2);
+    const unsigned rs = (unsigned)r & 3u;  // the row's slot skew
     const BalSched sc = bal_schedule<OP, 0, kCls>(lr, NB, P.nulh);
+    // wedge, lc, rc and regressive run from the role's schedule table
+    constexpr bool kTab = OP != OP_INNER && OP != OP_GEOM;
+    __shared__ unsigned short tab[kTab ? kBalTabEntries : 1];
+    if (kTab) {
+        if (wave == 0 && lane < (int)NB) bal_build_tab<OP, 0>(sc, lr, NB, P, tab);
+        __syncthreads();
+    }
     const long long ngrp = (P.batch + R - 1) / R;
     const long long gstride = (long long)gridDim.x * 4;
     long long grp = (long long)blockIdx.x * 4 + wave;
@@ -876,7 +1019,8 @@ __global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A,
         wave_lds_sync();
         const long long row = grp * R + r;
         float4* out = row < P.batch ? reinterpret_cast<float4*>(C) + (row << (n - 2)) : nullptr;
-        bal_role<OP, 0, kCls, LOWNEG>(sc, sa + roff, sb + roff, nullptr, heads, lr, out, NB, P);
+        if constexpr (kTab) bal_role_tab<OP, 0, LOWNEG>(sc, tab, sa + roff, sb + roff, nullptr, heads, lr, out, NB, P, rs);
+        else bal_role<OP, 0, kCls, LOWNEG>(sc, sa + roff, sb + roff, nullptr, heads, lr, out, NB, P, rs);
         wave_lds_sync();
     }
 }
@@ -903,10 +1047,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     float4* sb = sa + kBalGroupF4;
     float4* sg = sb + kBalGroupF4;
     const int roff = r << (n - 2);
+    const unsigned rs = (unsigned)r & 3u;  // the row's slot skew
     const int hoff = (r << lpr_log) * 4;
     const bool want_a = GA != nullptr, want_b = GB != nullptr;
     const BalSched sca = bal_schedule<OP, 1, kCls>(lr, NB, P.nulh);
     const BalSched scb = bal_schedule<OP, 2, kCls>(lr, NB, P.nulh);
+    // wedge, lc, rc and regressive run from the roles' schedule tables
+    constexpr bool kTab = OP != OP_INNER && OP != OP_GEOM;
+    __shared__ unsigned short tab[2][kTab ? kBalTabEntries : 1];
+    if (kTab) {
+        if (wave == 0 && lane < (int)NB) {
+            bal_build_tab<OP, 1>(sca, lr, NB, P, tab[0]);
+            bal_build_tab<OP, 2>(scb, lr, NB, P, tab[1]);
+        }
+        __syncthreads();
+    }
     const long long ngrp = (P.batch + R - 1) / R;
     const long long gstride = (long long)gridDim.x * 4;
     long long grp = (long long)blockIdx.x * 4 + wave;
@@ -924,7 +1079,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
             pb = bal_fetch(B, grp + gstride, P.batch, n, lane);
             wave_lds_sync();
             float4* out = row_ok ? reinterpret_cast<float4*>(GA) + (row << (n - 2)) : nullptr;
-            bal_role<OP, 1, kCls, LOWNEG>(sca, nullptr, sb + roff, sg + roff, sa + hoff, lr, out, NB, P);
+            if constexpr (kTab) bal_role_tab<OP, 1, LOWNEG>(sca, tab[0], nullptr, sb + roff, sg + roff, sa + hoff, lr, out, NB, P, rs);
+            else bal_role<OP, 1, kCls, LOWNEG>(sca, nullptr, sb + roff, sg + roff, sa + hoff, lr, out, NB, P, rs);
             wave_lds_sync();
         }
         if (want_b) {
@@ -932,7 +1088,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
             pa = bal_fetch(A, grp + gstride, P.batch, n, lane);
             wave_lds_sync();
             float4* out = row_ok ? reinterpret_cast<float4*>(GB) + (row << (n - 2)) : nullptr;
-            bal_role<OP, 2, kCls, LOWNEG>(scb, sa + roff, nullptr, sg + roff, sb + hoff, lr, out, NB, P);
+            if constexpr (kTab) bal_role_tab<OP, 2, LOWNEG>(scb, tab[1], sa + roff, nullptr, sg + roff, sb + hoff, lr, out, NB, P, rs);
+            else bal_role<OP, 2, kCls, LOWNEG>(scb, sa + roff, nullptr, sg + roff, sb + hoff, lr, out, NB, P, rs);
         }
         wave_lds_sync();
     }
