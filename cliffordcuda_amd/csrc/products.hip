@@ -65,6 +65,18 @@ __device__ __forceinline__ void load_blk(const float4* __restrict__ base, unsign
     }
 }
 
+// a block stored by store_blk (no swizzle): the inner product's partial slot
+__device__ __forceinline__ void load_blk_plain(const float4* __restrict__ base, unsigned blk, float (&v)[16]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 t = base[(blk << 2) + q];
+        v[4 * q + 0] = t.x;
+        v[4 * q + 1] = t.y;
+        v[4 * q + 2] = t.z;
+        v[4 * q + 3] = t.w;
+    }
+}
+
 // reversed element order: v[y] = block[15 - y]
 __device__ __forceinline__ void load_blk_rev(const float4* __restrict__ base, unsigned blk, float (&v)[16],
                                              unsigned rs = 0u) {
@@ -415,6 +427,68 @@ __global__ __launch_bounds__(256) void prod_fwd_blk(const float* __restrict__ A,
     }
 }
 
+// The inner product's backward for one output block h (one lane per output):
+// its partner blocks are walked by relation class, so the lanes of a wave run
+// the same low pattern at every step: the strict supersets m of h (ga pairs
+// (h, m) in the lc relation, gb pairs (m, h) in the rc relation), the strict
+// subsets (the other way round), then m = h (both patterns). A lane whose
+// class has fewer partners than another lane's idles for the difference; the
+// wave stops a class when no lane has partners left.
+template <int CLASS, bool LOWNEG>
+__device__ __forceinline__ void inner_pair(const float4* __restrict__ la, const float4* __restrict__ lb,
+                                           const float4* __restrict__ lg, unsigned h, unsigned m, unsigned fullh,
+                                           bool do_a, bool do_b, float (&ga)[16], float (&gb)[16],
+                                           const BlkParams& P) {
+    // CLASS 0: m strict superset of h; 1: strict subset; 2: m = h
+    constexpr int VA = CLASS == 0 ? LV_LC : CLASS == 1 ? LV_RC : LV_INNER;
+    constexpr int VB = CLASS == 0 ? LV_RC : CLASS == 1 ? LV_LC : LV_INNER;
+    const HiSign sa = hi_sign<OP_INNER>(h, m, P.negh, P.nulh, fullh, P.nm1, P.mu);
+    const HiSign sb = hi_sign<OP_INNER>(m, h, P.negh, P.nulh, fullh, P.nm1, P.mu);
+    do_a = do_a && sa.valid;
+    do_b = do_b && sb.valid;
+    if (!do_a && !do_b) return;
+    float g[16];
+    load_blk(lg, h ^ m, g);
+    if (do_a) {
+        float bv[16];
+        load_blk(lb, m, bv);
+        apply_flips(bv, sa.mask, sa.mask ^ (cross_pi<OP_INNER>(h, P.nm1) << 31));
+        lowblock_ga<VA, LOWNEG>(ga, bv, g);
+    }
+    if (do_b) {
+        const unsigned pm = cross_pi<OP_INNER>(m, P.nm1) << 31;
+        float av[16], gt[16];
+        load_blk(la, m, av);
+        apply_flips(av, sb.mask, sb.mask ^ pm);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) gt[e] = (cpopc((unsigned)e) & 1) ? flip(g[e], pm) : g[e];
+        lowblock_gb<VB, LOWNEG>(gb, av, gt);
+    }
+}
+
+template <bool LOWNEG>
+__device__ __forceinline__ void inner_bwd_blocks(const float4* __restrict__ la, const float4* __restrict__ lb,
+                                                 const float4* __restrict__ lg, unsigned h, unsigned fullh,
+                                                 bool want_a, bool want_b, float (&ga)[16], float (&gb)[16],
+                                                 const BlkParams& P) {
+    const unsigned co = fullh & ~h;
+    // strict supersets m = h | S, S a nonempty subset of co, in increasing order
+    const int nsup = (1 << __popc(co)) - 1;
+    unsigned S = 0u;
+    for (int k = 0; __any(k < nsup); ++k) {
+        S = (S - co) & co;
+        inner_pair<0, LOWNEG>(la, lb, lg, h, h | S, fullh, want_a && k < nsup, want_b && k < nsup, ga, gb, P);
+    }
+    // strict subsets m of h (the empty set first)
+    const int nsub = (1 << __popc(h)) - 1;
+    unsigned T = 0u;
+    for (int k = 0; __any(k < nsub); ++k) {
+        inner_pair<1, LOWNEG>(la, lb, lg, h, T, fullh, want_a && k < nsub, want_b && k < nsub, ga, gb, P);
+        T = (T - h) & h;
+    }
+    inner_pair<2, LOWNEG>(la, lb, lg, h, h, fullh, want_a, want_b, ga, gb, P);
+}
+
 template <int OP, bool LOWNEG>
 __global__ __launch_bounds__(256) void prod_bwd_blk(const float* __restrict__ A, const float* __restrict__ B,
                                                      const float* __restrict__ GC, float* __restrict__ GA,
@@ -446,6 +520,9 @@ __global__ __launch_bounds__(256) void prod_bwd_blk(const float* __restrict__ A,
             ga[e] = 0.f;
             gb[e] = 0.f;
         }
+        if constexpr (OP == OP_INNER) {
+            inner_bwd_blocks<LOWNEG>(la, lb, lg, h, fullh, want_a, want_b, ga, gb, P);
+        } else
         for (unsigned m = 0; m < NB; ++m) {
             const unsigned x = h ^ m;
             const HiSign sa = hi_sign<OP>(h, m, P.negh, P.nulh, fullh, P.nm1, P.mu);  // (i, j) = (h, m)
@@ -563,6 +640,12 @@ __device__ __forceinline__ BalFam bal_family(unsigned o, unsigned full, unsigned
     // inner, fused forward round: output o, partners S (ih = S, jh = S | o for the
     // lc half, ih = S | o, jh = S for the rc half)
     if (CLS == 3) return BalFam{0u, con, 0, ncon};
+    // inner, backward in two deals: deal A (class 5) takes the partners on the
+    // far side of the output (role 1: jh = o | S, lc relation; role 2:
+    // ih = o | S, rc relation), deal B (class 6) those on the near side
+    // (S inside o, the other relation), both with the pair ih = jh
+    if (CLS == 5) return BalFam{o, co, 0, onul ? 0 : nco};
+    if (CLS == 6) return BalFam{0u, onn, 0, nonn};
     // inner, backward round: all partners of an output, the lc side (with the
     // pair ih = jh) first, then the rc side
     if (CLS == 4) {
@@ -832,12 +915,16 @@ constexpr int kTabActShift = 14;
 constexpr int kBalTMax = 12;  // steps: at most ceil(3^nh / 2^nh) = 12 pairs per lane (nh <= 6)
 constexpr int kBalTabEntries = kBalTMax * 64;
 
-template <int OP, int ROLE>
+// The lane's tail (its last segment continues in later lanes) is packed in a
+// header word: bit 0 tail, bits 1-6 the last lane holding pairs of that
+// output, bits 7-12 the output.
+template <int OP, int ROLE, int CLS = 0>
 __device__ __forceinline__ void bal_build_tab(const BalSched& sc, unsigned lr, unsigned NB, const BlkParams& P,
-                                              unsigned short* __restrict__ tab) {
+                                              unsigned short* __restrict__ tab, unsigned* __restrict__ hdr) {
     const unsigned full = NB - 1u;
+    hdr[lr] = (sc.tail ? 1u : 0u) | ((unsigned)sc.last_lane << 1) | (sc.olast << 7);
     unsigned o = sc.o0;
-    BalFam f = bal_family<OP, ROLE, 0>(o, full, P.nulh);
+    BalFam f = bal_family<OP, ROLE, CLS>(o, full, P.nulh);
     int s = sc.s0;
     unsigned S = deposit_bits((unsigned)(f.first + s), f.mask);
     bool first = true;
@@ -862,7 +949,7 @@ __device__ __forceinline__ void bal_build_tab(const BalSched& sc, unsigned lr, u
                     do {
                         ++o;
                         if (o >= NB) break;
-                        f = bal_family<OP, ROLE, 0>(o, full, P.nulh);
+                        f = bal_family<OP, ROLE, CLS>(o, full, P.nulh);
                     } while (f.count == 0);
                     s = 0;
                     S = deposit_bits((unsigned)f.first, f.mask);
@@ -873,18 +960,62 @@ __device__ __forceinline__ void bal_build_tab(const BalSched& sc, unsigned lr, u
     }
 }
 
-// One role over one row from its table (see bal_role for the arguments).
-template <int OP, int ROLE, bool LOWNEG>
-__device__ __forceinline__ void bal_role_tab(const BalSched& sc, const unsigned short* __restrict__ tab,
+// sum_e s_lo(e, e) x[e] y0 terms of a pair ih = jh: the terms both deals of
+// the inner product's backward count (subtracted once from the output)
+template <bool LOWNEG, int... E>
+__device__ __forceinline__ void diag_sub(float (&acc)[16], const float (&x)[16], float y0,
+                                        std::integer_sequence<int, E...>) {
+    ((acc[E] = low_sign(LV_LC, LOWNEG, (unsigned)E, (unsigned)E) > 0 ? __builtin_fmaf(-x[E], y0, acc[E])
+                                                                      : __builtin_fmaf(x[E], y0, acc[E])),
+     ...);
+}
+
+// One role over one row from its table (see bal_role for the arguments; T is
+// the table's step count, hdr the lane's tail header). MODE 0 stores completed
+// outputs; the inner product's deal A (MODE 1) leaves them in the row's
+// partial slot `part`, its deal B (MODE 2) adds the partial (outputs whose
+// deal A had pairs), takes off the terms of the pair ih = jh that both deals
+// counted, and stores.
+template <int OP, int ROLE, bool LOWNEG, int MODE = 0>
+__device__ __forceinline__ void bal_role_tab(int T, unsigned hdr, const unsigned short* __restrict__ tab,
                                              const float4* __restrict__ la, const float4* __restrict__ lb,
                                              const float4* __restrict__ lg, float4* __restrict__ heads, unsigned lr,
-                                             float4* __restrict__ out, unsigned NB, const BlkParams& P, unsigned rs) {
+                                             float4* __restrict__ out, unsigned NB, const BlkParams& P, unsigned rs,
+                                             float4* __restrict__ part = nullptr) {
     const unsigned full = NB - 1u;
     constexpr bool kRev = OP == OP_REGR && ROLE == 0;
+    // the inner product's deals: role 1 deal A and role 2 deal B pair blocks
+    // in the lc relation, the others in the rc relation
+    constexpr int VAR = OP != OP_INNER ? OP : ((ROLE == 1) == (MODE == 1) ? LV_LC : LV_RC);
     float acc[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.f;
-    for (int t = 0; t < sc.T; ++t) {
+    // completion of output ob: store (MODE 0), park (MODE 1) or finish (MODE 2)
+    auto finish = [&](unsigned ob) {
+        if (MODE == 1) {
+            store_blk(part, ob, acc, false);
+            return;
+        }
+        if (MODE == 2) {
+            const unsigned nul = P.nulh;
+            if ((ob & nul) == 0u) {  // deal A had pairs and both deals had the pair (ob, ob)
+                float pv[16];
+                load_blk_plain(part, ob, pv);
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[e] += pv[e];
+                const HiSign hs = hi_sign<OP>(ob, ob, P.negh, P.nulh, full, P.nm1, P.mu);
+                const unsigned sm = hs.mask;
+                const unsigned pm = cross_pi<OP>(ob, P.nm1) << 31;
+                float xv[16];
+                load_blk(ROLE == 1 ? lb : la, ob, xv, rs);
+                apply_flips(xv, sm, sm ^ pm);
+                const float g0 = reinterpret_cast<const float*>(lg)[4u * (swz(0u) ^ rs)];  // gc element 0
+                diag_sub<LOWNEG>(acc, xv, g0, std::make_integer_sequence<int, 16>{});
+            }
+        }
+        if (out) store_blk(out, kRev ? (full ^ ob) : ob, acc, kRev);
+    };
+    for (int t = 0; t < T; ++t) {
         const unsigned e = tab[t * NB + lr];
         const unsigned pb = e & 63u, ob = (e >> 6) & 63u;
         if (e & kTabCompute) {
@@ -904,7 +1035,8 @@ __device__ __forceinline__ void bal_role_tab(const BalSched& sc, const unsigned 
                     float bv[16];
                     load_blk(lb, pb, bv, rs);
                     apply_flips(bv, sm, sm ^ (cross_pi<OP>(ob, P.nm1) << 31));
-                    ga_block_dispatch<OP, LOWNEG>(acc, bv, g, ob, pb);
+                    if (OP == OP_INNER) lowblock_ga<VAR, LOWNEG>(acc, bv, g);
+                    else ga_block_dispatch<OP, LOWNEG>(acc, bv, g, ob, pb);
                 } else {  // h = ob (jh), m = pb (ih)
                     const unsigned pm = cross_pi<OP>(pb, P.nm1) << 31;
                     float av[16], gt[16];
@@ -912,7 +1044,8 @@ __device__ __forceinline__ void bal_role_tab(const BalSched& sc, const unsigned 
                     apply_flips(av, sm, sm ^ pm);
 #pragma unroll
                     for (int k = 0; k < 16; ++k) gt[k] = (cpopc((unsigned)k) & 1) ? flip(g[k], pm) : g[k];
-                    gb_block_dispatch<OP, LOWNEG>(acc, av, gt, pb, ob);
+                    if (OP == OP_INNER) lowblock_gb<VAR, LOWNEG>(acc, av, gt);
+                    else gb_block_dispatch<OP, LOWNEG>(acc, av, gt, pb, ob);
                 }
             }
         }
@@ -921,8 +1054,8 @@ __device__ __forceinline__ void bal_role_tab(const BalSched& sc, const unsigned 
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 heads[lr * 4 + q] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
-        } else if (act == 2u && out) {
-            store_blk(out, kRev ? (full ^ ob) : ob, acc, kRev);
+        } else if (act == 2u) {
+            finish(ob);
         }
         if (act != 0u) {
 #pragma unroll
@@ -930,8 +1063,9 @@ __device__ __forceinline__ void bal_role_tab(const BalSched& sc, const unsigned 
         }
     }
     wave_lds_sync();
-    if (sc.tail) {
-        for (int l = (int)lr + 1; l <= sc.last_lane; ++l) {
+    if (hdr & 1u) {
+        const int last_lane = (int)((hdr >> 1) & 63u);
+        for (int l = (int)lr + 1; l <= last_lane; ++l) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const float4 v = heads[l * 4 + q];
@@ -941,7 +1075,7 @@ __device__ __forceinline__ void bal_role_tab(const BalSched& sc, const unsigned 
                 acc[4 * q + 3] += v.w;
             }
         }
-        if (out) store_blk(out, kRev ? (full ^ sc.olast) : sc.olast, acc, kRev);
+        finish((hdr >> 7) & 63u);
     }
 }
 
@@ -1002,10 +1136,12 @@ __global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A,
     // wedge, lc, rc and regressive run from the role's schedule table
     constexpr bool kTab = OP != OP_INNER && OP != OP_GEOM;
     __shared__ unsigned short tab[kTab ? kBalTabEntries : 1];
+    __shared__ unsigned hdr[kTab ? 64 : 1];
     if (kTab) {
-        if (wave == 0 && lane < (int)NB) bal_build_tab<OP, 0>(sc, lr, NB, P, tab);
+        if (wave == 0 && lane < (int)NB) bal_build_tab<OP, 0>(sc, lr, NB, P, tab, hdr);
         __syncthreads();
     }
+    const unsigned my_hdr = kTab ? hdr[lr] : 0u;
     const long long ngrp = (P.batch + R - 1) / R;
     const long long gstride = (long long)gridDim.x * 4;
     long long grp = (long long)blockIdx.x * 4 + wave;
@@ -1019,7 +1155,7 @@ __global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A,
         wave_lds_sync();
         const long long row = grp * R + r;
         float4* out = row < P.batch ? reinterpret_cast<float4*>(C) + (row << (n - 2)) : nullptr;
-        if constexpr (kTab) bal_role_tab<OP, 0, LOWNEG>(sc, tab, sa + roff, sb + roff, nullptr, heads, lr, out, NB, P, rs);
+        if constexpr (kTab) bal_role_tab<OP, 0, LOWNEG>(sc.T, my_hdr, tab, sa + roff, sb + roff, nullptr, heads, lr, out, NB, P, rs);
         else bal_role<OP, 0, kCls, LOWNEG>(sc, sa + roff, sb + roff, nullptr, heads, lr, out, NB, P, rs);
         wave_lds_sync();
     }
@@ -1027,15 +1163,20 @@ __global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A,
 
 // Backward: b and gc are staged first and the left-operand gradient runs with
 // its heads in the a slot; then a is staged and the right-operand gradient
-// runs with its heads in the b slot (12 KB of LDS per wave; 16 KB for inner).
+// runs with its heads in the b slot (12 KB of LDS per wave). The inner product
+// runs each gradient in two deals (classes 5 and 6: the lc-relation and the
+// rc-relation partners, 81 terms per pair each) whose sums meet in a fourth
+// slot (16 KB per wave).
 template <int OP, bool LOWNEG>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void prod_bwd_bal(const float* __restrict__ A, const float* __restrict__ B,
                                                      const float* __restrict__ GC, float* __restrict__ GA,
                                                      float* __restrict__ GB, BlkParams P) {
-    // The inner product runs its backward round (class 4: all partners of an
-    // output, lc side then rc side, with the low pattern split by term class).
-    constexpr int kCls = OP == OP_INNER ? 4 : 0;
-    __shared__ float4 lds[4][3 * kBalGroupF4];  // a | b | gc
+    constexpr bool kDeals = OP == OP_INNER;
+    constexpr bool kTab = OP != OP_GEOM;  // every op but geom runs from schedule tables
+    constexpr int kTabs = kDeals ? 4 : 2;
+    __shared__ float4 lds[4][(kDeals ? 4 : 3) * kBalGroupF4];  // a | b | gc [| the inner product's partials]
+    __shared__ unsigned short tab[kTab ? kTabs : 1][kTab ? kBalTabEntries : 1];
+    __shared__ unsigned hdr[kTab ? kTabs : 1][64];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int n = P.n;
     const int lpr_log = n - 4;
@@ -1046,22 +1187,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     float4* sa = lds[wave];
     float4* sb = sa + kBalGroupF4;
     float4* sg = sb + kBalGroupF4;
+    float4* sp = sg + kBalGroupF4;  // inner product only
     const int roff = r << (n - 2);
     const unsigned rs = (unsigned)r & 3u;  // the row's slot skew
     const int hoff = (r << lpr_log) * 4;
     const bool want_a = GA != nullptr, want_b = GB != nullptr;
-    const BalSched sca = bal_schedule<OP, 1, kCls>(lr, NB, P.nulh);
-    const BalSched scb = bal_schedule<OP, 2, kCls>(lr, NB, P.nulh);
-    // wedge, lc, rc and regressive run from the roles' schedule tables
-    constexpr bool kTab = OP != OP_INNER && OP != OP_GEOM;
-    __shared__ unsigned short tab[2][kTab ? kBalTabEntries : 1];
-    if (kTab) {
+    // step counts of the roles' tables (deals A, B for the inner product)
+    int T[kTabs];
+    if constexpr (kDeals) {
+        const BalSched s0 = bal_schedule<OP, 1, 5>(lr, NB, P.nulh), s1 = bal_schedule<OP, 1, 6>(lr, NB, P.nulh);
+        const BalSched s2 = bal_schedule<OP, 2, 5>(lr, NB, P.nulh), s3 = bal_schedule<OP, 2, 6>(lr, NB, P.nulh);
         if (wave == 0 && lane < (int)NB) {
-            bal_build_tab<OP, 1>(sca, lr, NB, P, tab[0]);
-            bal_build_tab<OP, 2>(scb, lr, NB, P, tab[1]);
+            bal_build_tab<OP, 1, 5>(s0, lr, NB, P, tab[0], hdr[0]);
+            bal_build_tab<OP, 1, 6>(s1, lr, NB, P, tab[1], hdr[1]);
+            bal_build_tab<OP, 2, 5>(s2, lr, NB, P, tab[2], hdr[2]);
+            bal_build_tab<OP, 2, 6>(s3, lr, NB, P, tab[3], hdr[3]);
         }
-        __syncthreads();
+        T[0] = s0.T;
+        T[1] = s1.T;
+        T[2] = s2.T;
+        T[3] = s3.T;
+    } else if constexpr (kTab) {
+        const BalSched sca = bal_schedule<OP, 1, 0>(lr, NB, P.nulh), scb = bal_schedule<OP, 2, 0>(lr, NB, P.nulh);
+        if (wave == 0 && lane < (int)NB) {
+            bal_build_tab<OP, 1>(sca, lr, NB, P, tab[0], hdr[0]);
+            bal_build_tab<OP, 2>(scb, lr, NB, P, tab[1], hdr[1]);
+        }
+        T[0] = sca.T;
+        T[1] = scb.T;
     }
+    if (kTab) __syncthreads();
+    const BalSched sca = bal_schedule<OP, 1, 0>(lr, NB, P.nulh);  // geom only
+    const BalSched scb = bal_schedule<OP, 2, 0>(lr, NB, P.nulh);
     const long long ngrp = (P.batch + R - 1) / R;
     const long long gstride = (long long)gridDim.x * 4;
     long long grp = (long long)blockIdx.x * 4 + wave;
@@ -1079,8 +1236,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
             pb = bal_fetch(B, grp + gstride, P.batch, n, lane);
             wave_lds_sync();
             float4* out = row_ok ? reinterpret_cast<float4*>(GA) + (row << (n - 2)) : nullptr;
-            if constexpr (kTab) bal_role_tab<OP, 1, LOWNEG>(sca, tab[0], nullptr, sb + roff, sg + roff, sa + hoff, lr, out, NB, P, rs);
-            else bal_role<OP, 1, kCls, LOWNEG>(sca, nullptr, sb + roff, sg + roff, sa + hoff, lr, out, NB, P, rs);
+            if constexpr (kDeals) {
+                bal_role_tab<OP, 1, LOWNEG, 1>(T[0], hdr[0][lr], tab[0], nullptr, sb + roff, sg + roff, sa + hoff, lr,
+                                               nullptr, NB, P, rs, sp + roff);
+                wave_lds_sync();
+                bal_role_tab<OP, 1, LOWNEG, 2>(T[1], hdr[1][lr], tab[1], nullptr, sb + roff, sg + roff, sa + hoff, lr,
+                                               out, NB, P, rs, sp + roff);
+            } else if constexpr (kTab) {
+                bal_role_tab<OP, 1, LOWNEG>(T[0], hdr[0][lr], tab[0], nullptr, sb + roff, sg + roff, sa + hoff, lr,
+                                            out, NB, P, rs);
+            } else {
+                bal_role<OP, 1, 0, LOWNEG>(sca, nullptr, sb + roff, sg + roff, sa + hoff, lr, out, NB, P, rs);
+            }
             wave_lds_sync();
         }
         if (want_b) {
@@ -1088,8 +1255,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
             pa = bal_fetch(A, grp + gstride, P.batch, n, lane);
             wave_lds_sync();
             float4* out = row_ok ? reinterpret_cast<float4*>(GB) + (row << (n - 2)) : nullptr;
-            if constexpr (kTab) bal_role_tab<OP, 2, LOWNEG>(scb, tab[1], sa + roff, nullptr, sg + roff, sb + hoff, lr, out, NB, P, rs);
-            else bal_role<OP, 2, kCls, LOWNEG>(scb, sa + roff, nullptr, sg + roff, sb + hoff, lr, out, NB, P, rs);
+            if constexpr (kDeals) {
+                bal_role_tab<OP, 2, LOWNEG, 1>(T[2], hdr[2][lr], tab[2], sa + roff, nullptr, sg + roff, sb + hoff, lr,
+                                               nullptr, NB, P, rs, sp + roff);
+                wave_lds_sync();
+                bal_role_tab<OP, 2, LOWNEG, 2>(T[3], hdr[3][lr], tab[3], sa + roff, nullptr, sg + roff, sb + hoff, lr,
+                                               out, NB, P, rs, sp + roff);
+            } else if constexpr (kTab) {
+                bal_role_tab<OP, 2, LOWNEG>(T[1], hdr[1][lr], tab[1], sa + roff, nullptr, sg + roff, sb + hoff, lr,
+                                            out, NB, P, rs);
+            } else {
+                bal_role<OP, 2, 0, LOWNEG>(scb, sa + roff, nullptr, sg + roff, sb + hoff, lr, out, NB, P, rs);
+            }
         }
         wave_lds_sync();
     }
@@ -1390,14 +1567,12 @@ static bool tiled_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, 
 static bool tiled_forced() { return options().product_path == PATH_TILED; }
 static bool generic_forced() { return options().product_path == PATH_GENERIC; }
 
-// Balanced kernels: wedge, lc, rc, regressive and the inner product's forward
-// for 4 <= n <= 10, the inner product's backward for n >= 8
-// (CLF_PRODUCT_PATH=blocked keeps them on the one-lane-per-output kernels).
-// The inner backward's round computes both low patterns per pair and runs at
-// three waves per SIMD with a few spilled registers; at n = 7 the blocked
-// kernel is faster (measured), from n = 8 the balanced round. The geometric
-// product, whose outputs all have the same work, gains nothing; both use the
-// balanced kernels only when CLF_PRODUCT_PATH=balanced.
+// Balanced kernels: wedge, lc, rc, regressive and the inner product for
+// 4 <= n <= 10 (CLF_PRODUCT_PATH=blocked keeps them on the one-lane-per-output
+// kernels). Below n = 8 the inner product's backward runs on the blocked
+// kernel, whose partner walk by relation class is faster there (measured). The
+// geometric product, whose outputs all have the same work, gains nothing; both
+// use the balanced kernels only when CLF_PRODUCT_PATH=balanced.
 static bool bal_plan(int op, int n, uint32_t neg, uint32_t nul, bool fwd, BlkParams& P, bool& lowneg) {
     if (n < kBalMinN || n > kBalMaxN) return false;
     const bool opt_in = op == OP_GEOM || (op == OP_INNER && !fwd && n < 8);
