@@ -261,17 +261,18 @@ __device__ __forceinline__ void gather_pair_fresh(const float* __restrict__ row,
     gather_pair(row, e, m, w);
 }
 
-// out half (rows 2g, 2g + 1 at dst, row stride 1024) = T^-1 of the product in acc
-__device__ __forceinline__ void split_store(const floatx16& acc, float* __restrict__ sx, float* __restrict__ dst,
-                                            long long g, long long batch, const unsigned (&en)[16], unsigned mout,
-                                            int lane) {
+// out half = T^-1 of the product in acc: relayout through `rel` (1280 floats),
+// then the two half rows in blade order into `rows` (1024 floats; it may be
+// the start of `rel`)
+__device__ __forceinline__ void split_finish(const floatx16& acc, float* __restrict__ rel, float* __restrict__ rows,
+                                             const unsigned (&en)[16], unsigned mout, int lane) {
     const int b = lane >> 4, r = b >> 1;
     const unsigned s = (unsigned)b & 1u, x = lane & 15u;
     const float pm = s ? -1.f : 1.f;
-    relayout_store(sx, acc, lane);
+    relayout_store(rel, acc, lane);
     wave_lds_sync();
     float w[16];
-    relayout_load(sx, b, x, w);
+    relayout_load(rel, b, x, w);
     wave_lds_sync();
     wht_inplace<16>(w);
 #pragma unroll
@@ -279,10 +280,15 @@ __device__ __forceinline__ void split_store(const floatx16& acc, float* __restri
         const float other = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(w[z]), 0x401F));
         const float v = __builtin_fmaf(pm, w[z], other) * (1.f / 32.f);
         const unsigned blade = s ? ((en[z] >> 9) & 511u) : (en[z] & 511u);
-        sx[r * 512 + blade] = __uint_as_float(__float_as_uint(v) ^ (((mout >> z) & 1u) << 31));
+        rows[r * 512 + blade] = __uint_as_float(__float_as_uint(v) ^ (((mout >> z) & 1u) << 31));
     }
     wave_lds_sync();
-    const float4* src = reinterpret_cast<const float4*>(sx);
+}
+
+// the two half rows of group g (rows 2g, 2g + 1 at dst, row stride 1024)
+__device__ __forceinline__ void split_emit(const float* __restrict__ rows, float* __restrict__ dst, long long g,
+                                           long long batch, int lane) {
+    const float4* src = reinterpret_cast<const float4*>(rows);
     const float4 o0 = src[lane], o1 = src[lane + 64], o2 = src[lane + 128], o3 = src[lane + 192];
     long long r0 = 2 * g, r1 = 2 * g + 1;
     r0 = r0 < batch ? r0 : batch - 1;  // clamped rows repeat the last row's values
@@ -293,14 +299,17 @@ __device__ __forceinline__ void split_store(const floatx16& acc, float* __restri
     d0[lane + 64] = o1;
     d1[lane] = o2;
     d1[lane + 64] = o3;
-    wave_lds_sync();
 }
 
 // LDS per wave: four regions of two half rows (1024 floats each) so that the
 // stage-0 halves stay staged through stage 1 and are gathered again where a
 // sum needs them (instead of holding their operands in registers). Each
-// output's relayout and scatter use two adjacent regions whose halves are
-// consumed by then: region order per KIND is chosen for that.
+// output's relayout (1280 floats) uses regions whose halves are consumed by
+// then, and its rows wait in a region the next stage does not overwrite: a
+// wave's loads and stores share one completion counter that is drained before
+// staged rows are used, so the rows are stored right after the next stage's
+// wait rather than just before it (the forward, whose first half is complete
+// before stage 1, keeps its rows in a fifth region).
 template <int KIND>
 struct FusedRegions {
     // offsets (in units of 1024 floats) of X0, Y0, X1, Y1
@@ -308,9 +317,12 @@ struct FusedRegions {
     static constexpr int y0 = KIND == 1 ? 3 : 1;
     static constexpr int x1 = 2;
     static constexpr int y1 = KIND == 1 ? 1 : 3;
-    // adjacent free regions for the outputs: out0, out1
-    static constexpr int out0 = KIND == 0 ? 2 : (KIND == 1 ? 0 : 1);
-    static constexpr int out1 = KIND == 0 ? 0 : (KIND == 1 ? 0 : 1);
+    // relayout areas and row slots of out0 / out1
+    static constexpr int rel0 = KIND == 0 ? 2 : (KIND == 1 ? 0 : 1);
+    static constexpr int rows0 = KIND == 0 ? 4 : (KIND == 1 ? 1 : 2);
+    static constexpr int rel1 = KIND == 0 ? 0 : (KIND == 1 ? 2 : 0);
+    static constexpr int rows1 = KIND == 0 ? 4 : (KIND == 1 ? 2 : 3);
+    static constexpr int regions = KIND == 0 ? 5 : 4;
 };
 
 // waves per workgroup of the fused kernels
@@ -318,9 +330,9 @@ constexpr int kFusedWaves = 4;
 
 template <int KIND>
 __global__ __launch_bounds__(64 * kFusedWaves) void split_fused_kernel(FusedSplit P, SplitTable T) {
-    __shared__ float lds[kFusedWaves][4 * 1024];
     using RG = FusedRegions<KIND>;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __shared__ float lds[kFusedWaves][RG::regions * 1024];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int b = lane >> 4, r = b >> 1;
     const unsigned s = (unsigned)b & 1u, x = lane & 15u;
     float* base = &lds[wave][0];
@@ -367,7 +379,8 @@ __global__ __launch_bounds__(64 * kFusedWaves) void split_fused_kernel(FusedSpli
     const float* Y0 = P.Y;
     const float* X1 = P.X + 512;
     const float* Y1 = P.Y + 512;
-    long long g = (long long)blockIdx.x * kFusedWaves + wave;
+    const long long g0 = (long long)blockIdx.x * kFusedWaves + wave;
+    long long g = g0;
     float4 ax0, ax1, ax2, ax3, ay0, ay1, ay2, ay3;
     CLF_SPLIT_FETCH(ax0, ax1, ax2, ax3, X0, 1024, 2 * g);
     CLF_SPLIT_FETCH(ay0, ay1, ay2, ay3, Y0, 1024, 2 * g);
@@ -385,6 +398,10 @@ __global__ __launch_bounds__(64 * kFusedWaves) void split_fused_kernel(FusedSpli
         CLF_SPLIT_STAGE(sy0, ay0, ay1, ay2, ay3);
         CLF_SPLIT_FETCH(ax0, ax1, ax2, ax3, X1, 1024, 2 * g);
         CLF_SPLIT_FETCH(ay0, ay1, ay2, ay3, Y1, 1024, 2 * g);
+        if (g != g0) {  // uniform: the previous group's rows wait in regions stage 0 does not touch
+            if (KIND != 0) split_emit(base + RG::rows0 * 1024, P.out, g - gstride, batch, lane);
+            split_emit(base + RG::rows1 * 1024, P.out + 512, g - gstride, batch, lane);
+        }
         wave_lds_sync();
         floatx16 acc0;
         {
@@ -394,13 +411,14 @@ __global__ __launch_bounds__(64 * kFusedWaves) void split_fused_kernel(FusedSpli
             acc0 = mfma_chain(wx, wy);
         }
         if constexpr (KIND == 0) {  // C0 = L0 R0 is complete; X1 / Y1 regions are still free
-            split_store(acc0, base + RG::out0 * 1024, P.out, g, batch, en, mout, lane);
+            split_finish(acc0, base + RG::rel0 * 1024, base + RG::rows0 * 1024, en, mout, lane);
         }
         // stage 1: X1, Y1
         CLF_SPLIT_STAGE(sx1, ax0, ax1, ax2, ax3);
         CLF_SPLIT_STAGE(sy1, ay0, ay1, ay2, ay3);
         CLF_SPLIT_FETCH(ax0, ax1, ax2, ax3, X0, 1024, 2 * (g + gstride));
         CLF_SPLIT_FETCH(ay0, ay1, ay2, ay3, Y0, 1024, 2 * (g + gstride));
+        if constexpr (KIND == 0) split_emit(base + RG::rows0 * 1024, P.out, g, batch, lane);
         wave_lds_sync();
         if constexpr (KIND == 0) {
             // C1 = L0 R1 + L1 R0^
@@ -418,7 +436,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void split_fused_kernel(FusedSpli
                 acc1 = mfma_chain_acc(acc1, wx, wy, std::make_integer_sequence<unsigned, 16>{});
             }
             wave_lds_sync();
-            split_store(acc1, base + RG::out1 * 1024, P.out + 512, g, batch, en, mout, lane);
+            split_finish(acc1, base + RG::rel1 * 1024, base + RG::rows1 * 1024, en, mout, lane);
         } else if constexpr (KIND == 1) {
             // out0 += G1 R1^T; out1 = G1 (R0^)^T
             float wx[16];
@@ -429,7 +447,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void split_fused_kernel(FusedSpli
                 acc0 = mfma_chain_acc(acc0, wx, wy, std::make_integer_sequence<unsigned, 16>{});
             }
             wave_lds_sync();
-            split_store(acc0, base + RG::out0 * 1024, P.out, g, batch, en, mout, lane);
+            split_finish(acc0, base + RG::rel0 * 1024, base + RG::rows0 * 1024, en, mout, lane);
             floatx16 acc1;
             {
                 float wy[16];
@@ -437,7 +455,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void split_fused_kernel(FusedSpli
                 acc1 = mfma_chain(wx, wy);
             }
             wave_lds_sync();
-            split_store(acc1, base + RG::out1 * 1024, P.out + 512, g, batch, en, mout, lane);
+            split_finish(acc1, base + RG::rel1 * 1024, base + RG::rows1 * 1024, en, mout, lane);
         } else {
             // out0 += (L1^)^T G1^; out1 = L0^T G1
             {
@@ -447,7 +465,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void split_fused_kernel(FusedSpli
                 acc0 = mfma_chain_acc(acc0, wx, wy, std::make_integer_sequence<unsigned, 16>{});
             }
             wave_lds_sync();
-            split_store(acc0, base + RG::out0 * 1024, P.out, g, batch, en, mout, lane);
+            split_finish(acc0, base + RG::rel0 * 1024, base + RG::rows0 * 1024, en, mout, lane);
             floatx16 acc1;
             {
                 float wx[16], wy[16];
@@ -456,8 +474,12 @@ __global__ __launch_bounds__(64 * kFusedWaves) void split_fused_kernel(FusedSpli
                 acc1 = mfma_chain(wx, wy);
             }
             wave_lds_sync();
-            split_store(acc1, base + RG::out1 * 1024, P.out + 512, g, batch, en, mout, lane);
+            split_finish(acc1, base + RG::rel1 * 1024, base + RG::rows1 * 1024, en, mout, lane);
         }
+    }
+    if (g != g0) {
+        if (KIND != 0) split_emit(base + RG::rows0 * 1024, P.out, g - gstride, batch, lane);
+        split_emit(base + RG::rows1 * 1024, P.out + 512, g - gstride, batch, lane);
     }
 }
 
