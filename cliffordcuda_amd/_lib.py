@@ -51,6 +51,7 @@ SIGNATURES = {
     "clf_product_max_n": (_i32, []),
     "clf_product_fwd": (_i32, [_i32, _i32, _u32, _u32, _vp, _vp, _vp, _i64, _vp]),
     "clf_product_bwd": (_i32, [_i32, _i32, _u32, _u32, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
+    "clf_product_bwd_ld": (_i32, [_i32, _i32, _u32, _u32, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp]),
     "clf_graded": (_i32, [_i32, _i32, _u32, _u32, _i32, _vp, _vp, _i64, _vp]),
     "clf_norm_sq_fwd": (_i32, [_i32, _u32, _u32, _vp, _vp, _i64, _vp]),
     "clf_norm_sq_bwd": (_i32, [_i32, _u32, _u32, _vp, _vp, _vp, _i64, _vp]),
@@ -60,9 +61,11 @@ SIGNATURES = {
     "clf_rotor_apply_fwd": (_i32, [_i32, _vp, _vp, _vp, _i64, _vp]),
     "clf_rotor_apply_ws_bytes": (_sz, [_i32, _i64]),
     "clf_rotor_apply_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
+    "clf_rotor_apply_bwd_ld": (_i32, [_i32, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _sz, _vp]),
     "clf_rotor_cs_apply_fwd": (_i32, [_i32, _vp, _vp, _vp, _i64, _vp]),
     "clf_rotor_cs_apply_ws_bytes": (_sz, [_i32, _i64]),
     "clf_rotor_cs_apply_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
+    "clf_rotor_cs_apply_bwd_ld": (_i32, [_i32, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _sz, _vp]),
     "clf_rotor_cs_compile_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp]),
     "clf_inverse_rep_supported": (_i32, [_i32, _u32, _u32]),
     "clf_inverse_rep": (_i32, [_i32, _u32, _u32, _vp, _vp, _vp, _i64, _vp]),
@@ -70,6 +73,8 @@ SIGNATURES = {
     "clf_product_bcast_ws_bytes": (_sz, [_i32, _i64]),
     "clf_product_bcast_fwd": (_i32, [_i32, _i32, _i32, _u32, _u32, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
     "clf_product_bcast_bwd": (_i32, [_i32, _i32, _i32, _u32, _u32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
+    "clf_product_bcast_bwd_ld": (
+        _i32, [_i32, _i32, _i32, _u32, _u32, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _sz, _vp]),
     "clf_product_bcast_bwd_noalloc_scratch_bytes": (_sz, []),
     "clf_product_bcast_bwd_noalloc": (_i32, [_i32, _i32, _i32, _u32, _u32, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
 }
@@ -119,6 +124,20 @@ def check(rc: int, what: str):
 
 def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
+
+
+def grad_rows(g: torch.Tensor, dim: int):
+    """(tensor, row stride in floats) for an upstream gradient of shape
+    (batch, dim). A gradient whose batch stride is 0 (autograd's expansion of
+    the gradient of a sum) is handed over as its one row with stride 0, so the
+    kernels read that row for every batch row instead of a materialised copy;
+    any other layout is made contiguous (stride dim)."""
+    if g.dim() == 2 and g.shape[0] > 1 and g.stride(0) == 0:
+        row = g[0]
+        if row.stride(0) != 1 or row.data_ptr() % 16:
+            row = row.clone(memory_format=torch.contiguous_format)
+        return row, 0
+    return g.contiguous(), dim
 
 
 def reload_options() -> None:

@@ -46,7 +46,7 @@ def _(a, b, op, n, neg, nul):
 def product_bwd(a: Tensor, b: Tensor, gc: Tensor, op: int, n: int, neg: int, nul: int, need_a: bool,
                 need_b: bool) -> Tuple[Tensor, Tensor]:
     from .products import _product_bwd
-    ga, gb = _product_bwd(op, n, neg, nul, a, b, gc.contiguous(), need_a, need_b)
+    ga, gb = _product_bwd(op, n, neg, nul, a, b, gc, need_a, need_b)
     return (ga if ga is not None else _placeholder(a)), (gb if gb is not None else _placeholder(b))
 
 
@@ -170,7 +170,7 @@ def _bcast_setup(ctx, inputs, output):
 def _bcast_backward(ctx, gy):
     x, w = ctx.saved_tensors
     need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-    gx, gw = bcast_product_bwd(x, w, gy.contiguous(), *ctx.meta, need_x, need_w)
+    gx, gw = bcast_product_bwd(x, w, gy, *ctx.meta, need_x, need_w)
     return _none_if_unneeded(gx, need_x), _none_if_unneeded(gw, need_w), None, None, None, None, None
 
 
@@ -254,7 +254,7 @@ def _rotor_apply_setup(ctx, inputs, output):
 def _rotor_apply_backward(ctx, gy):
     state, x = ctx.saved_tensors
     need_state, need_x = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-    g_state, gx = rotor_apply_bwd(state, x, gy.contiguous(), ctx.n, need_state, need_x)
+    g_state, gx = rotor_apply_bwd(state, x, gy, ctx.n, need_state, need_x)
     return _none_if_unneeded(g_state, need_state), _none_if_unneeded(gx, need_x), None
 
 
@@ -326,7 +326,7 @@ def _rotor_cs_apply_setup(ctx, inputs, output):
 def _rotor_cs_apply_backward(ctx, gy):
     cs, y = ctx.saved_tensors
     need_cs, need_x = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-    g_cs, gx = rotor_cs_apply_bwd(cs, y, gy.contiguous(), ctx.n, need_cs, need_x)
+    g_cs, gx = rotor_cs_apply_bwd(cs, y, gy, ctx.n, need_cs, need_x)
     return _none_if_unneeded(g_cs, need_cs), _none_if_unneeded(gx, need_x), None
 
 

@@ -37,15 +37,15 @@ def _bcast_bwd(x, w, gy, op_code, side, n, neg, nul, need_x, need_w):
     if not (need_x or need_w):
         return None, None
     lib = _lib.load()
-    gy = gy.contiguous()
+    gy, ldg = _lib.grad_rows(gy, x.shape[1])
     gx = torch.empty_like(x) if need_x else None
     gw = torch.empty_like(w) if need_w else None
     ws, nbytes = _ws(lib, n, x.shape[0], x.device)
     with torch.cuda.device(x.device):
-        rc = lib.clf_product_bcast_bwd(op_code, side, n, neg, nul, x.data_ptr(), w.data_ptr(), gy.data_ptr(),
-                                       _lib.ptr(gx), _lib.ptr(gw), x.shape[0], ws.data_ptr(), nbytes,
-                                       _lib.stream_of(x))
-    _lib.check(rc, "clf_product_bcast_bwd")
+        rc = lib.clf_product_bcast_bwd_ld(op_code, side, n, neg, nul, x.data_ptr(), w.data_ptr(), gy.data_ptr(),
+                                          ldg, _lib.ptr(gx), _lib.ptr(gw), x.shape[0], ws.data_ptr(), nbytes,
+                                          _lib.stream_of(x))
+    _lib.check(rc, "clf_product_bcast_bwd_ld")
     return gx, gw
 
 

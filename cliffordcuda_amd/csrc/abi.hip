@@ -136,7 +136,7 @@ unsigned resident_grid(const void* kernel, int block_threads, size_t dyn_lds, lo
 int product_fwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const float* b, float* c,
                 int64_t batch, void* stream);
 int product_bwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const float* b, const float* gc,
-                float* ga, float* gb, int64_t batch, void* stream);
+                int64_t ldg, float* ga, float* gb, int64_t batch, void* stream);
 int graded(int kind, int n, uint32_t neg, uint32_t nul, int grade, const float* x, float* y, int64_t batch,
            void* stream);
 int norm_sq_fwd(int n, uint32_t neg, uint32_t nul, const float* x, float* out, int64_t batch, void* stream);
@@ -148,19 +148,19 @@ size_t rotor_apply_ws_bytes(int n, int64_t batch);
 int rotor_compile_fwd(int n, const float* biv, float* state, float* cs, void* stream);
 int rotor_compile_bwd(int n, const float* biv, const float* g_state, float* g_biv, void* stream);
 int rotor_apply_fwd(int n, const float* state, const float* x, float* y, int64_t batch, void* stream);
-int rotor_apply_bwd(int n, const float* state, const float* x, const float* gy, float* gx, float* g_state,
-                    int64_t batch, void* ws, size_t ws_bytes, void* stream);
+int rotor_apply_bwd(int n, const float* state, const float* x, const float* gy, int64_t ldg, float* gx,
+                    float* g_state, int64_t batch, void* ws, size_t ws_bytes, void* stream);
 size_t rotor_cs_apply_ws_bytes(int n, int64_t batch);
 int rotor_cs_apply_fwd(int n, const float* cs, const float* x, float* y, int64_t batch, void* stream);
-int rotor_cs_apply_bwd(int n, const float* cs, const float* y, const float* gy, float* gx, float* g_cs,
-                       int64_t batch, void* ws, size_t ws_bytes, void* stream);
+int rotor_cs_apply_bwd(int n, const float* cs, const float* y, const float* gy, int64_t ldg, float* gx,
+                       float* g_cs, int64_t batch, void* ws, size_t ws_bytes, void* stream);
 int rotor_cs_compile_bwd(int n, const float* biv, const float* g_cs, float* g_biv, void* stream);
 
 size_t bcast_ws_bytes(int n, int64_t batch);
 int bcast_fwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w, float* y,
               int64_t batch, void* ws, size_t ws_bytes, void* stream);
 int bcast_bwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w, const float* gy,
-              float* gx, float* gw, int64_t batch, void* ws, size_t ws_bytes, void* stream);
+              int64_t ldg, float* gx, float* gw, int64_t batch, void* ws, size_t ws_bytes, void* stream);
 int inverse_rep_supported(int n, uint32_t neg, uint32_t nul);
 int inverse_rep(int n, uint32_t neg, uint32_t nul, const float* x, float* y, int* singular, int64_t batch,
                 void* stream);
@@ -168,7 +168,11 @@ int inverse_versor(int n, const float* x, const float* xr, float* y, int* flags,
                    void* stream);
 size_t bcast_scratch_bytes();
 int bcast_bwd_noalloc(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w,
-                      const float* gy, float* gx, float* gw, int64_t batch, void* stream);
+                      const float* gy, int64_t ldg, float* gx, float* gw, int64_t batch, void* stream);
+
+// Floats between the rows of a dense batch of n-dimensional multivectors; an
+// out-of-range n maps to 0 and is rejected by the callee's own check on n.
+inline int64_t dense_ld(int n) { return (n >= 0 && n <= kMaxN) ? (int64_t(1) << n) : 0; }
 
 }  // namespace clf
 
@@ -208,7 +212,13 @@ int clf_product_fwd(int op, int n, uint32_t neg_mask, uint32_t null_mask, const 
 int clf_product_bwd(int op, int n, uint32_t neg_mask, uint32_t null_mask, const float* a, const float* b,
                     const float* gc, float* ga, float* gb, int64_t batch, void* stream) {
     clf::clear_error();
-    return clf::product_bwd(op, n, neg_mask, null_mask, a, b, gc, ga, gb, batch, stream);
+    return clf::product_bwd(op, n, neg_mask, null_mask, a, b, gc, clf::dense_ld(n), ga, gb, batch, stream);
+}
+
+int clf_product_bwd_ld(int op, int n, uint32_t neg_mask, uint32_t null_mask, const float* a, const float* b,
+                       const float* gc, int64_t ldg, float* ga, float* gb, int64_t batch, void* stream) {
+    clf::clear_error();
+    return clf::product_bwd(op, n, neg_mask, null_mask, a, b, gc, ldg, ga, gb, batch, stream);
 }
 
 int clf_graded(int kind, int n, uint32_t neg_mask, uint32_t null_mask, int grade, const float* x, float* y,
@@ -251,7 +261,13 @@ size_t clf_rotor_apply_ws_bytes(int n, int64_t batch) { return clf::rotor_apply_
 int clf_rotor_apply_bwd(int n, const float* state, const float* x, const float* gy, float* gx, float* g_state,
                         int64_t batch, void* ws, size_t ws_bytes, void* stream) {
     clf::clear_error();
-    return clf::rotor_apply_bwd(n, state, x, gy, gx, g_state, batch, ws, ws_bytes, stream);
+    return clf::rotor_apply_bwd(n, state, x, gy, clf::dense_ld(n), gx, g_state, batch, ws, ws_bytes, stream);
+}
+
+int clf_rotor_apply_bwd_ld(int n, const float* state, const float* x, const float* gy, int64_t ldg, float* gx,
+                           float* g_state, int64_t batch, void* ws, size_t ws_bytes, void* stream) {
+    clf::clear_error();
+    return clf::rotor_apply_bwd(n, state, x, gy, ldg, gx, g_state, batch, ws, ws_bytes, stream);
 }
 
 int clf_rotor_cs_apply_fwd(int n, const float* cs, const float* x, float* y, int64_t batch, void* stream) {
@@ -264,7 +280,13 @@ size_t clf_rotor_cs_apply_ws_bytes(int n, int64_t batch) { return clf::rotor_cs_
 int clf_rotor_cs_apply_bwd(int n, const float* cs, const float* y, const float* gy, float* gx, float* g_cs,
                            int64_t batch, void* ws, size_t ws_bytes, void* stream) {
     clf::clear_error();
-    return clf::rotor_cs_apply_bwd(n, cs, y, gy, gx, g_cs, batch, ws, ws_bytes, stream);
+    return clf::rotor_cs_apply_bwd(n, cs, y, gy, clf::dense_ld(n), gx, g_cs, batch, ws, ws_bytes, stream);
+}
+
+int clf_rotor_cs_apply_bwd_ld(int n, const float* cs, const float* y, const float* gy, int64_t ldg, float* gx,
+                              float* g_cs, int64_t batch, void* ws, size_t ws_bytes, void* stream) {
+    clf::clear_error();
+    return clf::rotor_cs_apply_bwd(n, cs, y, gy, ldg, gx, g_cs, batch, ws, ws_bytes, stream);
 }
 
 int clf_rotor_cs_compile_bwd(int n, const float* biv, const float* g_cs, float* g_biv, void* stream) {
@@ -300,7 +322,15 @@ int clf_product_bcast_bwd(int op, int side, int n, uint32_t neg_mask, uint32_t n
                           const float* w, const float* gy, float* gx, float* gw, int64_t batch, void* ws,
                           size_t ws_bytes, void* stream) {
     clf::clear_error();
-    return clf::bcast_bwd(op, side, n, neg_mask, null_mask, x, w, gy, gx, gw, batch, ws, ws_bytes, stream);
+    return clf::bcast_bwd(op, side, n, neg_mask, null_mask, x, w, gy, clf::dense_ld(n), gx, gw, batch, ws, ws_bytes,
+                          stream);
+}
+
+int clf_product_bcast_bwd_ld(int op, int side, int n, uint32_t neg_mask, uint32_t null_mask, const float* x,
+                             const float* w, const float* gy, int64_t ldg, float* gx, float* gw, int64_t batch,
+                             void* ws, size_t ws_bytes, void* stream) {
+    clf::clear_error();
+    return clf::bcast_bwd(op, side, n, neg_mask, null_mask, x, w, gy, ldg, gx, gw, batch, ws, ws_bytes, stream);
 }
 
 size_t clf_product_bcast_bwd_noalloc_scratch_bytes(void) { return clf::bcast_scratch_bytes(); }
@@ -309,7 +339,8 @@ int clf_product_bcast_bwd_noalloc(int op, int side, int n, uint32_t neg_mask, ui
                                   const float* w, const float* gy, float* gx, float* gw, int64_t batch,
                                   void* stream) {
     clf::clear_error();
-    return clf::bcast_bwd_noalloc(op, side, n, neg_mask, null_mask, x, w, gy, gx, gw, batch, stream);
+    return clf::bcast_bwd_noalloc(op, side, n, neg_mask, null_mask, x, w, gy, clf::dense_ld(n), gx, gw, batch,
+                                  stream);
 }
 
 }  // extern "C"

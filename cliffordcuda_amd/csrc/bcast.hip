@@ -33,9 +33,10 @@ constexpr int kBcastMinN = 7;  // D >= 128: whole 128-wide tiles
 // x^T gy). Both tiles are stored k-major in LDS exactly as they sit in HBM;
 // rows past the split's end are loaded clamped and zeroed (no branches). The
 // next chunk is prefetched into registers while the current one is consumed.
+// ldb: floats between the k-rows of Bm (N, or 0 for one row broadcast over K)
 __global__ __launch_bounds__(256) void gemm_tn_kernel(const float* __restrict__ A, const float* __restrict__ Bm,
                                                        float* __restrict__ C, int M, int N, long long K,
-                                                       long long k_per_split) {
+                                                       long long k_per_split, long long ldb) {
     __shared__ float As[GBK][GBM + GPAD];
     __shared__ float Bs[GBK][GBN + GPAD];
     const int m_base = blockIdx.x * GBM;
@@ -64,7 +65,7 @@ __global__ __launch_bounds__(256) void gemm_tn_kernel(const float* __restrict__ 
         const bool ok = kr < k_end;                                                        \
         const long long kc = ok ? kr : (k_end - 1);                                        \
         ra##P = *reinterpret_cast<const float4*>(A + kc * M + m_base + col4);              \
-        rb##P = *reinterpret_cast<const float4*>(Bm + kc * N + n_base + col4);             \
+        rb##P = *reinterpret_cast<const float4*>(Bm + kc * ldb + n_base + col4);           \
         if (!ok) {                                                                         \
             ra##P = make_float4(0.f, 0.f, 0.f, 0.f);                                       \
             rb##P = make_float4(0.f, 0.f, 0.f, 0.f);                                       \
@@ -120,8 +121,10 @@ __global__ __launch_bounds__(256) void gemm_tn_kernel(const float* __restrict__ 
 // 0-31 and k = 8kb + 4 + s on lanes 32-63; A and B use the same permutation).
 // The next K chunk is loaded into registers while the current one is consumed.
 constexpr int NBK = 32, NPAD = 4;
+// lda: floats between the rows of A (K, or 0 for one row broadcast over M)
 __global__ __launch_bounds__(256) void gemm_nn_kernel(const float* __restrict__ A, const float* __restrict__ Bt,
-                                                       float* __restrict__ C, long long M, int N, int K) {
+                                                       float* __restrict__ C, long long M, int N, int K,
+                                                       long long lda) {
     __shared__ float As[GBM][NBK + NPAD];
     __shared__ float Bs[GBN][NBK + NPAD];
     const long long m_base = (long long)blockIdx.x * GBM;
@@ -145,7 +148,7 @@ __global__ __launch_bounds__(256) void gemm_nn_kernel(const float* __restrict__ 
     {                                                                                                         \
         /* rows past M read row M-1 (always valid); their results are never stored */                  \
         const long long gm = (m_base + (P) * 32 + lrow) < M ? (m_base + (P) * 32 + lrow) : (M - 1);          \
-        ra##P = *reinterpret_cast<const float4*>(A + gm * K + (K0) + lk);                                    \
+        ra##P = *reinterpret_cast<const float4*>(A + gm * lda + (K0) + lk);                                  \
         rb##P = *reinterpret_cast<const float4*>(Bt + (long long)(n_base + (P) * 32 + lrow) * K + (K0) + lk);   \
     }
 #define CLF_NN_FETCH(K0) CLF_NN_FETCH1(0, K0) CLF_NN_FETCH1(1, K0) CLF_NN_FETCH1(2, K0) CLF_NN_FETCH1(3, K0)
@@ -264,8 +267,8 @@ bool rep_bcast_applicable(int op, int n, uint32_t neg, uint32_t nul);
 size_t rep_bcast_ws_floats(int64_t batch);
 int rep_bcast_fwd(int side, int n, uint32_t neg, const float* x, const float* w, float* y, int64_t batch,
                   void* stream);
-int rep_bcast_bwd(int side, int n, uint32_t neg, const float* x, const float* w, const float* gy, float* gx, float* gw,
-                  int64_t batch, float* ws, void* stream);
+int rep_bcast_bwd(int side, int n, uint32_t neg, const float* x, const float* w, const float* gy, int64_t ldg,
+                  float* gx, float* gw, int64_t batch, float* ws, void* stream);
 
 static int bcast_splits(int64_t batch, int cap = 128) {
     long long s = (batch + 2047) / 2048;
@@ -301,15 +304,16 @@ static int check_bcast(int op, int side, int n, uint32_t neg, uint32_t nul, int6
 }
 
 static void launch_tn(const float* A, const float* B, float* C, int D, long long K, long long kps, int splits,
-                      hipStream_t s) {
+                      hipStream_t s, long long ldb) {
     const dim3 grid((unsigned)(D / GBM), (unsigned)(D / GBN), (unsigned)splits);
-    hipLaunchKernelGGL(gemm_tn_kernel, grid, dim3(256), 0, s, A, B, C, D, D, K, kps);
+    hipLaunchKernelGGL(gemm_tn_kernel, grid, dim3(256), 0, s, A, B, C, D, D, K, kps, ldb);
 }
 
-// C = A * Bt^T, A (rows x D), Bt (D x D) given transposed
-static void launch_nn(const float* A, const float* Bt, float* C, long long rows, int D, hipStream_t s) {
+// C = A * Bt^T, A (rows x D, rows lda apart), Bt (D x D) given transposed
+static void launch_nn(const float* A, const float* Bt, float* C, long long rows, int D, hipStream_t s,
+                      long long lda) {
     const dim3 grid((unsigned)((rows + GBM - 1) / GBM), (unsigned)(D / GBN));
-    hipLaunchKernelGGL(gemm_nn_kernel, grid, dim3(256), 0, s, A, Bt, C, rows, D, D);
+    hipLaunchKernelGGL(gemm_nn_kernel, grid, dim3(256), 0, s, A, Bt, C, rows, D, D, lda);
 }
 
 int bcast_fwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w, float* y,
@@ -330,15 +334,17 @@ int bcast_fwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* 
     float* MwT = (float*)ws;
     hipLaunchKernelGGL(bcast_build_kernel, dim3((unsigned)((D * D + 255) / 256)), dim3(256), 0, s, op, side, n, neg,
                        nul, w, (float*)nullptr, MwT);
-    launch_nn(x, MwT, y, batch, D, s);
+    launch_nn(x, MwT, y, batch, D, s, D);
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }
 
 // Argument checks shared by both backward entry points (no HIP call).
+// gy's rows are ldg floats apart: 2^n, or 0 for one row broadcast over the batch
 static int check_bcast_bwd_args(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w,
-                                const float* gy, float* gx, float* gw, int64_t batch) {
+                                const float* gy, int64_t ldg, float* gx, float* gw, int64_t batch) {
     if (int rc = check_bcast(op, side, n, neg, nul, batch)) return rc;
+    if (ldg != 0 && ldg != (1LL << n)) return set_error(CLF_ERR_ARG, "gy row stride must be 0 or 2^n");
     if (!gx && !gw) return CLF_OK;
     if (!w || (batch > 0 && (!gy || (gw && !x)))) return set_error(CLF_ERR_ARG, "null pointer argument");
     if ((((uintptr_t)x) | ((uintptr_t)gy) | ((uintptr_t)gx)) & 15u)
@@ -351,9 +357,10 @@ static int check_bcast_bwd_args(int op, int side, int n, uint32_t neg, uint32_t 
 // matrix), then `splits` partial products of x^T gy and their sum G; the split
 // count is at most max_splits.
 static int bcast_bwd_launch(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w,
-                            const float* gy, float* gx, float* gw, int64_t batch, float* ws, int max_splits,
-                            void* stream) {
-    if (rep_bcast_applicable(op, n, neg, nul)) return rep_bcast_bwd(side, n, neg, x, w, gy, gx, gw, batch, ws, stream);
+                            const float* gy, int64_t ldg, float* gx, float* gw, int64_t batch, float* ws,
+                            int max_splits, void* stream) {
+    if (rep_bcast_applicable(op, n, neg, nul))
+        return rep_bcast_bwd(side, n, neg, x, w, gy, ldg, gx, gw, batch, ws, stream);
     hipStream_t s = (hipStream_t)stream;
     const int D = 1 << n;
     const size_t DD = (size_t)D * D;
@@ -364,13 +371,13 @@ static int bcast_bwd_launch(int op, int side, int n, uint32_t neg, uint32_t nul,
         float* Mw = ws;
         hipLaunchKernelGGL(bcast_build_kernel, dim3((unsigned)((DD + 255) / 256)), dim3(256), 0, s, op, side, n, neg,
                            nul, w, Mw, (float*)nullptr);
-        launch_nn(gy, Mw, gx, batch, D, s);
+        launch_nn(gy, Mw, gx, batch, D, s, ldg);
     }
     if (gw) {
         if (batch > 0) {
             const long long kps = ((batch + splits - 1) / splits + GBK - 1) / GBK * GBK;
             const int used = (int)((batch + kps - 1) / kps);
-            launch_tn(x, gy, parts, D, batch, kps, used, s);
+            launch_tn(x, gy, parts, D, batch, kps, used, s, ldg);
             hipLaunchKernelGGL(bcast_reduce_kernel, dim3((unsigned)((DD / 4 + 255) / 256)), dim3(256), 0, s,
                                reinterpret_cast<const float4*>(parts), used, (int)(DD / 4), reinterpret_cast<float4*>(G));
         } else {
@@ -384,8 +391,8 @@ static int bcast_bwd_launch(int op, int side, int n, uint32_t neg, uint32_t nul,
 }
 
 int bcast_bwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w, const float* gy,
-              float* gx, float* gw, int64_t batch, void* ws, size_t ws_bytes, void* stream) {
-    if (int rc = check_bcast_bwd_args(op, side, n, neg, nul, x, w, gy, gx, gw, batch)) return rc;
+              int64_t ldg, float* gx, float* gw, int64_t batch, void* ws, size_t ws_bytes, void* stream) {
+    if (int rc = check_bcast_bwd_args(op, side, n, neg, nul, x, w, gy, ldg, gx, gw, batch)) return rc;
     if (!gx && !gw) return CLF_OK;
     if (!ws) return set_error(CLF_ERR_ARG, "null pointer argument");
     if (((uintptr_t)ws) & 15u) return set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
@@ -394,7 +401,7 @@ int bcast_bwd(int op, int side, int n, uint32_t neg, uint32_t nul, const float* 
                                                 " bytes required");
     if (rep_bcast_applicable(op, n, neg, nul) && rep_bcast_ws_floats(batch) * sizeof(float) > ws_bytes)
         return set_error(CLF_ERR_WORKSPACE, "workspace too small for the weight-gradient partials");
-    return bcast_bwd_launch(op, side, n, neg, nul, x, w, gy, gx, gw, batch, (float*)ws, 128, stream);
+    return bcast_bwd_launch(op, side, n, neg, nul, x, w, gy, ldg, gx, gw, batch, (float*)ws, 128, stream);
 }
 
 // ---- allocation-free backward ------------------------------------------------
@@ -445,8 +452,8 @@ static int noalloc_max_splits(int n) {
 }
 
 int bcast_bwd_noalloc(int op, int side, int n, uint32_t neg, uint32_t nul, const float* x, const float* w,
-                      const float* gy, float* gx, float* gw, int64_t batch, void* stream) {
-    if (int rc = check_bcast_bwd_args(op, side, n, neg, nul, x, w, gy, gx, gw, batch)) return rc;
+                      const float* gy, int64_t ldg, float* gx, float* gw, int64_t batch, void* stream) {
+    if (int rc = check_bcast_bwd_args(op, side, n, neg, nul, x, w, gy, ldg, gx, gw, batch)) return rc;
     if (!gx && !gw) return CLF_OK;
     size_t need;
     if (rep_bcast_applicable(op, n, neg, nul)) {
@@ -463,7 +470,8 @@ int bcast_bwd_noalloc(int op, int side, int n, uint32_t neg, uint32_t nul, const
                                                 "allocation-free backward has " + std::to_string(kBcastScratchBytes));
     float* ws = nullptr;
     if (int rc = scratch_address(&ws)) return rc;
-    return bcast_bwd_launch(op, side, n, neg, nul, x, w, gy, gx, gw, batch, ws, noalloc_max_splits(n), stream);
+    return bcast_bwd_launch(op, side, n, neg, nul, x, w, gy, ldg, gx, gw, batch, ws, noalloc_max_splits(n),
+                            stream);
 }
 
 }  // namespace clf

@@ -329,6 +329,7 @@ __device__ __forceinline__ void gb_block_dispatch(float (&acc)[16], const float 
 
 struct BlkParams {
     long long batch;
+    long long ldg4;  // float4 between the rows of the upstream gradient: 1 << (n - 2), or 0 (one row for all)
     int n;          // algebra dimension, 4 <= n <= kMaxN (20)
     unsigned negh;  // metric masks >> 4
     unsigned nulh;
@@ -346,7 +347,9 @@ struct BlkParams {
 template <int NOPS>
 __device__ __forceinline__ void stage_rows(float4* __restrict__ lds, const float4* __restrict__ s0,
                                            const float4* __restrict__ s1, const float4* __restrict__ s2,
-                                           long long row0, int nrows, int n) {
+                                           long long row0, int nrows, int n, long long m2 = -1) {
+    // m2 masks s2's float4 index: -1 (packed like s0 and s1) or 2^(n-2) - 1
+    // (one row for all rows: the row offset drops out)
     const int d4_log = n - 2;
     const int D4 = 1 << d4_log;
     const int total = nrows << d4_log;
@@ -359,10 +362,10 @@ __device__ __forceinline__ void stage_rows(float4* __restrict__ lds, const float
         const float4 b0 = s1[g0 + i0], b1 = s1[g0 + c1], b2 = s1[g0 + c2], b3 = s1[g0 + c3];
         float4 e0, e1, e2, e3;
         if constexpr (NOPS == 3) {
-            e0 = s2[g0 + i0];
-            e1 = s2[g0 + c1];
-            e2 = s2[g0 + c2];
-            e3 = s2[g0 + c3];
+            e0 = s2[(g0 + i0) & m2];
+            e1 = s2[(g0 + c1) & m2];
+            e2 = s2[(g0 + c2) & m2];
+            e3 = s2[(g0 + c3) & m2];
         }
         auto put = [&](int idx, const float4& x, const float4& y, const float4& z) {
             const int r = idx >> d4_log;
@@ -500,7 +503,7 @@ __global__ __launch_bounds__(256) void prod_bwd_blk(const float* __restrict__ A,
     const long long row0 = (long long)blockIdx.x * P.rows_per_wg;
     const int nrows = (int)((P.batch - row0) < P.rows_per_wg ? (P.batch - row0) : P.rows_per_wg);
     stage_rows<3>(lds, reinterpret_cast<const float4*>(A), reinterpret_cast<const float4*>(B),
-                  reinterpret_cast<const float4*>(GC), row0, nrows, n);
+                  reinterpret_cast<const float4*>(GC), row0, nrows, n, P.ldg4 ? -1LL : (1LL << (n - 2)) - 1);
     __syncthreads();
     const int r = threadIdx.x >> P.lpr_log;
     if (r >= nrows) return;
@@ -1085,8 +1088,10 @@ struct BalPre {
     float4 v[4];
 };
 
+// cmask masks the float4 index: -1 (packed rows) or 2^(n-2) - 1 (one row for
+// all rows, an upstream gradient broadcast over the batch)
 __device__ __forceinline__ BalPre bal_fetch(const float* __restrict__ src, long long grp, long long batch, int n,
-                                            int lane) {
+                                            int lane, long long cmask = -1) {
     BalPre p;
     const int d4_log = n - 2;
     const long long last = (batch << d4_log) - (1LL << d4_log);  // first chunk of the last row
@@ -1094,7 +1099,7 @@ __device__ __forceinline__ BalPre bal_fetch(const float* __restrict__ src, long 
     for (int i = 0; i < 4; ++i) {
         long long c = grp * kBalGroupF4 + lane + 64 * i;
         if (c >= (batch << d4_log)) c = last + (c & ((1LL << d4_log) - 1));
-        p.v[i] = reinterpret_cast<const float4*>(src)[c];
+        p.v[i] = reinterpret_cast<const float4*>(src)[c & cmask];
     }
     return p;
 }
@@ -1225,12 +1230,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     BalPre pa, pb;
     if (want_b) pa = bal_fetch(A, grp, P.batch, n, lane);
     if (want_a) pb = bal_fetch(B, grp, P.batch, n, lane);
-    BalPre pg = bal_fetch(GC, grp, P.batch, n, lane);
+    const long long gmask = P.ldg4 ? -1LL : (1LL << (n - 2)) - 1;
+    BalPre pg = bal_fetch(GC, grp, P.batch, n, lane, gmask);
     for (; grp < ngrp; grp += gstride) {
         const long long row = grp * R + r;
         const bool row_ok = row < P.batch;
         bal_stage(sg, pg, n, lane);
-        pg = bal_fetch(GC, grp + gstride, P.batch, n, lane);
+        pg = bal_fetch(GC, grp + gstride, P.batch, n, lane, gmask);
         if (want_a) {  // uniform: a kernel argument
             bal_stage(sb, pb, n, lane);
             pb = bal_fetch(B, grp + gstride, P.batch, n, lane);
@@ -1375,7 +1381,7 @@ __global__ __launch_bounds__(256) void prod_bwd_tiled(const float* __restrict__ 
         const bool want_a = GA != nullptr, want_b = GB != nullptr;
         const float4* arow = reinterpret_cast<const float4*>(A) + (row << (n - 2));
         const float4* brow = reinterpret_cast<const float4*>(B) + (row << (n - 2));
-        const float4* grow = reinterpret_cast<const float4*>(GC) + (row << (n - 2));
+        const float4* grow = reinterpret_cast<const float4*>(GC) + row * P.ldg4;
         const unsigned pi_h = cross_pi<OP>(h, P.nm1);
         float ga[16], gb[16];
 #pragma unroll
@@ -1459,7 +1465,7 @@ __global__ __launch_bounds__(256) void prod_fwd_generic(int op, int n, unsigned 
 // gb[k] = sum_i sigma(i, k) a[i] gf[i^k]   (which == 1)
 __global__ __launch_bounds__(256) void prod_bwd_generic(int op, int n, unsigned neg, unsigned nul, int which,
                                                          const float* __restrict__ X, const float* __restrict__ GC,
-                                                         float* __restrict__ OUT, long long batch) {
+                                                         long long ldg, float* __restrict__ OUT, long long batch) {
     const unsigned D = 1u << n;
     const long long total = batch << n;
     for (long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
@@ -1467,7 +1473,7 @@ __global__ __launch_bounds__(256) void prod_bwd_generic(int op, int n, unsigned 
         const long long row = idx >> n;
         const unsigned k = (unsigned)(idx & (D - 1));
         const float* x = X + (row << n);
-        const float* gc = GC + (row << n);
+        const float* gc = GC + row * ldg;  // ldg = 2^n, or 0 for one row broadcast over the batch
         float acc = 0.f;
         for (unsigned u = 0; u < D; ++u) {
             const int s = which == 0 ? full_sign(op, n, k, u, neg, nul) : full_sign(op, n, u, k, neg, nul);
@@ -1616,8 +1622,8 @@ static void launch_bwd(dim3 g, dim3 b, size_t lds, hipStream_t s, const float* A
 bool rep_applicable(int op, int n, uint32_t neg, uint32_t nul);
 bool rep_disabled_by_env();
 int rep_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64_t batch, void* stream);
-int rep_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc, float* ga, float* gb, int64_t batch,
-            void* stream);
+int rep_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc, int64_t ldg, float* ga, float* gb,
+            int64_t batch, void* stream);
 
 // The geometric product of real-matrix-type signatures goes through the matrix
 // representation unless CLF_GEOM_PATH=direct asks for the per-term kernels.
@@ -1695,20 +1701,24 @@ int product_fwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
     return CLF_OK;
 }
 
+// gc's rows are ldg floats apart: 2^n (packed) or 0 (one row broadcast over
+// the batch, e.g. the gradient of a sum)
 int product_bwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const float* b, const float* gc,
-                float* ga, float* gb, int64_t batch, void* stream) {
+                int64_t ldg, float* ga, float* gb, int64_t batch, void* stream) {
     int rc = check_common(op, n, neg, nul, batch);
     if (rc) return rc;
+    if (ldg != 0 && ldg != (1LL << n)) return set_error(CLF_ERR_ARG, "gc row stride must be 0 or 2^n");
     if (batch == 0 || (!ga && !gb)) return CLF_OK;
     if (!a || !b || !gc) return set_error(CLF_ERR_ARG, "null pointer argument");
     if ((ga && (ga == a || ga == b || ga == gc)) || (gb && (gb == a || gb == b || gb == gc)) || (ga && ga == gb))
         return set_error(CLF_ERR_ARG, "gradient outputs must not alias inputs or each other");
     if ((((uintptr_t)a) | ((uintptr_t)b) | ((uintptr_t)gc) | ((uintptr_t)ga) | ((uintptr_t)gb)) & 15u)
         return set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
-    if (use_rep(op, n, neg, nul)) return rep_bwd(n, neg, a, b, gc, ga, gb, batch, stream);
+    if (use_rep(op, n, neg, nul)) return rep_bwd(n, neg, a, b, gc, ldg, ga, gb, batch, stream);
     hipStream_t s = (hipStream_t)stream;
     BlkParams P{};
     P.batch = batch;
+    P.ldg4 = ldg >> 2;
     bool ln = false;
     dim3 g, bl;
     size_t lds = 0;
@@ -1760,11 +1770,11 @@ int product_bwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
         const long long want = (total + 255) / 256;
         const unsigned blocks = (unsigned)(want < kMaxGrid ? want : kMaxGrid);
         if (ga)
-            hipLaunchKernelGGL(prod_bwd_generic, dim3(blocks), dim3(256), 0, s, op, n, neg, nul, 0, b, gc, ga,
-                               (long long)batch);
+            hipLaunchKernelGGL(prod_bwd_generic, dim3(blocks), dim3(256), 0, s, op, n, neg, nul, 0, b, gc,
+                               (long long)ldg, ga, (long long)batch);
         if (gb)
-            hipLaunchKernelGGL(prod_bwd_generic, dim3(blocks), dim3(256), 0, s, op, n, neg, nul, 1, a, gc, gb,
-                               (long long)batch);
+            hipLaunchKernelGGL(prod_bwd_generic, dim3(blocks), dim3(256), 0, s, op, n, neg, nul, 1, a, gc,
+                               (long long)ldg, gb, (long long)batch);
     }
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;

@@ -127,7 +127,8 @@ struct Pre {
 
 template <int M>
 __device__ __forceinline__ Pre<RowGroup<M>::CH> fetch_group(const float* __restrict__ src, long long row0,
-                                                            long long batch, int lane) {
+                                                            long long batch, int lane,
+                                                            long long ld = RowGroup<M>::D) {
     constexpr int D = RowGroup<M>::D, CH = RowGroup<M>::CH;
     Pre<CH> p;
 #pragma unroll
@@ -136,7 +137,7 @@ __device__ __forceinline__ Pre<RowGroup<M>::CH> fetch_group(const float* __restr
         const int rl = (f * 4) / D;           // row inside the group
         long long row = row0 + rl;
         row = row < batch ? row : batch - 1;  // rows past the end re-read the last row; never stored
-        p.v[j] = reinterpret_cast<const float4*>(src + row * D)[(f * 4 - rl * D) / 4];
+        p.v[j] = reinterpret_cast<const float4*>(src + (row & row_mask(ld)) * D)[(f * 4 - rl * D) / 4];
     }
     return p;
 }
@@ -217,8 +218,9 @@ __global__ __launch_bounds__(256) void rep_fwd_kernel(const float* __restrict__ 
 
 template <int LOGM>
 __global__ __launch_bounds__(256) void rep_bwd_kernel(const float* __restrict__ A, const float* __restrict__ B,
-                                                       const float* __restrict__ GC, float* __restrict__ GA,
-                                                       float* __restrict__ GB, long long batch, RepTable T) {
+                                                       const float* __restrict__ GC, long long ldg,
+                                                       float* __restrict__ GA, float* __restrict__ GB, long long batch,
+                                                       RepTable T) {
     constexpr int M = 1 << LOGM;
     constexpr int D = M * M;
     constexpr int RPW = RowGroup<M>::RPW;
@@ -239,14 +241,14 @@ __global__ __launch_bounds__(256) void rep_bwd_kernel(const float* __restrict__ 
     long long row0 = ((long long)blockIdx.x * 4 + wave) * RPW;
     Pre<CH> pa = fetch_group<M>(A, row0, batch, lane);
     Pre<CH> pb = fetch_group<M>(B, row0, batch, lane);
-    Pre<CH> pg = fetch_group<M>(GC, row0, batch, lane);
+    Pre<CH> pg = fetch_group<M>(GC, row0, batch, lane, ldg);
     for (; row0 < batch; row0 += waves_total * RPW) {
         stage_group<CH>(sa, pa, lane);
         stage_group<CH>(sb, pb, lane);
         stage_group<CH>(sg, pg, lane);
         pa = fetch_group<M>(A, row0 + waves_total * RPW, batch, lane);
         pb = fetch_group<M>(B, row0 + waves_total * RPW, batch, lane);
-        pg = fetch_group<M>(GC, row0 + waves_total * RPW, batch, lane);
+        pg = fetch_group<M>(GC, row0 + waves_total * RPW, batch, lane, ldg);
         wave_lds_sync();
         float* ra = sa + rl * D;
         float* rb = sb + rl * D;
@@ -399,8 +401,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
 // second wait, dB right after the next group's first wait.
 template <bool NT, bool WA, bool WB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void rep16_bwd_kernel(
-    const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ GC, float* __restrict__ GA,
-    float* __restrict__ GB, long long batch, RepTable T) {
+    const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ GC, long long ldg,
+    float* __restrict__ GA, float* __restrict__ GB, long long batch, RepTable T) {
     // per wave: gc | b, then a over b | scratch for each gradient's relayout and
     // its rows in blade order; only two converted operands are live at a time
     __shared__ float lds[4][2 * 4 * 256 + kRelayoutFloats];
@@ -421,7 +423,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void r
     // gc and b of a group are loaded while the previous group's dB runs, a
     // while the group's dA runs
     Pre16 pb = fetch16<NT>(B, row0, batch, lane);
-    Pre16 pg = fetch16<NT>(GC, row0, batch, lane);
+    Pre16 pg = fetch16<NT>(GC, row0, batch, lane, ldg);
     for (; row0 < batch; row0 += stride) {
         // the table values are re-derived where they are used rather than kept
         // in registers across the loop (register pressure sets the occupancy)
@@ -449,7 +451,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void r
         }
         wave_lds_sync();
         stage16(s1, pa, lane, oddc);
-        pg = fetch16<NT>(GC, row0 + stride, batch, lane);
+        pg = fetch16<NT>(GC, row0 + stride, batch, lane, ldg);
         pb = fetch16<NT>(B, row0 + stride, batch, lane);
         if (WA) store16<NT>(GA, sr, row0, batch, lane, oddc);
         wave_lds_sync();
@@ -548,8 +550,8 @@ __global__ __launch_bounds__(256) void rep16_bcast_fwd_kernel(const float* __res
 // parts[blockIdx.x * 256 + r * 16 + c]: the workgroup's sum of the 16x16 weight-gradient products
 template <int SIDE, bool NT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void rep16_bcast_bwd_kernel(
-    const float* __restrict__ X, const float* __restrict__ W, const float* __restrict__ GY, float* __restrict__ GX,
-    float* __restrict__ parts, long long batch, RepTable T) {
+    const float* __restrict__ X, const float* __restrict__ W, const float* __restrict__ GY, long long ldg,
+    float* __restrict__ GX, float* __restrict__ parts, long long batch, RepTable T) {
     __shared__ float lds[4][2 * 4 * 256];  // per wave: staged x | staged gy; later relayout, then gx rows
     static_assert(2 * 4 * 256 >= kRelayoutFloats, "relayout must fit the wave's LDS slots");
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -572,7 +574,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void r
     const long long stride = (long long)gridDim.x * 4 * 4;
     long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
     Pre16 px = fetch16<NT>(X, row0, batch, lane);
-    Pre16 pg = fetch16<NT>(GY, row0, batch, lane);
+    Pre16 pg = fetch16<NT>(GY, row0, batch, lane, ldg);
     for (; row0 < batch; row0 += stride) {
         // the table values are re-derived where they are used rather than kept
         // in registers across the loop (register pressure sets the occupancy)
@@ -604,7 +606,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void r
             else
                 accw = mfma_chain_pre<true, true>(accw, wgw, wx, std::make_integer_sequence<unsigned, 16>{});
         }
-        pg = fetch16<NT>(GY, row0 + stride, batch, lane);
+        pg = fetch16<NT>(GY, row0 + stride, batch, lane, ldg);
         wave_lds_sync();
         if (want_x) {
             float wgx[16];
@@ -737,11 +739,11 @@ bool rep_table(int n, uint32_t neg, RepTable& T) {
 bool split_applicable(int op, int n, uint32_t neg, uint32_t nul);
 bool rep7_applicable(uint32_t neg);
 int rep7_fwd(uint32_t neg, const float* a, const float* b, float* c, int64_t batch, void* stream);
-int rep7_bwd(uint32_t neg, const float* a, const float* b, const float* gc, float* ga, float* gb, int64_t batch,
-             void* stream);
+int rep7_bwd(uint32_t neg, const float* a, const float* b, const float* gc, int64_t ldg, float* ga, float* gb,
+             int64_t batch, void* stream);
 int split_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64_t batch, void* stream);
-int split_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc, float* ga, float* gb,
-              int64_t batch, void* stream);
+int split_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc, int64_t ldg, float* ga,
+              float* gb, int64_t batch, void* stream);
 
 // The matrix path serves the geometric product when the signature allows it
 // (real type, n = 4, 6, 8; every non-degenerate n = 7 signature; split type
@@ -793,26 +795,26 @@ int rep_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64
     return CLF_OK;
 }
 
-int rep_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc, float* ga, float* gb, int64_t batch,
-            void* stream) {
-    if (n == 9 || n == 10) return split_bwd(n, neg, a, b, gc, ga, gb, batch, stream);
-    if (n == 7) return rep7_bwd(neg, a, b, gc, ga, gb, batch, stream);
+int rep_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc, int64_t ldg, float* ga, float* gb,
+            int64_t batch, void* stream) {
+    if (n == 9 || n == 10) return split_bwd(n, neg, a, b, gc, ldg, ga, gb, batch, stream);
+    if (n == 7) return rep7_bwd(neg, a, b, gc, ldg, ga, gb, batch, stream);
     RepTable T;
     if (!rep_table(n, neg, T)) return set_error(CLF_ERR_UNSUPPORTED, "signature has no real matrix representation");
     hipStream_t s = (hipStream_t)stream;
     const long long want = rep_blocks(n, batch);
     switch (n) {
-        case 4: hipLaunchKernelGGL((rep_bwd_kernel<2>), CLF_REP_GRID(rep_bwd_kernel<2>), dim3(256), 0, s, a, b, gc, ga,
-                                   gb, (long long)batch, T); break;
-        case 6: hipLaunchKernelGGL((rep_bwd_kernel<3>), CLF_REP_GRID(rep_bwd_kernel<3>), dim3(256), 0, s, a, b, gc, ga,
-                                   gb, (long long)batch, T); break;
+        case 4: hipLaunchKernelGGL((rep_bwd_kernel<2>), CLF_REP_GRID(rep_bwd_kernel<2>), dim3(256), 0, s, a, b, gc,
+                                   (long long)ldg, ga, gb, (long long)batch, T); break;
+        case 6: hipLaunchKernelGGL((rep_bwd_kernel<3>), CLF_REP_GRID(rep_bwd_kernel<3>), dim3(256), 0, s, a, b, gc,
+                                   (long long)ldg, ga, gb, (long long)batch, T); break;
         case 8:
             if (!ga && !gb) break;
             {
                 const bool nt = stream_nt((3 + (ga != nullptr) + (gb != nullptr)) * 1024.0 * (double)batch);
 #define CLF_REP16_BWD(NT, WA, WB)                                                                                 \
-    hipLaunchKernelGGL((rep16_bwd_kernel<NT, WA, WB>), dim3((unsigned)want), dim3(256), 0, s, a, b, gc, ga, gb,   \
-                       (long long)batch, T)
+    hipLaunchKernelGGL((rep16_bwd_kernel<NT, WA, WB>), dim3((unsigned)want), dim3(256), 0, s, a, b, gc,          \
+                       (long long)ldg, ga, gb, (long long)batch, T)
                 if (ga && gb) {
                     if (nt) CLF_REP16_BWD(true, true, true);
                     else CLF_REP16_BWD(false, true, true);
@@ -884,8 +886,8 @@ int rep_bcast_fwd(int side, int n, uint32_t neg, const float* x, const float* w,
 }
 
 // ws: at least rep_bcast_ws_floats(batch) floats when gw != nullptr
-int rep_bcast_bwd(int side, int n, uint32_t neg, const float* x, const float* w, const float* gy, float* gx, float* gw,
-                  int64_t batch, float* ws, void* stream) {
+int rep_bcast_bwd(int side, int n, uint32_t neg, const float* x, const float* w, const float* gy, int64_t ldg,
+                  float* gx, float* gw, int64_t batch, float* ws, void* stream) {
     RepTable T;
     if (n != 8 || !rep_table(n, neg, T)) return set_error(CLF_ERR_UNSUPPORTED, "no m = 16 matrix representation");
     hipStream_t s = (hipStream_t)stream;
@@ -894,8 +896,8 @@ int rep_bcast_bwd(int side, int n, uint32_t neg, const float* x, const float* w,
     if (batch > 0) {
         const bool nt = stream_nt((1 + (gw != nullptr) + (gx != nullptr)) * 1024.0 * (double)batch);
 #define CLF_BCAST_BWD(SIDE, NT)                                                                                     \
-    hipLaunchKernelGGL((rep16_bcast_bwd_kernel<SIDE, NT>), dim3((unsigned)nb), dim3(256), 0, s, x, w, gy, gx, parts, \
-                       (long long)batch, T)
+    hipLaunchKernelGGL((rep16_bcast_bwd_kernel<SIDE, NT>), dim3((unsigned)nb), dim3(256), 0, s, x, w, gy,          \
+                       (long long)ldg, gx, parts, (long long)batch, T)
         if (side == 0) {
             if (nt) CLF_BCAST_BWD(0, true);
             else CLF_BCAST_BWD(0, false);

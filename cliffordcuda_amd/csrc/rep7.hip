@@ -56,15 +56,17 @@ struct Pre7 {
     float4 v[2];
 };
 
+// ld: floats between rows (128 packed; 0 for one row broadcast over the batch)
 template <bool NT>
-__device__ __forceinline__ Pre7 fetch7(const float* __restrict__ src, long long row0, long long batch, int lane) {
+__device__ __forceinline__ Pre7 fetch7(const float* __restrict__ src, long long row0, long long batch, int lane,
+                                       long long ld = kRep7Dim) {
     Pre7 p;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int c = lane + 64 * j;
         long long row = row0 + (c >> 5);
         row = row < batch ? row : batch - 1;
-        const float4* q = reinterpret_cast<const float4*>(src + row * kRep7Dim) + (c & 31);
+        const float4* q = reinterpret_cast<const float4*>(src + ((row & row_mask(ld)) << 7)) + (c & 31);
         p.v[j] = NT ? load_stream(q) : *q;
     }
     return p;
@@ -261,8 +263,8 @@ __global__ __launch_bounds__(256) void rep7_fwd_kernel(const float* __restrict__
 // slot, so few converted operands are live at once.
 template <bool PAIR, bool NT, bool WA, bool WB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void rep7_bwd_kernel(
-    const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ GC, float* __restrict__ GA,
-    float* __restrict__ GB, long long batch, Rep7Table T) {
+    const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ GC, long long ldg,
+    float* __restrict__ GA, float* __restrict__ GB, long long batch, Rep7Table T) {
     constexpr int D = PAIR ? 2 : 3;
     constexpr int L = 1 << D;
     __shared__ float lds[4][2 * kRep7GroupFloats + kRelayoutFloats];  // per wave: gc | b, then a | scratch
@@ -280,7 +282,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
     const long long rfirst = ((long long)blockIdx.x * 4 + wave) * 4;
     long long row0 = rfirst;
     Pre7 pb = fetch7<NT>(B, row0, batch, lane);
-    Pre7 pg = fetch7<NT>(GC, row0, batch, lane);
+    Pre7 pg = fetch7<NT>(GC, row0, batch, lane, ldg);
     for (; row0 < batch; row0 += stride) {
         // the table values are re-derived where they are used rather than kept
         // in registers across the loop (register pressure sets the occupancy)
@@ -311,7 +313,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
         }
         wave_lds_sync();
         stage7(sx, pa, lane, oddc);
-        pg = fetch7<NT>(GC, row0 + stride, batch, lane);
+        pg = fetch7<NT>(GC, row0 + stride, batch, lane, ldg);
         pb = fetch7<NT>(B, row0 + stride, batch, lane);
         if (WA) store7<NT>(GA, sr, row0, batch, lane, oddc);  // after this group's second wait
         wave_lds_sync();
@@ -516,8 +518,8 @@ int rep7_fwd(uint32_t neg, const float* a, const float* b, float* c, int64_t bat
     return CLF_OK;
 }
 
-int rep7_bwd(uint32_t neg, const float* a, const float* b, const float* gc, float* ga, float* gb, int64_t batch,
-             void* stream) {
+int rep7_bwd(uint32_t neg, const float* a, const float* b, const float* gc, int64_t ldg, float* ga, float* gb,
+             int64_t batch, void* stream) {
     Rep7Table T;
     if (!rep7_table(neg & 0x7fu, T)) return set_error(CLF_ERR_UNSUPPORTED, "no n = 7 matrix representation found");
     const bool pair = (host_popc(neg & 0x7fu) & 1) != 0;
@@ -526,7 +528,8 @@ int rep7_bwd(uint32_t neg, const float* a, const float* b, const float* gc, floa
     const bool nt = stream_nt((3 + (ga != nullptr) + (gb != nullptr)) * 512.0 * (double)batch);
     if (!ga && !gb) return CLF_OK;
 #define CLF_REP7_BWD(P, NT, WA, WB) \
-    hipLaunchKernelGGL((rep7_bwd_kernel<P, NT, WA, WB>), g, dim3(256), 0, s, a, b, gc, ga, gb, (long long)batch, T)
+    hipLaunchKernelGGL((rep7_bwd_kernel<P, NT, WA, WB>), g, dim3(256), 0, s, a, b, gc, (long long)ldg, ga, gb, \
+                       (long long)batch, T)
 #define CLF_REP7_BWD_W(P, NT)                 \
     do {                                      \
         if (ga && gb) CLF_REP7_BWD(P, NT, true, true);   \

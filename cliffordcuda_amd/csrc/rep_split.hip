@@ -246,6 +246,7 @@ struct FusedSplit {
     const float* Y;
     float* out;
     long long batch;
+    long long ldx, ldy;  // floats between rows: 1024, or 0 for one row broadcast over the batch
 };
 
 // gather_pair with a fresh opaque copy of the table entries, so that the
@@ -382,8 +383,8 @@ __global__ __launch_bounds__(64 * kFusedWaves) void split_fused_kernel(FusedSpli
     const long long g0 = (long long)blockIdx.x * kFusedWaves + wave;
     long long g = g0;
     float4 ax0, ax1, ax2, ax3, ay0, ay1, ay2, ay3;
-    CLF_SPLIT_FETCH(ax0, ax1, ax2, ax3, X0, 1024, 2 * g);
-    CLF_SPLIT_FETCH(ay0, ay1, ay2, ay3, Y0, 1024, 2 * g);
+    CLF_SPLIT_FETCH(ax0, ax1, ax2, ax3, X0, P.ldx, 2 * g);
+    CLF_SPLIT_FETCH(ay0, ay1, ay2, ay3, Y0, P.ldy, 2 * g);
     for (; g < ngroups; g += gstride) {
         unsigned m_x0 = mx0, m_y0 = my0, m_y0b = my0b, m_x1 = mx1, m_y1 = my1, m_y1b = my1b, mout = mo;
         asm volatile("" : "+v"(m_x0), "+v"(m_y0), "+v"(m_y0b), "+v"(m_x1), "+v"(m_y1), "+v"(m_y1b), "+v"(mout));
@@ -396,8 +397,8 @@ __global__ __launch_bounds__(64 * kFusedWaves) void split_fused_kernel(FusedSpli
         // stage 0: X0, Y0 (staged until the group ends)
         CLF_SPLIT_STAGE(sx0, ax0, ax1, ax2, ax3);
         CLF_SPLIT_STAGE(sy0, ay0, ay1, ay2, ay3);
-        CLF_SPLIT_FETCH(ax0, ax1, ax2, ax3, X1, 1024, 2 * g);
-        CLF_SPLIT_FETCH(ay0, ay1, ay2, ay3, Y1, 1024, 2 * g);
+        CLF_SPLIT_FETCH(ax0, ax1, ax2, ax3, X1, P.ldx, 2 * g);
+        CLF_SPLIT_FETCH(ay0, ay1, ay2, ay3, Y1, P.ldy, 2 * g);
         if (g != g0) {  // uniform: the previous group's rows wait in regions stage 0 does not touch
             if (KIND != 0) split_emit(base + RG::rows0 * 1024, P.out, g - gstride, batch, lane);
             split_emit(base + RG::rows1 * 1024, P.out + 512, g - gstride, batch, lane);
@@ -416,8 +417,8 @@ __global__ __launch_bounds__(64 * kFusedWaves) void split_fused_kernel(FusedSpli
         // stage 1: X1, Y1
         CLF_SPLIT_STAGE(sx1, ax0, ax1, ax2, ax3);
         CLF_SPLIT_STAGE(sy1, ay0, ay1, ay2, ay3);
-        CLF_SPLIT_FETCH(ax0, ax1, ax2, ax3, X0, 1024, 2 * (g + gstride));
-        CLF_SPLIT_FETCH(ay0, ay1, ay2, ay3, Y0, 1024, 2 * (g + gstride));
+        CLF_SPLIT_FETCH(ax0, ax1, ax2, ax3, X0, P.ldx, 2 * (g + gstride));
+        CLF_SPLIT_FETCH(ay0, ay1, ay2, ay3, Y0, P.ldy, 2 * (g + gstride));
         if constexpr (KIND == 0) split_emit(base + RG::rows0 * 1024, P.out, g, batch, lane);
         wave_lds_sync();
         if constexpr (KIND == 0) {
@@ -559,10 +560,13 @@ bool split_applicable(int op, int n, uint32_t neg, uint32_t nul) {
     return split_table(neg & 511u, T);
 }
 
+// ldx / ldy: floats between rows of X / Y (0: one row broadcast over the batch;
+// -1: the launch's ld_in)
 struct PairSpec {
     const float* X;
     const float* Y;
     unsigned flags;
+    long long ldx = -1, ldy = -1;
 };
 
 static int launch_pairs(const SplitTable& T, const PairSpec* ps, int npairs, long long ld_in, float* out,
@@ -572,8 +576,8 @@ static int launch_pairs(const SplitTable& T, const PairSpec* ps, int npairs, lon
         const PairSpec& q = ps[p < npairs ? p : 0];
         P.X[p] = q.X;
         P.Y[p] = q.Y;
-        P.ldx[p] = ld_in;
-        P.ldy[p] = ld_in;
+        P.ldx[p] = q.ldx < 0 ? ld_in : q.ldx;
+        P.ldy[p] = q.ldy < 0 ? ld_in : q.ldy;
         P.flags[p] = q.flags;
     }
     P.npairs = npairs;
@@ -597,8 +601,8 @@ static bool split_fused_enabled() { return !options().split_pairs; }
 
 template <int KIND>
 static void launch_fused(const SplitTable& T, const float* X, const float* Y, float* out, int64_t batch,
-                         hipStream_t s) {
-    FusedSplit P{X, Y, out, (long long)batch};
+                         hipStream_t s, long long ldx = 1024, long long ldy = 1024) {
+    FusedSplit P{X, Y, out, (long long)batch, ldx, ldy};
     const long long groups = (batch + 1) / 2;
     // grid rule of the pair sums: at most the resident workgroups
     const dim3 grid(resident_grid((const void*)split_fused_kernel<KIND>, 64 * kFusedWaves, 0,
@@ -625,34 +629,36 @@ int split_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int
     return CLF_OK;
 }
 
-int split_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc, float* ga, float* gb,
-              int64_t batch, void* stream) {
+// gc's rows are ldg floats apart: 2^n, or 0 for one row broadcast over the batch
+int split_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc, int64_t ldg, float* ga,
+              float* gb, int64_t batch, void* stream) {
     SplitTable T;
     if (!split_table(neg & 511u, T)) return set_error(CLF_ERR_UNSUPPORTED, "signature has no split representation");
     hipStream_t s = (hipStream_t)stream;
+    const long long lg = (long long)ldg;
     if (n == 9) {
         if (ga) {
-            const PairSpec p[1] = {{gc, b, kTransB}};
+            const PairSpec p[1] = {{gc, b, kTransB, lg, -1}};
             launch_pairs(T, p, 1, 512, ga, 512, batch, s);
         }
         if (gb) {
-            const PairSpec p[1] = {{a, gc, kTransA}};
+            const PairSpec p[1] = {{a, gc, kTransA, -1, lg}};
             launch_pairs(T, p, 1, 512, gb, 512, batch, s);
         }
     } else if (split_fused_enabled()) {
-        if (ga) launch_fused<1>(T, gc, b, ga, batch, s);
-        if (gb) launch_fused<2>(T, a, gc, gb, batch, s);
+        if (ga) launch_fused<1>(T, gc, b, ga, batch, s, lg, 1024);
+        if (gb) launch_fused<2>(T, a, gc, gb, batch, s, 1024, lg);
     } else {
         const float *L0 = a, *L1 = a + 512, *R0 = b, *R1 = b + 512, *G0 = gc, *G1 = gc + 512;
         if (ga) {
-            const PairSpec l0[2] = {{G0, R0, kTransB}, {G1, R1, kTransB}};
-            const PairSpec l1[1] = {{G1, R0, kTransB | kHatY}};
+            const PairSpec l0[2] = {{G0, R0, kTransB, lg, -1}, {G1, R1, kTransB, lg, -1}};
+            const PairSpec l1[1] = {{G1, R0, kTransB | kHatY, lg, -1}};
             launch_pairs(T, l0, 2, 1024, ga, 1024, batch, s);
             launch_pairs(T, l1, 1, 1024, ga + 512, 1024, batch, s);
         }
         if (gb) {
-            const PairSpec r0[2] = {{L0, G0, kTransA}, {L1, G1, kTransA | kHatX | kHatY}};
-            const PairSpec r1[1] = {{L0, G1, kTransA}};
+            const PairSpec r0[2] = {{L0, G0, kTransA, -1, lg}, {L1, G1, kTransA | kHatX | kHatY, -1, lg}};
+            const PairSpec r1[1] = {{L0, G1, kTransA, -1, lg}};
             launch_pairs(T, r0, 2, 1024, gb, 1024, batch, s);
             launch_pairs(T, r1, 1, 1024, gb + 512, 1024, batch, s);
         }

@@ -222,10 +222,12 @@ __device__ __forceinline__ void store_row_part(const float (&v)[1 << RB], float*
 // stored; their prefetch re-reads the last row (a cache hit, no branch).
 // The loop condition is the same for all lanes of a row, so a row's lanes
 // stay active together and every shuffle partner is active.
+// ldx: floats between the input's rows (2^N, or 0 for one row broadcast over
+// the batch: the transposed action on the gradient of a sum)
 template <int N, bool FWD>
 __global__ __launch_bounds__(256) void rotor_apply_kernel(const float* __restrict__ cs,
                                                            const float* __restrict__ X, float* __restrict__ Y,
-                                                           long long batch) {
+                                                           long long batch, long long ldx) {
     constexpr int RB = rotor_rb(N);
     constexpr int LB = N - RB;
     const unsigned L = threadIdx.x & ((1u << LB) - 1u);
@@ -234,11 +236,11 @@ __global__ __launch_bounds__(256) void rotor_apply_kernel(const float* __restric
     long long row = (long long)blockIdx.x * rows_per_block + (threadIdx.x >> LB);
     const long long lane_off = (long long)L << RB;
     float v[1 << RB];
-    load_row_part<RB>(v, X + ((row < batch ? row : batch - 1) << N) + lane_off);
+    load_row_part<RB>(v, X + (row < batch ? row : batch - 1) * ldx + lane_off);
     for (; row < batch; row += stride) {
         const long long nrow = row + stride;
         float nv[1 << RB];
-        load_row_part<RB>(nv, X + ((nrow < batch ? nrow : batch - 1) << N) + lane_off);
+        load_row_part<RB>(nv, X + (nrow < batch ? nrow : batch - 1) * ldx + lane_off);
         // an opaque copy of L per row keeps the per-plane lane factors inside
         // the loop instead of being hoisted into VGPRs for all planes
         unsigned Lr = L;
@@ -344,7 +346,8 @@ __global__ __launch_bounds__(256) void rotor_apply_bwd_kernel(const float* __res
                                                                const float* __restrict__ X,
                                                                const float* __restrict__ GY,
                                                                float* __restrict__ GX,
-                                                               float* __restrict__ gamma_ws, long long batch) {
+                                                               float* __restrict__ gamma_ws, long long batch,
+                                                               long long ldg) {
     constexpr int RB = rotor_rb(N);
     constexpr int LB = N - RB;
     constexpr int LPR = 1 << LB;
@@ -366,7 +369,7 @@ __global__ __launch_bounds__(256) void rotor_apply_bwd_kernel(const float* __res
             asm volatile("" : "+v"(Lr));
             const long long off = (row << N) + ((long long)Lr << RB);
             float g[1 << RB];
-            load_row_part<RB>(g, GY + off);
+            load_row_part<RB>(g, GY + row * ldg + ((long long)Lr << RB));  // ldg: 2^N, or 0 (one row for all)
             rot_chain<N, RB, false>(g, cs, Lr);
             if (GX) store_row_part<RB>(g, GX + off);
             if (want_gamma) {
@@ -428,7 +431,8 @@ template <int MODE>
 __global__ __launch_bounds__(256) void rotor_chain_lds_kernel(int n, const float* __restrict__ cs,
                                                                const float* __restrict__ A,
                                                                const float* __restrict__ B, float* __restrict__ OUT,
-                                                               float* __restrict__ parts, long long batch) {
+                                                               float* __restrict__ parts, long long batch,
+                                                               long long lda, long long ldb) {
     constexpr bool TWO = (MODE == LDS_CS_BWD || MODE == LDS_GAMMA);
     constexpr int kMaxW = 2 * 66;  // 2 C(12, 2)
     __shared__ float va[kLdsBlades];
@@ -446,8 +450,10 @@ __global__ __launch_bounds__(256) void rotor_chain_lds_kernel(int n, const float
         const int nb = (int)(rows << n);
         __syncthreads();  // the previous group's last plane and stores are done
         for (int e = tid * 4; e < nb; e += blockDim.x * 4) {
-            *reinterpret_cast<float4*>(&va[e]) = *reinterpret_cast<const float4*>(A + (row0 << n) + e);
-            if (TWO) *reinterpret_cast<float4*>(&vb[e]) = *reinterpret_cast<const float4*>(B + (row0 << n) + e);
+            // rows of A and B are lda / ldb floats apart (2^n, or 0: one row for all)
+            const long long r = row0 + (e >> n), c = e & (D - 1);
+            *reinterpret_cast<float4*>(&va[e]) = *reinterpret_cast<const float4*>(A + r * lda + c);
+            if (TWO) *reinterpret_cast<float4*>(&vb[e]) = *reinterpret_cast<const float4*>(B + r * ldb + c);
         }
         if (MODE == LDS_GAMMA) {
             // gx = chain^T gy on vb (planes last to first), then K from (va = x, vb = gx)
@@ -1304,67 +1310,72 @@ static unsigned lds_grid(int n, int64_t batch, long long cap) {
 
 template <int MODE>
 static void launch_lds(int n, const float* cs, const float* a, const float* b, float* out, float* parts, int64_t batch,
-                       unsigned grid, hipStream_t s) {
+                       unsigned grid, hipStream_t s, long long lda, long long ldb) {
     hipLaunchKernelGGL((rotor_chain_lds_kernel<MODE>), dim3(grid), dim3(256), 0, s, n, cs, a, b, out, parts,
-                       (long long)batch);
+                       (long long)batch, lda, ldb);
 }
 
 template <int N>
-static void launch_apply_reg(bool fwd, const float* cs, const float* x, float* y, int64_t batch, hipStream_t s) {
+static void launch_apply_reg(bool fwd, const float* cs, const float* x, float* y, int64_t batch, hipStream_t s,
+                             long long ldx) {
     constexpr int LB = N - rotor_rb(N);
     const long long threads = (long long)batch << LB;
     const long long wanted = (threads + 255) / 256;
     if (fwd) {
         const dim3 grid(resident_grid((const void*)rotor_apply_kernel<N, true>, 256, 0, wanted));
-        hipLaunchKernelGGL((rotor_apply_kernel<N, true>), grid, dim3(256), 0, s, cs, x, y, (long long)batch);
+        hipLaunchKernelGGL((rotor_apply_kernel<N, true>), grid, dim3(256), 0, s, cs, x, y, (long long)batch, ldx);
     } else {
         const dim3 grid(resident_grid((const void*)rotor_apply_kernel<N, false>, 256, 0, wanted));
-        hipLaunchKernelGGL((rotor_apply_kernel<N, false>), grid, dim3(256), 0, s, cs, x, y, (long long)batch);
+        hipLaunchKernelGGL((rotor_apply_kernel<N, false>), grid, dim3(256), 0, s, cs, x, y, (long long)batch, ldx);
     }
 }
 
-// y = chain(cs) x (fwd) or chain(cs)^T x, any n in range, batch > 0
-static void launch_chain(int n, bool fwd, const float* cs, const float* x, float* y, int64_t batch, hipStream_t s) {
+// y = chain(cs) x (fwd) or chain(cs)^T x, any n in range, batch > 0; x's rows
+// are ldx floats apart (2^n, or 0 for one row broadcast over the batch)
+static void launch_chain(int n, bool fwd, const float* cs, const float* x, float* y, int64_t batch, hipStream_t s,
+                         long long ldx) {
     if (n <= kRegChainMaxN) {
-#define CLF_CALL(N) launch_apply_reg<N>(fwd, cs, x, y, batch, s)
+#define CLF_CALL(N) launch_apply_reg<N>(fwd, cs, x, y, batch, s, ldx)
         CLF_ROTOR_DISPATCH(n, CLF_CALL)
 #undef CLF_CALL
     } else if (fwd) {
-        launch_lds<LDS_FWD>(n, cs, x, nullptr, y, nullptr, batch, lds_grid<LDS_FWD>(n, batch, 1LL << 30), s);
+        launch_lds<LDS_FWD>(n, cs, x, nullptr, y, nullptr, batch, lds_grid<LDS_FWD>(n, batch, 1LL << 30), s, ldx, 0);
     } else {
-        launch_lds<LDS_TR>(n, cs, x, nullptr, y, nullptr, batch, lds_grid<LDS_TR>(n, batch, 1LL << 30), s);
+        launch_lds<LDS_TR>(n, cs, x, nullptr, y, nullptr, batch, lds_grid<LDS_TR>(n, batch, 1LL << 30), s, ldx, 0);
     }
 }
 
 // Composite backward with the K statistics: the register kernel (n <= 10) or
 // the LDS-staged kernel; returns the number of partials written.
 template <int N>
-static int launch_apply_bwd_reg(const float* cs, const float* x, const float* gy, float* gx, float* ws, int64_t batch,
-                                hipStream_t s) {
+static int launch_apply_bwd_reg(const float* cs, const float* x, const float* gy, long long ldg, float* gx, float* ws,
+                                int64_t batch, hipStream_t s) {
     const unsigned grid = resident_grid((const void*)rotor_apply_bwd_kernel<N>, 256, 0, rotor_bwd_grid(N, batch));
-    hipLaunchKernelGGL((rotor_apply_bwd_kernel<N>), dim3(grid), dim3(256), 0, s, cs, x, gy, gx, ws, (long long)batch);
+    hipLaunchKernelGGL((rotor_apply_bwd_kernel<N>), dim3(grid), dim3(256), 0, s, cs, x, gy, gx, ws, (long long)batch,
+                       ldg);
     return (int)grid;
 }
 
-static int launch_gamma(int n, const float* cs, const float* x, const float* gy, float* gx, float* ws, int64_t batch,
-                        hipStream_t s) {
+static int launch_gamma(int n, const float* cs, const float* x, const float* gy, long long ldg, float* gx, float* ws,
+                        int64_t batch, hipStream_t s) {
     int nparts = 0;
     if (n <= kRegChainMaxN) {
-#define CLF_CALL(N) nparts = launch_apply_bwd_reg<N>(cs, x, gy, gx, ws, batch, s)
+#define CLF_CALL(N) nparts = launch_apply_bwd_reg<N>(cs, x, gy, ldg, gx, ws, batch, s)
         CLF_ROTOR_DISPATCH(n, CLF_CALL)
 #undef CLF_CALL
     } else {
         const unsigned grid = lds_grid<LDS_GAMMA>(n, batch, rotor_bwd_grid(n, batch));
-        launch_lds<LDS_GAMMA>(n, cs, x, gy, gx, ws, batch, grid, s);
+        launch_lds<LDS_GAMMA>(n, cs, x, gy, gx, ws, batch, grid, s, 1LL << n, ldg);
         nparts = (int)grid;
     }
     return nparts;
 }
 
 bool rotor16_enabled(int n);
-int rotor16_apply(bool fwd, const float* U, const float* x, float* y, int64_t batch, void* stream);
-int rotor16_bwd(const float* U, const float* x, const float* gy, float* gx, float* gamma_ws, int64_t batch,
-                unsigned grid, void* stream);
+int rotor16_apply(bool fwd, const float* U, const float* x, float* y, int64_t batch, void* stream,
+                  long long ldx = 256);
+int rotor16_bwd(const float* U, const float* x, const float* gy, long long ldg, float* gx, float* gamma_ws,
+                int64_t batch, unsigned grid, void* stream);
 unsigned rotor16_bwd_grid(long long wanted);
 
 int rotor_apply_fwd(int n, const float* state, const float* x, float* y, int64_t batch, void* stream) {
@@ -1375,15 +1386,17 @@ int rotor_apply_fwd(int n, const float* state, const float* x, float* y, int64_t
     if (x == y) return set_error(CLF_ERR_ARG, "output must not alias the input");
     if ((((uintptr_t)x) | ((uintptr_t)y)) & 15u) return set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
     if (rotor16_enabled(n)) return rotor16_apply(true, state + spin_offset(n), x, y, batch, stream);
-    launch_chain(n, true, state + n * n, x, y, batch, (hipStream_t)stream);
+    launch_chain(n, true, state + n * n, x, y, batch, (hipStream_t)stream, 1LL << n);
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }
 
-int rotor_apply_bwd(int n, const float* state, const float* x, const float* gy, float* gx, float* g_state,
-                    int64_t batch, void* ws, size_t ws_bytes, void* stream) {
+// gy's rows are ldg floats apart: 2^n, or 0 for one row broadcast over the batch
+int rotor_apply_bwd(int n, const float* state, const float* x, const float* gy, int64_t ldg, float* gx,
+                    float* g_state, int64_t batch, void* ws, size_t ws_bytes, void* stream) {
     if (int rc = check_rotor_n(n)) return rc;
     if (batch < 0) return set_error(CLF_ERR_ARG, "batch must be >= 0");
+    if (ldg != 0 && ldg != (1LL << n)) return set_error(CLF_ERR_ARG, "gy row stride must be 0 or 2^n");
     if (!gx && !g_state) return CLF_OK;
     if (!state || (batch > 0 && (!gy || (g_state && !x)))) return set_error(CLF_ERR_ARG, "null pointer argument");
     if ((((uintptr_t)x) | ((uintptr_t)gy) | ((uintptr_t)gx)) & 15u)
@@ -1398,13 +1411,14 @@ int rotor_apply_bwd(int n, const float* state, const float* x, const float* gy, 
     int nparts = 0;
     if (batch > 0) {
         if (!g_state) {
-            if (mat) return rotor16_apply(false, state + spin_offset(n), gy, gx, batch, stream);
-            launch_chain(n, false, state + n * n, gy, gx, batch, s);
+            if (mat) return rotor16_apply(false, state + spin_offset(n), gy, gx, batch, stream, ldg);
+            launch_chain(n, false, state + n * n, gy, gx, batch, s, ldg);
         } else if (mat) {
             nparts = (int)rotor16_bwd_grid(rotor_bwd_grid(n, batch));
-            if (int rc = rotor16_bwd(state + spin_offset(n), x, gy, gx, gws, batch, (unsigned)nparts, stream)) return rc;
+            if (int rc = rotor16_bwd(state + spin_offset(n), x, gy, ldg, gx, gws, batch, (unsigned)nparts, stream))
+                return rc;
         } else {
-            nparts = launch_gamma(n, state + n * n, x, gy, gx, gws, batch, s);
+            nparts = launch_gamma(n, state + n * n, x, gy, ldg, gx, gws, batch, s);
         }
         CLF_HIP_CHECK(hipGetLastError());
     }
@@ -1424,15 +1438,17 @@ int rotor_cs_apply_fwd(int n, const float* cs, const float* x, float* y, int64_t
     if (!cs || !x || !y) return set_error(CLF_ERR_ARG, "null pointer argument");
     if (x == y) return set_error(CLF_ERR_ARG, "output must not alias the input");
     if ((((uintptr_t)x) | ((uintptr_t)y)) & 15u) return set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
-    launch_chain(n, true, cs, x, y, batch, (hipStream_t)stream);
+    launch_chain(n, true, cs, x, y, batch, (hipStream_t)stream, 1LL << n);
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }
 
-int rotor_cs_apply_bwd(int n, const float* cs, const float* y, const float* gy, float* gx, float* g_cs,
+// gy's rows are ldg floats apart: 2^n, or 0 for one row broadcast over the batch
+int rotor_cs_apply_bwd(int n, const float* cs, const float* y, const float* gy, int64_t ldg, float* gx, float* g_cs,
                        int64_t batch, void* ws, size_t ws_bytes, void* stream) {
     if (int rc = check_rotor_n(n)) return rc;
     if (batch < 0) return set_error(CLF_ERR_ARG, "batch must be >= 0");
+    if (ldg != 0 && ldg != (1LL << n)) return set_error(CLF_ERR_ARG, "gy row stride must be 0 or 2^n");
     if (!gx && !g_cs) return CLF_OK;
     if (!cs || (batch > 0 && (!gy || (g_cs && !y)))) return set_error(CLF_ERR_ARG, "null pointer argument");
     if ((((uintptr_t)y) | ((uintptr_t)gy) | ((uintptr_t)gx)) & 15u)
@@ -1446,10 +1462,10 @@ int rotor_cs_apply_bwd(int n, const float* cs, const float* y, const float* gy, 
     int nparts = 0;
     if (batch > 0) {
         if (!g_cs) {
-            launch_chain(n, false, cs, gy, gx, batch, s);
+            launch_chain(n, false, cs, gy, gx, batch, s, ldg);
         } else {
             const unsigned grid = lds_grid<LDS_CS_BWD>(n, batch, cs_bwd_grid(n, batch));
-            launch_lds<LDS_CS_BWD>(n, cs, y, gy, gx, parts, batch, grid, s);
+            launch_lds<LDS_CS_BWD>(n, cs, y, gy, gx, parts, batch, grid, s, 1LL << n, ldg);
             nparts = (int)grid;
         }
         CLF_HIP_CHECK(hipGetLastError());

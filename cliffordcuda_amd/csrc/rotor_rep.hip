@@ -55,9 +55,12 @@ __device__ __forceinline__ void load_spin_operand(const float* __restrict__ U, u
 // bookkeeping runs on the scalar unit and the row clamps need no branches.
 constexpr int kApplyWaveFloats = kRelayoutFloats + 4 * 256;  // staged x, then the relayout | the previous group's y
 
+// ldx: floats between the input's rows (256, or 0 for one row broadcast over
+// the batch: the transposed action on the gradient of a sum)
 template <bool TRANS, bool NT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void rotor16_apply_kernel(
-    const float* __restrict__ U, const float* __restrict__ X, float* __restrict__ Y, long long batch, RepTable T) {
+    const float* __restrict__ U, const float* __restrict__ X, float* __restrict__ Y, long long batch, RepTable T,
+    long long ldx) {
     __shared__ float lds[4][kApplyWaveFloats];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const unsigned x = lane & 15u;
@@ -79,14 +82,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
     const long long stride = (long long)gridDim.x * 4 * 4;
     const long long rfirst = ((long long)blockIdx.x * 4 + wave) * 4;
     long long row0 = rfirst;
-    Pre16 px = fetch16<NT>(X, row0, batch, lane);
+    Pre16 px = fetch16<NT>(X, row0, batch, lane, ldx);
     for (; row0 < batch; row0 += stride) {
         // the table values are re-derived where they are used rather than kept
         // in registers across the loop (register pressure sets the occupancy)
 #pragma unroll
         for (int z = 0; z < 16; ++z) asm volatile("" : "+v"(ent[z]));
         stage16(sx, px, lane, oddc);
-        px = fetch16<NT>(X, row0 + stride, batch, lane);
+        px = fetch16<NT>(X, row0 + stride, batch, lane, ldx);
         wave_lds_sync();
         float wx[16];
         gather16<0>(sx + rb * 256, ent, wx);
@@ -128,8 +131,8 @@ constexpr int kRotorBwdWaveFloats = 4 * 256 + kRelayoutFloats + 4 * 256;
 
 template <bool NT, bool WGX>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void rotor16_bwd_kernel(
-    const float* __restrict__ U, const float* __restrict__ X, const float* __restrict__ GY, float* __restrict__ GX,
-    float* __restrict__ gamma_ws, long long batch, RepTable T, SpinTable S) {
+    const float* __restrict__ U, const float* __restrict__ X, const float* __restrict__ GY, long long ldg,
+    float* __restrict__ GX, float* __restrict__ gamma_ws, long long batch, RepTable T, SpinTable S) {
     // the W_x^T address forms below need the wave slots 1024-byte aligned
     static_assert((kRotorBwdWaveFloats * 4) % 1024 == 0, "wave slots stay 1024-byte aligned");
     __shared__ __attribute__((aligned(1024))) float lds[4][kRotorBwdWaveFloats];
@@ -158,12 +161,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void r
     const long long rfirst = ((long long)blockIdx.x * 4 + wave) * 4;
     long long row0 = rfirst;
     Pre16 px = fetch16<NT>(X, row0, batch, lane);
-    Pre16 pg = fetch16<NT>(GY, row0, batch, lane);
+    Pre16 pg = fetch16<NT>(GY, row0, batch, lane, ldg);
     for (; row0 < batch; row0 += stride) {
         stage16(sx, px, lane, oddc);
         stage16(sg, pg, lane, oddc);
         px = fetch16<NT>(X, row0 + stride, batch, lane);
-        pg = fetch16<NT>(GY, row0 + stride, batch, lane);
+        pg = fetch16<NT>(GY, row0 + stride, batch, lane, ldg);
         wave_lds_sync();
         float wg[16], wx[16];
         gather16<0>(sg + rb * 256, ent, wg);
@@ -282,7 +285,7 @@ static unsigned rotor16_grid(int64_t batch) {
     return (unsigned)(g < 1 ? 1 : (g > cap ? cap : g));
 }
 
-int rotor16_apply(bool fwd, const float* U, const float* x, float* y, int64_t batch, void* stream) {
+int rotor16_apply(bool fwd, const float* U, const float* x, float* y, int64_t batch, void* stream, long long ldx) {
     RepTable T;
     SpinTable S;
     if (!spin_tables(T, S)) return set_error(CLF_ERR_UNSUPPORTED, "Cl(8,0) representation tables unavailable");
@@ -290,7 +293,7 @@ int rotor16_apply(bool fwd, const float* U, const float* x, float* y, int64_t ba
     const dim3 grid(rotor16_grid(batch));
     const bool nt = stream_nt(2.0 * 1024.0 * (double)batch);
 #define CLF_ROTOR16(TR, NT) \
-    hipLaunchKernelGGL((rotor16_apply_kernel<TR, NT>), grid, dim3(256), 0, s, U, x, y, (long long)batch, T)
+    hipLaunchKernelGGL((rotor16_apply_kernel<TR, NT>), grid, dim3(256), 0, s, U, x, y, (long long)batch, T, ldx)
     if (fwd) {
         if (nt) CLF_ROTOR16(false, true);
         else CLF_ROTOR16(false, false);
@@ -312,15 +315,15 @@ unsigned rotor16_bwd_grid(long long wanted) {
 }
 
 // grid = the number of partials the gamma finalize reads (<= the workspace bound)
-int rotor16_bwd(const float* U, const float* x, const float* gy, float* gx, float* gamma_ws, int64_t batch,
-                unsigned grid, void* stream) {
+int rotor16_bwd(const float* U, const float* x, const float* gy, long long ldg, float* gx, float* gamma_ws,
+                int64_t batch, unsigned grid, void* stream) {
     RepTable T;
     SpinTable S;
     if (!spin_tables(T, S)) return set_error(CLF_ERR_UNSUPPORTED, "Cl(8,0) representation tables unavailable");
     hipStream_t s = (hipStream_t)stream;
     const bool nt = stream_nt((2 + (gx != nullptr)) * 1024.0 * (double)batch);
 #define CLF_ROTOR16_BWD(NT, WGX)                                                                                 \
-    hipLaunchKernelGGL((rotor16_bwd_kernel<NT, WGX>), dim3(grid), dim3(256), 0, s, U, x, gy, gx, gamma_ws,       \
+    hipLaunchKernelGGL((rotor16_bwd_kernel<NT, WGX>), dim3(grid), dim3(256), 0, s, U, x, gy, ldg, gx, gamma_ws,  \
                        (long long)batch, T, S)
     if (gx) {
         if (nt) CLF_ROTOR16_BWD(true, true);

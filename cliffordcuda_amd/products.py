@@ -47,11 +47,12 @@ def _product_bwd(op_code, n, neg, nul, a, b, gc, need_a, need_b):
     gb = torch.empty_like(b) if need_b else None
     if ga is None and gb is None:
         return None, None
+    gc, ldg = _lib.grad_rows(gc, a.shape[1])
     lib = _lib.load()
     with torch.cuda.device(a.device):
-        rc = lib.clf_product_bwd(op_code, n, neg, nul, a.data_ptr(), b.data_ptr(), gc.data_ptr(),
-                                 _lib.ptr(ga), _lib.ptr(gb), a.shape[0], _lib.stream_of(a))
-    _lib.check(rc, "clf_product_bwd")
+        rc = lib.clf_product_bwd_ld(op_code, n, neg, nul, a.data_ptr(), b.data_ptr(), gc.data_ptr(), ldg,
+                                    _lib.ptr(ga), _lib.ptr(gb), a.shape[0], _lib.stream_of(a))
+    _lib.check(rc, "clf_product_bwd_ld")
     return ga, gb
 
 
@@ -72,7 +73,7 @@ class _ProductFunc(torch.autograd.Function):
     def backward(ctx, gc):
         a, b = ctx.saved_tensors
         op_code, n, neg, nul = ctx.meta
-        ga, gb = _product_bwd(op_code, n, neg, nul, a, b, gc.contiguous(),
+        ga, gb = _product_bwd(op_code, n, neg, nul, a, b, gc,
                               ctx.needs_input_grad[0], ctx.needs_input_grad[1])
         return ga, gb, None, None, None, None
 

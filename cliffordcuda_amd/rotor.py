@@ -94,7 +94,7 @@ def _apply_fwd(state: torch.Tensor, x: torch.Tensor, n: int) -> torch.Tensor:
 def _apply_bwd(state: torch.Tensor, x: torch.Tensor, gy: torch.Tensor, n: int, need_state: bool, need_x: bool):
     if not (need_state or need_x):
         return None, None
-    gy = gy.contiguous()
+    gy, ldg = _lib.grad_rows(gy, x.shape[1])
     gx = torch.empty_like(x) if need_x else None
     g_state = torch.empty_like(state) if need_state else None
     lib = _lib.load()
@@ -104,9 +104,9 @@ def _apply_bwd(state: torch.Tensor, x: torch.Tensor, gy: torch.Tensor, n: int, n
         ws_bytes = lib.clf_rotor_apply_ws_bytes(n, x.shape[0])
         ws = torch.empty(max(1, ws_bytes // 4), dtype=torch.float32, device=x.device)
     with torch.cuda.device(x.device):
-        rc = lib.clf_rotor_apply_bwd(n, state.data_ptr(), x.data_ptr(), gy.data_ptr(), _lib.ptr(gx),
-                                     _lib.ptr(g_state), x.shape[0], _lib.ptr(ws), ws_bytes, _lib.stream_of(x))
-    _lib.check(rc, "clf_rotor_apply_bwd")
+        rc = lib.clf_rotor_apply_bwd_ld(n, state.data_ptr(), x.data_ptr(), gy.data_ptr(), ldg, _lib.ptr(gx),
+                                        _lib.ptr(g_state), x.shape[0], _lib.ptr(ws), ws_bytes, _lib.stream_of(x))
+    _lib.check(rc, "clf_rotor_apply_bwd_ld")
     return g_state, gx
 
 
@@ -122,7 +122,7 @@ def _cs_apply_fwd(cs: torch.Tensor, x: torch.Tensor, n: int) -> torch.Tensor:
 def _cs_apply_bwd(cs: torch.Tensor, y: torch.Tensor, gy: torch.Tensor, n: int, need_cs: bool, need_x: bool):
     if not (need_cs or need_x):
         return None, None
-    gy = gy.contiguous()
+    gy, ldg = _lib.grad_rows(gy, y.shape[1])
     gx = torch.empty_like(y) if need_x else None
     g_cs = torch.empty_like(cs) if need_cs else None
     lib = _lib.load()
@@ -132,9 +132,9 @@ def _cs_apply_bwd(cs: torch.Tensor, y: torch.Tensor, gy: torch.Tensor, n: int, n
         ws_bytes = lib.clf_rotor_cs_apply_ws_bytes(n, y.shape[0])
         ws = torch.empty(max(1, ws_bytes // 4), dtype=torch.float32, device=y.device)
     with torch.cuda.device(y.device):
-        rc = lib.clf_rotor_cs_apply_bwd(n, cs.data_ptr(), y.data_ptr(), gy.data_ptr(), _lib.ptr(gx), _lib.ptr(g_cs),
-                                        y.shape[0], _lib.ptr(ws), ws_bytes, _lib.stream_of(y))
-    _lib.check(rc, "clf_rotor_cs_apply_bwd")
+        rc = lib.clf_rotor_cs_apply_bwd_ld(n, cs.data_ptr(), y.data_ptr(), gy.data_ptr(), ldg, _lib.ptr(gx),
+                                           _lib.ptr(g_cs), y.shape[0], _lib.ptr(ws), ws_bytes, _lib.stream_of(y))
+    _lib.check(rc, "clf_rotor_cs_apply_bwd_ld")
     return g_cs, gx
 
 

@@ -110,6 +110,16 @@ int clf_product_bwd(int op, int n, uint32_t neg_mask, uint32_t null_mask,
                     const float* a, const float* b, const float* gc,
                     float* ga, float* gb, int64_t batch, void* stream);
 
+/* clf_product_bwd with gc's row stride given: ldg = 2^n (packed rows, what
+ * clf_product_bwd uses) or 0 (one gc row read for every batch row: the
+ * gradient of a sum, which autograd hands over as a stride-0 expansion).
+ * Any other stride returns CLF_ERR_ARG. Same route and kernels as the packed
+ * call; no counterpart entry in the reference, whose wrappers make gc
+ * contiguous first (extensions/ga/geom_prod.py:242-250). */
+int clf_product_bwd_ld(int op, int n, uint32_t neg_mask, uint32_t null_mask,
+                       const float* a, const float* b, const float* gc, int64_t ldg,
+                       float* ga, float* gb, int64_t batch, void* stream);
+
 /* Single-pass graded op: y = kind(x). `grade` is used by PROJECTION only.
  * DUAL / DUAL_ADJ need a non-degenerate metric. y must not alias x for the
  * dual kinds (they permute). Replaces the eager torch passes of
@@ -174,6 +184,12 @@ int clf_rotor_apply_bwd(int n, const float* state, const float* x, const float* 
                         float* gx, float* g_state, int64_t batch,
                         void* ws, size_t ws_bytes, void* stream);
 
+/* clf_rotor_apply_bwd with gy's row stride given: 2^n (packed) or 0 (one gy
+ * row for the whole batch); other strides return CLF_ERR_ARG. */
+int clf_rotor_apply_bwd_ld(int n, const float* state, const float* x, const float* gy, int64_t ldg,
+                           float* gx, float* g_state, int64_t batch,
+                           void* ws, size_t ws_bytes, void* stream);
+
 /* y = chain(cs) x for a caller's cs (any pairs, unit or not), `batch` rows.
  * Replaces givens_mb_perm_packed_fwd (kernels/rotor/givens_apply_mb_perm_packed.cu:250-267). */
 int clf_rotor_cs_apply_fwd(int n, const float* cs, const float* x, float* y,
@@ -191,6 +207,11 @@ size_t clf_rotor_cs_apply_ws_bytes(int n, int64_t batch);
 int clf_rotor_cs_apply_bwd(int n, const float* cs, const float* y, const float* gy,
                            float* gx, float* g_cs, int64_t batch,
                            void* ws, size_t ws_bytes, void* stream);
+
+/* clf_rotor_cs_apply_bwd with gy's row stride given: 2^n or 0. */
+int clf_rotor_cs_apply_bwd_ld(int n, const float* cs, const float* y, const float* gy, int64_t ldg,
+                              float* gx, float* g_cs, int64_t batch,
+                              void* ws, size_t ws_bytes, void* stream);
 
 /* g_biv = d/d(biv) of <g_cs, cs(biv)> through the Givens factorisation and
  * expm (fp64, one single-workgroup launch). Replaces givens_factor_bwd_v2
@@ -242,6 +263,12 @@ int clf_product_bcast_bwd(int op, int side, int n, uint32_t neg_mask, uint32_t n
                           const float* x, const float* w, const float* gy,
                           float* gx, float* gw, int64_t batch,
                           void* ws, size_t ws_bytes, void* stream);
+
+/* clf_product_bcast_bwd with gy's row stride given: 2^n or 0. */
+int clf_product_bcast_bwd_ld(int op, int side, int n, uint32_t neg_mask, uint32_t null_mask,
+                             const float* x, const float* w, const float* gy, int64_t ldg,
+                             float* gx, float* gw, int64_t batch,
+                             void* ws, size_t ws_bytes, void* stream);
 
 /* Allocation-free variant of clf_product_bcast_bwd. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
