@@ -26,7 +26,7 @@ def _bcast_fwd(x, w, op_code, side, n, neg, nul):
     lib = _lib.load()
     y = torch.empty_like(x)
     ws, nbytes = _ws(lib, n, x.shape[0], x.device)
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x):
         rc = lib.clf_product_bcast_fwd(op_code, side, n, neg, nul, x.data_ptr(), w.data_ptr(), y.data_ptr(),
                                        x.shape[0], ws.data_ptr(), nbytes, _lib.stream_of(x))
     _lib.check(rc, "clf_product_bcast_fwd")
@@ -41,7 +41,7 @@ def _bcast_bwd(x, w, gy, op_code, side, n, neg, nul, need_x, need_w):
     gx = torch.empty_like(x) if need_x else None
     gw = torch.empty_like(w) if need_w else None
     ws, nbytes = _ws(lib, n, x.shape[0], x.device)
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x):
         rc = lib.clf_product_bcast_bwd_ld(op_code, side, n, neg, nul, x.data_ptr(), w.data_ptr(), gy.data_ptr(),
                                           ldg, _lib.ptr(gx), _lib.ptr(gw), x.shape[0], ws.data_ptr(), nbytes,
                                           _lib.stream_of(x))

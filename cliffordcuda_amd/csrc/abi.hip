@@ -150,6 +150,9 @@ int rotor_compile_bwd(int n, const float* biv, const float* g_state, float* g_bi
 int rotor_apply_fwd(int n, const float* state, const float* x, float* y, int64_t batch, void* stream);
 int rotor_apply_bwd(int n, const float* state, const float* x, const float* gy, int64_t ldg, float* gx,
                     float* g_state, int64_t batch, void* ws, size_t ws_bytes, void* stream);
+size_t rotor_biv_apply_ws_bytes(int n, int64_t batch);
+int rotor_biv_apply_bwd(int n, const float* biv, const float* state, const float* x, const float* gy, int64_t ldg,
+                        float* gx, float* g_biv, int64_t batch, void* ws, size_t ws_bytes, void* stream);
 size_t rotor_cs_apply_ws_bytes(int n, int64_t batch);
 int rotor_cs_apply_fwd(int n, const float* cs, const float* x, float* y, int64_t batch, void* stream);
 int rotor_cs_apply_bwd(int n, const float* cs, const float* y, const float* gy, int64_t ldg, float* gx,
@@ -268,6 +271,15 @@ int clf_rotor_apply_bwd_ld(int n, const float* state, const float* x, const floa
                            float* g_state, int64_t batch, void* ws, size_t ws_bytes, void* stream) {
     clf::clear_error();
     return clf::rotor_apply_bwd(n, state, x, gy, ldg, gx, g_state, batch, ws, ws_bytes, stream);
+}
+
+size_t clf_rotor_bivector_apply_ws_bytes(int n, int64_t batch) { return clf::rotor_biv_apply_ws_bytes(n, batch); }
+
+int clf_rotor_bivector_apply_bwd(int n, const float* biv, const float* state, const float* x, const float* gy,
+                                 int64_t ldg, float* gx, float* g_biv, int64_t batch, void* ws, size_t ws_bytes,
+                                 void* stream) {
+    clf::clear_error();
+    return clf::rotor_biv_apply_bwd(n, biv, state, x, gy, ldg, gx, g_biv, batch, ws, ws_bytes, stream);
 }
 
 int clf_rotor_cs_apply_fwd(int n, const float* cs, const float* x, float* y, int64_t batch, void* stream) {

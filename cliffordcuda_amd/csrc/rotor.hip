@@ -793,30 +793,35 @@ __global__ __launch_bounds__(64) void rotor_compile_fwd_cols_kernel(const float*
 }
 
 // dL/dQ (tangent part) = Q skew(Gamma), skew(Gamma)[p][q] = K_pq / 2 = -skew(Gamma)[q][p],
-// K = sum of the per-workgroup partials. Writes the Q slot of g_state and zeroes
-// its chain slot. 1024 threads: entries padded to EP (a power of two >= C(n,2)),
-// thread t sums partials p = t/EP, t/EP + 1024/EP, ... of entry t % EP, then the
-// 1024/EP groups are added.
-__global__ __launch_bounds__(1024) void rotor_gamma_finalize_kernel(int n, const float* __restrict__ state,
-                                                                     const float* __restrict__ gamma_ws, int nparts,
-                                                                     float* __restrict__ g_state) {
-    __shared__ double part[1024];
-    __shared__ double S[kRotorMaxN * kRotorMaxN];
+// K = sum of the per-workgroup partials. Called by all 1024 threads of the
+// workgroup (it holds barriers); thread t < n^2 gets entry t (row-major) of
+// Q skew(Gamma), the others 0. Entries are padded to EP (a power of two >=
+// C(n,2)): thread t sums partials p = t/EP, t/EP + 1024/EP, ... of entry
+// t % EP, then the 1024/EP groups are added.
+__device__ double gamma_q_skew(int n, const float* __restrict__ state, const float* __restrict__ gamma_ws,
+                               int nparts, double* __restrict__ part, double* __restrict__ S) {
     const int C = n_planes(n);
     int ep = 1;
     while (ep < C) ep <<= 1;
     const int ngrp = 1024 / ep;
     const int e = threadIdx.x & (ep - 1), grp = threadIdx.x / ep;
-    // eight independent loads per iteration, so their latencies overlap
-    double t[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+    // sixteen independent loads per iteration, so their latencies overlap (the
+    // usual partial count, 512 at n = 8, takes one iteration)
+    float t[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) t[u] = 0.f;
+    double acc = 0.0;
     if (e < C) {
         int p = grp;
-        for (; p + 7 * ngrp < nparts; p += 8 * ngrp)
+        for (; p + 15 * ngrp < nparts; p += 16 * ngrp) {
 #pragma unroll
-            for (int u = 0; u < 8; ++u) t[u] += (double)gamma_ws[(long long)(p + u * ngrp) * C + e];
-        for (; p < nparts; p += ngrp) t[0] += (double)gamma_ws[(long long)p * C + e];
+            for (int u = 0; u < 16; ++u) t[u] = gamma_ws[(long long)(p + u * ngrp) * C + e];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) acc += (double)t[u];
+        }
+        for (; p < nparts; p += ngrp) acc += (double)gamma_ws[(long long)p * C + e];
     }
-    part[threadIdx.x] = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+    part[threadIdx.x] = acc;
     for (int i = threadIdx.x; i < n * n; i += blockDim.x) S[i] = 0.0;
     __syncthreads();
     if ((int)threadIdx.x < C) {
@@ -827,12 +832,22 @@ __global__ __launch_bounds__(1024) void rotor_gamma_finalize_kernel(int n, const
         S[q * n + p] = -0.5 * u;
     }
     __syncthreads();
+    double v = 0.0;
     if ((int)threadIdx.x < n * n) {
         const int i = threadIdx.x / n, j = threadIdx.x % n;
-        double v = 0.0;
         for (int k = 0; k < n; ++k) v += (double)state[i * n + k] * S[k * n + j];
-        g_state[threadIdx.x] = (float)v;
     }
+    return v;
+}
+
+// Writes the Q slot of g_state (Q skew(Gamma)) and zeroes its other slots.
+__global__ __launch_bounds__(1024) void rotor_gamma_finalize_kernel(int n, const float* __restrict__ state,
+                                                                     const float* __restrict__ gamma_ws, int nparts,
+                                                                     float* __restrict__ g_state) {
+    __shared__ double part[1024];
+    __shared__ double S[kRotorMaxN * kRotorMaxN];
+    const double v = gamma_q_skew(n, state, gamma_ws, nparts, part, S);
+    if ((int)threadIdx.x < n * n) g_state[threadIdx.x] = (float)v;
     for (int i = n * n + threadIdx.x; i < state_floats(n); i += blockDim.x) g_state[i] = 0.f;
 }
 
@@ -1109,20 +1124,20 @@ __global__ __launch_bounds__(128) void rotor_compile_fwd_ent_kernel(const float*
 
 // Adjoint Frechet derivative by the block identity (see the column version):
 // lane (i, j) holds E[i][j] and L[i][j]; X = A^T and G rows in registers.
+// Run by one whole wave (lanes 0..63); g holds row i of dL/dQ for lane
+// (i, j) = (lane / N, lane % N) (row 0 for lanes past N^2).
 template <int N>
-__global__ __launch_bounds__(64) void rotor_compile_bwd_ent_kernel(const float* __restrict__ biv,
-                                                                    const float* __restrict__ g_state,
-                                                                    float* __restrict__ g_biv) {
+__device__ __forceinline__ void compile_bwd_ent(const float* __restrict__ biv, double (&g)[N],
+                                                float* __restrict__ g_biv) {
     static_assert(N * N <= 64, "one entry per lane");
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
     const bool active = lane < N * N;
     const int i = active ? lane / N : 0, j = active ? lane % N : 0;
-    double x[N], g[N];
+    double x[N];
     double xs = 0.0, gs = 0.0;
 #pragma unroll
     for (int l = 0; l < N; ++l) {
         x[l] = generator_entry(biv, N, l, i);  // (A^T)[i][l]
-        g[l] = (double)g_state[i * N + l];
         xs += fabs(x[l]);
         gs += fabs(g[l]);
     }
@@ -1169,6 +1184,41 @@ __global__ __launch_bounds__(64) void rotor_compile_bwd_ent_kernel(const float* 
         const int k = i * N - i * (i + 1) / 2 + (j - i - 1);
         g_biv[k] = (float)(-2.0 * (L - ft));
     }
+}
+
+template <int N>
+__global__ __launch_bounds__(64) void rotor_compile_bwd_ent_kernel(const float* __restrict__ biv,
+                                                                    const float* __restrict__ g_state,
+                                                                    float* __restrict__ g_biv) {
+    const int lane = threadIdx.x;
+    const int i = lane < N * N ? lane / N : 0;
+    double g[N];
+#pragma unroll
+    for (int l = 0; l < N; ++l) g[l] = (double)g_state[i * N + l];
+    compile_bwd_ent<N>(biv, g, g_biv);
+}
+
+// The bivector gradient straight from the apply backward's partials (n <= 8):
+// the batch sum and Q skew(Gamma) of the finalize, kept in LDS in fp64, then
+// wave 0 runs the compile backward on it. One launch instead of two, and no
+// g_state round trip through memory.
+template <int N>
+__global__ __launch_bounds__(1024) void rotor_gamma_biv_kernel(const float* __restrict__ biv,
+                                                                const float* __restrict__ state,
+                                                                const float* __restrict__ gamma_ws, int nparts,
+                                                                float* __restrict__ g_biv) {
+    __shared__ double part[1024];
+    __shared__ double S[N * N];
+    __shared__ double G[N * N];
+    const double v = gamma_q_skew(N, state, gamma_ws, nparts, part, S);
+    if ((int)threadIdx.x < N * N) G[threadIdx.x] = v;
+    __syncthreads();
+    if (threadIdx.x >= 64) return;  // no barrier follows
+    const int i = (int)threadIdx.x < N * N ? (int)threadIdx.x / N : 0;
+    double g[N];
+#pragma unroll
+    for (int l = 0; l < N; ++l) g[l] = G[i * N + l];
+    compile_bwd_ent<N>(biv, g, g_biv);
 }
 
 // ---- host side --------------------------------------------------------------
@@ -1229,6 +1279,20 @@ static void launch_compile_bwd(const float* biv, const float* g_state, float* g_
     if constexpr (N * N <= 64)
         hipLaunchKernelGGL((rotor_compile_bwd_ent_kernel<N>), dim3(1), dim3(64), 0, s, biv, g_state, g_biv);
     else hipLaunchKernelGGL((rotor_compile_bwd_cols_kernel<N>), dim3(1), dim3(64), 0, s, biv, g_state, g_biv);
+}
+
+// Partials -> g_biv: one fused launch while Q is n x n <= 64 entries (one per
+// lane of the compile backward), else the finalize into g_state and the
+// column compile backward.
+template <int N>
+static void launch_gamma_biv(const float* biv, const float* state, const float* gws, int nparts, float* g_state,
+                             float* g_biv, hipStream_t s) {
+    if constexpr (N * N <= 64) {
+        hipLaunchKernelGGL((rotor_gamma_biv_kernel<N>), dim3(1), dim3(1024), 0, s, biv, state, gws, nparts, g_biv);
+    } else {
+        hipLaunchKernelGGL(rotor_gamma_finalize_kernel, dim3(1), dim3(1024), 0, s, N, state, gws, nparts, g_state);
+        launch_compile_bwd<N>(biv, g_state, g_biv, s);
+    }
 }
 
 static int check_rotor_n(int n) {
@@ -1378,6 +1442,22 @@ int rotor16_bwd(const float* U, const float* x, const float* gy, long long ldg, 
                 int64_t batch, unsigned grid, void* stream);
 unsigned rotor16_bwd_grid(long long wanted);
 
+// gx (when given) and the per-workgroup partials of Gamma for the batch;
+// nparts = the partial count (0 for an empty batch)
+static int launch_gamma_parts(int n, const float* state, const float* x, const float* gy, int64_t ldg, float* gx,
+                              float* gws, int64_t batch, hipStream_t s, int& nparts) {
+    nparts = 0;
+    if (batch == 0) return CLF_OK;
+    if (rotor16_enabled(n)) {
+        nparts = (int)rotor16_bwd_grid(rotor_bwd_grid(n, batch));
+        if (int rc = rotor16_bwd(state + spin_offset(n), x, gy, ldg, gx, gws, batch, (unsigned)nparts, s)) return rc;
+    } else {
+        nparts = launch_gamma(n, state + n * n, x, gy, ldg, gx, gws, batch, s);
+    }
+    CLF_HIP_CHECK(hipGetLastError());
+    return CLF_OK;
+}
+
 int rotor_apply_fwd(int n, const float* state, const float* x, float* y, int64_t batch, void* stream) {
     if (int rc = check_rotor_n(n)) return rc;
     if (batch < 0) return set_error(CLF_ERR_ARG, "batch must be >= 0");
@@ -1406,26 +1486,51 @@ int rotor_apply_bwd(int n, const float* state, const float* x, const float* gy, 
     if (g_state && (!ws || ws_bytes < need))
         return set_error(CLF_ERR_WORKSPACE, "workspace of at least " + std::to_string(need) + " bytes required");
     hipStream_t s = (hipStream_t)stream;
-    float* gws = g_state ? (float*)ws : nullptr;
-    const bool mat = rotor16_enabled(n);
+    if (!g_state) {
+        if (batch == 0) return CLF_OK;
+        if (rotor16_enabled(n)) return rotor16_apply(false, state + spin_offset(n), gy, gx, batch, stream, ldg);
+        launch_chain(n, false, state + n * n, gy, gx, batch, s, ldg);
+        CLF_HIP_CHECK(hipGetLastError());
+        return CLF_OK;
+    }
+    float* gws = (float*)ws;
     int nparts = 0;
-    if (batch > 0) {
-        if (!g_state) {
-            if (mat) return rotor16_apply(false, state + spin_offset(n), gy, gx, batch, stream, ldg);
-            launch_chain(n, false, state + n * n, gy, gx, batch, s, ldg);
-        } else if (mat) {
-            nparts = (int)rotor16_bwd_grid(rotor_bwd_grid(n, batch));
-            if (int rc = rotor16_bwd(state + spin_offset(n), x, gy, ldg, gx, gws, batch, (unsigned)nparts, stream))
-                return rc;
-        } else {
-            nparts = launch_gamma(n, state + n * n, x, gy, ldg, gx, gws, batch, s);
-        }
-        CLF_HIP_CHECK(hipGetLastError());
-    }
-    if (g_state) {
-        hipLaunchKernelGGL(rotor_gamma_finalize_kernel, dim3(1), dim3(1024), 0, s, n, state, gws, nparts, g_state);
-        CLF_HIP_CHECK(hipGetLastError());
-    }
+    if (int rc = launch_gamma_parts(n, state, x, gy, ldg, gx, gws, batch, s, nparts)) return rc;
+    hipLaunchKernelGGL(rotor_gamma_finalize_kernel, dim3(1), dim3(1024), 0, s, n, state, gws, nparts, g_state);
+    CLF_HIP_CHECK(hipGetLastError());
+    return CLF_OK;
+}
+
+size_t rotor_biv_apply_ws_bytes(int n, int64_t batch) {
+    if (n < kRotorMinN || n > kRotorMaxN || batch < 0) return 0;
+    return ((rotor_apply_ws_bytes(n, batch) + 255) & ~size_t(255)) + (size_t)state_floats(n) * sizeof(float);
+}
+
+// The backward of apply(compile(biv), x) to biv and x: the apply backward's
+// partials, then their sum and the compile backward (one fused launch for
+// n <= 8; the finalize into the workspace and the compile backward above).
+int rotor_biv_apply_bwd(int n, const float* biv, const float* state, const float* x, const float* gy, int64_t ldg,
+                        float* gx, float* g_biv, int64_t batch, void* ws, size_t ws_bytes, void* stream) {
+    if (int rc = check_rotor_n(n)) return rc;
+    if (batch < 0) return set_error(CLF_ERR_ARG, "batch must be >= 0");
+    if (ldg != 0 && ldg != (1LL << n)) return set_error(CLF_ERR_ARG, "gy row stride must be 0 or 2^n");
+    if (!g_biv) return rotor_apply_bwd(n, state, x, gy, ldg, gx, nullptr, batch, nullptr, 0, stream);
+    if (!biv || !state || (batch > 0 && (!gy || !x))) return set_error(CLF_ERR_ARG, "null pointer argument");
+    if ((((uintptr_t)x) | ((uintptr_t)gy) | ((uintptr_t)gx)) & 15u)
+        return set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
+    if (gx && (gx == gy || gx == x)) return set_error(CLF_ERR_ARG, "gx must not alias x or gy");
+    const size_t need = rotor_biv_apply_ws_bytes(n, batch);
+    if (!ws || ws_bytes < need)
+        return set_error(CLF_ERR_WORKSPACE, "workspace of at least " + std::to_string(need) + " bytes required");
+    hipStream_t s = (hipStream_t)stream;
+    float* gws = (float*)ws;
+    int nparts = 0;
+    if (int rc = launch_gamma_parts(n, state, x, gy, ldg, gx, gws, batch, s, nparts)) return rc;
+    float* g_state = (float*)((char*)ws + ((rotor_apply_ws_bytes(n, batch) + 255) & ~size_t(255)));
+#define CLF_CALL(N) launch_gamma_biv<N>(biv, state, gws, nparts, g_state, g_biv, s)
+    CLF_COMPILE_DISPATCH(n, CLF_CALL)
+#undef CLF_CALL
+    CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }
 

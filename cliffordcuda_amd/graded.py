@@ -16,7 +16,7 @@ from ._validate import dim_to_n
 def _graded_launch(kind: int, n: int, neg: int, nul: int, grade: int, x: torch.Tensor) -> torch.Tensor:
     y = torch.empty_like(x)
     lib = _lib.load()
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x):
         rc = lib.clf_graded(kind, n, neg, nul, grade, x.data_ptr(), y.data_ptr(), x.shape[0],
                             _lib.stream_of(x))
     _lib.check(rc, "clf_graded")
@@ -55,7 +55,7 @@ def graded(kind: str, x: torch.Tensor, neg: int = 0, nul: int = 0, grade: int = 
 def _norm_sq_fwd(x: torch.Tensor, n: int, neg: int, nul: int) -> torch.Tensor:
     out = torch.empty(x.shape[0], dtype=x.dtype, device=x.device)
     lib = _lib.load()
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x):
         rc = lib.clf_norm_sq_fwd(n, neg, nul, x.data_ptr(), out.data_ptr(), x.shape[0], _lib.stream_of(x))
     _lib.check(rc, "clf_norm_sq_fwd")
     return out
@@ -65,7 +65,7 @@ def _norm_sq_bwd(x: torch.Tensor, gout: torch.Tensor, n: int, neg: int, nul: int
     gx = torch.empty_like(x)
     gout = gout.contiguous()
     lib = _lib.load()
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x):
         rc = lib.clf_norm_sq_bwd(n, neg, nul, x.data_ptr(), gout.data_ptr(), gx.data_ptr(), x.shape[0],
                                  _lib.stream_of(x))
     _lib.check(rc, "clf_norm_sq_bwd")

@@ -65,7 +65,7 @@ def _versor_try(xf, n, neg, nul, rtol):
     y = torch.empty_like(xf)
     flags = torch.empty(xf.shape[0], dtype=torch.int32, device=xf.device)
     lib = _lib.load()
-    with torch.cuda.device(xf.device):
+    with _lib.on_device(xf):
         rc = lib.clf_inverse_versor(n, xf.data_ptr(), xr.data_ptr(), y.data_ptr(), flags.data_ptr(), float(rtol),
                                     xf.shape[0], _lib.stream_of(xf))
     _lib.check(rc, "clf_inverse_versor")
@@ -81,7 +81,7 @@ def _rep_inverse(xf, n, neg, nul):
     y = torch.empty_like(xf)
     singular = torch.empty(xf.shape[0], dtype=torch.int32, device=xf.device)
     lib = _lib.load()
-    with torch.cuda.device(xf.device):
+    with _lib.on_device(xf):
         rc = lib.clf_inverse_rep(n, neg, nul, xf.data_ptr(), y.data_ptr(), singular.data_ptr(), xf.shape[0],
                                  _lib.stream_of(xf))
     _lib.check(rc, "clf_inverse_rep")

@@ -35,7 +35,7 @@ def _check_operands(a: torch.Tensor, b: torch.Tensor, name: str):
 def _product_fwd(op_code, n, neg, nul, a, b):
     c = torch.empty_like(a)
     lib = _lib.load()
-    with torch.cuda.device(a.device):
+    with _lib.on_device(a):
         rc = lib.clf_product_fwd(op_code, n, neg, nul, a.data_ptr(), b.data_ptr(), c.data_ptr(),
                                  a.shape[0], _lib.stream_of(a))
     _lib.check(rc, "clf_product_fwd")
@@ -49,7 +49,7 @@ def _product_bwd(op_code, n, neg, nul, a, b, gc, need_a, need_b):
         return None, None
     gc, ldg = _lib.grad_rows(gc, a.shape[1])
     lib = _lib.load()
-    with torch.cuda.device(a.device):
+    with _lib.on_device(a):
         rc = lib.clf_product_bwd_ld(op_code, n, neg, nul, a.data_ptr(), b.data_ptr(), gc.data_ptr(), ldg,
                                     _lib.ptr(ga), _lib.ptr(gb), a.shape[0], _lib.stream_of(a))
     _lib.check(rc, "clf_product_bwd_ld")
@@ -89,13 +89,14 @@ def product(op: str, a: torch.Tensor, b: torch.Tensor, metric=None) -> torch.Ten
         raise ValueError(f"regressive product undefined for degenerate metric {metric}")
     neg, nul = metric_masks(metric)
     shape = a.shape
-    a2 = a.contiguous().reshape(-1, dim)
-    b2 = b.contiguous().reshape(-1, dim)
+    flat = a.dim() != 2  # (batch, dim) inputs go in as they are: no view nodes in the autograd graph
+    a2 = a.contiguous().reshape(-1, dim) if flat else a.contiguous()
+    b2 = b.contiguous().reshape(-1, dim) if flat else b.contiguous()
     if torch.compiler.is_compiling():
         out = _ops.product(a2, b2, _lib.OP_CODES[op], n, neg, nul)
     else:
         out = _ProductFunc.apply(a2, b2, _lib.OP_CODES[op], n, neg, nul)
-    return out.reshape(shape)
+    return out.reshape(shape) if flat else out
 
 
 def geom_prod(a, b, metric=None):

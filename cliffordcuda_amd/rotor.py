@@ -54,7 +54,7 @@ def _compile_fwd(biv: torch.Tensor, n: int, want_cs: bool = False):
     state = torch.empty(_state_len(n), dtype=torch.float32, device=biv.device)
     cs = torch.empty(n_planes(n), 2, dtype=torch.float32, device=biv.device) if want_cs else None
     lib = _lib.load()
-    with torch.cuda.device(biv.device):
+    with _lib.on_device(biv):
         rc = lib.clf_rotor_compile_fwd(n, biv.data_ptr(), state.data_ptr(), _lib.ptr(cs), _lib.stream_of(biv))
     _lib.check(rc, "clf_rotor_compile_fwd")
     return (state, cs) if want_cs else state
@@ -65,7 +65,7 @@ def _compile_bwd(biv: torch.Tensor, g_state: torch.Tensor, n: int) -> torch.Tens
     g_state = g_state.contiguous()
     g_biv = torch.empty_like(biv)
     lib = _lib.load()
-    with torch.cuda.device(biv.device):
+    with _lib.on_device(biv):
         rc = lib.clf_rotor_compile_bwd(n, biv.data_ptr(), g_state.data_ptr(), g_biv.data_ptr(), _lib.stream_of(biv))
     _lib.check(rc, "clf_rotor_compile_bwd")
     return g_biv
@@ -76,7 +76,7 @@ def _cs_compile_bwd(biv: torch.Tensor, g_cs: torch.Tensor, n: int) -> torch.Tens
     g_cs = g_cs.contiguous()
     g_biv = torch.empty_like(biv)
     lib = _lib.load()
-    with torch.cuda.device(biv.device):
+    with _lib.on_device(biv):
         rc = lib.clf_rotor_cs_compile_bwd(n, biv.data_ptr(), g_cs.data_ptr(), g_biv.data_ptr(), _lib.stream_of(biv))
     _lib.check(rc, "clf_rotor_cs_compile_bwd")
     return g_biv
@@ -85,7 +85,7 @@ def _cs_compile_bwd(biv: torch.Tensor, g_cs: torch.Tensor, n: int) -> torch.Tens
 def _apply_fwd(state: torch.Tensor, x: torch.Tensor, n: int) -> torch.Tensor:
     y = torch.empty_like(x)
     lib = _lib.load()
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x):
         rc = lib.clf_rotor_apply_fwd(n, state.data_ptr(), x.data_ptr(), y.data_ptr(), x.shape[0], _lib.stream_of(x))
     _lib.check(rc, "clf_rotor_apply_fwd")
     return y
@@ -103,17 +103,39 @@ def _apply_bwd(state: torch.Tensor, x: torch.Tensor, gy: torch.Tensor, n: int, n
     if need_state:
         ws_bytes = lib.clf_rotor_apply_ws_bytes(n, x.shape[0])
         ws = torch.empty(max(1, ws_bytes // 4), dtype=torch.float32, device=x.device)
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x):
         rc = lib.clf_rotor_apply_bwd_ld(n, state.data_ptr(), x.data_ptr(), gy.data_ptr(), ldg, _lib.ptr(gx),
                                         _lib.ptr(g_state), x.shape[0], _lib.ptr(ws), ws_bytes, _lib.stream_of(x))
     _lib.check(rc, "clf_rotor_apply_bwd_ld")
     return g_state, gx
 
 
+def _biv_apply_bwd(biv: torch.Tensor, state: torch.Tensor, x: torch.Tensor, gy: torch.Tensor, n: int,
+                   need_biv: bool, need_x: bool):
+    """Gradients of apply(compile(biv), x) to biv and x in one library call."""
+    if not (need_biv or need_x):
+        return None, None
+    gy, ldg = _lib.grad_rows(gy, x.shape[1])
+    gx = torch.empty_like(x) if need_x else None
+    g_biv = torch.empty_like(biv) if need_biv else None
+    lib = _lib.load()
+    ws = None
+    ws_bytes = 0
+    if need_biv:
+        ws_bytes = lib.clf_rotor_bivector_apply_ws_bytes(n, x.shape[0])
+        ws = torch.empty(max(1, ws_bytes // 4), dtype=torch.float32, device=x.device)
+    with _lib.on_device(x):
+        rc = lib.clf_rotor_bivector_apply_bwd(n, biv.data_ptr(), state.data_ptr(), x.data_ptr(), gy.data_ptr(), ldg,
+                                              _lib.ptr(gx), _lib.ptr(g_biv), x.shape[0], _lib.ptr(ws), ws_bytes,
+                                              _lib.stream_of(x))
+    _lib.check(rc, "clf_rotor_bivector_apply_bwd")
+    return g_biv, gx
+
+
 def _cs_apply_fwd(cs: torch.Tensor, x: torch.Tensor, n: int) -> torch.Tensor:
     y = torch.empty_like(x)
     lib = _lib.load()
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x):
         rc = lib.clf_rotor_cs_apply_fwd(n, cs.data_ptr(), x.data_ptr(), y.data_ptr(), x.shape[0], _lib.stream_of(x))
     _lib.check(rc, "clf_rotor_cs_apply_fwd")
     return y
@@ -131,7 +153,7 @@ def _cs_apply_bwd(cs: torch.Tensor, y: torch.Tensor, gy: torch.Tensor, n: int, n
     if need_cs:
         ws_bytes = lib.clf_rotor_cs_apply_ws_bytes(n, y.shape[0])
         ws = torch.empty(max(1, ws_bytes // 4), dtype=torch.float32, device=y.device)
-    with torch.cuda.device(y.device):
+    with _lib.on_device(y):
         rc = lib.clf_rotor_cs_apply_bwd_ld(n, cs.data_ptr(), y.data_ptr(), gy.data_ptr(), ldg, _lib.ptr(gx),
                                            _lib.ptr(g_cs), y.shape[0], _lib.ptr(ws), ws_bytes, _lib.stream_of(y))
     _lib.check(rc, "clf_rotor_cs_apply_bwd_ld")
@@ -139,22 +161,6 @@ def _cs_apply_bwd(cs: torch.Tensor, y: torch.Tensor, gy: torch.Tensor, n: int, n
 
 
 # ---- autograd ---------------------------------------------------------------------
-
-class _CompileStateFunc(torch.autograd.Function):
-    """bivector -> internal rotor state; the backward reads the Q block of the
-    state's gradient only (the cs and spin blocks are caches of Q)."""
-
-    @staticmethod
-    def forward(ctx, biv, n):
-        ctx.save_for_backward(biv)
-        ctx.n = n
-        return _compile_fwd(biv, n)
-
-    @staticmethod
-    def backward(ctx, g_state):
-        (biv,) = ctx.saved_tensors
-        return _compile_bwd(biv, g_state, ctx.n), None
-
 
 class _KnownStateFunc(torch.autograd.Function):
     """A state already compiled from ``biv``, attached to biv's graph."""
@@ -183,6 +189,25 @@ class _StateApplyFunc(torch.autograd.Function):
         state, x = ctx.saved_tensors
         g_state, gx = _apply_bwd(state, x, gy, ctx.n, ctx.needs_input_grad[0], ctx.needs_input_grad[1])
         return g_state, gx, None
+
+
+class _BivectorApplyFunc(torch.autograd.Function):
+    """y = ~R x R with R compiled from the bivector in the same call: one
+    autograd node for compile and apply, whose backward is one library call
+    (apply backward, batch sum and compile backward)."""
+
+    @staticmethod
+    def forward(ctx, biv, x, n):
+        state = _compile_fwd(biv, n)
+        ctx.save_for_backward(biv, state, x)
+        ctx.n = n
+        return _apply_fwd(state, x, n)
+
+    @staticmethod
+    def backward(ctx, gy):
+        biv, state, x = ctx.saved_tensors
+        g_biv, gx = _biv_apply_bwd(biv, state, x, gy, ctx.n, ctx.needs_input_grad[0], ctx.needs_input_grad[1])
+        return g_biv, gx, None
 
 
 class _CompileCsFunc(torch.autograd.Function):
@@ -287,7 +312,7 @@ def apply_bivector(bivector: torch.Tensor, x: torch.Tensor, n: int) -> torch.Ten
     """y = ~R x R, R = exp(sum_m b_m e_{i_m} e_{j_m}); differentiable to the
     bivector and to x (one compile launch, the state never leaves this call)."""
     _check_n(n)
-    biv = bivector.reshape(-1)
     if torch.compiler.is_compiling():
-        return _ops.rotor_apply(_ops.rotor_compile(biv.contiguous(), n), x.contiguous(), n)
-    return _StateApplyFunc.apply(_CompileStateFunc.apply(biv, n), x, n)
+        return _ops.rotor_apply(_ops.rotor_compile(bivector.reshape(-1).contiguous(), n), x.contiguous(), n)
+    # the kernels read the C(n,2) floats of a contiguous bivector whatever its shape
+    return _BivectorApplyFunc.apply(bivector.contiguous(), x, n)

@@ -190,6 +190,23 @@ int clf_rotor_apply_bwd_ld(int n, const float* state, const float* x, const floa
                            float* gx, float* g_state, int64_t batch,
                            void* ws, size_t ws_bytes, void* stream);
 
+/* Bytes of device workspace clf_rotor_bivector_apply_bwd needs when g_biv != NULL. */
+size_t clf_rotor_bivector_apply_ws_bytes(int n, int64_t batch);
+
+/* Backward of y = apply(compile(biv), x) straight to the bivector: gx = the
+ * transposed sandwich of gy, g_biv = dL/dbiv (C(n,2) floats, summed over the
+ * batch), from the state clf_rotor_compile_fwd made of biv. One call for what
+ * clf_rotor_apply_bwd + clf_rotor_compile_bwd do in two (for n <= 8 the batch
+ * sum and the compile backward share one launch and g_state never goes
+ * through memory). gy's rows are ldg floats apart (2^n, or 0 for one row read
+ * for every batch row). gx or g_biv may be NULL. Replaces the backward of the
+ * reference's apply_rotor(compile_bivector(b), x) chain
+ * (extensions/rotor/givens_apply/mb_perm_packed.py:20-42 with
+ * kernels/rotor/givens_factor.cu:202-231 and kernels/rotor/eigh_exp.cu:325-361). */
+int clf_rotor_bivector_apply_bwd(int n, const float* biv, const float* state, const float* x,
+                                 const float* gy, int64_t ldg, float* gx, float* g_biv,
+                                 int64_t batch, void* ws, size_t ws_bytes, void* stream);
+
 /* y = chain(cs) x for a caller's cs (any pairs, unit or not), `batch` rows.
  * Replaces givens_mb_perm_packed_fwd (kernels/rotor/givens_apply_mb_perm_packed.cu:250-267). */
 int clf_rotor_cs_apply_fwd(int n, const float* cs, const float* x, float* y,

@@ -305,3 +305,58 @@ def test_rotor8_state_spin_block():
         assert state.numel() == 8 * 8 + 56 + 256
         U = state[120:].double().view(16, 16).cpu()
         torch.testing.assert_close(U @ U.T, torch.eye(16, dtype=torch.float64), atol=2e-6, rtol=0)
+
+
+@pytest.mark.parametrize("n,B", [(3, 5), (7, 333), (8, 1), (8, 40001), (9, 77), (12, 9)])
+def test_bivector_apply_bwd_matches_two_call_backward(n, B):
+    """clf_rotor_bivector_apply_bwd (one call: apply backward, batch sum and
+    compile backward, fused into one launch for n <= 8) against
+    clf_rotor_apply_bwd + clf_rotor_compile_bwd through the C ABI: gx bitwise,
+    the bivector gradient to 1e-6 (the fused launch keeps dL/dQ in fp64
+    instead of rounding it to fp32 between the two launches); then the
+    oracle on small batches."""
+    from cliffordcuda_amd import _lib, rotor
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(n * 1000 + B)
+    C = n * (n - 1) // 2
+    biv = (0.6 * torch.randn(1, C, generator=g)).cuda()
+    x = torch.randn(B, 1 << n, generator=g).cuda()
+    gy = torch.randn(B, 1 << n, generator=g).cuda()
+    state = rotor._compile_fwd(biv, n)
+    s = _lib.stream_of(x)
+    print(f"[case] bivector apply bwd n={n} B={B}", flush=True)
+    ws_bytes = lib.clf_rotor_bivector_apply_ws_bytes(n, B)
+    ws = torch.empty(ws_bytes // 4 + 64, device="cuda")
+    gx1 = torch.empty_like(x)
+    gb1 = torch.empty_like(biv)
+    _lib.check(lib.clf_rotor_bivector_apply_bwd(n, biv.data_ptr(), state.data_ptr(), x.data_ptr(), gy.data_ptr(),
+                                                1 << n, gx1.data_ptr(), gb1.data_ptr(), B, ws.data_ptr(), ws_bytes,
+                                                s), "clf_rotor_bivector_apply_bwd")
+    ws2_bytes = lib.clf_rotor_apply_ws_bytes(n, B)
+    ws2 = torch.empty(ws2_bytes // 4 + 64, device="cuda")
+    gx2 = torch.empty_like(x)
+    gstate = torch.empty_like(state)
+    gb2 = torch.empty_like(biv)
+    _lib.check(lib.clf_rotor_apply_bwd(n, state.data_ptr(), x.data_ptr(), gy.data_ptr(), gx2.data_ptr(),
+                                       gstate.data_ptr(), B, ws2.data_ptr(), ws2_bytes, s), "clf_rotor_apply_bwd")
+    _lib.check(lib.clf_rotor_compile_bwd(n, biv.data_ptr(), gstate.data_ptr(), gb2.data_ptr(), s),
+               "clf_rotor_compile_bwd")
+    # gx only and g_biv only
+    gx3 = torch.empty_like(x)
+    gb3 = torch.empty_like(biv)
+    _lib.check(lib.clf_rotor_bivector_apply_bwd(n, biv.data_ptr(), state.data_ptr(), x.data_ptr(), gy.data_ptr(),
+                                                1 << n, gx3.data_ptr(), None, B, None, 0, s), "gx only")
+    _lib.check(lib.clf_rotor_bivector_apply_bwd(n, biv.data_ptr(), state.data_ptr(), x.data_ptr(), gy.data_ptr(),
+                                                1 << n, None, gb3.data_ptr(), B, ws.data_ptr(), ws_bytes, s),
+               "g_biv only")
+    torch.cuda.synchronize()
+    assert torch.equal(gx1, gx2) and torch.equal(gx3, gx1)
+    assert torch.equal(gb3, gb1)
+    assert rel_err(gb1, gb2) <= 1e-6
+    if B <= 400 and n <= 9:
+        _, gb64, gx64 = oracle_step(biv.cpu(), x.cpu(), gy.cpu(), n)
+        assert rel_err(gb1, gb64) <= TOL and rel_err(gx1, gx64) <= TOL
+    # a workspace below the stated size is refused before any launch
+    assert lib.clf_rotor_bivector_apply_bwd(n, biv.data_ptr(), state.data_ptr(), x.data_ptr(), gy.data_ptr(),
+                                            1 << n, None, gb3.data_ptr(), B, ws.data_ptr(), ws_bytes - 4,
+                                            s) == _lib.CLF_ERR_WORKSPACE
