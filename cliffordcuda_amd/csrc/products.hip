@@ -50,11 +50,8 @@ __device__ __forceinline__ float flip(float x, unsigned m) { return __uint_as_fl
 // XOR swizzle of the float4 slot inside a 64-byte block
 __device__ __forceinline__ unsigned swz(unsigned blk) { return ((blk >> 1) ^ (blk >> 3)) & 3u; }
 
-// rs: the staged row's extra slot skew (balanced kernels: rows that share a
-// quarter-wave read the same blocks at the same step, so their slots differ)
-__device__ __forceinline__ void load_blk(const float4* __restrict__ base, unsigned blk, float (&v)[16],
-                                         unsigned rs = 0u) {
-    const unsigned s = swz(blk) ^ rs;
+__device__ __forceinline__ void load_blk(const float4* __restrict__ base, unsigned blk, float (&v)[16]) {
+    const unsigned s = swz(blk);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const float4 t = base[(blk << 2) + ((unsigned)q ^ s)];
@@ -62,6 +59,30 @@ __device__ __forceinline__ void load_blk(const float4* __restrict__ base, unsign
         v[4 * q + 1] = t.y;
         v[4 * q + 2] = t.z;
         v[4 * q + 3] = t.w;
+    }
+}
+
+// The balanced kernels' staged groups sit in static LDS arrays aligned to 64
+// bytes, so a block's four slots (blk << 2) + (q ^ s) are one slot address
+// xor 16 q: one address per block instead of one per slot. rs is the staged
+// row's extra slot skew (rows that share a quarter-wave read the same blocks
+// at the same step, so their slots differ).
+typedef __attribute__((address_space(3))) float4 lds_f4;
+__device__ __forceinline__ unsigned lds_addr4(const float4* p) { return (unsigned)(uintptr_t)(const lds_f4*)p; }
+__device__ __forceinline__ float4 lds_ld4(unsigned a) { return *(const lds_f4*)(uintptr_t)a; }
+
+// load_blk / load_blk_rev on a 64-byte aligned staged row (REV: v[y] = block[15 - y])
+template <bool REV = false>
+__device__ __forceinline__ void load_blk_x(const float4* __restrict__ base, unsigned blk, float (&v)[16],
+                                           unsigned rs) {
+    const unsigned a0 = lds_addr4(base + ((blk << 2) | (swz(blk) ^ rs)));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 t = lds_ld4(a0 ^ ((unsigned)q << 4));
+        v[REV ? 15 - (4 * q + 0) : 4 * q + 0] = t.x;
+        v[REV ? 15 - (4 * q + 1) : 4 * q + 1] = t.y;
+        v[REV ? 15 - (4 * q + 2) : 4 * q + 2] = t.z;
+        v[REV ? 15 - (4 * q + 3) : 4 * q + 3] = t.w;
     }
 }
 
@@ -78,9 +99,8 @@ __device__ __forceinline__ void load_blk_plain(const float4* __restrict__ base, 
 }
 
 // reversed element order: v[y] = block[15 - y]
-__device__ __forceinline__ void load_blk_rev(const float4* __restrict__ base, unsigned blk, float (&v)[16],
-                                             unsigned rs = 0u) {
-    const unsigned s = swz(blk) ^ rs;
+__device__ __forceinline__ void load_blk_rev(const float4* __restrict__ base, unsigned blk, float (&v)[16]) {
+    const unsigned s = swz(blk);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const float4 t = base[(blk << 2) + ((unsigned)q ^ s)];
@@ -795,8 +815,8 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
             const HiSign hr = hi_sign<OP>(part ^ o, part, P.negh, P.nulh, full, P.nm1, P.mu);
             {
                 float av[16], bv[16];
-                load_blk(la, part, av, rs);
-                load_blk(lb, part ^ o, bv, rs);
+                load_blk_x(la, part, av, rs);
+                load_blk_x(lb, part ^ o, bv, rs);
                 const unsigned m = hl.valid ? hl.mask : 0u;
                 apply_flips(bv, m, m ^ (cross_pi<OP>(part, P.nm1) << 31));
                 if (hl.valid) {
@@ -807,8 +827,8 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
             }
             if (hr.valid) {
                 float av[16], bv[16];
-                load_blk(la, part ^ o, av, rs);
-                load_blk(lb, part, bv, rs);
+                load_blk_x(la, part ^ o, av, rs);
+                load_blk_x(lb, part, bv, rs);
                 apply_flips(bv, hr.mask, hr.mask ^ (cross_pi<OP>(part ^ o, P.nm1) << 31));
                 lowblock_fwd<LV_RC, kLowNeg>(acc, av, bv);
             }
@@ -817,8 +837,8 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
             const HiSign hs = hi_sign<OP>(ih, jh, P.negh, P.nulh, full, P.nm1, P.mu);
             if (hs.valid) {
                 float av[16], bv[16];
-                load_blk(la, ih, av, rs);
-                load_blk(lb, jh, bv, rs);
+                load_blk_x(la, ih, av, rs);
+                load_blk_x(lb, jh, bv, rs);
                 apply_flips(bv, hs.mask, hs.mask ^ (cross_pi<OP>(ih, P.nm1) << 31));
                 if (OP == OP_INNER) lowblock_fwd<VAR, kLowNeg>(acc, av, bv);
                 else fwd_block_dispatch<OP, LOWNEG>(acc, av, bv, ih, jh);
@@ -829,11 +849,11 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
                                         : hi_sign<OP>(m, h, P.negh, P.nulh, full, P.nm1, P.mu);
             if (hs.valid) {
                 float g[16];
-                if (OP == OP_REGR) load_blk_rev(lg, full ^ x, g, rs);
-                else load_blk(lg, x, g, rs);
+                if (OP == OP_REGR) load_blk_x<true>(lg, full ^ x, g, rs);
+                else load_blk_x(lg, x, g, rs);
                 if (ROLE == 1) {
                     float bv[16];
-                    load_blk(lb, m, bv, rs);
+                    load_blk_x(lb, m, bv, rs);
                     apply_flips(bv, hs.mask, hs.mask ^ (cross_pi<OP>(h, P.nm1) << 31));
                     if (OP == OP_INNER && CLS == 4)  // ih = h, jh = m
                         lowblock_ga_split<kLowNeg>(acc, bv, (h & ~m) == 0u, (m & ~h) == 0u, g);
@@ -842,7 +862,7 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
                 } else {
                     const unsigned pm = cross_pi<OP>(m, P.nm1) << 31;
                     float av[16], gt[16];
-                    load_blk(la, m, av, rs);
+                    load_blk_x(la, m, av, rs);
                     apply_flips(av, hs.mask, hs.mask ^ pm);
 #pragma unroll
                     for (int e = 0; e < 16; ++e) gt[e] = (cpopc((unsigned)e) & 1) ? flip(g[e], pm) : g[e];
@@ -1010,7 +1030,7 @@ __device__ __forceinline__ void bal_role_tab(int T, unsigned hdr, const unsigned
                 const unsigned sm = hs.mask;
                 const unsigned pm = cross_pi<OP>(ob, P.nm1) << 31;
                 float xv[16];
-                load_blk(ROLE == 1 ? lb : la, ob, xv, rs);
+                load_blk_x(ROLE == 1 ? lb : la, ob, xv, rs);
                 apply_flips(xv, sm, sm ^ pm);
                 const float g0 = reinterpret_cast<const float*>(lg)[4u * (swz(0u) ^ rs)];  // gc element 0
                 diag_sub<LOWNEG>(acc, xv, g0, std::make_integer_sequence<int, 16>{});
@@ -1025,25 +1045,25 @@ __device__ __forceinline__ void bal_role_tab(int T, unsigned hdr, const unsigned
             const unsigned sm = (e & kTabSign) << 19;  // bit 12 -> the float sign bit
             if (ROLE == 0) {  // ih = pb, jh = pb ^ ob
                 float av[16], bv[16];
-                load_blk(la, pb, av, rs);
-                load_blk(lb, pb ^ ob, bv, rs);
+                load_blk_x(la, pb, av, rs);
+                load_blk_x(lb, pb ^ ob, bv, rs);
                 apply_flips(bv, sm, sm ^ (cross_pi<OP>(pb, P.nm1) << 31));
                 fwd_block_dispatch<OP, LOWNEG>(acc, av, bv, pb, pb ^ ob);
             } else {
                 const unsigned x = ob ^ pb;
                 float g[16];
-                if (OP == OP_REGR) load_blk_rev(lg, full ^ x, g, rs);
-                else load_blk(lg, x, g, rs);
+                if (OP == OP_REGR) load_blk_x<true>(lg, full ^ x, g, rs);
+                else load_blk_x(lg, x, g, rs);
                 if (ROLE == 1) {  // h = ob, m = pb
                     float bv[16];
-                    load_blk(lb, pb, bv, rs);
+                    load_blk_x(lb, pb, bv, rs);
                     apply_flips(bv, sm, sm ^ (cross_pi<OP>(ob, P.nm1) << 31));
                     if (OP == OP_INNER) lowblock_ga<VAR, LOWNEG>(acc, bv, g);
                     else ga_block_dispatch<OP, LOWNEG>(acc, bv, g, ob, pb);
                 } else {  // h = ob (jh), m = pb (ih)
                     const unsigned pm = cross_pi<OP>(pb, P.nm1) << 31;
                     float av[16], gt[16];
-                    load_blk(la, pb, av, rs);
+                    load_blk_x(la, pb, av, rs);
                     apply_flips(av, sm, sm ^ pm);
 #pragma unroll
                     for (int k = 0; k < 16; ++k) gt[k] = (cpopc((unsigned)k) & 1) ? flip(g[k], pm) : g[k];
@@ -1088,34 +1108,65 @@ struct BalPre {
     float4 v[4];
 };
 
-// cmask masks the float4 index: -1 (packed rows) or 2^(n-2) - 1 (one row for
-// all rows, an upstream gradient broadcast over the batch)
-__device__ __forceinline__ BalPre bal_fetch(const float* __restrict__ src, long long grp, long long batch, int n,
-                                            int lane, long long cmask = -1) {
-    BalPre p;
+// A lane's share of a group (1024 floats per operand): chunks c = lane + 64 i
+// (i < 4), row rr = c >> (n - 2) of the group, float4 ff = c & (D4 - 1), and
+// the chunk's staged LDS byte offset (stage_rows' layout: row rr at rr * D4,
+// float4 slots swizzled inside a block, with the row's skew rr & 3 xor-ed into
+// the slot). Fixed for the kernel, so a group's fetch and staging take no
+// per-group index arithmetic.
+struct BalLane {
+    unsigned rr[4], ff[4], so[4];
+};
+
+__device__ __forceinline__ BalLane bal_lane(int n, int lane) {
+    BalLane L;
     const int d4_log = n - 2;
-    const long long last = (batch << d4_log) - (1LL << d4_log);  // first chunk of the last row
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        long long c = grp * kBalGroupF4 + lane + 64 * i;
-        if (c >= (batch << d4_log)) c = last + (c & ((1LL << d4_log) - 1));
-        p.v[i] = reinterpret_cast<const float4*>(src)[c & cmask];
+        const unsigned c = (unsigned)(lane + 64 * i);
+        const unsigned r = c >> d4_log, f = c & ((1u << d4_log) - 1u);
+        const unsigned blk = f >> 2, q = f & 3u;
+        L.rr[i] = r;
+        L.ff[i] = f;
+        L.so[i] = 16u * ((r << d4_log) + (blk << 2) + (q ^ swz(blk) ^ (r & 3u)));
+    }
+    return L;
+}
+
+// Where a group's rows come from: the first row's address (wave-uniform) and
+// the last row of the group to read; rows past it re-read it (the end of the
+// batch; every row is row 0 of an upstream gradient broadcast over the batch;
+// a group past the end reads the batch's last row).
+struct BalSrc {
+    const float4* g0;
+    unsigned rlim;
+};
+
+__device__ __forceinline__ BalSrc bal_src(const float* __restrict__ src, long long grp, long long batch, int n, int R,
+                                          bool bcast = false) {
+    const long long row0 = grp * R;
+    const bool in = row0 < batch;
+    const long long first = bcast ? 0 : (in ? row0 : batch - 1);
+    const long long left = (bcast || !in) ? 1 : (batch - row0 < R ? batch - row0 : R);
+    return {reinterpret_cast<const float4*>(src) + (first << (n - 2)), (unsigned)(left - 1)};
+}
+
+__device__ __forceinline__ BalPre bal_fetch(const BalSrc& s, const BalLane& L, int d4_log) {
+    BalPre p;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const unsigned row = L.rr[i] < s.rlim ? L.rr[i] : s.rlim;
+        p.v[i] = s.g0[(row << d4_log) | L.ff[i]];
     }
     return p;
 }
 
-// staged like stage_rows: row r at r * D4, float4 slots swizzled inside a block,
-// with the row's skew (r & 3) xor-ed into the slot
-__device__ __forceinline__ void bal_stage(float4* __restrict__ dst, const BalPre& p, int n, int lane) {
-    const int d4_log = n - 2;
+__device__ __forceinline__ void lds_st4(unsigned a, float4 v) { *(lds_f4*)(uintptr_t)a = v; }
+
+__device__ __forceinline__ void bal_stage(float4* __restrict__ dst, const BalPre& p, const BalLane& L) {
+    const unsigned a = lds_addr4(dst);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int c = lane + 64 * i;
-        const int r = c >> d4_log;
-        const unsigned f = (unsigned)c & ((1u << d4_log) - 1u);
-        const unsigned blk = f >> 2, q = f & 3u;
-        dst[(r << d4_log) + (int)((blk << 2) + (q ^ swz(blk) ^ ((unsigned)r & 3u)))] = p.v[i];
-    }
+    for (int i = 0; i < 4; ++i) lds_st4(a + L.so[i], p.v[i]);
 }
 
 template <int OP, bool LOWNEG>
@@ -1124,8 +1175,8 @@ __global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A,
     // LDS per wave: a | b | heads. The inner product runs its fused round
     // (class 3: lc and rc halves of every pair), so every op stores directly.
     constexpr int kCls = OP == OP_INNER ? 3 : 0;
-    __shared__ float4 lds[4][3 * kBalGroupF4];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __shared__ __attribute__((aligned(64))) float4 lds[4][3 * kBalGroupF4];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int n = P.n;
     const int lpr_log = n - 4;
     const unsigned NB = 1u << lpr_log;
@@ -1150,13 +1201,15 @@ __global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A,
     const long long ngrp = (P.batch + R - 1) / R;
     const long long gstride = (long long)gridDim.x * 4;
     long long grp = (long long)blockIdx.x * 4 + wave;
-    BalPre pa = bal_fetch(A, grp, P.batch, n, lane);
-    BalPre pb = bal_fetch(B, grp, P.batch, n, lane);
+    const BalLane L = bal_lane(n, lane);
+    const int d4_log = n - 2;
+    BalPre pa = bal_fetch(bal_src(A, grp, P.batch, n, R), L, d4_log);
+    BalPre pb = bal_fetch(bal_src(B, grp, P.batch, n, R), L, d4_log);
     for (; grp < ngrp; grp += gstride) {
-        bal_stage(sa, pa, n, lane);
-        bal_stage(sb, pb, n, lane);
-        pa = bal_fetch(A, grp + gstride, P.batch, n, lane);
-        pb = bal_fetch(B, grp + gstride, P.batch, n, lane);
+        bal_stage(sa, pa, L);
+        bal_stage(sb, pb, L);
+        pa = bal_fetch(bal_src(A, grp + gstride, P.batch, n, R), L, d4_log);
+        pb = bal_fetch(bal_src(B, grp + gstride, P.batch, n, R), L, d4_log);
         wave_lds_sync();
         const long long row = grp * R + r;
         float4* out = row < P.batch ? reinterpret_cast<float4*>(C) + (row << (n - 2)) : nullptr;
@@ -1179,10 +1232,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     constexpr bool kDeals = OP == OP_INNER;
     constexpr bool kTab = OP != OP_GEOM;  // every op but geom runs from schedule tables
     constexpr int kTabs = kDeals ? 4 : 2;
-    __shared__ float4 lds[4][(kDeals ? 4 : 3) * kBalGroupF4];  // a | b | gc [| the inner product's partials]
+    __shared__ __attribute__((aligned(64))) float4 lds[4][(kDeals ? 4 : 3) * kBalGroupF4];  // a | b | gc [| the inner product's partials]
     __shared__ unsigned short tab[kTab ? kTabs : 1][kTab ? kBalTabEntries : 1];
     __shared__ unsigned hdr[kTab ? kTabs : 1][64];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int n = P.n;
     const int lpr_log = n - 4;
     const unsigned NB = 1u << lpr_log;
@@ -1227,19 +1280,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     const long long ngrp = (P.batch + R - 1) / R;
     const long long gstride = (long long)gridDim.x * 4;
     long long grp = (long long)blockIdx.x * 4 + wave;
+    const BalLane L = bal_lane(n, lane);
+    const int d4_log = n - 2;
+    const bool gbc = P.ldg4 == 0;  // gc: one row for all rows
     BalPre pa, pb;
-    if (want_b) pa = bal_fetch(A, grp, P.batch, n, lane);
-    if (want_a) pb = bal_fetch(B, grp, P.batch, n, lane);
-    const long long gmask = P.ldg4 ? -1LL : (1LL << (n - 2)) - 1;
-    BalPre pg = bal_fetch(GC, grp, P.batch, n, lane, gmask);
+    if (want_b) pa = bal_fetch(bal_src(A, grp, P.batch, n, R), L, d4_log);
+    if (want_a) pb = bal_fetch(bal_src(B, grp, P.batch, n, R), L, d4_log);
+    BalPre pg = bal_fetch(bal_src(GC, grp, P.batch, n, R, gbc), L, d4_log);
     for (; grp < ngrp; grp += gstride) {
         const long long row = grp * R + r;
         const bool row_ok = row < P.batch;
-        bal_stage(sg, pg, n, lane);
-        pg = bal_fetch(GC, grp + gstride, P.batch, n, lane, gmask);
+        bal_stage(sg, pg, L);
+        pg = bal_fetch(bal_src(GC, grp + gstride, P.batch, n, R, gbc), L, d4_log);
         if (want_a) {  // uniform: a kernel argument
-            bal_stage(sb, pb, n, lane);
-            pb = bal_fetch(B, grp + gstride, P.batch, n, lane);
+            bal_stage(sb, pb, L);
+            pb = bal_fetch(bal_src(B, grp + gstride, P.batch, n, R), L, d4_log);
             wave_lds_sync();
             float4* out = row_ok ? reinterpret_cast<float4*>(GA) + (row << (n - 2)) : nullptr;
             if constexpr (kDeals) {
@@ -1257,8 +1312,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
             wave_lds_sync();
         }
         if (want_b) {
-            bal_stage(sa, pa, n, lane);
-            pa = bal_fetch(A, grp + gstride, P.batch, n, lane);
+            bal_stage(sa, pa, L);
+            pa = bal_fetch(bal_src(A, grp + gstride, P.batch, n, R), L, d4_log);
             wave_lds_sync();
             float4* out = row_ok ? reinterpret_cast<float4*>(GB) + (row << (n - 2)) : nullptr;
             if constexpr (kDeals) {
