@@ -67,9 +67,13 @@ __device__ __forceinline__ void load_blk(const float4* __restrict__ base, unsign
 // xor 16 q: one address per block instead of one per slot. rs is the staged
 // row's extra slot skew (rows that share a quarter-wave read the same blocks
 // at the same step, so their slots differ).
-typedef __attribute__((address_space(3))) float4 lds_f4;
-__device__ __forceinline__ unsigned lds_addr4(const float4* p) { return (unsigned)(uintptr_t)(const lds_f4*)p; }
-__device__ __forceinline__ float4 lds_ld4(unsigned a) { return *(const lds_f4*)(uintptr_t)a; }
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4f_t lds_v4f;
+__device__ __forceinline__ unsigned lds_addr4(const float4* p) { return (unsigned)(uintptr_t)(const lds_v4f*)p; }
+__device__ __forceinline__ float4 lds_ld4(unsigned a) {
+    const v4f_t v = *(const lds_v4f*)(uintptr_t)a;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
 
 // load_blk / load_blk_rev on a 64-byte aligned staged row (REV: v[y] = block[15 - y])
 template <bool REV = false>
@@ -1161,7 +1165,9 @@ __device__ __forceinline__ BalPre bal_fetch(const BalSrc& s, const BalLane& L, i
     return p;
 }
 
-__device__ __forceinline__ void lds_st4(unsigned a, float4 v) { *(lds_f4*)(uintptr_t)a = v; }
+__device__ __forceinline__ void lds_st4(unsigned a, float4 v) {
+    *(lds_v4f*)(uintptr_t)a = v4f_t{v.x, v.y, v.z, v.w};
+}
 
 __device__ __forceinline__ void bal_stage(float4* __restrict__ dst, const BalPre& p, const BalLane& L) {
     const unsigned a = lds_addr4(dst);
