@@ -768,6 +768,17 @@ static long long rep_blocks(int n, int64_t batch) {
     return g < 1 ? 1 : (g > cap ? cap : g);
 }
 
+// The n = 8 backward launches one workgroup per 16 rows (each wave one group
+// of four rows) instead of walking a capped grid: at the headline shape
+// (262144 rows) 213 against 224 us with the 2048-workgroup cap (4096 and 8192
+// workgroups: 221 and 217 us). The cap only bounds the grid dimension; the
+// kernel's grid-stride loop covers any batch.
+static long long rep16_bwd_blocks(int64_t batch) {
+    const long long g = (batch + 15) / 16;
+    const long long cap = 1LL << 24;
+    return g < 1 ? 1 : (g > cap ? cap : g);
+}
+
 int rep_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64_t batch, void* stream) {
     if (n == 9 || n == 10) return split_fwd(n, neg, a, b, c, batch, stream);
     if (n == 7) return rep7_fwd(neg, a, b, c, batch, stream);
@@ -813,7 +824,8 @@ int rep_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc
             {
                 const bool nt = stream_nt((3 + (ga != nullptr) + (gb != nullptr)) * 1024.0 * (double)batch);
 #define CLF_REP16_BWD(NT, WA, WB)                                                                                 \
-    hipLaunchKernelGGL((rep16_bwd_kernel<NT, WA, WB>), dim3((unsigned)want), dim3(256), 0, s, a, b, gc,          \
+    hipLaunchKernelGGL((rep16_bwd_kernel<NT, WA, WB>), dim3((unsigned)rep16_bwd_blocks(batch)), dim3(256), 0, s,  \
+                       a, b, gc,                                                                                 \
                        (long long)ldg, ga, gb, (long long)batch, T)
                 if (ga && gb) {
                     if (nt) CLF_REP16_BWD(true, true, true);
