@@ -398,8 +398,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
 
 // GA and GB are compile-time flags (a gradient that is not wanted has no
 // branch around its stores). dA of a group is stored right after the group's
-// second wait, dB right after the next group's first wait.
-template <bool NT, bool WA, bool WB>
+// second wait, dB right after the next group's first wait. ONE: the grid covers
+// the batch (one group per wave), so no next group is prefetched.
+template <bool NT, bool WA, bool WB, bool ONE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void rep16_bwd_kernel(
     const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ GC, long long ldg,
     float* __restrict__ GA, float* __restrict__ GB, long long batch, RepTable T) {
@@ -451,8 +452,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void r
         }
         wave_lds_sync();
         stage16(s1, pa, lane, oddc);
-        pg = fetch16<NT>(GC, row0 + stride, batch, lane, ldg);
-        pb = fetch16<NT>(B, row0 + stride, batch, lane);
+        if (!ONE) {
+            pg = fetch16<NT>(GC, row0 + stride, batch, lane, ldg);
+            pb = fetch16<NT>(B, row0 + stride, batch, lane);
+        }
         if (WA) store16<NT>(GA, sr, row0, batch, lane, oddc);
         wave_lds_sync();
         if (WB) {
@@ -823,10 +826,17 @@ int rep_bwd(int n, uint32_t neg, const float* a, const float* b, const float* gc
             if (!ga && !gb) break;
             {
                 const bool nt = stream_nt((3 + (ga != nullptr) + (gb != nullptr)) * 1024.0 * (double)batch);
-#define CLF_REP16_BWD(NT, WA, WB)                                                                                 \
-    hipLaunchKernelGGL((rep16_bwd_kernel<NT, WA, WB>), dim3((unsigned)rep16_bwd_blocks(batch)), dim3(256), 0, s,  \
-                       a, b, gc,                                                                                 \
-                       (long long)ldg, ga, gb, (long long)batch, T)
+                const long long nb = rep16_bwd_blocks(batch);
+                const bool one = nb * 16 >= batch;
+#define CLF_REP16_BWD(NT, WA, WB)                                                                               \
+    do {                                                                                                       \
+        if (one)                                                                                               \
+            hipLaunchKernelGGL((rep16_bwd_kernel<NT, WA, WB, true>), dim3((unsigned)nb), dim3(256), 0, s, a, b, \
+                               gc, (long long)ldg, ga, gb, (long long)batch, T);                               \
+        else                                                                                                   \
+            hipLaunchKernelGGL((rep16_bwd_kernel<NT, WA, WB, false>), dim3((unsigned)nb), dim3(256), 0, s, a,   \
+                               b, gc, (long long)ldg, ga, gb, (long long)batch, T);                            \
+    } while (0)
                 if (ga && gb) {
                     if (nt) CLF_REP16_BWD(true, true, true);
                     else CLF_REP16_BWD(false, true, true);
