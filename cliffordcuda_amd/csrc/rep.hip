@@ -339,7 +339,7 @@ __global__ __launch_bounds__(256) void rep_bwd_kernel(const float* __restrict__ 
 // the next wait: they then have a full group's time to complete. The wave index
 // is wave-uniform (readfirstlane), so the row bookkeeping and the clamps run on
 // the scalar unit.
-template <bool NT>
+template <bool NT, bool ONE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void rep16_fwd_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, long long batch, RepTable T) {
     // per wave: staged a | staged b; later the relayout (over a and the start
@@ -373,7 +373,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
             wave_lds_sync();
         }
         stage16(sb, pb, lane, oddc);
-        pa = fetch16<NT>(A, row0 + stride, batch, lane);
+        if (!ONE) pa = fetch16<NT>(A, row0 + stride, batch, lane);
         wave_lds_sync();
         float wa[16], wb[16];
         gather16<0>(sa + rb * 256, ent, wa);
@@ -384,7 +384,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
         const floatx16 acc = mfma_chain(wa, wb);
         // b's next rows are requested once the operands are consumed (fewer
         // registers live across the product)
-        pb = fetch16<NT>(B, row0 + stride, batch, lane);
+        if (!ONE) pb = fetch16<NT>(B, row0 + stride, batch, lane);
         relayout_store(sa, acc, lane);
         wave_lds_sync();
         float wc[16];
@@ -795,14 +795,23 @@ int rep_fwd(int n, uint32_t neg, const float* a, const float* b, float* c, int64
                                    (long long)batch, T); break;
         case 6: hipLaunchKernelGGL((rep_fwd_kernel<3>), CLF_REP_GRID(rep_fwd_kernel<3>), dim3(256), 0, s, a, b, c,
                                    (long long)batch, T); break;
-        case 8:
-            if (stream_nt(3.0 * 1024.0 * (double)batch))
-                hipLaunchKernelGGL(rep16_fwd_kernel<true>, dim3((unsigned)want), dim3(256), 0, s, a, b, c,
-                                   (long long)batch, T);
-            else
-                hipLaunchKernelGGL(rep16_fwd_kernel<false>, dim3((unsigned)want), dim3(256), 0, s, a, b, c,
-                                   (long long)batch, T);
+        case 8: {
+            const long long nb = rep16_bwd_blocks(batch);
+            const bool one = nb * 16 >= batch;
+#define CLF_REP16_FWD(NT)                                                                                     \
+    do {                                                                                                     \
+        if (one)                                                                                             \
+            hipLaunchKernelGGL((rep16_fwd_kernel<NT, true>), dim3((unsigned)nb), dim3(256), 0, s, a, b, c,     \
+                               (long long)batch, T);                                                         \
+        else                                                                                                 \
+            hipLaunchKernelGGL((rep16_fwd_kernel<NT, false>), dim3((unsigned)nb), dim3(256), 0, s, a, b, c,    \
+                               (long long)batch, T);                                                         \
+    } while (0)
+            if (stream_nt(3.0 * 1024.0 * (double)batch)) CLF_REP16_FWD(true);
+            else CLF_REP16_FWD(false);
+#undef CLF_REP16_FWD
             break;
+        }
         default: return set_error(CLF_ERR_UNSUPPORTED, "matrix path supports n = 4, 6, 8");
     }
     CLF_HIP_CHECK(hipGetLastError());
