@@ -200,7 +200,9 @@ __device__ __forceinline__ void product_q7(float* __restrict__ rel, const float 
 // are used, so each group's results stay in an LDS slot and are stored right
 // after the next group's wait, with a full group's time to complete. The wave
 // index is wave-uniform, so the row bookkeeping runs on the scalar unit.
-template <bool PAIR, bool NT>
+// ONE: the grid covers the batch (one group per wave), so no next group is
+// prefetched (the same in the backward)
+template <bool PAIR, bool NT, bool ONE>
 __global__ __launch_bounds__(256) void rep7_fwd_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                         float* __restrict__ C, long long batch, Rep7Table T) {
     constexpr int D = PAIR ? 2 : 3;
@@ -230,8 +232,10 @@ __global__ __launch_bounds__(256) void rep7_fwd_kernel(const float* __restrict__
             wave_lds_sync();
         }
         stage7(sb, pb, lane, oddc);
-        pa = fetch7<NT>(A, row0 + stride, batch, lane);
-        pb = fetch7<NT>(B, row0 + stride, batch, lane);
+        if (!ONE) {
+            pa = fetch7<NT>(A, row0 + stride, batch, lane);
+            pb = fetch7<NT>(B, row0 + stride, batch, lane);
+        }
         wave_lds_sync();
         if constexpr (PAIR) {
             float ta[4], tah[4], tb[4], tbh[4];
@@ -261,7 +265,7 @@ __global__ __launch_bounds__(256) void rep7_fwd_kernel(const float* __restrict__
 // after the other: gc and b are staged first (a is loaded meanwhile), then a
 // over b, and each gradient's relayout and rows in blade order use a scratch
 // slot, so few converted operands are live at once.
-template <bool PAIR, bool NT, bool WA, bool WB>
+template <bool PAIR, bool NT, bool WA, bool WB, bool ONE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void rep7_bwd_kernel(
     const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ GC, long long ldg,
     float* __restrict__ GA, float* __restrict__ GB, long long batch, Rep7Table T) {
@@ -313,8 +317,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
         }
         wave_lds_sync();
         stage7(sx, pa, lane, oddc);
-        pg = fetch7<NT>(GC, row0 + stride, batch, lane, ldg);
-        pb = fetch7<NT>(B, row0 + stride, batch, lane);
+        if (!ONE) {
+            pg = fetch7<NT>(GC, row0 + stride, batch, lane, ldg);
+            pb = fetch7<NT>(B, row0 + stride, batch, lane);
+        }
         if (WA) store7<NT>(GA, sr, row0, batch, lane, oddc);  // after this group's second wait
         wave_lds_sync();
         if (WB) {
@@ -492,11 +498,13 @@ bool rep7_applicable(uint32_t neg) {
     return rep7_table(neg & 0x7fu, T);
 }
 
-// Workgroups: one per 16 rows, at most 4096 (16 per CU; C2's 65536 rows in one
-// pass measured 1-2 % faster than 2048 or 1024 workgroups); grid-stride waves.
+// Workgroups: one per 16 rows (one group per wave), so that the kernels run
+// their variant without the next-group prefetch; the cap only bounds the grid
+// dimension, and the grid-stride loop covers larger batches. (With the
+// prefetch, 2048 or 4096 workgroups for C2's 65536 rows measured within 2 %.)
 static unsigned rep7_grid(int64_t batch) {
     const long long g = (batch + 15) / 16;
-    const long long cap = 256LL * 16;
+    const long long cap = 1LL << 24;
     return (unsigned)(g < 1 ? 1 : (g > cap ? cap : g));
 }
 
@@ -506,14 +514,21 @@ int rep7_fwd(uint32_t neg, const float* a, const float* b, float* c, int64_t bat
     const bool pair = (host_popc(neg & 0x7fu) & 1) != 0;
     hipStream_t s = (hipStream_t)stream;
     const dim3 g(rep7_grid(batch));
+    const bool one = (long long)g.x * 16 >= batch;
     const bool nt = stream_nt(3.0 * 512.0 * (double)batch);
+#define CLF_REP7_FWD(P, NT)                                                                                        \
+    do {                                                                                                          \
+        if (one) hipLaunchKernelGGL((rep7_fwd_kernel<P, NT, true>), g, dim3(256), 0, s, a, b, c, (long long)batch, T); \
+        else hipLaunchKernelGGL((rep7_fwd_kernel<P, NT, false>), g, dim3(256), 0, s, a, b, c, (long long)batch, T); \
+    } while (0)
     if (pair) {
-        if (nt) hipLaunchKernelGGL((rep7_fwd_kernel<true, true>), g, dim3(256), 0, s, a, b, c, (long long)batch, T);
-        else hipLaunchKernelGGL((rep7_fwd_kernel<true, false>), g, dim3(256), 0, s, a, b, c, (long long)batch, T);
+        if (nt) CLF_REP7_FWD(true, true);
+        else CLF_REP7_FWD(true, false);
     } else {
-        if (nt) hipLaunchKernelGGL((rep7_fwd_kernel<false, true>), g, dim3(256), 0, s, a, b, c, (long long)batch, T);
-        else hipLaunchKernelGGL((rep7_fwd_kernel<false, false>), g, dim3(256), 0, s, a, b, c, (long long)batch, T);
+        if (nt) CLF_REP7_FWD(false, true);
+        else CLF_REP7_FWD(false, false);
     }
+#undef CLF_REP7_FWD
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }
@@ -525,11 +540,18 @@ int rep7_bwd(uint32_t neg, const float* a, const float* b, const float* gc, int6
     const bool pair = (host_popc(neg & 0x7fu) & 1) != 0;
     hipStream_t s = (hipStream_t)stream;
     const dim3 g(rep7_grid(batch));
+    const bool one = (long long)g.x * 16 >= batch;
     const bool nt = stream_nt((3 + (ga != nullptr) + (gb != nullptr)) * 512.0 * (double)batch);
     if (!ga && !gb) return CLF_OK;
-#define CLF_REP7_BWD(P, NT, WA, WB) \
-    hipLaunchKernelGGL((rep7_bwd_kernel<P, NT, WA, WB>), g, dim3(256), 0, s, a, b, gc, (long long)ldg, ga, gb, \
-                       (long long)batch, T)
+#define CLF_REP7_BWD(P, NT, WA, WB)                                                                        \
+    do {                                                                                                  \
+        if (one)                                                                                          \
+            hipLaunchKernelGGL((rep7_bwd_kernel<P, NT, WA, WB, true>), g, dim3(256), 0, s, a, b, gc,       \
+                               (long long)ldg, ga, gb, (long long)batch, T);                              \
+        else                                                                                              \
+            hipLaunchKernelGGL((rep7_bwd_kernel<P, NT, WA, WB, false>), g, dim3(256), 0, s, a, b, gc,      \
+                               (long long)ldg, ga, gb, (long long)batch, T);                              \
+    } while (0)
 #define CLF_REP7_BWD_W(P, NT)                 \
     do {                                      \
         if (ga && gb) CLF_REP7_BWD(P, NT, true, true);   \
