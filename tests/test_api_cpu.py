@@ -79,3 +79,28 @@ def test_bench_refuses_several_gpus():
     assert res.returncode == 2
     msg = json.loads(res.stdout.strip().splitlines()[-1])
     assert "one GPU" in msg["error"]
+
+
+def test_grad_rows_hands_over_stride0_gradients_as_one_row():
+    """The backward entries take the upstream gradient's row stride: a batch
+    stride of 0 (autograd's expansion of the gradient of a sum) goes over as
+    its one row with stride 0, anything else as a contiguous tensor with
+    stride 2^n."""
+    from cliffordcuda_amd import _lib
+    D = 32
+    row = torch.arange(D, dtype=torch.float32)
+    g, ld = _lib.grad_rows(row.expand(7, D), D)          # expanded row: (0, 1) strides
+    assert ld == 0 and g.shape == (D,) and g.is_contiguous() and torch.equal(g, row)
+    g, ld = _lib.grad_rows(torch.ones(()).expand(5, D), D)  # expanded scalar: (0, 0) strides
+    assert ld == 0 and g.shape == (D,) and g.is_contiguous() and torch.equal(g, torch.ones(D))
+    full = torch.randn(6, D)
+    g, ld = _lib.grad_rows(full, D)                        # packed rows go as they are
+    assert ld == D and g.data_ptr() == full.data_ptr()
+    t = torch.randn(D, 6).t()                              # other layouts are made contiguous
+    g, ld = _lib.grad_rows(t, D)
+    assert ld == D and g.is_contiguous() and torch.equal(g, t)
+    g, ld = _lib.grad_rows(row.expand(1, D), D)            # one row: nothing to save
+    assert ld == D and g.shape == (1, D)
+    odd = torch.randn(2 * D + 1)[1:D + 1]                  # a row 4 bytes off 16-byte alignment
+    g, ld = _lib.grad_rows(odd.expand(3, D), D)
+    assert ld == 0 and g.data_ptr() % 16 == 0 and torch.equal(g, odd)
