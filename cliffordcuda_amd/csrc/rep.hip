@@ -503,15 +503,21 @@ __device__ __forceinline__ void weight_operand(const float* __restrict__ w, cons
     shuffle_operand(t, op, std::make_integer_sequence<unsigned, 16>{});
 }
 
+// Each group's y rows wait in their own LDS slot and are stored after the next
+// group's loads have been waited for (the loads and stores of a wave share one
+// completion counter, so stores at the end of an iteration would hold up the
+// next group's prefetched loads); the wave index is wave-uniform.
+constexpr int kBcastFwdWaveFloats = kRelayoutFloats + 4 * 256;  // staged x, then the relayout | the previous group's y
+
 template <int SIDE, bool NT>
-__global__ __launch_bounds__(256) void rep16_bcast_fwd_kernel(const float* __restrict__ X, const float* __restrict__ W,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void rep16_bcast_fwd_kernel(const float* __restrict__ X, const float* __restrict__ W,
                                                                float* __restrict__ Y, long long batch, RepTable T) {
-    // per wave: staged x rows (1024 floats); later the relayout (1280), then y rows
-    __shared__ float lds[4][kRelayoutFloats];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __shared__ float lds[4][kBcastFwdWaveFloats];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const unsigned x = lane & 15u;
     const int rb = lane >> 4;
     float* sx = &lds[wave][0];
+    float* sy = sx + kRelayoutFloats;
     const unsigned oddx = (rb & 1) ? T.odd_xor : 0u, oddc = T.odd_xor >> 2;
     unsigned ent[16];
 #pragma unroll
@@ -521,9 +527,12 @@ __global__ __launch_bounds__(256) void rep16_bcast_fwd_kernel(const float* __res
     weight_operand<SIDE == 0 ? 1 : 0>(W, T, x, wop);
 
     const long long stride = (long long)gridDim.x * 4 * 4;
-    long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
+    const long long rfirst = ((long long)blockIdx.x * 4 + wave) * 4;
+    long long row0 = rfirst;
     Pre16 px = fetch16<NT>(X, row0, batch, lane);
     for (; row0 < batch; row0 += stride) {
+#pragma unroll
+        for (int z = 0; z < 16; ++z) asm volatile("" : "+v"(ent[z]));
         stage16(sx, px, lane, oddc);
         px = fetch16<NT>(X, row0 + stride, batch, lane);
         wave_lds_sync();
@@ -538,16 +547,15 @@ __global__ __launch_bounds__(256) void rep16_bcast_fwd_kernel(const float* __res
             acc = mfma_chain_pre<true, false>(zero, wx, wop, std::make_integer_sequence<unsigned, 16>{});
         else
             acc = mfma_chain_pre<false, true>(zero, wop, wx, std::make_integer_sequence<unsigned, 16>{});
+        if (row0 != rfirst) store16<NT>(Y, sy, row0 - stride, batch, lane, oddc);  // uniform
         relayout_store(sx, acc, lane);
         wave_lds_sync();
         float wc[16];
         relayout_load(sx, rb, x, wc);
-        wave_lds_sync();
-        unconvert16(wc, sx + rb * 256, ent);
-        wave_lds_sync();
-        store16<NT>(Y, sx, row0, batch, lane, oddc);
+        unconvert16(wc, sy + rb * 256, ent);
         wave_lds_sync();
     }
+    if (row0 != rfirst) store16<NT>(Y, sy, row0 - stride, batch, lane, oddc);
 }
 
 // parts[blockIdx.x * 256 + r * 16 + c]: the workgroup's sum of the 16x16 weight-gradient products
