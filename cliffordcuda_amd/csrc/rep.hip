@@ -558,32 +558,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
     if (row0 != rfirst) store16<NT>(Y, sy, row0 - stride, batch, lane, oddc);
 }
 
-// parts[blockIdx.x * 256 + r * 16 + c]: the workgroup's sum of the 16x16 weight-gradient products
-template <int SIDE, bool NT>
+// parts[blockIdx.x * 256 + r * 16 + c]: the workgroup's sum of the 16x16 weight-gradient products.
+// WX / WW: gx / the weight gradient wanted (compile-time, so no branch runs
+// around a load or a store). A group's gx rows wait in their own LDS slot and
+// are stored after the next group's first wait; the wave index is wave-uniform.
+template <int SIDE, bool NT, bool WX, bool WW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void rep16_bcast_bwd_kernel(
     const float* __restrict__ X, const float* __restrict__ W, const float* __restrict__ GY, long long ldg,
     float* __restrict__ GX, float* __restrict__ parts, long long batch, RepTable T) {
-    __shared__ float lds[4][2 * 4 * 256];  // per wave: staged x | staged gy; later relayout, then gx rows
-    static_assert(2 * 4 * 256 >= kRelayoutFloats, "relayout must fit the wave's LDS slots");
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // per wave: staged x | staged gy (the relayout over x and the start of gy) | the previous group's gx rows
+    __shared__ float lds[4][3 * 4 * 256];
+    static_assert(2 * 4 * 256 >= kRelayoutFloats, "relayout must fit the wave's staging slots");
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const unsigned x = lane & 15u;
     const int rb = lane >> 4;
     float* sx = &lds[wave][0];
     float* sg = sx + 4 * 256;
+    float* so = sg + 4 * 256;
     const unsigned oddx = (rb & 1) ? T.odd_xor : 0u, oddc = T.odd_xor >> 2;
     unsigned ent[16];
 #pragma unroll
     for (int z = 0; z < 16; ++z) ent[z] = T.e[x * 16 + z] ^ oddx;
-    const bool want_x = GX != nullptr, want_w = parts != nullptr;
     // gx operand of the weight: side 0: B = column x of phi(w)^T = row x of phi(w);
     // side 1: A = row x of phi(w)^T (transposed signs)
     float wop[16];
-    weight_operand<SIDE == 0 ? 0 : 1>(W, T, x, wop);
+    if (WX) weight_operand<SIDE == 0 ? 0 : 1>(W, T, x, wop);
     const floatx16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     floatx16 accw = zero;
 
     const long long stride = (long long)gridDim.x * 4 * 4;
-    long long row0 = ((long long)blockIdx.x * 4 + wave) * 4;
+    const long long rfirst = ((long long)blockIdx.x * 4 + wave) * 4;
+    long long row0 = rfirst;
     Pre16 px = fetch16<NT>(X, row0, batch, lane);
     Pre16 pg = fetch16<NT>(GY, row0, batch, lane, ldg);
     for (; row0 < batch; row0 += stride) {
@@ -599,7 +604,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void r
         // transposed signs, with gy in transposed signs; side 1: B = column of
         // phi(x)^T = row of phi(x), with gy in plain signs), then gx from gy in
         // the other convention; one converted pair is live at a time
-        if (want_w) {
+        if (WW) {
             float wx[16], wgw[16];
             gather16<SIDE == 0 ? 1 : 0>(sx + rb * 256, ent, wx);
             gather16<SIDE == 0 ? 1 : 0>(sg + rb * 256, ent, wgw);
@@ -618,8 +623,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void r
                 accw = mfma_chain_pre<true, true>(accw, wgw, wx, std::make_integer_sequence<unsigned, 16>{});
         }
         pg = fetch16<NT>(GY, row0 + stride, batch, lane, ldg);
+        if (WX && row0 != rfirst) store16<NT>(GX, so, row0 - stride, batch, lane, oddc);  // uniform
         wave_lds_sync();
-        if (want_x) {
+        if (WX) {
             float wgx[16];
             gather16<SIDE == 0 ? 0 : 1>(sg + rb * 256, ent, wgx);
             wht_inplace<16>(wgx);
@@ -632,14 +638,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void r
             wave_lds_sync();
             float wc[16];
             relayout_load(sx, rb, x, wc);
-            wave_lds_sync();
-            unconvert16(wc, sx + rb * 256, ent);
-            wave_lds_sync();
-            store16<NT>(GX, sx, row0, batch, lane, oddc);
+            unconvert16(wc, so + rb * 256, ent);
         }
         wave_lds_sync();
     }
-    if (!want_w) return;  // uniform: a kernel argument
+    if (WX && row0 != rfirst) store16<NT>(GX, so, row0 - stride, batch, lane, oddc);
+    if (!WW) return;
     // sum the four blocks (rows) of the wave: lane (g, j) holds S[4g + t][j]
     __syncthreads();  // every wave is done with its LDS slots
     float* red = &lds[0][0];  // [4 waves][256]
@@ -936,9 +940,15 @@ int rep_bcast_bwd(int side, int n, uint32_t neg, const float* x, const float* w,
     float* parts = gw ? ws : nullptr;
     if (batch > 0) {
         const bool nt = stream_nt((1 + (gw != nullptr) + (gx != nullptr)) * 1024.0 * (double)batch);
-#define CLF_BCAST_BWD(SIDE, NT)                                                                                     \
-    hipLaunchKernelGGL((rep16_bcast_bwd_kernel<SIDE, NT>), dim3((unsigned)nb), dim3(256), 0, s, x, w, gy,          \
+#define CLF_BCAST_BWD3(SIDE, NT, WX, WW)                                                                        \
+    hipLaunchKernelGGL((rep16_bcast_bwd_kernel<SIDE, NT, WX, WW>), dim3((unsigned)nb), dim3(256), 0, s, x, w, gy,   \
                        (long long)ldg, gx, parts, (long long)batch, T)
+#define CLF_BCAST_BWD(SIDE, NT)                              \
+    do {                                                     \
+        if (gx && gw) CLF_BCAST_BWD3(SIDE, NT, true, true);  \
+        else if (gx) CLF_BCAST_BWD3(SIDE, NT, true, false);  \
+        else if (gw) CLF_BCAST_BWD3(SIDE, NT, false, true);  \
+    } while (0)
         if (side == 0) {
             if (nt) CLF_BCAST_BWD(0, true);
             else CLF_BCAST_BWD(0, false);
@@ -947,6 +957,7 @@ int rep_bcast_bwd(int side, int n, uint32_t neg, const float* x, const float* w,
             else CLF_BCAST_BWD(1, false);
         }
 #undef CLF_BCAST_BWD
+#undef CLF_BCAST_BWD3
     }
     if (gw) {
         int nsums = 0;
