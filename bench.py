@@ -176,10 +176,11 @@ class Timer:
         return (time.perf_counter() - t0) * 1e3 / steps
 
 
-# Sub-millisecond steps (C3, C4) are timed over at least this many steps: the
-# first few steps after an idle synchronize run up to 30 % slower (the GPU's
-# clocks ramp back up), which dominates a 20-step window of 0.15 ms steps.
-MIN_SHORT_STEPS, MIN_SHORT_WARMUP = 200, 20
+# Sub-millisecond steps (C3, C4) are timed over at least this many steps (0.15-
+# 0.25 s of work): the first steps after an idle synchronize run up to 30 %
+# slower, which dominates a 20-step window of 0.15 ms steps and still shows in a
+# 200-step one.
+MIN_SHORT_STEPS, MIN_SHORT_WARMUP = 1000, 50
 
 
 def load_traffic():
