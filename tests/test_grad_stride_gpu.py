@@ -150,6 +150,34 @@ def test_rotor_apply_bwd_stride0_equals_materialised(n, env, clf_env):
                     assert torch.equal(r0, rm)
 
 
+@pytest.mark.parametrize("n,env", [(7, {}), (8, {}), (8, {"CLF_ROTOR_PATH": "chain"}), (10, {}), (12, {})],
+                         ids=["n7", "n8-matrix", "n8-chain", "n10", "n12"])
+def test_bivector_apply_bwd_stride0_equals_materialised(n, env, clf_env):
+    """The one-call bivector backward (apply backward, partial sum and compile
+    backward) on an expanded gradient: bitwise the materialised gradient's
+    results; an empty batch gives a zero bivector gradient."""
+    for k, v in env.items():
+        clf_env.setenv(k, v)
+    g = torch.Generator().manual_seed(n + 20)
+    biv = (0.6 * torch.randn(1, n * (n - 1) // 2, generator=g)).cuda()
+    state = rotor._compile_fwd(biv, n)
+    for batch in (1, 27, 4097):
+        print(f"[case] bivector apply stride0 n={n} env={env} batch={batch}", flush=True)
+        (x,) = _rows(batch, n, batch, 1)
+        g0, gm = _expanded(batch, n, batch)
+        for need in ((True, True), (True, False), (False, True)):
+            gb0, gx0 = rotor._biv_apply_bwd(biv, state, x, g0, n, *need)
+            gbm, gxm = rotor._biv_apply_bwd(biv, state, x, gm, n, *need)
+            for r0, rm in ((gb0, gbm), (gx0, gxm)):
+                assert (r0 is None) == (rm is None)
+                if r0 is not None:
+                    assert torch.equal(r0, rm)
+    x = torch.empty(0, 1 << n, device="cuda")
+    gb, _ = rotor._biv_apply_bwd(biv, state, x, torch.empty_like(x), n, True, False)
+    torch.cuda.synchronize()
+    assert torch.equal(gb, torch.zeros_like(biv))
+
+
 @pytest.mark.parametrize("n", [7, 8, 12])
 def test_rotor_cs_apply_bwd_stride0_equals_materialised(n):
     g = torch.Generator().manual_seed(n + 50)
