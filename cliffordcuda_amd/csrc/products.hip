@@ -1339,6 +1339,260 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     }
 }
 
+// ---- inner product backward for 4 <= n <= 7: one lane per output block ------
+// Lane h of a row computes both gradient blocks h: ga[h] over the partners
+// jh = p of the relation (p inside h: rc pairs; p containing h: lc pairs) and
+// gb[h] over ih = p, with the same partner list, so one gc block g[h ^ p]
+// serves both. A partner p inside h needs the "sub" low pattern (q inside o),
+// one containing h the "sup" pattern (q containing o); lanes of a wave are
+// at different points of their lists, so the wave runs one instruction stream
+// by turning sub pairs into sup pairs: with o' = ~o, q' = ~q (4-bit
+// complements), q inside o is q' containing o', and o ^ q = o' ^ q'. A lane in
+// sub mode reads its partner block reversed (element ~q' at position q') and
+// accumulates in the reversed frame (position o' holds output ~o'); the
+// sign of the reversed pair factors into
+//   s_lo(~i, ~j) = s_lo(i, j) (-1)^{w1(i) + w2(j)} [low metric: (-1)^{|i|+|j|}]
+// with w1(k) = k1 ^ k3 and w2(k) = k0 ^ k2 (the reorder parities of complemented
+// indices), so the partner's flips take the w-term and the frame change takes
+// the output's. Every lane walks its sub partners (subsets of h, ascending,
+// ending with h) and then its sup partners (h | S, ascending from h), turning
+// its accumulators to the normal frame in between (position k <- +-position
+// 15 - k; w1, w2 and the parity are invariant under the complement, so the
+// turn is its own inverse). The pair (h, h) is walked in both modes and its
+// diagonal terms il = jl, counted twice, are taken off once. Lanes have
+// 2^|h| + 2^(nh - |h|) steps (at most 2^nh + 1); a lane stores when its list
+// ends and idles (with a repeated partner) until the wave's last step.
+// The a and b blocks are staged with float4 slot q holding elements
+// 4q + (c ^ q) in component c, so the reversed block is the slot order
+// reversed (an address xor) with the same element-to-register map.
+constexpr int kFrameMinN = 4, kFrameMaxN = 7;
+
+// register of element e of a frame-staged block
+__host__ __device__ constexpr int fr_reg(int e) { return (e & 12) | ((e & 3) ^ (e >> 2)); }
+__host__ __device__ constexpr int par4(int k) { return (k ^ (k >> 1) ^ (k >> 2) ^ (k >> 3)) & 1; }
+__host__ __device__ constexpr int w1b(int k) { return ((k >> 1) ^ (k >> 3)) & 1; }
+__host__ __device__ constexpr int w2b(int k) { return (k ^ (k >> 2)) & 1; }
+
+// steps c (counted from 1) after which some lane's list ends
+template <int NH>
+__host__ __device__ constexpr bool frame_store_step(int c) {
+    for (int k = 0; k <= NH; ++k)
+        if ((1 << k) + (1 << (NH - k)) == c) return true;
+    return false;
+}
+
+// out.c = in.(c ^ q): a global float4 of block slot q in the frame layout
+__device__ __forceinline__ float4 frame_perm(float4 v, unsigned q) {
+    const bool b0 = (q & 1u) != 0u, b1 = (q & 2u) != 0u;
+    const float x = b0 ? v.y : v.x, y = b0 ? v.x : v.y, z = b0 ? v.w : v.z, w = b0 ? v.z : v.w;
+    return b1 ? make_float4(z, w, x, y) : make_float4(x, y, z, w);
+}
+
+// sup pattern: ca[o] += s_lo(o, q) wa[q] g[o ^ q] (ga: il = o, jl = q) and
+// cb[o] += s_lo(q, o) wb[q] gt[o ^ q] (gb: il = q, jl = o), q containing o
+template <bool LOWNEG, bool WA, bool WB, int... Is>
+__device__ __forceinline__ void frame_sup(float (&ca)[16], float (&cb)[16], const float (&wa)[16],
+                                          const float (&wb)[16], const float (&g)[16], const float (&gt)[16],
+                                          std::integer_sequence<int, Is...>) {
+    auto term = [&](auto oq) {
+        constexpr int O = decltype(oq)::value >> 4, Q = decltype(oq)::value & 15;
+        if constexpr ((O & ~Q) == 0) {
+            constexpr int sa = low_sign(LV_LC, LOWNEG, (unsigned)O, (unsigned)Q);
+            constexpr int sb = low_sign(LV_RC, LOWNEG, (unsigned)Q, (unsigned)O);
+            if constexpr (WA) ca[O] = __builtin_fmaf(sa > 0 ? wa[fr_reg(Q)] : -wa[fr_reg(Q)], g[O ^ Q], ca[O]);
+            if constexpr (WB) cb[O] = __builtin_fmaf(sb > 0 ? wb[fr_reg(Q)] : -wb[fr_reg(Q)], gt[O ^ Q], cb[O]);
+        }
+    };
+    (term(std::integral_constant<int, Is>{}), ...);
+}
+
+// turn an accumulator between the reversed and the normal frame where cond
+// holds: c[k] <- f(k) c[15 - k], f = w2 (gb) or w1 (ga), times the parity
+// for a negative low metric
+template <bool LOWNEG, bool GB>
+__device__ __forceinline__ void frame_turn(float (&c)[16], bool cond) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const bool f = ((GB ? w2b(k) : w1b(k)) ^ (LOWNEG ? par4(k) : 0)) != 0;
+        const float x = c[k], y = c[15 - k];
+        c[k] = cond ? (f ? -y : y) : x;
+        c[15 - k] = cond ? (f ? -x : x) : y;
+    }
+}
+
+template <class F, int... Ts>
+__device__ __forceinline__ void frame_steps(F&& f, std::integer_sequence<int, Ts...>) {
+    (f(std::integral_constant<int, Ts>{}), ...);
+}
+
+template <int N, bool LOWNEG, bool WA, bool WB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void prod_bwd_inner_frame(
+    const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ GC, float* __restrict__ GA,
+    float* __restrict__ GB, BlkParams P) {
+    constexpr int NH = N - 4, NB = 1 << NH, R = 64 >> NH, T = NB + 1;
+    constexpr unsigned full = NB - 1u;
+    __shared__ __attribute__((aligned(64))) float4 lds[4][3 * kBalGroupF4];  // a | b | gc
+    // the steps of lane (h, row slot skew rs): tab[t][rs * NB + h]
+    __shared__ unsigned tab[T][4 * NB];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const unsigned h = (unsigned)lane & full;
+    const int r = lane >> NH;
+    const unsigned rs = (unsigned)r & 3u;
+    const int kh = __popc(h);
+    const int cs = 1 << kh, cnt = cs + (1 << (NH - kh));
+    // one group of R rows per wave (the host splits batches larger than one grid)
+    const long long ngrp = (P.batch + R - 1) / R;
+    const long long grp = (long long)blockIdx.x * 4 + wave;
+    const BalLane L = bal_lane(N, lane);
+    const bool gbc = P.ldg4 == 0;
+    // the group's loads are in flight while the step table is built
+    BalPre pa, pb, pg;
+    if (WB) pa = bal_fetch(bal_src(A, grp, P.batch, N, R), L, N - 2);
+    if (WA) pb = bal_fetch(bal_src(B, grp, P.batch, N, R), L, N - 2);
+    pg = bal_fetch(bal_src(GC, grp, P.batch, N, R, gbc), L, N - 2);
+    // entry: partner block offsets (gc block h ^ p; partner p, its slot order
+    // reversed in sub mode), sub flag, the high-part signs and |p|'s parity
+    if (wave == 0 && lane < 4 * NB) {
+        const unsigned th = (unsigned)lane & full, trs = (unsigned)lane >> NH;
+        const int tk = __popc(th);
+        const int tcs = 1 << tk, tcnt = tcs + (1 << (NH - tk));
+        const unsigned co = full & ~th;
+        unsigned S = 0u, Sp = 0u;
+        for (int t = 0; t < T; ++t) {
+            unsigned p = th;
+            bool sub = false;
+            if (t < tcs) {
+                p = S;
+                sub = true;
+                S = (S - th) & th;
+            } else if (t < tcnt) {
+                p = th | Sp;
+                Sp = (Sp - co) & co;
+            }
+            const unsigned X = th ^ p;
+            const HiSign sga = hi_sign<OP_INNER>(th, p, P.negh, P.nulh, full, P.nm1, P.mu);
+            const HiSign sgb = hi_sign<OP_INNER>(p, th, P.negh, P.nulh, full, P.nm1, P.mu);
+            const unsigned offg = ((X << 2) | (swz(X) ^ trs)) << 4;
+            const unsigned offw = ((p << 2) | (swz(p) ^ trs ^ (sub ? 3u : 0u))) << 4;
+            tab[t][lane] = offg | (offw << 10) | ((sub ? 1u : 0u) << 20) | ((sga.mask >> 31) << 21) |
+                           ((sgb.mask >> 31) << 22) | (((unsigned)__popc(p) & 1u) << 23);
+        }
+    }
+    __syncthreads();
+    const int tix = (int)(rs * NB + h);
+    const unsigned hodd = ((unsigned)kh & 1u) << 31;
+    float4* sa = lds[wave];
+    float4* sb = sa + kBalGroupF4;
+    float4* sg = sb + kBalGroupF4;
+    const unsigned base = lds_addr4(sa + (r << (N - 2)));  // the row's a block 0; b at +4 KB, gc at +8 KB
+    const unsigned fq = (unsigned)lane & 3u;  // block slot of the lane's staged chunks
+    if (grp < ngrp) {
+        {
+            const unsigned a0 = lds_addr4(sa);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (WB) lds_st4(a0 + L.so[i], frame_perm(pa.v[i], fq));
+                if (WA) lds_st4(a0 + 4096u + L.so[i], frame_perm(pb.v[i], fq));
+                lds_st4(a0 + 8192u + L.so[i], pg.v[i]);
+            }
+        }
+        wave_lds_sync();
+        const long long row = grp * R + r;
+        const bool row_ok = row < P.batch;
+        float ca[16], cb[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            ca[e] = 0.f;
+            cb[e] = 0.f;
+        }
+        auto step = [&](auto tc) {
+            constexpr int t = decltype(tc)::value;
+            // steps do not overlap: two steps' operands (56 registers each) would
+            // not fit beside the accumulators at three waves per SIMD
+            __builtin_amdgcn_sched_barrier(0);
+            constexpr bool kTurn = t >= 1 && t <= NB && (t & (t - 1)) == 0;  // some lane's first sup step
+            const bool turn = kTurn && cs == t;
+            if constexpr (kTurn) {
+                if (WA) frame_turn<LOWNEG, false>(ca, turn);
+                if (WB) frame_turn<LOWNEG, true>(cb, turn);
+            }
+            unsigned e = tab[t][tix];
+            asm volatile("" : "+v"(e));  // decoded per group, not kept for every step across the loop
+            const unsigned ga0 = base + 8192u + (e & 1023u);
+            const unsigned wa0 = base + ((e >> 10) & 1023u);
+            const unsigned subm = (e << 11) & 0x80000000u;
+            const unsigned sga = (e << 10) & 0x80000000u, sgb = (e << 9) & 0x80000000u;
+            const unsigned podd = (e << 8) & 0x80000000u;
+            const unsigned subln = LOWNEG ? subm : 0u;
+            float g[16], wa[16], wb[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 vg = lds_ld4(ga0 ^ ((unsigned)q << 4));
+                g[4 * q] = vg.x;
+                g[4 * q + 1] = vg.y;
+                g[4 * q + 2] = vg.z;
+                g[4 * q + 3] = vg.w;
+                if (WA) {
+                    const float4 v = lds_ld4((wa0 ^ ((unsigned)q << 4)) + 4096u);
+                    wa[4 * q] = v.x;
+                    wa[4 * q + 1] = v.y;
+                    wa[4 * q + 2] = v.z;
+                    wa[4 * q + 3] = v.w;
+                }
+                if (WB) {
+                    const float4 v = lds_ld4(wa0 ^ ((unsigned)q << 4));
+                    wb[4 * q] = v.x;
+                    wb[4 * q + 1] = v.y;
+                    wb[4 * q + 2] = v.z;
+                    wb[4 * q + 3] = v.w;
+                }
+            }
+            // partner flips by element class (parity, w-term): pair sign, cross
+            // sign (|h| for ga, |p| for gb, on odd elements), sub-mode w-term and
+            // (negative low metric) sub-mode parity
+            if (WA) {
+                const unsigned m1 = sga ^ hodd ^ subln, m2 = sga ^ subm, m3 = m1 ^ subm;
+#pragma unroll
+                for (int el = 0; el < 16; ++el) {
+                    const int cl = par4(el) + 2 * w2b(el);
+                    const unsigned m = cl == 0 ? sga : cl == 1 ? m1 : cl == 2 ? m2 : m3;
+                    wa[fr_reg(el)] = flip(wa[fr_reg(el)], m);
+                }
+            }
+            float gt[16];
+            if (WB) {
+                const unsigned m1 = sgb ^ podd ^ subln, m2 = sgb ^ subm, m3 = m1 ^ subm;
+#pragma unroll
+                for (int el = 0; el < 16; ++el) {
+                    const int cl = par4(el) + 2 * w1b(el);
+                    const unsigned m = cl == 0 ? sgb : cl == 1 ? m1 : cl == 2 ? m2 : m3;
+                    wb[fr_reg(el)] = flip(wb[fr_reg(el)], m);
+                }
+#pragma unroll
+                for (int x = 0; x < 16; ++x) gt[x] = par4(x) ? flip(g[x], podd) : g[x];
+            }
+            frame_sup<LOWNEG, WA, WB>(ca, cb, wa, wb, g, gt, std::make_integer_sequence<int, 256>{});
+            if constexpr (kTurn) {
+                // the pair (h, h) in sup mode: its diagonal was counted in sub mode too
+                const float g0 = turn ? g[0] : 0.f;
+#pragma unroll
+                for (int o = 0; o < 16; ++o) {
+                    const bool pos = low_sign(LV_LC, LOWNEG, (unsigned)o, (unsigned)o) > 0;
+                    if (WA) ca[o] = __builtin_fmaf(pos ? -wa[fr_reg(o)] : wa[fr_reg(o)], g0, ca[o]);
+                    if (WB) cb[o] = __builtin_fmaf(pos ? -wb[fr_reg(o)] : wb[fr_reg(o)], g0, cb[o]);
+                }
+            }
+            if constexpr (frame_store_step<NH>(t + 1)) {
+                if (cnt == t + 1 && row_ok) {
+                    if (WA) store_blk(reinterpret_cast<float4*>(GA) + (row << (N - 2)), h, ca, false);
+                    if (WB) store_blk(reinterpret_cast<float4*>(GB) + (row << (N - 2)), h, cb, false);
+                }
+            }
+        };
+        frame_steps(step, std::make_integer_sequence<int, T>{});
+    }
+}
+
 // ---- tiled path (rows larger than LDS, n >= 12) -----------------------------
 // A workgroup of 256 lanes owns 256 output blocks kh = K0 + lane of one row and
 // walks the input blocks in aligned tiles of 256 (I0 = 256 t). Because both
@@ -1634,6 +1888,60 @@ static bool tiled_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, 
 static bool tiled_forced() { return options().product_path == PATH_TILED; }
 static bool generic_forced() { return options().product_path == PATH_GENERIC; }
 
+// The inner product's backward for 4 <= n <= 7 runs on the per-lane frame
+// kernel when the low generators share one metric value and no generator is
+// null (CLF_PRODUCT_PATH=blocked or =balanced keep it on those kernels).
+static bool frame_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, bool& lowneg) {
+    if (op != OP_INNER || n < kFrameMinN || n > kFrameMaxN || nul != 0u) return false;
+    if (options().product_path != PATH_DEFAULT) return false;
+    if (!blocked_metric(op, n, neg, nul, lowneg)) return false;
+    block_sign_params(n, neg, nul, P);
+    return true;
+}
+
+template <int N, bool LN, bool WA, bool WB>
+static void launch_frame3(hipStream_t s, const float* A, const float* B, const float* GCp, float* GA, float* GB,
+                          const BlkParams& P) {
+    // one wave per group of R rows: batches beyond kMaxGrid workgroups go in
+    // several launches over consecutive rows
+    const long long R = 64 >> (N - 4);
+    const long long chunk = kMaxGrid * 4 * R;
+    const long long D = 1LL << N;
+    for (long long r0 = 0; r0 < P.batch; r0 += chunk) {
+        BlkParams Q = P;
+        Q.batch = P.batch - r0 < chunk ? P.batch - r0 : chunk;
+        const long long groups = (Q.batch + R - 1) / R;
+        const dim3 g((unsigned)((groups + 3) / 4));
+        const long long off = r0 * D;
+        hipLaunchKernelGGL((prod_bwd_inner_frame<N, LN, WA, WB>), g, dim3(256), 0, s, A + off, B + off,
+                           GCp + (P.ldg4 ? off : 0), GA ? GA + off : nullptr, GB ? GB + off : nullptr, Q);
+    }
+}
+
+template <int N, bool LN>
+static void launch_frame2(hipStream_t s, const float* A, const float* B, const float* GCp, float* GA, float* GB,
+                          const BlkParams& P) {
+    if (GA && GB) launch_frame3<N, LN, true, true>(s, A, B, GCp, GA, GB, P);
+    else if (GA) launch_frame3<N, LN, true, false>(s, A, B, GCp, GA, GB, P);
+    else launch_frame3<N, LN, false, true>(s, A, B, GCp, GA, GB, P);
+}
+
+static void launch_frame(int n, bool ln, hipStream_t s, const float* A, const float* B, const float* GCp, float* GA,
+                         float* GB, const BlkParams& P) {
+#define CLF_FRAME_N(NV)                                                  \
+    case NV:                                                             \
+        if (ln) launch_frame2<NV, true>(s, A, B, GCp, GA, GB, P);        \
+        else launch_frame2<NV, false>(s, A, B, GCp, GA, GB, P);          \
+        break;
+    switch (n) {
+        CLF_FRAME_N(4)
+        CLF_FRAME_N(5)
+        CLF_FRAME_N(6)
+        CLF_FRAME_N(7)
+    }
+#undef CLF_FRAME_N
+}
+
 // Balanced kernels: wedge, lc, rc, regressive and the inner product for
 // 4 <= n <= 10 (CLF_PRODUCT_PATH=blocked keeps them on the one-lane-per-output
 // kernels). Below n = 8 the inner product's backward runs on the blocked
@@ -1784,7 +2092,9 @@ int product_bwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
     dim3 g, bl;
     size_t lds = 0;
     const bool force_tiled = n >= 12 && tiled_forced(), force_generic = generic_forced();
-    if (!force_generic && bal_plan(op, n, neg, nul, false, P, ln)) {
+    if (frame_plan(op, n, neg, nul, P, ln)) {
+        launch_frame(n, ln, s, a, b, gc, ga, gb, P);
+    } else if (!force_generic && bal_plan(op, n, neg, nul, false, P, ln)) {
 #define CLF_BWD_BAL(OPV)                                                       \
     case OPV:                                                                  \
         if (ln) launch_bwd_bal<OPV, true>(s, a, b, gc, ga, gb, P);             \
