@@ -1381,13 +1381,6 @@ __host__ __device__ constexpr bool frame_store_step(int c) {
     return false;
 }
 
-// out.c = in.(c ^ q): a global float4 of block slot q in the frame layout
-__device__ __forceinline__ float4 frame_perm(float4 v, unsigned q) {
-    const bool b0 = (q & 1u) != 0u, b1 = (q & 2u) != 0u;
-    const float x = b0 ? v.y : v.x, y = b0 ? v.x : v.y, z = b0 ? v.w : v.z, w = b0 ? v.z : v.w;
-    return b1 ? make_float4(z, w, x, y) : make_float4(x, y, z, w);
-}
-
 // sup pattern: ca[o] += s_lo(o, q) wa[q] g[o ^ q] (ga: il = o, jl = q) and
 // cb[o] += s_lo(q, o) wb[q] gt[o ^ q] (gb: il = q, jl = o), q containing o
 template <bool LOWNEG, bool WA, bool WB, int... Is>
@@ -1425,11 +1418,72 @@ __device__ __forceinline__ void frame_steps(F&& f, std::integer_sequence<int, Ts
     (f(std::integral_constant<int, Ts>{}), ...);
 }
 
+// At n = 7 the lanes of outputs 0 and 7 have 9 steps and the others 6, so
+// the last two pairs of outputs 0 and 7 go to two lanes each of the same
+// quad that have finished their own (lanes 1, 2 for output 0, its sup pairs
+// 6 and 7; lanes 5, 6 for output 7, its sub pairs 6 and 7), and quad DPP
+// moves add them in after the wave's 7th step. Output 7 walks its one sup
+// pair (7, 7) first, so its last pairs are sub pairs like its helpers'.
+template <int NH>
+struct FrameSched {
+    static constexpr bool kHelp = NH == 3;
+    static constexpr int NB = 1 << NH;
+    static constexpr int T = kHelp ? 7 : NB + 1;
+    // a lane may turn its frame before step t / take off the diagonal at t /
+    // store after t
+    static constexpr bool turn(int t) { return t >= 1 && t <= (kHelp ? 4 : NB) && (t & (t - 1)) == 0; }
+    static constexpr bool diag(int t) { return turn(t) || (kHelp && t == 0); }
+    static constexpr bool store(int t) {
+        if (kHelp) return t == 5 || t == 6;
+        for (int k = 0; k <= NH; ++k)
+            if ((1 << k) + (1 << (NH - k)) == t + 1) return true;
+        return false;
+    }
+};
+
+// step t of lane h: output block o, partner block p, sub mode
+struct FrameStep {
+    unsigned o, p;
+    bool sub;
+};
+
+template <int NH>
+__device__ __forceinline__ FrameStep frame_step(unsigned h, int t) {
+    constexpr unsigned full = (1u << NH) - 1u;
+    if (FrameSched<NH>::kHelp) {
+        if (h == 0u) return t == 0 ? FrameStep{0u, 0u, true} : FrameStep{0u, (unsigned)(t - 1), false};
+        if (h == full) return t == 0 ? FrameStep{full, full, false} : FrameStep{full, (unsigned)(t - 1), true};
+        if (t == 6) {  // helpers: the last two pairs of outputs 0 and 7
+            if (h == 1u || h == 2u) return FrameStep{0u, 5u + h, false};
+            if (h == 5u || h == 6u) return FrameStep{full, 1u + h, true};
+            return FrameStep{h, h, false};  // idle
+        }
+    }
+    const int cs = 1 << __popc(h), cnt = cs + (1 << (NH - __popc(h)));
+    if (t < cs) return FrameStep{h, deposit_bits((unsigned)t, h), true};
+    if (t < cnt) return FrameStep{h, h | deposit_bits((unsigned)(t - cs), full & ~h), false};
+    return FrameStep{h, h, false};  // idle
+}
+
+// x + x[quad lane 1] + x[quad lane 2] on quad lanes 0 and 3 (other lanes:
+// unused sums). Two DPP adds; each s_nop gives the DPP read of x the wait
+// states a VALU write of x right before it would need.
+__device__ __forceinline__ float quad_merge(float x) {
+    float t, y;
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %2 quad_perm:[1,1,2,1] row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "=v"(t) : "v"(x), "v"(x));
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %2 quad_perm:[2,1,2,2] row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "=v"(y) : "v"(x), "v"(t));
+    return y;
+}
+
 template <int N, bool LOWNEG, bool WA, bool WB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void prod_bwd_inner_frame(
     const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ GC, float* __restrict__ GA,
     float* __restrict__ GB, BlkParams P) {
-    constexpr int NH = N - 4, NB = 1 << NH, R = 64 >> NH, T = NB + 1;
+    constexpr int NH = N - 4, NB = 1 << NH, R = 64 >> NH;
+    using Sch = FrameSched<NH>;
+    constexpr int T = Sch::T;
     constexpr unsigned full = NB - 1u;
     __shared__ __attribute__((aligned(64))) float4 lds[4][3 * kBalGroupF4];  // a | b | gc
     // the steps of lane (h, row slot skew rs): tab[t][rs * NB + h]
@@ -1438,8 +1492,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     const unsigned h = (unsigned)lane & full;
     const int r = lane >> NH;
     const unsigned rs = (unsigned)r & 3u;
+    // the lane's frame turn (before its first sup step), diagonal (at its pair
+    // (h, h) in sup mode) and store steps
     const int kh = __popc(h);
-    const int cs = 1 << kh, cnt = cs + (1 << (NH - kh));
+    const int cs = 1 << kh;
+    const bool edge = Sch::kHelp && (h == 0u || h == full);
+    const int turn_t = edge ? 1 : cs;
+    const int diag_t = Sch::kHelp && h == full ? 0 : cs;
+    const int store_t = Sch::kHelp ? (edge ? 6 : 5) : cs + (1 << (NH - kh)) - 1;
     // one group of R rows per wave (the host splits batches larger than one grid)
     const long long ngrp = (P.batch + R - 1) / R;
     const long long grp = (long long)blockIdx.x * 4 + wave;
@@ -1450,147 +1510,165 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     if (WB) pa = bal_fetch(bal_src(A, grp, P.batch, N, R), L, N - 2);
     if (WA) pb = bal_fetch(bal_src(B, grp, P.batch, N, R), L, N - 2);
     pg = bal_fetch(bal_src(GC, grp, P.batch, N, R, gbc), L, N - 2);
-    // entry: partner block offsets (gc block h ^ p; partner p, its slot order
-    // reversed in sub mode), sub flag, the high-part signs and |p|'s parity
+    // entry: block offsets (gc block o ^ p; partner p, its slot order reversed
+    // in sub mode), sub flag, the high-part signs and the parities of p and o
     if (wave == 0 && lane < 4 * NB) {
         const unsigned th = (unsigned)lane & full, trs = (unsigned)lane >> NH;
-        const int tk = __popc(th);
-        const int tcs = 1 << tk, tcnt = tcs + (1 << (NH - tk));
-        const unsigned co = full & ~th;
-        unsigned S = 0u, Sp = 0u;
         for (int t = 0; t < T; ++t) {
-            unsigned p = th;
-            bool sub = false;
-            if (t < tcs) {
-                p = S;
-                sub = true;
-                S = (S - th) & th;
-            } else if (t < tcnt) {
-                p = th | Sp;
-                Sp = (Sp - co) & co;
-            }
-            const unsigned X = th ^ p;
-            const HiSign sga = hi_sign<OP_INNER>(th, p, P.negh, P.nulh, full, P.nm1, P.mu);
-            const HiSign sgb = hi_sign<OP_INNER>(p, th, P.negh, P.nulh, full, P.nm1, P.mu);
+            const FrameStep st = frame_step<NH>(th, t);
+            const unsigned X = st.o ^ st.p;
+            const HiSign sga = hi_sign<OP_INNER>(st.o, st.p, P.negh, P.nulh, full, P.nm1, P.mu);
+            const HiSign sgb = hi_sign<OP_INNER>(st.p, st.o, P.negh, P.nulh, full, P.nm1, P.mu);
             const unsigned offg = ((X << 2) | (swz(X) ^ trs)) << 4;
-            const unsigned offw = ((p << 2) | (swz(p) ^ trs ^ (sub ? 3u : 0u))) << 4;
-            tab[t][lane] = offg | (offw << 10) | ((sub ? 1u : 0u) << 20) | ((sga.mask >> 31) << 21) |
-                           ((sgb.mask >> 31) << 22) | (((unsigned)__popc(p) & 1u) << 23);
+            const unsigned offw = ((st.p << 2) | (swz(st.p) ^ trs ^ (st.sub ? 3u : 0u))) << 4;
+            tab[t][lane] = offg | (offw << 10) | ((st.sub ? 1u : 0u) << 20) | ((sga.mask >> 31) << 21) |
+                           ((sgb.mask >> 31) << 22) | (((unsigned)__popc(st.p) & 1u) << 23) |
+                           (((unsigned)__popc(st.o) & 1u) << 24);
         }
     }
     __syncthreads();
+    if (grp >= ngrp) return;
     const int tix = (int)(rs * NB + h);
-    const unsigned hodd = ((unsigned)kh & 1u) << 31;
     float4* sa = lds[wave];
-    float4* sb = sa + kBalGroupF4;
-    float4* sg = sb + kBalGroupF4;
     const unsigned base = lds_addr4(sa + (r << (N - 2)));  // the row's a block 0; b at +4 KB, gc at +8 KB
-    const unsigned fq = (unsigned)lane & 3u;  // block slot of the lane's staged chunks
-    if (grp < ngrp) {
-        {
-            const unsigned a0 = lds_addr4(sa);
+    {
+        // a and b in the frame layout: component c of the lane's chunks (block
+        // slot fq) goes to component c ^ fq, one dword store each
+        const unsigned fq = (unsigned)lane & 3u;
+        const unsigned a0 = lds_addr4(sa);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (WB) lds_st4(a0 + L.so[i], frame_perm(pa.v[i], fq));
-                if (WA) lds_st4(a0 + 4096u + L.so[i], frame_perm(pb.v[i], fq));
-                lds_st4(a0 + 8192u + L.so[i], pg.v[i]);
+        for (int i = 0; i < 4; ++i) {
+            const unsigned ad = (a0 + L.so[i]) | (fq << 2);
+            const float va[4] = {pa.v[i].x, pa.v[i].y, pa.v[i].z, pa.v[i].w};
+            const float vb[4] = {pb.v[i].x, pb.v[i].y, pb.v[i].z, pb.v[i].w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const unsigned adc = ad ^ ((unsigned)c << 2);
+                if (WB) *(__attribute__((address_space(3))) float*)(uintptr_t)adc = va[c];
+                if (WA) *(__attribute__((address_space(3))) float*)(uintptr_t)(adc + 4096u) = vb[c];
             }
+            lds_st4(a0 + 8192u + L.so[i], pg.v[i]);
         }
-        wave_lds_sync();
-        const long long row = grp * R + r;
-        const bool row_ok = row < P.batch;
-        float ca[16], cb[16];
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            ca[e] = 0.f;
-            cb[e] = 0.f;
-        }
-        auto step = [&](auto tc) {
-            constexpr int t = decltype(tc)::value;
-            // steps do not overlap: two steps' operands (56 registers each) would
-            // not fit beside the accumulators at three waves per SIMD
-            __builtin_amdgcn_sched_barrier(0);
-            constexpr bool kTurn = t >= 1 && t <= NB && (t & (t - 1)) == 0;  // some lane's first sup step
-            const bool turn = kTurn && cs == t;
-            if constexpr (kTurn) {
-                if (WA) frame_turn<LOWNEG, false>(ca, turn);
-                if (WB) frame_turn<LOWNEG, true>(cb, turn);
-            }
-            unsigned e = tab[t][tix];
-            asm volatile("" : "+v"(e));  // decoded per group, not kept for every step across the loop
-            const unsigned ga0 = base + 8192u + (e & 1023u);
-            const unsigned wa0 = base + ((e >> 10) & 1023u);
-            const unsigned subm = (e << 11) & 0x80000000u;
-            const unsigned sga = (e << 10) & 0x80000000u, sgb = (e << 9) & 0x80000000u;
-            const unsigned podd = (e << 8) & 0x80000000u;
-            const unsigned subln = LOWNEG ? subm : 0u;
-            float g[16], wa[16], wb[16];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float4 vg = lds_ld4(ga0 ^ ((unsigned)q << 4));
-                g[4 * q] = vg.x;
-                g[4 * q + 1] = vg.y;
-                g[4 * q + 2] = vg.z;
-                g[4 * q + 3] = vg.w;
-                if (WA) {
-                    const float4 v = lds_ld4((wa0 ^ ((unsigned)q << 4)) + 4096u);
-                    wa[4 * q] = v.x;
-                    wa[4 * q + 1] = v.y;
-                    wa[4 * q + 2] = v.z;
-                    wa[4 * q + 3] = v.w;
-                }
-                if (WB) {
-                    const float4 v = lds_ld4(wa0 ^ ((unsigned)q << 4));
-                    wb[4 * q] = v.x;
-                    wb[4 * q + 1] = v.y;
-                    wb[4 * q + 2] = v.z;
-                    wb[4 * q + 3] = v.w;
-                }
-            }
-            // partner flips by element class (parity, w-term): pair sign, cross
-            // sign (|h| for ga, |p| for gb, on odd elements), sub-mode w-term and
-            // (negative low metric) sub-mode parity
-            if (WA) {
-                const unsigned m1 = sga ^ hodd ^ subln, m2 = sga ^ subm, m3 = m1 ^ subm;
-#pragma unroll
-                for (int el = 0; el < 16; ++el) {
-                    const int cl = par4(el) + 2 * w2b(el);
-                    const unsigned m = cl == 0 ? sga : cl == 1 ? m1 : cl == 2 ? m2 : m3;
-                    wa[fr_reg(el)] = flip(wa[fr_reg(el)], m);
-                }
-            }
-            float gt[16];
-            if (WB) {
-                const unsigned m1 = sgb ^ podd ^ subln, m2 = sgb ^ subm, m3 = m1 ^ subm;
-#pragma unroll
-                for (int el = 0; el < 16; ++el) {
-                    const int cl = par4(el) + 2 * w1b(el);
-                    const unsigned m = cl == 0 ? sgb : cl == 1 ? m1 : cl == 2 ? m2 : m3;
-                    wb[fr_reg(el)] = flip(wb[fr_reg(el)], m);
-                }
-#pragma unroll
-                for (int x = 0; x < 16; ++x) gt[x] = par4(x) ? flip(g[x], podd) : g[x];
-            }
-            frame_sup<LOWNEG, WA, WB>(ca, cb, wa, wb, g, gt, std::make_integer_sequence<int, 256>{});
-            if constexpr (kTurn) {
-                // the pair (h, h) in sup mode: its diagonal was counted in sub mode too
-                const float g0 = turn ? g[0] : 0.f;
-#pragma unroll
-                for (int o = 0; o < 16; ++o) {
-                    const bool pos = low_sign(LV_LC, LOWNEG, (unsigned)o, (unsigned)o) > 0;
-                    if (WA) ca[o] = __builtin_fmaf(pos ? -wa[fr_reg(o)] : wa[fr_reg(o)], g0, ca[o]);
-                    if (WB) cb[o] = __builtin_fmaf(pos ? -wb[fr_reg(o)] : wb[fr_reg(o)], g0, cb[o]);
-                }
-            }
-            if constexpr (frame_store_step<NH>(t + 1)) {
-                if (cnt == t + 1 && row_ok) {
-                    if (WA) store_blk(reinterpret_cast<float4*>(GA) + (row << (N - 2)), h, ca, false);
-                    if (WB) store_blk(reinterpret_cast<float4*>(GB) + (row << (N - 2)), h, cb, false);
-                }
-            }
-        };
-        frame_steps(step, std::make_integer_sequence<int, T>{});
     }
+    wave_lds_sync();
+    const long long row = grp * R + r;
+    const bool row_ok = row < P.batch;
+    float ca[16], cb[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        ca[e] = 0.f;
+        cb[e] = 0.f;
+    }
+    auto store = [&]() {
+        if (row_ok) {
+            if (WA) store_blk(reinterpret_cast<float4*>(GA) + (row << (N - 2)), h, ca, false);
+            if (WB) store_blk(reinterpret_cast<float4*>(GB) + (row << (N - 2)), h, cb, false);
+        }
+    };
+    auto step = [&](auto tc) {
+        constexpr int t = decltype(tc)::value;
+        // steps do not overlap: two steps' operands (56 registers each) would
+        // not fit beside the accumulators at three waves per SIMD
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (Sch::turn(t)) {
+            const bool turn = turn_t == t;
+            if (WA) frame_turn<LOWNEG, false>(ca, turn);
+            if (WB) frame_turn<LOWNEG, true>(cb, turn);
+        }
+        unsigned e = tab[t][tix];
+        asm volatile("" : "+v"(e));  // decoded per step, not kept for every step across the kernel
+        const unsigned ga0 = base + 8192u + (e & 1023u);
+        const unsigned wa0 = base + ((e >> 10) & 1023u);
+        const unsigned subm = (e << 11) & 0x80000000u;
+        const unsigned sga = (e << 10) & 0x80000000u, sgb = (e << 9) & 0x80000000u;
+        const unsigned podd = (e << 8) & 0x80000000u, oodd = (e << 7) & 0x80000000u;
+        const unsigned subln = LOWNEG ? subm : 0u;
+        float g[16], wa[16], wb[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 vg = lds_ld4(ga0 ^ ((unsigned)q << 4));
+            g[4 * q] = vg.x;
+            g[4 * q + 1] = vg.y;
+            g[4 * q + 2] = vg.z;
+            g[4 * q + 3] = vg.w;
+            if (WA) {
+                const float4 v = lds_ld4((wa0 ^ ((unsigned)q << 4)) + 4096u);
+                wa[4 * q] = v.x;
+                wa[4 * q + 1] = v.y;
+                wa[4 * q + 2] = v.z;
+                wa[4 * q + 3] = v.w;
+            }
+            if (WB) {
+                const float4 v = lds_ld4(wa0 ^ ((unsigned)q << 4));
+                wb[4 * q] = v.x;
+                wb[4 * q + 1] = v.y;
+                wb[4 * q + 2] = v.z;
+                wb[4 * q + 3] = v.w;
+            }
+        }
+        // partner flips by element class (parity, w-term): pair sign, cross
+        // sign (|o| for ga, |p| for gb, on odd elements), sub-mode w-term and
+        // (negative low metric) sub-mode parity
+        // (the masks are formed once: opaque to the compiler, which would
+        // otherwise fold the bit extraction into each element's flip)
+        if (WA) {
+            unsigned m0 = sga, m1 = sga ^ oodd ^ subln, m2 = sga ^ subm, m3 = m1 ^ subm;
+            asm volatile("" : "+v"(m0), "+v"(m1), "+v"(m2), "+v"(m3));
+#pragma unroll
+            for (int el = 0; el < 16; ++el) {
+                const int cl = par4(el) + 2 * w2b(el);
+                const unsigned m = cl == 0 ? m0 : cl == 1 ? m1 : cl == 2 ? m2 : m3;
+                wa[fr_reg(el)] = flip(wa[fr_reg(el)], m);
+            }
+        }
+        float gt[16];
+        if (WB) {
+            unsigned m0 = sgb, m1 = sgb ^ podd ^ subln, m2 = sgb ^ subm, m3 = m1 ^ subm, mp = podd;
+            asm volatile("" : "+v"(m0), "+v"(m1), "+v"(m2), "+v"(m3), "+v"(mp));
+#pragma unroll
+            for (int el = 0; el < 16; ++el) {
+                const int cl = par4(el) + 2 * w1b(el);
+                const unsigned m = cl == 0 ? m0 : cl == 1 ? m1 : cl == 2 ? m2 : m3;
+                wb[fr_reg(el)] = flip(wb[fr_reg(el)], m);
+            }
+#pragma unroll
+            for (int x = 0; x < 16; ++x) gt[x] = par4(x) ? flip(g[x], mp) : g[x];
+        }
+        frame_sup<LOWNEG, WA, WB>(ca, cb, wa, wb, g, gt, std::make_integer_sequence<int, 256>{});
+        if constexpr (Sch::diag(t)) {
+            // the pair (h, h) in sup mode: its diagonal was counted in sub mode too
+            const float g0 = diag_t == t ? g[0] : 0.f;
+#pragma unroll
+            for (int o = 0; o < 16; ++o) {
+                const bool pos = low_sign(LV_LC, LOWNEG, (unsigned)o, (unsigned)o) > 0;
+                if (WA) ca[o] = __builtin_fmaf(pos ? -wa[fr_reg(o)] : wa[fr_reg(o)], g0, ca[o]);
+                if (WB) cb[o] = __builtin_fmaf(pos ? -wb[fr_reg(o)] : wb[fr_reg(o)], g0, cb[o]);
+            }
+        }
+        if constexpr (Sch::kHelp && t == 6) {
+            // outputs 0 and 7 (quad lanes 0 and 3) add their helpers' sums
+            // (quad lanes 1 and 2), then output 7 turns to the normal frame
+#pragma unroll
+            for (int el = 0; el < 16; ++el) {
+                if (WA) ca[el] = quad_merge(ca[el]);
+                if (WB) cb[el] = quad_merge(cb[el]);
+            }
+            if (WA) frame_turn<LOWNEG, false>(ca, h == full);
+            if (WB) frame_turn<LOWNEG, true>(cb, h == full);
+        }
+        if constexpr (Sch::store(t)) {
+            if (store_t == t) store();
+            if constexpr (Sch::kHelp && t == 5) {  // the helpers start from zero
+                const bool z = store_t == 5;
+#pragma unroll
+                for (int el = 0; el < 16; ++el) {
+                    if (WA) ca[el] = z ? 0.f : ca[el];
+                    if (WB) cb[el] = z ? 0.f : cb[el];
+                }
+            }
+        }
+    };
+    frame_steps(step, std::make_integer_sequence<int, T>{});
 }
 
 // ---- tiled path (rows larger than LDS, n >= 12) -----------------------------

@@ -474,3 +474,130 @@ def inner_union_backward(a, b, gc, metric):
             for i, j in terms(m, o):
                 gb[..., j] += sig[i, j] * a[..., i] * gc[..., i ^ j]
     return ga, gb
+
+
+def frame_step(nh, h, t):
+    """Step t of lane h in prod_bwd_inner_frame: (output block o, partner
+    block p, sub mode). Sub partners (subsets of h, ascending) first, then sup
+    partners (h | S, ascending). At nh = 3 outputs 0 and 7 keep their first
+    seven steps (output 7 walks its sup pair (7, 7) first) and quad lanes 1, 2
+    and 5, 6 take their last two pairs at step 6; lanes 3 and 4 idle there."""
+    full = (1 << nh) - 1
+    if nh == 3:
+        if h == 0:
+            return (0, 0, True) if t == 0 else (0, t - 1, False)
+        if h == full:
+            return (full, full, False) if t == 0 else (full, t - 1, True)
+        if t == 6:
+            if h in (1, 2):
+                return 0, 5 + h, False
+            if h in (5, 6):
+                return full, 1 + h, True
+            return h, h, False
+    cs = 1 << popc(h)
+    cnt = cs + (1 << (nh - popc(h)))
+    subs = subsets(h)
+    sups = [h | S for S in subsets(full & ~h)]
+    if t < cs:
+        return h, subs[t], True
+    if t < cnt:
+        return h, sups[t - cs], False
+    return h, h, False
+
+
+def _frame_w1(k):
+    return ((k >> 1) ^ (k >> 3)) & 1
+
+
+def _frame_w2(k):
+    return (k ^ (k >> 2)) & 1
+
+
+def inner_frame_backward(a, b, gc, metric):
+    """The inner product's backward as prod_bwd_inner_frame computes it
+    (4 <= n <= 7, low generators of one metric value, no null generator).
+    Lane h accumulates both gradient blocks h in the sup pattern only
+    (partner element q containing output element o):
+        ga: acc[o] += s_lo(o, q)  Wb[q] g[o ^ q]
+        gb: acc[o] += s_lo(q, o)  Wa[q] gt[o ^ q]
+    A sub pair (partner inside the output) reads its partner block reversed
+    (position q holds element ~q) into an accumulator kept in the reversed
+    frame (position o holds output ~o). The partner's flips are the pair's
+    high sign, the cross sign on odd elements (|o| for ga, |p| for gb) and, in
+    sub mode, w2 (ga) or w1 (gb) plus the parity for a negative low metric;
+    gt is g with odd elements flipped when |p| is odd. The frame turn is
+    acc[k] <- f(k) acc[15 - k] with f = w1 (ga) or w2 (gb) [+ parity]. The
+    pair (h, h) in sup mode takes the diagonal off once. At nh = 3 the helper
+    lanes' sums are added to outputs 0 and 7 after step 6. Returns (ga, gb)."""
+    n = len(metric)
+    nh = n - 4
+    NB = 1 << nh
+    full = NB - 1
+    neg = sum(1 << k for k, m in enumerate(metric) if m == -1)
+    assert all(m != 0 for m in metric) and (neg & 15) in (0, 15)
+    lowneg = (neg & 15) == 15
+    negh = neg >> 4
+    help_ = nh == 3
+    T = 7 if help_ else NB + 1
+    fa = [(_frame_w1(k) ^ (lowneg & popc(k))) & 1 for k in range(16)]
+    fb = [(_frame_w2(k) ^ (lowneg & popc(k))) & 1 for k in range(16)]
+    rows = a.shape[:-1]
+    ca = [np.zeros(rows + (16,)) for _ in range(NB)]
+    cb = [np.zeros(rows + (16,)) for _ in range(NB)]
+    ga = np.zeros(a.shape)
+    gb = np.zeros(b.shape)
+
+    def turn(acc, f):
+        return np.stack([(-1.0 if f[k] else 1.0) * acc[..., 15 - k] for k in range(16)], -1)
+
+    def is_turn(t):
+        return 1 <= t <= (4 if help_ else NB) and (t & (t - 1)) == 0
+
+    ctl = []
+    for h in range(NB):
+        cs = 1 << popc(h)
+        edge = help_ and h in (0, full)
+        ctl.append((1 if edge else cs, 0 if (help_ and h == full) else cs,
+                    (6 if edge else 5) if help_ else cs + (1 << (nh - popc(h))) - 1))
+    for t in range(T):
+        for h in range(NB):
+            if is_turn(t) and ctl[h][0] == t:
+                ca[h], cb[h] = turn(ca[h], fa), turn(cb[h], fb)
+            o, p, sub = frame_step(nh, h, t)
+            X = o ^ p
+            g = gc[..., X * 16:(X + 1) * 16]
+            podd, oodd = popc(p) & 1, popc(o) & 1
+            gt = np.stack([g[..., x] * (-1.0 if (popc(x) & 1 and podd) else 1.0) for x in range(16)], -1)
+            _, s_ga = hi_sign(INNER, o, p, negh, 0, full, 0, 0)
+            _, s_gb = hi_sign(INNER, p, o, negh, 0, full, 0, 0)
+            wa, wb = [], []
+            for q in range(16):
+                e = 15 - q if sub else q
+                par = popc(q) & 1
+                fla = s_ga * (-1 if par and oodd else 1) * (-1 if sub and (_frame_w2(q) ^ (lowneg & par)) else 1)
+                flb = s_gb * (-1 if par and podd else 1) * (-1 if sub and (_frame_w1(q) ^ (lowneg & par)) else 1)
+                wa.append(fla * b[..., p * 16 + e])
+                wb.append(flb * a[..., p * 16 + e])
+            for oo in range(16):
+                for q in range(16):
+                    if oo & ~q & 15:
+                        continue
+                    ca[h][..., oo] += low_sign(LC, lowneg, oo, q) * wa[q] * g[..., oo ^ q]
+                    cb[h][..., oo] += low_sign(RC, lowneg, q, oo) * wb[q] * gt[..., oo ^ q]
+            if ctl[h][1] == t and (is_turn(t) or (help_ and t == 0)):
+                for oo in range(16):
+                    ca[h][..., oo] -= low_sign(LC, lowneg, oo, oo) * wa[oo] * g[..., 0]
+                    cb[h][..., oo] -= low_sign(LC, lowneg, oo, oo) * wb[oo] * g[..., 0]
+        if help_ and t == 6:
+            ca[0] = ca[0] + ca[1] + ca[2]
+            cb[0] = cb[0] + cb[1] + cb[2]
+            ca[full] = turn(ca[full] + ca[5] + ca[6], fa)
+            cb[full] = turn(cb[full] + cb[5] + cb[6], fb)
+        for h in range(NB):
+            if ctl[h][2] == t:
+                ga[..., h * 16:(h + 1) * 16] = ca[h]
+                gb[..., h * 16:(h + 1) * 16] = cb[h]
+                if help_ and t == 5:
+                    ca[h] = np.zeros(rows + (16,))
+                    cb[h] = np.zeros(rows + (16,))
+    return ga, gb

@@ -148,3 +148,52 @@ def test_inner_union_backward_round(metric):
     ga, gb = K.inner_union_backward(a, b, gc, list(metric))
     np.testing.assert_allclose(ga, at.grad.numpy(), atol=1e-10)
     np.testing.assert_allclose(gb, bt.grad.numpy(), atol=1e-10)
+
+
+@pytest.mark.parametrize("metric", [(1,) * 4, (-1,) * 4, (1,) * 4 + (-1,), (1,) * 6, (-1,) * 5 + (1,),
+                                    (1,) * 6 + (-1,), (-1,) * 7, (1, 1, 1, 1, -1, 1, -1), (-1,) * 4 + (1, -1, 1)],
+                         ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
+def test_inner_frame_backward(metric):
+    """The per-lane-frame backward of the inner product (4 <= n <= 7): sub
+    pairs run as sup pairs on reversed partner blocks into reversed-frame
+    accumulators, with the complement sign factors s_lo(~i, ~j) =
+    s_lo(i, j) (-1)^{w1(i) + w2(j)} [parity terms for a negative low metric];
+    at n = 7 helper lanes take the last pairs of outputs 0 and 7. Gives the
+    oracle's gradients."""
+    n = len(metric)
+    rng = np.random.default_rng(n + 7)
+    a = rng.standard_normal((2, 1 << n))
+    b = rng.standard_normal((2, 1 << n))
+    gc = rng.standard_normal((2, 1 << n))
+    at = torch.tensor(a, requires_grad=True)
+    bt = torch.tensor(b, requires_grad=True)
+    O.einsum_product("inner", at, bt, list(metric)).backward(torch.tensor(gc))
+    ga, gb = K.inner_frame_backward(a, b, gc, list(metric))
+    np.testing.assert_allclose(ga, at.grad.numpy(), atol=1e-10)
+    np.testing.assert_allclose(gb, bt.grad.numpy(), atol=1e-10)
+
+
+def test_inner_frame_schedule_covers_every_pair():
+    """Every related (output, partner) block pair of the inner product's
+    backward is walked once in sub and once in sup mode when the blocks are
+    equal, once otherwise, and at n = 7 no lane exceeds seven steps."""
+    for nh in range(4):
+        NB = 1 << nh
+        full = NB - 1
+        T = 7 if nh == 3 else NB + 1
+        seen = {}
+        for h in range(NB):
+            for t in range(T):
+                o, p, sub = K.frame_step(nh, h, t)
+                idle = (o, p) == (h, h) and not sub and t >= (1 << K.popc(h)) + (1 << (nh - K.popc(h)))
+                idle = idle or (nh == 3 and t == 6 and h in (3, 4))
+                if not idle:
+                    seen[(o, p, sub)] = seen.get((o, p, sub), 0) + 1
+        want = {}
+        for o in range(NB):
+            for p in range(NB):
+                if (p & ~o) == 0:
+                    want[(o, p, True)] = 1
+                if (o & ~p) == 0:
+                    want[(o, p, False)] = 1
+        assert seen == want, nh
