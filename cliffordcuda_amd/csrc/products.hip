@@ -1671,6 +1671,150 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     frame_steps(step, std::make_integer_sequence<int, T>{});
 }
 
+// ---- inner product forward at n = 7: one lane per output block -------------
+// Output block o of a row takes, for every partner S inside ~o, the lc half
+// (a[S], b[S | o], il inside jl) and the rc half (a[S | o], b[S], jl inside
+// il) of the fused round, so every lane runs the same two patterns at every
+// step; for o = 0 both halves are (a[S], b[S]) and the diagonal il = jl,
+// counted twice, is taken off the scalar once. Output o has 2^(3 - |o|)
+// partners (27 per row), so eight lanes cover a row in four steps when the
+// lanes of outputs 3 and 7, done early, take four of output 0's eight:
+//   o = 0: S = 0..3 | o = 1, 2, 4: their four | o = 3: S = 0, 4, then o = 0
+//   with S = 4, 5 | o = 5, 6: their two | o = 7: S = 0, idle, then o = 0 with
+//   S = 6, 7,
+// and output 0 adds lane 3's sum (quad DPP) and lane 7's (row shift by 7).
+__device__ __forceinline__ FrameStep fwd7_step(unsigned h, int t) {
+    if (h == 0u) return FrameStep{0u, (unsigned)t, false};
+    if (h == 3u) return t < 2 ? FrameStep{3u, t == 0 ? 0u : 4u, false} : FrameStep{0u, (unsigned)(t + 2), false};
+    if (h == 7u) {
+        if (t == 0) return FrameStep{7u, 0u, false};
+        if (t == 1) return FrameStep{7u, 0u, true};  // idle (sub marks it)
+        return FrameStep{0u, (unsigned)(t + 4), false};
+    }
+    const unsigned co = 7u & ~h;
+    const int cnt = 1 << __popc(co);
+    if (t < cnt) return FrameStep{h, deposit_bits((unsigned)t, co), false};
+    return FrameStep{h, 0u, true};  // idle
+}
+
+// acc[0] += fac * sum_l s_lo(l, l) a[l] b[l] (the diagonal of an o = 0 pair)
+template <bool LOWNEG, int... L>
+__device__ __forceinline__ void fwd7_diag(float (&acc)[16], const float (&a)[16], const float (&b)[16], float fac,
+                                          std::integer_sequence<int, L...>) {
+    float e = 0.f;
+    ((e = low_sign(LV_LC, LOWNEG, (unsigned)L, (unsigned)L) > 0 ? __builtin_fmaf(a[L], b[L], e)
+                                                                 : __builtin_fmaf(-a[L], b[L], e)),
+     ...);
+    acc[0] = __builtin_fmaf(fac, e, acc[0]);
+}
+
+// x + x[lane 3 of the quad] + x[lane + 7 of the DPP row], the sum wanted on
+// lane 0 of each row of eight (other lanes get other sums); s_nop as in
+// quad_merge
+__device__ __forceinline__ float fwd7_merge(float x) {
+    float t, y;
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %2 quad_perm:[3,1,2,3] row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "=v"(t) : "v"(x), "v"(x));
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %2 row_shl:7 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "=v"(y) : "v"(x), "v"(t));
+    return y;
+}
+
+template <bool LOWNEG>
+__global__ __launch_bounds__(256) void prod_fwd_inner7(const float* __restrict__ A, const float* __restrict__ B,
+                                                       float* __restrict__ C, BlkParams P) {
+    constexpr int N = 7, R = 8, T = 4;
+    constexpr unsigned full = 7u;
+    __shared__ __attribute__((aligned(64))) float4 lds[4][2 * kBalGroupF4];  // a | b
+    // tab[t][rs * 8 + h]: block offsets of S and S | o, the halves' high signs,
+    // the cross parities of S and S | o, o = 0
+    __shared__ unsigned tab[T][32];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const unsigned h = (unsigned)lane & full;
+    const int r = lane >> 3;
+    const unsigned rs = (unsigned)r & 3u;
+    const long long ngrp = (P.batch + R - 1) / R;
+    const long long grp = (long long)blockIdx.x * 4 + wave;
+    const BalLane L = bal_lane(N, lane);
+    const BalPre pa = bal_fetch(bal_src(A, grp, P.batch, N, R), L, N - 2);
+    const BalPre pb = bal_fetch(bal_src(B, grp, P.batch, N, R), L, N - 2);
+    if (wave == 0 && lane < 32) {
+        const unsigned th = (unsigned)lane & full, trs = (unsigned)lane >> 3;
+        for (int t = 0; t < T; ++t) {
+            const FrameStep st = fwd7_step(th, t);
+            const unsigned S = st.p, So = st.p | st.o;
+            const HiSign hl = hi_sign<OP_INNER>(S, So, P.negh, P.nulh, full, P.nm1, P.mu);
+            const HiSign hr = hi_sign<OP_INNER>(So, S, P.negh, P.nulh, full, P.nm1, P.mu);
+            const unsigned offs = ((S << 2) | (swz(S) ^ trs)) << 4;
+            const unsigned offo = ((So << 2) | (swz(So) ^ trs)) << 4;
+            tab[t][lane] = offs | (offo << 10) | ((hl.mask >> 31) << 20) | ((hr.mask >> 31) << 21) |
+                           (((unsigned)__popc(S) & 1u) << 22) | (((unsigned)__popc(So) & 1u) << 23) |
+                           ((st.o == 0u ? 1u : 0u) << 24);
+        }
+    }
+    __syncthreads();
+    if (grp >= ngrp) return;
+    const int tix = (int)(rs * 8 + h);
+    float4* sa = lds[wave];
+    bal_stage(sa, pa, L);
+    bal_stage(sa + kBalGroupF4, pb, L);
+    wave_lds_sync();
+    const unsigned base = lds_addr4(sa + (r << (N - 2)));  // the row's a; b at +4 KB
+    const long long row = grp * R + r;
+    const bool row_ok = row < P.batch;
+    float acc[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+    auto store = [&]() {
+        if (row_ok) store_blk(reinterpret_cast<float4*>(C) + (row << (N - 2)), h, acc, false);
+    };
+    auto step = [&](auto tc) {
+        constexpr int t = decltype(tc)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        unsigned e = tab[t][tix];
+        asm volatile("" : "+v"(e));
+        const unsigned as0 = base + (e & 1023u), ao0 = base + ((e >> 10) & 1023u);
+        unsigned hl = (e << 11) & 0x80000000u, hr = (e << 10) & 0x80000000u;
+        unsigned hlo = hl ^ ((e << 9) & 0x80000000u), hro = hr ^ ((e << 8) & 0x80000000u);
+        asm volatile("" : "+v"(hl), "+v"(hr), "+v"(hlo), "+v"(hro));
+        const float fac = (e >> 24) & 1u ? -1.f : 0.f;
+        float av[16], bv[16], av2[16], bv2[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const unsigned xs = as0 ^ ((unsigned)q << 4), xo = ao0 ^ ((unsigned)q << 4);
+            const float4 v0 = lds_ld4(xs), v1 = lds_ld4(xo + 4096u), v2 = lds_ld4(xo), v3 = lds_ld4(xs + 4096u);
+            av[4 * q] = v0.x; av[4 * q + 1] = v0.y; av[4 * q + 2] = v0.z; av[4 * q + 3] = v0.w;
+            bv[4 * q] = v1.x; bv[4 * q + 1] = v1.y; bv[4 * q + 2] = v1.z; bv[4 * q + 3] = v1.w;
+            av2[4 * q] = v2.x; av2[4 * q + 1] = v2.y; av2[4 * q + 2] = v2.z; av2[4 * q + 3] = v2.w;
+            bv2[4 * q] = v3.x; bv2[4 * q + 1] = v3.y; bv2[4 * q + 2] = v3.z; bv2[4 * q + 3] = v3.w;
+        }
+        apply_flips(bv, hl, hlo);   // lc half (S, S | o): cross parity |S|
+        apply_flips(bv2, hr, hro);  // rc half (S | o, S): cross parity |S | o|
+        lowblock_fwd<LV_LC, LOWNEG>(acc, av, bv);
+        fwd7_diag<LOWNEG>(acc, av, bv, fac, std::make_integer_sequence<int, 16>{});
+        lowblock_fwd<LV_RC, LOWNEG>(acc, av2, bv2);
+        if constexpr (t == 0) {
+            if (h == 7u) store();
+        }
+        if constexpr (t == 1) {
+            const bool done = h == 3u || h == 5u || h == 6u;
+            if (done) store();
+            const bool z = h == 3u || h == 7u;  // lanes 3 and 7 turn to output 0
+#pragma unroll
+            for (int el = 0; el < 16; ++el) acc[el] = z ? 0.f : acc[el];
+        }
+        if constexpr (t == 3) {
+#pragma unroll
+            for (int el = 0; el < 16; ++el) {
+                const float m = fwd7_merge(acc[el]);
+                acc[el] = h == 0u ? m : acc[el];
+            }
+            if (h == 0u || h == 1u || h == 2u || h == 4u) store();
+        }
+    };
+    frame_steps(step, std::make_integer_sequence<int, T>{});
+}
+
 // ---- tiled path (rows larger than LDS, n >= 12) -----------------------------
 // A workgroup of 256 lanes owns 256 output blocks kh = K0 + lane of one row and
 // walks the input blocks in aligned tiles of 256 (I0 = 256 t). Because both
@@ -2096,7 +2240,17 @@ int product_fwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
     dim3 g, bl;
     size_t lds = 0;
     const bool force_tiled = n >= 12 && tiled_forced(), force_generic = generic_forced();
-    if (!force_generic && bal_plan(op, n, neg, nul, true, P, ln)) {
+    if (frame_plan(op, n, neg, nul, P, ln) && n == 7) {
+        const long long groups = (batch + 7) / 8;
+        for (long long g0 = 0; g0 < groups; g0 += kMaxGrid * 4) {  // one group of 8 rows per wave
+            const long long gn = groups - g0 < kMaxGrid * 4 ? groups - g0 : kMaxGrid * 4;
+            BlkParams Q = P;
+            Q.batch = (g0 + gn) * 8 < batch ? gn * 8 : batch - g0 * 8;
+            const long long off = g0 * 8 * 128;
+            if (ln) hipLaunchKernelGGL(prod_fwd_inner7<true>, dim3((unsigned)((gn + 3) / 4)), dim3(256), 0, s, a + off, b + off, c + off, Q);
+            else hipLaunchKernelGGL(prod_fwd_inner7<false>, dim3((unsigned)((gn + 3) / 4)), dim3(256), 0, s, a + off, b + off, c + off, Q);
+        }
+    } else if (!force_generic && bal_plan(op, n, neg, nul, true, P, ln)) {
 #define CLF_FWD_BAL(OPV)                                               \
     case OPV:                                                          \
         if (ln) launch_fwd_bal<OPV, true>(s, a, b, c, P);              \

@@ -601,3 +601,18 @@ def inner_frame_backward(a, b, gc, metric):
                     ca[h] = np.zeros(rows + (16,))
                     cb[h] = np.zeros(rows + (16,))
     return ga, gb
+
+
+def fwd7_step(h, t):
+    """Step t of lane h in prod_fwd_inner7 (n = 7): (output block o, partner S)
+    or None (idle). Lanes 3 and 7 finish their outputs early and then take
+    partners 4, 5 and 6, 7 of output 0, whose lane adds their sums after the
+    last step."""
+    if h == 0:
+        return 0, t
+    if h == 3:
+        return (3, (0, 4)[t]) if t < 2 else (0, t + 2)
+    if h == 7:
+        return (7, 0) if t == 0 else (None if t == 1 else (0, t + 4))
+    parts = subsets(7 & ~h)
+    return (h, parts[t]) if t < len(parts) else None

@@ -197,3 +197,25 @@ def test_inner_frame_schedule_covers_every_pair():
                 if (o & ~p) == 0:
                     want[(o, p, False)] = 1
         assert seen == want, nh
+
+
+def test_inner_fwd7_schedule_covers_every_pair():
+    """The n = 7 forward's four steps per lane walk every (output block o,
+    partner S inside ~o) pair of the fused round exactly once; partners of
+    output 0 walked on lanes 3 and 7 come after those lanes' own outputs."""
+    seen = {}
+    for h in range(8):
+        own_done = False
+        for t in range(4):
+            st = K.fwd7_step(h, t)
+            if st is None:
+                continue
+            o, S = st
+            if o != h:
+                assert h in (3, 7) and o == 0
+                own_done = True
+            else:
+                assert not own_done
+            seen[(o, S)] = seen.get((o, S), 0) + 1
+    want = {(o, S): 1 for o in range(8) for S in K.subsets(7 & ~o)}
+    assert seen == want
