@@ -1106,6 +1106,151 @@ __device__ __forceinline__ void bal_role_tab(int T, unsigned hdr, const unsigned
     }
 }
 
+// ---- register-held steps (wedge, lc, rc, regressive) ----------------------
+// The same schedule as the tables above, held per lane in registers (one
+// 32-bit word per step) with the staged blocks' LDS byte offsets precomputed,
+// so a step decodes two offsets and three bits instead of walking the swizzle:
+//   bits 0-11   offset of the first block (role 0: a[ih]; role 1: b[jh]; role 2: a[ih])
+//   bits 12-23  offset of the second block (role 0: b[jh]; roles 1 and 2: gc[ih ^ jh],
+//               regressive: gc[~(ih ^ jh)])
+//   bit 24      high-part sign; bit 25 cross parity (role 0 and 2: the partner's,
+//               role 1: the output's); bit 26 compute; bits 27-28 the table's action
+// Every output of these ops has at least one pair, so a lane's outputs are
+// consecutive from its first one and the output of a step is counted, not
+// stored. Each lane builds its own words (its row's slot skew is in the
+// offsets) once per kernel.
+constexpr unsigned kRegCompute = 1u << 26;
+constexpr int kRegActShift = 27;
+
+__device__ __forceinline__ unsigned bal_blk_off(unsigned blk, unsigned rs) {
+    return ((blk << 2) | (swz(blk) ^ rs)) << 4;
+}
+
+template <int OP, int ROLE>
+__device__ __forceinline__ void bal_reg_entries(const BalSched& sc, unsigned NB, const BlkParams& P, unsigned rs,
+                                                unsigned (&E)[kBalTMax]) {
+    const unsigned full = NB - 1u;
+    unsigned o = sc.o0;
+    BalFam f = bal_family<OP, ROLE, 0>(o, full, P.nulh);
+    int s = sc.s0;
+    unsigned S = deposit_bits((unsigned)(f.first + s), f.mask);
+    bool first = true;
+    int p = sc.p0;
+#pragma unroll
+    for (int t = 0; t < kBalTMax; ++t) {
+        unsigned e = 0u;
+        if (p < sc.p1) {
+            const unsigned part = f.base | S;
+            const HiSign hs = ROLE == 0   ? hi_sign<OP>(part, part ^ o, P.negh, P.nulh, full, P.nm1, P.mu)
+                              : ROLE == 1 ? hi_sign<OP>(o, part, P.negh, P.nulh, full, P.nm1, P.mu)
+                                          : hi_sign<OP>(part, o, P.negh, P.nulh, full, P.nm1, P.mu);
+            const unsigned x = part ^ o;
+            const unsigned b2 = ROLE == 0 ? x : (OP == OP_REGR ? full ^ x : x);
+            const unsigned cr = cross_pi<OP>(ROLE == 1 ? o : part, P.nm1);
+            e = bal_blk_off(part, rs) | (bal_blk_off(b2, rs) << 12) | ((hs.mask >> 31) << 24) | (cr << 25) |
+                (hs.valid ? kRegCompute : 0u);
+            ++p;
+            ++s;
+            S = (S - f.mask) & f.mask;
+            const bool done = s == f.count;
+            if (done || p == sc.p1) {
+                if (first && sc.cont0) e |= 1u << kRegActShift;
+                else if (done) e |= 2u << kRegActShift;
+                if (done) {
+                    first = false;
+                    ++o;  // every output has pairs
+                    f = bal_family<OP, ROLE, 0>(o < NB ? o : 0u, full, P.nulh);
+                    s = 0;
+                    S = deposit_bits((unsigned)f.first, f.mask);
+                }
+            }
+        }
+        E[t] = e;
+    }
+}
+
+// One role over one row from the lane's words (T: the schedule's step count,
+// hdr: the lane's tail header, o0: its first output). b1 / b2: LDS byte
+// addresses of the row's first and second staged operand (role 0: a, b;
+// role 1: b, gc; role 2: a, gc).
+template <int OP, int ROLE, bool LOWNEG>
+__device__ __forceinline__ void bal_role_reg(int T, const unsigned (&E)[kBalTMax], unsigned hdr, unsigned o0,
+                                             unsigned b1, unsigned b2, float4* __restrict__ heads, unsigned lr,
+                                             float4* __restrict__ out, unsigned NB) {
+    const unsigned full = NB - 1u;
+    constexpr bool kRev = OP == OP_REGR && ROLE == 0;
+    T = __builtin_amdgcn_readfirstlane(T);  // the same for every lane of the row's schedule
+    unsigned o = o0;
+    float acc[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int t = 0; t < kBalTMax; ++t) {
+        if (t >= T) break;
+        unsigned e = E[t];
+        asm volatile("" : "+v"(e));  // decoded at its step, not ahead of the loop
+        if (e & kRegCompute) {
+            const unsigned a1 = b1 + (e & 4095u), a2 = b2 + ((e >> 12) & 4095u);
+            const unsigned sm = (e << 7) & 0x80000000u;
+            const unsigned cm = (e << 6) & 0x80000000u;
+            float v1[16], v2[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 x1 = lds_ld4(a1 ^ ((unsigned)q << 4));
+                const float4 x2 = lds_ld4(a2 ^ ((unsigned)q << 4));
+                v1[4 * q] = x1.x; v1[4 * q + 1] = x1.y; v1[4 * q + 2] = x1.z; v1[4 * q + 3] = x1.w;
+                constexpr bool kR2 = OP == OP_REGR && ROLE != 0;  // regressive gc blocks read reversed
+                v2[kR2 ? 15 - 4 * q : 4 * q] = x2.x;
+                v2[kR2 ? 14 - 4 * q : 4 * q + 1] = x2.y;
+                v2[kR2 ? 13 - 4 * q : 4 * q + 2] = x2.z;
+                v2[kR2 ? 12 - 4 * q : 4 * q + 3] = x2.w;
+            }
+            if (ROLE == 0) {  // v1 = a[ih], v2 = b[jh]
+                apply_flips(v2, sm, sm ^ cm);
+                fwd_block_dispatch<OP, LOWNEG>(acc, v1, v2, 0u, 0u);
+            } else if (ROLE == 1) {  // v1 = b[jh], v2 = gc
+                apply_flips(v1, sm, sm ^ cm);
+                ga_block_dispatch<OP, LOWNEG>(acc, v1, v2, 0u, 0u);
+            } else {  // v1 = a[ih], v2 = gc
+                apply_flips(v1, sm, sm ^ cm);
+                float gt[16];
+#pragma unroll
+                for (int k = 0; k < 16; ++k) gt[k] = (cpopc((unsigned)k) & 1) ? flip(v2[k], cm) : v2[k];
+                gb_block_dispatch<OP, LOWNEG>(acc, v1, gt, 0u, 0u);
+            }
+        }
+        const unsigned act = e >> kRegActShift;
+        if (act == 1u) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                heads[lr * 4 + q] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+        } else if (act == 2u) {
+            if (out) store_blk(out, kRev ? (full ^ o) : o, acc, kRev);
+        }
+        if (act != 0u) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) acc[k] = 0.f;
+            ++o;
+        }
+    }
+    wave_lds_sync();
+    if (hdr & 1u) {
+        const int last_lane = (int)((hdr >> 1) & 63u);
+        for (int l = (int)lr + 1; l <= last_lane; ++l) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 v = heads[l * 4 + q];
+                acc[4 * q] += v.x;
+                acc[4 * q + 1] += v.y;
+                acc[4 * q + 2] += v.z;
+                acc[4 * q + 3] += v.w;
+            }
+        }
+        const unsigned ol = (hdr >> 7) & 63u;
+        if (out) store_blk(out, kRev ? (full ^ ol) : ol, acc, kRev);
+    }
+}
+
 // A group's operand: float4 chunk lane + 64 i (i < 4) of R consecutive rows,
 // rows past the end clamped to the last row.
 struct BalPre {
@@ -1195,15 +1340,11 @@ __global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A,
     const int roff = r << (n - 2);
     const unsigned rs = (unsigned)r & 3u;  // the row's slot skew
     const BalSched sc = bal_schedule<OP, 0, kCls>(lr, NB, P.nulh);
-    // wedge, lc, rc and regressive run from the role's schedule table
+    // wedge, lc, rc and regressive run from the lane's register-held steps
     constexpr bool kTab = OP != OP_INNER && OP != OP_GEOM;
-    __shared__ unsigned short tab[kTab ? kBalTabEntries : 1];
-    __shared__ unsigned hdr[kTab ? 64 : 1];
-    if (kTab) {
-        if (wave == 0 && lane < (int)NB) bal_build_tab<OP, 0>(sc, lr, NB, P, tab, hdr);
-        __syncthreads();
-    }
-    const unsigned my_hdr = kTab ? hdr[lr] : 0u;
+    unsigned E[kBalTMax];
+    if constexpr (kTab) bal_reg_entries<OP, 0>(sc, NB, P, rs, E);
+    const unsigned my_hdr = (sc.tail ? 1u : 0u) | ((unsigned)sc.last_lane << 1) | (sc.olast << 7);
     const long long ngrp = (P.batch + R - 1) / R;
     const long long gstride = (long long)gridDim.x * 4;
     long long grp = (long long)blockIdx.x * 4 + wave;
@@ -1219,7 +1360,9 @@ __global__ __launch_bounds__(256) void prod_fwd_bal(const float* __restrict__ A,
         wave_lds_sync();
         const long long row = grp * R + r;
         float4* out = row < P.batch ? reinterpret_cast<float4*>(C) + (row << (n - 2)) : nullptr;
-        if constexpr (kTab) bal_role_tab<OP, 0, LOWNEG>(sc.T, my_hdr, tab, sa + roff, sb + roff, nullptr, heads, lr, out, NB, P, rs);
+        if constexpr (kTab)
+            bal_role_reg<OP, 0, LOWNEG>(sc.T, E, my_hdr, sc.o0, lds_addr4(sa + roff), lds_addr4(sb + roff), heads, lr,
+                                        out, NB);
         else bal_role<OP, 0, kCls, LOWNEG>(sc, sa + roff, sb + roff, nullptr, heads, lr, out, NB, P, rs);
         wave_lds_sync();
     }
@@ -1239,8 +1382,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     constexpr bool kTab = OP != OP_GEOM;  // every op but geom runs from schedule tables
     constexpr int kTabs = kDeals ? 4 : 2;
     __shared__ __attribute__((aligned(64))) float4 lds[4][(kDeals ? 4 : 3) * kBalGroupF4];  // a | b | gc [| the inner product's partials]
-    __shared__ unsigned short tab[kTab ? kTabs : 1][kTab ? kBalTabEntries : 1];
-    __shared__ unsigned hdr[kTab ? kTabs : 1][64];
+    __shared__ unsigned short tab[kDeals ? kTabs : 1][kDeals ? kBalTabEntries : 1];
+    __shared__ unsigned hdr[kDeals ? kTabs : 1][64];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int n = P.n;
     const int lpr_log = n - 4;
@@ -1271,16 +1414,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
         T[1] = s1.T;
         T[2] = s2.T;
         T[3] = s3.T;
-    } else if constexpr (kTab) {
+    }
+    if (kDeals) __syncthreads();
+    // wedge, lc, rc and regressive: the lane's register-held steps per role
+    unsigned EA[kBalTMax], EB[kBalTMax];
+    unsigned hdr_a = 0u, hdr_b = 0u, o0_a = 0u, o0_b = 0u;
+    if constexpr (kTab && !kDeals) {
         const BalSched sca = bal_schedule<OP, 1, 0>(lr, NB, P.nulh), scb = bal_schedule<OP, 2, 0>(lr, NB, P.nulh);
-        if (wave == 0 && lane < (int)NB) {
-            bal_build_tab<OP, 1>(sca, lr, NB, P, tab[0], hdr[0]);
-            bal_build_tab<OP, 2>(scb, lr, NB, P, tab[1], hdr[1]);
-        }
+        bal_reg_entries<OP, 1>(sca, NB, P, rs, EA);
+        bal_reg_entries<OP, 2>(scb, NB, P, rs, EB);
+        hdr_a = (sca.tail ? 1u : 0u) | ((unsigned)sca.last_lane << 1) | (sca.olast << 7);
+        hdr_b = (scb.tail ? 1u : 0u) | ((unsigned)scb.last_lane << 1) | (scb.olast << 7);
+        o0_a = sca.o0;
+        o0_b = scb.o0;
         T[0] = sca.T;
         T[1] = scb.T;
     }
-    if (kTab) __syncthreads();
     const BalSched sca = bal_schedule<OP, 1, 0>(lr, NB, P.nulh);  // geom only
     const BalSched scb = bal_schedule<OP, 2, 0>(lr, NB, P.nulh);
     const long long ngrp = (P.batch + R - 1) / R;
@@ -1310,8 +1459,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
                 bal_role_tab<OP, 1, LOWNEG, 2>(T[1], hdr[1][lr], tab[1], nullptr, sb + roff, sg + roff, sa + hoff, lr,
                                                out, NB, P, rs, sp + roff);
             } else if constexpr (kTab) {
-                bal_role_tab<OP, 1, LOWNEG>(T[0], hdr[0][lr], tab[0], nullptr, sb + roff, sg + roff, sa + hoff, lr,
-                                            out, NB, P, rs);
+                bal_role_reg<OP, 1, LOWNEG>(T[0], EA, hdr_a, o0_a, lds_addr4(sb + roff), lds_addr4(sg + roff), sa + hoff,
+                                            lr, out, NB);
             } else {
                 bal_role<OP, 1, 0, LOWNEG>(sca, nullptr, sb + roff, sg + roff, sa + hoff, lr, out, NB, P, rs);
             }
@@ -1329,8 +1478,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
                 bal_role_tab<OP, 2, LOWNEG, 2>(T[3], hdr[3][lr], tab[3], sa + roff, nullptr, sg + roff, sb + hoff, lr,
                                                out, NB, P, rs, sp + roff);
             } else if constexpr (kTab) {
-                bal_role_tab<OP, 2, LOWNEG>(T[1], hdr[1][lr], tab[1], sa + roff, nullptr, sg + roff, sb + hoff, lr,
-                                            out, NB, P, rs);
+                bal_role_reg<OP, 2, LOWNEG>(T[1], EB, hdr_b, o0_b, lds_addr4(sa + roff), lds_addr4(sg + roff), sb + hoff,
+                                            lr, out, NB);
             } else {
                 bal_role<OP, 2, 0, LOWNEG>(scb, sa + roff, nullptr, sg + roff, sb + hoff, lr, out, NB, P, rs);
             }
