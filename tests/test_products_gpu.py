@@ -387,3 +387,49 @@ def test_n7_matrix_path_equals_direct_path(metric, clf_env):
         assert rel_err(c, c0) <= TOL and rel_err(ga, ga0) <= TOL and rel_err(gb, gb0) <= TOL
         assert torch.equal(ga1, ga) and torch.equal(gb1, gb)
         assert not torch.equal(c, c0)
+
+
+FRAME_METRICS = [(1,) * 4, (-1,) * 4, (1,) * 4 + (-1,), (-1,) * 5 + (1,), (1,) * 6 + (-1,), (-1,) * 7,
+                 (1, 1, 1, 1, -1, 1, -1), (-1, -1, -1, -1, 1, -1, 1)]
+
+
+@pytest.mark.parametrize("metric", FRAME_METRICS, ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
+def test_inner_frame_kernels_match_oracle_and_blocked(metric, clf_env):
+    """The inner product's one-lane-per-output kernels (backward for
+    4 <= n <= 7 with per-lane frames, forward at n = 7 with helper lanes):
+    values and each gradient alone or both against the fp64 oracle, batches
+    that end inside a group of rows (and a single row), and equal to the
+    blocked kernels (CLF_PRODUCT_PATH=blocked) within rounding."""
+    from cliffordcuda_amd import _lib, products
+    from cliffordcuda_amd._validate import metric_masks
+    n = len(metric)
+    neg, nul = metric_masks(metric)
+    R = 1024 >> n
+    for batch in (1, R - 1, 3 * R + 5, 4 * 64 * R + 7):
+        print(f"[case] inner frame metric={metric} batch={batch}", flush=True)
+        a, b, gc = seeded(batch, n, batch + n, 3)
+        a64 = a.double().requires_grad_()
+        b64 = b.double().requires_grad_()
+        c64 = O.einsum_product("inner", a64, b64, metric)
+        c64.backward(gc.double())
+        ad, bd, gd = a.cuda(), b.cuda(), gc.cuda()
+        c = products.product("inner", ad, bd, metric)
+        assert rel_err(c, c64) <= TOL
+        got = {}
+        for need in ((True, True), (True, False), (False, True)):
+            ga, gb = products._product_bwd(_lib.OP_CODES["inner"], n, neg, nul, ad, bd, gd, *need)
+            assert (ga is None) != need[0] and (gb is None) != need[1]
+            if ga is not None:
+                assert rel_err(ga, a64.grad) <= TOL
+            if gb is not None:
+                assert rel_err(gb, b64.grad) <= TOL
+            got[need] = (ga, gb)
+        # each gradient alone equals the one computed together with the other
+        assert torch.equal(got[(True, False)][0], got[(True, True)][0])
+        assert torch.equal(got[(False, True)][1], got[(True, True)][1])
+        clf_env.setenv("CLF_PRODUCT_PATH", "blocked")
+        cb = products.product("inner", ad, bd, metric)
+        gab, gbb = products._product_bwd(_lib.OP_CODES["inner"], n, neg, nul, ad, bd, gd, True, True)
+        clf_env.delenv("CLF_PRODUCT_PATH")
+        assert rel_err(c, cb) <= 1e-6
+        assert rel_err(got[(True, True)][0], gab) <= 1e-6 and rel_err(got[(True, True)][1], gbb) <= 1e-6
