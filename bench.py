@@ -150,9 +150,17 @@ class Timer:
         self.torch, self.stream, self.reps = torch, stream, reps
 
     def kernel_ms(self, fn):
-        """Average duration of fn() over `reps` back-to-back calls, HIP events on the launch stream."""
+        """Average duration of fn() over `reps` back-to-back calls, HIP events on the launch stream,
+        after at least 20 ms and max(10, reps / 4) calls of untimed work: the first calls after an
+        idle GPU run slower (C2's first-timed kernels read 20 % slow after one warmup call)."""
         torch = self.torch
-        fn()
+        t0 = time.perf_counter()
+        calls = 0
+        while calls < max(10, self.reps // 4) or time.perf_counter() - t0 < 0.02:
+            fn()
+            calls += 1
+            if calls % 10 == 0:
+                torch.cuda.synchronize()
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
