@@ -925,7 +925,7 @@ __device__ __forceinline__ void bal_role(const BalSched& sc, const float4* __res
     }
 }
 
-// ---- table-driven rounds (wedge, lc, rc, regressive) ----------------------
+// ---- table-driven rounds (the inner product's deals, n >= 8) --------------
 // The schedule of a role is the same for every row, so its per-pair
 // bookkeeping (the family walk, the high-part sign, segment ends) is done once
 // per workgroup into a table in LDS: one 16-bit entry per (step, lane of the
@@ -1107,14 +1107,15 @@ __device__ __forceinline__ void bal_role_tab(int T, unsigned hdr, const unsigned
 }
 
 // ---- register-held steps (wedge, lc, rc, regressive) ----------------------
-// The same schedule as the tables above, held per lane in registers (one
+// The same schedule as the deals' tables, held per lane in registers (one
 // 32-bit word per step) with the staged blocks' LDS byte offsets precomputed,
 // so a step decodes two offsets and three bits instead of walking the swizzle:
 //   bits 0-11   offset of the first block (role 0: a[ih]; role 1: b[jh]; role 2: a[ih])
 //   bits 12-23  offset of the second block (role 0: b[jh]; roles 1 and 2: gc[ih ^ jh],
 //               regressive: gc[~(ih ^ jh)])
 //   bit 24      high-part sign; bit 25 cross parity (role 0 and 2: the partner's,
-//               role 1: the output's); bit 26 compute; bits 27-28 the table's action
+//               role 1: the output's); bit 26 compute; bits 27-28 the action at the step's
+//               end (as in the tables: continue, write the head slot, store)
 // Every output of these ops has at least one pair, so a lane's outputs are
 // consecutive from its first one and the output of a step is counted, not
 // stored. Each lane builds its own words (its row's slot skew is in the
@@ -1379,7 +1380,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
                                                      const float* __restrict__ GC, float* __restrict__ GA,
                                                      float* __restrict__ GB, BlkParams P) {
     constexpr bool kDeals = OP == OP_INNER;
-    constexpr bool kTab = OP != OP_GEOM;  // every op but geom runs from schedule tables
+    constexpr bool kTab = OP != OP_GEOM;  // every op but geom runs from precomputed steps (registers, or
+                                          // LDS tables for the inner product's deals)
     constexpr int kTabs = kDeals ? 4 : 2;
     __shared__ __attribute__((aligned(64))) float4 lds[4][(kDeals ? 4 : 3) * kBalGroupF4];  // a | b | gc [| the inner product's partials]
     __shared__ unsigned short tab[kDeals ? kTabs : 1][kDeals ? kBalTabEntries : 1];
@@ -2315,10 +2317,11 @@ static void launch_frame(int n, bool ln, hipStream_t s, const float* A, const fl
 
 // Balanced kernels: wedge, lc, rc, regressive and the inner product for
 // 4 <= n <= 10 (CLF_PRODUCT_PATH=blocked keeps them on the one-lane-per-output
-// kernels). Below n = 8 the inner product's backward runs on the blocked
-// kernel, whose partner walk by relation class is faster there (measured). The
-// geometric product, whose outputs all have the same work, gains nothing; both
-// use the balanced kernels only when CLF_PRODUCT_PATH=balanced.
+// kernels). Below n = 8 the inner product's backward runs on the per-lane
+// frame kernels (frame_plan; the blocked kernel when the metric has a null
+// generator), and at n = 7 its forward too. The geometric product, whose
+// outputs all have the same work, gains nothing; both use the balanced
+// kernels only when CLF_PRODUCT_PATH=balanced.
 static bool bal_plan(int op, int n, uint32_t neg, uint32_t nul, bool fwd, BlkParams& P, bool& lowneg) {
     if (n < kBalMinN || n > kBalMaxN) return false;
     const bool opt_in = op == OP_GEOM || (op == OP_INNER && !fwd && n < 8);
