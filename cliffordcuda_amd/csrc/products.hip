@@ -1509,8 +1509,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
 // ending with h) and then its sup partners (h | S, ascending from h), turning
 // its accumulators to the normal frame in between (position k <- +-position
 // 15 - k; w1, w2 and the parity are invariant under the complement, so the
-// turn is its own inverse). The pair (h, h) is walked in both modes and its
-// diagonal terms il = jl, counted twice, are taken off once. Lanes have
+// turn is its own inverse). The pair (h, h) is walked in both modes; its
+// diagonal terms il = jl are the only terms of any pair that read element 0
+// of gc block 0, so the sub-mode walk zeroes that element and they count
+// once. Lanes have
 // 2^|h| + 2^(nh - |h|) steps (at most 2^nh + 1); a lane stores when its list
 // ends and idles (with a repeated partner) until the wave's last step.
 // The a and b blocks are staged with float4 slot q holding elements
@@ -1583,7 +1585,6 @@ struct FrameSched {
     // a lane may turn its frame before step t / take off the diagonal at t /
     // store after t
     static constexpr bool turn(int t) { return t >= 1 && t <= (kHelp ? 4 : NB) && (t & (t - 1)) == 0; }
-    static constexpr bool diag(int t) { return turn(t) || (kHelp && t == 0); }
     static constexpr bool store(int t) {
         if (kHelp) return t == 5 || t == 6;
         for (int k = 0; k <= NH; ++k)
@@ -1643,13 +1644,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     const unsigned h = (unsigned)lane & full;
     const int r = lane >> NH;
     const unsigned rs = (unsigned)r & 3u;
-    // the lane's frame turn (before its first sup step), diagonal (at its pair
-    // (h, h) in sup mode) and store steps
+    // the lane's frame turn (before its first sup step) and store steps
     const int kh = __popc(h);
     const int cs = 1 << kh;
     const bool edge = Sch::kHelp && (h == 0u || h == full);
     const int turn_t = edge ? 1 : cs;
-    const int diag_t = Sch::kHelp && h == full ? 0 : cs;
     const int store_t = Sch::kHelp ? (edge ? 6 : 5) : cs + (1 << (NH - kh)) - 1;
     // one group of R rows per wave (the host splits batches larger than one grid)
     const long long ngrp = (P.batch + R - 1) / R;
@@ -1662,7 +1661,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     if (WA) pb = bal_fetch(bal_src(B, grp, P.batch, N, R), L, N - 2);
     pg = bal_fetch(bal_src(GC, grp, P.batch, N, R, gbc), L, N - 2);
     // entry: block offsets (gc block o ^ p; partner p, its slot order reversed
-    // in sub mode), sub flag, the high-part signs and the parities of p and o
+    // in sub mode), sub flag, the high-part signs, the parities of p and o, and
+    // whether the step is the pair (o, o) in sub mode
     if (wave == 0 && lane < 4 * NB) {
         const unsigned th = (unsigned)lane & full, trs = (unsigned)lane >> NH;
         for (int t = 0; t < T; ++t) {
@@ -1674,7 +1674,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
             const unsigned offw = ((st.p << 2) | (swz(st.p) ^ trs ^ (st.sub ? 3u : 0u))) << 4;
             tab[t][lane] = offg | (offw << 10) | ((st.sub ? 1u : 0u) << 20) | ((sga.mask >> 31) << 21) |
                            ((sgb.mask >> 31) << 22) | (((unsigned)__popc(st.p) & 1u) << 23) |
-                           (((unsigned)__popc(st.o) & 1u) << 24);
+                           (((unsigned)__popc(st.o) & 1u) << 24) | ((st.sub && st.p == st.o ? 1u : 0u) << 25);
         }
     }
     __syncthreads();
@@ -1738,7 +1738,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const float4 vg = lds_ld4(ga0 ^ ((unsigned)q << 4));
-            g[4 * q] = vg.x;
+            // the pair (o, o) is walked in both modes and its diagonal terms (the
+            // only ones that read gc element 0 of block 0) count in sup mode only
+            g[4 * q] = q == 0 && ((e >> 25) & 1u) ? 0.f : vg.x;
             g[4 * q + 1] = vg.y;
             g[4 * q + 2] = vg.z;
             g[4 * q + 3] = vg.w;
@@ -1786,16 +1788,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
             for (int x = 0; x < 16; ++x) gt[x] = par4(x) ? flip(g[x], mp) : g[x];
         }
         frame_sup<LOWNEG, WA, WB>(ca, cb, wa, wb, g, gt, std::make_integer_sequence<int, 256>{});
-        if constexpr (Sch::diag(t)) {
-            // the pair (h, h) in sup mode: its diagonal was counted in sub mode too
-            const float g0 = diag_t == t ? g[0] : 0.f;
-#pragma unroll
-            for (int o = 0; o < 16; ++o) {
-                const bool pos = low_sign(LV_LC, LOWNEG, (unsigned)o, (unsigned)o) > 0;
-                if (WA) ca[o] = __builtin_fmaf(pos ? -wa[fr_reg(o)] : wa[fr_reg(o)], g0, ca[o]);
-                if (WB) cb[o] = __builtin_fmaf(pos ? -wb[fr_reg(o)] : wb[fr_reg(o)], g0, cb[o]);
-            }
-        }
         if constexpr (Sch::kHelp && t == 6) {
             // outputs 0 and 7 (quad lanes 0 and 3) add their helpers' sums
             // (quad lanes 1 and 2), then output 7 turns to the normal frame

@@ -527,7 +527,8 @@ def inner_frame_backward(a, b, gc, metric):
     sub mode, w2 (ga) or w1 (gb) plus the parity for a negative low metric;
     gt is g with odd elements flipped when |p| is odd. The frame turn is
     acc[k] <- f(k) acc[15 - k] with f = w1 (ga) or w2 (gb) [+ parity]. The
-    pair (h, h) in sup mode takes the diagonal off once. At nh = 3 the helper
+    pair (h, h) in sub mode reads gc element 0 of block 0 as zero, so its
+    diagonal (the only terms reading it) counts once. At nh = 3 the helper
     lanes' sums are added to outputs 0 and 7 after step 6. Returns (ga, gb)."""
     n = len(metric)
     nh = n - 4
@@ -557,7 +558,7 @@ def inner_frame_backward(a, b, gc, metric):
     for h in range(NB):
         cs = 1 << popc(h)
         edge = help_ and h in (0, full)
-        ctl.append((1 if edge else cs, 0 if (help_ and h == full) else cs,
+        ctl.append((1 if edge else cs, None,
                     (6 if edge else 5) if help_ else cs + (1 << (nh - popc(h))) - 1))
     for t in range(T):
         for h in range(NB):
@@ -565,7 +566,9 @@ def inner_frame_backward(a, b, gc, metric):
                 ca[h], cb[h] = turn(ca[h], fa), turn(cb[h], fb)
             o, p, sub = frame_step(nh, h, t)
             X = o ^ p
-            g = gc[..., X * 16:(X + 1) * 16]
+            g = gc[..., X * 16:(X + 1) * 16].copy()
+            if sub and p == o:  # the diagonal of (o, o) counts in sup mode only
+                g[..., 0] = 0.0
             podd, oodd = popc(p) & 1, popc(o) & 1
             gt = np.stack([g[..., x] * (-1.0 if (popc(x) & 1 and podd) else 1.0) for x in range(16)], -1)
             _, s_ga = hi_sign(INNER, o, p, negh, 0, full, 0, 0)
@@ -584,10 +587,6 @@ def inner_frame_backward(a, b, gc, metric):
                         continue
                     ca[h][..., oo] += low_sign(LC, lowneg, oo, q) * wa[q] * g[..., oo ^ q]
                     cb[h][..., oo] += low_sign(RC, lowneg, q, oo) * wb[q] * gt[..., oo ^ q]
-            if ctl[h][1] == t and (is_turn(t) or (help_ and t == 0)):
-                for oo in range(16):
-                    ca[h][..., oo] -= low_sign(LC, lowneg, oo, oo) * wa[oo] * g[..., 0]
-                    cb[h][..., oo] -= low_sign(LC, lowneg, oo, oo) * wb[oo] * g[..., 0]
         if help_ and t == 6:
             ca[0] = ca[0] + ca[1] + ca[2]
             cb[0] = cb[0] + cb[1] + cb[2]
