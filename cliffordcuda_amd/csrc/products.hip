@@ -1512,9 +1512,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
 // turn is its own inverse). The pair (h, h) is walked in both modes; its
 // diagonal terms il = jl are the only terms of any pair that read element 0
 // of gc block 0, so the sub-mode walk zeroes that element and they count
-// once. Lanes have
-// 2^|h| + 2^(nh - |h|) steps (at most 2^nh + 1); a lane stores when its list
-// ends and idles (with a repeated partner) until the wave's last step.
+// once. Lanes have 2^|h| + 2^(nh - |h|) steps (at most 2^nh + 1); a lane
+// stores when its list ends and idles (with a repeated partner) until the
+// wave's last step.
 // The a and b blocks are staged with float4 slot q holding elements
 // 4q + (c ^ q) in component c, so the reversed block is the slot order
 // reversed (an address xor) with the same element-to-register map.
@@ -1525,14 +1525,6 @@ __host__ __device__ constexpr int fr_reg(int e) { return (e & 12) | ((e & 3) ^ (
 __host__ __device__ constexpr int par4(int k) { return (k ^ (k >> 1) ^ (k >> 2) ^ (k >> 3)) & 1; }
 __host__ __device__ constexpr int w1b(int k) { return ((k >> 1) ^ (k >> 3)) & 1; }
 __host__ __device__ constexpr int w2b(int k) { return (k ^ (k >> 2)) & 1; }
-
-// steps c (counted from 1) after which some lane's list ends
-template <int NH>
-__host__ __device__ constexpr bool frame_store_step(int c) {
-    for (int k = 0; k <= NH; ++k)
-        if ((1 << k) + (1 << (NH - k)) == c) return true;
-    return false;
-}
 
 // sup pattern: ca[o] += s_lo(o, q) wa[q] g[o ^ q] (ga: il = o, jl = q) and
 // cb[o] += s_lo(q, o) wb[q] gt[o ^ q] (gb: il = q, jl = o), q containing o
@@ -1582,8 +1574,7 @@ struct FrameSched {
     static constexpr bool kHelp = NH == 3;
     static constexpr int NB = 1 << NH;
     static constexpr int T = kHelp ? 7 : NB + 1;
-    // a lane may turn its frame before step t / take off the diagonal at t /
-    // store after t
+    // a lane may turn its frame before step t / store after step t
     static constexpr bool turn(int t) { return t >= 1 && t <= (kHelp ? 4 : NB) && (t & (t - 1)) == 0; }
     static constexpr bool store(int t) {
         if (kHelp) return t == 5 || t == 6;
