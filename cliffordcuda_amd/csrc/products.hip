@@ -1490,7 +1490,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     }
 }
 
-// ---- inner product backward for 4 <= n <= 7: one lane per output block ------
+// ---- inner product backward for 4 <= n <= 8: one lane per output block ------
 // Lane h of a row computes both gradient blocks h: ga[h] over the partners
 // jh = p of the relation (p inside h: rc pairs; p containing h: lc pairs) and
 // gb[h] over ih = p, with the same partner list, so one gc block g[h ^ p]
@@ -1518,7 +1518,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
 // The a and b blocks are staged with float4 slot q holding elements
 // 4q + (c ^ q) in component c, so the reversed block is the slot order
 // reversed (an address xor) with the same element-to-register map.
-constexpr int kFrameMinN = 4, kFrameMaxN = 7;
+constexpr int kFrameMinN = 4, kFrameMaxN = 8;
 
 // register of element e of a frame-staged block
 __host__ __device__ constexpr int fr_reg(int e) { return (e & 12) | ((e & 3) ^ (e >> 2)); }
@@ -1563,25 +1563,41 @@ __device__ __forceinline__ void frame_steps(F&& f, std::integer_sequence<int, Ts
     (f(std::integral_constant<int, Ts>{}), ...);
 }
 
-// At n = 7 the lanes of outputs 0 and 7 have 9 steps and the others 6, so
-// the last two pairs of outputs 0 and 7 go to two lanes each of the same
-// quad that have finished their own (lanes 1, 2 for output 0, its sup pairs
-// 6 and 7; lanes 5, 6 for output 7, its sub pairs 6 and 7), and quad DPP
-// moves add them in after the wave's 7th step. Output 7 walks its one sup
-// pair (7, 7) first, so its last pairs are sub pairs like its helpers'.
+// At n = 7 and 8 the lanes of outputs 0 and full have 2^nh + 1 steps and
+// the others at most 2^(nh-1) + 2, so the last pairs of outputs 0 and full go
+// to helper lanes that have finished their own lists, C pairs each in the
+// wave's last C steps, and DPP adds merge them after the last step:
+//   n = 7 (7 steps, C = 1): quad lanes 1, 2 help output 0 (its sup pairs 6,
+//          7), lanes 5, 6 output 7 (its sub pairs 6, 7); quad_perm merges;
+//   n = 8 (11 steps, C = 2): lanes 3, 5, 6 help output 0 (sup pairs 10..15),
+//          lanes 9, 10, 12 output 15 (sub pairs 10..15); row-shift merges.
+// Output full walks its one sup pair (full, full) first, so its last pairs
+// are sub pairs like its helpers'. A helper stores its own output when its
+// list ends and starts from zero before its first helper step.
 template <int NH>
 struct FrameSched {
-    static constexpr bool kHelp = NH == 3;
+    static constexpr bool kHelp = NH == 3 || NH == 4;
     static constexpr int NB = 1 << NH;
-    static constexpr int T = kHelp ? 7 : NB + 1;
+    static constexpr int T = NH == 3 ? 7 : NH == 4 ? 11 : NB + 1;
+    static constexpr int C = NH == 3 ? 1 : 2;  // pairs per helper lane
     // a lane may turn its frame before step t / store after step t
-    static constexpr bool turn(int t) { return t >= 1 && t <= (kHelp ? 4 : NB) && (t & (t - 1)) == 0; }
+    static constexpr bool turn(int t) { return t >= 1 && t <= (kHelp ? NB / 2 : NB) && (t & (t - 1)) == 0; }
     static constexpr bool store(int t) {
-        if (kHelp) return t == 5 || t == 6;
-        for (int k = 0; k <= NH; ++k)
+        if (kHelp && t == T - 1) return true;
+        for (int k = kHelp ? 1 : 0; k <= (kHelp ? NH - 1 : NH); ++k)
             if ((1 << k) + (1 << (NH - k)) == t + 1) return true;
         return false;
     }
+    static constexpr bool helper(unsigned h) {
+        return NH == 3 ? (h == 1u || h == 2u || h == 5u || h == 6u)
+                       : (h == 3u || h == 5u || h == 6u || h == 9u || h == 10u || h == 12u);
+    }
+    // helper index 0..2 among the helpers of its output (output 0: the first
+    // group, output full: the second)
+    static constexpr int help_rank(unsigned h) {
+        return NH == 3 ? (h == 1u || h == 5u ? 0 : 1) : (h == 3u || h == 9u ? 0 : h == 5u || h == 10u ? 1 : 2);
+    }
+    static constexpr bool helps_zero(unsigned h) { return NH == 3 ? h < 4u : h < 8u; }
 };
 
 // step t of lane h: output block o, partner block p, sub mode
@@ -1592,14 +1608,14 @@ struct FrameStep {
 
 template <int NH>
 __device__ __forceinline__ FrameStep frame_step(unsigned h, int t) {
+    using Sch = FrameSched<NH>;
     constexpr unsigned full = (1u << NH) - 1u;
-    if (FrameSched<NH>::kHelp) {
+    if (Sch::kHelp) {
         if (h == 0u) return t == 0 ? FrameStep{0u, 0u, true} : FrameStep{0u, (unsigned)(t - 1), false};
         if (h == full) return t == 0 ? FrameStep{full, full, false} : FrameStep{full, (unsigned)(t - 1), true};
-        if (t == 6) {  // helpers: the last two pairs of outputs 0 and 7
-            if (h == 1u || h == 2u) return FrameStep{0u, 5u + h, false};
-            if (h == 5u || h == 6u) return FrameStep{full, 1u + h, true};
-            return FrameStep{h, h, false};  // idle
+        if (t >= Sch::T - Sch::C && Sch::helper(h)) {  // the last pairs of outputs 0 and full
+            const unsigned p = (unsigned)(Sch::T - 1 + Sch::C * Sch::help_rank(h) + (t - (Sch::T - Sch::C)));
+            return Sch::helps_zero(h) ? FrameStep{0u, p, false} : FrameStep{full, p, true};
         }
     }
     const int cs = 1 << __popc(h), cnt = cs + (1 << (NH - __popc(h)));
@@ -1618,6 +1634,26 @@ __device__ __forceinline__ float quad_merge(float x) {
     asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %2 quad_perm:[2,1,2,2] row_mask:0xf bank_mask:0xf bound_ctrl:1"
         : "=v"(y) : "v"(x), "v"(t));
     return y;
+}
+
+// n = 8: x + x[lane + 3] + x[lane + 5] + x[lane + 6] on lane 0 of each row
+// of 16 (its helpers 3, 5, 6) and x + x[lane - 6] + x[lane - 5] + x[lane - 3]
+// on lane 15 (helpers 9, 10, 12); other lanes keep x. s_nop as in quad_merge.
+__device__ __forceinline__ float row16_merge(float x, unsigned h) {
+    float a1, a2, a3, b1, b2, b3;
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %2 row_shl:3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "=v"(a1) : "v"(x), "v"(x));
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %2 row_shl:5 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "=v"(a2) : "v"(x), "v"(a1));
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %2 row_shl:6 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "=v"(a3) : "v"(x), "v"(a2));
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %2 row_shr:6 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "=v"(b1) : "v"(x), "v"(x));
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %2 row_shr:5 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "=v"(b2) : "v"(x), "v"(b1));
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %2 row_shr:3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "=v"(b3) : "v"(x), "v"(b2));
+    return h == 0u ? a3 : (h == 15u ? b3 : x);
 }
 
 template <int N, bool LOWNEG, bool WA, bool WB>
@@ -1640,7 +1676,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     const int cs = 1 << kh;
     const bool edge = Sch::kHelp && (h == 0u || h == full);
     const int turn_t = edge ? 1 : cs;
-    const int store_t = Sch::kHelp ? (edge ? 6 : 5) : cs + (1 << (NH - kh)) - 1;
+    const int store_t = edge ? Sch::T - 1 : cs + (1 << (NH - kh)) - 1;
     // one group of R rows per wave (the host splits batches larger than one grid)
     const long long ngrp = (P.batch + R - 1) / R;
     const long long grp = (long long)blockIdx.x * 4 + wave;
@@ -1779,26 +1815,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
             for (int x = 0; x < 16; ++x) gt[x] = par4(x) ? flip(g[x], mp) : g[x];
         }
         frame_sup<LOWNEG, WA, WB>(ca, cb, wa, wb, g, gt, std::make_integer_sequence<int, 256>{});
-        if constexpr (Sch::kHelp && t == 6) {
-            // outputs 0 and 7 (quad lanes 0 and 3) add their helpers' sums
-            // (quad lanes 1 and 2), then output 7 turns to the normal frame
+        if constexpr (Sch::kHelp && t == T - 1) {
+            // outputs 0 and full add their helpers' sums (the other lanes have
+            // stored theirs), then output full turns to the normal frame
 #pragma unroll
             for (int el = 0; el < 16; ++el) {
-                if (WA) ca[el] = quad_merge(ca[el]);
-                if (WB) cb[el] = quad_merge(cb[el]);
+                if constexpr (NH == 3) {
+                    if (WA) ca[el] = quad_merge(ca[el]);
+                    if (WB) cb[el] = quad_merge(cb[el]);
+                } else {
+                    if (WA) ca[el] = row16_merge(ca[el], h);
+                    if (WB) cb[el] = row16_merge(cb[el], h);
+                }
             }
             if (WA) frame_turn<LOWNEG, false>(ca, h == full);
             if (WB) frame_turn<LOWNEG, true>(cb, h == full);
         }
         if constexpr (Sch::store(t)) {
             if (store_t == t) store();
-            if constexpr (Sch::kHelp && t == 5) {  // the helpers start from zero
-                const bool z = store_t == 5;
+        }
+        if constexpr (Sch::kHelp && t == T - Sch::C - 1) {  // the helpers start from zero
+            const bool z = Sch::helper(h);
 #pragma unroll
-                for (int el = 0; el < 16; ++el) {
-                    if (WA) ca[el] = z ? 0.f : ca[el];
-                    if (WB) cb[el] = z ? 0.f : cb[el];
-                }
+            for (int el = 0; el < 16; ++el) {
+                if (WA) ca[el] = z ? 0.f : ca[el];
+                if (WB) cb[el] = z ? 0.f : cb[el];
             }
         }
     };
@@ -2244,7 +2285,7 @@ static bool tiled_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, 
 static bool tiled_forced() { return options().product_path == PATH_TILED; }
 static bool generic_forced() { return options().product_path == PATH_GENERIC; }
 
-// The inner product's backward for 4 <= n <= 7 runs on the per-lane frame
+// The inner product's backward for 4 <= n <= 8 runs on the per-lane frame
 // kernel when the low generators share one metric value and no generator is
 // null (CLF_PRODUCT_PATH=blocked or =balanced keep it on those kernels).
 static bool frame_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, bool& lowneg) {
@@ -2294,13 +2335,14 @@ static void launch_frame(int n, bool ln, hipStream_t s, const float* A, const fl
         CLF_FRAME_N(5)
         CLF_FRAME_N(6)
         CLF_FRAME_N(7)
+        CLF_FRAME_N(8)
     }
 #undef CLF_FRAME_N
 }
 
 // Balanced kernels: wedge, lc, rc, regressive and the inner product for
 // 4 <= n <= 10 (CLF_PRODUCT_PATH=blocked keeps them on the one-lane-per-output
-// kernels). Below n = 8 the inner product's backward runs on the per-lane
+// kernels). Up to n = 8 the inner product's backward runs on the per-lane
 // frame kernels (frame_plan; the blocked kernel when the metric has a null
 // generator), and at n = 7 its forward too. The geometric product, whose
 // outputs all have the same work, gains nothing; both use the balanced

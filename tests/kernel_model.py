@@ -476,24 +476,36 @@ def inner_union_backward(a, b, gc, metric):
     return ga, gb
 
 
+# helper lanes of outputs 0 and full (each takes FRAME_HELP[nh][2] of their
+# last pairs in the wave's last steps)
+FRAME_HELP = {3: (7, ((1, 2), (5, 6)), 1), 4: (11, ((3, 5, 6), (9, 10, 12)), 2)}
+
+
+def frame_steps_count(nh):
+    return FRAME_HELP[nh][0] if nh in FRAME_HELP else (1 << nh) + 1
+
+
 def frame_step(nh, h, t):
     """Step t of lane h in prod_bwd_inner_frame: (output block o, partner
     block p, sub mode). Sub partners (subsets of h, ascending) first, then sup
-    partners (h | S, ascending). At nh = 3 outputs 0 and 7 keep their first
-    seven steps (output 7 walks its sup pair (7, 7) first) and quad lanes 1, 2
-    and 5, 6 take their last two pairs at step 6; lanes 3 and 4 idle there."""
+    partners (h | S, ascending). At nh = 3 and 4 outputs 0 and full keep their
+    first T steps (output full walks its sup pair (full, full) first, then its
+    sub pairs) and helper lanes that finished their own lists take the rest in
+    the wave's last steps (nh = 3: quad lanes 1, 2 and 5, 6, one pair each at
+    step 6; nh = 4: lanes 3, 5, 6 and 9, 10, 12, two pairs each at steps 9
+    and 10); other lanes idle there."""
     full = (1 << nh) - 1
-    if nh == 3:
+    if nh in FRAME_HELP:
+        T, (h0, hf), c = FRAME_HELP[nh]
         if h == 0:
             return (0, 0, True) if t == 0 else (0, t - 1, False)
         if h == full:
             return (full, full, False) if t == 0 else (full, t - 1, True)
-        if t == 6:
-            if h in (1, 2):
-                return 0, 5 + h, False
-            if h in (5, 6):
-                return full, 1 + h, True
-            return h, h, False
+        if t >= T - c and h in h0 + hf:
+            k = t - (T - c)
+            if h in h0:
+                return 0, T - 1 + c * h0.index(h) + k, False
+            return full, T - 1 + c * hf.index(h) + k, True
     cs = 1 << popc(h)
     cnt = cs + (1 << (nh - popc(h)))
     subs = subsets(h)
@@ -538,8 +550,9 @@ def inner_frame_backward(a, b, gc, metric):
     assert all(m != 0 for m in metric) and (neg & 15) in (0, 15)
     lowneg = (neg & 15) == 15
     negh = neg >> 4
-    help_ = nh == 3
-    T = 7 if help_ else NB + 1
+    help_ = nh in FRAME_HELP
+    T = frame_steps_count(nh)
+    h0, hf, c = (FRAME_HELP[nh][1][0], FRAME_HELP[nh][1][1], FRAME_HELP[nh][2]) if help_ else ((), (), 0)
     fa = [(_frame_w1(k) ^ (lowneg & popc(k))) & 1 for k in range(16)]
     fb = [(_frame_w2(k) ^ (lowneg & popc(k))) & 1 for k in range(16)]
     rows = a.shape[:-1]
@@ -552,14 +565,13 @@ def inner_frame_backward(a, b, gc, metric):
         return np.stack([(-1.0 if f[k] else 1.0) * acc[..., 15 - k] for k in range(16)], -1)
 
     def is_turn(t):
-        return 1 <= t <= (4 if help_ else NB) and (t & (t - 1)) == 0
+        return 1 <= t <= (NB // 2 if help_ else NB) and (t & (t - 1)) == 0
 
     ctl = []
     for h in range(NB):
         cs = 1 << popc(h)
         edge = help_ and h in (0, full)
-        ctl.append((1 if edge else cs, None,
-                    (6 if edge else 5) if help_ else cs + (1 << (nh - popc(h))) - 1))
+        ctl.append((1 if edge else cs, None, T - 1 if edge else cs + (1 << (nh - popc(h))) - 1))
     for t in range(T):
         for h in range(NB):
             if is_turn(t) and ctl[h][0] == t:
@@ -587,18 +599,18 @@ def inner_frame_backward(a, b, gc, metric):
                         continue
                     ca[h][..., oo] += low_sign(LC, lowneg, oo, q) * wa[q] * g[..., oo ^ q]
                     cb[h][..., oo] += low_sign(RC, lowneg, q, oo) * wb[q] * gt[..., oo ^ q]
-        if help_ and t == 6:
-            ca[0] = ca[0] + ca[1] + ca[2]
-            cb[0] = cb[0] + cb[1] + cb[2]
-            ca[full] = turn(ca[full] + ca[5] + ca[6], fa)
-            cb[full] = turn(cb[full] + cb[5] + cb[6], fb)
+        if help_ and t == T - 1:
+            ca[0] = ca[0] + sum(ca[x] for x in h0)
+            cb[0] = cb[0] + sum(cb[x] for x in h0)
+            ca[full] = turn(ca[full] + sum(ca[x] for x in hf), fa)
+            cb[full] = turn(cb[full] + sum(cb[x] for x in hf), fb)
         for h in range(NB):
             if ctl[h][2] == t:
                 ga[..., h * 16:(h + 1) * 16] = ca[h]
                 gb[..., h * 16:(h + 1) * 16] = cb[h]
-                if help_ and t == 5:
-                    ca[h] = np.zeros(rows + (16,))
-                    cb[h] = np.zeros(rows + (16,))
+            if help_ and t == T - c - 1 and h in h0 + hf:  # helpers start from zero
+                ca[h] = np.zeros(rows + (16,))
+                cb[h] = np.zeros(rows + (16,))
     return ga, gb
 
 

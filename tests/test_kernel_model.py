@@ -151,7 +151,8 @@ def test_inner_union_backward_round(metric):
 
 
 @pytest.mark.parametrize("metric", [(1,) * 4, (-1,) * 4, (1,) * 4 + (-1,), (1,) * 6, (-1,) * 5 + (1,),
-                                    (1,) * 6 + (-1,), (-1,) * 7, (1, 1, 1, 1, -1, 1, -1), (-1,) * 4 + (1, -1, 1)],
+                                    (1,) * 6 + (-1,), (-1,) * 7, (1, 1, 1, 1, -1, 1, -1), (-1,) * 4 + (1, -1, 1),
+                                    (1,) * 8, (1,) * 7 + (-1,), (-1,) * 4 + (1, -1, 1, -1)],
                          ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
 def test_inner_frame_backward(metric):
     """The per-lane-frame backward of the inner product (4 <= n <= 7): sub
@@ -176,17 +177,17 @@ def test_inner_frame_backward(metric):
 def test_inner_frame_schedule_covers_every_pair():
     """Every related (output, partner) block pair of the inner product's
     backward is walked once in sub and once in sup mode when the blocks are
-    equal, once otherwise, and at n = 7 no lane exceeds seven steps."""
-    for nh in range(4):
+    equal, once otherwise, within the kernel's step count (7 at n = 7, 11 at
+    n = 8)."""
+    for nh in range(5):
         NB = 1 << nh
         full = NB - 1
-        T = 7 if nh == 3 else NB + 1
+        T = K.frame_steps_count(nh)
         seen = {}
         for h in range(NB):
             for t in range(T):
                 o, p, sub = K.frame_step(nh, h, t)
                 idle = (o, p) == (h, h) and not sub and t >= (1 << K.popc(h)) + (1 << (nh - K.popc(h)))
-                idle = idle or (nh == 3 and t == 6 and h in (3, 4))
                 if not idle:
                     seen[(o, p, sub)] = seen.get((o, p, sub), 0) + 1
         want = {}

@@ -390,13 +390,14 @@ def test_n7_matrix_path_equals_direct_path(metric, clf_env):
 
 
 FRAME_METRICS = [(1,) * 4, (-1,) * 4, (1,) * 4 + (-1,), (-1,) * 5 + (1,), (1,) * 6 + (-1,), (-1,) * 7,
-                 (1, 1, 1, 1, -1, 1, -1), (-1, -1, -1, -1, 1, -1, 1)]
+                 (1, 1, 1, 1, -1, 1, -1), (-1, -1, -1, -1, 1, -1, 1), (1,) * 8, (1,) * 7 + (-1,),
+                 (-1, -1, -1, -1, 1, -1, 1, -1)]
 
 
 @pytest.mark.parametrize("metric", FRAME_METRICS, ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
 def test_inner_frame_kernels_match_oracle_and_blocked(metric, clf_env):
     """The inner product's one-lane-per-output kernels (backward for
-    4 <= n <= 7 with per-lane frames, forward at n = 7 with helper lanes):
+    4 <= n <= 8 with per-lane frames, forward at n = 7 with helper lanes):
     values and each gradient alone or both against the fp64 oracle, batches
     that end inside a group of rows (and a single row), and equal to the
     blocked kernels (CLF_PRODUCT_PATH=blocked) within rounding."""
