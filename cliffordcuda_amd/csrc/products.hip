@@ -1846,12 +1846,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     frame_steps(step, std::make_integer_sequence<int, T>{});
 }
 
-// ---- inner product forward at n = 7: one lane per output block -------------
+// ---- inner, lc and rc forward at n = 7: one lane per output block ---------
 // Output block o of a row takes, for every partner S inside ~o, the lc half
 // (a[S], b[S | o], il inside jl) and the rc half (a[S | o], b[S], jl inside
 // il) of the fused round, so every lane runs the same two patterns at every
 // step; for o = 0 both halves are (a[S], b[S]) and the diagonal il = jl,
-// counted twice, is taken off the scalar once. Output o has 2^(3 - |o|)
+// counted twice, is taken off the scalar once. The left contraction is the
+// lc half alone and the right contraction the rc half alone (the pairs
+// (S, S | o) and (S | o, S) are exactly their block pairs), with the same
+// schedule and no diagonal correction. Output o has 2^(3 - |o|)
 // partners (27 per row), so eight lanes cover a row in four steps when the
 // lanes of outputs 3 and 7, done early, take four of output 0's eight:
 //   o = 0: S = 0..3 | o = 1, 2, 4: their four | o = 3: S = 0, 4, then o = 0
@@ -1895,9 +1898,11 @@ __device__ __forceinline__ float fwd7_merge(float x) {
     return y;
 }
 
-template <bool LOWNEG>
-__global__ __launch_bounds__(256) void prod_fwd_inner7(const float* __restrict__ A, const float* __restrict__ B,
-                                                       float* __restrict__ C, BlkParams P) {
+template <int OP, bool LOWNEG>
+__global__ __launch_bounds__(256) void prod_fwd_out7(const float* __restrict__ A, const float* __restrict__ B,
+                                                     float* __restrict__ C, BlkParams P) {
+    static_assert(OP == OP_INNER || OP == OP_LC || OP == OP_RC, "lc and rc halves only");
+    constexpr bool kL = OP != OP_RC, kR = OP != OP_LC;  // the halves this op takes
     constexpr int N = 7, R = 8, T = 4;
     constexpr unsigned full = 7u;
     __shared__ __attribute__((aligned(64))) float4 lds[4][2 * kBalGroupF4];  // a | b
@@ -1951,23 +1956,33 @@ __global__ __launch_bounds__(256) void prod_fwd_inner7(const float* __restrict__
         const unsigned as0 = base + (e & 1023u), ao0 = base + ((e >> 10) & 1023u);
         unsigned hl = (e << 11) & 0x80000000u, hr = (e << 10) & 0x80000000u;
         unsigned hlo = hl ^ ((e << 9) & 0x80000000u), hro = hr ^ ((e << 8) & 0x80000000u);
-        asm volatile("" : "+v"(hl), "+v"(hr), "+v"(hlo), "+v"(hro));
+        if (kL) asm volatile("" : "+v"(hl), "+v"(hlo));
+        if (kR) asm volatile("" : "+v"(hr), "+v"(hro));
         const float fac = (e >> 24) & 1u ? -1.f : 0.f;
         float av[16], bv[16], av2[16], bv2[16];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const unsigned xs = as0 ^ ((unsigned)q << 4), xo = ao0 ^ ((unsigned)q << 4);
-            const float4 v0 = lds_ld4(xs), v1 = lds_ld4(xo + 4096u), v2 = lds_ld4(xo), v3 = lds_ld4(xs + 4096u);
-            av[4 * q] = v0.x; av[4 * q + 1] = v0.y; av[4 * q + 2] = v0.z; av[4 * q + 3] = v0.w;
-            bv[4 * q] = v1.x; bv[4 * q + 1] = v1.y; bv[4 * q + 2] = v1.z; bv[4 * q + 3] = v1.w;
-            av2[4 * q] = v2.x; av2[4 * q + 1] = v2.y; av2[4 * q + 2] = v2.z; av2[4 * q + 3] = v2.w;
-            bv2[4 * q] = v3.x; bv2[4 * q + 1] = v3.y; bv2[4 * q + 2] = v3.z; bv2[4 * q + 3] = v3.w;
+            if (kL) {
+                const float4 v0 = lds_ld4(xs), v1 = lds_ld4(xo + 4096u);
+                av[4 * q] = v0.x; av[4 * q + 1] = v0.y; av[4 * q + 2] = v0.z; av[4 * q + 3] = v0.w;
+                bv[4 * q] = v1.x; bv[4 * q + 1] = v1.y; bv[4 * q + 2] = v1.z; bv[4 * q + 3] = v1.w;
+            }
+            if (kR) {
+                const float4 v2 = lds_ld4(xo), v3 = lds_ld4(xs + 4096u);
+                av2[4 * q] = v2.x; av2[4 * q + 1] = v2.y; av2[4 * q + 2] = v2.z; av2[4 * q + 3] = v2.w;
+                bv2[4 * q] = v3.x; bv2[4 * q + 1] = v3.y; bv2[4 * q + 2] = v3.z; bv2[4 * q + 3] = v3.w;
+            }
         }
-        apply_flips(bv, hl, hlo);   // lc half (S, S | o): cross parity |S|
-        apply_flips(bv2, hr, hro);  // rc half (S | o, S): cross parity |S | o|
-        lowblock_fwd<LV_LC, LOWNEG>(acc, av, bv);
-        fwd7_diag<LOWNEG>(acc, av, bv, fac, std::make_integer_sequence<int, 16>{});
-        lowblock_fwd<LV_RC, LOWNEG>(acc, av2, bv2);
+        if (kL) {  // lc half (S, S | o): cross parity |S|
+            apply_flips(bv, hl, hlo);
+            lowblock_fwd<LV_LC, LOWNEG>(acc, av, bv);
+        }
+        if (OP == OP_INNER) fwd7_diag<LOWNEG>(acc, av, bv, fac, std::make_integer_sequence<int, 16>{});
+        if (kR) {  // rc half (S | o, S): cross parity |S | o|
+            apply_flips(bv2, hr, hro);
+            lowblock_fwd<LV_RC, LOWNEG>(acc, av2, bv2);
+        }
         if constexpr (t == 0) {
             if (h == 7u) store();
         }
@@ -2296,6 +2311,30 @@ static bool frame_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, 
     return true;
 }
 
+// the one-lane-per-output forward at n = 7: inner, lc and rc without a null
+// generator (blocked_metric: a uniform low metric)
+static bool out7_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, bool& lowneg) {
+    if (n != 7 || nul != 0u || (op != OP_INNER && op != OP_LC && op != OP_RC)) return false;
+    if (options().product_path != PATH_DEFAULT) return false;
+    if (!blocked_metric(op, n, neg, nul, lowneg)) return false;
+    block_sign_params(n, neg, nul, P);
+    return true;
+}
+
+template <int OP>
+static void launch_out7(hipStream_t s, bool ln, const float* a, const float* b, float* c, const BlkParams& P) {
+    const long long groups = (P.batch + 7) / 8;
+    for (long long g0 = 0; g0 < groups; g0 += kMaxGrid * 4) {  // one group of 8 rows per wave
+        const long long gn = groups - g0 < kMaxGrid * 4 ? groups - g0 : kMaxGrid * 4;
+        BlkParams Q = P;
+        Q.batch = (g0 + gn) * 8 < P.batch ? gn * 8 : P.batch - g0 * 8;
+        const long long off = g0 * 8 * 128;
+        const dim3 grid((unsigned)((gn + 3) / 4));
+        if (ln) hipLaunchKernelGGL((prod_fwd_out7<OP, true>), grid, dim3(256), 0, s, a + off, b + off, c + off, Q);
+        else hipLaunchKernelGGL((prod_fwd_out7<OP, false>), grid, dim3(256), 0, s, a + off, b + off, c + off, Q);
+    }
+}
+
 template <int N, bool LN, bool WA, bool WB>
 static void launch_frame3(hipStream_t s, const float* A, const float* B, const float* GCp, float* GA, float* GB,
                           const BlkParams& P) {
@@ -2417,16 +2456,10 @@ int product_fwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
     dim3 g, bl;
     size_t lds = 0;
     const bool force_tiled = n >= 12 && tiled_forced(), force_generic = generic_forced();
-    if (frame_plan(op, n, neg, nul, P, ln) && n == 7) {
-        const long long groups = (batch + 7) / 8;
-        for (long long g0 = 0; g0 < groups; g0 += kMaxGrid * 4) {  // one group of 8 rows per wave
-            const long long gn = groups - g0 < kMaxGrid * 4 ? groups - g0 : kMaxGrid * 4;
-            BlkParams Q = P;
-            Q.batch = (g0 + gn) * 8 < batch ? gn * 8 : batch - g0 * 8;
-            const long long off = g0 * 8 * 128;
-            if (ln) hipLaunchKernelGGL(prod_fwd_inner7<true>, dim3((unsigned)((gn + 3) / 4)), dim3(256), 0, s, a + off, b + off, c + off, Q);
-            else hipLaunchKernelGGL(prod_fwd_inner7<false>, dim3((unsigned)((gn + 3) / 4)), dim3(256), 0, s, a + off, b + off, c + off, Q);
-        }
+    if (out7_plan(op, n, neg, nul, P, ln)) {
+        if (op == OP_INNER) launch_out7<OP_INNER>(s, ln, a, b, c, P);
+        else if (op == OP_LC) launch_out7<OP_LC>(s, ln, a, b, c, P);
+        else launch_out7<OP_RC>(s, ln, a, b, c, P);
     } else if (!force_generic && bal_plan(op, n, neg, nul, true, P, ln)) {
 #define CLF_FWD_BAL(OPV)                                               \
     case OPV:                                                          \

@@ -434,3 +434,24 @@ def test_inner_frame_kernels_match_oracle_and_blocked(metric, clf_env):
         clf_env.delenv("CLF_PRODUCT_PATH")
         assert rel_err(c, cb) <= 1e-6
         assert rel_err(got[(True, True)][0], gab) <= 1e-6 and rel_err(got[(True, True)][1], gbb) <= 1e-6
+
+
+@pytest.mark.parametrize("metric", [m for m in FRAME_METRICS if len(m) == 7],
+                         ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
+@pytest.mark.parametrize("op", ["inner", "lc", "rc"])
+def test_out7_forward_matches_oracle_and_blocked(op, metric, clf_env):
+    """The n = 7 one-lane-per-output forward (inner: both halves, lc and rc:
+    one half each) against the fp64 oracle on batches that end inside a group
+    of eight rows, and equal to the blocked kernel within rounding."""
+    from cliffordcuda_amd import products
+    n = 7
+    for batch in (1, 7, 29, 4 * 64 * 8 + 7):
+        print(f"[case] out7 forward op={op} metric={metric} batch={batch}", flush=True)
+        a, b = seeded(batch, n, batch + 3 * n, 2)
+        c64 = O.einsum_product(op, a.double(), b.double(), metric)
+        c = products.product(op, a.cuda(), b.cuda(), metric)
+        assert rel_err(c, c64) <= TOL
+        clf_env.setenv("CLF_PRODUCT_PATH", "blocked")
+        cb = products.product(op, a.cuda(), b.cuda(), metric)
+        clf_env.delenv("CLF_PRODUCT_PATH")
+        assert rel_err(c, cb) <= 1e-6
