@@ -614,6 +614,108 @@ def inner_frame_backward(a, b, gc, metric):
     return ga, gb
 
 
+def _rho(k):
+    """Reversion sign of a blade of grade |k|: (-1)^(|k| (|k| - 1) / 2)."""
+    return -1.0 if (popc(k) >> 1) & 1 else 1.0
+
+
+def contraction_frame_backward(op, a, b, gc, metric):
+    """The left (LC) or right (RC) contraction's backward as
+    prod_bwd_contr_frame computes it: the inner product's frame schedule
+    (frame_step) with one accumulator per lane. A step yields ga (lc: sup
+    pairs, rc: sub pairs) or gb (lc: sub pairs, rc: sup pairs) and every step
+    runs the ga sup pattern acc[o] += s_lc(o, q) w[q] g[o ^ q]. A gb step uses
+    s_rc(q, o) = s_lc(o, q) rho(o) rho(q) rho(o ^ q) (rho: the reversion sign;
+    o inside q): its partner and gc blocks take rho(q), rho(x) on top of the
+    inner kernel's flips and the result takes rho(o) when stored. A lane
+    stores its first output when its first mode ends (turned to the normal
+    frame if that mode was sub) and starts from zero, and its second at the
+    end of its list; outputs 0 and full add their helpers' sums first.
+    Returns (ga, gb)."""
+    n = len(metric)
+    nh = n - 4
+    NB = 1 << nh
+    full = NB - 1
+    neg = sum(1 << k for k, m in enumerate(metric) if m == -1)
+    assert op in (LC, RC) and all(m != 0 for m in metric) and (neg & 15) in (0, 15)
+    lowneg = (neg & 15) == 15
+    negh = neg >> 4
+    help_ = nh in FRAME_HELP
+    T = frame_steps_count(nh)
+    h0, hf, c = (FRAME_HELP[nh][1][0], FRAME_HELP[nh][1][1], FRAME_HELP[nh][2]) if help_ else ((), (), 0)
+    fa = [(_frame_w1(k) ^ (lowneg & popc(k))) & 1 for k in range(16)]
+    fb = [(_frame_w2(k) ^ (lowneg & popc(k))) & 1 for k in range(16)]
+    rows = a.shape[:-1]
+    acc = [np.zeros(rows + (16,)) for _ in range(NB)]
+    ga = np.zeros(a.shape)
+    gb = np.zeros(b.shape)
+
+    def yields_gb(sub):
+        return sub if op == LC else not sub
+
+    def result(x, sub):
+        """the stored block of an accumulator that ran in mode sub"""
+        if yields_gb(sub):
+            x = x * np.array([_rho(k) for k in range(16)])
+        if sub:
+            f = fb if yields_gb(sub) else fa
+            x = np.stack([(-1.0 if f[k] else 1.0) * x[..., 15 - k] for k in range(16)], -1)
+        return x
+
+    def put(h, x, sub):
+        dst = gb if yields_gb(sub) else ga
+        dst[..., h * 16:(h + 1) * 16] = result(x, sub)
+
+    for t in range(T):
+        for h in range(NB):
+            o, p, sub = frame_step(nh, h, t)
+            X = o ^ p
+            g = gc[..., X * 16:(X + 1) * 16]
+            podd, oodd = popc(p) & 1, popc(o) & 1
+            w = []
+            for q in range(16):
+                e = 15 - q if sub else q
+                par = popc(q) & 1
+                if yields_gb(sub):
+                    _, s = hi_sign(INNER, p, o, negh, 0, full, 0, 0)
+                    f = s * (-1 if par and podd else 1) * (-1 if sub and (_frame_w1(q) ^ (lowneg & par)) else 1)
+                    w.append(f * _rho(q) * a[..., p * 16 + e])
+                else:
+                    _, s = hi_sign(INNER, o, p, negh, 0, full, 0, 0)
+                    f = s * (-1 if par and oodd else 1) * (-1 if sub and (_frame_w2(q) ^ (lowneg & par)) else 1)
+                    w.append(f * b[..., p * 16 + e])
+            if yields_gb(sub):
+                gg = [g[..., x] * (-1.0 if (popc(x) & 1 and podd) else 1.0) * _rho(x) for x in range(16)]
+            else:
+                gg = [g[..., x] for x in range(16)]
+            for oo in range(16):
+                for q in range(16):
+                    if oo & ~q & 15:
+                        continue
+                    acc[h][..., oo] += low_sign(LC, lowneg, oo, q) * w[q] * gg[oo ^ q]
+        for h in range(NB):
+            o, p, sub = frame_step(nh, h, t)
+            last = t == T - 1
+            edge = help_ and h in (0, full)
+            if edge:
+                if t == 0:  # the one-pair first mode of outputs 0 and full
+                    put(h, acc[h], sub)
+                    acc[h] = np.zeros(rows + (16,))
+                elif last:
+                    put(h, acc[h] + sum(acc[x] for x in (h0 if h == 0 else hf)), sub)
+                continue
+            cs = 1 << popc(h)
+            end = cs + (1 << (nh - popc(h))) - 1
+            if t == cs - 1:  # sub pairs done: the first output
+                put(h, acc[h], True)
+                acc[h] = np.zeros(rows + (16,))
+            if t == end:
+                put(h, acc[h], False)
+            if help_ and t == T - c - 1 and h in h0 + hf:  # helpers start from zero
+                acc[h] = np.zeros(rows + (16,))
+    return ga, gb
+
+
 def fwd7_step(h, t):
     """Step t of lane h in prod_fwd_inner7 (n = 7): (output block o, partner S)
     or None (idle). Lanes 3 and 7 finish their outputs early and then take

@@ -174,6 +174,40 @@ def test_inner_frame_backward(metric):
     np.testing.assert_allclose(gb, bt.grad.numpy(), atol=1e-10)
 
 
+@pytest.mark.parametrize("metric", [(1,) * 4, (-1,) * 4, (1,) * 4 + (-1,), (-1,) * 5 + (1,), (1,) * 6 + (-1,),
+                                    (-1,) * 7, (1, 1, 1, 1, -1, 1, -1), (1,) * 8, (-1,) * 4 + (1, -1, 1, -1)],
+                         ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
+@pytest.mark.parametrize("op", ["lc", "rc"])
+def test_contraction_frame_backward(op, metric):
+    """The contractions' backward on the inner product's frame schedule with
+    one accumulator per lane: every step runs the ga sup pattern, gb steps
+    through s_rc(q, o) = s_lc(o, q) rho(o) rho(q) rho(o ^ q) (o inside q, rho
+    the reversion sign). Gives the oracle's gradients."""
+    n = len(metric)
+    rng = np.random.default_rng(n + 11)
+    a, b, gc = (rng.standard_normal((2, 1 << n)) for _ in range(3))
+    at = torch.tensor(a, requires_grad=True)
+    bt = torch.tensor(b, requires_grad=True)
+    O.einsum_product(op, at, bt, list(metric)).backward(torch.tensor(gc))
+    ga, gb = K.contraction_frame_backward(K.OPS[op], a, b, gc, list(metric))
+    np.testing.assert_allclose(ga, at.grad.numpy(), atol=1e-10)
+    np.testing.assert_allclose(gb, bt.grad.numpy(), atol=1e-10)
+
+
+def test_reversion_sign_factorisation():
+    """s_rc(q, o) = s_lc(o, q) rho(o) rho(q) rho(o ^ q) for every o inside q
+    of a 4-bit low block, either low metric: the identity that lets one sign
+    pattern serve both gradients of a contraction."""
+    for lowneg in (False, True):
+        for o in range(16):
+            for q in range(16):
+                if o & ~q:
+                    continue
+                lhs = K.low_sign(K.RC, lowneg, q, o)
+                rhs = K.low_sign(K.LC, lowneg, o, q) * K._rho(o) * K._rho(q) * K._rho(o ^ q)
+                assert lhs == rhs, (lowneg, o, q)
+
+
 def test_inner_frame_schedule_covers_every_pair():
     """Every related (output, partner) block pair of the inner product's
     backward is walked once in sub and once in sup mode when the blocks are
