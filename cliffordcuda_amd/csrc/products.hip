@@ -1846,6 +1846,251 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     frame_steps(step, std::make_integer_sequence<int, T>{});
 }
 
+// ---- left and right contraction backward for 4 <= n <= 8 -----------------
+// The inner product's frame schedule (frame_step, helpers, merges) and layout
+// with one accumulator per lane. A contraction's pair is related one way
+// only, so a step yields one gradient: the left contraction's sub pairs
+// (partner a[p], p inside h) give gb[h] and its sup pairs (b[p], p containing
+// h) give ga[h]; the right contraction the other way round. Every step runs
+// the ga sup pattern acc[o] += s_lc(o, q) w[q] g[o ^ q] (q containing o); a
+// gb step uses s_rc(q, o) = s_lc(o, q) rho(o) rho(q) rho(o ^ q), rho the
+// reversion sign (-1)^(|k| (|k| - 1) / 2): its partner block takes rho(q) and
+// its gc block rho(x) on top of the inner kernel's flips, and the stored block
+// takes rho(o). A lane stores its first output when its first mode ends
+// (turned to the normal frame if that mode was sub) and starts from zero, and
+// its second output at the end of its list; outputs 0 and full (which walk
+// one pair in their first mode) add their helpers' sums first.
+__host__ __device__ constexpr int rho4(int k) { return (__builtin_popcount((unsigned)k) >> 1) & 1; }
+
+template <int NH>
+struct ContrSched {
+    using S = FrameSched<NH>;
+    static constexpr int NB = 1 << NH;
+    static constexpr bool edge(unsigned h) { return S::kHelp && (h == 0u || h == (unsigned)(NB - 1)); }
+    // steps after which lane h stores its first and its second output
+    static constexpr int first_t(unsigned h) { return edge(h) ? 0 : (1 << __builtin_popcount(h)) - 1; }
+    static constexpr int second_t(unsigned h) {
+        return edge(h) ? S::T - 1 : (1 << __builtin_popcount(h)) + (1 << (NH - __builtin_popcount(h))) - 1;
+    }
+    // the mode of a lane's first output: sub, except output full with helpers
+    static constexpr bool first_sub(unsigned h) { return !(edge(h) && h == (unsigned)(NB - 1)); }
+    // modes of the outputs stored after step t: bit 0 sub, bit 1 sup
+    static constexpr int kinds(int t) {
+        int k = 0;
+        for (unsigned h = 0; h < (unsigned)NB; ++h) {
+            if (first_t(h) == t) k |= first_sub(h) ? 1 : 2;
+            if (second_t(h) == t) k |= first_sub(h) ? 2 : 1;
+        }
+        return k;
+    }
+    static constexpr bool any_first(int t) {
+        for (unsigned h = 0; h < (unsigned)NB; ++h)
+            if (first_t(h) == t) return true;
+        return false;
+    }
+    static constexpr bool any_second(int t) {
+        for (unsigned h = 0; h < (unsigned)NB; ++h)
+            if (second_t(h) == t) return true;
+        return false;
+    }
+};
+
+// y = the stored block of an accumulator whose mode was sub (turned to the
+// normal frame) or sup; GBK: the block is a gb block (rho(o) on the
+// accumulator's positions)
+template <bool LOWNEG, bool GBK>
+__device__ __forceinline__ float contr_out_sub(const float (&x)[16], int k) {
+    const int src = 15 - k;
+    const bool f = (((GBK ? w2b(k) : w1b(k)) ^ (LOWNEG ? par4(k) : 0) ^ (GBK ? rho4(src) : 0)) & 1) != 0;
+    return f ? -x[src] : x[src];
+}
+
+template <bool GBK>
+__device__ __forceinline__ float contr_out_sup(const float (&x)[16], int k) {
+    return GBK && rho4(k) ? -x[k] : x[k];
+}
+
+template <int OP, int N, bool LOWNEG>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void prod_bwd_contr_frame(
+    const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ GC, float* __restrict__ GA,
+    float* __restrict__ GB, BlkParams P) {
+    static_assert(OP == OP_LC || OP == OP_RC, "contractions only");
+    constexpr int NH = N - 4, NB = 1 << NH, R = 64 >> NH;
+    using Sch = FrameSched<NH>;
+    using Cs = ContrSched<NH>;
+    constexpr int T = Sch::T;
+    constexpr unsigned full = NB - 1u;
+    constexpr bool kLC = OP == OP_LC;  // sub steps yield gb (lc) or ga (rc)
+    __shared__ __attribute__((aligned(64))) float4 lds[4][3 * kBalGroupF4];  // a | b | gc
+    // the steps of lane (h, row slot skew rs): tab[t][rs * NB + h]
+    __shared__ unsigned tab[T][4 * NB];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const unsigned h = (unsigned)lane & full;
+    const int r = lane >> NH;
+    const unsigned rs = (unsigned)r & 3u;
+    const int first_t = Cs::first_t(h), second_t = Cs::second_t(h);
+    const bool first_sub = Cs::first_sub(h);
+    // one group of R rows per wave (the host splits batches larger than one grid)
+    const long long ngrp = (P.batch + R - 1) / R;
+    const long long grp = (long long)blockIdx.x * 4 + wave;
+    const BalLane L = bal_lane(N, lane);
+    const bool gbc = P.ldg4 == 0;
+    const BalPre pa = bal_fetch(bal_src(A, grp, P.batch, N, R), L, N - 2);
+    const BalPre pb = bal_fetch(bal_src(B, grp, P.batch, N, R), L, N - 2);
+    const BalPre pg = bal_fetch(bal_src(GC, grp, P.batch, N, R, gbc), L, N - 2);
+    // entry: gc block offset (o ^ p), partner offset (a at +0, b at +4 KB; slot
+    // order reversed in sub mode), then the step's flip bits: pair sign S,
+    // parity term Pm, w1 and w2 terms (sub mode), rho (gb steps), gc parity
+    // term Gp (gb steps)
+    if (wave == 0 && lane < 4 * NB) {
+        const unsigned th = (unsigned)lane & full, trs = (unsigned)lane >> NH;
+        for (int t = 0; t < T; ++t) {
+            const FrameStep st = frame_step<NH>(th, t);
+            const unsigned X = st.o ^ st.p;
+            const bool gbs = kLC ? st.sub : !st.sub;
+            const HiSign hs = gbs ? hi_sign<OP_INNER>(st.p, st.o, P.negh, P.nulh, full, P.nm1, P.mu)
+                                  : hi_sign<OP_INNER>(st.o, st.p, P.negh, P.nulh, full, P.nm1, P.mu);
+            const unsigned podd = (unsigned)__popc(st.p) & 1u, oodd = (unsigned)__popc(st.o) & 1u;
+            const unsigned sub = st.sub ? 1u : 0u, gb = gbs ? 1u : 0u;
+            const unsigned offg = ((X << 2) | (swz(X) ^ trs)) << 4;
+            const unsigned offw = (((st.p << 2) | (swz(st.p) ^ trs ^ (st.sub ? 3u : 0u))) << 4) + (gbs ? 0u : 4096u);
+            const unsigned pm = (gb ? podd : oodd) ^ (LOWNEG ? sub : 0u);
+            tab[t][lane] = offg | (offw << 10) | ((hs.mask >> 31) << 23) | (pm << 24) | ((gb & sub) << 25) |
+                           (((gb ^ 1u) & sub) << 26) | (gb << 27) | ((gb & podd) << 28);
+        }
+    }
+    __syncthreads();
+    if (grp >= ngrp) return;
+    const int tix = (int)(rs * NB + h);
+    float4* sa = lds[wave];
+    const unsigned base = lds_addr4(sa + (r << (N - 2)));  // the row's a block 0; b at +4 KB, gc at +8 KB
+    {
+        // a and b in the frame layout: component c of the lane's chunks (block
+        // slot fq) goes to component c ^ fq, one dword store each
+        const unsigned fq = (unsigned)lane & 3u;
+        const unsigned a0 = lds_addr4(sa);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const unsigned ad = (a0 + L.so[i]) | (fq << 2);
+            const float va[4] = {pa.v[i].x, pa.v[i].y, pa.v[i].z, pa.v[i].w};
+            const float vb[4] = {pb.v[i].x, pb.v[i].y, pb.v[i].z, pb.v[i].w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const unsigned adc = ad ^ ((unsigned)c << 2);
+                *(__attribute__((address_space(3))) float*)(uintptr_t)adc = va[c];
+                *(__attribute__((address_space(3))) float*)(uintptr_t)(adc + 4096u) = vb[c];
+            }
+            lds_st4(a0 + 8192u + L.so[i], pg.v[i]);
+        }
+    }
+    wave_lds_sync();
+    // the lane's two output blocks wait in registers (y1: the first mode's,
+    // y2: the second's) and leave through LDS in row order after the last step
+    float acc[16], y1[16], y2[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        acc[e] = 0.f;
+        y1[e] = 0.f;
+        y2[e] = 0.f;
+    }
+    auto step = [&](auto tc) {
+        constexpr int t = decltype(tc)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        unsigned e = tab[t][tix];
+        asm volatile("" : "+v"(e));  // decoded per step, not kept for every step across the kernel
+        const unsigned g0 = base + 8192u + (e & 1023u);
+        const unsigned w0 = base + ((e >> 10) & 8191u);
+        unsigned ms = (e << 8) & 0x80000000u, mp = (e << 7) & 0x80000000u, m1 = (e << 6) & 0x80000000u;
+        unsigned m2 = (e << 5) & 0x80000000u, mr = (e << 4) & 0x80000000u, mg = (e << 3) & 0x80000000u;
+        asm volatile("" : "+v"(ms), "+v"(mp), "+v"(m1), "+v"(m2), "+v"(mr), "+v"(mg));
+        float g[16], w[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 vg = lds_ld4(g0 ^ ((unsigned)q << 4));
+            const float4 vw = lds_ld4(w0 ^ ((unsigned)q << 4));
+            g[4 * q] = vg.x;
+            g[4 * q + 1] = vg.y;
+            g[4 * q + 2] = vg.z;
+            g[4 * q + 3] = vg.w;
+            w[4 * q] = vw.x;
+            w[4 * q + 1] = vw.y;
+            w[4 * q + 2] = vw.z;
+            w[4 * q + 3] = vw.w;
+        }
+        // partner flips by element class: one mask by (parity, rho) with the
+        // pair sign, one by (w1, w2), both xor-ed in one three-input op; gc
+        // flips by (parity, rho)
+        unsigned x1 = ms ^ mp, x2 = ms ^ mr, x3 = x1 ^ mr, y3 = m1 ^ m2, gpr = mg ^ mr;
+        asm volatile("" : "+v"(x1), "+v"(x2), "+v"(x3), "+v"(y3), "+v"(gpr));
+#pragma unroll
+        for (int el = 0; el < 16; ++el) {
+            const unsigned xa = par4(el) ? (rho4(el) ? x3 : x1) : (rho4(el) ? x2 : ms);
+            const int wcl = w1b(el) + 2 * w2b(el);
+            const unsigned u = __float_as_uint(w[fr_reg(el)]);
+            w[fr_reg(el)] = __uint_as_float(wcl == 0 ? u ^ xa : u ^ xa ^ (wcl == 1 ? m1 : wcl == 2 ? m2 : y3));
+            if (par4(el) || rho4(el)) g[el] = flip(g[el], par4(el) && rho4(el) ? gpr : par4(el) ? mg : mr);
+        }
+        frame_sup<LOWNEG, true, false>(acc, acc, w, w, g, g, std::make_integer_sequence<int, 256>{});
+        if constexpr (Sch::kHelp && t == T - 1) {  // outputs 0 and full add their helpers' sums
+#pragma unroll
+            for (int el = 0; el < 16; ++el) {
+                if constexpr (NH == 3) acc[el] = quad_merge(acc[el]);
+                else acc[el] = row16_merge(acc[el], h);
+            }
+        }
+        constexpr int K = Cs::kinds(t);
+        if constexpr (K != 0) {
+            const bool first = first_t == t, second = second_t == t;
+            const bool sub = first == first_sub;  // the mode of the output completed here
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const float ys = contr_out_sub<LOWNEG, kLC>(acc, k);
+                const float yp = contr_out_sup<!kLC>(acc, k);
+                const float y = K == 1 ? ys : K == 2 ? yp : (sub ? ys : yp);
+                if constexpr (Cs::any_first(t)) y1[k] = first ? y : y1[k];
+                if constexpr (Cs::any_second(t)) y2[k] = second ? y : y2[k];
+            }
+            if constexpr (Cs::any_first(t)) {
+#pragma unroll
+                for (int el = 0; el < 16; ++el) acc[el] = first ? 0.f : acc[el];
+            }
+        }
+        if constexpr (Sch::kHelp && t == T - Sch::C - 1) {  // the helpers start from zero
+            const bool z = Sch::helper(h);
+#pragma unroll
+            for (int el = 0; el < 16; ++el) acc[el] = z ? 0.f : acc[el];
+        }
+    };
+    frame_steps(step, std::make_integer_sequence<int, T>{});
+    // ga rows over the staged a, gb rows over b, in the staging layout (block
+    // h of row r at slots 4h + (q ^ swz(h) ^ (r & 3))); then row-order stores
+    wave_lds_sync();
+    {
+        const bool first_gb = first_sub == kLC;  // the first mode's output is a gb block
+        const unsigned rowb = lds_addr4(sa) + ((unsigned)r << (N + 2));
+        const unsigned o1 = rowb + (first_gb ? 4096u : 0u), o2 = rowb + (first_gb ? 0u : 4096u);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const unsigned slot = (((h << 2) | ((unsigned)q ^ swz(h) ^ rs)) << 4);
+            lds_st4(o1 + slot, make_float4(y1[4 * q], y1[4 * q + 1], y1[4 * q + 2], y1[4 * q + 3]));
+            lds_st4(o2 + slot, make_float4(y2[4 * q], y2[4 * q + 1], y2[4 * q + 2], y2[4 * q + 3]));
+        }
+    }
+    wave_lds_sync();
+    {
+        const unsigned a0 = lds_addr4(sa);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const long long rr = grp * R + (long long)L.rr[i];
+            if (rr < P.batch) {
+                const long long at = (rr << (N - 2)) + (long long)L.ff[i];
+                if (GA) reinterpret_cast<float4*>(GA)[at] = lds_ld4(a0 + L.so[i]);
+                if (GB) reinterpret_cast<float4*>(GB)[at] = lds_ld4(a0 + 4096u + L.so[i]);
+            }
+        }
+    }
+}
+
 // ---- inner, lc and rc forward at n = 7: one lane per output block ---------
 // Output block o of a row takes, for every partner S inside ~o, the lc half
 // (a[S], b[S | o], il inside jl) and the rc half (a[S | o], b[S], jl inside
@@ -2379,6 +2624,52 @@ static void launch_frame(int n, bool ln, hipStream_t s, const float* A, const fl
 #undef CLF_FRAME_N
 }
 
+// The contractions' backward on the frame schedule: lc and rc for
+// 4 <= n <= 8 without a null generator and with a uniform low metric.
+static bool contr_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, bool& lowneg) {
+    if ((op != OP_LC && op != OP_RC) || n < kFrameMinN || n > kFrameMaxN || nul != 0u) return false;
+    if (options().product_path != PATH_DEFAULT) return false;
+    if (!blocked_metric(op, n, neg, nul, lowneg)) return false;
+    block_sign_params(n, neg, nul, P);
+    return true;
+}
+
+template <int OP, int N, bool LN>
+static void launch_contr3(hipStream_t s, const float* A, const float* B, const float* GCp, float* GA, float* GB,
+                          const BlkParams& P) {
+    // one wave per group of R rows, as launch_frame3
+    const long long R = 64 >> (N - 4);
+    const long long chunk = kMaxGrid * 4 * R;
+    const long long D = 1LL << N;
+    for (long long r0 = 0; r0 < P.batch; r0 += chunk) {
+        BlkParams Q = P;
+        Q.batch = P.batch - r0 < chunk ? P.batch - r0 : chunk;
+        const long long groups = (Q.batch + R - 1) / R;
+        const dim3 g((unsigned)((groups + 3) / 4));
+        const long long off = r0 * D;
+        hipLaunchKernelGGL((prod_bwd_contr_frame<OP, N, LN>), g, dim3(256), 0, s, A + off, B + off,
+                           GCp + (P.ldg4 ? off : 0), GA ? GA + off : nullptr, GB ? GB + off : nullptr, Q);
+    }
+}
+
+template <int OP>
+static void launch_contr(int n, bool ln, hipStream_t s, const float* A, const float* B, const float* GCp, float* GA,
+                         float* GB, const BlkParams& P) {
+#define CLF_CONTR_N(NV)                                                  \
+    case NV:                                                             \
+        if (ln) launch_contr3<OP, NV, true>(s, A, B, GCp, GA, GB, P);    \
+        else launch_contr3<OP, NV, false>(s, A, B, GCp, GA, GB, P);      \
+        break;
+    switch (n) {
+        CLF_CONTR_N(4)
+        CLF_CONTR_N(5)
+        CLF_CONTR_N(6)
+        CLF_CONTR_N(7)
+        CLF_CONTR_N(8)
+    }
+#undef CLF_CONTR_N
+}
+
 // Balanced kernels: wedge, lc, rc, regressive and the inner product for
 // 4 <= n <= 10 (CLF_PRODUCT_PATH=blocked keeps them on the one-lane-per-output
 // kernels). Up to n = 8 the inner product's backward runs on the per-lane
@@ -2536,6 +2827,9 @@ int product_bwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
     const bool force_tiled = n >= 12 && tiled_forced(), force_generic = generic_forced();
     if (frame_plan(op, n, neg, nul, P, ln)) {
         launch_frame(n, ln, s, a, b, gc, ga, gb, P);
+    } else if (contr_plan(op, n, neg, nul, P, ln)) {
+        if (op == OP_LC) launch_contr<OP_LC>(n, ln, s, a, b, gc, ga, gb, P);
+        else launch_contr<OP_RC>(n, ln, s, a, b, gc, ga, gb, P);
     } else if (!force_generic && bal_plan(op, n, neg, nul, false, P, ln)) {
 #define CLF_BWD_BAL(OPV)                                                       \
     case OPV:                                                                  \

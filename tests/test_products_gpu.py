@@ -455,3 +455,40 @@ def test_out7_forward_matches_oracle_and_blocked(op, metric, clf_env):
         cb = products.product(op, a.cuda(), b.cuda(), metric)
         clf_env.delenv("CLF_PRODUCT_PATH")
         assert rel_err(c, cb) <= 1e-6
+
+
+@pytest.mark.parametrize("metric", FRAME_METRICS, ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
+@pytest.mark.parametrize("op", ["lc", "rc"])
+def test_contraction_frame_backward_matches_oracle_and_blocked(op, metric, clf_env):
+    """The contractions' backward on the frame schedule (4 <= n <= 8, one
+    accumulator per lane, a store at each mode's end): each gradient alone and
+    both against the fp64 oracle, batches that end inside a group of rows (and
+    a single row), each alone bitwise equal to both, and equal to the blocked
+    kernels (CLF_PRODUCT_PATH=blocked) within rounding."""
+    from cliffordcuda_amd import _lib, products
+    from cliffordcuda_amd._validate import metric_masks
+    n = len(metric)
+    neg, nul = metric_masks(metric)
+    R = 1024 >> n
+    for batch in (1, R - 1, 3 * R + 5, 4 * 64 * R + 7):
+        print(f"[case] contraction frame op={op} metric={metric} batch={batch}", flush=True)
+        a, b, gc = seeded(batch, n, batch + 2 * n, 3)
+        a64 = a.double().requires_grad_()
+        b64 = b.double().requires_grad_()
+        O.einsum_product(op, a64, b64, metric).backward(gc.double())
+        ad, bd, gd = a.cuda(), b.cuda(), gc.cuda()
+        got = {}
+        for need in ((True, True), (True, False), (False, True)):
+            ga, gb = products._product_bwd(_lib.OP_CODES[op], n, neg, nul, ad, bd, gd, *need)
+            assert (ga is None) != need[0] and (gb is None) != need[1]
+            if ga is not None:
+                assert rel_err(ga, a64.grad) <= TOL
+            if gb is not None:
+                assert rel_err(gb, b64.grad) <= TOL
+            got[need] = (ga, gb)
+        assert torch.equal(got[(True, False)][0], got[(True, True)][0])
+        assert torch.equal(got[(False, True)][1], got[(True, True)][1])
+        clf_env.setenv("CLF_PRODUCT_PATH", "blocked")
+        gab, gbb = products._product_bwd(_lib.OP_CODES[op], n, neg, nul, ad, bd, gd, True, True)
+        clf_env.delenv("CLF_PRODUCT_PATH")
+        assert rel_err(got[(True, True)][0], gab) <= 1e-6 and rel_err(got[(True, True)][1], gbb) <= 1e-6
