@@ -2144,7 +2144,7 @@ __device__ __forceinline__ float fwd7_merge(float x) {
 }
 
 template <int OP, bool LOWNEG>
-__global__ __launch_bounds__(256) void prod_fwd_out7(const float* __restrict__ A, const float* __restrict__ B,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void prod_fwd_out7(const float* __restrict__ A, const float* __restrict__ B,
                                                      float* __restrict__ C, BlkParams P) {
     static_assert(OP == OP_INNER || OP == OP_LC || OP == OP_RC, "lc and rc halves only");
     constexpr bool kL = OP != OP_RC, kR = OP != OP_LC;  // the halves this op takes
@@ -2185,13 +2185,27 @@ __global__ __launch_bounds__(256) void prod_fwd_out7(const float* __restrict__ A
     bal_stage(sa + kBalGroupF4, pb, L);
     wave_lds_sync();
     const unsigned base = lds_addr4(sa + (r << (N - 2)));  // the row's a; b at +4 KB
+    // lc and rc: outputs 7 and 3, 5, 6 are complete after steps 0 and 1 and
+    // wait in y (lanes 3 and 7 go on with output 0); every output leaves
+    // through LDS in row order after the last step. The inner product (twice
+    // the operands per step) stores each output block when it is complete:
+    // holding y as well would halve its occupancy.
+    constexpr bool kRowOut = OP != OP_INNER;
     const long long row = grp * R + r;
     const bool row_ok = row < P.batch;
-    float acc[16];
+    float acc[16], y[16];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
-    auto store = [&]() {
-        if (row_ok) store_blk(reinterpret_cast<float4*>(C) + (row << (N - 2)), h, acc, false);
+    for (int e = 0; e < 16; ++e) {
+        acc[e] = 0.f;
+        y[e] = 0.f;
+    }
+    auto keep = [&](bool done) {
+        if constexpr (kRowOut) {
+#pragma unroll
+            for (int el = 0; el < 16; ++el) y[el] = done ? acc[el] : y[el];
+        } else if (done && row_ok) {
+            store_blk(reinterpret_cast<float4*>(C) + (row << (N - 2)), h, acc, false);
+        }
     };
     auto step = [&](auto tc) {
         constexpr int t = decltype(tc)::value;
@@ -2228,12 +2242,9 @@ __global__ __launch_bounds__(256) void prod_fwd_out7(const float* __restrict__ A
             apply_flips(bv2, hr, hro);
             lowblock_fwd<LV_RC, LOWNEG>(acc, av2, bv2);
         }
-        if constexpr (t == 0) {
-            if (h == 7u) store();
-        }
+        if constexpr (t == 0) keep(h == 7u);
         if constexpr (t == 1) {
-            const bool done = h == 3u || h == 5u || h == 6u;
-            if (done) store();
+            keep(h == 3u || h == 5u || h == 6u);
             const bool z = h == 3u || h == 7u;  // lanes 3 and 7 turn to output 0
 #pragma unroll
             for (int el = 0; el < 16; ++el) acc[el] = z ? 0.f : acc[el];
@@ -2244,10 +2255,25 @@ __global__ __launch_bounds__(256) void prod_fwd_out7(const float* __restrict__ A
                 const float m = fwd7_merge(acc[el]);
                 acc[el] = h == 0u ? m : acc[el];
             }
-            if (h == 0u || h == 1u || h == 2u || h == 4u) store();
+            keep(h == 0u || h == 1u || h == 2u || h == 4u);
         }
     };
     frame_steps(step, std::make_integer_sequence<int, T>{});
+    if constexpr (!kRowOut) return;
+    // block h of row r over the staged a (slots 4h + (q ^ swz(h) ^ (r & 3))),
+    // then row-order stores
+    wave_lds_sync();
+    const unsigned a0 = lds_addr4(sa);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        lds_st4(a0 + ((unsigned)r << (N + 2)) + (((h << 2) | ((unsigned)q ^ swz(h) ^ rs)) << 4),
+                make_float4(y[4 * q], y[4 * q + 1], y[4 * q + 2], y[4 * q + 3]));
+    wave_lds_sync();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const long long rr = grp * R + (long long)L.rr[i];
+        if (rr < P.batch) reinterpret_cast<float4*>(C)[(rr << (N - 2)) + (long long)L.ff[i]] = lds_ld4(a0 + L.so[i]);
+    }
 }
 
 // ---- tiled path (rows larger than LDS, n >= 12) -----------------------------
