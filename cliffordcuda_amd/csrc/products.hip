@@ -1737,8 +1737,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
         ca[e] = 0.f;
         cb[e] = 0.f;
     }
+    // a lane's output blocks wait in ya / yb once complete and leave through
+    // LDS in row order after the last step (n = 5, which has no registers to
+    // spare, stores each block when it is complete)
+    constexpr bool kRowOut = N != 5;
+    float ya[16], yb[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        ya[e] = 0.f;
+        yb[e] = 0.f;
+    }
     auto store = [&]() {
-        if (row_ok) {
+        if constexpr (kRowOut) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                if (WA) ya[e] = ca[e];
+                if (WB) yb[e] = cb[e];
+            }
+        } else if (row_ok) {
             if (WA) store_blk(reinterpret_cast<float4*>(GA) + (row << (N - 2)), h, ca, false);
             if (WB) store_blk(reinterpret_cast<float4*>(GB) + (row << (N - 2)), h, cb, false);
         }
@@ -1844,6 +1860,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
         }
     };
     frame_steps(step, std::make_integer_sequence<int, T>{});
+    if constexpr (kRowOut) {
+        // ga rows over the staged a, gb rows over b, in the staging layout of
+        // gc (block h of row r at slots 4h + (q ^ swz(h) ^ (r & 3))); then
+        // row-order stores
+        wave_lds_sync();
+        const unsigned a0 = lds_addr4(sa);
+        const unsigned rowb = a0 + ((unsigned)r << (N + 2));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const unsigned slot = ((h << 2) | ((unsigned)q ^ swz(h) ^ rs)) << 4;
+            if (WA) lds_st4(rowb + slot, make_float4(ya[4 * q], ya[4 * q + 1], ya[4 * q + 2], ya[4 * q + 3]));
+            if (WB) lds_st4(rowb + 4096u + slot, make_float4(yb[4 * q], yb[4 * q + 1], yb[4 * q + 2], yb[4 * q + 3]));
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const long long rr = grp * R + (long long)L.rr[i];
+            if (rr < P.batch) {
+                const long long at = (rr << (N - 2)) + (long long)L.ff[i];
+                if (WA) reinterpret_cast<float4*>(GA)[at] = lds_ld4(a0 + L.so[i]);
+                if (WB) reinterpret_cast<float4*>(GB)[at] = lds_ld4(a0 + 4096u + L.so[i]);
+            }
+        }
+    }
 }
 
 // ---- left and right contraction backward for 4 <= n <= 8 -----------------
