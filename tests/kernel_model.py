@@ -717,7 +717,7 @@ def contraction_frame_backward(op, a, b, gc, metric):
 
 
 def fwd7_step(h, t):
-    """Step t of lane h in prod_fwd_inner7 (n = 7): (output block o, partner S)
+    """Step t of lane h in prod_fwd_out7 (n = 7): (output block o, partner S)
     or None (idle). Lanes 3 and 7 finish their outputs early and then take
     partners 4, 5 and 6, 7 of output 0, whose lane adds their sums after the
     last step."""
