@@ -2184,10 +2184,13 @@ __device__ __forceinline__ float fwd7_merge(float x) {
 }
 
 template <int OP, bool LOWNEG>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void prod_fwd_out7(const float* __restrict__ A, const float* __restrict__ B,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OP == OP_WEDGE ? 3 : 4))) void prod_fwd_out7(const float* __restrict__ A, const float* __restrict__ B,
                                                      float* __restrict__ C, BlkParams P) {
-    static_assert(OP == OP_INNER || OP == OP_LC || OP == OP_RC, "lc and rc halves only");
-    constexpr bool kL = OP != OP_RC, kR = OP != OP_LC;  // the halves this op takes
+    static_assert(OP == OP_INNER || OP == OP_LC || OP == OP_RC || OP == OP_WEDGE, "lc and rc halves only");
+    // the halves this op takes; the wedge product runs the lc half's reads on
+    // complemented outputs (below)
+    constexpr bool kL = OP != OP_RC, kR = OP == OP_INNER || OP == OP_RC;
+    constexpr bool kW = OP == OP_WEDGE;
     constexpr int N = 7, R = 8, T = 4;
     constexpr unsigned full = 7u;
     __shared__ __attribute__((aligned(64))) float4 lds[4][2 * kBalGroupF4];  // a | b
@@ -2207,8 +2210,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
         const unsigned th = (unsigned)lane & full, trs = (unsigned)lane >> 3;
         for (int t = 0; t < T; ++t) {
             const FrameStep st = fwd7_step(th, t);
-            const unsigned S = st.p, So = st.p | st.o;
-            const HiSign hl = hi_sign<OP_INNER>(S, So, P.negh, P.nulh, full, P.nm1, P.mu);
+            // wedge: output ~o takes the pair (S, ~o ^ S) for every S inside ~o
+            const unsigned S = st.p, So = kW ? (full ^ st.o ^ S) : (st.p | st.o);
+            const HiSign hl = hi_sign<kW ? OP_WEDGE : OP_INNER>(S, So, P.negh, P.nulh, full, P.nm1, P.mu);
             const HiSign hr = hi_sign<OP_INNER>(So, S, P.negh, P.nulh, full, P.nm1, P.mu);
             const unsigned offs = ((S << 2) | (swz(S) ^ trs)) << 4;
             const unsigned offo = ((So << 2) | (swz(So) ^ trs)) << 4;
@@ -2273,9 +2277,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
                 bv2[4 * q] = v3.x; bv2[4 * q + 1] = v3.y; bv2[4 * q + 2] = v3.z; bv2[4 * q + 3] = v3.w;
             }
         }
-        if (kL) {  // lc half (S, S | o): cross parity |S|
+        if (kL) {  // lc half (S, S | o) or the wedge pair (S, ~o ^ S): cross parity |S|
             apply_flips(bv, hl, hlo);
-            lowblock_fwd<LV_LC, LOWNEG>(acc, av, bv);
+            lowblock_fwd<kW ? LV_WEDGE : LV_LC, LOWNEG>(acc, av, bv);
         }
         if (OP == OP_INNER) fwd7_diag<LOWNEG>(acc, av, bv, fac, std::make_integer_sequence<int, 16>{});
         if (kR) {  // rc half (S | o, S): cross parity |S | o|
@@ -2300,13 +2304,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
     };
     frame_steps(step, std::make_integer_sequence<int, T>{});
     if constexpr (!kRowOut) return;
-    // block h of row r over the staged a (slots 4h + (q ^ swz(h) ^ (r & 3))),
-    // then row-order stores
+    // output block ob of row r over the staged a (slots 4 ob + (q ^ swz(ob) ^
+    // (r & 3))), then row-order stores
     wave_lds_sync();
     const unsigned a0 = lds_addr4(sa);
+    const unsigned ob = kW ? full ^ h : h;
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-        lds_st4(a0 + ((unsigned)r << (N + 2)) + (((h << 2) | ((unsigned)q ^ swz(h) ^ rs)) << 4),
+        lds_st4(a0 + ((unsigned)r << (N + 2)) + (((ob << 2) | ((unsigned)q ^ swz(ob) ^ rs)) << 4),
                 make_float4(y[4 * q], y[4 * q + 1], y[4 * q + 2], y[4 * q + 3]));
     wave_lds_sync();
 #pragma unroll
@@ -2622,10 +2627,10 @@ static bool frame_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, 
     return true;
 }
 
-// the one-lane-per-output forward at n = 7: inner, lc and rc without a null
-// generator (blocked_metric: a uniform low metric)
+// the one-lane-per-output forward at n = 7: inner, lc, rc and wedge without a
+// null generator (blocked_metric: a uniform low metric for inner, lc and rc)
 static bool out7_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, bool& lowneg) {
-    if (n != 7 || nul != 0u || (op != OP_INNER && op != OP_LC && op != OP_RC)) return false;
+    if (n != 7 || nul != 0u || (op != OP_INNER && op != OP_LC && op != OP_RC && op != OP_WEDGE)) return false;
     if (options().product_path != PATH_DEFAULT) return false;
     if (!blocked_metric(op, n, neg, nul, lowneg)) return false;
     block_sign_params(n, neg, nul, P);
@@ -2816,7 +2821,8 @@ int product_fwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
     if (out7_plan(op, n, neg, nul, P, ln)) {
         if (op == OP_INNER) launch_out7<OP_INNER>(s, ln, a, b, c, P);
         else if (op == OP_LC) launch_out7<OP_LC>(s, ln, a, b, c, P);
-        else launch_out7<OP_RC>(s, ln, a, b, c, P);
+        else if (op == OP_RC) launch_out7<OP_RC>(s, ln, a, b, c, P);
+        else launch_out7<OP_WEDGE>(s, ln, a, b, c, P);
     } else if (!force_generic && bal_plan(op, n, neg, nul, true, P, ln)) {
 #define CLF_FWD_BAL(OPV)                                               \
     case OPV:                                                          \

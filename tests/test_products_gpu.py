@@ -438,11 +438,12 @@ def test_inner_frame_kernels_match_oracle_and_blocked(metric, clf_env):
 
 @pytest.mark.parametrize("metric", [m for m in FRAME_METRICS if len(m) == 7],
                          ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
-@pytest.mark.parametrize("op", ["inner", "lc", "rc"])
+@pytest.mark.parametrize("op", ["inner", "lc", "rc", "wedge"])
 def test_out7_forward_matches_oracle_and_blocked(op, metric, clf_env):
     """The n = 7 one-lane-per-output forward (inner: both halves, lc and rc:
-    one half each) against the fp64 oracle on batches that end inside a group
-    of eight rows, and equal to the blocked kernel within rounding."""
+    one half each, wedge: the lc half's schedule on complemented outputs)
+    against the fp64 oracle on batches that end inside a group of eight rows,
+    and equal to the blocked kernel within rounding."""
     from cliffordcuda_amd import products
     n = 7
     for batch in (1, 7, 29, 4 * 64 * 8 + 7):
