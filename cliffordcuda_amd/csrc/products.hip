@@ -1950,17 +1950,38 @@ __device__ __forceinline__ float contr_out_sup(const float (&x)[16], int k) {
     return GBK && rho4(k) ? -x[k] : x[k];
 }
 
+// disjoint pattern of the wedge product: acc[o] += s_w(o, q) w[q] g[o | q]
+template <int... Is>
+__device__ __forceinline__ void frame_disjoint(float (&acc)[16], const float (&w)[16], const float (&g)[16],
+                                               std::integer_sequence<int, Is...>) {
+    auto term = [&](auto oq) {
+        constexpr int O = decltype(oq)::value >> 4, Q = decltype(oq)::value & 15;
+        if constexpr ((O & Q) == 0) {
+            constexpr int sw = low_sign(LV_WEDGE, false, (unsigned)O, (unsigned)Q);
+            acc[O] = __builtin_fmaf(sw > 0 ? w[fr_reg(Q)] : -w[fr_reg(Q)], g[O ^ Q], acc[O]);
+        }
+    };
+    (term(std::integral_constant<int, Is>{}), ...);
+}
+
+// The wedge product on the same schedule: lane h takes ga[h] over its sup
+// steps (partner b[p ^ h], gc block p) and gb[~h] over its sub steps
+// (partner a[p], gc block ~h ^ p); both run the disjoint pattern, a gb step
+// through s_w(q, o) = s_w(o, q) rho(o) rho(q) rho(o | q) (o, q disjoint, from
+// C(|o| + |q|, 2) = C(|o|, 2) + C(|q|, 2) + |o||q|), and no block is read
+// reversed.
 template <int OP, int N, bool LOWNEG>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void prod_bwd_contr_frame(
     const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ GC, float* __restrict__ GA,
     float* __restrict__ GB, BlkParams P) {
-    static_assert(OP == OP_LC || OP == OP_RC, "contractions only");
+    static_assert(OP == OP_LC || OP == OP_RC || OP == OP_WEDGE, "contractions and the wedge product only");
     constexpr int NH = N - 4, NB = 1 << NH, R = 64 >> NH;
     using Sch = FrameSched<NH>;
     using Cs = ContrSched<NH>;
     constexpr int T = Sch::T;
     constexpr unsigned full = NB - 1u;
-    constexpr bool kLC = OP == OP_LC;  // sub steps yield gb (lc) or ga (rc)
+    constexpr bool kW = OP == OP_WEDGE;
+    constexpr bool kLC = OP != OP_RC;  // sub steps yield gb (lc, wedge) or ga (rc)
     __shared__ __attribute__((aligned(64))) float4 lds[4][3 * kBalGroupF4];  // a | b | gc
     // the steps of lane (h, row slot skew rs): tab[t][rs * NB + h]
     __shared__ unsigned tab[T][4 * NB];
@@ -1986,17 +2007,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
         const unsigned th = (unsigned)lane & full, trs = (unsigned)lane >> NH;
         for (int t = 0; t < T; ++t) {
             const FrameStep st = frame_step<NH>(th, t);
-            const unsigned X = st.o ^ st.p;
             const bool gbs = kLC ? st.sub : !st.sub;
-            const HiSign hs = gbs ? hi_sign<OP_INNER>(st.p, st.o, P.negh, P.nulh, full, P.nm1, P.mu)
-                                  : hi_sign<OP_INNER>(st.o, st.p, P.negh, P.nulh, full, P.nm1, P.mu);
             const unsigned podd = (unsigned)__popc(st.p) & 1u, oodd = (unsigned)__popc(st.o) & 1u;
             const unsigned sub = st.sub ? 1u : 0u, gb = gbs ? 1u : 0u;
+            unsigned X, wb, pm, cw;
+            HiSign hs;
+            if (kW) {  // gb[~o]: (ih, jh) = (p, ~o), gc block p | ~o; ga[o]: (o, p ^ o), gc block p
+                X = gbs ? (full ^ st.o ^ st.p) : st.p;
+                wb = gbs ? st.p : (st.p ^ st.o);
+                hs = gbs ? hi_sign<OP_WEDGE>(st.p, full ^ st.o, P.negh, P.nulh, full, P.nm1, P.mu)
+                         : hi_sign<OP_WEDGE>(st.o, st.p ^ st.o, P.negh, P.nulh, full, P.nm1, P.mu);
+                pm = gb ? podd : oodd;
+                cw = 0u;
+            } else {
+                X = st.o ^ st.p;
+                wb = st.p;
+                hs = gbs ? hi_sign<OP_INNER>(st.p, st.o, P.negh, P.nulh, full, P.nm1, P.mu)
+                         : hi_sign<OP_INNER>(st.o, st.p, P.negh, P.nulh, full, P.nm1, P.mu);
+                pm = (gb ? podd : oodd) ^ (LOWNEG ? sub : 0u);
+                cw = sub;
+            }
             const unsigned offg = ((X << 2) | (swz(X) ^ trs)) << 4;
-            const unsigned offw = (((st.p << 2) | (swz(st.p) ^ trs ^ (st.sub ? 3u : 0u))) << 4) + (gbs ? 0u : 4096u);
-            const unsigned pm = (gb ? podd : oodd) ^ (LOWNEG ? sub : 0u);
-            tab[t][lane] = offg | (offw << 10) | ((hs.mask >> 31) << 23) | (pm << 24) | ((gb & sub) << 25) |
-                           (((gb ^ 1u) & sub) << 26) | (gb << 27) | ((gb & podd) << 28);
+            const unsigned offw = (((wb << 2) | (swz(wb) ^ trs ^ (cw ? 3u : 0u))) << 4) + (gbs ? 0u : 4096u);
+            tab[t][lane] = offg | (offw << 10) | ((hs.mask >> 31) << 23) | (pm << 24) | ((gb & cw) << 25) |
+                           (((gb ^ 1u) & cw) << 26) | (gb << 27) | ((gb & podd) << 28);
         }
     }
     __syncthreads();
@@ -2070,7 +2104,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
             w[fr_reg(el)] = __uint_as_float(wcl == 0 ? u ^ xa : u ^ xa ^ (wcl == 1 ? m1 : wcl == 2 ? m2 : y3));
             if (par4(el) || rho4(el)) g[el] = flip(g[el], par4(el) && rho4(el) ? gpr : par4(el) ? mg : mr);
         }
-        frame_sup<LOWNEG, true, false>(acc, acc, w, w, g, g, std::make_integer_sequence<int, 256>{});
+        if constexpr (kW) frame_disjoint(acc, w, g, std::make_integer_sequence<int, 256>{});
+        else frame_sup<LOWNEG, true, false>(acc, acc, w, w, g, g, std::make_integer_sequence<int, 256>{});
         if constexpr (Sch::kHelp && t == T - 1) {  // outputs 0 and full add their helpers' sums
 #pragma unroll
             for (int el = 0; el < 16; ++el) {
@@ -2084,7 +2119,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
             const bool sub = first == first_sub;  // the mode of the output completed here
 #pragma unroll
             for (int k = 0; k < 16; ++k) {
-                const float ys = contr_out_sub<LOWNEG, kLC>(acc, k);
+                // the wedge product's sub-mode output is gb[~h] in the normal frame
+                const float ys = kW ? contr_out_sup<true>(acc, k) : contr_out_sub<LOWNEG, kLC>(acc, k);
                 const float yp = contr_out_sup<!kLC>(acc, k);
                 const float y = K == 1 ? ys : K == 2 ? yp : (sub ? ys : yp);
                 if constexpr (Cs::any_first(t)) y1[k] = first ? y : y1[k];
@@ -2109,11 +2145,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
         const bool first_gb = first_sub == kLC;  // the first mode's output is a gb block
         const unsigned rowb = lds_addr4(sa) + ((unsigned)r << (N + 2));
         const unsigned o1 = rowb + (first_gb ? 4096u : 0u), o2 = rowb + (first_gb ? 0u : 4096u);
+        // output blocks: ga h; gb h (contractions) or ~h (wedge)
+        const unsigned b1 = kW && first_gb ? full ^ h : h, b2 = kW && !first_gb ? full ^ h : h;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const unsigned slot = (((h << 2) | ((unsigned)q ^ swz(h) ^ rs)) << 4);
-            lds_st4(o1 + slot, make_float4(y1[4 * q], y1[4 * q + 1], y1[4 * q + 2], y1[4 * q + 3]));
-            lds_st4(o2 + slot, make_float4(y2[4 * q], y2[4 * q + 1], y2[4 * q + 2], y2[4 * q + 3]));
+            const unsigned s1 = ((b1 << 2) | ((unsigned)q ^ swz(b1) ^ rs)) << 4;
+            const unsigned s2 = ((b2 << 2) | ((unsigned)q ^ swz(b2) ^ rs)) << 4;
+            lds_st4(o1 + s1, make_float4(y1[4 * q], y1[4 * q + 1], y1[4 * q + 2], y1[4 * q + 3]));
+            lds_st4(o2 + s2, make_float4(y2[4 * q], y2[4 * q + 1], y2[4 * q + 2], y2[4 * q + 3]));
         }
     }
     wave_lds_sync();
@@ -2698,7 +2737,7 @@ static void launch_frame(int n, bool ln, hipStream_t s, const float* A, const fl
 // The contractions' backward on the frame schedule: lc and rc for
 // 4 <= n <= 8 without a null generator and with a uniform low metric.
 static bool contr_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, bool& lowneg) {
-    if ((op != OP_LC && op != OP_RC) || n < kFrameMinN || n > kFrameMaxN || nul != 0u) return false;
+    if ((op != OP_LC && op != OP_RC && op != OP_WEDGE) || n < kFrameMinN || n > kFrameMaxN || nul != 0u) return false;
     if (options().product_path != PATH_DEFAULT) return false;
     if (!blocked_metric(op, n, neg, nul, lowneg)) return false;
     block_sign_params(n, neg, nul, P);
@@ -2901,7 +2940,8 @@ int product_bwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
         launch_frame(n, ln, s, a, b, gc, ga, gb, P);
     } else if (contr_plan(op, n, neg, nul, P, ln)) {
         if (op == OP_LC) launch_contr<OP_LC>(n, ln, s, a, b, gc, ga, gb, P);
-        else launch_contr<OP_RC>(n, ln, s, a, b, gc, ga, gb, P);
+        else if (op == OP_RC) launch_contr<OP_RC>(n, ln, s, a, b, gc, ga, gb, P);
+        else launch_contr<OP_WEDGE>(n, false, s, a, b, gc, ga, gb, P);
     } else if (!force_generic && bal_plan(op, n, neg, nul, false, P, ln)) {
 #define CLF_BWD_BAL(OPV)                                                       \
     case OPV:                                                                  \

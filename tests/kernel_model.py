@@ -716,6 +716,77 @@ def contraction_frame_backward(op, a, b, gc, metric):
     return ga, gb
 
 
+def wedge_frame_backward(a, b, gc, metric):
+    """The wedge product's backward as prod_bwd_contr_frame<WEDGE> computes it
+    on the frame schedule: lane h takes ga[h] over its sup steps (partner
+    b[p ^ h], gc block p) and gb[~h] over its sub steps (partner a[p], gc
+    block ~h ^ p), both on the disjoint pattern acc[o] += s_w(o, q) w[q]
+    g[o | q]; a gb step uses s_w(q, o) = s_w(o, q) rho(o) rho(q) rho(o | q)
+    (o, q disjoint). No partner block is read reversed. Returns (ga, gb)."""
+    n = len(metric)
+    nh = n - 4
+    NB = 1 << nh
+    full = NB - 1
+    help_ = nh in FRAME_HELP
+    T = frame_steps_count(nh)
+    h0, hf, c = (FRAME_HELP[nh][1][0], FRAME_HELP[nh][1][1], FRAME_HELP[nh][2]) if help_ else ((), (), 0)
+    rows = a.shape[:-1]
+    acc = [np.zeros(rows + (16,)) for _ in range(NB)]
+    ga = np.zeros(a.shape)
+    gb = np.zeros(b.shape)
+    rho = np.array([_rho(k) for k in range(16)])
+
+    def put(h, x, sub):
+        if sub:
+            gb[..., (full ^ h) * 16:((full ^ h) + 1) * 16] = x * rho
+        else:
+            ga[..., h * 16:(h + 1) * 16] = x
+
+    for t in range(T):
+        for h in range(NB):
+            o, p, sub = frame_step(nh, h, t)
+            if sub:   # gb[~o]: ih = p, jh = ~o
+                jh = full ^ o
+                X = p | jh
+                _, s = hi_sign(WEDGE, p, jh, 0, 0, full, 0, 0)
+                cm = popc(p) & 1
+                w = [s * (-1 if (popc(q) & 1 and cm) else 1) * _rho(q) * a[..., p * 16 + q] for q in range(16)]
+                g = gc[..., X * 16:(X + 1) * 16]
+                gg = [g[..., x] * (-1.0 if (popc(x) & 1 and cm) else 1.0) * _rho(x) for x in range(16)]
+            else:     # ga[o]: ih = o, jh = p ^ o
+                jh = p ^ o
+                _, s = hi_sign(WEDGE, o, jh, 0, 0, full, 0, 0)
+                cm = popc(o) & 1
+                w = [s * (-1 if (popc(q) & 1 and cm) else 1) * b[..., jh * 16 + q] for q in range(16)]
+                g = gc[..., p * 16:(p + 1) * 16]
+                gg = [g[..., x] for x in range(16)]
+            for oo in range(16):
+                for q in range(16):
+                    if oo & q:
+                        continue
+                    acc[h][..., oo] += low_sign(WEDGE, False, oo, q) * w[q] * gg[oo | q]
+        for h in range(NB):
+            o, p, sub = frame_step(nh, h, t)
+            edge = help_ and h in (0, full)
+            if edge:
+                if t == 0:
+                    put(h, acc[h], sub)
+                    acc[h] = np.zeros(rows + (16,))
+                elif t == T - 1:
+                    put(h, acc[h] + sum(acc[x] for x in (h0 if h == 0 else hf)), sub)
+                continue
+            cs = 1 << popc(h)
+            end = cs + (1 << (nh - popc(h))) - 1
+            if t == cs - 1:
+                put(h, acc[h], True)
+                acc[h] = np.zeros(rows + (16,))
+            if t == end:
+                put(h, acc[h], False)
+            if help_ and t == T - c - 1 and h in h0 + hf:
+                acc[h] = np.zeros(rows + (16,))
+    return ga, gb
+
+
 def fwd7_step(h, t):
     """Step t of lane h in prod_fwd_out7 (n = 7): (output block o, partner S)
     or None (idle). Lanes 3 and 7 finish their outputs early and then take

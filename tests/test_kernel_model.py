@@ -194,6 +194,23 @@ def test_contraction_frame_backward(op, metric):
     np.testing.assert_allclose(gb, bt.grad.numpy(), atol=1e-10)
 
 
+@pytest.mark.parametrize("metric", [(1,) * 4, (-1,) * 5, (1,) * 6 + (-1,), (1, 1, 1, 1, -1, 1, -1), (1,) * 8],
+                         ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
+def test_wedge_frame_backward(metric):
+    """The wedge product's backward on the frame schedule (ga[h] over the sup
+    steps, gb[~h] over the sub steps, one disjoint pattern with the
+    reversion-sign factorisation for gb) gives the oracle's gradients."""
+    n = len(metric)
+    rng = np.random.default_rng(n + 13)
+    a, b, gc = (rng.standard_normal((2, 1 << n)) for _ in range(3))
+    at = torch.tensor(a, requires_grad=True)
+    bt = torch.tensor(b, requires_grad=True)
+    O.einsum_product("wedge", at, bt, list(metric)).backward(torch.tensor(gc))
+    ga, gb = K.wedge_frame_backward(a, b, gc, list(metric))
+    np.testing.assert_allclose(ga, at.grad.numpy(), atol=1e-10)
+    np.testing.assert_allclose(gb, bt.grad.numpy(), atol=1e-10)
+
+
 def test_reversion_sign_factorisation():
     """s_rc(q, o) = s_lc(o, q) rho(o) rho(q) rho(o ^ q) for every o inside q
     of a 4-bit low block, either low metric: the identity that lets one sign
@@ -206,6 +223,12 @@ def test_reversion_sign_factorisation():
                 lhs = K.low_sign(K.RC, lowneg, q, o)
                 rhs = K.low_sign(K.LC, lowneg, o, q) * K._rho(o) * K._rho(q) * K._rho(o ^ q)
                 assert lhs == rhs, (lowneg, o, q)
+    for o in range(16):  # the wedge product's disjoint pairs
+        for q in range(16):
+            if o & q:
+                continue
+            lhs = K.low_sign(K.WEDGE, False, q, o)
+            assert lhs == K.low_sign(K.WEDGE, False, o, q) * K._rho(o) * K._rho(q) * K._rho(o | q), (o, q)
 
 
 def test_inner_frame_schedule_covers_every_pair():

@@ -459,10 +459,11 @@ def test_out7_forward_matches_oracle_and_blocked(op, metric, clf_env):
 
 
 @pytest.mark.parametrize("metric", FRAME_METRICS, ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
-@pytest.mark.parametrize("op", ["lc", "rc"])
+@pytest.mark.parametrize("op", ["lc", "rc", "wedge"])
 def test_contraction_frame_backward_matches_oracle_and_blocked(op, metric, clf_env):
-    """The contractions' backward on the frame schedule (4 <= n <= 8, one
-    accumulator per lane, a store at each mode's end): each gradient alone and
+    """The contractions' and the wedge product's backward on the frame schedule
+    (4 <= n <= 8, one accumulator per lane, a store at each mode's end): each
+    gradient alone and
     both against the fp64 oracle, batches that end inside a group of rows (and
     a single row), each alone bitwise equal to both, and equal to the blocked
     kernels (CLF_PRODUCT_PATH=blocked) within rounding."""
