@@ -2223,13 +2223,15 @@ __device__ __forceinline__ float fwd7_merge(float x) {
 }
 
 template <int OP, bool LOWNEG>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OP == OP_WEDGE ? 3 : 4))) void prod_fwd_out7(const float* __restrict__ A, const float* __restrict__ B,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OP == OP_WEDGE || OP == OP_REGR ? 3 : 4))) void prod_fwd_out7(const float* __restrict__ A, const float* __restrict__ B,
                                                      float* __restrict__ C, BlkParams P) {
-    static_assert(OP == OP_INNER || OP == OP_LC || OP == OP_RC || OP == OP_WEDGE, "lc and rc halves only");
+    static_assert(OP == OP_INNER || OP == OP_LC || OP == OP_RC || OP == OP_WEDGE || OP == OP_REGR,
+                  "lc and rc halves only");
     // the halves this op takes; the wedge product runs the lc half's reads on
     // complemented outputs (below)
     constexpr bool kL = OP != OP_RC, kR = OP == OP_INNER || OP == OP_RC;
-    constexpr bool kW = OP == OP_WEDGE;
+    constexpr bool kW = OP == OP_WEDGE || OP == OP_REGR;
+    constexpr bool kRg = OP == OP_REGR;
     constexpr int N = 7, R = 8, T = 4;
     constexpr unsigned full = 7u;
     __shared__ __attribute__((aligned(64))) float4 lds[4][2 * kBalGroupF4];  // a | b
@@ -2249,14 +2251,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OP == OP_WE
         const unsigned th = (unsigned)lane & full, trs = (unsigned)lane >> 3;
         for (int t = 0; t < T; ++t) {
             const FrameStep st = fwd7_step(th, t);
-            // wedge: output ~o takes the pair (S, ~o ^ S) for every S inside ~o
-            const unsigned S = st.p, So = kW ? (full ^ st.o ^ S) : (st.p | st.o);
-            const HiSign hl = hi_sign<kW ? OP_WEDGE : OP_INNER>(S, So, P.negh, P.nulh, full, P.nm1, P.mu);
+            // wedge: output ~o takes the pair (S, ~o ^ S) for every S inside ~o;
+            // regressive: the pair (o | S, ~S) of xor index ~o, stored reversed
+            // at block o
+            const unsigned S = kRg ? (st.o | st.p) : st.p;
+            const unsigned So = kRg ? (full ^ st.p) : kW ? (full ^ st.o ^ S) : (st.p | st.o);
+            const HiSign hl = hi_sign<kRg ? OP_REGR : kW ? OP_WEDGE : OP_INNER>(S, So, P.negh, P.nulh, full, P.nm1,
+                                                                                 P.mu);
             const HiSign hr = hi_sign<OP_INNER>(So, S, P.negh, P.nulh, full, P.nm1, P.mu);
             const unsigned offs = ((S << 2) | (swz(S) ^ trs)) << 4;
             const unsigned offo = ((So << 2) | (swz(So) ^ trs)) << 4;
             tab[t][lane] = offs | (offo << 10) | ((hl.mask >> 31) << 20) | ((hr.mask >> 31) << 21) |
-                           (((unsigned)__popc(S) & 1u) << 22) | (((unsigned)__popc(So) & 1u) << 23) |
+                           ((cross_pi<kRg ? OP_REGR : OP_WEDGE>(S, P.nm1) & 1u) << 22) |
+                           (((unsigned)__popc(So) & 1u) << 23) |
                            ((st.o == 0u ? 1u : 0u) << 24);
         }
     }
@@ -2318,7 +2325,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OP == OP_WE
         }
         if (kL) {  // lc half (S, S | o) or the wedge pair (S, ~o ^ S): cross parity |S|
             apply_flips(bv, hl, hlo);
-            lowblock_fwd<kW ? LV_WEDGE : LV_LC, LOWNEG>(acc, av, bv);
+            lowblock_fwd<kRg ? LV_REGR : kW ? LV_WEDGE : LV_LC, LOWNEG>(acc, av, bv);
         }
         if (OP == OP_INNER) fwd7_diag<LOWNEG>(acc, av, bv, fac, std::make_integer_sequence<int, 16>{});
         if (kR) {  // rc half (S | o, S): cross parity |S | o|
@@ -2347,11 +2354,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OP == OP_WE
     // (r & 3))), then row-order stores
     wave_lds_sync();
     const unsigned a0 = lds_addr4(sa);
-    const unsigned ob = kW ? full ^ h : h;
+    const unsigned ob = kW && !kRg ? full ^ h : h;
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-        lds_st4(a0 + ((unsigned)r << (N + 2)) + (((ob << 2) | ((unsigned)q ^ swz(ob) ^ rs)) << 4),
-                make_float4(y[4 * q], y[4 * q + 1], y[4 * q + 2], y[4 * q + 3]));
+    for (int q = 0; q < 4; ++q) {
+        const unsigned at = a0 + ((unsigned)r << (N + 2)) + (((ob << 2) | ((unsigned)q ^ swz(ob) ^ rs)) << 4);
+        if (kRg)  // the regressive output block is the xor product's block reversed
+            lds_st4(at, make_float4(y[15 - 4 * q], y[14 - 4 * q], y[13 - 4 * q], y[12 - 4 * q]));
+        else lds_st4(at, make_float4(y[4 * q], y[4 * q + 1], y[4 * q + 2], y[4 * q + 3]));
+    }
     wave_lds_sync();
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -2669,7 +2679,8 @@ static bool frame_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, 
 // the one-lane-per-output forward at n = 7: inner, lc, rc and wedge without a
 // null generator (blocked_metric: a uniform low metric for inner, lc and rc)
 static bool out7_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, bool& lowneg) {
-    if (n != 7 || nul != 0u || (op != OP_INNER && op != OP_LC && op != OP_RC && op != OP_WEDGE)) return false;
+    if (n != 7 || nul != 0u || (op != OP_INNER && op != OP_LC && op != OP_RC && op != OP_WEDGE && op != OP_REGR))
+        return false;
     if (options().product_path != PATH_DEFAULT) return false;
     if (!blocked_metric(op, n, neg, nul, lowneg)) return false;
     block_sign_params(n, neg, nul, P);
@@ -2861,7 +2872,8 @@ int product_fwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
         if (op == OP_INNER) launch_out7<OP_INNER>(s, ln, a, b, c, P);
         else if (op == OP_LC) launch_out7<OP_LC>(s, ln, a, b, c, P);
         else if (op == OP_RC) launch_out7<OP_RC>(s, ln, a, b, c, P);
-        else launch_out7<OP_WEDGE>(s, ln, a, b, c, P);
+        else if (op == OP_WEDGE) launch_out7<OP_WEDGE>(s, ln, a, b, c, P);
+        else launch_out7<OP_REGR>(s, ln, a, b, c, P);
     } else if (!force_generic && bal_plan(op, n, neg, nul, true, P, ln)) {
 #define CLF_FWD_BAL(OPV)                                               \
     case OPV:                                                          \

@@ -438,7 +438,7 @@ def test_inner_frame_kernels_match_oracle_and_blocked(metric, clf_env):
 
 @pytest.mark.parametrize("metric", [m for m in FRAME_METRICS if len(m) == 7],
                          ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
-@pytest.mark.parametrize("op", ["inner", "lc", "rc", "wedge"])
+@pytest.mark.parametrize("op", ["inner", "lc", "rc", "wedge", "regressive"])
 def test_out7_forward_matches_oracle_and_blocked(op, metric, clf_env):
     """The n = 7 one-lane-per-output forward (inner: both halves, lc and rc:
     one half each, wedge: the lc half's schedule on complemented outputs)
