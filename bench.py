@@ -48,7 +48,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=100)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--workload", default="headline", choices=["headline", "c1", "c2", "c3", "c4", "c5", "all", "copycal"])
+    p.add_argument("--workload", default="headline",
+                   choices=["headline", "c1", "c2", "c3", "c4", "c5", "all", "copycal", "published"])
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
     return p.parse_args()
@@ -145,9 +146,62 @@ def cpu_product(op, metric, rows, fwd_only, budget_s):
     return cpu_rate(work, rows, budget_s, f"{op} {'fwd' if fwd_only else 'fwd+bwd'} {metric}")
 
 
+class Clock:
+    """Mean engine clock over a stretch of GPU work: clf_clock_sample launches
+    one-wave workgroups that read the shader-clock counter (s_memtime) and the
+    constant-rate counter (s_memrealtime) with their XCD index; a sample on the
+    launch stream before the work and one after give, per XCD, cycles over
+    real time."""
+
+    SLOTS = 64
+
+    def __init__(self, torch, lib, stream):
+        from cliffordcuda_amd import _lib
+        self.torch, self.lib, self.stream = torch, lib, stream
+        info = _lib.device_info(0)
+        self.info = info
+        self.buf = torch.zeros(2, 3 * self.SLOTS, dtype=torch.int64, device="cuda")
+
+    def sample(self, k):
+        from cliffordcuda_amd import _lib
+        _lib.check(self.lib.clf_clock_sample(self.buf[k].data_ptr(), self.SLOTS, self.stream.cuda_stream),
+                   "clf_clock_sample")
+
+    def ghz(self):
+        """Median over XCDs of the mean clock between the two samples (None if
+        the counters do not give a plausible value)."""
+        h = self.buf.cpu().view(2, self.SLOTS, 3).tolist()
+        per_xcd = {}
+        for k in range(2):
+            for xcc, cyc, rt in h[k]:
+                d = per_xcd.setdefault(xcc, [[None, None], [None, None]])
+                if d[k][0] is None or cyc < d[k][0]:
+                    d[k] = [cyc, rt]
+        rate = self.info.wall_clock_khz * 1e3
+        vals = []
+        for xcc, ((c0, r0), (c1, r1)) in per_xcd.items():
+            if None in (c0, c1) or r1 <= r0 or rate <= 0:
+                continue
+            vals.append((c1 - c0) / ((r1 - r0) / rate) / 1e9)
+        vals.sort()
+        if not vals or not 0.3 < vals[len(vals) // 2] < 4.0:
+            return None, vals
+        return vals[len(vals) // 2], vals
+
+    def device(self, ghz, vals, what):
+        return {"compute_units": self.info.compute_units, "max_engine_clock_mhz": self.info.clock_khz / 1e3,
+                "measured_engine_clock_ghz": ghz,
+                "measured_engine_clock_ghz_per_xcd": [round(v, 3) for v in vals],
+                "clock_method": f"clf_clock_sample before and after {what} on its stream: shader-clock cycles "
+                                f"(s_memtime) over real time (s_memrealtime, {self.info.wall_clock_khz} kHz), "
+                                f"per XCD, median"}
+
+
 class Timer:
     def __init__(self, torch, stream, reps):
         self.torch, self.stream, self.reps = torch, stream, reps
+        self.clock = None
+        self.last_clock = (None, [])
 
     def kernel_ms(self, fn):
         """Average duration of fn() over `reps` back-to-back calls, HIP events on the launch stream,
@@ -164,11 +218,17 @@ class Timer:
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
+        if self.clock is not None:
+            self.clock.sample(0)
         e0.record(self.stream)
         for _ in range(self.reps):
             fn()
         e1.record(self.stream)
+        if self.clock is not None:
+            self.clock.sample(1)
         e1.synchronize()
+        if self.clock is not None:
+            self.last_clock = self.clock.ghz()
         return e0.elapsed_time(e1) / self.reps
 
     def step_ms(self, fn, warmup, steps):
@@ -229,6 +289,7 @@ def headline(args, torch, cc, lib, T):
     # runs the matrix-representation kernels (rep16_fwd_kernel / rep16_bwd_kernel)
     fwd_ms = T.kernel_ms(fwd)
     bwd_ms = T.kernel_ms(bwd)
+    bwd_clock = T.last_clock
     # the per-term kernels (the path of every other signature and product),
     # forced for comparison at the same shape
     with path_switch("CLF_GEOM_PATH", "direct"):
@@ -258,7 +319,8 @@ def headline(args, torch, cc, lib, T):
         "roofline": {"bound": "hbm", "kernel": "rep16_bwd_kernel", "achieved": achieved,
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
                      "traffic": load_traffic().get("rep16_bwd_kernel Cl(8,0) B=262144"),
-                     "kernel_ms": bwd_ms, "algorithmic_bytes_per_launch": bwd_bytes},
+                     "kernel_ms": bwd_ms, "algorithmic_bytes_per_launch": bwd_bytes,
+                     "device": T.clock.device(*bwd_clock, "the rep16_bwd_kernel timing loop") if T.clock else None},
         "kernels": {
             "rep16_fwd_kernel": {"ms": fwd_ms, "gbs": fwd_bytes / (fwd_ms * 1e-3) / 1e9,
                                  "hbm_frac": fwd_bytes / (fwd_ms * 1e-3) / 1e9 / PEAK_HBM_GBS},
@@ -271,13 +333,11 @@ def headline(args, torch, cc, lib, T):
                 "ms": dbwd_ms, "tflops": bwd_flops / (dbwd_ms * 1e-3) / 1e12,
                 "valu_frac": bwd_flops / (dbwd_ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS},
         },
-        # the reference's flop count (4^n multiply-adds per product) over the
-        # step time: an equivalent rate for comparison with the per-term
-        # formulation, not a utilisation -- the matrix path does 16^3
-        # multiply-adds per product on the matrix cores
-        "reference_equivalent": {
-            "tflops": (fwd_flops + bwd_flops) / (ms * 1e-3) / 1e12,
-            "frac_of_fp32_peak": (fwd_flops + bwd_flops) / (ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS},
+        # the reference's term count (4^n multiply-adds per product, 3 products
+        # per step) over the step time: how fast the per-term formulation would
+        # have to run to match this step. Not a utilisation: the matrix path does
+        # 16^3 multiply-adds per product on the matrix cores.
+        "term_count_equivalent_tflops": (fwd_flops + bwd_flops) / (ms * 1e-3) / 1e12,
         "cpu_baseline": None if args.no_cpu else cpu_baseline(n, args.cpu_seconds),
     }
 
@@ -388,12 +448,138 @@ def c3_layer(args, torch, cc, lib, T):
             "bcast_bwd_frac_hbm": bwd_bytes / (bms * 1e-3) / 1e9 / PEAK_HBM_GBS,
             # the dense-contraction count (2 D^2 flops per row forward, 4 D^2
             # backward) over the step: an equivalent rate, not a utilisation
-            "reference_equivalent_tflops": flops / (ms * 1e-3) / 1e12,
+            "dense_contraction_equivalent_tflops": flops / (ms * 1e-3) / 1e12,
             "gemm_path": {"fwd_ms": gfms, "bwd_ms": gbms,
                           "fwd_frac_mfma": 2.0 * D * D * B / (gfms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS,
                           "bwd_frac_mfma": 4.0 * D * D * B / (gbms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS,
                           "frac_mfma": 6.0 * D * D * B / ((gfms + gbms) * 1e-3) / 1e12 / PEAK_FP32_TFLOPS},
             "hbm_gbs_algorithmic": byts / (ms * 1e-3) / 1e9, "cpu_baseline": None}
+
+
+# The reference's published table (NVIDIA A100, figures/tables.md:6-54; the
+# minimum over its kernel variants per cell), for context beside the MI355X
+# numbers measured the same way: {op: {n: us}} at batch 64, and the geometric
+# product at batch 1 and 16.
+A100_US = {
+    "fwd": {64: {"geom": [17.3, 21.0, 34.3, 79.8, 254.9, 970.7], "wedge": [14.5, 18.0, 24.1, 41.3, 90.6, 245.5],
+                 "inner": [14.7, 18.2, 24.4, 44.1, 104.8, 286.9], "lc": [14.2, 17.2, 22.0, 36.8, 79.5, 228.3],
+                 "rc": [14.1, 18.7, 21.6, 36.6, 81.2, 225.9],
+                 "regressive": [23.9, 28.3, 38.1, 72.0, 163.8, 275.6],
+                 "rotor_apply": [24.8, 28.9, 34.6, 45.0, 49.3, 102.9]},
+            1: {"geom": [15.5, 15.7, 16.1, 19.6, 31.8, 55.8]}, 16: {"geom": [16.0, 17.1, 20.7, 32.2, 74.1, 242.1]}},
+    "bwd": {64: {"geom": [71.4, 72.3, 81.4, 159.7, 528.8, 1983.6], "wedge": [79.0, 82.1, 85.1, 137.2, 371.9, 1331.2],
+                 "inner": [78.9, 77.7, 89.9, 178.6, 466.2, 1638.8], "lc": [77.1, 78.9, 84.9, 143.7, 403.1, 1334.3],
+                 "rc": [78.1, 53.7, 83.2, 143.5, 401.9, 1330.8],
+                 "regressive": [89.1, 89.1, 93.8, 166.9, 429.3, 1374.7]},
+            1: {"geom": [72.5, 72.0, 72.5, 72.9, 69.7, 132.5]}, 16: {"geom": [72.0, 71.5, 72.1, 81.0, 153.9, 514.5]}},
+}
+
+
+def published(args, torch, cc, lib, T):
+    """The reference's published latency table, measured the way its harness
+    does (benchmark/_harness.py:41-50,98-145): Cl(n,0), n = 7..12, batch 1, 16,
+    64, a, b ~ N(0,1) on the GPU; the clock warmed with 2 s of matmuls; every
+    call synchronised before and after and timed with the wall clock; 25
+    untimed calls, then the median over 10 trials of the mean of 10 calls.
+    Forward rows time the product call; backward rows build the forward graph
+    outside the timer and time torch.autograd.grad(c, (a, b), gc) with a seeded
+    N(0,1) gc (bench_geom_prod_bwd.py); the rotor row times apply_rotor(cs, x)
+    with cs compiled outside the timer (bench_rotor_apply.py). Each cell also
+    carries the device time of the same call (HIP events over 100 back-to-back
+    calls)."""
+    import statistics
+    dev = torch.device("cuda", 0)
+    a0 = torch.randn(4096, 4096, device=dev)
+    b0 = torch.randn(4096, 4096, device=dev)
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 2.0:
+        a0 = a0 @ b0
+    torch.cuda.synchronize()
+    del a0, b0
+
+    def harness_us(time_one, warmup=25, iters=10, trials=10):
+        for _ in range(warmup):
+            time_one()
+        ts = []
+        for _ in range(trials):
+            acc = 0.0
+            for _ in range(iters):
+                acc += time_one()
+            ts.append(acc / iters * 1e6)
+        return statistics.median(ts)
+
+    def sync_timed(fn):
+        def one():
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            return time.perf_counter() - t
+        return one
+
+    def bwd_timed(fwd, inputs, gc):
+        def one():
+            torch.cuda.synchronize()
+            c = fwd()
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            torch.autograd.grad(c, inputs, gc)
+            torch.cuda.synchronize()
+            return time.perf_counter() - t
+        return one
+
+    def device_us(fn, reps=100):
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(T.stream)
+        for _ in range(reps):
+            fn()
+        e1.record(T.stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3
+
+    ops = ["geom", "wedge", "inner", "lc", "rc", "regressive"]
+    table = {"fwd": {}, "bwd": {}}
+    g = torch.Generator().manual_seed(0)
+    for n in range(7, 13):
+        D = 1 << n
+        cl = cc.CliffordAlgebra([1] * n, device=dev)
+        meth = {"geom": cl.geom_prod, "wedge": cl.wedge_prod, "inner": cl.inner_prod, "lc": cl.left_contraction,
+                "rc": cl.right_contraction, "regressive": cl.regressive_prod}
+        for B in (1, 16, 64):
+            a = torch.randn(B, D, generator=g).to(dev).requires_grad_()
+            b = torch.randn(B, D, generator=g).to(dev).requires_grad_()
+            gc = torch.randn(B, D, generator=g).to(dev)
+            for op in ops:
+                f = meth[op]
+                cell_f = table["fwd"].setdefault(op, {}).setdefault(str(n), {})
+                cell_b = table["bwd"].setdefault(op, {}).setdefault(str(n), {})
+                with torch.no_grad():
+                    fus = harness_us(sync_timed(lambda: f(a, b)))
+                    fdev = device_us(lambda: f(a, b))
+                bus = harness_us(bwd_timed(lambda: f(a, b), (a, b), gc))
+                c = f(a, b)
+                bdev = device_us(lambda: torch.autograd.grad(c, (a, b), gc, retain_graph=True))
+                cell_f[str(B)] = {"us": round(fus, 2), "device_us": round(fdev, 2)}
+                cell_b[str(B)] = {"us": round(bus, 2), "device_us": round(bdev, 2)}
+            biv = torch.randn(1, n * (n - 1) // 2, generator=g).to(dev)
+            x = torch.randn(B, D, generator=g).to(dev)
+            with torch.no_grad():
+                cs = cl.compile_bivector(biv)
+                rus = harness_us(sync_timed(lambda: cl.apply_rotor(cs, x)))
+                rdev = device_us(lambda: cl.apply_rotor(cs, x))
+            table["fwd"].setdefault("rotor_apply", {}).setdefault(str(n), {})[str(B)] = {
+                "us": round(rus, 2), "device_us": round(rdev, 2)}
+        print(f"[published] n={n} done", file=sys.stderr, flush=True)
+    return {"workload": "published: the reference's latency table (Cl(n,0), n = 7..12, batch 1/16/64), "
+                        "harness-style sync-timed wall clock, median of 10 x 10 after 25 warmups",
+            "unit": "us", "table": table,
+            "reference_a100_us_context": {"note": "NVIDIA A100 numbers published by the reference "
+                                                  "(figures/tables.md:6-54), different hardware: context only",
+                                          "n": list(range(7, 13)), **A100_US}}
 
 
 def cpu_layer(budget_s):
@@ -504,6 +690,7 @@ def main():
     torch.cuda.set_device(0)
     lib = _lib.load()
     T = Timer(torch, torch.cuda.current_stream(0), max(5, args.steps))
+    T.clock = Clock(torch, lib, T.stream)
     if args.workload == "headline":
         print(json.dumps(headline(args, torch, cc, lib, T)))
         return
@@ -533,6 +720,9 @@ def main():
                           "copy_ms": ms, "copy_gbs": 2.0 * nbytes / (ms * 1e-3) / 1e9,
                           "add_ms": ams, "add_gbs": 3.0 * nbytes / (ams * 1e-3) / 1e9,
                           "add_by_operand_mib": by_size}))
+        return
+    if args.workload == "published":
+        print(json.dumps(published(args, torch, cc, lib, T)))
         return
     runs = ["c1", "c2", "c3", "c4", "c5"] if args.workload == "all" else [args.workload]
     out = []

@@ -15,7 +15,7 @@ import torch
 LIB_NAME = "libclifford_hip.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 2  # CLF_ABI_VERSION of include/clifford_hip.h
+ABI_VERSION = 3  # CLF_ABI_VERSION of include/clifford_hip.h
 
 # status codes (include/clifford_hip.h)
 CLF_OK = 0
@@ -39,7 +39,7 @@ class DeviceInfo(ctypes.Structure):
     _fields_ = [("device", ctypes.c_int), ("compute_units", ctypes.c_int),
                 ("lds_bytes_per_block", ctypes.c_int), ("clock_khz", ctypes.c_int),
                 ("memory_clock_khz", ctypes.c_int), ("memory_bus_width_bits", ctypes.c_int),
-                ("arch_name", ctypes.c_char * 64)]
+                ("arch_name", ctypes.c_char * 64), ("wall_clock_khz", ctypes.c_int)]
 
 
 # name -> (restype, argtypes); the exact export list of include/clifford_hip.h
@@ -48,6 +48,7 @@ SIGNATURES = {
     "clf_options_reload": (None, []),
     "clf_last_error": (ctypes.c_char_p, []),
     "clf_device_info_get": (_i32, [_i32, ctypes.POINTER(DeviceInfo)]),
+    "clf_clock_sample": (_i32, [_vp, _i32, _vp]),
     "clf_product_max_n": (_i32, []),
     "clf_product_fwd": (_i32, [_i32, _i32, _u32, _u32, _vp, _vp, _vp, _i64, _vp]),
     "clf_product_bwd": (_i32, [_i32, _i32, _u32, _u32, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),

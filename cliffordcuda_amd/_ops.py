@@ -90,10 +90,10 @@ def _graded_setup(ctx, inputs, output):
 
 
 def _graded_backward(ctx, gy):
-    from . import _lib
+    from .graded import graded_adjoint
     kind, n, neg, nul, grade = ctx.meta
-    adj = _lib.GRADED_CODES["dual_adj"] if kind == _lib.GRADED_CODES["dual"] else kind
-    return graded(gy.contiguous(), adj, n, neg, nul, grade), None, None, None, None, None
+    g = graded_adjoint(kind, n, neg, nul, grade, gy, lambda k, n_, ng, nl, gr, t: graded(t, k, n_, ng, nl, gr))
+    return g, None, None, None, None, None
 
 
 graded.register_autograd(_graded_backward, setup_context=_graded_setup)

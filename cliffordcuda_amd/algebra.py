@@ -117,7 +117,10 @@ class CliffordAlgebra:
     def apply_rotor(self, cs, x):
         """Apply a cs chain (from ``compile_bivector``, or any (C(n,2), 2)
         tensor of (c, s) pairs) to a batch of multivectors; differentiable to
-        cs and to x."""
+        cs and to x. The gradient to cs follows the reference's rule
+        (``givens_apply_mb_perm_packed.cu:111-160``: each plane's input rebuilt
+        from the output with the transposed pair map), which is the true
+        derivative for unit (c, s) pairs only; the gradient to x is exact."""
         self._check_rotor_supported()
         _validate.check_mv(x, "x", self.dim, self.device, self.dtype)
         return _rotor.apply_rotor(cs, x, self.n)

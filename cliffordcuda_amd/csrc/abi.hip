@@ -177,6 +177,18 @@ int bcast_bwd_noalloc(int op, int side, int n, uint32_t neg, uint32_t nul, const
 // out-of-range n maps to 0 and is rejected by the callee's own check on n.
 inline int64_t dense_ld(int n) { return (n >= 0 && n <= kMaxN) ? (int64_t(1) << n) : 0; }
 
+// One wave per workgroup: its XCD index and the two clock counters, read back
+// to back (the real-time counter right after the shader-clock counter).
+__global__ __launch_bounds__(64) void clock_sample_kernel(int64_t* out) {
+    if (threadIdx.x != 0) return;
+    const unsigned xcc = __builtin_amdgcn_s_getreg(0xf814) & 15u;   // hwreg(HW_REG_XCC_ID)
+    const int64_t cyc = (int64_t)__builtin_readcyclecounter();     // s_memtime
+    const int64_t rt = (int64_t)__builtin_amdgcn_s_memrealtime();
+    out[3 * (int64_t)blockIdx.x] = xcc;
+    out[3 * (int64_t)blockIdx.x + 1] = cyc;
+    out[3 * (int64_t)blockIdx.x + 2] = rt;
+}
+
 }  // namespace clf
 
 extern "C" {
@@ -201,6 +213,18 @@ int clf_device_info_get(int device, clf_device_info* out) {
     out->memory_clock_khz = p.memoryClockRate;
     out->memory_bus_width_bits = p.memoryBusWidth;
     std::strncpy(out->arch_name, p.gcnArchName, sizeof(out->arch_name) - 1);
+    int wall = 0;
+    CLF_HIP_CHECK(hipDeviceGetAttribute(&wall, hipDeviceAttributeWallClockRate, device));
+    out->wall_clock_khz = wall;
+    return CLF_OK;
+}
+
+int clf_clock_sample(int64_t* out, int slots, void* stream) {
+    clf::clear_error();
+    if (!out) return clf::set_error(CLF_ERR_ARG, "out must not be NULL");
+    if (slots < 1 || slots > 4096) return clf::set_error(CLF_ERR_ARG, "slots must be in [1, 4096]");
+    hipLaunchKernelGGL(clf::clock_sample_kernel, dim3(slots), dim3(64), 0, (hipStream_t)stream, out);
+    CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }
 

@@ -23,6 +23,19 @@ def _graded_launch(kind: int, n: int, neg: int, nul: int, grade: int, x: torch.T
     return y
 
 
+def graded_adjoint(kind: int, n: int, neg: int, nul: int, grade: int, gy: torch.Tensor, launch) -> torch.Tensor:
+    """The backward of a graded op: its adjoint (the op itself for the sign and
+    mask ops, DUAL_ADJ for the dual) applied to the upstream gradient. The op is
+    row by row, so an upstream gradient whose batch stride is 0 (autograd's
+    expansion of the gradient of a sum) gives a result with the same one row:
+    it is computed on that row and handed back expanded, with no full-size
+    read or write."""
+    adj = _lib.GRADED_CODES["dual_adj"] if kind == _lib.GRADED_CODES["dual"] else kind
+    if gy.dim() == 2 and gy.shape[0] > 1 and gy.stride(0) == 0:
+        return launch(adj, n, neg, nul, grade, gy[:1].contiguous()).expand(gy.shape)
+    return launch(adj, n, neg, nul, grade, gy.contiguous())
+
+
 class _GradedFunc(torch.autograd.Function):
     """y = kind(x); sign / mask ops are self-adjoint, the dual's adjoint is
     the DUAL_ADJ kernel."""
@@ -35,8 +48,7 @@ class _GradedFunc(torch.autograd.Function):
     @staticmethod
     def backward(ctx, gy):
         kind, n, neg, nul, grade = ctx.meta
-        adj = _lib.GRADED_CODES["dual_adj"] if kind == _lib.GRADED_CODES["dual"] else kind
-        return _graded_launch(adj, n, neg, nul, grade, gy.contiguous()), None, None, None, None, None
+        return graded_adjoint(kind, n, neg, nul, grade, gy, _graded_launch), None, None, None, None, None
 
 
 def graded(kind: str, x: torch.Tensor, neg: int = 0, nul: int = 0, grade: int = 0) -> torch.Tensor:

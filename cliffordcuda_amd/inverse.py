@@ -165,7 +165,9 @@ class _InverseFunc(torch.autograd.Function):
     def backward(ctx, gy):
         xf, y = ctx.saved_tensors
         n, neg, nul, versor, metric = ctx.meta
-        gy = gy.contiguous()
+        # gy is used as autograd hands it over: the elementwise versor formula
+        # broadcasts a batch-stride-0 gradient, and the product backwards read
+        # such a gradient as its one row
         if versor:
             # y = rev(x) / s(x), s(x) = sum_A w_A x_A^2
             rs = _reverse_signs(n, xf.device)

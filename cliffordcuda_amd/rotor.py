@@ -19,9 +19,15 @@ Besides cs, a compile produces the library's own rotor state: the rotation Q
 and, for n = 8, the rotor's 16 x 16 matrix in the real representation of
 Cl(8,0), which the n = 8 sandwich kernels run on the matrix cores. The state is
 internal: ``apply_bivector`` (and ``RotorLayer``) differentiate through it to
-the bivector directly, and ``apply_rotor`` uses it when it is handed a cs that
-``compile_bivector`` produced and that has not changed since; any other cs
-runs the plane chain itself.
+the bivector directly, and ``apply_rotor`` runs its forward on it when it is
+handed a cs that ``compile_bivector`` produced and that has not changed since
+(cs stays in y's autograd graph; its gradient comes from the plane chain's
+backward); any other cs runs the plane chain itself.
+
+The gradient to cs follows the reference's rule (each plane's input rebuilt
+from the chain's output with the transposed pair map), which is the true
+derivative for unit (c, s) pairs, the pairs ``compile_bivector`` makes; for
+other pairs it is the reference's value, not the derivative.
 """
 from __future__ import annotations
 
@@ -162,21 +168,6 @@ def _cs_apply_bwd(cs: torch.Tensor, y: torch.Tensor, gy: torch.Tensor, n: int, n
 
 # ---- autograd ---------------------------------------------------------------------
 
-class _KnownStateFunc(torch.autograd.Function):
-    """A state already compiled from ``biv``, attached to biv's graph."""
-
-    @staticmethod
-    def forward(ctx, biv, state, n):
-        ctx.save_for_backward(biv)
-        ctx.n = n
-        return state.clone()
-
-    @staticmethod
-    def backward(ctx, g_state):
-        (biv,) = ctx.saved_tensors
-        return _compile_bwd(biv, g_state, ctx.n), None, None
-
-
 class _StateApplyFunc(torch.autograd.Function):
     @staticmethod
     def forward(ctx, state, x, n):
@@ -208,6 +199,30 @@ class _BivectorApplyFunc(torch.autograd.Function):
         biv, state, x = ctx.saved_tensors
         g_biv, gx = _biv_apply_bwd(biv, state, x, gy, ctx.n, ctx.needs_input_grad[0], ctx.needs_input_grad[1])
         return g_biv, gx, None
+
+
+class _CompiledCsApplyFunc(torch.autograd.Function):
+    """y = chain(cs) x for a cs that ``compile_bivector`` made and nobody has
+    changed since: the forward runs on that compile's state (the n = 8 kernels
+    on the matrix cores), cs stays an input of the node, so gradients and hooks
+    reach cs and, through cs's own node, the bivector."""
+
+    @staticmethod
+    def forward(ctx, cs, x, state, n):
+        y = _apply_fwd(state, x, n)
+        ctx.save_for_backward(cs, state, x, y)
+        ctx.n = n
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        cs, state, x, y = ctx.saved_tensors
+        if ctx.needs_input_grad[0]:
+            g_cs, gx = _cs_apply_bwd(cs, y, gy, ctx.n, True, ctx.needs_input_grad[1])
+        else:
+            _, gx = _apply_bwd(state, x, gy, ctx.n, False, ctx.needs_input_grad[1])
+            g_cs = None
+        return g_cs, gx, None, None
 
 
 class _CompileCsFunc(torch.autograd.Function):
@@ -245,18 +260,15 @@ class _CsApplyFunc(torch.autograd.Function):
 
 class _Compiled:
     """What ``compile_bivector`` knows about the cs it returned: the internal
-    state of the same compile, the bivector it came from, and the versions and
-    addresses that say whether either has changed since."""
+    state of the same compile, and the version and address that say whether cs
+    has changed since."""
 
-    __slots__ = ("state", "biv", "biv_version", "cs_version", "cs_ptr", "node")
+    __slots__ = ("state", "cs_version", "cs_ptr")
 
-    def __init__(self, state, biv, cs):
+    def __init__(self, state, cs):
         self.state = state
-        self.biv = biv
-        self.biv_version = biv._version
         self.cs_version = cs._version
         self.cs_ptr = cs.data_ptr()
-        self.node = cs.grad_fn
 
     def unchanged(self, cs) -> bool:
         return cs._version == self.cs_version and cs.data_ptr() == self.cs_ptr
@@ -273,7 +285,7 @@ def compile_bivector(bivector: torch.Tensor, n: int) -> torch.Tensor:
         return _ops.rotor_compile_cs(biv.contiguous(), n)
     holder = []
     cs = _CompileCsFunc.apply(biv, n, holder)
-    cs._clf_rotor = _Compiled(holder[0], biv, cs)
+    cs._clf_rotor = _Compiled(holder[0], cs)
     return cs
 
 
@@ -298,13 +310,9 @@ def apply_rotor(cs: torch.Tensor, x: torch.Tensor, n: int) -> torch.Tensor:
         return _ops.rotor_cs_apply(cs.contiguous(), x.contiguous(), n)
     info = getattr(cs, "_clf_rotor", None)
     if info is not None and info.unchanged(cs):
-        if not (torch.is_grad_enabled() and cs.requires_grad):
-            return _StateApplyFunc.apply(info.state, x, n)
-        if cs.grad_fn is info.node and not cs.retains_grad and info.biv._version == info.biv_version:
-            # cs is the untouched output of compile_bivector: route its
-            # gradient to the bivector through the state (the same value
-            # compile_bivector's own backward would give)
-            return _StateApplyFunc.apply(_KnownStateFunc.apply(info.biv, info.state, n), x, n)
+        if torch.is_grad_enabled() and cs.requires_grad:
+            return _CompiledCsApplyFunc.apply(cs, x, info.state, n)
+        return _StateApplyFunc.apply(info.state, x, n)
     return _CsApplyFunc.apply(cs.contiguous(), x, n)
 
 

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define CLF_ABI_VERSION 2
+#define CLF_ABI_VERSION 3
 
 /* status codes */
 #define CLF_OK               0
@@ -62,6 +62,7 @@ typedef struct clf_device_info {
     int    memory_clock_khz;
     int    memory_bus_width_bits;
     char   arch_name[64];
+    int    wall_clock_khz;        /* rate of the s_memrealtime counter (clf_clock_sample) */
 } clf_device_info;
 
 /* ABI version (CLF_ABI_VERSION). */
@@ -80,6 +81,17 @@ void clf_options_reload(void);
  * (src/cliffordcuda/extensions/ga/geom_prod_tiled.py:88-117,
  *  kernels/ga/geom_prod_tiled.cu:169-175). */
 int clf_device_info_get(int device, clf_device_info* out);
+
+/* Engine-clock sample for the roofline report: launches `slots` one-wave
+ * workgroups on `stream`; workgroup w writes out[3w] = its XCD (accelerator
+ * complex die) index, out[3w+1] = the shader-clock counter (s_memtime) and
+ * out[3w+2] = the constant-rate counter (s_memrealtime, wall_clock_khz).
+ * Two samples on one stream around a timed region give, per XCD, the mean
+ * engine clock over that region: (cycles delta) / (real-time delta).
+ * `out` is device memory of 3 * slots int64; 1 <= slots <= 4096.
+ * No counterpart in the reference (its harness warms the clock up instead,
+ * benchmark/_harness.py:41-50, and records none). */
+int clf_clock_sample(int64_t* out, int slots, void* stream);
 
 /* Largest n the product kernels accept (20; rows past the LDS budget, n >= 13,
  * run tiled kernels, as the reference's geom_prod_tiled_fused does,

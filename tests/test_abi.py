@@ -32,8 +32,17 @@ def test_all_declared_symbols_exported():
 
 def test_abi_version_and_limits():
     lib = _lib.load()
-    assert lib.clf_abi_version() == 2
+    assert lib.clf_abi_version() == _lib.ABI_VERSION == 3
     assert lib.clf_product_max_n() >= 10
+
+
+def test_clock_sample_rejects_bad_arguments():
+    lib = _lib.load()
+    assert lib.clf_clock_sample(None, 8, None) == 1
+    assert "NULL" in lib.clf_last_error().decode()
+    for slots in (0, -1, 4097):
+        assert lib.clf_clock_sample(16, slots, None) == 1
+        assert "slots" in lib.clf_last_error().decode()
 
 
 def test_rotor_state_length_matches_python():

@@ -213,3 +213,66 @@ def test_ld_entries_reject_other_strides():
             assert call() == _lib.CLF_ERR_ARG
             assert "row stride" in _lib.last_error()
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("kind", ["reverse", "grade_involution", "clifford_conjugation", "grade_projection", "dual"])
+def test_graded_bwd_stride0_equals_materialised(kind):
+    """The graded ops' backward computes a batch-stride-0 upstream gradient's
+    one row and hands it back expanded (no full-size write): bitwise equal to
+    the backward of the materialised gradient, and still stride 0."""
+    n = 10
+    cl = cc.CliffordAlgebra((1,) * 9 + (0,) if kind != "dual" else (1,) * 8 + (-1, 1), device="cuda")
+    (x,) = _rows(37, n, 71, 1)
+    exp, mat = _expanded(37, n, 71)
+    fn = {"grade_projection": lambda t: cl.grade_projection(t, 2)}.get(kind, getattr(cl, kind))
+    outs = []
+    for g in (exp, mat):
+        xd = x.clone().requires_grad_()
+        y = fn(xd)
+        (gx,) = torch.autograd.grad(y, (xd,), g)
+        outs.append(gx)
+    assert torch.equal(outs[0], outs[1])
+
+
+def test_graded_after_sum_keeps_stride0_into_the_product_backward():
+    """C5's chain grade_projection(geom_prod(a, b), 2).sum().backward(): the
+    projection's backward hands the product backward an expanded row, and the
+    gradients equal those of the materialised upstream gradient."""
+    n = 10
+    cl = cc.CliffordAlgebra((1,) * 9 + (0,), device="cuda")
+    a, b = _rows(29, n, 72, 2)
+    res = []
+    for mode in ("sum", "ones"):
+        ad = a.clone().requires_grad_()
+        bd = b.clone().requires_grad_()
+        pr = cl.grade_projection(cl.geom_prod(ad, bd), 2)
+        if mode == "sum":
+            pr.sum().backward()
+        else:
+            pr.backward(torch.ones_like(pr))
+        res.append((ad.grad, bd.grad))
+    assert torch.equal(res[0][0], res[1][0]) and torch.equal(res[0][1], res[1][1])
+
+
+def test_inverse_bwd_accepts_stride0():
+    """The inverse's backward (versor formula and the dense path's product
+    backwards) takes the expanded gradient of a sum as it is."""
+    n = 5
+    cl = cc.CliffordAlgebra((1,) * 5, device="cuda")
+    g = torch.Generator().manual_seed(73)
+    v = torch.randn(19, n, generator=g)
+    x = torch.zeros(19, 1 << n)
+    for i in range(n):
+        x[:, 1 << i] = v[:, i]                    # vectors: versors
+    y = torch.randn(19, 1 << n, generator=g) + 3.0 * torch.nn.functional.one_hot(torch.zeros(19, dtype=torch.long), 1 << n)
+    for xin, method in ((x, "versor"), (y, "lu")):
+        grads = []
+        for mode in ("sum", "ones"):
+            xd = xin.cuda().requires_grad_()
+            inv = cl.inverse(xd, method=method)
+            if mode == "sum":
+                inv.sum().backward()
+            else:
+                inv.backward(torch.ones_like(inv))
+            grads.append(xd.grad)
+        torch.testing.assert_close(grads[0], grads[1], rtol=1e-6, atol=1e-6)

@@ -110,38 +110,79 @@ def test_c2_cl61_six_products_full_batch():
 
 
 def test_c5_degenerate_n10():
-    """Cl(9,0,1), GP and lc fwd + bwd, then norm_sq and
-    grade_projection(2) of the product (oracle on 16 rows of the batch; the
-    full batch of 16384 is exercised for finiteness and row independence)."""
+    """Cl(9,0,1), batch 16384. The left contraction fwd + bwd
+    on its own (seeded upstream gradient, so its gradients are isolated), and the
+    geometric product fwd + bwd with norm_sq and grade_projection(2) of it in
+    the loss. Checks: the oracle on 8 rows of the batch (values and all
+    gradients); the full batch by bilinearity of both forwards; bitwise row
+    independence of both forwards and backwards (rows computed inside the full
+    batch equal the same rows computed alone, including an odd-sized batch)."""
     metric = (1,) * 9 + (0,)
     g = torch.Generator().manual_seed(0)
     B = 16384
     a = torch.randn(B, 1024, generator=g)
     b = torch.randn(B, 1024, generator=g)
+    glc = torch.randn(B, 1024, generator=g)
     cl = cc.CliffordAlgebra(metric, device="cuda")
-    x = a.cuda().requires_grad_()
-    y = b.cuda().requires_grad_()
-    gp = cl.geom_prod(x, y)
-    lc = cl.left_contraction(x, y)
-    ns = cl.norm_sq(gp)
-    pr = cl.grade_projection(gp, 2)
-    (gp.sum() + lc.sum() + ns.sum() + pr.sum()).backward()
+    ad, bd, glcd = a.cuda(), b.cuda(), glc.cuda()
     rows = torch.tensor([0, 1, 2, 3, 100, 5000, 9999, B - 1])
+    rs = rows.cuda()
     a64 = a[rows].double().requires_grad_()
     b64 = b[rows].double().requires_grad_()
-    gp64 = O.einsum_product("geom", a64, b64, metric)
+
+    print("[case] C5 lc fwd+bwd", flush=True)
+    x = ad.clone().requires_grad_()
+    y = bd.clone().requires_grad_()
+    lc = cl.left_contraction(x, y)
+    lc.backward(glcd)
     lc64 = O.einsum_product("lc", a64, b64, metric)
+    lc64.backward(glc[rows].double())
+    assert rel_err(lc[rs], lc64) <= TOL
+    assert rel_err(x.grad[rs], a64.grad) <= TOL
+    assert rel_err(y.grad[rs], b64.grad) <= TOL
+    lc_ga, lc_gb = x.grad, y.grad
+
+    print("[case] C5 geom + norm_sq + grade_projection fwd+bwd", flush=True)
+    a64.grad = None
+    b64.grad = None
+    x = ad.clone().requires_grad_()
+    y = bd.clone().requires_grad_()
+    gp = cl.geom_prod(x, y)
+    ns = cl.norm_sq(gp)
+    pr = cl.grade_projection(gp, 2)
+    (gp.sum() + ns.sum() + pr.sum()).backward()
+    gp64 = O.einsum_product("geom", a64, b64, metric)
     ns64 = O.norm_sq(gp64, metric)
     pr64 = O.grade_projection(gp64, 2)
-    (gp64.sum() + lc64.sum() + ns64.sum() + pr64.sum()).backward()
-    rs = rows.cuda()
+    (gp64.sum() + ns64.sum() + pr64.sum()).backward()
     assert rel_err(gp[rs], gp64) <= TOL
-    assert rel_err(lc[rs], lc64) <= TOL
     assert rel_err(ns[rs], ns64) <= TOL
     assert rel_err(pr[rs], pr64) <= TOL
     assert rel_err(x.grad[rs], a64.grad) <= TOL
     assert rel_err(y.grad[rs], b64.grad) <= TOL
-    assert torch.isfinite(x.grad).all() and torch.isfinite(y.grad).all()
+    gp_ga, gp_gb = x.grad, y.grad
+
+    print("[case] C5 full-batch bilinearity", flush=True)
+    with torch.no_grad():
+        for meth, c in ((cl.geom_prod, gp), (cl.left_contraction, lc)):
+            lhs = meth(ad, bd + 2 * ad)
+            rhs = c + 2 * meth(ad, ad)
+            assert rel_err(lhs, rhs) <= TOL
+
+    print("[case] C5 row independence", flush=True)
+    idx = torch.tensor([0, 5, 6, 7, 4097, 8191, 12345, B - 3, B - 2, B - 1], device="cuda")
+    xs = ad[idx].clone().requires_grad_()
+    ys = bd[idx].clone().requires_grad_()
+    lcs = cl.left_contraction(xs, ys)
+    lcs.backward(glcd[idx])
+    assert torch.equal(lcs, lc[idx].detach())
+    assert torch.equal(xs.grad, lc_ga[idx]) and torch.equal(ys.grad, lc_gb[idx])
+    xs = ad[idx].clone().requires_grad_()
+    ys = bd[idx].clone().requires_grad_()
+    gps = cl.geom_prod(xs, ys)
+    (gps.sum() + cl.norm_sq(gps).sum() + cl.grade_projection(gps, 2).sum()).backward()
+    assert torch.equal(gps, gp[idx].detach())
+    assert torch.equal(xs.grad, gp_ga[idx]) and torch.equal(ys.grad, gp_gb[idx])
 
 
 def test_headline_shape_row_independence():

@@ -169,6 +169,40 @@ def test_compile_then_apply_gradients_on_every_path(n):
             assert rel_err(cs.grad, cs64.grad) <= TOL, mode
 
 
+@pytest.mark.parametrize("n", [8, 9])
+def test_compiled_cs_stays_in_the_graph(n):
+    """apply_rotor on the untouched output of compile_bivector keeps cs in y's
+    autograd graph, as the reference's GivensFactorFunc output is:
+    torch.autograd.grad(y, cs) works and equals the oracle's cs gradient, a
+    hook registered on the non-leaf cs fires, and the bivector gradient that
+    then flows through cs's node is the oracle's."""
+    cl = cc.CliffordAlgebra([1] * n, device="cuda")
+    C = n * (n - 1) // 2
+    g = torch.Generator().manual_seed(80 + n)
+    biv = 0.5 * torch.randn(1, C, generator=g)
+    x = torch.randn(7, 1 << n, generator=g)
+    gy = torch.randn(7, 1 << n, generator=g)
+    y64, gb64, gx64 = oracle_cs_step(biv, x, gy, n)
+    b64 = biv.double().requires_grad_()
+    cs64 = O.compile_bivector_cs(b64, n)
+    cs64.retain_grad()
+    O.givens_chain_apply(cs64, x.double(), n).backward(gy.double())
+    print(f"[case] compiled cs in graph n={n}", flush=True)
+    bd = biv.cuda().requires_grad_()
+    xd = x.cuda().requires_grad_()
+    cs = cl.compile_bivector(bd)
+    y = cl.apply_rotor(cs, xd)
+    (g_cs,) = torch.autograd.grad(y, (cs,), gy.cuda(), retain_graph=True)
+    assert rel_err(g_cs, cs64.grad) <= TOL
+    seen = []
+    cs.register_hook(lambda g_: seen.append(g_.detach().clone()))
+    y.backward(gy.cuda())
+    assert len(seen) == 1 and rel_err(seen[0], cs64.grad) <= TOL
+    assert rel_err(y, y64) <= TOL
+    assert rel_err(xd.grad, gx64) <= TOL
+    assert rel_err(bd.grad, gb64) <= TOL
+
+
 def test_rotor_layer_c4_shape():
     """RotorLayer train mode on Cl(7,1), bivector ~ N(0, 0.1),
     x (131072, 256): full-batch forward + backward against the fp64 oracle.
@@ -220,25 +254,62 @@ def test_compile_then_apply_eval_cache_and_properties():
                                    cl.apply_rotor(cs, cl.grade_projection(x, k)), rtol=1e-5, atol=1e-5)
 
 
-def test_large_and_equal_angles():
-    """Equal plane angles (where the reference's eigh pair pick is fragile) and a
-    large bivector (scaling and squaring)."""
-    n = 8
+def _planes_bivector(n, angles, rot_seed=None):
+    """Bivector of B = sum_k angle_k (e_{2k} e_{2k+1} plane), optionally turned
+    by a random rotation Q (B -> Q B Q^T), so that equal-angle planes are not
+    coordinate planes; b_m = B[i_m, j_m] / 2 (B = 2 (M - M^T))."""
+    B = torch.zeros(n, n, dtype=torch.float64)
+    for k, t in enumerate(angles):
+        B[2 * k, 2 * k + 1] = t
+        B[2 * k + 1, 2 * k] = -t
+    if rot_seed is not None:
+        g = torch.Generator().manual_seed(rot_seed)
+        Q, _ = torch.linalg.qr(torch.randn(n, n, generator=g, dtype=torch.float64))
+        B = Q @ B @ Q.T
+    iu = torch.triu_indices(n, n, 1)
+    return (B[iu[0], iu[1]] / 2).reshape(1, -1).float()
+
+
+EQUAL_ANGLE_CASES = [
+    (8, [0.7, 0.7], None),                  # two equal coordinate planes
+    (8, [0.7, 0.7], 3),                     # two equal planes, turned
+    (7, [0.7, 0.7, 0.7], None),             # three equal planes and the zero-angle axis e6
+    (7, [0.7, 0.7, 0.7], 4),
+    (8, [0.7, 0.7, 0.7, 0.0], 5),           # three equal planes and a zero-angle plane
+    (8, [0.7, 0.7 + 1e-6, 0.3], 6),         # nearly equal: inside the reference's 1e-4 cut
+    (8, [0.7, 0.7 + 1e-4, 0.3], 7),         # at the cut (eigh_exp.cu:236-237)
+]
+
+
+@pytest.mark.parametrize("scale", [1.0, 25.0])
+@pytest.mark.parametrize("n,angles,rot", EQUAL_ANGLE_CASES)
+def test_equal_and_large_angles(n, angles, rot, scale):
+    """Equal plane angles, where the reference's eigenvector pair pick
+    (eigh_exp.cu:297-306) and its 1e-4 cut of near-equal eigenvalues in the
+    backward (:236-237) are fragile: the expm-based compile has no such
+    branch. Scale 1 and scale 25 (angles up to 17.5 rad, scaling and squaring)
+    are both held to the 1e-5 bar, on y, x's gradient and the bivector's
+    gradient, with an all-ones and a random upstream gradient, through
+    apply_bivector and through compile_bivector + apply_rotor."""
     cl = cc.CliffordAlgebra([1] * n, device="cuda")
-    biv = torch.zeros(1, 28)
-    # two commuting planes (0,1) and (2,3) with the same angle, and a big one
-    biv[0, 0] = 0.7
-    biv[0, 13] = 0.7     # pair (2,3): index of (2,3) in lex order is 7+6 = 13
-    g = torch.Generator().manual_seed(5)
-    x = torch.randn(8, 256, generator=g)
-    for scale in (1.0, 25.0):
-        b = biv * scale
-        bd = b.cuda().requires_grad_()
-        y = cl.apply_bivector(bd, x.cuda())
-        y.sum().backward()
-        y64, gb64, _ = oracle_step(b, x, torch.ones(8, 256), n)
-        assert rel_err(y, y64) <= 5e-5, scale
-        assert rel_err(bd.grad, gb64) <= 5e-4, scale
+    biv = _planes_bivector(n, [scale * t for t in angles], rot)
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(8, 1 << n, generator=g)
+    for gname, gy in (("ones", torch.ones(8, 1 << n)), ("randn", torch.randn(8, 1 << n, generator=g))):
+        print(f"[case] equal angles n={n} {angles} rot={rot} scale={scale} gy={gname}", flush=True)
+        y64, gb64, gx64 = oracle_step(biv, x, gy, n)
+        bd = biv.cuda().requires_grad_()
+        xd = x.cuda().requires_grad_()
+        y = cl.apply_bivector(bd, xd)
+        y.backward(gy.cuda())
+        assert rel_err(y, y64) <= TOL
+        assert rel_err(xd.grad, gx64) <= TOL
+        assert rel_err(bd.grad, gb64) <= TOL
+        bd2 = biv.cuda().requires_grad_()
+        y2 = cl.apply_rotor(cl.compile_bivector(bd2), x.cuda())
+        y2.backward(gy.cuda())
+        assert rel_err(y2, y64) <= TOL
+        assert rel_err(bd2.grad, gb64) <= TOL
 
 
 def test_rotor_errors():
