@@ -153,7 +153,7 @@ class Clock:
     launch stream before the work and one after give, per XCD, cycles over
     real time."""
 
-    SLOTS = 64
+    SLOTS = 4096
 
     def __init__(self, torch, lib, stream):
         from cliffordcuda_amd import _lib
@@ -168,33 +168,37 @@ class Clock:
                    "clf_clock_sample")
 
     def ghz(self):
-        """Median over XCDs of the mean clock between the two samples (None if
-        the counters do not give a plausible value)."""
+        """Median over compute units (seen in both samples) of the mean clock
+        between the two samples, and the per-XCD medians (None if the counters
+        do not give a plausible value)."""
         h = self.buf.cpu().view(2, self.SLOTS, 3).tolist()
-        per_xcd = {}
+        first = [{}, {}]
         for k in range(2):
-            for xcc, cyc, rt in h[k]:
-                d = per_xcd.setdefault(xcc, [[None, None], [None, None]])
-                if d[k][0] is None or cyc < d[k][0]:
-                    d[k] = [cyc, rt]
+            for loc, cyc, rt in h[k]:
+                if loc not in first[k] or cyc < first[k][loc][0]:
+                    first[k][loc] = (cyc, rt)
         rate = self.info.wall_clock_khz * 1e3
-        vals = []
-        for xcc, ((c0, r0), (c1, r1)) in per_xcd.items():
-            if None in (c0, c1) or r1 <= r0 or rate <= 0:
+        per_cu, per_xcd = [], {}
+        for loc in set(first[0]) & set(first[1]):
+            (c0, r0), (c1, r1) = first[0][loc], first[1][loc]
+            if r1 <= r0 or c1 <= c0 or rate <= 0:
                 continue
-            vals.append((c1 - c0) / ((r1 - r0) / rate) / 1e9)
-        vals.sort()
-        if not vals or not 0.3 < vals[len(vals) // 2] < 4.0:
-            return None, vals
-        return vals[len(vals) // 2], vals
+            v = (c1 - c0) / ((r1 - r0) / rate) / 1e9
+            per_cu.append(v)
+            per_xcd.setdefault(loc & 15, []).append(v)
+        per_cu.sort()
+        xcd = [sorted(v)[len(v) // 2] for _, v in sorted(per_xcd.items())]
+        if not per_cu or not 0.3 < per_cu[len(per_cu) // 2] < 4.0:
+            return None, xcd
+        return per_cu[len(per_cu) // 2], xcd
 
     def device(self, ghz, vals, what):
         return {"compute_units": self.info.compute_units, "max_engine_clock_mhz": self.info.clock_khz / 1e3,
                 "measured_engine_clock_ghz": ghz,
                 "measured_engine_clock_ghz_per_xcd": [round(v, 3) for v in vals],
                 "clock_method": f"clf_clock_sample before and after {what} on its stream: shader-clock cycles "
-                                f"(s_memtime) over real time (s_memrealtime, {self.info.wall_clock_khz} kHz), "
-                                f"per XCD, median"}
+                                f"(s_memtime) over real time (s_memrealtime, {self.info.wall_clock_khz} kHz) "
+                                f"per compute unit, median over compute units (per-XCD medians listed)"}
 
 
 class Timer:

@@ -177,14 +177,17 @@ int bcast_bwd_noalloc(int op, int side, int n, uint32_t neg, uint32_t nul, const
 // out-of-range n maps to 0 and is rejected by the callee's own check on n.
 inline int64_t dense_ld(int n) { return (n >= 0 && n <= kMaxN) ? (int64_t(1) << n) : 0; }
 
-// One wave per workgroup: its XCD index and the two clock counters, read back
-// to back (the real-time counter right after the shader-clock counter).
+// One wave per workgroup: where it runs (XCD index, and the compute unit,
+// shader array and shader engine fields of the hardware id) and the two clock
+// counters, read back to back (the real-time counter right after the
+// shader-clock counter, which is not synchronised across compute units).
 __global__ __launch_bounds__(64) void clock_sample_kernel(int64_t* out) {
     if (threadIdx.x != 0) return;
     const unsigned xcc = __builtin_amdgcn_s_getreg(0xf814) & 15u;   // hwreg(HW_REG_XCC_ID)
+    const unsigned hw = __builtin_amdgcn_s_getreg(0xf804);          // hwreg(HW_REG_HW_ID)
     const int64_t cyc = (int64_t)__builtin_readcyclecounter();     // s_memtime
     const int64_t rt = (int64_t)__builtin_amdgcn_s_memrealtime();
-    out[3 * (int64_t)blockIdx.x] = xcc;
+    out[3 * (int64_t)blockIdx.x] = (int64_t)(xcc | (hw & 0xff00u));
     out[3 * (int64_t)blockIdx.x + 1] = cyc;
     out[3 * (int64_t)blockIdx.x + 2] = rt;
 }

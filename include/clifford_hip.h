@@ -83,12 +83,14 @@ void clf_options_reload(void);
 int clf_device_info_get(int device, clf_device_info* out);
 
 /* Engine-clock sample for the roofline report: launches `slots` one-wave
- * workgroups on `stream`; workgroup w writes out[3w] = its XCD (accelerator
- * complex die) index, out[3w+1] = the shader-clock counter (s_memtime) and
- * out[3w+2] = the constant-rate counter (s_memrealtime, wall_clock_khz).
- * Two samples on one stream around a timed region give, per XCD, the mean
- * engine clock over that region: (cycles delta) / (real-time delta).
- * `out` is device memory of 3 * slots int64; 1 <= slots <= 4096.
+ * workgroups on `stream`; workgroup w writes out[3w] = where it ran (bits 0..3:
+ * XCD index; bits 8..15: compute-unit, shader-array and shader-engine fields
+ * of the hardware id), out[3w+1] = that compute unit's shader-clock counter
+ * (s_memtime) and out[3w+2] = the constant-rate counter (s_memrealtime,
+ * wall_clock_khz). Two samples on one stream around a timed region give, per
+ * compute unit seen in both, the mean engine clock over that region:
+ * (cycles delta) / (real-time delta). `out` is device memory of 3 * slots
+ * int64; 1 <= slots <= 4096 (4096 covers every compute unit in practice).
  * No counterpart in the reference (its harness warms the clock up instead,
  * benchmark/_harness.py:41-50, and records none). */
 int clf_clock_sample(int64_t* out, int slots, void* stream);

@@ -1,5 +1,6 @@
-"""clf_clock_sample: XCD indices and clock counters that give a plausible
-engine clock over a stretch of GPU work (the roofline report's clock)."""
+"""clf_clock_sample: XCD indices, hardware ids and clock counters that give a
+plausible engine clock over a stretch of GPU work (the roofline report's
+clock), per compute unit seen in both samples."""
 import pytest
 import torch
 
@@ -12,7 +13,7 @@ def test_clock_sample_gives_a_plausible_engine_clock():
     lib = _lib.load()
     info = _lib.device_info(0)
     assert info.wall_clock_khz > 0 and info.compute_units > 0
-    slots = 64
+    slots = 4096
     buf = torch.zeros(2, 3 * slots, dtype=torch.int64, device="cuda")
     s = torch.cuda.current_stream().cuda_stream
     x = torch.randn(1 << 24, device="cuda")
@@ -21,15 +22,21 @@ def test_clock_sample_gives_a_plausible_engine_clock():
         x = x * 1.0001 + 0.5
     _lib.check(lib.clf_clock_sample(buf[1].data_ptr(), slots, s), "clf_clock_sample")
     torch.cuda.synchronize()
-    h = buf.cpu().view(2, slots, 3)
-    assert int(h[:, :, 0].min()) >= 0 and int(h[:, :, 0].max()) < 16
-    xccs = set(h[0, :, 0].tolist())
-    assert xccs == set(h[1, :, 0].tolist())
-    for xcc in xccs:
-        pre = h[0][h[0, :, 0] == xcc]
-        post = h[1][h[1, :, 0] == xcc]
-        dc = int(post[:, 1].min()) - int(pre[:, 1].min())
-        dr = int(post[:, 2].min()) - int(pre[:, 2].min())
-        assert dc > 0 and dr > 0
-        ghz = dc / (dr / (info.wall_clock_khz * 1e3)) / 1e9
-        assert 0.3 < ghz < 4.0, (xcc, ghz)
+    h = buf.cpu().view(2, slots, 3).tolist()
+    first = [{}, {}]
+    for k in range(2):
+        for loc, cyc, rt in h[k]:
+            assert 0 <= (loc & 15) < 16
+            if loc not in first[k] or cyc < first[k][loc][0]:
+                first[k][loc] = (cyc, rt)
+    common = set(first[0]) & set(first[1])
+    assert len(common) >= info.compute_units // 2
+    ghz = []
+    for loc in common:
+        (c0, r0), (c1, r1) = first[0][loc], first[1][loc]
+        assert r1 > r0
+        ghz.append((c1 - c0) / ((r1 - r0) / (info.wall_clock_khz * 1e3)) / 1e9)
+    ghz.sort()
+    print(f"[clock] {len(common)} compute units, median {ghz[len(ghz) // 2]:.3f} GHz, "
+          f"range {ghz[0]:.3f} .. {ghz[-1]:.3f}", flush=True)
+    assert 0.3 < ghz[len(ghz) // 2] < 4.0
