@@ -36,6 +36,7 @@ static Options read_options() {
         else if (std::strcmp(e, "balanced") == 0) o.product_path = PATH_BALANCED;
         else if (std::strcmp(e, "tiled") == 0) o.product_path = PATH_TILED;
         else if (std::strcmp(e, "generic") == 0) o.product_path = PATH_GENERIC;
+        else if (std::strcmp(e, "split") == 0) o.product_path = PATH_SPLIT;
     }
     e = std::getenv("CLF_GEOM_PATH");
     o.geom_direct = e && std::strcmp(e, "direct") == 0;

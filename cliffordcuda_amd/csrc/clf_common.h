@@ -46,7 +46,7 @@ bool stream_nt(double footprint_bytes);
 //   CLF_GEOM_PATH=direct         geometric product on the per-term kernels
 //   CLF_SPLIT_PATH=pairs         n = 10 split path as separate pair sums
 //   CLF_ROTOR_PATH=chain         n = 8 rotor on the register plane chain
-enum ProductPath { PATH_DEFAULT = 0, PATH_BLOCKED, PATH_BALANCED, PATH_TILED, PATH_GENERIC };
+enum ProductPath { PATH_DEFAULT = 0, PATH_BLOCKED, PATH_BALANCED, PATH_TILED, PATH_GENERIC, PATH_SPLIT };
 struct Options {
     int stream_nt;  // -1 by size, 0 off, 1 on
     int product_path;

@@ -362,6 +362,8 @@ struct BlkParams {
     int lpr_log;    // log2(lanes per row)
     int rows_per_wg;
     int kpl;        // output blocks per lane
+    int split_log;  // small-batch kernels: log2 of the partner splits S per output block
+    int wpr_log;    // small-batch kernels: log2 of the workgroups per row
 };
 
 // Stage NOPS (2 or 3) row-major operands s0, s1[, s2] for the workgroup's rows
@@ -588,6 +590,150 @@ __global__ __launch_bounds__(256) void prod_bwd_blk(const float* __restrict__ A,
             for (int q = 0; q < 4; ++q)
                 o[(h << 2) + q] = make_float4(gb[4 * q], gb[4 * q + 1], gb[4 * q + 2], gb[4 * q + 3]);
         }
+    }
+}
+
+// ---- small-batch kernels (10 <= n <= 12): the partner loop split over lanes ----
+// At batches of a few rows the one-lane-per-output-block kernels run one or
+// two waves per row, so a row of n = 12 takes 256 dependent block pairs on one
+// lane (0.65 ms at batch 1). Here a workgroup of 256 lanes owns G = 256 / S
+// output blocks of one row: lane (o, s) walks partners ih = s, s + S, ... (NB / S
+// of them, the pairs the op keeps), then the S partial blocks of each output
+// are summed in LDS in a fixed order. S = NB / 4, so every lane walks 4
+// partners and a row spreads over NB / G workgroups, each staging the whole
+// row (the same row is read NB / G times: small batches only).
+__device__ __forceinline__ int split_slot(unsigned o, unsigned s, int split_log) {
+    // 20-float slots: the four float4 writes of 16 consecutive slots hit 16 bank groups
+    return (int)((o << split_log) + s) * 20;
+}
+
+template <int OP, bool LOWNEG>
+__global__ __launch_bounds__(256) void prod_fwd_split(const float* __restrict__ A, const float* __restrict__ B,
+                                                       float* __restrict__ C, BlkParams P) {
+    extern __shared__ float4 lds[];
+    const int n = P.n;
+    const unsigned NB = 1u << (n - 4);
+    const unsigned S = 1u << P.split_log;
+    const long long row = (long long)(blockIdx.x >> P.wpr_log);
+    const unsigned ogrp = blockIdx.x & ((1u << P.wpr_log) - 1u);
+    stage_rows<2>(lds, reinterpret_cast<const float4*>(A), reinterpret_cast<const float4*>(B), nullptr, row, 1, n);
+    __syncthreads();
+    const unsigned sl = threadIdx.x & (S - 1u), ol = threadIdx.x >> P.split_log;
+    const unsigned G = 256u >> P.split_log;
+    const unsigned kh = ogrp * G + ol;
+    const float4* la = lds;
+    const float4* lb = lds + (1 << (n - 2));
+    const unsigned fullh = NB - 1u;
+    float acc[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+    for (unsigned ih = sl; ih < NB; ih += S) {
+        const unsigned jh = ih ^ kh;
+        const HiSign hs = hi_sign<OP>(ih, jh, P.negh, P.nulh, fullh, P.nm1, P.mu);
+        if (!hs.valid) continue;
+        float av[16], bv[16];
+        load_blk(la, ih, av);
+        load_blk(lb, jh, bv);
+        apply_flips(bv, hs.mask, hs.mask ^ (cross_pi<OP>(ih, P.nm1) << 31));
+        fwd_block_dispatch<OP, LOWNEG>(acc, av, bv, ih, jh);
+    }
+    __syncthreads();  // the staged row is no longer read: the partials go over it
+    float* red = reinterpret_cast<float*>(lds);
+    {
+        float4* slot = reinterpret_cast<float4*>(red + split_slot(ol, sl, P.split_log));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) slot[q] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+    }
+    __syncthreads();
+    // lane i: element e = i & 15 of output ol = i >> 4 (G * 16 = 256 values... or fewer lanes busy)
+    const unsigned e = threadIdx.x & 15u, o2 = threadIdx.x >> 4;
+    for (unsigned o = o2; o < G; o += 16u) {
+        float v = 0.f;
+        for (unsigned k = 0; k < S; ++k) v += red[split_slot(o, k, P.split_log) + (int)e];
+        const unsigned ko = ogrp * G + o;
+        float* out = C + (row << n);
+        if (OP == OP_REGR) out[((fullh ^ ko) << 4) + (15u - e)] = v;
+        else out[(ko << 4) + e] = v;
+    }
+}
+
+template <int OP, bool LOWNEG>
+__global__ __launch_bounds__(256) void prod_bwd_split(const float* __restrict__ A, const float* __restrict__ B,
+                                                       const float* __restrict__ GC, float* __restrict__ GA,
+                                                       float* __restrict__ GB, BlkParams P) {
+    extern __shared__ float4 lds[];
+    const int n = P.n;
+    const unsigned NB = 1u << (n - 4);
+    const unsigned S = 1u << P.split_log;
+    const long long row = (long long)(blockIdx.x >> P.wpr_log);
+    const unsigned ogrp = blockIdx.x & ((1u << P.wpr_log) - 1u);
+    stage_rows<3>(lds, reinterpret_cast<const float4*>(A), reinterpret_cast<const float4*>(B),
+                  reinterpret_cast<const float4*>(GC), row, 1, n, P.ldg4 ? -1LL : (1LL << (n - 2)) - 1);
+    __syncthreads();
+    const unsigned sl = threadIdx.x & (S - 1u), ol = threadIdx.x >> P.split_log;
+    const unsigned G = 256u >> P.split_log;
+    const unsigned h = ogrp * G + ol;
+    const int D4 = 1 << (n - 2);
+    const float4* la = lds;
+    const float4* lb = lds + D4;
+    const float4* lg = lds + 2 * D4;
+    const unsigned fullh = NB - 1u;
+    const bool want_a = GA != nullptr, want_b = GB != nullptr;
+    const unsigned pi_h = cross_pi<OP>(h, P.nm1);
+    float ga[16], gb[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        ga[e] = 0.f;
+        gb[e] = 0.f;
+    }
+    for (unsigned m = sl; m < NB; m += S) {
+        const unsigned x = h ^ m;
+        const HiSign sa = hi_sign<OP>(h, m, P.negh, P.nulh, fullh, P.nm1, P.mu);  // (i, j) = (h, m)
+        const HiSign sb = hi_sign<OP>(m, h, P.negh, P.nulh, fullh, P.nm1, P.mu);  // (i, j) = (m, h)
+        const bool do_a = want_a && sa.valid, do_b = want_b && sb.valid;
+        if (!do_a && !do_b) continue;
+        float g[16];
+        if (OP == OP_REGR) load_blk_rev(lg, fullh ^ x, g);
+        else load_blk(lg, x, g);
+        if (do_a) {
+            float bv[16];
+            load_blk(lb, m, bv);
+            apply_flips(bv, sa.mask, sa.mask ^ (pi_h << 31));
+            ga_block_dispatch<OP, LOWNEG>(ga, bv, g, h, m);
+        }
+        if (do_b) {
+            const unsigned pm = cross_pi<OP>(m, P.nm1) << 31;
+            float av[16], gt[16];
+            load_blk(la, m, av);
+            apply_flips(av, sb.mask, sb.mask ^ pm);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) gt[e] = (cpopc((unsigned)e) & 1) ? flip(g[e], pm) : g[e];
+            gb_block_dispatch<OP, LOWNEG>(gb, av, gt, m, h);
+        }
+    }
+    __syncthreads();  // the staged row is no longer read: the partials go over it
+    float* red = reinterpret_cast<float*>(lds);
+    const int half = (int)(256u * 20u);  // gb partials after the ga partials
+    {
+        float4* sa4 = reinterpret_cast<float4*>(red + split_slot(ol, sl, P.split_log));
+        float4* sb4 = reinterpret_cast<float4*>(red + half + split_slot(ol, sl, P.split_log));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            sa4[q] = make_float4(ga[4 * q], ga[4 * q + 1], ga[4 * q + 2], ga[4 * q + 3]);
+            sb4[q] = make_float4(gb[4 * q], gb[4 * q + 1], gb[4 * q + 2], gb[4 * q + 3]);
+        }
+    }
+    __syncthreads();
+    const unsigned e = threadIdx.x & 15u, o2 = threadIdx.x >> 4;
+    for (unsigned o = o2; o < G; o += 16u) {
+        float va = 0.f, vb = 0.f;
+        for (unsigned k = 0; k < S; ++k) {
+            va += red[split_slot(o, k, P.split_log) + (int)e];
+            vb += red[half + split_slot(o, k, P.split_log) + (int)e];
+        }
+        const long long at = (row << n) + (long long)(((ogrp * G + o) << 4) + e);
+        if (want_a) GA[at] = va;
+        if (want_b) GB[at] = vb;
     }
 }
 
@@ -2813,6 +2959,31 @@ static unsigned bal_grid(const void* kernel, const BlkParams& P) {
     return resident_grid(kernel, 256, 0, (groups + 3) / 4);
 }
 
+// Small-batch kernels: 10 <= n <= 12 (whole row in LDS) when the one-lane-
+// per-output-block kernels would run fewer than 512 waves (batch * NB < 2^15);
+// CLF_PRODUCT_PATH=split forces them at any batch, =blocked or =balanced
+// turn them off.
+static bool split_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, bool& lowneg, bool fwd, dim3& grid,
+                       size_t& lds_bytes) {
+    if (n < 10 || n > 12) return false;
+    const int pp = options().product_path;
+    if (pp == PATH_BLOCKED || pp == PATH_BALANCED || pp == PATH_TILED || pp == PATH_GENERIC) return false;
+    const long long NB = 1LL << (n - 4);
+    if (pp != PATH_SPLIT && P.batch * NB >= (1LL << 15)) return false;
+    if (!blocked_metric(op, n, neg, nul, lowneg)) return false;
+    block_sign_params(n, neg, nul, P);
+    P.split_log = n - 6;                 // S = NB / 4: four partners per lane
+    const int g_log = 8 - P.split_log;   // G = 256 / S output blocks per workgroup
+    P.wpr_log = (n - 4) - g_log;
+    const long long wgs = P.batch << P.wpr_log;
+    if (wgs > kMaxGrid) return false;
+    grid = dim3((unsigned)wgs);
+    const size_t stage = (size_t)(fwd ? 2 : 3) * ((size_t)4 << n);
+    const size_t red = (size_t)(fwd ? 1 : 2) * 256 * 20 * sizeof(float);
+    lds_bytes = stage > red ? stage : red;
+    return true;
+}
+
 template <int OP, bool LN>
 static void launch_fwd_bal(hipStream_t s, const float* A, const float* B, float* C, const BlkParams& P) {
     const dim3 g(bal_grid((const void*)prod_fwd_bal<OP, LN>, P));
@@ -2868,7 +3039,18 @@ int product_fwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
     dim3 g, bl;
     size_t lds = 0;
     const bool force_tiled = n >= 12 && tiled_forced(), force_generic = generic_forced();
-    if (out7_plan(op, n, neg, nul, P, ln)) {
+    if (split_plan(op, n, neg, nul, P, ln, true, g, lds)) {
+#define CLF_FWD_SPLIT(OPV, LNV) hipLaunchKernelGGL((prod_fwd_split<OPV, LNV>), g, dim3(256), lds, s, a, b, c, P)
+        switch (op) {
+            case OP_GEOM: if (ln) CLF_FWD_SPLIT(OP_GEOM, true); else CLF_FWD_SPLIT(OP_GEOM, false); break;
+            case OP_INNER: if (ln) CLF_FWD_SPLIT(OP_INNER, true); else CLF_FWD_SPLIT(OP_INNER, false); break;
+            case OP_LC: if (ln) CLF_FWD_SPLIT(OP_LC, true); else CLF_FWD_SPLIT(OP_LC, false); break;
+            case OP_RC: if (ln) CLF_FWD_SPLIT(OP_RC, true); else CLF_FWD_SPLIT(OP_RC, false); break;
+            case OP_WEDGE: CLF_FWD_SPLIT(OP_WEDGE, false); break;
+            case OP_REGR: CLF_FWD_SPLIT(OP_REGR, false); break;
+        }
+#undef CLF_FWD_SPLIT
+    } else if (out7_plan(op, n, neg, nul, P, ln)) {
         if (op == OP_INNER) launch_out7<OP_INNER>(s, ln, a, b, c, P);
         else if (op == OP_LC) launch_out7<OP_LC>(s, ln, a, b, c, P);
         else if (op == OP_RC) launch_out7<OP_RC>(s, ln, a, b, c, P);
@@ -2948,7 +3130,19 @@ int product_bwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
     dim3 g, bl;
     size_t lds = 0;
     const bool force_tiled = n >= 12 && tiled_forced(), force_generic = generic_forced();
-    if (frame_plan(op, n, neg, nul, P, ln)) {
+    if (split_plan(op, n, neg, nul, P, ln, false, g, lds)) {
+#define CLF_BWD_SPLIT(OPV, LNV) \
+    hipLaunchKernelGGL((prod_bwd_split<OPV, LNV>), g, dim3(256), lds, s, a, b, gc, ga, gb, P)
+        switch (op) {
+            case OP_GEOM: if (ln) CLF_BWD_SPLIT(OP_GEOM, true); else CLF_BWD_SPLIT(OP_GEOM, false); break;
+            case OP_INNER: if (ln) CLF_BWD_SPLIT(OP_INNER, true); else CLF_BWD_SPLIT(OP_INNER, false); break;
+            case OP_LC: if (ln) CLF_BWD_SPLIT(OP_LC, true); else CLF_BWD_SPLIT(OP_LC, false); break;
+            case OP_RC: if (ln) CLF_BWD_SPLIT(OP_RC, true); else CLF_BWD_SPLIT(OP_RC, false); break;
+            case OP_WEDGE: CLF_BWD_SPLIT(OP_WEDGE, false); break;
+            case OP_REGR: CLF_BWD_SPLIT(OP_REGR, false); break;
+        }
+#undef CLF_BWD_SPLIT
+    } else if (frame_plan(op, n, neg, nul, P, ln)) {
         launch_frame(n, ln, s, a, b, gc, ga, gb, P);
     } else if (contr_plan(op, n, neg, nul, P, ln)) {
         if (op == OP_LC) launch_contr<OP_LC>(n, ln, s, a, b, gc, ga, gb, P);

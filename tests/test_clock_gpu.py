@@ -16,10 +16,14 @@ def test_clock_sample_gives_a_plausible_engine_clock():
     slots = 4096
     buf = torch.zeros(2, 3 * slots, dtype=torch.int64, device="cuda")
     s = torch.cuda.current_stream().cuda_stream
-    x = torch.randn(1 << 24, device="cuda")
+    # keep the GPU busy between the samples (an idle GPU lowers its clock, and
+    # the first matrix product of a process spends a while loading its library)
+    m = torch.randn(4096, 4096, device="cuda")
+    m = torch.mm(m, m) * 1e-2
+    torch.cuda.synchronize()
     _lib.check(lib.clf_clock_sample(buf[0].data_ptr(), slots, s), "clf_clock_sample")
-    for _ in range(50):
-        x = x * 1.0001 + 0.5
+    for _ in range(8):
+        m = torch.mm(m, m) * 1e-2
     _lib.check(lib.clf_clock_sample(buf[1].data_ptr(), slots, s), "clf_clock_sample")
     torch.cuda.synchronize()
     h = buf.cpu().view(2, slots, 3).tolist()
@@ -39,4 +43,4 @@ def test_clock_sample_gives_a_plausible_engine_clock():
     ghz.sort()
     print(f"[clock] {len(common)} compute units, median {ghz[len(ghz) // 2]:.3f} GHz, "
           f"range {ghz[0]:.3f} .. {ghz[-1]:.3f}", flush=True)
-    assert 0.3 < ghz[len(ghz) // 2] < 4.0
+    assert 0.5 < ghz[len(ghz) // 2] < 4.0

@@ -48,7 +48,10 @@ PRODUCT_CASES = [
     ("geom", (1,) * 9 + (0,), {"CLF_SPLIT_PATH": "pairs"}),
     ("lc", (1,) * 9 + (0,), {}),
     ("inner", (1,) * 9 + (0,), {}),
-    ("geom", (1,) * 12, {}),                                      # blocked at n = 12
+    ("geom", (1,) * 12, {"CLF_PRODUCT_PATH": "blocked"}),         # blocked at n = 12
+    ("geom", (1,) * 12, {}),                                      # small-batch split kernels
+    ("regressive", (1,) * 11, {}),
+    ("inner", (1,) * 9 + (0,), {"CLF_PRODUCT_PATH": "split"}),
     ("wedge", (1,) * 12, {"CLF_PRODUCT_PATH": "tiled"}),
 ]
 

@@ -54,7 +54,7 @@ def test_tiled_equals_whole_row_n12(op, metric, clf_env):
         pytest.skip("regressive is undefined for degenerate metrics")
     a, b, gc = inputs(12, 3, 12)
     print(f"[case] n=12 op={op} metric={metric}", flush=True)
-    e = compare(run(op, metric, a, b, gc, clf_env), run(op, metric, a, b, gc, clf_env, "tiled"))
+    e = compare(run(op, metric, a, b, gc, clf_env, "blocked"), run(op, metric, a, b, gc, clf_env, "tiled"))
     assert max(e) <= TOL, e
 
 
