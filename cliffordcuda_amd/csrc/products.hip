@@ -23,6 +23,7 @@
 #include <utility>
 
 #include "clf_common.h"
+#include "contr5_schedule.h"
 
 namespace clf {
 
@@ -2316,6 +2317,249 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     }
 }
 
+// ---- left and right contraction backward on 5 high bits --------------------
+// n = 9, and n = 10 whose only null generator is the top one (C5's Cl(9,0,1)).
+// With e9 null and rightmost in every blade, a = a0 + a1 e9 and b = b0 + b1 e9
+// (halves of 512 floats), the left contraction's pairs with e9 in the
+// contracted blade vanish and those with e9 in b only append e9, so
+//   ga0 = ga9(b0, gc0) + ga9(b1, gc1),  ga1 = 0,  gb0 = gb9(a0, gc0),  gb1 = gb9(a0, gc1)
+// with the n = 9 left contraction of e0..e8: two n = 9 problems sharing a0 (a1
+// is never read). A wave runs two problems of 32 lanes (two rows at n = 9, the
+// two halves at n = 10) on the frame schedule of prod_bwd_contr_frame (sub
+// pairs read the partner reversed into a reversed-frame accumulator, one sup
+// pattern for every lane) with the lane schedule of contr5_schedule.h: 16
+// steps per lane in three pieces (steps 0-7, 8-11, 12-15), each its own
+// accumulator, so a lane starts a fresh accumulator at the same steps as every
+// other lane and no step needs a per-lane conditional zeroing. A lane's pieces
+// are its own outputs (|h| = 2, 3: one per piece), parts of one output (|h| =
+// 0, 1, 4, 5: summed), or a helper item (a small output of another lane, or a
+// 4-pair chunk of output 0's or 31's 32-pair list, added by its owner through
+// LDS). The pair order inside pieces, the slot of each h and the blocks' LDS
+// slot swizzle were chosen (a search on the CPU) to keep each quarter-wave's
+// 16 block reads on distinct bank groups. Finished blocks are staged in LDS
+// and leave in row order.
+
+__device__ __forceinline__ unsigned swz5(unsigned blk) { return (unsigned)(kContr5Swz >> (2u * blk)) & 3u; }
+
+// an accumulator's output block, turned to the normal frame if its mode was
+// sub, with the gb reversion signs: y[k] = contr_out_sub(x, k) or contr_out_sup(x, k)
+template <bool LOWNEG, bool KLC>
+__device__ __forceinline__ void contr5_result(const float (&x)[16], bool sub, float (&y)[16]) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const float ys = contr_out_sub<LOWNEG, KLC>(x, k);
+        const float yp = contr_out_sup<!KLC>(x, k);
+        y[k] = sub ? ys : yp;
+    }
+}
+
+template <int OP, bool LOWNEG, bool NULLTOP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void prod_bwd_contr5(
+    const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ GC, float* __restrict__ GA,
+    float* __restrict__ GB, BlkParams P) {
+    static_assert(OP == OP_LC || OP == OP_RC, "contractions only");
+    static_assert(!NULLTOP || OP == OP_LC, "the null-top split is the left contraction's");
+    constexpr int N = NULLTOP ? 10 : 9;
+    constexpr int R = NULLTOP ? 1 : 2;  // rows per wave
+    constexpr bool kLC = OP == OP_LC;
+    constexpr unsigned full = 31u;
+    // per wave (float4): a at 0 (two rows of 128; NULLTOP: a0 only), b at 256, gc at 512, a zero block at 768
+    __shared__ __attribute__((aligned(64))) float4 lds[4][3 * 256 + 4];
+    __shared__ unsigned tab[16][64];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const unsigned slot = (unsigned)lane & 31u, prob = (unsigned)lane >> 5;
+    const long long ngrp = (P.batch + R - 1) / R;
+    const long long grp = (long long)blockIdx.x * 4 + wave;
+    const BalLane L = bal_lane(N, lane);
+    const bool gbc = P.ldg4 == 0;
+    BalPre pa;
+    {
+        const BalSrc sa = bal_src(A, grp, P.batch, N, R);
+        if constexpr (NULLTOP) {  // a0 only: chunks 0, 1 of the row
+#pragma unroll
+            for (int i = 0; i < 2; ++i) pa.v[i] = sa.g0[L.ff[i]];
+        } else {
+            pa = bal_fetch(sa, L, N - 2);
+        }
+    }
+    const BalPre pb = bal_fetch(bal_src(B, grp, P.batch, N, R), L, N - 2);
+    const BalPre pg = bal_fetch(bal_src(GC, grp, P.batch, N, R, gbc), L, N - 2);
+    // step entries: partner float4 offset (bits 0-9), gc float4 offset (10-19), then the
+    // flips of prod_bwd_contr_frame: pair sign S (23), parity term (24), w1 (25), w2 (26),
+    // rho (27), gc parity (28)
+    if (wave == 0) {
+        for (int t = 0; t < 16; ++t) {
+            const unsigned st = kContr5Steps[slot][t];
+            unsigned e;
+            if (st & 2048u) {  // idle: the zero block
+                e = 768u | (768u << 10);
+            } else {
+                const unsigned o = st & 31u, p = (st >> 5) & 31u, sub = (st >> 10) & 1u;
+                const unsigned gb = kLC ? sub : sub ^ 1u;
+                const unsigned podd = (unsigned)__popc(p) & 1u, oodd = (unsigned)__popc(o) & 1u;
+                const HiSign hs = gb ? hi_sign<OP_INNER>(p, o, P.negh, 0u, full, 0, 0)
+                                     : hi_sign<OP_INNER>(o, p, P.negh, 0u, full, 0, 0);
+                const unsigned pm = (gb ? podd : oodd) ^ (LOWNEG ? sub : 0u);
+                const unsigned x = o ^ p;
+                // partner: gb steps read a (NULLTOP: a0, row 0), ga steps read b (the problem's row)
+                const unsigned prow = (NULLTOP && gb) ? 0u : prob;
+                const unsigned pw = (gb ? 0u : 256u) + prow * 128u + ((p << 2) | (swz5(p) ^ (sub ? 3u : 0u)));
+                const unsigned pg4 = 512u + prob * 128u + ((x << 2) | swz5(x));
+                e = pw | (pg4 << 10) | ((hs.mask >> 31) << 23) | (pm << 24) | ((gb & sub) << 25) |
+                    (((gb ^ 1u) & sub) << 26) | (gb << 27) | ((gb & podd) << 28);
+            }
+            tab[t][lane] = e;
+        }
+    }
+    __syncthreads();
+    if (grp >= ngrp) return;
+    float4* sw = lds[wave];
+    const unsigned base = lds_addr4(sw);
+    {
+        // a and b in the frame layout (component c of a chunk in float4 slot q goes to
+        // component c ^ q), gc as it is; slot q of block blk at (blk << 2) | (q ^ swz5(blk))
+        const unsigned fq = (unsigned)lane & 3u;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const unsigned c = (unsigned)lane + 64u * (unsigned)i;
+            const unsigned hr = c >> 7, f = c & 127u, blk = f >> 2;
+            const unsigned so = 16u * (hr * 128u + ((blk << 2) | ((f & 3u) ^ swz5(blk))));
+            const unsigned ad = (base + so) | (fq << 2);
+            const float vb[4] = {pb.v[i].x, pb.v[i].y, pb.v[i].z, pb.v[i].w};
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc)
+                *(__attribute__((address_space(3))) float*)(uintptr_t)((ad ^ ((unsigned)cc << 2)) + 4096u) = vb[cc];
+            if (!NULLTOP || i < 2) {
+                const float va[4] = {pa.v[i].x, pa.v[i].y, pa.v[i].z, pa.v[i].w};
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc)
+                    *(__attribute__((address_space(3))) float*)(uintptr_t)(ad ^ ((unsigned)cc << 2)) = va[cc];
+            }
+            lds_st4(base + 8192u + so, pg.v[i]);
+        }
+        if (lane < 4) lds_st4(base + 16u * (768u + (unsigned)lane), make_float4(0.f, 0.f, 0.f, 0.f));
+    }
+    wave_lds_sync();
+    float acc[16], y1[16], y2[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+    auto step = [&](auto tc) {
+        constexpr int t = decltype(tc)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        unsigned e = tab[t][lane];
+        asm volatile("" : "+v"(e));
+        const unsigned w0 = base + ((e & 1023u) << 4);
+        const unsigned g0 = base + (((e >> 10) & 1023u) << 4);
+        unsigned ms = (e << 8) & 0x80000000u, mp = (e << 7) & 0x80000000u, m1 = (e << 6) & 0x80000000u;
+        unsigned m2 = (e << 5) & 0x80000000u, mr = (e << 4) & 0x80000000u, mg = (e << 3) & 0x80000000u;
+        asm volatile("" : "+v"(ms), "+v"(mp), "+v"(m1), "+v"(m2), "+v"(mr), "+v"(mg));
+        float g[16], w[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 vg = lds_ld4(g0 ^ ((unsigned)q << 4));
+            const float4 vw = lds_ld4(w0 ^ ((unsigned)q << 4));
+            g[4 * q] = vg.x;
+            g[4 * q + 1] = vg.y;
+            g[4 * q + 2] = vg.z;
+            g[4 * q + 3] = vg.w;
+            w[4 * q] = vw.x;
+            w[4 * q + 1] = vw.y;
+            w[4 * q + 2] = vw.z;
+            w[4 * q + 3] = vw.w;
+        }
+        unsigned x1 = ms ^ mp, x2 = ms ^ mr, x3 = x1 ^ mr, y3 = m1 ^ m2, gpr = mg ^ mr;
+        asm volatile("" : "+v"(x1), "+v"(x2), "+v"(x3), "+v"(y3), "+v"(gpr));
+#pragma unroll
+        for (int el = 0; el < 16; ++el) {
+            const unsigned xa = par4(el) ? (rho4(el) ? x3 : x1) : (rho4(el) ? x2 : ms);
+            const int wcl = w1b(el) + 2 * w2b(el);
+            const unsigned u = __float_as_uint(w[fr_reg(el)]);
+            w[fr_reg(el)] = __uint_as_float(wcl == 0 ? u ^ xa : u ^ xa ^ (wcl == 1 ? m1 : wcl == 2 ? m2 : y3));
+            if (par4(el) || rho4(el)) g[el] = flip(g[el], par4(el) && rho4(el) ? gpr : par4(el) ? mg : mr);
+        }
+        frame_sup<LOWNEG, true, false>(acc, acc, w, w, g, g, std::make_integer_sequence<int, 256>{});
+        if constexpr (t == 7 || t == 11) {  // a piece ends: keep it, start from zero
+#pragma unroll
+            for (int el = 0; el < 16; ++el) {
+                if constexpr (t == 7) y1[el] = acc[el];
+                else y2[el] = acc[el];
+                acc[el] = 0.f;
+            }
+        }
+    };
+    frame_steps(step, std::make_integer_sequence<int, 16>{});
+    // acc holds the third piece (steps 12-15)
+    wave_lds_sync();  // every block read of the wave is done: its LDS takes the results
+    const unsigned dU = kContr5Out[slot][0], dV = kContr5Out[slot][1], dW = kContr5Out[slot][2];
+    const unsigned chunk_f4 = 512u + prob * 128u;  // the problem's chunk slots (4 float4 each), over its gc rows
+    if ((dW >> 6) >= 4u) {  // a helper chunk of output 0 or 31: to its slot
+        const unsigned a = base + 16u * (chunk_f4 + 4u * ((dW >> 6) - 4u));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) lds_st4(a + 16u * (unsigned)q, make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]));
+    }
+    wave_lds_sync();
+    float u[16];
+    const unsigned hU = dU >> 6;
+#pragma unroll
+    for (int el = 0; el < 16; ++el) u[el] = hU == 1u ? y1[el] : (y1[el] + y2[el]) + acc[el];
+    if (hU == 3u) {  // outputs 0 and 31 add their four helper chunks, in order
+        const unsigned a = base + 16u * (chunk_f4 + ((dU & 32u) ? 16u : 0u));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 v = lds_ld4(a + 16u * (4u * (unsigned)k + (unsigned)q));
+                u[4 * q] += v.x;
+                u[4 * q + 1] += v.y;
+                u[4 * q + 2] += v.z;
+                u[4 * q + 3] += v.w;
+            }
+        }
+    }
+    wave_lds_sync();
+    // results into the staging rows: ga blocks over a (row = problem), gb blocks over b
+    auto put = [&](const float (&x)[16], unsigned d) {
+        const unsigned blk = d & 31u;
+        const bool sub = (d >> 5) & 1u;
+        const bool gbk = kLC ? sub : !sub;
+        float y[16];
+        contr5_result<LOWNEG, kLC>(x, sub, y);
+        const unsigned rowb = base + 16u * ((gbk ? 256u : 0u) + prob * 128u);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            lds_st4(rowb + 16u * ((blk << 2) | ((unsigned)q ^ swz5(blk))), make_float4(y[4 * q], y[4 * q + 1], y[4 * q + 2], y[4 * q + 3]));
+    };
+    put(u, dU);
+    if (dV >> 6) put(y2, dV);
+    if ((dW >> 6) == 1u) put(acc, dW);
+    wave_lds_sync();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const unsigned c = (unsigned)lane + 64u * (unsigned)i;
+        const unsigned hr = c >> 7, f = c & 127u, blk = f >> 2;
+        const unsigned so = 16u * (hr * 128u + ((blk << 2) | ((f & 3u) ^ swz5(blk))));
+        if constexpr (NULLTOP) {
+            const long long at = (grp << 8) + (long long)c;  // float4 of the row: half hr, float4 f
+            if (GA) {
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (hr == 0u) {  // ga0 = the two problems' ga
+                    const float4 p0 = lds_ld4(base + so), p1 = lds_ld4(base + 2048u + so);
+                    v = make_float4(p0.x + p1.x, p0.y + p1.y, p0.z + p1.z, p0.w + p1.w);
+                }
+                reinterpret_cast<float4*>(GA)[at] = v;
+            }
+            if (GB) reinterpret_cast<float4*>(GB)[at] = lds_ld4(base + 4096u + so);
+        } else {
+            const long long row = grp * 2 + (long long)hr;
+            if (row < P.batch) {
+                const long long at = (row << 7) + (long long)f;
+                if (GA) reinterpret_cast<float4*>(GA)[at] = lds_ld4(base + so);
+                if (GB) reinterpret_cast<float4*>(GB)[at] = lds_ld4(base + 4096u + so);
+            }
+        }
+    }
+}
+
 // ---- inner, lc and rc forward at n = 7: one lane per output block ---------
 // Output block o of a row takes, for every partner S inside ~o, the lc half
 // (a[S], b[S | o], il inside jl) and the rc half (a[S | o], b[S], jl inside
@@ -2937,6 +3181,52 @@ static void launch_contr(int n, bool ln, hipStream_t s, const float* A, const fl
 #undef CLF_CONTR_N
 }
 
+// prod_bwd_contr5: lc and rc at n = 9 without null generators, lc at n = 10
+// whose only null generator is e9 (low generators of one metric value).
+static bool contr5_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, bool& lowneg, bool& nulltop) {
+    if (op != OP_LC && op != OP_RC) return false;
+    if (options().product_path != PATH_DEFAULT) return false;
+    if (n == 9 && nul == 0u) nulltop = false;
+    else if (n == 10 && nul == (1u << 9) && op == OP_LC) nulltop = true;
+    else return false;
+    if (!blocked_metric(op, n, neg, nul, lowneg)) return false;
+    block_sign_params(n, neg, nul, P);
+    P.negh = (neg >> 4) & 31u;  // the n = 9 problem's high generators
+    P.nulh = 0u;
+    return true;
+}
+
+template <int OP, bool LN, bool NT>
+static void launch_contr5_t(hipStream_t s, const float* A, const float* B, const float* GCp, float* GA, float* GB,
+                            const BlkParams& P) {
+    const long long R = NT ? 1 : 2;
+    const long long chunk = kMaxGrid * 4 * R;
+    const long long D = NT ? 1024 : 512;
+    for (long long r0 = 0; r0 < P.batch; r0 += chunk) {
+        BlkParams Q = P;
+        Q.batch = P.batch - r0 < chunk ? P.batch - r0 : chunk;
+        const long long groups = (Q.batch + R - 1) / R;
+        const dim3 g((unsigned)((groups + 3) / 4));
+        const long long off = r0 * D;
+        hipLaunchKernelGGL((prod_bwd_contr5<OP, LN, NT>), g, dim3(256), 0, s, A + off, B + off,
+                           GCp + (P.ldg4 ? off : 0), GA ? GA + off : nullptr, GB ? GB + off : nullptr, Q);
+    }
+}
+
+static void launch_contr5(int op, bool ln, bool nt, hipStream_t s, const float* A, const float* B, const float* GCp,
+                          float* GA, float* GB, const BlkParams& P) {
+    if (nt) {
+        if (ln) launch_contr5_t<OP_LC, true, true>(s, A, B, GCp, GA, GB, P);
+        else launch_contr5_t<OP_LC, false, true>(s, A, B, GCp, GA, GB, P);
+    } else if (op == OP_LC) {
+        if (ln) launch_contr5_t<OP_LC, true, false>(s, A, B, GCp, GA, GB, P);
+        else launch_contr5_t<OP_LC, false, false>(s, A, B, GCp, GA, GB, P);
+    } else {
+        if (ln) launch_contr5_t<OP_RC, true, false>(s, A, B, GCp, GA, GB, P);
+        else launch_contr5_t<OP_RC, false, false>(s, A, B, GCp, GA, GB, P);
+    }
+}
+
 // Balanced kernels: wedge, lc, rc, regressive and the inner product for
 // 4 <= n <= 10 (CLF_PRODUCT_PATH=blocked keeps them on the one-lane-per-output
 // kernels). Up to n = 8 the inner product's backward runs on the per-lane
@@ -3126,7 +3416,7 @@ int product_bwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
     BlkParams P{};
     P.batch = batch;
     P.ldg4 = ldg >> 2;
-    bool ln = false;
+    bool ln = false, nt5 = false;
     dim3 g, bl;
     size_t lds = 0;
     const bool force_tiled = n >= 12 && tiled_forced(), force_generic = generic_forced();
@@ -3144,6 +3434,8 @@ int product_bwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
 #undef CLF_BWD_SPLIT
     } else if (frame_plan(op, n, neg, nul, P, ln)) {
         launch_frame(n, ln, s, a, b, gc, ga, gb, P);
+    } else if (contr5_plan(op, n, neg, nul, P, ln, nt5)) {
+        launch_contr5(op, ln, nt5, s, a, b, gc, ga, gb, P);
     } else if (contr_plan(op, n, neg, nul, P, ln)) {
         if (op == OP_LC) launch_contr<OP_LC>(n, ln, s, a, b, gc, ga, gb, P);
         else if (op == OP_RC) launch_contr<OP_RC>(n, ln, s, a, b, gc, ga, gb, P);

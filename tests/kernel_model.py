@@ -800,3 +800,131 @@ def fwd7_step(h, t):
         return (7, 0) if t == 0 else (None if t == 1 else (0, t + 4))
     parts = subsets(7 & ~h)
     return (h, parts[t]) if t < len(parts) else None
+
+
+# ---- prod_bwd_contr5: contraction backward on 5 high bits -------------------
+def contr5_schedule_module():
+    """cliffordcuda_amd/csrc/gen_contr5_schedule.py, the generator of the lane
+    schedule the kernel compiles in (contr5_schedule.h)."""
+    import importlib.util
+    import os
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "cliffordcuda_amd", "csrc",
+                        "gen_contr5_schedule.py")
+    spec = importlib.util.spec_from_file_location("gen_contr5_schedule", path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def _contr5_problem(op, a, b, gc, negh, lowneg, sched):
+    """One n = 9 problem as prod_bwd_contr5 runs it: per lane slot, 16 steps of
+    the frame schedule (contraction_frame_backward's per-pair arithmetic) in
+    three pieces, then the lane's outputs U, V, W (and the helper chunks added
+    to outputs 0 and 31) turned to the normal frame. Returns (ga, gb) blocks."""
+    steps, outs = sched.steps_by_slot(), sched.outputs_by_slot()
+    rows = a.shape[:-1]
+    full = 31
+
+    def yields_gb(sub):
+        return sub if op == LC else not sub
+
+    def contrib(o, p, sub):
+        X = o ^ p
+        g = gc[..., X * 16:(X + 1) * 16]
+        podd, oodd = popc(p) & 1, popc(o) & 1
+        w = []
+        for q in range(16):
+            e = 15 - q if sub else q
+            par = popc(q) & 1
+            if yields_gb(sub):
+                _, s = hi_sign(INNER, p, o, negh, 0, full, 0, 0)
+                f = s * (-1 if par and podd else 1) * (-1 if sub and (_frame_w1(q) ^ (lowneg & par)) else 1)
+                w.append(f * _rho(q) * a[..., p * 16 + e])
+            else:
+                _, s = hi_sign(INNER, o, p, negh, 0, full, 0, 0)
+                f = s * (-1 if par and oodd else 1) * (-1 if sub and (_frame_w2(q) ^ (lowneg & par)) else 1)
+                w.append(f * b[..., p * 16 + e])
+        if yields_gb(sub):
+            gg = [g[..., x] * (-1.0 if (popc(x) & 1 and podd) else 1.0) * _rho(x) for x in range(16)]
+        else:
+            gg = [g[..., x] for x in range(16)]
+        acc = np.zeros(rows + (16,))
+        for oo in range(16):
+            for q in range(16):
+                if oo & ~q & 15:
+                    continue
+                acc[..., oo] += low_sign(LC, lowneg, oo, q) * w[q] * gg[oo ^ q]
+        return acc
+
+    fa = [(_frame_w1(k) ^ (lowneg & popc(k))) & 1 for k in range(16)]
+    fb = [(_frame_w2(k) ^ (lowneg & popc(k))) & 1 for k in range(16)]
+
+    def result(x, sub):
+        if yields_gb(sub):
+            x = x * np.array([_rho(k) for k in range(16)])
+        if sub:
+            f = fb if yields_gb(sub) else fa
+            x = np.stack([(-1.0 if f[k] else 1.0) * x[..., 15 - k] for k in range(16)], -1)
+        return x
+
+    pieces = []
+    for slot in range(32):
+        ys = []
+        for t0, t1 in sched.PIECES:
+            acc = np.zeros(rows + (16,))
+            for t in range(t0, t1):
+                if steps[slot][t] is not None:
+                    acc = acc + contrib(*steps[slot][t])
+            ys.append(acc)
+        pieces.append(ys)
+    chunks = {}
+    for slot in range(32):
+        W = outs[slot][2]
+        if W is not None and isinstance(W[2], tuple):
+            chunks[W[2][1]] = pieces[slot][2]
+    ga = np.zeros(a.shape)
+    gb = np.zeros(b.shape)
+    seen = set()
+
+    def put(blk, sub, x):
+        assert (blk, sub) not in seen
+        seen.add((blk, sub))
+        dst = gb if yields_gb(sub) else ga
+        dst[..., blk * 16:(blk + 1) * 16] = result(x, sub)
+
+    for slot in range(32):
+        U, V, W = outs[slot]
+        y1, y2, y3 = pieces[slot]
+        u = y1 if U[2] == "y1" else (y1 + y2) + y3
+        if U[2] == "sum3+chunks":
+            base = 4 if U[1] else 0
+            for k in range(4):
+                u = u + chunks[base + k]
+        put(U[0], U[1], u)
+        if V is not None:
+            put(V[0], V[1], y2)
+        if W is not None and W[2] == "y3":
+            put(W[0], W[1], y3)
+    assert len(seen) == 64
+    return ga, gb
+
+
+def contraction5_backward(op, a, b, gc, metric):
+    """prod_bwd_contr5's backward: lc or rc at n = 9 (no null generator), or lc
+    at n = 10 whose only null generator is e9 (two n = 9 problems sharing a0:
+    ga0 = ga9(b0, gc0) + ga9(b1, gc1), ga1 = 0, gb0 = gb9(a0, gc0), gb1 =
+    gb9(a0, gc1)). Returns (ga, gb)."""
+    sched = contr5_schedule_module()
+    n = len(metric)
+    neg = sum(1 << k for k, m in enumerate(metric) if m == -1)
+    lowneg = (neg & 15) == 15
+    negh = (neg >> 4) & 31
+    if n == 9:
+        assert 0 not in metric
+        return _contr5_problem(op, a, b, gc, negh, lowneg, sched)
+    assert n == 10 and op == LC and metric[9] == 0 and 0 not in metric[:9]
+    h = 512
+    ga0p, gb0 = _contr5_problem(LC, a[..., :h], b[..., :h], gc[..., :h], negh, lowneg, sched)
+    ga1p, gb1 = _contr5_problem(LC, a[..., :h], b[..., h:], gc[..., h:], negh, lowneg, sched)
+    ga = np.concatenate([ga0p + ga1p, np.zeros_like(a[..., h:])], -1)
+    return ga, np.concatenate([gb0, gb1], -1)

@@ -277,3 +277,62 @@ def test_inner_fwd7_schedule_covers_every_pair():
             seen[(o, S)] = seen.get((o, S), 0) + 1
     want = {(o, S): 1 for o in range(8) for S in K.subsets(7 & ~o)}
     assert seen == want
+
+
+def test_contr5_header_is_the_generators():
+    """csrc/contr5_schedule.h is what gen_contr5_schedule.py writes."""
+    import os
+    sched = K.contr5_schedule_module()
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "cliffordcuda_amd", "csrc",
+                        "contr5_schedule.h")
+    assert open(path).read() == sched.header_text()
+
+
+def test_contr5_schedule_covers_every_pair_once():
+    """Every (output, partner, mode) block pair of a 5-high-bit problem appears
+    exactly once across the 32 lanes' 16 steps (sub: p inside o, sup: p
+    containing o; the pair (o, o) once in each mode), and every output is
+    written by exactly one lane's U, V or W (outputs 0 and 31 also taking the
+    four helper chunks of their list)."""
+    sched = K.contr5_schedule_module()
+    seen = []
+    for row in sched.steps_by_slot():
+        for s in row:
+            if s is not None:
+                seen.append(s)
+    want = [(o, p, True) for o in range(32) for p in range(32) if p & ~o == 0]
+    want += [(o, p, False) for o in range(32) for p in range(32) if o & ~p == 0]
+    assert sorted(seen) == sorted(want)
+    outs = [d for slot in sched.outputs_by_slot() for d in slot if d is not None and not isinstance(d[2], tuple)]
+    assert sorted((d[0], d[1]) for d in outs) == sorted((o, s) for o in range(32) for s in (False, True))
+    assert sorted(sched.PERM) == list(range(32))
+
+
+def test_contr5_lds_conflicts_recorded():
+    """The searched layout's bank-conflict count (extra LDS cycles per problem
+    row, 64 read groups of 4 instructions) stays at its recorded value."""
+    sched = K.contr5_schedule_module()
+    assert sched.lds_conflicts() <= 62
+
+
+@pytest.mark.parametrize("op", [K.LC, K.RC])
+@pytest.mark.parametrize("metric", [(1,) * 9, (-1,) * 4 + (1, -1, 1, 1, -1), (1,) * 4 + (-1,) * 5])
+def test_contraction5_backward_n9(op, metric):
+    g = torch.Generator().manual_seed(9)
+    a, b, gc = (torch.randn(2, 512, generator=g, dtype=torch.float64) for _ in range(3))
+    ga, gb = K.contraction5_backward(op, a.numpy(), b.numpy(), gc.numpy(), metric)
+    at, bt = a.clone().requires_grad_(), b.clone().requires_grad_()
+    O.einsum_product("lc" if op == K.LC else "rc", at, bt, metric).backward(gc)
+    np.testing.assert_allclose(ga, at.grad.numpy(), rtol=0, atol=1e-10)
+    np.testing.assert_allclose(gb, bt.grad.numpy(), rtol=0, atol=1e-10)
+
+
+@pytest.mark.parametrize("metric", [(1,) * 9 + (0,), (1,) * 4 + (-1, 1, 1, -1, 1, 0), (-1,) * 9 + (0,)])
+def test_contraction5_backward_null_top(metric):
+    g = torch.Generator().manual_seed(10)
+    a, b, gc = (torch.randn(2, 1024, generator=g, dtype=torch.float64) for _ in range(3))
+    ga, gb = K.contraction5_backward(K.LC, a.numpy(), b.numpy(), gc.numpy(), metric)
+    at, bt = a.clone().requires_grad_(), b.clone().requires_grad_()
+    O.einsum_product("lc", at, bt, metric).backward(gc)
+    np.testing.assert_allclose(ga, at.grad.numpy(), rtol=0, atol=1e-10)
+    np.testing.assert_allclose(gb, bt.grad.numpy(), rtol=0, atol=1e-10)

@@ -109,15 +109,15 @@ def test_c2_cl61_six_products_full_batch():
             assert rel_err(lhs, rhs) <= 1e-5, op
 
 
-def test_c5_degenerate_n10(clf_env):
+def test_c5_degenerate_n10():
     """Cl(9,0,1), batch 16384. The left contraction fwd + bwd
     on its own (seeded upstream gradient, so its gradients are isolated), and the
     geometric product fwd + bwd with norm_sq and grade_projection(2) of it in
     the loss. Checks: the oracle on 8 rows of the batch (values and all
     gradients); the full batch by bilinearity of both forwards; bitwise row
     independence of both forwards and backwards (rows computed inside the full
-    batch equal the same rows computed alone, on the same kernels: a batch this
-    small would otherwise take the small-batch kernels)."""
+    batch equal the same rows computed in a batch of their own, large enough to
+    run on the same kernels)."""
     metric = (1,) * 9 + (0,)
     g = torch.Generator().manual_seed(0)
     B = 16384
@@ -171,14 +171,17 @@ def test_c5_degenerate_n10(clf_env):
             assert rel_err(lhs, rhs) <= TOL
 
     print("[case] C5 row independence", flush=True)
-    clf_env.setenv("CLF_PRODUCT_PATH", "balanced")
     idx = torch.tensor([0, 5, 6, 7, 4097, 8191, 12345, B - 3, B - 2, B - 1], device="cuda")
-    xs = ad[idx].clone().requires_grad_()
-    ys = bd[idx].clone().requires_grad_()
+    # the rows again inside a batch of 520 (52 copies): large enough for the kernels of the full batch
+    # (fewer than 512 rows of n = 10 take the small-batch kernels)
+    rep = idx.repeat(52)
+    xs = ad[rep].clone().requires_grad_()
+    ys = bd[rep].clone().requires_grad_()
     lcs = cl.left_contraction(xs, ys)
-    lcs.backward(glcd[idx])
-    assert torch.equal(lcs, lc[idx].detach())
-    assert torch.equal(xs.grad, lc_ga[idx]) and torch.equal(ys.grad, lc_gb[idx])
+    lcs.backward(glcd[rep])
+    k = len(idx)
+    assert torch.equal(lcs[:k], lc[idx].detach())
+    assert torch.equal(xs.grad[:k], lc_ga[idx]) and torch.equal(ys.grad[:k], lc_gb[idx])
     xs = ad[idx].clone().requires_grad_()
     ys = bd[idx].clone().requires_grad_()
     gps = cl.geom_prod(xs, ys)
