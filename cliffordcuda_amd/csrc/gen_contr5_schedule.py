@@ -1,31 +1,33 @@
-"""Lane schedule of prod_bwd_contr5 (csrc/products.hip): the left and right
-contraction's backward on 5 high bits (n = 9, and the two halves of n = 10
-with a null top generator). Writes csrc/contr5_schedule.h; tests/
+"""Lane schedules of prod_bwd_contr5 and prod_fwd_contr5 (csrc/products.hip):
+the left and right contraction on 5 high bits (n = 9, and the two halves of
+n = 10 with a null top generator). Writes csrc/contr5_schedule.h; tests/
 test_kernel_model.py rebuilds the header from this module and checks that it
-is the committed one, that the schedule covers every block pair once and that
-the CPU model of the kernel on it equals the oracle.
+is the committed one, that every schedule covers every block pair once and
+that the CPU model of the kernels on them equals the oracle.
 
-One problem has 32 output blocks h and 16 steps per lane. Lane h's "sub"
-pairs (partner p inside h: 2^|h| of them) give one output and its "sup"
-pairs (p containing h: 2^(5-|h|)) the other (for lc: gb and ga). A lane's
-16 steps are three pieces, steps 0-7, 8-11 and 12-15, each summed in its
-own accumulator, so every lane starts a fresh accumulator at the same steps:
-  |h| = 2: sup (8) | sub (4) | helper item      |h| = 3: sub (8) | sup (4) | item
-  |h| = 1: its 16 sup pairs; its 2 sub pairs are a helper item
-  |h| = 4: its 16 sub pairs; its 2 sup pairs are a helper item
-  h = 0:  the first 16 of its 32 sup pairs; the rest are 4 helper chunks of 4;
-          its one sub pair is a helper item
-  h = 31: the same with sub and sup exchanged.
-The 20 lanes with |h| = 2, 3 take the 20 helper items (steps 12-15, idle
-steps read a zero block). Which lane takes which item, the order of the pairs
-inside each piece, which lane slot holds which h and the per-block LDS slot
-swizzle are free; the values below were searched (simulated annealing, on
-the CPU) to minimise LDS bank conflicts of the partner and gc block reads of
-each quarter-wave (16 lanes: slots 0-15, 16-31)."""
+Backward. One problem has 32 output blocks o and 16 steps per lane: steps
+0-7 compute ga pairs only and steps 8-15 gb pairs only, so the sign pattern
+of a step is fixed at compile time for every lane (no per-lane mode). For lc,
+ga[o] takes the partners p containing o (2^(5-|o|) pairs), gb[o] those inside
+o (2^|o|); for rc the other way round. Each phase is 32 lane roles of two
+4-step pieces: a full 8-pair output (F), half of a 16-pair output (H, two
+lanes), a quarter of the 32-pair output (Q, four lanes), or two outputs of at
+most four pairs (D, idle steps read a zero block). H and Q outputs are summed
+through LDS by one of their lanes (the owner) after the last step.
+
+Forward. 8 steps in two 4-step pieces; lane h owns output h (its
+2^(5-|h|) pairs: lc (a[S], b[S | h]), rc (a[S | h], b[S]), S inside ~h):
+|h| = 2 lanes walk their 8 pairs, |h| = 3, 4, 5 lanes their 4, 2, 1 pairs and
+then a 4-pair chunk of output 0 (6 chunks) or of a |h| = 1 output (2 chunks
+each), which the owner adds through LDS.
+
+Which slot holds which role, the pair order inside each piece and the
+blocks' LDS slot swizzle are free; the values in LAYOUT were searched
+(simulated annealing on the CPU, lds_conflicts below) so that the 16 lanes of
+a quarter-wave read blocks on distinct 16-byte bank groups."""
 from __future__ import annotations
 
-NB, FULL, T = 32, 31, 16
-PIECES = ((0, 8), (8, 12), (12, 16))
+NB, FULL = 32, 31
 
 
 def popc(x):
@@ -40,175 +42,289 @@ def subsets(m):
     return out
 
 
-def sup_list(h):
-    return [h | S for S in subsets(FULL & ~h)]
+# ---- backward -------------------------------------------------------------------
+def plist(o, phase, lc=True):
+    """Partners of output o in a phase: 'A' the ga pairs, 'B' the gb pairs
+    (lc: ga partners contain o, gb partners are inside o; rc: the other way)."""
+    sup = (phase == "A") == lc
+    return [o | S for S in subsets(FULL & ~o)] if sup else subsets(o)
 
 
-def sub_list(h):
-    return subsets(h)
+def roles(phase, lc=True):
+    """The 32 lane roles of a phase: ('F', o), ('H', o, k), ('Q', o, k), ('D', o1, o2)."""
+    rs, singles = [], []
+    for o in range(NB):
+        s = len(plist(o, phase, lc))
+        if s == 8:
+            rs.append(("F", o))
+        elif s == 16:
+            rs += [("H", o, 0), ("H", o, 1)]
+        elif s == 32:
+            rs += [("Q", o, k) for k in range(4)]
+        else:
+            singles.append(o)
+    singles.sort(key=lambda o: (-len(plist(o, phase, lc)), o))
+    for i in range(8):
+        rs.append(("D", singles[i], singles[15 - i]))
+    assert len(rs) == 32
+    return rs
 
 
-def helper_items():
-    items = [("C0", k) for k in range(4)] + [("C31", k) for k in range(4)]
-    items += [("S1", 1 << b) for b in range(5)] + [("P4", FULL ^ (1 << b)) for b in range(5)]
-    return items + [("S0", 0), ("P31", FULL)]
+def role_steps(role, phase, lc=True):
+    """The 8 steps (o, p) or None (idle) of a role, pieces 0 and 1 = steps 0-3, 4-7."""
+    if role[0] == "F":
+        return [(role[1], p) for p in plist(role[1], phase, lc)]
+    if role[0] in ("H", "Q"):
+        o, k = role[1], role[2]
+        return [(o, p) for p in plist(o, phase, lc)[8 * k:8 * k + 8]]
+    l1 = [(role[1], p) for p in plist(role[1], phase, lc)]
+    l2 = [(role[2], p) for p in plist(role[2], phase, lc)]
+    return l1 + [None] * (4 - len(l1)) + l2 + [None] * (4 - len(l2))
 
 
-HELPERS = [h for h in range(NB) if popc(h) in (2, 3)]
+def partial_slots(phase, lc=True):
+    """Partial slot of each helper role (H k = 1, Q k = 1..3) and the first slot
+    and count of each owner (H k = 0, Q k = 0); slots 0-7 phase A, 8-15 phase B."""
+    base = 0 if phase == "A" else 8
+    slots, owners, nxt = {}, {}, base
+    for r in roles(phase, lc):
+        if r[0] == "H" and r[2] == 0:
+            owners[r] = (nxt, 1)
+            slots[("H", r[1], 1)] = nxt
+            nxt += 1
+    for r in roles(phase, lc):
+        if r[0] == "Q" and r[2] == 0:
+            owners[r] = (nxt, 3)
+            for k in (1, 2, 3):
+                slots[("Q", r[1], k)] = nxt
+                nxt += 1
+    assert nxt - base == 8
+    return slots, owners
 
 
-def item_step(item, j):
-    kind, x = item
-    if kind == "C0":
-        return (0, 16 + 4 * x + j, False)
-    if kind == "C31":
-        return (FULL, 16 + 4 * x + j, True)
-    if kind == "S1":
-        return (x, sub_list(x)[j], True) if j < 2 else None
-    if kind == "P4":
-        return (x, sup_list(x)[j], False) if j < 2 else None
-    if kind == "S0":
-        return (0, 0, True) if j == 0 else None
-    return (FULL, FULL, False) if j == 0 else None
+class Layout:
+    """Slot of each role, pair order inside pieces, LDS slot swizzle."""
+
+    def __init__(self, slotA, slotB, ordA, ordB, swz):  # noqa: D107
+        self.slotA, self.slotB, self.ordA, self.ordB, self.swz = slotA, slotB, ordA, ordB, swz
+
+    @staticmethod
+    def default():
+        ident = [list(range(8)) for _ in range(32)]
+        return Layout(list(range(32)), list(range(32)), ident, [list(x) for x in ident],
+                      [((b >> 1) ^ (b >> 3)) & 3 for b in range(32)])
 
 
-def natural_steps(h, assign):
-    m = popc(h)
-    if m == 0:
-        st = [(0, p, False) for p in sup_list(0)[:16]]
-    elif m == 5:
-        st = [(FULL, p, True) for p in sub_list(FULL)[:16]]
-    elif m == 1:
-        st = [(h, p, False) for p in sup_list(h)]
-    elif m == 4:
-        st = [(h, p, True) for p in sub_list(h)]
-    elif m == 2:
-        st = [(h, p, False) for p in sup_list(h)] + [(h, p, True) for p in sub_list(h)]
-    else:
-        st = [(h, p, True) for p in sub_list(h)] + [(h, p, False) for p in sup_list(h)]
-    if m in (2, 3):
-        st += [item_step(assign[h], j) for j in range(4)]
-    assert len(st) == T
-    return st
-
-
-# ---- searched layout (see the module docstring) ----
-PERM = list(range(32))                        # lane slot -> h
-ASSIGN = dict(zip(HELPERS, helper_items()))   # helper lane h -> item
-ORDER = {h: list(range(16)) for h in range(NB)}   # step -> index into the lane's natural steps (within pieces)
-SWZ = [((b >> 1) ^ (b >> 3)) & 3 for b in range(32)]  # LDS slot swizzle of block b
-
-
-def steps_by_slot(perm=None, assign=None, order=None):
-    perm, assign, order = perm or PERM, assign or ASSIGN, order or ORDER
+def steps_by_slot(lc=True, lay=None):
+    """steps[slot][t] = (o, p) or None, t = 0..15 (0-7 ga, 8-15 gb)."""
+    lay = lay or LAYOUT[lc]
+    rA, rB = roles("A", lc), roles("B", lc)
     out = []
-    for slot in range(NB):
-        h = perm[slot]
-        nat = natural_steps(h, assign)
-        out.append([nat[order[h][t]] for t in range(T)])
+    for s in range(NB):
+        a, b = lay.slotA[s], lay.slotB[s]
+        na, nb = role_steps(rA[a], "A", lc), role_steps(rB[b], "B", lc)
+        out.append([na[lay.ordA[a][t]] for t in range(8)] + [nb[lay.ordB[b][t]] for t in range(8)])
     return out
 
 
-def outputs_by_slot(perm=None, assign=None):
-    """Per slot: U (own main output), V (second own output), W (helper item):
-    each (block, sub, how) or None; how for U: 'y1' or 'sum3' (+ 'chunks' for
-    h = 0 and 31), V: 'y2', W: 'y3' or ('chunk', k) (k: 0-3 output 0, 4-7
-    output 31)."""
-    perm, assign = perm or PERM, assign or ASSIGN
+def outputs_by_slot(lc=True, lay=None):
+    """Per slot and phase: (type, block1, block2, partial slot, count) with type
+    'F' (out = y1 + y2 -> block1), 'D' (y1 -> block1, y2 -> block2), 'help'
+    (y1 + y2 -> partial slot), 'own' (y1 + y2 + count partials from slot on -> block1)."""
+    lay = lay or LAYOUT[lc]
     res = []
-    for slot in range(NB):
-        h = perm[slot]
-        m = popc(h)
-        U = V = W = None
-        if m == 0:
-            U = (0, False, "sum3+chunks")
-        elif m == 5:
-            U = (FULL, True, "sum3+chunks")
-        elif m == 1:
-            U = (h, False, "sum3")
-        elif m == 4:
-            U = (h, True, "sum3")
-        elif m == 2:
-            U, V = (h, False, "y1"), (h, True, "y2")
-        else:
-            U, V = (h, True, "y1"), (h, False, "y2")
-        if m in (2, 3):
-            kind, x = assign[h]
-            if kind == "C0":
-                W = (0, False, ("chunk", x))
-            elif kind == "C31":
-                W = (FULL, True, ("chunk", 4 + x))
+    for s in range(NB):
+        row = []
+        for phase, slots_ in (("A", lay.slotA), ("B", lay.slotB)):
+            r = roles(phase, lc)[slots_[s]]
+            ps, own = partial_slots(phase, lc)
+            if r[0] == "F":
+                row.append(("F", r[1], 0, 0, 0))
+            elif r[0] == "D":
+                row.append(("D", r[1], r[2], 0, 0))
+            elif r in own:
+                row.append(("own", r[1], 0, own[r][0], own[r][1]))
             else:
-                W = {"S1": (x, True, "y3"), "P4": (x, False, "y3"), "S0": (0, True, "y3"),
-                     "P31": (FULL, False, "y3")}[kind]
-        res.append((U, V, W))
+                row.append(("help", r[1], 0, ps[r], 0))
+        res.append(tuple(row))
     return res
 
 
-def lds_conflicts(steps=None, swz=None):
-    """Extra LDS cycles of one problem's block reads: per step, quarter-wave
-    and operand (partner, gc), the largest number of distinct blocks that
-    share a bank group, minus one (ds_read_b128: 16 lanes per cycle, 16-byte
-    bank groups; the same address read by several lanes costs nothing)."""
-    steps, swz = steps or steps_by_slot(), swz or SWZ
+def lds_conflicts(lc=True, lay=None):
+    """Extra LDS cycles of one problem's block reads: per step, quarter-wave and
+    operand (partner, gc), the largest number of distinct blocks on one 16-byte
+    bank group, minus one (ds_read_b128 serves 16 lanes per cycle; the same
+    address read by several lanes was measured to cost nothing)."""
+    lay = lay or LAYOUT[lc]
+    steps = steps_by_slot(lc, lay)
     total = 0
-    for t in range(T):
+    for t in range(16):
         for qw in range(2):
             for kind in (0, 1):
                 groups = {}
-                for slot in range(16 * qw, 16 * qw + 16):
-                    s = steps[slot][t]
-                    if s is None:
-                        addr, bank = ("zero",), (0, 0)
+                for s in range(16 * qw, 16 * qw + 16):
+                    st = steps[s][t]
+                    if st is None:
+                        addr, bank = ("z",), (0, 0)
                     else:
-                        o, p, sub = s
+                        o, p = st
                         blk = p if kind == 0 else o ^ p
-                        rev = 3 if (kind == 0 and sub) else 0
-                        region = ("a" if sub else "b") if kind == 0 else "g"
-                        addr, bank = (region, blk), (blk & 3, swz[blk] ^ rev)
+                        addr, bank = (kind, blk), (blk & 3, lay.swz[blk])
                     groups.setdefault(bank, set()).add(addr)
                 total += max(len(v) for v in groups.values()) - 1
     return total
 
 
+# searched layouts (extra LDS cycles per problem row: lc 2, rc 4; 40 for Layout.default())
+LAYOUT = {
+    True: Layout(
+        slotA=[7, 0, 17, 2, 22, 29, 3, 26, 5, 10, 24, 15, 27, 14, 23, 16, 8, 13, 30, 20, 31, 12, 19, 9, 1, 4, 6, 11, 28, 21, 25, 18],
+        slotB=[3, 13, 7, 19, 30, 10, 17, 31, 16, 1, 6, 2, 18, 8, 11, 12, 15, 20, 25, 27, 5, 0, 9, 23, 29, 14, 21, 26, 28, 24, 22, 4],
+        ordA=[[3, 2, 0, 1, 5, 4, 7, 6], [3, 0, 2, 1, 5, 4, 7, 6], [3, 1, 0, 2, 4, 5, 6, 7], [3, 2, 1, 0, 6, 5, 7, 4], [0, 3, 1, 2, 4, 5, 7, 6], [1, 0, 2, 3, 5, 7, 4, 6], [2, 3, 1, 0, 5, 6, 7, 4], [1, 3, 2, 0, 7, 5, 4, 6], [2, 3, 0, 1, 4, 5, 7, 6], [1, 0, 2, 3, 4, 7, 6, 5], [1, 2, 3, 0, 6, 5, 7, 4], [3, 2, 0, 1, 4, 5, 7, 6], [0, 3, 2, 1, 4, 7, 5, 6], [3, 2, 0, 1, 5, 4, 7, 6], [1, 2, 3, 0, 4, 6, 5, 7], [2, 0, 3, 1, 5, 6, 4, 7], [2, 1, 3, 0, 6, 4, 7, 5], [1, 0, 2, 3, 6, 7, 4, 5], [0, 2, 3, 1, 4, 6, 7, 5], [0, 2, 1, 3, 6, 7, 5, 4], [0, 2, 3, 1, 7, 6, 5, 4], [3, 0, 1, 2, 4, 7, 5, 6], [2, 3, 0, 1, 6, 7, 4, 5], [3, 2, 0, 1, 4, 6, 7, 5], [0, 3, 2, 1, 5, 6, 7, 4], [1, 0, 2, 3, 7, 6, 4, 5], [0, 1, 2, 3, 6, 7, 5, 4], [0, 3, 2, 1, 7, 5, 6, 4], [1, 3, 2, 0, 7, 6, 4, 5], [2, 3, 1, 0, 5, 7, 6, 4], [3, 2, 1, 0, 7, 6, 4, 5], [3, 0, 2, 1, 6, 7, 4, 5]],
+        ordB=[[2, 1, 3, 0, 5, 6, 7, 4], [1, 3, 0, 2, 7, 5, 6, 4], [0, 3, 1, 2, 6, 5, 7, 4], [0, 2, 1, 3, 5, 7, 6, 4], [0, 3, 1, 2, 6, 5, 4, 7], [1, 2, 3, 0, 6, 4, 7, 5], [3, 1, 0, 2, 6, 5, 7, 4], [0, 3, 1, 2, 6, 5, 7, 4], [3, 2, 1, 0, 5, 7, 6, 4], [1, 0, 2, 3, 5, 6, 4, 7], [3, 0, 2, 1, 4, 7, 5, 6], [3, 1, 0, 2, 6, 5, 7, 4], [0, 3, 1, 2, 6, 7, 5, 4], [2, 0, 1, 3, 5, 7, 6, 4], [3, 1, 2, 0, 5, 4, 7, 6], [0, 2, 3, 1, 4, 6, 7, 5], [0, 3, 2, 1, 5, 4, 6, 7], [3, 2, 1, 0, 4, 6, 7, 5], [0, 3, 2, 1, 5, 4, 6, 7], [0, 2, 1, 3, 5, 6, 7, 4], [3, 0, 1, 2, 4, 5, 6, 7], [1, 0, 2, 3, 5, 6, 7, 4], [0, 1, 2, 3, 7, 6, 5, 4], [3, 2, 0, 1, 7, 4, 6, 5], [2, 1, 0, 3, 5, 6, 4, 7], [3, 2, 1, 0, 5, 6, 4, 7], [2, 1, 3, 0, 6, 4, 5, 7], [2, 3, 1, 0, 5, 7, 4, 6], [1, 2, 0, 3, 5, 6, 4, 7], [1, 2, 3, 0, 6, 4, 5, 7], [1, 2, 3, 0, 7, 5, 4, 6], [1, 3, 2, 0, 4, 5, 7, 6]],
+        swz=[0, 3, 0, 2, 2, 1, 2, 1, 1, 2, 3, 0, 3, 3, 1, 3, 3, 0, 1, 3, 1, 1, 3, 1, 2, 2, 2, 0, 3, 0, 0, 2]),
+    False: Layout(
+        slotA=[11, 16, 4, 1, 7, 13, 12, 15, 18, 17, 31, 19, 22, 21, 8, 20, 14, 23, 24, 0, 2, 29, 27, 9, 10, 25, 5, 6, 30, 3, 26, 28],
+        slotB=[25, 5, 21, 15, 17, 0, 23, 9, 16, 13, 20, 28, 10, 19, 30, 11, 1, 22, 7, 12, 2, 29, 24, 14, 3, 31, 27, 18, 26, 4, 8, 6],
+        ordA=[[1, 0, 2, 3, 4, 6, 5, 7], [3, 2, 0, 1, 6, 4, 7, 5], [2, 0, 3, 1, 6, 5, 7, 4], [3, 0, 2, 1, 6, 5, 4, 7], [0, 3, 2, 1, 5, 4, 6, 7], [0, 3, 1, 2, 4, 6, 7, 5], [1, 0, 3, 2, 6, 5, 7, 4], [3, 0, 2, 1, 6, 7, 4, 5], [0, 2, 3, 1, 6, 5, 4, 7], [2, 1, 0, 3, 4, 7, 5, 6], [0, 3, 1, 2, 6, 4, 7, 5], [3, 2, 1, 0, 5, 4, 7, 6], [3, 2, 0, 1, 5, 4, 7, 6], [0, 3, 1, 2, 6, 7, 4, 5], [0, 3, 1, 2, 7, 4, 6, 5], [3, 0, 1, 2, 5, 4, 7, 6], [0, 3, 1, 2, 6, 4, 7, 5], [0, 2, 3, 1, 7, 5, 6, 4], [0, 1, 2, 3, 6, 4, 7, 5], [3, 2, 0, 1, 4, 5, 7, 6], [1, 0, 2, 3, 7, 4, 6, 5], [2, 1, 0, 3, 4, 5, 7, 6], [0, 3, 1, 2, 4, 6, 5, 7], [3, 0, 2, 1, 5, 6, 4, 7], [3, 2, 1, 0, 6, 4, 7, 5], [2, 1, 0, 3, 7, 4, 6, 5], [2, 3, 1, 0, 7, 4, 5, 6], [3, 1, 2, 0, 5, 4, 6, 7], [1, 0, 2, 3, 6, 4, 7, 5], [2, 3, 1, 0, 6, 4, 5, 7], [1, 3, 0, 2, 4, 5, 7, 6], [3, 0, 1, 2, 4, 5, 6, 7]],
+        ordB=[[2, 3, 0, 1, 6, 5, 7, 4], [1, 0, 2, 3, 5, 6, 7, 4], [3, 2, 1, 0, 5, 6, 4, 7], [1, 3, 0, 2, 7, 4, 5, 6], [1, 3, 0, 2, 6, 5, 4, 7], [1, 2, 0, 3, 5, 4, 7, 6], [0, 1, 3, 2, 7, 5, 4, 6], [3, 0, 2, 1, 6, 4, 7, 5], [3, 1, 0, 2, 4, 6, 5, 7], [2, 0, 3, 1, 4, 6, 5, 7], [0, 2, 1, 3, 7, 4, 5, 6], [2, 3, 1, 0, 6, 5, 4, 7], [3, 1, 2, 0, 4, 6, 5, 7], [3, 1, 2, 0, 7, 6, 4, 5], [2, 0, 3, 1, 5, 6, 4, 7], [1, 3, 0, 2, 6, 5, 4, 7], [2, 3, 1, 0, 6, 5, 7, 4], [3, 2, 0, 1, 5, 7, 4, 6], [2, 0, 1, 3, 6, 7, 4, 5], [1, 2, 3, 0, 6, 7, 4, 5], [2, 1, 3, 0, 4, 5, 6, 7], [3, 1, 2, 0, 4, 6, 5, 7], [0, 2, 1, 3, 7, 6, 4, 5], [1, 2, 0, 3, 7, 5, 4, 6], [2, 0, 3, 1, 7, 5, 4, 6], [1, 3, 0, 2, 5, 7, 4, 6], [1, 2, 3, 0, 4, 7, 5, 6], [0, 2, 3, 1, 6, 7, 4, 5], [0, 3, 1, 2, 5, 7, 4, 6], [3, 2, 0, 1, 5, 7, 4, 6], [1, 3, 0, 2, 6, 5, 7, 4], [2, 1, 3, 0, 4, 5, 6, 7]],
+        swz=[2, 0, 1, 0, 1, 2, 0, 1, 3, 3, 3, 3, 3, 3, 2, 1, 0, 1, 2, 2, 0, 2, 0, 0, 1, 1, 3, 2, 2, 0, 1, 3]),
+}
+
+
+# ---- forward ----------------------------------------------------------------------
+FT = 8
+
+
+def fwd_list(o):
+    return subsets(FULL & ~o)
+
+
+def fwd_chunks():
+    return [(0, k) for k in range(6)] + [(1 << b, k) for b in range(5) for k in range(2)]
+
+
+FHELPERS = [h for h in range(NB) if popc(h) >= 3]
+
+
+class FwdLayout:
+    def __init__(self, perm, assign, order, swz):
+        self.perm, self.assign, self.order, self.swz = perm, assign, order, swz
+
+    @staticmethod
+    def default():
+        return FwdLayout(list(range(32)), dict(zip(FHELPERS, fwd_chunks())), {h: list(range(FT)) for h in range(NB)},
+                         [((b >> 1) ^ (b >> 3)) & 3 for b in range(32)])
+
+
+def fwd_natural_steps(h, assign):
+    m = popc(h)
+    own = [(h, S) for S in fwd_list(h)]
+    if m <= 2:
+        return own[:8]
+    owner, k = assign[h]
+    return own + [None] * (4 - len(own)) + [(owner, S) for S in fwd_list(owner)[8 + 4 * k:12 + 4 * k]]
+
+
+def fwd_steps_by_slot(lay=None):
+    lay = lay or FWD_LAYOUT
+    return [[fwd_natural_steps(lay.perm[s], lay.assign)[lay.order[lay.perm[s]][t]] for t in range(FT)]
+            for s in range(NB)]
+
+
+def fwd_chunk_slot(owner, k):
+    return k if owner == 0 else 6 + 2 * (owner.bit_length() - 1) + k
+
+
+def fwd_outputs_by_slot(lay=None):
+    """Per slot: (own block, 'y1' | 'y1+y2', first chunk slot added, chunk count, chunk slot written or -1)."""
+    lay = lay or FWD_LAYOUT
+    res = []
+    for s in range(NB):
+        h = lay.perm[s]
+        m = popc(h)
+        if m == 2:
+            res.append((h, "y1+y2", 0, 0, -1))
+        elif m >= 3:
+            owner, k = lay.assign[h]
+            res.append((h, "y1", 0, 0, fwd_chunk_slot(owner, k)))
+        elif m == 1:
+            res.append((h, "y1+y2", fwd_chunk_slot(h, 0), 2, -1))
+        else:
+            res.append((h, "y1+y2", 0, 6, -1))
+    return res
+
+
+def fwd_lds_conflicts(lc=True, lay=None):
+    lay = lay or FWD_LAYOUT
+    steps = fwd_steps_by_slot(lay)
+    total = 0
+    for t in range(FT):
+        for qw in range(2):
+            for kind in (0, 1):
+                groups = {}
+                for s in range(16 * qw, 16 * qw + 16):
+                    st = steps[s][t]
+                    if st is None:
+                        addr, bank = ("z",), (0, 0)
+                    else:
+                        o, S = st
+                        ablk, bblk = (S, S | o) if lc else (S | o, S)
+                        blk = ablk if kind == 0 else bblk
+                        addr, bank = (kind, blk), (blk & 3, lay.swz[blk])
+                    groups.setdefault(bank, set()).add(addr)
+                total += max(len(v) for v in groups.values()) - 1
+    return total
+
+
+# searched layout (extra LDS cycles per problem row of lc: 0; 18 for FwdLayout.default())
+FWD_LAYOUT = FwdLayout(
+    perm=[22, 0, 4, 7, 29, 20, 19, 24, 17, 18, 2, 21, 27, 1, 8, 16, 31, 12, 14, 23, 26, 30, 3, 25, 15, 10, 28, 13, 5, 6, 9, 11],
+    assign={7: (2, 1), 11: (1, 1), 13: (1, 0), 14: (4, 0), 15: (0, 3), 19: (16, 0), 21: (0, 0), 22: (16, 1), 23: (0, 2), 25: (8, 1), 26: (8, 0), 27: (0, 5), 28: (2, 0), 29: (0, 1), 30: (0, 4), 31: (4, 1)},
+    order={0: [3, 2, 0, 1, 5, 4, 7, 6], 1: [1, 0, 2, 3, 7, 5, 4, 6], 2: [1, 2, 0, 3, 7, 5, 4, 6], 3: [2, 3, 1, 0, 4, 7, 5, 6], 4: [3, 0, 1, 2, 5, 6, 4, 7], 5: [1, 3, 0, 2, 7, 6, 5, 4], 6: [3, 2, 0, 1, 7, 5, 6, 4], 7: [0, 1, 3, 2, 6, 4, 5, 7], 8: [2, 0, 1, 3, 7, 6, 4, 5], 9: [1, 3, 0, 2, 6, 7, 4, 5], 10: [1, 3, 0, 2, 6, 7, 5, 4], 11: [3, 2, 1, 0, 6, 5, 4, 7], 12: [3, 1, 0, 2, 7, 6, 4, 5], 13: [3, 2, 1, 0, 4, 5, 7, 6], 14: [2, 1, 3, 0, 6, 7, 4, 5], 15: [3, 1, 0, 2, 7, 5, 6, 4], 16: [0, 1, 3, 2, 4, 6, 7, 5], 17: [2, 1, 0, 3, 7, 4, 5, 6], 18: [2, 1, 0, 3, 6, 4, 5, 7], 19: [1, 2, 0, 3, 7, 6, 5, 4], 20: [3, 0, 2, 1, 7, 4, 5, 6], 21: [2, 0, 3, 1, 5, 7, 6, 4], 22: [1, 3, 0, 2, 6, 5, 4, 7], 23: [3, 1, 2, 0, 6, 7, 4, 5], 24: [2, 3, 0, 1, 4, 7, 6, 5], 25: [3, 1, 2, 0, 6, 4, 7, 5], 26: [3, 1, 2, 0, 6, 7, 5, 4], 27: [3, 0, 1, 2, 4, 7, 6, 5], 28: [3, 1, 2, 0, 5, 6, 7, 4], 29: [0, 2, 1, 3, 6, 5, 4, 7], 30: [2, 3, 1, 0, 6, 7, 4, 5], 31: [1, 2, 0, 3, 5, 4, 7, 6]},
+    swz=[1, 3, 3, 3, 3, 0, 0, 2, 2, 1, 1, 1, 1, 2, 1, 0, 3, 2, 1, 2, 1, 1, 0, 0, 0, 0, 2, 1, 2, 3, 3, 3])
+
+
+# ---- header -------------------------------------------------------------------------
+_TYPE = {"F": 0, "D": 1, "help": 2, "own": 3}
+
+
 def header_text():
-    steps = steps_by_slot()
-    outs = outputs_by_slot()
-    lines = ["// Generated by gen_contr5_schedule.py (lane schedule of prod_bwd_contr5); do not edit.",
-             "#pragma once", "", "namespace clf {", "",
-             "// kContr5Steps[slot][t]: output block | partner block << 5 | sub << 10 | idle << 11",
-             "__constant__ unsigned short kContr5Steps[32][16] = {"]
-    for slot in range(NB):
-        row = []
-        for t in range(T):
-            s = steps[slot][t]
-            row.append(1 << 11 if s is None else s[0] | (s[1] << 5) | (int(s[2]) << 10))
-        lines.append("    {" + ", ".join(str(v) for v in row) + "},")
+    lines = ["// Generated by gen_contr5_schedule.py (lane schedules of prod_bwd_contr5 and prod_fwd_contr5); do not edit.",
+             "#pragma once", "", "namespace clf {", ""]
+    for lc, tag in ((True, "Lc"), (False, "Rc")):
+        steps = steps_by_slot(lc)
+        lines.append(f"// kContr5Steps{tag}[slot][t]: output block | partner block << 5 | idle << 11 (t < 8: ga, t >= 8: gb)")
+        lines.append(f"__constant__ unsigned short kContr5Steps{tag}[32][16] = {{")
+        for s in range(NB):
+            lines.append("    {" + ", ".join(str(2048 if x is None else x[0] | (x[1] << 5)) for x in steps[s]) + "},")
+        lines.append("};")
+        lines.append(f"// kContr5Out{tag}[slot][phase]: type (0 F, 1 D, 2 helper, 3 owner) | block1 << 2 | block2 << 7 |")
+        lines.append("// partial slot << 12 | partial count << 16")
+        lines.append(f"__constant__ unsigned kContr5Out{tag}[32][2] = {{")
+        for s, row in enumerate(outputs_by_slot(lc)):
+            enc = [_TYPE[t] | (b1 << 2) | (b2 << 7) | (ps << 12) | (cnt << 16) for t, b1, b2, ps, cnt in row]
+            lines.append("    {" + ", ".join(str(v) for v in enc) + "},")
+        lines.append("};")
+        swz = sum(LAYOUT[lc].swz[b] << (2 * b) for b in range(NB))
+        lines.append(f"constexpr unsigned long long kContr5Swz{tag} = 0x{swz:016x}ull;")
+        lines.append("")
+    steps = fwd_steps_by_slot()
+    lines.append("// kContr5Fwd[slot][t]: output block | S << 5 | idle << 11 (pair (a[S], b[S | o]) for lc)")
+    lines.append("__constant__ unsigned short kContr5Fwd[32][8] = {")
+    for s in range(NB):
+        lines.append("    {" + ", ".join(str(2048 if x is None else x[0] | (x[1] << 5)) for x in steps[s]) + "},")
     lines.append("};")
-    lines.append("")
-    lines.append("// kContr5Out[slot][k] (k = U, V, W): block | sub << 5 | how << 6; how: 0 none, 1 y1 (U) / y2 (V) /")
-    lines.append("// y3 (W), 2 y1 + y2 + y3 (U), 3 y1 + y2 + y3 + the 4 chunks of the block (U), 4 + c chunk slot c (W)")
-    lines.append("__constant__ unsigned short kContr5Out[32][3] = {")
-    for slot in range(NB):
-        enc = []
-        for k, d in enumerate(outs[slot]):
-            if d is None:
-                enc.append(0)
-                continue
-            blk, sub, how = d
-            if isinstance(how, tuple):
-                code = 4 + how[1]
-            else:
-                code = {"y1": 1, "y2": 1, "y3": 1, "sum3": 2, "sum3+chunks": 3}[how]
-            enc.append(blk | (int(sub) << 5) | (code << 6))
-        lines.append("    {" + ", ".join(str(v) for v in enc) + "},")
+    lines.append("// kContr5FwdOut[slot]: own block | sum of both pieces << 5 | first chunk slot added << 6 |")
+    lines.append("// chunk count << 10 | chunk slot written + 1 << 13")
+    lines.append("__constant__ unsigned kContr5FwdOut[32] = {")
+    enc = []
+    for h, how, c0, cnt, cw in fwd_outputs_by_slot():
+        enc.append(h | ((how == "y1+y2") << 5) | (c0 << 6) | (cnt << 10) | ((cw + 1) << 13))
+    lines.append("    " + ", ".join(str(v) for v in enc) + ",")
     lines.append("};")
-    lines.append("")
-    swz = 0
-    for b in range(NB):
-        swz |= SWZ[b] << (2 * b)
-    lines.append(f"// LDS float4-slot swizzle of block b: (kContr5Swz >> 2b) & 3")
-    lines.append(f"constexpr unsigned long long kContr5Swz = 0x{swz:016x}ull;")
+    swz = sum(FWD_LAYOUT.swz[b] << (2 * b) for b in range(NB))
+    lines.append(f"constexpr unsigned long long kContr5FwdSwz = 0x{swz:016x}ull;")
     lines.append("")
     lines.append("}  // namespace clf")
     return "\n".join(lines) + "\n"
@@ -219,91 +335,4 @@ if __name__ == "__main__":
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "contr5_schedule.h")
     with open(path, "w") as f:
         f.write(header_text())
-    print("conflict cycles per problem-row:", lds_conflicts())
-
-
-# ---- forward (prod_fwd_contr5) ------------------------------------------------
-# Output block o of a problem takes the pairs (a[S], b[S | o]) for S inside ~o
-# (lc; rc: (a[S | o], b[S])): 2^(5-|o|) of them. 8 steps per lane in two pieces
-# (0-3, 4-7); lane h owns output h:
-#   |h| = 2: its 8 pairs; |h| = 3, 4, 5: its 4, 2, 1 pairs in piece 0 and a
-#   helper chunk in piece 1; |h| = 1: its first 8 pairs, two chunks of 4 by
-#   helpers; h = 0: its first 8 of 32, six chunks by helpers.
-FT = 8
-FPIECES = ((0, 4), (4, 8))
-FHELPERS = [h for h in range(NB) if popc(h) >= 3]
-
-
-def fwd_chunks():
-    return [(0, k) for k in range(6)] + [(1 << b, k) for b in range(5) for k in range(2)]
-
-
-def fwd_list(o):
-    return subsets(FULL & ~o)
-
-
-FASSIGN = dict(zip(FHELPERS, fwd_chunks()))        # helper lane h -> (owner output, chunk index)
-FORDER = {h: list(range(FT)) for h in range(NB)}
-FPERM = list(range(32))
-FSWZ = [((b >> 1) ^ (b >> 3)) & 3 for b in range(32)]
-
-
-def fwd_natural_steps(h, fassign):
-    m = popc(h)
-    own = [(h, S) for S in fwd_list(h)]
-    if m <= 2:
-        st = own[:8]
-    else:
-        st = own + [None] * (4 - len(own))
-        owner, k = fassign[h]
-        st += [(owner, S) for S in fwd_list(owner)[8 + 4 * k:12 + 4 * k]]
-    assert len(st) == FT
-    return st
-
-
-def fwd_steps_by_slot(perm=None, fassign=None, order=None):
-    perm, fassign, order = perm or FPERM, fassign or FASSIGN, order or FORDER
-    return [[fwd_natural_steps(perm[s], fassign)[order[perm[s]][t]] for t in range(FT)] for s in range(NB)]
-
-
-def fwd_chunk_slot(owner, k):
-    return k if owner == 0 else 6 + 2 * (owner.bit_length() - 1) + k
-
-
-def fwd_outputs_by_slot(perm=None, fassign=None):
-    """Per slot: (own block h, 'y1' | 'y1+y2' | ('y1+y2+chunks', first slot, count), chunk slot of piece 1 or None)."""
-    perm, fassign = perm or FPERM, fassign or FASSIGN
-    res = []
-    for s in range(NB):
-        h = perm[s]
-        m = popc(h)
-        if m == 2:
-            res.append((h, "y1+y2", None))
-        elif m >= 3:
-            owner, k = fassign[h]
-            res.append((h, "y1", fwd_chunk_slot(owner, k)))
-        elif m == 1:
-            res.append((h, ("y1+y2+chunks", fwd_chunk_slot(h, 0), 2), None))
-        else:
-            res.append((h, ("y1+y2+chunks", 0, 6), None))
-    return res
-
-
-def fwd_lds_conflicts(steps=None, swz=None, lc=True):
-    steps, swz = steps or fwd_steps_by_slot(), swz or FSWZ
-    total = 0
-    for t in range(FT):
-        for qw in range(2):
-            for kind in (0, 1):
-                groups = {}
-                for slot in range(16 * qw, 16 * qw + 16):
-                    s = steps[slot][t]
-                    if s is None:
-                        addr, bank = ("zero",), (0, 0)
-                    else:
-                        o, S = s
-                        blk = (S if lc else S | o) if kind == 0 else (S | o if lc else S)
-                        addr, bank = ("ab"[kind], blk), (blk & 3, swz[blk])
-                    groups.setdefault(bank, set()).add(addr)
-                total += max(len(v) for v in groups.values()) - 1
-    return total
+    print("bwd conflicts lc/rc:", lds_conflicts(True), lds_conflicts(False), "fwd:", fwd_lds_conflicts())

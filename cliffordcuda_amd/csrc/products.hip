@@ -2317,41 +2317,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     }
 }
 
-// ---- left and right contraction backward on 5 high bits --------------------
+// ---- left and right contraction on 5 high bits ------------------------------
 // n = 9, and n = 10 whose only null generator is the top one (C5's Cl(9,0,1)).
 // With e9 null and rightmost in every blade, a = a0 + a1 e9 and b = b0 + b1 e9
 // (halves of 512 floats), the left contraction's pairs with e9 in the
 // contracted blade vanish and those with e9 in b only append e9, so
+//   c0 = lc9(a0, b0),  c1 = lc9(a0, b1)
 //   ga0 = ga9(b0, gc0) + ga9(b1, gc1),  ga1 = 0,  gb0 = gb9(a0, gc0),  gb1 = gb9(a0, gc1)
 // with the n = 9 left contraction of e0..e8: two n = 9 problems sharing a0 (a1
 // is never read). A wave runs two problems of 32 lanes (two rows at n = 9, the
-// two halves at n = 10) on the frame schedule of prod_bwd_contr_frame (sub
-// pairs read the partner reversed into a reversed-frame accumulator, one sup
-// pattern for every lane) with the lane schedule of contr5_schedule.h: 16
-// steps per lane in three pieces (steps 0-7, 8-11, 12-15), each its own
-// accumulator, so a lane starts a fresh accumulator at the same steps as every
-// other lane and no step needs a per-lane conditional zeroing. A lane's pieces
-// are its own outputs (|h| = 2, 3: one per piece), parts of one output (|h| =
-// 0, 1, 4, 5: summed), or a helper item (a small output of another lane, or a
-// 4-pair chunk of output 0's or 31's 32-pair list, added by its owner through
-// LDS). The pair order inside pieces, the slot of each h and the blocks' LDS
-// slot swizzle were chosen (a search on the CPU) to keep each quarter-wave's
-// 16 block reads on distinct bank groups. Finished blocks are staged in LDS
-// and leave in row order.
+// two halves at n = 10). The lane schedules (contr5_schedule.h, written by
+// gen_contr5_schedule.py) split every output's block pairs into 4-step pieces:
+// in the backward, steps 0-7 are ga pairs and 8-15 gb pairs for every lane, so
+// each step's sign pattern is fixed at compile time (the blocked kernels'
+// arithmetic, no per-lane mode); a lane's pieces are a full output, two small
+// outputs, or part of a larger output whose owner lane adds the other parts
+// through LDS after the last step. Every lane starts a fresh accumulator at the
+// same steps, so no step zeroes conditionally. The pair order inside pieces,
+// the slot of each role and the blocks' LDS slot swizzle were searched on the
+// CPU to keep each quarter-wave's 16 block reads on distinct bank groups.
+// Finished blocks are staged in LDS and leave in row order.
 
-__device__ __forceinline__ unsigned swz5(unsigned blk) { return (unsigned)(kContr5Swz >> (2u * blk)) & 3u; }
-
-// an accumulator's output block, turned to the normal frame if its mode was
-// sub, with the gb reversion signs: y[k] = contr_out_sub(x, k) or contr_out_sup(x, k)
-template <bool LOWNEG, bool KLC>
-__device__ __forceinline__ void contr5_result(const float (&x)[16], bool sub, float (&y)[16]) {
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        const float ys = contr_out_sub<LOWNEG, KLC>(x, k);
-        const float yp = contr_out_sup<!KLC>(x, k);
-        y[k] = sub ? ys : yp;
-    }
-}
+template <unsigned long long SWZ>
+__device__ __forceinline__ unsigned swz5(unsigned blk) { return (unsigned)(SWZ >> (2u * blk)) & 3u; }
 
 template <int OP, bool LOWNEG, bool NULLTOP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void prod_bwd_contr5(
@@ -2362,8 +2350,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     constexpr int N = NULLTOP ? 10 : 9;
     constexpr int R = NULLTOP ? 1 : 2;  // rows per wave
     constexpr bool kLC = OP == OP_LC;
+    constexpr int V = kLC ? LV_LC : LV_RC;
+    constexpr unsigned long long SW = kLC ? kContr5SwzLc : kContr5SwzRc;
     constexpr unsigned full = 31u;
-    // per wave (float4): a at 0 (two rows of 128; NULLTOP: a0 only), b at 256, gc at 512, a zero block at 768
+    // per wave (float4): a at 0 (rows 0, 1 of 128; NULLTOP: a0 in row 0), b at 256, gc at 512, zero block at 768
     __shared__ __attribute__((aligned(64))) float4 lds[4][3 * 256 + 4];
     __shared__ unsigned tab[16][64];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -2371,42 +2361,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     const long long ngrp = (P.batch + R - 1) / R;
     const long long grp = (long long)blockIdx.x * 4 + wave;
     const BalLane L = bal_lane(N, lane);
-    const bool gbc = P.ldg4 == 0;
     BalPre pa;
     {
         const BalSrc sa = bal_src(A, grp, P.batch, N, R);
         if constexpr (NULLTOP) {  // a0 only: chunks 0, 1 of the row
-#pragma unroll
-            for (int i = 0; i < 2; ++i) pa.v[i] = sa.g0[L.ff[i]];
+            pa.v[0] = sa.g0[L.ff[0]];
+            pa.v[1] = sa.g0[L.ff[1]];
         } else {
             pa = bal_fetch(sa, L, N - 2);
         }
     }
     const BalPre pb = bal_fetch(bal_src(B, grp, P.batch, N, R), L, N - 2);
-    const BalPre pg = bal_fetch(bal_src(GC, grp, P.batch, N, R, gbc), L, N - 2);
-    // step entries: partner float4 offset (bits 0-9), gc float4 offset (10-19), then the
-    // flips of prod_bwd_contr_frame: pair sign S (23), parity term (24), w1 (25), w2 (26),
-    // rho (27), gc parity (28)
+    const BalPre pg = bal_fetch(bal_src(GC, grp, P.batch, N, R, P.ldg4 == 0), L, N - 2);
+    // step entries: partner byte offset (bits 0-13), gc byte offset (14-27), the pair's high
+    // sign (28) and the cross parity of the odd partner elements (29): |o| for ga, |p| for gb
     if (wave == 0) {
         for (int t = 0; t < 16; ++t) {
-            const unsigned st = kContr5Steps[slot][t];
+            const unsigned st = kLC ? kContr5StepsLc[slot][t] : kContr5StepsRc[slot][t];
             unsigned e;
-            if (st & 2048u) {  // idle: the zero block
-                e = 768u | (768u << 10);
+            if (st & 2048u) {  // idle: the zero block for both reads
+                e = (768u << 4) | (768u << 18);
             } else {
-                const unsigned o = st & 31u, p = (st >> 5) & 31u, sub = (st >> 10) & 1u;
-                const unsigned gb = kLC ? sub : sub ^ 1u;
-                const unsigned podd = (unsigned)__popc(p) & 1u, oodd = (unsigned)__popc(o) & 1u;
-                const HiSign hs = gb ? hi_sign<OP_INNER>(p, o, P.negh, 0u, full, 0, 0)
-                                     : hi_sign<OP_INNER>(o, p, P.negh, 0u, full, 0, 0);
-                const unsigned pm = (gb ? podd : oodd) ^ (LOWNEG ? sub : 0u);
-                const unsigned x = o ^ p;
-                // partner: gb steps read a (NULLTOP: a0, row 0), ga steps read b (the problem's row)
-                const unsigned prow = (NULLTOP && gb) ? 0u : prob;
-                const unsigned pw = (gb ? 0u : 256u) + prow * 128u + ((p << 2) | (swz5(p) ^ (sub ? 3u : 0u)));
-                const unsigned pg4 = 512u + prob * 128u + ((x << 2) | swz5(x));
-                e = pw | (pg4 << 10) | ((hs.mask >> 31) << 23) | (pm << 24) | ((gb & sub) << 25) |
-                    (((gb ^ 1u) & sub) << 26) | (gb << 27) | ((gb & podd) << 28);
+                const unsigned o = st & 31u, p = (st >> 5) & 31u, x = o ^ p;
+                const bool ga = t < 8;
+                const HiSign hs = ga ? hi_sign<OP>(o, p, P.negh, 0u, full, 0, 0) : hi_sign<OP>(p, o, P.negh, 0u, full, 0, 0);
+                const unsigned par = (unsigned)__popc(ga ? o : p) & 1u;
+                const unsigned prow = (NULLTOP && !ga) ? 0u : prob;  // gb partners: a (NULLTOP: a0, row 0)
+                const unsigned pw = (ga ? 256u : 0u) + prow * 128u + ((p << 2) | swz5<SW>(p));
+                const unsigned pg4 = 512u + prob * 128u + ((x << 2) | swz5<SW>(x));
+                e = (pw << 4) | (pg4 << 18) | ((hs.mask >> 31) << 28) | (par << 29);
             }
             tab[t][lane] = e;
         }
@@ -2415,32 +2398,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     if (grp >= ngrp) return;
     float4* sw = lds[wave];
     const unsigned base = lds_addr4(sw);
-    {
-        // a and b in the frame layout (component c of a chunk in float4 slot q goes to
-        // component c ^ q), gc as it is; slot q of block blk at (blk << 2) | (q ^ swz5(blk))
-        const unsigned fq = (unsigned)lane & 3u;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const unsigned c = (unsigned)lane + 64u * (unsigned)i;
-            const unsigned hr = c >> 7, f = c & 127u, blk = f >> 2;
-            const unsigned so = 16u * (hr * 128u + ((blk << 2) | ((f & 3u) ^ swz5(blk))));
-            const unsigned ad = (base + so) | (fq << 2);
-            const float vb[4] = {pb.v[i].x, pb.v[i].y, pb.v[i].z, pb.v[i].w};
-#pragma unroll
-            for (int cc = 0; cc < 4; ++cc)
-                *(__attribute__((address_space(3))) float*)(uintptr_t)((ad ^ ((unsigned)cc << 2)) + 4096u) = vb[cc];
-            if (!NULLTOP || i < 2) {
-                const float va[4] = {pa.v[i].x, pa.v[i].y, pa.v[i].z, pa.v[i].w};
-#pragma unroll
-                for (int cc = 0; cc < 4; ++cc)
-                    *(__attribute__((address_space(3))) float*)(uintptr_t)(ad ^ ((unsigned)cc << 2)) = va[cc];
-            }
-            lds_st4(base + 8192u + so, pg.v[i]);
-        }
-        if (lane < 4) lds_st4(base + 16u * (768u + (unsigned)lane), make_float4(0.f, 0.f, 0.f, 0.f));
+    for (int i = 0; i < 4; ++i) {  // slot q of block blk at (blk << 2) | (q ^ swz(blk))
+        const unsigned c = (unsigned)lane + 64u * (unsigned)i;
+        const unsigned hr = c >> 7, f = c & 127u, blk = f >> 2;
+        const unsigned so = 16u * (hr * 128u + ((blk << 2) | ((f & 3u) ^ swz5<SW>(blk))));
+        if (!NULLTOP || i < 2) lds_st4(base + so, pa.v[i]);
+        lds_st4(base + 4096u + so, pb.v[i]);
+        lds_st4(base + 8192u + so, pg.v[i]);
     }
+    if (lane < 4) lds_st4(base + 16u * (768u + (unsigned)lane), make_float4(0.f, 0.f, 0.f, 0.f));
     wave_lds_sync();
-    float acc[16], y1[16], y2[16];
+    float acc[16], y1[16], y2[16], y3[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.f;
     auto step = [&](auto tc) {
@@ -2448,11 +2417,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
         __builtin_amdgcn_sched_barrier(0);
         unsigned e = tab[t][lane];
         asm volatile("" : "+v"(e));
-        const unsigned w0 = base + ((e & 1023u) << 4);
-        const unsigned g0 = base + (((e >> 10) & 1023u) << 4);
-        unsigned ms = (e << 8) & 0x80000000u, mp = (e << 7) & 0x80000000u, m1 = (e << 6) & 0x80000000u;
-        unsigned m2 = (e << 5) & 0x80000000u, mr = (e << 4) & 0x80000000u, mg = (e << 3) & 0x80000000u;
-        asm volatile("" : "+v"(ms), "+v"(mp), "+v"(m1), "+v"(m2), "+v"(mr), "+v"(mg));
+        const unsigned w0 = base + (e & 16383u);
+        const unsigned g0 = base + ((e >> 14) & 16383u);
+        const unsigned ms = (e << 3) & 0x80000000u, mq = (e << 2) & 0x80000000u;
         float g[16], w[16];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -2467,77 +2434,91 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
             w[4 * q + 2] = vw.z;
             w[4 * q + 3] = vw.w;
         }
-        unsigned x1 = ms ^ mp, x2 = ms ^ mr, x3 = x1 ^ mr, y3 = m1 ^ m2, gpr = mg ^ mr;
-        asm volatile("" : "+v"(x1), "+v"(x2), "+v"(x3), "+v"(y3), "+v"(gpr));
+        apply_flips(w, ms, ms ^ mq);
+        if constexpr (t < 8) {
+            lowblock_ga<V, LOWNEG>(acc, w, g);
+        } else {
 #pragma unroll
-        for (int el = 0; el < 16; ++el) {
-            const unsigned xa = par4(el) ? (rho4(el) ? x3 : x1) : (rho4(el) ? x2 : ms);
-            const int wcl = w1b(el) + 2 * w2b(el);
-            const unsigned u = __float_as_uint(w[fr_reg(el)]);
-            w[fr_reg(el)] = __uint_as_float(wcl == 0 ? u ^ xa : u ^ xa ^ (wcl == 1 ? m1 : wcl == 2 ? m2 : y3));
-            if (par4(el) || rho4(el)) g[el] = flip(g[el], par4(el) && rho4(el) ? gpr : par4(el) ? mg : mr);
+            for (int el = 0; el < 16; ++el)
+                if (cpopc((unsigned)el) & 1) g[el] = flip(g[el], mq);
+            lowblock_gb<V, LOWNEG>(acc, w, g);
         }
-        frame_sup<LOWNEG, true, false>(acc, acc, w, w, g, g, std::make_integer_sequence<int, 256>{});
-        if constexpr (t == 7 || t == 11) {  // a piece ends: keep it, start from zero
+        if constexpr ((t & 3) == 3 && t < 15) {  // a piece ends: keep it, start from zero
 #pragma unroll
             for (int el = 0; el < 16; ++el) {
-                if constexpr (t == 7) y1[el] = acc[el];
-                else y2[el] = acc[el];
+                if constexpr (t == 3) y1[el] = acc[el];
+                else if constexpr (t == 7) y2[el] = acc[el];
+                else y3[el] = acc[el];
                 acc[el] = 0.f;
             }
         }
     };
     frame_steps(step, std::make_integer_sequence<int, 16>{});
-    // acc holds the third piece (steps 12-15)
+    // pieces: y1, y2 (ga), y3, acc (gb)
     wave_lds_sync();  // every block read of the wave is done: its LDS takes the results
-    const unsigned dU = kContr5Out[slot][0], dV = kContr5Out[slot][1], dW = kContr5Out[slot][2];
-    const unsigned chunk_f4 = 512u + prob * 128u;  // the problem's chunk slots (4 float4 each), over its gc rows
-    if ((dW >> 6) >= 4u) {  // a helper chunk of output 0 or 31: to its slot
-        const unsigned a = base + 16u * (chunk_f4 + 4u * ((dW >> 6) - 4u));
+    const unsigned dA = kLC ? kContr5OutLc[slot][0] : kContr5OutRc[slot][0];
+    const unsigned dB = kLC ? kContr5OutLc[slot][1] : kContr5OutRc[slot][1];
+    const unsigned part = base + 16u * (512u + prob * 128u);  // 16 partial slots of 4 float4, over the gc rows
+    float sA[16], sB[16];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) lds_st4(a + 16u * (unsigned)q, make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]));
+    for (int el = 0; el < 16; ++el) {
+        sA[el] = y1[el] + y2[el];
+        sB[el] = y3[el] + acc[el];
     }
-    wave_lds_sync();
-    float u[16];
-    const unsigned hU = dU >> 6;
+    auto st16 = [&](unsigned a, const float (&x)[16]) {
 #pragma unroll
-    for (int el = 0; el < 16; ++el) u[el] = hU == 1u ? y1[el] : (y1[el] + y2[el]) + acc[el];
-    if (hU == 3u) {  // outputs 0 and 31 add their four helper chunks, in order
-        const unsigned a = base + 16u * (chunk_f4 + ((dU & 32u) ? 16u : 0u));
+        for (int q = 0; q < 4; ++q) lds_st4(a + 16u * (unsigned)q, make_float4(x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]));
+    };
+    auto add16 = [&](unsigned a, float (&x)[16]) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float4 v = lds_ld4(a + 16u * (4u * (unsigned)k + (unsigned)q));
-                u[4 * q] += v.x;
-                u[4 * q + 1] += v.y;
-                u[4 * q + 2] += v.z;
-                u[4 * q + 3] += v.w;
-            }
+        for (int q = 0; q < 4; ++q) {
+            const float4 v = lds_ld4(a + 16u * (unsigned)q);
+            x[4 * q] += v.x;
+            x[4 * q + 1] += v.y;
+            x[4 * q + 2] += v.z;
+            x[4 * q + 3] += v.w;
         }
-    }
+    };
+    if ((dA & 3u) == 2u) st16(part + 64u * ((dA >> 12) & 15u), sA);  // helpers' partials
+    if ((dB & 3u) == 2u) st16(part + 64u * ((dB >> 12) & 15u), sB);
     wave_lds_sync();
-    // results into the staging rows: ga blocks over a (row = problem), gb blocks over b
-    auto put = [&](const float (&x)[16], unsigned d) {
-        const unsigned blk = d & 31u;
-        const bool sub = (d >> 5) & 1u;
-        const bool gbk = kLC ? sub : !sub;
-        float y[16];
-        contr5_result<LOWNEG, kLC>(x, sub, y);
-        const unsigned rowb = base + 16u * ((gbk ? 256u : 0u) + prob * 128u);
+    if ((dA & 3u) == 3u) {  // owners add them, in slot order
+        const unsigned p0 = (dA >> 12) & 15u, cnt = (dA >> 16) & 3u;
+        for (unsigned k = 0; k < cnt; ++k) add16(part + 64u * (p0 + k), sA);
+    }
+    if ((dB & 3u) == 3u) {
+        const unsigned p0 = (dB >> 12) & 15u, cnt = (dB >> 16) & 3u;
+        for (unsigned k = 0; k < cnt; ++k) add16(part + 64u * (p0 + k), sB);
+    }
+    // results into the staging rows (over the dead inputs): ga over a, gb over b, row = problem
+    auto put = [&](unsigned region, unsigned blk, const float (&x)[16]) {
+        const unsigned rowb = base + 16u * (region + prob * 128u);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            lds_st4(rowb + 16u * ((blk << 2) | ((unsigned)q ^ swz5(blk))), make_float4(y[4 * q], y[4 * q + 1], y[4 * q + 2], y[4 * q + 3]));
+            lds_st4(rowb + 16u * ((blk << 2) | ((unsigned)q ^ swz5<SW>(blk))),
+                    make_float4(x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]));
     };
-    put(u, dU);
-    if (dV >> 6) put(y2, dV);
-    if ((dW >> 6) == 1u) put(acc, dW);
+    {
+        const unsigned tA = dA & 3u, tB = dB & 3u;
+        if (tA == 1u) {
+            put(0u, (dA >> 2) & 31u, y1);
+            put(0u, (dA >> 7) & 31u, y2);
+        } else if (tA != 2u) {
+            put(0u, (dA >> 2) & 31u, sA);
+        }
+        if (tB == 1u) {
+            put(256u, (dB >> 2) & 31u, y3);
+            put(256u, (dB >> 7) & 31u, acc);
+        } else if (tB != 2u) {
+            put(256u, (dB >> 2) & 31u, sB);
+        }
+    }
     wave_lds_sync();
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const unsigned c = (unsigned)lane + 64u * (unsigned)i;
         const unsigned hr = c >> 7, f = c & 127u, blk = f >> 2;
-        const unsigned so = 16u * (hr * 128u + ((blk << 2) | ((f & 3u) ^ swz5(blk))));
+        const unsigned so = 16u * (hr * 128u + ((blk << 2) | ((f & 3u) ^ swz5<SW>(blk))));
         if constexpr (NULLTOP) {
             const long long at = (grp << 8) + (long long)c;  // float4 of the row: half hr, float4 f
             if (GA) {
@@ -2556,6 +2537,159 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
                 if (GA) reinterpret_cast<float4*>(GA)[at] = lds_ld4(base + so);
                 if (GB) reinterpret_cast<float4*>(GB)[at] = lds_ld4(base + 4096u + so);
             }
+        }
+    }
+}
+
+// Forward: lane slot s walks 8 pairs of kContr5Fwd in two pieces, (a[S], b[S | o])
+// for lc and (a[S | o], b[S]) for rc; the owner of an output adds the helper
+// chunks of its list; the lane's own block leaves through LDS in row order.
+template <int OP, bool LOWNEG, bool NULLTOP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void prod_fwd_contr5(
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, BlkParams P) {
+    static_assert(OP == OP_LC || OP == OP_RC, "contractions only");
+    static_assert(!NULLTOP || OP == OP_LC, "the null-top split is the left contraction's");
+    constexpr int N = NULLTOP ? 10 : 9;
+    constexpr int R = NULLTOP ? 1 : 2;
+    constexpr bool kLC = OP == OP_LC;
+    constexpr int V = kLC ? LV_LC : LV_RC;
+    constexpr unsigned long long SW = kContr5FwdSwz;
+    constexpr unsigned full = 31u;
+    // per wave (float4): a at 0 (rows 0, 1; NULLTOP: a0 in row 0), b at 256, zero block at 512
+    __shared__ __attribute__((aligned(64))) float4 lds[4][2 * 256 + 4];
+    __shared__ unsigned tab[8][64];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const unsigned slot = (unsigned)lane & 31u, prob = (unsigned)lane >> 5;
+    const long long ngrp = (P.batch + R - 1) / R;
+    const long long grp = (long long)blockIdx.x * 4 + wave;
+    const BalLane L = bal_lane(N, lane);
+    BalPre pa;
+    {
+        const BalSrc sa = bal_src(A, grp, P.batch, N, R);
+        if constexpr (NULLTOP) {
+            pa.v[0] = sa.g0[L.ff[0]];
+            pa.v[1] = sa.g0[L.ff[1]];
+        } else {
+            pa = bal_fetch(sa, L, N - 2);
+        }
+    }
+    const BalPre pb = bal_fetch(bal_src(B, grp, P.batch, N, R), L, N - 2);
+    // entries: a byte offset (bits 0-13), b byte offset (14-27), high sign (28), cross parity |ih| (29)
+    if (wave == 0) {
+        for (int t = 0; t < 8; ++t) {
+            const unsigned st = kContr5Fwd[slot][t];
+            unsigned e;
+            if (st & 2048u) {
+                e = (512u << 4) | (512u << 18);
+            } else {
+                const unsigned o = st & 31u, S = (st >> 5) & 31u;
+                const unsigned ih = kLC ? S : (S | o), jh = kLC ? (S | o) : S;
+                const HiSign hs = hi_sign<OP>(ih, jh, P.negh, 0u, full, 0, 0);
+                const unsigned arow = NULLTOP ? 0u : prob;
+                const unsigned pa4 = arow * 128u + ((ih << 2) | swz5<SW>(ih));
+                const unsigned pb4 = 256u + prob * 128u + ((jh << 2) | swz5<SW>(jh));
+                e = (pa4 << 4) | (pb4 << 18) | ((hs.mask >> 31) << 28) | (((unsigned)__popc(ih) & 1u) << 29);
+            }
+            tab[t][lane] = e;
+        }
+    }
+    __syncthreads();
+    if (grp >= ngrp) return;
+    float4* sw = lds[wave];
+    const unsigned base = lds_addr4(sw);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const unsigned c = (unsigned)lane + 64u * (unsigned)i;
+        const unsigned hr = c >> 7, f = c & 127u, blk = f >> 2;
+        const unsigned so = 16u * (hr * 128u + ((blk << 2) | ((f & 3u) ^ swz5<SW>(blk))));
+        if (!NULLTOP || i < 2) lds_st4(base + so, pa.v[i]);
+        lds_st4(base + 4096u + so, pb.v[i]);
+    }
+    if (lane < 4) lds_st4(base + 16u * (512u + (unsigned)lane), make_float4(0.f, 0.f, 0.f, 0.f));
+    wave_lds_sync();
+    float acc[16], y1[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+    auto step = [&](auto tc) {
+        constexpr int t = decltype(tc)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        unsigned e = tab[t][lane];
+        asm volatile("" : "+v"(e));
+        const unsigned a0 = base + (e & 16383u);
+        const unsigned b0 = base + ((e >> 14) & 16383u);
+        const unsigned ms = (e << 3) & 0x80000000u, mq = (e << 2) & 0x80000000u;
+        float av[16], bv[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 va = lds_ld4(a0 ^ ((unsigned)q << 4));
+            const float4 vb = lds_ld4(b0 ^ ((unsigned)q << 4));
+            av[4 * q] = va.x;
+            av[4 * q + 1] = va.y;
+            av[4 * q + 2] = va.z;
+            av[4 * q + 3] = va.w;
+            bv[4 * q] = vb.x;
+            bv[4 * q + 1] = vb.y;
+            bv[4 * q + 2] = vb.z;
+            bv[4 * q + 3] = vb.w;
+        }
+        apply_flips(bv, ms, ms ^ mq);
+        lowblock_fwd<V, LOWNEG>(acc, av, bv);
+        if constexpr (t == 3) {
+#pragma unroll
+            for (int el = 0; el < 16; ++el) {
+                y1[el] = acc[el];
+                acc[el] = 0.f;
+            }
+        }
+    };
+    frame_steps(step, std::make_integer_sequence<int, 8>{});
+    wave_lds_sync();
+    const unsigned d = kContr5FwdOut[slot];
+    const unsigned chunks = base + 16u * (256u + prob * 128u);  // 16 chunk slots of 4 float4, over the b rows
+    const int cw = (int)(d >> 13) - 1;
+    if (cw >= 0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            lds_st4(chunks + 64u * (unsigned)cw + 16u * (unsigned)q,
+                    make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]));
+    }
+    wave_lds_sync();
+    float u[16];
+    const bool both = (d >> 5) & 1u;
+#pragma unroll
+    for (int el = 0; el < 16; ++el) u[el] = both ? y1[el] + acc[el] : y1[el];
+    {
+        const unsigned c0 = (d >> 6) & 15u, cnt = (d >> 10) & 7u;
+        for (unsigned k = 0; k < cnt; ++k) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 v = lds_ld4(chunks + 64u * (c0 + k) + 16u * (unsigned)q);
+                u[4 * q] += v.x;
+                u[4 * q + 1] += v.y;
+                u[4 * q + 2] += v.z;
+                u[4 * q + 3] += v.w;
+            }
+        }
+    }
+    {
+        const unsigned blk = d & 31u;
+        const unsigned rowb = base + 16u * (prob * 128u);  // over a
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            lds_st4(rowb + 16u * ((blk << 2) | ((unsigned)q ^ swz5<SW>(blk))),
+                    make_float4(u[4 * q], u[4 * q + 1], u[4 * q + 2], u[4 * q + 3]));
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const unsigned c = (unsigned)lane + 64u * (unsigned)i;
+        const unsigned hr = c >> 7, f = c & 127u, blk = f >> 2;
+        const unsigned so = 16u * (hr * 128u + ((blk << 2) | ((f & 3u) ^ swz5<SW>(blk))));
+        if constexpr (NULLTOP) {
+            reinterpret_cast<float4*>(C)[(grp << 8) + (long long)c] = lds_ld4(base + so);
+        } else {
+            const long long row = grp * 2 + (long long)hr;
+            if (row < P.batch) reinterpret_cast<float4*>(C)[(row << 7) + (long long)f] = lds_ld4(base + so);
         }
     }
 }
@@ -3213,6 +3347,35 @@ static void launch_contr5_t(hipStream_t s, const float* A, const float* B, const
     }
 }
 
+template <int OP, bool LN, bool NT>
+static void launch_fcontr5_t(hipStream_t s, const float* A, const float* B, float* C, const BlkParams& P) {
+    const long long R = NT ? 1 : 2;
+    const long long chunk = kMaxGrid * 4 * R;
+    const long long D = NT ? 1024 : 512;
+    for (long long r0 = 0; r0 < P.batch; r0 += chunk) {
+        BlkParams Q = P;
+        Q.batch = P.batch - r0 < chunk ? P.batch - r0 : chunk;
+        const long long groups = (Q.batch + R - 1) / R;
+        const dim3 g((unsigned)((groups + 3) / 4));
+        const long long off = r0 * D;
+        hipLaunchKernelGGL((prod_fwd_contr5<OP, LN, NT>), g, dim3(256), 0, s, A + off, B + off, C + off, Q);
+    }
+}
+
+static void launch_fcontr5(int op, bool ln, bool nt, hipStream_t s, const float* A, const float* B, float* C,
+                           const BlkParams& P) {
+    if (nt) {
+        if (ln) launch_fcontr5_t<OP_LC, true, true>(s, A, B, C, P);
+        else launch_fcontr5_t<OP_LC, false, true>(s, A, B, C, P);
+    } else if (op == OP_LC) {
+        if (ln) launch_fcontr5_t<OP_LC, true, false>(s, A, B, C, P);
+        else launch_fcontr5_t<OP_LC, false, false>(s, A, B, C, P);
+    } else {
+        if (ln) launch_fcontr5_t<OP_RC, true, false>(s, A, B, C, P);
+        else launch_fcontr5_t<OP_RC, false, false>(s, A, B, C, P);
+    }
+}
+
 static void launch_contr5(int op, bool ln, bool nt, hipStream_t s, const float* A, const float* B, const float* GCp,
                           float* GA, float* GB, const BlkParams& P) {
     if (nt) {
@@ -3325,7 +3488,7 @@ int product_fwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
     hipStream_t s = (hipStream_t)stream;
     BlkParams P{};
     P.batch = batch;
-    bool ln = false;
+    bool ln = false, nt5 = false;
     dim3 g, bl;
     size_t lds = 0;
     const bool force_tiled = n >= 12 && tiled_forced(), force_generic = generic_forced();
@@ -3340,6 +3503,8 @@ int product_fwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
             case OP_REGR: CLF_FWD_SPLIT(OP_REGR, false); break;
         }
 #undef CLF_FWD_SPLIT
+    } else if (contr5_plan(op, n, neg, nul, P, ln, nt5)) {
+        launch_fcontr5(op, ln, nt5, s, a, b, c, P);
     } else if (out7_plan(op, n, neg, nul, P, ln)) {
         if (op == OP_INNER) launch_out7<OP_INNER>(s, ln, a, b, c, P);
         else if (op == OP_LC) launch_out7<OP_LC>(s, ln, a, b, c, P);

@@ -802,10 +802,10 @@ def fwd7_step(h, t):
     return (h, parts[t]) if t < len(parts) else None
 
 
-# ---- prod_bwd_contr5: contraction backward on 5 high bits -------------------
+# ---- prod_bwd_contr5 / prod_fwd_contr5: contractions on 5 high bits -----------
 def contr5_schedule_module():
     """cliffordcuda_amd/csrc/gen_contr5_schedule.py, the generator of the lane
-    schedule the kernel compiles in (contr5_schedule.h)."""
+    schedules the kernels compile in (contr5_schedule.h)."""
     import importlib.util
     import os
     path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "cliffordcuda_amd", "csrc",
@@ -817,94 +817,77 @@ def contr5_schedule_module():
 
 
 def _contr5_problem(op, a, b, gc, negh, lowneg, sched):
-    """One n = 9 problem as prod_bwd_contr5 runs it: per lane slot, 16 steps of
-    the frame schedule (contraction_frame_backward's per-pair arithmetic) in
-    three pieces, then the lane's outputs U, V, W (and the helper chunks added
-    to outputs 0 and 31) turned to the normal frame. Returns (ga, gb) blocks."""
-    steps, outs = sched.steps_by_slot(), sched.outputs_by_slot()
+    """One n = 9 problem as prod_bwd_contr5 runs it: per lane slot, steps 0-7
+    ga pairs and 8-15 gb pairs (the blocked backward's per-pair arithmetic),
+    four 4-step pieces, then per phase the slot's outputs (F, D, H/Q owners
+    adding their helpers' partials in slot order). Returns (ga, gb)."""
+    lc = op == LC
+    steps, outs = sched.steps_by_slot(lc), sched.outputs_by_slot(lc)
+    T = _tables(lowneg)
     rows = a.shape[:-1]
+    il = np.arange(16)
     full = 31
 
-    def yields_gb(sub):
-        return sub if op == LC else not sub
-
-    def contrib(o, p, sub):
-        X = o ^ p
-        g = gc[..., X * 16:(X + 1) * 16]
-        podd, oodd = popc(p) & 1, popc(o) & 1
-        w = []
-        for q in range(16):
-            e = 15 - q if sub else q
-            par = popc(q) & 1
-            if yields_gb(sub):
-                _, s = hi_sign(INNER, p, o, negh, 0, full, 0, 0)
-                f = s * (-1 if par and podd else 1) * (-1 if sub and (_frame_w1(q) ^ (lowneg & par)) else 1)
-                w.append(f * _rho(q) * a[..., p * 16 + e])
-            else:
-                _, s = hi_sign(INNER, o, p, negh, 0, full, 0, 0)
-                f = s * (-1 if par and oodd else 1) * (-1 if sub and (_frame_w2(q) ^ (lowneg & par)) else 1)
-                w.append(f * b[..., p * 16 + e])
-        if yields_gb(sub):
-            gg = [g[..., x] * (-1.0 if (popc(x) & 1 and podd) else 1.0) * _rho(x) for x in range(16)]
-        else:
-            gg = [g[..., x] for x in range(16)]
+    def pair(t, o, p):
+        g = gc[..., (o ^ p) * 16:((o ^ p) + 1) * 16]
         acc = np.zeros(rows + (16,))
-        for oo in range(16):
-            for q in range(16):
-                if oo & ~q & 15:
-                    continue
-                acc[..., oo] += low_sign(LC, lowneg, oo, q) * w[q] * gg[oo ^ q]
+        if t < 8:  # ga[o] over partner b[p]
+            ok, s = hi_sign(op, o, p, negh, 0, full, 0, 0)
+            assert ok
+            bt = b[..., p * 16:(p + 1) * 16] * s * np.where(PARITY16 & (popc(o) & 1), -1.0, 1.0)
+            tab = T[op]
+            for jl in range(16):
+                acc += tab[il, jl] * bt[..., jl:jl + 1] * g[..., il ^ jl]
+        else:  # gb[o] over partner a[p]
+            ok, s = hi_sign(op, p, o, negh, 0, full, 0, 0)
+            assert ok
+            fl = np.where(PARITY16 & (popc(p) & 1), -1.0, 1.0)
+            at = a[..., p * 16:(p + 1) * 16] * s * fl
+            gt = g * fl
+            tab = T[op]
+            for jl in range(16):
+                acc[..., jl] += (tab[il, jl] * at[..., il] * gt[..., il ^ jl]).sum(-1)
         return acc
-
-    fa = [(_frame_w1(k) ^ (lowneg & popc(k))) & 1 for k in range(16)]
-    fb = [(_frame_w2(k) ^ (lowneg & popc(k))) & 1 for k in range(16)]
-
-    def result(x, sub):
-        if yields_gb(sub):
-            x = x * np.array([_rho(k) for k in range(16)])
-        if sub:
-            f = fb if yields_gb(sub) else fa
-            x = np.stack([(-1.0 if f[k] else 1.0) * x[..., 15 - k] for k in range(16)], -1)
-        return x
 
     pieces = []
     for slot in range(32):
         ys = []
-        for t0, t1 in sched.PIECES:
+        for t0 in (0, 4, 8, 12):
             acc = np.zeros(rows + (16,))
-            for t in range(t0, t1):
+            for t in range(t0, t0 + 4):
                 if steps[slot][t] is not None:
-                    acc = acc + contrib(*steps[slot][t])
+                    acc = acc + pair(t, *steps[slot][t])
             ys.append(acc)
         pieces.append(ys)
-    chunks = {}
+    partial = {}
     for slot in range(32):
-        W = outs[slot][2]
-        if W is not None and isinstance(W[2], tuple):
-            chunks[W[2][1]] = pieces[slot][2]
+        for ph in range(2):
+            typ, b1, b2, ps, cnt = outs[slot][ph]
+            if typ == "help":
+                partial[ps] = pieces[slot][2 * ph] + pieces[slot][2 * ph + 1]
     ga = np.zeros(a.shape)
     gb = np.zeros(b.shape)
     seen = set()
 
-    def put(blk, sub, x):
-        assert (blk, sub) not in seen
-        seen.add((blk, sub))
-        dst = gb if yields_gb(sub) else ga
-        dst[..., blk * 16:(blk + 1) * 16] = result(x, sub)
+    def put(ph, blk, x):
+        assert (ph, blk) not in seen
+        seen.add((ph, blk))
+        (ga if ph == 0 else gb)[..., blk * 16:(blk + 1) * 16] = x
 
     for slot in range(32):
-        U, V, W = outs[slot]
-        y1, y2, y3 = pieces[slot]
-        u = y1 if U[2] == "y1" else (y1 + y2) + y3
-        if U[2] == "sum3+chunks":
-            base = 4 if U[1] else 0
-            for k in range(4):
-                u = u + chunks[base + k]
-        put(U[0], U[1], u)
-        if V is not None:
-            put(V[0], V[1], y2)
-        if W is not None and W[2] == "y3":
-            put(W[0], W[1], y3)
+        for ph in range(2):
+            typ, b1, b2, ps, cnt = outs[slot][ph]
+            y1, y2 = pieces[slot][2 * ph], pieces[slot][2 * ph + 1]
+            if typ == "F":
+                put(ph, b1, y1 + y2)
+            elif typ == "D":
+                put(ph, b1, y1)
+                put(ph, b2, y2)
+            elif typ == "own":
+                u = y1 + y2
+                for k in range(cnt):
+                    u = u + partial[ps + k]
+                put(ph, b1, u)
     assert len(seen) == 64
     return ga, gb
 
@@ -928,3 +911,60 @@ def contraction5_backward(op, a, b, gc, metric):
     ga1p, gb1 = _contr5_problem(LC, a[..., :h], b[..., h:], gc[..., h:], negh, lowneg, sched)
     ga = np.concatenate([ga0p + ga1p, np.zeros_like(a[..., h:])], -1)
     return ga, np.concatenate([gb0, gb1], -1)
+
+
+def contraction5_forward(op, a, b, metric):
+    """prod_fwd_contr5's forward: lc or rc at n = 9, lc at n = 10 with a null
+    top generator (c0 = lc9(a0, b0), c1 = lc9(a0, b1)). Per slot, 8 steps of
+    pairs (a[S], b[S | o]) (rc: (a[S | o], b[S])) in two pieces, helper chunks
+    added by their owners."""
+    sched = contr5_schedule_module()
+    n = len(metric)
+    neg = sum(1 << k for k, m in enumerate(metric) if m == -1)
+    lowneg = (neg & 15) == 15
+    negh = (neg >> 4) & 31
+    T = _tables(lowneg)
+    full = 31
+
+    def problem(a9, b9):
+        steps, outs = sched.fwd_steps_by_slot(), sched.fwd_outputs_by_slot()
+        rows = a9.shape[:-1]
+        pieces = []
+        for slot in range(32):
+            ys = []
+            for t0 in (0, 4):
+                acc = np.zeros(rows + (16,))
+                for t in range(t0, t0 + 4):
+                    st = steps[slot][t]
+                    if st is None:
+                        continue
+                    o, S = st
+                    ih, jh = (S, S | o) if op == LC else (S | o, S)
+                    ok, s = hi_sign(op, ih, jh, negh, 0, full, 0, 0)
+                    assert ok
+                    bt = b9[..., jh * 16:(jh + 1) * 16] * s * np.where(PARITY16 & (popc(ih) & 1), -1.0, 1.0)
+                    av = a9[..., ih * 16:(ih + 1) * 16]
+                    tab = T[op]
+                    for tt in range(16):
+                        l = np.arange(16)
+                        acc[..., tt] += (tab[l, l ^ tt] * av[..., l] * bt[..., l ^ tt]).sum(-1)
+                ys.append(acc)
+            pieces.append(ys)
+        chunks = {}
+        for slot in range(32):
+            h, how, c0, cnt, cw = outs[slot]
+            if cw >= 0:
+                chunks[cw] = pieces[slot][1]
+        c = np.zeros(a9.shape)
+        for slot in range(32):
+            h, how, c0, cnt, cw = outs[slot]
+            u = pieces[slot][0] + pieces[slot][1] if how == "y1+y2" else pieces[slot][0]
+            for k in range(cnt):
+                u = u + chunks[c0 + k]
+            c[..., h * 16:(h + 1) * 16] = u
+        return c
+
+    if n == 9:
+        return problem(a, b)
+    assert n == 10 and op == LC and metric[9] == 0
+    return np.concatenate([problem(a[..., :512], b[..., :512]), problem(a[..., :512], b[..., 512:])], -1)

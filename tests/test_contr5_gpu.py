@@ -1,9 +1,9 @@
-"""prod_bwd_contr5 (the contractions' backward on 5 high bits: lc and rc at
-n = 9, lc at n = 10 whose only null generator is e9, C5's Cl(9,0,1)): parity
-with the fp64 oracle, with the balanced kernels it replaces
+"""prod_fwd_contr5 / prod_bwd_contr5 (the contractions on 5 high bits: lc and
+rc at n = 9, lc at n = 10 whose only null generator is e9, C5's Cl(9,0,1)):
+parity with the fp64 oracle, with the balanced kernels they replace
 (CLF_PRODUCT_PATH=balanced), on ragged batches (two rows per wave at n = 9),
 with a batch-stride-0 upstream gradient, and bitwise row independence.
-Bar: normwise relative error <= 1e-5 for both gradients."""
+Bar: normwise relative error <= 1e-5 for the product and both gradients."""
 import pytest
 import torch
 
@@ -53,6 +53,9 @@ def test_contr5_matches_oracle(case):
     b64 = b[rows].double().requires_grad_()
     O.einsum_product(op, a64, b64, metric).backward(gc[rows].double())
     rs = rows.cuda()
+    with torch.no_grad():
+        c64 = O.einsum_product(op, a[rows].double(), b[rows].double(), metric)
+    assert rel_err(c[rs], c64) <= TOL
     assert rel_err(x.grad[rs], a64.grad) <= TOL
     assert rel_err(y.grad[rs], b64.grad) <= TOL
 
@@ -74,11 +77,12 @@ def test_contr5_equals_balanced_kernels(case, clf_env):
             y = b.clone().requires_grad_()
             c = products.product(op, x, y, metric)
             c.backward(gc)
-            res.append((x.grad, y.grad))
+            res.append((x.grad, y.grad, c.detach()))
             if path:
                 clf_env.delenv("CLF_PRODUCT_PATH")
         assert rel_err(res[0][0], res[1][0]) <= TOL
         assert rel_err(res[0][1], res[1][1]) <= TOL
+        assert rel_err(res[0][2], res[1][2]) <= TOL
 
 
 @pytest.mark.parametrize("case", CASES[::3], ids=_ids)
@@ -115,3 +119,6 @@ def test_contr5_rows_are_independent():
     ga_s, gb_s = products._product_bwd(code, 10, neg, nul, a[idx].contiguous(), b[idx].contiguous(),
                                        gc[idx].contiguous(), True, True)
     assert torch.equal(ga[idx], ga_s) and torch.equal(gb[idx], gb_s)
+    c = products._product_fwd(code, 10, neg, nul, a, b)
+    c_s = products._product_fwd(code, 10, neg, nul, a[idx].contiguous(), b[idx].contiguous())
+    assert torch.equal(c[idx], c_s)

@@ -288,31 +288,50 @@ def test_contr5_header_is_the_generators():
     assert open(path).read() == sched.header_text()
 
 
-def test_contr5_schedule_covers_every_pair_once():
-    """Every (output, partner, mode) block pair of a 5-high-bit problem appears
-    exactly once across the 32 lanes' 16 steps (sub: p inside o, sup: p
-    containing o; the pair (o, o) once in each mode), and every output is
-    written by exactly one lane's U, V or W (outputs 0 and 31 also taking the
-    four helper chunks of their list)."""
+@pytest.mark.parametrize("lc", [True, False])
+def test_contr5_schedule_covers_every_pair_once(lc):
+    """Every ga pair (steps 0-7) and gb pair (steps 8-15) of a 5-high-bit
+    problem appears exactly once across the 32 lanes, every output is written
+    once per phase, and every helper partial is read by one owner."""
     sched = K.contr5_schedule_module()
-    seen = []
-    for row in sched.steps_by_slot():
-        for s in row:
-            if s is not None:
-                seen.append(s)
-    want = [(o, p, True) for o in range(32) for p in range(32) if p & ~o == 0]
-    want += [(o, p, False) for o in range(32) for p in range(32) if o & ~p == 0]
-    assert sorted(seen) == sorted(want)
-    outs = [d for slot in sched.outputs_by_slot() for d in slot if d is not None and not isinstance(d[2], tuple)]
-    assert sorted((d[0], d[1]) for d in outs) == sorted((o, s) for o in range(32) for s in (False, True))
-    assert sorted(sched.PERM) == list(range(32))
+    steps = sched.steps_by_slot(lc)
+    for phase, lo in (("A", 0), ("B", 8)):
+        seen = sorted(s for row in steps for s in row[lo:lo + 8] if s is not None)
+        want = sorted((o, p) for o in range(32) for p in sched.plist(o, phase, lc))
+        assert seen == want
+    outs = sched.outputs_by_slot(lc)
+    for ph in range(2):
+        blocks, written, read = [], set(), []
+        for row in outs:
+            typ, b1, b2, ps, cnt = row[ph]
+            if typ == "D":
+                blocks += [b1, b2]
+            elif typ in ("F", "own"):
+                blocks.append(b1)
+            if typ == "help":
+                written.add(ps)
+            if typ == "own":
+                read += list(range(ps, ps + cnt))
+        assert sorted(blocks) == list(range(32))
+        assert sorted(read) == sorted(written) and len(read) == 8
+
+
+def test_contr5_fwd_schedule_covers_every_pair_once():
+    sched = K.contr5_schedule_module()
+    seen = sorted(s for row in sched.fwd_steps_by_slot() for s in row if s is not None)
+    assert seen == sorted((o, S) for o in range(32) for S in sched.fwd_list(o))
+    written = sorted(cw for h, how, c0, cnt, cw in sched.fwd_outputs_by_slot() if cw >= 0)
+    read = sorted(c0 + k for h, how, c0, cnt, cw in sched.fwd_outputs_by_slot() for k in range(cnt))
+    assert written == read == list(range(16))
+    assert sorted(h for h, *_ in sched.fwd_outputs_by_slot()) == list(range(32))
 
 
 def test_contr5_lds_conflicts_recorded():
-    """The searched layout's bank-conflict count (extra LDS cycles per problem
-    row, 64 read groups of 4 instructions) stays at its recorded value."""
+    """The searched layouts' bank-conflict counts (extra LDS cycles per problem
+    row) stay at their recorded values."""
     sched = K.contr5_schedule_module()
-    assert sched.lds_conflicts() <= 62
+    assert sched.lds_conflicts(True) <= 2 and sched.lds_conflicts(False) <= 4
+    assert sched.fwd_lds_conflicts() <= 0
 
 
 @pytest.mark.parametrize("op", [K.LC, K.RC])
@@ -325,6 +344,24 @@ def test_contraction5_backward_n9(op, metric):
     O.einsum_product("lc" if op == K.LC else "rc", at, bt, metric).backward(gc)
     np.testing.assert_allclose(ga, at.grad.numpy(), rtol=0, atol=1e-10)
     np.testing.assert_allclose(gb, bt.grad.numpy(), rtol=0, atol=1e-10)
+
+
+@pytest.mark.parametrize("op", [K.LC, K.RC])
+@pytest.mark.parametrize("metric", [(1,) * 9, (-1,) * 4 + (1, -1, 1, 1, -1), (1,) * 4 + (-1,) * 5])
+def test_contraction5_forward_n9(op, metric):
+    g = torch.Generator().manual_seed(19)
+    a, b = (torch.randn(2, 512, generator=g, dtype=torch.float64) for _ in range(2))
+    c = K.contraction5_forward(op, a.numpy(), b.numpy(), metric)
+    ref = O.einsum_product("lc" if op == K.LC else "rc", a, b, metric)
+    np.testing.assert_allclose(c, ref.numpy(), rtol=0, atol=1e-10)
+
+
+@pytest.mark.parametrize("metric", [(1,) * 9 + (0,), (1,) * 4 + (-1, 1, 1, -1, 1, 0)])
+def test_contraction5_forward_null_top(metric):
+    g = torch.Generator().manual_seed(20)
+    a, b = (torch.randn(2, 1024, generator=g, dtype=torch.float64) for _ in range(2))
+    c = K.contraction5_forward(K.LC, a.numpy(), b.numpy(), metric)
+    np.testing.assert_allclose(c, O.einsum_product("lc", a, b, metric).numpy(), rtol=0, atol=1e-10)
 
 
 @pytest.mark.parametrize("metric", [(1,) * 9 + (0,), (1,) * 4 + (-1, 1, 1, -1, 1, 0), (-1,) * 9 + (0,)])
