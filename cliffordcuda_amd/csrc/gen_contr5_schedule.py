@@ -22,9 +22,10 @@ then a 4-pair chunk of output 0 (6 chunks) or of a |h| = 1 output (2 chunks
 each), which the owner adds through LDS.
 
 Which slot holds which role, the pair order inside each piece and the
-blocks' LDS slot swizzle are free; the values in LAYOUT were searched
-(simulated annealing on the CPU, lds_conflicts below) so that the 16 lanes of
-a quarter-wave read blocks on distinct 16-byte bank groups."""
+blocks' LDS slot swizzle are free; the values in LAYOUT and FWD_LAYOUT were
+searched (simulated annealing on the CPU) against the LDS rules measured on
+MI355X (LDS_SETS, WRITE_SETS below): the block reads of every step and the
+result traffic after the last one (partials, chunks, puts)."""
 from __future__ import annotations
 
 NB, FULL = 32, 31
@@ -150,19 +151,27 @@ def outputs_by_slot(lc=True, lay=None):
     return res
 
 
+# ds_read_b128 on gfx950 serves a wave in four cycles of 16 lanes: each 32-lane
+# half in two sets split by the parity of lane bits 2-4 ({0-3, 12-15, 20-23,
+# 24-27} and {4-7, 8-11, 16-19, 28-31}); a set takes one cycle per distinct
+# address on its busiest 16-byte bank group (address bits 4-7), and lanes
+# reading the same address share it. Fitted to SQ_LDS_BANK_CONFLICT over 139
+# address patterns on MI355X. A problem's 32 lanes are one half.
+LDS_SETS = [[s for s in range(32) if popc(s & 28) % 2 == k] for k in (0, 1)]
+
+
 def lds_conflicts(lc=True, lay=None):
-    """Extra LDS cycles of one problem's block reads: per step, quarter-wave and
-    operand (partner, gc), the largest number of distinct blocks on one 16-byte
-    bank group, minus one (ds_read_b128 serves 16 lanes per cycle; the same
-    address read by several lanes was measured to cost nothing)."""
+    """Extra LDS cycles of one problem's block reads: per step, lane set (LDS_SETS)
+    and operand (partner, gc), the largest number of distinct blocks on one
+    16-byte bank group, minus one."""
     lay = lay or LAYOUT[lc]
     steps = steps_by_slot(lc, lay)
     total = 0
     for t in range(16):
-        for qw in range(2):
+        for lanes in LDS_SETS:
             for kind in (0, 1):
                 groups = {}
-                for s in range(16 * qw, 16 * qw + 16):
+                for s in lanes:
                     st = steps[s][t]
                     if st is None:
                         addr, bank = ("z",), (0, 0)
@@ -175,20 +184,68 @@ def lds_conflicts(lc=True, lay=None):
     return total
 
 
-# searched layouts (extra LDS cycles per problem row: lc 2, rc 4; 40 for Layout.default())
+def _set_cost(items, sets, gmask):
+    """Extra cycles of one instruction: per lane set, the largest number of
+    distinct addresses on one bank group (address bits 4 and up, masked), minus one."""
+    tot = 0
+    for lanes in sets:
+        groups = {}
+        for s, a in items:
+            if s in lanes:
+                groups.setdefault((a >> 4) & gmask, set()).add(a)
+        if groups:
+            tot += max(len(v) for v in groups.values()) - 1
+    return tot
+
+
+# ds_write_b128 serves 8 consecutive lanes per cycle over 32 banks: bank group =
+# address bits 4-6 (fitted the same way, 87 patterns).
+WRITE_SETS = [set(range(8 * i, 8 * i + 8)) for i in range(4)]
+READ_SETS = [set(x) for x in LDS_SETS]
+
+
+def lds_write_conflicts(lc=True, lay=None):
+    """Extra LDS cycles of one problem's result traffic, per 16-byte chunk q (the
+    same for every q): helpers' partial stores, owners' partial reads, and the
+    blocks put into the staging rows (D lanes' two blocks and the others' one are
+    separate instructions). Reads count 0.7 of a cycle per conflict, as measured."""
+    lay = lay or LAYOUT[lc]
+    outs = outputs_by_slot(lc, lay)
+    tot = 0.0
+    for ph in (0, 1):
+        put1, put2, putf, helpers = [], [], [], []
+        owner_reads = [[], [], []]
+        for s, o in enumerate(outs):
+            kind, b1, b2, ps, cnt = o[ph]
+            if kind == "D":
+                put1.append((s, 16 * ((b1 << 2) | lay.swz[b1])))
+                put2.append((s, 16 * ((b2 << 2) | lay.swz[b2])))
+            elif kind == "help":
+                helpers.append((s, 64 * ps))
+            else:
+                putf.append((s, 16 * ((b1 << 2) | lay.swz[b1])))
+                for k in range(cnt):
+                    owner_reads[k].append((s, 64 * (ps + k)))
+        tot += sum(_set_cost(x, WRITE_SETS, 7) for x in (put1, put2, putf, helpers))
+        tot += 0.7 * sum(_set_cost(x, READ_SETS, 15) for x in owner_reads)
+    return tot
+
+
+# searched layouts (conflict units per problem and chunk q, reads (lds_conflicts) + result traffic
+# (lds_write_conflicts): lc 3 + 0, rc 1 + 0.7; Layout.default(): 43 + 18.4)
 LAYOUT = {
     True: Layout(
-        slotA=[7, 0, 17, 2, 22, 29, 3, 26, 5, 10, 24, 15, 27, 14, 23, 16, 8, 13, 30, 20, 31, 12, 19, 9, 1, 4, 6, 11, 28, 21, 25, 18],
-        slotB=[3, 13, 7, 19, 30, 10, 17, 31, 16, 1, 6, 2, 18, 8, 11, 12, 15, 20, 25, 27, 5, 0, 9, 23, 29, 14, 21, 26, 28, 24, 22, 4],
-        ordA=[[3, 2, 0, 1, 5, 4, 7, 6], [3, 0, 2, 1, 5, 4, 7, 6], [3, 1, 0, 2, 4, 5, 6, 7], [3, 2, 1, 0, 6, 5, 7, 4], [0, 3, 1, 2, 4, 5, 7, 6], [1, 0, 2, 3, 5, 7, 4, 6], [2, 3, 1, 0, 5, 6, 7, 4], [1, 3, 2, 0, 7, 5, 4, 6], [2, 3, 0, 1, 4, 5, 7, 6], [1, 0, 2, 3, 4, 7, 6, 5], [1, 2, 3, 0, 6, 5, 7, 4], [3, 2, 0, 1, 4, 5, 7, 6], [0, 3, 2, 1, 4, 7, 5, 6], [3, 2, 0, 1, 5, 4, 7, 6], [1, 2, 3, 0, 4, 6, 5, 7], [2, 0, 3, 1, 5, 6, 4, 7], [2, 1, 3, 0, 6, 4, 7, 5], [1, 0, 2, 3, 6, 7, 4, 5], [0, 2, 3, 1, 4, 6, 7, 5], [0, 2, 1, 3, 6, 7, 5, 4], [0, 2, 3, 1, 7, 6, 5, 4], [3, 0, 1, 2, 4, 7, 5, 6], [2, 3, 0, 1, 6, 7, 4, 5], [3, 2, 0, 1, 4, 6, 7, 5], [0, 3, 2, 1, 5, 6, 7, 4], [1, 0, 2, 3, 7, 6, 4, 5], [0, 1, 2, 3, 6, 7, 5, 4], [0, 3, 2, 1, 7, 5, 6, 4], [1, 3, 2, 0, 7, 6, 4, 5], [2, 3, 1, 0, 5, 7, 6, 4], [3, 2, 1, 0, 7, 6, 4, 5], [3, 0, 2, 1, 6, 7, 4, 5]],
-        ordB=[[2, 1, 3, 0, 5, 6, 7, 4], [1, 3, 0, 2, 7, 5, 6, 4], [0, 3, 1, 2, 6, 5, 7, 4], [0, 2, 1, 3, 5, 7, 6, 4], [0, 3, 1, 2, 6, 5, 4, 7], [1, 2, 3, 0, 6, 4, 7, 5], [3, 1, 0, 2, 6, 5, 7, 4], [0, 3, 1, 2, 6, 5, 7, 4], [3, 2, 1, 0, 5, 7, 6, 4], [1, 0, 2, 3, 5, 6, 4, 7], [3, 0, 2, 1, 4, 7, 5, 6], [3, 1, 0, 2, 6, 5, 7, 4], [0, 3, 1, 2, 6, 7, 5, 4], [2, 0, 1, 3, 5, 7, 6, 4], [3, 1, 2, 0, 5, 4, 7, 6], [0, 2, 3, 1, 4, 6, 7, 5], [0, 3, 2, 1, 5, 4, 6, 7], [3, 2, 1, 0, 4, 6, 7, 5], [0, 3, 2, 1, 5, 4, 6, 7], [0, 2, 1, 3, 5, 6, 7, 4], [3, 0, 1, 2, 4, 5, 6, 7], [1, 0, 2, 3, 5, 6, 7, 4], [0, 1, 2, 3, 7, 6, 5, 4], [3, 2, 0, 1, 7, 4, 6, 5], [2, 1, 0, 3, 5, 6, 4, 7], [3, 2, 1, 0, 5, 6, 4, 7], [2, 1, 3, 0, 6, 4, 5, 7], [2, 3, 1, 0, 5, 7, 4, 6], [1, 2, 0, 3, 5, 6, 4, 7], [1, 2, 3, 0, 6, 4, 5, 7], [1, 2, 3, 0, 7, 5, 4, 6], [1, 3, 2, 0, 4, 5, 7, 6]],
-        swz=[0, 3, 0, 2, 2, 1, 2, 1, 1, 2, 3, 0, 3, 3, 1, 3, 3, 0, 1, 3, 1, 1, 3, 1, 2, 2, 2, 0, 3, 0, 0, 2]),
+        slotA=[24, 27, 16, 30, 14, 21, 19, 4, 0, 25, 5, 15, 23, 18, 1, 20, 7, 17, 9, 10, 6, 31, 13, 26, 2, 22, 12, 29, 28, 11, 8, 3],
+        slotB=[22, 26, 20, 25, 4, 23, 24, 6, 21, 5, 28, 0, 18, 29, 8, 12, 27, 11, 2, 13, 14, 15, 16, 10, 7, 31, 1, 30, 3, 19, 17, 9],
+        ordA=[[1, 0, 3, 2, 6, 5, 4, 7], [2, 3, 0, 1, 5, 7, 6, 4], [3, 1, 0, 2, 5, 4, 6, 7], [0, 1, 3, 2, 4, 6, 7, 5], [1, 2, 0, 3, 6, 5, 4, 7], [0, 3, 1, 2, 6, 4, 5, 7], [1, 0, 2, 3, 7, 4, 5, 6], [1, 2, 0, 3, 6, 7, 5, 4], [0, 1, 2, 3, 7, 6, 4, 5], [1, 0, 2, 3, 5, 6, 4, 7], [2, 3, 0, 1, 7, 6, 5, 4], [3, 1, 0, 2, 4, 6, 7, 5], [1, 0, 2, 3, 4, 6, 5, 7], [3, 0, 1, 2, 7, 5, 4, 6], [0, 2, 3, 1, 7, 4, 6, 5], [3, 0, 1, 2, 5, 7, 4, 6], [0, 1, 2, 3, 7, 5, 4, 6], [0, 3, 1, 2, 4, 7, 5, 6], [0, 2, 1, 3, 6, 7, 5, 4], [3, 2, 0, 1, 6, 7, 5, 4], [1, 3, 2, 0, 5, 4, 7, 6], [1, 3, 0, 2, 6, 5, 4, 7], [2, 0, 3, 1, 6, 4, 7, 5], [0, 3, 2, 1, 7, 6, 5, 4], [0, 2, 1, 3, 5, 4, 6, 7], [2, 1, 0, 3, 6, 7, 4, 5], [2, 0, 1, 3, 5, 4, 6, 7], [2, 0, 3, 1, 5, 4, 6, 7], [0, 1, 2, 3, 7, 4, 5, 6], [2, 1, 3, 0, 5, 4, 6, 7], [2, 1, 3, 0, 4, 5, 7, 6], [2, 3, 1, 0, 6, 5, 4, 7]],
+        ordB=[[2, 3, 0, 1, 5, 6, 7, 4], [0, 2, 1, 3, 7, 6, 5, 4], [0, 2, 3, 1, 7, 6, 4, 5], [3, 1, 2, 0, 5, 6, 4, 7], [2, 3, 0, 1, 5, 6, 7, 4], [0, 1, 3, 2, 7, 6, 5, 4], [3, 1, 2, 0, 6, 7, 5, 4], [2, 0, 1, 3, 4, 7, 5, 6], [0, 1, 2, 3, 5, 4, 6, 7], [0, 2, 1, 3, 6, 4, 7, 5], [0, 3, 1, 2, 7, 6, 5, 4], [3, 2, 0, 1, 6, 4, 5, 7], [3, 0, 2, 1, 5, 4, 6, 7], [3, 0, 2, 1, 6, 5, 4, 7], [1, 2, 0, 3, 7, 5, 4, 6], [0, 2, 1, 3, 4, 6, 7, 5], [1, 0, 3, 2, 5, 7, 6, 4], [3, 1, 2, 0, 4, 5, 6, 7], [1, 0, 3, 2, 5, 7, 6, 4], [2, 1, 3, 0, 4, 5, 6, 7], [3, 0, 2, 1, 5, 4, 6, 7], [0, 2, 1, 3, 7, 6, 5, 4], [3, 0, 2, 1, 6, 5, 4, 7], [1, 3, 2, 0, 5, 7, 4, 6], [3, 1, 0, 2, 5, 7, 4, 6], [2, 1, 0, 3, 7, 5, 6, 4], [2, 1, 0, 3, 6, 7, 5, 4], [3, 0, 1, 2, 7, 5, 4, 6], [3, 0, 2, 1, 6, 5, 4, 7], [1, 2, 0, 3, 6, 7, 5, 4], [0, 3, 2, 1, 6, 5, 7, 4], [0, 3, 2, 1, 4, 5, 6, 7]],
+        swz=[2, 1, 3, 1, 1, 3, 2, 3, 0, 2, 1, 0, 2, 2, 1, 0, 3, 0, 0, 2, 3, 3, 2, 2, 1, 1, 0, 3, 1, 0, 3, 1]),
     False: Layout(
-        slotA=[11, 16, 4, 1, 7, 13, 12, 15, 18, 17, 31, 19, 22, 21, 8, 20, 14, 23, 24, 0, 2, 29, 27, 9, 10, 25, 5, 6, 30, 3, 26, 28],
-        slotB=[25, 5, 21, 15, 17, 0, 23, 9, 16, 13, 20, 28, 10, 19, 30, 11, 1, 22, 7, 12, 2, 29, 24, 14, 3, 31, 27, 18, 26, 4, 8, 6],
-        ordA=[[1, 0, 2, 3, 4, 6, 5, 7], [3, 2, 0, 1, 6, 4, 7, 5], [2, 0, 3, 1, 6, 5, 7, 4], [3, 0, 2, 1, 6, 5, 4, 7], [0, 3, 2, 1, 5, 4, 6, 7], [0, 3, 1, 2, 4, 6, 7, 5], [1, 0, 3, 2, 6, 5, 7, 4], [3, 0, 2, 1, 6, 7, 4, 5], [0, 2, 3, 1, 6, 5, 4, 7], [2, 1, 0, 3, 4, 7, 5, 6], [0, 3, 1, 2, 6, 4, 7, 5], [3, 2, 1, 0, 5, 4, 7, 6], [3, 2, 0, 1, 5, 4, 7, 6], [0, 3, 1, 2, 6, 7, 4, 5], [0, 3, 1, 2, 7, 4, 6, 5], [3, 0, 1, 2, 5, 4, 7, 6], [0, 3, 1, 2, 6, 4, 7, 5], [0, 2, 3, 1, 7, 5, 6, 4], [0, 1, 2, 3, 6, 4, 7, 5], [3, 2, 0, 1, 4, 5, 7, 6], [1, 0, 2, 3, 7, 4, 6, 5], [2, 1, 0, 3, 4, 5, 7, 6], [0, 3, 1, 2, 4, 6, 5, 7], [3, 0, 2, 1, 5, 6, 4, 7], [3, 2, 1, 0, 6, 4, 7, 5], [2, 1, 0, 3, 7, 4, 6, 5], [2, 3, 1, 0, 7, 4, 5, 6], [3, 1, 2, 0, 5, 4, 6, 7], [1, 0, 2, 3, 6, 4, 7, 5], [2, 3, 1, 0, 6, 4, 5, 7], [1, 3, 0, 2, 4, 5, 7, 6], [3, 0, 1, 2, 4, 5, 6, 7]],
-        ordB=[[2, 3, 0, 1, 6, 5, 7, 4], [1, 0, 2, 3, 5, 6, 7, 4], [3, 2, 1, 0, 5, 6, 4, 7], [1, 3, 0, 2, 7, 4, 5, 6], [1, 3, 0, 2, 6, 5, 4, 7], [1, 2, 0, 3, 5, 4, 7, 6], [0, 1, 3, 2, 7, 5, 4, 6], [3, 0, 2, 1, 6, 4, 7, 5], [3, 1, 0, 2, 4, 6, 5, 7], [2, 0, 3, 1, 4, 6, 5, 7], [0, 2, 1, 3, 7, 4, 5, 6], [2, 3, 1, 0, 6, 5, 4, 7], [3, 1, 2, 0, 4, 6, 5, 7], [3, 1, 2, 0, 7, 6, 4, 5], [2, 0, 3, 1, 5, 6, 4, 7], [1, 3, 0, 2, 6, 5, 4, 7], [2, 3, 1, 0, 6, 5, 7, 4], [3, 2, 0, 1, 5, 7, 4, 6], [2, 0, 1, 3, 6, 7, 4, 5], [1, 2, 3, 0, 6, 7, 4, 5], [2, 1, 3, 0, 4, 5, 6, 7], [3, 1, 2, 0, 4, 6, 5, 7], [0, 2, 1, 3, 7, 6, 4, 5], [1, 2, 0, 3, 7, 5, 4, 6], [2, 0, 3, 1, 7, 5, 4, 6], [1, 3, 0, 2, 5, 7, 4, 6], [1, 2, 3, 0, 4, 7, 5, 6], [0, 2, 3, 1, 6, 7, 4, 5], [0, 3, 1, 2, 5, 7, 4, 6], [3, 2, 0, 1, 5, 7, 4, 6], [1, 3, 0, 2, 6, 5, 7, 4], [2, 1, 3, 0, 4, 5, 6, 7]],
-        swz=[2, 0, 1, 0, 1, 2, 0, 1, 3, 3, 3, 3, 3, 3, 2, 1, 0, 1, 2, 2, 0, 2, 0, 0, 1, 1, 3, 2, 2, 0, 1, 3]),
+        slotA=[30, 5, 29, 26, 11, 21, 9, 3, 23, 2, 22, 15, 27, 8, 0, 16, 1, 31, 7, 19, 6, 10, 28, 20, 14, 25, 18, 24, 13, 12, 17, 4],
+        slotB=[12, 31, 24, 2, 4, 1, 6, 8, 14, 13, 30, 19, 29, 21, 17, 26, 5, 7, 22, 28, 20, 18, 27, 16, 25, 15, 3, 9, 11, 10, 23, 0],
+        ordA=[[3, 0, 1, 2, 4, 6, 7, 5], [1, 0, 3, 2, 5, 4, 7, 6], [3, 0, 1, 2, 6, 5, 7, 4], [1, 0, 3, 2, 5, 4, 7, 6], [0, 2, 1, 3, 7, 4, 6, 5], [0, 3, 2, 1, 5, 7, 4, 6], [3, 0, 1, 2, 7, 6, 4, 5], [0, 1, 3, 2, 5, 7, 6, 4], [3, 0, 2, 1, 4, 6, 7, 5], [1, 3, 2, 0, 5, 4, 6, 7], [3, 0, 2, 1, 5, 4, 6, 7], [0, 1, 2, 3, 5, 6, 7, 4], [0, 1, 3, 2, 5, 6, 7, 4], [2, 3, 1, 0, 7, 5, 4, 6], [0, 3, 2, 1, 6, 5, 4, 7], [0, 1, 3, 2, 7, 6, 5, 4], [2, 1, 3, 0, 5, 7, 4, 6], [0, 3, 2, 1, 6, 7, 4, 5], [2, 0, 3, 1, 5, 4, 7, 6], [2, 0, 1, 3, 6, 7, 4, 5], [2, 1, 0, 3, 4, 5, 6, 7], [1, 2, 3, 0, 4, 7, 6, 5], [2, 1, 3, 0, 4, 7, 5, 6], [3, 1, 0, 2, 4, 5, 7, 6], [1, 2, 3, 0, 5, 4, 6, 7], [3, 1, 2, 0, 5, 4, 6, 7], [3, 1, 0, 2, 7, 4, 5, 6], [3, 0, 2, 1, 7, 4, 5, 6], [3, 1, 0, 2, 6, 5, 4, 7], [3, 0, 2, 1, 6, 4, 7, 5], [1, 2, 3, 0, 4, 6, 5, 7], [2, 3, 1, 0, 7, 5, 4, 6]],
+        ordB=[[3, 2, 1, 0, 6, 4, 7, 5], [1, 2, 3, 0, 6, 7, 4, 5], [2, 0, 1, 3, 5, 7, 4, 6], [3, 1, 2, 0, 5, 6, 4, 7], [1, 2, 3, 0, 6, 4, 5, 7], [2, 3, 1, 0, 4, 5, 7, 6], [1, 2, 3, 0, 5, 4, 6, 7], [2, 0, 1, 3, 4, 5, 7, 6], [0, 3, 1, 2, 5, 6, 4, 7], [0, 3, 1, 2, 4, 7, 5, 6], [2, 3, 0, 1, 4, 7, 6, 5], [2, 3, 0, 1, 6, 7, 4, 5], [2, 0, 1, 3, 6, 7, 5, 4], [2, 1, 3, 0, 7, 4, 5, 6], [0, 3, 1, 2, 4, 5, 6, 7], [3, 2, 0, 1, 7, 5, 6, 4], [3, 0, 2, 1, 7, 4, 6, 5], [3, 0, 2, 1, 7, 4, 6, 5], [0, 2, 1, 3, 7, 6, 5, 4], [2, 3, 1, 0, 5, 7, 4, 6], [1, 3, 0, 2, 4, 7, 5, 6], [0, 3, 2, 1, 4, 7, 5, 6], [1, 3, 2, 0, 7, 6, 5, 4], [2, 3, 0, 1, 7, 4, 5, 6], [1, 2, 0, 3, 4, 7, 6, 5], [3, 0, 2, 1, 4, 7, 6, 5], [0, 3, 2, 1, 5, 7, 4, 6], [1, 2, 0, 3, 5, 7, 4, 6], [2, 3, 0, 1, 6, 4, 7, 5], [3, 2, 1, 0, 4, 7, 6, 5], [1, 3, 2, 0, 5, 6, 7, 4], [0, 3, 1, 2, 6, 5, 4, 7]],
+        swz=[1, 3, 3, 1, 2, 0, 0, 0, 0, 1, 1, 2, 1, 2, 1, 0, 3, 2, 2, 3, 2, 0, 0, 3, 3, 1, 2, 2, 3, 3, 3, 1]),
 }
 
 
@@ -260,10 +317,10 @@ def fwd_lds_conflicts(lc=True, lay=None):
     steps = fwd_steps_by_slot(lay)
     total = 0
     for t in range(FT):
-        for qw in range(2):
+        for lanes in LDS_SETS:
             for kind in (0, 1):
                 groups = {}
-                for s in range(16 * qw, 16 * qw + 16):
+                for s in lanes:
                     st = steps[s][t]
                     if st is None:
                         addr, bank = ("z",), (0, 0)
@@ -277,12 +334,36 @@ def fwd_lds_conflicts(lc=True, lay=None):
     return total
 
 
-# searched layout (extra LDS cycles per problem row of lc: 0; 18 for FwdLayout.default())
+def fwd_chunk_swz(c):
+    """Slot swizzle of chunk slot c: its float4 q sits at 4 c + (q ^ fwd_chunk_swz(c))."""
+    return (c >> 1) & 3
+
+
+def fwd_lds_write_conflicts(lay=None):
+    """The forward's result traffic, averaged over the chunk's float4 q: helpers'
+    chunk stores, owners' chunk reads (all owners run the longest count's
+    iterations) and the puts of every lane's own block."""
+    lay = lay or FWD_LAYOUT
+    outs = fwd_outputs_by_slot(lay)
+
+    def chunk(c, q):
+        return 16 * (4 * c + (q ^ fwd_chunk_swz(c)))
+
+    tot = float(_set_cost([(s, 16 * ((o[0] << 2) | lay.swz[o[0]])) for s, o in enumerate(outs)], WRITE_SETS, 7))
+    for q in range(4):
+        tot += 0.25 * _set_cost([(s, chunk(o[4], q)) for s, o in enumerate(outs) if o[4] >= 0], WRITE_SETS, 7)
+        for k in range(6):
+            tot += 0.25 * 0.7 * _set_cost([(s, chunk(o[2] + k, q)) for s, o in enumerate(outs) if k < o[3]],
+                                          READ_SETS, 15)
+    return tot
+
+
+# searched layout (lc: reads 0, result traffic 1.4)
 FWD_LAYOUT = FwdLayout(
-    perm=[22, 0, 4, 7, 29, 20, 19, 24, 17, 18, 2, 21, 27, 1, 8, 16, 31, 12, 14, 23, 26, 30, 3, 25, 15, 10, 28, 13, 5, 6, 9, 11],
-    assign={7: (2, 1), 11: (1, 1), 13: (1, 0), 14: (4, 0), 15: (0, 3), 19: (16, 0), 21: (0, 0), 22: (16, 1), 23: (0, 2), 25: (8, 1), 26: (8, 0), 27: (0, 5), 28: (2, 0), 29: (0, 1), 30: (0, 4), 31: (4, 1)},
-    order={0: [3, 2, 0, 1, 5, 4, 7, 6], 1: [1, 0, 2, 3, 7, 5, 4, 6], 2: [1, 2, 0, 3, 7, 5, 4, 6], 3: [2, 3, 1, 0, 4, 7, 5, 6], 4: [3, 0, 1, 2, 5, 6, 4, 7], 5: [1, 3, 0, 2, 7, 6, 5, 4], 6: [3, 2, 0, 1, 7, 5, 6, 4], 7: [0, 1, 3, 2, 6, 4, 5, 7], 8: [2, 0, 1, 3, 7, 6, 4, 5], 9: [1, 3, 0, 2, 6, 7, 4, 5], 10: [1, 3, 0, 2, 6, 7, 5, 4], 11: [3, 2, 1, 0, 6, 5, 4, 7], 12: [3, 1, 0, 2, 7, 6, 4, 5], 13: [3, 2, 1, 0, 4, 5, 7, 6], 14: [2, 1, 3, 0, 6, 7, 4, 5], 15: [3, 1, 0, 2, 7, 5, 6, 4], 16: [0, 1, 3, 2, 4, 6, 7, 5], 17: [2, 1, 0, 3, 7, 4, 5, 6], 18: [2, 1, 0, 3, 6, 4, 5, 7], 19: [1, 2, 0, 3, 7, 6, 5, 4], 20: [3, 0, 2, 1, 7, 4, 5, 6], 21: [2, 0, 3, 1, 5, 7, 6, 4], 22: [1, 3, 0, 2, 6, 5, 4, 7], 23: [3, 1, 2, 0, 6, 7, 4, 5], 24: [2, 3, 0, 1, 4, 7, 6, 5], 25: [3, 1, 2, 0, 6, 4, 7, 5], 26: [3, 1, 2, 0, 6, 7, 5, 4], 27: [3, 0, 1, 2, 4, 7, 6, 5], 28: [3, 1, 2, 0, 5, 6, 7, 4], 29: [0, 2, 1, 3, 6, 5, 4, 7], 30: [2, 3, 1, 0, 6, 7, 4, 5], 31: [1, 2, 0, 3, 5, 4, 7, 6]},
-    swz=[1, 3, 3, 3, 3, 0, 0, 2, 2, 1, 1, 1, 1, 2, 1, 0, 3, 2, 1, 2, 1, 1, 0, 0, 0, 0, 2, 1, 2, 3, 3, 3])
+    perm=[12, 27, 30, 21, 25, 4, 26, 19, 23, 24, 22, 8, 29, 13, 10, 9, 28, 11, 5, 18, 16, 3, 7, 14, 2, 1, 31, 0, 6, 20, 17, 15],
+    assign={7: (1, 0), 11: (16, 1), 13: (2, 0), 14: (4, 0), 15: (16, 0), 19: (2, 1), 21: (0, 2), 22: (0, 4), 23: (4, 1), 25: (8, 0), 26: (1, 1), 27: (0, 3), 28: (0, 1), 29: (0, 5), 30: (0, 0), 31: (8, 1)},
+    order={0: [1, 2, 0, 3, 5, 7, 4, 6], 1: [2, 0, 1, 3, 6, 4, 7, 5], 2: [2, 0, 1, 3, 7, 5, 6, 4], 3: [0, 3, 2, 1, 7, 6, 5, 4], 4: [2, 1, 0, 3, 4, 6, 7, 5], 5: [0, 3, 2, 1, 4, 7, 5, 6], 6: [0, 2, 3, 1, 4, 5, 7, 6], 7: [0, 1, 2, 3, 6, 5, 7, 4], 8: [2, 0, 1, 3, 7, 4, 6, 5], 9: [3, 0, 1, 2, 7, 4, 6, 5], 10: [0, 3, 1, 2, 6, 4, 7, 5], 11: [1, 2, 3, 0, 7, 6, 5, 4], 12: [3, 0, 1, 2, 6, 4, 7, 5], 13: [3, 1, 2, 0, 6, 5, 7, 4], 14: [1, 3, 2, 0, 6, 4, 5, 7], 15: [3, 1, 0, 2, 7, 6, 4, 5], 16: [2, 1, 0, 3, 5, 6, 4, 7], 17: [2, 3, 0, 1, 4, 6, 5, 7], 18: [2, 0, 3, 1, 5, 6, 4, 7], 19: [1, 2, 3, 0, 5, 4, 7, 6], 20: [2, 3, 0, 1, 4, 6, 7, 5], 21: [3, 1, 2, 0, 6, 7, 5, 4], 22: [1, 2, 3, 0, 7, 6, 4, 5], 23: [3, 0, 1, 2, 7, 6, 5, 4], 24: [2, 0, 3, 1, 7, 4, 6, 5], 25: [0, 3, 1, 2, 4, 5, 7, 6], 26: [0, 3, 1, 2, 7, 5, 6, 4], 27: [2, 0, 3, 1, 7, 6, 4, 5], 28: [0, 2, 3, 1, 7, 5, 4, 6], 29: [2, 3, 0, 1, 4, 6, 7, 5], 30: [2, 1, 3, 0, 4, 5, 6, 7], 31: [2, 1, 3, 0, 7, 6, 5, 4]},
+    swz=[3, 2, 2, 2, 1, 3, 1, 1, 1, 0, 3, 0, 2, 2, 1, 3, 2, 1, 0, 3, 0, 0, 2, 1, 0, 1, 0, 2, 3, 3, 3, 0])
 
 
 # ---- header -------------------------------------------------------------------------
@@ -335,4 +416,5 @@ if __name__ == "__main__":
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "contr5_schedule.h")
     with open(path, "w") as f:
         f.write(header_text())
-    print("bwd conflicts lc/rc:", lds_conflicts(True), lds_conflicts(False), "fwd:", fwd_lds_conflicts())
+    print("bwd conflicts lc/rc:", lds_conflicts(True), lds_conflicts(False), "+", lds_write_conflicts(True),
+          lds_write_conflicts(False), "fwd:", fwd_lds_conflicts(), "+", fwd_lds_write_conflicts())

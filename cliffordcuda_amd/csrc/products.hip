@@ -66,7 +66,7 @@ __device__ __forceinline__ void load_blk(const float4* __restrict__ base, unsign
 // The balanced kernels' staged groups sit in static LDS arrays aligned to 64
 // bytes, so a block's four slots (blk << 2) + (q ^ s) are one slot address
 // xor 16 q: one address per block instead of one per slot. rs is the staged
-// row's extra slot skew (rows that share a quarter-wave read the same blocks
+// row's extra slot skew (rows that share a lane set read the same blocks
 // at the same step, so their slots differ).
 typedef float v4f_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4f_t lds_v4f;
@@ -113,6 +113,30 @@ __device__ __forceinline__ void load_blk_rev(const float4* __restrict__ base, un
         v[15 - (4 * q + 1)] = t.y;
         v[15 - (4 * q + 2)] = t.z;
         v[15 - (4 * q + 3)] = t.w;
+    }
+}
+
+// Blocked kernels (one lane per output block, rows side by side in a wave):
+// the float4 slot q of block blk sits at (blk << 2) | (q ^ bslot(blk, t)), with
+// t the staged row's skew. ds_read_b128 serves a 32-lane half in two 16-lane
+// sets (lane bits 2-4 of even and of odd parity), one cycle per distinct
+// address on the busiest 16-byte bank group, so a set's lanes, which read one
+// block per row (the broadcast operand) and blocks ih ^ kh (the lane's
+// partner), must not put two blocks of one row, or the same block of two rows,
+// on one group: (blk >> 2) & 3 spreads the partner blocks of a set, and the row
+// skews (host: blocked_row_skew) separate the rows of a set.
+__device__ __forceinline__ unsigned bslot(unsigned blk, unsigned t) { return ((blk >> 2) ^ t) & 3u; }
+
+template <bool REV = false>
+__device__ __forceinline__ void load_blk_s(const float4* __restrict__ base, unsigned blk, unsigned s,
+                                           float (&v)[16]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 t = base[(blk << 2) + ((unsigned)q ^ s)];
+        v[REV ? 15 - (4 * q + 0) : 4 * q + 0] = t.x;
+        v[REV ? 15 - (4 * q + 1) : 4 * q + 1] = t.y;
+        v[REV ? 15 - (4 * q + 2) : 4 * q + 2] = t.z;
+        v[REV ? 15 - (4 * q + 3) : 4 * q + 3] = t.w;
     }
 }
 
@@ -365,16 +389,18 @@ struct BlkParams {
     int kpl;        // output blocks per lane
     int split_log;  // small-batch kernels: log2 of the partner splits S per output block
     int wpr_log;    // small-batch kernels: log2 of the workgroups per row
+    unsigned rskew; // blocked kernels: 2-bit slot skew of staged row r at bits 2 (r & 15)
 };
 
 // Stage NOPS (2 or 3) row-major operands s0, s1[, s2] for the workgroup's rows
 // into LDS (swizzled). Each thread issues all its loads (up to four float4 per
 // operand per pass, addresses clamped to the last valid chunk) before any LDS
 // write, so a pass costs one memory latency instead of one per chunk.
-template <int NOPS>
+template <int NOPS, bool BSLOT = false>
 __device__ __forceinline__ void stage_rows(float4* __restrict__ lds, const float4* __restrict__ s0,
                                            const float4* __restrict__ s1, const float4* __restrict__ s2,
-                                           long long row0, int nrows, int n, long long m2 = -1) {
+                                           long long row0, int nrows, int n, long long m2 = -1, unsigned rskew = 0u) {
+    // BSLOT: the blocked kernels' slots (bslot with the row skews in rskew), else swz
     // m2 masks s2's float4 index: -1 (packed like s0 and s1) or 2^(n-2) - 1
     // (one row for all rows: the row offset drops out)
     const int d4_log = n - 2;
@@ -398,7 +424,8 @@ __device__ __forceinline__ void stage_rows(float4* __restrict__ lds, const float
             const int r = idx >> d4_log;
             const unsigned f = (unsigned)(idx & (D4 - 1));
             const unsigned blk = f >> 2, q = f & 3u;
-            const int dst = r * NOPS * D4 + (int)((blk << 2) + (q ^ swz(blk)));
+            const unsigned sx = BSLOT ? bslot(blk, rskew >> (2 * (r & 15))) : swz(blk);
+            const int dst = r * NOPS * D4 + (int)((blk << 2) + (q ^ sx));
             lds[dst] = x;
             lds[dst + D4] = y;
             if constexpr (NOPS == 3) lds[dst + 2 * D4] = z;
@@ -419,10 +446,12 @@ __global__ __launch_bounds__(256) void prod_fwd_blk(const float* __restrict__ A,
     const unsigned NB = 1u << (n - 4);
     const long long row0 = (long long)blockIdx.x * P.rows_per_wg;
     const int nrows = (int)((P.batch - row0) < P.rows_per_wg ? (P.batch - row0) : P.rows_per_wg);
-    stage_rows<2>(lds, reinterpret_cast<const float4*>(A), reinterpret_cast<const float4*>(B), nullptr, row0, nrows, n);
+    stage_rows<2, true>(lds, reinterpret_cast<const float4*>(A), reinterpret_cast<const float4*>(B), nullptr, row0,
+                        nrows, n, -1, P.rskew);
     __syncthreads();
     const int r = threadIdx.x >> P.lpr_log;
     if (r >= nrows) return;
+    const unsigned t = (P.rskew >> (2 * (r & 15))) & 3u;
     const unsigned lane_blk = threadIdx.x & ((1u << P.lpr_log) - 1u);
     const float4* la = lds + r * 2 * D4;
     const float4* lb = la + D4;
@@ -439,8 +468,8 @@ __global__ __launch_bounds__(256) void prod_fwd_blk(const float* __restrict__ A,
             const HiSign hs = hi_sign<OP>(ih, jh, P.negh, P.nulh, fullh, P.nm1, P.mu);
             if (!hs.valid) continue;
             float av[16], bv[16];
-            load_blk(la, ih, av);
-            load_blk(lb, jh, bv);
+            load_blk_s(la, ih, bslot(ih, t), av);
+            load_blk_s(lb, jh, bslot(jh, t), bv);
             apply_flips(bv, hs.mask, hs.mask ^ (cross_pi<OP>(ih, P.nm1) << 31));
             fwd_block_dispatch<OP, LOWNEG>(acc, av, bv, ih, jh);
         }
@@ -468,7 +497,7 @@ template <int CLASS, bool LOWNEG>
 __device__ __forceinline__ void inner_pair(const float4* __restrict__ la, const float4* __restrict__ lb,
                                            const float4* __restrict__ lg, unsigned h, unsigned m, unsigned fullh,
                                            bool do_a, bool do_b, float (&ga)[16], float (&gb)[16],
-                                           const BlkParams& P) {
+                                           const BlkParams& P, unsigned t) {
     // CLASS 0: m strict superset of h; 1: strict subset; 2: m = h
     constexpr int VA = CLASS == 0 ? LV_LC : CLASS == 1 ? LV_RC : LV_INNER;
     constexpr int VB = CLASS == 0 ? LV_RC : CLASS == 1 ? LV_LC : LV_INNER;
@@ -478,17 +507,17 @@ __device__ __forceinline__ void inner_pair(const float4* __restrict__ la, const 
     do_b = do_b && sb.valid;
     if (!do_a && !do_b) return;
     float g[16];
-    load_blk(lg, h ^ m, g);
+    load_blk_s(lg, h ^ m, bslot(h ^ m, t), g);
     if (do_a) {
         float bv[16];
-        load_blk(lb, m, bv);
+        load_blk_s(lb, m, bslot(m, t), bv);
         apply_flips(bv, sa.mask, sa.mask ^ (cross_pi<OP_INNER>(h, P.nm1) << 31));
         lowblock_ga<VA, LOWNEG>(ga, bv, g);
     }
     if (do_b) {
         const unsigned pm = cross_pi<OP_INNER>(m, P.nm1) << 31;
         float av[16], gt[16];
-        load_blk(la, m, av);
+        load_blk_s(la, m, bslot(m, t), av);
         apply_flips(av, sb.mask, sb.mask ^ pm);
 #pragma unroll
         for (int e = 0; e < 16; ++e) gt[e] = (cpopc((unsigned)e) & 1) ? flip(g[e], pm) : g[e];
@@ -500,23 +529,23 @@ template <bool LOWNEG>
 __device__ __forceinline__ void inner_bwd_blocks(const float4* __restrict__ la, const float4* __restrict__ lb,
                                                  const float4* __restrict__ lg, unsigned h, unsigned fullh,
                                                  bool want_a, bool want_b, float (&ga)[16], float (&gb)[16],
-                                                 const BlkParams& P) {
+                                                 const BlkParams& P, unsigned t) {
     const unsigned co = fullh & ~h;
     // strict supersets m = h | S, S a nonempty subset of co, in increasing order
     const int nsup = (1 << __popc(co)) - 1;
     unsigned S = 0u;
     for (int k = 0; __any(k < nsup); ++k) {
         S = (S - co) & co;
-        inner_pair<0, LOWNEG>(la, lb, lg, h, h | S, fullh, want_a && k < nsup, want_b && k < nsup, ga, gb, P);
+        inner_pair<0, LOWNEG>(la, lb, lg, h, h | S, fullh, want_a && k < nsup, want_b && k < nsup, ga, gb, P, t);
     }
     // strict subsets m of h (the empty set first)
     const int nsub = (1 << __popc(h)) - 1;
     unsigned T = 0u;
     for (int k = 0; __any(k < nsub); ++k) {
-        inner_pair<1, LOWNEG>(la, lb, lg, h, T, fullh, want_a && k < nsub, want_b && k < nsub, ga, gb, P);
+        inner_pair<1, LOWNEG>(la, lb, lg, h, T, fullh, want_a && k < nsub, want_b && k < nsub, ga, gb, P, t);
         T = (T - h) & h;
     }
-    inner_pair<2, LOWNEG>(la, lb, lg, h, h, fullh, want_a, want_b, ga, gb, P);
+    inner_pair<2, LOWNEG>(la, lb, lg, h, h, fullh, want_a, want_b, ga, gb, P, t);
 }
 
 template <int OP, bool LOWNEG>
@@ -529,11 +558,13 @@ __global__ __launch_bounds__(256) void prod_bwd_blk(const float* __restrict__ A,
     const unsigned NB = 1u << (n - 4);
     const long long row0 = (long long)blockIdx.x * P.rows_per_wg;
     const int nrows = (int)((P.batch - row0) < P.rows_per_wg ? (P.batch - row0) : P.rows_per_wg);
-    stage_rows<3>(lds, reinterpret_cast<const float4*>(A), reinterpret_cast<const float4*>(B),
-                  reinterpret_cast<const float4*>(GC), row0, nrows, n, P.ldg4 ? -1LL : (1LL << (n - 2)) - 1);
+    stage_rows<3, true>(lds, reinterpret_cast<const float4*>(A), reinterpret_cast<const float4*>(B),
+                        reinterpret_cast<const float4*>(GC), row0, nrows, n, P.ldg4 ? -1LL : (1LL << (n - 2)) - 1,
+                        P.rskew);
     __syncthreads();
     const int r = threadIdx.x >> P.lpr_log;
     if (r >= nrows) return;
+    const unsigned t = (P.rskew >> (2 * (r & 15))) & 3u;
     const unsigned lane_blk = threadIdx.x & ((1u << P.lpr_log) - 1u);
     const float4* la = lds + r * 3 * D4;
     const float4* lb = la + D4;
@@ -551,7 +582,7 @@ __global__ __launch_bounds__(256) void prod_bwd_blk(const float* __restrict__ A,
             gb[e] = 0.f;
         }
         if constexpr (OP == OP_INNER) {
-            inner_bwd_blocks<LOWNEG>(la, lb, lg, h, fullh, want_a, want_b, ga, gb, P);
+            inner_bwd_blocks<LOWNEG>(la, lb, lg, h, fullh, want_a, want_b, ga, gb, P, t);
         } else
         for (unsigned m = 0; m < NB; ++m) {
             const unsigned x = h ^ m;
@@ -560,18 +591,18 @@ __global__ __launch_bounds__(256) void prod_bwd_blk(const float* __restrict__ A,
             const bool do_a = want_a && sa.valid, do_b = want_b && sb.valid;
             if (!do_a && !do_b) continue;
             float g[16];
-            if (OP == OP_REGR) load_blk_rev(lg, fullh ^ x, g);
-            else load_blk(lg, x, g);
+            if (OP == OP_REGR) load_blk_s<true>(lg, fullh ^ x, bslot(fullh ^ x, t), g);
+            else load_blk_s(lg, x, bslot(x, t), g);
             if (do_a) {
                 float bv[16];
-                load_blk(lb, m, bv);
+                load_blk_s(lb, m, bslot(m, t), bv);
                 apply_flips(bv, sa.mask, sa.mask ^ (pi_h << 31));
                 ga_block_dispatch<OP, LOWNEG>(ga, bv, g, h, m);
             }
             if (do_b) {
                 const unsigned pm = cross_pi<OP>(m, P.nm1) << 31;
                 float av[16], gt[16];
-                load_blk(la, m, av);
+                load_blk_s(la, m, bslot(m, t), av);
                 apply_flips(av, sb.mask, sb.mask ^ pm);
 #pragma unroll
                 for (int e = 0; e < 16; ++e) gt[e] = (cpopc((unsigned)e) & 1) ? flip(g[e], pm) : g[e];
@@ -2335,14 +2366,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
 // through LDS after the last step. Every lane starts a fresh accumulator at the
 // same steps, so no step zeroes conditionally. The pair order inside pieces,
 // the slot of each role and the blocks' LDS slot swizzle were searched on the
-// CPU to keep each quarter-wave's 16 block reads on distinct bank groups.
+// CPU against the measured LDS rules (ds_read_b128: per 32-lane half, two sets
+// of 16 lanes by the parity of lane bits 2-4, one cycle per distinct address on
+// the busiest 16-byte bank group mod 256 bytes; ds_write_b128: 8 consecutive
+// lanes per cycle, groups mod 128 bytes), so the block reads and the result
+// traffic of a wave run at one cycle per lane set.
 // Finished blocks are staged in LDS and leave in row order.
 
 template <unsigned long long SWZ>
 __device__ __forceinline__ unsigned swz5(unsigned blk) { return (unsigned)(SWZ >> (2u * blk)) & 3u; }
 
 template <int OP, bool LOWNEG, bool NULLTOP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void prod_bwd_contr5(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NULLTOP ? 2 : 3))) void prod_bwd_contr5(
     const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ GC, float* __restrict__ GA,
     float* __restrict__ GB, BlkParams P) {
     static_assert(OP == OP_LC || OP == OP_RC, "contractions only");
@@ -2359,20 +2394,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const unsigned slot = (unsigned)lane & 31u, prob = (unsigned)lane >> 5;
     const long long ngrp = (P.batch + R - 1) / R;
-    const long long grp = (long long)blockIdx.x * 4 + wave;
-    const BalLane L = bal_lane(N, lane);
-    BalPre pa;
-    {
-        const BalSrc sa = bal_src(A, grp, P.batch, N, R);
+    // PF (the null-top split): the grid is resident and a wave walks groups grp, grp + 4 * grid, ...,
+    // loading the next group's operands into registers while the steps of the current one run, so
+    // the waves of a compute unit do not all wait on memory at the same time
+    constexpr bool PF = NULLTOP;
+    const long long gstride = PF ? (long long)gridDim.x * 4 : 0;
+    long long grp = (long long)blockIdx.x * 4 + wave;
+    BalPre pa, pb, pg;
+    auto fetch = [&](long long g) {
+        unsigned lo = (unsigned)lane;  // opaque: the loop keeps no lane-derived pointers
+        asm volatile("" : "+v"(lo));
+        const BalLane L = bal_lane(N, (int)lo);
+        const BalSrc sa = bal_src(A, g, P.batch, N, R);
         if constexpr (NULLTOP) {  // a0 only: chunks 0, 1 of the row
             pa.v[0] = sa.g0[L.ff[0]];
             pa.v[1] = sa.g0[L.ff[1]];
         } else {
             pa = bal_fetch(sa, L, N - 2);
         }
-    }
-    const BalPre pb = bal_fetch(bal_src(B, grp, P.batch, N, R), L, N - 2);
-    const BalPre pg = bal_fetch(bal_src(GC, grp, P.batch, N, R, P.ldg4 == 0), L, N - 2);
+        pb = bal_fetch(bal_src(B, g, P.batch, N, R), L, N - 2);
+        pg = bal_fetch(bal_src(GC, g, P.batch, N, R, P.ldg4 == 0), L, N - 2);
+    };
+    fetch(grp < ngrp ? grp : ngrp - 1);
     // step entries: partner byte offset (bits 0-13), gc byte offset (14-27), the pair's high
     // sign (28) and the cross parity of the odd partner elements (29): |o| for ga, |p| for gb
     if (wave == 0) {
@@ -2398,6 +2441,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     if (grp >= ngrp) return;
     float4* sw = lds[wave];
     const unsigned base = lds_addr4(sw);
+    if (lane < 4) lds_st4(base + 16u * (768u + (unsigned)lane), make_float4(0.f, 0.f, 0.f, 0.f));
+    for (;;) {
+    // lane and base as opaque copies: every address of the body is formed inside the loop
+    // instead of being kept in registers across it
+    unsigned lane_o = (unsigned)lane, base_o = base;
+    asm volatile("" : "+v"(lane_o), "+v"(base_o) :: "memory");
+    {
+    const int lane = (int)lane_o;
+    const unsigned base = base_o, slot = lane_o & 31u, prob = lane_o >> 5;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {  // slot q of block blk at (blk << 2) | (q ^ swz(blk))
         const unsigned c = (unsigned)lane + 64u * (unsigned)i;
@@ -2407,14 +2459,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
         lds_st4(base + 4096u + so, pb.v[i]);
         lds_st4(base + 8192u + so, pg.v[i]);
     }
-    if (lane < 4) lds_st4(base + 16u * (768u + (unsigned)lane), make_float4(0.f, 0.f, 0.f, 0.f));
     wave_lds_sync();
+    const long long nxt = grp + gstride;
+    if (PF && nxt < ngrp) fetch(nxt);
     float acc[16], y1[16], y2[16], y3[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.f;
     auto step = [&](auto tc) {
         constexpr int t = decltype(tc)::value;
         __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");  // the step's block reads stay in the step
         unsigned e = tab[t][lane];
         asm volatile("" : "+v"(e));
         const unsigned w0 = base + (e & 16383u);
@@ -2443,6 +2497,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
                 if (cpopc((unsigned)el) & 1) g[el] = flip(g[el], mq);
             lowblock_gb<V, LOWNEG>(acc, w, g);
         }
+#pragma unroll
+        for (int el = 0; el < 16; ++el) asm volatile("" : "+v"(acc[el]));  // the step's FMAs end here
         if constexpr ((t & 3) == 3 && t < 15) {  // a piece ends: keep it, start from zero
 #pragma unroll
             for (int el = 0; el < 16; ++el) {
@@ -2539,6 +2595,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
             }
         }
     }
+    if (!PF || nxt >= ngrp) break;
+    grp = nxt;
+    wave_lds_sync();  // the result reads are done before the next group's staging
+    }
+    }
 }
 
 // Forward: lane slot s walks 8 pairs of kContr5Fwd in two pieces, (a[S], b[S | o])
@@ -2561,19 +2622,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const unsigned slot = (unsigned)lane & 31u, prob = (unsigned)lane >> 5;
     const long long ngrp = (P.batch + R - 1) / R;
-    const long long grp = (long long)blockIdx.x * 4 + wave;
-    const BalLane L = bal_lane(N, lane);
-    BalPre pa;
-    {
-        const BalSrc sa = bal_src(A, grp, P.batch, N, R);
+    // resident grid: a wave walks groups grp, grp + 4 * grid, ..., loading the next group's
+    // operands into registers while the steps of the current one run
+    const long long gstride = (long long)gridDim.x * 4;
+    long long grp = (long long)blockIdx.x * 4 + wave;
+    BalPre pa, pb;
+    auto fetch = [&](long long g) {
+        unsigned lo = (unsigned)lane;  // opaque: the loop keeps no lane-derived addresses
+        asm volatile("" : "+v"(lo));
+        const BalLane L = bal_lane(N, (int)lo);
+        const BalSrc sa = bal_src(A, g, P.batch, N, R);
         if constexpr (NULLTOP) {
             pa.v[0] = sa.g0[L.ff[0]];
             pa.v[1] = sa.g0[L.ff[1]];
         } else {
             pa = bal_fetch(sa, L, N - 2);
         }
-    }
-    const BalPre pb = bal_fetch(bal_src(B, grp, P.batch, N, R), L, N - 2);
+        pb = bal_fetch(bal_src(B, g, P.batch, N, R), L, N - 2);
+    };
+    fetch(grp < ngrp ? grp : ngrp - 1);
     // entries: a byte offset (bits 0-13), b byte offset (14-27), high sign (28), cross parity |ih| (29)
     if (wave == 0) {
         for (int t = 0; t < 8; ++t) {
@@ -2597,6 +2664,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
     if (grp >= ngrp) return;
     float4* sw = lds[wave];
     const unsigned base = lds_addr4(sw);
+    if (lane < 4) lds_st4(base + 16u * (512u + (unsigned)lane), make_float4(0.f, 0.f, 0.f, 0.f));
+    for (;;) {
+    // lane and base as opaque copies: every address of the body is formed inside the loop
+    // instead of being kept in registers across it
+    unsigned lane_o = (unsigned)lane, base_o = base;
+    asm volatile("" : "+v"(lane_o), "+v"(base_o) :: "memory");
+    {
+    const int lane = (int)lane_o;
+    const unsigned base = base_o, slot = lane_o & 31u, prob = lane_o >> 5;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const unsigned c = (unsigned)lane + 64u * (unsigned)i;
@@ -2605,14 +2681,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
         if (!NULLTOP || i < 2) lds_st4(base + so, pa.v[i]);
         lds_st4(base + 4096u + so, pb.v[i]);
     }
-    if (lane < 4) lds_st4(base + 16u * (512u + (unsigned)lane), make_float4(0.f, 0.f, 0.f, 0.f));
     wave_lds_sync();
+    const long long nxt = grp + gstride;
+    if (nxt < ngrp) fetch(nxt);
     float acc[16], y1[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.f;
     auto step = [&](auto tc) {
         constexpr int t = decltype(tc)::value;
         __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");  // the step's block reads stay in the step
         unsigned e = tab[t][lane];
         asm volatile("" : "+v"(e));
         const unsigned a0 = base + (e & 16383u);
@@ -2634,6 +2712,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
         }
         apply_flips(bv, ms, ms ^ mq);
         lowblock_fwd<V, LOWNEG>(acc, av, bv);
+#pragma unroll
+        for (int el = 0; el < 16; ++el) asm volatile("" : "+v"(acc[el]));  // the step's FMAs end here
         if constexpr (t == 3) {
 #pragma unroll
             for (int el = 0; el < 16; ++el) {
@@ -2647,10 +2727,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
     const unsigned d = kContr5FwdOut[slot];
     const unsigned chunks = base + 16u * (256u + prob * 128u);  // 16 chunk slots of 4 float4, over the b rows
     const int cw = (int)(d >> 13) - 1;
+    // float4 q of chunk slot c at 4 c + (q ^ ((c >> 1) & 3)): the helpers of a write set and the
+    // owners of a read set whose chunks share bank groups differ in the swizzle
     if (cw >= 0) {
+        const unsigned cx = ((unsigned)cw >> 1) & 3u;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            lds_st4(chunks + 64u * (unsigned)cw + 16u * (unsigned)q,
+            lds_st4(chunks + 64u * (unsigned)cw + 16u * ((unsigned)q ^ cx),
                     make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]));
     }
     wave_lds_sync();
@@ -2661,9 +2744,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
     {
         const unsigned c0 = (d >> 6) & 15u, cnt = (d >> 10) & 7u;
         for (unsigned k = 0; k < cnt; ++k) {
+            const unsigned cx = ((c0 + k) >> 1) & 3u;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const float4 v = lds_ld4(chunks + 64u * (c0 + k) + 16u * (unsigned)q);
+                const float4 v = lds_ld4(chunks + 64u * (c0 + k) + 16u * ((unsigned)q ^ cx));
                 u[4 * q] += v.x;
                 u[4 * q + 1] += v.y;
                 u[4 * q + 2] += v.z;
@@ -2691,6 +2775,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
             const long long row = grp * 2 + (long long)hr;
             if (row < P.batch) reinterpret_cast<float4*>(C)[(row << 7) + (long long)f] = lds_ld4(base + so);
         }
+    }
+    if (nxt >= ngrp) break;
+    grp = nxt;
+    wave_lds_sync();  // the result reads are done before the next group's staging
+    }
     }
 }
 
@@ -3147,6 +3236,18 @@ constexpr size_t kBlockedLdsMax = 48 * 1024;
 
 // Launch shape for the whole-row blocked kernels. Returns false if the rows do
 // not fit the LDS budget (tiled path) or the metric needs the generic path.
+// Row skews of the blocked kernels' slots (bslot), 2 bits per staged row r at
+// bits 2 (r & 15): the rows that share a lane set of a ds_read_b128 (4 at n = 7,
+// 2 at n = 8, 4 of the 8 at n <= 6) get distinct skews, chosen on the CPU so
+// that neither the broadcast nor the partner reads put two addresses of one
+// set on a bank group; at n >= 9 a half-wave holds one row.
+static unsigned blocked_row_skew(int n) {
+    if (n <= 6) return 0xE4E4E4E4u;  // 0, 1, 2, 3
+    if (n == 7) return 0x78787878u;  // 0, 2, 3, 1
+    if (n == 8) return 0xCCCCCCCCu;  // 0, 3
+    return 0u;
+}
+
 static bool blocked_plan(int op, int n, uint32_t neg, uint32_t nul, int nops, BlkParams& P, bool& lowneg,
                          dim3& grid, dim3& block, size_t& lds_bytes) {
     if (!blocked_metric(op, n, neg, nul, lowneg)) return false;
@@ -3164,6 +3265,7 @@ static bool blocked_plan(int op, int n, uint32_t neg, uint32_t nul, int nops, Bl
     P.lpr_log = lpr_log;
     P.rows_per_wg = nwaves * rpw;
     P.kpl = NB / lpr;
+    P.rskew = blocked_row_skew(n);
     grid = dim3((unsigned)((P.batch + P.rows_per_wg - 1) / P.rows_per_wg));
     block = dim3(64 * nwaves);
     lds_bytes = (size_t)P.rows_per_wg * row_bytes;
@@ -3340,7 +3442,8 @@ static void launch_contr5_t(hipStream_t s, const float* A, const float* B, const
         BlkParams Q = P;
         Q.batch = P.batch - r0 < chunk ? P.batch - r0 : chunk;
         const long long groups = (Q.batch + R - 1) / R;
-        const dim3 g((unsigned)((groups + 3) / 4));
+        const dim3 g(NT ? resident_grid((const void*)prod_bwd_contr5<OP, LN, NT>, 256, 0, (groups + 3) / 4)
+                        : (unsigned)((groups + 3) / 4));
         const long long off = r0 * D;
         hipLaunchKernelGGL((prod_bwd_contr5<OP, LN, NT>), g, dim3(256), 0, s, A + off, B + off,
                            GCp + (P.ldg4 ? off : 0), GA ? GA + off : nullptr, GB ? GB + off : nullptr, Q);
@@ -3356,7 +3459,7 @@ static void launch_fcontr5_t(hipStream_t s, const float* A, const float* B, floa
         BlkParams Q = P;
         Q.batch = P.batch - r0 < chunk ? P.batch - r0 : chunk;
         const long long groups = (Q.batch + R - 1) / R;
-        const dim3 g((unsigned)((groups + 3) / 4));
+        const dim3 g(resident_grid((const void*)prod_fwd_contr5<OP, LN, NT>, 256, 0, (groups + 3) / 4));
         const long long off = r0 * D;
         hipLaunchKernelGGL((prod_fwd_contr5<OP, LN, NT>), g, dim3(256), 0, s, A + off, B + off, C + off, Q);
     }
