@@ -2377,7 +2377,7 @@ template <unsigned long long SWZ>
 __device__ __forceinline__ unsigned swz5(unsigned blk) { return (unsigned)(SWZ >> (2u * blk)) & 3u; }
 
 template <int OP, bool LOWNEG, bool NULLTOP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NULLTOP ? 2 : 3))) void prod_bwd_contr5(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void prod_bwd_contr5(
     const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ GC, float* __restrict__ GA,
     float* __restrict__ GB, BlkParams P) {
     static_assert(OP == OP_LC || OP == OP_RC, "contractions only");
@@ -2394,10 +2394,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NULLTOP ? 2
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const unsigned slot = (unsigned)lane & 31u, prob = (unsigned)lane >> 5;
     const long long ngrp = (P.batch + R - 1) / R;
-    // PF (the null-top split): the grid is resident and a wave walks groups grp, grp + 4 * grid, ...,
-    // loading the next group's operands into registers while the steps of the current one run, so
-    // the waves of a compute unit do not all wait on memory at the same time
-    constexpr bool PF = NULLTOP;
+    // the grid is resident and a wave walks groups grp, grp + 4 * grid, ..., loading the next
+    // group's operands into registers while the steps of the current one run, so the waves of a
+    // compute unit do not all wait on memory at the same time
+    constexpr bool PF = true;
     const long long gstride = PF ? (long long)gridDim.x * 4 : 0;
     long long grp = (long long)blockIdx.x * 4 + wave;
     BalPre pa, pb, pg;
@@ -2596,6 +2596,294 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NULLTOP ? 2
         }
     }
     if (!PF || nxt >= ngrp) break;
+    grp = nxt;
+    wave_lds_sync();  // the result reads are done before the next group's staging
+    }
+    }
+}
+
+// ---- inner product backward on the contraction schedules ------------------
+// The inner product's block pairs are the left contraction's (ih inside jh)
+// and the right contraction's (jh inside ih); the (o, o) pairs belong to both,
+// and so does their element diagonal (il = jl), which the two low patterns
+// would count twice. prod_bwd_inner5 runs the lc and the rc lane schedules of
+// prod_bwd_contr5 one after the other on the same staged rows: four sub-phases
+// of 8 steps (lc ga, rc ga, lc gb, rc gb), each with its compile-time low
+// pattern, each flushed into result rows in LDS by its owners (helpers'
+// partials first), then the element diagonal taken off once:
+//   ga[i] -= F(i) b[i] gc[0],  gb[i] -= F(i) a[i] gc[0],
+//   F((o, il)) = s_hi(o, o) (-1)^{|il| |o|} s_lo(il, il).
+// n = 9: two rows per wave, one problem each. n = 10 whose only null
+// generator is the top one: with a = a0 + a1 e9, b = b0 + b1 e9 the pairs with
+// e9 in both vanish and moving e9 past a blade of b gives (-1)^{|j|} (beta,
+// the grade involution), so c0 = inner9(a0, b0), c1 = lc9(a0, b1) +
+// rc9(a1, beta b0):
+//   ga0 = inner9_ga(b0, gc0) + lc9_ga(b1, gc1),  ga1 = rc9_ga(beta b0, gc1),
+//   gb0 = inner9_gb(a0, gc0) + beta rc9_gb(a1, gc1),  gb1 = lc9_gb(a0, gc1);
+// problem 0 (lanes 0-31) is the inner9 problem, problem 1 runs the lc
+// sub-phases on (a0, b1, gc1) and the rc ones on (a1, beta b0, gc1), beta
+// folded into the step signs (rc ga) and into the flush (rc gb).
+template <bool LOWNEG, bool NULLTOP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void prod_bwd_inner5(
+    const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ GC, float* __restrict__ GA,
+    float* __restrict__ GB, BlkParams P) {
+    constexpr int N = NULLTOP ? 10 : 9;
+    constexpr int R = NULLTOP ? 1 : 2;
+    constexpr unsigned long long SW = kContr5SwzLc;
+    constexpr unsigned full = 31u;
+    // per wave (float4): a at 0 (rows 0, 1 or halves a0, a1), b at 256, gc at 512, the zero block at
+    // 768, partial slots at 772 (8 slots of 4 float4 per problem), ga rows at 836; the gb rows go
+    // over b once the ga sub-phases are done
+    constexpr unsigned kZero = 768u, kPart = 772u, kGa = 836u, kGb = 256u;
+    __shared__ __attribute__((aligned(64))) float4 lds[4][1092];
+    __shared__ unsigned tab[32][64];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const long long ngrp = (P.batch + R - 1) / R;
+    // resident grid: a wave walks groups grp, grp + 4 * grid, ..., loading the next group's
+    // operands into registers while the current group's steps run
+    const long long gstride = (long long)gridDim.x * 4;
+    long long grp = (long long)blockIdx.x * 4 + wave;
+    BalPre pa, pb, pg;
+    auto fetch = [&](long long g) {
+        unsigned lo = (unsigned)lane;  // opaque: the loop keeps no lane-derived pointers
+        asm volatile("" : "+v"(lo));
+        const BalLane L = bal_lane(N, (int)lo);
+        pa = bal_fetch(bal_src(A, g, P.batch, N, R), L, N - 2);
+        pb = bal_fetch(bal_src(B, g, P.batch, N, R), L, N - 2);
+        pg = bal_fetch(bal_src(GC, g, P.batch, N, R, P.ldg4 == 0), L, N - 2);
+    };
+    fetch(grp < ngrp ? grp : ngrp - 1);
+    // step entries of sub-phase u (0 lc ga, 1 rc ga, 2 lc gb, 3 rc gb) at tab[8 u + t]: partner
+    // byte offset (bits 0-13), gc byte offset (14-27), high sign (28), cross parity (29)
+    if (wave == 0) {
+        const unsigned slot = (unsigned)lane & 31u, prob = (unsigned)lane >> 5;
+        for (int u = 0; u < 4; ++u) {
+            const bool lcr = (u & 1) == 0, ga = u < 2;
+            for (int t = 0; t < 8; ++t) {
+                const int tt = t + (ga ? 0 : 8);
+                const unsigned st = lcr ? kContr5StepsLc[slot][tt] : kContr5StepsRc[slot][tt];
+                unsigned e;
+                if (st & 2048u) {
+                    e = (kZero << 4) | (kZero << 18);
+                } else {
+                    const unsigned o = st & 31u, p = (st >> 5) & 31u, x = o ^ p;
+                    const HiSign hs = ga ? (lcr ? hi_sign<OP_LC>(o, p, P.negh, 0u, full, 0, 0)
+                                                : hi_sign<OP_RC>(o, p, P.negh, 0u, full, 0, 0))
+                                         : (lcr ? hi_sign<OP_LC>(p, o, P.negh, 0u, full, 0, 0)
+                                                : hi_sign<OP_RC>(p, o, P.negh, 0u, full, 0, 0));
+                    unsigned hsb = hs.mask >> 31, par = (unsigned)__popc(ga ? o : p) & 1u;
+                    // null-top: rc ga of problem 1 reads b0 (beta b0), lc gb of both problems reads a0
+                    const bool row0 = NULLTOP && ((u == 1) || (u == 2));
+                    const unsigned prow = row0 ? 0u : prob;
+                    if (NULLTOP && u == 1 && prob == 1u) {  // beta b0: (-1)^{|p| + |jl|}
+                        hsb ^= (unsigned)__popc(p) & 1u;
+                        par ^= 1u;
+                    }
+                    const unsigned pw = (ga ? 256u : 0u) + prow * 128u + ((p << 2) | swz5<SW>(p));
+                    const unsigned pg4 = 512u + prob * 128u + ((x << 2) | swz5<SW>(x));
+                    e = (pw << 4) | (pg4 << 18) | (hsb << 28) | (par << 29);
+                }
+                tab[8 * u + t][lane] = e;
+            }
+        }
+    }
+    __syncthreads();
+    if (grp >= ngrp) return;
+    float4* sw = lds[wave];
+    const unsigned base = lds_addr4(sw);
+    if (lane < 4) lds_st4(base + 16u * (kZero + (unsigned)lane), make_float4(0.f, 0.f, 0.f, 0.f));
+    for (;;) {
+    // lane and base as opaque copies: every address of the body is formed inside the loop
+    unsigned lane_o = (unsigned)lane, base_o = base;
+    asm volatile("" : "+v"(lane_o), "+v"(base_o) :: "memory");
+    {
+    const int lane = (int)lane_o;
+    const unsigned base = base_o, slot = lane_o & 31u, prob = lane_o >> 5;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // slot q of block blk at (blk << 2) | (q ^ swz(blk))
+        const unsigned c = (unsigned)lane + 64u * (unsigned)i;
+        const unsigned hr = c >> 7, f = c & 127u, blk = f >> 2;
+        const unsigned so = 16u * (hr * 128u + ((blk << 2) | ((f & 3u) ^ swz5<SW>(blk))));
+        lds_st4(base + so, pa.v[i]);
+        lds_st4(base + 4096u + so, pb.v[i]);
+        lds_st4(base + 8192u + so, pg.v[i]);
+    }
+    wave_lds_sync();
+    const long long nxt = grp + gstride;
+    if (nxt < ngrp) fetch(nxt);
+    auto st16 = [&](unsigned a, const float (&x)[16]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) lds_st4(a + 16u * (unsigned)q, make_float4(x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]));
+    };
+    auto add16 = [&](unsigned a, float (&x)[16]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 v = lds_ld4(a + 16u * (unsigned)q);
+            x[4 * q] += v.x;
+            x[4 * q + 1] += v.y;
+            x[4 * q + 2] += v.z;
+            x[4 * q + 3] += v.w;
+        }
+    };
+    // block blk of the result row at rowb (slots swizzled as the staged rows) = x (put) or += x
+    auto addblk = [&](unsigned rowb, unsigned blk, const float (&x)[16], bool put) {
+        const unsigned s0 = swz5<SW>(blk);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const unsigned at = rowb + 16u * ((blk << 2) | ((unsigned)q ^ s0));
+            if (put) {
+                lds_st4(at, make_float4(x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]));
+            } else {
+                const float4 v = lds_ld4(at);
+                lds_st4(at, make_float4(v.x + x[4 * q], v.y + x[4 * q + 1], v.z + x[4 * q + 2], v.w + x[4 * q + 3]));
+            }
+        }
+    };
+    auto subphase = [&](auto uc) {
+        constexpr int U = decltype(uc)::value;
+        constexpr bool kL = (U & 1) == 0, kGA = U < 2;
+        constexpr int V = kL ? LV_LC : LV_RC;
+        float acc[16], y1[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+        auto step = [&](auto tc) {
+            constexpr int t = decltype(tc)::value;
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("" ::: "memory");  // the step's block reads stay in the step
+            unsigned e = tab[8 * U + t][lane];
+            asm volatile("" : "+v"(e));
+            const unsigned w0 = base + (e & 16383u);
+            const unsigned g0 = base + ((e >> 14) & 16383u);
+            const unsigned ms = (e << 3) & 0x80000000u, mq = (e << 2) & 0x80000000u;
+            float g[16], w[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 vg = lds_ld4(g0 ^ ((unsigned)q << 4));
+                const float4 vw = lds_ld4(w0 ^ ((unsigned)q << 4));
+                g[4 * q] = vg.x;
+                g[4 * q + 1] = vg.y;
+                g[4 * q + 2] = vg.z;
+                g[4 * q + 3] = vg.w;
+                w[4 * q] = vw.x;
+                w[4 * q + 1] = vw.y;
+                w[4 * q + 2] = vw.z;
+                w[4 * q + 3] = vw.w;
+            }
+            apply_flips(w, ms, ms ^ mq);
+            if constexpr (kGA) {
+                lowblock_ga<V, LOWNEG>(acc, w, g);
+            } else {
+#pragma unroll
+                for (int el = 0; el < 16; ++el)
+                    if (cpopc((unsigned)el) & 1) g[el] = flip(g[el], mq);
+                lowblock_gb<V, LOWNEG>(acc, w, g);
+            }
+#pragma unroll
+            for (int el = 0; el < 16; ++el) asm volatile("" : "+v"(acc[el]));  // the step's FMAs end here
+            if constexpr (t == 3) {  // the first piece ends
+#pragma unroll
+                for (int el = 0; el < 16; ++el) {
+                    y1[el] = acc[el];
+                    acc[el] = 0.f;
+                }
+            }
+        };
+        frame_steps(step, std::make_integer_sequence<int, 8>{});
+        wave_lds_sync();  // every block read of the sub-phase is done
+        const unsigned d = kL ? kContr5OutLc[slot][U >> 1] : kContr5OutRc[slot][U >> 1];
+        const unsigned typ = d & 3u;
+        const unsigned part = base + 16u * (kPart + prob * 32u);
+        float sv[16];
+#pragma unroll
+        for (int el = 0; el < 16; ++el) sv[el] = y1[el] + acc[el];
+        if (typ == 2u) st16(part + 64u * ((d >> 12) & 7u), sv);  // helpers' partials
+        wave_lds_sync();
+        if (typ == 3u) {  // owners add them, in slot order
+            const unsigned p0 = (d >> 12) & 7u, cnt = (d >> 16) & 3u;
+            for (unsigned k = 0; k < cnt; ++k) add16(part + 64u * (p0 + k), sv);
+        }
+        // the row this problem's results of the sub-phase go to (NULLTOP: lc ga of both problems
+        // into ga0, rc gb of both into gb0)
+        constexpr bool kShared = NULLTOP && (U == 0 || U == 3);
+        const unsigned rowb = base + 16u * ((kGA ? kGa : kGb) + (kShared ? 0u : prob * 128u));
+        const unsigned b1 = (d >> 2) & 31u, b2 = (d >> 7) & 31u;
+        if constexpr (NULLTOP && U == 3) {  // problem 1: beta rc9_gb(a1, gc1), (-1)^{|o| + |el|}
+            const unsigned on = prob == 1u ? 0x80000000u : 0u;
+            const unsigned m1 = (((unsigned)__popc(b1) & 1u) << 31) & on, m2 = (((unsigned)__popc(b2) & 1u) << 31) & on;
+            apply_flips(y1, m1, m1 ^ on);
+            apply_flips(acc, m2, m2 ^ on);
+            apply_flips(sv, m1, m1 ^ on);
+        }
+        // the first contribution to a row block is stored, the later ones added: lc ga puts ga
+        // (NULLTOP: problem 0 into ga0, problem 1 adds), rc ga adds (NULLTOP problem 1 puts ga1),
+        // lc gb puts, rc gb adds
+        const bool put = U == 2 || (U == 0 && (!NULLTOP || prob == 0u)) || (U == 1 && NULLTOP && prob == 1u);
+#pragma unroll
+        for (unsigned r = 0; r < (kShared ? 2u : 1u); ++r) {  // kShared: problem 0, then problem 1
+            if (!kShared || prob == r) {
+                if (typ == 1u) {
+                    addblk(rowb, b1, y1, put);
+                    addblk(rowb, b2, acc, put);
+                } else if (typ != 2u) {
+                    addblk(rowb, b1, sv, put);
+                }
+            }
+            if (kShared && r == 0u) wave_lds_sync();
+        }
+        if constexpr (U == 1 || U == 3) {
+            // the element diagonal, once: lane slot o takes block o of its problem's row (the
+            // inner9 problems: both rows at n = 9, problem 0 at n = 10)
+            wave_lds_sync();
+            if (!NULLTOP || prob == 0u) {
+                const unsigned o = slot;
+                const unsigned src = base + 16u * ((kGA ? 256u : 0u) + prob * 128u);  // b (ga) or a (gb)
+                const float gc0 = lds_ld4(base + 16u * (512u + prob * 128u + (0u ^ swz5<SW>(0u)))).x;
+                const unsigned mh = hi_sign<OP_LC>(o, o, P.negh, 0u, full, 0, 0).mask;
+                const unsigned mo = ((unsigned)__popc(o) & 1u) << 31;
+                float x[16], corr[16];
+                const unsigned s0 = swz5<SW>(o);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 v = lds_ld4(src + 16u * ((o << 2) | ((unsigned)q ^ s0)));
+                    x[4 * q] = v.x;
+                    x[4 * q + 1] = v.y;
+                    x[4 * q + 2] = v.z;
+                    x[4 * q + 3] = v.w;
+                }
+#pragma unroll
+                for (int el = 0; el < 16; ++el) {
+                    const bool lo_neg = low_sign(LV_LC, LOWNEG, (unsigned)el, (unsigned)el) < 0;
+                    const unsigned m = mh ^ ((cpopc((unsigned)el) & 1) ? mo : 0u) ^ (lo_neg ? 0x80000000u : 0u);
+                    corr[el] = flip(x[el], m) * -gc0;
+                }
+                addblk(base + 16u * ((kGA ? kGa : kGb) + prob * 128u), o, corr, false);
+            }
+        }
+    };
+    subphase(std::integral_constant<int, 0>{});
+    subphase(std::integral_constant<int, 1>{});
+    subphase(std::integral_constant<int, 2>{});
+    subphase(std::integral_constant<int, 3>{});
+    wave_lds_sync();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const unsigned c = (unsigned)lane + 64u * (unsigned)i;
+        const unsigned hr = c >> 7, f = c & 127u, blk = f >> 2;
+        const unsigned so = 16u * (hr * 128u + ((blk << 2) | ((f & 3u) ^ swz5<SW>(blk))));
+        if constexpr (NULLTOP) {
+            const long long at = (grp << 8) + (long long)c;
+            if (GA) reinterpret_cast<float4*>(GA)[at] = lds_ld4(base + 16u * kGa + so);
+            if (GB) reinterpret_cast<float4*>(GB)[at] = lds_ld4(base + 16u * kGb + so);
+        } else {
+            const long long row = grp * 2 + (long long)hr;
+            if (row < P.batch) {
+                const long long at = (row << 7) + (long long)f;
+                if (GA) reinterpret_cast<float4*>(GA)[at] = lds_ld4(base + 16u * kGa + so);
+                if (GB) reinterpret_cast<float4*>(GB)[at] = lds_ld4(base + 16u * kGb + so);
+            }
+        }
+    }
+    if (nxt >= ngrp) break;
     grp = nxt;
     wave_lds_sync();  // the result reads are done before the next group's staging
     }
@@ -3432,6 +3720,49 @@ static bool contr5_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P,
     return true;
 }
 
+// prod_bwd_inner5: the inner product's backward at n = 9 without a null
+// generator and at n = 10 whose only null generator is the top one
+static bool inner5_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, bool& lowneg, bool& nulltop) {
+    if (op != OP_INNER) return false;
+    if (options().product_path != PATH_DEFAULT) return false;
+    if (n == 9 && nul == 0u) nulltop = false;
+    else if (n == 10 && nul == (1u << 9)) nulltop = true;
+    else return false;
+    if (!blocked_metric(op, n, neg, nul, lowneg)) return false;
+    block_sign_params(n, neg, nul, P);
+    P.negh = (neg >> 4) & 31u;  // the n = 9 problems' high generators
+    P.nulh = 0u;
+    return true;
+}
+
+template <bool LN, bool NT>
+static void launch_inner5_t(hipStream_t s, const float* A, const float* B, const float* GCp, float* GA, float* GB,
+                            const BlkParams& P) {
+    const long long R = NT ? 1 : 2;
+    const long long chunk = kMaxGrid * 4 * R;
+    const long long D = NT ? 1024 : 512;
+    for (long long r0 = 0; r0 < P.batch; r0 += chunk) {
+        BlkParams Q = P;
+        Q.batch = P.batch - r0 < chunk ? P.batch - r0 : chunk;
+        const long long groups = (Q.batch + R - 1) / R;
+        const dim3 g(resident_grid((const void*)prod_bwd_inner5<LN, NT>, 256, 0, (groups + 3) / 4));
+        const long long off = r0 * D;
+        hipLaunchKernelGGL((prod_bwd_inner5<LN, NT>), g, dim3(256), 0, s, A + off, B + off,
+                           GCp + (P.ldg4 ? off : 0), GA ? GA + off : nullptr, GB ? GB + off : nullptr, Q);
+    }
+}
+
+static void launch_inner5(bool ln, bool nt, hipStream_t s, const float* A, const float* B, const float* GCp, float* GA,
+                          float* GB, const BlkParams& P) {
+    if (nt) {
+        if (ln) launch_inner5_t<true, true>(s, A, B, GCp, GA, GB, P);
+        else launch_inner5_t<false, true>(s, A, B, GCp, GA, GB, P);
+    } else {
+        if (ln) launch_inner5_t<true, false>(s, A, B, GCp, GA, GB, P);
+        else launch_inner5_t<false, false>(s, A, B, GCp, GA, GB, P);
+    }
+}
+
 template <int OP, bool LN, bool NT>
 static void launch_contr5_t(hipStream_t s, const float* A, const float* B, const float* GCp, float* GA, float* GB,
                             const BlkParams& P) {
@@ -3442,8 +3773,7 @@ static void launch_contr5_t(hipStream_t s, const float* A, const float* B, const
         BlkParams Q = P;
         Q.batch = P.batch - r0 < chunk ? P.batch - r0 : chunk;
         const long long groups = (Q.batch + R - 1) / R;
-        const dim3 g(NT ? resident_grid((const void*)prod_bwd_contr5<OP, LN, NT>, 256, 0, (groups + 3) / 4)
-                        : (unsigned)((groups + 3) / 4));
+        const dim3 g(resident_grid((const void*)prod_bwd_contr5<OP, LN, NT>, 256, 0, (groups + 3) / 4));
         const long long off = r0 * D;
         hipLaunchKernelGGL((prod_bwd_contr5<OP, LN, NT>), g, dim3(256), 0, s, A + off, B + off,
                            GCp + (P.ldg4 ? off : 0), GA ? GA + off : nullptr, GB ? GB + off : nullptr, Q);
@@ -3704,6 +4034,8 @@ int product_bwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
         launch_frame(n, ln, s, a, b, gc, ga, gb, P);
     } else if (contr5_plan(op, n, neg, nul, P, ln, nt5)) {
         launch_contr5(op, ln, nt5, s, a, b, gc, ga, gb, P);
+    } else if (inner5_plan(op, n, neg, nul, P, ln, nt5)) {
+        launch_inner5(ln, nt5, s, a, b, gc, ga, gb, P);
     } else if (contr_plan(op, n, neg, nul, P, ln)) {
         if (op == OP_LC) launch_contr<OP_LC>(n, ln, s, a, b, gc, ga, gb, P);
         else if (op == OP_RC) launch_contr<OP_RC>(n, ln, s, a, b, gc, ga, gb, P);

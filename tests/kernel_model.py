@@ -968,3 +968,51 @@ def contraction5_forward(op, a, b, metric):
         return problem(a, b)
     assert n == 10 and op == LC and metric[9] == 0
     return np.concatenate([problem(a[..., :512], b[..., :512]), problem(a[..., :512], b[..., 512:])], -1)
+
+
+def _inner5_diag(a, b, gc, negh, lowneg):
+    """The element diagonal (i, i) of the (o, o) block pairs, which the lc and the
+    rc schedules both count: factor F(o, il) = s_hi(o, o) (-1)^{|il| |o|} s_lo(il, il),
+    returned as the corrections (-F b_i gc_0, -F a_i gc_0) for (ga, gb)."""
+    f = np.zeros(a.shape[-1])
+    for o in range(32):
+        _, s = hi_sign(LC, o, o, negh, 0, 31, 0, 0)
+        for il in range(16):
+            lo = low_sign(LC, lowneg, il, il)
+            f[o * 16 + il] = s * lo * (-1.0 if (popc(il) * popc(o)) & 1 else 1.0)
+    g0 = gc[..., :1]
+    return -f * b * g0, -f * a * g0
+
+
+def inner5_backward(a, b, gc, metric):
+    """prod_bwd_inner5: the inner product's backward on the lc and rc lane schedules
+    of prod_bwd_contr5 (the lc pairs, the rc pairs, then the element diagonal of the
+    (o, o) block pairs taken off once). n = 9 without a null generator, or n = 10
+    whose only null generator is e9: with a = a0 + a1 e9 and b = b0 + b1 e9,
+    c0 = inner9(a0, b0) and c1 = lc9(a0, b1) + rc9(a1, beta b0) (beta: the grade
+    involution, from moving e9 past the blades of b), so
+    ga0 = inner9_ga(b0, gc0) + lc9_ga(b1, gc1), ga1 = rc9_ga(beta b0, gc1),
+    gb0 = inner9_gb(a0, gc0) + beta rc9_gb(a1, gc1), gb1 = lc9_gb(a0, gc1)."""
+    sched = contr5_schedule_module()
+    n = len(metric)
+    neg = sum(1 << k for k, m in enumerate(metric) if m == -1)
+    lowneg = (neg & 15) == 15
+    negh = (neg >> 4) & 31
+
+    def inner9(a9, b9, g9):
+        gal, gbl = _contr5_problem(LC, a9, b9, g9, negh, lowneg, sched)
+        gar, gbr = _contr5_problem(RC, a9, b9, g9, negh, lowneg, sched)
+        ca, cb = _inner5_diag(a9, b9, g9, negh, lowneg)
+        return gal + gar + ca, gbl + gbr + cb
+
+    if n == 9:
+        assert 0 not in metric
+        return inner9(a, b, gc)
+    assert n == 10 and metric[9] == 0 and 0 not in metric[:9]
+    h = 512
+    beta = np.array([-1.0 if popc(j) & 1 else 1.0 for j in range(h)])
+    a0, a1, b0, b1, g0, g1 = a[..., :h], a[..., h:], b[..., :h], b[..., h:], gc[..., :h], gc[..., h:]
+    ga0, gb0 = inner9(a0, b0, g0)
+    gal, gb1 = _contr5_problem(LC, a0, b1, g1, negh, lowneg, sched)
+    ga1, gbr = _contr5_problem(RC, a1, beta * b0, g1, negh, lowneg, sched)
+    return np.concatenate([ga0 + gal, ga1], -1), np.concatenate([gb0 + beta * gbr, gb1], -1)

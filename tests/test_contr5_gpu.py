@@ -1,9 +1,11 @@
 """prod_fwd_contr5 / prod_bwd_contr5 (the contractions on 5 high bits: lc and
-rc at n = 9, lc at n = 10 whose only null generator is e9, C5's Cl(9,0,1)):
-parity with the fp64 oracle, with the balanced kernels they replace
-(CLF_PRODUCT_PATH=balanced), on ragged batches (two rows per wave at n = 9),
-with a batch-stride-0 upstream gradient, and bitwise row independence.
-Bar: normwise relative error <= 1e-5 for the product and both gradients."""
+rc at n = 9, lc at n = 10 whose only null generator is e9, C5's Cl(9,0,1)) and
+prod_bwd_inner5 (the inner product's backward on the same schedules, n = 9
+and the null-top n = 10): parity with the fp64 oracle, with the balanced
+kernels they replace (CLF_PRODUCT_PATH=balanced), on ragged batches (two rows
+per wave at n = 9), with a batch-stride-0 upstream gradient, and bitwise row
+independence. Bar: normwise relative error <= 1e-5 for the product and both
+gradients."""
 import pytest
 import torch
 
@@ -29,7 +31,9 @@ def inputs(n, batch, seed):
 
 
 CASES = [("lc", (1,) * 9), ("rc", (1,) * 9), ("lc", (-1,) * 4 + (1, -1, 1, 1, -1)), ("rc", (1,) * 4 + (-1,) * 5),
-         ("lc", (1,) * 9 + (0,)), ("lc", (-1,) * 4 + (1, -1, 1, 1, -1, 0))]
+         ("lc", (1,) * 9 + (0,)), ("lc", (-1,) * 4 + (1, -1, 1, 1, -1, 0)),
+         ("inner", (1,) * 9), ("inner", (-1,) * 4 + (1, -1, 1, 1, -1)), ("inner", (1,) * 9 + (0,)),
+         ("inner", (-1,) * 4 + (1, 1, -1, 1, -1, 0))]
 
 
 def _ids(c):
@@ -106,13 +110,15 @@ def test_contr5_stride0_and_one_gradient(case):
     assert torch.equal(ga1, gam) and torch.equal(gb1, gbm)
 
 
-def test_contr5_rows_are_independent():
+@pytest.mark.parametrize("op", ["lc", "inner"])
+def test_contr5_rows_are_independent(op):
     """C5's shape: rows computed in the full batch of 16384 equal, bit for bit,
-    the same rows inside a batch of 1025 (both on prod_bwd_contr5)."""
+    the same rows inside a batch of 1025 (both on prod_bwd_contr5 or
+    prod_bwd_inner5)."""
     metric = (1,) * 9 + (0,)
     B = 16384
     a, b, gc = [t.cuda() for t in inputs(10, B, 80)]
-    code = _lib.OP_CODES["lc"]
+    code = _lib.OP_CODES[op]
     neg, nul = metric_masks(metric)
     ga, gb = products._product_bwd(code, 10, neg, nul, a, b, gc, True, True)
     idx = torch.cat([torch.arange(0, 512), torch.arange(B - 513, B)]).cuda()

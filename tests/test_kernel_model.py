@@ -406,3 +406,19 @@ def test_contraction5_backward_null_top(metric):
     O.einsum_product("lc", at, bt, metric).backward(gc)
     np.testing.assert_allclose(ga, at.grad.numpy(), rtol=0, atol=1e-10)
     np.testing.assert_allclose(gb, bt.grad.numpy(), rtol=0, atol=1e-10)
+
+
+@pytest.mark.parametrize("metric", [(1,) * 9, (-1,) * 4 + (1, -1, 1, 1, -1), (1,) * 9 + (0,),
+                                    (-1,) * 4 + (1, 1, -1, 1, -1, 0)])
+def test_inner5_backward(metric):
+    """prod_bwd_inner5's decomposition (lc and rc schedules, the element diagonal
+    taken off once, the null-top routing with the grade involution) equals the
+    oracle's inner-product gradients."""
+    n = len(metric)
+    g = torch.Generator().manual_seed(11)
+    a, b, gc = (torch.randn(2, 1 << n, generator=g, dtype=torch.float64) for _ in range(3))
+    ga, gb = K.inner5_backward(a.numpy(), b.numpy(), gc.numpy(), metric)
+    at, bt = a.clone().requires_grad_(), b.clone().requires_grad_()
+    O.einsum_product("inner", at, bt, metric).backward(gc)
+    np.testing.assert_allclose(ga, at.grad.numpy(), rtol=0, atol=1e-10)
+    np.testing.assert_allclose(gb, bt.grad.numpy(), rtol=0, atol=1e-10)
