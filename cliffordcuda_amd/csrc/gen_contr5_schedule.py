@@ -249,6 +249,26 @@ LAYOUT = {
 }
 
 
+
+# prod_bwd_inner5 stages a row once for both schedules, so its lc and rc layouts
+# share one block swizzle (searched jointly; per problem and chunk q, reads +
+# result traffic: lc 8 + 0, rc 9 + 0)
+INNER_LAYOUT = {
+    True: Layout(
+        slotA=[30, 26, 2, 29, 8, 7, 6, 20, 17, 22, 28, 14, 23, 24, 27, 19, 21, 15, 5, 4, 1, 31, 18, 0, 9, 10, 11, 13, 25, 16, 3, 12],
+        slotB=[13, 18, 7, 25, 23, 4, 15, 14, 9, 19, 16, 1, 30, 24, 31, 21, 3, 8, 10, 2, 22, 26, 27, 11, 29, 20, 6, 28, 5, 12, 0, 17],
+        ordA=[[1, 3, 0, 2, 5, 4, 7, 6], [2, 1, 3, 0, 6, 7, 4, 5], [2, 1, 0, 3, 5, 4, 7, 6], [2, 3, 1, 0, 5, 4, 6, 7], [2, 1, 3, 0, 5, 7, 4, 6], [2, 3, 1, 0, 6, 5, 7, 4], [3, 1, 2, 0, 5, 7, 4, 6], [3, 2, 1, 0, 6, 4, 5, 7], [1, 3, 2, 0, 4, 7, 6, 5], [1, 2, 0, 3, 6, 5, 4, 7], [3, 0, 2, 1, 4, 7, 5, 6], [2, 0, 3, 1, 5, 7, 4, 6], [1, 2, 0, 3, 4, 5, 6, 7], [2, 1, 3, 0, 7, 6, 4, 5], [2, 3, 1, 0, 6, 5, 7, 4], [2, 3, 0, 1, 5, 6, 4, 7], [2, 1, 0, 3, 4, 6, 7, 5], [3, 2, 1, 0, 4, 6, 7, 5], [2, 1, 0, 3, 7, 6, 4, 5], [3, 2, 1, 0, 4, 7, 6, 5], [2, 1, 3, 0, 5, 4, 7, 6], [3, 1, 2, 0, 4, 6, 7, 5], [1, 2, 3, 0, 4, 5, 7, 6], [3, 0, 1, 2, 5, 4, 6, 7], [1, 3, 2, 0, 7, 4, 5, 6], [1, 3, 0, 2, 4, 7, 5, 6], [0, 2, 1, 3, 5, 6, 4, 7], [2, 1, 0, 3, 7, 6, 5, 4], [1, 3, 0, 2, 6, 5, 4, 7], [1, 2, 0, 3, 6, 4, 5, 7], [1, 3, 2, 0, 5, 4, 7, 6], [1, 3, 2, 0, 7, 6, 4, 5]],
+        ordB=[[3, 2, 0, 1, 7, 4, 6, 5], [0, 1, 2, 3, 5, 6, 4, 7], [0, 1, 2, 3, 4, 5, 6, 7], [0, 3, 2, 1, 7, 5, 4, 6], [1, 2, 0, 3, 7, 4, 6, 5], [2, 3, 1, 0, 7, 6, 5, 4], [0, 1, 2, 3, 7, 5, 4, 6], [0, 3, 1, 2, 4, 6, 7, 5], [3, 1, 2, 0, 6, 4, 5, 7], [1, 2, 3, 0, 5, 4, 7, 6], [2, 3, 1, 0, 6, 5, 4, 7], [2, 3, 0, 1, 4, 7, 6, 5], [3, 1, 2, 0, 6, 4, 5, 7], [0, 1, 2, 3, 6, 5, 7, 4], [2, 1, 3, 0, 4, 5, 6, 7], [0, 3, 2, 1, 7, 4, 6, 5], [0, 1, 2, 3, 5, 4, 7, 6], [0, 1, 2, 3, 6, 5, 7, 4], [2, 3, 1, 0, 4, 7, 6, 5], [0, 2, 1, 3, 6, 4, 7, 5], [0, 2, 3, 1, 7, 4, 6, 5], [1, 0, 3, 2, 4, 7, 5, 6], [1, 2, 0, 3, 4, 6, 5, 7], [0, 3, 1, 2, 4, 5, 7, 6], [0, 3, 1, 2, 5, 7, 6, 4], [3, 2, 1, 0, 4, 6, 7, 5], [3, 1, 2, 0, 5, 6, 7, 4], [3, 1, 0, 2, 5, 6, 7, 4], [3, 2, 1, 0, 4, 7, 6, 5], [2, 3, 1, 0, 7, 4, 6, 5], [1, 3, 2, 0, 5, 4, 7, 6], [1, 3, 2, 0, 5, 7, 6, 4]],
+        swz=[2, 3, 0, 2, 1, 0, 2, 3, 0, 2, 3, 1, 2, 1, 2, 0, 3, 1, 1, 0, 3, 2, 1, 2, 1, 0, 3, 3, 2, 3, 0, 1]),
+    False: Layout(
+        slotA=[29, 24, 25, 28, 3, 10, 22, 30, 7, 0, 6, 21, 27, 15, 20, 19, 17, 4, 1, 14, 18, 16, 12, 26, 13, 31, 5, 2, 9, 11, 8, 23],
+        slotB=[4, 10, 21, 27, 0, 31, 16, 3, 14, 2, 8, 11, 12, 20, 24, 26, 18, 7, 17, 23, 13, 5, 30, 25, 22, 9, 6, 1, 19, 15, 29, 28],
+        ordA=[[0, 2, 3, 1, 6, 7, 4, 5], [1, 0, 3, 2, 5, 6, 4, 7], [3, 2, 1, 0, 7, 6, 4, 5], [0, 3, 2, 1, 5, 4, 6, 7], [1, 2, 3, 0, 6, 5, 4, 7], [2, 1, 0, 3, 5, 7, 6, 4], [2, 3, 1, 0, 4, 5, 6, 7], [2, 3, 0, 1, 4, 7, 5, 6], [1, 0, 2, 3, 7, 4, 5, 6], [0, 1, 2, 3, 7, 6, 4, 5], [3, 1, 0, 2, 6, 5, 7, 4], [2, 3, 0, 1, 7, 6, 4, 5], [1, 3, 0, 2, 5, 6, 7, 4], [1, 3, 2, 0, 6, 5, 7, 4], [3, 2, 1, 0, 5, 4, 7, 6], [0, 3, 1, 2, 4, 6, 5, 7], [1, 3, 2, 0, 7, 6, 4, 5], [2, 0, 1, 3, 6, 4, 5, 7], [1, 3, 0, 2, 5, 6, 7, 4], [0, 2, 3, 1, 4, 7, 5, 6], [3, 2, 1, 0, 7, 6, 5, 4], [1, 0, 2, 3, 5, 7, 4, 6], [3, 0, 1, 2, 7, 6, 5, 4], [2, 0, 3, 1, 6, 7, 5, 4], [1, 3, 2, 0, 6, 7, 4, 5], [2, 3, 1, 0, 6, 7, 4, 5], [2, 3, 1, 0, 4, 6, 5, 7], [2, 3, 1, 0, 4, 7, 5, 6], [1, 3, 0, 2, 4, 7, 5, 6], [1, 3, 2, 0, 7, 6, 4, 5], [0, 2, 1, 3, 7, 4, 6, 5], [1, 3, 2, 0, 4, 7, 5, 6]],
+        ordB=[[3, 2, 0, 1, 5, 6, 7, 4], [0, 2, 1, 3, 4, 7, 5, 6], [1, 3, 2, 0, 4, 6, 5, 7], [1, 2, 3, 0, 6, 4, 5, 7], [0, 3, 1, 2, 4, 6, 5, 7], [0, 2, 3, 1, 5, 4, 6, 7], [2, 3, 1, 0, 4, 6, 5, 7], [2, 1, 0, 3, 4, 6, 7, 5], [3, 1, 0, 2, 6, 7, 5, 4], [2, 0, 3, 1, 4, 6, 5, 7], [2, 3, 0, 1, 6, 5, 4, 7], [3, 1, 2, 0, 6, 4, 5, 7], [3, 0, 2, 1, 6, 7, 5, 4], [3, 2, 1, 0, 7, 4, 6, 5], [2, 1, 0, 3, 4, 6, 5, 7], [0, 2, 3, 1, 5, 7, 6, 4], [3, 2, 0, 1, 6, 4, 7, 5], [3, 0, 2, 1, 7, 4, 5, 6], [1, 0, 2, 3, 5, 6, 7, 4], [1, 0, 3, 2, 4, 5, 7, 6], [3, 0, 2, 1, 7, 6, 4, 5], [2, 3, 0, 1, 6, 7, 4, 5], [2, 1, 0, 3, 7, 6, 4, 5], [2, 1, 3, 0, 5, 6, 7, 4], [2, 3, 1, 0, 6, 7, 5, 4], [1, 3, 2, 0, 6, 5, 4, 7], [1, 3, 0, 2, 5, 4, 6, 7], [2, 3, 1, 0, 6, 5, 7, 4], [3, 1, 2, 0, 7, 6, 4, 5], [2, 0, 3, 1, 6, 7, 4, 5], [2, 3, 0, 1, 7, 5, 6, 4], [2, 0, 3, 1, 5, 7, 4, 6]],
+        swz=[2, 3, 0, 2, 1, 0, 2, 3, 0, 2, 3, 1, 2, 1, 2, 0, 3, 1, 1, 0, 3, 2, 1, 2, 1, 0, 3, 3, 2, 3, 0, 1]),
+}
+assert INNER_LAYOUT[True].swz == INNER_LAYOUT[False].swz
+
 # ---- forward ----------------------------------------------------------------------
 FT = 8
 
@@ -371,25 +391,28 @@ _TYPE = {"F": 0, "D": 1, "help": 2, "own": 3}
 
 
 def header_text():
-    lines = ["// Generated by gen_contr5_schedule.py (lane schedules of prod_bwd_contr5 and prod_fwd_contr5); do not edit.",
+    lines = ["// Generated by gen_contr5_schedule.py (lane schedules of prod_bwd_contr5, prod_bwd_inner5 and prod_fwd_contr5); do not edit.",
              "#pragma once", "", "namespace clf {", ""]
-    for lc, tag in ((True, "Lc"), (False, "Rc")):
-        steps = steps_by_slot(lc)
-        lines.append(f"// kContr5Steps{tag}[slot][t]: output block | partner block << 5 | idle << 11 (t < 8: ga, t >= 8: gb)")
-        lines.append(f"__constant__ unsigned short kContr5Steps{tag}[32][16] = {{")
-        for s in range(NB):
-            lines.append("    {" + ", ".join(str(2048 if x is None else x[0] | (x[1] << 5)) for x in steps[s]) + "},")
-        lines.append("};")
-        lines.append(f"// kContr5Out{tag}[slot][phase]: type (0 F, 1 D, 2 helper, 3 owner) | block1 << 2 | block2 << 7 |")
-        lines.append("// partial slot << 12 | partial count << 16")
-        lines.append(f"__constant__ unsigned kContr5Out{tag}[32][2] = {{")
-        for s, row in enumerate(outputs_by_slot(lc)):
-            enc = [_TYPE[t] | (b1 << 2) | (b2 << 7) | (ps << 12) | (cnt << 16) for t, b1, b2, ps, cnt in row]
-            lines.append("    {" + ", ".join(str(v) for v in enc) + "},")
-        lines.append("};")
-        swz = sum(LAYOUT[lc].swz[b] << (2 * b) for b in range(NB))
-        lines.append(f"constexpr unsigned long long kContr5Swz{tag} = 0x{swz:016x}ull;")
-        lines.append("")
+    for lays, pre in ((LAYOUT, "kContr5"), (INNER_LAYOUT, "kContr5In")):
+        for lc, tag in ((True, "Lc"), (False, "Rc")):
+            lay = lays[lc]
+            steps = steps_by_slot(lc, lay)
+            lines.append(f"// {pre}Steps{tag}[slot][t]: output block | partner block << 5 | idle << 11 (t < 8: ga, t >= 8: gb)")
+            lines.append(f"__constant__ unsigned short {pre}Steps{tag}[32][16] = {{")
+            for s in range(NB):
+                lines.append("    {" + ", ".join(str(2048 if x is None else x[0] | (x[1] << 5)) for x in steps[s]) + "},")
+            lines.append("};")
+            lines.append(f"// {pre}Out{tag}[slot][phase]: type (0 F, 1 D, 2 helper, 3 owner) | block1 << 2 | block2 << 7 |")
+            lines.append("// partial slot << 12 | partial count << 16")
+            lines.append(f"__constant__ unsigned {pre}Out{tag}[32][2] = {{")
+            for s, row in enumerate(outputs_by_slot(lc, lay)):
+                enc = [_TYPE[t] | (b1 << 2) | (b2 << 7) | (ps << 12) | (cnt << 16) for t, b1, b2, ps, cnt in row]
+                lines.append("    {" + ", ".join(str(v) for v in enc) + "},")
+            lines.append("};")
+            if lays is LAYOUT or lc:
+                swz = sum(lay.swz[b] << (2 * b) for b in range(NB))
+                lines.append(f"constexpr unsigned long long {pre}Swz{tag if lays is LAYOUT else ''} = 0x{swz:016x}ull;")
+            lines.append("")
     steps = fwd_steps_by_slot()
     lines.append("// kContr5Fwd[slot][t]: output block | S << 5 | idle << 11 (pair (a[S], b[S | o]) for lc)")
     lines.append("__constant__ unsigned short kContr5Fwd[32][8] = {")

@@ -390,6 +390,7 @@ struct BlkParams {
     int split_log;  // small-batch kernels: log2 of the partner splits S per output block
     int wpr_log;    // small-batch kernels: log2 of the workgroups per row
     unsigned rskew; // blocked kernels: 2-bit slot skew of staged row r at bits 2 (r & 15)
+    unsigned negl;  // metric mask, bits 0-3 (the regressive product's dual signs)
 };
 
 // Stage NOPS (2 or 3) row-major operands s0, s1[, s2] for the workgroup's rows
@@ -2142,6 +2143,30 @@ __device__ __forceinline__ void frame_disjoint(float (&acc)[16], const float (&w
     (term(std::integral_constant<int, Is>{}), ...);
 }
 
+// The regressive product as a wedge product of duals (the reference's definition,
+// c = dual(dual(a) ^ dual(b))): with (D x)[k] = t(~k) x[~k] and
+// t(m) = (-1)^{bitsum(m) + |m & NEG| + C(n,2) + |NEG|}, c = D wedge(D a, D b), so its
+// backward is the wedge backward on (D a, D b, D^T gc) followed by D^T on both
+// gradients ((D^T y)[k] = t(k) y[~k]). On a float4 chunk F (elements 4F + c) the
+// complement reverses the chunk order and the components; dual_chunk_mask(F) has
+// bit c set where t(4F + c) = -1.
+__device__ __forceinline__ unsigned dual_chunk_mask(unsigned F, unsigned neg, unsigned c0) {
+    const unsigned b = ((unsigned)bitsum_parity(F) ^ (unsigned)__popc(F & (neg >> 2)) ^ c0) & 1u;
+    unsigned m = 0u;
+#pragma unroll
+    for (unsigned c = 0; c < 4u; ++c) m |= ((b ^ (c >> 1) ^ (unsigned)__popc(c & neg & 3u)) & 1u) << c;
+    return m;
+}
+
+// out.c = src.(3 - c), negated where bit (3 - c) (SRC: the source element's sign) or bit c
+// (the destination element's) of m is set
+template <bool SRC>
+__device__ __forceinline__ float4 dual_chunk(const float4& v, unsigned m) {
+    auto sg = [&](float x, unsigned bit) { return ((m >> bit) & 1u) ? -x : x; };
+    return SRC ? make_float4(sg(v.w, 3), sg(v.z, 2), sg(v.y, 1), sg(v.x, 0))
+               : make_float4(sg(v.w, 0), sg(v.z, 1), sg(v.y, 2), sg(v.x, 3));
+}
+
 // The wedge product on the same schedule: lane h takes ga[h] over its sup
 // steps (partner b[p ^ h], gc block p) and gb[~h] over its sub steps
 // (partner a[p], gc block ~h ^ p); both run the disjoint pattern, a gb step
@@ -2152,14 +2177,17 @@ template <int OP, int N, bool LOWNEG>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void prod_bwd_contr_frame(
     const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ GC, float* __restrict__ GA,
     float* __restrict__ GB, BlkParams P) {
-    static_assert(OP == OP_LC || OP == OP_RC || OP == OP_WEDGE, "contractions and the wedge product only");
+    static_assert(OP == OP_LC || OP == OP_RC || OP == OP_WEDGE || OP == OP_REGR,
+                  "contractions, the wedge product and the regressive product only");
+    constexpr bool kRg = OP == OP_REGR;  // the wedge schedule on the duals (dual_chunk_mask)
+    constexpr int OPW = kRg ? OP_WEDGE : OP;
     constexpr int NH = N - 4, NB = 1 << NH, R = 64 >> NH;
     using Sch = FrameSched<NH>;
     using Cs = ContrSched<NH>;
     constexpr int T = Sch::T;
     constexpr unsigned full = NB - 1u;
-    constexpr bool kW = OP == OP_WEDGE;
-    constexpr bool kLC = OP != OP_RC;  // sub steps yield gb (lc, wedge) or ga (rc)
+    constexpr bool kW = OPW == OP_WEDGE;
+    constexpr bool kLC = OPW != OP_RC;  // sub steps yield gb (lc, wedge) or ga (rc)
     __shared__ __attribute__((aligned(64))) float4 lds[4][3 * kBalGroupF4];  // a | b | gc
     // the steps of lane (h, row slot skew rs): tab[t][rs * NB + h]
     __shared__ unsigned tab[T][4 * NB];
@@ -2174,9 +2202,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     const long long grp = (long long)blockIdx.x * 4 + wave;
     const BalLane L = bal_lane(N, lane);
     const bool gbc = P.ldg4 == 0;
-    const BalPre pa = bal_fetch(bal_src(A, grp, P.batch, N, R), L, N - 2);
-    const BalPre pb = bal_fetch(bal_src(B, grp, P.batch, N, R), L, N - 2);
-    const BalPre pg = bal_fetch(bal_src(GC, grp, P.batch, N, R, gbc), L, N - 2);
+    constexpr unsigned D4 = 1u << (N - 2);
+    // regressive: D a, D b and D^T gc, from the complemented chunks
+    auto fetch = [&](const float* src, bool bc, int w) {
+        const BalSrc sv = bal_src(src, grp, P.batch, N, R, bc);
+        BalPre p;
+        if constexpr (!kRg) {
+            p = bal_fetch(sv, L, N - 2);
+        } else {
+            const unsigned neg = (P.negh << 4) | P.negl;
+            const unsigned c0 = (unsigned)((N * (N - 1) / 2 + __popc(neg)) & 1);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const unsigned row = L.rr[i] < sv.rlim ? L.rr[i] : sv.rlim;
+                const unsigned fr = D4 - 1u - L.ff[i];
+                const float4 v = sv.g0[(row << (N - 2)) | fr];
+                p.v[i] = w < 2 ? dual_chunk<true>(v, dual_chunk_mask(fr, neg, c0))
+                               : dual_chunk<false>(v, dual_chunk_mask(L.ff[i], neg, c0));
+            }
+        }
+        return p;
+    };
+    const BalPre pa = fetch(A, false, 0);
+    const BalPre pb = fetch(B, false, 1);
+    const BalPre pg = fetch(GC, gbc, 2);
     // entry: gc block offset (o ^ p), partner offset (a at +0, b at +4 KB; slot
     // order reversed in sub mode), then the step's flip bits: pair sign S,
     // parity term Pm, w1 and w2 terms (sub mode), rho (gb steps), gc parity
@@ -2341,8 +2390,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
             const long long rr = grp * R + (long long)L.rr[i];
             if (rr < P.batch) {
                 const long long at = (rr << (N - 2)) + (long long)L.ff[i];
-                if (GA) reinterpret_cast<float4*>(GA)[at] = lds_ld4(a0 + L.so[i]);
-                if (GB) reinterpret_cast<float4*>(GB)[at] = lds_ld4(a0 + 4096u + L.so[i]);
+                if constexpr (kRg) {  // D^T of the wedge gradients: the complemented chunk, dest signs
+                    const unsigned neg = (P.negh << 4) | P.negl;
+                    const unsigned c0 = (unsigned)((N * (N - 1) / 2 + __popc(neg)) & 1);
+                    const unsigned m = dual_chunk_mask(L.ff[i], neg, c0);
+                    const unsigned fr = D4 - 1u - L.ff[i], blk = fr >> 2, r4 = L.rr[i];
+                    const unsigned so = 16u * ((r4 << (N - 2)) + (blk << 2) + ((fr & 3u) ^ swz(blk) ^ (r4 & 3u)));
+                    if (GA) reinterpret_cast<float4*>(GA)[at] = dual_chunk<false>(lds_ld4(a0 + so), m);
+                    if (GB) reinterpret_cast<float4*>(GB)[at] = dual_chunk<false>(lds_ld4(a0 + 4096u + so), m);
+                } else {
+                    if (GA) reinterpret_cast<float4*>(GA)[at] = lds_ld4(a0 + L.so[i]);
+                    if (GB) reinterpret_cast<float4*>(GB)[at] = lds_ld4(a0 + 4096u + L.so[i]);
+                }
             }
         }
     }
@@ -2607,7 +2666,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 // and the right contraction's (jh inside ih); the (o, o) pairs belong to both,
 // and so does their element diagonal (il = jl), which the two low patterns
 // would count twice. prod_bwd_inner5 runs the lc and the rc lane schedules of
-// prod_bwd_contr5 one after the other on the same staged rows: four sub-phases
+// prod_bwd_contr5 (their searched layouts for one shared block swizzle,
+// kContr5In*) one after the other on the same staged rows: four sub-phases
 // of 8 steps (lc ga, rc ga, lc gb, rc gb), each with its compile-time low
 // pattern, each flushed into result rows in LDS by its owners (helpers'
 // partials first), then the element diagonal taken off once:
@@ -2629,7 +2689,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     float* __restrict__ GB, BlkParams P) {
     constexpr int N = NULLTOP ? 10 : 9;
     constexpr int R = NULLTOP ? 1 : 2;
-    constexpr unsigned long long SW = kContr5SwzLc;
+    constexpr unsigned long long SW = kContr5InSwz;
     constexpr unsigned full = 31u;
     // per wave (float4): a at 0 (rows 0, 1 or halves a0, a1), b at 256, gc at 512, the zero block at
     // 768, partial slots at 772 (8 slots of 4 float4 per problem), ga rows at 836; the gb rows go
@@ -2661,7 +2721,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
             const bool lcr = (u & 1) == 0, ga = u < 2;
             for (int t = 0; t < 8; ++t) {
                 const int tt = t + (ga ? 0 : 8);
-                const unsigned st = lcr ? kContr5StepsLc[slot][tt] : kContr5StepsRc[slot][tt];
+                const unsigned st = lcr ? kContr5InStepsLc[slot][tt] : kContr5InStepsRc[slot][tt];
                 unsigned e;
                 if (st & 2048u) {
                     e = (kZero << 4) | (kZero << 18);
@@ -2790,7 +2850,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         };
         frame_steps(step, std::make_integer_sequence<int, 8>{});
         wave_lds_sync();  // every block read of the sub-phase is done
-        const unsigned d = kL ? kContr5OutLc[slot][U >> 1] : kContr5OutRc[slot][U >> 1];
+        const unsigned d = kL ? kContr5InOutLc[slot][U >> 1] : kContr5InOutRc[slot][U >> 1];
         const unsigned typ = d & 3u;
         const unsigned part = base + 16u * (kPart + prob * 32u);
         float sv[16];
@@ -3518,6 +3578,7 @@ static void block_sign_params(int n, uint32_t neg, uint32_t nul, BlkParams& P) {
     P.nulh = nul >> 4;
     P.nm1 = (n - 1) & 1;
     P.mu = popc_rt(neg) & 1;
+    P.negl = neg & 15u;
 }
 
 constexpr size_t kBlockedLdsMax = 48 * 1024;
@@ -3660,9 +3721,13 @@ static void launch_frame(int n, bool ln, hipStream_t s, const float* A, const fl
 }
 
 // The contractions' backward on the frame schedule: lc and rc for
-// 4 <= n <= 8 without a null generator and with a uniform low metric.
+// 4 <= n <= 8 without a null generator and with a uniform low metric; the
+// wedge product, and the regressive product as the wedge of duals, for any
+// metric without a null generator.
 static bool contr_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, bool& lowneg) {
-    if ((op != OP_LC && op != OP_RC && op != OP_WEDGE) || n < kFrameMinN || n > kFrameMaxN || nul != 0u) return false;
+    if ((op != OP_LC && op != OP_RC && op != OP_WEDGE && op != OP_REGR) || n < kFrameMinN || n > kFrameMaxN ||
+        nul != 0u)
+        return false;
     if (options().product_path != PATH_DEFAULT) return false;
     if (!blocked_metric(op, n, neg, nul, lowneg)) return false;
     block_sign_params(n, neg, nul, P);
@@ -4039,6 +4104,7 @@ int product_bwd(int op, int n, uint32_t neg, uint32_t nul, const float* a, const
     } else if (contr_plan(op, n, neg, nul, P, ln)) {
         if (op == OP_LC) launch_contr<OP_LC>(n, ln, s, a, b, gc, ga, gb, P);
         else if (op == OP_RC) launch_contr<OP_RC>(n, ln, s, a, b, gc, ga, gb, P);
+        else if (op == OP_REGR) launch_contr<OP_REGR>(n, false, s, a, b, gc, ga, gb, P);
         else launch_contr<OP_WEDGE>(n, false, s, a, b, gc, ga, gb, P);
     } else if (!force_generic && bal_plan(op, n, neg, nul, false, P, ln)) {
 #define CLF_BWD_BAL(OPV)                                                       \

@@ -816,13 +816,13 @@ def contr5_schedule_module():
     return mod
 
 
-def _contr5_problem(op, a, b, gc, negh, lowneg, sched):
+def _contr5_problem(op, a, b, gc, negh, lowneg, sched, lay=None):
     """One n = 9 problem as prod_bwd_contr5 runs it: per lane slot, steps 0-7
     ga pairs and 8-15 gb pairs (the blocked backward's per-pair arithmetic),
     four 4-step pieces, then per phase the slot's outputs (F, D, H/Q owners
     adding their helpers' partials in slot order). Returns (ga, gb)."""
     lc = op == LC
-    steps, outs = sched.steps_by_slot(lc), sched.outputs_by_slot(lc)
+    steps, outs = sched.steps_by_slot(lc, lay), sched.outputs_by_slot(lc, lay)
     T = _tables(lowneg)
     rows = a.shape[:-1]
     il = np.arange(16)
@@ -999,9 +999,11 @@ def inner5_backward(a, b, gc, metric):
     lowneg = (neg & 15) == 15
     negh = (neg >> 4) & 31
 
+    lays = sched.INNER_LAYOUT
+
     def inner9(a9, b9, g9):
-        gal, gbl = _contr5_problem(LC, a9, b9, g9, negh, lowneg, sched)
-        gar, gbr = _contr5_problem(RC, a9, b9, g9, negh, lowneg, sched)
+        gal, gbl = _contr5_problem(LC, a9, b9, g9, negh, lowneg, sched, lays[True])
+        gar, gbr = _contr5_problem(RC, a9, b9, g9, negh, lowneg, sched, lays[False])
         ca, cb = _inner5_diag(a9, b9, g9, negh, lowneg)
         return gal + gar + ca, gbl + gbr + cb
 
@@ -1013,6 +1015,6 @@ def inner5_backward(a, b, gc, metric):
     beta = np.array([-1.0 if popc(j) & 1 else 1.0 for j in range(h)])
     a0, a1, b0, b1, g0, g1 = a[..., :h], a[..., h:], b[..., :h], b[..., h:], gc[..., :h], gc[..., h:]
     ga0, gb0 = inner9(a0, b0, g0)
-    gal, gb1 = _contr5_problem(LC, a0, b1, g1, negh, lowneg, sched)
-    ga1, gbr = _contr5_problem(RC, a1, beta * b0, g1, negh, lowneg, sched)
+    gal, gb1 = _contr5_problem(LC, a0, b1, g1, negh, lowneg, sched, lays[True])
+    ga1, gbr = _contr5_problem(RC, a1, beta * b0, g1, negh, lowneg, sched, lays[False])
     return np.concatenate([ga0 + gal, ga1], -1), np.concatenate([gb0 + beta * gbr, gb1], -1)

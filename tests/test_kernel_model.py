@@ -289,17 +289,20 @@ def test_contr5_header_is_the_generators():
 
 
 @pytest.mark.parametrize("lc", [True, False])
-def test_contr5_schedule_covers_every_pair_once(lc):
+@pytest.mark.parametrize("which", ["LAYOUT", "INNER_LAYOUT"])
+def test_contr5_schedule_covers_every_pair_once(lc, which):
     """Every ga pair (steps 0-7) and gb pair (steps 8-15) of a 5-high-bit
     problem appears exactly once across the 32 lanes, every output is written
-    once per phase, and every helper partial is read by one owner."""
+    once per phase, and every helper partial is read by one owner (the
+    contraction kernels' layouts and the inner kernel's)."""
     sched = K.contr5_schedule_module()
-    steps = sched.steps_by_slot(lc)
+    lay = getattr(sched, which)[lc]
+    steps = sched.steps_by_slot(lc, lay)
     for phase, lo in (("A", 0), ("B", 8)):
         seen = sorted(s for row in steps for s in row[lo:lo + 8] if s is not None)
         want = sorted((o, p) for o in range(32) for p in sched.plist(o, phase, lc))
         assert seen == want
-    outs = sched.outputs_by_slot(lc)
+    outs = sched.outputs_by_slot(lc, lay)
     for ph in range(2):
         blocks, written, read = [], set(), []
         for row in outs:
