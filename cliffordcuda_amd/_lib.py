@@ -150,6 +150,9 @@ def reload_options() -> None:
 
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+# torch.cuda.current_device() less its lazy-init check (a tensor on the GPU exists, so
+# the runtime is up)
+_current_device = getattr(torch._C, "_cuda_getDevice", None) or torch.cuda.current_device
 
 
 def stream_of(t: torch.Tensor) -> int:
@@ -157,7 +160,7 @@ def stream_of(t: torch.Tensor) -> int:
     HIP on ROCm), as the raw handle the C ABI takes; the direct query skips
     building a Stream object per call (about 1.7 us of host time each)."""
     if _raw_stream is not None:
-        return _raw_stream(t.device.index)
+        return _raw_stream(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
@@ -177,8 +180,8 @@ _CURRENT = _CurrentDevice()
 def on_device(t: torch.Tensor):
     """Context making ``t``'s device current for a library call (the library
     keeps its tables per device); a no-op when it already is."""
-    idx = t.device.index
-    if idx == torch.cuda.current_device():
+    idx = t.get_device()
+    if idx == _current_device():
         return _CURRENT
     return torch.cuda.device(idx)
 
