@@ -626,7 +626,7 @@ __global__ __launch_bounds__(256) void prod_bwd_blk(const float* __restrict__ A,
     }
 }
 
-// ---- small-batch kernels (10 <= n <= 12): the partner loop split over lanes ----
+// ---- small-batch kernels (9 <= n <= 12): the partner loop split over lanes ----
 // At batches of a few rows the one-lane-per-output-block kernels run one or
 // two waves per row, so a row of n = 12 takes 256 dependent block pairs on one
 // lane (0.65 ms at batch 1). Here a workgroup of 256 lanes owns G = 256 / S
@@ -3910,13 +3910,13 @@ static unsigned bal_grid(const void* kernel, const BlkParams& P) {
     return resident_grid(kernel, 256, 0, (groups + 3) / 4);
 }
 
-// Small-batch kernels: 10 <= n <= 12 (whole row in LDS) when the one-lane-
+// Small-batch kernels: 9 <= n <= 12 (whole row in LDS) when the one-lane-
 // per-output-block kernels would run fewer than 512 waves (batch * NB < 2^15);
 // CLF_PRODUCT_PATH=split forces them at any batch, =blocked or =balanced
 // turn them off.
 static bool split_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, bool& lowneg, bool fwd, dim3& grid,
                        size_t& lds_bytes) {
-    if (n < 10 || n > 12) return false;
+    if (n < 9 || n > 12) return false;
     const int pp = options().product_path;
     if (pp == PATH_BLOCKED || pp == PATH_BALANCED || pp == PATH_TILED || pp == PATH_GENERIC) return false;
     const long long NB = 1LL << (n - 4);

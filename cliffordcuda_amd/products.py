@@ -13,10 +13,33 @@ its forward kernel twice (``extensions/ga/geom_prod.py:242-250``).
 """
 from __future__ import annotations
 
+import importlib.util
+import os
+
 import torch
 
 from . import _lib, _ops
 from ._validate import dim_to_n, metric_masks, normalize_metric
+
+_EXT_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_clf_autograd.so")
+_ext = None
+_ext_tried = False
+
+
+def _autograd_ext():
+    """The products' C++ autograd node (csrc/torch_autograd.cpp, built in-tree
+    by __graft_entry__.build()), or None when it is not built: then the Python
+    autograd.Function below runs the same library calls."""
+    global _ext, _ext_tried
+    if not _ext_tried:
+        _ext_tried = True
+        if os.path.exists(_EXT_PATH):
+            _lib.load()  # the library first: its ABI check, and the extension links to it
+            spec = importlib.util.spec_from_file_location("_clf_autograd", _EXT_PATH)
+            mod = importlib.util.module_from_spec(spec)
+            spec.loader.exec_module(mod)
+            _ext = mod
+    return _ext
 
 
 def _check_operands(a: torch.Tensor, b: torch.Tensor, name: str):
@@ -112,11 +135,15 @@ def product(op: str, a: torch.Tensor, b: torch.Tensor, metric=None) -> torch.Ten
     flat = len(shape) != 2  # (batch, dim) inputs go in as they are: no view nodes in the autograd graph
     a2 = a.contiguous().reshape(-1, dim) if flat else a.contiguous()
     b2 = b.contiguous().reshape(-1, dim) if flat else b.contiguous()
+    ext = _ext if _ext_tried else _autograd_ext()
     if torch.compiler.is_compiling():
         out = _ops.product(a2, b2, code, n, neg, nul)
     elif torch.is_grad_enabled() and (a2.requires_grad or b2.requires_grad):
-        out = _ProductFunc.apply(a2, b2, code, n, neg, nul)
-    else:  # nothing to differentiate: the launch without the autograd node
+        out = ext.product(a2, b2, code, n, neg, nul) if ext is not None else _ProductFunc.apply(a2, b2, code, n, neg,
+                                                                                                nul)
+    elif ext is not None:  # nothing to differentiate: the launch without the autograd node
+        out = ext.product_fwd(a2, b2, code, n, neg, nul)
+    else:
         out = _product_fwd(code, n, neg, nul, a2, b2)
     return out.reshape(shape) if flat else out
 

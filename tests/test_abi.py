@@ -119,3 +119,15 @@ def test_rotor_cs_argument_errors():
     assert lib.clf_rotor_cs_apply_bwd(8, 16, 32, 48, 48, None, 4, None, 0, None) == 1    # gx aliases gy
     assert lib.clf_rotor_cs_compile_bwd(8, 16, None, 32, None) == 1
     assert lib.clf_rotor_compile_fwd(1, 16, 32, None, None) == 1
+
+
+def test_autograd_extension_loads_when_built():
+    """The products' C++ autograd node, when built, loads on a host without a GPU
+    and exports its two entries (products.py falls back to the Python Function
+    only when it is absent)."""
+    import os
+    from cliffordcuda_amd import products
+    if not os.path.exists(products._EXT_PATH):
+        pytest.skip("the C++ autograd node is not built here")
+    ext = products._autograd_ext()
+    assert ext is not None and callable(ext.product) and callable(ext.product_fwd)

@@ -86,7 +86,9 @@ def test_product_bwd_stride0_equals_materialised(case, clf_env):
 def test_autograd_hands_over_stride0_rows(monkeypatch):
     """sum() and sum(0) backward reach the kernels with row stride 0 (the
     expansion is not materialised), with the gradients of the materialised
-    upstream gradient."""
+    upstream gradient. Spied on the Python autograd.Function's path (the C++
+    node, csrc/torch_autograd.cpp, applies the same rule and is compared with
+    this path bit for bit in test_autograd_ext_gpu.py)."""
     seen = []
     real = _lib.grad_rows
 
@@ -95,6 +97,9 @@ def test_autograd_hands_over_stride0_rows(monkeypatch):
         seen.append(out[1])
         return out
 
+    from cliffordcuda_amd import products
+    monkeypatch.setattr(products, "_ext", None)
+    monkeypatch.setattr(products, "_ext_tried", True)
     monkeypatch.setattr(_lib, "grad_rows", spy)
     metric = (1,) * 7 + (-1,)
     cl = cc.CliffordAlgebra(metric, device="cuda")

@@ -1,8 +1,8 @@
-"""The small-batch kernels (prod_fwd_split / prod_bwd_split, 10 <= n <= 12):
+"""The small-batch kernels (prod_fwd_split / prod_bwd_split, 9 <= n <= 12):
 at the reference's published shapes (batch 1 .. 64) a row's partner loop is
 split over the lanes of several workgroups and the partial blocks are summed in
-LDS in a fixed order. Parity with the fp64 oracle for every op at n = 10, 11,
-12 (Euclidean, negative and null high generators), forced onto larger ragged
+LDS in a fixed order. Parity with the fp64 oracle for every op at n = 9, 10,
+11, 12 (Euclidean, negative and null high generators), forced onto larger ragged
 batches, against the whole-row kernels, and bitwise row independence.
 Bar: normwise relative error <= 1e-5 for values and both gradients."""
 import pytest
@@ -37,7 +37,7 @@ def inputs(n, batch, seed):
 
 
 METRICS = [(1,) * 10, (1,) * 6 + (-1, 1, -1, 1), (1,) * 9 + (0,), (-1,) * 4 + (1,) * 6 + (-1,),
-           (1,) * 4 + (-1, 0, 1, 1, 1, 1, 1)]
+           (1,) * 4 + (-1, 0, 1, 1, 1, 1, 1), (1,) * 9, (-1,) * 4 + (1, -1, 0, 1, 1)]
 
 
 @pytest.mark.parametrize("metric", METRICS, ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
@@ -74,10 +74,10 @@ def test_small_batch_parity_n12(op):
 
 @pytest.mark.parametrize("op", O.OPS)
 def test_split_forced_equals_whole_row_kernels(op, clf_env):
-    """CLF_PRODUCT_PATH=split at a ragged batch of 300 rows (n = 10) and 37 rows
-    (n = 11) against the balanced / whole-row kernels (=blocked), which the
+    """CLF_PRODUCT_PATH=split at a ragged batch of 300 rows (n = 10), 37 rows
+    (n = 11) and 129 rows (n = 9) against the balanced / whole-row kernels (=blocked), which the
     oracle tests pin on their own."""
-    for metric, batch in (((1,) * 8 + (-1, 1), 300), ((1,) * 11, 37)):
+    for metric, batch in (((1,) * 8 + (-1, 1), 300), ((1,) * 11, 37), ((1,) * 5 + (-1, 1, 1, 1), 129)):
         n = len(metric)
         a, b, gc = [t.cuda() for t in inputs(n, batch, 130 + n)]
         print(f"[case] split forced op={op} n={n} batch={batch}", flush=True)
