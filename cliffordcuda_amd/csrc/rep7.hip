@@ -128,24 +128,76 @@ __device__ __forceinline__ void gather7_single(const float* __restrict__ row, co
     wht_inplace<8>(t);
 }
 
-// W[x][c] = s_x(c >> D) T[c & (2^D - 1)]; sm[m] holds s_x(m) as a sign bit (sm[0] = 0)
-template <int D>
-__device__ __forceinline__ void expand7(const float (&t)[1 << D], const unsigned (&sm)[16 >> D], float (&w)[16]) {
-    constexpr int L = 1 << D;
-#pragma unroll
-    for (int c = 0; c < 16; ++c)
-        w[c] = (c < L) ? t[c] : __uint_as_float(__float_as_uint(t[c & (L - 1)]) ^ sm[c >> D]);
+// Operand k of the chain at lane x is W[x ^ k][k] = s_{x ^ k}(k >> D) T_{x ^ k}[k & (L - 1)]
+// with W[x][c] = s_x(c >> D) T[c & (L - 1)]. zhi is linear in x (the labels
+// form a subspace), so s_{x ^ k}(m) = s_x(m) s_k(m); the lane-independent
+// factor s_k(k >> D) appears in both operands of step k and cancels in the
+// product, which leaves op[k] = s_x(k >> D) T[k & (L - 1)] read from lane x ^ k.
+// The 16 shuffles come from L source registers, so they share their DPP
+// stages, and the sign (sg[m] = s_x(m) as +-1.0) multiplies the last stage,
+// which the compiler fuses into one DPP multiply. DPP controls: quad_perm
+// xor 1 (0xB1), 2 (0x4E), 3 (0x1B); row_half_mirror = xor 7 (0x141);
+// row_mirror = xor 15 (0x140).
+template <unsigned J>
+__device__ __forceinline__ float quad_xor(float v) {
+    if constexpr (J == 1u) return dpp16<0xB1>(v);
+    else if constexpr (J == 2u) return dpp16<0x4E>(v);
+    else if constexpr (J == 3u) return dpp16<0x1B>(v);
+    else return v;
 }
 
-// Q[i] = sum_c W_C[x][c] (-1)^{popc((zhi << D | i) & c)}
+template <unsigned J>
+__device__ __forceinline__ void operand7_d2(const float (&t)[4], const float (&sg)[4], float (&op)[16]) {
+    const float q = quad_xor<J>(t[J]);      // lane x ^ J
+    const float r = quad_xor<J ^ 3u>(t[J]);  // lane x ^ J ^ 3
+    const float h = dpp16<0x141>(q);         // lane x ^ J ^ 7
+    op[J] = q;
+    op[4 + J] = dpp16<0x141>(r) * sg[1];   // x ^ J ^ 3 ^ 7 = x ^ (4 + J)
+    op[12 + J] = dpp16<0x140>(r) * sg[3];  // x ^ J ^ 3 ^ 15 = x ^ (12 + J)
+    op[8 + J] = dpp16<0x140>(h) * sg[2];   // x ^ J ^ 7 ^ 15 = x ^ (8 + J)
+}
+
+template <unsigned J>
+__device__ __forceinline__ void operand7_d3(const float (&t)[8], const float (&sg)[2], float (&op)[16]) {
+    if constexpr (J < 4u) {
+        const float q = quad_xor<J>(t[J]);                 // lane x ^ J
+        op[J] = q;
+        op[8 + J] = dpp16<0x140>(dpp16<0x141>(q)) * sg[1];  // x ^ J ^ 7 ^ 15 = x ^ (8 + J)
+    } else {
+        const float q = quad_xor<J ^ 7u>(t[J]);   // lane x ^ J ^ 7
+        op[J] = dpp16<0x141>(q);                  // x ^ J
+        op[8 + J] = dpp16<0x140>(q) * sg[1];      // x ^ J ^ 7 ^ 15 = x ^ (8 + J)
+    }
+}
+
 template <int D>
-__device__ __forceinline__ void lane_q7(const float (&wc)[16], const unsigned (&sm)[16 >> D], float (&q)[1 << D]) {
+__device__ __forceinline__ void operand7(const float (&t)[1 << D], const float (&sg)[16 >> D], float (&op)[16]) {
+    if constexpr (D == 2) {
+        operand7_d2<0>(t, sg, op);
+        operand7_d2<1>(t, sg, op);
+        operand7_d2<2>(t, sg, op);
+        operand7_d2<3>(t, sg, op);
+    } else {
+        operand7_d3<0>(t, sg, op);
+        operand7_d3<1>(t, sg, op);
+        operand7_d3<2>(t, sg, op);
+        operand7_d3<3>(t, sg, op);
+        operand7_d3<4>(t, sg, op);
+        operand7_d3<5>(t, sg, op);
+        operand7_d3<6>(t, sg, op);
+        operand7_d3<7>(t, sg, op);
+    }
+}
+
+// Q[i] = sum_c W_C[x][c] (-1)^{popc((zhi << D | i) & c)} (multiplications by +-1 are exact)
+template <int D>
+__device__ __forceinline__ void lane_q7(const float (&wc)[16], const float (&sg)[16 >> D], float (&q)[1 << D]) {
     constexpr int L = 1 << D;
 #pragma unroll
     for (int j = 0; j < L; ++j) {
         float y = wc[j];
 #pragma unroll
-        for (int m = 1; m < (16 >> D); ++m) y += __uint_as_float(__float_as_uint(wc[m * L + j]) ^ sm[m]);
+        for (int m = 1; m < (16 >> D); ++m) y = __builtin_fmaf(wc[m * L + j], sg[m], y);
         q[j] = y;
     }
     wht_inplace<L>(q);
@@ -169,30 +221,31 @@ __device__ __forceinline__ void scatter7_single(float* __restrict__ row, const u
 // per-lane constants: table entries (odd rows' offsets xor-ed) and the sign bits s_x(m)
 template <int D>
 __device__ __forceinline__ void lane_consts7(const Rep7Table& T, unsigned x, int rb, unsigned (&ent)[8],
-                                             unsigned (&sm)[16 >> D]) {
+                                             float (&sg)[16 >> D]) {
     const unsigned oddx = (rb & 1) ? T.odd_xor : 0u;
 #pragma unroll
     for (int k = 0; k < 8; ++k) ent[k] = T.e[x * 8 + k] ^ oddx;
     const unsigned zhi = T.zhi[x];
 #pragma unroll
-    for (int m = 0; m < (16 >> D); ++m) sm[m] = (unsigned)(__popc(zhi & (unsigned)m) & 1) << 31;
+    for (int m = 0; m < (16 >> D); ++m) sg[m] = __uint_as_float(0x3f800000u | ((unsigned)(__popc(zhi & (unsigned)m) & 1) << 31));
 }
 
 // product of the converted operands through the relayout; returns Q of the lane's row
 template <int D>
 __device__ __forceinline__ void product_q7(float* __restrict__ rel, const float (&ta)[1 << D], const float (&tb)[1 << D],
-                                           const unsigned (&sm)[16 >> D], int lane, int rb, unsigned x,
+                                           const float (&sg)[16 >> D], int lane, int rb, unsigned x,
                                            float (&q)[1 << D]) {
-    float wa[16], wb[16];
-    expand7<D>(ta, sm, wa);
-    expand7<D>(tb, sm, wb);
-    const floatx16 acc = mfma_chain(wa, wb);
+    float oa[16], ob[16];
+    operand7<D>(ta, sg, oa);
+    operand7<D>(tb, sg, ob);
+    const floatx16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const floatx16 acc = mfma_chain_pre<false, false>(zero, oa, ob, std::make_integer_sequence<unsigned, 16>{});
     relayout_store(rel, acc, lane);
     wave_lds_sync();
     float wc[16];
     relayout_load(rel, rb, x, wc);
     wave_lds_sync();
-    lane_q7<D>(wc, sm, q);
+    lane_q7<D>(wc, sg, q);
 }
 
 // Memory pipeline (both n = 7 kernels): a wave's loads and stores share one
@@ -216,8 +269,9 @@ __global__ __launch_bounds__(256) void rep7_fwd_kernel(const float* __restrict__
     float* sa = &lds[wave][0];
     float* sb = sa + kRep7GroupFloats;
     const unsigned oddc = T.odd_xor >> 2;
-    unsigned ent[8], sm[16 >> D];
-    lane_consts7<D>(T, x, rb, ent, sm);
+    unsigned ent[8];
+    float sgn[16 >> D];
+    lane_consts7<D>(T, x, rb, ent, sgn);
 
     const long long stride = (long long)gridDim.x * 16;
     const long long rfirst = ((long long)blockIdx.x * 4 + wave) * 4;
@@ -243,8 +297,8 @@ __global__ __launch_bounds__(256) void rep7_fwd_kernel(const float* __restrict__
             gather7_pair<1>(sb + rb * kRep7Dim, ent, tb, tbh);
             wave_lds_sync();
             float q[4], qh[4];
-            product_q7<2>(sa, ta, tb, sm, lane, rb, x, q);
-            product_q7<2>(sa, tah, tbh, sm, lane, rb, x, qh);
+            product_q7<2>(sa, ta, tb, sgn, lane, rb, x, q);
+            product_q7<2>(sa, tah, tbh, sgn, lane, rb, x, qh);
             scatter7_pair(sb + rb * kRep7Dim, ent, q, qh);
         } else {
             float ta[8], tb[8];
@@ -252,7 +306,7 @@ __global__ __launch_bounds__(256) void rep7_fwd_kernel(const float* __restrict__
             gather7_single<1>(sb + rb * kRep7Dim, ent, tb);
             wave_lds_sync();
             float q[8];
-            product_q7<3>(sa, ta, tb, sm, lane, rb, x, q);
+            product_q7<3>(sa, ta, tb, sgn, lane, rb, x, q);
             scatter7_single(sb + rb * kRep7Dim, ent, q);
         }
         wave_lds_sync();
@@ -279,8 +333,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
     float* sx = sg + kRep7GroupFloats;
     float* sr = sx + kRep7GroupFloats;
     const unsigned oddc = T.odd_xor >> 2;
-    unsigned ent[8], sm[16 >> D];
-    lane_consts7<D>(T, x, rb, ent, sm);
+    unsigned ent[8];
+    float sgn[16 >> D];
+    lane_consts7<D>(T, x, rb, ent, sgn);
 
     const long long stride = (long long)gridDim.x * 16;
     const long long rfirst = ((long long)blockIdx.x * 4 + wave) * 4;
@@ -304,14 +359,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
                 float tg[4], tgh[4], tb[4], tbh[4], qh[4];
                 gather7_pair<0>(sg + rb * kRep7Dim, ent, tg, tgh);
                 gather7_pair<0>(sx + rb * kRep7Dim, ent, tb, tbh);
-                product_q7<2>(sr, tg, tb, sm, lane, rb, x, q);
-                product_q7<2>(sr, tgh, tbh, sm, lane, rb, x, qh);
+                product_q7<2>(sr, tg, tb, sgn, lane, rb, x, q);
+                product_q7<2>(sr, tgh, tbh, sgn, lane, rb, x, qh);
                 scatter7_pair(sr + rb * kRep7Dim, ent, q, qh);
             } else {
                 float tg[8], tb[8];
                 gather7_single<0>(sg + rb * kRep7Dim, ent, tg);
                 gather7_single<0>(sx + rb * kRep7Dim, ent, tb);
-                product_q7<3>(sr, tg, tb, sm, lane, rb, x, q);
+                product_q7<3>(sr, tg, tb, sgn, lane, rb, x, q);
                 scatter7_single(sr + rb * kRep7Dim, ent, q);
             }
         }
@@ -329,14 +384,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
                 float tat[4], tath[4], tgt[4], tgth[4], qh[4];
                 gather7_pair<1>(sx + rb * kRep7Dim, ent, tat, tath);
                 gather7_pair<1>(sg + rb * kRep7Dim, ent, tgt, tgth);
-                product_q7<2>(sr, tat, tgt, sm, lane, rb, x, q);
-                product_q7<2>(sr, tath, tgth, sm, lane, rb, x, qh);
+                product_q7<2>(sr, tat, tgt, sgn, lane, rb, x, q);
+                product_q7<2>(sr, tath, tgth, sgn, lane, rb, x, qh);
                 scatter7_pair(sr + rb * kRep7Dim, ent, q, qh);
             } else {
                 float tat[8], tgt[8];
                 gather7_single<1>(sx + rb * kRep7Dim, ent, tat);
                 gather7_single<1>(sg + rb * kRep7Dim, ent, tgt);
-                product_q7<3>(sr, tat, tgt, sm, lane, rb, x, q);
+                product_q7<3>(sr, tat, tgt, sgn, lane, rb, x, q);
                 scatter7_single(sr + rb * kRep7Dim, ent, q);
             }
         }
@@ -465,6 +520,10 @@ static bool rep7_table_build(uint32_t neg, Rep7Table& T) {
         const bool tsign = negsign != ((host_popc(x & z) & 1) != 0);
         T.e[x * 8 + k] = I | (negsign ? 0x80000000u : 0u) | (tsign ? 0x40000000u : 0u);
     }
+    // the kernels' operand signs rely on zhi being linear in x
+    for (unsigned x = 0; x < 16u; ++x)
+        for (unsigned y = 0; y < 16u; ++y)
+            if (T.zhi[x ^ y] != (T.zhi[x] ^ T.zhi[y])) return false;
     // odd-row offset xor with the fewest bank collisions over the gathers of a
     // half-wave (two rows)
     int best = 1 << 30;

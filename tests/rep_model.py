@@ -651,6 +651,48 @@ def rep7_expand(T, zhi, pair):
     return W
 
 
+def rep7_dest_operand(T, zhi, pair):
+    """Operand register k of lane (b, x) as the kernels build it:
+    s_x(k >> d) T[b][x ^ k][k & low]. It differs from xor_operand(rep7_expand(T))
+    by the lane-independent sign s_k(k >> d), which both operands of step k
+    carry and which therefore cancels in the product (zhi is linear in x)."""
+    d = 2 if pair else 3
+    low = (1 << d) - 1
+    op = np.zeros(T.shape[:2] + (16,))
+    for x in range(16):
+        for k in range(16):
+            s = -1 if popc(zhi[x] & (k >> d)) & 1 else 1
+            op[:, x, k] = s * T[:, x ^ k, k & low]
+    return op
+
+
+# DPP row permutations of the operand builder (lane x reads lane perm(x)):
+# quad_perm xor 1, 2, 3, row_half_mirror (xor 7), row_mirror (xor 15)
+DPP_XOR = {"q1": 1, "q2": 2, "q3": 3, "hm": 7, "m": 15}
+
+
+def rep7_operand_dpp_plan(pair):
+    """For each operand register k, the DPP stages (in order) that the kernels
+    apply to source register k & low (operand7_d2 / operand7_d3)."""
+    q = lambda j: [] if j == 0 else ["q%d" % j]
+    plan = {}
+    if pair:
+        for j in range(4):
+            plan[j] = q(j)
+            plan[4 + j] = q(j ^ 3) + ["hm"]
+            plan[12 + j] = q(j ^ 3) + ["m"]
+            plan[8 + j] = q(j) + ["hm", "m"]
+    else:
+        for j in range(8):
+            if j < 4:
+                plan[j] = q(j)
+                plan[8 + j] = q(j) + ["hm", "m"]
+            else:
+                plan[j] = q(j ^ 7) + ["hm"]
+                plan[8 + j] = q(j ^ 7) + ["m"]
+    return plan
+
+
 def rep7_lane_Q(Wc, zhi, pair):
     """Q[b][x][i] = sum_c W_c[b][x][c] (-1)^{popc(z_i & c)}, z_i = zhi << d | i."""
     d = 2 if pair else 3
@@ -685,11 +727,11 @@ def _rep7_product(Xs, tabs, fwd_pairs):
     for X, Y, tx, ty in fwd_pairs:
         TX, ThX = rep7_lane_T(X, ent, pair, tx)
         TY, ThY = rep7_lane_T(Y, ent, pair, ty)
-        accs[0] = accs[0] + mfma_4block_16x16x1(xor_operand(rep7_expand(TX, zhi, pair)),
-                                                xor_operand(rep7_expand(TY, zhi, pair)))
+        accs[0] = accs[0] + mfma_4block_16x16x1(rep7_dest_operand(TX, zhi, pair),
+                                                rep7_dest_operand(TY, zhi, pair))
         if pair:
-            accs[1] = accs[1] + mfma_4block_16x16x1(xor_operand(rep7_expand(ThX, zhi, pair)),
-                                                    xor_operand(rep7_expand(ThY, zhi, pair)))
+            accs[1] = accs[1] + mfma_4block_16x16x1(rep7_dest_operand(ThX, zhi, pair),
+                                                    rep7_dest_operand(ThY, zhi, pair))
     Q = rep7_lane_Q(relayout(accs[0]), zhi, pair)
     Qh = rep7_lane_Q(relayout(accs[1]), zhi, pair) if pair else None
     return rep7_unconvert(Q, Qh, ent, pair)

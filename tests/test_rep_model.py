@@ -164,6 +164,17 @@ def test_rep7_lane_model(metric):
             M = sum(rowvals[r, I] * sign[I] * R.pauli(*label[I], 16) for I in range(128))
             Wd = np.array([[M[x ^ c, c] for c in range(16)] for x in range(16)])
             np.testing.assert_allclose(Wrow[r], Wd, atol=1e-12)
+    # operands with the receiving lane's sign: zhi is linear, and each step's
+    # operand differs from the xor-shuffled W by one lane-independent sign
+    for x in range(16):
+        for y in range(16):
+            assert zhi[x ^ y] == zhi[x] ^ zhi[y]
+    d = 2 if pair else 3
+    for TT in [T] + ([Th] if pair else []):
+        ratio = R.rep7_dest_operand(TT, zhi, pair) / R.xor_operand(R.rep7_expand(TT, zhi, pair))
+        for k in range(16):
+            uk = -1 if R.popc(zhi[k] & (k >> d)) & 1 else 1
+            np.testing.assert_allclose(ratio[:, :, k], uk)
     b = rng.standard_normal((4, 128))
     gc = rng.standard_normal((4, 128))
     tabs = (pair, ent, zhi, gens)
@@ -175,3 +186,17 @@ def test_rep7_lane_model(metric):
     ga, gb = R.kernel7_bwd(a, b, gc, tabs)
     np.testing.assert_allclose(ga, aq.grad.numpy(), atol=1e-10)
     np.testing.assert_allclose(gb, bq.grad.numpy(), atol=1e-10)
+
+
+@pytest.mark.parametrize("pair", [True, False])
+def test_rep7_operand_dpp_stages(pair):
+    """The DPP stages of rep7.hip's operand builder move register k & low of
+    lane x ^ k to lane x for every k."""
+    plan = R.rep7_operand_dpp_plan(pair)
+    assert sorted(plan) == list(range(16))
+    for k, stages in plan.items():
+        src = 0
+        for st in stages:           # lane x reads lane x ^ s at each stage
+            src ^= R.DPP_XOR[st]
+        assert src == k, (k, stages)
+        assert all(st in R.DPP_XOR for st in stages)
