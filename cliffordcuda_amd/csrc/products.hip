@@ -1447,6 +1447,12 @@ struct BalLane {
     unsigned rr[4], ff[4], so[4];
 };
 
+// RX: the row term of the chunk slots as a 4-entry table of 2-bit values
+// (entry r & 3 at bits 2 (r & 3)); 0xE4 is r & 3
+template <unsigned RX = 0xE4u>
+__device__ __forceinline__ unsigned row_x(unsigned r) { return (RX >> (2u * (r & 3u))) & 3u; }
+
+template <unsigned RX = 0xE4u>
 __device__ __forceinline__ BalLane bal_lane(int n, int lane) {
     BalLane L;
     const int d4_log = n - 2;
@@ -1457,7 +1463,7 @@ __device__ __forceinline__ BalLane bal_lane(int n, int lane) {
         const unsigned blk = f >> 2, q = f & 3u;
         L.rr[i] = r;
         L.ff[i] = f;
-        L.so[i] = 16u * ((r << d4_log) + (blk << 2) + (q ^ swz(blk) ^ (r & 3u)));
+        L.so[i] = 16u * ((r << d4_log) + (blk << 2) + (q ^ swz(blk) ^ row_x<RX>(r)));
     }
     return L;
 }
@@ -3139,26 +3145,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
 // counted twice, is taken off the scalar once. The left contraction is the
 // lc half alone and the right contraction the rc half alone (the pairs
 // (S, S | o) and (S | o, S) are exactly their block pairs), with the same
-// schedule and no diagonal correction. Output o has 2^(3 - |o|)
-// partners (27 per row), so eight lanes cover a row in four steps when the
-// lanes of outputs 3 and 7, done early, take four of output 0's eight:
-//   o = 0: S = 0..3 | o = 1, 2, 4: their four | o = 3: S = 0, 4, then o = 0
-//   with S = 4, 5 | o = 5, 6: their two | o = 7: S = 0, idle, then o = 0 with
-//   S = 6, 7,
-// and output 0 adds lane 3's sum (quad DPP) and lane 7's (row shift by 7).
-__device__ __forceinline__ FrameStep fwd7_step(unsigned h, int t) {
-    if (h == 0u) return FrameStep{0u, (unsigned)t, false};
-    if (h == 3u) return t < 2 ? FrameStep{3u, t == 0 ? 0u : 4u, false} : FrameStep{0u, (unsigned)(t + 2), false};
-    if (h == 7u) {
-        if (t == 0) return FrameStep{7u, 0u, false};
-        if (t == 1) return FrameStep{7u, 0u, true};  // idle (sub marks it)
-        return FrameStep{0u, (unsigned)(t + 4), false};
-    }
-    const unsigned co = 7u & ~h;
-    const int cnt = 1 << __popc(co);
-    if (t < cnt) return FrameStep{h, deposit_bits((unsigned)t, co), false};
-    return FrameStep{h, 0u, true};  // idle
-}
+// schedule and no diagonal correction. Output o has 2^(3 - |o|) partners (27
+// per row), so eight lanes cover a row in four steps when the lanes of
+// outputs 3 and 7, done after step 1, take four of output 0's eight: lanes
+// 3, 5, 6 finish their outputs in steps 0 and 1, lane 7 in step 0 (idle in
+// step 1), lanes 3 and 7 then run two o = 0 pairs each, and output 0 adds
+// lane 3's sum (quad DPP) and lane 7's (row shift by 7).
+// Byte h of kFwd7Sched[t] is lane h's pair (o << 3 | p) at step t, or 0x80 |
+// S << 3 | So for an idle step (the blocks read, result discarded); the
+// constants keep the lookup in registers (no memory load before the table). The step orders,
+// the idle reads and the row term of the LDS slots (kFwd7RowX: rows 0..3 ->
+// 3, 0, 2, 1) were searched together so that, under the measured b128 read
+// rule, the 16 lanes of each bank set read one address per 16-byte bank group
+// at every step of all five ops (inner, lc, rc, wedge, regressive), and the
+// row-order output stores stay conflict-free.
+constexpr unsigned kFwd7RowX = 0x63u;
+constexpr unsigned long long kFwd7Sched[4] = {0x38312a2018100a00ull, 0xb73028231c140e01ull, 0x04a5b32106110803ull, 0x07afa02205150c02ull};
 
 // acc[0] += fac * sum_l s_lo(l, l) a[l] b[l] (the diagonal of an o = 0 pair)
 template <bool LOWNEG, int... L>
@@ -3205,18 +3207,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OP == OP_WE
     const unsigned rs = (unsigned)r & 3u;
     const long long ngrp = (P.batch + R - 1) / R;
     const long long grp = (long long)blockIdx.x * 4 + wave;
-    const BalLane L = bal_lane(N, lane);
+    const BalLane L = bal_lane<kFwd7RowX>(N, lane);
     const BalPre pa = bal_fetch(bal_src(A, grp, P.batch, N, R), L, N - 2);
     const BalPre pb = bal_fetch(bal_src(B, grp, P.batch, N, R), L, N - 2);
     if (wave == 0 && lane < 32) {
-        const unsigned th = (unsigned)lane & full, trs = (unsigned)lane >> 3;
+        const unsigned th = (unsigned)lane & full, trs = row_x<kFwd7RowX>((unsigned)lane >> 3);
         for (int t = 0; t < T; ++t) {
-            const FrameStep st = fwd7_step(th, t);
+            const unsigned code = (unsigned)(kFwd7Sched[t] >> (8u * th)) & 0xffu;
+            const bool idle = (code & 0x80u) != 0u;
+            const FrameStep st{(code >> 3) & 7u, code & 7u, idle};
             // wedge: output ~o takes the pair (S, ~o ^ S) for every S inside ~o;
             // regressive: the pair (o | S, ~S) of xor index ~o, stored reversed
-            // at block o
-            const unsigned S = kRg ? (st.o | st.p) : st.p;
-            const unsigned So = kRg ? (full ^ st.p) : kW ? (full ^ st.o ^ S) : (st.p | st.o);
+            // at block o; an idle step reads blocks S = o, So = p of its code
+            const unsigned S = idle ? st.o : kRg ? (st.o | st.p) : st.p;
+            const unsigned So = idle ? st.p : kRg ? (full ^ st.p) : kW ? (full ^ st.o ^ S) : (st.p | st.o);
             const HiSign hl = hi_sign<kRg ? OP_REGR : kW ? OP_WEDGE : OP_INNER>(S, So, P.negh, P.nulh, full, P.nm1,
                                                                                  P.mu);
             const HiSign hr = hi_sign<OP_INNER>(So, S, P.negh, P.nulh, full, P.nm1, P.mu);
@@ -3225,7 +3229,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OP == OP_WE
             tab[t][lane] = offs | (offo << 10) | ((hl.mask >> 31) << 20) | ((hr.mask >> 31) << 21) |
                            ((cross_pi<kRg ? OP_REGR : OP_WEDGE>(S, P.nm1) & 1u) << 22) |
                            (((unsigned)__popc(So) & 1u) << 23) |
-                           ((st.o == 0u ? 1u : 0u) << 24);
+                           ((!idle && st.o == 0u ? 1u : 0u) << 24);
         }
     }
     __syncthreads();
@@ -3312,13 +3316,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OP == OP_WE
     frame_steps(step, std::make_integer_sequence<int, T>{});
     if constexpr (!kRowOut) return;
     // output block ob of row r over the staged a (slots 4 ob + (q ^ swz(ob) ^
-    // (r & 3))), then row-order stores
+    // row_x(r))), then row-order stores
     wave_lds_sync();
     const unsigned a0 = lds_addr4(sa);
     const unsigned ob = kW && !kRg ? full ^ h : h;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const unsigned at = a0 + ((unsigned)r << (N + 2)) + (((ob << 2) | ((unsigned)q ^ swz(ob) ^ rs)) << 4);
+        const unsigned at = a0 + ((unsigned)r << (N + 2)) + (((ob << 2) | ((unsigned)q ^ swz(ob) ^ row_x<kFwd7RowX>(rs))) << 4);
         if (kRg)  // the regressive output block is the xor product's block reversed
             lds_st4(at, make_float4(y[15 - 4 * q], y[14 - 4 * q], y[13 - 4 * q], y[12 - 4 * q]));
         else lds_st4(at, make_float4(y[4 * q], y[4 * q + 1], y[4 * q + 2], y[4 * q + 3]));

@@ -787,19 +787,76 @@ def wedge_frame_backward(a, b, gc, metric):
     return ga, gb
 
 
+def fwd7_tables():
+    """(kFwd7Sched, kFwd7RowX) as prod_fwd_out7 compiles them, read from
+    csrc/products.hip: per lane h and step t the pair code (o << 3 | p, or
+    0x80 | S << 3 | So for an idle step; byte h of the step's constant), and
+    the row term of the LDS slots (entry r & 3 at bits 2 (r & 3))."""
+    import os
+    import re
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "cliffordcuda_amd", "csrc",
+                        "products.hip")
+    text = open(path).read()
+    rowx = int(re.search(r"kFwd7RowX = (0x[0-9a-fA-F]+)u;", text).group(1), 16)
+    body = re.search(r"kFwd7Sched\[4\] = \{(.*?)\};", text, re.S).group(1)
+    steps = [int(v, 16) for v in re.findall(r"0x([0-9a-fA-F]+)ull", body)]
+    assert len(steps) == 4
+    return [[(steps[t] >> (8 * h)) & 0xff for t in range(4)] for h in range(8)], rowx
+
+
 def fwd7_step(h, t):
     """Step t of lane h in prod_fwd_out7 (n = 7): (output block o, partner S)
-    or None (idle). Lanes 3 and 7 finish their outputs early and then take
-    partners 4, 5 and 6, 7 of output 0, whose lane adds their sums after the
-    last step."""
-    if h == 0:
-        return 0, t
-    if h == 3:
-        return (3, (0, 4)[t]) if t < 2 else (0, t + 2)
-    if h == 7:
-        return (7, 0) if t == 0 else (None if t == 1 else (0, t + 4))
-    parts = subsets(7 & ~h)
-    return (h, parts[t]) if t < len(parts) else None
+    or None (idle)."""
+    code = fwd7_tables()[0][h][t]
+    return None if code & 0x80 else ((code >> 3) & 7, code & 7)
+
+
+def fwd7_read_blocks(op, code):
+    """Blocks (S, So) that a step with this code reads: a[S] and b[So] for the
+    lc half (the wedge's pair (S, ~o ^ S), the regressive's (o | S, ~S)), a[So]
+    and b[S] for the rc half; an idle step names its blocks."""
+    full = 7
+    if code & 0x80:
+        return (code >> 3) & 7, code & 7
+    o, p = (code >> 3) & 7, code & 7
+    if op == "regressive":
+        return o | p, full ^ p
+    if op == "wedge":
+        return p, full ^ o ^ p
+    return p, p | o
+
+
+def fwd7_lds_conflicts(op, sched=None, rowx=None, swz=None):
+    """Extra LDS cycles of prod_fwd_out7's block reads (per chunk, one 32-lane
+    half: rows 0..3; rows 4..7 repeat it) and of its row-order output stores,
+    under the measured rules of gen_contr5_schedule (READ_SETS, WRITE_SETS).
+    Lane r * 8 + h reads row r's blocks at slot 4 X + (swz(X) ^ rowx(r))."""
+    g = contr5_schedule_module()
+    if sched is None or rowx is None:
+        ts, tr = fwd7_tables()
+        sched = ts if sched is None else sched
+        rowx = tr if rowx is None else rowx
+    swz = swz or (lambda b: ((b >> 1) ^ (b >> 3)) & 3)
+    rx = lambda r: (rowx >> (2 * (r & 3))) & 3
+    slot = lambda r, X, arr: arr * 4096 + r * 512 + 16 * ((X << 2) | (swz(X) ^ rx(r)))
+    kL = op != "rc"
+    kR = op in ("inner", "rc")
+    reads = 0
+    for t in range(4):
+        ins = {"as": [], "bo": [], "ao": [], "bs": []}
+        for lane in range(32):
+            h, r = lane & 7, lane >> 3
+            S, So = fwd7_read_blocks(op, sched[h][t])
+            if kL:
+                ins["as"].append((lane, slot(r, S, 0)))
+                ins["bo"].append((lane, slot(r, So, 1)))
+            if kR:
+                ins["ao"].append((lane, slot(r, So, 0)))
+                ins["bs"].append((lane, slot(r, S, 1)))
+        reads += sum(g._set_cost(v, g.READ_SETS, 15) for v in ins.values() if v)
+    ob = (lambda h: 7 ^ h) if op == "wedge" else (lambda h: h)
+    writes = g._set_cost([(lane, slot(lane >> 3, ob(lane & 7), 0)) for lane in range(32)], g.WRITE_SETS, 7)
+    return reads, writes
 
 
 # ---- prod_bwd_contr5 / prod_fwd_contr5: contractions on 5 high bits -----------

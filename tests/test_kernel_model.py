@@ -258,25 +258,52 @@ def test_inner_frame_schedule_covers_every_pair():
 
 
 def test_inner_fwd7_schedule_covers_every_pair():
-    """The n = 7 forward's four steps per lane walk every (output block o,
-    partner S inside ~o) pair of the fused round exactly once; partners of
-    output 0 walked on lanes 3 and 7 come after those lanes' own outputs."""
+    """The n = 7 forward's four steps per lane (kFwd7Sched, as compiled) walk
+    every (output block o, partner S inside ~o) pair of the fused round exactly
+    once, and each lane's steps fit the kernel's output points: outputs 3, 5, 6
+    are complete after step 1 and output 7 after step 0 (lanes 3 and 7 then
+    take partners of output 0), outputs 0, 1, 2, 4 after step 3."""
     seen = {}
+    last = {}
     for h in range(8):
-        own_done = False
         for t in range(4):
             st = K.fwd7_step(h, t)
             if st is None:
                 continue
             o, S = st
             if o != h:
-                assert h in (3, 7) and o == 0
-                own_done = True
+                assert h in (3, 7) and o == 0 and t >= 2
             else:
-                assert not own_done
+                last[o] = max(last.get(o, -1), t)
             seen[(o, S)] = seen.get((o, S), 0) + 1
     want = {(o, S): 1 for o in range(8) for S in K.subsets(7 & ~o)}
     assert seen == want
+    assert last[7] == 0 and max(last[3], last[5], last[6]) <= 1
+
+
+def _fwd7_unsearched(h, t):
+    """The schedule before the search: own partners in subset order, lanes 3
+    and 7 taking output 0's partners 4, 5 and 6, 7; idle steps read (0, o)."""
+    if h == 0:
+        return t
+    if h == 3:
+        return (3 << 3 | (0, 4)[t]) if t < 2 else t + 2
+    if h == 7:
+        return 7 << 3 if t == 0 else (0x80 | 7 if t == 1 else t + 4)
+    parts = K.subsets(7 & ~h)
+    return (h << 3 | parts[t]) if t < len(parts) else (0x80 | h)
+
+
+@pytest.mark.parametrize("op", ["inner", "lc", "rc", "wedge", "regressive"])
+def test_fwd7_schedule_lds_conflicts(op):
+    """Under the measured b128 rules, the searched schedule and row term of
+    prod_fwd_out7 have no bank conflicts in their block reads or row-order
+    output stores for any of the five ops; the schedule before the search (row
+    term r & 3) had 12 to 28 extra cycles per chunk and half-wave."""
+    assert K.fwd7_lds_conflicts(op) == (0, 0)
+    old = [[_fwd7_unsearched(h, t) for t in range(4)] for h in range(8)]
+    reads, writes = K.fwd7_lds_conflicts(op, sched=old, rowx=0xE4)
+    assert reads >= 12 and writes == 0
 
 
 def test_contr5_header_is_the_generators():
