@@ -1452,7 +1452,15 @@ struct BalLane {
 template <unsigned RX = 0xE4u>
 __device__ __forceinline__ unsigned row_x(unsigned r) { return (RX >> (2u * (r & 3u))) & 3u; }
 
-template <unsigned RX = 0xE4u>
+// SW: the block swizzle as an 8-entry table of 2-bit values (blocks 0..7), or
+// 0 for swz()
+template <unsigned SW = 0u>
+__device__ __forceinline__ unsigned blk_swz(unsigned blk) {
+    if constexpr (SW == 0u) return swz(blk);
+    else return (SW >> (2u * (blk & 7u))) & 3u;
+}
+
+template <unsigned RX = 0xE4u, unsigned SW = 0u>
 __device__ __forceinline__ BalLane bal_lane(int n, int lane) {
     BalLane L;
     const int d4_log = n - 2;
@@ -1463,7 +1471,7 @@ __device__ __forceinline__ BalLane bal_lane(int n, int lane) {
         const unsigned blk = f >> 2, q = f & 3u;
         L.rr[i] = r;
         L.ff[i] = f;
-        L.so[i] = 16u * ((r << d4_log) + (blk << 2) + (q ^ swz(blk) ^ row_x<RX>(r)));
+        L.so[i] = 16u * ((r << d4_log) + (blk << 2) + (q ^ blk_swz<SW>(blk) ^ row_x<RX>(r)));
     }
     return L;
 }
@@ -1789,12 +1797,41 @@ struct FrameSched {
 struct FrameStep {
     unsigned o, p;
     bool sub;
+    bool idle = false;  // frame_step at n = 7: the step reads blocks X = o, W = p, result unused
+};
+
+// n = 7 (NH = 3): the frame schedule as searched for the LDS bank rules of the
+// backward kernels (prod_bwd_inner_frame, prod_bwd_contr_frame). Byte h of
+// kFrame7Sched[t] is lane h's step t: p (bits 0-2), o (3-5), sub (6), idle
+// (7; then o and p name the gc and partner blocks it reads). The lists are
+// the ones frame_step builds (sub partners, then sup partners; outputs 0 and
+// 7 keep six pairs and helpers 1, 2 and 5, 6 take one each at step 6) in
+// searched orders; with the block swizzle kFrame7Swz and the row term
+// kFrame7RowX of the LDS slots, the 16 lanes of each bank set read one
+// address per 16-byte group at every step of the inner product and the
+// contractions (the wedge and regressive products: one extra cycle per two
+// steps), and the row-order output stores stay conflict-free.
+constexpr unsigned long long kFrame7Sched[7] = {0x3f746d645b504940ull, 0x7972696059524807ull, 0x7a70682758170f05ull,
+                                                0x7e766c255a130900ull, 0x7c372f261b120b03ull, 0x7f362d241f160d06ull,
+                                                0x7b7d78aea3020104ull};
+constexpr unsigned kFrame7RowX = 0x8Du;   // rows 0..3 -> 1, 3, 0, 2
+constexpr unsigned kFrame7Swz = 0x50AFu;  // blocks 0..7 -> 3, 3, 2, 2, 0, 0, 1, 1
+
+// LDS slot terms of the frame kernels: the searched ones at n = 7
+template <int N>
+struct FrameLayout {
+    static constexpr unsigned kRowX = N == 7 ? kFrame7RowX : 0xE4u;
+    static constexpr unsigned kSwz = N == 7 ? kFrame7Swz : 0u;
 };
 
 template <int NH>
 __device__ __forceinline__ FrameStep frame_step(unsigned h, int t) {
     using Sch = FrameSched<NH>;
     constexpr unsigned full = (1u << NH) - 1u;
+    if constexpr (NH == 3) {
+        const unsigned c = (unsigned)(kFrame7Sched[t] >> (8u * h)) & 0xffu;
+        return FrameStep{(c >> 3) & 7u, c & 7u, ((c >> 6) & 1u) != 0u, (c >> 7) != 0u};
+    }
     if (Sch::kHelp) {
         if (h == 0u) return t == 0 ? FrameStep{0u, 0u, true} : FrameStep{0u, (unsigned)(t - 1), false};
         if (h == full) return t == 0 ? FrameStep{full, full, false} : FrameStep{full, (unsigned)(t - 1), true};
@@ -1847,6 +1884,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     float* __restrict__ GB, BlkParams P) {
     constexpr int NH = N - 4, NB = 1 << NH, R = 64 >> NH;
     using Sch = FrameSched<NH>;
+    using FL = FrameLayout<N>;
     constexpr int T = Sch::T;
     constexpr unsigned full = NB - 1u;
     __shared__ __attribute__((aligned(64))) float4 lds[4][3 * kBalGroupF4];  // a | b | gc
@@ -1865,7 +1903,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     // one group of R rows per wave (the host splits batches larger than one grid)
     const long long ngrp = (P.batch + R - 1) / R;
     const long long grp = (long long)blockIdx.x * 4 + wave;
-    const BalLane L = bal_lane(N, lane);
+    const BalLane L = bal_lane<FL::kRowX, FL::kSwz>(N, lane);
     const bool gbc = P.ldg4 == 0;
     // the group's loads are in flight while the step table is built
     BalPre pa, pb, pg;
@@ -1876,14 +1914,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     // in sub mode), sub flag, the high-part signs, the parities of p and o, and
     // whether the step is the pair (o, o) in sub mode
     if (wave == 0 && lane < 4 * NB) {
-        const unsigned th = (unsigned)lane & full, trs = (unsigned)lane >> NH;
+        const unsigned th = (unsigned)lane & full, trs = row_x<FL::kRowX>((unsigned)lane >> NH);
+#pragma unroll
         for (int t = 0; t < T; ++t) {
             const FrameStep st = frame_step<NH>(th, t);
-            const unsigned X = st.o ^ st.p;
+            const unsigned X = st.idle ? st.o : st.o ^ st.p;
             const HiSign sga = hi_sign<OP_INNER>(st.o, st.p, P.negh, P.nulh, full, P.nm1, P.mu);
             const HiSign sgb = hi_sign<OP_INNER>(st.p, st.o, P.negh, P.nulh, full, P.nm1, P.mu);
-            const unsigned offg = ((X << 2) | (swz(X) ^ trs)) << 4;
-            const unsigned offw = ((st.p << 2) | (swz(st.p) ^ trs ^ (st.sub ? 3u : 0u))) << 4;
+            const unsigned offg = ((X << 2) | (blk_swz<FL::kSwz>(X) ^ trs)) << 4;
+            const unsigned offw = ((st.p << 2) | (blk_swz<FL::kSwz>(st.p) ^ trs ^ (st.sub ? 3u : 0u))) << 4;
             tab[t][lane] = offg | (offw << 10) | ((st.sub ? 1u : 0u) << 20) | ((sga.mask >> 31) << 21) |
                            ((sgb.mask >> 31) << 22) | (((unsigned)__popc(st.p) & 1u) << 23) |
                            (((unsigned)__popc(st.o) & 1u) << 24) | ((st.sub && st.p == st.o ? 1u : 0u) << 25);
@@ -2047,14 +2086,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     frame_steps(step, std::make_integer_sequence<int, T>{});
     if constexpr (kRowOut) {
         // ga rows over the staged a, gb rows over b, in the staging layout of
-        // gc (block h of row r at slots 4h + (q ^ swz(h) ^ (r & 3))); then
-        // row-order stores
+        // gc (block h of row r at slots 4h + (q ^ swz(h) ^ row_x(r)), the
+        // kernel's swizzle and row term); then row-order stores
         wave_lds_sync();
         const unsigned a0 = lds_addr4(sa);
         const unsigned rowb = a0 + ((unsigned)r << (N + 2));
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const unsigned slot = ((h << 2) | ((unsigned)q ^ swz(h) ^ rs)) << 4;
+            const unsigned slot = ((h << 2) | ((unsigned)q ^ blk_swz<FL::kSwz>(h) ^ row_x<FL::kRowX>(rs))) << 4;
             if (WA) lds_st4(rowb + slot, make_float4(ya[4 * q], ya[4 * q + 1], ya[4 * q + 2], ya[4 * q + 3]));
             if (WB) lds_st4(rowb + 4096u + slot, make_float4(yb[4 * q], yb[4 * q + 1], yb[4 * q + 2], yb[4 * q + 3]));
         }
@@ -2190,6 +2229,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     constexpr int NH = N - 4, NB = 1 << NH, R = 64 >> NH;
     using Sch = FrameSched<NH>;
     using Cs = ContrSched<NH>;
+    using FL = FrameLayout<N>;
     constexpr int T = Sch::T;
     constexpr unsigned full = NB - 1u;
     constexpr bool kW = OPW == OP_WEDGE;
@@ -2206,7 +2246,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     // one group of R rows per wave (the host splits batches larger than one grid)
     const long long ngrp = (P.batch + R - 1) / R;
     const long long grp = (long long)blockIdx.x * 4 + wave;
-    const BalLane L = bal_lane(N, lane);
+    const BalLane L = bal_lane<FL::kRowX, FL::kSwz>(N, lane);
     const bool gbc = P.ldg4 == 0;
     constexpr unsigned D4 = 1u << (N - 2);
     // regressive: D a, D b and D^T gc, from the complemented chunks
@@ -2237,7 +2277,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     // parity term Pm, w1 and w2 terms (sub mode), rho (gb steps), gc parity
     // term Gp (gb steps)
     if (wave == 0 && lane < 4 * NB) {
-        const unsigned th = (unsigned)lane & full, trs = (unsigned)lane >> NH;
+        const unsigned th = (unsigned)lane & full, trs = row_x<FL::kRowX>((unsigned)lane >> NH);
+#pragma unroll
         for (int t = 0; t < T; ++t) {
             const FrameStep st = frame_step<NH>(th, t);
             const bool gbs = kLC ? st.sub : !st.sub;
@@ -2245,7 +2286,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
             const unsigned sub = st.sub ? 1u : 0u, gb = gbs ? 1u : 0u;
             unsigned X, wb, pm, cw;
             HiSign hs;
-            if (kW) {  // gb[~o]: (ih, jh) = (p, ~o), gc block p | ~o; ga[o]: (o, p ^ o), gc block p
+            if (st.idle) {  // reads only: gc block o, partner block p
+                X = st.o;
+                wb = st.p;
+                hs = hi_sign<OP_INNER>(0u, 0u, P.negh, P.nulh, full, P.nm1, P.mu);
+                pm = 0u;
+                cw = 0u;
+            } else if (kW) {  // gb[~o]: (ih, jh) = (p, ~o), gc block p | ~o; ga[o]: (o, p ^ o), gc block p
                 X = gbs ? (full ^ st.o ^ st.p) : st.p;
                 wb = gbs ? st.p : (st.p ^ st.o);
                 hs = gbs ? hi_sign<OP_WEDGE>(st.p, full ^ st.o, P.negh, P.nulh, full, P.nm1, P.mu)
@@ -2260,8 +2307,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
                 pm = (gb ? podd : oodd) ^ (LOWNEG ? sub : 0u);
                 cw = sub;
             }
-            const unsigned offg = ((X << 2) | (swz(X) ^ trs)) << 4;
-            const unsigned offw = (((wb << 2) | (swz(wb) ^ trs ^ (cw ? 3u : 0u))) << 4) + (gbs ? 0u : 4096u);
+            const unsigned offg = ((X << 2) | (blk_swz<FL::kSwz>(X) ^ trs)) << 4;
+            const unsigned offw = (((wb << 2) | (blk_swz<FL::kSwz>(wb) ^ trs ^ (cw ? 3u : 0u))) << 4) + (gbs ? 0u : 4096u);
             tab[t][lane] = offg | (offw << 10) | ((hs.mask >> 31) << 23) | (pm << 24) | ((gb & cw) << 25) |
                            (((gb ^ 1u) & cw) << 26) | (gb << 27) | ((gb & podd) << 28);
         }
@@ -2372,7 +2419,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     };
     frame_steps(step, std::make_integer_sequence<int, T>{});
     // ga rows over the staged a, gb rows over b, in the staging layout (block
-    // h of row r at slots 4h + (q ^ swz(h) ^ (r & 3))); then row-order stores
+    // h of row r at slots 4h + (q ^ swz(h) ^ row_x(r)), the kernel's swizzle
+    // and row term); then row-order stores
     wave_lds_sync();
     {
         const bool first_gb = first_sub == kLC;  // the first mode's output is a gb block
@@ -2382,8 +2430,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
         const unsigned b1 = kW && first_gb ? full ^ h : h, b2 = kW && !first_gb ? full ^ h : h;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const unsigned s1 = ((b1 << 2) | ((unsigned)q ^ swz(b1) ^ rs)) << 4;
-            const unsigned s2 = ((b2 << 2) | ((unsigned)q ^ swz(b2) ^ rs)) << 4;
+            const unsigned s1 = ((b1 << 2) | ((unsigned)q ^ blk_swz<FL::kSwz>(b1) ^ row_x<FL::kRowX>(rs))) << 4;
+            const unsigned s2 = ((b2 << 2) | ((unsigned)q ^ blk_swz<FL::kSwz>(b2) ^ row_x<FL::kRowX>(rs))) << 4;
             lds_st4(o1 + s1, make_float4(y1[4 * q], y1[4 * q + 1], y1[4 * q + 2], y1[4 * q + 3]));
             lds_st4(o2 + s2, make_float4(y2[4 * q], y2[4 * q + 1], y2[4 * q + 2], y2[4 * q + 3]));
         }
@@ -2401,7 +2449,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
                     const unsigned c0 = (unsigned)((N * (N - 1) / 2 + __popc(neg)) & 1);
                     const unsigned m = dual_chunk_mask(L.ff[i], neg, c0);
                     const unsigned fr = D4 - 1u - L.ff[i], blk = fr >> 2, r4 = L.rr[i];
-                    const unsigned so = 16u * ((r4 << (N - 2)) + (blk << 2) + ((fr & 3u) ^ swz(blk) ^ (r4 & 3u)));
+                    const unsigned so =
+                        16u * ((r4 << (N - 2)) + (blk << 2) + ((fr & 3u) ^ blk_swz<FL::kSwz>(blk) ^ row_x<FL::kRowX>(r4)));
                     if (GA) reinterpret_cast<float4*>(GA)[at] = dual_chunk<false>(lds_ld4(a0 + so), m);
                     if (GB) reinterpret_cast<float4*>(GB)[at] = dual_chunk<false>(lds_ld4(a0 + 4096u + so), m);
                 } else {
@@ -3212,10 +3261,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OP == OP_WE
     const BalPre pb = bal_fetch(bal_src(B, grp, P.batch, N, R), L, N - 2);
     if (wave == 0 && lane < 32) {
         const unsigned th = (unsigned)lane & full, trs = row_x<kFwd7RowX>((unsigned)lane >> 3);
+#pragma unroll
         for (int t = 0; t < T; ++t) {
             const unsigned code = (unsigned)(kFwd7Sched[t] >> (8u * th)) & 0xffu;
             const bool idle = (code & 0x80u) != 0u;
-            const FrameStep st{(code >> 3) & 7u, code & 7u, idle};
+            const FrameStep st{(code >> 3) & 7u, code & 7u, false, idle};
             // wedge: output ~o takes the pair (S, ~o ^ S) for every S inside ~o;
             // regressive: the pair (o | S, ~S) of xor index ~o, stored reversed
             // at block o; an idle step reads blocks S = o, So = p of its code

@@ -488,13 +488,17 @@ def frame_steps_count(nh):
 def frame_step(nh, h, t):
     """Step t of lane h in prod_bwd_inner_frame: (output block o, partner
     block p, sub mode). Sub partners (subsets of h, ascending) first, then sup
-    partners (h | S, ascending). At nh = 3 and 4 outputs 0 and full keep their
+    partners (h | S, ascending); at nh = 3 the same lists in the searched
+    orders that prod_bwd_*_frame compile (kFrame7Sched). At nh = 3 and 4 outputs 0 and full keep their
     first T steps (output full walks its sup pair (full, full) first, then its
     sub pairs) and helper lanes that finished their own lists take the rest in
     the wave's last steps (nh = 3: quad lanes 1, 2 and 5, 6, one pair each at
     step 6; nh = 4: lanes 3, 5, 6 and 9, 10, 12, two pairs each at steps 9
     and 10); other lanes idle there."""
     full = (1 << nh) - 1
+    if nh == 3:  # the compiled table (frame7_tables); an idle step as (h, h, False)
+        code = frame7_tables()[0][h][t]
+        return (h, h, False) if code & 0x80 else ((code >> 3) & 7, code & 7, bool(code & 0x40))
     if nh in FRAME_HELP:
         T, (h0, hf), c = FRAME_HELP[nh]
         if h == 0:
@@ -785,6 +789,67 @@ def wedge_frame_backward(a, b, gc, metric):
             if help_ and t == T - c - 1 and h in h0 + hf:
                 acc[h] = np.zeros(rows + (16,))
     return ga, gb
+
+
+def _products_hip():
+    import os
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "cliffordcuda_amd", "csrc",
+                        "products.hip")
+    return open(path).read()
+
+
+def frame7_tables():
+    """(kFrame7Sched, kFrame7RowX, kFrame7Swz) as the n = 7 frame kernels
+    compile them: per lane h and step t the code p | o << 3 | sub << 6 |
+    idle << 7 (an idle step's o and p name the gc and partner blocks it reads),
+    the row term and the block swizzle of the LDS slots (2-bit entries)."""
+    import re
+    text = _products_hip()
+    body = re.search(r"kFrame7Sched\[7\] = \{(.*?)\};", text, re.S).group(1)
+    steps = [int(v, 16) for v in re.findall(r"0x([0-9a-fA-F]+)ull", body)]
+    assert len(steps) == 7
+    rowx = int(re.search(r"kFrame7RowX = (0x[0-9a-fA-F]+)u;", text).group(1), 16)
+    swz = int(re.search(r"kFrame7Swz = (0x[0-9a-fA-F]+)u;", text).group(1), 16)
+    return [[(steps[t] >> (8 * h)) & 0xff for t in range(7)] for h in range(8)], rowx, swz
+
+
+def frame7_lds_conflicts(op, sched=None, rowx=None, swz=None):
+    """Extra LDS cycles of the n = 7 frame kernels' block reads per chunk and
+    32-lane half (rows 0..3; rows 4..7 repeat it) and of their row-order output
+    stores, under the measured rules of gen_contr5_schedule. op: "inner"
+    (prod_bwd_inner_frame: gc, b and a blocks), "lc", "rc", "wedge" (also the
+    regressive product's reads; prod_bwd_contr_frame: gc and one partner
+    block). Lane r * 8 + h reads row r's block X at slot 4 X + (swz(X) ^
+    rowx(r)), in sub mode the partner's slots reversed (^ 3; not the wedge)."""
+    g = contr5_schedule_module()
+    if sched is None:
+        sched, rowx, swz = frame7_tables()
+    sw = (lambda b: (swz >> (2 * b)) & 3) if swz else (lambda b: ((b >> 1) ^ (b >> 3)) & 3)
+    rx = lambda r: (rowx >> (2 * (r & 3))) & 3
+    slot = lambda r, X, rev=False: r * 512 + 16 * ((X << 2) | (sw(X) ^ rx(r) ^ (3 if rev else 0)))
+    reads = 0
+    for t in range(7):
+        ins = {}
+        for lane in range(32):
+            h, r = lane & 7, lane >> 3
+            c = sched[h][t]
+            o, p, sub = (c >> 3) & 7, c & 7, bool(c & 0x40)
+            if c & 0x80:
+                X, W, rev = o, p, False
+            elif op == "inner":
+                X, W, rev = o ^ p, p, sub
+            elif op == "wedge":
+                gbs = sub
+                X, W, rev = ((7 ^ o ^ p) if gbs else p), (p if gbs else p ^ o), False
+            else:
+                X, W, rev = o ^ p, p, sub
+            ins.setdefault("g", []).append((lane, 8192 + slot(r, X)))
+            ins.setdefault("w", []).append((lane, slot(r, W, rev)))
+            if op == "inner":
+                ins.setdefault("w2", []).append((lane, 4096 + slot(r, W, rev)))
+        reads += sum(g._set_cost(v, g.READ_SETS, 15) for v in ins.values())
+    writes = g._set_cost([(lane, slot(lane >> 3, lane & 7)) for lane in range(32)], g.WRITE_SETS, 7)
+    return reads, writes
 
 
 def fwd7_tables():
