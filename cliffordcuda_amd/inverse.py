@@ -12,8 +12,10 @@ kernels (``clf_inverse_versor``, ``clf_inverse_rep``, the product kernels).
   LDS; for a degenerate metric the null part is added by Newton steps
   y <- y (2 - x y): the error 1 - x y is nilpotent (it lies in the ideal of the
   null generators), so ceil(log2(r + 1)) steps make it exactly zero.
-* lu: the dense solve L(x) y = e_0 with L(x) the left-multiplication matrix,
-  whose columns L e_j = x e_j come from the product kernel.
+* lu: the dense solve L(x) y = e_0 with L(x) the left-multiplication matrix
+  (L e_j = x e_j), gathered from x with a table of blade-product signs, so the
+  memory guard's 2 B 4^n floats (L and the solver's factorised copy) is the
+  real peak.
 
 "auto" tries the versor test first, then the representation, then the dense
 solve. Every result is checked by the residual |x y - 1| (one product launch).
@@ -96,8 +98,30 @@ def _rep_inverse(xf, n, neg, nul):
     return y
 
 
+def _lmul_tables(n, neg, nul, device):
+    """The left-multiplication matrix L(x) (L e_j = x e_j) as a gather: its
+    entry (K, j) is s(K ^ j, j) x[K ^ j], with s(I, J) the sign of the blade
+    product e_I e_J (0 when I and J share a null generator): (-1) to the number
+    of pairs (i in I, j in J) with i > j, times the squares of the shared
+    generators. Returns the index table K ^ j and the sign table."""
+    dim = 1 << n
+    k = torch.arange(dim, device=device)
+    pc = torch.zeros(dim, dtype=torch.int64, device=device)
+    for b in range(n):
+        pc += (k >> b) & 1
+    K, J = k.view(dim, 1), k.view(1, dim)
+    I = K ^ J
+    swaps = torch.zeros(dim, dim, dtype=torch.int64, device=device)
+    for b in range(n):
+        swaps += ((J >> b) & 1) * pc[I >> (b + 1)]
+    common = I & J
+    sign = (1 - 2 * ((swaps + pc[common & neg]) & 1)).to(torch.float32)
+    return I, torch.where((common & nul) != 0, torch.zeros_like(sign), sign)
+
+
 def _dense_inverse(xf, n, neg, nul):
     B, dim = xf.shape
+    # L(x) and the solver's factorised copy of it
     need = 2 * B * dim * dim * xf.element_size()
     free, _ = torch.cuda.mem_get_info(xf.device)
     if need > 0.8 * free:
@@ -106,13 +130,16 @@ def _dense_inverse(xf, n, neg, nul):
             f"system (~{need/1e9:.1f} GB) but only {free/1e9:.1f} GB is free. "
             f"If x is a versor/blade use method='versor' (no matrix); otherwise "
             f"reduce batch or n.")
-    # columns of L(x): x e_j for every basis blade e_j, from the product kernel
-    basis = torch.eye(dim, device=xf.device).repeat(B, 1)
-    cols = _geom(xf.repeat_interleave(dim, 0), basis, n, neg, nul).view(B, dim, dim)
+    # L(x) gathered from x with the blade-product signs (exact: each entry is
+    # +-x_I or 0), built in place
+    idx, sign = _lmul_tables(n, neg, nul, xf.device)
+    lmat = xf[:, idx]
+    lmat.mul_(sign)
+    del idx, sign
     rhs = torch.zeros(B, dim, 1, device=xf.device)
     rhs[:, 0, 0] = 1.0
     try:
-        y = torch.linalg.solve(cols.transpose(1, 2), rhs).squeeze(-1).contiguous()
+        y = torch.linalg.solve(lmat, rhs).squeeze(-1).contiguous()
     except torch.linalg.LinAlgError as e:
         raise ValueError(f"multivector is not invertible ({e}).")
     return y

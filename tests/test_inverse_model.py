@@ -208,3 +208,24 @@ def test_scatter_passes_never_share_a_label(metric):
             a, b, _ = blade_label(A, metric)
             assert (a, b) not in seen
             seen.add((a, b))
+
+
+@pytest.mark.parametrize("metric", [(1, 1, 1), (1, -1, 0, 1), (-1, -1, 1, 0, 1), (0, 1, -1, 1, -1)])
+def test_dense_lmul_matrix_is_left_multiplication(metric):
+    """The dense inverse's L(x) gathered with the blade-product sign table
+    (inverse._lmul_tables) is left multiplication by x: L(x) y equals the
+    oracle's geometric product x y for random x, y (negative and null
+    generators, null ones not only last). A sign or index mistake in the table
+    changes a column and fails this."""
+    from cliffordcuda_amd.inverse import _lmul_tables
+    from cliffordcuda_amd._validate import metric_masks
+    n = len(metric)
+    neg, nul = metric_masks(metric)
+    g = torch.Generator().manual_seed(7 + n)
+    x = torch.randn(3, 1 << n, generator=g, dtype=torch.float64)
+    y = torch.randn(3, 1 << n, generator=g, dtype=torch.float64)
+    idx, sign = _lmul_tables(n, neg, nul, "cpu")
+    lmat = x[:, idx] * sign.double()
+    got = torch.einsum("bkj,bj->bk", lmat, y)
+    want = O.einsum_product("geom", x, y, list(metric))
+    assert torch.allclose(got, want, atol=1e-12)
