@@ -2207,7 +2207,10 @@ __device__ __forceinline__ unsigned dual_chunk_mask(unsigned F, unsigned neg, un
 // (the destination element's) of m is set
 template <bool SRC>
 __device__ __forceinline__ float4 dual_chunk(const float4& v, unsigned m) {
-    auto sg = [&](float x, unsigned bit) { return ((m >> bit) & 1u) ? -x : x; };
+    // the mask bit moved to the sign bit and xor-ed in (no compare and select)
+    auto sg = [&](float x, unsigned bit) {
+        return __uint_as_float(__float_as_uint(x) ^ ((m << (31u - bit)) & 0x80000000u));
+    };
     return SRC ? make_float4(sg(v.w, 3), sg(v.z, 2), sg(v.y, 1), sg(v.x, 0))
                : make_float4(sg(v.w, 0), sg(v.z, 1), sg(v.y, 2), sg(v.x, 3));
 }
