@@ -1737,17 +1737,35 @@ __device__ __forceinline__ void frame_sup(float (&ca)[16], float (&cb)[16], cons
     (term(std::integral_constant<int, Is>{}), ...);
 }
 
+// Lane-dependent selects of whole accumulators: a mask that is all ones
+// where the lane's condition holds, formed once and opaque to the compiler
+// (which would turn the bit operations back into conditional moves, twice
+// the issue cost of a three-input bit operation on gfx950)
+__device__ __forceinline__ unsigned lane_mask(bool c) {
+    unsigned m = c ? ~0u : 0u;
+    asm volatile("" : "+v"(m));
+    return m;
+}
+__device__ __forceinline__ float bsel(unsigned m, float a, float b) {  // a where m, else b
+    return __uint_as_float((__float_as_uint(a) & m) | (__float_as_uint(b) & ~m));
+}
+__device__ __forceinline__ float bzero(unsigned m, float a) {  // 0 where m, else a
+    return __uint_as_float(__float_as_uint(a) & ~m);
+}
+
 // turn an accumulator between the reversed and the normal frame where cond
 // holds: c[k] <- f(k) c[15 - k], f = w2 (gb) or w1 (ga), times the parity
-// for a negative low metric
+// for a negative low metric (negated elements: one conditional move with a
+// negate modifier; the others a bit select)
 template <bool LOWNEG, bool GB>
 __device__ __forceinline__ void frame_turn(float (&c)[16], bool cond) {
+    const unsigned m = lane_mask(cond);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const bool f = ((GB ? w2b(k) : w1b(k)) ^ (LOWNEG ? par4(k) : 0)) != 0;
         const float x = c[k], y = c[15 - k];
-        c[k] = cond ? (f ? -y : y) : x;
-        c[15 - k] = cond ? (f ? -x : x) : y;
+        c[k] = f ? (cond ? -y : x) : bsel(m, y, x);
+        c[15 - k] = f ? (cond ? -x : y) : bsel(m, x, y);
     }
 }
 
@@ -2072,14 +2090,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
             if (WB) frame_turn<LOWNEG, true>(cb, h == full);
         }
         if constexpr (Sch::store(t)) {
-            if (store_t == t) store();
+            if constexpr (kRowOut) {  // the lanes whose outputs complete here keep them
+                const unsigned ms = lane_mask(store_t == t);
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    if (WA) ya[e] = bsel(ms, ca[e], ya[e]);
+                    if (WB) yb[e] = bsel(ms, cb[e], yb[e]);
+                }
+            } else if (store_t == t) {
+                store();
+            }
         }
         if constexpr (Sch::kHelp && t == T - Sch::C - 1) {  // the helpers start from zero
-            const bool z = Sch::helper(h);
+            const unsigned mz = lane_mask(Sch::helper(h));
 #pragma unroll
             for (int el = 0; el < 16; ++el) {
-                if (WA) ca[el] = z ? 0.f : ca[el];
-                if (WB) cb[el] = z ? 0.f : cb[el];
+                if (WA) ca[el] = bzero(mz, ca[el]);
+                if (WB) cb[el] = bzero(mz, cb[el]);
             }
         }
     };
@@ -2400,24 +2427,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
         if constexpr (K != 0) {
             const bool first = first_t == t, second = second_t == t;
             const bool sub = first == first_sub;  // the mode of the output completed here
+            const unsigned m1 = lane_mask(first), m2 = lane_mask(second), msub = lane_mask(sub);
 #pragma unroll
             for (int k = 0; k < 16; ++k) {
                 // the wedge product's sub-mode output is gb[~h] in the normal frame
                 const float ys = kW ? contr_out_sup<true>(acc, k) : contr_out_sub<LOWNEG, kLC>(acc, k);
                 const float yp = contr_out_sup<!kLC>(acc, k);
-                const float y = K == 1 ? ys : K == 2 ? yp : (sub ? ys : yp);
-                if constexpr (Cs::any_first(t)) y1[k] = first ? y : y1[k];
-                if constexpr (Cs::any_second(t)) y2[k] = second ? y : y2[k];
+                const float y = K == 1 ? ys : K == 2 ? yp : bsel(msub, ys, yp);
+                if constexpr (Cs::any_first(t)) y1[k] = bsel(m1, y, y1[k]);
+                if constexpr (Cs::any_second(t)) y2[k] = bsel(m2, y, y2[k]);
             }
             if constexpr (Cs::any_first(t)) {
 #pragma unroll
-                for (int el = 0; el < 16; ++el) acc[el] = first ? 0.f : acc[el];
+                for (int el = 0; el < 16; ++el) acc[el] = bzero(m1, acc[el]);
             }
         }
         if constexpr (Sch::kHelp && t == T - Sch::C - 1) {  // the helpers start from zero
-            const bool z = Sch::helper(h);
+            const unsigned mz = lane_mask(Sch::helper(h));
 #pragma unroll
-            for (int el = 0; el < 16; ++el) acc[el] = z ? 0.f : acc[el];
+            for (int el = 0; el < 16; ++el) acc[el] = bzero(mz, acc[el]);
         }
     };
     frame_steps(step, std::make_integer_sequence<int, T>{});
@@ -3309,8 +3337,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OP == OP_WE
     }
     auto keep = [&](bool done) {
         if constexpr (kRowOut) {
+            const unsigned md = lane_mask(done);
 #pragma unroll
-            for (int el = 0; el < 16; ++el) y[el] = done ? acc[el] : y[el];
+            for (int el = 0; el < 16; ++el) y[el] = bsel(md, acc[el], y[el]);
         } else if (done && row_ok) {
             store_blk(reinterpret_cast<float4*>(C) + (row << (N - 2)), h, acc, false);
         }
@@ -3353,16 +3382,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OP == OP_WE
         if constexpr (t == 0) keep(h == 7u);
         if constexpr (t == 1) {
             keep(h == 3u || h == 5u || h == 6u);
-            const bool z = h == 3u || h == 7u;  // lanes 3 and 7 turn to output 0
+            const unsigned mz = lane_mask(h == 3u || h == 7u);  // lanes 3 and 7 turn to output 0
 #pragma unroll
-            for (int el = 0; el < 16; ++el) acc[el] = z ? 0.f : acc[el];
+            for (int el = 0; el < 16; ++el) acc[el] = bzero(mz, acc[el]);
         }
         if constexpr (t == 3) {
+            const unsigned m0 = lane_mask(h == 0u);
 #pragma unroll
-            for (int el = 0; el < 16; ++el) {
-                const float m = fwd7_merge(acc[el]);
-                acc[el] = h == 0u ? m : acc[el];
-            }
+            for (int el = 0; el < 16; ++el) acc[el] = bsel(m0, fwd7_merge(acc[el]), acc[el]);
             keep(h == 0u || h == 1u || h == 2u || h == 4u);
         }
     };
