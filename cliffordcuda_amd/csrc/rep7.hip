@@ -137,7 +137,7 @@ __device__ __forceinline__ void gather7_single(const float* __restrict__ row, co
 // stages, and the sign (sg[m] = s_x(m) as +-1.0) multiplies the last stage,
 // which the compiler fuses into one DPP multiply. DPP controls: quad_perm
 // xor 1 (0xB1), 2 (0x4E), 3 (0x1B); row_half_mirror = xor 7 (0x141);
-// row_mirror = xor 15 (0x140).
+// row_mirror = xor 15 (0x140); row_ror:8 = xor 8 (0x128).
 template <unsigned J>
 __device__ __forceinline__ float quad_xor(float v) {
     if constexpr (J == 1u) return dpp16<0xB1>(v);
@@ -150,19 +150,18 @@ template <unsigned J>
 __device__ __forceinline__ void operand7_d2(const float (&t)[4], const float (&sg)[4], float (&op)[16]) {
     const float q = quad_xor<J>(t[J]);      // lane x ^ J
     const float r = quad_xor<J ^ 3u>(t[J]);  // lane x ^ J ^ 3
-    const float h = dpp16<0x141>(q);         // lane x ^ J ^ 7
     op[J] = q;
     op[4 + J] = dpp16<0x141>(r) * sg[1];   // x ^ J ^ 3 ^ 7 = x ^ (4 + J)
     op[12 + J] = dpp16<0x140>(r) * sg[3];  // x ^ J ^ 3 ^ 15 = x ^ (12 + J)
-    op[8 + J] = dpp16<0x140>(h) * sg[2];   // x ^ J ^ 7 ^ 15 = x ^ (8 + J)
+    op[8 + J] = dpp16<0x128>(q) * sg[2];   // x ^ J ^ 8
 }
 
 template <unsigned J>
 __device__ __forceinline__ void operand7_d3(const float (&t)[8], const float (&sg)[2], float (&op)[16]) {
     if constexpr (J < 4u) {
-        const float q = quad_xor<J>(t[J]);                 // lane x ^ J
+        const float q = quad_xor<J>(t[J]);     // lane x ^ J
         op[J] = q;
-        op[8 + J] = dpp16<0x140>(dpp16<0x141>(q)) * sg[1];  // x ^ J ^ 7 ^ 15 = x ^ (8 + J)
+        op[8 + J] = dpp16<0x128>(q) * sg[1];  // x ^ J ^ 8
     } else {
         const float q = quad_xor<J ^ 7u>(t[J]);   // lane x ^ J ^ 7
         op[J] = dpp16<0x141>(q);                  // x ^ J

@@ -32,7 +32,8 @@ __device__ __forceinline__ void wht_inplace(float (&v)[M]) {
 // block b taking its operands from lanes 16b .. 16b + 15. With lane x holding
 // W[x][.] of a conversion (phi[r][c] = W[r ^ c][c]), operand k of lane x is
 // W[x ^ k][k]: an xor shuffle inside the 16-lane row, done with DPP moves
-// (quad_perm for xor 1..3, row_half_mirror = xor 7, row_mirror = xor 15).
+// (quad_perm for xor 1..3, row_half_mirror = xor 7, row_mirror = xor 15,
+// row_ror:8 = xor 8).
 // The product C_b[4g + t][j] lands in lane 16g + j, register 4b + t; it goes
 // back through LDS as W_c[i ^ j][j] at row stride 20 floats, which keeps both
 // the scattered b32 writes and the b128 row reads free of bank conflicts.
@@ -44,12 +45,16 @@ __device__ __forceinline__ float dpp16(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 
-// value of v at lane (lane ^ K) of the same 16-lane row
+// value of v at lane (lane ^ K) of the same 16-lane row: row_ror:8 (a
+// rotation by 8 inside the row is xor 8) for K = 8..11, else row_mirror (xor
+// 15) and row_half_mirror (xor 7); then a quad_perm for the low bits
 template <unsigned K>
 __device__ __forceinline__ float xor16(float v) {
-    constexpr unsigned k1 = (K & 8u) ? (K ^ 15u) : K;    // row_mirror: xor 15
-    constexpr unsigned k2 = (k1 & 4u) ? (k1 ^ 7u) : k1;  // row_half_mirror: xor 7
-    if constexpr ((K & 8u) != 0u) v = dpp16<0x140>(v);
+    constexpr bool ror8 = (K & 12u) == 8u;
+    constexpr unsigned k1 = ror8 ? (K ^ 8u) : (K & 8u) ? (K ^ 15u) : K;
+    constexpr unsigned k2 = (k1 & 4u) ? (k1 ^ 7u) : k1;
+    if constexpr (ror8) v = dpp16<0x128>(v);
+    else if constexpr ((K & 8u) != 0u) v = dpp16<0x140>(v);
     if constexpr ((k1 & 4u) != 0u) v = dpp16<0x141>(v);
     if constexpr (k2 == 1u) v = dpp16<0xB1>(v);       // quad_perm [1,0,3,2]
     else if constexpr (k2 == 2u) v = dpp16<0x4E>(v);  // quad_perm [2,3,0,1]

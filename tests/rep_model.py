@@ -667,8 +667,9 @@ def rep7_dest_operand(T, zhi, pair):
 
 
 # DPP row permutations of the operand builder (lane x reads lane perm(x)):
-# quad_perm xor 1, 2, 3, row_half_mirror (xor 7), row_mirror (xor 15)
-DPP_XOR = {"q1": 1, "q2": 2, "q3": 3, "hm": 7, "m": 15}
+# quad_perm xor 1, 2, 3, row_half_mirror (xor 7), row_mirror (xor 15),
+# row_ror:8 (a rotation by 8 in a 16-lane row: xor 8)
+DPP_XOR = {"q1": 1, "q2": 2, "q3": 3, "hm": 7, "m": 15, "r8": 8}
 
 
 def rep7_operand_dpp_plan(pair):
@@ -681,12 +682,12 @@ def rep7_operand_dpp_plan(pair):
             plan[j] = q(j)
             plan[4 + j] = q(j ^ 3) + ["hm"]
             plan[12 + j] = q(j ^ 3) + ["m"]
-            plan[8 + j] = q(j) + ["hm", "m"]
+            plan[8 + j] = q(j) + ["r8"]
     else:
         for j in range(8):
             if j < 4:
                 plan[j] = q(j)
-                plan[8 + j] = q(j) + ["hm", "m"]
+                plan[8 + j] = q(j) + ["r8"]
             else:
                 plan[j] = q(j ^ 7) + ["hm"]
                 plan[8 + j] = q(j ^ 7) + ["m"]
