@@ -249,25 +249,37 @@ struct FusedSplit {
     long long ldx, ldy;  // floats between rows: 1024, or 0 for one row broadcast over the batch
 };
 
-// gather_pair with a fresh opaque copy of the table entries, so that the
-// blade offsets of several gathers in one group are not kept live together
-__device__ __forceinline__ void gather_pair_fresh(const float* __restrict__ row, const unsigned (&ent)[16], unsigned m,
-                                                  float (&w)[16]) {
-    unsigned e[16];
+// The fused kernels' gathers and scatters at LDS byte addresses formed once per
+// lane: pa0[z] / pa1[z] = the lane's row in region 0 plus blade I0 / I1 of
+// entry z, po[z] the one of the lane's output half; a region's offset
+// (REG * 4096 bytes) goes into the instruction's immediate offset, so a
+// gather or scatter element needs no address arithmetic.
+// Blade I1 of every entry is I0 ^ 511 (the host table checks it), so pa1[z] =
+// c1 - pa0[z] with c1 = 2 * row + 4 * 511: the kernel with the fewest free
+// registers (PICK) keeps c1 instead of pa1.
+template <unsigned REG, bool PICK>
+__device__ __forceinline__ void gather_pair_at(const unsigned (&pa0)[16], const unsigned (&pa1)[16], unsigned c1,
+                                               unsigned m, float (&w)[16]) {
 #pragma unroll
     for (int z = 0; z < 16; ++z) {
-        e[z] = ent[z];
-        asm volatile("" : "+v"(e[z]));
+        const float v0 = lds_load(pa0[z] + REG * 4096u);
+        const float v1 = lds_load((PICK ? c1 - pa0[z] : pa1[z]) + REG * 4096u);
+        const unsigned s0 = (m << (31 - 2 * z)) & 0x80000000u;
+        const unsigned s1 = (m << (30 - 2 * z)) & 0x80000000u;
+        w[z] = __uint_as_float(__float_as_uint(v0) ^ s0) + __uint_as_float(__float_as_uint(v1) ^ s1);
     }
-    gather_pair(row, e, m, w);
+    wht_inplace<16>(w);
 }
 
-// out half = T^-1 of the product in acc: relayout through `rel` (1280 floats),
-// then the two half rows in blade order into `rows` (1024 floats; it may be
-// the start of `rel`)
-__device__ __forceinline__ void split_finish(const floatx16& acc, float* __restrict__ rel, float* __restrict__ rows,
-                                             const unsigned (&en)[16], unsigned mout, int lane) {
-    const int b = lane >> 4, r = b >> 1;
+// the output half's row, the inverse conversion of acc through the relayout
+// at rel, written at po[z] + ROWS * 4096 bytes (PICK: po is chosen per
+// element from pa0 and c1 - pa0 by the lane mask ms, which keeps 32 fewer
+// registers live)
+template <unsigned ROWS, bool PICK>
+__device__ __forceinline__ void split_finish_at(const floatx16& acc, float* __restrict__ rel, const unsigned (&po)[16],
+                                                const unsigned (&pa0)[16], unsigned c1, unsigned ms, unsigned mout,
+                                                int lane) {
+    const int b = lane >> 4;
     const unsigned s = (unsigned)b & 1u, x = lane & 15u;
     const float pm = s ? -1.f : 1.f;
     relayout_store(rel, acc, lane);
@@ -280,8 +292,8 @@ __device__ __forceinline__ void split_finish(const floatx16& acc, float* __restr
     for (int z = 0; z < 16; ++z) {
         const float other = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(w[z]), 0x401F));
         const float v = __builtin_fmaf(pm, w[z], other) * (1.f / 32.f);
-        const unsigned blade = s ? ((en[z] >> 9) & 511u) : (en[z] & 511u);
-        rows[r * 512 + blade] = __uint_as_float(__float_as_uint(v) ^ (((mout >> z) & 1u) << 31));
+        const unsigned at = PICK ? (((c1 - pa0[z]) & ms) | (pa0[z] & ~ms)) : po[z];
+        lds_store(at + ROWS * 4096u, __uint_as_float(__float_as_uint(v) ^ (((mout >> z) & 1u) << 31)));
     }
     wave_lds_sync();
 }
@@ -330,7 +342,7 @@ struct FusedRegions {
 constexpr int kFusedWaves = 4;
 
 template <int KIND>
-__global__ __launch_bounds__(64 * kFusedWaves) void split_fused_kernel(FusedSplit P, SplitTable T) {
+__global__ __launch_bounds__(64 * kFusedWaves) __attribute__((amdgpu_waves_per_eu(2))) void split_fused_kernel(FusedSplit P, SplitTable T) {
     using RG = FusedRegions<KIND>;
     __shared__ float lds[kFusedWaves][RG::regions * 1024];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -372,6 +384,26 @@ __global__ __launch_bounds__(64 * kFusedWaves) void split_fused_kernel(FusedSpli
     unsigned mo = 0;
 #pragma unroll
     for (int z = 0; z < 16; ++z) mo |= ((ent[z] >> (18 + s)) & 1u) << z;
+    // LDS byte addresses of the lane's blades in its row of region 0 (kept:
+    // opaque, so they are not re-derived from the entries in the loop)
+    // (the forward, whose registers are fullest, picks the output half's
+    // addresses per element instead of keeping them)
+    constexpr bool kPick = KIND == 0;
+    unsigned pa0[16], pa1[16], po[16];
+    unsigned ms = s ? ~0u : 0u;
+    const unsigned lb = lds_byte_addr(base) + (unsigned)r * 2048u;
+    unsigned c1 = 2u * lb + 4u * 511u;
+    asm volatile("" : "+v"(ms), "+v"(c1));
+#pragma unroll
+    for (int z = 0; z < 16; ++z) {
+        pa0[z] = lb + 4u * (ent[z] & 511u);
+        asm volatile("" : "+v"(pa0[z]));
+        if constexpr (!kPick) {
+            pa1[z] = lb + 4u * ((ent[z] >> 9) & 511u);
+            po[z] = s ? pa1[z] : pa0[z];
+            asm volatile("" : "+v"(pa1[z]), "+v"(po[z]));
+        }
+    }
 
     const long long batch = P.batch;
     const long long ngroups = (batch + 1) / 2;
@@ -388,12 +420,6 @@ __global__ __launch_bounds__(64 * kFusedWaves) void split_fused_kernel(FusedSpli
     for (; g < ngroups; g += gstride) {
         unsigned m_x0 = mx0, m_y0 = my0, m_y0b = my0b, m_x1 = mx1, m_y1 = my1, m_y1b = my1b, mout = mo;
         asm volatile("" : "+v"(m_x0), "+v"(m_y0), "+v"(m_y0b), "+v"(m_x1), "+v"(m_y1), "+v"(m_y1b), "+v"(mout));
-        unsigned en[16];
-#pragma unroll
-        for (int z = 0; z < 16; ++z) {
-            en[z] = ent[z];
-            asm volatile("" : "+v"(en[z]));
-        }
         // stage 0: X0, Y0 (staged until the group ends)
         CLF_SPLIT_STAGE(sx0, ax0, ax1, ax2, ax3);
         CLF_SPLIT_STAGE(sy0, ay0, ay1, ay2, ay3);
@@ -407,12 +433,12 @@ __global__ __launch_bounds__(64 * kFusedWaves) void split_fused_kernel(FusedSpli
         floatx16 acc0;
         {
             float wx[16], wy[16];
-            gather_pair_fresh(sx0 + r * 512, en, m_x0, wx);
-            gather_pair_fresh(sy0 + r * 512, en, m_y0, wy);
+            gather_pair_at<RG::x0, kPick>(pa0, pa1, c1, m_x0, wx);
+            gather_pair_at<RG::y0, kPick>(pa0, pa1, c1, m_y0, wy);
             acc0 = mfma_chain(wx, wy);
         }
         if constexpr (KIND == 0) {  // C0 = L0 R0 is complete; X1 / Y1 regions are still free
-            split_finish(acc0, base + RG::rel0 * 1024, base + RG::rows0 * 1024, en, mout, lane);
+            split_finish_at<RG::rows0, kPick>(acc0, base + RG::rel0 * 1024, po, pa0, c1, ms, mout, lane);
         }
         // stage 1: X1, Y1
         CLF_SPLIT_STAGE(sx1, ax0, ax1, ax2, ax3);
@@ -426,56 +452,56 @@ __global__ __launch_bounds__(64 * kFusedWaves) void split_fused_kernel(FusedSpli
             floatx16 acc1;
             {
                 float wx[16], wy[16];
-                gather_pair_fresh(sx0 + r * 512, en, m_x0, wx);
-                gather_pair_fresh(sy1 + r * 512, en, m_y1, wy);
+                gather_pair_at<RG::x0, kPick>(pa0, pa1, c1, m_x0, wx);
+                gather_pair_at<RG::y1, kPick>(pa0, pa1, c1, m_y1, wy);
                 acc1 = mfma_chain(wx, wy);
             }
             {
                 float wx[16], wy[16];
-                gather_pair_fresh(sx1 + r * 512, en, m_x1, wx);
-                gather_pair_fresh(sy0 + r * 512, en, m_y0b, wy);
+                gather_pair_at<RG::x1, kPick>(pa0, pa1, c1, m_x1, wx);
+                gather_pair_at<RG::y0, kPick>(pa0, pa1, c1, m_y0b, wy);
                 acc1 = mfma_chain_acc(acc1, wx, wy, std::make_integer_sequence<unsigned, 16>{});
             }
             wave_lds_sync();
-            split_finish(acc1, base + RG::rel1 * 1024, base + RG::rows1 * 1024, en, mout, lane);
+            split_finish_at<RG::rows1, kPick>(acc1, base + RG::rel1 * 1024, po, pa0, c1, ms, mout, lane);
         } else if constexpr (KIND == 1) {
             // out0 += G1 R1^T; out1 = G1 (R0^)^T
             float wx[16];
-            gather_pair_fresh(sx1 + r * 512, en, m_x1, wx);
+            gather_pair_at<RG::x1, kPick>(pa0, pa1, c1, m_x1, wx);
             {
                 float wy[16];
-                gather_pair_fresh(sy1 + r * 512, en, m_y1, wy);
+                gather_pair_at<RG::y1, kPick>(pa0, pa1, c1, m_y1, wy);
                 acc0 = mfma_chain_acc(acc0, wx, wy, std::make_integer_sequence<unsigned, 16>{});
             }
             wave_lds_sync();
-            split_finish(acc0, base + RG::rel0 * 1024, base + RG::rows0 * 1024, en, mout, lane);
+            split_finish_at<RG::rows0, kPick>(acc0, base + RG::rel0 * 1024, po, pa0, c1, ms, mout, lane);
             floatx16 acc1;
             {
                 float wy[16];
-                gather_pair_fresh(sy0 + r * 512, en, m_y0b, wy);
+                gather_pair_at<RG::y0, kPick>(pa0, pa1, c1, m_y0b, wy);
                 acc1 = mfma_chain(wx, wy);
             }
             wave_lds_sync();
-            split_finish(acc1, base + RG::rel1 * 1024, base + RG::rows1 * 1024, en, mout, lane);
+            split_finish_at<RG::rows1, kPick>(acc1, base + RG::rel1 * 1024, po, pa0, c1, ms, mout, lane);
         } else {
             // out0 += (L1^)^T G1^; out1 = L0^T G1
             {
                 float wx[16], wy[16];
-                gather_pair_fresh(sx1 + r * 512, en, m_x1, wx);
-                gather_pair_fresh(sy1 + r * 512, en, m_y1, wy);
+                gather_pair_at<RG::x1, kPick>(pa0, pa1, c1, m_x1, wx);
+                gather_pair_at<RG::y1, kPick>(pa0, pa1, c1, m_y1, wy);
                 acc0 = mfma_chain_acc(acc0, wx, wy, std::make_integer_sequence<unsigned, 16>{});
             }
             wave_lds_sync();
-            split_finish(acc0, base + RG::rel0 * 1024, base + RG::rows0 * 1024, en, mout, lane);
+            split_finish_at<RG::rows0, kPick>(acc0, base + RG::rel0 * 1024, po, pa0, c1, ms, mout, lane);
             floatx16 acc1;
             {
                 float wx[16], wy[16];
-                gather_pair_fresh(sx0 + r * 512, en, m_x0, wx);
-                gather_pair_fresh(sy1 + r * 512, en, m_y1b, wy);
+                gather_pair_at<RG::x0, kPick>(pa0, pa1, c1, m_x0, wx);
+                gather_pair_at<RG::y1, kPick>(pa0, pa1, c1, m_y1b, wy);
                 acc1 = mfma_chain(wx, wy);
             }
             wave_lds_sync();
-            split_finish(acc1, base + RG::rel1 * 1024, base + RG::rows1 * 1024, en, mout, lane);
+            split_finish_at<RG::rows1, kPick>(acc1, base + RG::rel1 * 1024, po, pa0, c1, ms, mout, lane);
         }
     }
     if (g != g0) {
@@ -539,6 +565,9 @@ static bool split_table_build(uint32_t neg9, SplitTable& T) {
         }
     }
     for (unsigned key = 0; key < 256; ++key) {
+        // the kernels address blade I1 as I0 ^ 511 (the label of I | e_8 is
+        // the label of I times that of the Cl(8) pseudoscalar)
+        if (i1[key] != (i0[key] ^ 511u)) return false;
         const unsigned x = key >> 4, z = key & 15u;
         T.e[key] = i0[key] | (i1[key] << 9) | (s0[key] << 18) | (s1[key] << 19) |
                    ((unsigned)(host_popc(i0[key]) & 1) << 20) | ((unsigned)(host_popc(i1[key]) & 1) << 21) |

@@ -200,3 +200,20 @@ def test_rep7_operand_dpp_stages(pair):
             src ^= R.DPP_XOR[st]
         assert src == k, (k, stages)
         assert all(st in R.DPP_XOR for st in stages)
+
+
+@pytest.mark.parametrize("metric9", [(1,) * 9, (-1,) * 4 + (1,) * 5, (1, -1, 1, -1, 1, -1, 1, -1, 1), (-1,) * 8 + (1,)])
+def test_split_pair_blades_are_complements(metric9):
+    """The fused n = 9, 10 kernels address the second blade of a label as the
+    first xor 511 (csrc/rep_split.hip checks the host table for it): with the
+    split labels, the blade I | e_8 sharing a label with I < 256 is (I ^ 255)
+    | 256 for every p - q = 1 (mod 8) signature."""
+    tabs = R.split_tables(list(metric9))
+    assert tabs is not None
+    label, _ = tabs
+    first = {}
+    for I in range(256):
+        first[label[I]] = I
+    assert len(first) == 256
+    for J in range(256, 512):
+        assert J == first[label[J]] ^ 511
