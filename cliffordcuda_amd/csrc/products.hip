@@ -626,7 +626,7 @@ __global__ __launch_bounds__(256) void prod_bwd_blk(const float* __restrict__ A,
     }
 }
 
-// ---- small-batch kernels (9 <= n <= 12): the partner loop split over lanes ----
+// ---- small-batch kernels (9 <= n <= 12; the forward also at n = 8): the partner loop split over lanes ----
 // At batches of a few rows the one-lane-per-output-block kernels run one or
 // two waves per row, so a row of n = 12 takes 256 dependent block pairs on one
 // lane (0.65 ms at batch 1). Here a workgroup of 256 lanes owns G = 256 / S
@@ -4000,14 +4000,17 @@ static unsigned bal_grid(const void* kernel, const BlkParams& P) {
 // turn them off.
 static bool split_plan(int op, int n, uint32_t neg, uint32_t nul, BlkParams& P, bool& lowneg, bool fwd, dim3& grid,
                        size_t& lds_bytes) {
-    if (n < 9 || n > 12) return false;
+    // n = 8: the forward only (one workgroup per row, 16 lanes per output
+    // block, one partner each); the backward's one-lane-per-output kernels are
+    // short enough at n = 8
+    if (n < (fwd ? 8 : 9) || n > 12) return false;
     const int pp = options().product_path;
     if (pp == PATH_BLOCKED || pp == PATH_BALANCED || pp == PATH_TILED || pp == PATH_GENERIC) return false;
     const long long NB = 1LL << (n - 4);
     if (pp != PATH_SPLIT && P.batch * NB >= (1LL << 15)) return false;
     if (!blocked_metric(op, n, neg, nul, lowneg)) return false;
     block_sign_params(n, neg, nul, P);
-    P.split_log = n - 6;                 // S = NB / 4: four partners per lane
+    P.split_log = n == 8 ? 4 : n - 6;    // S = NB / 4: four partners per lane (n = 8: S = NB, one)
     const int g_log = 8 - P.split_log;   // G = 256 / S output blocks per workgroup
     P.wpr_log = (n - 4) - g_log;
     const long long wgs = P.batch << P.wpr_log;

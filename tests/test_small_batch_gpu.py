@@ -1,4 +1,5 @@
-"""The small-batch kernels (prod_fwd_split / prod_bwd_split, 9 <= n <= 12):
+"""The small-batch kernels (prod_fwd_split / prod_bwd_split, 9 <= n <= 12; the
+forward also at n = 8, one workgroup of 16 lanes per output block per row):
 at the reference's published shapes (batch 1 .. 64) a row's partner loop is
 split over the lanes of several workgroups and the partial blocks are summed in
 LDS in a fixed order. Parity with the fp64 oracle for every op at n = 9, 10,
@@ -100,3 +101,30 @@ def test_split_rows_are_independent():
         one = run("lc", metric, a[r:r + 1].contiguous(), b[r:r + 1].contiguous(), gc[r:r + 1].contiguous())
         for x, y in zip(full, one):
             assert torch.equal(x[r:r + 1], y)
+
+
+METRICS8 = [(1,) * 8, (1,) * 6 + (-1, 1), (1,) * 7 + (0,), (-1,) * 4 + (1, -1, 0, 1), (1,) * 4 + (-1, 1, -1, -1)]
+
+
+@pytest.mark.parametrize("metric", METRICS8, ids=lambda m: "".join({1: "+", -1: "-", 0: "0"}[x] for x in m))
+@pytest.mark.parametrize("op", O.OPS)
+def test_small_batch_forward_n8(op, metric, clf_env):
+    """n = 8 forward at the published batches (1, 3, 64) against the fp64
+    oracle, and forced onto the split kernel at a ragged batch of 129 rows
+    against the whole-row kernels (=blocked)."""
+    if op == "regressive" and 0 in metric:
+        pytest.skip("regressive undefined for degenerate metrics")
+    for batch in (1, 3, 64):
+        a, b, _ = inputs(8, batch, 150 + batch)
+        print(f"[case] small batch n=8 forward op={op} metric={metric} batch={batch}", flush=True)
+        c = cc.products.product(op, a.cuda(), b.cuda(), metric)
+        c64 = O.einsum_product(op, a.double(), b.double(), metric)
+        assert rel_err(c, c64) <= TOL
+    a, b, _ = [t.cuda() for t in inputs(8, 129, 158)]
+    print(f"[case] split forced n=8 forward op={op} metric={metric} batch=129", flush=True)
+    clf_env.setenv("CLF_PRODUCT_PATH", "split")
+    c_split = cc.products.product(op, a, b, metric)
+    clf_env.setenv("CLF_PRODUCT_PATH", "blocked")
+    c_blk = cc.products.product(op, a, b, metric)
+    clf_env.delenv("CLF_PRODUCT_PATH")
+    assert rel_err(c_split, c_blk) <= TOL
