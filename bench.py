@@ -490,7 +490,10 @@ def published(args, torch, cc, lib, T):
     N(0,1) gc (bench_geom_prod_bwd.py); the rotor row times apply_rotor(cs, x)
     with cs compiled outside the timer (bench_rotor_apply.py). Each cell also
     carries the device time of the same call (HIP events over 100 back-to-back
-    calls)."""
+    calls). A control row times torch's own elementwise `a * b` the same way
+    (forward and autograd.grad): at these sizes every cell is bounded below by
+    the host's synchronisation and autograd-engine hand-off costs, which vary
+    from box to box, and the control measures them in the same run."""
     import statistics
     dev = torch.device("cuda", 0)
     a0 = torch.randn(4096, 4096, device=dev)
@@ -545,14 +548,14 @@ def published(args, torch, cc, lib, T):
         e1.synchronize()
         return e0.elapsed_time(e1) / reps * 1e3
 
-    ops = ["geom", "wedge", "inner", "lc", "rc", "regressive"]
+    ops = ["geom", "wedge", "inner", "lc", "rc", "regressive", "torch_mul"]
     table = {"fwd": {}, "bwd": {}}
     g = torch.Generator().manual_seed(0)
     for n in range(7, 13):
         D = 1 << n
         cl = cc.CliffordAlgebra([1] * n, device=dev)
         meth = {"geom": cl.geom_prod, "wedge": cl.wedge_prod, "inner": cl.inner_prod, "lc": cl.left_contraction,
-                "rc": cl.right_contraction, "regressive": cl.regressive_prod}
+                "rc": cl.right_contraction, "regressive": cl.regressive_prod, "torch_mul": lambda x, y: x * y}
         for B in (1, 16, 64):
             a = torch.randn(B, D, generator=g).to(dev).requires_grad_()
             b = torch.randn(B, D, generator=g).to(dev).requires_grad_()
