@@ -299,6 +299,13 @@ def headline(args, torch, cc, lib, T):
     with path_switch("CLF_GEOM_PATH", "direct"):
         dfwd_ms = T.kernel_ms(fwd)
         dbwd_ms = T.kernel_ms(bwd)
+    # the same byte patterns without the arithmetic (clf_stream_probe over the
+    # same buffers, nontemporal as the kernels stream): the rate this memory
+    # system gives 3 reads + 2 writes (backward) and 2 reads + 1 write (forward)
+    sfwd_ms = T.kernel_ms(lambda: lib.clf_stream_probe(2, 1, a.data_ptr(), b.data_ptr(), 0, c.data_ptr(), 0,
+                                                       B * D, 1, sp))
+    sbwd_ms = T.kernel_ms(lambda: lib.clf_stream_probe(3, 2, a.data_ptr(), b.data_ptr(), gc.data_ptr(), ga.data_ptr(),
+                                                       gb.data_ptr(), B * D, 1, sp))
     nt = D * D
     bwd_flops = 4.0 * nt * B       # reference term-sum count: 2 products of 4^n multiply-adds
     fwd_flops = 2.0 * nt * B
@@ -324,11 +331,19 @@ def headline(args, torch, cc, lib, T):
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
                      "traffic": load_traffic().get("rep16_bwd_kernel Cl(8,0) B=262144"),
                      "kernel_ms": bwd_ms, "algorithmic_bytes_per_launch": bwd_bytes,
-                     "device": T.clock.device(*bwd_clock, "the rep16_bwd_kernel timing loop") if T.clock else None},
+                     "device": T.clock.device(*bwd_clock, "the rep16_bwd_kernel timing loop") if T.clock else None,
+                     "stream_ceiling": {
+                         "pattern": "clf_stream_probe: the same 3 reads + 2 writes of 268 MB, nontemporal, "
+                                    "no arithmetic", "achieved": bwd_bytes / (sbwd_ms * 1e-3) / 1e9, "unit": "GB/s",
+                         "kernel_ms": sbwd_ms, "frac_of_ceiling": sbwd_ms / bwd_ms}},
         "kernels": {
             "rep16_fwd_kernel": {"ms": fwd_ms, "gbs": fwd_bytes / (fwd_ms * 1e-3) / 1e9,
-                                 "hbm_frac": fwd_bytes / (fwd_ms * 1e-3) / 1e9 / PEAK_HBM_GBS},
-            "rep16_bwd_kernel": {"ms": bwd_ms, "gbs": achieved, "hbm_frac": achieved / PEAK_HBM_GBS},
+                                 "hbm_frac": fwd_bytes / (fwd_ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                                 "stream_ceiling_gbs": fwd_bytes / (sfwd_ms * 1e-3) / 1e9,
+                                 "frac_of_stream_ceiling": sfwd_ms / fwd_ms},
+            "rep16_bwd_kernel": {"ms": bwd_ms, "gbs": achieved, "hbm_frac": achieved / PEAK_HBM_GBS,
+                                 "stream_ceiling_gbs": bwd_bytes / (sbwd_ms * 1e-3) / 1e9,
+                                 "frac_of_stream_ceiling": sbwd_ms / bwd_ms},
             # per-term kernels: FP32 VALU bound, 4^n multiply-adds per product
             "prod_fwd_blk<GEOM> (per-term path)": {
                 "ms": dfwd_ms, "tflops": fwd_flops / (dfwd_ms * 1e-3) / 1e12,
@@ -723,7 +738,20 @@ def main():
             xs, ys, zs = x[:k], y[:k], z[:k]
             t = T.kernel_ms(lambda: torch.add(xs, ys, out=zs))
             by_size[str(mib)] = {"add_us": t * 1e3, "add_gbs": 3.0 * (mib << 20) / (t * 1e-3) / 1e9}
+        # clf_stream_probe: the product kernels' byte patterns without their
+        # arithmetic, plain and nontemporal, 256 MiB per operand
+        w = torch.empty_like(x)
+        v = torch.empty_like(x)
+        sp = T.stream.cuda_stream
+        probe = {}
+        for nin, nout, label in ((3, 2, "backward 3r+2w"), (2, 1, "forward 2r+1w"), (1, 1, "copy 1r+1w")):
+            for ntv in (1, 0):
+                t = T.kernel_ms(lambda: lib.clf_stream_probe(nin, nout, x.data_ptr(), y.data_ptr(), z.data_ptr(),
+                                                             w.data_ptr(), v.data_ptr(), nbytes // 4, ntv, sp))
+                probe[f"{label} {'nontemporal' if ntv else 'plain'}"] = {
+                    "us": t * 1e3, "gbs": (nin + nout) * nbytes / (t * 1e-3) / 1e9}
         print(json.dumps({"workload": "copycal", "bytes_read_per_copy": nbytes, "bytes_written_per_copy": nbytes,
+                          "stream_probe_256mib": probe,
                           "copy_ms": ms, "copy_gbs": 2.0 * nbytes / (ms * 1e-3) / 1e9,
                           "add_ms": ams, "add_gbs": 3.0 * nbytes / (ams * 1e-3) / 1e9,
                           "add_by_operand_mib": by_size}))

@@ -49,6 +49,7 @@ SIGNATURES = {
     "clf_last_error": (ctypes.c_char_p, []),
     "clf_device_info_get": (_i32, [_i32, ctypes.POINTER(DeviceInfo)]),
     "clf_clock_sample": (_i32, [_vp, _i32, _vp]),
+    "clf_stream_probe": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp]),
     "clf_product_max_n": (_i32, []),
     "clf_product_fwd": (_i32, [_i32, _i32, _u32, _u32, _vp, _vp, _vp, _i64, _vp]),
     "clf_product_bwd": (_i32, [_i32, _i32, _u32, _u32, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),

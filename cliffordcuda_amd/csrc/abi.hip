@@ -1,4 +1,5 @@
 // extern "C" entry points of libclifford_hip.so (declared in include/clifford_hip.h).
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 
@@ -193,6 +194,46 @@ __global__ __launch_bounds__(64) void clock_sample_kernel(int64_t* out) {
     out[3 * (int64_t)blockIdx.x + 2] = rt;
 }
 
+// Streaming calibration: out0 = in0 (+ in1 (+ in2)), out1 = in0 - out0, four
+// floats per lane and four float4 per lane per pass, grid-stride. The byte
+// pattern of a product launch without its arithmetic: its time is the rate
+// the memory system gives that pattern (3 reads + 2 writes: the backward,
+// 2 + 1: the forward, 1 + 1: a copy).
+template <int NIN, int NOUT, bool NT>
+__global__ __launch_bounds__(256) void stream_probe_kernel(const float4* __restrict__ a,
+                                                           const float4* __restrict__ b,
+                                                           const float4* __restrict__ c, float4* __restrict__ o0,
+                                                           float4* __restrict__ o1, int64_t n4) {
+    constexpr int U = 4;
+    const int64_t stride = (int64_t)gridDim.x * 256 * U;
+    for (int64_t base = (int64_t)blockIdx.x * 256 * U + threadIdx.x; base < n4; base += stride) {
+        float4 x[U], y[U], z[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t i = base + (int64_t)u * 256;
+            if (i < n4) {
+                x[u] = NT ? load_stream(a + i) : a[i];
+                if (NIN > 1) y[u] = NT ? load_stream(b + i) : b[i];
+                if (NIN > 2) z[u] = NT ? load_stream(c + i) : c[i];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t i = base + (int64_t)u * 256;
+            if (i < n4) {
+                float4 s = x[u];
+                if (NIN > 1) s = make_float4(s.x + y[u].x, s.y + y[u].y, s.z + y[u].z, s.w + y[u].w);
+                if (NIN > 2) s = make_float4(s.x + z[u].x, s.y + z[u].y, s.z + z[u].z, s.w + z[u].w);
+                if (NT) store_stream(o0 + i, s); else o0[i] = s;
+                if (NOUT > 1) {
+                    const float4 t = make_float4(x[u].x - s.x, x[u].y - s.y, x[u].z - s.z, x[u].w - s.w);
+                    if (NT) store_stream(o1 + i, t); else o1[i] = t;
+                }
+            }
+        }
+    }
+}
+
 }  // namespace clf
 
 extern "C" {
@@ -228,6 +269,44 @@ int clf_clock_sample(int64_t* out, int slots, void* stream) {
     if (!out) return clf::set_error(CLF_ERR_ARG, "out must not be NULL");
     if (slots < 1 || slots > 4096) return clf::set_error(CLF_ERR_ARG, "slots must be in [1, 4096]");
     hipLaunchKernelGGL(clf::clock_sample_kernel, dim3(slots), dim3(64), 0, (hipStream_t)stream, out);
+    CLF_HIP_CHECK(hipGetLastError());
+    return CLF_OK;
+}
+
+int clf_stream_probe(int n_in, int n_out, const float* in0, const float* in1, const float* in2, float* out0,
+                     float* out1, int64_t n_floats, int nontemporal, void* stream) {
+    clf::clear_error();
+    if (n_in < 1 || n_in > 3) return clf::set_error(CLF_ERR_ARG, "n_in must be 1, 2 or 3");
+    if (n_out < 1 || n_out > 2) return clf::set_error(CLF_ERR_ARG, "n_out must be 1 or 2");
+    if (n_floats < 0 || (n_floats & 3)) return clf::set_error(CLF_ERR_ARG, "n_floats must be a multiple of 4, >= 0");
+    const void* ptrs[5] = {in0, n_in > 1 ? in1 : in0, n_in > 2 ? in2 : in0, out0, n_out > 1 ? out1 : out0};
+    for (const void* q : ptrs) {
+        if (!q) return clf::set_error(CLF_ERR_ARG, "null pointer argument");
+        if (((uintptr_t)q) & 15u) return clf::set_error(CLF_ERR_ARG, "pointers must be 16-byte aligned");
+    }
+    if (n_floats == 0) return CLF_OK;
+    const int64_t n4 = n_floats / 4;
+    const int64_t wgs = std::min<int64_t>((n4 + 1023) / 1024, (int64_t)1 << 20);
+    const float4* a = (const float4*)ptrs[0];
+    const float4* b = (const float4*)ptrs[1];
+    const float4* c = (const float4*)ptrs[2];
+    float4* o0 = (float4*)out0;
+    float4* o1 = (float4*)ptrs[4];
+    hipStream_t s = (hipStream_t)stream;
+#define CLF_STREAM_PROBE(NI, NO, NTV) \
+    hipLaunchKernelGGL((clf::stream_probe_kernel<NI, NO, NTV>), dim3((unsigned)wgs), dim3(256), 0, s, a, b, c, o0, o1, n4)
+#define CLF_STREAM_PROBE_NT(NI, NO) \
+    do { if (nontemporal) CLF_STREAM_PROBE(NI, NO, true); else CLF_STREAM_PROBE(NI, NO, false); } while (0)
+    switch (n_in * 4 + n_out) {
+        case 5: CLF_STREAM_PROBE_NT(1, 1); break;
+        case 6: CLF_STREAM_PROBE_NT(1, 2); break;
+        case 9: CLF_STREAM_PROBE_NT(2, 1); break;
+        case 10: CLF_STREAM_PROBE_NT(2, 2); break;
+        case 13: CLF_STREAM_PROBE_NT(3, 1); break;
+        default: CLF_STREAM_PROBE_NT(3, 2); break;
+    }
+#undef CLF_STREAM_PROBE_NT
+#undef CLF_STREAM_PROBE
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
 }

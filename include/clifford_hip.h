@@ -95,6 +95,17 @@ int clf_device_info_get(int device, clf_device_info* out);
  * benchmark/_harness.py:41-50, and records none). */
 int clf_clock_sample(int64_t* out, int slots, void* stream);
 
+/* Streaming calibration for the roofline report: the byte pattern of a
+ * product launch without its arithmetic. Over n_floats floats (a multiple of
+ * 4), out0 = in0 (+ in1 (+ in2)) for 1 <= n_in <= 3 inputs and, when
+ * n_out == 2, out1 = in0 - out0; nontemporal != 0 streams with the
+ * nontemporal hint, as the product kernels do past the last-level cache. All
+ * pointers used are device memory, 16-byte aligned. The launch's time is the
+ * rate the memory system gives that pattern (n_in = 3, n_out = 2 is a product
+ * backward's, 2 + 1 a forward's). No counterpart in the reference. */
+int clf_stream_probe(int n_in, int n_out, const float* in0, const float* in1, const float* in2, float* out0,
+                     float* out1, int64_t n_floats, int nontemporal, void* stream);
+
 /* Largest n the product kernels accept (20; rows past the LDS budget, n >= 13,
  * run tiled kernels, as the reference's geom_prod_tiled_fused does,
  * src/cliffordcuda/extensions/ga/geom_prod_tiled.py:370-398, which has no

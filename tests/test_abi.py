@@ -45,6 +45,22 @@ def test_clock_sample_rejects_bad_arguments():
         assert "slots" in lib.clf_last_error().decode()
 
 
+def test_stream_probe_rejects_bad_arguments():
+    lib = _lib.load()
+    ok = 256  # a 16-byte aligned stand-in address; nothing is launched on rejection
+    cases = [((0, 1, ok, ok, ok, ok, ok, 16, 1, None), "n_in"), ((4, 1, ok, ok, ok, ok, ok, 16, 1, None), "n_in"),
+             ((1, 0, ok, ok, ok, ok, ok, 16, 1, None), "n_out"), ((1, 3, ok, ok, ok, ok, ok, 16, 1, None), "n_out"),
+             ((1, 1, ok, ok, ok, ok, ok, 18, 1, None), "multiple of 4"),
+             ((1, 1, ok, ok, ok, ok, ok, -4, 1, None), "multiple of 4"),
+             ((3, 2, ok, ok, None, ok, ok, 16, 1, None), "null"), ((2, 2, ok, ok, ok, ok, None, 16, 1, None), "null"),
+             ((2, 1, ok, ok + 4, ok, ok, ok, 16, 1, None), "aligned")]
+    for args, msg in cases:
+        assert lib.clf_stream_probe(*args) == 1, args
+        assert msg in lib.clf_last_error().decode(), (args, lib.clf_last_error())
+    # unused operands are not checked; zero floats launch nothing
+    assert lib.clf_stream_probe(1, 1, ok, None, None, ok, None, 0, 0, None) == 0
+
+
 def test_rotor_state_length_matches_python():
     """The traced-graph state length (computed in Python) equals the library's."""
     from cliffordcuda_amd.rotor import _state_len
