@@ -668,26 +668,42 @@ __global__ __launch_bounds__(256) void rep16_parts_sum_kernel(const float* __res
     const int p1 = p0 + kPartsPerSum < nparts ? p0 + kPartsPerSum : nparts;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     int p = p0;
-    for (; p + 8 <= p1; p += 8)
+    // sixteen loads in flight per batch: a full group of 32 partials is two round trips
+    for (; p + 16 <= p1; p += 16) {
+        float t[16];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) acc[u] += parts[(long long)(p + u) * 256 + e];
+        for (int u = 0; u < 16; ++u) t[u] = parts[(long long)(p + u) * 256 + e];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc[u] += t[u] + t[u + 8];
+    }
     for (; p < p1; ++p) acc[0] += parts[(long long)p * 256 + e];
     out[(long long)blockIdx.x * 256 + e] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
 }
 
-// gw = phi^-1(sum of the first-stage sums); one workgroup of 256 threads
-__global__ __launch_bounds__(256) void rep16_bcast_gw_kernel(const float* __restrict__ sums, int nsums,
-                                                              float* __restrict__ gw, RepTable T) {
+// gw = phi^-1(sum of the first-stage sums); one workgroup of 1024 threads.
+// Thread (q, e) sums the first-stage sums q, q + 4, q + 8, ... of element e
+// (sixteen loads in flight per batch: the usual 64 sums are one round trip),
+// and the four quarters are added in a fixed order.
+__global__ __launch_bounds__(1024) void rep16_bcast_gw_kernel(const float* __restrict__ sums, int nsums,
+                                                               float* __restrict__ gw, RepTable T) {
+    __shared__ double Q[1024];
     __shared__ float S[256];
-    const int e = threadIdx.x;
+    const int e = threadIdx.x & 255, q = threadIdx.x >> 8;
     double acc[4] = {0.0, 0.0, 0.0, 0.0};
-    int p = 0;
-    for (; p + 4 <= nsums; p += 4)
+    int p = q;
+    for (; p + 60 < nsums; p += 64) {
+        float t[16];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[u] += (double)sums[(long long)(p + u) * 256 + e];
-    for (; p < nsums; ++p) acc[0] += (double)sums[(long long)p * 256 + e];
-    S[e] = (float)((acc[0] + acc[1]) + (acc[2] + acc[3]));
+        for (int u = 0; u < 16; ++u) t[u] = sums[(long long)(p + 4 * u) * 256 + e];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) acc[u & 3] += (double)t[u];
+    }
+    for (; p < nsums; p += 4) acc[0] += (double)sums[(long long)p * 256 + e];
+    Q[threadIdx.x] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
     __syncthreads();
+    if (threadIdx.x < 256) S[e] = (float)((Q[e] + Q[256 + e]) + (Q[512 + e] + Q[768 + e]));
+    __syncthreads();
+    if (threadIdx.x >= 256) return;  // no barrier follows
     // thread (x, z): t[x][z] = (1/16) sum_c W[x][c] (-1)^{popc(z & c)}, W[x][c] = S[(x ^ c) * 16 + c]
     const unsigned xx = (unsigned)e >> 4, z = (unsigned)e & 15u;
     float t = 0.f;
@@ -966,7 +982,7 @@ int rep_bcast_bwd(int side, int n, uint32_t neg, const float* x, const float* w,
             nsums = (int)((nb + kPartsPerSum - 1) / kPartsPerSum);
             hipLaunchKernelGGL(rep16_parts_sum_kernel, dim3((unsigned)nsums), dim3(256), 0, s, parts, (int)nb, sums);
         }
-        hipLaunchKernelGGL(rep16_bcast_gw_kernel, dim3(1), dim3(256), 0, s, sums, nsums, gw, T);
+        hipLaunchKernelGGL(rep16_bcast_gw_kernel, dim3(1), dim3(1024), 0, s, sums, nsums, gw, T);
     }
     CLF_HIP_CHECK(hipGetLastError());
     return CLF_OK;
