@@ -29,12 +29,28 @@ class CliffordAlgebra:
         self._num_basis_biv = self.n * (self.n - 1) // 2
         self._neg, self._nul = _validate.metric_masks(metric)
         self._rotor_supported = self.n >= 7
+        self._dev_index = self.device.index
+        self._plans = {}
 
     # ── products (reference algebra.py:143-175) ─────────────────────────
     def _binary(self, op, a, b):
+        # The usual call, tested in one expression: plain 2-D contiguous fp32
+        # tensors of this algebra's row length and device, of one shape. It
+        # then goes straight to the launch with the plan cached per op. Any
+        # other call, and every call traced by torch.compile, takes the
+        # argument checks in the reference's order (same exceptions and
+        # messages) and the generic entry.
+        plan = self._plans.get(op)
+        if (plan is not None and not torch.compiler.is_compiling() and type(a) is torch.Tensor and type(b) is torch.Tensor and a.dim() == 2
+                and a.shape == b.shape and a.shape[1] == self.dim and a.dtype is torch.float32
+                and b.dtype is torch.float32 and a.is_cuda and b.is_cuda and a.get_device() == self._dev_index
+                and b.get_device() == self._dev_index and a.is_contiguous() and b.is_contiguous()):
+            return _products.run_rows(a, b, *plan)
         _validate.check_mv(a, "a", self.dim, self.device, self.dtype)
         _validate.check_mv(b, "b", self.dim, self.device, self.dtype)
-        return _products.product(op, a, b, self.metric)
+        out = _products.product(op, a, b, self.metric)
+        self._plans[op] = _products._plan(op, self.dim, self.metric)
+        return out
 
     def geom_prod(self, a, b):
         return self._binary("geom", a, b)

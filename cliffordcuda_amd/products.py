@@ -135,17 +135,23 @@ def product(op: str, a: torch.Tensor, b: torch.Tensor, metric=None) -> torch.Ten
     flat = len(shape) != 2  # (batch, dim) inputs go in as they are: no view nodes in the autograd graph
     a2 = a.contiguous().reshape(-1, dim) if flat else a.contiguous()
     b2 = b.contiguous().reshape(-1, dim) if flat else b.contiguous()
+    out = run_rows(a2, b2, code, n, neg, nul)
+    return out.reshape(shape) if flat else out
+
+
+def run_rows(a2, b2, code, n, neg, nul):
+    """The product of checked (batch, 2^n) contiguous fp32 GPU operands of one
+    shape: the custom op under torch.compile, the autograd node when a
+    gradient may be needed, else the launch alone."""
     ext = _ext if _ext_tried else _autograd_ext()
     if torch.compiler.is_compiling():
-        out = _ops.product(a2, b2, code, n, neg, nul)
-    elif torch.is_grad_enabled() and (a2.requires_grad or b2.requires_grad):
-        out = ext.product(a2, b2, code, n, neg, nul) if ext is not None else _ProductFunc.apply(a2, b2, code, n, neg,
-                                                                                                nul)
-    elif ext is not None:  # nothing to differentiate: the launch without the autograd node
-        out = ext.product_fwd(a2, b2, code, n, neg, nul)
-    else:
-        out = _product_fwd(code, n, neg, nul, a2, b2)
-    return out.reshape(shape) if flat else out
+        return _ops.product(a2, b2, code, n, neg, nul)
+    if torch.is_grad_enabled() and (a2.requires_grad or b2.requires_grad):
+        return ext.product(a2, b2, code, n, neg, nul) if ext is not None else _ProductFunc.apply(a2, b2, code, n, neg,
+                                                                                                 nul)
+    if ext is not None:  # nothing to differentiate: the launch without the autograd node
+        return ext.product_fwd(a2, b2, code, n, neg, nul)
+    return _product_fwd(code, n, neg, nul, a2, b2)
 
 
 def geom_prod(a, b, metric=None):
