@@ -216,7 +216,10 @@ __device__ __forceinline__ void store_row_part(const float (&v)[1 << RB], float*
     }
 }
 
-// y = Lambda(Q) x (FWD) or Lambda(Q)^T x (!FWD), one row per 2^(N-RB) lanes.
+// y = Lambda(Q) x (FWD) or Lambda(Q)^T x (!FWD), one row per 2^(N-RB) lanes
+// (RB: 2^RB floats of a row per lane; rotor_rb(N) for throughput, N - 6 for
+// one wave per row, which small batches take: a row's planes then run on 64
+// lanes with 2^(N-6) floats each instead of on 2^(N-6) lanes with 64 floats).
 // Persistent: the lanes of a row walk rows with a grid stride and load the
 // next row part while the current one is rotated. Rows past the end are never
 // stored; their prefetch re-reads the last row (a cache hit, no branch).
@@ -224,11 +227,11 @@ __device__ __forceinline__ void store_row_part(const float (&v)[1 << RB], float*
 // stay active together and every shuffle partner is active.
 // ldx: floats between the input's rows (2^N, or 0 for one row broadcast over
 // the batch: the transposed action on the gradient of a sum)
-template <int N, bool FWD>
+template <int N, bool FWD, int RB = rotor_rb(N)>
 __global__ __launch_bounds__(256) void rotor_apply_kernel(const float* __restrict__ cs,
                                                            const float* __restrict__ X, float* __restrict__ Y,
                                                            long long batch, long long ldx) {
-    constexpr int RB = rotor_rb(N);
+    static_assert(RB >= 1 && N - RB <= 6, "a row spans at most one wave");
     constexpr int LB = N - RB;
     const unsigned L = threadIdx.x & ((1u << LB) - 1u);
     const long long rows_per_block = 256 >> LB;
@@ -1394,11 +1397,44 @@ static void launch_apply_reg(bool fwd, const float* cs, const float* x, float* y
     }
 }
 
+// One wave per row (four rows per workgroup, 2^(n-6) floats per lane) where
+// it measured faster than the default layouts (rotor_rb: 64 floats on
+// 2^(n-6) lanes; the LDS-staged chain at n = 11, 12). Device time of one
+// forward apply, old -> wave rows: n = 9 19.5 -> 9.2 us at 64 to 2048 rows,
+// 24.2 -> 17.9 at 8192, even at 16384, 56 -> 66 at 32768 rows; n = 10
+// 30 -> 14.5 at 64 rows, 532 -> 455 at 131072; n = 11 43 -> 26.4 at 64 rows,
+// 1535 -> 532 at 65536; n = 12 51.4 -> 62.5 at 64 rows, 57.1 -> 63.8 at
+// 512, 77.9 -> 66.6 at 1024, 1848 -> 1100 at 32768.
+static bool use_wave_rows(int n, int64_t batch) {
+    switch (n) {
+        case 9: return batch <= 12288;
+        case 10:
+        case 11: return true;
+        case 12: return batch > 768;
+        default: return false;
+    }
+}
+
+template <int N>
+static void launch_apply_wave_rows(bool fwd, const float* cs, const float* x, float* y, int64_t batch, hipStream_t s,
+                                   long long ldx) {
+    const dim3 grid((unsigned)((batch + 3) / 4));
+    if (fwd) hipLaunchKernelGGL((rotor_apply_kernel<N, true, N - 6>), grid, dim3(256), 0, s, cs, x, y, (long long)batch, ldx);
+    else hipLaunchKernelGGL((rotor_apply_kernel<N, false, N - 6>), grid, dim3(256), 0, s, cs, x, y, (long long)batch, ldx);
+}
+
 // y = chain(cs) x (fwd) or chain(cs)^T x, any n in range, batch > 0; x's rows
 // are ldx floats apart (2^n, or 0 for one row broadcast over the batch)
 static void launch_chain(int n, bool fwd, const float* cs, const float* x, float* y, int64_t batch, hipStream_t s,
                          long long ldx) {
-    if (n <= kRegChainMaxN) {
+    if (use_wave_rows(n, batch)) {
+        switch (n) {
+            case 9: launch_apply_wave_rows<9>(fwd, cs, x, y, batch, s, ldx); break;
+            case 10: launch_apply_wave_rows<10>(fwd, cs, x, y, batch, s, ldx); break;
+            case 11: launch_apply_wave_rows<11>(fwd, cs, x, y, batch, s, ldx); break;
+            default: launch_apply_wave_rows<12>(fwd, cs, x, y, batch, s, ldx); break;
+        }
+    } else if (n <= kRegChainMaxN) {
 #define CLF_CALL(N) launch_apply_reg<N>(fwd, cs, x, y, batch, s, ldx)
         CLF_ROTOR_DISPATCH(n, CLF_CALL)
 #undef CLF_CALL
