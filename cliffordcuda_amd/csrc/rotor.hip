@@ -344,14 +344,14 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
 // Persistent: each workgroup walks rows with a grid stride, writes gx (if
 // requested) and, if gamma_ws != nullptr, its partial K (C(N,2) floats) to
 // gamma_ws[blockIdx.x * C(N,2)].
-template <int N>
+template <int N, int RB = rotor_rb(N)>
 __global__ __launch_bounds__(256) void rotor_apply_bwd_kernel(const float* __restrict__ cs,
                                                                const float* __restrict__ X,
                                                                const float* __restrict__ GY,
                                                                float* __restrict__ GX,
                                                                float* __restrict__ gamma_ws, long long batch,
                                                                long long ldg) {
-    constexpr int RB = rotor_rb(N);
+    static_assert(RB >= 1 && N - RB <= 6, "a row spans at most one wave");
     constexpr int LB = N - RB;
     constexpr int LPR = 1 << LB;
     constexpr int C = n_planes(N);
@@ -1310,9 +1310,12 @@ int rotor_state_floats(int n) { return (n >= kRotorMinN && n <= kRotorMaxN) ? st
 // Workgroups of a backward launch (and so partials in the workspace): the
 // register kernels take 256 >> (lanes per row) rows per workgroup, the
 // LDS-staged kernel kLdsBlades / 2^n rows.
+static bool use_wave_rows_bwd(int n, int64_t batch);
+
 static int rotor_bwd_grid(int n, int64_t batch) {
     long long rows_per_block;
-    if (n <= kRegChainMaxN) rows_per_block = 256 >> (n - rotor_rb(n));
+    if (use_wave_rows_bwd(n, batch)) rows_per_block = 4;
+    else if (n <= kRegChainMaxN) rows_per_block = 256 >> (n - rotor_rb(n));
     else rows_per_block = kLdsBlades >> n > 0 ? kLdsBlades >> n : 1;
     long long g = (batch + rows_per_block - 1) / rows_per_block;
     if (g > 1024) g = 1024;
@@ -1456,10 +1459,38 @@ static int launch_apply_bwd_reg(const float* cs, const float* x, const float* gy
     return (int)grid;
 }
 
+// The backward with the statistics on one wave per row (2^(n-6) floats per
+// lane) where it measured faster. Device time of one call (gx and the
+// partials), old -> wave rows: n = 9 40.1 -> 23.0 us at 64 rows, 40.8 -> 24.4
+// at 1024, 47.1 -> 50.5 at 8192; n = 10 55.8 -> 33.3 at 64, 58.5 -> 35.9 at
+// 1024, 79.5 -> 81.5 at 8192; n = 11 108 -> 63.5 at 64, 602 -> 178 at 8192
+// (the LDS-staged chain before); n = 12 132 -> 101 at 64, 725 -> 347 at 4096.
+static bool use_wave_rows_bwd(int n, int64_t batch) {
+    if (n == 9 || n == 10) return batch <= 4096;
+    return n == 11 || n == 12;
+}
+
+template <int N>
+static int launch_apply_bwd_wave_rows(const float* cs, const float* x, const float* gy, long long ldg, float* gx,
+                                      float* ws, int64_t batch, hipStream_t s) {
+    const unsigned grid =
+        resident_grid((const void*)rotor_apply_bwd_kernel<N, N - 6>, 256, 0, rotor_bwd_grid(N, batch));
+    hipLaunchKernelGGL((rotor_apply_bwd_kernel<N, N - 6>), dim3(grid), dim3(256), 0, s, cs, x, gy, gx, ws,
+                       (long long)batch, ldg);
+    return (int)grid;
+}
+
 static int launch_gamma(int n, const float* cs, const float* x, const float* gy, long long ldg, float* gx, float* ws,
                         int64_t batch, hipStream_t s) {
     int nparts = 0;
-    if (n <= kRegChainMaxN) {
+    if (use_wave_rows_bwd(n, batch)) {
+        switch (n) {
+            case 9: nparts = launch_apply_bwd_wave_rows<9>(cs, x, gy, ldg, gx, ws, batch, s); break;
+            case 10: nparts = launch_apply_bwd_wave_rows<10>(cs, x, gy, ldg, gx, ws, batch, s); break;
+            case 11: nparts = launch_apply_bwd_wave_rows<11>(cs, x, gy, ldg, gx, ws, batch, s); break;
+            default: nparts = launch_apply_bwd_wave_rows<12>(cs, x, gy, ldg, gx, ws, batch, s); break;
+        }
+    } else if (n <= kRegChainMaxN) {
 #define CLF_CALL(N) nparts = launch_apply_bwd_reg<N>(cs, x, gy, ldg, gx, ws, batch, s)
         CLF_ROTOR_DISPATCH(n, CLF_CALL)
 #undef CLF_CALL
