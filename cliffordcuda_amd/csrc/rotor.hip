@@ -398,9 +398,10 @@ __global__ __launch_bounds__(256) void rotor_apply_bwd_kernel(const float* __res
 }
 
 // ---- the chain with rows staged in LDS (any n up to 12, run-time planes) ----
-// Used for the reference's backward on a caller's cs (every n) and for all
-// chain work at n = 11, 12, whose rows (8 and 16 KB) do not fit a register
-// layout. A workgroup stages kLdsBlades floats per array (whole rows; one row
+// Used for the reference's backward on a caller's cs (every n) and for the
+// n = 12 forward and transposed apply up to 768 rows; the other chain work at
+// n = 11, 12 runs the register kernels with one wave per row (32 and 64
+// floats per lane), which measured faster there. A workgroup stages kLdsBlades floats per array (whole rows; one row
 // at n = 12) and walks the planes with a barrier between planes; each thread
 // owns kLdsBlades / 1024 blade pairs of every plane, found by inserting zero
 // bits at p and q into the pair number:
@@ -1258,7 +1259,7 @@ __global__ __launch_bounds__(1024) void rotor_gamma_biv_kernel(const float* __re
         default: break;                   \
     }
 
-constexpr int kRegChainMaxN = 10;  // larger rows run the LDS-staged chain
+constexpr int kRegChainMaxN = 10;  // largest n of the default register layout (64 floats on 2^(n-6) lanes)
 
 // one entry per lane up to n = 8 (64 entries), one column per lane above
 template <int N>
