@@ -391,12 +391,19 @@ def products_config(args, torch, cc, lib, T, name, metric, B, ops, fwd_only=Fals
             flops += 4.0 * nt * B
             byts += 20.0 * D * B
         t = (entry["fwd_ms"] + entry.get("bwd_ms", 0.0)) * 1e-3
-        # "tflops_algorithmic" counts the reference's nonzero sigma terms; for
-        # the geometric product of real / split signatures the library runs the
-        # matrix-representation kernels, so there it is an equivalent rate
-        entry.update({"pairs_per_s": B / t, "tflops_algorithmic": flops / t / 1e12,
-                      "frac_fp32_peak": flops / t / 1e12 / PEAK_FP32_TFLOPS,
-                      "hbm_gbs_algorithmic": byts / t / 1e9, "frac_hbm": byts / t / 1e9 / PEAK_HBM_GBS})
+        # The reference's nonzero sigma terms over the time. The masked products
+        # run per-term kernels, so there it is their VALU rate (with its
+        # fraction of the FP32 peak). The geometric product is served by the
+        # matrix-representation kernels where the signature has one, which do
+        # other (fewer or more) multiply-adds: there the figure only says how
+        # fast the per-term formulation would have to run, and gets no
+        # fraction of peak; the per-term kernels' own rate is per_term_path.
+        entry.update({"pairs_per_s": B / t, "hbm_gbs_algorithmic": byts / t / 1e9,
+                      "frac_hbm": byts / t / 1e9 / PEAK_HBM_GBS})
+        if op == "geom":
+            entry["term_count_equivalent_tflops"] = flops / t / 1e12
+        else:
+            entry.update({"tflops_algorithmic": flops / t / 1e12, "frac_fp32_peak": flops / t / 1e12 / PEAK_FP32_TFLOPS})
         if op == "geom":
             # the per-term kernels at the same shape (the path of every other op)
             with path_switch("CLF_GEOM_PATH", "direct"):
