@@ -309,11 +309,13 @@ def apply_rotor(cs: torch.Tensor, x: torch.Tensor, n: int) -> torch.Tensor:
     if torch.compiler.is_compiling():
         return _ops.rotor_cs_apply(cs.contiguous(), x.contiguous(), n)
     info = getattr(cs, "_clf_rotor", None)
+    grad = torch.is_grad_enabled() and (x.requires_grad or cs.requires_grad)
     if info is not None and info.unchanged(cs):
-        if torch.is_grad_enabled() and cs.requires_grad:
+        if grad and cs.requires_grad:
             return _CompiledCsApplyFunc.apply(cs, x, info.state, n)
-        return _StateApplyFunc.apply(info.state, x, n)
-    return _CsApplyFunc.apply(cs.contiguous(), x, n)
+        # nothing to differentiate: the launch without an autograd node
+        return _StateApplyFunc.apply(info.state, x, n) if grad else _apply_fwd(info.state, x, n)
+    return _CsApplyFunc.apply(cs.contiguous(), x, n) if grad else _cs_apply_fwd(cs.contiguous(), x, n)
 
 
 def apply_bivector(bivector: torch.Tensor, x: torch.Tensor, n: int) -> torch.Tensor:
