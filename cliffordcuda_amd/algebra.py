@@ -41,10 +41,11 @@ class CliffordAlgebra:
         # argument checks in the reference's order (same exceptions and
         # messages) and the generic entry.
         plan = self._plans.get(op)
-        if (plan is not None and not torch.compiler.is_compiling() and type(a) is torch.Tensor and type(b) is torch.Tensor and a.dim() == 2
-                and a.shape == b.shape and a.shape[1] == self.dim and a.dtype is torch.float32
-                and b.dtype is torch.float32 and a.is_cuda and b.is_cuda and a.get_device() == self._dev_index
-                and b.get_device() == self._dev_index and a.is_contiguous() and b.is_contiguous()):
+        if (plan is not None and not torch.compiler.is_compiling() and type(a) is torch.Tensor
+                and type(b) is torch.Tensor and a.dim() == 2 and a.shape == b.shape and a.shape[1] == self.dim
+                and a.dtype is torch.float32 and b.dtype is torch.float32 and a.is_cuda and b.is_cuda
+                and a.get_device() == self._dev_index and b.get_device() == self._dev_index
+                and a.is_contiguous() and b.is_contiguous()):
             return _products.run_rows(a, b, *plan)
         _validate.check_mv(a, "a", self.dim, self.device, self.dtype)
         _validate.check_mv(b, "b", self.dim, self.device, self.dtype)

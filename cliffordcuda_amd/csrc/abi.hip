@@ -293,8 +293,9 @@ int clf_stream_probe(int n_in, int n_out, const float* in0, const float* in1, co
     float4* o0 = (float4*)out0;
     float4* o1 = (float4*)ptrs[4];
     hipStream_t s = (hipStream_t)stream;
-#define CLF_STREAM_PROBE(NI, NO, NTV) \
-    hipLaunchKernelGGL((clf::stream_probe_kernel<NI, NO, NTV>), dim3((unsigned)wgs), dim3(256), 0, s, a, b, c, o0, o1, n4)
+#define CLF_STREAM_PROBE(NI, NO, NTV)                                                                     \
+    hipLaunchKernelGGL((clf::stream_probe_kernel<NI, NO, NTV>), dim3((unsigned)wgs), dim3(256), 0, s, a, b, c, o0, \
+                       o1, n4)
 #define CLF_STREAM_PROBE_NT(NI, NO) \
     do { if (nontemporal) CLF_STREAM_PROBE(NI, NO, true); else CLF_STREAM_PROBE(NI, NO, false); } while (0)
     switch (n_in * 4 + n_out) {

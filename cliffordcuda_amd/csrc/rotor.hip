@@ -217,9 +217,9 @@ __device__ __forceinline__ void store_row_part(const float (&v)[1 << RB], float*
 }
 
 // y = Lambda(Q) x (FWD) or Lambda(Q)^T x (!FWD), one row per 2^(N-RB) lanes
-// (RB: 2^RB floats of a row per lane; rotor_rb(N) for throughput, N - 6 for
-// one wave per row, which small batches take: a row's planes then run on 64
-// lanes with 2^(N-6) floats each instead of on 2^(N-6) lanes with 64 floats).
+// (RB: 2^RB floats of a row per lane; rotor_rb(N), or N - 6 for one wave per
+// row, where a row's planes run on 64 lanes with 2^(N-6) floats each instead
+// of on 2^(N-6) lanes with 64 floats; use_wave_rows picks by n and batch).
 // Persistent: the lanes of a row walk rows with a grid stride and load the
 // next row part while the current one is rotated. Rows past the end are never
 // stored; their prefetch re-reads the last row (a cache hit, no branch).
@@ -401,10 +401,11 @@ __global__ __launch_bounds__(256) void rotor_apply_bwd_kernel(const float* __res
 // Used for the reference's backward on a caller's cs (every n) and for the
 // n = 12 forward and transposed apply up to 768 rows; the other chain work at
 // n = 11, 12 runs the register kernels with one wave per row (32 and 64
-// floats per lane), which measured faster there. A workgroup stages kLdsBlades floats per array (whole rows; one row
-// at n = 12) and walks the planes with a barrier between planes; each thread
-// owns kLdsBlades / 1024 blade pairs of every plane, found by inserting zero
-// bits at p and q into the pair number:
+// floats per lane), which measured faster there. A workgroup stages
+// kLdsBlades floats per array (whole rows; one row at n = 12) and walks the
+// planes with a barrier between planes; each thread owns kLdsBlades / 1024
+// blade pairs of every plane, found by inserting zero bits at p and q into
+// the pair number:
 //   base = deposit(t), I = base | 2^p (p set, q clear), J = base | 2^q.
 // Modes:
 //   LDS_FWD    y = chain(cs) x
@@ -1423,8 +1424,12 @@ template <int N>
 static void launch_apply_wave_rows(bool fwd, const float* cs, const float* x, float* y, int64_t batch, hipStream_t s,
                                    long long ldx) {
     const dim3 grid((unsigned)((batch + 3) / 4));
-    if (fwd) hipLaunchKernelGGL((rotor_apply_kernel<N, true, N - 6>), grid, dim3(256), 0, s, cs, x, y, (long long)batch, ldx);
-    else hipLaunchKernelGGL((rotor_apply_kernel<N, false, N - 6>), grid, dim3(256), 0, s, cs, x, y, (long long)batch, ldx);
+    if (fwd)
+        hipLaunchKernelGGL((rotor_apply_kernel<N, true, N - 6>), grid, dim3(256), 0, s, cs, x, y, (long long)batch,
+                           ldx);
+    else
+        hipLaunchKernelGGL((rotor_apply_kernel<N, false, N - 6>), grid, dim3(256), 0, s, cs, x, y, (long long)batch,
+                           ldx);
 }
 
 // y = chain(cs) x (fwd) or chain(cs)^T x, any n in range, batch > 0; x's rows
